@@ -1,0 +1,215 @@
+/*
+ * bolt3_amd — C ABI of the MI355X (gfx950) Bolt-3 Dual-Field attention kernels.
+ *
+ * Each entry point replaces a group of PyTorch ops of the reference's pure
+ * Python implementation (vsa_lm/config/bolt3.py, cited per function below).
+ * Conventions shared by all entry points:
+ *   - arguments come in one plain struct of device pointers, element strides and
+ *     sizes; no allocation, no host synchronisation, no exceptions;
+ *   - `stream` is a hipStream_t passed as void*; work is enqueued on it only;
+ *   - return 0 on success, a positive B3_ERR_* domain code for a rejected
+ *     argument, or a hipError_t code from the launch;
+ *   - storage dtype is B3_F32 or B3_BF16 (raw bf16 bits); slot masses, utilities,
+ *     positions, gates and M_res are always fp32.
+ * Layout names: B batch rows, H query heads, HKV key/value heads, HD head dim,
+ * S attractor slots, C chunk length, bh = b*HKV + hkv.
+ */
+#ifndef BOLT3_AMD_H
+#define BOLT3_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { B3_F32 = 0, B3_BF16 = 1 };
+enum { B3_OK = 0, B3_ERR_ARG = 1001, B3_ERR_UNSUPPORTED = 1002, B3_ERR_WORKSPACE = 1003 };
+
+/* Rows of one decision-log record (per step, per bh, B3_LOG_COLS floats each). */
+enum {
+  B3_LOG_REL = 0,      /* rel_err per token                          */
+  B3_LOG_SCORE = 1,    /* eviction / fill score per token            */
+  B3_LOG_BEST = 2,     /* best slot cosine per token (steady)        */
+  B3_LOG_SIMV = 3,     /* value cosine with the best slot (steady)   */
+  B3_LOG_SLOT = 4,     /* argmax slot per token (steady)             */
+  B3_LOG_MERGE = 5,    /* 1 if merged                                */
+  B3_LOG_DELTA = 6,    /* 1 if written to M_res                      */
+  B3_LOG_TOPTOK = 7,   /* token order (steady: candidates; fill: picked) */
+  B3_LOG_BOTSLOT = 8,  /* slot order by keep, ascending (steady)     */
+  B3_LOG_WIN = 9,      /* 1 if the i-th pair (token, slot) swapped   */
+  B3_LOG_KEEP = 10,    /* keep value per slot                        */
+  B3_LOG_TOPVAL = 11,
+  B3_LOG_BOTVAL = 12,
+  B3_LOG_ROWS = 13,
+  B3_LOG_COLS = 256
+};
+
+/* [B][heads][t][HD] output view: element (b, h, t, d) at p + b*sb + h*sh + t*HD + d. */
+typedef struct { void* p; int64_t sb, sh; } b3_tensor_out;
+/* fp32 [B][heads][t] view: element (b, h, t) at p + b*sb + h*sh + t. */
+typedef struct { float* p; int64_t sb, sh; } b3_gate_out;
+
+typedef struct {
+  int32_t dtype, B, T, H, HKV, HD;
+  const void* lin;            /* [B][T][lin_row_stride]: q | k | v | beta | eta columns (projection output) */
+  int64_t lin_row_stride;
+  const float* qn_w;          /* [HD] q RMSNorm weight (fp32 values) or NULL */
+  const float* kn_w;          /* [HD] k RMSNorm weight or NULL */
+  int32_t has_qk_norm;
+  float eps;
+  const float* inv_freq;      /* [HD/2] RoPE inverse frequencies (fp32 values of the module buffer) */
+  int32_t pos0;               /* position of row t is pos0 + t */
+  b3_tensor_out q_raw, q_rope, k_raw, k_rope, v;  /* q_raw / k_raw may have p == NULL */
+  b3_gate_out beta, eta;      /* sigmoid / tanh gates, values rounded to the storage dtype */
+  float* pos_out;             /* optional fp32 [T]: pos0 + t */
+} b3_heads_args;
+
+/*
+ * Head preparation for a block of tokens: q/k RMSNorm, RoPE, beta/eta gates.
+ * Replaces head_qkv's norms + LlamaRoPE + gates:
+ * vsa_lm/config/bolt3.py:59-66 (head_qkv), :197-199 (forward) and :346-349 (step);
+ * vsa_lm/surgery.py:49-53 (LlamaRMSNorm), :86-93 (LlamaRoPE).
+ */
+int bolt3_heads(const b3_heads_args* a, void* stream);
+
+typedef struct {
+  int32_t dtype, B, HKV, HD, S;
+  /* consolidated tokens: element (bh, n, d) at kr + bh*tok_bh_stride + n*HD + d (same for kp, v) */
+  const void* kr;             /* un-roped keys   */
+  const void* kp;             /* roped keys      */
+  const void* v;
+  int64_t tok_bh_stride;
+  const float* pos;           /* fp32 position of token n (shared by all bh) */
+  const float* beta;          /* fp32 (bh, n) at beta + bh*beta_bh_stride + n */
+  int64_t beta_bh_stride;
+  int32_t n_steps;            /* consolidations run back to back                          */
+  int32_t off0, len0;         /* step 0 consumes tokens [off0, off0 + len0)               */
+  int32_t step_stride, step_len; /* step i > 0 consumes [i*step_stride, i*step_stride + step_len) */
+  int32_t n_filled;           /* filled slots before step 0 (0 => state must be the empty state) */
+  /* slot state, updated in place: ak/av [bh][S][HD] storage dtype (un-roped keys), mass/util/pm [bh][S],
+     act [bh][S] (0/1), m_res [bh][HD][HD] */
+  void* ak;
+  void* av;
+  float* mass;
+  float* util;
+  float* pm;
+  uint8_t* act;
+  float* m_res;
+  const float* kappa;         /* [HKV] */
+  const float* gamma;         /* [HKV] M_res decay */
+  const float* inv_freq;      /* [HD/2] */
+  /* optional outputs after every step (NULL to skip), packed per step: snap_k / snap_v
+     [n_steps][B*HKV][S][HD] roped slot keys and slot values (storage dtype), snap_bias
+     [n_steps][B*HKV][S] attention bias kappa*log(max(mass,1)) (-inf for inactive slots),
+     snap_m [n_steps][B*HKV][HD][HD] M_res */
+  void* snap_k;
+  void* snap_v;
+  float* snap_bias;
+  float* snap_m;
+  float* log;                 /* optional decision log [n_steps][bh][B3_LOG_ROWS][B3_LOG_COLS] */
+  void* work;                 /* scratch of >= bolt3_chain_workspace_bytes(...) bytes */
+  int64_t work_bytes;
+} b3_chain_args;
+
+/*
+ * Consolidation chain: n_steps successive _consolidate_functional calls per bh,
+ * one workgroup per bh with the slot state resident in LDS.
+ * Replaces vsa_lm/config/bolt3.py:68-192 (fill, score, merge, evict, Gershgorin
+ * delta-rule M_res update) as driven by the chunk loop at :262-273 and by
+ * Bolt3Decoder.step at :406-425.  Token lengths per step must be <= 256,
+ * S == 128, HD in {64, 128}.
+ */
+int bolt3_chain(const b3_chain_args* a, void* stream);
+int64_t bolt3_chain_workspace_bytes(int32_t dtype, int32_t B, int32_t HKV, int32_t HD, int32_t S);
+
+typedef struct {
+  int32_t dtype, B, H, HKV, HD, S, C, n_sinks;
+  int32_t mode;               /* 0: every chunk of a forward; 1: one block of queries against decoder state */
+  int32_t n_q;                /* queries per batch row (mode 0: T, mode 1: tokens in this step) */
+  int32_t score_round;        /* 1: q.k rounded to the storage dtype before scaling (forward); 0: fp32 (step) */
+  const void* q_rope;         /* (b, h, t, d) at + b*q_sb + h*q_sh + t*HD + d */
+  const void* q_raw;
+  int64_t q_sb, q_sh;
+  const float* eta;           /* (b, h, t) at + b*e_sb + h*e_sh + t */
+  int64_t e_sb, e_sh;
+  const void* win_k;          /* (b, hkv, n, d) at + b*w_sb + hkv*w_sh + n*HD + d; roped keys */
+  const void* win_v;
+  int64_t w_sb, w_sh;
+  int32_t a_start, a_len;     /* mode 1: older window segment [a_start, a_start + a_len) */
+  int32_t b_start, b_len;     /* mode 1: current segment; query t is at segment index b_len - n_q + t */
+  const void* sink_k;         /* mode 1: (b, hkv, n, d) at + b*s_sb + hkv*s_sh + n*HD + d */
+  const void* sink_v;
+  int64_t s_sb, s_sh;
+  int32_t n_sink_keys;        /* mode 1: number of sink keys present (0 = none) */
+  const void* slot_k;         /* [step][bh][S][HD] roped slot keys (mode 0: step = chunk - 2) */
+  const void* slot_v;
+  const float* slot_bias;     /* [step][bh][S] */
+  int64_t slot_step;          /* elements between steps of slot_k / slot_v (bias: slot_step / HD) */
+  int32_t has_slots;          /* mode 1 */
+  const float* m_res;         /* [step][bh][HD][HD] fp32 (mode 1: NULL = no readout) */
+  int64_t m_step;
+  const float* gamma;         /* [HKV] */
+  const float* res_w;         /* [HD] fp32 res_norm weight */
+  float eps;
+  void* y;                    /* (b, t, h, d) at + b*y_sb + t*y_st + h*HD + d, storage dtype */
+  int64_t y_sb, y_st;
+} b3_attn_args;
+
+/*
+ * Chunk attention: joint softmax over [sinks | attractor slots | causal window]
+ * with GQA sharing, plus the M_res readout, for every chunk of a forward (mode 0)
+ * or one step's queries (mode 1).
+ * Replaces vsa_lm/config/bolt3.py:219-258 (forward chunk body) and :365-402
+ * (Bolt3Decoder.step attention + readout).
+ */
+int bolt3_chunk_attn(const b3_attn_args* a, void* stream);
+
+typedef struct {
+  int32_t dtype, B, H, HKV, HD, S;
+  const void* lin;            /* [B][lin_row_stride] packed projection row of the new token */
+  int64_t lin_row_stride;
+  const float* qn_w;          /* [HD] fp32 q/k RMSNorm weights or NULL */
+  const float* kn_w;
+  int32_t has_qk_norm;
+  float eps;                  /* q/k norm and res_norm epsilon */
+  const float* inv_freq;
+  int32_t pos;                /* position of the new token */
+  void* win_kr;               /* window ring (b, hkv, n, d) at + b*w_sb + hkv*w_sh + n*HD + d */
+  void* win_kp;
+  void* win_v;
+  int64_t w_sb, w_sh;
+  float* win_beta;            /* (b, hkv, n) at + b*wb_sb + hkv*wb_sh + n */
+  int64_t wb_sb, wb_sh;
+  float* win_pos;             /* fp32 [n] */
+  int32_t a_start, a_len;     /* older window segment */
+  int32_t b_start, b_len;     /* current segment before the new token; new token goes to b_start + b_len */
+  const void* sink_k;
+  const void* sink_v;
+  int64_t s_sb, s_sh;
+  int32_t n_sink_keys;
+  const void* slot_k;         /* [bh][S][HD] roped slot keys */
+  const void* slot_v;
+  const float* slot_bias;     /* [bh][S] */
+  int32_t has_slots;
+  const float* m_res;         /* [bh][HD][HD] */
+  const float* gamma;
+  const float* res_w;
+  void* y;                    /* [B][H*HD] storage dtype */
+} b3_decode_args;
+
+/*
+ * One-token decode step of a Bolt-3 layer: head prep for the new token, append to
+ * the window ring, attention over sinks + slots + window in fp32 scores, M_res
+ * readout.  Replaces vsa_lm/config/bolt3.py:346-402 for t_s == 1.
+ */
+int bolt3_decode(const b3_decode_args* a, void* stream);
+
+/* Library identification: returns a static string (build flags, gfx target). */
+const char* bolt3_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BOLT3_AMD_H */

@@ -1,0 +1,154 @@
+"""Write the Bolt-3 golden vectors from the reference implementation.
+
+Run in the build container only (the reference tree is not present on GPU
+boxes):  python tests/golden/make_golden.py [/root/reference]
+
+It imports vsa_lm.config.bolt3 (Bolt3Attn, Bolt3Decoder) and
+vsa_lm.config.standard (UniversalVSALM) from the reference tree on CPU, feeds
+them the seeded synthetic inputs of tests/golden/recipes.py and stores what
+they compute as safetensors files next to this script.  These pin the parts of
+the oracle that no closed form covers: the composite Bolt3Attn.forward
+(vsa_lm/config/bolt3.py:194-276), the multi-step _consolidate_functional
+trajectories (:68-192) and the Bolt3Decoder.step state machine (:335-457).
+
+Every file carries a JSON header in its metadata (torch version, case
+parameters, seed).  Parameters and inputs are regenerated from the recipes by
+the tests; each file stores a checksum of them so a drifting recipe fails
+loudly instead of comparing different problems.
+"""
+from __future__ import annotations
+
+import hashlib
+import json
+import os
+import sys
+
+import torch
+from safetensors.torch import save_file
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, HERE)
+import recipes  # noqa: E402
+
+
+def digest(tensors: dict) -> str:
+    h = hashlib.sha256()
+    for k in sorted(tensors):
+        h.update(k.encode())
+        h.update(tensors[k].detach().float().contiguous().numpy().tobytes())
+    return h.hexdigest()
+
+
+def layer_cfg(D, H, HKV, HD, theta, eps, qk_norm, qkv_bias=False):
+    return dict(dim=D, num_heads=H, num_kv_heads=HKV, head_dim=HD, rope_theta=theta, eps=eps,
+                qk_norm=qk_norm, qkv_bias=qkv_bias, rope_scaling=None)
+
+
+def record_consolidations(mod):
+    """Wrap mod._consolidate_functional to keep each call's outputs."""
+    calls = []
+    orig = mod._consolidate_functional
+
+    def wrapped(*args, **kw):
+        out = orig(*args, **kw)
+        calls.append(tuple(o.detach().clone() if torch.is_tensor(o) else o for o in out))
+        return out
+
+    mod._consolidate_functional = wrapped
+    return calls
+
+
+def fwd_case(name, cfg, B, T, seed, dtype, nondefault, clustered=None, rows_every=1, S=128, C=128):
+    from vsa_lm.config.bolt3 import Bolt3Attn
+    mod = recipes.init_module(Bolt3Attn(cfg, S=S, C=C), seed, nondefault)
+    D = cfg["dim"]
+    x = recipes.clustered_hidden(seed, B, T, D, **clustered) if clustered else recipes.hidden(seed, B, T, D)
+    inputs = {f"param.{k}": v for k, v in mod.state_dict().items()}
+    inputs["x"] = x
+    mod = mod.to(dtype)
+    calls = record_consolidations(mod)
+    with torch.no_grad():
+        y = mod(x.to(dtype))
+    tensors = {"y": y[:, ::rows_every].contiguous()}
+    for i, c in enumerate(calls):
+        ak, av, mass, util, pm, act, m_res, n_filled = c
+        tensors[f"cons{i}.mass"] = mass.contiguous()
+        tensors[f"cons{i}.util"] = util.contiguous()
+        tensors[f"cons{i}.pm"] = pm.contiguous()
+        tensors[f"cons{i}.act"] = act.to(torch.uint8).contiguous()
+        tensors[f"cons{i}.m_res_rownorm"] = m_res.norm(dim=-1).contiguous()
+        if i == len(calls) - 1:
+            tensors["final.ak"] = ak.contiguous()
+            tensors["final.av"] = av.contiguous()
+            tensors["final.m_res"] = m_res.contiguous()
+    meta = dict(case=name, torch=torch.__version__, cfg=cfg, B=B, T=T, S=S, C=C, seed=seed,
+                dtype=str(dtype).replace("torch.", ""), nondefault=nondefault, clustered=clustered,
+                rows_every=rows_every, n_consolidations=len(calls), n_filled=[int(c[7]) for c in calls],
+                inputs_sha256=digest(inputs))
+    save_file(tensors, os.path.join(HERE, f"{name}.safetensors"), metadata={"header": json.dumps(meta)})
+    merged = sum(int((c[2] > 1).sum()) for c in calls[-1:])
+    print(f"{name}: y {tuple(y.shape)} consolidations={len(calls)} n_filled={meta['n_filled']} "
+          f"slots with mass>1 at end={merged}")
+
+
+def decoder_case(name, seed, dtype, n_prompt, n_decode, B=2):
+    from vsa_lm.config.bolt3 import Bolt3Decoder
+    from vsa_lm.config.standard import UniversalVSALM
+    mcfg = dict(vocab_size=96, dim=64, num_layers=2, num_heads=4, num_kv_heads=2, intermediate=128,
+                max_T=4096, chunk_size=32, hybrid_every=0, rope_theta=10000.0, eps=1e-5, head_dim=64,
+                tie_word_embeddings=True, layer_types=["vsa", "softmax"], is_bolt3=True,
+                bolt3_S=128, bolt3_C=128, qk_norm=True)
+    model = UniversalVSALM(**mcfg)
+    shapes = [(k, tuple(v.shape)) for k, v in model.state_dict().items()]
+    model.load_state_dict(recipes.model_params(shapes, seed), strict=False)
+    recipes.init_module(model.blocks[0].vsa, seed, nondefault=True)
+    inputs = {f"param.{k}": v for k, v in model.state_dict().items()}
+    ids = recipes.tokens(seed, B, n_prompt + n_decode, mcfg["vocab_size"])
+    inputs["ids"] = ids.float()
+    model = model.to(dtype).eval()
+    dec = Bolt3Decoder(model)
+    with torch.no_grad():
+        h, states, kv = dec.prefill(ids[:, :n_prompt])
+        hs = [h[:, -1].clone()]
+        pos = n_prompt
+        for _ in range(n_decode):
+            h, states, kv = dec.step(ids[:, pos:pos + 1], pos, states, kv)
+            hs.append(h[:, -1].clone())
+            pos += 1
+    sc = kv[0]
+    tensors = {"h_last": torch.stack(hs, dim=1).contiguous(), "final.m_res": states[0].contiguous()}
+    for key in ("ak", "av", "mass", "util", "pm", "sink_k", "sink_v", "prev_kp", "cur_kp"):
+        if sc.get(key) is not None:
+            tensors[f"final.{key}"] = sc[key].contiguous()
+    tensors["final.act"] = sc["act"].to(torch.uint8).contiguous()
+    meta = dict(case=name, torch=torch.__version__, model_cfg=mcfg, seed=seed, B=B, n_prompt=n_prompt,
+                n_decode=n_decode, dtype=str(dtype).replace("torch.", ""), n_filled=int(sc.get("n_filled", 0)),
+                inputs_sha256=digest(inputs))
+    save_file(tensors, os.path.join(HERE, f"{name}.safetensors"), metadata={"header": json.dumps(meta)})
+    print(f"{name}: steps={n_decode} n_filled={meta['n_filled']}")
+
+
+CASES = [
+    # name, cfg args, B, T, seed, dtype, nondefault, clustered, rows_every
+    ("fwd_fp32_default", (64, 4, 2, 64, 10000.0, 1e-5, False, False), 2, 896, 1, "float32", False, None, 1),
+    ("fwd_fp32_eta", (64, 4, 2, 64, 10000.0, 1e-5, True, True), 2, 1000, 2, "float32", True, None, 1),
+    ("fwd_fp32_g3", (96, 6, 2, 64, 500000.0, 1e-6, True, False), 1, 1152, 7, "float32", True, None, 1),
+    ("fwd_bf16_eta", (64, 4, 2, 64, 10000.0, 1e-5, True, True), 1, 1024, 3, "bfloat16", True, None, 1),
+    ("fwd_fp32_clustered", (64, 4, 2, 64, 10000.0, 1e-5, True, False), 1, 2048, 4, "float32", True,
+     dict(n_centres=24, noise=0.12), 1),
+    ("fwd_bf16_clustered", (64, 4, 2, 64, 10000.0, 1e-5, True, False), 1, 2048, 5, "bfloat16", True,
+     dict(n_centres=24, noise=0.12), 1),
+    ("fwd_cfg1_smollm", (576, 9, 3, 64, 10000.0, 1e-5, False, False), 1, 1024, 0, "float32", False, None, 8),
+]
+
+
+def main(ref_root: str):
+    sys.path.insert(0, ref_root)
+    torch.set_num_threads(min(8, os.cpu_count() or 1))
+    for name, c, B, T, seed, dt, nd, cl, every in CASES:
+        fwd_case(name, layer_cfg(*c), B, T, seed, getattr(torch, dt), nd, cl, every)
+    decoder_case("dec_fp32", seed=6, dtype=torch.float32, n_prompt=300, n_decode=220)
+
+
+if __name__ == "__main__":
+    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference")

@@ -1,0 +1,91 @@
+"""The C ABI: the library loads without a GPU, exports every function that
+include/bolt3_amd.h declares, and the ctypes mirrors of the argument structs
+have the C layout (field offsets and sizes taken from gcc on the header)."""
+import ctypes
+import os
+import re
+import subprocess
+import tempfile
+
+import pytest
+
+from bolt3_amd import _abi as A
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "bolt3_amd.h")
+
+
+def _declared_functions():
+    txt = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|int64_t|const char\s*\*)\s*(bolt3_\w+)\s*\(", txt, re.M)))
+
+
+def test_header_declares_the_bound_functions():
+    assert _declared_functions() == sorted(A.EXPORTS)
+
+
+def test_library_loads_and_exports_everything():
+    if not os.path.exists(A.LIB_PATH):
+        pytest.fail("libbolt3_amd.so not built (run __graft_entry__.build())")
+    lib = A.load()
+    for name in _declared_functions():
+        assert hasattr(lib, name), name
+    assert b"gfx950" in lib.bolt3_version()
+
+
+def test_workspace_size_formula():
+    lib = A.load()
+    assert lib.bolt3_chain_workspace_bytes(1, 4, 8, 128, 128) == 32 * 128 * 128 * 2 + 32 * 32 * 132 * 4
+    assert lib.bolt3_chain_workspace_bytes(0, 1, 3, 64, 128) == 3 * 128 * 64 * 4 + 3 * 32 * 68 * 4
+
+
+def test_rejects_bad_arguments_without_gpu_work():
+    """Argument checks run on the host before any launch."""
+    lib = A.load()
+    a = A.ChainArgs()
+    a.B, a.HKV, a.HD, a.S, a.n_steps = 1, 1, 96, 128, 1
+    assert lib.bolt3_chain(ctypes.byref(a), None) == 1002      # unsupported head dim
+    a.HD, a.S = 128, 64
+    assert lib.bolt3_chain(ctypes.byref(a), None) == 1002      # unsupported slot count
+    a.S, a.len0 = 128, 300
+    assert lib.bolt3_chain(ctypes.byref(a), None) == 1002      # chunk longer than 256 tokens
+    a.len0 = 128
+    assert lib.bolt3_chain(ctypes.byref(a), None) == 1001      # null pointers
+    h = A.HeadsArgs()
+    assert lib.bolt3_heads(ctypes.byref(h), None) == 1001
+    t = A.AttnArgs()
+    assert lib.bolt3_chunk_attn(ctypes.byref(t), None) == 1001
+    d = A.DecodeArgs()
+    assert lib.bolt3_decode(ctypes.byref(d), None) == 1001
+
+
+STRUCTS = {"b3_heads_args": A.HeadsArgs, "b3_chain_args": A.ChainArgs, "b3_attn_args": A.AttnArgs,
+           "b3_decode_args": A.DecodeArgs}
+
+
+def _flat_fields(st, prefix=""):
+    for name, typ in st._fields_:
+        yield prefix + name, getattr(st, name).offset, ctypes.sizeof(typ)
+
+
+def test_struct_layout_matches_header():
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {"]
+    for cname, st in STRUCTS.items():
+        lines.append(f'printf("{cname} sizeof %zu\\n", sizeof({cname}));')
+        for field, _, _ in _flat_fields(st):
+            lines.append(f'printf("{cname} {field} %zu\\n", offsetof({cname}, {field}));')
+    lines.append("return 0; }")
+    with tempfile.TemporaryDirectory() as d:
+        src, exe = os.path.join(d, "probe.c"), os.path.join(d, "probe")
+        open(src, "w").write("\n".join(lines))
+        subprocess.run(["gcc", "-std=c99", src, "-o", exe], check=True)
+        out = subprocess.run([exe], capture_output=True, text=True, check=True).stdout.split("\n")
+    got = {}
+    for ln in out:
+        if ln:
+            s, f, v = ln.split()
+            got[(s, f)] = int(v)
+    for cname, st in STRUCTS.items():
+        assert got[(cname, "sizeof")] == ctypes.sizeof(st), cname
+        for field, off, _ in _flat_fields(st):
+            assert got[(cname, field)] == off, (cname, field)

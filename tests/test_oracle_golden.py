@@ -1,0 +1,82 @@
+"""Pin the CPU oracle to vectors the reference itself computed (tests/golden).
+
+The fixtures were written by tests/golden/make_golden.py from
+vsa_lm/config/bolt3.py (Bolt3Attn.forward, the _consolidate_functional
+trajectory, Bolt3Decoder.prefill/step).  In fp32 the oracle issues the same
+torch ops in the same order, so outputs and slot states match to the last bit
+on the machine that wrote them; the check allows 1e-6 relative to absorb a
+different CPU's BLAS blocking, and requires the slot decisions (activity,
+masses, positions) to be identical.
+"""
+import pytest
+import torch
+
+from oracle.bolt3_oracle import Bolt3Params, ForwardTrace, HybridRef, forward
+from helpers import build_layer, build_model, fixture, rel_err
+
+FWD = ["fwd_fp32_default", "fwd_fp32_eta", "fwd_fp32_g3", "fwd_bf16_eta", "fwd_fp32_clustered",
+       "fwd_bf16_clustered", "fwd_cfg1_smollm"]
+
+
+@pytest.mark.parametrize("name", FWD)
+def test_forward_matches_reference(name):
+    g, meta = fixture(name)
+    mod, x = build_layer(meta)
+    p = Bolt3Params.from_module(mod)
+    tr = ForwardTrace()
+    with torch.no_grad():
+        y = forward(p, x, trace=tr)
+    every = meta["rows_every"]
+    y = y[:, ::every]
+    tol = 1e-6 if meta["dtype"] == "float32" else 1e-2
+    assert rel_err(y, g["y"]) <= tol, (name, rel_err(y, g["y"]))
+    assert len(tr.states) == meta["n_consolidations"]
+    assert [s.n_filled for s in tr.states] == meta["n_filled"]
+    for i, st in enumerate(tr.states):
+        assert torch.equal(st.act.to(torch.uint8), g[f"cons{i}.act"]), (name, i)
+        assert torch.equal(st.mass, g[f"cons{i}.mass"]), (name, i)
+        assert rel_err(st.pm, g[f"cons{i}.pm"]) <= 1e-6, (name, i)
+        assert rel_err(st.util, g[f"cons{i}.util"]) <= 1e-5, (name, i)
+        assert rel_err(st.m_res.norm(dim=-1), g[f"cons{i}.m_res_rownorm"]) <= 1e-5, (name, i)
+    last = tr.states[-1]
+    assert rel_err(last.ak.float(), g["final.ak"].float()) <= 1e-6
+    assert rel_err(last.av.float(), g["final.av"].float()) <= 1e-6
+    assert rel_err(last.m_res, g["final.m_res"]) <= 1e-5
+
+
+def test_forward_fp32_bit_exact_here():
+    """On the container that wrote the fixtures the fp32 restatement is bit-identical."""
+    g, meta = fixture("fwd_fp32_eta")
+    mod, x = build_layer(meta)
+    with torch.no_grad():
+        y = forward(Bolt3Params.from_module(mod), x)
+    if not torch.equal(y, g["y"]):
+        pytest.skip(f"different BLAS rounding on this host (rel {rel_err(y, g['y']):.2e}); tolerance test covers it")
+
+
+def test_clustered_fixture_exercises_merges():
+    g, meta = fixture("fwd_fp32_clustered")
+    assert int((g[f"cons{meta['n_consolidations'] - 1}.mass"] > 1).sum()) > 50
+
+
+def test_decoder_matches_reference():
+    g, meta = fixture("dec_fp32")
+    model, ids = build_model(meta)
+    ref = HybridRef(model)
+    n_prompt = meta["n_prompt"]
+    with torch.no_grad():
+        h, state = ref.prefill(ids[:, :n_prompt])
+        hs = [h[:, -1]]
+        for i in range(meta["n_decode"]):
+            pos = n_prompt + i
+            h = ref.step(ids[:, pos:pos + 1], pos, state)
+            hs.append(h[:, -1])
+    hs = torch.stack(hs, dim=1)
+    assert rel_err(hs, g["h_last"]) <= 1e-5
+    ms, cache = state[0]
+    assert rel_err(ms, g["final.m_res"]) <= 1e-5
+    assert cache.st.n_filled == meta["n_filled"]
+    assert torch.equal(cache.st.act.to(torch.uint8), g["final.act"])
+    assert torch.equal(cache.st.mass, g["final.mass"])
+    assert rel_err(cache.st.ak.float(), g["final.ak"].reshape(cache.st.ak.shape).float()) <= 1e-6
+    assert rel_err(cache.sinks[0], g["final.sink_k"]) <= 1e-6

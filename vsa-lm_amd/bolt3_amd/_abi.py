@@ -1,0 +1,140 @@
+"""ctypes binding of the C ABI declared in include/bolt3_amd.h.
+
+The library is loaded from ``libbolt3_amd.so`` next to this file.  There is no
+fallback: if the library is missing or a call returns a non-zero status a
+RuntimeError is raised.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libbolt3_amd.so")
+
+B3_F32, B3_BF16 = 0, 1
+ERRORS = {1001: "invalid argument", 1002: "unsupported shape or dtype", 1003: "workspace too small"}
+
+LOG_ROWS, LOG_COLS = 13, 256
+LOG_FIELDS = ("rel", "score", "best", "simv", "slot", "merge", "delta", "top_tok", "bot_slot", "win", "keep",
+              "top_val", "bot_val")
+
+p = C.c_void_p
+i32 = C.c_int32
+i64 = C.c_int64
+f32 = C.c_float
+
+
+class TensorOut(C.Structure):
+    _fields_ = [("p", p), ("sb", i64), ("sh", i64)]
+
+
+class GateOut(C.Structure):
+    _fields_ = [("p", p), ("sb", i64), ("sh", i64)]
+
+
+class HeadsArgs(C.Structure):
+    _fields_ = [
+        ("dtype", i32), ("B", i32), ("T", i32), ("H", i32), ("HKV", i32), ("HD", i32),
+        ("lin", p), ("lin_row_stride", i64), ("qn_w", p), ("kn_w", p), ("has_qk_norm", i32), ("eps", f32),
+        ("inv_freq", p), ("pos0", i32),
+        ("q_raw", TensorOut), ("q_rope", TensorOut), ("k_raw", TensorOut), ("k_rope", TensorOut), ("v", TensorOut),
+        ("beta", GateOut), ("eta", GateOut), ("pos_out", p),
+    ]
+
+
+class ChainArgs(C.Structure):
+    _fields_ = [
+        ("dtype", i32), ("B", i32), ("HKV", i32), ("HD", i32), ("S", i32),
+        ("kr", p), ("kp", p), ("v", p), ("tok_bh_stride", i64), ("pos", p), ("beta", p), ("beta_bh_stride", i64),
+        ("n_steps", i32), ("off0", i32), ("len0", i32), ("step_stride", i32), ("step_len", i32), ("n_filled", i32),
+        ("ak", p), ("av", p), ("mass", p), ("util", p), ("pm", p), ("act", p), ("m_res", p),
+        ("kappa", p), ("gamma", p), ("inv_freq", p),
+        ("snap_k", p), ("snap_v", p), ("snap_bias", p), ("snap_m", p), ("log", p),
+        ("work", p), ("work_bytes", i64),
+    ]
+
+
+class AttnArgs(C.Structure):
+    _fields_ = [
+        ("dtype", i32), ("B", i32), ("H", i32), ("HKV", i32), ("HD", i32), ("S", i32), ("C", i32), ("n_sinks", i32),
+        ("mode", i32), ("n_q", i32), ("score_round", i32),
+        ("q_rope", p), ("q_raw", p), ("q_sb", i64), ("q_sh", i64),
+        ("eta", p), ("e_sb", i64), ("e_sh", i64),
+        ("win_k", p), ("win_v", p), ("w_sb", i64), ("w_sh", i64),
+        ("a_start", i32), ("a_len", i32), ("b_start", i32), ("b_len", i32),
+        ("sink_k", p), ("sink_v", p), ("s_sb", i64), ("s_sh", i64), ("n_sink_keys", i32),
+        ("slot_k", p), ("slot_v", p), ("slot_bias", p), ("slot_step", i64), ("has_slots", i32),
+        ("m_res", p), ("m_step", i64),
+        ("gamma", p), ("res_w", p), ("eps", f32),
+        ("y", p), ("y_sb", i64), ("y_st", i64),
+    ]
+
+
+class DecodeArgs(C.Structure):
+    _fields_ = [
+        ("dtype", i32), ("B", i32), ("H", i32), ("HKV", i32), ("HD", i32), ("S", i32),
+        ("lin", p), ("lin_row_stride", i64), ("qn_w", p), ("kn_w", p), ("has_qk_norm", i32), ("eps", f32),
+        ("inv_freq", p), ("pos", i32),
+        ("win_kr", p), ("win_kp", p), ("win_v", p), ("w_sb", i64), ("w_sh", i64),
+        ("win_beta", p), ("wb_sb", i64), ("wb_sh", i64), ("win_pos", p),
+        ("a_start", i32), ("a_len", i32), ("b_start", i32), ("b_len", i32),
+        ("sink_k", p), ("sink_v", p), ("s_sb", i64), ("s_sh", i64), ("n_sink_keys", i32),
+        ("slot_k", p), ("slot_v", p), ("slot_bias", p), ("has_slots", i32),
+        ("m_res", p), ("gamma", p), ("res_w", p), ("y", p),
+    ]
+
+
+EXPORTS = ("bolt3_heads", "bolt3_chain", "bolt3_chain_workspace_bytes", "bolt3_chunk_attn", "bolt3_decode",
+           "bolt3_version")
+
+_lib = None
+
+
+def load():
+    """Load the HIP library once; raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is missing: build it with __graft_entry__.build() "
+                           f"(python -m bolt3_amd.build); there is no CPU implementation")
+    lib = C.CDLL(LIB_PATH)
+    for name, st in (("bolt3_heads", HeadsArgs), ("bolt3_chain", ChainArgs), ("bolt3_chunk_attn", AttnArgs),
+                     ("bolt3_decode", DecodeArgs)):
+        fn = getattr(lib, name)
+        fn.argtypes = [C.POINTER(st), p]
+        fn.restype = C.c_int
+    lib.bolt3_chain_workspace_bytes.argtypes = [i32, i32, i32, i32, i32]
+    lib.bolt3_chain_workspace_bytes.restype = i64
+    lib.bolt3_version.argtypes = []
+    lib.bolt3_version.restype = C.c_char_p
+    _lib = lib
+    return lib
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.float32:
+        return B3_F32
+    if dt == torch.bfloat16:
+        return B3_BF16
+    raise TypeError(f"Bolt-3 HIP kernels take float32 or bfloat16 activations, got {dt}")
+
+
+def stream_of(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def call(name: str, args, device: torch.device):
+    rc = getattr(load(), name)(C.byref(args), C.c_void_p(stream_of(device)))
+    if rc != 0:
+        raise RuntimeError(f"{name} failed: {ERRORS.get(rc, f'hip error {rc}')}")
+
+
+def chain_workspace_bytes(dt: torch.dtype, B: int, HKV: int, HD: int, S: int) -> int:
+    return int(load().bolt3_chain_workspace_bytes(dtype_code(dt), B, HKV, HD, S))

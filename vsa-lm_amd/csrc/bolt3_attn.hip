@@ -1,0 +1,387 @@
+// Chunk attention over the three Bolt-3 fields plus the M_res readout.
+//
+// Replaces the body of the chunk loop of Bolt3Attn.forward
+// (vsa_lm/config/bolt3.py:219-258) for all chunks at once (mode 0), and the
+// attention + readout of Bolt3Decoder.step (:365-402) for a block of queries
+// against decoder state (mode 1).  For every query the keys are
+//   [sinks (4) | attractor slots (S, roped at their mean positions, bias
+//    kappa*log(max(mass,1)), -inf when inactive) | window: previous chunk and
+//    the current chunk up to the query (causal)]
+// under ONE softmax; probabilities read the matching values.  The readout adds
+// eta * RMSNorm(normalize(q_raw) . M_res * (1-gamma)/sqrt(HD)).
+//
+// Layout: one workgroup per (bh, chunk, query tile) with G*QW wavefronts; a
+// wavefront owns 32 queries of one query head, so the G query heads of a kv
+// head share every K/V tile staged in LDS.  Scores are computed transposed
+// (keys x queries) with 32x32 MFMAs so that each lane owns one query column:
+// the online-softmax state is per lane and only one cross-half exchange is
+// needed per reduction.
+#include "bolt3_common.h"
+#include "bolt3_amd.h"
+
+namespace b3 {
+
+constexpr int KB = 32;  // keys per LDS stage
+
+template <typename T, int HD>
+struct AttnSmem {
+  static constexpr int KS = sizeof(T) == 2 ? HD + 8 : HD + 1;   // K row stride
+  static constexpr int VS = sizeof(T) == 2 ? KB + 8 : KB + 1;   // V^T row stride
+  static constexpr int MS = HD + 8;                             // M^T (bf16 hi/lo) row stride
+  static constexpr int MF = HD + 1;                             // M (fp32) row stride
+  static constexpr int KV_BYTES = KB * KS * sizeof(T) + HD * VS * sizeof(T);
+  static constexpr int M_BYTES = sizeof(T) == 2 ? 2 * HD * MS * 2 : HD * MF * 4;
+  static constexpr int BYTES = KV_BYTES > M_BYTES ? KV_BYTES : M_BYTES;
+  alignas(16) unsigned char raw[BYTES];
+  float bias[KB];
+  __device__ T* k() { return reinterpret_cast<T*>(raw); }
+  __device__ T* vt() { return reinterpret_cast<T*>(raw + KB * KS * sizeof(T)); }
+  __device__ uint16_t* mhi() { return reinterpret_cast<uint16_t*>(raw); }
+  __device__ uint16_t* mlo() { return reinterpret_cast<uint16_t*>(raw) + HD * MS; }
+  __device__ float* mf() { return reinterpret_cast<float*>(raw); }
+};
+
+// Query fragments: lane (q = lane%32, h) holds q[q][K sub-index].
+template <typename T, int HD> struct QFrag;
+template <int HD> struct QFrag<uint16_t, HD> {
+  u16x8 v[HD / 16];
+  __device__ void load(const uint16_t* row, bool ok, int h) {
+#pragma unroll
+    for (int ks = 0; ks < HD / 16; ++ks) {
+      if (ok) v[ks] = *reinterpret_cast<const u16x8*>(row + 16 * ks + 8 * h);
+      else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[ks][i] = 0;
+      }
+    }
+  }
+  __device__ float sumsq() const {
+    float s = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < HD / 16; ++ks)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) { const float x = bf2f(v[ks][i]); s += x * x; }
+    return s;
+  }
+};
+template <int HD> struct QFrag<float, HD> {
+  float v[HD / 2];
+  __device__ void load(const float* row, bool ok, int h) {
+#pragma unroll
+    for (int ks = 0; ks < HD / 2; ++ks) v[ks] = ok ? row[2 * ks + h] : 0.f;
+  }
+  __device__ float sumsq() const {
+    float s = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < HD / 2; ++ks) s += v[ks] * v[ks];
+    return s;
+  }
+};
+
+struct Seg {
+  const void* k;
+  const void* v;
+  long long stride_b, stride_h;  // (b, hkv) strides in elements
+  int start, len;
+  int kind;                      // 0 sinks, 1 slots, 2 window (older), 3 window (current, causal)
+};
+
+template <typename T, int HD>
+__global__ void __launch_bounds__(512) attn_kernel(b3_attn_args a, int QW) {
+  __shared__ AttnSmem<T, HD> sm;
+  const int G = a.H / a.HKV;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n = lane & 31, h = lane >> 5;
+  const int g = wave / QW, qsub = wave % QW;
+  const int bh = blockIdx.z, b = bh / a.HKV, hkv = bh % a.HKV;
+  const int hq = hkv * G + g;
+  const int chunk = blockIdx.y;
+  const float scale = 1.0f / sqrtf((float)HD);
+
+  // ---- queries of this wavefront
+  int qbase, nq_chunk, qb_off;  // first query index, queries in this chunk, B-segment index of query 0
+  Seg seg[4];
+  int nseg = 0;
+  int step = -1;  // slot / M_res snapshot index
+  if (a.mode == 0) {
+    qbase = chunk * a.C;
+    nq_chunk = min(a.C, a.n_q - qbase);
+    qb_off = 0;
+    if (chunk >= 2) {
+      step = chunk - 2;
+      seg[nseg++] = Seg{a.win_k, a.win_v, a.w_sb, a.w_sh, 0, min(a.n_sinks, a.C), 0};
+      seg[nseg++] = Seg{nullptr, nullptr, 0, 0, 0, a.S, 1};
+    }
+    if (chunk >= 1) seg[nseg++] = Seg{a.win_k, a.win_v, a.w_sb, a.w_sh, (chunk - 1) * a.C, a.C, 2};
+    seg[nseg++] = Seg{a.win_k, a.win_v, a.w_sb, a.w_sh, qbase, nq_chunk, 3};
+  } else {
+    qbase = 0;
+    nq_chunk = a.n_q;
+    qb_off = a.b_len - a.n_q;
+    if (a.n_sink_keys > 0) seg[nseg++] = Seg{a.sink_k, a.sink_v, a.s_sb, a.s_sh, 0, a.n_sink_keys, 0};
+    if (a.has_slots) { seg[nseg++] = Seg{nullptr, nullptr, 0, 0, 0, a.S, 1}; step = 0; }
+    if (a.a_len > 0) seg[nseg++] = Seg{a.win_k, a.win_v, a.w_sb, a.w_sh, a.a_start, a.a_len, 2};
+    seg[nseg++] = Seg{a.win_k, a.win_v, a.w_sb, a.w_sh, a.b_start, a.b_len, 3};
+  }
+  const int qt0 = blockIdx.x * 32 * QW;          // first query of the workgroup within the chunk
+  if (qt0 >= nq_chunk) return;                   // uniform across the workgroup
+  const int qi = qt0 + 32 * qsub + n;            // this lane's query within the chunk
+  const bool qok = qi < nq_chunk;
+  const int t = qbase + qi;                      // query index in the q / y arrays
+  const int wave_qmax = qt0 + 32 * qsub + 31;    // largest query of this wavefront (for causal skipping)
+
+  const T* qrow = reinterpret_cast<const T*>(a.q_rope) + b * a.q_sb + hq * a.q_sh + (long long)t * HD;
+  QFrag<T, HD> qf;
+  qf.load(qrow, qok, h);
+
+  constexpr int NDB = HD / 32;
+  f32x16 o[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) o[db] = zero16();
+  float m_run = -INFINITY, l_run = 0.f;
+
+  const T* slot_k = a.slot_k ? reinterpret_cast<const T*>(a.slot_k) + (long long)(step < 0 ? 0 : step) * a.slot_step +
+                                   (long long)bh * a.S * HD
+                             : nullptr;
+  const T* slot_v = a.slot_v ? reinterpret_cast<const T*>(a.slot_v) + (long long)(step < 0 ? 0 : step) * a.slot_step +
+                                   (long long)bh * a.S * HD
+                             : nullptr;
+  const float* slot_b = a.slot_bias ? a.slot_bias + (long long)(step < 0 ? 0 : step) * (a.slot_step / HD) +
+                                          (long long)bh * a.S
+                                    : nullptr;
+  const int nthreads = blockDim.x;
+
+  for (int si = 0; si < nseg; ++si) {
+    const Seg sg = seg[si];
+    const T* kbase;
+    const T* vbase;
+    if (sg.kind == 1) {
+      kbase = slot_k;
+      vbase = slot_v;
+    } else {
+      kbase = reinterpret_cast<const T*>(sg.k) + b * sg.stride_b + hkv * sg.stride_h + (long long)sg.start * HD;
+      vbase = reinterpret_cast<const T*>(sg.v) + b * sg.stride_b + hkv * sg.stride_h + (long long)sg.start * HD;
+    }
+    for (int k0 = 0; k0 < sg.len; k0 += KB) {
+      // causal skip: the whole block lies after every query of the workgroup
+      const bool wg_skip = sg.kind == 3 && k0 > qb_off + qt0 + 32 * QW - 1;
+      if (wg_skip) break;
+      __syncthreads();
+      // ---- stage K (rows) and V^T (columns) of keys k0 .. k0+KB-1
+      T* sK = sm.k();
+      T* sV = sm.vt();
+      if constexpr (St<T>::is_bf16) {
+        for (int it = tid; it < KB * (HD / 8); it += nthreads) {
+          const int r = it / (HD / 8), c8 = (it % (HD / 8)) * 8;
+          u16x8 kv, vv;
+          if (k0 + r < sg.len) {
+            kv = *reinterpret_cast<const u16x8*>(kbase + (long long)(k0 + r) * HD + c8);
+            vv = *reinterpret_cast<const u16x8*>(vbase + (long long)(k0 + r) * HD + c8);
+          } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) { kv[i] = 0; vv[i] = 0; }
+          }
+          *reinterpret_cast<u16x8*>(sK + r * sm.KS + c8) = kv;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) sV[(c8 + i) * sm.VS + r] = vv[i];
+        }
+      } else {
+        for (int it = tid; it < KB * HD; it += nthreads) {
+          const int r = it / HD, c = it % HD;
+          const bool ok = k0 + r < sg.len;
+          sK[r * sm.KS + c] = ok ? kbase[(long long)(k0 + r) * HD + c] : 0.f;
+          sV[c * sm.VS + r] = ok ? vbase[(long long)(k0 + r) * HD + c] : 0.f;
+        }
+      }
+      if (tid < KB) sm.bias[tid] = (sg.kind == 1 && k0 + tid < sg.len) ? slot_b[k0 + tid] : 0.f;
+      __syncthreads();
+      // waves whose queries all precede this block of the current chunk skip it
+      if (sg.kind == 3 && k0 > qb_off + wave_qmax) continue;
+
+      // ---- S^T[key][q] = K . Q^T
+      f32x16 s = zero16();
+      if constexpr (St<T>::is_bf16) {
+#pragma unroll
+        for (int ks = 0; ks < HD / 16; ++ks) {
+          const u16x8 av = *reinterpret_cast<const u16x8*>(sK + n * sm.KS + 16 * ks + 8 * h);
+          mma_bf16(s, av, qf.v[ks]);
+        }
+      } else {
+#pragma unroll 8
+        for (int ks = 0; ks < HD / 2; ++ks) mma_f32(s, sK[n * sm.KS + 2 * ks + h], qf.v[ks]);
+      }
+      float bm = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int kr = d_row(lane, r);
+        const int kidx = k0 + kr;
+        float x = a.score_round ? St<T>::rnd(s[r]) : s[r];
+        x = mul_rn(x, scale);
+        if (sg.kind == 1) x = add_rn(x, sm.bias[kr]);
+        bool ok = kidx < sg.len;
+        if (sg.kind == 3) ok = ok && kidx <= qb_off + qi;
+        x = ok ? x : -INFINITY;
+        s[r] = x;
+        bm = fmaxf(bm, x);
+      }
+      bm = fmaxf(bm, xor32(bm));
+      const float m_new = fmaxf(m_run, bm);
+      const float alpha = m_new == -INFINITY ? 1.f : expf(m_run - m_new);
+      float ps = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = m_new == -INFINITY ? 0.f : expf(s[r] - m_new);
+        s[r] = p;
+        ps += p;
+      }
+      ps += xor32(ps);
+      l_run = l_run * alpha + ps;
+      m_run = m_new;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+      // ---- O^T[d][q] += V^T . P^T
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+        const int d = 32 * db + n;
+        if constexpr (St<T>::is_bf16) {
+#pragma unroll
+          for (int kc = 0; kc < 2; ++kc) {
+            u16x8 av, pv;
+            const u16x4 lo = *reinterpret_cast<const u16x4*>(sV + d * sm.VS + 16 * kc + 4 * h);
+            const u16x4 hi = *reinterpret_cast<const u16x4*>(sV + d * sm.VS + 16 * kc + 8 + 4 * h);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) { av[i] = lo[i]; av[4 + i] = hi[i]; }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) pv[i] = f2bf(s[8 * kc + i]);
+            mma_bf16(o[db], av, pv);
+          }
+        } else {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mma_f32(o[db], sV[d * sm.VS + d_row(lane, r)], s[r]);
+        }
+      }
+    }
+  }
+
+  // ---- normalise; y = round(O)
+  const float inv_l = l_run > 0.f ? 1.0f / l_run : 0.f;
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[db][r] = St<T>::rnd(o[db][r] * inv_l);
+
+  // ---- readout: eta * RMSNorm(normalize(q_raw) . M * (1-gamma)/sqrt(HD))
+  const float* M = nullptr;
+  if (a.m_res && step >= 0) M = a.m_res + (long long)step * a.m_step + (long long)bh * HD * HD;
+  if (a.mode == 1 && a.m_res) M = a.m_res + (long long)bh * HD * HD;
+  if (M) {
+    __syncthreads();
+    if constexpr (St<T>::is_bf16) {
+      uint16_t* mh = sm.mhi();
+      uint16_t* ml = sm.mlo();
+      for (int it = tid; it < HD * HD; it += nthreads) {
+        const int c = it / HD, d = it % HD;  // M[c][d] -> M^T[d][c]
+        const float x = M[it];
+        const uint16_t hb = f2bf(x);
+        mh[d * sm.MS + c] = hb;
+        ml[d * sm.MS + c] = f2bf(x - bf2f(hb));
+      }
+    } else {
+      float* mf = sm.mf();
+      for (int it = tid; it < HD * HD; it += nthreads) mf[(it / HD) * sm.MF + it % HD] = M[it];
+    }
+    __syncthreads();
+    const T* rrow = reinterpret_cast<const T*>(a.q_raw) + b * a.q_sb + hq * a.q_sh + (long long)t * HD;
+    QFrag<T, HD> rf;
+    rf.load(rrow, qok, h);
+    float qq = rf.sumsq();
+    qq += xor32(qq);
+    const float inv_q = 1.0f / fmaxf(sqrtf(qq), 1e-12f);
+    const float coef = div_rn(1.0f - a.gamma[hkv], sqrtf((float)HD));
+    f32x16 rr[NDB];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      rr[db] = zero16();
+      const int d = 32 * db + n;
+      if constexpr (St<T>::is_bf16) {
+#pragma unroll
+        for (int ks = 0; ks < HD / 16; ++ks) {
+          const u16x8 ah = *reinterpret_cast<const u16x8*>(sm.mhi() + d * sm.MS + 16 * ks + 8 * h);
+          const u16x8 al = *reinterpret_cast<const u16x8*>(sm.mlo() + d * sm.MS + 16 * ks + 8 * h);
+          mma_bf16(rr[db], ah, rf.v[ks]);
+          mma_bf16(rr[db], al, rf.v[ks]);
+        }
+      } else {
+#pragma unroll 8
+        for (int ks = 0; ks < HD / 2; ++ks) mma_f32(rr[db], sm.mf()[(2 * ks + h) * sm.MF + d], rf.v[ks]);
+      }
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float y = mul_rn(rr[db][r] * inv_q, coef);
+        rr[db][r] = y;
+        ss += y * y;
+      }
+    ss += xor32(ss);
+    const float rs = 1.0f / sqrtf(div_rn(ss, (float)HD) + a.eps);
+    const float eta = qok ? a.eta[b * a.e_sb + hq * a.e_sh + t] : 0.f;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int d = 32 * db + d_row(lane, r);
+        const float ymn = mul_rn(mul_rn(rr[db][r], rs), a.res_w[d]);
+        o[db][r] = St<T>::rnd(add_rn(o[db][r], St<T>::rnd(mul_rn(eta, ymn))));
+      }
+  }
+
+  // ---- write y[b][t][hq][d]
+  if (qok) {
+    T* yrow = reinterpret_cast<T*>(a.y) + b * a.y_sb + (long long)t * a.y_st + hq * HD;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) yrow[32 * db + d_row(lane, r)] = St<T>::from_f(o[db][r]);
+  }
+}
+
+template <typename T, int HD>
+static int launch_attn(const b3_attn_args& a, hipStream_t st) {
+  const int G = a.H / a.HKV;
+  const int QW = G <= 4 ? 2 : 1;
+  const int per_wg = 32 * QW;
+  const int n_chunks = a.mode == 0 ? (a.n_q + a.C - 1) / a.C : 1;
+  const int qlen = a.mode == 0 ? a.C : a.n_q;
+  dim3 grid((qlen + per_wg - 1) / per_wg, n_chunks, a.B * a.HKV);
+  hipLaunchKernelGGL((attn_kernel<T, HD>), grid, dim3(64 * G * QW), 0, st, a, QW);
+  return (int)hipGetLastError();
+}
+
+}  // namespace b3
+
+extern "C" int bolt3_chunk_attn(const b3_attn_args* a, void* stream) {
+  if (!a || a->B <= 0 || a->HKV <= 0 || a->n_q <= 0 || a->H % a->HKV != 0) return B3_ERR_ARG;
+  if (a->H / a->HKV > 8 || (a->HD != 64 && a->HD != 128)) return B3_ERR_UNSUPPORTED;
+  if (!a->q_rope || !a->win_k || !a->win_v || !a->y || !a->gamma || !a->res_w || !a->eta) return B3_ERR_ARG;
+  if (a->mode == 0) {
+    if (a->C <= 0 || a->n_sinks < 0) return B3_ERR_ARG;
+    if (a->n_q > 2 * a->C && (!a->slot_k || !a->slot_v || !a->slot_bias)) return B3_ERR_ARG;
+  } else if (a->mode == 1) {
+    if (a->b_len < a->n_q || a->n_q > 256) return B3_ERR_ARG;
+    if (a->has_slots && (!a->slot_k || !a->slot_v || !a->slot_bias)) return B3_ERR_ARG;
+    if (a->n_sink_keys > 0 && (!a->sink_k || !a->sink_v)) return B3_ERR_ARG;
+  } else {
+    return B3_ERR_ARG;
+  }
+  if (a->m_res && !a->q_raw) return B3_ERR_ARG;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (a->dtype == B3_F32) return a->HD == 64 ? b3::launch_attn<float, 64>(*a, st) : b3::launch_attn<float, 128>(*a, st);
+  if (a->dtype == B3_BF16)
+    return a->HD == 64 ? b3::launch_attn<uint16_t, 64>(*a, st) : b3::launch_attn<uint16_t, 128>(*a, st);
+  return B3_ERR_UNSUPPORTED;
+}

@@ -1,0 +1,126 @@
+// Shared device helpers for the Bolt-3 gfx950 kernels.
+//
+// Matrix products use the CDNA3/CDNA4 32x32 MFMA family.  For every variant
+// used here the accumulator ("D") layout is the same: lane l of the 64-wide
+// wavefront holds column n = l % 32 and rows
+//     m(l, r) = 8 * (r / 4) + 4 * (l / 32) + (r % 4),   r = 0..15.
+// The A operand holds row m = l % 32 and the B operand column n = l % 32; both
+// carry the same K sub-index k(l, i), so any K permutation that A and B agree
+// on gives the same product.  bf16 products are exact in fp32, which lets a
+// bf16 operand pair reproduce fp32 dot products of bf16 data bit-for-bit up to
+// summation order.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace b3 {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+
+constexpr int WAVE = 64;
+
+// ---------------------------------------------------------------- bf16 <-> f32
+
+__device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
+
+// Round-to-nearest-even, NaN kept quiet (same rule as torch's fp32 -> bf16 cast).
+__device__ __forceinline__ uint16_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float round_bf(float f) { return bf2f(f2bf(f)); }
+
+// Storage-type traits: T is float (fp32 modules) or uint16_t holding bf16 bits.
+template <typename T> struct St;
+template <> struct St<float> {
+  static __device__ __forceinline__ float ld(const float* p) { return *p; }
+  static __device__ __forceinline__ float to_f(float v) { return v; }
+  static __device__ __forceinline__ float from_f(float v) { return v; }
+  static __device__ __forceinline__ float rnd(float v) { return v; }   // rounding to storage precision
+  static constexpr bool is_bf16 = false;
+};
+template <> struct St<uint16_t> {
+  static __device__ __forceinline__ float ld(const uint16_t* p) { return bf2f(*p); }
+  static __device__ __forceinline__ float to_f(uint16_t v) { return bf2f(v); }
+  static __device__ __forceinline__ uint16_t from_f(float v) { return f2bf(v); }
+  static __device__ __forceinline__ float rnd(float v) { return round_bf(v); }
+  static constexpr bool is_bf16 = true;
+};
+
+// IEEE single ops that the compiler must not contract into FMAs (the
+// reference evaluates these as separate tensor ops).
+__device__ __forceinline__ float mul_rn(float a, float b) { return __fmul_rn(a, b); }
+__device__ __forceinline__ float add_rn(float a, float b) { return __fadd_rn(a, b); }
+__device__ __forceinline__ float sub_rn(float a, float b) { return __fsub_rn(a, b); }
+__device__ __forceinline__ float div_rn(float a, float b) { return __fdiv_rn(a, b); }
+
+// ---------------------------------------------------------------- MFMA
+
+__device__ __forceinline__ int d_row(int lane, int r) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
+
+__device__ __forceinline__ f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = 0.f;
+  return z;
+}
+
+// D += A * B for one K=16 step with bf16 operands given as raw bf16 bits.
+__device__ __forceinline__ void mma_bf16(f32x16& acc, const u16x8& a, const u16x8& b) {
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
+                                                 acc, 0, 0, 0);
+}
+
+// D += A * B for one K=2 step with fp32 operands.
+__device__ __forceinline__ void mma_f32(f32x16& acc, float a, float b) {
+  acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc, 0, 0, 0);
+}
+
+// Split fp32 values into bf16 hi + bf16 lo (hi + lo carries ~16 mantissa bits).
+__device__ __forceinline__ void split8(const float* v, u16x8& hi, u16x8& lo) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    uint16_t h = f2bf(v[i]);
+    hi[i] = h;
+    lo[i] = f2bf(v[i] - bf2f(h));
+  }
+}
+
+// ---------------------------------------------------------------- reductions
+
+__device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32, 64); }
+__device__ __forceinline__ int xor32i(int v) { return __shfl_xor(v, 32, 64); }
+
+template <typename F>
+__device__ __forceinline__ float wave_reduce(float v, F op) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = op(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+  return wave_reduce(v, [](float a, float b) { return a + b; });
+}
+
+// Ordering used by every "largest first" selection: NaN ranks above numbers
+// (torch.topk / torch.max treat NaN as the largest value); among equal values
+// the lower index wins.
+__device__ __forceinline__ bool ranks_before_desc(float a, int ia, float b, int ib) {
+  const bool na = a != a, nb = b != b;
+  if (na || nb) return na && (!nb || ia < ib);
+  return a > b || (a == b && ia < ib);
+}
+// "smallest first" (torch.topk(largest=False)): NaN ranks last.
+__device__ __forceinline__ bool ranks_before_asc(float a, int ia, float b, int ib) {
+  const bool na = a != a, nb = b != b;
+  if (na || nb) return nb && (!na || ia < ib);
+  return a < b || (a == b && ia < ib);
+}
+
+}  // namespace b3

@@ -103,6 +103,19 @@ def gamma_delta(log_gamma: torch.Tensor) -> torch.Tensor:
     return (0.999 * torch.sigmoid(log_gamma)).clamp(1e-3, 0.999).float()
 
 
+def _select(x: torch.Tensor, k: int, largest: bool, ties: str):
+    """Top-k along the last dim.  ties="torch": torch.topk, the reference's own call, whose
+    order among exactly equal values is implementation-defined (introsort / nth_element on
+    CPU).  ties="index": exact ties resolved by the lower index (a stable sort) -- the rule the
+    HIP kernel uses.  Both put NaN first when largest and last otherwise."""
+    if ties == "torch":
+        return torch.topk(x, k=k, dim=-1, largest=largest)
+    if ties != "index":
+        raise ValueError(ties)
+    v, i = torch.sort(x, dim=-1, descending=largest, stable=True)
+    return v[..., :k], i[..., :k]
+
+
 def _expand_kv(t: torch.Tensor, groups: int) -> torch.Tensor:
     """[b, hkv, n, d] -> [b, hkv*groups, n, d]; query head h reads kv head h // groups."""
     return t if groups == 1 else t.repeat_interleave(groups, dim=1)
@@ -203,6 +216,17 @@ class SlotState:
                          self.pm.clone(), self.act.clone(), self.m_res.clone(), self.n_filled)
 
 
+def slot_bias(p: Bolt3Params, st: SlotState, b: int) -> torch.Tensor:
+    """Attention bias of the slots, kappa*log(max(mass,1)), -inf when inactive: [bh, S] fp32
+    (vsa_lm/config/bolt3.py:238-241)."""
+    kap = p.kappa.float().repeat(b).view(-1, 1)
+    return (kap * torch.log(st.mass.clamp_min(1.0))).masked_fill(~st.act, float("-inf"))
+
+
+def slot_keys(p: Bolt3Params, st: SlotState, b: int) -> torch.Tensor:
+    return _slot_keys(p, st, b)
+
+
 def _slot_keys(p: Bolt3Params, st: SlotState, b: int) -> torch.Tensor:
     """Attractor keys roped at their mean positions, [bh, S, HD] in storage dtype."""
     ak = st.ak.view(b, p.HKV, p.S, p.HD)
@@ -221,12 +245,13 @@ def _retrieval(p, st, b, kp, v32, dt, bias, mask_inactive):
 
 
 def consolidate(p: Bolt3Params, st: SlotState | None, kr, kp, v, pos, beta, gam, b: int,
-                log: dict | None = None) -> SlotState:
+                log: dict | None = None, ties: str = "torch") -> SlotState:
     """One consolidation of a chunk that left the window (vsa_lm/config/bolt3.py:68-192).
 
     kr/kp/v: [bh, l, HD] storage dtype (un-roped, roped keys, values); pos: [l] or
     [bh, l] fp32 positions; beta: [bh, l]; gam: [HKV] fp32.  Returns the new state.
-    ``log`` (optional dict) receives the per-token / per-slot decisions.
+    ``log`` (optional dict) receives the per-token / per-slot decisions; ``ties`` selects
+    the order among exactly equal scores (see ``_select``).
     """
     bh, l, hd = kr.shape
     dt = kr.dtype
@@ -255,7 +280,7 @@ def consolidate(p: Bolt3Params, st: SlotState | None, kr, kp, v, pos, beta, gam,
             else:
                 score = F.normalize(v32, dim=-1).var(dim=-1)
                 init_u = torch.full((bh, l), 0.15)
-            picked = torch.topk(score, k=m, dim=-1, largest=True).indices      # [bh, m]
+            picked = _select(score, m, True, ties)[1]                          # [bh, m]
         slots = torch.arange(st.n_filled, st.n_filled + m).expand(bh, m)
         st.ak[rows, slots] = kr[rows, picked]
         st.av[rows, slots] = v[rows, picked]
@@ -304,8 +329,8 @@ def consolidate(p: Bolt3Params, st: SlotState | None, kr, kp, v, pos, beta, gam,
         keep = st.util * (1.0 - pair.max(dim=-1).values.clamp(0.0, 0.98))
         cand = torch.where(merge, torch.full_like(score, -1e9), score)
         kc = min(l, S)
-        tv, tj = torch.topk(cand, k=kc, dim=-1, largest=True)
-        bv, bs = torch.topk(keep, k=kc, dim=-1, largest=False)
+        tv, tj = _select(cand, kc, True, ties)
+        bv, bs = _select(keep, kc, False, ties)
         win = (tv > bv) & (tv > -1e8)
         inserted = torch.zeros(bh, l, dtype=torch.bool)
         inserted[rows, tj] = win
@@ -389,9 +414,11 @@ class ForwardTrace:
     states: list = field(default_factory=list)   # SlotState after each consolidation
     logs: list = field(default_factory=list)     # decision log of each consolidation
     chunks: list = field(default_factory=list)   # (kr, kp, v, pos, beta) consolidated, [bh, l, HD]
+    y_pre: torch.Tensor | None = None            # attention + readout before o_proj, [b, H, T, HD]
+    heads: tuple | None = None                   # (q_raw, q_rope, k_raw, k_rope, v, beta, eta)
 
 
-def forward(p: Bolt3Params, x: torch.Tensor, trace: ForwardTrace | None = None) -> torch.Tensor:
+def forward(p: Bolt3Params, x: torch.Tensor, trace: ForwardTrace | None = None, ties: str = "torch") -> torch.Tensor:
     """Bolt3Attn.forward (vsa_lm/config/bolt3.py:194-276).  Returns [b, T, D]."""
     b, T, _ = x.shape
     q_raw, k_raw, v_all, beta_all, eta_all = project(p, x)
@@ -429,7 +456,7 @@ def forward(p: Bolt3Params, x: torch.Tensor, trace: ForwardTrace | None = None) 
                 chunk = (flat(k_raw[:, :, a:z]), flat(k_rope[:, :, a:z]), flat(v_all[:, :, a:z]),
                          torch.arange(a, z, dtype=torch.float32), flat(beta_all[:, :, a:z]))
                 log = {} if trace is not None else None
-                st = consolidate(p, st, *chunk, gam, b, log=log)
+                st = consolidate(p, st, *chunk, gam, b, log=log, ties=ties)
                 if trace is not None:
                     trace.states.append(st.clone())
                     trace.logs.append(log)
@@ -437,6 +464,9 @@ def forward(p: Bolt3Params, x: torch.Tensor, trace: ForwardTrace | None = None) 
             prev = (s0, e0)
 
     y = torch.cat(ys, dim=2)
+    if trace is not None:
+        trace.y_pre = y
+        trace.heads = (q_raw, q_rope, k_raw, k_rope, v_all, beta_all, eta_all)
     return F.linear(y.transpose(1, 2).reshape(b, T, p.H * p.HD), p.wo.to(y.dtype))
 
 
@@ -452,7 +482,7 @@ class LayerCache:
 
 
 def layer_step(p: Bolt3Params, h: torch.Tensor, pos_start: int, m_state: torch.Tensor, cache: LayerCache,
-               log: list | None = None):
+               log: list | None = None, ties: str = "torch"):
     """Bolt-3 branch of Bolt3Decoder.step for one layer (vsa_lm/config/bolt3.py:343-425).
 
     h: normed input [b, t, D].  m_state: M_res [b, HKV, HD, HD] fp32.  Returns
@@ -498,7 +528,8 @@ def layer_step(p: Bolt3Params, h: torch.Tensor, pos_start: int, m_state: torch.T
                 st_in.m_res = m_state.reshape(bh, p.HD, p.HD).clone()
             lg = {} if log is not None else None
             cache.st = consolidate(p, st_in, kr_.reshape(bh, n, p.HD), kp_.reshape(bh, n, p.HD),
-                                   v_.reshape(bh, n, p.HD), pos_.reshape(n), b_.reshape(bh, n), gam, b, log=lg)
+                                   v_.reshape(bh, n, p.HD), pos_.reshape(n), b_.reshape(bh, n), gam, b, log=lg,
+                                   ties=ties)
             if log is not None:
                 log.append(lg)
             m_state = cache.st.m_res.view(b, p.HKV, p.HD, p.HD)
@@ -512,9 +543,10 @@ class HybridRef:
     UniversalVSALM attribute names (embed_tokens, blocks[i].{norm1,norm2,mlp,vsa|attn},
     norm, lm_head)."""
 
-    def __init__(self, model, C: int = 128):
+    def __init__(self, model, C: int = 128, ties: str = "torch"):
         self.model = model
         self.C = C
+        self.ties = ties
         self.params = {}
         for li, blk in enumerate(model.blocks):
             if hasattr(blk, "vsa"):
@@ -539,7 +571,7 @@ class HybridRef:
             h = blk.norm1(x)
             if li in self.params:
                 ms, cache = state[li]
-                _, out, ms = layer_step(self.params[li], h, pos_start, ms, cache)
+                _, out, ms = layer_step(self.params[li], h, pos_start, ms, cache, ties=self.ties)
                 state[li][0] = ms
                 x = x + out
             else:

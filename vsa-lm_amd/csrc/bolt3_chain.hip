@@ -676,7 +676,9 @@ __global__ void __launch_bounds__(NT) chain_kernel(b3_chain_args a) {
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int row = 32 * mb + d_row(lane, r);
-            const float c = row == col ? -1.0f : acc[r] * sm.inv_nak[row] * sm.inv_nak[col];
+            // one rounded product of the two inverse norms keeps the matrix bitwise symmetric,
+            // so mutual nearest slots (equal utility) get bit-equal keep values as in the reference
+            const float c = row == col ? -1.0f : acc[r] * (sm.inv_nak[row] * sm.inv_nak[col]);
             has_nan |= (c != c);
             mx = fmaxf(mx, c);
           }

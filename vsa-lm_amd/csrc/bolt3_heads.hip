@@ -53,7 +53,7 @@ __global__ void __launch_bounds__(256) heads_kernel(b3_heads_args a) {
 #pragma unroll
     for (int o = HALF / 2; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
     if (live && kind < 2 && a.has_qk_norm) {
-      const T* w = reinterpret_cast<const T*>(kind == 0 ? a.qn_w : a.kn_w);
+      const float* w = kind == 0 ? a.qn_w : a.kn_w;
       const float r = 1.0f / sqrtf(div_rn(ss, (float)HD) + a.eps);
       x0 = St<T>::rnd(mul_rn(mul_rn(x0, r), w[i]));
       x1 = St<T>::rnd(mul_rn(mul_rn(x1, r), w[i + HALF]));

@@ -1,0 +1,232 @@
+#!/usr/bin/env python3
+"""Bolt-3 Dual-Field attention on one MI355X: prefill tokens/s, decode us/step, roofline.
+
+Workload ("cfg2"): one Bolt3Attn layer of Qwen3-4B shape
+(hidden 2560, 32 query / 8 kv heads, head_dim 128, RoPE theta 1e6, q/k norm,
+C=128, S=128), chunked forward over B=4 x T=4096 tokens; bf16 projections and
+activations, fp32 Bolt-3 parameters at their default init and fp32 state;
+hidden ~N(0,1), projection weights ~N(0,0.02) (synthetic, seeded).
+
+Decode (configs[2], "cfg3"): 64 sequences whose layer state was built by the
+decoder's chunked step over 8192 synthetic tokens, then single-token steps
+with fresh hidden ~N(0,1).  Several independent state sets are stepped in
+turn so that one round touches more than the 256 MB Infinity Cache; each set
+sees consecutive steps (consolidation every 128 of them).
+
+One JSON line on stdout.  ``value`` is prefill tokens/s of the whole forward
+(projections + HIP kernels + o_proj) with inputs resident in HBM.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+for _p in (REPO, os.path.join(REPO, "vsa-lm_amd"), os.path.join(REPO, "tests", "golden")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "Bolt3Attn prefill tokens/s + decode µs/step (Qwen3-4B layer); % roofline"
+PEAK_BF16 = 2.5e15        # dense bf16 MFMA, FLOP/s
+PEAK_HBM = 8.0e12         # HBM3E, B/s
+CFG = dict(dim=2560, num_heads=32, num_kv_heads=8, head_dim=128, rope_theta=1e6, eps=1e-6, qk_norm=True)
+B, T = 4, 4096
+SEED = 21
+
+
+def prefill_flops(b, t, D=2560, H=32, HKV=8, HD=128, C=128):
+    """Algorithmic FLOPs of one forward, split per part (dense attention rectangle)."""
+    n_chunks = (t + C - 1) // C
+    proj = 2 * b * t * D * (H * HD + 2 * HKV * HD + HKV + H) + 2 * b * t * H * HD * D
+    keys = sum(128 if c == 0 else 256 if c == 1 else 4 + 128 + 256 for c in range(n_chunks))
+    attn = 4 * b * H * C * HD * keys
+    readout = 2 * b * H * C * HD * HD * max(0, n_chunks - 2)
+    # consolidation: per steady step and bh, 5 HD-deep [C x S] / [C x C] products + 2 M_res products
+    steady = max(0, n_chunks - 4)
+    cons = b * HKV * steady * 2 * (5 * C * 128 * HD + 2 * C * HD * HD)
+    return dict(proj=proj, attn=attn, readout=readout, consolidation=cons)
+
+
+def build_layer(dev):
+    import torch
+    import recipes
+    from bolt3_amd import Bolt3Attn
+    mod = recipes.init_module(Bolt3Attn(CFG), SEED, nondefault=False)
+    for n, prm in mod.named_parameters():    # checkpoint layout: bf16 projections / norms, fp32 Bolt-3 params
+        if n.split(".")[0] in ("q_proj", "k_proj", "v_proj", "o_proj", "q_norm", "k_norm"):
+            prm.data = prm.data.to(torch.bfloat16)
+    return mod, mod.to(dev) if dev is not None else mod
+
+
+def bench_prefill(mod, dev, steps, warmup):
+    import torch
+    from bolt3_amd import _abi
+    g = torch.Generator(device=dev).manual_seed(SEED)
+    x = torch.randn(B, T, CFG["dim"], generator=g, device=dev).to(torch.bfloat16)
+    with torch.no_grad():
+        for _ in range(warmup):
+            mod(x)
+        torch.cuda.synchronize()
+        _abi.set_timing(True)
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            mod(x)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        kt = _abi.timings()
+        _abi.set_timing(False)
+    ms = (t1 - t0) * 1e3 / steps
+    kern = {k: sum(v) / len(v) for k, v in kt.items()}
+    return ms, kern
+
+
+def bench_decode(dev, n_sets, n_steps, prefill_tokens=8192, batch=64):
+    import torch
+    from bolt3_amd import Bolt3Decoder, Bolt3LayerState, HybridLM, _abi
+    mod = build_layer(dev)[1]
+    model = HybridLM(vocab_size=8, dim=CFG["dim"], num_layers=0, num_heads=32, num_kv_heads=8,
+                     intermediate=8, layer_types=[]).to(dev)
+    dec = Bolt3Decoder(model)
+    bf = torch.bfloat16
+    g = torch.Generator(device=dev).manual_seed(SEED + 1)
+    sets = []
+    with torch.no_grad():
+        for _ in range(n_sets):
+            st = Bolt3LayerState(mod, batch, dev, bf)
+            m = torch.zeros(batch, 8, 128, 128, device=dev)
+            for c in range(prefill_tokens // mod.C):
+                h = torch.randn(batch, mod.C, CFG["dim"], generator=g, device=dev).to(bf)
+                dec._bolt3_layer(mod, h, c * mod.C, m, st)
+            sets.append((st, m))
+        torch.cuda.synchronize()
+        hs = torch.randn(n_steps, batch, 1, CFG["dim"], generator=g, device=dev).to(bf)
+        win_lens = []
+        _abi.set_timing(True)
+        t0 = time.perf_counter()
+        for s in range(n_steps):
+            for st, m in sets:
+                win_lens.append(st.prev[1] + st.cur[1] + 1)
+                dec._bolt3_layer(mod, hs[s], prefill_tokens + s, m, st)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        kt = _abi.timings()
+        _abi.set_timing(False)
+    calls = n_steps * n_sets
+    step_us = (t1 - t0) * 1e6 / calls
+    dec_ms = kt.get("bolt3_decode", [])
+    cons_ms = kt.get("bolt3_chain", [])
+    avg_win = sum(win_lens) / len(win_lens)
+    # algorithmic bytes of one decode launch (per sequence and kv head, bf16 keys/values, fp32 M_res):
+    # new-token projection row slice, sinks, slot keys+values+bias, window keys+values, M_res, writes
+    per_bh = (6 * 128 * 2 + 2 * 4 * 128 * 2 + 2 * 128 * 128 * 2 + 128 * 4 + 2 * avg_win * 128 * 2
+              + 128 * 128 * 4 + 3 * 128 * 2 + 4 * 128 * 2)
+    bytes_launch = per_bh * batch * 8
+    dec_avg = sum(dec_ms) / max(1, len(dec_ms))
+    return dict(
+        batch=batch, prefill_tokens=prefill_tokens, state_sets=n_sets, steps_per_set=n_steps,
+        layer_step_us=round(step_us, 2),
+        decode_kernel_us=round(dec_avg * 1e3, 2),
+        consolidation_us=round(sum(cons_ms) / max(1, len(cons_ms)) * 1e3, 2) if cons_ms else None,
+        consolidations=len(cons_ms),
+        avg_window=round(avg_win, 1),
+        decode_kernel_bytes=int(bytes_launch),
+        decode_kernel_GBps=round(bytes_launch / (dec_avg * 1e-3) / 1e9, 1),
+        decode_kernel_frac_hbm=round(bytes_launch / (dec_avg * 1e-3) / PEAK_HBM, 4),
+        tokens_per_s=round(batch * 1e6 / step_us, 1),
+    )
+
+
+def cpu_baseline(sample_T=4096):
+    """The CPU oracle (torch restatement of the reference) on one sequence of the workload."""
+    import torch
+    import recipes
+    from oracle import bolt3_oracle as O
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    mod = build_layer(None)[0]
+    p = O.Bolt3Params.from_module(mod)
+    x = recipes.hidden(SEED, 1, sample_T, CFG["dim"]).to(torch.bfloat16)
+    with torch.no_grad():
+        O.forward(p, x[:, :256])
+        t0 = time.perf_counter()
+        O.forward(p, x)
+        dt = time.perf_counter() - t0
+    return dict(value=round(sample_T / dt, 1), unit="tokens/s", cores=cores, kind="port",
+                sample=f"oracle/bolt3_oracle.forward on B=1 T={sample_T} of the cfg2 workload (bf16, "
+                       f"torch CPU, {cores} threads, {platform.processor() or platform.machine()}), "
+                       f"{dt:.1f} s")
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--decode-steps", type=int, default=256)
+    ap.add_argument("--decode-sets", type=int, default=4)
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}, WORLD_SIZE {world}): the Bolt-3 path "
+              f"shards over (batch, kv-head) rows with no exchange, so N GPUs = N independent copies of this run.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    dev = torch.device("cuda:0")
+    _, mod = build_layer(dev)
+    ms, kern = bench_prefill(mod, dev, args.steps, args.warmup)
+    fl = prefill_flops(B, T)
+    total = sum(fl.values())
+    kernels = {
+        "bolt3_chunk_attn": dict(ms=round(kern.get("bolt3_chunk_attn", 0), 4), flops=fl["attn"] + fl["readout"]),
+        "bolt3_chain": dict(ms=round(kern.get("bolt3_chain", 0), 4), flops=fl["consolidation"]),
+        "bolt3_heads": dict(ms=round(kern.get("bolt3_heads", 0), 4), flops=0),
+    }
+    dom = max(kernels, key=lambda k: kernels[k]["ms"])
+    d = kernels[dom]
+    if dom == "bolt3_heads":
+        bytes_ = B * T * (6184 * 2 + (32 * 2 + 8 * 3) * 128 * 2 + 40 * 4)
+        roof = dict(bound="hbm", achieved=round(bytes_ / (d["ms"] * 1e-3) / 1e9, 1), peak=8000.0, unit="GB/s",
+                    frac=round(bytes_ / (d["ms"] * 1e-3) / PEAK_HBM, 4), traffic=None)
+    else:
+        ach = d["flops"] / (d["ms"] * 1e-3)
+        roof = dict(bound="mfma", achieved=round(ach / 1e12, 2), peak=PEAK_BF16 / 1e12, unit="TFLOP/s",
+                    frac=round(ach / PEAK_BF16, 4), traffic=None)
+    roof["kernel"] = dom
+    out = {
+        "metric": METRIC,
+        "value": round(B * T / (ms * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "cfg2: Bolt3Attn chunked forward, Qwen3-4B layer shape (hidden 2560, 32/8 heads, "
+                               "head_dim 128, C=128, S=128), bf16 projections, fp32 Bolt-3 params and state",
+                   "global_batch": B, "seq_len": T, "parallelism": "none (1 GPU)"},
+        "roofline": roof,
+        "whole_forward": dict(flops=total, tflops=round(total / (ms * 1e-3) / 1e12, 2),
+                              frac_bf16_peak=round(total / (ms * 1e-3) / PEAK_BF16, 4)),
+        "kernels": kernels,
+    }
+    if not args.no_decode:
+        out["decode"] = bench_decode(dev, args.decode_sets, args.decode_steps)
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

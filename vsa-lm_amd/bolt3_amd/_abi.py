@@ -130,10 +130,34 @@ def stream_of(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
+_timers: dict | None = None
+
+
+def set_timing(enabled: bool):
+    """Record a HIP event pair around every entry-point launch (on the launch stream) when
+    enabled; ``timings()`` then returns {entry point: [milliseconds per launch]}."""
+    global _timers
+    _timers = {} if enabled else None
+
+
+def timings() -> dict:
+    if _timers is None:
+        return {}
+    torch.cuda.synchronize()
+    return {k: [s.elapsed_time(e) for s, e in v] for k, v in _timers.items()}
+
+
 def call(name: str, args, device: torch.device):
-    rc = getattr(load(), name)(C.byref(args), C.c_void_p(stream_of(device)))
+    stream = torch.cuda.current_stream(device)
+    if _timers is not None:
+        ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+        ev[0].record(stream)
+    rc = getattr(load(), name)(C.byref(args), C.c_void_p(stream.cuda_stream))
     if rc != 0:
         raise RuntimeError(f"{name} failed: {ERRORS.get(rc, f'hip error {rc}')}")
+    if _timers is not None:
+        ev[1].record(stream)
+        _timers.setdefault(name, []).append(ev)
 
 
 def chain_workspace_bytes(dt: torch.dtype, B: int, HKV: int, HD: int, S: int) -> int:

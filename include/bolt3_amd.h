@@ -102,7 +102,8 @@ typedef struct {
   /* optional outputs after every step (NULL to skip), packed per step: snap_k / snap_v
      [n_steps][B*HKV][S][HD] roped slot keys and slot values (storage dtype), snap_bias
      [n_steps][B*HKV][S] attention bias kappa*log(max(mass,1)) (-inf for inactive slots),
-     snap_m [n_steps][B*HKV][HD][HD] M_res */
+     snap_m [n_steps][B*HKV] blocks of HD*HD floats holding M_res: fp32 storage M[c][d];
+     bf16 storage M^T[d][c] split into bf16 hi followed by bf16 lo */
   void* snap_k;
   void* snap_v;
   float* snap_bias;
@@ -147,8 +148,10 @@ typedef struct {
   const float* slot_bias;     /* [step][bh][S] */
   int64_t slot_step;          /* elements between steps of slot_k / slot_v (bias: slot_step / HD) */
   int32_t has_slots;          /* mode 1 */
-  const float* m_res;         /* [step][bh][HD][HD] fp32 (mode 1: NULL = no readout) */
-  int64_t m_step;
+  const float* m_res;         /* [step][bh] blocks of HD*HD floats (mode 1: NULL = no readout) */
+  int64_t m_step;             /* floats between steps */
+  int32_t m_split;            /* 0: block is M[c][d] fp32; 1 (bf16 only): block is M^T[d][c] as bf16 hi
+                                 then bf16 lo (the chain's snap_m layout for bf16 storage) */
   const float* gamma;         /* [HKV] */
   const float* res_w;         /* [HD] fp32 res_norm weight */
   float eps;

@@ -35,8 +35,10 @@ def test_library_loads_and_exports_everything():
 
 def test_workspace_size_formula():
     lib = A.load()
-    assert lib.bolt3_chain_workspace_bytes(1, 4, 8, 128, 128) == 32 * 128 * 128 * 2 + 32 * 32 * 132 * 4
-    assert lib.bolt3_chain_workspace_bytes(0, 1, 3, 64, 128) == 3 * 128 * 64 * 4 + 3 * 32 * 68 * 4
+    # per bh: roped slot keys + M^T fp32 + M^T bf16 hi and lo + two fp32 [HD][33] tiles
+    per_bh = lambda es, hd: 128 * hd * es + hd * hd * 4 + 2 * hd * hd * 2 + 2 * hd * 33 * 4
+    assert lib.bolt3_chain_workspace_bytes(1, 4, 8, 128, 128) == 32 * per_bh(2, 128)
+    assert lib.bolt3_chain_workspace_bytes(0, 1, 3, 64, 128) == 3 * per_bh(4, 64)
 
 
 def test_rejects_bad_arguments_without_gpu_work():

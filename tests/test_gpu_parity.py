@@ -268,7 +268,7 @@ def test_attention_from_oracle_states(name, gpu):
     snap_k = torch.stack([O.slot_keys(p, s, b) for s in tr.states])
     snap_v = torch.stack([s.av for s in tr.states])
     snap_b = torch.stack([O.slot_bias(p, s, b) for s in tr.states])
-    snap_m = torch.stack([s.m_res for s in tr.states])
+    snap_m = torch.stack([s.m_res for s in tr.states])       # fp32 M[c][d] blocks (m_split = 0)
     dv = lambda t: t.to(gpu).contiguous()
     from bolt3_amd import _abi as A
     mod = mod.to(gpu)

@@ -66,7 +66,7 @@ class AttnArgs(C.Structure):
         ("a_start", i32), ("a_len", i32), ("b_start", i32), ("b_len", i32),
         ("sink_k", p), ("sink_v", p), ("s_sb", i64), ("s_sh", i64), ("n_sink_keys", i32),
         ("slot_k", p), ("slot_v", p), ("slot_bias", p), ("slot_step", i64), ("has_slots", i32),
-        ("m_res", p), ("m_step", i64),
+        ("m_res", p), ("m_step", i64), ("m_split", i32),
         ("gamma", p), ("res_w", p), ("eps", f32),
         ("y", p), ("y_sb", i64), ("y_st", i64),
     ]

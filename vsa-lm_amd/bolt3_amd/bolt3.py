@@ -241,6 +241,7 @@ class Bolt3Attn(nn.Module):
             a.slot_k, a.slot_v, a.slot_bias = snaps[0].data_ptr(), snaps[1].data_ptr(), snaps[2].data_ptr()
             a.slot_step = bh * S * HD
             a.m_res, a.m_step = snaps[3].data_ptr(), bh * HD * HD
+            a.m_split = int(dt == torch.bfloat16)
         a.gamma, a.res_w, a.eps = gam.data_ptr(), side["res_w"].data_ptr(), float(self.res_norm.eps)
         a.y, a.y_sb, a.y_st = y.data_ptr(), y.stride(0), y.stride(1)
         A.call("bolt3_chunk_attn", a, dev)

@@ -281,12 +281,23 @@ __global__ void __launch_bounds__(512) attn_kernel(b3_attn_args a, int QW) {
     if constexpr (St<T>::is_bf16) {
       uint16_t* mh = sm.mhi();
       uint16_t* ml = sm.mlo();
-      for (int it = tid; it < HD * HD; it += nthreads) {
-        const int c = it / HD, d = it % HD;  // M[c][d] -> M^T[d][c]
-        const float x = M[it];
-        const uint16_t hb = f2bf(x);
-        mh[d * sm.MS + c] = hb;
-        ml[d * sm.MS + c] = f2bf(x - bf2f(hb));
+      if (a.m_split) {
+        // already M^T split into bf16 hi / lo: straight 16-byte copies
+        const uint16_t* src = reinterpret_cast<const uint16_t*>(M);
+        for (int it = tid; it < 2 * HD * (HD / 8); it += nthreads) {
+          const int part = it / (HD * (HD / 8)), rem = it % (HD * (HD / 8));
+          const int d = rem / (HD / 8), c8 = (rem % (HD / 8)) * 8;
+          *reinterpret_cast<u16x8*>((part ? ml : mh) + d * sm.MS + c8) =
+              *reinterpret_cast<const u16x8*>(src + part * HD * HD + d * HD + c8);
+        }
+      } else {
+        for (int it = tid; it < HD * HD; it += nthreads) {
+          const int c = it / HD, d = it % HD;  // M[c][d] -> M^T[d][c]
+          const float x = M[it];
+          const uint16_t hb = f2bf(x);
+          mh[d * sm.MS + c] = hb;
+          ml[d * sm.MS + c] = f2bf(x - bf2f(hb));
+        }
       }
     } else {
       float* mf = sm.mf();
@@ -379,6 +390,7 @@ extern "C" int bolt3_chunk_attn(const b3_attn_args* a, void* stream) {
     return B3_ERR_ARG;
   }
   if (a->m_res && !a->q_raw) return B3_ERR_ARG;
+  if (a->m_split && a->dtype != B3_BF16) return B3_ERR_ARG;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (a->dtype == B3_F32) return a->HD == 64 ? b3::launch_attn<float, 64>(*a, st) : b3::launch_attn<float, 128>(*a, st);
   if (a->dtype == B3_BF16)

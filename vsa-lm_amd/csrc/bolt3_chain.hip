@@ -14,14 +14,16 @@
 //          Gershgorin-safe delta rule M <- g*M + K^T diag(b) (V - K M).
 //
 // Layout: one 256-thread workgroup (4 wavefronts) per bh.  Slot keys/values,
-// masses, utilities, positions and activity stay in LDS for all steps; M_res
-// stays in the caller's fp32 [bh][HD][HD] array (L2 resident).  Every product
-// is a 32x32 MFMA tile: bf16 storage multiplies exact bf16 operands (products
-// are exact in fp32) and splits fp32 operands (M_res, delta-rule errors) into
-// bf16 hi+lo; fp32 storage uses the fp32 MFMA.  Decisions (argmax, thresholds,
-// the two orderings) are made on fp32 values with the reference's tie and NaN
-// rules: first index on ties, NaN ranks as the largest value.
+// masses, utilities, positions and activity stay in LDS for all steps.  M_res
+// is kept transposed in the workspace, in fp32 and (bf16 storage) split into
+// bf16 hi + lo, so every MFMA operand is one 16-byte load; the state array
+// [bh][HD][HD] is written after every step.  bf16 storage multiplies exact
+// bf16 operands (products are exact in fp32) and splits fp32 operands into
+// hi + lo; fp32 storage uses the fp32 MFMA.  Orderings are ranks computed by
+// counting on monotone integer keys (one pass, stable): the larger value
+// first (NaN first), equal values by lower index.
 #include "bolt3_common.h"
+#include "bolt3_math.h"
 #include "bolt3_amd.h"
 
 namespace b3 {
@@ -34,30 +36,46 @@ constexpr float SIM_K = 0.88f, SIM_V = 0.80f, UTIL_DECAY = 0.995f;
 
 enum : int { F_MERGE = 1, F_DELTA = 2, F_INS = 4 };
 
+// Workspace layout per bh (bytes): roped slot keys of the current state, M^T fp32,
+// M^T bf16 hi and lo, and (when they do not fit in LDS) the delta-rule tile buffers.
+template <typename T, int HD>
+struct Work {
+  static constexpr long long KREAD = (long long)S * HD * sizeof(T);
+  static constexpr long long MT32 = (long long)HD * HD * 4;
+  static constexpr long long MTBF = (long long)HD * HD * 2;
+  static constexpr long long TILE = 2LL * HD * 33 * 4;
+  static constexpr long long PER_BH = KREAD + MT32 + 2 * MTBF + TILE;
+};
+
 template <typename T, int HD>
 struct ChainSmem {
-  // bf16 rows padded by 16 bytes (16-byte aligned fragments); fp32 rows by one word.
-  static constexpr int KS = sizeof(T) == 2 ? HD + 8 : HD + 1;
-  static constexpr bool ERR_LDS = !(sizeof(T) == 4 && HD == 128);
-  static constexpr int ES = HD + 4;
+  static constexpr int KS = sizeof(T) == 2 ? HD + 8 : HD + 4;   // slot row stride (16-byte aligned rows)
+  static constexpr int TS = sizeof(T) == 2 ? 32 + 8 : 32 + 1;   // token-tile row stride (transposed tiles)
+  static constexpr bool TILE_LDS = !(sizeof(T) == 4 && HD == 128);
   alignas(16) T ak[S * KS];
   alignas(16) T av[S * KS];
   float mass[S], util[S], pm[S], inv_nak[S], keep[S], bias[S], psum[S];
   int act[S], cnt[S], off[S], hits[S];
-  float rel[LMAX], score[LMAX], best[LMAX], simv[LMAX], inv_nkr[LMAX], w[LMAX], bsafe[LMAX];
+  float rel[LMAX], score[LMAX], best[LMAX], simv[LMAX], inv_nkr[LMAX], w[LMAX], bsafe[LMAX], ck[LMAX];
   int slot[LMAX], flags[LMAX], mlist[LMAX];
   float sk_a[LMAX];
   int si_a[LMAX];
   float sk_b[S];
   int si_b[S];
-  float err[ERR_LDS ? 32 * ES : 1];
+  uint32_t ok_a[LMAX], ok_b[S];   // order keys
+  // delta-rule tiles: K^T [HD][32] and the error tile E^T [HD][32] (bf16: hi and lo)
+  static constexpr bool KREAD_LDS = sizeof(T) == 2;              // roped slot keys of the current state
+  alignas(16) T kread[KREAD_LDS ? S * KS : 1];
+  alignas(16) T krt[TILE_LDS ? HD * TS : 1];
+  alignas(16) T ert_hi[TILE_LDS ? HD * TS : 1];
+  alignas(16) uint16_t ert_lo[(TILE_LDS && sizeof(T) == 2) ? HD * TS : 1];
   int nhit;
 };
 
 // ----------------------------------------------------------------- fragments
 
-// Token tile fragment: lane (n = lane%32, h = lane/32) holds row tok = t0 + n,
-// K sub-index (per K-step ks) 16*ks + 8*h + i (bf16) or 2*ks + h (fp32).
+// Token-tile fragment: lane (n = lane%32, h = lane/32) holds row tok, K sub-index
+// 16*ks + 8*h + i (bf16) or 2*ks + h (fp32).
 template <typename T, int HD> struct Frag;
 template <int HD> struct Frag<uint16_t, HD> {
   static constexpr int NK = HD / 16;
@@ -72,6 +90,11 @@ template <int HD> struct Frag<uint16_t, HD> {
         for (int i = 0; i < 8; ++i) v[ks][i] = 0;
       }
     }
+  }
+  __device__ __forceinline__ void load_lds(const uint16_t* rows, int rs, int r, int lane) {
+    const int h = lane >> 5;
+#pragma unroll
+    for (int ks = 0; ks < NK; ++ks) v[ks] = *reinterpret_cast<const u16x8*>(rows + r * rs + 16 * ks + 8 * h);
   }
   __device__ __forceinline__ float sumsq() const {
     float s = 0.f;
@@ -90,6 +113,11 @@ template <int HD> struct Frag<float, HD> {
 #pragma unroll
     for (int ks = 0; ks < NK; ++ks) v[ks] = tok < l ? base[(long long)tok * HD + 2 * ks + h] : 0.f;
   }
+  __device__ __forceinline__ void load_lds(const float* rows, int rs, int r, int lane) {
+    const int h = lane >> 5;
+#pragma unroll
+    for (int ks = 0; ks < NK; ++ks) v[ks] = rows[r * rs + 2 * ks + h];
+  }
   __device__ __forceinline__ float sumsq() const {
     float s = 0.f;
 #pragma unroll
@@ -98,7 +126,7 @@ template <int HD> struct Frag<float, HD> {
   }
 };
 
-// acc (rows = 32 rows of `rows` starting at row0, stride rs) += rows . frag^T over HD.
+// acc += rows[row0 + lane%32][:] . frag over HD  (rows: LDS or global, row stride rs)
 template <int HD>
 __device__ __forceinline__ void mm_rows_frag(f32x16& acc, const uint16_t* rows, int rs, int row0,
                                              const Frag<uint16_t, HD>& f, int lane) {
@@ -117,70 +145,95 @@ __device__ __forceinline__ void mm_rows_frag(f32x16& acc, const float* rows, int
   for (int ks = 0; ks < HD / 2; ++ks) mma_f32(acc, rows[m * rs + 2 * ks + h], f.v[ks]);
 }
 
+// 8 consecutive elements as floats (16-byte bf16 or two 16-byte fp32 loads)
+__device__ __forceinline__ void ld8(const uint16_t* p, float* o) {
+  const u16x8 v = *reinterpret_cast<const u16x8*>(p);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o[i] = bf2f(v[i]);
+}
+__device__ __forceinline__ void ld8(const float* p, float* o) {
+  const float4 a = *reinterpret_cast<const float4*>(p), b = *reinterpret_cast<const float4*>(p + 4);
+  o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w; o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
+}
+
+// 8 consecutive elements, 16-byte (bf16) or 2 x 16-byte (fp32) moves; both pointers aligned
+__device__ __forceinline__ void copy8(uint16_t* d, const uint16_t* s) {
+  *reinterpret_cast<u16x8*>(d) = *reinterpret_cast<const u16x8*>(s);
+}
+__device__ __forceinline__ void copy8(float* d, const float* s) {
+  *reinterpret_cast<float4*>(d) = *reinterpret_cast<const float4*>(s);
+  *reinterpret_cast<float4*>(d + 4) = *reinterpret_cast<const float4*>(s + 4);
+}
+
 // ----------------------------------------------------------------- helpers
 
+// Slot keys roped at their mean positions -> `dst` (global, may be null) and, for bf16
+// storage, the LDS copy the next scoring reads.
 template <typename T, int HD>
-__device__ void rope_slots_to(T* dst, const ChainSmem<T, HD>& sm, const float* inv_freq, int tid) {
+__device__ void rope_slots_to(T* dst, ChainSmem<T, HD>& sm, const float* inv_freq, int tid) {
   constexpr int HALF = HD / 2;
   for (int it = tid; it < S * HALF; it += NT) {
     const int s = it / HALF, i = it % HALF;
-    const float ang = mul_rn(sm.pm[s], inv_freq[i]);
     float sn, cs;
-    sincosf(ang, &sn, &cs);
+    sincos_rope(mul_rn(sm.pm[s], inv_freq[i]), &sn, &cs);
     const float c = St<T>::rnd(cs), si = St<T>::rnd(sn);
     const float x0 = St<T>::to_f(sm.ak[s * sm.KS + i]), x1 = St<T>::to_f(sm.ak[s * sm.KS + i + HALF]);
-    dst[s * HD + i] = St<T>::from_f(add_rn(St<T>::rnd(mul_rn(x0, c)), St<T>::rnd(mul_rn(-x1, si))));
-    dst[s * HD + i + HALF] = St<T>::from_f(add_rn(St<T>::rnd(mul_rn(x1, c)), St<T>::rnd(mul_rn(x0, si))));
+    const T r0 = St<T>::from_f(add_rn(St<T>::rnd(mul_rn(x0, c)), St<T>::rnd(mul_rn(-x1, si))));
+    const T r1 = St<T>::from_f(add_rn(St<T>::rnd(mul_rn(x1, c)), St<T>::rnd(mul_rn(x0, si))));
+    if (dst) {
+      dst[s * HD + i] = r0;
+      dst[s * HD + i + HALF] = r1;
+    }
+    if constexpr (ChainSmem<T, HD>::KREAD_LDS) {
+      sm.kread[s * sm.KS + i] = r0;
+      sm.kread[s * sm.KS + i + HALF] = r1;
+    }
   }
 }
 
-// 1 / max(||ak_s||, 1e-12) for every slot.
+// 1 / max(||ak_s||, 1e-12) for every slot (two threads per slot).
 template <typename T, int HD>
 __device__ void slot_norms(ChainSmem<T, HD>& sm, int tid) {
   const int s = tid >> 1, half = tid & 1;
   float ss = 0.f;
-  for (int d = half * (HD / 2); d < (half + 1) * (HD / 2); ++d) {
-    const float x = St<T>::to_f(sm.ak[s * sm.KS + d]);
-    ss += x * x;
+#pragma unroll
+  for (int d = half * (HD / 2); d < (half + 1) * (HD / 2); d += 8) {
+    float x[8];
+    ld8(&sm.ak[s * sm.KS + d], x);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ss += x[i] * x[i];
   }
   ss += __shfl_xor(ss, 1, 64);
   if (half == 0) sm.inv_nak[s] = 1.0f / fmaxf(sqrtf(ss), 1e-12f);
 }
 
-// Bitonic sort of NT keys (with indices) in LDS; desc: largest first.
-__device__ void bitonic_256(float* key, int* idx, bool desc, int tid) {
-  for (int k = 2; k <= NT; k <<= 1) {
-    for (int j = k >> 1; j > 0; j >>= 1) {
-      const int p = tid ^ j;
-      if (p > tid) {
-        const bool up = (tid & k) == 0;  // this pair sorted in the requested direction
-        const float a = key[tid], b = key[p];
-        const int ia = idx[tid], ib = idx[p];
-        const bool b_first = desc ? ranks_before_desc(b, ib, a, ia) : ranks_before_asc(b, ib, a, ia);
-        const bool swap = up ? b_first : !b_first;
-        if (swap) { key[tid] = b; key[p] = a; idx[tid] = ib; idx[p] = ia; }
-      }
-      __syncthreads();
-    }
-  }
+// Monotone integer image of a float: a < b  <=>  ord(a) < ord(b); NaN maps above +inf, so
+// it ranks first in a descending and last in an ascending order (torch.topk's placement).
+// -0 and +0 map to adjacent keys.
+__device__ __forceinline__ uint32_t ord_key(float f) {
+  const uint32_t u = __float_as_uint(f);
+  if (f != f) return 0xffffffffu;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-// Same for the first S entries, executed by threads < S (all threads reach the barriers).
-__device__ void bitonic_128_asc(float* key, int* idx, int tid) {
-  for (int k = 2; k <= S; k <<= 1) {
-    for (int j = k >> 1; j > 0; j >>= 1) {
-      const int p = tid ^ j;
-      if (tid < S && p > tid) {
-        const bool up = (tid & k) == 0;
-        const float a = key[tid], b = key[p];
-        const int ia = idx[tid], ib = idx[p];
-        const bool b_first = ranks_before_asc(b, ib, a, ia);
-        const bool swap = up ? b_first : !b_first;
-        if (swap) { key[tid] = b; key[p] = a; idx[tid] = ib; idx[p] = ia; }
-      }
-      __syncthreads();
-    }
+// Rank of element `me` among ok[0..n) (order keys), ties by lower index.
+__device__ __forceinline__ int rank_desc(const uint32_t* ok, int n, int me) {
+  const uint32_t x = ok[me];
+  int r = 0;
+  for (int i = 0; i < n; ++i) {
+    const uint32_t y = ok[i];
+    r += (y > x || (y == x && i < me)) ? 1 : 0;
   }
+  return r;
+}
+__device__ __forceinline__ int rank_asc(const uint32_t* ok, int n, int me) {
+  const uint32_t x = ok[me];
+  int r = 0;
+  for (int i = 0; i < n; ++i) {
+    const uint32_t y = ok[i];
+    r += (y < x || (y == x && i < me)) ? 1 : 0;
+  }
+  return r;
 }
 
 // ----------------------------------------------------------------- retrieval (phase A)
@@ -201,7 +254,8 @@ __device__ void score_tile(ChainSmem<T, HD>& sm, const T* kread, const T* kr, co
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb) {
       acc[mb] = zero16();
-      mm_rows_frag<HD>(acc[mb], kread, HD, 32 * mb, f, lane);
+      if constexpr (ChainSmem<T, HD>::KREAD_LDS) mm_rows_frag<HD>(acc[mb], sm.kread, sm.KS, 32 * mb, f, lane);
+      else mm_rows_frag<HD>(acc[mb], kread, HD, 32 * mb, f, lane);
     }
   }
   // softmax over the slots (column of this lane pair)
@@ -264,16 +318,29 @@ __device__ void score_tile(ChainSmem<T, HD>& sm, const T* kread, const T* kr, co
   }
   // rel_err = ||v - v_hat|| / (||v|| + 1e-6)
   float e2 = 0.f, v2 = 0.f;
+  if (tok < l) {
 #pragma unroll
-  for (int db = 0; db < NDB; ++db)
+    for (int db = 0; db < NDB; ++db)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int d = 32 * db + d_row(lane, r);
-      const float x = tok < l ? St<T>::ld(v + (long long)tok * HD + d) : 0.f;
-      const float dv = x - St<T>::rnd(vh[db][r]);
-      e2 += dv * dv;
-      v2 += x * x;
-    }
+      for (int g = 0; g < 4; ++g) {
+        const int d0 = 32 * db + 8 * g + 4 * h;
+        float x[4];
+        if constexpr (St<T>::is_bf16) {
+          const u16x4 q = *reinterpret_cast<const u16x4*>(v + (long long)tok * HD + d0);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) x[i] = bf2f(q[i]);
+        } else {
+          const float4 q = *reinterpret_cast<const float4*>(v + (long long)tok * HD + d0);
+          x[0] = q.x; x[1] = q.y; x[2] = q.z; x[3] = q.w;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float dv = x[i] - St<T>::rnd(vh[db][4 * g + i]);
+          e2 += dv * dv;
+          v2 += x[i] * x[i];
+        }
+      }
+  }
   e2 += xor32(e2);
   v2 += xor32(v2);
   const float rel = sqrtf(e2) / (sqrtf(v2) + 1e-6f);
@@ -297,7 +364,7 @@ __device__ void score_tile(ChainSmem<T, HD>& sm, const T* kread, const T* kr, co
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int s = 32 * mb + d_row(lane, r);
-      float c = acc[mb][r] * sm.inv_nak[s] * inv_nk;
+      float c = acc[mb][r] * (sm.inv_nak[s] * inv_nk);
       if (!steady && !sm.act[s]) c = 0.f;
       if (first || ranks_before_desc(c, s, bv, bs)) { bv = c; bs = s; first = false; }
     }
@@ -313,12 +380,17 @@ __device__ void score_tile(ChainSmem<T, HD>& sm, const T* kread, const T* kr, co
     // cos(v_tok, av[best]) over this lane's half of the features
     float dvv = 0.f, vv = 0.f, aa = 0.f;
     if (tok < l) {
-      for (int d = h * (HD / 2); d < (h + 1) * (HD / 2); ++d) {
-        const float x = St<T>::ld(v + (long long)tok * HD + d);
-        const float y = St<T>::to_f(sm.av[bs * sm.KS + d]);
-        dvv += x * y;
-        vv += x * x;
-        aa += y * y;
+#pragma unroll
+      for (int d = h * (HD / 2); d < (h + 1) * (HD / 2); d += 8) {
+        float x[8], y[8];
+        ld8(v + (long long)tok * HD + d, x);
+        ld8(&sm.av[bs * sm.KS + d], y);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          dvv += x[i] * y[i];
+          vv += x[i] * x[i];
+          aa += y[i] * y[i];
+        }
       }
     }
     dvv += xor32(dvv);
@@ -348,31 +420,24 @@ __device__ void gershgorin(ChainSmem<T, HD>& sm, const T* kr, int l, int wave, i
     const int j = 32 * tj + n;
     Frag<T, HD> fj;
     fj.load(kr, j, l, lane);
+    const float inj = j < l ? sm.inv_nkr[j] : 0.f;
     float colsum = 0.f;
     for (int ti = 0; ti < nT; ++ti) {
       f32x16 acc = zero16();
-      // rows i of tile ti as A operand, read from global memory
-      const int m = 32 * ti + (lane & 31), h = lane >> 5;
+      Frag<T, HD> fi;
+      fi.load(kr, 32 * ti + (lane & 31), l, lane);
+      // rows i of tile ti as the A operand: same fragment layout as a B fragment
       if constexpr (St<T>::is_bf16) {
 #pragma unroll
-        for (int ks = 0; ks < HD / 16; ++ks) {
-          u16x8 a;
-          if (m < l) a = *reinterpret_cast<const u16x8*>(kr + (long long)m * HD + 16 * ks + 8 * h);
-          else {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) a[i] = 0;
-          }
-          mma_bf16(acc, a, fj.v[ks]);
-        }
+        for (int ks = 0; ks < HD / 16; ++ks) mma_bf16(acc, fi.v[ks], fj.v[ks]);
       } else {
 #pragma unroll 8
-        for (int ks = 0; ks < HD / 2; ++ks) mma_f32(acc, m < l ? kr[(long long)m * HD + 2 * ks + h] : 0.f, fj.v[ks]);
+        for (int ks = 0; ks < HD / 2; ++ks) mma_f32(acc, fi.v[ks], fj.v[ks]);
       }
-      const float inj = j < l ? sm.inv_nkr[j] : 0.f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int i = 32 * ti + d_row(lane, r);
-        if (i < l) colsum += fabsf(acc[r] * sm.inv_nkr[i] * inj) * sm.w[i];
+        if (i < l) colsum += fabsf(acc[r] * (sm.inv_nkr[i] * inj)) * sm.w[i];
       }
     }
     colsum += xor32(colsum);
@@ -380,15 +445,21 @@ __device__ void gershgorin(ChainSmem<T, HD>& sm, const T* kr, int l, int wave, i
   }
 }
 
-// M <- gamma*M + K^T diag(bsafe) (V - K M) with K = normalized keys.
+// M <- gamma*M + K^T diag(bsafe) (V - K M) with K = normalized keys, M kept as M^T.
 template <typename T, int HD>
-__device__ void delta_update(ChainSmem<T, HD>& sm, float* M, float* errg, const T* kr, const T* v, int l,
-                             float gam, int wave, int lane, int tid) {
-  constexpr int NB = HD / 32;               // row/col blocks of M
+__device__ void delta_update(ChainSmem<T, HD>& sm, char* ws, float* M, float* snap_m, const T* kr, const T* v,
+                             int l, float gam, int wave, int lane, int tid) {
+  using W = Work<T, HD>;
+  constexpr int NB = HD / 32;
   constexpr int NBLK = NB * NB;
   constexpr int PER_WAVE = (NBLK + NWAVE - 1) / NWAVE;
-  float* err = sm.ERR_LDS ? sm.err : errg;  // [32][ES] error tile
-  const int ES = sm.ES;
+  const int TS = sm.TS;
+  float* mt32 = reinterpret_cast<float*>(ws + W::KREAD);
+  uint16_t* mthi = reinterpret_cast<uint16_t*>(ws + W::KREAD + W::MT32);
+  uint16_t* mtlo = mthi + HD * HD;
+  T* krt = sm.TILE_LDS ? sm.krt : reinterpret_cast<T*>(ws + W::KREAD + W::MT32 + 2 * W::MTBF);
+  T* ert = sm.TILE_LDS ? sm.ert_hi : krt + HD * 33;
+  uint16_t* erl = sm.ert_lo;
   const int n = lane & 31, h = lane >> 5;
   f32x16 upd[PER_WAVE];
 #pragma unroll
@@ -397,7 +468,19 @@ __device__ void delta_update(ChainSmem<T, HD>& sm, float* M, float* errg, const 
 
   for (int t = 0; t < nT; ++t) {
     const int t0 = 32 * t;
-    // v_pred^T[d][j] = sum_c M[c][d] kr[j][c]; wave w takes d-block w
+    // K^T tile: krt[c][j] = kr[t0 + j][c]
+    for (int it = tid; it < 32 * (HD / 8); it += NT) {
+      const int j = it / (HD / 8), c8 = (it % (HD / 8)) * 8;
+      float x[8];
+      if (t0 + j < l) ld8(kr + (long long)(t0 + j) * HD + c8, x);
+      else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x[i] = 0.f;
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) krt[(c8 + i) * TS + j] = St<T>::from_f(x[i]);
+    }
+    // v_pred^T[d][j] = sum_c M^T[d][c] kr[j][c]; error tile E^T[d][j] = (v - v_pred) * bsafe_j / |k_j|
     for (int db = wave; db < NB; db += NWAVE) {
       const int j = t0 + n;
       Frag<T, HD> fj;
@@ -407,30 +490,46 @@ __device__ void delta_update(ChainSmem<T, HD>& sm, float* M, float* errg, const 
       if constexpr (St<T>::is_bf16) {
 #pragma unroll
         for (int ks = 0; ks < HD / 16; ++ks) {
-          float mv[8];
-#pragma unroll
-          for (int i = 0; i < 8; ++i) mv[i] = M[(16 * ks + 8 * h + i) * HD + d];
-          u16x8 hi, lo;
-          split8(mv, hi, lo);
+          const u16x8 hi = *reinterpret_cast<const u16x8*>(mthi + d * HD + 16 * ks + 8 * h);
+          const u16x8 lo = *reinterpret_cast<const u16x8*>(mtlo + d * HD + 16 * ks + 8 * h);
           mma_bf16(acc, hi, fj.v[ks]);
           mma_bf16(acc, lo, fj.v[ks]);
         }
       } else {
 #pragma unroll 8
-        for (int ks = 0; ks < HD / 2; ++ks) mma_f32(acc, M[(2 * ks + h) * HD + d], fj.v[ks]);
+        for (int ks = 0; ks < HD / 2; ++ks) mma_f32(acc, mt32[d * HD + 2 * ks + h], fj.v[ks]);
       }
       const float inj = j < l ? sm.inv_nkr[j] : 0.f;
       const float bj = j < l ? sm.bsafe[j] : 0.f;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int dd = 32 * db + d_row(lane, r);
-        const float x = j < l ? St<T>::ld(v + (long long)j * HD + dd) : 0.f;
-        const float e = (x - acc[r] * inj) * bj;
-        err[n * ES + dd] = e * inj;
+      for (int g = 0; g < 4; ++g) {
+        const int d0 = 32 * db + 8 * g + 4 * h;
+        float x[4] = {0.f, 0.f, 0.f, 0.f};
+        if (j < l) {
+          if constexpr (St<T>::is_bf16) {
+            const u16x4 q = *reinterpret_cast<const u16x4*>(v + (long long)j * HD + d0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) x[i] = bf2f(q[i]);
+          } else {
+            const float4 q = *reinterpret_cast<const float4*>(v + (long long)j * HD + d0);
+            x[0] = q.x; x[1] = q.y; x[2] = q.z; x[3] = q.w;
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float e = ((x[i] - acc[4 * g + i] * inj) * bj) * inj;
+          if constexpr (St<T>::is_bf16) {
+            const uint16_t hb = f2bf(e);
+            ert[(d0 + i) * TS + n] = hb;
+            erl[(d0 + i) * TS + n] = f2bf(e - bf2f(hb));
+          } else {
+            ert[(d0 + i) * TS + n] = e;
+          }
+        }
       }
     }
     __syncthreads();
-    // upd[c][d] += sum_j kr[j][c] err[j][d]
+    // upd[c][d] += sum_j K^T[c][j] E^T[d][j]
 #pragma unroll
     for (int q = 0; q < PER_WAVE; ++q) {
       const int blk = wave + NWAVE * q;
@@ -440,32 +539,22 @@ __device__ void delta_update(ChainSmem<T, HD>& sm, float* M, float* errg, const 
         if constexpr (St<T>::is_bf16) {
 #pragma unroll
           for (int kc = 0; kc < 2; ++kc) {
-            u16x8 a;
-            float ev[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-              const int jj = 16 * kc + 8 * h + i;
-              a[i] = (t0 + jj < l) ? kr[(long long)(t0 + jj) * HD + c] : (uint16_t)0;
-              ev[i] = err[jj * ES + d];
-            }
-            u16x8 hi, lo;
-            split8(ev, hi, lo);
-            mma_bf16(upd[q], a, hi);
-            mma_bf16(upd[q], a, lo);
+            const u16x8 a = *reinterpret_cast<const u16x8*>(krt + c * TS + 16 * kc + 8 * h);
+            const u16x8 bh_ = *reinterpret_cast<const u16x8*>(ert + d * TS + 16 * kc + 8 * h);
+            const u16x8 bl_ = *reinterpret_cast<const u16x8*>(erl + d * TS + 16 * kc + 8 * h);
+            mma_bf16(upd[q], a, bh_);
+            mma_bf16(upd[q], a, bl_);
           }
         } else {
 #pragma unroll
-          for (int kc = 0; kc < 16; ++kc) {
-            const int jj = 2 * kc + h;
-            const float a = (t0 + jj < l) ? kr[(long long)(t0 + jj) * HD + c] : 0.f;
-            mma_f32(upd[q], a, err[jj * ES + d]);
-          }
+          for (int kc = 0; kc < 16; ++kc) mma_f32(upd[q], krt[c * TS + 2 * kc + h], ert[d * TS + 2 * kc + h]);
         }
       }
     }
     __syncthreads();
   }
-  // M = gamma*M + upd (two rounded ops, as the reference evaluates them)
+  // M = gamma*M + upd (two rounded ops, as the reference evaluates them); write M^T (fp32 and
+  // bf16 hi/lo), the state M[c][d] and the snapshot
 #pragma unroll
   for (int q = 0; q < PER_WAVE; ++q) {
     const int blk = wave + NWAVE * q;
@@ -473,10 +562,34 @@ __device__ void delta_update(ChainSmem<T, HD>& sm, float* M, float* errg, const 
       const int cb = blk / NB, db = blk % NB;
       const int d = 32 * db + n;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int c = 32 * cb + d_row(lane, r);
-        float* p = M + c * HD + d;
-        *p = add_rn(mul_rn(gam, *p), upd[q][r]);
+      for (int g = 0; g < 4; ++g) {
+        const int c0 = 32 * cb + 8 * g + 4 * h;
+        const float4 old = *reinterpret_cast<const float4*>(mt32 + d * HD + c0);
+        float nw[4];
+        nw[0] = add_rn(mul_rn(gam, old.x), upd[q][4 * g + 0]);
+        nw[1] = add_rn(mul_rn(gam, old.y), upd[q][4 * g + 1]);
+        nw[2] = add_rn(mul_rn(gam, old.z), upd[q][4 * g + 2]);
+        nw[3] = add_rn(mul_rn(gam, old.w), upd[q][4 * g + 3]);
+        *reinterpret_cast<float4*>(mt32 + d * HD + c0) = make_float4(nw[0], nw[1], nw[2], nw[3]);
+        u16x4 hi4, lo4;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          hi4[i] = f2bf(nw[i]);
+          lo4[i] = f2bf(nw[i] - bf2f(hi4[i]));
+          M[(c0 + i) * HD + d] = nw[i];
+        }
+        *reinterpret_cast<u16x4*>(mthi + d * HD + c0) = hi4;
+        *reinterpret_cast<u16x4*>(mtlo + d * HD + c0) = lo4;
+        if (snap_m) {
+          if constexpr (St<T>::is_bf16) {
+            uint16_t* sh = reinterpret_cast<uint16_t*>(snap_m);
+            *reinterpret_cast<u16x4*>(sh + d * HD + c0) = hi4;
+            *reinterpret_cast<u16x4*>(sh + HD * HD + d * HD + c0) = lo4;
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) snap_m[(c0 + i) * HD + d] = nw[i];
+          }
+        }
       }
     }
   }
@@ -487,6 +600,7 @@ __device__ void delta_update(ChainSmem<T, HD>& sm, float* M, float* errg, const 
 template <typename T, int HD>
 __global__ void __launch_bounds__(NT) chain_kernel(b3_chain_args a) {
   __shared__ ChainSmem<T, HD> sm;
+  using W = Work<T, HD>;
   const int bh = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hkv = bh % a.HKV;
@@ -497,16 +611,26 @@ __global__ void __launch_bounds__(NT) chain_kernel(b3_chain_args a) {
   T* g_ak = reinterpret_cast<T*>(a.ak) + (long long)bh * S * HD;
   T* g_av = reinterpret_cast<T*>(a.av) + (long long)bh * S * HD;
   float* M = a.m_res + (long long)bh * HD * HD;
-  const long long kv_blk = (long long)a.B * a.HKV * S * HD;  // elements per step in snapshot arrays
-  // scratch: roped slot keys of the current state, and (fp32 HD=128) the error tile
-  T* kread_w = reinterpret_cast<T*>(a.work) + (long long)bh * S * HD;
-  float* errg = reinterpret_cast<float*>(reinterpret_cast<char*>(a.work) + kv_blk * sizeof(T)) + (long long)bh * 32 * sm.ES;
+  const long long BH = (long long)a.B * a.HKV;
+  char* ws = reinterpret_cast<char*>(a.work) + (long long)bh * W::PER_BH;
+  T* kread_w = reinterpret_cast<T*>(ws);
+  float* mt32 = reinterpret_cast<float*>(ws + W::KREAD);
+  uint16_t* mthi = reinterpret_cast<uint16_t*>(ws + W::KREAD + W::MT32);
+  uint16_t* mtlo = mthi + HD * HD;
 
-  // load state
+  // load state; M -> M^T (fp32, bf16 hi/lo) in the workspace
   for (int it = tid; it < S * HD; it += NT) {
     const int s = it / HD, d = it % HD;
     sm.ak[s * KS + d] = g_ak[it];
     sm.av[s * KS + d] = g_av[it];
+  }
+  for (int it = tid; it < HD * HD; it += NT) {
+    const int c = it / HD, d = it % HD;
+    const float x = M[it];
+    mt32[d * HD + c] = x;
+    const uint16_t hb = f2bf(x);
+    mthi[d * HD + c] = hb;
+    mtlo[d * HD + c] = f2bf(x - bf2f(hb));
   }
   if (tid < S) {
     sm.mass[tid] = a.mass[bh * S + tid];
@@ -517,10 +641,8 @@ __global__ void __launch_bounds__(NT) chain_kernel(b3_chain_args a) {
   __syncthreads();
   int nf = a.n_filled;
   const T* kread = kread_w;
-  if (nf > 0) {
-    rope_slots_to<T, HD>(kread_w, sm, a.inv_freq, tid);
-    __threadfence_block();
-  }
+  if (nf > 0) rope_slots_to<T, HD>(sm.KREAD_LDS ? nullptr : kread_w, sm, a.inv_freq, tid);
+  __threadfence_block();
   __syncthreads();
 
   for (int step = 0; step < a.n_steps; ++step) {
@@ -534,10 +656,11 @@ __global__ void __launch_bounds__(NT) chain_kernel(b3_chain_args a) {
     const float* beta = a.beta + (long long)bh * a.beta_bh_stride + off;
     const int nT = (l + 31) / 32;
     const bool steady = nf >= S;
-    float* log = a.log ? a.log + ((long long)step * (a.B * a.HKV) + bh) * (B3_LOG_ROWS * B3_LOG_COLS) : nullptr;
+    float* log = a.log ? a.log + ((long long)step * BH + bh) * (B3_LOG_ROWS * B3_LOG_COLS) : nullptr;
+    float* snap_m = a.snap_m ? a.snap_m + (long long)step * BH * HD * HD + (long long)bh * HD * HD : nullptr;
 
-    if (tid < S) sm.util[tid] = mul_rn(sm.util[tid], UTIL_DECAY);
     if (tid < S) {
+      sm.util[tid] = mul_rn(sm.util[tid], UTIL_DECAY);
       const float lm = logf(fmaxf(sm.mass[tid], 1.0f));
       sm.bias[tid] = steady ? mul_rn(kap, lm) : lm;
     }
@@ -554,13 +677,28 @@ __global__ void __launch_bounds__(NT) chain_kernel(b3_chain_args a) {
         if (j < l) {
           const T* vr = v + (long long)j * HD;
           float ss = 0.f;
-          for (int d = 0; d < HD; ++d) { const float x = St<T>::ld(vr + d); ss += x * x; }
+          for (int d = 0; d < HD; d += 8) {
+            float x[8];
+            ld8(vr + d, x);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) ss += x[i] * x[i];
+          }
           const float nrm = fmaxf(sqrtf(ss), 1e-12f);
           float mean = 0.f;
-          for (int d = 0; d < HD; ++d) mean += div_rn(St<T>::ld(vr + d), nrm);
+          for (int d = 0; d < HD; d += 8) {
+            float x[8];
+            ld8(vr + d, x);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) mean += div_rn(x[i], nrm);
+          }
           mean /= (float)HD;
           float var = 0.f;
-          for (int d = 0; d < HD; ++d) { const float u = div_rn(St<T>::ld(vr + d), nrm) - mean; var += u * u; }
+          for (int d = 0; d < HD; d += 8) {
+            float x[8];
+            ld8(vr + d, x);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) { const float u = div_rn(x[i], nrm) - mean; var += u * u; }
+          }
           sm.score[j] = var / (float)(HD - 1);
           sm.rel[j] = 0.15f;
         }
@@ -568,16 +706,20 @@ __global__ void __launch_bounds__(NT) chain_kernel(b3_chain_args a) {
         for (int t = wave; t < nT; t += NWAVE) score_tile<T, HD>(sm, kread, kr, kp, v, 32 * t, l, false, scale, lane);
       }
       __syncthreads();
-      sm.sk_a[tid] = tid < l ? sm.score[tid] : -INFINITY;
-      sm.si_a[tid] = tid;
+      if (tid < l) sm.ok_a[tid] = ord_key(sm.score[tid]);
       __syncthreads();
-      bitonic_256(sm.sk_a, sm.si_a, true, tid);
+      if (tid < l) {
+        const int r = rank_desc(sm.ok_a, l, tid);
+        sm.si_a[r] = tid;
+        sm.sk_a[r] = sm.score[tid];
+      }
+      __syncthreads();
       // slots nf + i <- token si_a[i]
-      for (int it = tid; it < m * HD; it += NT) {
-        const int i = it / HD, d = it % HD;
+      for (int it = tid; it < m * (HD / 8); it += NT) {
+        const int i = it / (HD / 8), d8 = (it % (HD / 8)) * 8;
         const int j = sm.si_a[i], s = nf + i;
-        sm.ak[s * KS + d] = kr[(long long)j * HD + d];
-        sm.av[s * KS + d] = v[(long long)j * HD + d];
+        copy8(&sm.ak[s * KS + d8], kr + (long long)j * HD + d8);
+        copy8(&sm.av[s * KS + d8], v + (long long)j * HD + d8);
       }
       if (tid < m) {
         const int j = sm.si_a[tid], s = nf + tid;
@@ -593,35 +735,47 @@ __global__ void __launch_bounds__(NT) chain_kernel(b3_chain_args a) {
           log[B3_LOG_TOPTOK * B3_LOG_COLS + j] = j < m ? (float)sm.si_a[j] : -1.f;
         }
       }
+      // M_res is unchanged by a fill: its snapshot is the current M
+      if (snap_m) {
+        for (int it = tid; it < HD * HD; it += NT) {
+          if constexpr (St<T>::is_bf16) {
+            reinterpret_cast<uint16_t*>(snap_m)[it] = mthi[it];
+            reinterpret_cast<uint16_t*>(snap_m)[HD * HD + it] = mtlo[it];
+          } else {
+            snap_m[it] = M[it];
+          }
+        }
+      }
       nf += m;
       __syncthreads();
     } else {
       // ---------------- steady: score
       for (int t = wave; t < nT; t += NWAVE) score_tile<T, HD>(sm, kread, kr, kp, v, 32 * t, l, true, scale, lane);
-      __syncthreads();
+      const int has = tid < l && (sm.flags[tid] & F_MERGE);
+      const int any_merge = __syncthreads_or(has);
 
       // ---------------- merge: per-slot mass-weighted means, tokens in ascending order
-      if (tid < S) {
-        int c = 0;
-        float ps = 0.f;
-        for (int j = 0; j < l; ++j)
-          if ((sm.flags[j] & F_MERGE) && sm.slot[j] == tid) { ++c; ps += pos[j]; }
-        sm.cnt[tid] = c;
-        sm.psum[tid] = ps;
-      }
-      __syncthreads();
-      if (tid == 0) {
-        int o = 0, nh = 0;
-        for (int s = 0; s < S; ++s) {
-          sm.off[s] = o;
-          o += sm.cnt[s];
-          if (sm.cnt[s] > 0) sm.hits[nh++] = s;
+      if (any_merge) {
+        if (tid < S) {
+          int c = 0;
+          float ps = 0.f;
+          for (int j = 0; j < l; ++j)
+            if ((sm.flags[j] & F_MERGE) && sm.slot[j] == tid) { ++c; ps += pos[j]; }
+          sm.cnt[tid] = c;
+          sm.psum[tid] = ps;
         }
-        sm.nhit = nh;
-      }
-      __syncthreads();
-      const int nhit = sm.nhit;
-      if (nhit > 0) {
+        __syncthreads();
+        if (tid == 0) {
+          int o = 0, nh = 0;
+          for (int s = 0; s < S; ++s) {
+            sm.off[s] = o;
+            o += sm.cnt[s];
+            if (sm.cnt[s] > 0) sm.hits[nh++] = s;
+          }
+          sm.nhit = nh;
+        }
+        __syncthreads();
+        const int nhit = sm.nhit;
         if (tid < l && (sm.flags[tid] & F_MERGE)) {
           const int s = sm.slot[tid];
           int rank = 0;
@@ -657,16 +811,7 @@ __global__ void __launch_bounds__(NT) chain_kernel(b3_chain_args a) {
         const int n = lane & 31;
         const int col = 32 * wave + n;  // 4 waves x 32 columns = S
         Frag<T, HD> fc;
-        {
-          const int h = lane >> 5;
-          if constexpr (St<T>::is_bf16) {
-#pragma unroll
-            for (int ks = 0; ks < HD / 16; ++ks) fc.v[ks] = *reinterpret_cast<const u16x8*>(&sm.ak[col * KS + 16 * ks + 8 * h]);
-          } else {
-#pragma unroll
-            for (int ks = 0; ks < HD / 2; ++ks) fc.v[ks] = sm.ak[col * KS + 2 * ks + h];
-          }
-        }
+        fc.load_lds(sm.ak, KS, col, lane);
         float mx = -INFINITY;
         bool has_nan = false;
 #pragma unroll
@@ -688,13 +833,25 @@ __global__ void __launch_bounds__(NT) chain_kernel(b3_chain_args a) {
         if (has_nan) mx = NAN;
         if ((lane >> 5) == 0) sm.keep[col] = mul_rn(sm.util[col], 1.0f - fminf(fmaxf(mx, 0.0f), 0.98f));
       }
-      // ---------------- eviction candidates vs least useful slots
-      sm.sk_a[tid] = tid < l ? ((sm.flags[tid] & F_MERGE) ? -1e9f : sm.score[tid]) : -INFINITY;
-      sm.si_a[tid] = tid;
+      if (tid < l) {
+        sm.ck[tid] = (sm.flags[tid] & F_MERGE) ? -1e9f : sm.score[tid];
+        sm.ok_a[tid] = ord_key(sm.ck[tid]);
+      }
       __syncthreads();
-      if (tid < S) { sm.sk_b[tid] = sm.keep[tid]; sm.si_b[tid] = tid; }
-      bitonic_256(sm.sk_a, sm.si_a, true, tid);
-      bitonic_128_asc(sm.sk_b, sm.si_b, tid);
+      if (tid < S) sm.ok_b[tid] = ord_key(sm.keep[tid]);
+      __syncthreads();
+      // ---------------- orderings: best free tokens (desc) against least useful slots (asc)
+      if (tid < l) {
+        const int r = rank_desc(sm.ok_a, l, tid);
+        sm.sk_a[r] = sm.ck[tid];
+        sm.si_a[r] = tid;
+      }
+      if (tid < S) {
+        const int r = rank_asc(sm.ok_b, S, tid);
+        sm.sk_b[r] = sm.keep[tid];
+        sm.si_b[r] = tid;
+      }
+      __syncthreads();
       const int kc = min(l, S);
       // win_i = top_i > bot_i and top_i > -1e8 ; token top_i replaces slot bot_i
       if (tid < kc) {
@@ -702,13 +859,13 @@ __global__ void __launch_bounds__(NT) chain_kernel(b3_chain_args a) {
         if (tv > bv && tv > -1e8f) sm.flags[sm.si_a[tid]] |= F_INS;
       }
       __syncthreads();
-      for (int it = tid; it < kc * HD; it += NT) {
-        const int i = it / HD, d = it % HD;
+      for (int it = tid; it < kc * (HD / 8); it += NT) {
+        const int i = it / (HD / 8), d8 = (it % (HD / 8)) * 8;
         const float tv = sm.sk_a[i], bv = sm.sk_b[i];
         if (tv > bv && tv > -1e8f) {
           const int j = sm.si_a[i], s = sm.si_b[i];
-          sm.ak[s * KS + d] = kr[(long long)j * HD + d];
-          sm.av[s * KS + d] = v[(long long)j * HD + d];
+          copy8(&sm.ak[s * KS + d8], kr + (long long)j * HD + d8);
+          copy8(&sm.av[s * KS + d8], v + (long long)j * HD + d8);
         }
       }
       if (tid < kc) {
@@ -750,31 +907,31 @@ __global__ void __launch_bounds__(NT) chain_kernel(b3_chain_args a) {
       // ---------------- Gershgorin-safe delta rule into M_res
       gershgorin<T, HD>(sm, kr, l, wave, lane);
       __syncthreads();
-      delta_update<T, HD>(sm, M, errg, kr, v, l, gam, wave, lane, tid);
+      delta_update<T, HD>(sm, ws, M, snap_m, kr, v, l, gam, wave, lane, tid);
       __syncthreads();
     }
 
     // ---------------- per-step outputs; the roped keys also serve the next step
-    T* kdst = a.snap_k ? reinterpret_cast<T*>(a.snap_k) + step * kv_blk + (long long)bh * S * HD : kread_w;
+    T* kdst = a.snap_k ? reinterpret_cast<T*>(a.snap_k) + step * BH * S * HD + (long long)bh * S * HD
+                       : (sm.KREAD_LDS ? nullptr : kread_w);
     rope_slots_to<T, HD>(kdst, sm, a.inv_freq, tid);
-    kread = kdst;
+    if (kdst) kread = kdst;
     if (a.snap_v) {
-      T* vd = reinterpret_cast<T*>(a.snap_v) + step * kv_blk + (long long)bh * S * HD;
-      for (int it = tid; it < S * HD; it += NT) vd[it] = sm.av[(it / HD) * KS + it % HD];
+      T* vd = reinterpret_cast<T*>(a.snap_v) + step * BH * S * HD + (long long)bh * S * HD;
+      for (int it = tid; it < S * (HD / 8); it += NT) {
+        const int s = it / (HD / 8), d8 = (it % (HD / 8)) * 8;
+        copy8(vd + s * HD + d8, &sm.av[s * KS + d8]);
+      }
     }
     if (a.snap_bias && tid < S) {
-      a.snap_bias[(long long)step * a.B * a.HKV * S + bh * S + tid] =
+      a.snap_bias[(long long)step * BH * S + bh * S + tid] =
           sm.act[tid] ? mul_rn(kap, logf(fmaxf(sm.mass[tid], 1.0f))) : -INFINITY;
-    }
-    if (a.snap_m) {
-      float* md = a.snap_m + (long long)step * a.B * a.HKV * HD * HD + (long long)bh * HD * HD;
-      for (int it = tid; it < HD * HD; it += NT) md[it] = M[it];
     }
     __threadfence_block();
     __syncthreads();
   }
 
-  // store state
+  // store state (M was written after every steady step)
   for (int it = tid; it < S * HD; it += NT) {
     g_ak[it] = sm.ak[(it / HD) * KS + it % HD];
     g_av[it] = sm.av[(it / HD) * KS + it % HD];
@@ -796,9 +953,9 @@ static int launch_chain(const b3_chain_args& a, hipStream_t st) {
 }  // namespace b3
 
 extern "C" int64_t bolt3_chain_workspace_bytes(int32_t dtype, int32_t B, int32_t HKV, int32_t HD, int32_t S) {
-  const int64_t es = dtype == B3_BF16 ? 2 : 4;
   const int64_t bh = (int64_t)B * HKV;
-  return bh * S * HD * es + bh * 32 * (HD + 4) * 4;
+  if (dtype == B3_BF16) return bh * (HD == 64 ? b3::Work<uint16_t, 64>::PER_BH : b3::Work<uint16_t, 128>::PER_BH);
+  return bh * (HD == 64 ? b3::Work<float, 64>::PER_BH : b3::Work<float, 128>::PER_BH);
 }
 
 extern "C" int bolt3_chain(const b3_chain_args* a, void* stream) {

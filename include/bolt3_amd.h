@@ -114,15 +114,20 @@ typedef struct {
 } b3_chain_args;
 
 /*
- * Consolidation chain: n_steps successive _consolidate_functional calls per bh,
- * one workgroup per bh with the slot state resident in LDS.
+ * Consolidation chain: n_steps successive _consolidate_functional calls per bh.
+ * Three kernels on the stream: the slot decisions (one workgroup per bh, slot
+ * state resident in LDS), the Gershgorin scales (one workgroup per step and bh)
+ * and the M_res delta rule (one workgroup per bh and 32 columns of M).
  * Replaces vsa_lm/config/bolt3.py:68-192 (fill, score, merge, evict, Gershgorin
  * delta-rule M_res update) as driven by the chunk loop at :262-273 and by
  * Bolt3Decoder.step at :406-425.  Token lengths per step must be <= 256,
  * S == 128, HD in {64, 128}.
  */
 int bolt3_chain(const b3_chain_args* a, void* stream);
-int64_t bolt3_chain_workspace_bytes(int32_t dtype, int32_t B, int32_t HKV, int32_t HD, int32_t S);
+/* Workspace bytes for a launch of n_steps steps: per-step delta-rule weights and Gershgorin
+   scales (3 x n_steps x B*HKV x 256 floats) plus, for fp32 storage with HD == 128, the roped
+   slot keys (B*HKV x S x HD floats). */
+int64_t bolt3_chain_workspace_bytes(int32_t dtype, int32_t B, int32_t HKV, int32_t HD, int32_t S, int32_t n_steps);
 
 typedef struct {
   int32_t dtype, B, H, HKV, HD, S, C, n_sinks;

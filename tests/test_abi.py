@@ -35,10 +35,11 @@ def test_library_loads_and_exports_everything():
 
 def test_workspace_size_formula():
     lib = A.load()
-    # per bh: roped slot keys + M^T fp32 + M^T bf16 hi and lo + two fp32 [HD][33] tiles
-    per_bh = lambda es, hd: 128 * hd * es + hd * hd * 4 + 2 * hd * hd * 2 + 2 * hd * 33 * 4
-    assert lib.bolt3_chain_workspace_bytes(1, 4, 8, 128, 128) == 32 * per_bh(2, 128)
-    assert lib.bolt3_chain_workspace_bytes(0, 1, 3, 64, 128) == 3 * per_bh(4, 64)
+    # per (step, bh): w, bsafe and 1/|k| rows of 256 floats; fp32 / HD=128 adds the roped slot keys per bh
+    rows = lambda steps, bh: 3 * steps * bh * 256 * 4
+    assert lib.bolt3_chain_workspace_bytes(1, 4, 8, 128, 128, 30) == rows(30, 32)
+    assert lib.bolt3_chain_workspace_bytes(0, 1, 3, 64, 128, 1) == rows(1, 3)
+    assert lib.bolt3_chain_workspace_bytes(0, 2, 2, 128, 128, 5) == rows(5, 4) + 4 * 128 * 128 * 4
 
 
 def test_rejects_bad_arguments_without_gpu_work():

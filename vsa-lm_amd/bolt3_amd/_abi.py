@@ -106,7 +106,7 @@ def load():
         fn = getattr(lib, name)
         fn.argtypes = [C.POINTER(st), p]
         fn.restype = C.c_int
-    lib.bolt3_chain_workspace_bytes.argtypes = [i32, i32, i32, i32, i32]
+    lib.bolt3_chain_workspace_bytes.argtypes = [i32, i32, i32, i32, i32, i32]
     lib.bolt3_chain_workspace_bytes.restype = i64
     lib.bolt3_version.argtypes = []
     lib.bolt3_version.restype = C.c_char_p
@@ -160,5 +160,5 @@ def call(name: str, args, device: torch.device):
         _timers.setdefault(name, []).append(ev)
 
 
-def chain_workspace_bytes(dt: torch.dtype, B: int, HKV: int, HD: int, S: int) -> int:
-    return int(load().bolt3_chain_workspace_bytes(dtype_code(dt), B, HKV, HD, S))
+def chain_workspace_bytes(dt: torch.dtype, B: int, HKV: int, HD: int, S: int, n_steps: int) -> int:
+    return int(load().bolt3_chain_workspace_bytes(dtype_code(dt), B, HKV, HD, S, n_steps))

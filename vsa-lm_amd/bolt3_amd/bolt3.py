@@ -153,7 +153,7 @@ class Bolt3Attn(nn.Module):
     def _chain(self, dt, device, B, kr, kp, v, tok_bh_stride, pos, beta, beta_bh_stride, n_steps, off0, len0,
                step_stride, step_len, n_filled, st: dict, m_res, gam, side, snap_k=None, snap_v=None,
                snap_bias=None, snap_m=None, log=None):
-        work = torch.empty(A.chain_workspace_bytes(dt, B, self.HKV, self.HD, self.S), dtype=torch.uint8,
+        work = torch.empty(A.chain_workspace_bytes(dt, B, self.HKV, self.HD, self.S, n_steps), dtype=torch.uint8,
                            device=device)
         a = A.ChainArgs()
         a.dtype, a.B, a.HKV, a.HD, a.S = A.dtype_code(dt), B, self.HKV, self.HD, self.S

@@ -1,5 +1,5 @@
-// Consolidation chain: successive attractor consolidations of one (batch,
-// kv-head) row per workgroup.
+// Consolidation chain: successive attractor consolidations of every (batch,
+// kv-head) row.
 //
 // Replaces Bolt3Attn._consolidate_functional (vsa_lm/config/bolt3.py:68-192)
 // as driven by the chunk loop (:262-273) and Bolt3Decoder.step (:406-425).
@@ -13,15 +13,23 @@
 //          replace the least useful slots; the rest go into M_res by the
 //          Gershgorin-safe delta rule M <- g*M + K^T diag(b) (V - K M).
 //
-// Layout: one 256-thread workgroup (4 wavefronts) per bh.  Slot keys/values,
-// masses, utilities, positions and activity stay in LDS for all steps.  M_res
-// is kept transposed in the workspace, in fp32 and (bf16 storage) split into
-// bf16 hi + lo, so every MFMA operand is one 16-byte load; the state array
-// [bh][HD][HD] is written after every step.  bf16 storage multiplies exact
-// bf16 operands (products are exact in fp32) and splits fp32 operands into
-// hi + lo; fp32 storage uses the fp32 MFMA.  Orderings are ranks computed by
-// counting on monotone integer keys (one pass, stable): the larger value
-// first (NaN first), equal values by lower index.
+// The slot decisions never read M_res, so one launch of bolt3_chain runs three
+// kernels on the stream:
+//   decide_kernel  one 512-thread workgroup per bh walks all steps with the
+//                  slot state in LDS and writes, per step, the delta-rule
+//                  weight w_j = beta_j * [token j goes to M_res], the roped
+//                  slot keys / values / bias snapshots and the decision log;
+//   gersh_kernel   one workgroup per (step, bh), all in parallel: Gershgorin
+//                  column sums of |Khat Khat^T| diag(w) -> bsafe_j, and 1/|k_j|;
+//   mres_kernel    one workgroup per (bh, 32 columns of M): the columns of M
+//                  evolve independently under the delta rule, so HD/32
+//                  workgroups per bh walk the steps, each keeping its M^T block
+//                  in LDS (fp32 and, for bf16 storage, bf16 hi + lo so every
+//                  MFMA operand is exact bf16).
+// bf16 storage multiplies exact bf16 operands (products are exact in fp32) and
+// splits fp32 operands into hi + lo; fp32 storage uses the fp32 MFMA.
+// Orderings are ranks computed by counting on monotone integer keys (one pass,
+// stable): the larger value first (NaN first), equal values by lower index.
 #include "bolt3_common.h"
 #include "bolt3_math.h"
 #include "bolt3_amd.h"
@@ -30,46 +38,54 @@ namespace b3 {
 
 constexpr int S = 128;     // attractor slots
 constexpr int LMAX = 256;  // tokens per consolidation step
-constexpr int NT = 256;    // threads per workgroup
-constexpr int NWAVE = NT / WAVE;
+constexpr int DT = 512;    // decide_kernel threads
+constexpr int DWAVES = DT / WAVE;
+constexpr int MT = 256;    // gersh_kernel / mres_kernel threads
+constexpr int MWAVES = MT / WAVE;
 constexpr float SIM_K = 0.88f, SIM_V = 0.80f, UTIL_DECAY = 0.995f;
 
 enum : int { F_MERGE = 1, F_DELTA = 2, F_INS = 4 };
 
-// Workspace layout per bh (bytes): roped slot keys of the current state, M^T fp32,
-// M^T bf16 hi and lo, and (when they do not fit in LDS) the delta-rule tile buffers.
+// Workspace: roped slot keys per bh when they do not fit in LDS (fp32, HD=128), then
+// three [n_steps][bh][LMAX] float arrays: w, bsafe, 1/|k|.
 template <typename T, int HD>
 struct Work {
-  static constexpr long long KREAD = (long long)S * HD * sizeof(T);
-  static constexpr long long MT32 = (long long)HD * HD * 4;
-  static constexpr long long MTBF = (long long)HD * HD * 2;
-  static constexpr long long TILE = 2LL * HD * 33 * 4;
-  static constexpr long long PER_BH = KREAD + MT32 + 2 * MTBF + TILE;
+  static constexpr bool KREAD_LDS = sizeof(T) == 2 || HD == 64;
+  static constexpr long long KREAD = KREAD_LDS ? 0 : (long long)S * HD * sizeof(T);
+  static long long bytes(long long bh, long long n_steps) { return bh * KREAD + 3 * n_steps * bh * LMAX * 4; }
 };
 
+// Token range of a step.  Steps are fill steps while slots are free; the slot count
+// after each step depends only on the token counts, so every kernel derives it alike.
+__device__ __forceinline__ int step_len(const b3_chain_args& a, int step) { return step == 0 ? a.len0 : a.step_len; }
+__device__ __forceinline__ int step_off(const b3_chain_args& a, int step) {
+  return step == 0 ? a.off0 : step * a.step_stride;
+}
+
+// ----------------------------------------------------------------- decide_kernel LDS
+
 template <typename T, int HD>
-struct ChainSmem {
+struct DecSmem {
   static constexpr int KS = sizeof(T) == 2 ? HD + 8 : HD + 4;   // slot row stride (16-byte aligned rows)
-  static constexpr int TS = sizeof(T) == 2 ? 32 + 8 : 32 + 1;   // token-tile row stride (transposed tiles)
-  static constexpr bool TILE_LDS = !(sizeof(T) == 4 && HD == 128);
+  static constexpr bool KREAD_LDS = Work<T, HD>::KREAD_LDS;
   alignas(16) T ak[S * KS];
   alignas(16) T av[S * KS];
-  float mass[S], util[S], pm[S], inv_nak[S], keep[S], bias[S], psum[S];
-  int act[S], cnt[S], off[S], hits[S];
-  float rel[LMAX], score[LMAX], best[LMAX], simv[LMAX], inv_nkr[LMAX], w[LMAX], bsafe[LMAX], ck[LMAX];
-  int slot[LMAX], flags[LMAX], mlist[LMAX];
+  alignas(16) T kread[KREAD_LDS ? S * KS : 1];                    // roped slot keys
+  float mass[S], util[S], pm[S], inv_nak[S], keep[S], bias[S];
+  int act[S], dirty[S];
+  float invf[HD / 2];
+  float rel[LMAX], score[LMAX], best[LMAX], simv[LMAX], ck[LMAX];
+  int slot[LMAX], flags[LMAX];
   float sk_a[LMAX];
   int si_a[LMAX];
   float sk_b[S];
   int si_b[S];
-  uint32_t ok_a[LMAX], ok_b[S];   // order keys
-  // delta-rule tiles: K^T [HD][32] and the error tile E^T [HD][32] (bf16: hi and lo)
-  static constexpr bool KREAD_LDS = sizeof(T) == 2;              // roped slot keys of the current state
-  alignas(16) T kread[KREAD_LDS ? S * KS : 1];
-  alignas(16) T krt[TILE_LDS ? HD * TS : 1];
-  alignas(16) T ert_hi[TILE_LDS ? HD * TS : 1];
-  alignas(16) uint16_t ert_lo[(TILE_LDS && sizeof(T) == 2) ? HD * TS : 1];
-  int nhit;
+  union {  // phase-local buffers
+    struct { float e2[2][LMAX], v2[2][LMAX], bv[2][LMAX]; int bs[2][LMAX]; } sc;
+    struct { int cnt[S], off[S], hits[S], mlist[LMAX]; float psum[S]; int nhit; } mg;
+    struct { float mx[2][S]; int nan[2][S]; } kp;
+    struct { alignas(16) uint32_t a[LMAX]; alignas(16) uint32_t b[S]; } ok;
+  } u;
 };
 
 // ----------------------------------------------------------------- fragments
@@ -155,6 +171,34 @@ __device__ __forceinline__ void ld8(const float* p, float* o) {
   const float4 a = *reinterpret_cast<const float4*>(p), b = *reinterpret_cast<const float4*>(p + 4);
   o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w; o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
 }
+// 4 consecutive elements as floats
+__device__ __forceinline__ void ld4(const uint16_t* p, float* o) {
+  const u16x4 q = *reinterpret_cast<const u16x4*>(p);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = bf2f(q[i]);
+}
+__device__ __forceinline__ void ld4(const float* p, float* o) {
+  const float4 q = *reinterpret_cast<const float4*>(p);
+  o[0] = q.x; o[1] = q.y; o[2] = q.z; o[3] = q.w;
+}
+
+// 4 consecutive storage elements kept packed in registers (bf16: 2 VGPRs)
+template <typename T> struct V4;
+template <> struct V4<uint16_t> {
+  u16x4 x;
+  __device__ __forceinline__ void load(const uint16_t* p, bool ok) {
+    if (ok) x = *reinterpret_cast<const u16x4*>(p);
+    else { x[0] = 0; x[1] = 0; x[2] = 0; x[3] = 0; }
+  }
+  __device__ __forceinline__ float get(int q) const { return bf2f(x[q]); }
+};
+template <> struct V4<float> {
+  float4 x;
+  __device__ __forceinline__ void load(const float* p, bool ok) {
+    x = ok ? *reinterpret_cast<const float4*>(p) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  __device__ __forceinline__ float get(int q) const { return q == 0 ? x.x : q == 1 ? x.y : q == 2 ? x.z : x.w; }
+};
 
 // 8 consecutive elements, 16-byte (bf16) or 2 x 16-byte (fp32) moves; both pointers aligned
 __device__ __forceinline__ void copy8(uint16_t* d, const uint16_t* s) {
@@ -165,47 +209,7 @@ __device__ __forceinline__ void copy8(float* d, const float* s) {
   *reinterpret_cast<float4*>(d + 4) = *reinterpret_cast<const float4*>(s + 4);
 }
 
-// ----------------------------------------------------------------- helpers
-
-// Slot keys roped at their mean positions -> `dst` (global, may be null) and, for bf16
-// storage, the LDS copy the next scoring reads.
-template <typename T, int HD>
-__device__ void rope_slots_to(T* dst, ChainSmem<T, HD>& sm, const float* inv_freq, int tid) {
-  constexpr int HALF = HD / 2;
-  for (int it = tid; it < S * HALF; it += NT) {
-    const int s = it / HALF, i = it % HALF;
-    float sn, cs;
-    sincos_rope(mul_rn(sm.pm[s], inv_freq[i]), &sn, &cs);
-    const float c = St<T>::rnd(cs), si = St<T>::rnd(sn);
-    const float x0 = St<T>::to_f(sm.ak[s * sm.KS + i]), x1 = St<T>::to_f(sm.ak[s * sm.KS + i + HALF]);
-    const T r0 = St<T>::from_f(add_rn(St<T>::rnd(mul_rn(x0, c)), St<T>::rnd(mul_rn(-x1, si))));
-    const T r1 = St<T>::from_f(add_rn(St<T>::rnd(mul_rn(x1, c)), St<T>::rnd(mul_rn(x0, si))));
-    if (dst) {
-      dst[s * HD + i] = r0;
-      dst[s * HD + i + HALF] = r1;
-    }
-    if constexpr (ChainSmem<T, HD>::KREAD_LDS) {
-      sm.kread[s * sm.KS + i] = r0;
-      sm.kread[s * sm.KS + i + HALF] = r1;
-    }
-  }
-}
-
-// 1 / max(||ak_s||, 1e-12) for every slot (two threads per slot).
-template <typename T, int HD>
-__device__ void slot_norms(ChainSmem<T, HD>& sm, int tid) {
-  const int s = tid >> 1, half = tid & 1;
-  float ss = 0.f;
-#pragma unroll
-  for (int d = half * (HD / 2); d < (half + 1) * (HD / 2); d += 8) {
-    float x[8];
-    ld8(&sm.ak[s * sm.KS + d], x);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) ss += x[i] * x[i];
-  }
-  ss += __shfl_xor(ss, 1, 64);
-  if (half == 0) sm.inv_nak[s] = 1.0f / fmaxf(sqrtf(ss), 1e-12f);
-}
+// ----------------------------------------------------------------- orderings
 
 // Monotone integer image of a float: a < b  <=>  ord(a) < ord(b); NaN maps above +inf, so
 // it ranks first in a descending and last in an ascending order (torch.topk's placement).
@@ -216,47 +220,114 @@ __device__ __forceinline__ uint32_t ord_key(float f) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-// Rank of element `me` among ok[0..n) (order keys), ties by lower index.
+// Rank of element `me` among ok[0..n) (order keys, 16-byte aligned array), ties by lower
+// index.  Descending: keys above, plus equal keys at lower indices.
 __device__ __forceinline__ int rank_desc(const uint32_t* ok, int n, int me) {
   const uint32_t x = ok[me];
-  int r = 0;
-  for (int i = 0; i < n; ++i) {
-    const uint32_t y = ok[i];
-    r += (y > x || (y == x && i < me)) ? 1 : 0;
+  int r = 0, i = 0;
+#pragma unroll 8
+  for (; i + 4 <= n; i += 4) {
+    const uint4 y = *reinterpret_cast<const uint4*>(ok + i);
+    r += (y.x > x || (y.x == x && i + 0 < me)) ? 1 : 0;
+    r += (y.y > x || (y.y == x && i + 1 < me)) ? 1 : 0;
+    r += (y.z > x || (y.z == x && i + 2 < me)) ? 1 : 0;
+    r += (y.w > x || (y.w == x && i + 3 < me)) ? 1 : 0;
   }
+  for (; i < n; ++i) r += (ok[i] > x || (ok[i] == x && i < me)) ? 1 : 0;
   return r;
 }
 __device__ __forceinline__ int rank_asc(const uint32_t* ok, int n, int me) {
   const uint32_t x = ok[me];
-  int r = 0;
-  for (int i = 0; i < n; ++i) {
-    const uint32_t y = ok[i];
-    r += (y < x || (y == x && i < me)) ? 1 : 0;
+  int r = 0, i = 0;
+#pragma unroll 8
+  for (; i + 4 <= n; i += 4) {
+    const uint4 y = *reinterpret_cast<const uint4*>(ok + i);
+    r += (y.x < x || (y.x == x && i + 0 < me)) ? 1 : 0;
+    r += (y.y < x || (y.y == x && i + 1 < me)) ? 1 : 0;
+    r += (y.z < x || (y.z == x && i + 2 < me)) ? 1 : 0;
+    r += (y.w < x || (y.w == x && i + 3 < me)) ? 1 : 0;
   }
+  for (; i < n; ++i) r += (ok[i] < x || (ok[i] == x && i < me)) ? 1 : 0;
   return r;
 }
 
-// ----------------------------------------------------------------- retrieval (phase A)
+// ----------------------------------------------------------------- decide: helpers
 
-// For one 32-token tile: rel_err from the softmax read of the slots, cosine
-// match, and (steady) the merge test.  `kread` holds the roped slot keys.
+// Roped copies of the dirty slot keys (rotation at the slot's mean position), into the
+// LDS copy (bf16) or the workspace copy (fp32, HD=128).  8 rotation pairs per item.
 template <typename T, int HD>
-__device__ void score_tile(ChainSmem<T, HD>& sm, const T* kread, const T* kr, const T* kp, const T* v,
-                           int t0, int l, bool steady, float scale, int lane) {
+__device__ void rope_dirty(DecSmem<T, HD>& sm, T* kread_g, int tid) {
+  constexpr int HALF = HD / 2, P8 = HALF / 8;
+  T* dst = sm.KREAD_LDS ? sm.kread : kread_g;
+  const int rs = sm.KREAD_LDS ? sm.KS : HD;
+  for (int it = tid; it < S * P8; it += DT) {
+    const int s = it / P8, i0 = (it % P8) * 8;
+    if (!sm.dirty[s]) continue;
+    float x0[8], x1[8];
+    ld8(&sm.ak[s * sm.KS + i0], x0);
+    ld8(&sm.ak[s * sm.KS + i0 + HALF], x1);
+    const float p = sm.pm[s];
+    alignas(16) T r0[8];
+    alignas(16) T r1[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      float sn, cs;
+      sincos_rope(mul_rn(p, sm.invf[i0 + q]), &sn, &cs);
+      const float c = St<T>::rnd(cs), si = St<T>::rnd(sn);
+      r0[q] = St<T>::from_f(add_rn(St<T>::rnd(mul_rn(x0[q], c)), St<T>::rnd(mul_rn(-x1[q], si))));
+      r1[q] = St<T>::from_f(add_rn(St<T>::rnd(mul_rn(x1[q], c)), St<T>::rnd(mul_rn(x0[q], si))));
+    }
+    copy8(dst + s * rs + i0, r0);
+    copy8(dst + s * rs + i0 + HALF, r1);
+  }
+}
+
+// 1 / max(||ak_s||, 1e-12) for every slot (four threads per slot).
+template <typename T, int HD>
+__device__ void slot_norms(DecSmem<T, HD>& sm, int tid) {
+  const int s = tid >> 2, q = tid & 3;
+  float ss = 0.f;
+#pragma unroll
+  for (int d = q * (HD / 4); d < (q + 1) * (HD / 4); d += 8) {
+    float x[8];
+    ld8(&sm.ak[s * sm.KS + d], x);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ss += x[i] * x[i];
+  }
+  ss += __shfl_xor(ss, 1, 64);
+  ss += __shfl_xor(ss, 2, 64);
+  if (q == 0) sm.inv_nak[s] = 1.0f / fmaxf(sqrtf(ss), 1e-12f);
+}
+
+// ----------------------------------------------------------------- decide: retrieval
+
+// One 32-token tile, one half of the work: both waves of a pair compute the slot
+// softmax for the tile (identical results); wave `half` then forms v_hat on its half of
+// the feature dims and the cosine match on its half of the slots, and leaves partial
+// sums / partial argmax in LDS for the combine pass.
+template <typename T, int HD>
+__device__ void score_tile(DecSmem<T, HD>& sm, const T* kread, const T* kr, const T* kp, const T* v,
+                           int t0, int l, bool steady, float scale, int half, int lane) {
   const int n = lane & 31, h = lane >> 5;
   const int tok = t0 + n;
-  f32x16 acc[4];
+  constexpr int NDB = HD / 32, HDB = NDB / 2;
+  const bool in = tok < l;
 
-  // scores^T[slot][tok] = kread . kp^T
-  {
-    Frag<T, HD> f;
-    f.load(kp, tok, l, lane);
+  Frag<T, HD> fq;
+  fq.load(kp, tok, l, lane);
+  V4<T> vx[HDB][4];   // v[tok][32*db + 8*g + 4*h + q], raw storage values
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
-      acc[mb] = zero16();
-      if constexpr (ChainSmem<T, HD>::KREAD_LDS) mm_rows_frag<HD>(acc[mb], sm.kread, sm.KS, 32 * mb, f, lane);
-      else mm_rows_frag<HD>(acc[mb], kread, HD, 32 * mb, f, lane);
-    }
+  for (int i = 0; i < HDB; ++i)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) vx[i][g].load(v + (long long)tok * HD + 32 * (half * HDB + i) + 8 * g + 4 * h, in);
+
+  // scores^T[slot][tok] = kread . kp^T over all slots
+  f32x16 acc[4];
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) {
+    acc[mb] = zero16();
+    if constexpr (DecSmem<T, HD>::KREAD_LDS) mm_rows_frag<HD>(acc[mb], sm.kread, sm.KS, 32 * mb, fq, lane);
+    else mm_rows_frag<HD>(acc[mb], kread, HD, 32 * mb, fq, lane);
   }
   // softmax over the slots (column of this lane pair)
   float mx = -INFINITY;
@@ -287,24 +358,24 @@ __device__ void score_tile(ChainSmem<T, HD>& sm, const T* kread, const T* kr, co
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[mb][r] = St<T>::rnd(mul_rn(acc[mb][r], rs));
 
-  // v_hat^T[d][tok] = av^T . P^T
-  constexpr int NDB = HD / 32;
-  f32x16 vh[NDB];
+  // v_hat^T[d][tok] = av^T . P^T on this wave's feature half; partial rel_err sums
+  float e2 = 0.f, v2 = 0.f;
 #pragma unroll
-  for (int db = 0; db < NDB; ++db) {
-    vh[db] = zero16();
+  for (int i = 0; i < HDB; ++i) {
+    const int db = half * HDB + i;
+    f32x16 vh = zero16();
     const int d = 32 * db + n;
     if constexpr (St<T>::is_bf16) {
 #pragma unroll
       for (int kc = 0; kc < 8; ++kc) {
-        u16x8 a, b;
+        u16x8 av8, p8;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const int s = 16 * kc + 8 * (i >> 2) + 4 * h + (i & 3);
-          a[i] = sm.av[s * sm.KS + d];
-          b[i] = f2bf(acc[kc >> 1][8 * (kc & 1) + i]);
+        for (int q = 0; q < 8; ++q) {
+          const int s = 16 * kc + 8 * (q >> 2) + 4 * h + (q & 3);
+          av8[q] = sm.av[s * sm.KS + d];
+          p8[q] = f2bf(acc[kc >> 1][8 * (kc & 1) + q]);
         }
-        mma_bf16(vh[db], a, b);
+        mma_bf16(vh, av8, p8);
       }
     } else {
 #pragma unroll
@@ -312,76 +383,83 @@ __device__ void score_tile(ChainSmem<T, HD>& sm, const T* kread, const T* kr, co
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int s = 32 * mb + d_row(lane, r);
-          mma_f32(vh[db], sm.av[s * sm.KS + d], acc[mb][r]);
+          mma_f32(vh, sm.av[s * sm.KS + d], acc[mb][r]);
         }
     }
-  }
-  // rel_err = ||v - v_hat|| / (||v|| + 1e-6)
-  float e2 = 0.f, v2 = 0.f;
-  if (tok < l) {
 #pragma unroll
-    for (int db = 0; db < NDB; ++db)
+    for (int g = 0; g < 4; ++g)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int d0 = 32 * db + 8 * g + 4 * h;
-        float x[4];
-        if constexpr (St<T>::is_bf16) {
-          const u16x4 q = *reinterpret_cast<const u16x4*>(v + (long long)tok * HD + d0);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) x[i] = bf2f(q[i]);
-        } else {
-          const float4 q = *reinterpret_cast<const float4*>(v + (long long)tok * HD + d0);
-          x[0] = q.x; x[1] = q.y; x[2] = q.z; x[3] = q.w;
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float dv = x[i] - St<T>::rnd(vh[db][4 * g + i]);
-          e2 += dv * dv;
-          v2 += x[i] * x[i];
-        }
+      for (int q = 0; q < 4; ++q) {
+        const float x = vx[i][g].get(q);
+        const float dv = x - St<T>::rnd(vh[4 * g + q]);
+        e2 += dv * dv;
+        v2 += x * x;
       }
   }
   e2 += xor32(e2);
   v2 += xor32(v2);
-  const float rel = sqrtf(e2) / (sqrtf(v2) + 1e-6f);
 
-  // cos^T[slot][tok] = ak . kr^T / (|ak| |kr|)
+  // cos^T[slot][tok] = ak . kr^T / (|ak| |kr|) on this wave's half of the slots
   Frag<T, HD> fk;
   fk.load(kr, tok, l, lane);
   float kk = fk.sumsq();
   kk += xor32(kk);
   const float inv_nk = 1.0f / fmaxf(sqrtf(kk), 1e-12f);
-#pragma unroll
-  for (int mb = 0; mb < 4; ++mb) {
-    acc[mb] = zero16();
-    mm_rows_frag<HD>(acc[mb], sm.ak, sm.KS, 32 * mb, fk, lane);
-  }
   float bv = -INFINITY;
   int bs = 0;
   bool first = true;
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb)
+  for (int m2 = 0; m2 < 2; ++m2) {
+    const int mb = 2 * half + m2;
+    f32x16 c = zero16();
+    mm_rows_frag<HD>(c, sm.ak, sm.KS, 32 * mb, fk, lane);
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int s = 32 * mb + d_row(lane, r);
-      float c = acc[mb][r] * (sm.inv_nak[s] * inv_nk);
-      if (!steady && !sm.act[s]) c = 0.f;
-      if (first || ranks_before_desc(c, s, bv, bs)) { bv = c; bs = s; first = false; }
+      float cv = c[r] * (sm.inv_nak[s] * inv_nk);
+      if (!steady && !sm.act[s]) cv = 0.f;
+      if (first || ranks_before_desc(cv, s, bv, bs)) { bv = cv; bs = s; first = false; }
     }
+  }
   {
     const float ov = xor32(bv);
     const int os = xor32i(bs);
     if (ranks_before_desc(ov, os, bv, bs)) { bv = ov; bs = os; }
   }
-  const float score = rel * (1.0f - fminf(fmaxf(bv, 0.0f), 1.0f));
+  if (h == 0 && in) {
+    sm.u.sc.e2[half][tok] = e2;
+    sm.u.sc.v2[half][tok] = v2;
+    sm.u.sc.bv[half][tok] = bv;
+    sm.u.sc.bs[half][tok] = bs;
+  }
+}
 
+// Combine the two halves per token (two threads per token): rel_err, best slot, score,
+// value cosine with the best slot (steady), merge flag.  Returns this token's merge flag
+// on the token's first thread.
+template <typename T, int HD>
+__device__ bool score_combine(DecSmem<T, HD>& sm, const T* v, int l, bool steady, int tid) {
+  const int tok = tid >> 1, part = tid & 1;
+  const bool in = tok < l;
+  float rel = 0.f, bv = 0.f, score = 0.f;
+  int bs = 0;
+  if (in) {
+    const float e2 = sm.u.sc.e2[0][tok] + sm.u.sc.e2[1][tok];
+    const float v2 = sm.u.sc.v2[0][tok] + sm.u.sc.v2[1][tok];
+    rel = sqrtf(e2) / (sqrtf(v2) + 1e-6f);
+    bv = sm.u.sc.bv[0][tok];
+    bs = sm.u.sc.bs[0][tok];
+    const float b1 = sm.u.sc.bv[1][tok];
+    const int s1 = sm.u.sc.bs[1][tok];
+    if (ranks_before_desc(b1, s1, bv, bs)) { bv = b1; bs = s1; }
+    score = rel * (1.0f - fminf(fmaxf(bv, 0.0f), 1.0f));
+  }
   float simv = 0.f;
   if (steady) {
-    // cos(v_tok, av[best]) over this lane's half of the features
     float dvv = 0.f, vv = 0.f, aa = 0.f;
-    if (tok < l) {
+    if (in) {
 #pragma unroll
-      for (int d = h * (HD / 2); d < (h + 1) * (HD / 2); d += 8) {
+      for (int d = part * (HD / 2); d < (part + 1) * (HD / 2); d += 8) {
         float x[8], y[8];
         ld8(v + (long long)tok * HD + d, x);
         ld8(&sm.av[bs * sm.KS + d], y);
@@ -393,261 +471,64 @@ __device__ void score_tile(ChainSmem<T, HD>& sm, const T* kread, const T* kr, co
         }
       }
     }
-    dvv += xor32(dvv);
-    vv += xor32(vv);
-    aa += xor32(aa);
+    dvv += __shfl_xor(dvv, 1, 64);
+    vv += __shfl_xor(vv, 1, 64);
+    aa += __shfl_xor(aa, 1, 64);
     simv = dvv / (fmaxf(sqrtf(vv), 1e-8f) * fmaxf(sqrtf(aa), 1e-8f));
   }
-  if (h == 0 && tok < l) {
+  const bool merge = in && steady && bv >= SIM_K && simv >= SIM_V;
+  if (part == 0 && in) {
     sm.rel[tok] = rel;
     sm.score[tok] = score;
     sm.best[tok] = bv;
     sm.simv[tok] = simv;
     sm.slot[tok] = bs;
-    sm.inv_nkr[tok] = inv_nk;
-    sm.flags[tok] = (steady && bv >= SIM_K && simv >= SIM_V) ? F_MERGE : 0;
+    sm.flags[tok] = merge ? F_MERGE : 0;
   }
+  return merge && part == 0;
 }
 
-// ----------------------------------------------------------------- delta rule (phase E)
-
-// gersh_j = max(sum_i |khat_i . khat_j| w_i, 1); bsafe_j = w_j / gersh_j
-template <typename T, int HD>
-__device__ void gershgorin(ChainSmem<T, HD>& sm, const T* kr, int l, int wave, int lane) {
-  const int nT = (l + 31) / 32;
-  const int n = lane & 31;
-  for (int tj = wave; tj < nT; tj += NWAVE) {
-    const int j = 32 * tj + n;
-    Frag<T, HD> fj;
-    fj.load(kr, j, l, lane);
-    const float inj = j < l ? sm.inv_nkr[j] : 0.f;
-    float colsum = 0.f;
-    for (int ti = 0; ti < nT; ++ti) {
-      f32x16 acc = zero16();
-      Frag<T, HD> fi;
-      fi.load(kr, 32 * ti + (lane & 31), l, lane);
-      // rows i of tile ti as the A operand: same fragment layout as a B fragment
-      if constexpr (St<T>::is_bf16) {
-#pragma unroll
-        for (int ks = 0; ks < HD / 16; ++ks) mma_bf16(acc, fi.v[ks], fj.v[ks]);
-      } else {
-#pragma unroll 8
-        for (int ks = 0; ks < HD / 2; ++ks) mma_f32(acc, fi.v[ks], fj.v[ks]);
-      }
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int i = 32 * ti + d_row(lane, r);
-        if (i < l) colsum += fabsf(acc[r] * (sm.inv_nkr[i] * inj)) * sm.w[i];
-      }
-    }
-    colsum += xor32(colsum);
-    if ((lane >> 5) == 0 && j < l) sm.bsafe[j] = sm.w[j] / fmaxf(colsum, 1.0f);
-  }
-}
-
-// M <- gamma*M + K^T diag(bsafe) (V - K M) with K = normalized keys, M kept as M^T.
-template <typename T, int HD>
-__device__ void delta_update(ChainSmem<T, HD>& sm, char* ws, float* M, float* snap_m, const T* kr, const T* v,
-                             int l, float gam, int wave, int lane, int tid) {
-  using W = Work<T, HD>;
-  constexpr int NB = HD / 32;
-  constexpr int NBLK = NB * NB;
-  constexpr int PER_WAVE = (NBLK + NWAVE - 1) / NWAVE;
-  const int TS = sm.TS;
-  float* mt32 = reinterpret_cast<float*>(ws + W::KREAD);
-  uint16_t* mthi = reinterpret_cast<uint16_t*>(ws + W::KREAD + W::MT32);
-  uint16_t* mtlo = mthi + HD * HD;
-  T* krt = sm.TILE_LDS ? sm.krt : reinterpret_cast<T*>(ws + W::KREAD + W::MT32 + 2 * W::MTBF);
-  T* ert = sm.TILE_LDS ? sm.ert_hi : krt + HD * 33;
-  uint16_t* erl = sm.ert_lo;
-  const int n = lane & 31, h = lane >> 5;
-  f32x16 upd[PER_WAVE];
-#pragma unroll
-  for (int q = 0; q < PER_WAVE; ++q) upd[q] = zero16();
-  const int nT = (l + 31) / 32;
-
-  for (int t = 0; t < nT; ++t) {
-    const int t0 = 32 * t;
-    // K^T tile: krt[c][j] = kr[t0 + j][c]
-    for (int it = tid; it < 32 * (HD / 8); it += NT) {
-      const int j = it / (HD / 8), c8 = (it % (HD / 8)) * 8;
-      float x[8];
-      if (t0 + j < l) ld8(kr + (long long)(t0 + j) * HD + c8, x);
-      else {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) x[i] = 0.f;
-      }
-#pragma unroll
-      for (int i = 0; i < 8; ++i) krt[(c8 + i) * TS + j] = St<T>::from_f(x[i]);
-    }
-    // v_pred^T[d][j] = sum_c M^T[d][c] kr[j][c]; error tile E^T[d][j] = (v - v_pred) * bsafe_j / |k_j|
-    for (int db = wave; db < NB; db += NWAVE) {
-      const int j = t0 + n;
-      Frag<T, HD> fj;
-      fj.load(kr, j, l, lane);
-      f32x16 acc = zero16();
-      const int d = 32 * db + n;
-      if constexpr (St<T>::is_bf16) {
-#pragma unroll
-        for (int ks = 0; ks < HD / 16; ++ks) {
-          const u16x8 hi = *reinterpret_cast<const u16x8*>(mthi + d * HD + 16 * ks + 8 * h);
-          const u16x8 lo = *reinterpret_cast<const u16x8*>(mtlo + d * HD + 16 * ks + 8 * h);
-          mma_bf16(acc, hi, fj.v[ks]);
-          mma_bf16(acc, lo, fj.v[ks]);
-        }
-      } else {
-#pragma unroll 8
-        for (int ks = 0; ks < HD / 2; ++ks) mma_f32(acc, mt32[d * HD + 2 * ks + h], fj.v[ks]);
-      }
-      const float inj = j < l ? sm.inv_nkr[j] : 0.f;
-      const float bj = j < l ? sm.bsafe[j] : 0.f;
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int d0 = 32 * db + 8 * g + 4 * h;
-        float x[4] = {0.f, 0.f, 0.f, 0.f};
-        if (j < l) {
-          if constexpr (St<T>::is_bf16) {
-            const u16x4 q = *reinterpret_cast<const u16x4*>(v + (long long)j * HD + d0);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) x[i] = bf2f(q[i]);
-          } else {
-            const float4 q = *reinterpret_cast<const float4*>(v + (long long)j * HD + d0);
-            x[0] = q.x; x[1] = q.y; x[2] = q.z; x[3] = q.w;
-          }
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float e = ((x[i] - acc[4 * g + i] * inj) * bj) * inj;
-          if constexpr (St<T>::is_bf16) {
-            const uint16_t hb = f2bf(e);
-            ert[(d0 + i) * TS + n] = hb;
-            erl[(d0 + i) * TS + n] = f2bf(e - bf2f(hb));
-          } else {
-            ert[(d0 + i) * TS + n] = e;
-          }
-        }
-      }
-    }
-    __syncthreads();
-    // upd[c][d] += sum_j K^T[c][j] E^T[d][j]
-#pragma unroll
-    for (int q = 0; q < PER_WAVE; ++q) {
-      const int blk = wave + NWAVE * q;
-      if (blk < NBLK) {
-        const int cb = blk / NB, db = blk % NB;
-        const int c = 32 * cb + n, d = 32 * db + n;
-        if constexpr (St<T>::is_bf16) {
-#pragma unroll
-          for (int kc = 0; kc < 2; ++kc) {
-            const u16x8 a = *reinterpret_cast<const u16x8*>(krt + c * TS + 16 * kc + 8 * h);
-            const u16x8 bh_ = *reinterpret_cast<const u16x8*>(ert + d * TS + 16 * kc + 8 * h);
-            const u16x8 bl_ = *reinterpret_cast<const u16x8*>(erl + d * TS + 16 * kc + 8 * h);
-            mma_bf16(upd[q], a, bh_);
-            mma_bf16(upd[q], a, bl_);
-          }
-        } else {
-#pragma unroll
-          for (int kc = 0; kc < 16; ++kc) mma_f32(upd[q], krt[c * TS + 2 * kc + h], ert[d * TS + 2 * kc + h]);
-        }
-      }
-    }
-    __syncthreads();
-  }
-  // M = gamma*M + upd (two rounded ops, as the reference evaluates them); write M^T (fp32 and
-  // bf16 hi/lo), the state M[c][d] and the snapshot
-#pragma unroll
-  for (int q = 0; q < PER_WAVE; ++q) {
-    const int blk = wave + NWAVE * q;
-    if (blk < NBLK) {
-      const int cb = blk / NB, db = blk % NB;
-      const int d = 32 * db + n;
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int c0 = 32 * cb + 8 * g + 4 * h;
-        const float4 old = *reinterpret_cast<const float4*>(mt32 + d * HD + c0);
-        float nw[4];
-        nw[0] = add_rn(mul_rn(gam, old.x), upd[q][4 * g + 0]);
-        nw[1] = add_rn(mul_rn(gam, old.y), upd[q][4 * g + 1]);
-        nw[2] = add_rn(mul_rn(gam, old.z), upd[q][4 * g + 2]);
-        nw[3] = add_rn(mul_rn(gam, old.w), upd[q][4 * g + 3]);
-        *reinterpret_cast<float4*>(mt32 + d * HD + c0) = make_float4(nw[0], nw[1], nw[2], nw[3]);
-        u16x4 hi4, lo4;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          hi4[i] = f2bf(nw[i]);
-          lo4[i] = f2bf(nw[i] - bf2f(hi4[i]));
-          M[(c0 + i) * HD + d] = nw[i];
-        }
-        *reinterpret_cast<u16x4*>(mthi + d * HD + c0) = hi4;
-        *reinterpret_cast<u16x4*>(mtlo + d * HD + c0) = lo4;
-        if (snap_m) {
-          if constexpr (St<T>::is_bf16) {
-            uint16_t* sh = reinterpret_cast<uint16_t*>(snap_m);
-            *reinterpret_cast<u16x4*>(sh + d * HD + c0) = hi4;
-            *reinterpret_cast<u16x4*>(sh + HD * HD + d * HD + c0) = lo4;
-          } else {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) snap_m[(c0 + i) * HD + d] = nw[i];
-          }
-        }
-      }
-    }
-  }
-}
-
-// ----------------------------------------------------------------- kernel
+// ----------------------------------------------------------------- decide_kernel
 
 template <typename T, int HD>
-__global__ void __launch_bounds__(NT) chain_kernel(b3_chain_args a) {
-  __shared__ ChainSmem<T, HD> sm;
-  using W = Work<T, HD>;
+__global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
+  __shared__ DecSmem<T, HD> sm;
   const int bh = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hkv = bh % a.HKV;
-  const float kap = a.kappa[hkv], gam = a.gamma[hkv];
+  const float kap = a.kappa[hkv];
   const float scale = 1.0f / sqrtf((float)HD);
   const int KS = sm.KS;
+  const long long BH = (long long)a.B * a.HKV;
 
   T* g_ak = reinterpret_cast<T*>(a.ak) + (long long)bh * S * HD;
   T* g_av = reinterpret_cast<T*>(a.av) + (long long)bh * S * HD;
-  float* M = a.m_res + (long long)bh * HD * HD;
-  const long long BH = (long long)a.B * a.HKV;
-  char* ws = reinterpret_cast<char*>(a.work) + (long long)bh * W::PER_BH;
-  T* kread_w = reinterpret_cast<T*>(ws);
-  float* mt32 = reinterpret_cast<float*>(ws + W::KREAD);
-  uint16_t* mthi = reinterpret_cast<uint16_t*>(ws + W::KREAD + W::MT32);
-  uint16_t* mtlo = mthi + HD * HD;
+  char* ws = reinterpret_cast<char*>(a.work);
+  T* kread_g = reinterpret_cast<T*>(ws) + (long long)bh * S * HD;   // used only when !KREAD_LDS
+  float* w_all = reinterpret_cast<float*>(ws + BH * Work<T, HD>::KREAD);
+  const T* kread = sm.KREAD_LDS ? sm.kread : kread_g;
 
-  // load state; M -> M^T (fp32, bf16 hi/lo) in the workspace
-  for (int it = tid; it < S * HD; it += NT) {
-    const int s = it / HD, d = it % HD;
-    sm.ak[s * KS + d] = g_ak[it];
-    sm.av[s * KS + d] = g_av[it];
-  }
-  for (int it = tid; it < HD * HD; it += NT) {
-    const int c = it / HD, d = it % HD;
-    const float x = M[it];
-    mt32[d * HD + c] = x;
-    const uint16_t hb = f2bf(x);
-    mthi[d * HD + c] = hb;
-    mtlo[d * HD + c] = f2bf(x - bf2f(hb));
+  for (int it = tid; it < S * (HD / 8); it += DT) {
+    const int s = it / (HD / 8), d8 = (it % (HD / 8)) * 8;
+    copy8(&sm.ak[s * KS + d8], g_ak + s * HD + d8);
+    copy8(&sm.av[s * KS + d8], g_av + s * HD + d8);
   }
   if (tid < S) {
     sm.mass[tid] = a.mass[bh * S + tid];
     sm.util[tid] = a.util[bh * S + tid];
     sm.pm[tid] = a.pm[bh * S + tid];
     sm.act[tid] = a.act[bh * S + tid] ? 1 : 0;
+    sm.dirty[tid] = 1;
   }
+  if (tid < HD / 2) sm.invf[tid] = a.inv_freq[tid];
   __syncthreads();
   int nf = a.n_filled;
-  const T* kread = kread_w;
-  if (nf > 0) rope_slots_to<T, HD>(sm.KREAD_LDS ? nullptr : kread_w, sm, a.inv_freq, tid);
+  rope_dirty<T, HD>(sm, kread_g, tid);   // every slot, empty ones included (their rows stay zero)
   __threadfence_block();
   __syncthreads();
 
   for (int step = 0; step < a.n_steps; ++step) {
-    const int off = step == 0 ? a.off0 : step * a.step_stride;
-    const int l = step == 0 ? a.len0 : a.step_len;
+    const int off = step_off(a, step), l = step_len(a, step);
     const long long tb = (long long)bh * a.tok_bh_stride + (long long)off * HD;
     const T* kr = reinterpret_cast<const T*>(a.kr) + tb;
     const T* kp = reinterpret_cast<const T*>(a.kp) + tb;
@@ -657,15 +538,15 @@ __global__ void __launch_bounds__(NT) chain_kernel(b3_chain_args a) {
     const int nT = (l + 31) / 32;
     const bool steady = nf >= S;
     float* log = a.log ? a.log + ((long long)step * BH + bh) * (B3_LOG_ROWS * B3_LOG_COLS) : nullptr;
-    float* snap_m = a.snap_m ? a.snap_m + (long long)step * BH * HD * HD + (long long)bh * HD * HD : nullptr;
+    float* w_out = w_all + ((long long)step * BH + bh) * LMAX;
 
     if (tid < S) {
       sm.util[tid] = mul_rn(sm.util[tid], UTIL_DECAY);
       const float lm = logf(fmaxf(sm.mass[tid], 1.0f));
       sm.bias[tid] = steady ? mul_rn(kap, lm) : lm;
+      sm.dirty[tid] = 0;
     }
     slot_norms<T, HD>(sm, tid);
-    for (int j = tid; j < LMAX; j += NT) { sm.flags[j] = 0; sm.w[j] = 0.f; sm.bsafe[j] = 0.f; }
     __syncthreads();
 
     if (!steady) {
@@ -703,19 +584,22 @@ __global__ void __launch_bounds__(NT) chain_kernel(b3_chain_args a) {
           sm.rel[j] = 0.15f;
         }
       } else {
-        for (int t = wave; t < nT; t += NWAVE) score_tile<T, HD>(sm, kread, kr, kp, v, 32 * t, l, false, scale, lane);
+        for (int t = wave >> 1; t < nT; t += DWAVES / 2)
+          score_tile<T, HD>(sm, kread, kr, kp, v, 32 * t, l, false, scale, wave & 1, lane);
+        __syncthreads();
+        score_combine<T, HD>(sm, v, l, false, tid);
       }
       __syncthreads();
-      if (tid < l) sm.ok_a[tid] = ord_key(sm.score[tid]);
+      if (tid < l) sm.u.ok.a[tid] = ord_key(sm.score[tid]);
       __syncthreads();
       if (tid < l) {
-        const int r = rank_desc(sm.ok_a, l, tid);
+        const int r = rank_desc(sm.u.ok.a, l, tid);
         sm.si_a[r] = tid;
         sm.sk_a[r] = sm.score[tid];
       }
       __syncthreads();
       // slots nf + i <- token si_a[i]
-      for (int it = tid; it < m * (HD / 8); it += NT) {
+      for (int it = tid; it < m * (HD / 8); it += DT) {
         const int i = it / (HD / 8), d8 = (it % (HD / 8)) * 8;
         const int j = sm.si_a[i], s = nf + i;
         copy8(&sm.ak[s * KS + d8], kr + (long long)j * HD + d8);
@@ -727,31 +611,23 @@ __global__ void __launch_bounds__(NT) chain_kernel(b3_chain_args a) {
         sm.mass[s] = 1.0f;
         sm.util[s] = sm.rel[j];
         sm.act[s] = 1;
+        sm.dirty[s] = 1;
       }
       if (log) {
-        for (int j = tid; j < B3_LOG_COLS; j += NT) {
+        for (int j = tid; j < B3_LOG_COLS; j += DT) {
           log[B3_LOG_REL * B3_LOG_COLS + j] = j < l ? sm.rel[j] : 0.f;
           log[B3_LOG_SCORE * B3_LOG_COLS + j] = j < l ? sm.score[j] : 0.f;
           log[B3_LOG_TOPTOK * B3_LOG_COLS + j] = j < m ? (float)sm.si_a[j] : -1.f;
-        }
-      }
-      // M_res is unchanged by a fill: its snapshot is the current M
-      if (snap_m) {
-        for (int it = tid; it < HD * HD; it += NT) {
-          if constexpr (St<T>::is_bf16) {
-            reinterpret_cast<uint16_t*>(snap_m)[it] = mthi[it];
-            reinterpret_cast<uint16_t*>(snap_m)[HD * HD + it] = mtlo[it];
-          } else {
-            snap_m[it] = M[it];
-          }
         }
       }
       nf += m;
       __syncthreads();
     } else {
       // ---------------- steady: score
-      for (int t = wave; t < nT; t += NWAVE) score_tile<T, HD>(sm, kread, kr, kp, v, 32 * t, l, true, scale, lane);
-      const int has = tid < l && (sm.flags[tid] & F_MERGE);
+      for (int t = wave >> 1; t < nT; t += DWAVES / 2)
+        score_tile<T, HD>(sm, kread, kr, kp, v, 32 * t, l, true, scale, wave & 1, lane);
+      __syncthreads();
+      const bool has = score_combine<T, HD>(sm, v, l, true, tid);
       const int any_merge = __syncthreads_or(has);
 
       // ---------------- merge: per-slot mass-weighted means, tokens in ascending order
@@ -761,45 +637,46 @@ __global__ void __launch_bounds__(NT) chain_kernel(b3_chain_args a) {
           float ps = 0.f;
           for (int j = 0; j < l; ++j)
             if ((sm.flags[j] & F_MERGE) && sm.slot[j] == tid) { ++c; ps += pos[j]; }
-          sm.cnt[tid] = c;
-          sm.psum[tid] = ps;
+          sm.u.mg.cnt[tid] = c;
+          sm.u.mg.psum[tid] = ps;
         }
         __syncthreads();
         if (tid == 0) {
           int o = 0, nh = 0;
           for (int s = 0; s < S; ++s) {
-            sm.off[s] = o;
-            o += sm.cnt[s];
-            if (sm.cnt[s] > 0) sm.hits[nh++] = s;
+            sm.u.mg.off[s] = o;
+            o += sm.u.mg.cnt[s];
+            if (sm.u.mg.cnt[s] > 0) sm.u.mg.hits[nh++] = s;
           }
-          sm.nhit = nh;
+          sm.u.mg.nhit = nh;
         }
         __syncthreads();
-        const int nhit = sm.nhit;
+        const int nhit = sm.u.mg.nhit;
         if (tid < l && (sm.flags[tid] & F_MERGE)) {
           const int s = sm.slot[tid];
           int rank = 0;
           for (int j = 0; j < tid; ++j) rank += ((sm.flags[j] & F_MERGE) && sm.slot[j] == s) ? 1 : 0;
-          sm.mlist[sm.off[s] + rank] = tid;
+          sm.u.mg.mlist[sm.u.mg.off[s] + rank] = tid;
         }
         __syncthreads();
-        for (int it = tid; it < nhit * HD; it += NT) {
-          const int s = sm.hits[it / HD], d = it % HD;
+        for (int it = tid; it < nhit * HD; it += DT) {
+          const int s = sm.u.mg.hits[it / HD], d = it % HD;
           float ks = 0.f, vs = 0.f;
-          for (int q = 0; q < sm.cnt[s]; ++q) {
-            const int j = sm.mlist[sm.off[s] + q];
+          for (int q = 0; q < sm.u.mg.cnt[s]; ++q) {
+            const int j = sm.u.mg.mlist[sm.u.mg.off[s] + q];
             ks += St<T>::ld(kr + (long long)j * HD + d);
             vs += St<T>::ld(v + (long long)j * HD + d);
           }
-          const float m0 = sm.mass[s], nm = add_rn(m0, (float)sm.cnt[s]);
+          const float m0 = sm.mass[s], nm = add_rn(m0, (float)sm.u.mg.cnt[s]);
           sm.ak[s * KS + d] = St<T>::from_f(div_rn(add_rn(mul_rn(m0, St<T>::to_f(sm.ak[s * KS + d])), ks), nm));
           sm.av[s * KS + d] = St<T>::from_f(div_rn(add_rn(mul_rn(m0, St<T>::to_f(sm.av[s * KS + d])), vs), nm));
         }
         __syncthreads();
-        if (tid < S && sm.cnt[tid] > 0) {
-          const float m0 = sm.mass[tid], nm = add_rn(m0, (float)sm.cnt[tid]);
-          sm.pm[tid] = div_rn(add_rn(mul_rn(m0, sm.pm[tid]), sm.psum[tid]), nm);
+        if (tid < S && sm.u.mg.cnt[tid] > 0) {
+          const float m0 = sm.mass[tid], nm = add_rn(m0, (float)sm.u.mg.cnt[tid]);
+          sm.pm[tid] = div_rn(add_rn(mul_rn(m0, sm.pm[tid]), sm.u.mg.psum[tid]), nm);
           sm.mass[tid] = nm;
+          sm.dirty[tid] = 1;
         }
         __syncthreads();
         slot_norms<T, HD>(sm, tid);
@@ -809,13 +686,15 @@ __global__ void __launch_bounds__(NT) chain_kernel(b3_chain_args a) {
       // ---------------- keep score: util * (1 - clamp(max_{s'!=s} cos(ak_s, ak_s'), 0, .98))
       {
         const int n = lane & 31;
-        const int col = 32 * wave + n;  // 4 waves x 32 columns = S
+        const int cb = wave & 3, rh = wave >> 2;
+        const int col = 32 * cb + n;
         Frag<T, HD> fc;
         fc.load_lds(sm.ak, KS, col, lane);
         float mx = -INFINITY;
         bool has_nan = false;
 #pragma unroll
-        for (int mb = 0; mb < 4; ++mb) {
+        for (int m2 = 0; m2 < 2; ++m2) {
+          const int mb = 2 * rh + m2;
           f32x16 acc = zero16();
           mm_rows_frag<HD>(acc, sm.ak, KS, 32 * mb, fc, lane);
 #pragma unroll
@@ -830,36 +709,53 @@ __global__ void __launch_bounds__(NT) chain_kernel(b3_chain_args a) {
         }
         mx = fmaxf(mx, xor32(mx));
         has_nan |= __shfl_xor((int)has_nan, 32, 64) != 0;
-        if (has_nan) mx = NAN;
-        if ((lane >> 5) == 0) sm.keep[col] = mul_rn(sm.util[col], 1.0f - fminf(fmaxf(mx, 0.0f), 0.98f));
-      }
-      if (tid < l) {
-        sm.ck[tid] = (sm.flags[tid] & F_MERGE) ? -1e9f : sm.score[tid];
-        sm.ok_a[tid] = ord_key(sm.ck[tid]);
+        if ((lane >> 5) == 0) {
+          sm.u.kp.mx[rh][col] = mx;
+          sm.u.kp.nan[rh][col] = has_nan ? 1 : 0;
+        }
       }
       __syncthreads();
-      if (tid < S) sm.ok_b[tid] = ord_key(sm.keep[tid]);
+      float keep_v = 0.f, ck_v = 0.f;
+      if (tid < S) {
+        float mx = fmaxf(sm.u.kp.mx[0][tid], sm.u.kp.mx[1][tid]);
+        if (sm.u.kp.nan[0][tid] | sm.u.kp.nan[1][tid]) mx = NAN;
+        keep_v = mul_rn(sm.util[tid], 1.0f - fminf(fmaxf(mx, 0.0f), 0.98f));
+        sm.keep[tid] = keep_v;
+      }
+      if (tid < l) {
+        ck_v = (sm.flags[tid] & F_MERGE) ? -1e9f : sm.score[tid];
+        sm.ck[tid] = ck_v;
+      }
+      __syncthreads();
+      if (tid < l) sm.u.ok.a[tid] = ord_key(ck_v);
+      if (tid < S) sm.u.ok.b[tid] = ord_key(keep_v);
       __syncthreads();
       // ---------------- orderings: best free tokens (desc) against least useful slots (asc)
       if (tid < l) {
-        const int r = rank_desc(sm.ok_a, l, tid);
+        const int r = rank_desc(sm.u.ok.a, l, tid);
         sm.sk_a[r] = sm.ck[tid];
         sm.si_a[r] = tid;
-      }
-      if (tid < S) {
-        const int r = rank_asc(sm.ok_b, S, tid);
-        sm.sk_b[r] = sm.keep[tid];
-        sm.si_b[r] = tid;
+      } else if (tid >= DT - S) {
+        const int s = tid - (DT - S);
+        const int r = rank_asc(sm.u.ok.b, S, s);
+        sm.sk_b[r] = sm.keep[s];
+        sm.si_b[r] = s;
       }
       __syncthreads();
       const int kc = min(l, S);
       // win_i = top_i > bot_i and top_i > -1e8 ; token top_i replaces slot bot_i
       if (tid < kc) {
         const float tv = sm.sk_a[tid], bv = sm.sk_b[tid];
-        if (tv > bv && tv > -1e8f) sm.flags[sm.si_a[tid]] |= F_INS;
+        if (tv > bv && tv > -1e8f) {
+          const int j = sm.si_a[tid], s = sm.si_b[tid];
+          sm.flags[j] |= F_INS;
+          sm.pm[s] = pos[j];
+          sm.mass[s] = 1.0f;
+          sm.util[s] = sm.rel[j];
+          sm.dirty[s] = 1;
+        }
       }
-      __syncthreads();
-      for (int it = tid; it < kc * (HD / 8); it += NT) {
+      for (int it = tid; it < kc * (HD / 8); it += DT) {
         const int i = it / (HD / 8), d8 = (it % (HD / 8)) * 8;
         const float tv = sm.sk_a[i], bv = sm.sk_b[i];
         if (tv > bv && tv > -1e8f) {
@@ -868,24 +764,16 @@ __global__ void __launch_bounds__(NT) chain_kernel(b3_chain_args a) {
           copy8(&sm.av[s * KS + d8], v + (long long)j * HD + d8);
         }
       }
-      if (tid < kc) {
-        const float tv = sm.sk_a[tid], bv = sm.sk_b[tid];
-        if (tv > bv && tv > -1e8f) {
-          const int j = sm.si_a[tid], s = sm.si_b[tid];
-          sm.pm[s] = pos[j];
-          sm.mass[s] = 1.0f;
-          sm.util[s] = sm.rel[j];
-        }
-      }
+      __syncthreads();
       if (tid < l) {
         const int f = sm.flags[tid];
         const bool dl = !(f & F_MERGE) && !(f & F_INS);
         if (dl) sm.flags[tid] = f | F_DELTA;
-        sm.w[tid] = dl ? beta[tid] : 0.f;
+        w_out[tid] = dl ? beta[tid] : 0.f;
       }
       __syncthreads();
       if (log) {
-        for (int j = tid; j < B3_LOG_COLS; j += NT) {
+        for (int j = tid; j < B3_LOG_COLS; j += DT) {
           const bool in = j < l;
           log[B3_LOG_REL * B3_LOG_COLS + j] = in ? sm.rel[j] : 0.f;
           log[B3_LOG_SCORE * B3_LOG_COLS + j] = in ? sm.score[j] : 0.f;
@@ -903,38 +791,38 @@ __global__ void __launch_bounds__(NT) chain_kernel(b3_chain_args a) {
           log[B3_LOG_BOTVAL * B3_LOG_COLS + j] = j < kc ? sm.sk_b[j] : 0.f;
         }
       }
-
-      // ---------------- Gershgorin-safe delta rule into M_res
-      gershgorin<T, HD>(sm, kr, l, wave, lane);
-      __syncthreads();
-      delta_update<T, HD>(sm, ws, M, snap_m, kr, v, l, gam, wave, lane, tid);
-      __syncthreads();
     }
 
     // ---------------- per-step outputs; the roped keys also serve the next step
-    T* kdst = a.snap_k ? reinterpret_cast<T*>(a.snap_k) + step * BH * S * HD + (long long)bh * S * HD
-                       : (sm.KREAD_LDS ? nullptr : kread_w);
-    rope_slots_to<T, HD>(kdst, sm, a.inv_freq, tid);
-    if (kdst) kread = kdst;
+    rope_dirty<T, HD>(sm, kread_g, tid);
+    __threadfence_block();
+    __syncthreads();
+    if (a.snap_k) {
+      T* kd = reinterpret_cast<T*>(a.snap_k) + (step * BH + bh) * S * HD;
+      const int rs = sm.KREAD_LDS ? KS : HD;
+      for (int it = tid; it < S * (HD / 8); it += DT) {
+        const int s = it / (HD / 8), d8 = (it % (HD / 8)) * 8;
+        copy8(kd + s * HD + d8, kread + s * rs + d8);
+      }
+    }
     if (a.snap_v) {
-      T* vd = reinterpret_cast<T*>(a.snap_v) + step * BH * S * HD + (long long)bh * S * HD;
-      for (int it = tid; it < S * (HD / 8); it += NT) {
+      T* vd = reinterpret_cast<T*>(a.snap_v) + (step * BH + bh) * S * HD;
+      for (int it = tid; it < S * (HD / 8); it += DT) {
         const int s = it / (HD / 8), d8 = (it % (HD / 8)) * 8;
         copy8(vd + s * HD + d8, &sm.av[s * KS + d8]);
       }
     }
     if (a.snap_bias && tid < S) {
-      a.snap_bias[(long long)step * BH * S + bh * S + tid] =
+      a.snap_bias[(step * BH + bh) * S + tid] =
           sm.act[tid] ? mul_rn(kap, logf(fmaxf(sm.mass[tid], 1.0f))) : -INFINITY;
     }
-    __threadfence_block();
-    __syncthreads();
   }
 
-  // store state (M was written after every steady step)
-  for (int it = tid; it < S * HD; it += NT) {
-    g_ak[it] = sm.ak[(it / HD) * KS + it % HD];
-    g_av[it] = sm.av[(it / HD) * KS + it % HD];
+  // store the slot state
+  for (int it = tid; it < S * (HD / 8); it += DT) {
+    const int s = it / (HD / 8), d8 = (it % (HD / 8)) * 8;
+    copy8(g_ak + s * HD + d8, &sm.ak[s * KS + d8]);
+    copy8(g_av + s * HD + d8, &sm.av[s * KS + d8]);
   }
   if (tid < S) {
     a.mass[bh * S + tid] = sm.mass[tid];
@@ -944,18 +832,299 @@ __global__ void __launch_bounds__(NT) chain_kernel(b3_chain_args a) {
   }
 }
 
+// ----------------------------------------------------------------- gersh_kernel
+
+// For steady step blockIdx.x and row blockIdx.y:
+//   inv_j   = 1 / max(|k_j|, 1e-12)
+//   bsafe_j = w_j / max(sum_i |khat_i . khat_j| w_i, 1)
+template <typename T, int HD>
+__global__ void __launch_bounds__(MT) gersh_kernel(b3_chain_args a) {
+  __shared__ float s_inv[LMAX], s_w[LMAX];
+  const int step = blockIdx.x, bh = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, n = lane & 31;
+  int nf = a.n_filled;
+  for (int s = 0; s < step && nf < S; ++s) nf += min(S - nf, step_len(a, s));
+  if (nf < S) return;  // fill step: M_res untouched
+  const long long BH = (long long)a.B * a.HKV;
+  const int l = step_len(a, step);
+  const T* kr =
+      reinterpret_cast<const T*>(a.kr) + (long long)bh * a.tok_bh_stride + (long long)step_off(a, step) * HD;
+  char* ws = reinterpret_cast<char*>(a.work) + BH * Work<T, HD>::KREAD;
+  const long long row = ((long long)step * BH + bh) * LMAX;
+  const long long plane = (long long)a.n_steps * BH * LMAX;
+  const float* w = reinterpret_cast<const float*>(ws) + row;
+  float* bsafe = reinterpret_cast<float*>(ws) + plane + row;
+  float* inv = reinterpret_cast<float*>(ws) + 2 * plane + row;
+
+  if (tid < l) {
+    float ss = 0.f;
+    for (int d = 0; d < HD; d += 8) {
+      float x[8];
+      ld8(kr + (long long)tid * HD + d, x);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ss += x[i] * x[i];
+    }
+    const float iv = 1.0f / fmaxf(sqrtf(ss), 1e-12f);
+    s_inv[tid] = iv;
+    s_w[tid] = w[tid];
+    inv[tid] = iv;
+  }
+  __syncthreads();
+  const int nT = (l + 31) / 32;
+  for (int tj = wave; tj < nT; tj += MWAVES) {
+    const int j = 32 * tj + n;
+    Frag<T, HD> fj;
+    fj.load(kr, j, l, lane);
+    const float inj = j < l ? s_inv[j] : 0.f;
+    float colsum = 0.f;
+    for (int ti = 0; ti < nT; ++ti) {
+      f32x16 acc = zero16();
+      Frag<T, HD> fi;
+      fi.load(kr, 32 * ti + n, l, lane);
+      // rows i of tile ti as the A operand: same fragment layout as a B fragment
+      if constexpr (St<T>::is_bf16) {
+#pragma unroll
+        for (int ks = 0; ks < HD / 16; ++ks) mma_bf16(acc, fi.v[ks], fj.v[ks]);
+      } else {
+#pragma unroll 8
+        for (int ks = 0; ks < HD / 2; ++ks) mma_f32(acc, fi.v[ks], fj.v[ks]);
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int i = 32 * ti + d_row(lane, r);
+        if (i < l) colsum += fabsf(acc[r] * (s_inv[i] * inj)) * s_w[i];
+      }
+    }
+    colsum += xor32(colsum);
+    if ((lane >> 5) == 0 && j < l) bsafe[j] = s_w[j] / fmaxf(colsum, 1.0f);
+  }
+}
+
+// ----------------------------------------------------------------- mres_kernel
+
+template <typename T, int HD>
+struct MSmem {
+  static constexpr int MS = HD + 4;                               // fp32 M^T row stride
+  static constexpr int BS = HD + 8;                               // bf16 M^T row stride
+  static constexpr int ES = sizeof(T) == 2 ? LMAX + 8 : LMAX + 1; // E^T row stride
+  static constexpr int KC = 128;                                  // tokens per K^T staging chunk
+  static constexpr int KTS = sizeof(T) == 2 ? KC + 8 : KC + 1;    // K^T row stride
+  alignas(16) float mt[32 * MS];                                  // M^T rows d of this block
+  alignas(16) uint16_t mhi[sizeof(T) == 2 ? 32 * BS : 1];
+  alignas(16) uint16_t mlo[sizeof(T) == 2 ? 32 * BS : 1];
+  alignas(16) T ert[32 * ES];                                     // E^T[d][j] (bf16: hi)
+  alignas(16) uint16_t erl[sizeof(T) == 2 ? 32 * ES : 1];         // E^T lo
+  alignas(16) T krt[HD * KTS];                                    // K^T[c][j] of one chunk
+  float bsafe[LMAX], inv[LMAX];
+};
+
+// Columns [32*db, 32*db + 32) of M for row bh = blockIdx.x / (HD/32):
+//   E^T[d][j] = (v[j][d] - (K M)[j][d] / |k_j|) * bsafe_j / |k_j|
+//   M^T[d][c] <- gamma * M^T[d][c] + sum_j E^T[d][j] k[j][c]
+template <typename T, int HD>
+__global__ void __launch_bounds__(MT) mres_kernel(b3_chain_args a) {
+  __shared__ MSmem<T, HD> sm;
+  using Sm = MSmem<T, HD>;
+  constexpr int NDB = HD / 32, NCB = HD / 32;
+  const int bh = blockIdx.x / NDB, db = blockIdx.x % NDB;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, n = lane & 31, h = lane >> 5;
+  const int hkv = bh % a.HKV;
+  const float gam = a.gamma[hkv];
+  const long long BH = (long long)a.B * a.HKV;
+  float* M = a.m_res + (long long)bh * HD * HD;
+  const char* ws = reinterpret_cast<const char*>(a.work) + BH * Work<T, HD>::KREAD;
+  const long long plane = (long long)a.n_steps * BH * LMAX;
+  const float* bsafe_all = reinterpret_cast<const float*>(ws) + plane;
+  const float* inv_all = reinterpret_cast<const float*>(ws) + 2 * plane;
+
+  // M^T block: mt[dd][c] = M[c][32*db + dd]
+  for (int it = tid; it < HD * 32; it += MT) {
+    const int c = it / 32, dd = it % 32;
+    const float x = M[c * HD + 32 * db + dd];
+    sm.mt[dd * Sm::MS + c] = x;
+    if constexpr (St<T>::is_bf16) {
+      const uint16_t hb = f2bf(x);
+      sm.mhi[dd * Sm::BS + c] = hb;
+      sm.mlo[dd * Sm::BS + c] = f2bf(x - bf2f(hb));
+    }
+  }
+  __syncthreads();
+
+  int nf = a.n_filled;
+  for (int step = 0; step < a.n_steps; ++step) {
+    const int l = step_len(a, step);
+    float* snap = a.snap_m ? a.snap_m + (step * BH + bh) * HD * HD : nullptr;
+    if (nf >= S) {
+      const long long tb = (long long)bh * a.tok_bh_stride + (long long)step_off(a, step) * HD;
+      const T* kr = reinterpret_cast<const T*>(a.kr) + tb;
+      const T* v = reinterpret_cast<const T*>(a.v) + tb;
+      const long long row = ((long long)step * BH + bh) * LMAX;
+      if (tid < l) {
+        sm.bsafe[tid] = bsafe_all[row + tid];
+        sm.inv[tid] = inv_all[row + tid];
+      }
+      __syncthreads();
+      // E^T tile per 32 tokens: prediction from the old M, error scaled by bsafe / |k|; the
+      // columns up to the end of the last staging chunk are written (zero past l)
+      const int nT = ((l + Sm::KC - 1) / Sm::KC) * (Sm::KC / 32);
+      for (int t = wave; t < nT; t += MWAVES) {
+        const int j = 32 * t + n;
+        Frag<T, HD> fj;
+        fj.load(kr, j, l, lane);
+        float vx[4][4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int d0 = 32 * db + 8 * g + 4 * h;
+          if (j < l) ld4(v + (long long)j * HD + d0, vx[g]);
+          else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) vx[g][q] = 0.f;
+          }
+        }
+        f32x16 acc = zero16();
+        if constexpr (St<T>::is_bf16) {
+#pragma unroll
+          for (int ks = 0; ks < HD / 16; ++ks) {
+            const u16x8 hi = *reinterpret_cast<const u16x8*>(&sm.mhi[n * Sm::BS + 16 * ks + 8 * h]);
+            const u16x8 lo = *reinterpret_cast<const u16x8*>(&sm.mlo[n * Sm::BS + 16 * ks + 8 * h]);
+            mma_bf16(acc, hi, fj.v[ks]);
+            mma_bf16(acc, lo, fj.v[ks]);
+          }
+        } else {
+#pragma unroll 8
+          for (int ks = 0; ks < HD / 2; ++ks) mma_f32(acc, sm.mt[n * Sm::MS + 2 * ks + h], fj.v[ks]);
+        }
+        const float inj = j < l ? sm.inv[j] : 0.f;
+        const float bj = j < l ? sm.bsafe[j] : 0.f;
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int dd = 8 * g + 4 * h + q;
+            const float e = ((vx[g][q] - acc[4 * g + q] * inj) * bj) * inj;
+            if constexpr (St<T>::is_bf16) {
+              const uint16_t hb = f2bf(e);
+              sm.ert[dd * Sm::ES + j] = hb;
+              sm.erl[dd * Sm::ES + j] = f2bf(e - bf2f(hb));
+            } else {
+              sm.ert[dd * Sm::ES + j] = e;
+            }
+          }
+      }
+      // upd[c][d] = sum_j K^T[c][j] E^T[d][j], K^T staged per chunk of Sm::KC tokens
+      f32x16 upd = zero16();
+      const int cb = wave;
+      for (int j0 = 0; j0 < l; j0 += Sm::KC) {
+        const int jn = min(Sm::KC, l - j0);
+        // 8 tokens x 8 channels per item: row reads, transposed row writes
+        for (int it = tid; it < (Sm::KC / 8) * (HD / 8); it += MT) {
+          const int jb = (it % (Sm::KC / 8)) * 8, c8 = (it / (Sm::KC / 8)) * 8;
+          float x[8][8];
+#pragma unroll
+          for (int r = 0; r < 8; ++r) {
+            if (jb + r < jn) ld8(kr + (long long)(j0 + jb + r) * HD + c8, x[r]);
+            else {
+#pragma unroll
+              for (int q = 0; q < 8; ++q) x[r][q] = 0.f;
+            }
+          }
+#pragma unroll
+          for (int q = 0; q < 8; ++q) {
+            if constexpr (St<T>::is_bf16) {
+              u16x8 col;
+#pragma unroll
+              for (int r = 0; r < 8; ++r) col[r] = f2bf(x[r][q]);
+              *reinterpret_cast<u16x8*>(&sm.krt[(c8 + q) * Sm::KTS + jb]) = col;
+            } else {
+#pragma unroll
+              for (int r = 0; r < 8; ++r) sm.krt[(c8 + q) * Sm::KTS + jb + r] = x[r][q];
+            }
+          }
+        }
+        __syncthreads();
+        if (cb < NCB) {
+          const int c = 32 * cb + n;
+          if constexpr (St<T>::is_bf16) {
+#pragma unroll
+            for (int kc = 0; kc < Sm::KC / 16; ++kc) {
+              const u16x8 ka = *reinterpret_cast<const u16x8*>(&sm.krt[c * Sm::KTS + 16 * kc + 8 * h]);
+              const u16x8 eh = *reinterpret_cast<const u16x8*>(&sm.ert[n * Sm::ES + j0 + 16 * kc + 8 * h]);
+              const u16x8 el = *reinterpret_cast<const u16x8*>(&sm.erl[n * Sm::ES + j0 + 16 * kc + 8 * h]);
+              mma_bf16(upd, ka, eh);
+              mma_bf16(upd, ka, el);
+            }
+          } else {
+#pragma unroll 8
+            for (int kc = 0; kc < Sm::KC / 2; ++kc)
+              mma_f32(upd, sm.krt[c * Sm::KTS + 2 * kc + h], sm.ert[n * Sm::ES + j0 + 2 * kc + h]);
+          }
+        }
+        __syncthreads();
+      }
+      // M = gamma*M + upd (two rounded ops, as the reference evaluates them); lane holds
+      // column d = n of the block and rows c = 32*cb + d_row(lane, r)
+      if (cb < NCB) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int c = 32 * cb + d_row(lane, r);
+          const float nw = add_rn(mul_rn(gam, sm.mt[n * Sm::MS + c]), upd[r]);
+          sm.mt[n * Sm::MS + c] = nw;
+          if constexpr (St<T>::is_bf16) {
+            const uint16_t hb = f2bf(nw);
+            sm.mhi[n * Sm::BS + c] = hb;
+            sm.mlo[n * Sm::BS + c] = f2bf(nw - bf2f(hb));
+          }
+        }
+      }
+      __syncthreads();
+    } else {
+      nf += min(S - nf, l);
+    }
+    // snapshot of this block after the step (a fill step leaves M unchanged)
+    if (snap) {
+      if constexpr (St<T>::is_bf16) {
+        uint16_t* sh = reinterpret_cast<uint16_t*>(snap);
+        for (int it = tid; it < 32 * (HD / 8); it += MT) {
+          const int dd = it / (HD / 8), c8 = (it % (HD / 8)) * 8;
+          const int d = 32 * db + dd;
+          copy8(sh + d * HD + c8, &sm.mhi[dd * Sm::BS + c8]);
+          copy8(sh + HD * HD + d * HD + c8, &sm.mlo[dd * Sm::BS + c8]);
+        }
+      } else {
+        for (int it = tid; it < HD * 32; it += MT) {
+          const int c = it / 32, dd = it % 32;
+          snap[c * HD + 32 * db + dd] = sm.mt[dd * Sm::MS + c];
+        }
+      }
+    }
+  }
+  for (int it = tid; it < HD * 32; it += MT) {
+    const int c = it / 32, dd = it % 32;
+    M[c * HD + 32 * db + dd] = sm.mt[dd * Sm::MS + c];
+  }
+}
+
 template <typename T, int HD>
 static int launch_chain(const b3_chain_args& a, hipStream_t st) {
-  hipLaunchKernelGGL((chain_kernel<T, HD>), dim3(a.B * a.HKV), dim3(NT), 0, st, a);
+  const int BH = a.B * a.HKV;
+  hipLaunchKernelGGL((decide_kernel<T, HD>), dim3(BH), dim3(DT), 0, st, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  hipLaunchKernelGGL((gersh_kernel<T, HD>), dim3(a.n_steps, BH), dim3(MT), 0, st, a);
+  e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  hipLaunchKernelGGL((mres_kernel<T, HD>), dim3(BH * (HD / 32)), dim3(MT), 0, st, a);
   return (int)hipGetLastError();
 }
 
 }  // namespace b3
 
-extern "C" int64_t bolt3_chain_workspace_bytes(int32_t dtype, int32_t B, int32_t HKV, int32_t HD, int32_t S) {
+extern "C" int64_t bolt3_chain_workspace_bytes(int32_t dtype, int32_t B, int32_t HKV, int32_t HD, int32_t S,
+                                               int32_t n_steps) {
   const int64_t bh = (int64_t)B * HKV;
-  if (dtype == B3_BF16) return bh * (HD == 64 ? b3::Work<uint16_t, 64>::PER_BH : b3::Work<uint16_t, 128>::PER_BH);
-  return bh * (HD == 64 ? b3::Work<float, 64>::PER_BH : b3::Work<float, 128>::PER_BH);
+  if (dtype == B3_BF16)
+    return HD == 64 ? b3::Work<uint16_t, 64>::bytes(bh, n_steps) : b3::Work<uint16_t, 128>::bytes(bh, n_steps);
+  return HD == 64 ? b3::Work<float, 64>::bytes(bh, n_steps) : b3::Work<float, 128>::bytes(bh, n_steps);
 }
 
 extern "C" int bolt3_chain(const b3_chain_args* a, void* stream) {
@@ -968,7 +1137,8 @@ extern "C" int bolt3_chain(const b3_chain_args* a, void* stream) {
   if (!a->kr || !a->kp || !a->v || !a->pos || !a->beta || !a->ak || !a->av || !a->mass || !a->util || !a->pm ||
       !a->act || !a->m_res || !a->kappa || !a->gamma || !a->inv_freq || !a->work)
     return B3_ERR_ARG;
-  if (a->work_bytes < bolt3_chain_workspace_bytes(a->dtype, a->B, a->HKV, a->HD, a->S)) return B3_ERR_WORKSPACE;
+  if (a->work_bytes < bolt3_chain_workspace_bytes(a->dtype, a->B, a->HKV, a->HD, a->S, a->n_steps))
+    return B3_ERR_WORKSPACE;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (a->dtype == B3_F32) return a->HD == 64 ? b3::launch_chain<float, 64>(*a, st) : b3::launch_chain<float, 128>(*a, st);
   if (a->dtype == B3_BF16)

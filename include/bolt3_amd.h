@@ -87,6 +87,8 @@ typedef struct {
   int32_t off0, len0;         /* step 0 consumes tokens [off0, off0 + len0)               */
   int32_t step_stride, step_len; /* step i > 0 consumes [i*step_stride, i*step_stride + step_len) */
   int32_t n_filled;           /* filled slots before step 0 (0 => state must be the empty state) */
+  int32_t kp_exact;           /* 1: kp rows are bolt3_heads / bolt3_decode RoPE of kr at pos (bit-exact),
+                                 so a slot taken from a token copies its roped key; 0: recompute */
   /* slot state, updated in place: ak/av [bh][S][HD] storage dtype (un-roped keys), mass/util/pm [bh][S],
      act [bh][S] (0/1), m_res [bh][HD][HD] */
   void* ak;

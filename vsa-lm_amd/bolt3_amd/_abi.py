@@ -49,6 +49,7 @@ class ChainArgs(C.Structure):
         ("dtype", i32), ("B", i32), ("HKV", i32), ("HD", i32), ("S", i32),
         ("kr", p), ("kp", p), ("v", p), ("tok_bh_stride", i64), ("pos", p), ("beta", p), ("beta_bh_stride", i64),
         ("n_steps", i32), ("off0", i32), ("len0", i32), ("step_stride", i32), ("step_len", i32), ("n_filled", i32),
+        ("kp_exact", i32),
         ("ak", p), ("av", p), ("mass", p), ("util", p), ("pm", p), ("act", p), ("m_res", p),
         ("kappa", p), ("gamma", p), ("inv_freq", p),
         ("snap_k", p), ("snap_v", p), ("snap_bias", p), ("snap_m", p), ("log", p),

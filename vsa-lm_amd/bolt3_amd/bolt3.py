@@ -152,7 +152,7 @@ class Bolt3Attn(nn.Module):
 
     def _chain(self, dt, device, B, kr, kp, v, tok_bh_stride, pos, beta, beta_bh_stride, n_steps, off0, len0,
                step_stride, step_len, n_filled, st: dict, m_res, gam, side, snap_k=None, snap_v=None,
-               snap_bias=None, snap_m=None, log=None):
+               snap_bias=None, snap_m=None, log=None, kp_exact=False):
         work = torch.empty(A.chain_workspace_bytes(dt, B, self.HKV, self.HD, self.S, n_steps), dtype=torch.uint8,
                            device=device)
         a = A.ChainArgs()
@@ -160,7 +160,7 @@ class Bolt3Attn(nn.Module):
         a.kr, a.kp, a.v, a.tok_bh_stride = kr, kp, v, tok_bh_stride
         a.pos, a.beta, a.beta_bh_stride = pos, beta, beta_bh_stride
         a.n_steps, a.off0, a.len0, a.step_stride, a.step_len = n_steps, off0, len0, step_stride, step_len
-        a.n_filled = n_filled
+        a.n_filled, a.kp_exact = n_filled, int(kp_exact)
         a.ak, a.av = st["ak"].data_ptr(), st["av"].data_ptr()
         a.mass, a.util, a.pm = st["mass"].data_ptr(), st["util"].data_ptr(), st["pm"].data_ptr()
         a.act, a.m_res = st["act"].data_ptr(), m_res.data_ptr()
@@ -223,7 +223,8 @@ class Bolt3Attn(nn.Module):
             if trace is not None:
                 log = torch.zeros(n_cons, bh, A.LOG_ROWS, A.LOG_COLS, device=dev)
             self._chain(dt, dev, b, k_raw.data_ptr(), k_rope.data_ptr(), v.data_ptr(), T * HD, pos.data_ptr(),
-                        beta.data_ptr(), T, n_cons, ns, C - ns, C, C, 0, st, m_res, gam, side, *snaps, log=log)
+                        beta.data_ptr(), T, n_cons, ns, C - ns, C, C, 0, st, m_res, gam, side, *snaps, log=log,
+                        kp_exact=True)
             if trace is not None:
                 trace.update(state=st, m_res=m_res, snap_k=snaps[0], snap_v=snaps[1], snap_bias=snaps[2],
                              snap_m=snaps[3], log=log)
@@ -516,7 +517,7 @@ class Bolt3Decoder:
             ly._chain(st.dtype, m_state.device, st.B, st.win_kr.data_ptr(), st.win_kp.data_ptr(),
                       st.win_v.data_ptr(), st.cap * st.HD, st.win_pos.data_ptr(), st.win_b.data_ptr(), st.cap,
                       1, off, l, l, l, st.n_filled, st.slots, m_state, gam, side,
-                      snap_k=st.slot_k, snap_bias=st.slot_bias)
+                      snap_k=st.slot_k, snap_bias=st.slot_bias, kp_exact=True)
             if st.n_filled < ly.S:
                 st.n_filled += min(ly.S - st.n_filled, l)
             st.has_slots = True

@@ -80,11 +80,23 @@ struct DecSmem {
   int si_a[LMAX];
   float sk_b[S];
   int si_b[S];
+  // Softmax exchange of a wave pair (bf16 storage): per-half max and sum per token, and the
+  // probabilities of each half, P[tok][slot] with row stride PS.
+  static constexpr bool SPLIT = sizeof(T) == 2;
+  static constexpr int PS = S + 4;
+  struct PairX {
+    float mx[DWAVES / 2][2][32], sum[DWAVES / 2][2][32];
+    alignas(16) uint16_t p[DWAVES / 2][32 * PS];
+  };
   union {  // phase-local buffers
-    struct { float e2[2][LMAX], v2[2][LMAX], bv[2][LMAX]; int bs[2][LMAX]; } sc;
+    struct {
+      float e2[2][LMAX], v2[2][LMAX], bv[2][LMAX];
+      int bs[2][LMAX];
+      PairX x[SPLIT ? 1 : 0];
+    } sc;
     struct { int cnt[S], off[S], hits[S], mlist[LMAX]; float psum[S]; int nhit; } mg;
     struct { float mx[2][S]; int nan[2][S]; } kp;
-    struct { alignas(16) uint32_t a[LMAX]; alignas(16) uint32_t b[S]; } ok;
+    struct { alignas(16) uint64_t a[LMAX]; alignas(16) uint64_t b[S]; } ok;
   } u;
 };
 
@@ -220,34 +232,34 @@ __device__ __forceinline__ uint32_t ord_key(float f) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-// Rank of element `me` among ok[0..n) (order keys, 16-byte aligned array), ties by lower
-// index.  Descending: keys above, plus equal keys at lower indices.
-__device__ __forceinline__ int rank_desc(const uint32_t* ok, int n, int me) {
-  const uint32_t x = ok[me];
-  int r = 0, i = 0;
+// 64-bit sort keys that carry the tie rule: descending order = larger key first with the
+// lower index on equal values; ascending order = smaller key first, lower index first.
+__device__ __forceinline__ uint64_t desc_key(float f, int i) {
+  return ((uint64_t)ord_key(f) << 32) | (uint32_t)(0xffffffffu - (uint32_t)i);
+}
+__device__ __forceinline__ uint64_t asc_key(float f, int i) { return ((uint64_t)ord_key(f) << 32) | (uint32_t)i; }
+
+// Rank of key x among keys[0..n) (distinct keys, 16-byte aligned array): the number of keys
+// above x (descending order) or below x (ascending order).  The range [i0, i1) of indices
+// is counted, so several threads can share one rank.
+__device__ __forceinline__ int count_above(const uint64_t* keys, int i0, int i1, uint64_t x) {
+  int r = 0, i = i0;
 #pragma unroll 8
-  for (; i + 4 <= n; i += 4) {
-    const uint4 y = *reinterpret_cast<const uint4*>(ok + i);
-    r += (y.x > x || (y.x == x && i + 0 < me)) ? 1 : 0;
-    r += (y.y > x || (y.y == x && i + 1 < me)) ? 1 : 0;
-    r += (y.z > x || (y.z == x && i + 2 < me)) ? 1 : 0;
-    r += (y.w > x || (y.w == x && i + 3 < me)) ? 1 : 0;
+  for (; i + 2 <= i1; i += 2) {
+    const ulonglong2 y = *reinterpret_cast<const ulonglong2*>(keys + i);
+    r += (y.x > x ? 1 : 0) + (y.y > x ? 1 : 0);
   }
-  for (; i < n; ++i) r += (ok[i] > x || (ok[i] == x && i < me)) ? 1 : 0;
+  for (; i < i1; ++i) r += keys[i] > x ? 1 : 0;
   return r;
 }
-__device__ __forceinline__ int rank_asc(const uint32_t* ok, int n, int me) {
-  const uint32_t x = ok[me];
-  int r = 0, i = 0;
+__device__ __forceinline__ int count_below(const uint64_t* keys, int i0, int i1, uint64_t x) {
+  int r = 0, i = i0;
 #pragma unroll 8
-  for (; i + 4 <= n; i += 4) {
-    const uint4 y = *reinterpret_cast<const uint4*>(ok + i);
-    r += (y.x < x || (y.x == x && i + 0 < me)) ? 1 : 0;
-    r += (y.y < x || (y.y == x && i + 1 < me)) ? 1 : 0;
-    r += (y.z < x || (y.z == x && i + 2 < me)) ? 1 : 0;
-    r += (y.w < x || (y.w == x && i + 3 < me)) ? 1 : 0;
+  for (; i + 2 <= i1; i += 2) {
+    const ulonglong2 y = *reinterpret_cast<const ulonglong2*>(keys + i);
+    r += (y.x < x ? 1 : 0) + (y.y < x ? 1 : 0);
   }
-  for (; i < n; ++i) r += (ok[i] < x || (ok[i] == x && i < me)) ? 1 : 0;
+  for (; i < i1; ++i) r += keys[i] < x ? 1 : 0;
   return r;
 }
 
@@ -301,17 +313,24 @@ __device__ void slot_norms(DecSmem<T, HD>& sm, int tid) {
 
 // ----------------------------------------------------------------- decide: retrieval
 
-// One 32-token tile, one half of the work: both waves of a pair compute the slot
-// softmax for the tile (identical results); wave `half` then forms v_hat on its half of
-// the feature dims and the cosine match on its half of the slots, and leaves partial
-// sums / partial argmax in LDS for the combine pass.
+// One 32-token tile, one half of the work, for wave `half` of wave pair `pair`.
+// bf16 storage: each wave scores its half of the slots; the pair exchanges per-token max
+// and sum, and the probabilities, through LDS.  fp32 storage (no LDS room for the
+// exchange): both waves compute the whole softmax.  Then wave `half` forms v_hat on its half
+// of the feature dims and the cosine match on its half of the slots, and leaves partial sums
+// and the partial argmax in LDS for the combine pass.  Contains barriers: every thread of
+// the workgroup calls it the same number of times (tokens past l are inert).
 template <typename T, int HD>
 __device__ void score_tile(DecSmem<T, HD>& sm, const T* kread, const T* kr, const T* kp, const T* v,
-                           int t0, int l, bool steady, float scale, int half, int lane) {
+                           int t0, int l, bool steady, float scale, int pair, int half, int lane) {
+  using Sm = DecSmem<T, HD>;
+  constexpr bool SPLIT = Sm::SPLIT;
+  constexpr int NMB = SPLIT ? 2 : 4;   // slot blocks scored by this wave
   const int n = lane & 31, h = lane >> 5;
   const int tok = t0 + n;
   constexpr int NDB = HD / 32, HDB = NDB / 2;
   const bool in = tok < l;
+  const int mb0 = SPLIT ? 2 * half : 0;
 
   Frag<T, HD> fq;
   fq.load(kp, tok, l, lane);
@@ -321,42 +340,71 @@ __device__ void score_tile(DecSmem<T, HD>& sm, const T* kread, const T* kr, cons
 #pragma unroll
     for (int g = 0; g < 4; ++g) vx[i][g].load(v + (long long)tok * HD + 32 * (half * HDB + i) + 8 * g + 4 * h, in);
 
-  // scores^T[slot][tok] = kread . kp^T over all slots
-  f32x16 acc[4];
+  // scores^T[slot][tok] = kread . kp^T
+  f32x16 acc[NMB];
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb) {
-    acc[mb] = zero16();
-    if constexpr (DecSmem<T, HD>::KREAD_LDS) mm_rows_frag<HD>(acc[mb], sm.kread, sm.KS, 32 * mb, fq, lane);
-    else mm_rows_frag<HD>(acc[mb], kread, HD, 32 * mb, fq, lane);
+  for (int m2 = 0; m2 < NMB; ++m2) {
+    acc[m2] = zero16();
+    if constexpr (Sm::KREAD_LDS) mm_rows_frag<HD>(acc[m2], sm.kread, Sm::KS, 32 * (mb0 + m2), fq, lane);
+    else mm_rows_frag<HD>(acc[m2], kread, HD, 32 * (mb0 + m2), fq, lane);
   }
   // softmax over the slots (column of this lane pair)
   float mx = -INFINITY;
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb)
+  for (int m2 = 0; m2 < NMB; ++m2)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int s = 32 * mb + d_row(lane, r);
-      float x = add_rn(mul_rn(St<T>::rnd(acc[mb][r]), scale), sm.bias[s]);
-      if (!steady && !sm.act[s]) x = -1e9f;
-      acc[mb][r] = x;
-      mx = fmaxf(mx, x);
+    for (int r4 = 0; r4 < 4; ++r4) {
+      const int s0 = 32 * (mb0 + m2) + 8 * r4 + 4 * h;
+      const float4 b4 = *reinterpret_cast<const float4*>(&sm.bias[s0]);
+      const float bb[4] = {b4.x, b4.y, b4.z, b4.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float x = add_rn(mul_rn(St<T>::rnd(acc[m2][4 * r4 + q]), scale), bb[q]);
+        if (!steady && !sm.act[s0 + q]) x = -1e9f;
+        acc[m2][4 * r4 + q] = x;
+        mx = fmaxf(mx, x);
+      }
     }
   mx = fmaxf(mx, xor32(mx));
+  if constexpr (SPLIT) {
+    if (h == 0) sm.u.sc.x[0].mx[pair][half][n] = mx;
+    __syncthreads();
+    mx = fmaxf(sm.u.sc.x[0].mx[pair][0][n], sm.u.sc.x[0].mx[pair][1][n]);
+  }
   float sum = 0.f;
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb)
+  for (int m2 = 0; m2 < NMB; ++m2)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const float e = expf(acc[mb][r] - mx);
-      acc[mb][r] = e;
+      const float e = expf(acc[m2][r] - mx);
+      acc[m2][r] = e;
       sum += e;
     }
   sum += xor32(sum);
+  if constexpr (SPLIT) {
+    if (h == 0) sm.u.sc.x[0].sum[pair][half][n] = sum;
+    __syncthreads();
+    sum = sm.u.sc.x[0].sum[pair][0][n] + sm.u.sc.x[0].sum[pair][1][n];
+  }
   const float rs = 1.0f / sum;
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb)
+  for (int m2 = 0; m2 < NMB; ++m2)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[mb][r] = St<T>::rnd(mul_rn(acc[mb][r], rs));
+    for (int r = 0; r < 16; ++r) acc[m2][r] = St<T>::rnd(mul_rn(acc[m2][r], rs));
+  if constexpr (SPLIT) {
+    // this half's probabilities for the partner: P[tok][slot], 4 consecutive slots per store
+    uint16_t* pp = sm.u.sc.x[0].p[pair] + n * Sm::PS;
+#pragma unroll
+    for (int m2 = 0; m2 < NMB; ++m2)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        u16x4 q4;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) q4[q] = f2bf(acc[m2][4 * r4 + q]);
+        *reinterpret_cast<u16x4*>(pp + 32 * (mb0 + m2) + 8 * r4 + 4 * h) = q4;
+      }
+    __syncthreads();
+  }
 
   // v_hat^T[d][tok] = av^T . P^T on this wave's feature half; partial rel_err sums
   float e2 = 0.f, v2 = 0.f;
@@ -366,14 +414,25 @@ __device__ void score_tile(DecSmem<T, HD>& sm, const T* kread, const T* kr, cons
     f32x16 vh = zero16();
     const int d = 32 * db + n;
     if constexpr (St<T>::is_bf16) {
+      const uint16_t* pp = sm.u.sc.x[0].p[pair] + n * Sm::PS;
 #pragma unroll
       for (int kc = 0; kc < 8; ++kc) {
+        // slots 16*kc + 8*(q>>2) + 4*h + (q&3): own half from registers, the other from LDS
         u16x8 av8, p8;
+        const int mb = kc >> 1;
+        if (mb >> 1 == half) {
+#pragma unroll
+          for (int q = 0; q < 8; ++q) p8[q] = f2bf(acc[mb & 1][8 * (kc & 1) + q]);
+        } else {
+          const u16x4 lo = *reinterpret_cast<const u16x4*>(pp + 16 * kc + 4 * h);
+          const u16x4 hi = *reinterpret_cast<const u16x4*>(pp + 16 * kc + 8 + 4 * h);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) { p8[q] = lo[q]; p8[4 + q] = hi[q]; }
+        }
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
           const int s = 16 * kc + 8 * (q >> 2) + 4 * h + (q & 3);
-          av8[q] = sm.av[s * sm.KS + d];
-          p8[q] = f2bf(acc[kc >> 1][8 * (kc & 1) + q]);
+          av8[q] = sm.av[s * Sm::KS + d];
         }
         mma_bf16(vh, av8, p8);
       }
@@ -383,7 +442,7 @@ __device__ void score_tile(DecSmem<T, HD>& sm, const T* kread, const T* kr, cons
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int s = 32 * mb + d_row(lane, r);
-          mma_f32(vh, sm.av[s * sm.KS + d], acc[mb][r]);
+          mma_f32(vh, sm.av[s * Sm::KS + d], acc[mb][r]);
         }
     }
 #pragma unroll
@@ -399,32 +458,41 @@ __device__ void score_tile(DecSmem<T, HD>& sm, const T* kread, const T* kr, cons
   e2 += xor32(e2);
   v2 += xor32(v2);
 
-  // cos^T[slot][tok] = ak . kr^T / (|ak| |kr|) on this wave's half of the slots
+  // cos^T[slot][tok] = ak . kr^T / (|ak| |kr|) on this wave's half of the slots; argmax on
+  // integer keys: slots ascend along the scan, so a strictly larger key keeps the lower index
+  // on ties, and NaN (largest key) wins as torch.max does
   Frag<T, HD> fk;
   fk.load(kr, tok, l, lane);
   float kk = fk.sumsq();
   kk += xor32(kk);
   const float inv_nk = 1.0f / fmaxf(sqrtf(kk), 1e-12f);
-  float bv = -INFINITY;
-  int bs = 0;
-  bool first = true;
+  uint32_t bkey = 0;
+  float bv = 0.f;
+  int bs = -1;
 #pragma unroll
   for (int m2 = 0; m2 < 2; ++m2) {
     const int mb = 2 * half + m2;
     f32x16 c = zero16();
-    mm_rows_frag<HD>(c, sm.ak, sm.KS, 32 * mb, fk, lane);
+    mm_rows_frag<HD>(c, sm.ak, Sm::KS, 32 * mb, fk, lane);
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int s = 32 * mb + d_row(lane, r);
-      float cv = c[r] * (sm.inv_nak[s] * inv_nk);
-      if (!steady && !sm.act[s]) cv = 0.f;
-      if (first || ranks_before_desc(cv, s, bv, bs)) { bv = cv; bs = s; first = false; }
+    for (int r4 = 0; r4 < 4; ++r4) {
+      const int s0 = 32 * mb + 8 * r4 + 4 * h;
+      const float4 n4 = *reinterpret_cast<const float4*>(&sm.inv_nak[s0]);
+      const float nn[4] = {n4.x, n4.y, n4.z, n4.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float cv = c[4 * r4 + q] * (nn[q] * inv_nk);
+        if (!steady && !sm.act[s0 + q]) cv = 0.f;
+        const uint32_t k = ord_key(cv + 0.0f);   // -0 ranks with +0, as in a float compare
+        if (bs < 0 || k > bkey) { bkey = k; bv = cv; bs = s0 + q; }
+      }
     }
   }
   {
+    const uint32_t ok = (uint32_t)__shfl_xor((int)bkey, 32, 64);
     const float ov = xor32(bv);
     const int os = xor32i(bs);
-    if (ranks_before_desc(ov, os, bv, bs)) { bv = ov; bs = os; }
+    if (ok > bkey || (ok == bkey && os < bs)) { bkey = ok; bv = ov; bs = os; }
   }
   if (h == 0 && in) {
     sm.u.sc.e2[half][tok] = e2;
@@ -507,6 +575,9 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
   T* kread_g = reinterpret_cast<T*>(ws) + (long long)bh * S * HD;   // used only when !KREAD_LDS
   float* w_all = reinterpret_cast<float*>(ws + BH * Work<T, HD>::KREAD);
   const T* kread = sm.KREAD_LDS ? sm.kread : kread_g;
+  T* kread_w = sm.KREAD_LDS ? sm.kread : kread_g;   // writable view of the roped slot keys
+  const int krs = sm.KREAD_LDS ? KS : HD;
+  const bool kp_copy = a.kp_exact != 0;              // a slot taken from token j gets kp_j as its roped key
 
   for (int it = tid; it < S * (HD / 8); it += DT) {
     const int s = it / (HD / 8), d8 = (it % (HD / 8)) * 8;
@@ -584,18 +655,24 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
           sm.rel[j] = 0.15f;
         }
       } else {
-        for (int t = wave >> 1; t < nT; t += DWAVES / 2)
-          score_tile<T, HD>(sm, kread, kr, kp, v, 32 * t, l, false, scale, wave & 1, lane);
+        for (int t = wave >> 1; t < ((nT + 3) & ~3); t += DWAVES / 2)
+          score_tile<T, HD>(sm, kread, kr, kp, v, 32 * t, l, false, scale, wave >> 1, wave & 1, lane);
         __syncthreads();
         score_combine<T, HD>(sm, v, l, false, tid);
       }
       __syncthreads();
-      if (tid < l) sm.u.ok.a[tid] = ord_key(sm.score[tid]);
+      if (tid < l) sm.u.ok.a[tid] = desc_key(sm.score[tid], tid);
       __syncthreads();
-      if (tid < l) {
-        const int r = rank_desc(sm.u.ok.a, l, tid);
-        sm.si_a[r] = tid;
-        sm.sk_a[r] = sm.score[tid];
+      {
+        // two threads per token, each counting half of the keys
+        const int j = tid >> 1, part = tid & 1, mid = (l >> 1) & ~1;
+        int r = 0;
+        if (j < l) r = count_above(sm.u.ok.a, part ? mid : 0, part ? l : mid, sm.u.ok.a[j]);
+        r += __shfl_xor(r, 1, 64);
+        if (j < l && part == 0) {
+          sm.si_a[r] = j;
+          sm.sk_a[r] = sm.score[j];
+        }
       }
       __syncthreads();
       // slots nf + i <- token si_a[i]
@@ -604,6 +681,7 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
         const int j = sm.si_a[i], s = nf + i;
         copy8(&sm.ak[s * KS + d8], kr + (long long)j * HD + d8);
         copy8(&sm.av[s * KS + d8], v + (long long)j * HD + d8);
+        if (kp_copy) copy8(kread_w + s * krs + d8, kp + (long long)j * HD + d8);
       }
       if (tid < m) {
         const int j = sm.si_a[tid], s = nf + tid;
@@ -611,7 +689,7 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
         sm.mass[s] = 1.0f;
         sm.util[s] = sm.rel[j];
         sm.act[s] = 1;
-        sm.dirty[s] = 1;
+        if (!kp_copy) sm.dirty[s] = 1;
       }
       if (log) {
         for (int j = tid; j < B3_LOG_COLS; j += DT) {
@@ -624,8 +702,8 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
       __syncthreads();
     } else {
       // ---------------- steady: score
-      for (int t = wave >> 1; t < nT; t += DWAVES / 2)
-        score_tile<T, HD>(sm, kread, kr, kp, v, 32 * t, l, true, scale, wave & 1, lane);
+      for (int t = wave >> 1; t < ((nT + 3) & ~3); t += DWAVES / 2)
+        score_tile<T, HD>(sm, kread, kr, kp, v, 32 * t, l, true, scale, wave >> 1, wave & 1, lane);
       __syncthreads();
       const bool has = score_combine<T, HD>(sm, v, l, true, tid);
       const int any_merge = __syncthreads_or(has);
@@ -727,19 +805,33 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
         sm.ck[tid] = ck_v;
       }
       __syncthreads();
-      if (tid < l) sm.u.ok.a[tid] = ord_key(ck_v);
-      if (tid < S) sm.u.ok.b[tid] = ord_key(keep_v);
+      if (tid < l) sm.u.ok.a[tid] = desc_key(ck_v, tid);
+      if (tid < S) sm.u.ok.b[tid] = asc_key(keep_v, tid);
       __syncthreads();
       // ---------------- orderings: best free tokens (desc) against least useful slots (asc)
-      if (tid < l) {
-        const int r = rank_desc(sm.u.ok.a, l, tid);
-        sm.sk_a[r] = sm.ck[tid];
-        sm.si_a[r] = tid;
-      } else if (tid >= DT - S) {
-        const int s = tid - (DT - S);
-        const int r = rank_asc(sm.u.ok.b, S, s);
-        sm.sk_b[r] = sm.keep[s];
-        sm.si_b[r] = s;
+      {
+        // l + S items, two threads each, each counting half of the keys
+        const int item = tid >> 1, part = tid & 1;
+        for (int base = 0; base < l + S; base += DT / 2) {
+          const int it = base + item;
+          int r = 0;
+          if (it < l) {
+            const int mid = (l >> 1) & ~1;
+            r = count_above(sm.u.ok.a, part ? mid : 0, part ? l : mid, sm.u.ok.a[it]);
+          } else if (it < l + S) {
+            r = count_below(sm.u.ok.b, part ? S / 2 : 0, part ? S : S / 2, sm.u.ok.b[it - l]);
+          }
+          r += __shfl_xor(r, 1, 64);
+          if (part == 0) {
+            if (it < l) {
+              sm.sk_a[r] = sm.ck[it];
+              sm.si_a[r] = it;
+            } else if (it < l + S) {
+              sm.sk_b[r] = sm.keep[it - l];
+              sm.si_b[r] = it - l;
+            }
+          }
+        }
       }
       __syncthreads();
       const int kc = min(l, S);
@@ -752,7 +844,7 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
           sm.pm[s] = pos[j];
           sm.mass[s] = 1.0f;
           sm.util[s] = sm.rel[j];
-          sm.dirty[s] = 1;
+          if (!kp_copy) sm.dirty[s] = 1;
         }
       }
       for (int it = tid; it < kc * (HD / 8); it += DT) {
@@ -762,6 +854,7 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
           const int j = sm.si_a[i], s = sm.si_b[i];
           copy8(&sm.ak[s * KS + d8], kr + (long long)j * HD + d8);
           copy8(&sm.av[s * KS + d8], v + (long long)j * HD + d8);
+          if (kp_copy) copy8(kread_w + s * krs + d8, kp + (long long)j * HD + d8);
         }
       }
       __syncthreads();
@@ -799,10 +892,9 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
     __syncthreads();
     if (a.snap_k) {
       T* kd = reinterpret_cast<T*>(a.snap_k) + (step * BH + bh) * S * HD;
-      const int rs = sm.KREAD_LDS ? KS : HD;
       for (int it = tid; it < S * (HD / 8); it += DT) {
         const int s = it / (HD / 8), d8 = (it % (HD / 8)) * 8;
-        copy8(kd + s * HD + d8, kread + s * rs + d8);
+        copy8(kd + s * HD + d8, kread + s * krs + d8);
       }
     }
     if (a.snap_v) {

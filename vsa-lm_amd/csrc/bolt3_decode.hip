@@ -13,6 +13,7 @@
 // The step is bound by reading the window, the slots and M_res once; every
 // load is a 16-byte vector load spread over HD/8 lanes per key.
 #include "bolt3_common.h"
+#include "bolt3_math.h"
 #include "bolt3_amd.h"
 
 namespace b3 {
@@ -64,7 +65,7 @@ __global__ void __launch_bounds__(DNT) decode_kernel(b3_decode_args a) {
   {
     const int i = tid % HALF;
     float sn, cs;
-    sincosf(mul_rn(pos, a.inv_freq[i]), &sn, &cs);
+    sincos_rope(mul_rn(pos, a.inv_freq[i]), &sn, &cs);
     const float c = St<T>::rnd(cs), si = St<T>::rnd(sn);
     constexpr int UNITS = DNT / HALF;
     for (int u0 = 0; u0 < G + 2; u0 += UNITS) {

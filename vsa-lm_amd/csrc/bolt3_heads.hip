@@ -11,6 +11,7 @@
 // the RoPE pair (i, i + HD/2).  Every value is rounded to the storage type at
 // the same points as the reference's per-op evaluation.
 #include "bolt3_common.h"
+#include "bolt3_math.h"
 #include "bolt3_amd.h"
 
 namespace b3 {
@@ -30,7 +31,7 @@ __global__ void __launch_bounds__(256) heads_kernel(b3_heads_args a) {
   const float inv = a.inv_freq[i];
   const float ang = mul_rn(pos, inv);
   float sn, cs;
-  sincosf(ang, &sn, &cs);
+  sincos_rope(ang, &sn, &cs);
   const float c = St<T>::rnd(cs), s = St<T>::rnd(sn);
 
   for (int u0 = 0; u0 < n_units; u0 += UNITS) {

@@ -361,6 +361,312 @@ __global__ void __launch_bounds__(512) attn_kernel(b3_attn_args a, int QW) {
   }
 }
 
+// ----------------------------------------------------------------- forward, bf16
+
+// Forward (mode 0) with bf16 storage.  Workgroup = (query tile of 32*QW, chunk, bh) with
+// G*QW wavefronts as above.  The keys of a chunk are walked as 32-key blocks:
+//   [sink block | S/32 slot blocks | C/32 previous-chunk blocks | current-chunk blocks up to
+//    the tile's last query]
+// with one barrier per block: the next block is loaded into registers while the current one
+// is multiplied, then written to the other LDS buffer (K rows and V^T columns).  Softmax is
+// online in base 2 (x*log2e folded into one FMA).  The M_res readout stages M^T (bf16 hi/lo)
+// in two halves of the feature rows through the same LDS.
+template <int HD>
+struct FwdSmem {
+  static constexpr int KS = HD + 8;              // K row stride
+  static constexpr int VS = KB + 8;              // V^T row stride
+  static constexpr int MS = HD + 8;              // M^T row stride
+  static constexpr int KV = KB * KS + HD * VS;   // elements of one K/V buffer
+  static constexpr int MH = (HD / 2) * MS;       // elements of one M^T half (hi or lo)
+  static constexpr int RAW = 2 * KV > 2 * MH ? 2 * KV : 2 * MH;
+  alignas(16) uint16_t raw[RAW];
+  float bias[2][KB];
+  __device__ uint16_t* k(int buf) { return raw + buf * KV; }
+  __device__ uint16_t* vt(int buf) { return raw + buf * KV + KB * KS; }
+};
+
+// Block i of the schedule: key rows, number of valid keys, slot bias row, causal offset.
+struct FwdBlock {
+  const uint16_t* k;
+  const uint16_t* v;
+  const float* bias;   // null: no bias
+  int nvalid;
+  int kpos;            // current-chunk block: index of its first key within the chunk; else -1
+};
+
+__device__ __forceinline__ uint16_t f2bf_fin(float f) {   // RNE for finite values
+  uint32_t u = __float_as_uint(f);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+template <int HD, int IPT>
+__global__ void __launch_bounds__(512) attn_fwd_kernel(b3_attn_args a, int QW) {
+  using Sm = FwdSmem<HD>;
+  __shared__ Sm sm;
+  constexpr int NDB = HD / 32;
+  constexpr int ITEMS = KB * (HD / 8);
+  const int G = a.H / a.HKV;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n = lane & 31, h = lane >> 5;
+  const int nthreads = blockDim.x;
+  const int g = wave / QW, qsub = wave % QW;
+  const int bh = blockIdx.z, b = bh / a.HKV, hkv = bh % a.HKV;
+  const int hq = hkv * G + g;
+  const int chunk = blockIdx.y, C = a.C;
+  const int qbase = chunk * C;
+  const int nq_chunk = min(C, a.n_q - qbase);
+  const int qt0 = blockIdx.x * 32 * QW;
+  if (qt0 >= nq_chunk) return;                  // uniform across the workgroup
+  const int qi = qt0 + 32 * qsub + n;           // this lane's query within the chunk
+  const bool qok = qi < nq_chunk;
+  const int t = qbase + qi;
+  const int wave_q0 = qt0 + 32 * qsub;
+  const int wg_qend = min(qt0 + 32 * QW, nq_chunk);
+  const int step = chunk - 2;
+  const float L2E = 1.4426950408889634f;
+  const float scale = 1.0f / sqrtf((float)HD);
+
+  // ---- block schedule
+  const long long wofs = (long long)b * a.w_sb + (long long)hkv * a.w_sh;
+  const uint16_t* wk = reinterpret_cast<const uint16_t*>(a.win_k) + wofs;
+  const uint16_t* wv = reinterpret_cast<const uint16_t*>(a.win_v) + wofs;
+  const int n_pre = chunk >= 2 ? 1 + (a.S + KB - 1) / KB : 0;
+  const int n_prev = chunk >= 1 ? (C + KB - 1) / KB : 0;
+  const int n_cur = (wg_qend + KB - 1) / KB;
+  const int nb = n_pre + n_prev + n_cur;
+  auto block = [&](int i) -> FwdBlock {
+    FwdBlock f;
+    f.bias = nullptr;
+    f.kpos = -1;
+    if (i < n_pre) {
+      if (i == 0) {
+        f.k = wk;
+        f.v = wv;
+        f.nvalid = min(a.n_sinks, C);
+      } else {
+        const long long so = (long long)step * a.slot_step + (long long)bh * a.S * HD + (long long)(i - 1) * KB * HD;
+        f.k = reinterpret_cast<const uint16_t*>(a.slot_k) + so;
+        f.v = reinterpret_cast<const uint16_t*>(a.slot_v) + so;
+        f.bias = a.slot_bias + (long long)step * (a.slot_step / HD) + (long long)bh * a.S + (i - 1) * KB;
+        f.nvalid = min(KB, a.S - (i - 1) * KB);
+      }
+    } else if (i < n_pre + n_prev) {
+      const int j = i - n_pre;
+      const long long o = ((long long)(chunk - 1) * C + j * KB) * HD;
+      f.k = wk + o;
+      f.v = wv + o;
+      f.nvalid = min(KB, C - j * KB);
+    } else {
+      const int j = i - n_pre - n_prev;
+      const long long o = ((long long)qbase + j * KB) * HD;
+      f.k = wk + o;
+      f.v = wv + o;
+      f.nvalid = min(KB, nq_chunk - j * KB);
+      f.kpos = j * KB;
+    }
+    return f;
+  };
+
+  // ---- staging registers: IPT 16-byte K and V pieces per thread, plus one bias value
+  u16x8 rk[IPT], rv[IPT];
+  float rb = 0.f;
+  auto load = [&](int i) {
+    const FwdBlock f = block(i);
+#pragma unroll
+    for (int q = 0; q < IPT; ++q) {
+      const int it = tid + q * nthreads;
+      const int r = it / (HD / 8), c8 = (it % (HD / 8)) * 8;
+      if (it < ITEMS && r < f.nvalid) {
+        rk[q] = *reinterpret_cast<const u16x8*>(f.k + (long long)r * HD + c8);
+        rv[q] = *reinterpret_cast<const u16x8*>(f.v + (long long)r * HD + c8);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) { rk[q][e] = 0; rv[q][e] = 0; }
+      }
+    }
+    rb = (tid < KB && f.bias && tid < f.nvalid) ? f.bias[tid] : 0.f;
+  };
+  auto store = [&](int buf) {
+    uint16_t* sK = sm.k(buf);
+    uint16_t* sV = sm.vt(buf);
+#pragma unroll
+    for (int q = 0; q < IPT; ++q) {
+      const int it = tid + q * nthreads;
+      if (it < ITEMS) {
+        const int r = it / (HD / 8), c8 = (it % (HD / 8)) * 8;
+        *reinterpret_cast<u16x8*>(sK + r * Sm::KS + c8) = rk[q];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sV[(c8 + e) * Sm::VS + r] = rv[q][e];
+      }
+    }
+    if (tid < KB) sm.bias[buf][tid] = rb;
+  };
+
+  const uint16_t* qrow = reinterpret_cast<const uint16_t*>(a.q_rope) + b * a.q_sb + hq * a.q_sh + (long long)t * HD;
+  QFrag<uint16_t, HD> qf;
+  qf.load(qrow, qok, h);
+  f32x16 o[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) o[db] = zero16();
+  float m_run = -INFINITY, l_run = 0.f;
+
+  load(0);
+  store(0);
+  __syncthreads();
+  for (int i = 0; i < nb; ++i) {
+    const int buf = i & 1;
+    if (i + 1 < nb) load(i + 1);
+    const FwdBlock f = block(i);
+    // a wave whose queries all precede the block's first key skips it
+    if (!(f.kpos >= 0 && f.kpos > wave_q0 + 31)) {
+      const uint16_t* sK = sm.k(buf);
+      const uint16_t* sV = sm.vt(buf);
+      f32x16 s = zero16();
+#pragma unroll
+      for (int ks = 0; ks < HD / 16; ++ks) {
+        const u16x8 av = *reinterpret_cast<const u16x8*>(sK + n * Sm::KS + 16 * ks + 8 * h);
+        mma_bf16(s, av, qf.v[ks]);
+      }
+      // valid keys of this lane's query: kr <= lim
+      const int lim = min(f.nvalid - 1, f.kpos >= 0 ? qi - f.kpos : KB - 1);
+      const bool has_bias = f.bias != nullptr;
+      float bm = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int kr = d_row(lane, r);
+        float x = mul_rn(round_bf(s[r]), scale);
+        if (has_bias) x = add_rn(x, sm.bias[buf][kr]);
+        x = kr <= lim ? x : -INFINITY;
+        s[r] = x;
+        bm = fmaxf(bm, x);
+      }
+      bm = fmaxf(bm, xor32(bm));
+      const float m_new = fmaxf(m_run, bm);
+      if (m_new != -INFINITY) {
+        const float mL = m_new * L2E;
+        const float alpha = __builtin_amdgcn_exp2f(fmaf(m_run, L2E, -mL));
+        float ps = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float p = __builtin_amdgcn_exp2f(fmaf(s[r], L2E, -mL));
+          s[r] = p;
+          ps += p;
+        }
+        ps += xor32(ps);
+        l_run = l_run * alpha + ps;
+        m_run = m_new;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+        u16x8 pv[2];
+#pragma unroll
+        for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) pv[kc][e] = f2bf_fin(s[8 * kc + e]);
+        // ---- O^T[d][q] += V^T . P^T
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+          const int d = 32 * db + n;
+#pragma unroll
+          for (int kc = 0; kc < 2; ++kc) {
+            u16x8 av;
+            const u16x4 lo = *reinterpret_cast<const u16x4*>(sV + d * Sm::VS + 16 * kc + 4 * h);
+            const u16x4 hi = *reinterpret_cast<const u16x4*>(sV + d * Sm::VS + 16 * kc + 8 + 4 * h);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) { av[e] = lo[e]; av[4 + e] = hi[e]; }
+            mma_bf16(o[db], av, pv[kc]);
+          }
+        }
+      }
+    }
+    if (i + 1 < nb) store(buf ^ 1);
+    __syncthreads();
+  }
+
+  // ---- normalise; y = round(O)
+  const float inv_l = l_run > 0.f ? 1.0f / l_run : 0.f;
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[db][r] = round_bf(o[db][r] * inv_l);
+
+  // ---- readout: eta * RMSNorm(normalize(q_raw) . M * (1-gamma)/sqrt(HD)), M^T staged by halves
+  if (a.m_res && step >= 0) {
+    const uint16_t* src = reinterpret_cast<const uint16_t*>(a.m_res + (long long)step * a.m_step) +
+                          (long long)bh * 2 * HD * HD;   // bf16 M^T hi, then lo (HD*HD floats of room)
+    const uint16_t* rrow = reinterpret_cast<const uint16_t*>(a.q_raw) + b * a.q_sb + hq * a.q_sh + (long long)t * HD;
+    QFrag<uint16_t, HD> rf;
+    rf.load(rrow, qok, h);
+    float qq = rf.sumsq();
+    qq += xor32(qq);
+    const float inv_q = 1.0f / fmaxf(sqrtf(qq), 1e-12f);
+    const float coef = div_rn(1.0f - a.gamma[hkv], sqrtf((float)HD));
+    f32x16 rr[NDB];
+    uint16_t* mh = sm.raw;
+    uint16_t* ml = sm.raw + Sm::MH;
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      if (p > 0) __syncthreads();
+      for (int it = tid; it < 2 * (HD / 2) * (HD / 8); it += nthreads) {
+        const int part = it / ((HD / 2) * (HD / 8)), rem = it % ((HD / 2) * (HD / 8));
+        const int dr = rem / (HD / 8), c8 = (rem % (HD / 8)) * 8;
+        *reinterpret_cast<u16x8*>((part ? ml : mh) + dr * Sm::MS + c8) =
+            *reinterpret_cast<const u16x8*>(src + part * HD * HD + (long long)((HD / 2) * p + dr) * HD + c8);
+      }
+      __syncthreads();
+#pragma unroll
+      for (int dh = 0; dh < NDB / 2; ++dh) {
+        const int db = (NDB / 2) * p + dh;
+        rr[db] = zero16();
+        const int dr = 32 * dh + n;
+#pragma unroll
+        for (int ks = 0; ks < HD / 16; ++ks) {
+          const u16x8 ah = *reinterpret_cast<const u16x8*>(mh + dr * Sm::MS + 16 * ks + 8 * h);
+          const u16x8 al = *reinterpret_cast<const u16x8*>(ml + dr * Sm::MS + 16 * ks + 8 * h);
+          mma_bf16(rr[db], ah, rf.v[ks]);
+          mma_bf16(rr[db], al, rf.v[ks]);
+        }
+      }
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float y = mul_rn(rr[db][r] * inv_q, coef);
+        rr[db][r] = y;
+        ss += y * y;
+      }
+    ss += xor32(ss);
+    const float rs = 1.0f / sqrtf(div_rn(ss, (float)HD) + a.eps);
+    const float eta = qok ? a.eta[b * a.e_sb + hq * a.e_sh + t] : 0.f;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int d = 32 * db + d_row(lane, r);
+        const float ymn = mul_rn(mul_rn(rr[db][r], rs), a.res_w[d]);
+        o[db][r] = round_bf(add_rn(o[db][r], round_bf(mul_rn(eta, ymn))));
+      }
+  }
+
+  // ---- write y[b][t][hq][d], 4 consecutive features per store
+  if (qok) {
+    uint16_t* yrow = reinterpret_cast<uint16_t*>(a.y) + b * a.y_sb + (long long)t * a.y_st + hq * HD;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        u16x4 w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[e] = f2bf(o[db][4 * r4 + e]);
+        *reinterpret_cast<u16x4*>(yrow + 32 * db + 8 * r4 + 4 * h) = w;
+      }
+  }
+}
+
 template <typename T, int HD>
 static int launch_attn(const b3_attn_args& a, hipStream_t st) {
   const int G = a.H / a.HKV;
@@ -369,7 +675,17 @@ static int launch_attn(const b3_attn_args& a, hipStream_t st) {
   const int n_chunks = a.mode == 0 ? (a.n_q + a.C - 1) / a.C : 1;
   const int qlen = a.mode == 0 ? a.C : a.n_q;
   dim3 grid((qlen + per_wg - 1) / per_wg, n_chunks, a.B * a.HKV);
-  hipLaunchKernelGGL((attn_kernel<T, HD>), grid, dim3(64 * G * QW), 0, st, a, QW);
+  const int nthreads = 64 * G * QW;
+  if constexpr (St<T>::is_bf16) {
+    if (a.mode == 0 && (!a.m_res || a.m_split)) {
+      const int ipt = (KB * (HD / 8) + nthreads - 1) / nthreads;
+      if (ipt <= 1) hipLaunchKernelGGL((attn_fwd_kernel<HD, 1>), grid, dim3(nthreads), 0, st, a, QW);
+      else if (ipt <= 2) hipLaunchKernelGGL((attn_fwd_kernel<HD, 2>), grid, dim3(nthreads), 0, st, a, QW);
+      else hipLaunchKernelGGL((attn_fwd_kernel<HD, 4>), grid, dim3(nthreads), 0, st, a, QW);
+      return (int)hipGetLastError();
+    }
+  }
+  hipLaunchKernelGGL((attn_kernel<T, HD>), grid, dim3(nthreads), 0, st, a, QW);
   return (int)hipGetLastError();
 }
 

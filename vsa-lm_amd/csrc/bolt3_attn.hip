@@ -394,12 +394,6 @@ struct FwdBlock {
   int kpos;            // current-chunk block: index of its first key within the chunk; else -1
 };
 
-__device__ __forceinline__ uint16_t f2bf_fin(float f) {   // RNE for finite values
-  uint32_t u = __float_as_uint(f);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
-}
-
 template <int HD, int IPT>
 __global__ void __launch_bounds__(512) attn_fwd_kernel(b3_attn_args a, int QW) {
   using Sm = FwdSmem<HD>;
@@ -530,13 +524,12 @@ __global__ void __launch_bounds__(512) attn_fwd_kernel(b3_attn_args a, int QW) {
       }
       // valid keys of this lane's query: kr <= lim
       const int lim = min(f.nvalid - 1, f.kpos >= 0 ? qi - f.kpos : KB - 1);
-      const bool has_bias = f.bias != nullptr;
       float bm = -INFINITY;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int kr = d_row(lane, r);
-        float x = mul_rn(round_bf(s[r]), scale);
-        if (has_bias) x = add_rn(x, sm.bias[buf][kr]);
+        // the staged bias is 0 outside slot blocks
+        float x = add_rn(mul_rn(round_bf(s[r]), scale), sm.bias[buf][kr]);
         x = kr <= lim ? x : -INFINITY;
         s[r] = x;
         bm = fmaxf(bm, x);
@@ -564,7 +557,7 @@ __global__ void __launch_bounds__(512) attn_fwd_kernel(b3_attn_args a, int QW) {
 #pragma unroll
         for (int kc = 0; kc < 2; ++kc)
 #pragma unroll
-          for (int e = 0; e < 8; ++e) pv[kc][e] = f2bf_fin(s[8 * kc + e]);
+          for (int e = 0; e < 8; ++e) pv[kc][e] = f2bf(s[8 * kc + e]);
         // ---- O^T[d][q] += V^T . P^T
 #pragma unroll
         for (int db = 0; db < NDB; ++db) {

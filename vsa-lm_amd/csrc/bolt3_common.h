@@ -26,13 +26,9 @@ constexpr int WAVE = 64;
 
 __device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
 
-// Round-to-nearest-even, NaN kept quiet (same rule as torch's fp32 -> bf16 cast).
-__device__ __forceinline__ uint16_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
-}
+// Round-to-nearest-even (torch's fp32 -> bf16 cast): gfx950's v_cvt_pk_bf16_f32, which
+// rounds to nearest even and keeps NaN a NaN.
+__device__ __forceinline__ uint16_t f2bf(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 
 __device__ __forceinline__ float round_bf(float f) { return bf2f(f2bf(f)); }
 

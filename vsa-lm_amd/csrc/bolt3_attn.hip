@@ -507,7 +507,7 @@ __global__ void __launch_bounds__(512) attn_fwd_kernel(b3_attn_args a, int QW) {
 
   load(0);
   store(0);
-  __syncthreads();
+  sync_lds();
   for (int i = 0; i < nb; ++i) {
     const int buf = i & 1;
     if (i + 1 < nb) load(i + 1);
@@ -575,7 +575,7 @@ __global__ void __launch_bounds__(512) attn_fwd_kernel(b3_attn_args a, int QW) {
       }
     }
     if (i + 1 < nb) store(buf ^ 1);
-    __syncthreads();
+    sync_lds();
   }
 
   // ---- normalise; y = round(O)
@@ -601,14 +601,14 @@ __global__ void __launch_bounds__(512) attn_fwd_kernel(b3_attn_args a, int QW) {
     uint16_t* ml = sm.raw + Sm::MH;
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
-      if (p > 0) __syncthreads();
+      if (p > 0) sync_lds();
       for (int it = tid; it < 2 * (HD / 2) * (HD / 8); it += nthreads) {
         const int part = it / ((HD / 2) * (HD / 8)), rem = it % ((HD / 2) * (HD / 8));
         const int dr = rem / (HD / 8), c8 = (rem % (HD / 8)) * 8;
         *reinterpret_cast<u16x8*>((part ? ml : mh) + dr * Sm::MS + c8) =
             *reinterpret_cast<const u16x8*>(src + part * HD * HD + (long long)((HD / 2) * p + dr) * HD + c8);
       }
-      __syncthreads();
+      sync_lds();
 #pragma unroll
       for (int dh = 0; dh < NDB / 2; ++dh) {
         const int db = (NDB / 2) * p + dh;

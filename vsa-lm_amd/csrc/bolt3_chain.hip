@@ -73,32 +73,38 @@ struct DecSmem {
   alignas(16) T kread[KREAD_LDS ? S * KS : 1];                    // roped slot keys
   float mass[S], util[S], pm[S], inv_nak[S], keep[S], bias[S];
   int act[S], dirty[S];
+  int any_merge;
   float invf[HD / 2];
-  float rel[LMAX], score[LMAX], best[LMAX], simv[LMAX], ck[LMAX];
+  float rel[LMAX], score[LMAX];
   int slot[LMAX], flags[LMAX];
   float sk_a[LMAX];
   int si_a[LMAX];
   float sk_b[S];
   int si_b[S];
-  // Softmax exchange of a wave pair (bf16 storage): per-half max and sum per token, and the
-  // probabilities of each half, P[tok][slot] with row stride PS.
+  // Tiles are scored in rounds of 128 tokens (4 wave pairs x 32).  Within a pair, one
+  // exchange carries each half's softmax max / sum and best slot; for bf16 storage a second
+  // one carries the probabilities, P[tok][slot] with row stride PS (fp32 storage has no LDS
+  // room for it and computes the whole softmax in both waves).
   static constexpr bool SPLIT = sizeof(T) == 2;
   static constexpr int PS = S + 4;
-  struct PairX {
-    float mx[DWAVES / 2][2][32], sum[DWAVES / 2][2][32];
-    alignas(16) uint16_t p[DWAVES / 2][32 * PS];
-  };
+  static constexpr int NP = DWAVES / 2;
   union {  // phase-local buffers
     struct {
-      float e2[2][LMAX], v2[2][LMAX], bv[2][LMAX];
-      int bs[2][LMAX];
-      PairX x[SPLIT ? 1 : 0];
+      float e2[2][128], v2[2][128], dv[2][128], vv[2][128], aa[2][128], bv[2][128];
+      int bs[2][128];
+      float xmx[NP][2][32], xsum[NP][2][32], xbv[NP][2][32];
+      uint32_t xkey[NP][2][32];
+      int xbs[NP][2][32];
+      alignas(16) uint16_t p[SPLIT ? NP : 1][SPLIT ? 32 * PS : 1];
     } sc;
     struct { int cnt[S], off[S], hits[S], mlist[LMAX]; float psum[S]; int nhit; } mg;
     struct { float mx[2][S]; int nan[2][S]; } kp;
     struct { alignas(16) uint64_t a[LMAX]; alignas(16) uint64_t b[S]; } ok;
   } u;
 };
+static_assert(sizeof(DecSmem<uint16_t, 128>) <= 160 * 1024, "decide_kernel LDS");
+static_assert(sizeof(DecSmem<float, 128>) <= 160 * 1024, "decide_kernel LDS");
+static_assert(sizeof(DecSmem<float, 64>) <= 160 * 1024, "decide_kernel LDS");
 
 // ----------------------------------------------------------------- fragments
 
@@ -313,41 +319,56 @@ __device__ void slot_norms(DecSmem<T, HD>& sm, int tid) {
 
 // ----------------------------------------------------------------- decide: retrieval
 
-// One 32-token tile, one half of the work, for wave `half` of wave pair `pair`.
-// bf16 storage: each wave scores its half of the slots; the pair exchanges per-token max
-// and sum, and the probabilities, through LDS.  fp32 storage (no LDS room for the
-// exchange): both waves compute the whole softmax.  Then wave `half` forms v_hat on its half
-// of the feature dims and the cosine match on its half of the slots, and leaves partial sums
-// and the partial argmax in LDS for the combine pass.  Contains barriers: every thread of
-// the workgroup calls it the same number of times (tokens past l are inert).
+// Token data of one 32-token tile for wave `half` of a pair: the roped key fragment and
+// the values on this wave's half of the feature dims (the un-roped key fragment is loaded
+// by the tile itself).
 template <typename T, int HD>
-__device__ void score_tile(DecSmem<T, HD>& sm, const T* kread, const T* kr, const T* kp, const T* v,
-                           int t0, int l, bool steady, float scale, int pair, int half, int lane) {
+struct TileIn {
+  static constexpr int HDB = HD / 64;
+  Frag<T, HD> fq;
+  V4<T> vx[HDB][4];   // v[tok][32*(half*HDB + i) + 8*g + 4*h + q]
+  __device__ __forceinline__ void load(const T* kp, const T* kr, const T* v, int t0, int l, int half, int lane) {
+    const int n = lane & 31, h = lane >> 5, tok = t0 + n;
+    fq.load(kp, tok, l, lane);
+#pragma unroll
+    for (int i = 0; i < HDB; ++i)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        vx[i][g].load(v + (long long)tok * HD + 32 * (half * HDB + i) + 8 * g + 4 * h, tok < l);
+  }
+};
+
+// One 32-token tile, one half of the work, for wave `half` of wave pair `pair`.
+// bf16 storage: each wave scores and cosine-matches its half of the slots; one LDS exchange
+// gives the pair the softmax max / sum and the best slot, a second one the probabilities.
+// fp32 storage (no LDS room for the exchange): both waves compute the whole softmax.  Then
+// wave `half` forms v_hat and the value cosine on its half of the feature dims and leaves
+// partial sums in LDS for the combine pass.  Contains barriers: every thread of the
+// workgroup calls it the same number of times (tokens past l are inert).
+template <typename T, int HD>
+__device__ void score_tile(DecSmem<T, HD>& sm, const T* kread, const TileIn<T, HD>& td, const T* kr, int t0, int l,
+                           bool steady, float scale, int pair, int half, int lane) {
   using Sm = DecSmem<T, HD>;
   constexpr bool SPLIT = Sm::SPLIT;
   constexpr int NMB = SPLIT ? 2 : 4;   // slot blocks scored by this wave
+  constexpr int HDB = TileIn<T, HD>::HDB;
   const int n = lane & 31, h = lane >> 5;
   const int tok = t0 + n;
-  constexpr int NDB = HD / 32, HDB = NDB / 2;
   const bool in = tok < l;
   const int mb0 = SPLIT ? 2 * half : 0;
 
-  Frag<T, HD> fq;
-  fq.load(kp, tok, l, lane);
-  V4<T> vx[HDB][4];   // v[tok][32*db + 8*g + 4*h + q], raw storage values
-#pragma unroll
-  for (int i = 0; i < HDB; ++i)
-#pragma unroll
-    for (int g = 0; g < 4; ++g) vx[i][g].load(v + (long long)tok * HD + 32 * (half * HDB + i) + 8 * g + 4 * h, in);
+  Frag<T, HD> fk;   // un-roped keys: consumed after the softmax, so their latency hides behind it
+  fk.load(kr, tok, l, lane);
 
   // scores^T[slot][tok] = kread . kp^T
   f32x16 acc[NMB];
 #pragma unroll
   for (int m2 = 0; m2 < NMB; ++m2) {
     acc[m2] = zero16();
-    if constexpr (Sm::KREAD_LDS) mm_rows_frag<HD>(acc[m2], sm.kread, Sm::KS, 32 * (mb0 + m2), fq, lane);
-    else mm_rows_frag<HD>(acc[m2], kread, HD, 32 * (mb0 + m2), fq, lane);
+    if constexpr (Sm::KREAD_LDS) mm_rows_frag<HD>(acc[m2], sm.kread, Sm::KS, 32 * (mb0 + m2), td.fq, lane);
+    else mm_rows_frag<HD>(acc[m2], kread, HD, 32 * (mb0 + m2), td.fq, lane);
   }
+
   // softmax over the slots (column of this lane pair)
   float mx = -INFINITY;
 #pragma unroll
@@ -366,11 +387,6 @@ __device__ void score_tile(DecSmem<T, HD>& sm, const T* kread, const T* kr, cons
       }
     }
   mx = fmaxf(mx, xor32(mx));
-  if constexpr (SPLIT) {
-    if (h == 0) sm.u.sc.x[0].mx[pair][half][n] = mx;
-    __syncthreads();
-    mx = fmaxf(sm.u.sc.x[0].mx[pair][0][n], sm.u.sc.x[0].mx[pair][1][n]);
-  }
   float sum = 0.f;
 #pragma unroll
   for (int m2 = 0; m2 < NMB; ++m2)
@@ -381,19 +397,75 @@ __device__ void score_tile(DecSmem<T, HD>& sm, const T* kread, const T* kr, cons
       sum += e;
     }
   sum += xor32(sum);
-  if constexpr (SPLIT) {
-    if (h == 0) sm.u.sc.x[0].sum[pair][half][n] = sum;
-    __syncthreads();
-    sum = sm.u.sc.x[0].sum[pair][0][n] + sm.u.sc.x[0].sum[pair][1][n];
+  // cos^T[slot][tok] = ak . kr^T / (|ak| |kr|) on this wave's half of the slots; argmax on
+  // integer keys: slots ascend along the scan, so a strictly larger key keeps the lower index
+  // on ties, and NaN (largest key) wins as torch.max does
+  float kk = fk.sumsq();
+  kk += xor32(kk);
+  const float inv_nk = 1.0f / fmaxf(sqrtf(kk), 1e-12f);
+  uint32_t bkey = 0;
+  float bv = 0.f;
+  int bs = -1;
+#pragma unroll
+  for (int m2 = 0; m2 < 2; ++m2) {
+    const int mb = 2 * half + m2;
+    f32x16 c = zero16();
+    mm_rows_frag<HD>(c, sm.ak, Sm::KS, 32 * mb, fk, lane);
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      const int s0 = 32 * mb + 8 * r4 + 4 * h;
+      const float4 n4 = *reinterpret_cast<const float4*>(&sm.inv_nak[s0]);
+      const float nn[4] = {n4.x, n4.y, n4.z, n4.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float cv = c[4 * r4 + q] * (nn[q] * inv_nk);
+        if (!steady && !sm.act[s0 + q]) cv = 0.f;
+        const uint32_t k = ord_key(cv + 0.0f);   // -0 ranks with +0, as in a float compare
+        if (bs < 0 || k > bkey) { bkey = k; bv = cv; bs = s0 + q; }
+      }
+    }
   }
-  const float rs = 1.0f / sum;
+  {
+    const uint32_t ok = (uint32_t)__shfl_xor((int)bkey, 32, 64);
+    const float ov = xor32(bv);
+    const int os = xor32i(bs);
+    if (ok > bkey || (ok == bkey && os < bs)) { bkey = ok; bv = ov; bs = os; }
+  }
+
+  float rs = 1.0f / sum;
+  if constexpr (SPLIT) {
+    // one exchange: max, sum (relative to the own max) and best slot of each half
+    if (h == 0) {
+      sm.u.sc.xmx[pair][half][n] = mx;
+      sm.u.sc.xsum[pair][half][n] = sum;
+    }
+  }
+  // the pair's best slot (and, split, the softmax max / sum) through one exchange
+  if (h == 0) {
+    sm.u.sc.xkey[pair][half][n] = bkey;
+    sm.u.sc.xbv[pair][half][n] = bv;
+    sm.u.sc.xbs[pair][half][n] = bs;
+  }
+  sync_lds();
+  {
+    const int o = half ^ 1;
+    if constexpr (SPLIT) {
+      const float m_o = sm.u.sc.xmx[pair][o][n], s_o = sm.u.sc.xsum[pair][o][n];
+      const float m = fmaxf(mx, m_o);
+      const float f_self = expf(mx - m), f_o = expf(m_o - m);
+      rs = f_self / (sum * f_self + s_o * f_o);
+    }
+    const uint32_t ko = sm.u.sc.xkey[pair][o][n];
+    const int so = sm.u.sc.xbs[pair][o][n];
+    if (ko > bkey || (ko == bkey && so < bs)) { bkey = ko; bv = sm.u.sc.xbv[pair][o][n]; bs = so; }
+  }
 #pragma unroll
   for (int m2 = 0; m2 < NMB; ++m2)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[m2][r] = St<T>::rnd(mul_rn(acc[m2][r], rs));
   if constexpr (SPLIT) {
     // this half's probabilities for the partner: P[tok][slot], 4 consecutive slots per store
-    uint16_t* pp = sm.u.sc.x[0].p[pair] + n * Sm::PS;
+    uint16_t* pp = sm.u.sc.p[pair] + n * Sm::PS;
 #pragma unroll
     for (int m2 = 0; m2 < NMB; ++m2)
 #pragma unroll
@@ -403,8 +475,31 @@ __device__ void score_tile(DecSmem<T, HD>& sm, const T* kread, const T* kr, cons
         for (int q = 0; q < 4; ++q) q4[q] = f2bf(acc[m2][4 * r4 + q]);
         *reinterpret_cast<u16x4*>(pp + 32 * (mb0 + m2) + 8 * r4 + 4 * h) = q4;
       }
-    __syncthreads();
   }
+
+  // value cosine with the best slot, partial over this wave's feature half (from registers)
+  float dvv = 0.f, vv = 0.f, aa = 0.f;
+  if (steady) {
+    const int bsr = bs < 0 ? 0 : bs;
+#pragma unroll
+    for (int i = 0; i < HDB; ++i)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        float y[4];
+        ld4(&sm.av[bsr * Sm::KS + 32 * (half * HDB + i) + 8 * g + 4 * h], y);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float x = td.vx[i][g].get(q);
+          dvv += x * y[q];
+          vv += x * x;
+          aa += y[q] * y[q];
+        }
+      }
+    dvv += xor32(dvv);
+    vv += xor32(vv);
+    aa += xor32(aa);
+  }
+  if constexpr (SPLIT) sync_lds();
 
   // v_hat^T[d][tok] = av^T . P^T on this wave's feature half; partial rel_err sums
   float e2 = 0.f, v2 = 0.f;
@@ -414,9 +509,10 @@ __device__ void score_tile(DecSmem<T, HD>& sm, const T* kread, const T* kr, cons
     f32x16 vh = zero16();
     const int d = 32 * db + n;
     if constexpr (St<T>::is_bf16) {
-      const uint16_t* pp = sm.u.sc.x[0].p[pair] + n * Sm::PS;
+      const uint16_t* pp = sm.u.sc.p[pair] + n * Sm::PS;
 #pragma unroll
       for (int kc = 0; kc < 8; ++kc) {
+        if (kc == 2 || kc == 4 || kc == 6) __builtin_amdgcn_sched_barrier(0);   // bound the gathers in flight
         // slots 16*kc + 8*(q>>2) + 4*h + (q&3): own half from registers, the other from LDS
         u16x8 av8, p8;
         const int mb = kc >> 1;
@@ -449,7 +545,7 @@ __device__ void score_tile(DecSmem<T, HD>& sm, const T* kread, const T* kr, cons
     for (int g = 0; g < 4; ++g)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const float x = vx[i][g].get(q);
+        const float x = td.vx[i][g].get(q);
         const float dv = x - St<T>::rnd(vh[4 * g + q]);
         e2 += dv * dv;
         v2 += x * x;
@@ -457,103 +553,80 @@ __device__ void score_tile(DecSmem<T, HD>& sm, const T* kread, const T* kr, cons
   }
   e2 += xor32(e2);
   v2 += xor32(v2);
-
-  // cos^T[slot][tok] = ak . kr^T / (|ak| |kr|) on this wave's half of the slots; argmax on
-  // integer keys: slots ascend along the scan, so a strictly larger key keeps the lower index
-  // on ties, and NaN (largest key) wins as torch.max does
-  Frag<T, HD> fk;
-  fk.load(kr, tok, l, lane);
-  float kk = fk.sumsq();
-  kk += xor32(kk);
-  const float inv_nk = 1.0f / fmaxf(sqrtf(kk), 1e-12f);
-  uint32_t bkey = 0;
-  float bv = 0.f;
-  int bs = -1;
-#pragma unroll
-  for (int m2 = 0; m2 < 2; ++m2) {
-    const int mb = 2 * half + m2;
-    f32x16 c = zero16();
-    mm_rows_frag<HD>(c, sm.ak, Sm::KS, 32 * mb, fk, lane);
-#pragma unroll
-    for (int r4 = 0; r4 < 4; ++r4) {
-      const int s0 = 32 * mb + 8 * r4 + 4 * h;
-      const float4 n4 = *reinterpret_cast<const float4*>(&sm.inv_nak[s0]);
-      const float nn[4] = {n4.x, n4.y, n4.z, n4.w};
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        float cv = c[4 * r4 + q] * (nn[q] * inv_nk);
-        if (!steady && !sm.act[s0 + q]) cv = 0.f;
-        const uint32_t k = ord_key(cv + 0.0f);   // -0 ranks with +0, as in a float compare
-        if (bs < 0 || k > bkey) { bkey = k; bv = cv; bs = s0 + q; }
-      }
-    }
-  }
-  {
-    const uint32_t ok = (uint32_t)__shfl_xor((int)bkey, 32, 64);
-    const float ov = xor32(bv);
-    const int os = xor32i(bs);
-    if (ok > bkey || (ok == bkey && os < bs)) { bkey = ok; bv = ov; bs = os; }
-  }
   if (h == 0 && in) {
-    sm.u.sc.e2[half][tok] = e2;
-    sm.u.sc.v2[half][tok] = v2;
-    sm.u.sc.bv[half][tok] = bv;
-    sm.u.sc.bs[half][tok] = bs;
+    const int pt = tok & 127;   // index within the round
+    sm.u.sc.e2[half][pt] = e2;
+    sm.u.sc.v2[half][pt] = v2;
+    sm.u.sc.dv[half][pt] = dvv;
+    sm.u.sc.vv[half][pt] = vv;
+    sm.u.sc.aa[half][pt] = aa;
+    sm.u.sc.bv[half][pt] = bv;
+    sm.u.sc.bs[half][pt] = bs;
   }
 }
 
-// Combine the two halves per token (two threads per token): rel_err, best slot, score,
-// value cosine with the best slot (steady), merge flag.  Returns this token's merge flag
-// on the token's first thread.
+// Combine the two halves for token tok of the current round (one thread per token):
+// rel_err, score, value cosine with the best slot (steady), merge flag; the decision log
+// gets the best cosine and value cosine here.  Returns the token's merge flag.
 template <typename T, int HD>
-__device__ bool score_combine(DecSmem<T, HD>& sm, const T* v, int l, bool steady, int tid) {
-  const int tok = tid >> 1, part = tid & 1;
-  const bool in = tok < l;
-  float rel = 0.f, bv = 0.f, score = 0.f;
-  int bs = 0;
-  if (in) {
-    const float e2 = sm.u.sc.e2[0][tok] + sm.u.sc.e2[1][tok];
-    const float v2 = sm.u.sc.v2[0][tok] + sm.u.sc.v2[1][tok];
-    rel = sqrtf(e2) / (sqrtf(v2) + 1e-6f);
-    bv = sm.u.sc.bv[0][tok];
-    bs = sm.u.sc.bs[0][tok];
-    const float b1 = sm.u.sc.bv[1][tok];
-    const int s1 = sm.u.sc.bs[1][tok];
-    if (ranks_before_desc(b1, s1, bv, bs)) { bv = b1; bs = s1; }
-    score = rel * (1.0f - fminf(fmaxf(bv, 0.0f), 1.0f));
-  }
+__device__ bool score_combine(DecSmem<T, HD>& sm, int l, bool steady, int tok, float* log) {
+  if (tok >= l) return false;
+  const int pt = tok & 127;
+  const float e2 = sm.u.sc.e2[0][pt] + sm.u.sc.e2[1][pt];
+  const float v2 = sm.u.sc.v2[0][pt] + sm.u.sc.v2[1][pt];
+  const float rel = sqrtf(e2) / (sqrtf(v2) + 1e-6f);
+  const float bv = sm.u.sc.bv[0][pt];
+  const int bs = sm.u.sc.bs[0][pt];
+  const float score = rel * (1.0f - fminf(fmaxf(bv, 0.0f), 1.0f));
   float simv = 0.f;
   if (steady) {
-    float dvv = 0.f, vv = 0.f, aa = 0.f;
-    if (in) {
-#pragma unroll
-      for (int d = part * (HD / 2); d < (part + 1) * (HD / 2); d += 8) {
-        float x[8], y[8];
-        ld8(v + (long long)tok * HD + d, x);
-        ld8(&sm.av[bs * sm.KS + d], y);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          dvv += x[i] * y[i];
-          vv += x[i] * x[i];
-          aa += y[i] * y[i];
-        }
-      }
-    }
-    dvv += __shfl_xor(dvv, 1, 64);
-    vv += __shfl_xor(vv, 1, 64);
-    aa += __shfl_xor(aa, 1, 64);
+    const float dvv = sm.u.sc.dv[0][pt] + sm.u.sc.dv[1][pt];
+    const float vv = sm.u.sc.vv[0][pt] + sm.u.sc.vv[1][pt];
+    const float aa = sm.u.sc.aa[0][pt] + sm.u.sc.aa[1][pt];
     simv = dvv / (fmaxf(sqrtf(vv), 1e-8f) * fmaxf(sqrtf(aa), 1e-8f));
   }
-  const bool merge = in && steady && bv >= SIM_K && simv >= SIM_V;
-  if (part == 0 && in) {
-    sm.rel[tok] = rel;
-    sm.score[tok] = score;
-    sm.best[tok] = bv;
-    sm.simv[tok] = simv;
-    sm.slot[tok] = bs;
-    sm.flags[tok] = merge ? F_MERGE : 0;
+  const bool merge = steady && bv >= SIM_K && simv >= SIM_V;
+  sm.rel[tok] = rel;
+  sm.score[tok] = score;
+  sm.slot[tok] = bs;
+  sm.flags[tok] = merge ? F_MERGE : 0;
+  if (log) {
+    log[B3_LOG_BEST * B3_LOG_COLS + tok] = steady ? bv : 0.f;
+    log[B3_LOG_SIMV * B3_LOG_COLS + tok] = simv;
   }
-  return merge && part == 0;
+  return merge;
+}
+
+// Eviction candidate value of token j: its score, or -1e9 when it merged.
+template <typename T, int HD>
+__device__ __forceinline__ float cand_value(const DecSmem<T, HD>& sm, int j) {
+  return (sm.flags[j] & F_MERGE) ? -1e9f : sm.score[j];
+}
+
+// All tiles of a step in rounds of 128 tokens (4 wave pairs x 32), each round followed by
+// the combine pass of its tokens.  `td` holds the first round's tile data on entry when
+// `ready`.  Returns this thread's merge flag; the caller's barrier publishes the results.
+template <typename T, int HD>
+__device__ bool score_phase(DecSmem<T, HD>& sm, const T* kread, TileIn<T, HD>& td, bool ready, const T* kr,
+                            const T* kp, const T* v, int l, bool steady, float scale, int wave, int lane, int tid,
+                            float* log) {
+  const int pair = wave >> 1, half = wave & 1;
+  if (l <= 128) {   // one round: the tile data may already be in registers
+    if (!ready) td.load(kp, kr, v, 32 * pair, l, half, lane);
+    score_tile<T, HD>(sm, kread, td, kr, 32 * pair, l, steady, scale, pair, half, lane);
+    sync_lds();
+    return tid < 128 && score_combine<T, HD>(sm, l, steady, tid, log);
+  }
+  bool merge = false;
+  for (int r = 0; r < (l + 127) / 128; ++r) {
+    const int t0 = 128 * r + 32 * pair;
+    TileIn<T, HD> tr;
+    tr.load(kp, kr, v, t0, l, half, lane);
+    score_tile<T, HD>(sm, kread, tr, kr, t0, l, steady, scale, pair, half, lane);
+    sync_lds();
+    if (tid < 128) merge |= score_combine<T, HD>(sm, l, steady, 128 * r + tid, log);
+  }
+  return merge;
 }
 
 // ----------------------------------------------------------------- decide_kernel
@@ -562,7 +635,8 @@ template <typename T, int HD>
 __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
   __shared__ DecSmem<T, HD> sm;
   const int bh = blockIdx.x;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid0 = threadIdx.x;
+  const int tid = tid0;
   const int hkv = bh % a.HKV;
   const float kap = a.kappa[hkv];
   const float scale = 1.0f / sqrtf((float)HD);
@@ -592,13 +666,33 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
     sm.dirty[tid] = 1;
   }
   if (tid < HD / 2) sm.invf[tid] = a.inv_freq[tid];
-  __syncthreads();
+  sync_lds();
   int nf = a.n_filled;
   rope_dirty<T, HD>(sm, kread_g, tid);   // every slot, empty ones included (their rows stay zero)
   __threadfence_block();
   __syncthreads();
 
+  // tile data of the next step's first round, loaded while the current step finishes (bf16)
+  TileIn<T, HD> td;
+  bool td_ready = false;
+  constexpr bool PREFETCH = St<T>::is_bf16;
+  auto prefetch = [&](int step, int wave, int lane) {
+    if constexpr (PREFETCH) {
+      if (step + 1 < a.n_steps) {
+        const long long nb = (long long)bh * a.tok_bh_stride + (long long)step_off(a, step + 1) * HD;
+        td.load(reinterpret_cast<const T*>(a.kp) + nb, reinterpret_cast<const T*>(a.kr) + nb,
+                reinterpret_cast<const T*>(a.v) + nb, 32 * (wave >> 1), step_len(a, step + 1), wave & 1, lane);
+        td_ready = true;
+      }
+    }
+  };
+
   for (int step = 0; step < a.n_steps; ++step) {
+    // Thread indices re-derived from an opaque copy each step: the lane-dependent LDS
+    // addresses are then recomputed per step instead of hoisted out of the loop and spilled.
+    int tid = tid0;
+    asm volatile("" : "+v"(tid));
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int off = step_off(a, step), l = step_len(a, step);
     const long long tb = (long long)bh * a.tok_bh_stride + (long long)off * HD;
     const T* kr = reinterpret_cast<const T*>(a.kr) + tb;
@@ -611,6 +705,7 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
     float* log = a.log ? a.log + ((long long)step * BH + bh) * (B3_LOG_ROWS * B3_LOG_COLS) : nullptr;
     float* w_out = w_all + ((long long)step * BH + bh) * LMAX;
 
+    if (tid == 0) sm.any_merge = 0;
     if (tid < S) {
       sm.util[tid] = mul_rn(sm.util[tid], UTIL_DECAY);
       const float lm = logf(fmaxf(sm.mass[tid], 1.0f));
@@ -618,51 +713,55 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
       sm.dirty[tid] = 0;
     }
     slot_norms<T, HD>(sm, tid);
-    __syncthreads();
+    sync_lds();
+
+    // ---------------- retrieval scores: first fill ranks by value variance; later fills and
+    // steady steps read the slots
+    bool has = false;
+    if (nf == 0) {
+      // score = unbiased variance of normalize(v)
+      const int j = tid;
+      if (j < l) {
+        const T* vr = v + (long long)j * HD;
+        float ss = 0.f;
+        for (int d = 0; d < HD; d += 8) {
+          float x[8];
+          ld8(vr + d, x);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) ss += x[i] * x[i];
+        }
+        const float nrm = fmaxf(sqrtf(ss), 1e-12f);
+        float mean = 0.f;
+        for (int d = 0; d < HD; d += 8) {
+          float x[8];
+          ld8(vr + d, x);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) mean += div_rn(x[i], nrm);
+        }
+        mean /= (float)HD;
+        float var = 0.f;
+        for (int d = 0; d < HD; d += 8) {
+          float x[8];
+          ld8(vr + d, x);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) { const float u = div_rn(x[i], nrm) - mean; var += u * u; }
+        }
+        sm.score[j] = var / (float)(HD - 1);
+        sm.rel[j] = 0.15f;
+      }
+    } else {
+      has = score_phase<T, HD>(sm, kread, td, td_ready, kr, kp, v, l, steady, scale, wave, lane, tid, log);
+    }
+    td_ready = false;
+    prefetch(step, wave, lane);
+    if (has) sm.any_merge = 1;
+    sync_lds();
 
     if (!steady) {
       // ---------------- fill
       const int m = min(S - nf, l);
-      if (nf == 0) {
-        // score = unbiased variance of normalize(v)
-        const int j = tid;
-        if (j < l) {
-          const T* vr = v + (long long)j * HD;
-          float ss = 0.f;
-          for (int d = 0; d < HD; d += 8) {
-            float x[8];
-            ld8(vr + d, x);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) ss += x[i] * x[i];
-          }
-          const float nrm = fmaxf(sqrtf(ss), 1e-12f);
-          float mean = 0.f;
-          for (int d = 0; d < HD; d += 8) {
-            float x[8];
-            ld8(vr + d, x);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) mean += div_rn(x[i], nrm);
-          }
-          mean /= (float)HD;
-          float var = 0.f;
-          for (int d = 0; d < HD; d += 8) {
-            float x[8];
-            ld8(vr + d, x);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) { const float u = div_rn(x[i], nrm) - mean; var += u * u; }
-          }
-          sm.score[j] = var / (float)(HD - 1);
-          sm.rel[j] = 0.15f;
-        }
-      } else {
-        for (int t = wave >> 1; t < ((nT + 3) & ~3); t += DWAVES / 2)
-          score_tile<T, HD>(sm, kread, kr, kp, v, 32 * t, l, false, scale, wave >> 1, wave & 1, lane);
-        __syncthreads();
-        score_combine<T, HD>(sm, v, l, false, tid);
-      }
-      __syncthreads();
       if (tid < l) sm.u.ok.a[tid] = desc_key(sm.score[tid], tid);
-      __syncthreads();
+      sync_lds();
       {
         // two threads per token, each counting half of the keys
         const int j = tid >> 1, part = tid & 1, mid = (l >> 1) & ~1;
@@ -674,7 +773,7 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
           sm.sk_a[r] = sm.score[j];
         }
       }
-      __syncthreads();
+      sync_lds();
       // slots nf + i <- token si_a[i]
       for (int it = tid; it < m * (HD / 8); it += DT) {
         const int i = it / (HD / 8), d8 = (it % (HD / 8)) * 8;
@@ -699,15 +798,9 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
         }
       }
       nf += m;
-      __syncthreads();
+      sync_lds();
     } else {
-      // ---------------- steady: score
-      for (int t = wave >> 1; t < ((nT + 3) & ~3); t += DWAVES / 2)
-        score_tile<T, HD>(sm, kread, kr, kp, v, 32 * t, l, true, scale, wave >> 1, wave & 1, lane);
-      __syncthreads();
-      const bool has = score_combine<T, HD>(sm, v, l, true, tid);
-      const int any_merge = __syncthreads_or(has);
-
+      const int any_merge = sm.any_merge;
       // ---------------- merge: per-slot mass-weighted means, tokens in ascending order
       if (any_merge) {
         if (tid < S) {
@@ -718,7 +811,7 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
           sm.u.mg.cnt[tid] = c;
           sm.u.mg.psum[tid] = ps;
         }
-        __syncthreads();
+        sync_lds();
         if (tid == 0) {
           int o = 0, nh = 0;
           for (int s = 0; s < S; ++s) {
@@ -728,7 +821,7 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
           }
           sm.u.mg.nhit = nh;
         }
-        __syncthreads();
+        sync_lds();
         const int nhit = sm.u.mg.nhit;
         if (tid < l && (sm.flags[tid] & F_MERGE)) {
           const int s = sm.slot[tid];
@@ -736,7 +829,7 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
           for (int j = 0; j < tid; ++j) rank += ((sm.flags[j] & F_MERGE) && sm.slot[j] == s) ? 1 : 0;
           sm.u.mg.mlist[sm.u.mg.off[s] + rank] = tid;
         }
-        __syncthreads();
+        sync_lds();
         for (int it = tid; it < nhit * HD; it += DT) {
           const int s = sm.u.mg.hits[it / HD], d = it % HD;
           float ks = 0.f, vs = 0.f;
@@ -749,16 +842,16 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
           sm.ak[s * KS + d] = St<T>::from_f(div_rn(add_rn(mul_rn(m0, St<T>::to_f(sm.ak[s * KS + d])), ks), nm));
           sm.av[s * KS + d] = St<T>::from_f(div_rn(add_rn(mul_rn(m0, St<T>::to_f(sm.av[s * KS + d])), vs), nm));
         }
-        __syncthreads();
+        sync_lds();
         if (tid < S && sm.u.mg.cnt[tid] > 0) {
           const float m0 = sm.mass[tid], nm = add_rn(m0, (float)sm.u.mg.cnt[tid]);
           sm.pm[tid] = div_rn(add_rn(mul_rn(m0, sm.pm[tid]), sm.u.mg.psum[tid]), nm);
           sm.mass[tid] = nm;
           sm.dirty[tid] = 1;
         }
-        __syncthreads();
+        sync_lds();
         slot_norms<T, HD>(sm, tid);
-        __syncthreads();
+        sync_lds();
       }
 
       // ---------------- keep score: util * (1 - clamp(max_{s'!=s} cos(ak_s, ak_s'), 0, .98))
@@ -792,8 +885,8 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
           sm.u.kp.nan[rh][col] = has_nan ? 1 : 0;
         }
       }
-      __syncthreads();
-      float keep_v = 0.f, ck_v = 0.f;
+      sync_lds();
+      float keep_v = 0.f, ck_v = 0.f;   // keep value of slot tid, candidate value of token tid
       if (tid < S) {
         float mx = fmaxf(sm.u.kp.mx[0][tid], sm.u.kp.mx[1][tid]);
         if (sm.u.kp.nan[0][tid] | sm.u.kp.nan[1][tid]) mx = NAN;
@@ -801,13 +894,12 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
         sm.keep[tid] = keep_v;
       }
       if (tid < l) {
-        ck_v = (sm.flags[tid] & F_MERGE) ? -1e9f : sm.score[tid];
-        sm.ck[tid] = ck_v;
+        ck_v = cand_value(sm, tid);
       }
-      __syncthreads();
+      sync_lds();
       if (tid < l) sm.u.ok.a[tid] = desc_key(ck_v, tid);
       if (tid < S) sm.u.ok.b[tid] = asc_key(keep_v, tid);
-      __syncthreads();
+      sync_lds();
       // ---------------- orderings: best free tokens (desc) against least useful slots (asc)
       {
         // l + S items, two threads each, each counting half of the keys
@@ -824,7 +916,7 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
           r += __shfl_xor(r, 1, 64);
           if (part == 0) {
             if (it < l) {
-              sm.sk_a[r] = sm.ck[it];
+              sm.sk_a[r] = cand_value(sm, it);
               sm.si_a[r] = it;
             } else if (it < l + S) {
               sm.sk_b[r] = sm.keep[it - l];
@@ -833,7 +925,7 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
           }
         }
       }
-      __syncthreads();
+      sync_lds();
       const int kc = min(l, S);
       // win_i = top_i > bot_i and top_i > -1e8 ; token top_i replaces slot bot_i
       if (tid < kc) {
@@ -857,21 +949,23 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
           if (kp_copy) copy8(kread_w + s * krs + d8, kp + (long long)j * HD + d8);
         }
       }
-      __syncthreads();
+      sync_lds();
       if (tid < l) {
         const int f = sm.flags[tid];
         const bool dl = !(f & F_MERGE) && !(f & F_INS);
         if (dl) sm.flags[tid] = f | F_DELTA;
         w_out[tid] = dl ? beta[tid] : 0.f;
       }
-      __syncthreads();
+      sync_lds();
       if (log) {
         for (int j = tid; j < B3_LOG_COLS; j += DT) {
           const bool in = j < l;
           log[B3_LOG_REL * B3_LOG_COLS + j] = in ? sm.rel[j] : 0.f;
           log[B3_LOG_SCORE * B3_LOG_COLS + j] = in ? sm.score[j] : 0.f;
-          log[B3_LOG_BEST * B3_LOG_COLS + j] = in ? sm.best[j] : 0.f;
-          log[B3_LOG_SIMV * B3_LOG_COLS + j] = in ? sm.simv[j] : 0.f;
+          if (!in) {
+            log[B3_LOG_BEST * B3_LOG_COLS + j] = 0.f;
+            log[B3_LOG_SIMV * B3_LOG_COLS + j] = 0.f;
+          }
           log[B3_LOG_SLOT * B3_LOG_COLS + j] = in ? (float)sm.slot[j] : -1.f;
           log[B3_LOG_MERGE * B3_LOG_COLS + j] = in ? (float)((sm.flags[j] & F_MERGE) != 0) : 0.f;
           log[B3_LOG_DELTA * B3_LOG_COLS + j] = in ? (float)((sm.flags[j] & F_DELTA) != 0) : 0.f;
@@ -888,8 +982,12 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
 
     // ---------------- per-step outputs; the roped keys also serve the next step
     rope_dirty<T, HD>(sm, kread_g, tid);
-    __threadfence_block();
-    __syncthreads();
+    if constexpr (DecSmem<T, HD>::KREAD_LDS) {
+      sync_lds();
+    } else {
+      __threadfence_block();   // roped keys in the workspace are read by other threads
+      __syncthreads();
+    }
     if (a.snap_k) {
       T* kd = reinterpret_cast<T*>(a.snap_k) + (step * BH + bh) * S * HD;
       for (int it = tid; it < S * (HD / 8); it += DT) {

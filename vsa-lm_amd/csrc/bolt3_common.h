@@ -88,6 +88,13 @@ __device__ __forceinline__ void split8(const float* v, u16x8& hi, u16x8& lo) {
   }
 }
 
+// ---------------------------------------------------------------- barriers
+
+// Workgroup barrier for data exchanged through LDS only: waits for this wave's LDS
+// operations, not for its outstanding global loads (which __syncthreads' workgroup fence
+// would drain), so register prefetches stay in flight across it.
+__device__ __forceinline__ void sync_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // ---------------------------------------------------------------- reductions
 
 __device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32, 64); }

@@ -1108,9 +1108,43 @@ struct MSmem {
   float bsafe[LMAX], inv[LMAX];
 };
 
+// Global inputs of one step for one thread of mres_kernel when the step has at most
+// MSmem::KC tokens: the token tile of wave w (tokens 32w..32w+31: key fragment, values of
+// the column block, 1/|k| and bsafe) and one 8 x 8 block of keys for the K^T staging.
+template <typename T, int HD>
+struct MStepIn {
+  Frag<T, HD> fj;
+  V4<T> vx[4];
+  float inj, bj;
+  T kb[8][8];
+  __device__ __forceinline__ void load(const T* kr, const T* v, const float* inv, const float* bsafe, int l, int db,
+                                       int tid, int lane, int wave) {
+    const int n = lane & 31, h = lane >> 5, j = 32 * wave + n;
+    fj.load(kr, j, l, lane);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) vx[g].load(v + (long long)j * HD + 32 * db + 8 * g + 4 * h, j < l);
+    inj = j < l ? inv[j] : 0.f;
+    bj = j < l ? bsafe[j] : 0.f;
+    constexpr int KC = 128;
+    const int jb = (tid % (KC / 8)) * 8, c8 = (tid / (KC / 8)) * 8;
+    if (tid < (KC / 8) * (HD / 8)) {
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        if (jb + r < l) copy8(kb[r], kr + (long long)(jb + r) * HD + c8);
+        else {
+#pragma unroll
+          for (int q = 0; q < 8; ++q) kb[r][q] = St<T>::from_f(0.f);
+        }
+      }
+    }
+  }
+};
+
 // Columns [32*db, 32*db + 32) of M for row bh = blockIdx.x / (HD/32):
 //   E^T[d][j] = (v[j][d] - (K M)[j][d] / |k_j|) * bsafe_j / |k_j|
 //   M^T[d][c] <- gamma * M^T[d][c] + sum_j E^T[d][j] k[j][c]
+// Steps of at most 128 tokens (every forward and decoder step) keep the next step's inputs
+// in registers across LDS-only barriers; longer steps load per chunk.
 template <typename T, int HD>
 __global__ void __launch_bounds__(MT) mres_kernel(b3_chain_args a) {
   __shared__ MSmem<T, HD> sm;
@@ -1126,6 +1160,8 @@ __global__ void __launch_bounds__(MT) mres_kernel(b3_chain_args a) {
   const long long plane = (long long)a.n_steps * BH * LMAX;
   const float* bsafe_all = reinterpret_cast<const float*>(ws) + plane;
   const float* inv_all = reinterpret_cast<const float*>(ws) + 2 * plane;
+  auto tok_base = [&](int step) { return (long long)bh * a.tok_bh_stride + (long long)step_off(a, step) * HD; };
+  auto row_base = [&](int step) { return ((long long)step * BH + bh) * LMAX; };
 
   // M^T block: mt[dd][c] = M[c][32*db + dd]
   for (int it = tid; it < HD * 32; it += MT) {
@@ -1140,116 +1176,192 @@ __global__ void __launch_bounds__(MT) mres_kernel(b3_chain_args a) {
   }
   __syncthreads();
 
+  // steady steps and whether their inputs are prefetched
   int nf = a.n_filled;
+  int first_steady = -1;
+  {
+    int f = nf;
+    for (int s = 0; s < a.n_steps && first_steady < 0; ++s) {
+      if (f >= S) first_steady = s;
+      else f += min(S - f, step_len(a, s));
+    }
+  }
+  MStepIn<T, HD> in;
+  bool in_ready = false;
+  auto fetch = [&](int step) {   // step must be steady with at most KC tokens; bf16 only (registers)
+    if constexpr (St<T>::is_bf16) {
+      const long long tb = tok_base(step), row = row_base(step);
+      in.load(reinterpret_cast<const T*>(a.kr) + tb, reinterpret_cast<const T*>(a.v) + tb, inv_all + row,
+              bsafe_all + row, step_len(a, step), db, tid, lane, wave);
+      in_ready = true;
+    }
+  };
+  if (first_steady >= 0 && step_len(a, first_steady) <= Sm::KC) fetch(first_steady);
+
   for (int step = 0; step < a.n_steps; ++step) {
     const int l = step_len(a, step);
     float* snap = a.snap_m ? a.snap_m + (step * BH + bh) * HD * HD : nullptr;
     if (nf >= S) {
-      const long long tb = (long long)bh * a.tok_bh_stride + (long long)step_off(a, step) * HD;
+      const long long tb = tok_base(step);
       const T* kr = reinterpret_cast<const T*>(a.kr) + tb;
       const T* v = reinterpret_cast<const T*>(a.v) + tb;
-      const long long row = ((long long)step * BH + bh) * LMAX;
-      if (tid < l) {
-        sm.bsafe[tid] = bsafe_all[row + tid];
-        sm.inv[tid] = inv_all[row + tid];
-      }
-      __syncthreads();
-      // E^T tile per 32 tokens: prediction from the old M, error scaled by bsafe / |k|; the
-      // columns up to the end of the last staging chunk are written (zero past l)
-      const int nT = ((l + Sm::KC - 1) / Sm::KC) * (Sm::KC / 32);
-      for (int t = wave; t < nT; t += MWAVES) {
-        const int j = 32 * t + n;
-        Frag<T, HD> fj;
-        fj.load(kr, j, l, lane);
-        float vx[4][4];
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int d0 = 32 * db + 8 * g + 4 * h;
-          if (j < l) ld4(v + (long long)j * HD + d0, vx[g]);
-          else {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) vx[g][q] = 0.f;
-          }
-        }
-        f32x16 acc = zero16();
-        if constexpr (St<T>::is_bf16) {
-#pragma unroll
-          for (int ks = 0; ks < HD / 16; ++ks) {
-            const u16x8 hi = *reinterpret_cast<const u16x8*>(&sm.mhi[n * Sm::BS + 16 * ks + 8 * h]);
-            const u16x8 lo = *reinterpret_cast<const u16x8*>(&sm.mlo[n * Sm::BS + 16 * ks + 8 * h]);
-            mma_bf16(acc, hi, fj.v[ks]);
-            mma_bf16(acc, lo, fj.v[ks]);
-          }
-        } else {
-#pragma unroll 8
-          for (int ks = 0; ks < HD / 2; ++ks) mma_f32(acc, sm.mt[n * Sm::MS + 2 * ks + h], fj.v[ks]);
-        }
-        const float inj = j < l ? sm.inv[j] : 0.f;
-        const float bj = j < l ? sm.bsafe[j] : 0.f;
-#pragma unroll
-        for (int g = 0; g < 4; ++g)
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const int dd = 8 * g + 4 * h + q;
-            const float e = ((vx[g][q] - acc[4 * g + q] * inj) * bj) * inj;
-            if constexpr (St<T>::is_bf16) {
-              const uint16_t hb = f2bf(e);
-              sm.ert[dd * Sm::ES + j] = hb;
-              sm.erl[dd * Sm::ES + j] = f2bf(e - bf2f(hb));
-            } else {
-              sm.ert[dd * Sm::ES + j] = e;
-            }
-          }
-      }
-      // upd[c][d] = sum_j K^T[c][j] E^T[d][j], K^T staged per chunk of Sm::KC tokens
       f32x16 upd = zero16();
       const int cb = wave;
-      for (int j0 = 0; j0 < l; j0 += Sm::KC) {
-        const int jn = min(Sm::KC, l - j0);
-        // 8 tokens x 8 channels per item: row reads, transposed row writes
-        for (int it = tid; it < (Sm::KC / 8) * (HD / 8); it += MT) {
-          const int jb = (it % (Sm::KC / 8)) * 8, c8 = (it / (Sm::KC / 8)) * 8;
-          float x[8][8];
+      if (St<T>::is_bf16 && l <= Sm::KC && in_ready) {
+        // ---- E^T for this wave's tile; K^T staging from registers
+        {
+          const int j = 32 * wave + n;
+          f32x16 acc = zero16();
+          if constexpr (St<T>::is_bf16) {
 #pragma unroll
-          for (int r = 0; r < 8; ++r) {
-            if (jb + r < jn) ld8(kr + (long long)(j0 + jb + r) * HD + c8, x[r]);
-            else {
-#pragma unroll
-              for (int q = 0; q < 8; ++q) x[r][q] = 0.f;
+            for (int ks = 0; ks < HD / 16; ++ks) {
+              const u16x8 hi = *reinterpret_cast<const u16x8*>(&sm.mhi[n * Sm::BS + 16 * ks + 8 * h]);
+              const u16x8 lo = *reinterpret_cast<const u16x8*>(&sm.mlo[n * Sm::BS + 16 * ks + 8 * h]);
+              mma_bf16(acc, hi, in.fj.v[ks]);
+              mma_bf16(acc, lo, in.fj.v[ks]);
             }
+          } else {
+#pragma unroll 8
+            for (int ks = 0; ks < HD / 2; ++ks) mma_f32(acc, sm.mt[n * Sm::MS + 2 * ks + h], in.fj.v[ks]);
           }
 #pragma unroll
-          for (int q = 0; q < 8; ++q) {
-            if constexpr (St<T>::is_bf16) {
-              u16x8 col;
+          for (int g = 0; g < 4; ++g)
 #pragma unroll
-              for (int r = 0; r < 8; ++r) col[r] = f2bf(x[r][q]);
-              *reinterpret_cast<u16x8*>(&sm.krt[(c8 + q) * Sm::KTS + jb]) = col;
-            } else {
+            for (int q = 0; q < 4; ++q) {
+              const int dd = 8 * g + 4 * h + q;
+              const float e = ((in.vx[g].get(q) - acc[4 * g + q] * in.inj) * in.bj) * in.inj;
+              if constexpr (St<T>::is_bf16) {
+                const uint16_t hb = f2bf(e);
+                sm.ert[dd * Sm::ES + j] = hb;
+                sm.erl[dd * Sm::ES + j] = f2bf(e - bf2f(hb));
+              } else {
+                sm.ert[dd * Sm::ES + j] = e;
+              }
+            }
+          if (tid < (Sm::KC / 8) * (HD / 8)) {
+            const int jb = (tid % (Sm::KC / 8)) * 8, c8 = (tid / (Sm::KC / 8)) * 8;
 #pragma unroll
-              for (int r = 0; r < 8; ++r) sm.krt[(c8 + q) * Sm::KTS + jb + r] = x[r][q];
+            for (int q = 0; q < 8; ++q) {
+              if constexpr (St<T>::is_bf16) {
+                u16x8 col;
+#pragma unroll
+                for (int r = 0; r < 8; ++r) col[r] = in.kb[r][q];
+                *reinterpret_cast<u16x8*>(&sm.krt[(c8 + q) * Sm::KTS + jb]) = col;
+              } else {
+#pragma unroll
+                for (int r = 0; r < 8; ++r) sm.krt[(c8 + q) * Sm::KTS + jb + r] = in.kb[r][q];
+              }
             }
           }
         }
-        __syncthreads();
+        in_ready = false;
+        // the next steady step's inputs load while this one finishes
+        if (step + 1 < a.n_steps && step_len(a, step + 1) <= Sm::KC) fetch(step + 1);
+        sync_lds();
         if (cb < NCB) {
           const int c = 32 * cb + n;
           if constexpr (St<T>::is_bf16) {
 #pragma unroll
             for (int kc = 0; kc < Sm::KC / 16; ++kc) {
               const u16x8 ka = *reinterpret_cast<const u16x8*>(&sm.krt[c * Sm::KTS + 16 * kc + 8 * h]);
-              const u16x8 eh = *reinterpret_cast<const u16x8*>(&sm.ert[n * Sm::ES + j0 + 16 * kc + 8 * h]);
-              const u16x8 el = *reinterpret_cast<const u16x8*>(&sm.erl[n * Sm::ES + j0 + 16 * kc + 8 * h]);
+              const u16x8 eh = *reinterpret_cast<const u16x8*>(&sm.ert[n * Sm::ES + 16 * kc + 8 * h]);
+              const u16x8 el = *reinterpret_cast<const u16x8*>(&sm.erl[n * Sm::ES + 16 * kc + 8 * h]);
               mma_bf16(upd, ka, eh);
               mma_bf16(upd, ka, el);
             }
           } else {
 #pragma unroll 8
             for (int kc = 0; kc < Sm::KC / 2; ++kc)
-              mma_f32(upd, sm.krt[c * Sm::KTS + 2 * kc + h], sm.ert[n * Sm::ES + j0 + 2 * kc + h]);
+              mma_f32(upd, sm.krt[c * Sm::KTS + 2 * kc + h], sm.ert[n * Sm::ES + 2 * kc + h]);
           }
         }
-        __syncthreads();
+      } else {
+        // ---- general path (steps longer than KC tokens)
+        const long long row = row_base(step);
+        const int nT = ((l + Sm::KC - 1) / Sm::KC) * (Sm::KC / 32);
+        for (int t = wave; t < nT; t += MWAVES) {
+          const int j = 32 * t + n;
+          Frag<T, HD> fj;
+          fj.load(kr, j, l, lane);
+          V4<T> vx[4];
+#pragma unroll
+          for (int g = 0; g < 4; ++g) vx[g].load(v + (long long)j * HD + 32 * db + 8 * g + 4 * h, j < l);
+          f32x16 acc = zero16();
+          if constexpr (St<T>::is_bf16) {
+#pragma unroll
+            for (int ks = 0; ks < HD / 16; ++ks) {
+              const u16x8 hi = *reinterpret_cast<const u16x8*>(&sm.mhi[n * Sm::BS + 16 * ks + 8 * h]);
+              const u16x8 lo = *reinterpret_cast<const u16x8*>(&sm.mlo[n * Sm::BS + 16 * ks + 8 * h]);
+              mma_bf16(acc, hi, fj.v[ks]);
+              mma_bf16(acc, lo, fj.v[ks]);
+            }
+          } else {
+#pragma unroll 8
+            for (int ks = 0; ks < HD / 2; ++ks) mma_f32(acc, sm.mt[n * Sm::MS + 2 * ks + h], fj.v[ks]);
+          }
+          const float inj = j < l ? inv_all[row + j] : 0.f;
+          const float bj = j < l ? bsafe_all[row + j] : 0.f;
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const int dd = 8 * g + 4 * h + q;
+              const float e = ((vx[g].get(q) - acc[4 * g + q] * inj) * bj) * inj;
+              if constexpr (St<T>::is_bf16) {
+                const uint16_t hb = f2bf(e);
+                sm.ert[dd * Sm::ES + j] = hb;
+                sm.erl[dd * Sm::ES + j] = f2bf(e - bf2f(hb));
+              } else {
+                sm.ert[dd * Sm::ES + j] = e;
+              }
+            }
+        }
+        for (int j0 = 0; j0 < l; j0 += Sm::KC) {
+          const int jn = min(Sm::KC, l - j0);
+          for (int it = tid; it < (Sm::KC / 8) * (HD / 8); it += MT) {
+            const int jb = (it % (Sm::KC / 8)) * 8, c8 = (it / (Sm::KC / 8)) * 8;
+            float x[8][8];
+#pragma unroll
+            for (int r = 0; r < 8; ++r) {
+              if (jb + r < jn) ld8(kr + (long long)(j0 + jb + r) * HD + c8, x[r]);
+              else {
+#pragma unroll
+                for (int q = 0; q < 8; ++q) x[r][q] = 0.f;
+              }
+            }
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+              if constexpr (St<T>::is_bf16) {
+                u16x8 col;
+#pragma unroll
+                for (int r = 0; r < 8; ++r) col[r] = f2bf(x[r][q]);
+                *reinterpret_cast<u16x8*>(&sm.krt[(c8 + q) * Sm::KTS + jb]) = col;
+              } else {
+#pragma unroll
+                for (int r = 0; r < 8; ++r) sm.krt[(c8 + q) * Sm::KTS + jb + r] = x[r][q];
+              }
+            }
+          }
+          sync_lds();
+          if (cb < NCB) {
+            const int c = 32 * cb + n;
+            if constexpr (St<T>::is_bf16) {
+#pragma unroll
+              for (int kc = 0; kc < Sm::KC / 16; ++kc) {
+                const u16x8 ka = *reinterpret_cast<const u16x8*>(&sm.krt[c * Sm::KTS + 16 * kc + 8 * h]);
+                const u16x8 eh = *reinterpret_cast<const u16x8*>(&sm.ert[n * Sm::ES + j0 + 16 * kc + 8 * h]);
+                const u16x8 el = *reinterpret_cast<const u16x8*>(&sm.erl[n * Sm::ES + j0 + 16 * kc + 8 * h]);
+                mma_bf16(upd, ka, eh);
+                mma_bf16(upd, ka, el);
+              }
+            } else {
+#pragma unroll 8
+              for (int kc = 0; kc < Sm::KC / 2; ++kc)
+                mma_f32(upd, sm.krt[c * Sm::KTS + 2 * kc + h], sm.ert[n * Sm::ES + j0 + 2 * kc + h]);
+            }
+          }
+          sync_lds();
+        }
       }
       // M = gamma*M + upd (two rounded ops, as the reference evaluates them); lane holds
       // column d = n of the block and rows c = 32*cb + d_row(lane, r)
@@ -1266,7 +1378,7 @@ __global__ void __launch_bounds__(MT) mres_kernel(b3_chain_args a) {
           }
         }
       }
-      __syncthreads();
+      sync_lds();
     } else {
       nf += min(S - nf, l);
     }

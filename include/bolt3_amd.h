@@ -52,7 +52,8 @@ typedef struct { float* p; int64_t sb, sh; } b3_gate_out;
 
 typedef struct {
   int32_t dtype, B, T, H, HKV, HD;
-  const void* lin;            /* [B][T][lin_row_stride]: q | k | v | beta | eta columns (projection output) */
+  const void* lin;            /* [B][T][lin_row_stride]: q | k | v | beta | eta columns (projection output);
+                                 rows and the head outputs must be 16-byte aligned */
   int64_t lin_row_stride;
   const float* qn_w;          /* [HD] q RMSNorm weight (fp32 values) or NULL */
   const float* kn_w;          /* [HD] k RMSNorm weight or NULL */

@@ -117,10 +117,16 @@ class Bolt3Attn(nn.Module):
             return self._pack
         with torch.no_grad():
             lins = (self.q_proj, self.k_proj, self.v_proj, self.beta_proj, self.eta_proj)
-            W = torch.cat([m.weight.to(device=device, dtype=dt) for m in lins], dim=0).contiguous()
+            # zero rows pad the packed output width to a multiple of 16 columns, so every row of
+            # the projection output starts 16-byte aligned (the head kernels move 16-byte vectors)
+            n_out = sum(m.out_features for m in lins)
+            pad = (-n_out) % 16
+            W = torch.cat([m.weight.to(device=device, dtype=dt) for m in lins] +
+                          [torch.zeros(pad, self.q_proj.in_features, device=device, dtype=dt)], dim=0).contiguous()
             if any(m.bias is not None for m in lins):
                 b = torch.cat([(m.bias if m.bias is not None else torch.zeros(m.out_features, device=device))
-                               .to(device=device, dtype=dt) for m in lins]).contiguous()
+                               .to(device=device, dtype=dt) for m in lins] +
+                              [torch.zeros(pad, device=device, dtype=dt)]).contiguous()
             else:
                 b = None
             side = dict(

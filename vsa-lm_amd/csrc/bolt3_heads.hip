@@ -7,100 +7,146 @@
 // vsa_lm/config/bolt3.py:197 and :347) and the gates
 // sigmoid(beta_proj x), tanh(eta_proj x) (vsa_lm/config/bolt3.py:198-199, :348-349).
 //
-// One workgroup per token row; a head is handled by HD/2 lanes, lane i owning
-// the RoPE pair (i, i + HD/2).  Every value is rounded to the storage type at
-// the same points as the reference's per-op evaluation.
+// Layout: a workgroup handles TOK consecutive tokens of one batch row.  A head unit
+// (q, k or v head of one token) is handled by HD/16 lanes; lane p owns the RoPE pairs
+// (8p..8p+7, HD/2+8p..HD/2+8p+7), so every load and store is a 16-byte vector and the
+// RMS statistic is a 3- (HD=128) or 2-step (HD=64) shuffle sum.  The rounded cos / sin
+// of the TOK positions come from an LDS table filled once per workgroup.  Every value is
+// rounded to the storage type at the same points as the reference's per-op evaluation.
 #include "bolt3_common.h"
 #include "bolt3_math.h"
 #include "bolt3_amd.h"
 
 namespace b3 {
 
+constexpr int HEADS_TOK = 4;    // tokens per workgroup
+constexpr int HEADS_NT = 256;   // threads per workgroup
+
+template <typename T> struct Vec8;   // 8 storage elements, one 16-byte (bf16) or 32-byte (fp32) move
+template <> struct Vec8<uint16_t> {
+  u16x8 x;
+  __device__ __forceinline__ void load(const uint16_t* p) { x = *reinterpret_cast<const u16x8*>(p); }
+  __device__ __forceinline__ void store(uint16_t* p) const { *reinterpret_cast<u16x8*>(p) = x; }
+  __device__ __forceinline__ float get(int i) const { return bf2f(x[i]); }
+  __device__ __forceinline__ void set(int i, float v) { x[i] = f2bf(v); }
+};
+template <> struct Vec8<float> {
+  float4 a, b;
+  __device__ __forceinline__ void load(const float* p) {
+    a = *reinterpret_cast<const float4*>(p);
+    b = *reinterpret_cast<const float4*>(p + 4);
+  }
+  __device__ __forceinline__ void store(float* p) const {
+    *reinterpret_cast<float4*>(p) = a;
+    *reinterpret_cast<float4*>(p + 4) = b;
+  }
+  __device__ __forceinline__ float get(int i) const {
+    const float4& q = i < 4 ? a : b;
+    const int k = i & 3;
+    return k == 0 ? q.x : k == 1 ? q.y : k == 2 ? q.z : q.w;
+  }
+  __device__ __forceinline__ void set(int i, float v) {
+    float4& q = i < 4 ? a : b;
+    const int k = i & 3;
+    if (k == 0) q.x = v; else if (k == 1) q.y = v; else if (k == 2) q.z = v; else q.w = v;
+  }
+};
+
 template <typename T, int HD>
-__global__ void __launch_bounds__(256) heads_kernel(b3_heads_args a) {
-  constexpr int HALF = HD / 2;
-  constexpr int UNITS = 256 / HALF;  // heads processed per pass
-  const int t = blockIdx.x, b = blockIdx.y;
+__global__ void __launch_bounds__(HEADS_NT) heads_kernel(b3_heads_args a) {
+  constexpr int HALF = HD / 2, P8 = HALF / 8;   // lanes per head unit
+  __shared__ float cs_tab[HEADS_TOK][HALF], sn_tab[HEADS_TOK][HALF];
+  const int b = blockIdx.y, t0 = blockIdx.x * HEADS_TOK;
   const int tid = threadIdx.x;
-  const T* row = reinterpret_cast<const T*>(a.lin) + ((long long)b * a.T + t) * a.lin_row_stride;
-  const float pos = (float)(a.pos0 + t);
+  const int ntok = min(HEADS_TOK, a.T - t0);
+
+  for (int it = tid; it < HEADS_TOK * HALF; it += HEADS_NT) {
+    const int tt = it / HALF, i = it % HALF;
+    float sn, cs;
+    sincos_rope(mul_rn((float)(a.pos0 + t0 + tt), a.inv_freq[i]), &sn, &cs);
+    cs_tab[tt][i] = St<T>::rnd(cs);
+    sn_tab[tt][i] = St<T>::rnd(sn);
+  }
+  __syncthreads();
 
   const int n_units = a.H + 2 * a.HKV;
-  const int unit_in_pass = tid / HALF;
-  const int i = tid % HALF;
-  const float inv = a.inv_freq[i];
-  const float ang = mul_rn(pos, inv);
-  float sn, cs;
-  sincos_rope(ang, &sn, &cs);
-  const float c = St<T>::rnd(cs), s = St<T>::rnd(sn);
-
-  for (int u0 = 0; u0 < n_units; u0 += UNITS) {
-    const int u = u0 + unit_in_pass;
-    const bool live = u < n_units;
-    int kind = 0, h = 0;  // 0: q, 1: k, 2: v
-    if (live) {
-      if (u < a.H) { kind = 0; h = u; }
-      else if (u < a.H + a.HKV) { kind = 1; h = u - a.H; }
-      else { kind = 2; h = u - a.H - a.HKV; }
-    }
-    const int col = kind == 0 ? h * HD : (kind == 1 ? (a.H + h) * HD : (a.H + a.HKV + h) * HD);
-    float x0 = 0.f, x1 = 0.f;
-    if (live) {
-      x0 = St<T>::ld(row + col + i);
-      x1 = St<T>::ld(row + col + i + HALF);
-    }
-    // RMSNorm over the head (q and k only, when the module has q/k norms).
-    float ss = x0 * x0 + x1 * x1;
-#pragma unroll
-    for (int o = HALF / 2; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
-    if (live && kind < 2 && a.has_qk_norm) {
-      const float* w = kind == 0 ? a.qn_w : a.kn_w;
-      const float r = 1.0f / sqrtf(div_rn(ss, (float)HD) + a.eps);
-      x0 = St<T>::rnd(mul_rn(mul_rn(x0, r), w[i]));
-      x1 = St<T>::rnd(mul_rn(mul_rn(x1, r), w[i + HALF]));
-    }
-    if (!live) continue;
+  const int items = HEADS_TOK * n_units * P8;   // P8 consecutive threads share one (token, unit)
+  for (int it = tid; it < items; it += HEADS_NT) {
+    const int p = it % P8, unit = (it / P8) % n_units, tt = it / (P8 * n_units);
+    if (tt >= ntok) continue;   // uniform across the P8 lanes of the unit
+    const int t = t0 + tt;
+    const T* row = reinterpret_cast<const T*>(a.lin) + ((long long)b * a.T + t) * a.lin_row_stride + unit * HD;
+    Vec8<T> x0, x1;
+    x0.load(row + 8 * p);
+    x1.load(row + HALF + 8 * p);
+    const int kind = unit < a.H ? 0 : (unit < a.H + a.HKV ? 1 : 2);   // q, k, v
+    const int h = kind == 0 ? unit : (kind == 1 ? unit - a.H : unit - a.H - a.HKV);
     if (kind == 2) {
       T* o = reinterpret_cast<T*>(a.v.p) + b * a.v.sb + h * a.v.sh + (long long)t * HD;
-      o[i] = St<T>::from_f(x0);
-      o[i + HALF] = St<T>::from_f(x1);
+      x0.store(o + 8 * p);
+      x1.store(o + HALF + 8 * p);
       continue;
     }
-    // out = x*cos + rotate_half(x)*sin, each product and the sum rounded.
-    const float r0 = St<T>::rnd(add_rn(St<T>::rnd(mul_rn(x0, c)), St<T>::rnd(mul_rn(-x1, s))));
-    const float r1 = St<T>::rnd(add_rn(St<T>::rnd(mul_rn(x1, c)), St<T>::rnd(mul_rn(x0, s))));
+    // RMSNorm over the head (fp32 statistic), then weight, one rounding
+    if (a.has_qk_norm) {
+      float ss = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float u = x0.get(e), w = x1.get(e);
+        ss += u * u + w * w;
+      }
+#pragma unroll
+      for (int o = P8 / 2; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+      const float* wt = kind == 0 ? a.qn_w : a.kn_w;
+      const float r = 1.0f / sqrtf(div_rn(ss, (float)HD) + a.eps);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        x0.set(e, mul_rn(mul_rn(x0.get(e), r), wt[8 * p + e]));
+        x1.set(e, mul_rn(mul_rn(x1.get(e), r), wt[HALF + 8 * p + e]));
+      }
+    }
     const b3_tensor_out& raw = kind == 0 ? a.q_raw : a.k_raw;
     const b3_tensor_out& rot = kind == 0 ? a.q_rope : a.k_rope;
     if (raw.p) {
       T* o = reinterpret_cast<T*>(raw.p) + b * raw.sb + h * raw.sh + (long long)t * HD;
-      o[i] = St<T>::from_f(x0);
-      o[i + HALF] = St<T>::from_f(x1);
+      x0.store(o + 8 * p);
+      x1.store(o + HALF + 8 * p);
+    }
+    // out = x*cos + rotate_half(x)*sin, each product and the sum rounded
+    Vec8<T> r0, r1;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float c = cs_tab[tt][8 * p + e], sn = sn_tab[tt][8 * p + e];
+      const float u = x0.get(e), w = x1.get(e);
+      r0.set(e, add_rn(St<T>::rnd(mul_rn(u, c)), St<T>::rnd(mul_rn(-w, sn))));
+      r1.set(e, add_rn(St<T>::rnd(mul_rn(w, c)), St<T>::rnd(mul_rn(u, sn))));
     }
     T* o = reinterpret_cast<T*>(rot.p) + b * rot.sb + h * rot.sh + (long long)t * HD;
-    o[i] = St<T>::from_f(r0);
-    o[i + HALF] = St<T>::from_f(r1);
+    r0.store(o + 8 * p);
+    r1.store(o + HALF + 8 * p);
   }
 
-  // Gates: beta = sigmoid(.) per kv head, eta = tanh(.) per query head, stored as
-  // fp32 copies of the storage-type values.
-  const int gcol = (a.H + 2 * a.HKV) * HD;
-  for (int g = tid; g < a.HKV + a.H; g += 256) {
-    const float z = St<T>::ld(row + gcol + g);
+  // Gates: beta = sigmoid(.) per kv head, eta = tanh(.) per query head, stored as fp32
+  // copies of the storage-type values.
+  const int ng = a.HKV + a.H;
+  for (int it = tid; it < HEADS_TOK * ng; it += HEADS_NT) {
+    const int tt = it / ng, g = it % ng;
+    if (tt >= ntok) continue;
+    const int t = t0 + tt;
+    const T* row = reinterpret_cast<const T*>(a.lin) + ((long long)b * a.T + t) * a.lin_row_stride;
+    const float z = St<T>::ld(row + (a.H + 2 * a.HKV) * HD + g);
     if (g < a.HKV) {
-      const float val = St<T>::rnd(1.0f / (1.0f + expf(-z)));
-      a.beta.p[b * a.beta.sb + g * a.beta.sh + t] = val;
+      a.beta.p[b * a.beta.sb + g * a.beta.sh + t] = St<T>::rnd(1.0f / (1.0f + expf(-z)));
     } else {
-      const int hq = g - a.HKV;
-      const float val = St<T>::rnd(tanhf(z));
-      a.eta.p[b * a.eta.sb + hq * a.eta.sh + t] = val;
+      a.eta.p[b * a.eta.sb + (g - a.HKV) * a.eta.sh + t] = St<T>::rnd(tanhf(z));
     }
   }
-  if (a.pos_out && b == 0 && tid == 0) a.pos_out[t] = pos;
+  if (a.pos_out && b == 0 && tid < ntok) a.pos_out[t0 + tid] = (float)(a.pos0 + t0 + tid);
 }
 
 template <typename T>
 static int launch_heads(const b3_heads_args& a, hipStream_t st) {
-  dim3 grid(a.T, a.B), block(256);
+  dim3 grid((a.T + HEADS_TOK - 1) / HEADS_TOK, a.B), block(HEADS_NT);
   if (a.HD == 64) hipLaunchKernelGGL((heads_kernel<T, 64>), grid, block, 0, st, a);
   else if (a.HD == 128) hipLaunchKernelGGL((heads_kernel<T, 128>), grid, block, 0, st, a);
   else return B3_ERR_UNSUPPORTED;
@@ -115,6 +161,12 @@ extern "C" int bolt3_heads(const b3_heads_args* a, void* stream) {
       !a->inv_freq)
     return B3_ERR_ARG;
   if (a->has_qk_norm && (!a->qn_w || !a->kn_w)) return B3_ERR_ARG;
+  // 16-byte vector moves: projection rows and head rows must start 16-byte aligned
+  const int64_t es = a->dtype == B3_BF16 ? 2 : 4;
+  if ((a->lin_row_stride * es) % 16 || reinterpret_cast<uintptr_t>(a->lin) % 16) return B3_ERR_ARG;
+  const b3_tensor_out* outs[5] = {&a->q_raw, &a->q_rope, &a->k_raw, &a->k_rope, &a->v};
+  for (const b3_tensor_out* o : outs)
+    if (o->p && (reinterpret_cast<uintptr_t>(o->p) % 16 || (o->sb * es) % 16 || (o->sh * es) % 16)) return B3_ERR_ARG;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (a->dtype == B3_F32) return b3::launch_heads<float>(*a, st);
   if (a->dtype == B3_BF16) return b3::launch_heads<uint16_t>(*a, st);

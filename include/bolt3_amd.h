@@ -52,9 +52,12 @@ typedef struct { float* p; int64_t sb, sh; } b3_gate_out;
 
 typedef struct {
   int32_t dtype, B, T, H, HKV, HD;
-  const void* lin;            /* [B][T][lin_row_stride]: q | k | v | beta | eta columns (projection output);
-                                 rows and the head outputs must be 16-byte aligned */
+  const void* lin;            /* [B][T][lin_row_stride]: q | k | v | beta | eta columns (projection output),
+                                 or q | eta columns when lin_kv is set; rows and head outputs 16-byte aligned */
   int64_t lin_row_stride;
+  const void* lin_kv;         /* optional [B][T][lin_kv_row_stride]: k | v | beta columns (a separate projection) */
+  int64_t lin_kv_row_stride;
+  int32_t parts;              /* 1: q heads and eta only; 2: k/v heads, beta and pos_out only; 0 or 3: all */
   const float* qn_w;          /* [HD] q RMSNorm weight (fp32 values) or NULL */
   const float* kn_w;          /* [HD] k RMSNorm weight or NULL */
   int32_t has_qk_norm;
@@ -87,7 +90,8 @@ typedef struct {
   int32_t n_steps;            /* consolidations run back to back                          */
   int32_t off0, len0;         /* step 0 consumes tokens [off0, off0 + len0)               */
   int32_t step_stride, step_len; /* step i > 0 consumes [i*step_stride, i*step_stride + step_len) */
-  int32_t n_filled;           /* filled slots before step 0 (0 => state must be the empty state) */
+  int32_t n_filled;           /* filled slots before step 0; 0: the chain starts from the empty state
+                                 (zero slots, mass 1, M_res 0) and the state arrays are outputs only */
   int32_t kp_exact;           /* 1: kp rows are bolt3_heads / bolt3_decode RoPE of kr at pos (bit-exact),
                                  so a slot taken from a token copies its roped key; 0: recompute */
   /* slot state, updated in place: ak/av [bh][S][HD] storage dtype (un-roped keys), mass/util/pm [bh][S],
@@ -165,6 +169,13 @@ typedef struct {
   float eps;
   void* y;                    /* (b, t, h, d) at + b*y_sb + t*y_st + h*HD + d, storage dtype */
   int64_t y_sb, y_st;
+  /* mode 0, bf16 only: split of the key fields so that the window part can run before the
+     consolidation chain has produced the slot snapshots.  part 0: all fields at once;
+     part 1: sinks + window for every chunk (chunks 0 and 1 complete; chunks >= 2 leave their
+     online-softmax state in `partial`); part 2: the slot field of chunks >= 2, merged with
+     that state, then the readout.  partial: [B][H][n_q][HD + 4] floats. */
+  int32_t part;
+  float* partial;
 } b3_attn_args;
 
 /*

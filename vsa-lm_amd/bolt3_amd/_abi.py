@@ -37,7 +37,8 @@ class GateOut(C.Structure):
 class HeadsArgs(C.Structure):
     _fields_ = [
         ("dtype", i32), ("B", i32), ("T", i32), ("H", i32), ("HKV", i32), ("HD", i32),
-        ("lin", p), ("lin_row_stride", i64), ("qn_w", p), ("kn_w", p), ("has_qk_norm", i32), ("eps", f32),
+        ("lin", p), ("lin_row_stride", i64), ("lin_kv", p), ("lin_kv_row_stride", i64), ("parts", i32),
+        ("qn_w", p), ("kn_w", p), ("has_qk_norm", i32), ("eps", f32),
         ("inv_freq", p), ("pos0", i32),
         ("q_raw", TensorOut), ("q_rope", TensorOut), ("k_raw", TensorOut), ("k_rope", TensorOut), ("v", TensorOut),
         ("beta", GateOut), ("eta", GateOut), ("pos_out", p),
@@ -70,6 +71,7 @@ class AttnArgs(C.Structure):
         ("m_res", p), ("m_step", i64), ("m_split", i32),
         ("gamma", p), ("res_w", p), ("eps", f32),
         ("y", p), ("y_sb", i64), ("y_st", i64),
+        ("part", i32), ("partial", p),
     ]
 
 

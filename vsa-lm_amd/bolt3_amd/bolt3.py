@@ -34,6 +34,17 @@ def _require_gpu(t: torch.Tensor, what: str):
                            f"there is no CPU implementation")
 
 
+_SIDE_STREAMS: dict = {}
+
+
+def _side_stream(dev: torch.device) -> torch.cuda.Stream:
+    """One extra stream per device (default priority) for the consolidation chain."""
+    key = dev.index if dev.index is not None else torch.cuda.current_device()
+    if key not in _SIDE_STREAMS:
+        _SIDE_STREAMS[key] = torch.cuda.Stream(device=dev)
+    return _SIDE_STREAMS[key]
+
+
 class _NoBackward(torch.autograd.Function):
     """Keeps autograd edges to the inputs but refuses to differentiate the HIP path."""
 
@@ -54,7 +65,9 @@ def _tout(t: torch.Tensor | None, offset: int = 0) -> A.TensorOut:
     return A.TensorOut(t.data_ptr() + offset * t.shape[-1] * es, t.stride(0), t.stride(1))
 
 
-def _gout(t: torch.Tensor, offset: int = 0) -> A.GateOut:
+def _gout(t: torch.Tensor | None, offset: int = 0) -> A.GateOut:
+    if t is None:
+        return A.GateOut(None, 0, 0)
     return A.GateOut(t.data_ptr() + offset * 4, t.stride(0), t.stride(1))
 
 
@@ -110,7 +123,9 @@ class Bolt3Attn(nn.Module):
     # ------------------------------------------------------------ packed parameters
 
     def _packed(self, dt: torch.dtype, device: torch.device):
-        """(W_all, b_all, W_o, fp32 side tensors) cached until a parameter changes."""
+        """(W_all, b_all, side) cached until a parameter changes.  W_all packs q | k | v | beta | eta
+        rows (the decoder's one projection); side holds W_o, the split projections q | eta and
+        k | v | beta used by the forward, and the fp32 tensors the kernels read."""
         params = list(self.parameters())
         key = (dt, device, tuple((q.data_ptr(), q._version) for q in params), self.rope.inv_freq.data_ptr())
         if key == self._pack_key:
@@ -129,7 +144,20 @@ class Bolt3Attn(nn.Module):
                               [torch.zeros(pad, device=device, dtype=dt)]).contiguous()
             else:
                 b = None
+            def pack(ms):
+                w = [m.weight.to(device=device, dtype=dt) for m in ms]
+                pd = (-sum(m.out_features for m in ms)) % 16
+                w.append(torch.zeros(pd, self.q_proj.in_features, device=device, dtype=dt))
+                bb = None
+                if any(m.bias is not None for m in ms):
+                    bb = torch.cat([(m.bias if m.bias is not None else torch.zeros(m.out_features, device=device))
+                                    .to(device=device, dtype=dt) for m in ms] +
+                                   [torch.zeros(pd, device=device, dtype=dt)]).contiguous()
+                return torch.cat(w, dim=0).contiguous(), bb
+            wq, bq = pack((self.q_proj, self.eta_proj))
+            wkv, bkv = pack((self.k_proj, self.v_proj, self.beta_proj))
             side = dict(
+                wq=wq, bq=bq, wkv=wkv, bkv=bkv,
                 wo=self.o_proj.weight.to(device=device, dtype=dt).contiguous(),
                 inv_freq=self.rope.inv_freq.to(device).float().contiguous(),
                 kappa=self.kappa.detach().to(device).float().contiguous(),
@@ -142,10 +170,14 @@ class Bolt3Attn(nn.Module):
         return self._pack
 
     def _heads(self, lin, B, T, dt, side, pos0, q_raw, q_rope, k_raw, k_rope, v, beta, eta, pos_out=None,
-               kv_offset=0):
+               kv_offset=0, lin_kv=None, parts=0):
         a = A.HeadsArgs()
         a.dtype, a.B, a.T, a.H, a.HKV, a.HD = A.dtype_code(dt), B, T, self.H, self.HKV, self.HD
-        a.lin, a.lin_row_stride = lin.data_ptr(), lin.shape[-1]
+        if lin is not None:
+            a.lin, a.lin_row_stride = lin.data_ptr(), lin.shape[-1]
+        if lin_kv is not None:
+            a.lin_kv, a.lin_kv_row_stride = lin_kv.data_ptr(), lin_kv.shape[-1]
+        a.parts = parts
         a.qn_w, a.kn_w = A.ptr(side["qn"]), A.ptr(side["kn"])
         a.has_qk_norm = int(side["qn"] is not None)
         a.eps = float(self.res_norm.eps)
@@ -154,7 +186,7 @@ class Bolt3Attn(nn.Module):
         a.k_raw, a.k_rope, a.v = _tout(k_raw, kv_offset), _tout(k_rope, kv_offset), _tout(v, kv_offset)
         a.beta, a.eta = _gout(beta, kv_offset), _gout(eta)
         a.pos_out = None if pos_out is None else pos_out.data_ptr() + kv_offset * 4
-        A.call("bolt3_heads", a, lin.device)
+        A.call("bolt3_heads", a, (lin if lin is not None else lin_kv).device)
 
     def _chain(self, dt, device, B, kr, kp, v, tok_bh_stride, pos, beta, beta_bh_stride, n_steps, off0, len0,
                step_stride, step_len, n_filled, st: dict, m_res, gam, side, snap_k=None, snap_v=None,
@@ -201,25 +233,31 @@ class Bolt3Attn(nn.Module):
         dt, dev = x.dtype, x.device
         H, HKV, HD, S, C = self.H, self.HKV, self.HD, self.S, self.C
         x = x.contiguous()
-        W, bias, side = self._packed(dt, dev)
-        lin = F.linear(x, W, bias)
-        q_raw = torch.empty(b, H, T, HD, dtype=dt, device=dev)
-        q_rope = torch.empty_like(q_raw)
+        _, _, side = self._packed(dt, dev)
+        gam = self.gamma_delta().to(dev).contiguous()
+        main = torch.cuda.current_stream(dev)
+        # k | v | beta first: the consolidation chain needs only them, so it runs on a side
+        # stream while the q | eta projection and head preparation proceed on this one
+        lin_kv = F.linear(x, side["wkv"], side["bkv"])
         k_raw = torch.empty(b, HKV, T, HD, dtype=dt, device=dev)
         k_rope, v = torch.empty_like(k_raw), torch.empty_like(k_raw)
         beta = torch.empty(b, HKV, T, device=dev)
-        eta = torch.empty(b, H, T, device=dev)
         pos = torch.empty(T, device=dev)
-        self._heads(lin, b, T, dt, side, 0, q_raw, q_rope, k_raw, k_rope, v, beta, eta, pos_out=pos)
-        gam = self.gamma_delta().to(dev).contiguous()
+        self._heads(None, b, T, dt, side, 0, None, None, k_raw, k_rope, v, beta, None, pos_out=pos,
+                    lin_kv=lin_kv, parts=2)
 
         n_chunks = (T + C - 1) // C
         n_cons = max(0, n_chunks - 2)
         bh = b * HKV
         snaps = (None, None, None, None)
+        chain_stream = None
         if n_cons > 0:
-            st = self._empty_slots(bh, dt, dev)
-            m_res = torch.zeros(bh, HD, HD, device=dev)
+            chain_stream = _side_stream(dev)
+            # n_filled = 0: the chain builds the empty state itself, these are outputs only
+            st = dict(ak=torch.empty(bh, S, HD, dtype=dt, device=dev), av=torch.empty(bh, S, HD, dtype=dt, device=dev),
+                      mass=torch.empty(bh, S, device=dev), util=torch.empty(bh, S, device=dev),
+                      pm=torch.empty(bh, S, device=dev), act=torch.empty(bh, S, dtype=torch.uint8, device=dev))
+            m_res = torch.empty(bh, HD, HD, device=dev)
             snaps = (torch.empty(n_cons, bh, S, HD, dtype=dt, device=dev),
                      torch.empty(n_cons, bh, S, HD, dtype=dt, device=dev),
                      torch.empty(n_cons, bh, S, device=dev),
@@ -228,12 +266,19 @@ class Bolt3Attn(nn.Module):
             log = None
             if trace is not None:
                 log = torch.zeros(n_cons, bh, A.LOG_ROWS, A.LOG_COLS, device=dev)
-            self._chain(dt, dev, b, k_raw.data_ptr(), k_rope.data_ptr(), v.data_ptr(), T * HD, pos.data_ptr(),
-                        beta.data_ptr(), T, n_cons, ns, C - ns, C, C, 0, st, m_res, gam, side, *snaps, log=log,
-                        kp_exact=True)
+            chain_stream.wait_stream(main)   # after the state initialisation enqueued above
+            with torch.cuda.stream(chain_stream):
+                self._chain(dt, dev, b, k_raw.data_ptr(), k_rope.data_ptr(), v.data_ptr(), T * HD,
+                            pos.data_ptr(), beta.data_ptr(), T, n_cons, ns, C - ns, C, C, 0, st, m_res, gam, side,
+                            *snaps, log=log, kp_exact=True)
             if trace is not None:
                 trace.update(state=st, m_res=m_res, snap_k=snaps[0], snap_v=snaps[1], snap_bias=snaps[2],
                              snap_m=snaps[3], log=log)
+        lin_q = F.linear(x, side["wq"], side["bq"])
+        q_raw = torch.empty(b, H, T, HD, dtype=dt, device=dev)
+        q_rope = torch.empty_like(q_raw)
+        eta = torch.empty(b, H, T, device=dev)
+        self._heads(lin_q, b, T, dt, side, 0, q_raw, q_rope, None, None, None, None, eta, lin_kv=lin_kv, parts=1)
         if trace is not None:
             trace.update(q_raw=q_raw, q_rope=q_rope, k_raw=k_raw, k_rope=k_rope, v=v, beta=beta, eta=eta, pos=pos)
 
@@ -251,7 +296,19 @@ class Bolt3Attn(nn.Module):
             a.m_split = int(dt == torch.bfloat16)
         a.gamma, a.res_w, a.eps = gam.data_ptr(), side["res_w"].data_ptr(), float(self.res_norm.eps)
         a.y, a.y_sb, a.y_st = y.data_ptr(), y.stride(0), y.stride(1)
-        A.call("bolt3_chunk_attn", a, dev)
+        if chain_stream is not None and dt == torch.bfloat16:
+            # sinks + window of every chunk while the chain runs, then the slot field merged into
+            # the saved online-softmax state once the snapshots exist
+            partial = torch.empty(b, H, T, HD + 4, device=dev)
+            a.part, a.partial = 1, partial.data_ptr()
+            A.call("bolt3_chunk_attn", a, dev)
+            main.wait_stream(chain_stream)
+            a.part = 2
+            A.call("bolt3_chunk_attn", a, dev)
+        else:
+            if chain_stream is not None:
+                main.wait_stream(chain_stream)
+            A.call("bolt3_chunk_attn", a, dev)
         if trace is not None:
             trace["y"] = y
         return F.linear(y, side["wo"])

@@ -407,7 +407,8 @@ __global__ void __launch_bounds__(512) attn_fwd_kernel(b3_attn_args a, int QW) {
   const int g = wave / QW, qsub = wave % QW;
   const int bh = blockIdx.z, b = bh / a.HKV, hkv = bh % a.HKV;
   const int hq = hkv * G + g;
-  const int chunk = blockIdx.y, C = a.C;
+  const int part = a.part;                       // 0 all fields, 1 sinks + window, 2 slots (chunks >= 2)
+  const int chunk = blockIdx.y + (part == 2 ? 2 : 0), C = a.C;
   const int qbase = chunk * C;
   const int nq_chunk = min(C, a.n_q - qbase);
   const int qt0 = blockIdx.x * 32 * QW;
@@ -425,25 +426,30 @@ __global__ void __launch_bounds__(512) attn_fwd_kernel(b3_attn_args a, int QW) {
   const long long wofs = (long long)b * a.w_sb + (long long)hkv * a.w_sh;
   const uint16_t* wk = reinterpret_cast<const uint16_t*>(a.win_k) + wofs;
   const uint16_t* wv = reinterpret_cast<const uint16_t*>(a.win_v) + wofs;
-  const int n_pre = chunk >= 2 ? 1 + (a.S + KB - 1) / KB : 0;
-  const int n_prev = chunk >= 1 ? (C + KB - 1) / KB : 0;
-  const int n_cur = (wg_qend + KB - 1) / KB;
+  const int n_sink = (chunk >= 2 && part != 2) ? 1 : 0;
+  const int n_slot = (chunk >= 2 && part != 1) ? (a.S + KB - 1) / KB : 0;
+  const int n_pre = n_sink + n_slot;
+  const int n_prev = (chunk >= 1 && part != 2) ? (C + KB - 1) / KB : 0;
+  const int n_cur = part != 2 ? (wg_qend + KB - 1) / KB : 0;
   const int nb = n_pre + n_prev + n_cur;
+  const bool keep_partial = part == 1 && chunk >= 2;   // the slot field follows in part 2
+  float* pq = a.partial ? a.partial + (((long long)b * a.H + hq) * a.n_q + t) * (HD + 4) : nullptr;
   auto block = [&](int i) -> FwdBlock {
     FwdBlock f;
     f.bias = nullptr;
     f.kpos = -1;
     if (i < n_pre) {
-      if (i == 0) {
+      if (i < n_sink) {
         f.k = wk;
         f.v = wv;
         f.nvalid = min(a.n_sinks, C);
       } else {
-        const long long so = (long long)step * a.slot_step + (long long)bh * a.S * HD + (long long)(i - 1) * KB * HD;
+        const int j = i - n_sink;
+        const long long so = (long long)step * a.slot_step + (long long)bh * a.S * HD + (long long)j * KB * HD;
         f.k = reinterpret_cast<const uint16_t*>(a.slot_k) + so;
         f.v = reinterpret_cast<const uint16_t*>(a.slot_v) + so;
-        f.bias = a.slot_bias + (long long)step * (a.slot_step / HD) + (long long)bh * a.S + (i - 1) * KB;
-        f.nvalid = min(KB, a.S - (i - 1) * KB);
+        f.bias = a.slot_bias + (long long)step * (a.slot_step / HD) + (long long)bh * a.S + j * KB;
+        f.nvalid = min(KB, a.S - j * KB);
       }
     } else if (i < n_pre + n_prev) {
       const int j = i - n_pre;
@@ -504,6 +510,21 @@ __global__ void __launch_bounds__(512) attn_fwd_kernel(b3_attn_args a, int QW) {
 #pragma unroll
   for (int db = 0; db < NDB; ++db) o[db] = zero16();
   float m_run = -INFINITY, l_run = 0.f;
+  if (part == 2 && qok) {
+    // online-softmax state left by part 1: lane half h holds features 64h.. in (db, r) order
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const float4 q4 = *reinterpret_cast<const float4*>(pq + h * (HD / 2) + 16 * db + 4 * r4);
+        o[db][4 * r4 + 0] = q4.x;
+        o[db][4 * r4 + 1] = q4.y;
+        o[db][4 * r4 + 2] = q4.z;
+        o[db][4 * r4 + 3] = q4.w;
+      }
+    m_run = pq[HD];
+    l_run = pq[HD + 1];
+  }
 
   load(0);
   store(0);
@@ -576,6 +597,22 @@ __global__ void __launch_bounds__(512) attn_fwd_kernel(b3_attn_args a, int QW) {
     }
     if (i + 1 < nb) store(buf ^ 1);
     sync_lds();
+  }
+
+  if (keep_partial) {
+    if (qok) {
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4)
+          *reinterpret_cast<float4*>(pq + h * (HD / 2) + 16 * db + 4 * r4) =
+              make_float4(o[db][4 * r4], o[db][4 * r4 + 1], o[db][4 * r4 + 2], o[db][4 * r4 + 3]);
+      if (h == 0) {
+        pq[HD] = m_run;
+        pq[HD + 1] = l_run;
+      }
+    }
+    return;
   }
 
   // ---- normalise; y = round(O)
@@ -665,7 +702,9 @@ static int launch_attn(const b3_attn_args& a, hipStream_t st) {
   const int G = a.H / a.HKV;
   const int QW = G <= 4 ? 2 : 1;
   const int per_wg = 32 * QW;
-  const int n_chunks = a.mode == 0 ? (a.n_q + a.C - 1) / a.C : 1;
+  int n_chunks = a.mode == 0 ? (a.n_q + a.C - 1) / a.C : 1;
+  if (a.part == 2) n_chunks -= 2;   // the slot field exists from chunk 2 on
+  if (n_chunks <= 0) return B3_OK;
   const int qlen = a.mode == 0 ? a.C : a.n_q;
   dim3 grid((qlen + per_wg - 1) / per_wg, n_chunks, a.B * a.HKV);
   const int nthreads = 64 * G * QW;
@@ -678,6 +717,7 @@ static int launch_attn(const b3_attn_args& a, hipStream_t st) {
       return (int)hipGetLastError();
     }
   }
+  if (a.part != 0) return B3_ERR_UNSUPPORTED;
   hipLaunchKernelGGL((attn_kernel<T, HD>), grid, dim3(nthreads), 0, st, a, QW);
   return (int)hipGetLastError();
 }
@@ -690,7 +730,7 @@ extern "C" int bolt3_chunk_attn(const b3_attn_args* a, void* stream) {
   if (!a->q_rope || !a->win_k || !a->win_v || !a->y || !a->gamma || !a->res_w || !a->eta) return B3_ERR_ARG;
   if (a->mode == 0) {
     if (a->C <= 0 || a->n_sinks < 0) return B3_ERR_ARG;
-    if (a->n_q > 2 * a->C && (!a->slot_k || !a->slot_v || !a->slot_bias)) return B3_ERR_ARG;
+    if (a->part == 0 && a->n_q > 2 * a->C && (!a->slot_k || !a->slot_v || !a->slot_bias)) return B3_ERR_ARG;
   } else if (a->mode == 1) {
     if (a->b_len < a->n_q || a->n_q > 256) return B3_ERR_ARG;
     if (a->has_slots && (!a->slot_k || !a->slot_v || !a->slot_bias)) return B3_ERR_ARG;
@@ -700,6 +740,8 @@ extern "C" int bolt3_chunk_attn(const b3_attn_args* a, void* stream) {
   }
   if (a->m_res && !a->q_raw) return B3_ERR_ARG;
   if (a->m_split && a->dtype != B3_BF16) return B3_ERR_ARG;
+  if (a->part < 0 || a->part > 2 || (a->part != 0 && (a->mode != 0 || !a->partial))) return B3_ERR_ARG;
+  if (a->part == 2 && a->n_q > 2 * a->C && (!a->slot_k || !a->slot_v || !a->slot_bias)) return B3_ERR_ARG;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (a->dtype == B3_F32) return a->HD == 64 ? b3::launch_attn<float, 64>(*a, st) : b3::launch_attn<float, 128>(*a, st);
   if (a->dtype == B3_BF16)

@@ -653,16 +653,26 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
   const int krs = sm.KREAD_LDS ? KS : HD;
   const bool kp_copy = a.kp_exact != 0;              // a slot taken from token j gets kp_j as its roped key
 
+  // state in; with n_filled == 0 the empty state (zero slots, mass 1) is built here
+  const bool fresh = a.n_filled == 0;
   for (int it = tid; it < S * (HD / 8); it += DT) {
     const int s = it / (HD / 8), d8 = (it % (HD / 8)) * 8;
-    copy8(&sm.ak[s * KS + d8], g_ak + s * HD + d8);
-    copy8(&sm.av[s * KS + d8], g_av + s * HD + d8);
+    if (fresh) {
+      alignas(16) T z[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) z[q] = St<T>::from_f(0.f);
+      copy8(&sm.ak[s * KS + d8], z);
+      copy8(&sm.av[s * KS + d8], z);
+    } else {
+      copy8(&sm.ak[s * KS + d8], g_ak + s * HD + d8);
+      copy8(&sm.av[s * KS + d8], g_av + s * HD + d8);
+    }
   }
   if (tid < S) {
-    sm.mass[tid] = a.mass[bh * S + tid];
-    sm.util[tid] = a.util[bh * S + tid];
-    sm.pm[tid] = a.pm[bh * S + tid];
-    sm.act[tid] = a.act[bh * S + tid] ? 1 : 0;
+    sm.mass[tid] = fresh ? 1.0f : a.mass[bh * S + tid];
+    sm.util[tid] = fresh ? 0.0f : a.util[bh * S + tid];
+    sm.pm[tid] = fresh ? 0.0f : a.pm[bh * S + tid];
+    sm.act[tid] = fresh ? 0 : (a.act[bh * S + tid] ? 1 : 0);
     sm.dirty[tid] = 1;
   }
   if (tid < HD / 2) sm.invf[tid] = a.inv_freq[tid];
@@ -1166,7 +1176,7 @@ __global__ void __launch_bounds__(MT) mres_kernel(b3_chain_args a) {
   // M^T block: mt[dd][c] = M[c][32*db + dd]
   for (int it = tid; it < HD * 32; it += MT) {
     const int c = it / 32, dd = it % 32;
-    const float x = M[c * HD + 32 * db + dd];
+    const float x = a.n_filled == 0 ? 0.0f : M[c * HD + 32 * db + dd];   // empty state: M_res = 0
     sm.mt[dd * Sm::MS + c] = x;
     if constexpr (St<T>::is_bf16) {
       const uint16_t hb = f2bf(x);

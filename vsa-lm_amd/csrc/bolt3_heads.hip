@@ -69,13 +69,21 @@ __global__ void __launch_bounds__(HEADS_NT) heads_kernel(b3_heads_args a) {
   }
   __syncthreads();
 
-  const int n_units = a.H + 2 * a.HKV;
+  // units: q heads 0..H-1, then k heads, then v heads; `parts` selects q or k/v
+  const int parts = a.parts == 0 ? 3 : a.parts;
+  const int u_begin = (parts & 1) ? 0 : a.H;
+  const int u_end = (parts & 2) ? a.H + 2 * a.HKV : a.H;
+  const int n_units = u_end - u_begin;
+  const bool split = a.lin_kv != nullptr;
   const int items = HEADS_TOK * n_units * P8;   // P8 consecutive threads share one (token, unit)
   for (int it = tid; it < items; it += HEADS_NT) {
-    const int p = it % P8, unit = (it / P8) % n_units, tt = it / (P8 * n_units);
+    const int p = it % P8, unit = u_begin + (it / P8) % n_units, tt = it / (P8 * n_units);
     if (tt >= ntok) continue;   // uniform across the P8 lanes of the unit
     const int t = t0 + tt;
-    const T* row = reinterpret_cast<const T*>(a.lin) + ((long long)b * a.T + t) * a.lin_row_stride + unit * HD;
+    const long long tok = (long long)b * a.T + t;
+    const T* row = (split && unit >= a.H)
+                       ? reinterpret_cast<const T*>(a.lin_kv) + tok * a.lin_kv_row_stride + (unit - a.H) * HD
+                       : reinterpret_cast<const T*>(a.lin) + tok * a.lin_row_stride + unit * HD;
     Vec8<T> x0, x1;
     x0.load(row + 8 * p);
     x1.load(row + HALF + 8 * p);
@@ -128,20 +136,24 @@ __global__ void __launch_bounds__(HEADS_NT) heads_kernel(b3_heads_args a) {
 
   // Gates: beta = sigmoid(.) per kv head, eta = tanh(.) per query head, stored as fp32
   // copies of the storage-type values.
-  const int ng = a.HKV + a.H;
+  const int g_begin = (parts & 2) ? 0 : a.HKV, g_end = (parts & 1) ? a.HKV + a.H : a.HKV;
+  const int ng = g_end - g_begin;
   for (int it = tid; it < HEADS_TOK * ng; it += HEADS_NT) {
-    const int tt = it / ng, g = it % ng;
+    const int tt = it / ng, g = g_begin + it % ng;
     if (tt >= ntok) continue;
     const int t = t0 + tt;
-    const T* row = reinterpret_cast<const T*>(a.lin) + ((long long)b * a.T + t) * a.lin_row_stride;
-    const float z = St<T>::ld(row + (a.H + 2 * a.HKV) * HD + g);
+    const long long tok = (long long)b * a.T + t;
+    float z;
+    if (!split) z = St<T>::ld(reinterpret_cast<const T*>(a.lin) + tok * a.lin_row_stride + (a.H + 2 * a.HKV) * HD + g);
+    else if (g < a.HKV) z = St<T>::ld(reinterpret_cast<const T*>(a.lin_kv) + tok * a.lin_kv_row_stride + 2 * a.HKV * HD + g);
+    else z = St<T>::ld(reinterpret_cast<const T*>(a.lin) + tok * a.lin_row_stride + a.H * HD + (g - a.HKV));
     if (g < a.HKV) {
       a.beta.p[b * a.beta.sb + g * a.beta.sh + t] = St<T>::rnd(1.0f / (1.0f + expf(-z)));
     } else {
       a.eta.p[b * a.eta.sb + (g - a.HKV) * a.eta.sh + t] = St<T>::rnd(tanhf(z));
     }
   }
-  if (a.pos_out && b == 0 && tid < ntok) a.pos_out[t0 + tid] = (float)(a.pos0 + t0 + tid);
+  if (a.pos_out && (parts & 2) && b == 0 && tid < ntok) a.pos_out[t0 + tid] = (float)(a.pos0 + t0 + tid);
 }
 
 template <typename T>
@@ -157,13 +169,15 @@ static int launch_heads(const b3_heads_args& a, hipStream_t st) {
 
 extern "C" int bolt3_heads(const b3_heads_args* a, void* stream) {
   if (!a || a->T <= 0 || a->B <= 0 || a->HKV <= 0) return B3_ERR_ARG;
-  if (a->H % a->HKV != 0 || !a->q_rope.p || !a->k_rope.p || !a->v.p || !a->beta.p || !a->eta.p || !a->lin ||
-      !a->inv_freq)
-    return B3_ERR_ARG;
+  const int parts = a->parts == 0 ? 3 : a->parts;
+  if (parts < 0 || parts > 3 || a->H % a->HKV != 0 || !a->inv_freq) return B3_ERR_ARG;
+  if ((parts & 1) && (!a->q_rope.p || !a->eta.p || !a->lin)) return B3_ERR_ARG;
+  if ((parts & 2) && (!a->k_rope.p || !a->v.p || !a->beta.p || (!a->lin && !a->lin_kv))) return B3_ERR_ARG;
   if (a->has_qk_norm && (!a->qn_w || !a->kn_w)) return B3_ERR_ARG;
   // 16-byte vector moves: projection rows and head rows must start 16-byte aligned
   const int64_t es = a->dtype == B3_BF16 ? 2 : 4;
-  if ((a->lin_row_stride * es) % 16 || reinterpret_cast<uintptr_t>(a->lin) % 16) return B3_ERR_ARG;
+  if (a->lin && ((a->lin_row_stride * es) % 16 || reinterpret_cast<uintptr_t>(a->lin) % 16)) return B3_ERR_ARG;
+  if (a->lin_kv && ((a->lin_kv_row_stride * es) % 16 || reinterpret_cast<uintptr_t>(a->lin_kv) % 16)) return B3_ERR_ARG;
   const b3_tensor_out* outs[5] = {&a->q_raw, &a->q_rope, &a->k_raw, &a->k_rope, &a->v};
   for (const b3_tensor_out* o : outs)
     if (o->p && (reinterpret_cast<uintptr_t>(o->p) % 16 || (o->sb * es) % 16 || (o->sh * es) % 16)) return B3_ERR_ARG;

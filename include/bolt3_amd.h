@@ -218,14 +218,20 @@ typedef struct {
   const float* gamma;
   const float* res_w;
   void* y;                    /* [B][H*HD] storage dtype */
+  float* work;                /* scratch of >= bolt3_decode_workspace_bytes(B, H, HKV, HD) bytes */
+  int64_t work_bytes;
 } b3_decode_args;
 
 /*
  * One-token decode step of a Bolt-3 layer: head prep for the new token, append to
  * the window ring, attention over sinks + slots + window in fp32 scores, M_res
- * readout.  Replaces vsa_lm/config/bolt3.py:346-402 for t_s == 1.
+ * readout.  Two kernels on the stream: key ranges of every (batch, kv head) in
+ * parallel plus the readout, then the merge of the ranges.
+ * Replaces vsa_lm/config/bolt3.py:346-402 for t_s == 1.
  */
 int bolt3_decode(const b3_decode_args* a, void* stream);
+/* Workspace of bolt3_decode: partial softmax state of the key ranges and the readout per (batch, kv head). */
+int64_t bolt3_decode_workspace_bytes(int32_t B, int32_t H, int32_t HKV, int32_t HD);
 
 /* Library identification: returns a static string (build flags, gfx target). */
 const char* bolt3_version(void);

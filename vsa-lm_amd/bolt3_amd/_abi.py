@@ -85,11 +85,12 @@ class DecodeArgs(C.Structure):
         ("a_start", i32), ("a_len", i32), ("b_start", i32), ("b_len", i32),
         ("sink_k", p), ("sink_v", p), ("s_sb", i64), ("s_sh", i64), ("n_sink_keys", i32),
         ("slot_k", p), ("slot_v", p), ("slot_bias", p), ("has_slots", i32),
-        ("m_res", p), ("gamma", p), ("res_w", p), ("y", p),
+        ("m_res", p), ("gamma", p), ("res_w", p), ("y", p), ("work", p), ("work_bytes", i64),
     ]
 
 
 EXPORTS = ("bolt3_heads", "bolt3_chain", "bolt3_chain_workspace_bytes", "bolt3_chunk_attn", "bolt3_decode",
+           "bolt3_decode_workspace_bytes",
            "bolt3_version")
 
 _lib = None
@@ -111,6 +112,8 @@ def load():
         fn.restype = C.c_int
     lib.bolt3_chain_workspace_bytes.argtypes = [i32, i32, i32, i32, i32, i32]
     lib.bolt3_chain_workspace_bytes.restype = i64
+    lib.bolt3_decode_workspace_bytes.argtypes = [i32, i32, i32, i32]
+    lib.bolt3_decode_workspace_bytes.restype = i64
     lib.bolt3_version.argtypes = []
     lib.bolt3_version.restype = C.c_char_p
     _lib = lib
@@ -161,6 +164,10 @@ def call(name: str, args, device: torch.device):
     if _timers is not None:
         ev[1].record(stream)
         _timers.setdefault(name, []).append(ev)
+
+
+def decode_workspace_bytes(B: int, H: int, HKV: int, HD: int) -> int:
+    return int(load().bolt3_decode_workspace_bytes(B, H, HKV, HD))
 
 
 def chain_workspace_bytes(dt: torch.dtype, B: int, HKV: int, HD: int, S: int, n_steps: int) -> int:

@@ -164,6 +164,7 @@ class Bolt3Attn(nn.Module):
                 res_w=self.res_norm.weight.detach().to(device).float().contiguous(),
                 qn=None if self.q_norm is None else self.q_norm.weight.detach().to(device).float().contiguous(),
                 kn=None if self.k_norm is None else self.k_norm.weight.detach().to(device).float().contiguous(),
+                gamma=self.gamma_delta().detach().to(device).contiguous(),
             )
         self._pack = (W, b, side)
         self._pack_key = key
@@ -234,7 +235,7 @@ class Bolt3Attn(nn.Module):
         H, HKV, HD, S, C = self.H, self.HKV, self.HD, self.S, self.C
         x = x.contiguous()
         _, _, side = self._packed(dt, dev)
-        gam = self.gamma_delta().to(dev).contiguous()
+        gam = side["gamma"]
         main = torch.cuda.current_stream(dev)
         # k | v | beta first: the consolidation chain needs only them, so it runs on a side
         # stream while the q | eta projection and head preparation proceed on this one
@@ -408,6 +409,14 @@ class Bolt3LayerState:
         self.n_filled = 0
         self.prev = (0, 0)          # (start, length) in the ring
         self.cur = (2 * C, 0)
+        self._dec_work = None
+
+    def decode_workspace(self, H: int) -> torch.Tensor:
+        """Scratch of the one-token decode kernels (partial softmax state per key range)."""
+        n = A.decode_workspace_bytes(self.B, H, self.HKV, self.HD) // 4
+        if self._dec_work is None or self._dec_work.numel() < n:
+            self._dec_work = torch.empty(n, device=self.win_kr.device)
+        return self._dec_work
 
     def _seg(self, name, seg):
         s, n = seg
@@ -512,7 +521,7 @@ class Bolt3Decoder:
         H, HKV, HD, S = ly.H, ly.HKV, ly.HD, ly.S
         W, bias, side = ly._packed(dt, dev)
         lin = F.linear(h.contiguous(), W, bias)
-        gam = ly.gamma_delta().to(dev).contiguous()
+        gam = side["gamma"]
         cs, cl = st.cur
         ps, pl = st.prev
         if t == 1:
@@ -532,6 +541,8 @@ class Bolt3Decoder:
             a.slot_k, a.slot_v, a.slot_bias = st.slot_k.data_ptr(), st.slots["av"].data_ptr(), st.slot_bias.data_ptr()
             a.has_slots = int(st.has_slots)
             a.m_res, a.gamma, a.res_w, a.y = m_state.data_ptr(), gam.data_ptr(), side["res_w"].data_ptr(), y.data_ptr()
+            work = st.decode_workspace(H)
+            a.work, a.work_bytes = work.data_ptr(), work.numel() * 4
             A.call("bolt3_decode", a, dev)
             y = y.view(B, 1, H * HD)
         else:

@@ -49,6 +49,37 @@ template <> struct St<uint16_t> {
   static constexpr bool is_bf16 = true;
 };
 
+// 8 consecutive storage elements: one 16-byte (bf16) or two 16-byte (fp32) moves
+template <typename T> struct Vec8;
+template <> struct Vec8<uint16_t> {
+  u16x8 x;
+  __device__ __forceinline__ void load(const uint16_t* p) { x = *reinterpret_cast<const u16x8*>(p); }
+  __device__ __forceinline__ void store(uint16_t* p) const { *reinterpret_cast<u16x8*>(p) = x; }
+  __device__ __forceinline__ float get(int i) const { return bf2f(x[i]); }
+  __device__ __forceinline__ void set(int i, float v) { x[i] = f2bf(v); }
+};
+template <> struct Vec8<float> {
+  float4 a, b;
+  __device__ __forceinline__ void load(const float* p) {
+    a = *reinterpret_cast<const float4*>(p);
+    b = *reinterpret_cast<const float4*>(p + 4);
+  }
+  __device__ __forceinline__ void store(float* p) const {
+    *reinterpret_cast<float4*>(p) = a;
+    *reinterpret_cast<float4*>(p + 4) = b;
+  }
+  __device__ __forceinline__ float get(int i) const {
+    const float4& q = i < 4 ? a : b;
+    const int k = i & 3;
+    return k == 0 ? q.x : k == 1 ? q.y : k == 2 ? q.z : q.w;
+  }
+  __device__ __forceinline__ void set(int i, float v) {
+    float4& q = i < 4 ? a : b;
+    const int k = i & 3;
+    if (k == 0) q.x = v; else if (k == 1) q.y = v; else if (k == 2) q.z = v; else q.w = v;
+  }
+};
+
 // IEEE single ops that the compiler must not contract into FMAs (the
 // reference evaluates these as separate tensor ops).
 __device__ __forceinline__ float mul_rn(float a, float b) { return __fmul_rn(a, b); }

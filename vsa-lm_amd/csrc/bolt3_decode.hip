@@ -3,21 +3,21 @@
 //
 // The step is bound by reading the window, the slots and M_res once, so it is
 // split over many workgroups (flash-decoding):
-//   decode_split_kernel, grid (NSPLIT + 1, B*HKV):
-//     workgroups 0..NSPLIT-1 each take a contiguous range of the keys
+//   decode_split_kernel, grid (ceil(keys / 128) + HD/32, B*HKV):
+//     attention workgroups take 128 keys of the list
 //     [sinks | attractor slots | window A | window B + new token] of one
-//     (batch, kv head): fp32 scores of the G query heads (q/k RMSNorm and RoPE
-//     of the new token recomputed per workgroup), a local softmax, and the
-//     value read with the probabilities rounded to the storage dtype; they
-//     leave (max, sum, unnormalised output) per head in the workspace.  The
-//     last range owns the new token: it appends its roped and un-roped key,
+//     (batch, kv head), one 32-key tile per wavefront: the key and value rows
+//     are requested first, then the queries are prepared (q/k RMSNorm, RoPE;
+//     recomputed per workgroup), S^T = K Q^T with the G query heads as MFMA
+//     columns, a local softmax per head column, and O^T = V^T P^T with the
+//     probabilities rounded to the storage dtype (V^T staged in LDS).  Each
+//     tile leaves (max, sum, unnormalised output) per head in the workspace.
+//     The workgroup holding the new token appends its roped and un-roped key,
 //     value, beta and position to the window ring.
-//     workgroup NSPLIT computes the M_res readout
-//     eta * RMSNorm(normalize(q_raw) M (1-gamma)/sqrt(HD)), rounded.
-//   decode_combine_kernel, grid (B*HKV): merges the NSPLIT partial softmaxes,
-//     rounds the attention output and adds the readout.
-// Every key or value row is read as 16-byte vectors by HD/8 lanes, several rows
-// per thread in flight.
+//     readout workgroups each multiply normalize(q_raw) by 32 rows of M_res.
+//   decode_combine_kernel, grid (B*HKV): merges the partial softmaxes, rounds
+//     the attention output, finishes the readout
+//     eta * RMSNorm(normalize(q_raw) M (1-gamma)/sqrt(HD)) and adds it.
 #include "bolt3_common.h"
 #include "bolt3_math.h"
 #include "bolt3_amd.h"
@@ -25,15 +25,20 @@
 namespace b3 {
 
 constexpr int DNT = 256;        // threads per decode workgroup
+constexpr int DWAVES = DNT / 64;
 constexpr int GMAX = 8;         // query heads per kv head
-constexpr int NSPLIT = 4;       // key ranges per (batch, kv head)
-constexpr int KCAP = 168;       // keys per range at most (4 sinks + 128 slots + two window halves of 256)
-constexpr int NKMAX = NSPLIT * KCAP;
+constexpr int KWG = 32 * DWAVES;   // keys per attention workgroup (one 32-key tile per wavefront)
+constexpr int NKMAX = 4 + 128 + 2 * 256 + 8;
+constexpr int NSPLIT_MAX = (NKMAX + KWG - 1) / KWG;
+constexpr int NPART = NSPLIT_MAX;            // partial softmax states per (batch, kv head)
+constexpr int RROWS = 32;       // rows of M_res per readout workgroup
 
-// per (bh): NSPLIT x G x (HD + 2) floats of partial softmax state, then G x HD readout floats
+// per (bh): NPART x G x (HD + 2) floats of partial softmax state, HD/RROWS x G x HD partial
+// readout floats, then G x 2 floats (1/|q_raw|, eta)
 __host__ __device__ constexpr long long dec_ws_per_bh(int G, int HD) {
-  return (long long)NSPLIT * G * (HD + 2) + (long long)G * HD;
+  return (long long)NPART * G * (HD + 2) + (long long)(HD / RROWS) * G * HD + 2LL * G;
 }
+__host__ __device__ inline int dec_nsplit(int nk) { return (nk + KWG - 1) / KWG; }
 
 template <typename T>
 __device__ __forceinline__ void load8(const T* p, float* out) {
@@ -51,370 +56,489 @@ __device__ __forceinline__ void load8(const T* p, float* out) {
 
 template <typename T, int HD>
 struct SplitSmem {
-  float q[GMAX][HD];          // roped queries (storage-dtype values)
-  float qr[GMAX][HD];         // un-roped queries after the norm
-  float kn[HD], vn[HD];       // new token's roped key and value
-  float s[GMAX][KCAP];        // scores, then probabilities of this range
-  float part[DNT / 64][GMAX][HD];   // per-wavefront partials of the value read; per row group of the readout
-  float eta[GMAX];
-  float stat[GMAX][2];
+  static constexpr int QS = sizeof(T) == 2 ? HD + 8 : HD + 4;   // query row stride (16-byte rows)
+  static constexpr int VS = sizeof(T) == 2 ? 32 + 8 : 32 + 1;   // V^T row stride of a key tile
+  alignas(16) T qt[32 * QS];      // roped queries as MFMA operand rows; rows G..31 zero
+  float qr[GMAX][HD];             // un-roped queries after the norm
+  float kn[HD], vn[HD];           // new token's roped key and value
+  float bias[DWAVES][32];         // slot bias of each wavefront's key tile
+  union {
+    T vt[DWAVES][HD * VS];        // V^T of each wavefront's key tile
+    float part[DNT / 64][GMAX][HD];   // readout row groups; per-wavefront outputs of the merge
+  } u;
+  float wm[DWAVES][GMAX], wl[DWAVES][GMAX];   // per-wavefront softmax max / sum
 };
 
 // Head preparation of the new token for G query heads (and, when `with_kv`, its key and
 // value, appended to the window ring): RMSNorm (fp32 statistic, one rounding), RoPE at `pos`
 // with per-op rounding.  HD/16 lanes per head unit, lane p owning the pairs
-// (8p..8p+7, HD/2+8p..HD/2+8p+7).
+// (8p..8p+7, HD/2+8p..HD/2+8p+7); at most one unit item per thread (G + 2 units).
+// load() requests every operand, compute() uses them: callers issue their own row loads
+// in between, so the waits of compute() do not cover those.
 template <typename T, int HD>
-__device__ void prep_token(const b3_decode_args& a, SplitSmem<T, HD>& sm, int b, int hkv, int G, bool with_kv,
-                           int tid) {
-  constexpr int HALF = HD / 2, P8 = HALF / 8;
-  const T* row = reinterpret_cast<const T*>(a.lin) + (long long)b * a.lin_row_stride;
-  const int n_units = G + (with_kv ? 2 : 0);
-  const float pos = (float)a.pos;
-  const long long wbase = (long long)b * a.w_sb + (long long)hkv * a.w_sh;
-  const int ni = a.b_start + a.b_len;   // ring index of the new token
-  for (int it = tid; it < n_units * P8; it += DNT) {
-    const int p = it % P8, u = it / P8;
-    const int kind = u < G ? 0 : (u == G ? 1 : 2);   // q, k, v
-    const int col = kind == 0 ? (hkv * G + u) * HD : (kind == 1 ? (a.H + hkv) * HD : (a.H + a.HKV + hkv) * HD);
-    float x0[8], x1[8];
-    load8<T>(row + col + 8 * p, x0);
-    load8<T>(row + col + HALF + 8 * p, x1);
+struct TokenPrep {
+  static constexpr int HALF = HD / 2, P8 = HALF / 8;
+  Vec8<T> xr0, xr1;              // raw loads, converted in compute()
+  Vec8<float> fr, wr0, wr1;
+  int p, u, kind, col;
+  bool live, norm;
+  __device__ __forceinline__ void load(const b3_decode_args& a, int b, int hkv, int G, bool with_kv, int tid) {
+    const T* row = reinterpret_cast<const T*>(a.lin) + (long long)b * a.lin_row_stride;
+    const int n_units = G + (with_kv ? 2 : 0);
+    p = tid % P8;
+    u = tid / P8;
+    live = tid < n_units * P8;
+    kind = u < G ? 0 : (u == G ? 1 : 2);   // q, k, v
+    col = kind == 0 ? (hkv * G + u) * HD : (kind == 1 ? (a.H + hkv) * HD : (a.H + a.HKV + hkv) * HD);
+    norm = kind < 2 && a.has_qk_norm;
+    if (!live) return;
+    xr0.load(row + col + 8 * p);
+    xr1.load(row + col + HALF + 8 * p);
+    fr.load(a.inv_freq + 8 * p);
+    if (norm) {
+      const float* w = kind == 0 ? a.qn_w : a.kn_w;
+      wr0.load(w + 8 * p);
+      wr1.load(w + HALF + 8 * p);
+    }
+  }
+  __device__ __forceinline__ void compute(const b3_decode_args& a, SplitSmem<T, HD>& sm, int b, int hkv) {
+    const long long wbase = (long long)b * a.w_sb + (long long)hkv * a.w_sh;
+    const int ni = a.b_start + a.b_len;   // ring index of the new token
+    float x0[8], x1[8], f[8], w0[8], w1[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      x0[e] = live ? xr0.get(e) : 0.f;
+      x1[e] = live ? xr1.get(e) : 0.f;
+      f[e] = live ? fr.get(e) : 0.f;
+      w0[e] = (live && norm) ? wr0.get(e) : 0.f;
+      w1[e] = (live && norm) ? wr1.get(e) : 0.f;
+    }
+    // the RMS statistic needs all P8 lanes of a unit: the shuffles run on every lane
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss += live ? x0[e] * x0[e] + x1[e] * x1[e] : 0.f;
+#pragma unroll
+    for (int o = P8 / 2; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    if (!live) return;
     if (kind == 2) {
       T* vo = reinterpret_cast<T*>(a.win_v) + wbase + (long long)ni * HD;
+      Vec8<T> v0, v1;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         sm.vn[8 * p + e] = x0[e];
         sm.vn[HALF + 8 * p + e] = x1[e];
-        vo[8 * p + e] = St<T>::from_f(x0[e]);
-        vo[HALF + 8 * p + e] = St<T>::from_f(x1[e]);
+        v0.set(e, x0[e]);
+        v1.set(e, x1[e]);
       }
-      continue;
+      v0.store(vo + 8 * p);
+      v1.store(vo + HALF + 8 * p);
+      return;
     }
-    if (a.has_qk_norm) {
-      float ss = 0.f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) ss += x0[e] * x0[e] + x1[e] * x1[e];
-#pragma unroll
-      for (int o = P8 / 2; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
-      const float* w = kind == 0 ? a.qn_w : a.kn_w;
+    if (norm) {
       const float r = 1.0f / sqrtf(div_rn(ss, (float)HD) + a.eps);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        x0[e] = St<T>::rnd(mul_rn(mul_rn(x0[e], r), w[8 * p + e]));
-        x1[e] = St<T>::rnd(mul_rn(mul_rn(x1[e], r), w[HALF + 8 * p + e]));
+        x0[e] = St<T>::rnd(mul_rn(mul_rn(x0[e], r), w0[e]));
+        x1[e] = St<T>::rnd(mul_rn(mul_rn(x1[e], r), w1[e]));
       }
     }
+    const float pos = (float)a.pos;
     float r0[8], r1[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       float sn, cs;
-      sincos_rope(mul_rn(pos, a.inv_freq[8 * p + e]), &sn, &cs);
+      sincos_rope(mul_rn(pos, f[e]), &sn, &cs);
       const float c = St<T>::rnd(cs), si = St<T>::rnd(sn);
       r0[e] = St<T>::rnd(add_rn(St<T>::rnd(mul_rn(x0[e], c)), St<T>::rnd(mul_rn(-x1[e], si))));
       r1[e] = St<T>::rnd(add_rn(St<T>::rnd(mul_rn(x1[e], c)), St<T>::rnd(mul_rn(x0[e], si))));
     }
     if (kind == 0) {
+      using Sm = SplitSmem<T, HD>;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        sm.q[u][8 * p + e] = r0[e];
-        sm.q[u][HALF + 8 * p + e] = r1[e];
+        sm.qt[u * Sm::QS + 8 * p + e] = St<T>::from_f(r0[e]);
+        sm.qt[u * Sm::QS + HALF + 8 * p + e] = St<T>::from_f(r1[e]);
         sm.qr[u][8 * p + e] = x0[e];
         sm.qr[u][HALF + 8 * p + e] = x1[e];
       }
     } else {
       T* kr = reinterpret_cast<T*>(a.win_kr) + wbase + (long long)ni * HD;
       T* kp = reinterpret_cast<T*>(a.win_kp) + wbase + (long long)ni * HD;
+      Vec8<T> a0, a1, b0, b1;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         sm.kn[8 * p + e] = r0[e];
         sm.kn[HALF + 8 * p + e] = r1[e];
-        kr[8 * p + e] = St<T>::from_f(x0[e]);
-        kr[HALF + 8 * p + e] = St<T>::from_f(x1[e]);
-        kp[8 * p + e] = St<T>::from_f(r0[e]);
-        kp[HALF + 8 * p + e] = St<T>::from_f(r1[e]);
+        a0.set(e, x0[e]);
+        a1.set(e, x1[e]);
+        b0.set(e, r0[e]);
+        b1.set(e, r1[e]);
       }
+      a0.store(kr + 8 * p);
+      a1.store(kr + HALF + 8 * p);
+      b0.store(kp + 8 * p);
+      b1.store(kp + HALF + 8 * p);
     }
   }
-}
+};
+
+// Key-row fragment of a 32-key tile: lane (key n = lane%32, h = lane/32) holds the K
+// sub-index 16*ks + 8*h + i (bf16) or 2*ks + h (fp32) of its key row.
+template <typename T, int HD> struct RowFrag;
+template <int HD> struct RowFrag<uint16_t, HD> {
+  static constexpr int NK = HD / 16;
+  u16x8 v[NK];
+  __device__ __forceinline__ void load(const uint16_t* row, int h) {
+#pragma unroll
+    for (int ks = 0; ks < NK; ++ks) v[ks] = *reinterpret_cast<const u16x8*>(row + 16 * ks + 8 * h);
+  }
+  __device__ __forceinline__ void zero() {
+#pragma unroll
+    for (int ks = 0; ks < NK; ++ks)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[ks][i] = 0;
+  }
+  __device__ __forceinline__ void from_lds(const float* x, int h) {
+#pragma unroll
+    for (int ks = 0; ks < NK; ++ks)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[ks][i] = f2bf(x[16 * ks + 8 * h + i]);
+  }
+  __device__ __forceinline__ float at(int ks, int i) const { return bf2f(v[ks][i]); }
+  static __device__ __forceinline__ int col(int ks, int i, int h) { return 16 * ks + 8 * h + i; }
+};
+template <int HD> struct RowFrag<float, HD> {
+  static constexpr int NK = HD / 2;
+  float v[NK];
+  __device__ __forceinline__ void load(const float* row, int h) {
+#pragma unroll
+    for (int ks = 0; ks < NK; ++ks) v[ks] = row[2 * ks + h];
+  }
+  __device__ __forceinline__ void zero() {
+#pragma unroll
+    for (int ks = 0; ks < NK; ++ks) v[ks] = 0.f;
+  }
+  __device__ __forceinline__ void from_lds(const float* x, int h) {
+#pragma unroll
+    for (int ks = 0; ks < NK; ++ks) v[ks] = x[2 * ks + h];
+  }
+};
 
 template <typename T, int HD>
 __global__ void __launch_bounds__(DNT) decode_split_kernel(b3_decode_args a) {
-  __shared__ SplitSmem<T, HD> sm;
-  constexpr int TPK = HD / 8;        // lanes per key row
-  constexpr int KPAR = DNT / TPK;    // rows per pass
-  constexpr int U = 2;               // passes in flight
-  const int split = blockIdx.x, bh = blockIdx.y, b = bh / a.HKV, hkv = bh % a.HKV;
+  using Sm = SplitSmem<T, HD>;
+  __shared__ Sm sm;
+  constexpr int NREAD = HD / RROWS;  // readout workgroups
+  constexpr int NDB = HD / 32;
+  const int bh = blockIdx.y, b = bh / a.HKV, hkv = bh % a.HKV;
   const int G = a.H / a.HKV;
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, n = lane & 31, h = lane >> 5;
   const long long wbase = (long long)b * a.w_sb + (long long)hkv * a.w_sh;
   const int ns = a.n_sink_keys, nsl = a.has_slots ? a.S : 0, na = a.a_len, nbk = a.b_len + 1;
   const int nk = ns + nsl + na + nbk;
+  const int nsplit = dec_nsplit(nk);
+  const int split = blockIdx.x;
   float* ws = a.work + (long long)bh * dec_ws_per_bh(G, HD);
+  float* ws_read = ws + NPART * G * (HD + 2);
+  float* ws_stat = ws_read + NREAD * G * HD;
   const T* row = reinterpret_cast<const T*>(a.lin) + (long long)b * a.lin_row_stride;
   const int gcol = (a.H + 2 * a.HKV) * HD;
 
-  if (split == NSPLIT) {
-    // ---------------- M_res readout
-    prep_token<T, HD>(a, sm, b, hkv, G, false, tid);
-    if (tid < G) sm.eta[tid] = St<T>::rnd(tanhf(St<T>::ld(row + gcol + a.HKV + hkv * G + tid)));
-    __syncthreads();
-    if (!a.m_res) {
-      for (int it = tid; it < G * HD; it += DNT) ws[NSPLIT * G * (HD + 2) + it] = 0.f;
-      return;
-    }
-    {
-      const int lane = tid & 63, wv = tid >> 6;
-      for (int g = wv; g < G; g += DNT / 64) {
-        float ss = 0.f;
-        for (int d = lane; d < HD; d += 64) ss += sm.qr[g][d] * sm.qr[g][d];
-        ss = wave_sum(ss);
-        if (lane == 0) sm.stat[g][0] = 1.0f / fmaxf(sqrtf(ss), 1e-12f);
-      }
-    }
-    const float* M = a.m_res + (long long)bh * HD * HD;
-    constexpr int CG = DNT / HD;   // row groups of M
+  if (split >= nsplit) {
+    // ---------------- rows [RROWS*r, RROWS*r + RROWS) of the M_res readout
+    const int r = split - nsplit;
+    constexpr int CG = DNT / HD;            // row groups
+    constexpr int RPT = RROWS / CG;         // rows per thread
     const int d = tid % HD, cg = tid / HD;
+    TokenPrep<T, HD> tp;
+    tp.load(a, b, hkv, G, false, tid);
+    float m[RPT];
+    const float* M = a.m_res ? a.m_res + (long long)bh * HD * HD : nullptr;
+#pragma unroll
+    for (int q = 0; q < RPT; ++q) m[q] = M ? M[(long long)(RROWS * r + cg + CG * q) * HD + d] : 0.f;
+    __builtin_amdgcn_sched_barrier(0);   // keep every load above issued before the first use
+    tp.compute(a, sm, b, hkv);
+    __syncthreads();
     float acc[GMAX];
 #pragma unroll
     for (int g = 0; g < GMAX; ++g) acc[g] = 0.f;
-#pragma unroll 8
-    for (int c = cg; c < HD; c += CG) {
-      const float m = M[(long long)c * HD + d];
+#pragma unroll
+    for (int q = 0; q < RPT; ++q) {
+      const int c = RROWS * r + cg + CG * q;
 #pragma unroll
       for (int g = 0; g < GMAX; ++g)
-        if (g < G) acc[g] += sm.qr[g][c] * m;
+        if (g < G) acc[g] += sm.qr[g][c] * m[q];
     }
 #pragma unroll
     for (int g = 0; g < GMAX; ++g)
-      if (g < G) sm.part[cg][g][d] = acc[g];
+      if (g < G) sm.u.part[cg][g][d] = acc[g];
     __syncthreads();
-    const float coef = div_rn(1.0f - a.gamma[hkv], sqrtf((float)HD));
     for (int it = tid; it < G * HD; it += DNT) {
-      const int g = it / HD, dd = it % HD;
       float s = 0.f;
-      for (int r = 0; r < CG; ++r) s += sm.part[r][g][dd];
-      sm.s[g][dd] = mul_rn(s * sm.stat[g][0], coef);   // scores area reused for ym
+#pragma unroll
+      for (int q = 0; q < CG; ++q) s += sm.u.part[q][it / HD][it % HD];
+      ws_read[r * G * HD + it] = s;
     }
-    __syncthreads();
-    {
-      const int lane = tid & 63, wv = tid >> 6;
-      for (int g = wv; g < G; g += DNT / 64) {
+    if (r == 0) {
+      for (int g = wave; g < G; g += DWAVES) {
         float ss = 0.f;
-        for (int dd = lane; dd < HD; dd += 64) ss += sm.s[g][dd] * sm.s[g][dd];
+        for (int dd = lane; dd < HD; dd += 64) ss += sm.qr[g][dd] * sm.qr[g][dd];
         ss = wave_sum(ss);
-        if (lane == 0) sm.stat[g][1] = 1.0f / sqrtf(div_rn(ss, (float)HD) + a.eps);
+        if (lane == 0) {
+          ws_stat[2 * g] = 1.0f / fmaxf(sqrtf(ss), 1e-12f);
+          ws_stat[2 * g + 1] = St<T>::rnd(tanhf(St<T>::ld(row + gcol + a.HKV + hkv * G + g)));
+        }
       }
-    }
-    __syncthreads();
-    for (int it = tid; it < G * HD; it += DNT) {
-      const int g = it / HD, dd = it % HD;
-      const float ymn = mul_rn(mul_rn(sm.s[g][dd], sm.stat[g][1]), a.res_w[dd]);
-      ws[NSPLIT * G * (HD + 2) + it] = St<T>::rnd(mul_rn(sm.eta[g], ymn));
     }
     return;
   }
 
-  // ---------------- attention over one key range
-  const int per = (nk + NSPLIT - 1) / NSPLIT;
-  const int k0 = split * per, k1 = min(nk, k0 + per);
-  const bool owns_new = split == (nk - 1) / per;   // the range holding the new token (key nk-1)
-  prep_token<T, HD>(a, sm, b, hkv, G, owns_new, tid);
+  // ---------------- attention: wavefront `wave` takes keys kt0 .. kt0+31 of the list
+  //   [sinks | attractor slots | window A | window B + new token]
+  const int kt0 = split * KWG + 32 * wave;
+  const int key = kt0 + n;                     // this lane's key row
+  const bool kin = key < nk;
+  const bool owns_new = split == (nk - 1) / KWG;
+  const T* kp = nullptr;
+  const T* vp = nullptr;
+  float bias_r = 0.f;
+  if (kin) {
+    int k = key;
+    if (k < ns) {
+      const long long o = (long long)b * a.s_sb + (long long)hkv * a.s_sh + (long long)k * HD;
+      kp = reinterpret_cast<const T*>(a.sink_k) + o;
+      vp = reinterpret_cast<const T*>(a.sink_v) + o;
+    } else if ((k -= ns) < nsl) {
+      kp = reinterpret_cast<const T*>(a.slot_k) + ((long long)bh * a.S + k) * HD;
+      vp = reinterpret_cast<const T*>(a.slot_v) + ((long long)bh * a.S + k) * HD;
+      bias_r = a.slot_bias[(long long)bh * a.S + k];
+    } else if ((k -= nsl) < na) {
+      kp = reinterpret_cast<const T*>(a.win_kp) + wbase + (long long)(a.a_start + k) * HD;
+      vp = reinterpret_cast<const T*>(a.win_v) + wbase + (long long)(a.a_start + k) * HD;
+    } else if ((k -= na) < a.b_len) {
+      kp = reinterpret_cast<const T*>(a.win_kp) + wbase + (long long)(a.b_start + k) * HD;
+      vp = reinterpret_cast<const T*>(a.win_v) + wbase + (long long)(a.b_start + k) * HD;
+    }   // else: the new token, prepared below
+  }
+  // loads in the order of use: the new token's operands, keys, values
+  TokenPrep<T, HD> tp;
+  tp.load(a, b, hkv, G, owns_new, tid);
+  RowFrag<T, HD> kf, vf;
+  if (kp) kf.load(kp, h);
+  else kf.zero();
+  if (vp) vf.load(vp, h);
+  else vf.zero();
+  __builtin_amdgcn_sched_barrier(0);   // keep every load above issued before the first use
+  // query rows G..31 of the operand are zero
+  for (int it = tid; it < (32 - G) * Sm::QS; it += DNT) sm.qt[G * Sm::QS + it] = St<T>::from_f(0.f);
+  tp.compute(a, sm, b, hkv);
   if (owns_new && tid == 0) {
     const float z = St<T>::ld(row + gcol + hkv);
     a.win_beta[b * a.wb_sb + hkv * a.wb_sh + a.b_start + a.b_len] = St<T>::rnd(1.0f / (1.0f + expf(-z)));
     if (bh == 0 && a.win_pos) a.win_pos[a.b_start + a.b_len] = (float)a.pos;
   }
+  if (h == 0) sm.bias[wave][n] = bias_r;
   __syncthreads();
-
-  const float scale = 1.0f / sqrtf((float)HD);
-  const T* sink_k = reinterpret_cast<const T*>(a.sink_k);
-  const T* slot_k = reinterpret_cast<const T*>(a.slot_k) + (long long)bh * a.S * HD;
-  const T* win_k = reinterpret_cast<const T*>(a.win_kp) + wbase;
-  const T* sink_v = reinterpret_cast<const T*>(a.sink_v);
-  const T* slot_v = reinterpret_cast<const T*>(a.slot_v) + (long long)bh * a.S * HD;
-  const T* win_v = reinterpret_cast<const T*>(a.win_v) + wbase;
-  // key kidx of the list -> row pointers (nullptr for the new token, held in LDS)
-  auto rows = [&](int kidx, const T*& kp, const T*& vp) {
-    int k = kidx;
-    if (k < ns) {
-      const long long o = (long long)b * a.s_sb + (long long)hkv * a.s_sh + (long long)k * HD;
-      kp = sink_k + o;
-      vp = sink_v + o;
-      return;
-    }
-    k -= ns;
-    if (k < nsl) { kp = slot_k + (long long)k * HD; vp = slot_v + (long long)k * HD; return; }
-    k -= nsl;
-    if (k < na) { kp = win_k + (long long)(a.a_start + k) * HD; vp = win_v + (long long)(a.a_start + k) * HD; return; }
-    k -= na;
-    if (k < a.b_len) { kp = win_k + (long long)(a.b_start + k) * HD; vp = win_v + (long long)(a.b_start + k) * HD; return; }
-    kp = nullptr;
-    vp = nullptr;
-  };
-
-  const int sub = tid % TPK, grp = tid / TPK;
-  const int nloc = k1 - k0;
-  // ---- scores
-  for (int base = 0; base < nloc; base += KPAR * U) {
-    float kv[U][8];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int kl = base + u * KPAR + grp;
-      const T* kp;
-      const T* vp;
-      if (kl < nloc) {
-        rows(k0 + kl, kp, vp);
-        if (kp) load8<T>(kp + 8 * sub, kv[u]);
-        else {
-#pragma unroll
-          for (int i = 0; i < 8; ++i) kv[u][i] = sm.kn[8 * sub + i];
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) kv[u][i] = 0.f;
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int kl = base + u * KPAR + grp;
-      for (int g = 0; g < G; ++g) {
-        float d = 0.f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) d += sm.q[g][8 * sub + i] * kv[u][i];
-#pragma unroll
-        for (int o = TPK / 2; o >= 1; o >>= 1) d += __shfl_xor(d, o, 64);
-        if (sub == 0 && kl < nloc) {
-          float x = mul_rn(d, scale);
-          const int kidx = k0 + kl;
-          if (kidx >= ns && kidx < ns + nsl) x = add_rn(x, a.slot_bias[(long long)bh * a.S + (kidx - ns)]);
-          sm.s[g][kl] = x;
-        }
-      }
-    }
+  if (kin && !kp) {   // the new token's key and value from LDS
+    kf.from_lds(sm.kn, h);
+    vf.from_lds(sm.vn, h);
   }
-  __syncthreads();
-  // ---- local softmax per head (one wavefront per head): p~ = exp(x - m), rounded to the storage dtype
+
+  // ---- S^T[key][head] = K . Q^T (heads as the columns)
+  f32x16 sc = zero16();
+  if constexpr (St<T>::is_bf16) {
+#pragma unroll
+    for (int ks = 0; ks < HD / 16; ++ks) {
+      const u16x8 qv = *reinterpret_cast<const u16x8*>(&sm.qt[n * Sm::QS + 16 * ks + 8 * h]);
+      mma_bf16(sc, kf.v[ks], qv);
+    }
+  } else {
+#pragma unroll 8
+    for (int ks = 0; ks < HD / 2; ++ks) mma_f32(sc, kf.v[ks], sm.qt[n * Sm::QS + 2 * ks + h]);
+  }
+  // V^T of the tile into LDS while the scores are finished
   {
-    const int lane = tid & 63, wv = tid >> 6;
-    for (int g = wv; g < G; g += DNT / 64) {
-      float mx = -INFINITY;
-      for (int k = lane; k < nloc; k += 64) mx = fmaxf(mx, sm.s[g][k]);
-      mx = wave_reduce(mx, [](float x, float y) { return fmaxf(x, y); });
-      float sum = 0.f;
-      for (int k = lane; k < nloc; k += 64) {
-        const float e = mx == -INFINITY ? 0.f : expf(sm.s[g][k] - mx);
-        sm.s[g][k] = St<T>::rnd(e);
-        sum += e;
-      }
-      sum = wave_sum(sum);
-      if (lane == 0) {
-        ws[(split * G + g) * (HD + 2) + HD] = mx;
-        ws[(split * G + g) * (HD + 2) + HD + 1] = sum;
+    T* vt = sm.u.vt[wave];
+    if constexpr (St<T>::is_bf16) {
+#pragma unroll
+      for (int ks = 0; ks < HD / 16; ++ks)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) vt[(16 * ks + 8 * h + i) * Sm::VS + n] = vf.v[ks][i];
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < HD / 2; ++ks) vt[(2 * ks + h) * Sm::VS + n] = vf.v[ks];
+    }
+  }
+  const float scale = 1.0f / sqrtf((float)HD);
+  float mx = -INFINITY;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int kr = d_row(lane, r);
+    float x = add_rn(mul_rn(sc[r], scale), sm.bias[wave][kr]);
+    x = kt0 + kr < nk ? x : -INFINITY;
+    sc[r] = x;
+    mx = fmaxf(mx, x);
+  }
+  mx = fmaxf(mx, xor32(mx));
+  float sum = 0.f;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const float e = mx == -INFINITY ? 0.f : expf(sc[r] - mx);
+    sc[r] = e;
+    sum += e;
+  }
+  sum += xor32(sum);
+  // ---- O^T[d][head] = V^T . P~^T with p~ = exp(x - max) rounded to the storage dtype
+  __syncthreads();   // V^T tiles written
+  f32x16 o[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) o[db] = zero16();
+  const T* vt = sm.u.vt[wave];
+  if constexpr (St<T>::is_bf16) {
+    u16x8 pv[2];
+#pragma unroll
+    for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) pv[kc][e] = f2bf(sc[8 * kc + e]);
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      const int d = 32 * db + n;
+#pragma unroll
+      for (int kc = 0; kc < 2; ++kc) {
+        u16x8 av;
+        const u16x4 lo = *reinterpret_cast<const u16x4*>(vt + d * Sm::VS + 16 * kc + 4 * h);
+        const u16x4 hi = *reinterpret_cast<const u16x4*>(vt + d * Sm::VS + 16 * kc + 8 + 4 * h);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) { av[e] = lo[e]; av[4 + e] = hi[e]; }
+        mma_bf16(o[db], av, pv[kc]);
       }
     }
+  } else {
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      const int d = 32 * db + n;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mma_f32(o[db], vt[d * Sm::VS + d_row(lane, r)], sc[r]);
+    }
+  }
+  // ---- merge the four tiles of the workgroup: lane column n = head, rows = features
+  if (n < G && h == 0) {
+    sm.wm[wave][n] = mx;
+    sm.wl[wave][n] = sum;
+  }
+  __syncthreads();   // every wavefront is done with its V^T tile (the union is reused below)
+  if (n < G) {
+    float m = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < DWAVES; ++w) m = fmaxf(m, sm.wm[w][n]);
+    const float f = mx == -INFINITY ? 0.f : expf(mx - m);
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4)
+        *reinterpret_cast<float4*>(&sm.u.part[wave][n][32 * db + 8 * r4 + 4 * h]) =
+            make_float4(o[db][4 * r4] * f, o[db][4 * r4 + 1] * f, o[db][4 * r4 + 2] * f, o[db][4 * r4 + 3] * f);
   }
   __syncthreads();
-  // ---- value read: o[g][d] = sum_k p~[g][k] v[k][d]
-  float acc[GMAX][8];
+  float* pw = ws + (long long)split * G * (HD + 2);
+  for (int it = tid; it < G * (HD / 4); it += DNT) {
+    const int g = it / (HD / 4), d4 = (it % (HD / 4)) * 4;
+    float4 acc4 = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-  for (int g = 0; g < GMAX; ++g)
-#pragma unroll
-    for (int i = 0; i < 8; ++i) acc[g][i] = 0.f;
-  for (int base = 0; base < nloc; base += KPAR * U) {
-    float vv[U][8];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int kl = base + u * KPAR + grp;
-      const T* kp;
-      const T* vp;
-      if (kl < nloc) {
-        rows(k0 + kl, kp, vp);
-        if (vp) load8<T>(vp + 8 * sub, vv[u]);
-        else {
-#pragma unroll
-          for (int i = 0; i < 8; ++i) vv[u][i] = sm.vn[8 * sub + i];
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) vv[u][i] = 0.f;
-      }
+    for (int w = 0; w < DWAVES; ++w) {
+      const float4 x = *reinterpret_cast<const float4*>(&sm.u.part[w][g][d4]);
+      acc4.x += x.x; acc4.y += x.y; acc4.z += x.z; acc4.w += x.w;
     }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int kl = base + u * KPAR + grp;
-      if (kl < nloc) {
-#pragma unroll
-        for (int g = 0; g < GMAX; ++g)
-          if (g < G) {
-            const float pg = sm.s[g][kl];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) acc[g][i] += pg * vv[u][i];
-          }
-      }
-    }
+    *reinterpret_cast<float4*>(pw + g * (HD + 2) + d4) = acc4;
   }
-  // reduce the KPAR row groups: the groups of one wavefront (lanes sharing `sub`) by shuffles,
-  // then the 4 wavefronts through two LDS rows
+  if (tid < G) {
+    float m = -INFINITY;
 #pragma unroll
-  for (int g = 0; g < GMAX; ++g)
-    if (g < G) {
+    for (int w = 0; w < DWAVES; ++w) m = fmaxf(m, sm.wm[w][tid]);
+    float l = 0.f;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        float x = acc[g][i];
-#pragma unroll
-        for (int o = TPK; o < 64; o <<= 1) x += __shfl_xor(x, o, 64);
-        acc[g][i] = x;
-      }
-    }
-  const int wv = tid >> 6, lane = tid & 63;
-  if (lane < TPK) {
-#pragma unroll
-    for (int g = 0; g < GMAX; ++g)
-      if (g < G) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) sm.part[wv][g][8 * sub + i] = acc[g][i];
-      }
-  }
-  __syncthreads();
-  for (int it = tid; it < G * HD; it += DNT) {
-    const int g = it / HD, d = it % HD;
-    float o = 0.f;
-#pragma unroll
-    for (int w = 0; w < DNT / 64; ++w) o += sm.part[w][g][d];
-    ws[(split * G + g) * (HD + 2) + d] = o;
+    for (int w = 0; w < DWAVES; ++w) l += sm.wm[w][tid] == -INFINITY ? 0.f : sm.wl[w][tid] * expf(sm.wm[w][tid] - m);
+    pw[tid * (HD + 2) + HD] = m;
+    pw[tid * (HD + 2) + HD + 1] = l;
   }
 }
 
-// Merge the NSPLIT partial softmaxes of one (batch, kv head), round, add the readout.
+// Merge the partial softmaxes of one (batch, kv head), round; finish and add the readout.
 template <typename T, int HD>
 __global__ void __launch_bounds__(DNT) decode_combine_kernel(b3_decode_args a) {
+  constexpr int NREAD = HD / RROWS;
+  constexpr int PER = GMAX * HD / DNT;   // outputs per thread at most
+  __shared__ float red[GMAX][DNT / 64];
   const int bh = blockIdx.x, b = bh / a.HKV, hkv = bh % a.HKV;
   const int G = a.H / a.HKV;
+  const int tid = threadIdx.x;
+  const int nk = a.n_sink_keys + (a.has_slots ? a.S : 0) + a.a_len + a.b_len + 1;
+  const int npart = dec_nsplit(nk);
   const float* ws = a.work + (long long)bh * dec_ws_per_bh(G, HD);
-  T* y = reinterpret_cast<T*>(a.y) + (long long)b * a.H * HD + (long long)hkv * G * HD;
-  for (int it = threadIdx.x; it < G * HD; it += DNT) {
-    const int g = it / HD, d = it % HD;
-    float m = -INFINITY;
+  const float* ws_read = ws + NPART * G * (HD + 2);
+  const float* ws_stat = ws_read + NREAD * G * HD;
+  const float coef = div_rn(1.0f - a.gamma[hkv], sqrtf((float)HD));
+  float att[PER], ym[PER];
 #pragma unroll
-    for (int s = 0; s < NSPLIT; ++s) m = fmaxf(m, ws[(s * G + g) * (HD + 2) + HD]);
-    float l = 0.f, o = 0.f;
+  for (int q = 0; q < PER; ++q) {
+    const int it = tid + DNT * q;
+    att[q] = 0.f;
+    ym[q] = 0.f;
+    if (it < G * HD) {
+      const int g = it / HD, d = it % HD;
+      float m = -INFINITY;
+      for (int s = 0; s < npart; ++s) m = fmaxf(m, ws[(s * G + g) * (HD + 2) + HD]);
+      float l = 0.f, o = 0.f;
+      for (int s = 0; s < npart; ++s) {
+        const float ms = ws[(s * G + g) * (HD + 2) + HD];
+        const float w = ms == -INFINITY ? 0.f : expf(ms - m);
+        l += ws[(s * G + g) * (HD + 2) + HD + 1] * w;
+        o += ws[(s * G + g) * (HD + 2) + d] * w;
+      }
+      att[q] = St<T>::rnd(o / l);
+      float r = 0.f;
 #pragma unroll
-    for (int s = 0; s < NSPLIT; ++s) {
-      const float ms = ws[(s * G + g) * (HD + 2) + HD];
-      const float w = ms == -INFINITY ? 0.f : expf(ms - m);
-      l += ws[(s * G + g) * (HD + 2) + HD + 1] * w;
-      o += ws[(s * G + g) * (HD + 2) + d] * w;
+      for (int k = 0; k < NREAD; ++k) r += ws_read[k * G * HD + it];
+      ym[q] = mul_rn(r * ws_stat[2 * g], coef);
     }
-    const float att = St<T>::rnd(o / l);
-    y[it] = St<T>::from_f(St<T>::rnd(add_rn(att, ws[NSPLIT * G * (HD + 2) + it])));
+  }
+  // mean square of ym per head: wavefront sums, then across wavefronts
+  const int lane = tid & 63, wv = tid >> 6;
+#pragma unroll
+  for (int g = 0; g < GMAX; ++g) {
+    if (g >= G) break;
+    float ss = 0.f;
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int it = tid + DNT * q;
+      if (it < G * HD && it / HD == g) ss += ym[q] * ym[q];
+    }
+    ss = wave_sum(ss);
+    if (lane == 0) red[g][wv] = ss;
+  }
+  __syncthreads();
+  T* y = reinterpret_cast<T*>(a.y) + (long long)b * a.H * HD + (long long)hkv * G * HD;
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    const int it = tid + DNT * q;
+    if (it < G * HD) {
+      const int g = it / HD, d = it % HD;
+      float ss = 0.f;
+#pragma unroll
+      for (int w = 0; w < DNT / 64; ++w) ss += red[g][w];
+      const float rs = 1.0f / sqrtf(div_rn(ss, (float)HD) + a.eps);
+      const float ymn = mul_rn(mul_rn(ym[q], rs), a.res_w[d]);
+      const float rd = a.m_res ? St<T>::rnd(mul_rn(ws_stat[2 * g + 1], ymn)) : 0.f;
+      y[it] = St<T>::from_f(St<T>::rnd(add_rn(att[q], rd)));
+    }
   }
 }
 
 template <typename T, int HD>
 static int launch_decode(const b3_decode_args& a, hipStream_t st) {
   const int BH = a.B * a.HKV;
-  hipLaunchKernelGGL((decode_split_kernel<T, HD>), dim3(NSPLIT + 1, BH), dim3(DNT), 0, st, a);
+  const int nk = a.n_sink_keys + (a.has_slots ? a.S : 0) + a.a_len + a.b_len + 1;
+  hipLaunchKernelGGL((decode_split_kernel<T, HD>), dim3(dec_nsplit(nk) + HD / RROWS, BH), dim3(DNT), 0, st, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return (int)e;
   hipLaunchKernelGGL((decode_combine_kernel<T, HD>), dim3(BH), dim3(DNT), 0, st, a);

@@ -34,8 +34,12 @@ constexpr int NPART = NSPLIT_MAX;            // partial softmax states per (batc
 constexpr int RROWS = 32;       // rows of M_res per readout workgroup
 
 // per (bh): NPART x G x (HD + 2) floats of partial softmax state, HD/RROWS x G x HD partial
-// readout floats, then G x 2 floats (1/|q_raw|, eta)
+// readout floats, G x 2 floats (1/|q_raw|, eta), then the prepared queries: G x HD roped
+// (storage dtype, in G x HD float slots) and G x HD un-roped after the norm (fp32)
 __host__ __device__ constexpr long long dec_ws_per_bh(int G, int HD) {
+  return (long long)NPART * G * (HD + 2) + (long long)(HD / RROWS) * G * HD + 2LL * G + 2LL * G * HD;
+}
+__host__ __device__ constexpr long long dec_ws_q(int G, int HD) {   // offset of the prepared queries
   return (long long)NPART * G * (HD + 2) + (long long)(HD / RROWS) * G * HD + 2LL * G;
 }
 __host__ __device__ inline int dec_nsplit(int nk) { return (nk + KWG - 1) / KWG; }
@@ -60,7 +64,6 @@ struct SplitSmem {
   static constexpr int VS = sizeof(T) == 2 ? 32 + 8 : 32 + 1;   // V^T row stride of a key tile
   alignas(16) T qt[32 * QS];      // roped queries as MFMA operand rows; rows G..31 zero
   float qr[GMAX][HD];             // un-roped queries after the norm
-  float kn[HD], vn[HD];           // new token's roped key and value
   float bias[DWAVES][32];         // slot bias of each wavefront's key tile
   union {
     T vt[DWAVES][HD * VS];        // V^T of each wavefront's key tile
@@ -69,118 +72,110 @@ struct SplitSmem {
   float wm[DWAVES][GMAX], wl[DWAVES][GMAX];   // per-wavefront softmax max / sum
 };
 
-// Head preparation of the new token for G query heads (and, when `with_kv`, its key and
-// value, appended to the window ring): RMSNorm (fp32 statistic, one rounding), RoPE at `pos`
-// with per-op rounding.  HD/16 lanes per head unit, lane p owning the pairs
-// (8p..8p+7, HD/2+8p..HD/2+8p+7); at most one unit item per thread (G + 2 units).
-// load() requests every operand, compute() uses them: callers issue their own row loads
-// in between, so the waits of compute() do not cover those.
+// Head preparation of the new token: its G query heads and its key and value, RMSNorm
+// (fp32 statistic, one rounding) and RoPE at `pos` with per-op rounding.  HD/16 lanes per
+// head unit, lane p owning the pairs (8p..8p+7, HD/2+8p..HD/2+8p+7).  The key (roped and
+// un-roped), value, beta and position go to the window ring; the roped queries (storage
+// dtype), the normalised un-roped queries (fp32), 1/|q_raw| and eta go to the workspace.
 template <typename T, int HD>
-struct TokenPrep {
-  static constexpr int HALF = HD / 2, P8 = HALF / 8;
-  Vec8<T> xr0, xr1;              // raw loads, converted in compute()
-  Vec8<float> fr, wr0, wr1;
-  int p, u, kind, col;
-  bool live, norm;
-  __device__ __forceinline__ void load(const b3_decode_args& a, int b, int hkv, int G, bool with_kv, int tid) {
-    const T* row = reinterpret_cast<const T*>(a.lin) + (long long)b * a.lin_row_stride;
-    const int n_units = G + (with_kv ? 2 : 0);
-    p = tid % P8;
-    u = tid / P8;
-    live = tid < n_units * P8;
-    kind = u < G ? 0 : (u == G ? 1 : 2);   // q, k, v
-    col = kind == 0 ? (hkv * G + u) * HD : (kind == 1 ? (a.H + hkv) * HD : (a.H + a.HKV + hkv) * HD);
-    norm = kind < 2 && a.has_qk_norm;
-    if (!live) return;
-    xr0.load(row + col + 8 * p);
-    xr1.load(row + col + HALF + 8 * p);
-    fr.load(a.inv_freq + 8 * p);
+__global__ void __launch_bounds__(128) decode_prep_kernel(b3_decode_args a) {
+  constexpr int HALF = HD / 2, P8 = HALF / 8;
+  const int bh = blockIdx.x, b = bh / a.HKV, hkv = bh % a.HKV;
+  const int G = a.H / a.HKV;
+  const int tid = threadIdx.x;
+  const T* row = reinterpret_cast<const T*>(a.lin) + (long long)b * a.lin_row_stride;
+  float* ws = a.work + (long long)bh * dec_ws_per_bh(G, HD);
+  float* ws_stat = ws + dec_ws_q(G, HD) - 2 * G;
+  T* q_rope = reinterpret_cast<T*>(ws + dec_ws_q(G, HD));
+  float* q_raw = ws + dec_ws_q(G, HD) + G * HD;
+  const long long wbase = (long long)b * a.w_sb + (long long)hkv * a.w_sh;
+  const int ni = a.b_start + a.b_len;   // ring index of the new token
+  const int gcol = (a.H + 2 * a.HKV) * HD;
+  const int p = tid % P8, u = tid / P8;
+  const bool live = u < G + 2;
+  const int kind = u < G ? 0 : (u == G ? 1 : 2);   // q, k, v
+  const int col = kind == 0 ? (hkv * G + u) * HD : (kind == 1 ? (a.H + hkv) * HD : (a.H + a.HKV + hkv) * HD);
+  const bool norm = kind < 2 && a.has_qk_norm;
+  float x0[8], x1[8], f[8], w0[8], w1[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) { x0[e] = 0.f; x1[e] = 0.f; f[e] = 0.f; w0[e] = 0.f; w1[e] = 0.f; }
+  if (live) {
+    load8<T>(row + col + 8 * p, x0);
+    load8<T>(row + col + HALF + 8 * p, x1);
+    load8<float>(a.inv_freq + 8 * p, f);
     if (norm) {
       const float* w = kind == 0 ? a.qn_w : a.kn_w;
-      wr0.load(w + 8 * p);
-      wr1.load(w + HALF + 8 * p);
+      load8<float>(w + 8 * p, w0);
+      load8<float>(w + HALF + 8 * p, w1);
     }
   }
-  __device__ __forceinline__ void compute(const b3_decode_args& a, SplitSmem<T, HD>& sm, int b, int hkv) {
-    const long long wbase = (long long)b * a.w_sb + (long long)hkv * a.w_sh;
-    const int ni = a.b_start + a.b_len;   // ring index of the new token
-    float x0[8], x1[8], f[8], w0[8], w1[8];
+  // the RMS statistic needs all P8 lanes of a unit: the shuffles run on every lane
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ss += x0[e] * x0[e] + x1[e] * x1[e];
+#pragma unroll
+  for (int o = P8 / 2; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+  if (norm) {
+    const float r = 1.0f / sqrtf(div_rn(ss, (float)HD) + a.eps);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      x0[e] = live ? xr0.get(e) : 0.f;
-      x1[e] = live ? xr1.get(e) : 0.f;
-      f[e] = live ? fr.get(e) : 0.f;
-      w0[e] = (live && norm) ? wr0.get(e) : 0.f;
-      w1[e] = (live && norm) ? wr1.get(e) : 0.f;
+      x0[e] = St<T>::rnd(mul_rn(mul_rn(x0[e], r), w0[e]));
+      x1[e] = St<T>::rnd(mul_rn(mul_rn(x1[e], r), w1[e]));
     }
-    // the RMS statistic needs all P8 lanes of a unit: the shuffles run on every lane
-    float ss = 0.f;
+  }
+  // |q_raw| after the norm, for the readout
+  float qq = 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) ss += live ? x0[e] * x0[e] + x1[e] * x1[e] : 0.f;
+  for (int e = 0; e < 8; ++e) qq += x0[e] * x0[e] + x1[e] * x1[e];
 #pragma unroll
-    for (int o = P8 / 2; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
-    if (!live) return;
+  for (int o = P8 / 2; o >= 1; o >>= 1) qq += __shfl_xor(qq, o, 64);
+  if (live) {
     if (kind == 2) {
-      T* vo = reinterpret_cast<T*>(a.win_v) + wbase + (long long)ni * HD;
       Vec8<T> v0, v1;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        sm.vn[8 * p + e] = x0[e];
-        sm.vn[HALF + 8 * p + e] = x1[e];
-        v0.set(e, x0[e]);
-        v1.set(e, x1[e]);
-      }
+      for (int e = 0; e < 8; ++e) { v0.set(e, x0[e]); v1.set(e, x1[e]); }
+      T* vo = reinterpret_cast<T*>(a.win_v) + wbase + (long long)ni * HD;
       v0.store(vo + 8 * p);
       v1.store(vo + HALF + 8 * p);
-      return;
-    }
-    if (norm) {
-      const float r = 1.0f / sqrtf(div_rn(ss, (float)HD) + a.eps);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        x0[e] = St<T>::rnd(mul_rn(mul_rn(x0[e], r), w0[e]));
-        x1[e] = St<T>::rnd(mul_rn(mul_rn(x1[e], r), w1[e]));
-      }
-    }
-    const float pos = (float)a.pos;
-    float r0[8], r1[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float sn, cs;
-      sincos_rope(mul_rn(pos, f[e]), &sn, &cs);
-      const float c = St<T>::rnd(cs), si = St<T>::rnd(sn);
-      r0[e] = St<T>::rnd(add_rn(St<T>::rnd(mul_rn(x0[e], c)), St<T>::rnd(mul_rn(-x1[e], si))));
-      r1[e] = St<T>::rnd(add_rn(St<T>::rnd(mul_rn(x1[e], c)), St<T>::rnd(mul_rn(x0[e], si))));
-    }
-    if (kind == 0) {
-      using Sm = SplitSmem<T, HD>;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        sm.qt[u * Sm::QS + 8 * p + e] = St<T>::from_f(r0[e]);
-        sm.qt[u * Sm::QS + HALF + 8 * p + e] = St<T>::from_f(r1[e]);
-        sm.qr[u][8 * p + e] = x0[e];
-        sm.qr[u][HALF + 8 * p + e] = x1[e];
-      }
     } else {
-      T* kr = reinterpret_cast<T*>(a.win_kr) + wbase + (long long)ni * HD;
-      T* kp = reinterpret_cast<T*>(a.win_kp) + wbase + (long long)ni * HD;
-      Vec8<T> a0, a1, b0, b1;
+      const float pos = (float)a.pos;
+      Vec8<T> r0, r1, u0, u1;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        sm.kn[8 * p + e] = r0[e];
-        sm.kn[HALF + 8 * p + e] = r1[e];
-        a0.set(e, x0[e]);
-        a1.set(e, x1[e]);
-        b0.set(e, r0[e]);
-        b1.set(e, r1[e]);
+        float sn, cs;
+        sincos_rope(mul_rn(pos, f[e]), &sn, &cs);
+        const float c = St<T>::rnd(cs), si = St<T>::rnd(sn);
+        r0.set(e, add_rn(St<T>::rnd(mul_rn(x0[e], c)), St<T>::rnd(mul_rn(-x1[e], si))));
+        r1.set(e, add_rn(St<T>::rnd(mul_rn(x1[e], c)), St<T>::rnd(mul_rn(x0[e], si))));
+        u0.set(e, x0[e]);
+        u1.set(e, x1[e]);
       }
-      a0.store(kr + 8 * p);
-      a1.store(kr + HALF + 8 * p);
-      b0.store(kp + 8 * p);
-      b1.store(kp + HALF + 8 * p);
+      if (kind == 0) {
+        r0.store(q_rope + u * HD + 8 * p);
+        r1.store(q_rope + u * HD + HALF + 8 * p);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          q_raw[u * HD + 8 * p + e] = x0[e];
+          q_raw[u * HD + HALF + 8 * p + e] = x1[e];
+        }
+        if (p == 0) ws_stat[2 * u] = 1.0f / fmaxf(sqrtf(qq), 1e-12f);
+      } else {
+        T* kr = reinterpret_cast<T*>(a.win_kr) + wbase + (long long)ni * HD;
+        T* kp = reinterpret_cast<T*>(a.win_kp) + wbase + (long long)ni * HD;
+        u0.store(kr + 8 * p);
+        u1.store(kr + HALF + 8 * p);
+        r0.store(kp + 8 * p);
+        r1.store(kp + HALF + 8 * p);
+      }
     }
   }
-};
+  if (tid < G) ws_stat[2 * tid + 1] = St<T>::rnd(tanhf(St<T>::ld(row + gcol + a.HKV + hkv * G + tid)));
+  if (tid == G) {
+    const float z = St<T>::ld(row + gcol + hkv);
+    a.win_beta[b * a.wb_sb + hkv * a.wb_sh + ni] = St<T>::rnd(1.0f / (1.0f + expf(-z)));
+    if (bh == 0 && a.win_pos) a.win_pos[ni] = (float)a.pos;
+  }
+}
 
 // Key-row fragment of a 32-key tile: lane (key n = lane%32, h = lane/32) holds the K
 // sub-index 16*ks + 8*h + i (bf16) or 2*ks + h (fp32) of its key row.
@@ -250,14 +245,12 @@ __global__ void __launch_bounds__(DNT) decode_split_kernel(b3_decode_args a) {
     constexpr int CG = DNT / HD;            // row groups
     constexpr int RPT = RROWS / CG;         // rows per thread
     const int d = tid % HD, cg = tid / HD;
-    TokenPrep<T, HD> tp;
-    tp.load(a, b, hkv, G, false, tid);
     float m[RPT];
     const float* M = a.m_res ? a.m_res + (long long)bh * HD * HD : nullptr;
 #pragma unroll
     for (int q = 0; q < RPT; ++q) m[q] = M ? M[(long long)(RROWS * r + cg + CG * q) * HD + d] : 0.f;
-    __builtin_amdgcn_sched_barrier(0);   // keep every load above issued before the first use
-    tp.compute(a, sm, b, hkv);
+    const float* q_raw = ws + dec_ws_q(G, HD) + G * HD;
+    for (int it = tid; it < G * HD; it += DNT) sm.qr[it / HD][it % HD] = q_raw[it];
     __syncthreads();
     float acc[GMAX];
 #pragma unroll
@@ -279,17 +272,6 @@ __global__ void __launch_bounds__(DNT) decode_split_kernel(b3_decode_args a) {
       for (int q = 0; q < CG; ++q) s += sm.u.part[q][it / HD][it % HD];
       ws_read[r * G * HD + it] = s;
     }
-    if (r == 0) {
-      for (int g = wave; g < G; g += DWAVES) {
-        float ss = 0.f;
-        for (int dd = lane; dd < HD; dd += 64) ss += sm.qr[g][dd] * sm.qr[g][dd];
-        ss = wave_sum(ss);
-        if (lane == 0) {
-          ws_stat[2 * g] = 1.0f / fmaxf(sqrtf(ss), 1e-12f);
-          ws_stat[2 * g + 1] = St<T>::rnd(tanhf(St<T>::ld(row + gcol + a.HKV + hkv * G + g)));
-        }
-      }
-    }
     return;
   }
 
@@ -298,7 +280,6 @@ __global__ void __launch_bounds__(DNT) decode_split_kernel(b3_decode_args a) {
   const int kt0 = split * KWG + 32 * wave;
   const int key = kt0 + n;                     // this lane's key row
   const bool kin = key < nk;
-  const bool owns_new = split == (nk - 1) / KWG;
   const T* kp = nullptr;
   const T* vp = nullptr;
   float bias_r = 0.f;
@@ -315,34 +296,33 @@ __global__ void __launch_bounds__(DNT) decode_split_kernel(b3_decode_args a) {
     } else if ((k -= nsl) < na) {
       kp = reinterpret_cast<const T*>(a.win_kp) + wbase + (long long)(a.a_start + k) * HD;
       vp = reinterpret_cast<const T*>(a.win_v) + wbase + (long long)(a.a_start + k) * HD;
-    } else if ((k -= na) < a.b_len) {
+    } else {   // window B, the new token (appended by decode_prep_kernel) included
+      k -= na;
       kp = reinterpret_cast<const T*>(a.win_kp) + wbase + (long long)(a.b_start + k) * HD;
       vp = reinterpret_cast<const T*>(a.win_v) + wbase + (long long)(a.b_start + k) * HD;
-    }   // else: the new token, prepared below
+    }
   }
-  // loads in the order of use: the new token's operands, keys, values
-  TokenPrep<T, HD> tp;
-  tp.load(a, b, hkv, G, owns_new, tid);
   RowFrag<T, HD> kf, vf;
   if (kp) kf.load(kp, h);
   else kf.zero();
   if (vp) vf.load(vp, h);
   else vf.zero();
-  __builtin_amdgcn_sched_barrier(0);   // keep every load above issued before the first use
-  // query rows G..31 of the operand are zero
-  for (int it = tid; it < (32 - G) * Sm::QS; it += DNT) sm.qt[G * Sm::QS + it] = St<T>::from_f(0.f);
-  tp.compute(a, sm, b, hkv);
-  if (owns_new && tid == 0) {
-    const float z = St<T>::ld(row + gcol + hkv);
-    a.win_beta[b * a.wb_sb + hkv * a.wb_sh + a.b_start + a.b_len] = St<T>::rnd(1.0f / (1.0f + expf(-z)));
-    if (bh == 0 && a.win_pos) a.win_pos[a.b_start + a.b_len] = (float)a.pos;
+  // query rows: G prepared rows from the workspace, rows G..31 zero
+  {
+    const T* qsrc = reinterpret_cast<const T*>(ws + dec_ws_q(G, HD));
+    for (int it = tid; it < 32 * (HD / 8); it += DNT) {
+      const int rr = it / (HD / 8), c8 = (it % (HD / 8)) * 8;
+      Vec8<T> x;
+      if (rr < G) x.load(qsrc + rr * HD + c8);
+      else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x.set(e, 0.f);
+      }
+      x.store(&sm.qt[rr * Sm::QS + c8]);
+    }
   }
   if (h == 0) sm.bias[wave][n] = bias_r;
   __syncthreads();
-  if (kin && !kp) {   // the new token's key and value from LDS
-    kf.from_lds(sm.kn, h);
-    vf.from_lds(sm.vn, h);
-  }
 
   // ---- S^T[key][head] = K . Q^T (heads as the columns)
   f32x16 sc = zero16();
@@ -538,6 +518,9 @@ template <typename T, int HD>
 static int launch_decode(const b3_decode_args& a, hipStream_t st) {
   const int BH = a.B * a.HKV;
   const int nk = a.n_sink_keys + (a.has_slots ? a.S : 0) + a.a_len + a.b_len + 1;
+  hipLaunchKernelGGL((decode_prep_kernel<T, HD>), dim3(BH), dim3(128), 0, st, a);
+  hipError_t e0 = hipGetLastError();
+  if (e0 != hipSuccess) return (int)e0;
   hipLaunchKernelGGL((decode_split_kernel<T, HD>), dim3(dec_nsplit(nk) + HD / RROWS, BH), dim3(DNT), 0, st, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return (int)e;

@@ -80,7 +80,8 @@ def bench_prefill(mod, dev, steps, warmup):
         kt = _abi.timings()
         _abi.set_timing(False)
     ms = (t1 - t0) * 1e3 / steps
-    kern = {k: sum(v) / len(v) for k, v in kt.items()}
+    # per entry point: milliseconds per forward (sum over its launches) and launches per forward
+    kern = {k: (sum(v) / steps, len(v) / steps) for k, v in kt.items()}
     return ms, kern
 
 
@@ -133,15 +134,30 @@ def bench_decode(dev, n_sets, n_steps, prefill_tokens=8192, batch=64):
         consolidation_us=round(sum(cons_ms) / max(1, len(cons_ms)) * 1e3, 2) if cons_ms else None,
         consolidations=len(cons_ms),
         avg_window=round(avg_win, 1),
-        decode_kernel_bytes=int(bytes_launch),
-        decode_kernel_GBps=round(bytes_launch / (dec_avg * 1e-3) / 1e9, 1),
-        decode_kernel_frac_hbm=round(bytes_launch / (dec_avg * 1e-3) / PEAK_HBM, 4),
         tokens_per_s=round(batch * 1e6 / step_us, 1),
+        roofline=dict(bound="hbm", achieved=round(bytes_launch / (dec_avg * 1e-3) / 1e9, 1),
+                      peak=PEAK_HBM / 1e9, unit="GB/s",
+                      frac=round(bytes_launch / (dec_avg * 1e-3) / PEAK_HBM, 4),
+                      traffic=measured_traffic("bolt3_decode"), kernel="bolt3_decode",
+                      algorithmic_bytes=int(bytes_launch), avg_launch_ms=round(dec_avg, 5)),
     )
 
 
-def cpu_baseline(sample_T=4096):
-    """The CPU oracle (torch restatement of the reference) on one sequence of the workload."""
+def measured_traffic(entry: str):
+    """HBM bytes per launch of an entry point from the rocprofv3 PMC summary committed under
+    profiles/ (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel calibration), or None."""
+    f = os.path.join(REPO, "profiles", "pmc_traffic.json")
+    if not os.path.exists(f):
+        return None
+    with open(f) as fh:
+        rec = json.load(fh).get(entry)
+    return None if rec is None else rec.get("bytes_per_launch")
+
+
+def cpu_baseline(min_s=10.0, max_s=30.0):
+    """The CPU oracle (the torch restatement of the reference path, oracle/bolt3_oracle.py) on the
+    full cfg2 forward (B=4, T=4096, same module layout and dtype), repeated until at least
+    ``min_s`` seconds of CPU work (a repeat is skipped when it would pass ``max_s``)."""
     import torch
     import recipes
     from oracle import bolt3_oracle as O
@@ -149,16 +165,22 @@ def cpu_baseline(sample_T=4096):
     torch.set_num_threads(cores)
     mod = build_layer(None)[0]
     p = O.Bolt3Params.from_module(mod)
-    x = recipes.hidden(SEED, 1, sample_T, CFG["dim"]).to(torch.bfloat16)
+    x = recipes.hidden(SEED, B, T, CFG["dim"]).to(torch.bfloat16)
     with torch.no_grad():
-        O.forward(p, x[:, :256])
-        t0 = time.perf_counter()
-        O.forward(p, x)
-        dt = time.perf_counter() - t0
-    return dict(value=round(sample_T / dt, 1), unit="tokens/s", cores=cores, kind="port",
-                sample=f"oracle/bolt3_oracle.forward on B=1 T={sample_T} of the cfg2 workload (bf16, "
-                       f"torch CPU, {cores} threads, {platform.processor() or platform.machine()}), "
-                       f"{dt:.1f} s")
+        O.forward(p, x[:1, :256])
+        runs, total = 0, 0.0
+        while total < min_s:
+            t0 = time.perf_counter()
+            O.forward(p, x)
+            dt = time.perf_counter() - t0
+            runs += 1
+            total += dt
+            if total + dt > max_s:
+                break
+    return dict(value=round(runs * B * T / total, 1), unit="tokens/s", cores=cores, kind="port",
+                sample=f"oracle/bolt3_oracle.forward on the full cfg2 workload (B={B}, T={T}, bf16 projections, "
+                       f"fp32 Bolt-3 params), {runs} forward(s) in {total:.1f} s, torch CPU with {cores} threads "
+                       f"({platform.processor() or platform.machine()})")
 
 
 def main():
@@ -170,6 +192,9 @@ def main():
     ap.add_argument("--decode-sets", type=int, default=4)
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="first run a plain elementwise copy of 256 MiB (fp32 negate) three times, the known-size "
+                         "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -180,26 +205,42 @@ def main():
 
     import torch
     dev = torch.device("cuda:0")
+    if args.calibrate_copy:
+        src = torch.ones(64 << 20, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
     _, mod = build_layer(dev)
     ms, kern = bench_prefill(mod, dev, args.steps, args.warmup)
     fl = prefill_flops(B, T)
     total = sum(fl.values())
-    kernels = {
-        "bolt3_chunk_attn": dict(ms=round(kern.get("bolt3_chunk_attn", 0), 4), flops=fl["attn"] + fl["readout"]),
-        "bolt3_chain": dict(ms=round(kern.get("bolt3_chain", 0), 4), flops=fl["consolidation"]),
-        "bolt3_heads": dict(ms=round(kern.get("bolt3_heads", 0), 4), flops=0),
-    }
-    dom = max(kernels, key=lambda k: kernels[k]["ms"])
+    # entry points: algorithmic work per forward (FLOPs, or bytes for the head preparation)
+    work = {"bolt3_chunk_attn": ("mfma", fl["attn"] + fl["readout"]),
+            "bolt3_chain": ("mfma", fl["consolidation"]),
+            "bolt3_heads": ("hbm", B * T * (6184 * 2 + (32 * 2 + 8 * 3) * 128 * 2 + 40 * 4))}
+    kernels = {}
+    for k, (bound, w) in work.items():
+        ms_k, calls = kern.get(k, (0.0, 0.0))
+        kernels[k] = dict(ms_per_forward=round(ms_k, 4), launches_per_forward=calls, bound=bound,
+                          **({"flops": w} if bound == "mfma" else {"bytes": w}))
+    dom = max(kernels, key=lambda k: kernels[k]["ms_per_forward"])
     d = kernels[dom]
-    if dom == "bolt3_heads":
-        bytes_ = B * T * (6184 * 2 + (32 * 2 + 8 * 3) * 128 * 2 + 40 * 4)
-        roof = dict(bound="hbm", achieved=round(bytes_ / (d["ms"] * 1e-3) / 1e9, 1), peak=8000.0, unit="GB/s",
-                    frac=round(bytes_ / (d["ms"] * 1e-3) / PEAK_HBM, 4), traffic=None)
+    bound, w = work[dom]
+    n_launch = max(1.0, d["launches_per_forward"])
+    per_launch_s = d["ms_per_forward"] * 1e-3 / n_launch
+    if bound == "hbm":
+        ach = w / n_launch / per_launch_s
+        roof = dict(bound="hbm", achieved=round(ach / 1e9, 1), peak=PEAK_HBM / 1e9, unit="GB/s",
+                    frac=round(ach / PEAK_HBM, 4))
     else:
-        ach = d["flops"] / (d["ms"] * 1e-3)
+        ach = w / n_launch / per_launch_s
         roof = dict(bound="mfma", achieved=round(ach / 1e12, 2), peak=PEAK_BF16 / 1e12, unit="TFLOP/s",
-                    frac=round(ach / PEAK_BF16, 4), traffic=None)
+                    frac=round(ach / PEAK_BF16, 4))
+    roof["traffic"] = measured_traffic(dom)
     roof["kernel"] = dom
+    roof["avg_launch_ms"] = round(per_launch_s * 1e3, 4)
     out = {
         "metric": METRIC,
         "value": round(B * T / (ms * 1e-3), 1),

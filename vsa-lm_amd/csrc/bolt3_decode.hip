@@ -2,19 +2,21 @@
 // Bolt3Decoder.step, vsa_lm/config/bolt3.py:346-402).
 //
 // The step is bound by reading the window, the slots and M_res once, so it is
-// split over many workgroups (flash-decoding):
+// split over many workgroups (flash-decoding), in three kernels:
+//   decode_prep_kernel, grid (B*HKV): head preparation of the new token (q/k
+//     RMSNorm, RoPE, beta/eta gates); appends its roped and un-roped key,
+//     value, beta and position to the window ring and leaves the roped and
+//     normalised un-roped queries, 1/|q_raw| and eta in the workspace.
 //   decode_split_kernel, grid (ceil(keys / 128) + HD/32, B*HKV):
 //     attention workgroups take 128 keys of the list
-//     [sinks | attractor slots | window A | window B + new token] of one
+//     [sinks | attractor slots | window A | window B | new token] of one
 //     (batch, kv head), one 32-key tile per wavefront: the key and value rows
-//     are requested first, then the queries are prepared (q/k RMSNorm, RoPE;
-//     recomputed per workgroup), S^T = K Q^T with the G query heads as MFMA
-//     columns, a local softmax per head column, and O^T = V^T P^T with the
-//     probabilities rounded to the storage dtype (V^T staged in LDS).  Each
-//     tile leaves (max, sum, unnormalised output) per head in the workspace.
-//     The workgroup holding the new token appends its roped and un-roped key,
-//     value, beta and position to the window ring.
-//     readout workgroups each multiply normalize(q_raw) by 32 rows of M_res.
+//     are requested first, then S^T = K Q^T with the G query heads as MFMA
+//     columns, a softmax per head column, and O^T = V^T P^T with the
+//     probabilities rounded to the storage dtype (V^T staged in LDS).  The
+//     four tiles of a workgroup are merged in LDS and leave one
+//     (max, sum, unnormalised output) per head in the workspace.
+//     Readout workgroups each multiply normalize(q_raw) by 32 rows of M_res.
 //   decode_combine_kernel, grid (B*HKV): merges the partial softmaxes, rounds
 //     the attention output, finishes the readout
 //     eta * RMSNorm(normalize(q_raw) M (1-gamma)/sqrt(HD)) and adds it.

@@ -118,6 +118,12 @@ typedef struct {
   float* log;                 /* optional decision log [n_steps][bh][B3_LOG_ROWS][B3_LOG_COLS] */
   void* work;                 /* scratch of >= bolt3_chain_workspace_bytes(...) bytes */
   int64_t work_bytes;
+  /* 0: the whole chain; 1: the slot decisions only (the slot state, snap_k / snap_v / snap_bias, the
+     log and the delta-rule weights in `work`); 2: the Gershgorin scales and the M_res updates
+     (m_res, snap_m) of the steps that a phase-1 call with the same arguments and the same `work`
+     decided.  Phase 2 may run concurrently with the phase-1 call of the next steps when that call
+     uses another `work` buffer. */
+  int32_t phase;
 } b3_chain_args;
 
 /*
@@ -176,6 +182,9 @@ typedef struct {
      that state, then the readout.  partial: [B][H][n_q][HD + 4] floats. */
   int32_t part;
   float* partial;
+  /* mode 0, bf16: only chunks [chunk_begin, chunk_end) (chunk_end == 0: to the last chunk), so that
+     the slot field of early chunks can run while the chain still works on later steps */
+  int32_t chunk_begin, chunk_end;
 } b3_attn_args;
 
 /*
@@ -225,8 +234,9 @@ typedef struct {
 /*
  * One-token decode step of a Bolt-3 layer: head prep for the new token, append to
  * the window ring, attention over sinks + slots + window in fp32 scores, M_res
- * readout.  Two kernels on the stream: key ranges of every (batch, kv head) in
- * parallel plus the readout, then the merge of the ranges.
+ * readout.  Three kernels on the stream: the new token's head preparation, the key
+ * ranges of every (batch, kv head) in parallel plus the readout, then the merge of
+ * the ranges.
  * Replaces vsa_lm/config/bolt3.py:346-402 for t_s == 1.
  */
 int bolt3_decode(const b3_decode_args* a, void* stream);

@@ -54,7 +54,7 @@ class ChainArgs(C.Structure):
         ("ak", p), ("av", p), ("mass", p), ("util", p), ("pm", p), ("act", p), ("m_res", p),
         ("kappa", p), ("gamma", p), ("inv_freq", p),
         ("snap_k", p), ("snap_v", p), ("snap_bias", p), ("snap_m", p), ("log", p),
-        ("work", p), ("work_bytes", i64),
+        ("work", p), ("work_bytes", i64), ("phase", i32),
     ]
 
 
@@ -71,7 +71,7 @@ class AttnArgs(C.Structure):
         ("m_res", p), ("m_step", i64), ("m_split", i32),
         ("gamma", p), ("res_w", p), ("eps", f32),
         ("y", p), ("y_sb", i64), ("y_st", i64),
-        ("part", i32), ("partial", p),
+        ("part", i32), ("partial", p), ("chunk_begin", i32), ("chunk_end", i32),
     ]
 
 

@@ -37,12 +37,25 @@ def _require_gpu(t: torch.Tensor, what: str):
 _SIDE_STREAMS: dict = {}
 
 
-def _side_stream(dev: torch.device) -> torch.cuda.Stream:
-    """One extra stream per device (default priority) for the consolidation chain."""
-    key = dev.index if dev.index is not None else torch.cuda.current_device()
+def _side_stream(dev: torch.device, i: int = 0) -> torch.cuda.Stream:
+    """Extra streams per device (default priority): 0 for the chain's slot decisions, 1 for its
+    M_res updates."""
+    key = (dev.index if dev.index is not None else torch.cuda.current_device(), i)
     if key not in _SIDE_STREAMS:
         _SIDE_STREAMS[key] = torch.cuda.Stream(device=dev)
     return _SIDE_STREAMS[key]
+
+
+# The forward's consolidation steps are issued in this many groups, so that the slot field and
+# readout of early chunks run while the chain still decides later steps.
+CHAIN_GROUPS = 4
+
+
+def _step_groups(n: int, k: int) -> list[tuple[int, int]]:
+    """Split steps [0, n) into at most k contiguous, nearly equal ranges."""
+    k = max(1, min(k, n))
+    bounds = [n * i // k for i in range(k + 1)]
+    return [(bounds[i], bounds[i + 1]) for i in range(k) if bounds[i + 1] > bounds[i]]
 
 
 class _NoBackward(torch.autograd.Function):
@@ -191,9 +204,10 @@ class Bolt3Attn(nn.Module):
 
     def _chain(self, dt, device, B, kr, kp, v, tok_bh_stride, pos, beta, beta_bh_stride, n_steps, off0, len0,
                step_stride, step_len, n_filled, st: dict, m_res, gam, side, snap_k=None, snap_v=None,
-               snap_bias=None, snap_m=None, log=None, kp_exact=False):
-        work = torch.empty(A.chain_workspace_bytes(dt, B, self.HKV, self.HD, self.S, n_steps), dtype=torch.uint8,
-                           device=device)
+               snap_bias=None, snap_m=None, log=None, kp_exact=False, phase=0, work=None):
+        if work is None:
+            work = torch.empty(A.chain_workspace_bytes(dt, B, self.HKV, self.HD, self.S, n_steps),
+                               dtype=torch.uint8, device=device)
         a = A.ChainArgs()
         a.dtype, a.B, a.HKV, a.HD, a.S = A.dtype_code(dt), B, self.HKV, self.HD, self.S
         a.kr, a.kp, a.v, a.tok_bh_stride = kr, kp, v, tok_bh_stride
@@ -207,6 +221,7 @@ class Bolt3Attn(nn.Module):
         a.snap_k, a.snap_v, a.snap_bias, a.snap_m = A.ptr(snap_k), A.ptr(snap_v), A.ptr(snap_bias), A.ptr(snap_m)
         a.log = A.ptr(log)
         a.work, a.work_bytes = work.data_ptr(), work.numel()
+        a.phase = phase
         A.call("bolt3_chain", a, device)
 
     def _empty_slots(self, bh, dt, device):
@@ -251,9 +266,15 @@ class Bolt3Attn(nn.Module):
         n_cons = max(0, n_chunks - 2)
         bh = b * HKV
         snaps = (None, None, None, None)
-        chain_stream = None
+        split = n_cons > 0 and dt == torch.bfloat16
+        # bf16: the chain's steps go out in groups; the slot decisions of a group run on one side
+        # stream, its Gershgorin scales and M_res updates on another, and the main stream adds the
+        # slot field and readout of a group's chunks as soon as that group is done
+        groups = _step_groups(n_cons, CHAIN_GROUPS if split else 1) if n_cons > 0 else []
+        done = []   # per group: event after its M_res updates
         if n_cons > 0:
-            chain_stream = _side_stream(dev)
+            s_dec = _side_stream(dev, 0)
+            s_m = _side_stream(dev, 1) if split else s_dec
             # n_filled = 0: the chain builds the empty state itself, these are outputs only
             st = dict(ak=torch.empty(bh, S, HD, dtype=dt, device=dev), av=torch.empty(bh, S, HD, dtype=dt, device=dev),
                       mass=torch.empty(bh, S, device=dev), util=torch.empty(bh, S, device=dev),
@@ -267,11 +288,34 @@ class Bolt3Attn(nn.Module):
             log = None
             if trace is not None:
                 log = torch.zeros(n_cons, bh, A.LOG_ROWS, A.LOG_COLS, device=dev)
-            chain_stream.wait_stream(main)   # after the state initialisation enqueued above
-            with torch.cuda.stream(chain_stream):
-                self._chain(dt, dev, b, k_raw.data_ptr(), k_rope.data_ptr(), v.data_ptr(), T * HD,
-                            pos.data_ptr(), beta.data_ptr(), T, n_cons, ns, C - ns, C, C, 0, st, m_res, gam, side,
-                            *snaps, log=log, kp_exact=True)
+            works = [torch.empty(A.chain_workspace_bytes(dt, b, HKV, HD, S, s1 - s0), dtype=torch.uint8, device=dev)
+                     for s0, s1 in groups]
+            s_dec.wait_stream(main)   # after the head preparation and the allocations above
+            esz = k_raw.element_size()
+            nf = 0
+            for (s0, s1), work in zip(groups, works):
+                # step 0 takes the first chunk after its sinks; step i > 0 takes chunk i
+                tok = s0 * C
+                off0, len0 = (ns, C - ns) if s0 == 0 else (0, C)
+                args = (dt, dev, b, k_raw.data_ptr() + tok * HD * esz, k_rope.data_ptr() + tok * HD * esz,
+                        v.data_ptr() + tok * HD * esz, T * HD, pos.data_ptr() + tok * 4, beta.data_ptr() + tok * 4,
+                        T, s1 - s0, off0, len0, C, C, nf, st, m_res, gam, side,
+                        *(t[s0:s1] for t in snaps))
+                kw = dict(log=None if log is None else log[s0:s1], kp_exact=True, work=work)
+                if split:
+                    with torch.cuda.stream(s_dec):
+                        self._chain(*args, phase=1, **kw)
+                    s_m.wait_stream(s_dec)
+                    with torch.cuda.stream(s_m):
+                        self._chain(*args, phase=2, **kw)
+                else:
+                    with torch.cuda.stream(s_dec):
+                        self._chain(*args, **kw)
+                ev = torch.cuda.Event()
+                ev.record(s_m)
+                done.append(ev)
+                for i in range(s0, s1):   # filled slots after each step depend only on the token counts
+                    nf = min(S, nf + (C - ns if i == 0 else C))
             if trace is not None:
                 trace.update(state=st, m_res=m_res, snap_k=snaps[0], snap_v=snaps[1], snap_bias=snaps[2],
                              snap_m=snaps[3], log=log)
@@ -297,18 +341,20 @@ class Bolt3Attn(nn.Module):
             a.m_split = int(dt == torch.bfloat16)
         a.gamma, a.res_w, a.eps = gam.data_ptr(), side["res_w"].data_ptr(), float(self.res_norm.eps)
         a.y, a.y_sb, a.y_st = y.data_ptr(), y.stride(0), y.stride(1)
-        if chain_stream is not None and dt == torch.bfloat16:
-            # sinks + window of every chunk while the chain runs, then the slot field merged into
-            # the saved online-softmax state once the snapshots exist
+        if split:
+            # sinks + window of every chunk while the chain runs, then, group by group, the slot
+            # field merged into the saved online-softmax state and the readout
             partial = torch.empty(b, H, T, HD + 4, device=dev)
             a.part, a.partial = 1, partial.data_ptr()
             A.call("bolt3_chunk_attn", a, dev)
-            main.wait_stream(chain_stream)
             a.part = 2
-            A.call("bolt3_chunk_attn", a, dev)
+            for (s0, s1), ev in zip(groups, done):
+                main.wait_event(ev)
+                a.chunk_begin, a.chunk_end = s0 + 2, s1 + 2
+                A.call("bolt3_chunk_attn", a, dev)
         else:
-            if chain_stream is not None:
-                main.wait_stream(chain_stream)
+            for ev in done:
+                main.wait_event(ev)
             A.call("bolt3_chunk_attn", a, dev)
         if trace is not None:
             trace["y"] = y

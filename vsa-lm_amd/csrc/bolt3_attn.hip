@@ -408,7 +408,7 @@ __global__ void __launch_bounds__(512) attn_fwd_kernel(b3_attn_args a, int QW) {
   const int bh = blockIdx.z, b = bh / a.HKV, hkv = bh % a.HKV;
   const int hq = hkv * G + g;
   const int part = a.part;                       // 0 all fields, 1 sinks + window, 2 slots (chunks >= 2)
-  const int chunk = blockIdx.y + (part == 2 ? 2 : 0), C = a.C;
+  const int chunk = blockIdx.y + a.chunk_begin, C = a.C;   // the launcher sets chunk_begin
   const int qbase = chunk * C;
   const int nq_chunk = min(C, a.n_q - qbase);
   const int qt0 = blockIdx.x * 32 * QW;
@@ -702,22 +702,26 @@ static int launch_attn(const b3_attn_args& a, hipStream_t st) {
   const int G = a.H / a.HKV;
   const int QW = G <= 4 ? 2 : 1;
   const int per_wg = 32 * QW;
-  int n_chunks = a.mode == 0 ? (a.n_q + a.C - 1) / a.C : 1;
-  if (a.part == 2) n_chunks -= 2;   // the slot field exists from chunk 2 on
+  const int all_chunks = a.mode == 0 ? (a.n_q + a.C - 1) / a.C : 1;
+  int c0 = a.chunk_begin, c1 = a.chunk_end == 0 ? all_chunks : min(a.chunk_end, all_chunks);
+  if (a.part == 2) c0 = max(c0, 2);   // the slot field exists from chunk 2 on
+  const int n_chunks = c1 - c0;
   if (n_chunks <= 0) return B3_OK;
   const int qlen = a.mode == 0 ? a.C : a.n_q;
   dim3 grid((qlen + per_wg - 1) / per_wg, n_chunks, a.B * a.HKV);
   const int nthreads = 64 * G * QW;
   if constexpr (St<T>::is_bf16) {
     if (a.mode == 0 && (!a.m_res || a.m_split)) {
+      b3_attn_args ab = a;
+      ab.chunk_begin = c0;
       const int ipt = (KB * (HD / 8) + nthreads - 1) / nthreads;
-      if (ipt <= 1) hipLaunchKernelGGL((attn_fwd_kernel<HD, 1>), grid, dim3(nthreads), 0, st, a, QW);
-      else if (ipt <= 2) hipLaunchKernelGGL((attn_fwd_kernel<HD, 2>), grid, dim3(nthreads), 0, st, a, QW);
-      else hipLaunchKernelGGL((attn_fwd_kernel<HD, 4>), grid, dim3(nthreads), 0, st, a, QW);
+      if (ipt <= 1) hipLaunchKernelGGL((attn_fwd_kernel<HD, 1>), grid, dim3(nthreads), 0, st, ab, QW);
+      else if (ipt <= 2) hipLaunchKernelGGL((attn_fwd_kernel<HD, 2>), grid, dim3(nthreads), 0, st, ab, QW);
+      else hipLaunchKernelGGL((attn_fwd_kernel<HD, 4>), grid, dim3(nthreads), 0, st, ab, QW);
       return (int)hipGetLastError();
     }
   }
-  if (a.part != 0) return B3_ERR_UNSUPPORTED;
+  if (a.part != 0 || c0 != 0 || c1 != all_chunks) return B3_ERR_UNSUPPORTED;
   hipLaunchKernelGGL((attn_kernel<T, HD>), grid, dim3(nthreads), 0, st, a, QW);
   return (int)hipGetLastError();
 }
@@ -741,6 +745,9 @@ extern "C" int bolt3_chunk_attn(const b3_attn_args* a, void* stream) {
   if (a->m_res && !a->q_raw) return B3_ERR_ARG;
   if (a->m_split && a->dtype != B3_BF16) return B3_ERR_ARG;
   if (a->part < 0 || a->part > 2 || (a->part != 0 && (a->mode != 0 || !a->partial))) return B3_ERR_ARG;
+  if (a->chunk_begin < 0 || a->chunk_end < 0 || (a->chunk_end != 0 && a->chunk_end < a->chunk_begin) ||
+      (a->mode != 0 && (a->chunk_begin != 0 || a->chunk_end != 0)))
+    return B3_ERR_ARG;
   if (a->part == 2 && a->n_q > 2 * a->C && (!a->slot_k || !a->slot_v || !a->slot_bias)) return B3_ERR_ARG;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (a->dtype == B3_F32) return a->HD == 64 ? b3::launch_attn<float, 64>(*a, st) : b3::launch_attn<float, 128>(*a, st);

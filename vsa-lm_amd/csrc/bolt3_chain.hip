@@ -1419,11 +1419,13 @@ __global__ void __launch_bounds__(MT) mres_kernel(b3_chain_args a) {
 template <typename T, int HD>
 static int launch_chain(const b3_chain_args& a, hipStream_t st) {
   const int BH = a.B * a.HKV;
-  hipLaunchKernelGGL((decide_kernel<T, HD>), dim3(BH), dim3(DT), 0, st, a);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return (int)e;
+  if (a.phase != 2) {
+    hipLaunchKernelGGL((decide_kernel<T, HD>), dim3(BH), dim3(DT), 0, st, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || a.phase == 1) return (int)e;
+  }
   hipLaunchKernelGGL((gersh_kernel<T, HD>), dim3(a.n_steps, BH), dim3(MT), 0, st, a);
-  e = hipGetLastError();
+  hipError_t e = hipGetLastError();
   if (e != hipSuccess) return (int)e;
   hipLaunchKernelGGL((mres_kernel<T, HD>), dim3(BH * (HD / 32)), dim3(MT), 0, st, a);
   return (int)hipGetLastError();
@@ -1445,7 +1447,7 @@ extern "C" int bolt3_chain(const b3_chain_args* a, void* stream) {
   if (a->n_steps == 0) return B3_OK;
   if (a->len0 < 1 || a->len0 > b3::LMAX || (a->n_steps > 1 && (a->step_len < 1 || a->step_len > b3::LMAX)))
     return B3_ERR_UNSUPPORTED;
-  if (a->n_filled < 0 || a->n_filled > b3::S) return B3_ERR_ARG;
+  if (a->n_filled < 0 || a->n_filled > b3::S || a->phase < 0 || a->phase > 2) return B3_ERR_ARG;
   if (!a->kr || !a->kp || !a->v || !a->pos || !a->beta || !a->ak || !a->av || !a->mass || !a->util || !a->pm ||
       !a->act || !a->m_res || !a->kappa || !a->gamma || !a->inv_freq || !a->work)
     return B3_ERR_ARG;

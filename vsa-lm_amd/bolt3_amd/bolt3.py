@@ -327,7 +327,7 @@ class Bolt3Attn(nn.Module):
         if trace is not None:
             trace.update(q_raw=q_raw, q_rope=q_rope, k_raw=k_raw, k_rope=k_rope, v=v, beta=beta, eta=eta, pos=pos)
 
-        y = torch.empty(b, T, H * HD, dtype=dt, device=dev)
+        K = H * HD
         a = A.AttnArgs()
         a.dtype, a.B, a.H, a.HKV, a.HD, a.S, a.C, a.n_sinks = A.dtype_code(dt), b, H, HKV, HD, S, C, self.n_sinks
         a.mode, a.n_q, a.score_round = 0, T, 1
@@ -340,25 +340,49 @@ class Bolt3Attn(nn.Module):
             a.m_res, a.m_step = snaps[3].data_ptr(), bh * HD * HD
             a.m_split = int(dt == torch.bfloat16)
         a.gamma, a.res_w, a.eps = gam.data_ptr(), side["res_w"].data_ptr(), float(self.res_norm.eps)
-        a.y, a.y_sb, a.y_st = y.data_ptr(), y.stride(0), y.stride(1)
-        if split:
-            # sinks + window of every chunk while the chain runs, then, group by group, the slot
-            # field merged into the saved online-softmax state and the readout
-            partial = torch.empty(b, H, T, HD + 4, device=dev)
-            a.part, a.partial = 1, partial.data_ptr()
-            A.call("bolt3_chunk_attn", a, dev)
-            a.part = 2
-            for (s0, s1), ev in zip(groups, done):
-                main.wait_event(ev)
-                a.chunk_begin, a.chunk_end = s0 + 2, s1 + 2
-                A.call("bolt3_chunk_attn", a, dev)
-        else:
+        if not split:
+            y = torch.empty(b, T, K, dtype=dt, device=dev)
+            a.y, a.y_sb, a.y_st = y.data_ptr(), y.stride(0), y.stride(1)
             for ev in done:
                 main.wait_event(ev)
             A.call("bolt3_chunk_attn", a, dev)
+            if trace is not None:
+                trace["y"] = y
+            return F.linear(y, side["wo"])
+
+        # Sinks + window of every chunk while the chain runs; then, group by group, the slot
+        # field merged into the saved online-softmax state, the readout and o_proj.  The
+        # attention output of a group of chunks is one [B * rows, H * HD] block (token ranges
+        # of all batch rows together), so o_proj of a group is one GEMM.
+        spans = [(0, min(T, (groups[0][1] + 2) * C))] + \
+                [(min(T, (s0 + 2) * C), min(T, (s1 + 2) * C)) for s0, s1 in groups[1:]]
+        y_all = torch.empty(b * T * K, dtype=dt, device=dev)
+        blocks, off = [], 0
+        for t0, t1 in spans:
+            blocks.append(y_all[off:off + b * (t1 - t0) * K].view(b * (t1 - t0), K))
+            off += b * (t1 - t0) * K
+        out = torch.empty(b, T, self.o_proj.out_features, dtype=dt, device=dev)
+        esz = y_all.element_size()
+
+        def point_y(gi):   # element (b, t) of block gi at block + (b * rows + t - t0) * K
+            t0, t1 = spans[gi]
+            a.y, a.y_sb, a.y_st = blocks[gi].data_ptr() - t0 * K * esz, (t1 - t0) * K, K
+
+        partial = torch.empty(b, H, T, HD + 4, device=dev)
+        a.part, a.partial = 1, partial.data_ptr()
+        point_y(0)   # part 1 writes the outputs of chunks 0 and 1 only
+        A.call("bolt3_chunk_attn", a, dev)
+        a.part = 2
+        for gi, ((s0, s1), ev) in enumerate(zip(groups, done)):
+            main.wait_event(ev)
+            a.chunk_begin, a.chunk_end = s0 + 2, s1 + 2
+            point_y(gi)
+            A.call("bolt3_chunk_attn", a, dev)
+            t0, t1 = spans[gi]
+            out[:, t0:t1].copy_(F.linear(blocks[gi], side["wo"]).view(b, t1 - t0, -1))
         if trace is not None:
-            trace["y"] = y
-        return F.linear(y, side["wo"])
+            trace["y"] = torch.cat([blk.view(b, t1 - t0, K) for blk, (t0, t1) in zip(blocks, spans)], dim=1)
+        return out
 
     # ------------------------------------------------------------ consolidation (reference internal API)
 

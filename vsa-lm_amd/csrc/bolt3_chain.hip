@@ -30,6 +30,8 @@
 // splits fp32 operands into hi + lo; fp32 storage uses the fp32 MFMA.
 // Orderings are ranks computed by counting on monotone integer keys (one pass,
 // stable): the larger value first (NaN first), equal values by lower index.
+#include <type_traits>
+
 #include "bolt3_common.h"
 #include "bolt3_math.h"
 #include "bolt3_amd.h"
@@ -68,11 +70,14 @@ template <typename T, int HD>
 struct DecSmem {
   static constexpr int KS = sizeof(T) == 2 ? HD + 8 : HD + 4;   // slot row stride (16-byte aligned rows)
   static constexpr bool KREAD_LDS = Work<T, HD>::KREAD_LDS;
+  static constexpr bool BF = sizeof(T) == 2;                     // bf16: 16-token tiles, av^T kept
+  static constexpr int VTS = S + 8;                               // av^T row stride
   alignas(16) T ak[S * KS];
   alignas(16) T av[S * KS];
   alignas(16) T kread[KREAD_LDS ? S * KS : 1];                    // roped slot keys
+  alignas(16) T avt[BF ? HD * VTS : 1];                           // av^T [d][slot] (bf16)
   float mass[S], util[S], pm[S], inv_nak[S], keep[S], bias[S];
-  int act[S], dirty[S];
+  int act[S], dirty[S], vdirty[S];
   int any_merge;
   float invf[HD / 2];
   float rel[LMAX], score[LMAX];
@@ -81,21 +86,19 @@ struct DecSmem {
   int si_a[LMAX];
   float sk_b[S];
   int si_b[S];
-  // Tiles are scored in rounds of 128 tokens (4 wave pairs x 32).  Within a pair, one
-  // exchange carries each half's softmax max / sum and best slot; for bf16 storage a second
-  // one carries the probabilities, P[tok][slot] with row stride PS (fp32 storage has no LDS
-  // room for it and computes the whole softmax in both waves).
-  static constexpr bool SPLIT = sizeof(T) == 2;
-  static constexpr int PS = S + 4;
+  // fp32 storage scores 32-token tiles in rounds of 128 tokens (4 wave pairs x 32); both
+  // waves of a pair compute the whole softmax, then each forms v_hat and the value cosine on
+  // half of the feature dims and leaves partial sums here for the combine pass.  bf16
+  // storage needs none of it: one wave owns 16 tokens and all slots.
+  static constexpr int SC = BF ? 1 : 128;
   static constexpr int NP = DWAVES / 2;
   union {  // phase-local buffers
     struct {
-      float e2[2][128], v2[2][128], dv[2][128], vv[2][128], aa[2][128], bv[2][128];
-      int bs[2][128];
-      float xmx[NP][2][32], xsum[NP][2][32], xbv[NP][2][32];
-      uint32_t xkey[NP][2][32];
-      int xbs[NP][2][32];
-      alignas(16) uint16_t p[SPLIT ? NP : 1][SPLIT ? 32 * PS : 1];
+      float e2[2][SC], v2[2][SC], dv[2][SC], vv[2][SC], aa[2][SC], bv[2][SC];
+      int bs[2][SC];
+      uint32_t xkey[NP][2][BF ? 1 : 32];
+      float xbv[NP][2][BF ? 1 : 32];
+      int xbs[NP][2][BF ? 1 : 32];
     } sc;
     struct { int cnt[S], off[S], hits[S], mlist[LMAX]; float psum[S]; int nhit; } mg;
     struct { float mx[2][S]; int nan[2][S]; } kp;
@@ -338,24 +341,22 @@ struct TileIn {
   }
 };
 
-// One 32-token tile, one half of the work, for wave `half` of wave pair `pair`.
-// bf16 storage: each wave scores and cosine-matches its half of the slots; one LDS exchange
-// gives the pair the softmax max / sum and the best slot, a second one the probabilities.
-// fp32 storage (no LDS room for the exchange): both waves compute the whole softmax.  Then
-// wave `half` forms v_hat and the value cosine on its half of the feature dims and leaves
-// partial sums in LDS for the combine pass.  Contains barriers: every thread of the
-// workgroup calls it the same number of times (tokens past l are inert).
+// fp32 storage: one 32-token tile, one half of the work, for wave `half` of wave pair
+// `pair`.  Both waves compute the whole softmax; each cosine-matches half of the slots and
+// one LDS exchange gives the pair the best slot.  Then wave `half` forms v_hat and the
+// value cosine on its half of the feature dims and leaves partial sums in LDS for the
+// combine pass.  Contains barriers: every thread of the workgroup calls it the same number
+// of times (tokens past l are inert).
 template <typename T, int HD>
 __device__ void score_tile(DecSmem<T, HD>& sm, const T* kread, const TileIn<T, HD>& td, const T* kr, int t0, int l,
                            bool steady, float scale, int pair, int half, int lane) {
+  static_assert(!St<T>::is_bf16, "bf16 storage uses score_tile16");
   using Sm = DecSmem<T, HD>;
-  constexpr bool SPLIT = Sm::SPLIT;
-  constexpr int NMB = SPLIT ? 2 : 4;   // slot blocks scored by this wave
+  constexpr int NMB = 4;
   constexpr int HDB = TileIn<T, HD>::HDB;
   const int n = lane & 31, h = lane >> 5;
   const int tok = t0 + n;
   const bool in = tok < l;
-  const int mb0 = SPLIT ? 2 * half : 0;
 
   Frag<T, HD> fk;   // un-roped keys: consumed after the softmax, so their latency hides behind it
   fk.load(kr, tok, l, lane);
@@ -365,8 +366,8 @@ __device__ void score_tile(DecSmem<T, HD>& sm, const T* kread, const TileIn<T, H
 #pragma unroll
   for (int m2 = 0; m2 < NMB; ++m2) {
     acc[m2] = zero16();
-    if constexpr (Sm::KREAD_LDS) mm_rows_frag<HD>(acc[m2], sm.kread, Sm::KS, 32 * (mb0 + m2), td.fq, lane);
-    else mm_rows_frag<HD>(acc[m2], kread, HD, 32 * (mb0 + m2), td.fq, lane);
+    if constexpr (Sm::KREAD_LDS) mm_rows_frag<HD>(acc[m2], sm.kread, Sm::KS, 32 * m2, td.fq, lane);
+    else mm_rows_frag<HD>(acc[m2], kread, HD, 32 * m2, td.fq, lane);
   }
 
   // softmax over the slots (column of this lane pair)
@@ -375,12 +376,12 @@ __device__ void score_tile(DecSmem<T, HD>& sm, const T* kread, const TileIn<T, H
   for (int m2 = 0; m2 < NMB; ++m2)
 #pragma unroll
     for (int r4 = 0; r4 < 4; ++r4) {
-      const int s0 = 32 * (mb0 + m2) + 8 * r4 + 4 * h;
+      const int s0 = 32 * m2 + 8 * r4 + 4 * h;
       const float4 b4 = *reinterpret_cast<const float4*>(&sm.bias[s0]);
       const float bb[4] = {b4.x, b4.y, b4.z, b4.w};
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        float x = add_rn(mul_rn(St<T>::rnd(acc[m2][4 * r4 + q]), scale), bb[q]);
+        float x = add_rn(mul_rn(acc[m2][4 * r4 + q], scale), bb[q]);
         if (!steady && !sm.act[s0 + q]) x = -1e9f;
         acc[m2][4 * r4 + q] = x;
         mx = fmaxf(mx, x);
@@ -431,16 +432,8 @@ __device__ void score_tile(DecSmem<T, HD>& sm, const T* kread, const TileIn<T, H
     const int os = xor32i(bs);
     if (ok > bkey || (ok == bkey && os < bs)) { bkey = ok; bv = ov; bs = os; }
   }
-
-  float rs = 1.0f / sum;
-  if constexpr (SPLIT) {
-    // one exchange: max, sum (relative to the own max) and best slot of each half
-    if (h == 0) {
-      sm.u.sc.xmx[pair][half][n] = mx;
-      sm.u.sc.xsum[pair][half][n] = sum;
-    }
-  }
-  // the pair's best slot (and, split, the softmax max / sum) through one exchange
+  const float rs = 1.0f / sum;
+  // the pair's best slot through one exchange
   if (h == 0) {
     sm.u.sc.xkey[pair][half][n] = bkey;
     sm.u.sc.xbv[pair][half][n] = bv;
@@ -449,12 +442,6 @@ __device__ void score_tile(DecSmem<T, HD>& sm, const T* kread, const TileIn<T, H
   sync_lds();
   {
     const int o = half ^ 1;
-    if constexpr (SPLIT) {
-      const float m_o = sm.u.sc.xmx[pair][o][n], s_o = sm.u.sc.xsum[pair][o][n];
-      const float m = fmaxf(mx, m_o);
-      const float f_self = expf(mx - m), f_o = expf(m_o - m);
-      rs = f_self / (sum * f_self + s_o * f_o);
-    }
     const uint32_t ko = sm.u.sc.xkey[pair][o][n];
     const int so = sm.u.sc.xbs[pair][o][n];
     if (ko > bkey || (ko == bkey && so < bs)) { bkey = ko; bv = sm.u.sc.xbv[pair][o][n]; bs = so; }
@@ -462,20 +449,7 @@ __device__ void score_tile(DecSmem<T, HD>& sm, const T* kread, const TileIn<T, H
 #pragma unroll
   for (int m2 = 0; m2 < NMB; ++m2)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[m2][r] = St<T>::rnd(mul_rn(acc[m2][r], rs));
-  if constexpr (SPLIT) {
-    // this half's probabilities for the partner: P[tok][slot], 4 consecutive slots per store
-    uint16_t* pp = sm.u.sc.p[pair] + n * Sm::PS;
-#pragma unroll
-    for (int m2 = 0; m2 < NMB; ++m2)
-#pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4) {
-        u16x4 q4;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) q4[q] = f2bf(acc[m2][4 * r4 + q]);
-        *reinterpret_cast<u16x4*>(pp + 32 * (mb0 + m2) + 8 * r4 + 4 * h) = q4;
-      }
-  }
+    for (int r = 0; r < 16; ++r) acc[m2][r] = mul_rn(acc[m2][r], rs);
 
   // value cosine with the best slot, partial over this wave's feature half (from registers)
   float dvv = 0.f, vv = 0.f, aa = 0.f;
@@ -499,7 +473,6 @@ __device__ void score_tile(DecSmem<T, HD>& sm, const T* kread, const TileIn<T, H
     vv += xor32(vv);
     aa += xor32(aa);
   }
-  if constexpr (SPLIT) sync_lds();
 
   // v_hat^T[d][tok] = av^T . P^T on this wave's feature half; partial rel_err sums
   float e2 = 0.f, v2 = 0.f;
@@ -508,45 +481,19 @@ __device__ void score_tile(DecSmem<T, HD>& sm, const T* kread, const TileIn<T, H
     const int db = half * HDB + i;
     f32x16 vh = zero16();
     const int d = 32 * db + n;
-    if constexpr (St<T>::is_bf16) {
-      const uint16_t* pp = sm.u.sc.p[pair] + n * Sm::PS;
 #pragma unroll
-      for (int kc = 0; kc < 8; ++kc) {
-        if (kc == 2 || kc == 4 || kc == 6) __builtin_amdgcn_sched_barrier(0);   // bound the gathers in flight
-        // slots 16*kc + 8*(q>>2) + 4*h + (q&3): own half from registers, the other from LDS
-        u16x8 av8, p8;
-        const int mb = kc >> 1;
-        if (mb >> 1 == half) {
+    for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-          for (int q = 0; q < 8; ++q) p8[q] = f2bf(acc[mb & 1][8 * (kc & 1) + q]);
-        } else {
-          const u16x4 lo = *reinterpret_cast<const u16x4*>(pp + 16 * kc + 4 * h);
-          const u16x4 hi = *reinterpret_cast<const u16x4*>(pp + 16 * kc + 8 + 4 * h);
-#pragma unroll
-          for (int q = 0; q < 4; ++q) { p8[q] = lo[q]; p8[4 + q] = hi[q]; }
-        }
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          const int s = 16 * kc + 8 * (q >> 2) + 4 * h + (q & 3);
-          av8[q] = sm.av[s * Sm::KS + d];
-        }
-        mma_bf16(vh, av8, p8);
+      for (int r = 0; r < 16; ++r) {
+        const int s = 32 * mb + d_row(lane, r);
+        mma_f32(vh, sm.av[s * Sm::KS + d], acc[mb][r]);
       }
-    } else {
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int s = 32 * mb + d_row(lane, r);
-          mma_f32(vh, sm.av[s * Sm::KS + d], acc[mb][r]);
-        }
-    }
 #pragma unroll
     for (int g = 0; g < 4; ++g)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const float x = td.vx[i][g].get(q);
-        const float dv = x - St<T>::rnd(vh[4 * g + q]);
+        const float dv = x - vh[4 * g + q];
         e2 += dv * dv;
         v2 += x * x;
       }
@@ -629,6 +576,247 @@ __device__ bool score_phase(DecSmem<T, HD>& sm, const T* kread, TileIn<T, HD>& t
   return merge;
 }
 
+// bf16 storage: one wavefront owns 16 tokens and all S slots, with 16x16x32 MFMAs, so a
+// token's softmax, best slot, v_hat and rel_err stay within the wavefront (the 128 slots
+// of a token column spread over the four lane groups l / 16).  Lane (n = l % 16, g = l / 16)
+// holds the operands of token t0 + n: K group g of every 32-feature step for the keys, and
+// features 16*db + 4*g + i of the values (the rows of the v_hat^T tile it owns).
+template <int HD>
+struct Tile16 {
+  static constexpr int NK = HD / 32;   // K steps
+  static constexpr int ND = HD / 16;   // 16-feature blocks
+  u16x8 q[NK];   // roped keys kp[tok][32*ks + 8*g + i]
+  u16x8 k[NK];   // un-roped keys kr[tok][32*ks + 8*g + i]
+  u16x4 v[ND];   // values v[tok][16*db + 4*g + i]
+  __device__ __forceinline__ void load(const uint16_t* kp, const uint16_t* kr, const uint16_t* vv, int t0, int l,
+                                       int lane) {
+    const int n = lane & 15, g = lane >> 4, tok = t0 + n;
+    const bool ok = tok < l;
+    const long long o = (long long)tok * HD;
+#pragma unroll
+    for (int ks = 0; ks < NK; ++ks) {
+      if (ok) {
+        q[ks] = *reinterpret_cast<const u16x8*>(kp + o + 32 * ks + 8 * g);
+        k[ks] = *reinterpret_cast<const u16x8*>(kr + o + 32 * ks + 8 * g);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) { q[ks][i] = 0; k[ks][i] = 0; }
+      }
+    }
+#pragma unroll
+    for (int db = 0; db < ND; ++db) {
+      if (ok) v[db] = *reinterpret_cast<const u16x4*>(vv + o + 16 * db + 4 * g);
+      else { v[db][0] = 0; v[db][1] = 0; v[db][2] = 0; v[db][3] = 0; }
+    }
+  }
+};
+
+// reductions over the four lane groups (the slot rows of one token column)
+__device__ __forceinline__ float sum4g(float v) {
+  v += __shfl_xor(v, 16, 64);
+  return v + __shfl_xor(v, 32, 64);
+}
+__device__ __forceinline__ float max4g(float v) {
+  v = fmaxf(v, __shfl_xor(v, 16, 64));
+  return fmaxf(v, __shfl_xor(v, 32, 64));
+}
+
+// Scores, softmax, v_hat, rel_err, best slot and value cosine of the 16 tokens
+// [t0, t0 + 16) of one wavefront (bf16 storage).  Writes rel / score / slot / flags (and
+// the log's best cosine and value cosine) of its tokens; no barrier inside.  Returns the
+// merge flag of token t0 + lane (lanes 0..15).
+template <int HD>
+__device__ bool score_tile16(DecSmem<uint16_t, HD>& sm, const Tile16<HD>& td, int t0, int l, bool steady,
+                             float scale, int lane, float* log) {
+  using Sm = DecSmem<uint16_t, HD>;
+  constexpr int NK = Tile16<HD>::NK, ND = Tile16<HD>::ND, NMB = S / 16;
+  const int n = lane & 15, g = lane >> 4;
+  const int tok = t0 + n;
+
+  // cos^T[slot][tok] = ak . kr^T / (|ak| |kr|); argmax on integer keys: slots ascend along
+  // each lane's scan and the cross-lane merge takes the lower slot on equal keys, so ties go
+  // to the lower index, and NaN (largest key) wins as torch.max does
+  float kk = 0.f;
+#pragma unroll
+  for (int ks = 0; ks < NK; ++ks)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) { const float x = bf2f(td.k[ks][i]); kk += x * x; }
+  kk = sum4g(kk);
+  const float inv_nk = 1.0f / fmaxf(sqrtf(kk), 1e-12f);
+  uint32_t bkey = 0;
+  float bv = 0.f;
+  int bs = -1;
+#pragma unroll
+  for (int mb = 0; mb < NMB; ++mb) {
+    f32x4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < NK; ++ks)
+      mma16_bf16(c, *reinterpret_cast<const u16x8*>(&sm.ak[(16 * mb + n) * Sm::KS + 32 * ks + 8 * g]), td.k[ks]);
+    const int s0 = 16 * mb + 4 * g;
+    const float4 n4 = *reinterpret_cast<const float4*>(&sm.inv_nak[s0]);
+    const float nn[4] = {n4.x, n4.y, n4.z, n4.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float cv = c[i] * (nn[i] * inv_nk);
+      if (!steady && !sm.act[s0 + i]) cv = 0.f;
+      const uint32_t key = ord_key(cv + 0.0f);   // -0 ranks with +0, as in a float compare
+      if (bs < 0 || key > bkey) { bkey = key; bv = cv; bs = s0 + i; }
+    }
+  }
+#pragma unroll
+  for (int o = 16; o <= 32; o <<= 1) {
+    const uint32_t ok = (uint32_t)__shfl_xor((int)bkey, o, 64);
+    const float ov = __shfl_xor(bv, o, 64);
+    const int os = __shfl_xor(bs, o, 64);
+    if (ok > bkey || (ok == bkey && os < bs)) { bkey = ok; bv = ov; bs = os; }
+  }
+
+  // scores^T[slot][tok] = kread . kp^T, rounded to bf16, scaled, plus the slot bias
+  f32x4 acc[NMB];
+#pragma unroll
+  for (int mb = 0; mb < NMB; ++mb) {
+    acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < NK; ++ks)
+      mma16_bf16(acc[mb], *reinterpret_cast<const u16x8*>(&sm.kread[(16 * mb + n) * Sm::KS + 32 * ks + 8 * g]),
+                 td.q[ks]);
+  }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int mb = 0; mb < NMB; ++mb) {
+    const int s0 = 16 * mb + 4 * g;
+    const float4 b4 = *reinterpret_cast<const float4*>(&sm.bias[s0]);
+    const float bb[4] = {b4.x, b4.y, b4.z, b4.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float x = add_rn(mul_rn(round_bf(acc[mb][i]), scale), bb[i]);
+      if (!steady && !sm.act[s0 + i]) x = -1e9f;
+      acc[mb][i] = x;
+      mx = fmaxf(mx, x);
+    }
+  }
+  mx = max4g(mx);
+  float sum = 0.f;
+#pragma unroll
+  for (int mb = 0; mb < NMB; ++mb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float e = expf(acc[mb][i] - mx);
+      acc[mb][i] = e;
+      sum += e;
+    }
+  sum = sum4g(sum);
+  const float rs = 1.0f / sum;
+  // probabilities rounded to bf16 as the B operand of v_hat^T = av^T . P^T; K step kk covers
+  // slots 32*kk .. 32*kk+31 with lane group g holding slots 32*kk + {4g..4g+3, 16+4g..16+4g+3}
+  u16x8 pb[S / 32];
+#pragma unroll
+  for (int kk2 = 0; kk2 < S / 32; ++kk2)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      pb[kk2][i] = f2bf(mul_rn(acc[2 * kk2][i], rs));
+      pb[kk2][4 + i] = f2bf(mul_rn(acc[2 * kk2 + 1][i], rs));
+    }
+
+  // v_hat^T[d][tok], rel_err sums; this lane owns features 16*db + 4*g + i of token tok
+  float e2 = 0.f, v2 = 0.f;
+#pragma unroll
+  for (int db = 0; db < ND; ++db) {
+    f32x4 vh = {0.f, 0.f, 0.f, 0.f};
+    const uint16_t* row = &sm.avt[(16 * db + n) * Sm::VTS + 4 * g];
+#pragma unroll
+    for (int kk2 = 0; kk2 < S / 32; ++kk2) {
+      const u16x4 lo = *reinterpret_cast<const u16x4*>(row + 32 * kk2);
+      const u16x4 hi = *reinterpret_cast<const u16x4*>(row + 32 * kk2 + 16);
+      u16x8 a;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) { a[i] = lo[i]; a[4 + i] = hi[i]; }
+      mma16_bf16(vh, a, pb[kk2]);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float x = bf2f(td.v[db][i]);
+      const float dv = x - round_bf(vh[i]);
+      e2 += dv * dv;
+      v2 += x * x;
+    }
+  }
+  e2 = sum4g(e2);
+  v2 = sum4g(v2);
+
+  // value cosine with the best slot
+  float simv = 0.f;
+  if (steady) {
+    const int bsr = bs < 0 ? 0 : bs;
+    float dvv = 0.f, aa = 0.f;
+#pragma unroll
+    for (int db = 0; db < ND; ++db) {
+      const u16x4 y4 = *reinterpret_cast<const u16x4*>(&sm.av[bsr * Sm::KS + 16 * db + 4 * g]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float x = bf2f(td.v[db][i]), y = bf2f(y4[i]);
+        dvv += x * y;
+        aa += y * y;
+      }
+    }
+    dvv = sum4g(dvv);
+    aa = sum4g(aa);
+    simv = dvv / (fmaxf(sqrtf(v2), 1e-8f) * fmaxf(sqrtf(aa), 1e-8f));
+  }
+  const float rel = sqrtf(e2) / (sqrtf(v2) + 1e-6f);
+  const float score = rel * (1.0f - fminf(fmaxf(bv, 0.0f), 1.0f));
+  const bool merge = steady && bv >= SIM_K && simv >= SIM_V;
+  if (g == 0 && tok < l) {
+    sm.rel[tok] = rel;
+    sm.score[tok] = score;
+    sm.slot[tok] = bs;
+    sm.flags[tok] = merge ? F_MERGE : 0;
+    if (log) {
+      log[B3_LOG_BEST * B3_LOG_COLS + tok] = steady ? bv : 0.f;
+      log[B3_LOG_SIMV * B3_LOG_COLS + tok] = simv;
+    }
+  }
+  return g == 0 && tok < l && merge;
+}
+
+// All tokens of a step, 16 per wavefront per round of 128.  `td` holds the first round's
+// tile data on entry when `ready`.  Returns this thread's merge flag; the caller's barrier
+// publishes the results.
+template <int HD>
+__device__ bool score_phase16(DecSmem<uint16_t, HD>& sm, Tile16<HD>& td, bool ready, const uint16_t* kr,
+                              const uint16_t* kp, const uint16_t* v, int l, bool steady, float scale, int wave,
+                              int lane, float* log) {
+  if (l <= 128) {
+    if (!ready) td.load(kp, kr, v, 16 * wave, l, lane);
+    return score_tile16<HD>(sm, td, 16 * wave, l, steady, scale, lane, log);
+  }
+  bool merge = false;
+  for (int r = 0; r < (l + 127) / 128; ++r) {
+    Tile16<HD> tr;
+    tr.load(kp, kr, v, 128 * r + 16 * wave, l, lane);
+    merge |= score_tile16<HD>(sm, tr, 128 * r + 16 * wave, l, steady, scale, lane, log);
+  }
+  return merge;
+}
+
+// av^T columns of the slots whose values changed (vdirty): an item is two adjacent slots
+// and 8 features, written as 8 dwords (lanes of a wavefront take adjacent slot pairs, so
+// their writes fall into distinct banks).
+template <typename T, int HD>
+__device__ void transpose_dirty_v(DecSmem<T, HD>& sm, int tid) {
+  if constexpr (DecSmem<T, HD>::BF) {
+    for (int it = tid; it < (S / 2) * (HD / 8); it += DT) {
+      const int s = 2 * (it % (S / 2)), d8 = (it / (S / 2)) * 8;
+      if (!sm.vdirty[s] && !sm.vdirty[s + 1]) continue;
+      const u16x8 x0 = *reinterpret_cast<const u16x8*>(&sm.av[s * sm.KS + d8]);
+      const u16x8 x1 = *reinterpret_cast<const u16x8*>(&sm.av[(s + 1) * sm.KS + d8]);
+#pragma unroll
+      for (int q = 0; q < 8; ++q)
+        *reinterpret_cast<uint32_t*>(&sm.avt[(d8 + q) * sm.VTS + s]) = (uint32_t)x0[q] | ((uint32_t)x1[q] << 16);
+    }
+  }
+}
+
 // ----------------------------------------------------------------- decide_kernel
 
 template <typename T, int HD>
@@ -674,24 +862,27 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
     sm.pm[tid] = fresh ? 0.0f : a.pm[bh * S + tid];
     sm.act[tid] = fresh ? 0 : (a.act[bh * S + tid] ? 1 : 0);
     sm.dirty[tid] = 1;
+    sm.vdirty[tid] = 1;
   }
   if (tid < HD / 2) sm.invf[tid] = a.inv_freq[tid];
   sync_lds();
   int nf = a.n_filled;
   rope_dirty<T, HD>(sm, kread_g, tid);   // every slot, empty ones included (their rows stay zero)
+  transpose_dirty_v<T, HD>(sm, tid);
   __threadfence_block();
   __syncthreads();
 
   // tile data of the next step's first round, loaded while the current step finishes (bf16)
-  TileIn<T, HD> td;
+  constexpr bool BF = St<T>::is_bf16;
+  using TD = std::conditional_t<BF, Tile16<HD>, TileIn<T, HD>>;
+  TD td;
   bool td_ready = false;
-  constexpr bool PREFETCH = St<T>::is_bf16;
   auto prefetch = [&](int step, int wave, int lane) {
-    if constexpr (PREFETCH) {
+    if constexpr (BF) {
       if (step + 1 < a.n_steps) {
         const long long nb = (long long)bh * a.tok_bh_stride + (long long)step_off(a, step + 1) * HD;
         td.load(reinterpret_cast<const T*>(a.kp) + nb, reinterpret_cast<const T*>(a.kr) + nb,
-                reinterpret_cast<const T*>(a.v) + nb, 32 * (wave >> 1), step_len(a, step + 1), wave & 1, lane);
+                reinterpret_cast<const T*>(a.v) + nb, 16 * wave, step_len(a, step + 1), lane);
         td_ready = true;
       }
     }
@@ -721,6 +912,7 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
       const float lm = logf(fmaxf(sm.mass[tid], 1.0f));
       sm.bias[tid] = steady ? mul_rn(kap, lm) : lm;
       sm.dirty[tid] = 0;
+      sm.vdirty[tid] = 0;
     }
     slot_norms<T, HD>(sm, tid);
     sync_lds();
@@ -760,7 +952,8 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
         sm.rel[j] = 0.15f;
       }
     } else {
-      has = score_phase<T, HD>(sm, kread, td, td_ready, kr, kp, v, l, steady, scale, wave, lane, tid, log);
+      if constexpr (BF) has = score_phase16<HD>(sm, td, td_ready, kr, kp, v, l, steady, scale, wave, lane, log);
+      else has = score_phase<T, HD>(sm, kread, td, td_ready, kr, kp, v, l, steady, scale, wave, lane, tid, log);
     }
     td_ready = false;
     prefetch(step, wave, lane);
@@ -798,6 +991,7 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
         sm.mass[s] = 1.0f;
         sm.util[s] = sm.rel[j];
         sm.act[s] = 1;
+        sm.vdirty[s] = 1;
         if (!kp_copy) sm.dirty[s] = 1;
       }
       if (log) {
@@ -858,6 +1052,7 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
           sm.pm[tid] = div_rn(add_rn(mul_rn(m0, sm.pm[tid]), sm.u.mg.psum[tid]), nm);
           sm.mass[tid] = nm;
           sm.dirty[tid] = 1;
+          sm.vdirty[tid] = 1;
         }
         sync_lds();
         slot_norms<T, HD>(sm, tid);
@@ -946,6 +1141,7 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
           sm.pm[s] = pos[j];
           sm.mass[s] = 1.0f;
           sm.util[s] = sm.rel[j];
+          sm.vdirty[s] = 1;
           if (!kp_copy) sm.dirty[s] = 1;
         }
       }
@@ -992,6 +1188,7 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
 
     // ---------------- per-step outputs; the roped keys also serve the next step
     rope_dirty<T, HD>(sm, kread_g, tid);
+    transpose_dirty_v<T, HD>(sm, tid);
     if constexpr (DecSmem<T, HD>::KREAD_LDS) {
       sync_lds();
     } else {

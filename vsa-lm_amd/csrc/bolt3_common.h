@@ -17,6 +17,7 @@ namespace b3 {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
 typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
 
@@ -101,6 +102,13 @@ __device__ __forceinline__ f32x16 zero16() {
 // D += A * B for one K=16 step with bf16 operands given as raw bf16 bits.
 __device__ __forceinline__ void mma_bf16(f32x16& acc, const u16x8& a, const u16x8& b) {
   acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
+                                                 acc, 0, 0, 0);
+}
+
+// 16x16 tiles (K = 32 per step): lane l holds A row l % 16, B column l % 16 and the K group
+// l / 16 (8 elements); D column l % 16, rows 4 * (l / 16) + i, i = 0..3.
+__device__ __forceinline__ void mma16_bf16(f32x4& acc, const u16x8& a, const u16x8& b) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
                                                  acc, 0, 0, 0);
 }
 

@@ -75,8 +75,13 @@ struct DecSmem {
   alignas(16) T ak[S * KS];
   alignas(16) T av[S * KS];
   alignas(16) T kread[KREAD_LDS ? S * KS : 1];                    // roped slot keys
-  alignas(16) T avt[BF ? HD * VTS : 1];                           // av^T [d][slot] (bf16)
+  // av^T [d][slot] (bf16); within each 32-slot block the slots are stored in the order
+  // 0-3, 16-19, 4-7, 20-23, ..., so that the 8 K elements of lane group g of a 16x16x32 MFMA
+  // operand (slots 4g..4g+3 and 16+4g..16+4g+3) are one 16-byte row piece
+  alignas(16) T avt[BF ? HD * VTS : 1];
   float mass[S], util[S], pm[S], inv_nak[S], keep[S], bias[S];
+  float tbl[S];   // bf16 scoring: bias * log2(e), -inf for slots masked in a fill step
+  float tnn[S];   // bf16 scoring: 1/|ak|, 0 for slots masked in a fill step
   int act[S], dirty[S], vdirty[S];
   int any_merge;
   float invf[HD / 2];
@@ -318,6 +323,13 @@ __device__ void slot_norms(DecSmem<T, HD>& sm, int tid) {
   ss += __shfl_xor(ss, 1, 64);
   ss += __shfl_xor(ss, 2, 64);
   if (q == 0) sm.inv_nak[s] = 1.0f / fmaxf(sqrtf(ss), 1e-12f);
+}
+
+// Inverse slot norms for the bf16 cosine match: 0 for the slots a fill step masks (their
+// rows are zero in every state the chain builds, so the cosine is exactly 0 either way).
+template <typename T, int HD>
+__device__ __forceinline__ void masked_norms(DecSmem<T, HD>& sm, int tid, bool steady) {
+  if (tid < S) sm.tnn[tid] = (steady || sm.act[tid]) ? sm.inv_nak[tid] : 0.f;
 }
 
 // ----------------------------------------------------------------- decide: retrieval
@@ -625,6 +637,10 @@ __device__ __forceinline__ float max4g(float v) {
 // [t0, t0 + 16) of one wavefront (bf16 storage).  Writes rel / score / slot / flags (and
 // the log's best cosine and value cosine) of its tokens; no barrier inside.  Returns the
 // merge flag of token t0 + lane (lanes 0..15).
+// The softmax runs in base 2: x' = round_bf(q.k) * scale*log2(e) + bias*log2(e) (one FMA),
+// p = exp2(x' - max x'), which equals the reference's exp(x - max x) up to the last bits of
+// the exponent argument; slots masked in a fill step carry a -inf bias (at least one slot is
+// active whenever the slots are read).
 template <int HD>
 __device__ bool score_tile16(DecSmem<uint16_t, HD>& sm, const Tile16<HD>& td, int t0, int l, bool steady,
                              float scale, int lane, float* log) {
@@ -633,9 +649,9 @@ __device__ bool score_tile16(DecSmem<uint16_t, HD>& sm, const Tile16<HD>& td, in
   const int n = lane & 15, g = lane >> 4;
   const int tok = t0 + n;
 
-  // cos^T[slot][tok] = ak . kr^T / (|ak| |kr|); argmax on integer keys: slots ascend along
-  // each lane's scan and the cross-lane merge takes the lower slot on equal keys, so ties go
-  // to the lower index, and NaN (largest key) wins as torch.max does
+  // cos^T[slot][tok] = ak . kr^T / (|ak| |kr|); torch.max semantics: the largest value,
+  // the first NaN if there is one, ties to the lower slot (each lane scans its slots in
+  // ascending order; the cross-lane merge compares indices)
   float kk = 0.f;
 #pragma unroll
   for (int ks = 0; ks < NK; ++ks)
@@ -643,54 +659,70 @@ __device__ bool score_tile16(DecSmem<uint16_t, HD>& sm, const Tile16<HD>& td, in
     for (int i = 0; i < 8; ++i) { const float x = bf2f(td.k[ks][i]); kk += x * x; }
   kk = sum4g(kk);
   const float inv_nk = 1.0f / fmaxf(sqrtf(kk), 1e-12f);
-  uint32_t bkey = 0;
-  float bv = 0.f;
+  float bv = -INFINITY;
   int bs = -1;
+  bool bnan = false;
+  // A operands of the next slot block are read from LDS while the current one multiplies
+  u16x8 op[2][NK];
+#pragma unroll
+  for (int ks = 0; ks < NK; ++ks) op[0][ks] = *reinterpret_cast<const u16x8*>(&sm.ak[n * Sm::KS + 32 * ks + 8 * g]);
 #pragma unroll
   for (int mb = 0; mb < NMB; ++mb) {
+    if (mb + 1 < NMB) {
+#pragma unroll
+      for (int ks = 0; ks < NK; ++ks)
+        op[(mb + 1) & 1][ks] = *reinterpret_cast<const u16x8*>(&sm.ak[(16 * (mb + 1) + n) * Sm::KS + 32 * ks + 8 * g]);
+    }
     f32x4 c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int ks = 0; ks < NK; ++ks)
-      mma16_bf16(c, *reinterpret_cast<const u16x8*>(&sm.ak[(16 * mb + n) * Sm::KS + 32 * ks + 8 * g]), td.k[ks]);
+    for (int ks = 0; ks < NK; ++ks) mma16_bf16(c, op[mb & 1][ks], td.k[ks]);
     const int s0 = 16 * mb + 4 * g;
-    const float4 n4 = *reinterpret_cast<const float4*>(&sm.inv_nak[s0]);
+    const float4 n4 = *reinterpret_cast<const float4*>(&sm.tnn[s0]);
     const float nn[4] = {n4.x, n4.y, n4.z, n4.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      float cv = c[i] * (nn[i] * inv_nk);
-      if (!steady && !sm.act[s0 + i]) cv = 0.f;
-      const uint32_t key = ord_key(cv + 0.0f);   // -0 ranks with +0, as in a float compare
-      if (bs < 0 || key > bkey) { bkey = key; bv = cv; bs = s0 + i; }
+      const float cv = c[i] * (nn[i] * inv_nk);
+      const bool isn = cv != cv;
+      const bool take = !bnan && (cv > bv || isn);   // selects, no branches
+      bv = take ? cv : bv;
+      bs = take ? s0 + i : bs;
+      bnan = bnan || isn;
     }
   }
 #pragma unroll
   for (int o = 16; o <= 32; o <<= 1) {
-    const uint32_t ok = (uint32_t)__shfl_xor((int)bkey, o, 64);
     const float ov = __shfl_xor(bv, o, 64);
     const int os = __shfl_xor(bs, o, 64);
-    if (ok > bkey || (ok == bkey && os < bs)) { bkey = ok; bv = ov; bs = os; }
+    const bool onan = ov != ov;
+    const bool take = onan ? (!bnan || os < bs) : (!bnan && (ov > bv || (ov == bv && os < bs)));
+    if (take) { bv = ov; bs = os; bnan = onan; }
   }
 
-  // scores^T[slot][tok] = kread . kp^T, rounded to bf16, scaled, plus the slot bias
+  // scores^T[slot][tok] = kread . kp^T, rounded to bf16, in base-2 units with the slot bias
   f32x4 acc[NMB];
 #pragma unroll
+  for (int ks = 0; ks < NK; ++ks) op[0][ks] = *reinterpret_cast<const u16x8*>(&sm.kread[n * Sm::KS + 32 * ks + 8 * g]);
+#pragma unroll
   for (int mb = 0; mb < NMB; ++mb) {
+    if (mb + 1 < NMB) {
+#pragma unroll
+      for (int ks = 0; ks < NK; ++ks)
+        op[(mb + 1) & 1][ks] =
+            *reinterpret_cast<const u16x8*>(&sm.kread[(16 * (mb + 1) + n) * Sm::KS + 32 * ks + 8 * g]);
+    }
     acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int ks = 0; ks < NK; ++ks)
-      mma16_bf16(acc[mb], *reinterpret_cast<const u16x8*>(&sm.kread[(16 * mb + n) * Sm::KS + 32 * ks + 8 * g]),
-                 td.q[ks]);
+    for (int ks = 0; ks < NK; ++ks) mma16_bf16(acc[mb], op[mb & 1][ks], td.q[ks]);
   }
+  const float sL = scale * 1.4426950408889634f;
   float mx = -INFINITY;
 #pragma unroll
   for (int mb = 0; mb < NMB; ++mb) {
-    const int s0 = 16 * mb + 4 * g;
-    const float4 b4 = *reinterpret_cast<const float4*>(&sm.bias[s0]);
+    const float4 b4 = *reinterpret_cast<const float4*>(&sm.tbl[16 * mb + 4 * g]);
     const float bb[4] = {b4.x, b4.y, b4.z, b4.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      float x = add_rn(mul_rn(round_bf(acc[mb][i]), scale), bb[i]);
-      if (!steady && !sm.act[s0 + i]) x = -1e9f;
+      const float x = fmaf(round_bf(acc[mb][i]), sL, bb[i]);
       acc[mb][i] = x;
       mx = fmaxf(mx, x);
     }
@@ -701,7 +733,7 @@ __device__ bool score_tile16(DecSmem<uint16_t, HD>& sm, const Tile16<HD>& td, in
   for (int mb = 0; mb < NMB; ++mb)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float e = expf(acc[mb][i] - mx);
+      const float e = __builtin_amdgcn_exp2f(acc[mb][i] - mx);
       acc[mb][i] = e;
       sum += e;
     }
@@ -714,31 +746,33 @@ __device__ bool score_tile16(DecSmem<uint16_t, HD>& sm, const Tile16<HD>& td, in
   for (int kk2 = 0; kk2 < S / 32; ++kk2)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      pb[kk2][i] = f2bf(mul_rn(acc[2 * kk2][i], rs));
-      pb[kk2][4 + i] = f2bf(mul_rn(acc[2 * kk2 + 1][i], rs));
+      pb[kk2][i] = f2bf(acc[2 * kk2][i] * rs);
+      pb[kk2][4 + i] = f2bf(acc[2 * kk2 + 1][i] * rs);
     }
 
   // v_hat^T[d][tok], rel_err sums; this lane owns features 16*db + 4*g + i of token tok
   float e2 = 0.f, v2 = 0.f;
+  u16x8 vo[2][S / 32];
+#pragma unroll
+  for (int kk2 = 0; kk2 < S / 32; ++kk2)
+    vo[0][kk2] = *reinterpret_cast<const u16x8*>(&sm.avt[n * Sm::VTS + 8 * g + 32 * kk2]);
 #pragma unroll
   for (int db = 0; db < ND; ++db) {
-    f32x4 vh = {0.f, 0.f, 0.f, 0.f};
-    const uint16_t* row = &sm.avt[(16 * db + n) * Sm::VTS + 4 * g];
+    if (db + 1 < ND) {
 #pragma unroll
-    for (int kk2 = 0; kk2 < S / 32; ++kk2) {
-      const u16x4 lo = *reinterpret_cast<const u16x4*>(row + 32 * kk2);
-      const u16x4 hi = *reinterpret_cast<const u16x4*>(row + 32 * kk2 + 16);
-      u16x8 a;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) { a[i] = lo[i]; a[4 + i] = hi[i]; }
-      mma16_bf16(vh, a, pb[kk2]);
+      for (int kk2 = 0; kk2 < S / 32; ++kk2)
+        vo[(db + 1) & 1][kk2] =
+            *reinterpret_cast<const u16x8*>(&sm.avt[(16 * (db + 1) + n) * Sm::VTS + 8 * g + 32 * kk2]);
     }
+    f32x4 vh = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk2 = 0; kk2 < S / 32; ++kk2) mma16_bf16(vh, vo[db & 1][kk2], pb[kk2]);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float x = bf2f(td.v[db][i]);
       const float dv = x - round_bf(vh[i]);
-      e2 += dv * dv;
-      v2 += x * x;
+      e2 = fmaf(dv, dv, e2);
+      v2 = fmaf(x, x, v2);
     }
   }
   e2 = sum4g(e2);
@@ -755,8 +789,8 @@ __device__ bool score_tile16(DecSmem<uint16_t, HD>& sm, const Tile16<HD>& td, in
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float x = bf2f(td.v[db][i]), y = bf2f(y4[i]);
-        dvv += x * y;
-        aa += y * y;
+        dvv = fmaf(x, y, dvv);
+        aa = fmaf(y, y, aa);
       }
     }
     dvv = sum4g(dvv);
@@ -800,8 +834,8 @@ __device__ bool score_phase16(DecSmem<uint16_t, HD>& sm, Tile16<HD>& td, bool re
 }
 
 // av^T columns of the slots whose values changed (vdirty): an item is two adjacent slots
-// and 8 features, written as 8 dwords (lanes of a wavefront take adjacent slot pairs, so
-// their writes fall into distinct banks).
+// (adjacent in the permuted column order too) and 8 features, written as 8 dwords; lanes of
+// a wavefront take adjacent slot pairs, so their writes fall into distinct banks.
 template <typename T, int HD>
 __device__ void transpose_dirty_v(DecSmem<T, HD>& sm, int tid) {
   if constexpr (DecSmem<T, HD>::BF) {
@@ -810,9 +844,10 @@ __device__ void transpose_dirty_v(DecSmem<T, HD>& sm, int tid) {
       if (!sm.vdirty[s] && !sm.vdirty[s + 1]) continue;
       const u16x8 x0 = *reinterpret_cast<const u16x8*>(&sm.av[s * sm.KS + d8]);
       const u16x8 x1 = *reinterpret_cast<const u16x8*>(&sm.av[(s + 1) * sm.KS + d8]);
+      const int r = s & 31, col = (s & ~31) + 8 * ((r & 15) >> 2) + 4 * (r >> 4) + (r & 3);
 #pragma unroll
       for (int q = 0; q < 8; ++q)
-        *reinterpret_cast<uint32_t*>(&sm.avt[(d8 + q) * sm.VTS + s]) = (uint32_t)x0[q] | ((uint32_t)x1[q] << 16);
+        *reinterpret_cast<uint32_t*>(&sm.avt[(d8 + q) * sm.VTS + col]) = (uint32_t)x0[q] | ((uint32_t)x1[q] << 16);
     }
   }
 }
@@ -911,11 +946,16 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
       sm.util[tid] = mul_rn(sm.util[tid], UTIL_DECAY);
       const float lm = logf(fmaxf(sm.mass[tid], 1.0f));
       sm.bias[tid] = steady ? mul_rn(kap, lm) : lm;
+      sm.tbl[tid] = (steady || sm.act[tid]) ? sm.bias[tid] * 1.4426950408889634f : -INFINITY;
       sm.dirty[tid] = 0;
       sm.vdirty[tid] = 0;
     }
     slot_norms<T, HD>(sm, tid);
     sync_lds();
+    if constexpr (BF) {
+      masked_norms<T, HD>(sm, tid, steady);
+      sync_lds();
+    }
 
     // ---------------- retrieval scores: first fill ranks by value variance; later fills and
     // steady steps read the slots

@@ -600,25 +600,36 @@ struct Tile16 {
   u16x8 q[NK];   // roped keys kp[tok][32*ks + 8*g + i]
   u16x8 k[NK];   // un-roped keys kr[tok][32*ks + 8*g + i]
   u16x4 v[ND];   // values v[tok][16*db + 4*g + i]
+  // part 1: roped keys, 2: un-roped keys, 4: values (a mask), so that the loads of a prefetch
+  // can be spread over the phases of a step
   __device__ __forceinline__ void load(const uint16_t* kp, const uint16_t* kr, const uint16_t* vv, int t0, int l,
-                                       int lane) {
+                                       int lane, int parts = 7) {
     const int n = lane & 15, g = lane >> 4, tok = t0 + n;
     const bool ok = tok < l;
     const long long o = (long long)tok * HD;
 #pragma unroll
     for (int ks = 0; ks < NK; ++ks) {
-      if (ok) {
-        q[ks] = *reinterpret_cast<const u16x8*>(kp + o + 32 * ks + 8 * g);
-        k[ks] = *reinterpret_cast<const u16x8*>(kr + o + 32 * ks + 8 * g);
-      } else {
+      if (parts & 1) {
+        if (ok) q[ks] = *reinterpret_cast<const u16x8*>(kp + o + 32 * ks + 8 * g);
+        else {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) { q[ks][i] = 0; k[ks][i] = 0; }
+          for (int i = 0; i < 8; ++i) q[ks][i] = 0;
+        }
+      }
+      if (parts & 2) {
+        if (ok) k[ks] = *reinterpret_cast<const u16x8*>(kr + o + 32 * ks + 8 * g);
+        else {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) k[ks][i] = 0;
+        }
       }
     }
+    if (parts & 4) {
 #pragma unroll
-    for (int db = 0; db < ND; ++db) {
-      if (ok) v[db] = *reinterpret_cast<const u16x4*>(vv + o + 16 * db + 4 * g);
-      else { v[db][0] = 0; v[db][1] = 0; v[db][2] = 0; v[db][3] = 0; }
+      for (int db = 0; db < ND; ++db) {
+        if (ok) v[db] = *reinterpret_cast<const u16x4*>(vv + o + 16 * db + 4 * g);
+        else { v[db][0] = 0; v[db][1] = 0; v[db][2] = 0; v[db][3] = 0; }
+      }
     }
   }
 };
@@ -912,12 +923,14 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
   using TD = std::conditional_t<BF, Tile16<HD>, TileIn<T, HD>>;
   TD td;
   bool td_ready = false;
-  auto prefetch = [&](int step, int wave, int lane) {
+  // parts: 1 roped keys, 2 un-roped keys, 4 values; a steady step issues them after the
+  // scoring, the keep scores and the orderings, a fill step all at once
+  auto prefetch = [&](int step, int wave, int lane, int parts) {
     if constexpr (BF) {
       if (step + 1 < a.n_steps) {
         const long long nb = (long long)bh * a.tok_bh_stride + (long long)step_off(a, step + 1) * HD;
         td.load(reinterpret_cast<const T*>(a.kp) + nb, reinterpret_cast<const T*>(a.kr) + nb,
-                reinterpret_cast<const T*>(a.v) + nb, 16 * wave, step_len(a, step + 1), lane);
+                reinterpret_cast<const T*>(a.v) + nb, 16 * wave, step_len(a, step + 1), lane, parts);
         td_ready = true;
       }
     }
@@ -996,7 +1009,7 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
       else has = score_phase<T, HD>(sm, kread, td, td_ready, kr, kp, v, l, steady, scale, wave, lane, tid, log);
     }
     td_ready = false;
-    prefetch(step, wave, lane);
+    prefetch(step, wave, lane, steady ? 1 : 7);
     if (has) sm.any_merge = 1;
     sync_lds();
 
@@ -1108,19 +1121,53 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
         fc.load_lds(sm.ak, KS, col, lane);
         float mx = -INFINITY;
         bool has_nan = false;
+        if constexpr (BF) {
+          // operands of a block read together; inverse norms as float4 (rows 4*(r/4)+.. are
+          // consecutive); NaN tracked through c*0
+          const float inv_c = sm.inv_nak[col];
+          const int h = lane >> 5;
+          float chk = 0.f;
 #pragma unroll
-        for (int m2 = 0; m2 < 2; ++m2) {
-          const int mb = 2 * rh + m2;
-          f32x16 acc = zero16();
-          mm_rows_frag<HD>(acc, sm.ak, KS, 32 * mb, fc, lane);
+          for (int m2 = 0; m2 < 2; ++m2) {
+            const int mb = 2 * rh + m2;
+            u16x8 ab[HD / 16];
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int row = 32 * mb + d_row(lane, r);
-            // one rounded product of the two inverse norms keeps the matrix bitwise symmetric,
-            // so mutual nearest slots (equal utility) get bit-equal keep values as in the reference
-            const float c = row == col ? -1.0f : acc[r] * (sm.inv_nak[row] * sm.inv_nak[col]);
-            has_nan |= (c != c);
-            mx = fmaxf(mx, c);
+            for (int ks = 0; ks < HD / 16; ++ks)
+              ab[ks] = *reinterpret_cast<const u16x8*>(&sm.ak[(32 * mb + n) * KS + 16 * ks + 8 * h]);
+            f32x16 acc = zero16();
+#pragma unroll
+            for (int ks = 0; ks < HD / 16; ++ks) mma_bf16(acc, ab[ks], fc.v[ks]);
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4) {
+              const float4 i4 = *reinterpret_cast<const float4*>(&sm.inv_nak[32 * mb + 8 * r4 + 4 * h]);
+              const float iv[4] = {i4.x, i4.y, i4.z, i4.w};
+#pragma unroll
+              for (int q = 0; q < 4; ++q) {
+                const int row = 32 * mb + 8 * r4 + 4 * h + q;
+                // one rounded product of the two inverse norms keeps the matrix bitwise
+                // symmetric, so mutual nearest slots (equal utility) get bit-equal keep values
+                const float c = row == col ? -1.0f : acc[4 * r4 + q] * (iv[q] * inv_c);
+                chk = fmaf(c, 0.f, chk);
+                mx = fmaxf(mx, c);
+              }
+            }
+          }
+          has_nan = chk != chk;
+        } else {
+#pragma unroll
+          for (int m2 = 0; m2 < 2; ++m2) {
+            const int mb = 2 * rh + m2;
+            f32x16 acc = zero16();
+            mm_rows_frag<HD>(acc, sm.ak, KS, 32 * mb, fc, lane);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int row = 32 * mb + d_row(lane, r);
+              // one rounded product of the two inverse norms keeps the matrix bitwise symmetric,
+              // so mutual nearest slots (equal utility) get bit-equal keep values as in the reference
+              const float c = row == col ? -1.0f : acc[r] * (sm.inv_nak[row] * sm.inv_nak[col]);
+              has_nan |= (c != c);
+              mx = fmaxf(mx, c);
+            }
           }
         }
         mx = fmaxf(mx, xor32(mx));
@@ -1131,6 +1178,7 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
         }
       }
       sync_lds();
+      prefetch(step, wave, lane, 2);
       float keep_v = 0.f, ck_v = 0.f;   // keep value of slot tid, candidate value of token tid
       if (tid < S) {
         float mx = fmaxf(sm.u.kp.mx[0][tid], sm.u.kp.mx[1][tid]);
@@ -1171,6 +1219,7 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
         }
       }
       sync_lds();
+      prefetch(step, wave, lane, 4);
       const int kc = min(l, S);
       // win_i = top_i > bot_i and top_i > -1e8 ; token top_i replaces slot bot_i
       if (tid < kc) {

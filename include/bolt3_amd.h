@@ -67,6 +67,9 @@ typedef struct {
   b3_tensor_out q_raw, q_rope, k_raw, k_rope, v;  /* q_raw / k_raw may have p == NULL */
   b3_gate_out beta, eta;      /* sigmoid / tanh gates, values rounded to the storage dtype */
   float* pos_out;             /* optional fp32 [T]: pos0 + t */
+  const void* gates;          /* optional [B][T][gates_row_stride]: beta (HKV) | eta (H) projection columns;
+                                 when set, the gates are read here instead of from lin / lin_kv */
+  int64_t gates_row_stride;
 } b3_heads_args;
 
 /*

@@ -41,7 +41,7 @@ class HeadsArgs(C.Structure):
         ("qn_w", p), ("kn_w", p), ("has_qk_norm", i32), ("eps", f32),
         ("inv_freq", p), ("pos0", i32),
         ("q_raw", TensorOut), ("q_rope", TensorOut), ("k_raw", TensorOut), ("k_rope", TensorOut), ("v", TensorOut),
-        ("beta", GateOut), ("eta", GateOut), ("pos_out", p),
+        ("beta", GateOut), ("eta", GateOut), ("pos_out", p), ("gates", p), ("gates_row_stride", i64),
     ]
 
 

@@ -52,9 +52,15 @@ CHAIN_GROUPS = 4
 
 
 def _step_groups(n: int, k: int) -> list[tuple[int, int]]:
-    """Split steps [0, n) into at most k contiguous, nearly equal ranges."""
+    """Split steps [0, n) into at most k contiguous ranges: a short first one (about n / (2k - 2)
+    steps, so that the attention can start while the q projection finishes), the rest nearly
+    equal."""
     k = max(1, min(k, n))
-    bounds = [n * i // k for i in range(k + 1)]
+    if k == 1:
+        return [(0, n)]
+    first = max(1, n // (2 * k - 2))
+    rest = n - first
+    bounds = [0, first] + [first + rest * i // (k - 1) for i in range(1, k)]
     return [(bounds[i], bounds[i + 1]) for i in range(k) if bounds[i + 1] > bounds[i]]
 
 
@@ -137,8 +143,8 @@ class Bolt3Attn(nn.Module):
 
     def _packed(self, dt: torch.dtype, device: torch.device):
         """(W_all, b_all, side) cached until a parameter changes.  W_all packs q | k | v | beta | eta
-        rows (the decoder's one projection); side holds W_o, the split projections q | eta and
-        k | v | beta used by the forward, and the fp32 tensors the kernels read."""
+        rows (the decoder's one projection); side holds W_o, the split projections q, k | v and
+        beta | eta used by the forward, and the fp32 tensors the kernels read."""
         params = list(self.parameters())
         key = (dt, device, tuple((q.data_ptr(), q._version) for q in params), self.rope.inv_freq.data_ptr())
         if key == self._pack_key:
@@ -167,10 +173,13 @@ class Bolt3Attn(nn.Module):
                                     .to(device=device, dtype=dt) for m in ms] +
                                    [torch.zeros(pd, device=device, dtype=dt)]).contiguous()
                 return torch.cat(w, dim=0).contiguous(), bb
-            wq, bq = pack((self.q_proj, self.eta_proj))
-            wkv, bkv = pack((self.k_proj, self.v_proj, self.beta_proj))
+            # the forward projects q, k | v and the gates beta | eta separately: q and k | v then
+            # have 4096 and 2048 columns, widths the GEMM tiles divide
+            wq, bq = pack((self.q_proj,))
+            wkv, bkv = pack((self.k_proj, self.v_proj))
+            wg, bg = pack((self.beta_proj, self.eta_proj))
             side = dict(
-                wq=wq, bq=bq, wkv=wkv, bkv=bkv,
+                wq=wq, bq=bq, wkv=wkv, bkv=bkv, wg=wg, bg=bg,
                 wo=self.o_proj.weight.to(device=device, dtype=dt).contiguous(),
                 inv_freq=self.rope.inv_freq.to(device).float().contiguous(),
                 kappa=self.kappa.detach().to(device).float().contiguous(),
@@ -184,7 +193,7 @@ class Bolt3Attn(nn.Module):
         return self._pack
 
     def _heads(self, lin, B, T, dt, side, pos0, q_raw, q_rope, k_raw, k_rope, v, beta, eta, pos_out=None,
-               kv_offset=0, lin_kv=None, parts=0):
+               kv_offset=0, lin_kv=None, parts=0, gates=None):
         a = A.HeadsArgs()
         a.dtype, a.B, a.T, a.H, a.HKV, a.HD = A.dtype_code(dt), B, T, self.H, self.HKV, self.HD
         if lin is not None:
@@ -192,6 +201,8 @@ class Bolt3Attn(nn.Module):
         if lin_kv is not None:
             a.lin_kv, a.lin_kv_row_stride = lin_kv.data_ptr(), lin_kv.shape[-1]
         a.parts = parts
+        if gates is not None:
+            a.gates, a.gates_row_stride = gates.data_ptr(), gates.shape[-1]
         a.qn_w, a.kn_w = A.ptr(side["qn"]), A.ptr(side["kn"])
         a.has_qk_norm = int(side["qn"] is not None)
         a.eps = float(self.res_norm.eps)
@@ -252,15 +263,19 @@ class Bolt3Attn(nn.Module):
         _, _, side = self._packed(dt, dev)
         gam = side["gamma"]
         main = torch.cuda.current_stream(dev)
-        # k | v | beta first: the consolidation chain needs only them, so it runs on a side
-        # stream while the q | eta projection and head preparation proceed on this one
+        # k | v and the gates first: the consolidation chain needs only k, v and beta, so it runs
+        # on a side stream while the q head preparation and the attention proceed on this one.
+        # The q projection comes before the chain starts: the slot decisions are latency-bound
+        # and a large GEMM beside them slows them several-fold.
         lin_kv = F.linear(x, side["wkv"], side["bkv"])
+        gates = F.linear(x, side["wg"], side["bg"])
+        lin_q = F.linear(x, side["wq"], side["bq"])
         k_raw = torch.empty(b, HKV, T, HD, dtype=dt, device=dev)
         k_rope, v = torch.empty_like(k_raw), torch.empty_like(k_raw)
         beta = torch.empty(b, HKV, T, device=dev)
         pos = torch.empty(T, device=dev)
         self._heads(None, b, T, dt, side, 0, None, None, k_raw, k_rope, v, beta, None, pos_out=pos,
-                    lin_kv=lin_kv, parts=2)
+                    lin_kv=lin_kv, parts=2, gates=gates)
 
         n_chunks = (T + C - 1) // C
         n_cons = max(0, n_chunks - 2)
@@ -319,11 +334,11 @@ class Bolt3Attn(nn.Module):
             if trace is not None:
                 trace.update(state=st, m_res=m_res, snap_k=snaps[0], snap_v=snaps[1], snap_bias=snaps[2],
                              snap_m=snaps[3], log=log)
-        lin_q = F.linear(x, side["wq"], side["bq"])
         q_raw = torch.empty(b, H, T, HD, dtype=dt, device=dev)
         q_rope = torch.empty_like(q_raw)
         eta = torch.empty(b, H, T, device=dev)
-        self._heads(lin_q, b, T, dt, side, 0, q_raw, q_rope, None, None, None, None, eta, lin_kv=lin_kv, parts=1)
+        self._heads(lin_q, b, T, dt, side, 0, q_raw, q_rope, None, None, None, None, eta, lin_kv=lin_kv, parts=1,
+                    gates=gates)
         if trace is not None:
             trace.update(q_raw=q_raw, q_rope=q_rope, k_raw=k_raw, k_rope=k_rope, v=v, beta=beta, eta=eta, pos=pos)
 
@@ -350,10 +365,11 @@ class Bolt3Attn(nn.Module):
                 trace["y"] = y
             return F.linear(y, side["wo"])
 
-        # Sinks + window of every chunk while the chain runs; then, group by group, the slot
-        # field merged into the saved online-softmax state, the readout and o_proj.  The
-        # attention output of a group of chunks is one [B * rows, H * HD] block (token ranges
-        # of all batch rows together), so o_proj of a group is one GEMM.
+        # Group by group, as soon as the chain has produced a group's snapshots: the attention
+        # over all key fields of the group's chunks (the first group also takes chunks 0 and 1),
+        # the readout and o_proj.  The attention output of a group of chunks is one
+        # [B * rows, H * HD] block (token ranges of all batch rows together), so o_proj of a
+        # group is one GEMM.
         spans = [(0, min(T, (groups[0][1] + 2) * C))] + \
                 [(min(T, (s0 + 2) * C), min(T, (s1 + 2) * C)) for s0, s1 in groups[1:]]
         y_all = torch.empty(b * T * K, dtype=dt, device=dev)
@@ -363,22 +379,14 @@ class Bolt3Attn(nn.Module):
             off += b * (t1 - t0) * K
         out = torch.empty(b, T, self.o_proj.out_features, dtype=dt, device=dev)
         esz = y_all.element_size()
-
-        def point_y(gi):   # element (b, t) of block gi at block + (b * rows + t - t0) * K
-            t0, t1 = spans[gi]
-            a.y, a.y_sb, a.y_st = blocks[gi].data_ptr() - t0 * K * esz, (t1 - t0) * K, K
-
-        partial = torch.empty(b, H, T, HD + 4, device=dev)
-        a.part, a.partial = 1, partial.data_ptr()
-        point_y(0)   # part 1 writes the outputs of chunks 0 and 1 only
-        A.call("bolt3_chunk_attn", a, dev)
-        a.part = 2
+        a.part = 0
         for gi, ((s0, s1), ev) in enumerate(zip(groups, done)):
-            main.wait_event(ev)
-            a.chunk_begin, a.chunk_end = s0 + 2, s1 + 2
-            point_y(gi)
-            A.call("bolt3_chunk_attn", a, dev)
             t0, t1 = spans[gi]
+            main.wait_event(ev)
+            a.chunk_begin, a.chunk_end = (0 if gi == 0 else s0 + 2), s1 + 2
+            # element (b, t) of block gi at block + (b * rows + t - t0) * K
+            a.y, a.y_sb, a.y_st = blocks[gi].data_ptr() - t0 * K * esz, (t1 - t0) * K, K
+            A.call("bolt3_chunk_attn", a, dev)
             out[:, t0:t1].copy_(F.linear(blocks[gi], side["wo"]).view(b, t1 - t0, -1))
         if trace is not None:
             trace["y"] = torch.cat([blk.view(b, t1 - t0, K) for blk, (t0, t1) in zip(blocks, spans)], dim=1)

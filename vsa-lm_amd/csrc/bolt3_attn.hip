@@ -421,6 +421,7 @@ __global__ void __launch_bounds__(512) attn_fwd_kernel(b3_attn_args a, int QW) {
   const int step = chunk - 2;
   const float L2E = 1.4426950408889634f;
   const float scale = 1.0f / sqrtf((float)HD);
+  const float sL = scale * L2E;
 
   // ---- block schedule
   const long long wofs = (long long)b * a.w_sb + (long long)hkv * a.w_sh;
@@ -468,8 +469,12 @@ __global__ void __launch_bounds__(512) attn_fwd_kernel(b3_attn_args a, int QW) {
     return f;
   };
 
-  // ---- staging registers: IPT 16-byte K and V pieces per thread, plus one bias value
-  u16x8 rk[IPT], rv[IPT];
+  // ---- staging registers: IPT 16-byte K pieces per thread (rows in order); V^T is staged by
+  // key pairs (keys 2p, 2p+1 at 8 features: 8 dword writes of two bf16 each; the lanes of a
+  // wavefront take consecutive pairs, so the writes fall into distinct banks); plus one bias
+  // value in log2 units
+  constexpr int VITEMS = (KB / 2) * (HD / 8);
+  u16x8 rk[IPT], rv0[IPT], rv1[IPT];
   float rb = 0.f;
   auto load = [&](int i) {
     const FwdBlock f = block(i);
@@ -477,15 +482,25 @@ __global__ void __launch_bounds__(512) attn_fwd_kernel(b3_attn_args a, int QW) {
     for (int q = 0; q < IPT; ++q) {
       const int it = tid + q * nthreads;
       const int r = it / (HD / 8), c8 = (it % (HD / 8)) * 8;
-      if (it < ITEMS && r < f.nvalid) {
-        rk[q] = *reinterpret_cast<const u16x8*>(f.k + (long long)r * HD + c8);
-        rv[q] = *reinterpret_cast<const u16x8*>(f.v + (long long)r * HD + c8);
-      } else {
+      if (it < ITEMS && r < f.nvalid) rk[q] = *reinterpret_cast<const u16x8*>(f.k + (long long)r * HD + c8);
+      else {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) { rk[q][e] = 0; rv[q][e] = 0; }
+        for (int e = 0; e < 8; ++e) rk[q][e] = 0;
+      }
+      const int pr = it % (KB / 2), vc8 = (it / (KB / 2)) * 8;
+      if (it < VITEMS && 2 * pr < f.nvalid) rv0[q] = *reinterpret_cast<const u16x8*>(f.v + (long long)(2 * pr) * HD + vc8);
+      else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) rv0[q][e] = 0;
+      }
+      if (it < VITEMS && 2 * pr + 1 < f.nvalid)
+        rv1[q] = *reinterpret_cast<const u16x8*>(f.v + (long long)(2 * pr + 1) * HD + vc8);
+      else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) rv1[q][e] = 0;
       }
     }
-    rb = (tid < KB && f.bias && tid < f.nvalid) ? f.bias[tid] : 0.f;
+    rb = (tid < KB && f.bias && tid < f.nvalid) ? f.bias[tid] * L2E : 0.f;
   };
   auto store = [&](int buf) {
     uint16_t* sK = sm.k(buf);
@@ -496,8 +511,16 @@ __global__ void __launch_bounds__(512) attn_fwd_kernel(b3_attn_args a, int QW) {
       if (it < ITEMS) {
         const int r = it / (HD / 8), c8 = (it % (HD / 8)) * 8;
         *reinterpret_cast<u16x8*>(sK + r * Sm::KS + c8) = rk[q];
+      }
+      if (it < VITEMS) {
+        const int pr = it % (KB / 2), vc8 = (it / (KB / 2)) * 8;
+        // key k sits at column (k & ~15) + 4*[0,2,1,3][(k >> 2) & 3] + (k & 3): the 8 keys
+        // 16kc + {4h..4h+3, 8+4h..8+4h+3} of MFMA lane group h are then 8 contiguous columns
+        const int k0 = 2 * pr, qd = (k0 >> 2) & 3;
+        const int col = (k0 & ~15) + 4 * ((qd == 1) ? 2 : (qd == 2) ? 1 : qd) + (k0 & 3);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) sV[(c8 + e) * Sm::VS + r] = rv[q][e];
+        for (int e = 0; e < 8; ++e)
+          *reinterpret_cast<uint32_t*>(sV + (vc8 + e) * Sm::VS + col) = (uint32_t)rv0[q][e] | ((uint32_t)rv1[q][e] << 16);
       }
     }
     if (tid < KB) sm.bias[buf][tid] = rb;
@@ -543,37 +566,54 @@ __global__ void __launch_bounds__(512) attn_fwd_kernel(b3_attn_args a, int QW) {
         const u16x8 av = *reinterpret_cast<const u16x8*>(sK + n * Sm::KS + 16 * ks + 8 * h);
         mma_bf16(s, av, qf.v[ks]);
       }
-      // valid keys of this lane's query: kr <= lim
-      const int lim = min(f.nvalid - 1, f.kpos >= 0 ? qi - f.kpos : KB - 1);
+      // scores in log2 units: round_bf(q.k) * scale*log2(e) (+ slot bias * log2(e)), one FMA
       float bm = -INFINITY;
+      if (f.bias) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int kr = d_row(lane, r);
-        // the staged bias is 0 outside slot blocks
-        float x = add_rn(mul_rn(round_bf(s[r]), scale), sm.bias[buf][kr]);
-        x = kr <= lim ? x : -INFINITY;
-        s[r] = x;
-        bm = fmaxf(bm, x);
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const float4 b4 = *reinterpret_cast<const float4*>(&sm.bias[buf][8 * r4 + 4 * h]);
+          const float bb[4] = {b4.x, b4.y, b4.z, b4.w};
+#pragma unroll
+          for (int q = 0; q < 4; ++q) s[4 * r4 + q] = fmaf(round_bf(s[4 * r4 + q]), sL, bb[q]);
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[r] = round_bf(s[r]) * sL;
       }
+      if (f.kpos >= 0 || f.nvalid < KB) {
+        // valid keys of this lane's query: kr <= lim
+        const int lim = min(f.nvalid - 1, f.kpos >= 0 ? qi - f.kpos : KB - 1);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[r] = d_row(lane, r) <= lim ? s[r] : -INFINITY;
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) bm = fmaxf(bm, s[r]);
       bm = fmaxf(bm, xor32(bm));
-      const float m_new = fmaxf(m_run, bm);
-      if (m_new != -INFINITY) {
-        const float mL = m_new * L2E;
-        const float alpha = __builtin_amdgcn_exp2f(fmaf(m_run, L2E, -mL));
+      // the running max moves only when it grows by more than 2^8 (probabilities up to 2^8
+      // before the final normalisation are exact enough in fp32 and rescale-free)
+      const bool grow = bm > m_run + 8.0f;
+      const float m_use = grow ? bm : m_run;
+      {
+        // a lane whose keys so far are all masked keeps m = -inf: p = 0 and alpha = 0 for it
+        const float mu = m_use == -INFINITY ? 0.f : m_use;
         float ps = 0.f;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const float p = __builtin_amdgcn_exp2f(fmaf(s[r], L2E, -mL));
+          const float p = __builtin_amdgcn_exp2f(s[r] - mu);
           s[r] = p;
           ps += p;
         }
         ps += xor32(ps);
-        l_run = l_run * alpha + ps;
-        m_run = m_new;
+        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+          const float alpha = __builtin_amdgcn_exp2f(m_run - mu);   // m_run = -inf: alpha = 0
 #pragma unroll
-        for (int db = 0; db < NDB; ++db)
+          for (int db = 0; db < NDB; ++db)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+            for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+          l_run *= alpha;
+        }
+        l_run += ps;
+        m_run = m_use;
         u16x8 pv[2];
 #pragma unroll
         for (int kc = 0; kc < 2; ++kc)
@@ -584,14 +624,8 @@ __global__ void __launch_bounds__(512) attn_fwd_kernel(b3_attn_args a, int QW) {
         for (int db = 0; db < NDB; ++db) {
           const int d = 32 * db + n;
 #pragma unroll
-          for (int kc = 0; kc < 2; ++kc) {
-            u16x8 av;
-            const u16x4 lo = *reinterpret_cast<const u16x4*>(sV + d * Sm::VS + 16 * kc + 4 * h);
-            const u16x4 hi = *reinterpret_cast<const u16x4*>(sV + d * Sm::VS + 16 * kc + 8 + 4 * h);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) { av[e] = lo[e]; av[4 + e] = hi[e]; }
-            mma_bf16(o[db], av, pv[kc]);
-          }
+          for (int kc = 0; kc < 2; ++kc)
+            mma_bf16(o[db], *reinterpret_cast<const u16x8*>(sV + d * Sm::VS + 16 * kc + 8 * h), pv[kc]);
         }
       }
     }

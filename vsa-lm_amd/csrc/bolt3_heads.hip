@@ -114,7 +114,8 @@ __global__ void __launch_bounds__(HEADS_NT) heads_kernel(b3_heads_args a) {
     const int t = t0 + tt;
     const long long tok = (long long)b * a.T + t;
     float z;
-    if (!split) z = St<T>::ld(reinterpret_cast<const T*>(a.lin) + tok * a.lin_row_stride + (a.H + 2 * a.HKV) * HD + g);
+    if (a.gates) z = St<T>::ld(reinterpret_cast<const T*>(a.gates) + tok * a.gates_row_stride + g);
+    else if (!split) z = St<T>::ld(reinterpret_cast<const T*>(a.lin) + tok * a.lin_row_stride + (a.H + 2 * a.HKV) * HD + g);
     else if (g < a.HKV) z = St<T>::ld(reinterpret_cast<const T*>(a.lin_kv) + tok * a.lin_kv_row_stride + 2 * a.HKV * HD + g);
     else z = St<T>::ld(reinterpret_cast<const T*>(a.lin) + tok * a.lin_row_stride + a.H * HD + (g - a.HKV));
     if (g < a.HKV) {
@@ -142,6 +143,7 @@ extern "C" int bolt3_heads(const b3_heads_args* a, void* stream) {
   const int parts = a->parts == 0 ? 3 : a->parts;
   if (parts < 0 || parts > 3 || a->H % a->HKV != 0 || !a->inv_freq) return B3_ERR_ARG;
   if ((parts & 1) && (!a->q_rope.p || !a->eta.p || !a->lin)) return B3_ERR_ARG;
+  if (a->gates && a->gates_row_stride < a->HKV + a->H) return B3_ERR_ARG;
   if ((parts & 2) && (!a->k_rope.p || !a->v.p || !a->beta.p || (!a->lin && !a->lin_kv))) return B3_ERR_ARG;
   if (a->has_qk_norm && (!a->qn_w || !a->kn_w)) return B3_ERR_ARG;
   // 16-byte vector moves: projection rows and head rows must start 16-byte aligned

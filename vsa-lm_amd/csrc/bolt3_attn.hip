@@ -731,6 +731,358 @@ __global__ void __launch_bounds__(512) attn_fwd_kernel(b3_attn_args a, int QW) {
   }
 }
 
+// ---------------------------------------------------------------- bf16 forward, DMA staging
+//
+// The same attention for the forward (mode 0, all key fields, bf16), with the K and V tiles
+// brought into LDS by global->LDS loads (global_load_lds_dwordx4) through a ring of NST
+// stages, NST - 1 tiles ahead of the MFMAs, so that no staging goes through registers and the
+// tile loads overlap NST - 2 blocks of compute.  Tiles keep the source row-major layout with
+// the 16-byte pieces of row r permuted by p ^ (r % (HD/8)) (conflict-free operand reads);
+// the V operand of O^T = V^T P^T is read with ds_read_b64_tr_b16, which transposes 16-bit
+// elements across lanes, so V needs no transpose when staged.  The M_res snapshot (M^T bf16
+// hi / lo) comes by the same loads, after the last tile.
+constexpr int NST = 4;
+
+template <int HD>
+struct Fwd2Smem {
+  static constexpr int TILE = KB * HD;   // elements of one K or V tile
+  alignas(16) uint16_t ring[NST][2][TILE];
+  alignas(16) uint16_t mt[2][HD * HD];   // M^T hi, lo
+  alignas(16) float sbias[128];          // slot bias row of the step (raw)
+};
+
+__device__ __forceinline__ void lds_dma16(const void* src, void* lds) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
+// wait until at most N vector-memory operations of this wave are outstanding
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (((N >> 4) & 3) << 14) | (7 << 4) | (15 << 8));
+}
+// ds_read_b64_tr_b16 as inline assembly: the compiler cannot tell these reads from the
+// LDS-DMA destinations and would otherwise wait for every outstanding tile load before them.
+// The caller waits for LDS (lds_wait8) before using the results.
+__device__ __forceinline__ u16x4 lds_read_tr(const uint16_t* p) {
+  u16x4 r;
+  const uint32_t addr = (uint32_t)(size_t)((__attribute__((address_space(3))) const uint16_t*)p);
+  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r) : "v"(addr) : "memory");
+  return r;
+}
+// The slot bias row goes through LDS by inline assembly as well (the compiler cannot separate
+// it from the LDS-DMA destinations either).
+__device__ __forceinline__ void lds_write_f32(float* p, float v) {
+  const uint32_t addr = (uint32_t)(size_t)((__attribute__((address_space(3))) const float*)p);
+  asm volatile("ds_write_b32 %0, %1" : : "v"(addr), "v"(v) : "memory");
+}
+__device__ __forceinline__ float4 lds_read_f4(const float* p) {
+  float4 r;
+  const uint32_t addr = (uint32_t)(size_t)((__attribute__((address_space(3))) const float*)p);
+  asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(r) : "v"(addr) : "memory");
+  return r;
+}
+// lgkmcnt(0), tied to the transposed-read results so that their users follow it
+__device__ __forceinline__ void lds_wait8(u16x4* r) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7]));
+}
+
+template <int HD, int NW>
+__global__ void __launch_bounds__(64 * NW) attn_fwd2_kernel(b3_attn_args a, int QW) {
+  using Sm = Fwd2Smem<HD>;
+  __shared__ Sm sm;
+  constexpr int NDB = HD / 32, NP = HD / 8;
+  constexpr int RPI = 1024 / (2 * HD);              // tile rows per 1 KB load instruction
+  constexpr int IPT = KB / RPI;                     // load instructions per tile
+  constexpr int LPB = 2 * IPT / NW;                 // per wave per block (K and V)
+  static_assert(LPB * NW == 2 * IPT, "tile loads must divide over the waves");
+  constexpr int MIPT = HD / RPI;                    // instructions per M^T half (hi or lo)
+  constexpr int LPM = 2 * MIPT / NW;
+  static_assert(LPM * NW == 2 * MIPT, "M^T loads must divide over the waves");
+  const int G = a.H / a.HKV;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n = lane & 31, h = lane >> 5;
+  const int g = wave / QW, qsub = wave % QW;
+  const int bh = blockIdx.z, b = bh / a.HKV, hkv = bh % a.HKV;
+  const int hq = hkv * G + g;
+  const int chunk = blockIdx.y + a.chunk_begin, C = a.C;
+  const int qbase = chunk * C;
+  const int nq_chunk = min(C, a.n_q - qbase);
+  const int qt0 = blockIdx.x * 32 * QW;
+  if (qt0 >= nq_chunk) return;                  // uniform across the workgroup
+  const int qi = qt0 + 32 * qsub + n;
+  const bool qok = qi < nq_chunk;
+  const int t = qbase + qi;
+  const int wave_q0 = qt0 + 32 * qsub;
+  const int wg_qend = min(qt0 + 32 * QW, nq_chunk);
+  const int step = chunk - 2;
+  const float L2E = 1.4426950408889634f;
+  const float sL = (1.0f / sqrtf((float)HD)) * L2E;
+
+  // ---- block schedule: [sinks | slots (step c-2) | previous chunk | current chunk (causal)]
+  const long long wofs = (long long)b * a.w_sb + (long long)hkv * a.w_sh;
+  const uint16_t* wk = reinterpret_cast<const uint16_t*>(a.win_k) + wofs;
+  const uint16_t* wv = reinterpret_cast<const uint16_t*>(a.win_v) + wofs;
+  const bool has_slots = chunk >= 2;
+  const int n_sink = has_slots ? 1 : 0;
+  const int n_slot = has_slots ? (a.S + KB - 1) / KB : 0;
+  const int n_pre = n_sink + n_slot;
+  const int n_prev = chunk >= 1 ? (C + KB - 1) / KB : 0;
+  const int n_cur = (wg_qend + KB - 1) / KB;
+  const int nb = n_pre + n_prev + n_cur;
+  auto block = [&](int i) -> FwdBlock {
+    FwdBlock f;
+    f.bias = nullptr;
+    f.kpos = -1;
+    if (i < n_pre) {
+      if (i < n_sink) {
+        f.k = wk;
+        f.v = wv;
+        f.nvalid = min(a.n_sinks, C);
+      } else {
+        const int j = i - n_sink;
+        const long long so = (long long)step * a.slot_step + (long long)bh * a.S * HD + (long long)j * KB * HD;
+        f.k = reinterpret_cast<const uint16_t*>(a.slot_k) + so;
+        f.v = reinterpret_cast<const uint16_t*>(a.slot_v) + so;
+        f.bias = sm.sbias + j * KB;
+        f.nvalid = min(KB, a.S - j * KB);
+      }
+    } else if (i < n_pre + n_prev) {
+      const int j = i - n_pre;
+      const long long o = ((long long)(chunk - 1) * C + j * KB) * HD;
+      f.k = wk + o;
+      f.v = wv + o;
+      f.nvalid = min(KB, C - j * KB);
+    } else {
+      const int j = i - n_pre - n_prev;
+      const long long o = ((long long)qbase + j * KB) * HD;
+      f.k = wk + o;
+      f.v = wv + o;
+      f.nvalid = min(KB, nq_chunk - j * KB);
+      f.kpos = j * KB;
+    }
+    return f;
+  };
+  // this wave's share of the tile loads of block i into stage st; rows past the valid ones
+  // repeat the last valid row (their scores are masked)
+  auto issue = [&](int i, int st) {
+    const FwdBlock f = block(i);
+    const int last = max(f.nvalid - 1, 0);
+#pragma unroll
+    for (int q = 0; q < LPB; ++q) {
+      const int ins = wave * LPB + q;
+      const int tile = ins / IPT, ch = ins % IPT;
+      const int r = ch * RPI + lane / NP, p = (lane % NP) ^ (r % NP);
+      lds_dma16((tile ? f.v : f.k) + (long long)min(r, last) * HD + 8 * p, &sm.ring[st][tile][ch * 512]);
+    }
+  };
+  const bool readout = a.m_res && step >= 0;
+  auto issue_m = [&]() {
+    const uint16_t* src = reinterpret_cast<const uint16_t*>(a.m_res + (long long)step * a.m_step) +
+                          (long long)bh * 2 * HD * HD;   // bf16 M^T hi, then lo
+#pragma unroll
+    for (int q = 0; q < LPM; ++q) {
+      const int ins = wave * LPM + q;
+      const int half = ins / MIPT, ch = ins % MIPT;
+      const int r = ch * RPI + lane / NP, p = (lane % NP) ^ (r % NP);
+      lds_dma16(src + half * HD * HD + (long long)r * HD + 8 * p, &sm.mt[half][ch * 512]);
+    }
+  };
+  // wait for the loads of a block while `ahead` later blocks (and the snapshot, if issued)
+  // may still be in flight
+  auto wait_block = [&](int ahead, bool m_issued) {
+    if (m_issued) {
+      if (ahead >= 2) wait_vm<2 * LPB + LPM>();
+      else if (ahead == 1) wait_vm<LPB + LPM>();
+      else wait_vm<LPM>();
+    } else {
+      if (ahead >= 2) wait_vm<2 * LPB>();
+      else if (ahead == 1) wait_vm<LPB>();
+      else wait_vm<0>();
+    }
+  };
+  static_assert(NST == 4, "wait_block covers up to NST - 2 blocks ahead");
+
+  // ---- prologue: the slot bias row and the query fragment into registers, the first NST - 1
+  // tiles into LDS; the bias goes to LDS after the tile loads are issued (in-order completion
+  // makes every later wait cover the loads issued before it)
+  const float sb = (has_slots && tid < 128)
+                       ? a.slot_bias[(long long)step * (a.slot_step / HD) + (long long)bh * a.S + tid] : 0.f;
+  const uint16_t* qrow = reinterpret_cast<const uint16_t*>(a.q_rope) + b * a.q_sb + hq * a.q_sh + (long long)t * HD;
+  QFrag<uint16_t, HD> qf;
+  qf.load(qrow, qok, h);
+  const int pre = min(nb, NST - 1);
+  for (int j = 0; j < pre; ++j) issue(j, j);
+  bool m_issued = false;
+  if (pre == nb && readout) { issue_m(); m_issued = true; }
+  if (tid < 128) lds_write_f32(&sm.sbias[tid], sb);
+
+  f32x16 o[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) o[db] = zero16();
+  float m_run = -INFINITY, l_run = 0.f;
+
+  for (int i = 0; i < nb; ++i) {
+    const int st = i % NST;
+    wait_block(min(nb - 1, i + NST - 2) - i, m_issued);
+    sync_lds();   // block i is in LDS; every wave is done with stage (i - 1) % NST
+    if (i + NST - 1 < nb) {
+      issue(i + NST - 1, (i + NST - 1) % NST);
+      if (i + NST - 1 == nb - 1 && readout) { issue_m(); m_issued = true; }
+    }
+    const FwdBlock f = block(i);
+    if (f.kpos >= 0 && f.kpos > wave_q0 + 31) continue;   // the wave's queries all precede the block
+    const uint16_t* sK = sm.ring[st][0];
+    const uint16_t* sV = sm.ring[st][1];
+    f32x16 sc = zero16();
+#pragma unroll
+    for (int ks = 0; ks < HD / 16; ++ks) {
+      const int piece = (2 * ks + h) ^ (n % NP);
+      mma_bf16(sc, *reinterpret_cast<const u16x8*>(sK + n * HD + 8 * piece), qf.v[ks]);
+    }
+    // scores in log2 units: round_bf(q.k) * scale*log2(e) (+ slot bias * log2(e)), one FMA
+    if (f.bias) {
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const float4 b4 = lds_read_f4(f.bias + 8 * r4 + 4 * h);
+        const float bb[4] = {b4.x * L2E, b4.y * L2E, b4.z * L2E, b4.w * L2E};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) sc[4 * r4 + q] = fmaf(round_bf(sc[4 * r4 + q]), sL, bb[q]);
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sc[r] = round_bf(sc[r]) * sL;
+    }
+    if (f.kpos >= 0 || f.nvalid < KB) {
+      const int lim = min(f.nvalid - 1, f.kpos >= 0 ? qi - f.kpos : KB - 1);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sc[r] = d_row(lane, r) <= lim ? sc[r] : -INFINITY;
+    }
+    float bm = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) bm = fmaxf(bm, sc[r]);
+    bm = fmaxf(bm, xor32(bm));
+    // the running max moves only when it grows by more than 2^8 (probabilities up to 2^8
+    // before the final normalisation are exact enough in fp32 and rescale-free)
+    const bool grow = bm > m_run + 8.0f;
+    const float m_use = grow ? bm : m_run;
+    const float mu = m_use == -INFINITY ? 0.f : m_use;   // all keys so far masked: p = 0
+    float ps = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float p = __builtin_amdgcn_exp2f(sc[r] - mu);
+      sc[r] = p;
+      ps += p;
+    }
+    ps += xor32(ps);
+    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+      const float alpha = __builtin_amdgcn_exp2f(m_run - mu);   // m_run = -inf: alpha = 0
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+      l_run *= alpha;
+    }
+    l_run += ps;
+    m_run = m_use;
+    u16x8 pv[2];
+#pragma unroll
+    for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) pv[kc][e] = f2bf(sc[8 * kc + e]);
+    // ---- O^T[d][q] += V^T . P^T; lane (j = l % 16, grp = l / 16) of a transposed read
+    // addresses row 16kc + 4h + j/4 (+ 8) and features 32db + 16*(grp & 1) + 4*(j & 3)
+    {
+      const int j = lane & 15, grp = lane >> 4;
+#pragma unroll
+      for (int kc = 0; kc < 2; ++kc) {
+        const int r1 = 16 * kc + 4 * h + (j >> 2), r2 = r1 + 8;
+        u16x4 tv[8];
+#pragma unroll
+        for (int db = 0; db < NDB && db < 4; ++db) {
+          const int f0 = 32 * db + 16 * (grp & 1) + 4 * (j & 3);
+          tv[2 * db] = lds_read_tr(sV + r1 * HD + 8 * ((f0 >> 3) ^ (r1 % NP)) + (f0 & 7));
+          tv[2 * db + 1] = lds_read_tr(sV + r2 * HD + 8 * ((f0 >> 3) ^ (r2 % NP)) + (f0 & 7));
+        }
+        lds_wait8(tv);
+#pragma unroll
+        for (int db = 0; db < NDB && db < 4; ++db) {
+          u16x8 av;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) { av[e] = tv[2 * db][e]; av[4 + e] = tv[2 * db + 1][e]; }
+          mma_bf16(o[db], av, pv[kc]);
+        }
+      }
+    }
+  }
+
+  // ---- normalise; y = round(O)
+  const float inv_l = l_run > 0.f ? 1.0f / l_run : 0.f;
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[db][r] = round_bf(o[db][r] * inv_l);
+
+  // ---- readout: eta * RMSNorm(normalize(q_raw) . M * (1-gamma)/sqrt(HD))
+  if (readout) {
+    wait_vm<0>();
+    sync_lds();
+    const uint16_t* rrow = reinterpret_cast<const uint16_t*>(a.q_raw) + b * a.q_sb + hq * a.q_sh + (long long)t * HD;
+    QFrag<uint16_t, HD> rf;
+    rf.load(rrow, qok, h);
+    float qq = rf.sumsq();
+    qq += xor32(qq);
+    const float inv_q = 1.0f / fmaxf(sqrtf(qq), 1e-12f);
+    const float coef = div_rn(1.0f - a.gamma[hkv], sqrtf((float)HD));
+    f32x16 rr[NDB];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      rr[db] = zero16();
+      const int dr = 32 * db + n;
+#pragma unroll
+      for (int ks = 0; ks < HD / 16; ++ks) {
+        const int piece = (2 * ks + h) ^ (dr % NP);
+        mma_bf16(rr[db], *reinterpret_cast<const u16x8*>(&sm.mt[0][dr * HD + 8 * piece]), rf.v[ks]);
+        mma_bf16(rr[db], *reinterpret_cast<const u16x8*>(&sm.mt[1][dr * HD + 8 * piece]), rf.v[ks]);
+      }
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float y = mul_rn(rr[db][r] * inv_q, coef);
+        rr[db][r] = y;
+        ss += y * y;
+      }
+    ss += xor32(ss);
+    const float rs = 1.0f / sqrtf(div_rn(ss, (float)HD) + a.eps);
+    const float eta = qok ? a.eta[b * a.e_sb + hq * a.e_sh + t] : 0.f;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int d = 32 * db + d_row(lane, r);
+        const float ymn = mul_rn(mul_rn(rr[db][r], rs), a.res_w[d]);
+        o[db][r] = round_bf(add_rn(o[db][r], round_bf(mul_rn(eta, ymn))));
+      }
+  }
+
+  // ---- write y[b][t][hq][d], 4 consecutive features per store
+  if (qok) {
+    uint16_t* yrow = reinterpret_cast<uint16_t*>(a.y) + b * a.y_sb + (long long)t * a.y_st + hq * HD;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        u16x4 w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[e] = f2bf(o[db][4 * r4 + e]);
+        *reinterpret_cast<u16x4*>(yrow + 32 * db + 8 * r4 + 4 * h) = w;
+      }
+  }
+}
+
 template <typename T, int HD>
 static int launch_attn(const b3_attn_args& a, hipStream_t st) {
   const int G = a.H / a.HKV;
@@ -748,6 +1100,13 @@ static int launch_attn(const b3_attn_args& a, hipStream_t st) {
     if (a.mode == 0 && (!a.m_res || a.m_split)) {
       b3_attn_args ab = a;
       ab.chunk_begin = c0;
+      const int nw = nthreads / 64;
+      if (a.part == 0 && (a.S == 128 || a.n_q <= 2 * a.C) && (nw == 2 || nw == 4 || nw == 8)) {
+        if (nw == 8) hipLaunchKernelGGL((attn_fwd2_kernel<HD, 8>), grid, dim3(nthreads), 0, st, ab, QW);
+        else if (nw == 4) hipLaunchKernelGGL((attn_fwd2_kernel<HD, 4>), grid, dim3(nthreads), 0, st, ab, QW);
+        else hipLaunchKernelGGL((attn_fwd2_kernel<HD, 2>), grid, dim3(nthreads), 0, st, ab, QW);
+        return (int)hipGetLastError();
+      }
       const int ipt = (KB * (HD / 8) + nthreads - 1) / nthreads;
       if (ipt <= 1) hipLaunchKernelGGL((attn_fwd_kernel<HD, 1>), grid, dim3(nthreads), 0, st, ab, QW);
       else if (ipt <= 2) hipLaunchKernelGGL((attn_fwd_kernel<HD, 2>), grid, dim3(nthreads), 0, st, ab, QW);

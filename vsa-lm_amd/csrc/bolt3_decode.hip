@@ -26,6 +26,23 @@
 
 namespace b3 {
 
+__device__ __forceinline__ void dec_dma16(const void* src, void* lds) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
+// ds_read_b64_tr_b16 as inline assembly (the compiler cannot separate these reads from the
+// LDS-DMA destination and would wait for all outstanding loads before them); the results are
+// used only after dec_lds_wait.
+__device__ __forceinline__ u16x4 dec_read_tr(const uint16_t* p) {
+  u16x4 r;
+  const uint32_t addr = (uint32_t)(size_t)((__attribute__((address_space(3))) const uint16_t*)p);
+  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r) : "v"(addr) : "memory");
+  return r;
+}
+__device__ __forceinline__ void dec_lds_wait(u16x4& a, u16x4& b) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); }
+
 constexpr int DNT = 256;        // threads per decode workgroup
 constexpr int DWAVES = DNT / 64;
 constexpr int GMAX = 8;         // query heads per kv head
@@ -64,11 +81,13 @@ template <typename T, int HD>
 struct SplitSmem {
   static constexpr int QS = sizeof(T) == 2 ? HD + 8 : HD + 4;   // query row stride (16-byte rows)
   static constexpr int VS = sizeof(T) == 2 ? 32 + 8 : 32 + 1;   // V^T row stride of a key tile
-  alignas(16) T qt[32 * QS];      // roped queries as MFMA operand rows; rows G..31 zero
+  static constexpr bool BF = sizeof(T) == 2;
+  alignas(16) T qt[(BF ? 16 : 32) * QS];   // roped queries as MFMA operand rows; rows G.. zero
   float qr[GMAX][HD];             // un-roped queries after the norm
   float bias[DWAVES][32];         // slot bias of each wavefront's key tile
   union {
-    T vt[DWAVES][HD * VS];        // V^T of each wavefront's key tile
+    T vt[BF ? 1 : DWAVES][HD * VS];   // V^T of each wavefront's key tile (fp32 storage)
+    T vrow[DWAVES][32 * HD];      // value rows of each wavefront's key tile (bf16: LDS-DMA target)
     float part[DNT / 64][GMAX][HD];   // readout row groups; per-wavefront outputs of the merge
   } u;
   float wm[DWAVES][GMAX], wl[DWAVES][GMAX];   // per-wavefront softmax max / sum
@@ -280,6 +299,168 @@ __global__ void __launch_bounds__(DNT) decode_split_kernel(b3_decode_args a) {
   // ---------------- attention: wavefront `wave` takes keys kt0 .. kt0+31 of the list
   //   [sinks | attractor slots | window A | window B + new token]
   const int kt0 = split * KWG + 32 * wave;
+  if constexpr (St<T>::is_bf16) {
+    // 16x16x32 MFMAs with the G query heads as columns: S^T[key][head] = K Q^T over two
+    // 16-key blocks, O^T[feature][head] += V^T P^T.  Key rows go to registers in operand
+    // order; the 32 value rows go to LDS by global->LDS loads (16-byte pieces of row r
+    // permuted by p ^ (r % (HD/8))) and are read transposed (ds_read_b64_tr_b16).
+    const int m = lane & 15, g4 = lane >> 4;
+    auto key_rows = [&](int key, const T*& kp, const T*& vp, float& bias) {
+      int k = min(key, nk - 1);
+      bias = 0.f;
+      if (k < ns) {
+        const long long o = (long long)b * a.s_sb + (long long)hkv * a.s_sh + (long long)k * HD;
+        kp = reinterpret_cast<const T*>(a.sink_k) + o;
+        vp = reinterpret_cast<const T*>(a.sink_v) + o;
+      } else if ((k -= ns) < nsl) {
+        kp = reinterpret_cast<const T*>(a.slot_k) + ((long long)bh * a.S + k) * HD;
+        vp = reinterpret_cast<const T*>(a.slot_v) + ((long long)bh * a.S + k) * HD;
+        bias = a.slot_bias[(long long)bh * a.S + k];
+      } else if ((k -= nsl) < na) {
+        kp = reinterpret_cast<const T*>(a.win_kp) + wbase + (long long)(a.a_start + k) * HD;
+        vp = reinterpret_cast<const T*>(a.win_v) + wbase + (long long)(a.a_start + k) * HD;
+      } else {   // window B, the new token (appended by decode_prep_kernel) included
+        k -= na;
+        kp = reinterpret_cast<const T*>(a.win_kp) + wbase + (long long)(a.b_start + k) * HD;
+        vp = reinterpret_cast<const T*>(a.win_v) + wbase + (long long)(a.b_start + k) * HD;
+      }
+    };
+    // value rows -> LDS: instruction ch fills rows RPI*ch .. RPI*ch + RPI-1 (1 KB)
+    constexpr int NP = HD / 8, RPI = 64 / NP;
+    T* vrow = sm.u.vrow[wave];
+#pragma unroll
+    for (int ch = 0; ch < 32 / RPI; ++ch) {
+      const int r = RPI * ch + lane / NP, piece = (lane % NP) ^ (r % NP);
+      const T* kp;
+      const T* vp;
+      float bias;
+      key_rows(kt0 + r, kp, vp, bias);
+      dec_dma16(vp + 8 * piece, vrow + ch * 512);
+    }
+    // key rows -> registers: lane (m, g4) holds features 32ks + 8g4 .. of key kt0 + 16kb + m
+    u16x8 ka[2][HD / 32];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      const T* kp;
+      const T* vp;
+      float bias;
+      key_rows(kt0 + 16 * kb + m, kp, vp, bias);
+#pragma unroll
+      for (int ks = 0; ks < HD / 32; ++ks) ka[kb][ks] = *reinterpret_cast<const u16x8*>(kp + 32 * ks + 8 * g4);
+      if (g4 == 0) sm.bias[wave][16 * kb + m] = bias;
+    }
+    // query rows (heads) from the workspace, rows G..15 zero
+    {
+      const T* qsrc = reinterpret_cast<const T*>(ws + dec_ws_q(G, HD));
+      for (int it = tid; it < 16 * (HD / 8); it += DNT) {
+        const int rr = it / (HD / 8), c8 = (it % (HD / 8)) * 8;
+        Vec8<T> x;
+        if (rr < G) x.load(qsrc + rr * HD + c8);
+        else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) x.set(e, 0.f);
+        }
+        x.store(&sm.qt[rr * Sm::QS + c8]);
+      }
+    }
+    __syncthreads();
+    f32x4 sc[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      sc[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < HD / 32; ++ks)
+        mma16_bf16(sc[kb], ka[kb][ks], *reinterpret_cast<const u16x8*>(&sm.qt[m * Sm::QS + 32 * ks + 8 * g4]));
+    }
+    // fp32 scores (the decoder step does not round q.k), slot bias, keys past nk masked
+    const float scale = 1.0f / sqrtf((float)HD);
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int kr = 16 * kb + 4 * g4 + i;
+        float x = add_rn(mul_rn(sc[kb][i], scale), sm.bias[wave][kr]);
+        x = kt0 + kr < nk ? x : -INFINITY;
+        sc[kb][i] = x;
+        mx = fmaxf(mx, x);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    float sum = 0.f;
+    u16x8 pb;   // P^T operand: keys 4g4 + i (i < 4) and 16 + 4g4 + i - 4
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float e = mx == -INFINITY ? 0.f : expf(sc[kb][i] - mx);
+        sum += e;
+        pb[4 * kb + i] = f2bf(e);
+      }
+    sum += __shfl_xor(sum, 16, 64);
+    sum += __shfl_xor(sum, 32, 64);
+    // O^T[16db + 4g4 + i][head m]; transposed reads: source lane s of a 16-lane group
+    // addresses row 4g4 + s/4 (+16) and features 16db + 4(s & 3)
+    // (value pieces of row r are permuted by p ^ (r % NP))
+    wait_vm0();
+    f32x4 o[HD / 16];
+    {
+      const int s = lane & 15;
+#pragma unroll
+      for (int db = 0; db < HD / 16; ++db) {
+        const int r1 = 4 * g4 + (s >> 2), r2 = r1 + 16;
+        const int pc = 2 * db + ((s & 3) >> 1), off = 4 * (s & 1);
+        u16x4 lo = dec_read_tr(vrow + r1 * HD + 8 * (pc ^ (r1 % NP)) + off);
+        u16x4 hi = dec_read_tr(vrow + r2 * HD + 8 * (pc ^ (r2 % NP)) + off);
+        dec_lds_wait(lo, hi);
+        u16x8 av;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) { av[e] = lo[e]; av[4 + e] = hi[e]; }
+        o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+        mma16_bf16(o[db], av, pb);
+      }
+    }
+    // ---- merge the four tiles of the workgroup: lane column m = head
+    if (m < G && g4 == 0) {
+      sm.wm[wave][m] = mx;
+      sm.wl[wave][m] = sum;
+    }
+    __syncthreads();   // every wavefront is done with its value rows (the union is reused below)
+    if (m < G) {
+      float mm = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < DWAVES; ++w) mm = fmaxf(mm, sm.wm[w][m]);
+      const float f = mx == -INFINITY ? 0.f : expf(mx - mm);
+#pragma unroll
+      for (int db = 0; db < HD / 16; ++db)
+        *reinterpret_cast<float4*>(&sm.u.part[wave][m][16 * db + 4 * g4]) =
+            make_float4(o[db][0] * f, o[db][1] * f, o[db][2] * f, o[db][3] * f);
+    }
+    __syncthreads();
+    float* pw = ws + (long long)split * G * (HD + 2);
+    for (int it = tid; it < G * (HD / 4); it += DNT) {
+      const int gg = it / (HD / 4), d4 = (it % (HD / 4)) * 4;
+      float4 acc4 = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int w = 0; w < DWAVES; ++w) {
+        const float4 x = *reinterpret_cast<const float4*>(&sm.u.part[w][gg][d4]);
+        acc4.x += x.x; acc4.y += x.y; acc4.z += x.z; acc4.w += x.w;
+      }
+      *reinterpret_cast<float4*>(pw + gg * (HD + 2) + d4) = acc4;
+    }
+    if (tid < G) {
+      float mm = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < DWAVES; ++w) mm = fmaxf(mm, sm.wm[w][tid]);
+      float l = 0.f;
+#pragma unroll
+      for (int w = 0; w < DWAVES; ++w)
+        l += sm.wm[w][tid] == -INFINITY ? 0.f : sm.wl[w][tid] * expf(sm.wm[w][tid] - mm);
+      pw[tid * (HD + 2) + HD] = mm;
+      pw[tid * (HD + 2) + HD + 1] = l;
+    }
+    return;
+  }
   const int key = kt0 + n;                     // this lane's key row
   const bool kin = key < nk;
   const T* kp = nullptr;

@@ -488,6 +488,7 @@ class Bolt3LayerState:
         self.prev = (0, 0)          # (start, length) in the ring
         self.cur = (2 * C, 0)
         self._dec_work = None
+        self._dec = None   # (key, DecodeArgs, y): the one-token step's argument block and output
 
     def decode_workspace(self, H: int) -> torch.Tensor:
         """Scratch of the one-token decode kernels (partial softmax state per key range)."""
@@ -603,24 +604,33 @@ class Bolt3Decoder:
         cs, cl = st.cur
         ps, pl = st.prev
         if t == 1:
-            y = torch.empty(B, H * HD, dtype=dt, device=dev)
-            a = A.DecodeArgs()
-            a.dtype, a.B, a.H, a.HKV, a.HD, a.S = A.dtype_code(dt), B, H, HKV, HD, S
-            a.lin, a.lin_row_stride = lin.data_ptr(), lin.shape[-1]
-            a.qn_w, a.kn_w, a.has_qk_norm = A.ptr(side["qn"]), A.ptr(side["kn"]), int(side["qn"] is not None)
-            a.eps, a.inv_freq, a.pos = float(ly.res_norm.eps), side["inv_freq"].data_ptr(), int(pos_start)
-            a.win_kr, a.win_kp, a.win_v = st.win_kr.data_ptr(), st.win_kp.data_ptr(), st.win_v.data_ptr()
-            a.w_sb, a.w_sh = st.win_kr.stride(0), st.win_kr.stride(1)
-            a.win_beta, a.wb_sb, a.wb_sh = st.win_b.data_ptr(), st.win_b.stride(0), st.win_b.stride(1)
-            a.win_pos = st.win_pos.data_ptr()
+            # the argument block and the output row are kept in the layer state; a step only
+            # refreshes the position, the ring segments and the projection row
+            key = (id(side), m_state.data_ptr(), lin.shape[-1])
+            if st._dec is None or st._dec[0] != key:
+                y = torch.empty(B, H * HD, dtype=dt, device=dev)
+                a = A.DecodeArgs()
+                a.dtype, a.B, a.H, a.HKV, a.HD, a.S = A.dtype_code(dt), B, H, HKV, HD, S
+                a.lin_row_stride = lin.shape[-1]
+                a.qn_w, a.kn_w, a.has_qk_norm = A.ptr(side["qn"]), A.ptr(side["kn"]), int(side["qn"] is not None)
+                a.eps, a.inv_freq = float(ly.res_norm.eps), side["inv_freq"].data_ptr()
+                a.win_kr, a.win_kp, a.win_v = st.win_kr.data_ptr(), st.win_kp.data_ptr(), st.win_v.data_ptr()
+                a.w_sb, a.w_sh = st.win_kr.stride(0), st.win_kr.stride(1)
+                a.win_beta, a.wb_sb, a.wb_sh = st.win_b.data_ptr(), st.win_b.stride(0), st.win_b.stride(1)
+                a.win_pos = st.win_pos.data_ptr()
+                a.sink_k, a.sink_v = st.sink_k.data_ptr(), st.sink_v.data_ptr()
+                a.s_sb, a.s_sh = st.sink_k.stride(0), st.sink_k.stride(1)
+                a.slot_k, a.slot_v, a.slot_bias = st.slot_k.data_ptr(), st.slots["av"].data_ptr(), \
+                    st.slot_bias.data_ptr()
+                a.m_res, a.gamma, a.res_w, a.y = m_state.data_ptr(), gam.data_ptr(), side["res_w"].data_ptr(), \
+                    y.data_ptr()
+                work = st.decode_workspace(H)
+                a.work, a.work_bytes = work.data_ptr(), work.numel() * 4
+                st._dec = (key, a, y, side)
+            _, a, y, _ = st._dec
+            a.lin, a.pos = lin.data_ptr(), int(pos_start)
             a.a_start, a.a_len, a.b_start, a.b_len = ps, pl, cs, cl
-            a.sink_k, a.sink_v = st.sink_k.data_ptr(), st.sink_v.data_ptr()
-            a.s_sb, a.s_sh, a.n_sink_keys = st.sink_k.stride(0), st.sink_k.stride(1), st.n_sink
-            a.slot_k, a.slot_v, a.slot_bias = st.slot_k.data_ptr(), st.slots["av"].data_ptr(), st.slot_bias.data_ptr()
-            a.has_slots = int(st.has_slots)
-            a.m_res, a.gamma, a.res_w, a.y = m_state.data_ptr(), gam.data_ptr(), side["res_w"].data_ptr(), y.data_ptr()
-            work = st.decode_workspace(H)
-            a.work, a.work_bytes = work.data_ptr(), work.numel() * 4
+            a.n_sink_keys, a.has_slots = st.n_sink, int(st.has_slots)
             A.call("bolt3_decode", a, dev)
             y = y.view(B, 1, H * HD)
         else:

@@ -246,6 +246,37 @@ int bolt3_decode(const b3_decode_args* a, void* stream);
 /* Workspace of bolt3_decode: partial softmax state of the key ranges and the readout per (batch, kv head). */
 int64_t bolt3_decode_workspace_bytes(int32_t B, int32_t H, int32_t HKV, int32_t HD);
 
+/*
+ * A whole one-token decode layer step in bf16: the packed input projection
+ * x . W_in^T + b_in (W_in rows q | k | v | beta | eta, zero rows padding to n_in), the
+ * bolt3_decode step on that row, then out = y . W_out^T + b_out.  The projections stream
+ * each weight once (workgroups of 128 weight rows x 512 columns of K, x staged in LDS) and
+ * leave fp32 partial products per K chunk in proj_work, added in order and rounded once by
+ * their consumer.
+ * Replaces vsa_lm/config/bolt3.py:346-402 for t_s == 1 together with the q/k/v/beta/eta
+ * projections it calls (:59-66, :349) and o_proj (:400-402).
+ */
+typedef struct {
+  b3_decode_args dec;         /* dec.lin unused (the row comes from the projection); dec.lin_row_stride = n_in;
+                                 dec.y: [B][H*HD] attention output, written */
+  const void* x;              /* [B][x_row_stride] layer input rows, 16-byte aligned */
+  int64_t x_row_stride;       /* multiple of 8 */
+  int32_t d_model;            /* columns of x = columns of W_in, multiple of 32 */
+  const void* w_in;           /* [n_in][d_model] row-major */
+  const void* b_in;           /* [n_in] or NULL */
+  int32_t n_in;               /* = dec.lin_row_stride, multiple of 16 */
+  const void* w_out;          /* [n_out][H*HD] row-major */
+  const void* b_out;          /* [n_out] or NULL */
+  int32_t n_out;              /* multiple of 16 */
+  void* out;                  /* [B][out_row_stride] */
+  int64_t out_row_stride;     /* multiple of 4 */
+  float* proj_work;           /* >= bolt3_decode_layer_workspace_bytes(B, d_model, n_in, H*HD, n_out) bytes */
+  int64_t proj_work_bytes;
+} b3_decode_layer_args;
+int bolt3_decode_layer(const b3_decode_layer_args* a, void* stream);
+/* Workspace of bolt3_decode_layer's projections (besides dec.work): the fp32 partial products. */
+int64_t bolt3_decode_layer_workspace_bytes(int32_t B, int32_t d_model, int32_t n_in, int32_t hd_total, int32_t n_out);
+
 /* Library identification: returns a static string (build flags, gfx target). */
 const char* bolt3_version(void);
 

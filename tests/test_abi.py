@@ -60,10 +60,15 @@ def test_rejects_bad_arguments_without_gpu_work():
     assert lib.bolt3_chunk_attn(ctypes.byref(t), None) == 1001
     d = A.DecodeArgs()
     assert lib.bolt3_decode(ctypes.byref(d), None) == 1001
+    la = A.DecodeLayerArgs()
+    la.dec.dtype = 0
+    assert lib.bolt3_decode_layer(ctypes.byref(la), None) == 1002   # fp32: the unfused step only
+    la.dec.dtype = 1
+    assert lib.bolt3_decode_layer(ctypes.byref(la), None) == 1001
 
 
 STRUCTS = {"b3_heads_args": A.HeadsArgs, "b3_chain_args": A.ChainArgs, "b3_attn_args": A.AttnArgs,
-           "b3_decode_args": A.DecodeArgs}
+           "b3_decode_args": A.DecodeArgs, "b3_decode_layer_args": A.DecodeLayerArgs}
 
 
 def _flat_fields(st, prefix=""):

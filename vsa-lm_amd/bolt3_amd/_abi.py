@@ -89,8 +89,16 @@ class DecodeArgs(C.Structure):
     ]
 
 
+class DecodeLayerArgs(C.Structure):
+    _fields_ = [
+        ("dec", DecodeArgs), ("x", p), ("x_row_stride", i64), ("d_model", i32),
+        ("w_in", p), ("b_in", p), ("n_in", i32), ("w_out", p), ("b_out", p), ("n_out", i32),
+        ("out", p), ("out_row_stride", i64), ("proj_work", p), ("proj_work_bytes", i64),
+    ]
+
+
 EXPORTS = ("bolt3_heads", "bolt3_chain", "bolt3_chain_workspace_bytes", "bolt3_chunk_attn", "bolt3_decode",
-           "bolt3_decode_workspace_bytes",
+           "bolt3_decode_layer", "bolt3_decode_layer_workspace_bytes", "bolt3_decode_workspace_bytes",
            "bolt3_version")
 
 _lib = None
@@ -106,12 +114,14 @@ def load():
                            f"(python -m bolt3_amd.build); there is no CPU implementation")
     lib = C.CDLL(LIB_PATH)
     for name, st in (("bolt3_heads", HeadsArgs), ("bolt3_chain", ChainArgs), ("bolt3_chunk_attn", AttnArgs),
-                     ("bolt3_decode", DecodeArgs)):
+                     ("bolt3_decode", DecodeArgs), ("bolt3_decode_layer", DecodeLayerArgs)):
         fn = getattr(lib, name)
         fn.argtypes = [C.POINTER(st), p]
         fn.restype = C.c_int
     lib.bolt3_chain_workspace_bytes.argtypes = [i32, i32, i32, i32, i32, i32]
     lib.bolt3_chain_workspace_bytes.restype = i64
+    lib.bolt3_decode_layer_workspace_bytes.argtypes = [i32, i32, i32, i32, i32]
+    lib.bolt3_decode_layer_workspace_bytes.restype = i64
     lib.bolt3_decode_workspace_bytes.argtypes = [i32, i32, i32, i32]
     lib.bolt3_decode_workspace_bytes.restype = i64
     lib.bolt3_version.argtypes = []
@@ -168,6 +178,10 @@ def call(name: str, args, device: torch.device):
 
 def decode_workspace_bytes(B: int, H: int, HKV: int, HD: int) -> int:
     return int(load().bolt3_decode_workspace_bytes(B, H, HKV, HD))
+
+
+def decode_layer_workspace_bytes(B: int, d_model: int, n_in: int, hd_total: int, n_out: int) -> int:
+    return int(load().bolt3_decode_layer_workspace_bytes(B, d_model, n_in, hd_total, n_out))
 
 
 def chain_workspace_bytes(dt: torch.dtype, B: int, HKV: int, HD: int, S: int, n_steps: int) -> int:

@@ -145,8 +145,11 @@ class Bolt3Attn(nn.Module):
         """(W_all, b_all, side) cached until a parameter changes.  W_all packs q | k | v | beta | eta
         rows (the decoder's one projection); side holds W_o, the split projections q, k | v and
         beta | eta used by the forward, and the fp32 tensors the kernels read."""
-        params = list(self.parameters())
-        key = (dt, device, tuple((q.data_ptr(), q._version) for q in params), self.rope.inv_freq.data_ptr())
+        # the parameters straight from the module dicts (one level of submodules), cheaper than
+        # self.parameters() on the decode path, where this runs once per layer and token
+        params = [q for q in self._parameters.values() if q is not None]
+        params += [q for m in self._modules.values() if m is not None for q in m._parameters.values() if q is not None]
+        key = (dt, device, tuple([(q.data_ptr(), q._version) for q in params]), self.rope.inv_freq.data_ptr())
         if key == self._pack_key:
             return self._pack
         with torch.no_grad():
@@ -488,7 +491,7 @@ class Bolt3LayerState:
         self.prev = (0, 0)          # (start, length) in the ring
         self.cur = (2 * C, 0)
         self._dec_work = None
-        self._dec = None   # (key, DecodeArgs, y): the one-token step's argument block and output
+        self._dec = None   # the one-token step: key, argument blocks, output and projection workspace
 
     def decode_workspace(self, H: int) -> torch.Tensor:
         """Scratch of the one-token decode kernels (partial softmax state per key range)."""
@@ -540,6 +543,9 @@ class Bolt3Decoder:
         self.max_T = model.config["max_T"]
         self.max_cache_pos = max_cache_pos
         self.C = int(model.config.get("bolt3_C", 128))
+        # bf16 one-token steps run as one bolt3_decode_layer call (projections included); False
+        # keeps the projections in torch around bolt3_decode (the tests compare the two)
+        self.fuse_projections = True
 
     def _graph_runner(self, B: int, need_len: int, device):
         return None
@@ -599,19 +605,27 @@ class Bolt3Decoder:
             raise NotImplementedError(f"step takes at most C={ly.C} tokens per call (got {t})")
         H, HKV, HD, S = ly.H, ly.HKV, ly.HD, ly.S
         W, bias, side = ly._packed(dt, dev)
-        lin = F.linear(h.contiguous(), W, bias)
         gam = side["gamma"]
         cs, cl = st.cur
         ps, pl = st.prev
+        h = h if h.is_contiguous() else h.contiguous()
         if t == 1:
-            # the argument block and the output row are kept in the layer state; a step only
-            # refreshes the position, the ring segments and the projection row
-            key = (id(side), m_state.data_ptr(), lin.shape[-1])
+            # The argument block, the projection row and the attention output are kept in the
+            # layer state; a step only refreshes the position, the ring segments and the input
+            # and output rows.  bf16 runs the whole step (both projections included) in one
+            # bolt3_decode_layer call.
+            fused = self.fuse_projections and dt == torch.bfloat16 and h.shape[-1] % 32 == 0 and \
+                side["wo"].shape[0] % 16 == 0
+            key = (id(side), m_state.data_ptr(), W.data_ptr(), fused)
             if st._dec is None or st._dec[0] != key:
                 y = torch.empty(B, H * HD, dtype=dt, device=dev)
-                a = A.DecodeArgs()
+                n_out = side["wo"].shape[0]
+                pw = torch.empty(A.decode_layer_workspace_bytes(B, h.shape[-1], W.shape[0], H * HD, n_out) // 4,
+                                 device=dev) if fused else None
+                la = A.DecodeLayerArgs() if fused else None
+                a = la.dec if fused else A.DecodeArgs()   # la.dec shares la's memory
                 a.dtype, a.B, a.H, a.HKV, a.HD, a.S = A.dtype_code(dt), B, H, HKV, HD, S
-                a.lin_row_stride = lin.shape[-1]
+                a.lin_row_stride = W.shape[0]
                 a.qn_w, a.kn_w, a.has_qk_norm = A.ptr(side["qn"]), A.ptr(side["kn"]), int(side["qn"] is not None)
                 a.eps, a.inv_freq = float(ly.res_norm.eps), side["inv_freq"].data_ptr()
                 a.win_kr, a.win_kp, a.win_v = st.win_kr.data_ptr(), st.win_kp.data_ptr(), st.win_v.data_ptr()
@@ -626,14 +640,31 @@ class Bolt3Decoder:
                     y.data_ptr()
                 work = st.decode_workspace(H)
                 a.work, a.work_bytes = work.data_ptr(), work.numel() * 4
-                st._dec = (key, a, y, side)
-            _, a, y, _ = st._dec
-            a.lin, a.pos = lin.data_ptr(), int(pos_start)
+                if fused:
+                    la.proj_work, la.proj_work_bytes = pw.data_ptr(), pw.numel() * 4
+                    la.x_row_stride, la.d_model = h.shape[-1], h.shape[-1]
+                    la.w_in, la.b_in, la.n_in = W.data_ptr(), A.ptr(bias), W.shape[0]
+                    la.w_out, la.b_out, la.n_out = side["wo"].data_ptr(), None, side["wo"].shape[0]
+                    la.out_row_stride = side["wo"].shape[0]
+                st._dec = (key, la if fused else a, a, y, pw, side, W, bias)
+            _, call_args, a, y, _, _, _, _ = st._dec
+            a.pos = int(pos_start)
             a.a_start, a.a_len, a.b_start, a.b_len = ps, pl, cs, cl
             a.n_sink_keys, a.has_slots = st.n_sink, int(st.has_slots)
+            if fused:
+                out = torch.empty(B, 1, side["wo"].shape[0], dtype=dt, device=dev)
+                call_args.x, call_args.out = h.data_ptr(), out.data_ptr()
+                A.call("bolt3_decode_layer", call_args, dev)
+                st.cur = (cs, cl + 1)
+                if st.cur[1] >= ly.C:
+                    self._consolidate(ly, st, m_state, gam, side)
+                return out
+            lin = F.linear(h, W, bias)
+            a.lin = lin.data_ptr()
             A.call("bolt3_decode", a, dev)
             y = y.view(B, 1, H * HD)
         else:
+            lin = F.linear(h, W, bias)
             q_raw = torch.empty(B, H, t, HD, dtype=dt, device=dev)
             q_rope = torch.empty_like(q_raw)
             eta = torch.empty(B, H, t, device=dev)

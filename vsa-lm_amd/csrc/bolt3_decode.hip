@@ -98,8 +98,18 @@ struct SplitSmem {
 // head unit, lane p owning the pairs (8p..8p+7, HD/2+8p..HD/2+8p+7).  The key (roped and
 // un-roped), value, beta and position go to the window ring; the roped queries (storage
 // dtype), the normalised un-roped queries (fp32), 1/|q_raw| and eta go to the workspace.
+// Source of the projection row when it comes as fp32 partial products of K chunks
+// (parts[chunk][b][c], chunk_stride floats apart): the row is the chunks added in order, plus
+// the bias, rounded once.  parts == nullptr: the row is a.lin.
+struct LinParts {
+  const float* parts;
+  int n_chunks;
+  long long chunk_stride;
+  const uint16_t* bias;
+};
+
 template <typename T, int HD>
-__global__ void __launch_bounds__(128) decode_prep_kernel(b3_decode_args a) {
+__global__ void __launch_bounds__(128) decode_prep_kernel(b3_decode_args a, LinParts lp) {
   constexpr int HALF = HD / 2, P8 = HALF / 8;
   const int bh = blockIdx.x, b = bh / a.HKV, hkv = bh % a.HKV;
   const int G = a.H / a.HKV;
@@ -120,9 +130,38 @@ __global__ void __launch_bounds__(128) decode_prep_kernel(b3_decode_args a) {
   float x0[8], x1[8], f[8], w0[8], w1[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) { x0[e] = 0.f; x1[e] = 0.f; f[e] = 0.f; w0[e] = 0.f; w1[e] = 0.f; }
+  // element c of the projection row (8 consecutive ones for lin8)
+  auto lin8 = [&](int c, float* out) {
+    if (lp.parts) {
+      const float* q = lp.parts + (long long)b * a.lin_row_stride + c;
+      f32x4 lo = *reinterpret_cast<const f32x4*>(q), hi = *reinterpret_cast<const f32x4*>(q + 4);
+      for (int k = 1; k < lp.n_chunks; ++k) {
+        const f32x4 l2 = *reinterpret_cast<const f32x4*>(q + k * lp.chunk_stride);
+        const f32x4 h2 = *reinterpret_cast<const f32x4*>(q + k * lp.chunk_stride + 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) { lo[e] += l2[e]; hi[e] += h2[e]; }
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        out[e] = St<T>::rnd(lp.bias ? lo[e] + bf2f(lp.bias[c + e]) : lo[e]);
+        out[4 + e] = St<T>::rnd(lp.bias ? hi[e] + bf2f(lp.bias[c + 4 + e]) : hi[e]);
+      }
+    } else {
+      load8<T>(row + c, out);
+    }
+  };
+  auto lin1 = [&](int c) -> float {
+    if (lp.parts) {
+      const float* q = lp.parts + (long long)b * a.lin_row_stride + c;
+      float v = q[0];
+      for (int k = 1; k < lp.n_chunks; ++k) v += q[k * lp.chunk_stride];
+      return St<T>::rnd(lp.bias ? v + bf2f(lp.bias[c]) : v);
+    }
+    return St<T>::ld(row + c);
+  };
   if (live) {
-    load8<T>(row + col + 8 * p, x0);
-    load8<T>(row + col + HALF + 8 * p, x1);
+    lin8(col + 8 * p, x0);
+    lin8(col + HALF + 8 * p, x1);
     load8<float>(a.inv_freq + 8 * p, f);
     if (norm) {
       const float* w = kind == 0 ? a.qn_w : a.kn_w;
@@ -190,9 +229,9 @@ __global__ void __launch_bounds__(128) decode_prep_kernel(b3_decode_args a) {
       }
     }
   }
-  if (tid < G) ws_stat[2 * tid + 1] = St<T>::rnd(tanhf(St<T>::ld(row + gcol + a.HKV + hkv * G + tid)));
+  if (tid < G) ws_stat[2 * tid + 1] = St<T>::rnd(tanhf(lin1(gcol + a.HKV + hkv * G + tid)));
   if (tid == G) {
-    const float z = St<T>::ld(row + gcol + hkv);
+    const float z = lin1(gcol + hkv);
     a.win_beta[b * a.wb_sb + hkv * a.wb_sh + ni] = St<T>::rnd(1.0f / (1.0f + expf(-z)));
     if (bh == 0 && a.win_pos) a.win_pos[ni] = (float)a.pos;
   }
@@ -697,11 +736,114 @@ __global__ void __launch_bounds__(DNT) decode_combine_kernel(b3_decode_args a) {
   }
 }
 
+// ---------------------------------------------------------------- projections of the decode layer
+//
+// y[m][n] = round(sum_k x[m][k] * W[n][k] + bias[n]) for few rows m (the batch of one-token
+// decode steps) and a row-major weight W[N][K] (nn.Linear layout).  The product is bound by
+// streaming W once, so every W element is read once and x, which every weight row needs, is
+// shared: a workgroup takes 8 tiles of 16 weight rows (one per wavefront) and one chunk of PKC
+// columns of K, stages x[64 rows][chunk] in LDS with global->LDS loads, and its wavefronts
+// multiply their W rows (loaded straight into MFMA operand registers, all steps of the chunk
+// before the first MFMA) by the staged x (v_mfma_f32_16x16x32_bf16: W rows as the A operand,
+// x rows as the B columns).  Each workgroup writes the fp32 partial product of its chunk to
+// parts[chunk][m][n]; the consumer adds the chunks in order, adds the bias and rounds once
+// (the decode prep kernel for the input projection, proj_reduce_kernel for o_proj).
+constexpr int PNW = 8;                 // wavefronts (weight-row tiles) per projection workgroup
+constexpr int PKC = 512;               // K columns per chunk
+constexpr int PKS = PKC / 32;          // MFMA K steps per chunk
+constexpr int PXS = PKC * 2 + 16;      // LDS bytes per staged x row (16-byte pad: conflict-free reads)
+
+__host__ __device__ inline int proj_chunks(int K) { return (K + PKC - 1) / PKC; }
+// floats of the fp32 partial products of one projection
+__host__ __device__ inline long long proj_parts_floats(int M, int N, int K) {
+  return (long long)proj_chunks(K) * M * N;
+}
+
+struct ProjArgs {
+  const uint16_t* x; int64_t x_rs;
+  const uint16_t* w;
+  float* parts;                        // [chunk][M][N]
+  int M, N, K;
+};
+
+__global__ void __launch_bounds__(64 * PNW, 2) rowproj_kernel(ProjArgs p) {
+  __shared__ __attribute__((aligned(16))) unsigned char xs[64 * PXS];
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nt = blockIdx.x * PNW + wv;            // this wavefront's 16-row tile of W
+  const int ch = blockIdx.y, m0 = blockIdx.z * 64;
+  const int kc0 = ch * PKC;
+  const int nst = min(PKS, (p.K - kc0) >> 5);      // K steps in this chunk
+  const int r = lane & 15, kg = lane >> 4;
+  const bool live = nt * 16 < p.N;
+  // W rows first: all steps of the chunk; steps past the chunk multiply a zero operand
+  u16x8 wa[PKS];
+  if (live) {
+    const uint16_t* wrow = p.w + (long long)(nt * 16 + r) * p.K + kc0 + 8 * kg;
+#pragma unroll
+    for (int i = 0; i < PKS; ++i) wa[i] = *reinterpret_cast<const u16x8*>(wrow + 32 * min(i, nst - 1));
+#pragma unroll
+    for (int i = 0; i < PKS; ++i)
+      if (i >= nst) wa[i] = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+  }
+  // x rows m0 .. m0+63 of the chunk, one 1 KB row per global->LDS load (lane: 8 columns);
+  // rows past M repeat row M - 1 and columns past K repeat the last 8 (both multiply zeros
+  // or are never stored)
+#pragma unroll
+  for (int j = 0; j < 64 / PNW; ++j) {
+    const int m = wv * (64 / PNW) + j;
+    const uint16_t* src = p.x + (long long)min(m0 + m, p.M - 1) * p.x_rs + min(kc0 + 8 * lane, p.K - 8);
+    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(xs + m * PXS), 16, 0, 0);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (!live) return;
+  f32x4 acc[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < PKS; ++i)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const u16x8 xb = *reinterpret_cast<const u16x8*>(xs + (16 * t + r) * PXS + (32 * i + 8 * kg) * 2);
+      mma16_bf16(acc[t], wa[i], xb);
+    }
+  // D of tile t: column m = 16t + r, rows n = 4 kg + i: four consecutive n per lane
+  float* out = p.parts + (long long)ch * p.M * p.N + nt * 16 + 4 * kg;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int m = m0 + 16 * t + r;
+    if (m < p.M) *reinterpret_cast<f32x4*>(out + (long long)m * p.N) = acc[t];
+  }
+}
+
+// y[m][n] = round(sum over chunks of parts + bias), four n per thread
+__global__ void __launch_bounds__(256) proj_reduce_kernel(const float* parts, int n_chunks, int M, int N,
+                                                          const uint16_t* bias, uint16_t* y, int64_t y_rs) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  const int m = i / (N / 4), n = 4 * (i % (N / 4));
+  if (m >= M) return;
+  f32x4 v = *reinterpret_cast<const f32x4*>(parts + (long long)m * N + n);
+  for (int c = 1; c < n_chunks; ++c) {
+    const f32x4 w = *reinterpret_cast<const f32x4*>(parts + ((long long)c * M + m) * N + n);
+    v[0] += w[0]; v[1] += w[1]; v[2] += w[2]; v[3] += w[3];
+  }
+  u16x4 o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) o[e] = f2bf(bias ? v[e] + bf2f(bias[n + e]) : v[e]);
+  *reinterpret_cast<u16x4*>(y + (long long)m * y_rs + n) = o;
+}
+
+static int launch_rowproj(const ProjArgs& p, hipStream_t st) {
+  const dim3 grid((p.N / 16 + PNW - 1) / PNW, proj_chunks(p.K), (p.M + 63) / 64);
+  hipLaunchKernelGGL(rowproj_kernel, grid, dim3(64 * PNW), 0, st, p);
+  return (int)hipGetLastError();
+}
+
 template <typename T, int HD>
-static int launch_decode(const b3_decode_args& a, hipStream_t st) {
+static int launch_decode(const b3_decode_args& a, hipStream_t st, LinParts lp) {
   const int BH = a.B * a.HKV;
   const int nk = a.n_sink_keys + (a.has_slots ? a.S : 0) + a.a_len + a.b_len + 1;
-  hipLaunchKernelGGL((decode_prep_kernel<T, HD>), dim3(BH), dim3(128), 0, st, a);
+  hipLaunchKernelGGL((decode_prep_kernel<T, HD>), dim3(BH), dim3(128), 0, st, a, lp);
   hipError_t e0 = hipGetLastError();
   if (e0 != hipSuccess) return (int)e0;
   hipLaunchKernelGGL((decode_split_kernel<T, HD>), dim3(dec_nsplit(nk) + HD / RROWS, BH), dim3(DNT), 0, st, a);
@@ -718,13 +860,15 @@ extern "C" int64_t bolt3_decode_workspace_bytes(int32_t B, int32_t H, int32_t HK
   return (int64_t)B * HKV * b3::dec_ws_per_bh(H / HKV, HD) * 4;
 }
 
-extern "C" int bolt3_decode(const b3_decode_args* a, void* stream) {
+// Argument checks shared by bolt3_decode and bolt3_decode_layer (need_lin: the row comes from
+// a->lin rather than from the layer's own projection).
+static int check_decode(const b3_decode_args* a, bool need_lin) {
   if (!a || a->B <= 0 || a->HKV <= 0 || a->H % a->HKV != 0) return B3_ERR_ARG;
   if (a->H / a->HKV > b3::GMAX || (a->HD != 64 && a->HD != 128)) return B3_ERR_UNSUPPORTED;
   const int nk = a->n_sink_keys + (a->has_slots ? a->S : 0) + a->a_len + a->b_len + 1;
   if (nk > b3::NKMAX || a->n_sink_keys < 0 || a->a_len < 0 || a->b_len < 0) return B3_ERR_UNSUPPORTED;
-  if (!a->lin || !a->win_kr || !a->win_kp || !a->win_v || !a->win_beta || !a->inv_freq || !a->gamma || !a->res_w ||
-      !a->y || !a->work)
+  if ((need_lin && !a->lin) || !a->win_kr || !a->win_kp || !a->win_v || !a->win_beta || !a->inv_freq ||
+      !a->gamma || !a->res_w || !a->y || !a->work)
     return B3_ERR_ARG;
   if (a->work_bytes < bolt3_decode_workspace_bytes(a->B, a->H, a->HKV, a->HD)) return B3_ERR_WORKSPACE;
   if (a->has_slots && (!a->slot_k || !a->slot_v || !a->slot_bias)) return B3_ERR_ARG;
@@ -732,12 +876,63 @@ extern "C" int bolt3_decode(const b3_decode_args* a, void* stream) {
   if (a->has_qk_norm && (!a->qn_w || !a->kn_w)) return B3_ERR_ARG;
   // 16-byte rows: the projection row and every key / value row
   const int64_t es = a->dtype == B3_BF16 ? 2 : 4;
-  if ((a->lin_row_stride * es) % 16 || reinterpret_cast<uintptr_t>(a->lin) % 16) return B3_ERR_ARG;
+  if ((a->lin_row_stride * es) % 16 || (need_lin && reinterpret_cast<uintptr_t>(a->lin) % 16)) return B3_ERR_ARG;
+  return 0;
+}
+
+extern "C" int bolt3_decode(const b3_decode_args* a, void* stream) {
+  const int rc = check_decode(a, true);
+  if (rc) return rc;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  if (a->dtype == B3_F32) return a->HD == 64 ? b3::launch_decode<float, 64>(*a, st) : b3::launch_decode<float, 128>(*a, st);
+  const b3::LinParts lp{nullptr, 0, 0, nullptr};
+  if (a->dtype == B3_F32)
+    return a->HD == 64 ? b3::launch_decode<float, 64>(*a, st, lp) : b3::launch_decode<float, 128>(*a, st, lp);
   if (a->dtype == B3_BF16)
-    return a->HD == 64 ? b3::launch_decode<uint16_t, 64>(*a, st) : b3::launch_decode<uint16_t, 128>(*a, st);
+    return a->HD == 64 ? b3::launch_decode<uint16_t, 64>(*a, st, lp) : b3::launch_decode<uint16_t, 128>(*a, st, lp);
   return B3_ERR_UNSUPPORTED;
+}
+
+extern "C" int64_t bolt3_decode_layer_workspace_bytes(int32_t B, int32_t d_model, int32_t n_in, int32_t hd_total,
+                                                      int32_t n_out) {
+  if (B <= 0 || d_model <= 0 || n_in <= 0 || hd_total <= 0 || n_out <= 0) return 0;
+  const long long a = b3::proj_parts_floats(B, n_in, d_model), b = b3::proj_parts_floats(B, n_out, hd_total);
+  return (int64_t)(a > b ? a : b) * 4;
+}
+
+extern "C" int bolt3_decode_layer(const b3_decode_layer_args* a, void* stream) {
+  if (!a) return B3_ERR_ARG;
+  const b3_decode_args& d = a->dec;
+  if (d.dtype != B3_BF16) return B3_ERR_UNSUPPORTED;
+  int rc = check_decode(&d, false);
+  if (rc) return rc;
+  const int hd_total = d.H * d.HD;
+  if (!a->x || !a->w_in || !a->w_out || !a->out || !a->proj_work) return B3_ERR_ARG;
+  if (a->d_model < 32 || a->d_model % 32 || a->n_in != d.lin_row_stride || a->n_in % 16 ||
+      a->n_in < d.H * d.HD + 2 * d.HKV * d.HD + d.HKV + d.H || a->n_out <= 0 || a->n_out % 16 ||
+      a->x_row_stride < a->d_model || a->x_row_stride % 8 || a->out_row_stride < a->n_out ||
+      a->out_row_stride % 4 || reinterpret_cast<uintptr_t>(a->x) % 16 || reinterpret_cast<uintptr_t>(a->out) % 8 ||
+      reinterpret_cast<uintptr_t>(a->proj_work) % 16)
+    return B3_ERR_ARG;
+  if (a->proj_work_bytes < bolt3_decode_layer_workspace_bytes(d.B, a->d_model, a->n_in, hd_total, a->n_out))
+    return B3_ERR_WORKSPACE;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const b3::ProjArgs pin{reinterpret_cast<const uint16_t*>(a->x), a->x_row_stride,
+                         reinterpret_cast<const uint16_t*>(a->w_in), a->proj_work, d.B, a->n_in, a->d_model};
+  rc = b3::launch_rowproj(pin, st);
+  if (rc) return rc;
+  const b3::LinParts lp{a->proj_work, b3::proj_chunks(a->d_model), (long long)d.B * a->n_in,
+                        reinterpret_cast<const uint16_t*>(a->b_in)};
+  rc = d.HD == 64 ? b3::launch_decode<uint16_t, 64>(d, st, lp) : b3::launch_decode<uint16_t, 128>(d, st, lp);
+  if (rc) return rc;
+  const b3::ProjArgs pout{reinterpret_cast<const uint16_t*>(d.y), hd_total,
+                          reinterpret_cast<const uint16_t*>(a->w_out), a->proj_work, d.B, a->n_out, hd_total};
+  rc = b3::launch_rowproj(pout, st);
+  if (rc) return rc;
+  const int n_thr = d.B * (a->n_out / 4);
+  hipLaunchKernelGGL(b3::proj_reduce_kernel, dim3((n_thr + 255) / 256), dim3(256), 0, st, a->proj_work,
+                     b3::proj_chunks(hd_total), d.B, a->n_out, reinterpret_cast<const uint16_t*>(a->b_out),
+                     reinterpret_cast<uint16_t*>(a->out), a->out_row_stride);
+  return (int)hipGetLastError();
 }
 
 extern "C" const char* bolt3_version(void) { return "bolt3_amd 0.1 gfx950 (MFMA 32x32, wave64)"; }

@@ -1,25 +1,21 @@
 // One-token decode step of a Bolt-3 layer (t_s == 1 branch of
 // Bolt3Decoder.step, vsa_lm/config/bolt3.py:346-402).
 //
-// The step is bound by reading the window, the slots and M_res once, so it is
-// split over many workgroups (flash-decoding), in three kernels:
-//   decode_prep_kernel, grid (B*HKV): head preparation of the new token (q/k
-//     RMSNorm, RoPE, beta/eta gates); appends its roped and un-roped key,
-//     value, beta and position to the window ring and leaves the roped and
-//     normalised un-roped queries, 1/|q_raw| and eta in the workspace.
-//   decode_split_kernel, grid (ceil(keys / 128) + HD/32, B*HKV):
-//     attention workgroups take 128 keys of the list
-//     [sinks | attractor slots | window A | window B | new token] of one
-//     (batch, kv head), one 32-key tile per wavefront: the key and value rows
-//     are requested first, then S^T = K Q^T with the G query heads as MFMA
-//     columns, a softmax per head column, and O^T = V^T P^T with the
-//     probabilities rounded to the storage dtype (V^T staged in LDS).  The
-//     four tiles of a workgroup are merged in LDS and leave one
-//     (max, sum, unnormalised output) per head in the workspace.
-//     Readout workgroups each multiply normalize(q_raw) by 32 rows of M_res.
-//   decode_combine_kernel, grid (B*HKV): merges the partial softmaxes, rounds
-//     the attention output, finishes the readout
-//     eta * RMSNorm(normalize(q_raw) M (1-gamma)/sqrt(HD)) and adds it.
+// The step is bound by reading the window, the slots and M_res once:
+//   decode_prep_kernel, grid (B*HKV): head preparation of the new token (q/k RMSNorm, RoPE,
+//     beta/eta gates) from the projection row (or from the fp32 K-chunk partial products of
+//     bolt3_decode_layer's projection); appends its roped and un-roped key, value, beta and
+//     position to the window ring and leaves the roped and normalised un-roped queries,
+//     1/|q_raw| and eta in the workspace.
+//   bf16: decode_attn_kernel, grid (B*HKV): attention over
+//     [sinks | attractor slots | window A | window B | new token] and the M_res readout of one
+//     (batch, kv head) per workgroup, merged in LDS, y written.
+//   fp32: decode_split_kernel, grid (ceil(keys / 128) + HD/32, B*HKV), 128-key pieces and
+//     32-row readout pieces in parallel with fp32 MFMAs, then decode_combine_kernel, grid
+//     (B*HKV), merges the partial softmaxes and finishes the readout.
+// bolt3_decode_layer (bf16) adds the two projections around these: rowproj_kernel streams
+// a weight once per step and leaves fp32 partial products per K chunk; the prep kernel sums
+// those of the input projection and proj_reduce_kernel those of o_proj.
 #include "bolt3_common.h"
 #include "bolt3_math.h"
 #include "bolt3_amd.h"
@@ -42,6 +38,12 @@ __device__ __forceinline__ void dec_lds_wait(u16x4& a, u16x4& b) {
   asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b));
 }
 __device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); }
+// wait until at most N vector-memory operations of this wavefront are outstanding
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (((N >> 4) & 3) << 14) | (7 << 4) | (15 << 8));
+}
 
 constexpr int DNT = 256;        // threads per decode workgroup
 constexpr int DWAVES = DNT / 64;
@@ -79,15 +81,13 @@ __device__ __forceinline__ void load8(const T* p, float* out) {
 
 template <typename T, int HD>
 struct SplitSmem {
-  static constexpr int QS = sizeof(T) == 2 ? HD + 8 : HD + 4;   // query row stride (16-byte rows)
-  static constexpr int VS = sizeof(T) == 2 ? 32 + 8 : 32 + 1;   // V^T row stride of a key tile
-  static constexpr bool BF = sizeof(T) == 2;
-  alignas(16) T qt[(BF ? 16 : 32) * QS];   // roped queries as MFMA operand rows; rows G.. zero
-  float qr[GMAX][HD];             // un-roped queries after the norm
-  float bias[DWAVES][32];         // slot bias of each wavefront's key tile
+  static constexpr int QS = HD + 4;   // query row stride (16-byte rows)
+  static constexpr int VS = 32 + 1;   // V^T row stride of a key tile
+  alignas(16) T qt[32 * QS];          // roped queries as MFMA operand rows; rows G.. zero
+  float qr[GMAX][HD];                 // un-roped queries after the norm
+  float bias[DWAVES][32];             // slot bias of each wavefront's key tile
   union {
-    T vt[BF ? 1 : DWAVES][HD * VS];   // V^T of each wavefront's key tile (fp32 storage)
-    T vrow[DWAVES][32 * HD];      // value rows of each wavefront's key tile (bf16: LDS-DMA target)
+    T vt[DWAVES][HD * VS];            // V^T of each wavefront's key tile
     float part[DNT / 64][GMAX][HD];   // readout row groups; per-wavefront outputs of the merge
   } u;
   float wm[DWAVES][GMAX], wl[DWAVES][GMAX];   // per-wavefront softmax max / sum
@@ -101,6 +101,8 @@ struct SplitSmem {
 // Source of the projection row when it comes as fp32 partial products of K chunks
 // (parts[chunk][b][c], chunk_stride floats apart): the row is the chunks added in order, plus
 // the bias, rounded once.  parts == nullptr: the row is a.lin.
+constexpr int LP_MAXC = 8;   // K chunks a projection row may come in (K <= 8 * 512)
+
 struct LinParts {
   const float* parts;
   int n_chunks;
@@ -134,13 +136,20 @@ __global__ void __launch_bounds__(128) decode_prep_kernel(b3_decode_args a, LinP
   auto lin8 = [&](int c, float* out) {
     if (lp.parts) {
       const float* q = lp.parts + (long long)b * a.lin_row_stride + c;
-      f32x4 lo = *reinterpret_cast<const f32x4*>(q), hi = *reinterpret_cast<const f32x4*>(q + 4);
-      for (int k = 1; k < lp.n_chunks; ++k) {
-        const f32x4 l2 = *reinterpret_cast<const f32x4*>(q + k * lp.chunk_stride);
-        const f32x4 h2 = *reinterpret_cast<const f32x4*>(q + k * lp.chunk_stride + 4);
+      // every chunk's loads first (at most LP_MAXC chunks), then the sums in chunk order
+      f32x4 pl[LP_MAXC], ph[LP_MAXC];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) { lo[e] += l2[e]; hi[e] += h2[e]; }
-      }
+      for (int k = 0; k < LP_MAXC; ++k)
+        if (k < lp.n_chunks) {
+          pl[k] = *reinterpret_cast<const f32x4*>(q + k * lp.chunk_stride);
+          ph[k] = *reinterpret_cast<const f32x4*>(q + k * lp.chunk_stride + 4);
+        }
+      f32x4 lo = pl[0], hi = ph[0];
+#pragma unroll
+      for (int k = 1; k < LP_MAXC; ++k)
+        if (k < lp.n_chunks)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) { lo[e] += pl[k][e]; hi[e] += ph[k][e]; }
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         out[e] = St<T>::rnd(lp.bias ? lo[e] + bf2f(lp.bias[c + e]) : lo[e]);
@@ -153,8 +162,14 @@ __global__ void __launch_bounds__(128) decode_prep_kernel(b3_decode_args a, LinP
   auto lin1 = [&](int c) -> float {
     if (lp.parts) {
       const float* q = lp.parts + (long long)b * a.lin_row_stride + c;
-      float v = q[0];
-      for (int k = 1; k < lp.n_chunks; ++k) v += q[k * lp.chunk_stride];
+      float pv[LP_MAXC];
+#pragma unroll
+      for (int k = 0; k < LP_MAXC; ++k)
+        if (k < lp.n_chunks) pv[k] = q[k * lp.chunk_stride];
+      float v = pv[0];
+#pragma unroll
+      for (int k = 1; k < LP_MAXC; ++k)
+        if (k < lp.n_chunks) v += pv[k];
       return St<T>::rnd(lp.bias ? v + bf2f(lp.bias[c]) : v);
     }
     return St<T>::ld(row + c);
@@ -237,31 +252,9 @@ __global__ void __launch_bounds__(128) decode_prep_kernel(b3_decode_args a, LinP
   }
 }
 
-// Key-row fragment of a 32-key tile: lane (key n = lane%32, h = lane/32) holds the K
-// sub-index 16*ks + 8*h + i (bf16) or 2*ks + h (fp32) of its key row.
+// Key-row fragment of a 32-key tile (fp32 storage): lane (key n = lane%32, h = lane/32) holds
+// the K sub-index 2*ks + h of its key row.
 template <typename T, int HD> struct RowFrag;
-template <int HD> struct RowFrag<uint16_t, HD> {
-  static constexpr int NK = HD / 16;
-  u16x8 v[NK];
-  __device__ __forceinline__ void load(const uint16_t* row, int h) {
-#pragma unroll
-    for (int ks = 0; ks < NK; ++ks) v[ks] = *reinterpret_cast<const u16x8*>(row + 16 * ks + 8 * h);
-  }
-  __device__ __forceinline__ void zero() {
-#pragma unroll
-    for (int ks = 0; ks < NK; ++ks)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) v[ks][i] = 0;
-  }
-  __device__ __forceinline__ void from_lds(const float* x, int h) {
-#pragma unroll
-    for (int ks = 0; ks < NK; ++ks)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) v[ks][i] = f2bf(x[16 * ks + 8 * h + i]);
-  }
-  __device__ __forceinline__ float at(int ks, int i) const { return bf2f(v[ks][i]); }
-  static __device__ __forceinline__ int col(int ks, int i, int h) { return 16 * ks + 8 * h + i; }
-};
 template <int HD> struct RowFrag<float, HD> {
   static constexpr int NK = HD / 2;
   float v[NK];
@@ -281,9 +274,9 @@ template <int HD> struct RowFrag<float, HD> {
 
 template <typename T, int HD>
 __global__ void __launch_bounds__(DNT) decode_split_kernel(b3_decode_args a) {
+  static_assert(!St<T>::is_bf16, "bf16 steps run decode_attn_kernel");
   using Sm = SplitSmem<T, HD>;
   __shared__ Sm sm;
-  constexpr int NREAD = HD / RROWS;  // readout workgroups
   constexpr int NDB = HD / 32;
   const int bh = blockIdx.y, b = bh / a.HKV, hkv = bh % a.HKV;
   const int G = a.H / a.HKV;
@@ -295,9 +288,6 @@ __global__ void __launch_bounds__(DNT) decode_split_kernel(b3_decode_args a) {
   const int split = blockIdx.x;
   float* ws = a.work + (long long)bh * dec_ws_per_bh(G, HD);
   float* ws_read = ws + NPART * G * (HD + 2);
-  float* ws_stat = ws_read + NREAD * G * HD;
-  const T* row = reinterpret_cast<const T*>(a.lin) + (long long)b * a.lin_row_stride;
-  const int gcol = (a.H + 2 * a.HKV) * HD;
 
   if (split >= nsplit) {
     // ---------------- rows [RROWS*r, RROWS*r + RROWS) of the M_res readout
@@ -338,168 +328,6 @@ __global__ void __launch_bounds__(DNT) decode_split_kernel(b3_decode_args a) {
   // ---------------- attention: wavefront `wave` takes keys kt0 .. kt0+31 of the list
   //   [sinks | attractor slots | window A | window B + new token]
   const int kt0 = split * KWG + 32 * wave;
-  if constexpr (St<T>::is_bf16) {
-    // 16x16x32 MFMAs with the G query heads as columns: S^T[key][head] = K Q^T over two
-    // 16-key blocks, O^T[feature][head] += V^T P^T.  Key rows go to registers in operand
-    // order; the 32 value rows go to LDS by global->LDS loads (16-byte pieces of row r
-    // permuted by p ^ (r % (HD/8))) and are read transposed (ds_read_b64_tr_b16).
-    const int m = lane & 15, g4 = lane >> 4;
-    auto key_rows = [&](int key, const T*& kp, const T*& vp, float& bias) {
-      int k = min(key, nk - 1);
-      bias = 0.f;
-      if (k < ns) {
-        const long long o = (long long)b * a.s_sb + (long long)hkv * a.s_sh + (long long)k * HD;
-        kp = reinterpret_cast<const T*>(a.sink_k) + o;
-        vp = reinterpret_cast<const T*>(a.sink_v) + o;
-      } else if ((k -= ns) < nsl) {
-        kp = reinterpret_cast<const T*>(a.slot_k) + ((long long)bh * a.S + k) * HD;
-        vp = reinterpret_cast<const T*>(a.slot_v) + ((long long)bh * a.S + k) * HD;
-        bias = a.slot_bias[(long long)bh * a.S + k];
-      } else if ((k -= nsl) < na) {
-        kp = reinterpret_cast<const T*>(a.win_kp) + wbase + (long long)(a.a_start + k) * HD;
-        vp = reinterpret_cast<const T*>(a.win_v) + wbase + (long long)(a.a_start + k) * HD;
-      } else {   // window B, the new token (appended by decode_prep_kernel) included
-        k -= na;
-        kp = reinterpret_cast<const T*>(a.win_kp) + wbase + (long long)(a.b_start + k) * HD;
-        vp = reinterpret_cast<const T*>(a.win_v) + wbase + (long long)(a.b_start + k) * HD;
-      }
-    };
-    // value rows -> LDS: instruction ch fills rows RPI*ch .. RPI*ch + RPI-1 (1 KB)
-    constexpr int NP = HD / 8, RPI = 64 / NP;
-    T* vrow = sm.u.vrow[wave];
-#pragma unroll
-    for (int ch = 0; ch < 32 / RPI; ++ch) {
-      const int r = RPI * ch + lane / NP, piece = (lane % NP) ^ (r % NP);
-      const T* kp;
-      const T* vp;
-      float bias;
-      key_rows(kt0 + r, kp, vp, bias);
-      dec_dma16(vp + 8 * piece, vrow + ch * 512);
-    }
-    // key rows -> registers: lane (m, g4) holds features 32ks + 8g4 .. of key kt0 + 16kb + m
-    u16x8 ka[2][HD / 32];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      const T* kp;
-      const T* vp;
-      float bias;
-      key_rows(kt0 + 16 * kb + m, kp, vp, bias);
-#pragma unroll
-      for (int ks = 0; ks < HD / 32; ++ks) ka[kb][ks] = *reinterpret_cast<const u16x8*>(kp + 32 * ks + 8 * g4);
-      if (g4 == 0) sm.bias[wave][16 * kb + m] = bias;
-    }
-    // query rows (heads) from the workspace, rows G..15 zero
-    {
-      const T* qsrc = reinterpret_cast<const T*>(ws + dec_ws_q(G, HD));
-      for (int it = tid; it < 16 * (HD / 8); it += DNT) {
-        const int rr = it / (HD / 8), c8 = (it % (HD / 8)) * 8;
-        Vec8<T> x;
-        if (rr < G) x.load(qsrc + rr * HD + c8);
-        else {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) x.set(e, 0.f);
-        }
-        x.store(&sm.qt[rr * Sm::QS + c8]);
-      }
-    }
-    __syncthreads();
-    f32x4 sc[2];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      sc[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < HD / 32; ++ks)
-        mma16_bf16(sc[kb], ka[kb][ks], *reinterpret_cast<const u16x8*>(&sm.qt[m * Sm::QS + 32 * ks + 8 * g4]));
-    }
-    // fp32 scores (the decoder step does not round q.k), slot bias, keys past nk masked
-    const float scale = 1.0f / sqrtf((float)HD);
-    float mx = -INFINITY;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int kr = 16 * kb + 4 * g4 + i;
-        float x = add_rn(mul_rn(sc[kb][i], scale), sm.bias[wave][kr]);
-        x = kt0 + kr < nk ? x : -INFINITY;
-        sc[kb][i] = x;
-        mx = fmaxf(mx, x);
-      }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    float sum = 0.f;
-    u16x8 pb;   // P^T operand: keys 4g4 + i (i < 4) and 16 + 4g4 + i - 4
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float e = mx == -INFINITY ? 0.f : expf(sc[kb][i] - mx);
-        sum += e;
-        pb[4 * kb + i] = f2bf(e);
-      }
-    sum += __shfl_xor(sum, 16, 64);
-    sum += __shfl_xor(sum, 32, 64);
-    // O^T[16db + 4g4 + i][head m]; transposed reads: source lane s of a 16-lane group
-    // addresses row 4g4 + s/4 (+16) and features 16db + 4(s & 3)
-    // (value pieces of row r are permuted by p ^ (r % NP))
-    wait_vm0();
-    f32x4 o[HD / 16];
-    {
-      const int s = lane & 15;
-#pragma unroll
-      for (int db = 0; db < HD / 16; ++db) {
-        const int r1 = 4 * g4 + (s >> 2), r2 = r1 + 16;
-        const int pc = 2 * db + ((s & 3) >> 1), off = 4 * (s & 1);
-        u16x4 lo = dec_read_tr(vrow + r1 * HD + 8 * (pc ^ (r1 % NP)) + off);
-        u16x4 hi = dec_read_tr(vrow + r2 * HD + 8 * (pc ^ (r2 % NP)) + off);
-        dec_lds_wait(lo, hi);
-        u16x8 av;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) { av[e] = lo[e]; av[4 + e] = hi[e]; }
-        o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
-        mma16_bf16(o[db], av, pb);
-      }
-    }
-    // ---- merge the four tiles of the workgroup: lane column m = head
-    if (m < G && g4 == 0) {
-      sm.wm[wave][m] = mx;
-      sm.wl[wave][m] = sum;
-    }
-    __syncthreads();   // every wavefront is done with its value rows (the union is reused below)
-    if (m < G) {
-      float mm = -INFINITY;
-#pragma unroll
-      for (int w = 0; w < DWAVES; ++w) mm = fmaxf(mm, sm.wm[w][m]);
-      const float f = mx == -INFINITY ? 0.f : expf(mx - mm);
-#pragma unroll
-      for (int db = 0; db < HD / 16; ++db)
-        *reinterpret_cast<float4*>(&sm.u.part[wave][m][16 * db + 4 * g4]) =
-            make_float4(o[db][0] * f, o[db][1] * f, o[db][2] * f, o[db][3] * f);
-    }
-    __syncthreads();
-    float* pw = ws + (long long)split * G * (HD + 2);
-    for (int it = tid; it < G * (HD / 4); it += DNT) {
-      const int gg = it / (HD / 4), d4 = (it % (HD / 4)) * 4;
-      float4 acc4 = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-      for (int w = 0; w < DWAVES; ++w) {
-        const float4 x = *reinterpret_cast<const float4*>(&sm.u.part[w][gg][d4]);
-        acc4.x += x.x; acc4.y += x.y; acc4.z += x.z; acc4.w += x.w;
-      }
-      *reinterpret_cast<float4*>(pw + gg * (HD + 2) + d4) = acc4;
-    }
-    if (tid < G) {
-      float mm = -INFINITY;
-#pragma unroll
-      for (int w = 0; w < DWAVES; ++w) mm = fmaxf(mm, sm.wm[w][tid]);
-      float l = 0.f;
-#pragma unroll
-      for (int w = 0; w < DWAVES; ++w)
-        l += sm.wm[w][tid] == -INFINITY ? 0.f : sm.wl[w][tid] * expf(sm.wm[w][tid] - mm);
-      pw[tid * (HD + 2) + HD] = mm;
-      pw[tid * (HD + 2) + HD + 1] = l;
-    }
-    return;
-  }
   const int key = kt0 + n;                     // this lane's key row
   const bool kin = key < nk;
   const T* kp = nullptr;
@@ -548,28 +376,13 @@ __global__ void __launch_bounds__(DNT) decode_split_kernel(b3_decode_args a) {
 
   // ---- S^T[key][head] = K . Q^T (heads as the columns)
   f32x16 sc = zero16();
-  if constexpr (St<T>::is_bf16) {
-#pragma unroll
-    for (int ks = 0; ks < HD / 16; ++ks) {
-      const u16x8 qv = *reinterpret_cast<const u16x8*>(&sm.qt[n * Sm::QS + 16 * ks + 8 * h]);
-      mma_bf16(sc, kf.v[ks], qv);
-    }
-  } else {
 #pragma unroll 8
-    for (int ks = 0; ks < HD / 2; ++ks) mma_f32(sc, kf.v[ks], sm.qt[n * Sm::QS + 2 * ks + h]);
-  }
+  for (int ks = 0; ks < HD / 2; ++ks) mma_f32(sc, kf.v[ks], sm.qt[n * Sm::QS + 2 * ks + h]);
   // V^T of the tile into LDS while the scores are finished
   {
     T* vt = sm.u.vt[wave];
-    if constexpr (St<T>::is_bf16) {
 #pragma unroll
-      for (int ks = 0; ks < HD / 16; ++ks)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) vt[(16 * ks + 8 * h + i) * Sm::VS + n] = vf.v[ks][i];
-    } else {
-#pragma unroll
-      for (int ks = 0; ks < HD / 2; ++ks) vt[(2 * ks + h) * Sm::VS + n] = vf.v[ks];
-    }
+    for (int ks = 0; ks < HD / 2; ++ks) vt[(2 * ks + h) * Sm::VS + n] = vf.v[ks];
   }
   const float scale = 1.0f / sqrtf((float)HD);
   float mx = -INFINITY;
@@ -596,32 +409,11 @@ __global__ void __launch_bounds__(DNT) decode_split_kernel(b3_decode_args a) {
 #pragma unroll
   for (int db = 0; db < NDB; ++db) o[db] = zero16();
   const T* vt = sm.u.vt[wave];
-  if constexpr (St<T>::is_bf16) {
-    u16x8 pv[2];
 #pragma unroll
-    for (int kc = 0; kc < 2; ++kc)
+  for (int db = 0; db < NDB; ++db) {
+    const int d = 32 * db + n;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) pv[kc][e] = f2bf(sc[8 * kc + e]);
-#pragma unroll
-    for (int db = 0; db < NDB; ++db) {
-      const int d = 32 * db + n;
-#pragma unroll
-      for (int kc = 0; kc < 2; ++kc) {
-        u16x8 av;
-        const u16x4 lo = *reinterpret_cast<const u16x4*>(vt + d * Sm::VS + 16 * kc + 4 * h);
-        const u16x4 hi = *reinterpret_cast<const u16x4*>(vt + d * Sm::VS + 16 * kc + 8 + 4 * h);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) { av[e] = lo[e]; av[4 + e] = hi[e]; }
-        mma_bf16(o[db], av, pv[kc]);
-      }
-    }
-  } else {
-#pragma unroll
-    for (int db = 0; db < NDB; ++db) {
-      const int d = 32 * db + n;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) mma_f32(o[db], vt[d * Sm::VS + d_row(lane, r)], sc[r]);
-    }
+    for (int r = 0; r < 16; ++r) mma_f32(o[db], vt[d * Sm::VS + d_row(lane, r)], sc[r]);
   }
   // ---- merge the four tiles of the workgroup: lane column n = head, rows = features
   if (n < G && h == 0) {
@@ -668,6 +460,7 @@ __global__ void __launch_bounds__(DNT) decode_split_kernel(b3_decode_args a) {
 // Merge the partial softmaxes of one (batch, kv head), round; finish and add the readout.
 template <typename T, int HD>
 __global__ void __launch_bounds__(DNT) decode_combine_kernel(b3_decode_args a) {
+  static_assert(!St<T>::is_bf16, "bf16 steps run decode_attn_kernel");
   constexpr int NREAD = HD / RROWS;
   constexpr int PER = GMAX * HD / DNT;   // outputs per thread at most
   __shared__ float red[GMAX][DNT / 64];
@@ -732,6 +525,309 @@ __global__ void __launch_bounds__(DNT) decode_combine_kernel(b3_decode_args a) {
       const float ymn = mul_rn(mul_rn(ym[q], rs), a.res_w[d]);
       const float rd = a.m_res ? St<T>::rnd(mul_rn(ws_stat[2 * g + 1], ymn)) : 0.f;
       y[it] = St<T>::from_f(St<T>::rnd(add_rn(att[q], rd)));
+    }
+  }
+}
+
+// ---------------------------------------------------------------- bf16 attention + readout, one workgroup per bh
+//
+// decode_attn_kernel, grid (B*HKV), 8 wavefronts, two workgroups per CU: the whole step of
+// one (batch, kv head) after the head preparation.  Wavefronts 0-3 take the 32-key tiles of
+// the key list [sinks | slots | window A | window B + new token] (tile j to wavefront j % 4),
+// with an online softmax per query head over a wavefront's tiles.  Per tile the key rows and
+// slot biases go to registers and the value rows to the wavefront's LDS buffer (global->LDS
+// loads, the 16-byte pieces of row r permuted by p ^ (r % (HD/8))); S^T = K Q^T with
+// v_mfma_f32_16x16x32_bf16 (keys as rows, the G query heads as columns), fp32 scores with the
+// slot bias, probabilities rounded to bf16, O^T += V^T P^T with the value rows read
+// transposed (ds_read_b64_tr_b16).  Wavefronts 4-7 each multiply a quarter of the rows of
+// M_res by the normalised query with fp32 MFMAs (v_mfma_f32_16x16x4f32: rows of M as the A
+// operand, the query heads as columns).  The softmax states and readout parts are merged in
+// LDS, the attention output rounded, the readout finished
+// (eta * RMSNorm(normalize(q_raw) M (1-gamma)/sqrt(HD))) and added, and y written.
+constexpr int ADW = 4;             // attention wavefronts
+constexpr int ARW = 4;             // readout wavefronts
+constexpr int ANT = 64 * (ADW + ARW);
+
+template <int HD>
+struct AttnDecSmem {
+  static constexpr int TILE = 32 * HD;   // bf16 elements of one value tile
+  union {
+    alignas(16) uint16_t vrow[ADW][TILE];
+    struct {
+      float o[ADW][GMAX][HD];            // unnormalised attention outputs of the wavefronts
+      float rd[ARW][GMAX][HD];           // readout parts
+    } mg;
+  } u;
+  float wm[ADW][GMAX], wl[ADW][GMAX];
+  float wt[GMAX][ADW], lsum[GMAX];       // merge weights exp(m_w - m) and normaliser per head
+  float red[GMAX][ANT / 64];
+};
+
+template <int HD>
+__global__ void __launch_bounds__(ANT, 4) decode_attn_kernel(b3_decode_args a) {
+  using Sm = AttnDecSmem<HD>;
+  __shared__ Sm sm;
+  constexpr int NP = HD / 8, RPI = 64 / NP, NKS = HD / 32, NDB = HD / 16;
+  const int bh = blockIdx.x, b = bh / a.HKV, hkv = bh % a.HKV;
+  const int G = a.H / a.HKV;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const long long wbase = (long long)b * a.w_sb + (long long)hkv * a.w_sh;
+  const int ns = a.n_sink_keys, nsl = a.has_slots ? a.S : 0, na = a.a_len, nbk = a.b_len + 1;
+  const int nk = ns + nsl + na + nbk;
+  const int ntile = (nk + 31) / 32;
+  const float* ws = a.work + (long long)bh * dec_ws_per_bh(G, HD);
+  const float* ws_stat = ws + dec_ws_q(G, HD) - 2 * G;
+  const uint16_t* q_rope = reinterpret_cast<const uint16_t*>(ws + dec_ws_q(G, HD));
+  const float* q_raw = ws + dec_ws_q(G, HD) + G * HD;
+  // constants of this thread's outputs (g, d) = (it / HD, it % HD), loaded first so that the
+  // merge at the end waits on nothing but LDS
+  constexpr int PER = (GMAX * HD + ANT - 1) / ANT;
+  float c_iq[PER], c_eta[PER], c_rw[PER];
+#pragma unroll
+  for (int qq = 0; qq < PER; ++qq) {
+    const int it = tid + ANT * qq;
+    c_iq[qq] = c_eta[qq] = c_rw[qq] = 0.f;
+    if (it < G * HD) {
+      c_iq[qq] = ws_stat[2 * (it / HD)];
+      c_eta[qq] = ws_stat[2 * (it / HD) + 1];
+      c_rw[qq] = a.res_w[it % HD];
+    }
+  }
+  const float gam = a.gamma[hkv];   // used in the merge; no wait here
+
+  const int m = lane & 15, g4 = lane >> 4;
+  float mx = -INFINITY, sum = 0.f;   // running softmax state of head column m
+  f32x4 o[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+  f32x4 rdv[HD / 16];   // readout wavefronts: r^T[16dt + 4(l/16) + i][head l%16]
+
+  if (wave < ADW) {
+    // key k of the list -> its key and value rows and slot bias (0 outside the slots)
+    auto key_rows = [&](int key, const uint16_t*& kp, const uint16_t*& vp, int& slot) {
+      int k = min(key, nk - 1);
+      slot = -1;
+      if (k < ns) {
+        const long long off = (long long)b * a.s_sb + (long long)hkv * a.s_sh + (long long)k * HD;
+        kp = reinterpret_cast<const uint16_t*>(a.sink_k) + off;
+        vp = reinterpret_cast<const uint16_t*>(a.sink_v) + off;
+      } else if ((k -= ns) < nsl) {
+        kp = reinterpret_cast<const uint16_t*>(a.slot_k) + ((long long)bh * a.S + k) * HD;
+        vp = reinterpret_cast<const uint16_t*>(a.slot_v) + ((long long)bh * a.S + k) * HD;
+        slot = k;
+      } else if ((k -= nsl) < na) {
+        kp = reinterpret_cast<const uint16_t*>(a.win_kp) + wbase + (long long)(a.a_start + k) * HD;
+        vp = reinterpret_cast<const uint16_t*>(a.win_v) + wbase + (long long)(a.a_start + k) * HD;
+      } else {
+        k -= na;
+        kp = reinterpret_cast<const uint16_t*>(a.win_kp) + wbase + (long long)(a.b_start + k) * HD;
+        vp = reinterpret_cast<const uint16_t*>(a.win_v) + wbase + (long long)(a.b_start + k) * HD;
+      }
+    };
+    // queries as the B operand: lane (head m, group g4) holds features 32ks + 8g4 .. of head m
+    u16x8 qb[NKS];
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      if (m < G) qb[ks] = *reinterpret_cast<const u16x8*>(q_rope + m * HD + 32 * ks + 8 * g4);
+      else qb[ks] = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    }
+    const float scale = 1.0f / sqrtf((float)HD);
+    uint16_t* vbuf = sm.u.vrow[wave];
+    for (int j = wave; j < ntile; j += ADW) {
+      const int kt0 = 32 * j;
+      // value rows -> LDS: instruction ch fills rows RPI*ch .. RPI*ch + RPI-1 (1 KB)
+#pragma unroll
+      for (int ch = 0; ch < 32 / RPI; ++ch) {
+        const int r = RPI * ch + lane / NP, piece = (lane % NP) ^ (r % NP);
+        const uint16_t* kp;
+        const uint16_t* vp;
+        int sl;
+        key_rows(kt0 + r, kp, vp, sl);
+        dec_dma16(vp + 8 * piece, vbuf + ch * 512);
+      }
+      // key rows -> registers: lane (m, g4) holds features 32ks + 8g4 .. of key kt0 + 16kb + m;
+      // slot biases of the lane's score rows (keys kt0 + 16kb + 4g4 + i)
+      u16x8 ka[2][NKS];
+      float bb[2][4];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const uint16_t* kp;
+        const uint16_t* vp;
+        int sl;
+        key_rows(kt0 + 16 * kb + m, kp, vp, sl);
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) ka[kb][ks] = *reinterpret_cast<const u16x8*>(kp + 32 * ks + 8 * g4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          key_rows(kt0 + 16 * kb + 4 * g4 + i, kp, vp, sl);
+          bb[kb][i] = sl >= 0 ? a.slot_bias[(long long)bh * a.S + sl] : 0.f;
+        }
+      }
+      f32x4 sc[2];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        sc[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) mma16_bf16(sc[kb], ka[kb][ks], qb[ks]);
+      }
+      // fp32 scores (the decoder step does not round q.k), slot bias, keys past nk masked
+      float tmx = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int key = kt0 + 16 * kb + 4 * g4 + i;
+          float x = add_rn(mul_rn(sc[kb][i], scale), bb[kb][i]);
+          x = key < nk ? x : -INFINITY;
+          sc[kb][i] = x;
+          tmx = fmaxf(tmx, x);
+        }
+      tmx = fmaxf(tmx, __shfl_xor(tmx, 16, 64));
+      tmx = fmaxf(tmx, __shfl_xor(tmx, 32, 64));
+      const float nmx = fmaxf(mx, tmx);
+      const float f = mx == -INFINITY ? 0.f : expf(mx - nmx);
+      float ts = 0.f;
+      u16x8 pb;   // P^T operand: keys 4g4 + i (i < 4) and 16 + 4g4 + i - 4
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float e = nmx == -INFINITY ? 0.f : expf(sc[kb][i] - nmx);
+          ts += e;
+          pb[4 * kb + i] = f2bf(e);
+        }
+      ts += __shfl_xor(ts, 16, 64);
+      ts += __shfl_xor(ts, 32, 64);
+      sum = sum * f + ts;
+      mx = nmx;
+      // every load of the tile (the value rows in LDS included) has landed
+      wait_vm<0>();
+      const int s = lane & 15;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+        const int r1 = 4 * g4 + (s >> 2), r2 = r1 + 16;
+        const int pc = 2 * db + ((s & 3) >> 1), off = 4 * (s & 1);
+        u16x4 lo = dec_read_tr(vbuf + r1 * HD + 8 * (pc ^ (r1 % NP)) + off);
+        u16x4 hi = dec_read_tr(vbuf + r2 * HD + 8 * (pc ^ (r2 % NP)) + off);
+        dec_lds_wait(lo, hi);
+        u16x8 av;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) { av[e] = lo[e]; av[4 + e] = hi[e]; }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[db][e] *= f;
+        mma16_bf16(o[db], av, pb);
+      }
+    }
+  } else if (a.m_res) {
+    // r^T[d][g] = sum over the wavefront's rows c of M[c][d] q^[g][c]: 16x16x4 fp32 MFMAs,
+    // lane (l % 16, l / 16) loads A = M[c0 + l/16][d0 + l%16] and B = q^[l%16][c0 + l/16]
+    constexpr int RR = HD / ARW, NCS = RR / 4, NDT = HD / 16;
+    const int q = wave - ADW;
+    const int r16 = lane & 15, k4 = lane >> 4;
+    const float* M = a.m_res + (long long)bh * HD * HD + (long long)(q * RR + k4) * HD + r16;
+    float ma[NCS][NDT];
+#pragma unroll
+    for (int cs = 0; cs < NCS; ++cs)
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) ma[cs][dt] = M[(long long)(4 * cs) * HD + 16 * dt];
+    float qv[NCS];
+#pragma unroll
+    for (int cs = 0; cs < NCS; ++cs) qv[cs] = r16 < G ? q_raw[r16 * HD + q * RR + 4 * cs + k4] : 0.f;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+      f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int cs = 0; cs < NCS; ++cs) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ma[cs][dt], qv[cs], acc, 0, 0, 0);
+      rdv[dt] = acc;
+    }
+  }
+  __syncthreads();   // every wavefront is done with its value tiles (the union is reused below)
+  if (wave < ADW) {
+    if (m < G) {
+      if (g4 == 0) {
+        sm.wm[wave][m] = mx;
+        sm.wl[wave][m] = sum;
+      }
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+        *reinterpret_cast<float4*>(&sm.u.mg.o[wave][m][16 * db + 4 * g4]) =
+            make_float4(o[db][0], o[db][1], o[db][2], o[db][3]);
+    }
+  } else {
+    const int q = wave - ADW;
+    if (m < G)
+#pragma unroll
+      for (int dt = 0; dt < HD / 16; ++dt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sm.u.mg.rd[q][m][16 * dt + 4 * g4 + i] = a.m_res ? rdv[dt][i] : 0.f;
+  }
+  __syncthreads();
+  // merge weights of the wavefronts' softmax states, once per head
+  if (tid < G) {
+    const int g = tid;
+    float mm = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < ADW; ++w) mm = fmaxf(mm, sm.wm[w][g]);
+    float l = 0.f;
+#pragma unroll
+    for (int w = 0; w < ADW; ++w) {
+      const float ms = sm.wm[w][g];
+      const float wt = ms == -INFINITY ? 0.f : expf(ms - mm);
+      sm.wt[g][w] = wt;
+      l += sm.wl[w][g] * wt;
+    }
+    sm.lsum[g] = l;
+  }
+  __syncthreads();
+  // merge: thread (g, d) for g < G
+  const float coef = div_rn(1.0f - gam, sqrtf((float)HD));
+  float att[PER], ym[PER];
+#pragma unroll
+  for (int qq = 0; qq < PER; ++qq) {
+    const int it = tid + ANT * qq;
+    att[qq] = 0.f;
+    ym[qq] = 0.f;
+    if (it < G * HD) {
+      const int g = it / HD, d = it % HD;
+      float ov = 0.f;
+#pragma unroll
+      for (int w = 0; w < ADW; ++w) ov += sm.u.mg.o[w][g][d] * sm.wt[g][w];
+      att[qq] = round_bf(ov / sm.lsum[g]);
+      float r = 0.f;
+#pragma unroll
+      for (int w = 0; w < ARW; ++w) r += sm.u.mg.rd[w][g][d];
+      ym[qq] = mul_rn(r * c_iq[qq], coef);
+    }
+  }
+  // mean square of ym per head: wavefront sums, then across wavefronts
+  const int wv = tid >> 6;
+#pragma unroll
+  for (int g = 0; g < GMAX; ++g) {
+    if (g >= G) break;
+    float ss = 0.f;
+#pragma unroll
+    for (int qq = 0; qq < PER; ++qq) {
+      const int it = tid + ANT * qq;
+      if (it < G * HD && it / HD == g) ss += ym[qq] * ym[qq];
+    }
+    ss = wave_sum(ss);
+    if (lane == 0) sm.red[g][wv] = ss;
+  }
+  __syncthreads();
+  uint16_t* y = reinterpret_cast<uint16_t*>(a.y) + (long long)b * a.H * HD + (long long)hkv * G * HD;
+#pragma unroll
+  for (int qq = 0; qq < PER; ++qq) {
+    const int it = tid + ANT * qq;
+    if (it < G * HD) {
+      const int g = it / HD;
+      float ss = 0.f;
+#pragma unroll
+      for (int w = 0; w < ANT / 64; ++w) ss += sm.red[g][w];
+      const float rs = 1.0f / sqrtf(div_rn(ss, (float)HD) + a.eps);
+      const float ymn = mul_rn(mul_rn(ym[qq], rs), c_rw[qq]);
+      const float rd = a.m_res ? round_bf(mul_rn(c_eta[qq], ymn)) : 0.f;
+      y[it] = f2bf(round_bf(add_rn(att[qq], rd)));
     }
   }
 }
@@ -822,11 +918,14 @@ __global__ void __launch_bounds__(256) proj_reduce_kernel(const float* parts, in
   const int i = blockIdx.x * 256 + threadIdx.x;
   const int m = i / (N / 4), n = 4 * (i % (N / 4));
   if (m >= M) return;
-  f32x4 v = *reinterpret_cast<const f32x4*>(parts + (long long)m * N + n);
-  for (int c = 1; c < n_chunks; ++c) {
-    const f32x4 w = *reinterpret_cast<const f32x4*>(parts + ((long long)c * M + m) * N + n);
-    v[0] += w[0]; v[1] += w[1]; v[2] += w[2]; v[3] += w[3];
-  }
+  f32x4 pc[LP_MAXC];
+#pragma unroll
+  for (int c = 0; c < LP_MAXC; ++c)
+    if (c < n_chunks) pc[c] = *reinterpret_cast<const f32x4*>(parts + ((long long)c * M + m) * N + n);
+  f32x4 v = pc[0];
+#pragma unroll
+  for (int c = 1; c < LP_MAXC; ++c)
+    if (c < n_chunks) { v[0] += pc[c][0]; v[1] += pc[c][1]; v[2] += pc[c][2]; v[3] += pc[c][3]; }
   u16x4 o;
 #pragma unroll
   for (int e = 0; e < 4; ++e) o[e] = f2bf(bias ? v[e] + bf2f(bias[n + e]) : v[e]);
@@ -846,10 +945,14 @@ static int launch_decode(const b3_decode_args& a, hipStream_t st, LinParts lp) {
   hipLaunchKernelGGL((decode_prep_kernel<T, HD>), dim3(BH), dim3(128), 0, st, a, lp);
   hipError_t e0 = hipGetLastError();
   if (e0 != hipSuccess) return (int)e0;
-  hipLaunchKernelGGL((decode_split_kernel<T, HD>), dim3(dec_nsplit(nk) + HD / RROWS, BH), dim3(DNT), 0, st, a);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return (int)e;
-  hipLaunchKernelGGL((decode_combine_kernel<T, HD>), dim3(BH), dim3(DNT), 0, st, a);
+  if constexpr (St<T>::is_bf16) {
+    hipLaunchKernelGGL((decode_attn_kernel<HD>), dim3(BH), dim3(ANT), 0, st, a);
+  } else {
+    hipLaunchKernelGGL((decode_split_kernel<T, HD>), dim3(dec_nsplit(nk) + HD / RROWS, BH), dim3(DNT), 0, st, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return (int)e;
+    hipLaunchKernelGGL((decode_combine_kernel<T, HD>), dim3(BH), dim3(DNT), 0, st, a);
+  }
   return (int)hipGetLastError();
 }
 
@@ -913,6 +1016,7 @@ extern "C" int bolt3_decode_layer(const b3_decode_layer_args* a, void* stream) {
       a->out_row_stride % 4 || reinterpret_cast<uintptr_t>(a->x) % 16 || reinterpret_cast<uintptr_t>(a->out) % 8 ||
       reinterpret_cast<uintptr_t>(a->proj_work) % 16)
     return B3_ERR_ARG;
+  if (b3::proj_chunks(a->d_model) > b3::LP_MAXC || b3::proj_chunks(hd_total) > b3::LP_MAXC) return B3_ERR_UNSUPPORTED;
   if (a->proj_work_bytes < bolt3_decode_layer_workspace_bytes(d.B, a->d_model, a->n_in, hd_total, a->n_out))
     return B3_ERR_WORKSPACE;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);

@@ -110,17 +110,30 @@ struct LinParts {
   const uint16_t* bias;
 };
 
+// Where the prepared token goes: roped queries [G][HD] (storage dtype), normalised
+// un-roped queries [G][HD] (fp32), (1/|q_raw|, eta) per head, and optionally copies of the
+// new token's roped key and value rows (besides the window ring).
+template <typename T>
+struct PrepOut {
+  T* q_rope;
+  float* q_raw;
+  float* stat;
+  T* new_k;
+  T* new_v;
+};
+
+// The head preparation of (batch, kv head) bh by the 128 threads tid = 0..127 (two whole
+// wavefronts).
 template <typename T, int HD>
-__global__ void __launch_bounds__(128) decode_prep_kernel(b3_decode_args a, LinParts lp) {
+__device__ __forceinline__ void prep_token(const b3_decode_args& a, const LinParts& lp, int bh, int tid,
+                                           const PrepOut<T>& out) {
   constexpr int HALF = HD / 2, P8 = HALF / 8;
-  const int bh = blockIdx.x, b = bh / a.HKV, hkv = bh % a.HKV;
+  const int b = bh / a.HKV, hkv = bh % a.HKV;
   const int G = a.H / a.HKV;
-  const int tid = threadIdx.x;
   const T* row = reinterpret_cast<const T*>(a.lin) + (long long)b * a.lin_row_stride;
-  float* ws = a.work + (long long)bh * dec_ws_per_bh(G, HD);
-  float* ws_stat = ws + dec_ws_q(G, HD) - 2 * G;
-  T* q_rope = reinterpret_cast<T*>(ws + dec_ws_q(G, HD));
-  float* q_raw = ws + dec_ws_q(G, HD) + G * HD;
+  float* ws_stat = out.stat;
+  T* q_rope = out.q_rope;
+  float* q_raw = out.q_raw;
   const long long wbase = (long long)b * a.w_sb + (long long)hkv * a.w_sh;
   const int ni = a.b_start + a.b_len;   // ring index of the new token
   const int gcol = (a.H + 2 * a.HKV) * HD;
@@ -212,6 +225,10 @@ __global__ void __launch_bounds__(128) decode_prep_kernel(b3_decode_args a, LinP
       T* vo = reinterpret_cast<T*>(a.win_v) + wbase + (long long)ni * HD;
       v0.store(vo + 8 * p);
       v1.store(vo + HALF + 8 * p);
+      if (out.new_v) {
+        v0.store(out.new_v + 8 * p);
+        v1.store(out.new_v + HALF + 8 * p);
+      }
     } else {
       const float pos = (float)a.pos;
       Vec8<T> r0, r1, u0, u1;
@@ -241,6 +258,10 @@ __global__ void __launch_bounds__(128) decode_prep_kernel(b3_decode_args a, LinP
         u1.store(kr + HALF + 8 * p);
         r0.store(kp + 8 * p);
         r1.store(kp + HALF + 8 * p);
+        if (out.new_k) {
+          r0.store(out.new_k + 8 * p);
+          r1.store(out.new_k + HALF + 8 * p);
+        }
       }
     }
   }
@@ -250,6 +271,16 @@ __global__ void __launch_bounds__(128) decode_prep_kernel(b3_decode_args a, LinP
     a.win_beta[b * a.wb_sb + hkv * a.wb_sh + ni] = St<T>::rnd(1.0f / (1.0f + expf(-z)));
     if (bh == 0 && a.win_pos) a.win_pos[ni] = (float)a.pos;
   }
+}
+
+template <typename T, int HD>
+__global__ void __launch_bounds__(128) decode_prep_kernel(b3_decode_args a, LinParts lp) {
+  const int bh = blockIdx.x;
+  const int G = a.H / a.HKV;
+  float* ws = a.work + (long long)bh * dec_ws_per_bh(G, HD);
+  const PrepOut<T> out{reinterpret_cast<T*>(ws + dec_ws_q(G, HD)), ws + dec_ws_q(G, HD) + G * HD,
+                       ws + dec_ws_q(G, HD) - 2 * G, nullptr, nullptr};
+  prep_token<T, HD>(a, lp, bh, threadIdx.x, out);
 }
 
 // Key-row fragment of a 32-key tile (fp32 storage): lane (key n = lane%32, h = lane/32) holds
@@ -544,8 +575,8 @@ __global__ void __launch_bounds__(DNT) decode_combine_kernel(b3_decode_args a) {
 // operand, the query heads as columns).  The softmax states and readout parts are merged in
 // LDS, the attention output rounded, the readout finished
 // (eta * RMSNorm(normalize(q_raw) M (1-gamma)/sqrt(HD))) and added, and y written.
-constexpr int ADW = 4;             // attention wavefronts
-constexpr int ARW = 4;             // readout wavefronts
+constexpr int ADW = 6;             // attention wavefronts
+constexpr int ARW = 2;             // readout wavefronts
 constexpr int ANT = 64 * (ADW + ARW);
 
 template <int HD>
@@ -561,10 +592,17 @@ struct AttnDecSmem {
   float wm[ADW][GMAX], wl[ADW][GMAX];
   float wt[GMAX][ADW], lsum[GMAX];       // merge weights exp(m_w - m) and normaliser per head
   float red[GMAX][ANT / 64];
+  // the prepared token: roped queries, normalised un-roped queries, (1/|q_raw|, eta) per head,
+  // and the new key (roped) and value rows
+  alignas(16) uint16_t qrope[GMAX][HD];
+  alignas(16) float qhat[GMAX][HD];
+  float stat[2 * GMAX];
+  alignas(16) uint16_t newk[HD];
+  alignas(16) uint16_t newv[HD];
 };
 
 template <int HD>
-__global__ void __launch_bounds__(ANT, 4) decode_attn_kernel(b3_decode_args a) {
+__global__ void __launch_bounds__(ANT, 4) decode_attn_kernel(b3_decode_args a, LinParts lp) {
   using Sm = AttnDecSmem<HD>;
   __shared__ Sm sm;
   constexpr int NP = HD / 8, RPI = 64 / NP, NKS = HD / 32, NDB = HD / 16;
@@ -576,23 +614,12 @@ __global__ void __launch_bounds__(ANT, 4) decode_attn_kernel(b3_decode_args a) {
   const int ns = a.n_sink_keys, nsl = a.has_slots ? a.S : 0, na = a.a_len, nbk = a.b_len + 1;
   const int nk = ns + nsl + na + nbk;
   const int ntile = (nk + 31) / 32;
-  const float* ws = a.work + (long long)bh * dec_ws_per_bh(G, HD);
-  const float* ws_stat = ws + dec_ws_q(G, HD) - 2 * G;
-  const uint16_t* q_rope = reinterpret_cast<const uint16_t*>(ws + dec_ws_q(G, HD));
-  const float* q_raw = ws + dec_ws_q(G, HD) + G * HD;
-  // constants of this thread's outputs (g, d) = (it / HD, it % HD), loaded first so that the
-  // merge at the end waits on nothing but LDS
   constexpr int PER = (GMAX * HD + ANT - 1) / ANT;
-  float c_iq[PER], c_eta[PER], c_rw[PER];
+  float c_rw[PER];   // res_norm weight of this thread's outputs (g, d) = (it / HD, it % HD)
 #pragma unroll
   for (int qq = 0; qq < PER; ++qq) {
     const int it = tid + ANT * qq;
-    c_iq[qq] = c_eta[qq] = c_rw[qq] = 0.f;
-    if (it < G * HD) {
-      c_iq[qq] = ws_stat[2 * (it / HD)];
-      c_eta[qq] = ws_stat[2 * (it / HD) + 1];
-      c_rw[qq] = a.res_w[it % HD];
-    }
+    c_rw[qq] = it < G * HD ? a.res_w[it % HD] : 0.f;
   }
   const float gam = a.gamma[hkv];   // used in the merge; no wait here
 
@@ -603,66 +630,89 @@ __global__ void __launch_bounds__(ANT, 4) decode_attn_kernel(b3_decode_args a) {
   for (int db = 0; db < NDB; ++db) o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
   f32x4 rdv[HD / 16];   // readout wavefronts: r^T[16dt + 4(l/16) + i][head l%16]
 
-  if (wave < ADW) {
-    // key k of the list -> its key and value rows and slot bias (0 outside the slots)
-    auto key_rows = [&](int key, const uint16_t*& kp, const uint16_t*& vp, int& slot) {
-      int k = min(key, nk - 1);
-      slot = -1;
-      if (k < ns) {
-        const long long off = (long long)b * a.s_sb + (long long)hkv * a.s_sh + (long long)k * HD;
-        kp = reinterpret_cast<const uint16_t*>(a.sink_k) + off;
-        vp = reinterpret_cast<const uint16_t*>(a.sink_v) + off;
-      } else if ((k -= ns) < nsl) {
-        kp = reinterpret_cast<const uint16_t*>(a.slot_k) + ((long long)bh * a.S + k) * HD;
-        vp = reinterpret_cast<const uint16_t*>(a.slot_v) + ((long long)bh * a.S + k) * HD;
-        slot = k;
-      } else if ((k -= nsl) < na) {
-        kp = reinterpret_cast<const uint16_t*>(a.win_kp) + wbase + (long long)(a.a_start + k) * HD;
-        vp = reinterpret_cast<const uint16_t*>(a.win_v) + wbase + (long long)(a.a_start + k) * HD;
-      } else {
-        k -= na;
-        kp = reinterpret_cast<const uint16_t*>(a.win_kp) + wbase + (long long)(a.b_start + k) * HD;
-        vp = reinterpret_cast<const uint16_t*>(a.win_v) + wbase + (long long)(a.b_start + k) * HD;
+  // key k of the list -> its key and value rows and slot bias (0 outside the slots)
+  auto key_rows = [&](int key, const uint16_t*& kp, const uint16_t*& vp, int& slot) {
+    int k = min(key, nk - 1);
+    slot = -1;
+    if (k < ns) {
+      const long long off = (long long)b * a.s_sb + (long long)hkv * a.s_sh + (long long)k * HD;
+      kp = reinterpret_cast<const uint16_t*>(a.sink_k) + off;
+      vp = reinterpret_cast<const uint16_t*>(a.sink_v) + off;
+    } else if ((k -= ns) < nsl) {
+      kp = reinterpret_cast<const uint16_t*>(a.slot_k) + ((long long)bh * a.S + k) * HD;
+      vp = reinterpret_cast<const uint16_t*>(a.slot_v) + ((long long)bh * a.S + k) * HD;
+      slot = k;
+    } else if ((k -= nsl) < na) {
+      kp = reinterpret_cast<const uint16_t*>(a.win_kp) + wbase + (long long)(a.a_start + k) * HD;
+      vp = reinterpret_cast<const uint16_t*>(a.win_v) + wbase + (long long)(a.a_start + k) * HD;
+    } else {
+      k -= na;
+      kp = reinterpret_cast<const uint16_t*>(a.win_kp) + wbase + (long long)(a.b_start + k) * HD;
+      vp = reinterpret_cast<const uint16_t*>(a.win_v) + wbase + (long long)(a.b_start + k) * HD;
+    }
+  };
+  // one tile's loads: the value rows to LDS (instruction ch fills rows RPI*ch .. RPI*ch +
+  // RPI-1, 1 KB), the key rows to registers (lane (m, g4): features 32ks + 8g4 .. of key
+  // kt0 + 16kb + m) and the slot biases of the lane's score rows (keys kt0 + 16kb + 4g4 + i)
+  uint16_t* vbuf = sm.u.vrow[wave];
+  u16x8 ka[2][NKS];
+  float bb[2][4];
+  auto load_tile = [&](int j) {
+    const int kt0 = 32 * j;
+#pragma unroll
+    for (int ch = 0; ch < 32 / RPI; ++ch) {
+      const int r = RPI * ch + lane / NP, piece = (lane % NP) ^ (r % NP);
+      const uint16_t* kp;
+      const uint16_t* vp;
+      int sl;
+      key_rows(kt0 + r, kp, vp, sl);
+      dec_dma16(vp + 8 * piece, vbuf + ch * 512);
+    }
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      const uint16_t* kp;
+      const uint16_t* vp;
+      int sl;
+      key_rows(kt0 + 16 * kb + m, kp, vp, sl);
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) ka[kb][ks] = *reinterpret_cast<const u16x8*>(kp + 32 * ks + 8 * g4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        key_rows(kt0 + 16 * kb + 4 * g4 + i, kp, vp, sl);
+        bb[kb][i] = sl >= 0 ? a.slot_bias[(long long)bh * a.S + sl] : 0.f;
       }
-    };
+    }
+  };
+  // attention wavefronts: the first tile goes out before the head preparation is waited for;
+  // readout wavefronts: the head preparation of the new token into LDS and the window ring
+  if (wave < ADW) {
+    if (wave < ntile) load_tile(wave);
+  } else {
+    const PrepOut<uint16_t> po{&sm.qrope[0][0], &sm.qhat[0][0], sm.stat, sm.newk, sm.newv};
+    prep_token<uint16_t, HD>(a, lp, bh, tid - 64 * ADW, po);
+  }
+  __syncthreads();   // the prepared token is in LDS
+  if (wave < ADW) {
     // queries as the B operand: lane (head m, group g4) holds features 32ks + 8g4 .. of head m
     u16x8 qb[NKS];
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) {
-      if (m < G) qb[ks] = *reinterpret_cast<const u16x8*>(q_rope + m * HD + 32 * ks + 8 * g4);
+      if (m < G) qb[ks] = *reinterpret_cast<const u16x8*>(&sm.qrope[m][32 * ks + 8 * g4]);
       else qb[ks] = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
     }
     const float scale = 1.0f / sqrtf((float)HD);
-    uint16_t* vbuf = sm.u.vrow[wave];
     for (int j = wave; j < ntile; j += ADW) {
       const int kt0 = 32 * j;
-      // value rows -> LDS: instruction ch fills rows RPI*ch .. RPI*ch + RPI-1 (1 KB)
+      if (j != wave) load_tile(j);
+      // the new token (key nk - 1) was read from the ring before it was written there: its
+      // key row comes from LDS instead (its value row below)
+      const int r_new = nk - 1 - kt0;
+      if (r_new < 32) {
 #pragma unroll
-      for (int ch = 0; ch < 32 / RPI; ++ch) {
-        const int r = RPI * ch + lane / NP, piece = (lane % NP) ^ (r % NP);
-        const uint16_t* kp;
-        const uint16_t* vp;
-        int sl;
-        key_rows(kt0 + r, kp, vp, sl);
-        dec_dma16(vp + 8 * piece, vbuf + ch * 512);
-      }
-      // key rows -> registers: lane (m, g4) holds features 32ks + 8g4 .. of key kt0 + 16kb + m;
-      // slot biases of the lane's score rows (keys kt0 + 16kb + 4g4 + i)
-      u16x8 ka[2][NKS];
-      float bb[2][4];
+        for (int kb = 0; kb < 2; ++kb)
+          if (16 * kb + m == r_new)
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const uint16_t* kp;
-        const uint16_t* vp;
-        int sl;
-        key_rows(kt0 + 16 * kb + m, kp, vp, sl);
-#pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) ka[kb][ks] = *reinterpret_cast<const u16x8*>(kp + 32 * ks + 8 * g4);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          key_rows(kt0 + 16 * kb + 4 * g4 + i, kp, vp, sl);
-          bb[kb][i] = sl >= 0 ? a.slot_bias[(long long)bh * a.S + sl] : 0.f;
-        }
+            for (int ks = 0; ks < NKS; ++ks) ka[kb][ks] = *reinterpret_cast<const u16x8*>(&sm.newk[32 * ks + 8 * g4]);
       }
       f32x4 sc[2];
 #pragma unroll
@@ -703,6 +753,9 @@ __global__ void __launch_bounds__(ANT, 4) decode_attn_kernel(b3_decode_args a) {
       mx = nmx;
       // every load of the tile (the value rows in LDS included) has landed
       wait_vm<0>();
+      if (r_new < 32 && lane < NP)
+        *reinterpret_cast<u16x8*>(vbuf + r_new * HD + 8 * (lane ^ (r_new % NP))) =
+            *reinterpret_cast<const u16x8*>(&sm.newv[8 * lane]);
       const int s = lane & 15;
 #pragma unroll
       for (int db = 0; db < NDB; ++db) {
@@ -719,27 +772,33 @@ __global__ void __launch_bounds__(ANT, 4) decode_attn_kernel(b3_decode_args a) {
         mma16_bf16(o[db], av, pb);
       }
     }
-  } else if (a.m_res) {
+  }
+  if (wave >= ADW && a.m_res) {
     // r^T[d][g] = sum over the wavefront's rows c of M[c][d] q^[g][c]: 16x16x4 fp32 MFMAs,
     // lane (l % 16, l / 16) loads A = M[c0 + l/16][d0 + l%16] and B = q^[l%16][c0 + l/16]
-    constexpr int RR = HD / ARW, NCS = RR / 4, NDT = HD / 16;
+    constexpr int RR = HD / ARW, NDT = HD / 16;
+    constexpr int NCS = RR / 4 < 8 ? RR / 4 : 8;   // K steps of 4 rows per pass (register budget)
+    constexpr int NPASS = RR / (4 * NCS);
     const int q = wave - ADW;
     const int r16 = lane & 15, k4 = lane >> 4;
-    const float* M = a.m_res + (long long)bh * HD * HD + (long long)(q * RR + k4) * HD + r16;
-    float ma[NCS][NDT];
 #pragma unroll
-    for (int cs = 0; cs < NCS; ++cs)
+    for (int dt = 0; dt < NDT; ++dt) rdv[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) ma[cs][dt] = M[(long long)(4 * cs) * HD + 16 * dt];
-    float qv[NCS];
+    for (int ps = 0; ps < NPASS; ++ps) {
+      const int c0 = q * RR + 4 * NCS * ps;
+      const float* M = a.m_res + (long long)bh * HD * HD + (long long)(c0 + k4) * HD + r16;
+      float ma[NCS][NDT];
 #pragma unroll
-    for (int cs = 0; cs < NCS; ++cs) qv[cs] = r16 < G ? q_raw[r16 * HD + q * RR + 4 * cs + k4] : 0.f;
+      for (int cs = 0; cs < NCS; ++cs)
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
-      f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int dt = 0; dt < NDT; ++dt) ma[cs][dt] = M[(long long)(4 * cs) * HD + 16 * dt];
+      float qv[NCS];
 #pragma unroll
-      for (int cs = 0; cs < NCS; ++cs) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ma[cs][dt], qv[cs], acc, 0, 0, 0);
-      rdv[dt] = acc;
+      for (int cs = 0; cs < NCS; ++cs) qv[cs] = r16 < G ? sm.qhat[r16][c0 + 4 * cs + k4] : 0.f;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int cs = 0; cs < NCS; ++cs) rdv[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(ma[cs][dt], qv[cs], rdv[dt], 0, 0, 0);
     }
   }
   __syncthreads();   // every wavefront is done with its value tiles (the union is reused below)
@@ -797,7 +856,7 @@ __global__ void __launch_bounds__(ANT, 4) decode_attn_kernel(b3_decode_args a) {
       float r = 0.f;
 #pragma unroll
       for (int w = 0; w < ARW; ++w) r += sm.u.mg.rd[w][g][d];
-      ym[qq] = mul_rn(r * c_iq[qq], coef);
+      ym[qq] = mul_rn(r * sm.stat[2 * g], coef);
     }
   }
   // mean square of ym per head: wavefront sums, then across wavefronts
@@ -826,7 +885,7 @@ __global__ void __launch_bounds__(ANT, 4) decode_attn_kernel(b3_decode_args a) {
       for (int w = 0; w < ANT / 64; ++w) ss += sm.red[g][w];
       const float rs = 1.0f / sqrtf(div_rn(ss, (float)HD) + a.eps);
       const float ymn = mul_rn(mul_rn(ym[qq], rs), c_rw[qq]);
-      const float rd = a.m_res ? round_bf(mul_rn(c_eta[qq], ymn)) : 0.f;
+      const float rd = a.m_res ? round_bf(mul_rn(sm.stat[2 * g + 1], ymn)) : 0.f;
       y[it] = f2bf(round_bf(add_rn(att[qq], rd)));
     }
   }
@@ -942,12 +1001,12 @@ template <typename T, int HD>
 static int launch_decode(const b3_decode_args& a, hipStream_t st, LinParts lp) {
   const int BH = a.B * a.HKV;
   const int nk = a.n_sink_keys + (a.has_slots ? a.S : 0) + a.a_len + a.b_len + 1;
-  hipLaunchKernelGGL((decode_prep_kernel<T, HD>), dim3(BH), dim3(128), 0, st, a, lp);
-  hipError_t e0 = hipGetLastError();
-  if (e0 != hipSuccess) return (int)e0;
   if constexpr (St<T>::is_bf16) {
-    hipLaunchKernelGGL((decode_attn_kernel<HD>), dim3(BH), dim3(ANT), 0, st, a);
+    hipLaunchKernelGGL((decode_attn_kernel<HD>), dim3(BH), dim3(ANT), 0, st, a, lp);
   } else {
+    hipLaunchKernelGGL((decode_prep_kernel<T, HD>), dim3(BH), dim3(128), 0, st, a, lp);
+    hipError_t e0 = hipGetLastError();
+    if (e0 != hipSuccess) return (int)e0;
     hipLaunchKernelGGL((decode_split_kernel<T, HD>), dim3(dec_nsplit(nk) + HD / RROWS, BH), dim3(DNT), 0, st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;

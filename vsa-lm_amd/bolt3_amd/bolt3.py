@@ -48,17 +48,17 @@ def _side_stream(dev: torch.device, i: int = 0) -> torch.cuda.Stream:
 
 # The forward's consolidation steps are issued in this many groups, so that the slot field and
 # readout of early chunks run while the chain still decides later steps.
-CHAIN_GROUPS = 4
+CHAIN_GROUPS = 3
 
 
 def _step_groups(n: int, k: int) -> list[tuple[int, int]]:
-    """Split steps [0, n) into at most k contiguous ranges: a short first one (about n / (2k - 2)
-    steps, so that the attention can start while the q projection finishes), the rest nearly
-    equal."""
+    """Split steps [0, n) into at most k contiguous ranges: a short first one (about
+    n / (2k - 2) + 1 steps, so that the attention starts soon after the q projection, which
+    runs beside it), the rest nearly equal."""
     k = max(1, min(k, n))
     if k == 1:
         return [(0, n)]
-    first = max(1, n // (2 * k - 2))
+    first = min(n - k + 1, max(1, (n + 1) // (2 * k - 2) + 1))
     rest = n - first
     bounds = [0, first] + [first + rest * i // (k - 1) for i in range(1, k)]
     return [(bounds[i], bounds[i + 1]) for i in range(k) if bounds[i + 1] > bounds[i]]
@@ -267,12 +267,11 @@ class Bolt3Attn(nn.Module):
         gam = side["gamma"]
         main = torch.cuda.current_stream(dev)
         # k | v and the gates first: the consolidation chain needs only k, v and beta, so it runs
-        # on a side stream while the q head preparation and the attention proceed on this one.
-        # The q projection comes before the chain starts: the slot decisions are latency-bound
-        # and a large GEMM beside them slows them several-fold.
+        # on side streams while the q projection, the q head preparation and the attention
+        # proceed on this one.  The q projection slows the latency-bound slot decisions of the
+        # first step group beside it, which the overlap more than pays for.
         lin_kv = F.linear(x, side["wkv"], side["bkv"])
         gates = F.linear(x, side["wg"], side["bg"])
-        lin_q = F.linear(x, side["wq"], side["bq"])
         k_raw = torch.empty(b, HKV, T, HD, dtype=dt, device=dev)
         k_rope, v = torch.empty_like(k_raw), torch.empty_like(k_raw)
         beta = torch.empty(b, HKV, T, device=dev)
@@ -337,6 +336,7 @@ class Bolt3Attn(nn.Module):
             if trace is not None:
                 trace.update(state=st, m_res=m_res, snap_k=snaps[0], snap_v=snaps[1], snap_bias=snaps[2],
                              snap_m=snaps[3], log=log)
+        lin_q = F.linear(x, side["wq"], side["bq"])
         q_raw = torch.empty(b, H, T, HD, dtype=dt, device=dev)
         q_rope = torch.empty_like(q_raw)
         eta = torch.empty(b, H, T, device=dev)

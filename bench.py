@@ -161,14 +161,16 @@ def bench_decode(dev, n_sets, n_steps, prefill_tokens=8192, batch=64):
 
 
 def measured_traffic(entry: str):
-    """HBM bytes per launch of an entry point from the rocprofv3 PMC summary committed under
-    profiles/ (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel calibration), or None."""
+    """HBM bytes of an entry point from the rocprofv3 PMC summary committed under profiles/
+    (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel calibration): per forward for the
+    prefill entry points (the unit of their roofline), per launch for the decode entry point;
+    None when absent."""
     f = os.path.join(REPO, "profiles", "pmc_traffic.json")
     if not os.path.exists(f):
         return None
     with open(f) as fh:
         rec = json.load(fh).get(entry)
-    return None if rec is None else rec.get("bytes_per_launch")
+    return None if rec is None else rec.get("bytes_per_forward", rec.get("bytes_per_launch"))
 
 
 def cpu_baseline(min_s=10.0, max_s=30.0):

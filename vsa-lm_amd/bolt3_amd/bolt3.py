@@ -53,12 +53,12 @@ CHAIN_GROUPS = 3
 
 def _step_groups(n: int, k: int) -> list[tuple[int, int]]:
     """Split steps [0, n) into at most k contiguous ranges: a short first one (about
-    n / (2k - 2) + 1 steps, so that the attention starts soon after the q projection, which
-    runs beside it), the rest nearly equal."""
+    n / (2k - 2) + 1 steps and at most n / k, so that the attention starts soon after the q
+    projection, which runs beside it), the rest nearly equal."""
     k = max(1, min(k, n))
     if k == 1:
         return [(0, n)]
-    first = min(n - k + 1, max(1, (n + 1) // (2 * k - 2) + 1))
+    first = max(1, min(n // k, (n + 1) // (2 * k - 2) + 1))
     rest = n - first
     bounds = [0, first] + [first + rest * i // (k - 1) for i in range(1, k)]
     return [(bounds[i], bounds[i + 1]) for i in range(k) if bounds[i + 1] > bounds[i]]

@@ -160,6 +160,39 @@ def bench_decode(dev, n_sets, n_steps, prefill_tokens=8192, batch=64):
     )
 
 
+def bench_long(dev, reps=3, T_long=65536):
+    """The consolidation-heavy configuration: B=1, T=65536, Qwen3-4B layer (bf16 projections,
+    fp32 Bolt-3 params), hidden states around 512 centres with noise 0.15 and Zipf(1.1)
+    cluster choice, so that many tokens merge; 510 consolidation steps per forward."""
+    import torch
+    import recipes
+    from bolt3_amd import _abi
+    mod = build_layer(dev)[1]
+    x = recipes.clustered_hidden(SEED + 2, 1, T_long, CFG["dim"], n_centres=512, noise=0.15).to(torch.bfloat16).to(dev)
+    with torch.no_grad():
+        trace = {}
+        mod(x, _trace=trace)                                # warm-up, and the decision log
+        steady = trace["log"][4:, :, :, :128]
+        merged, to_m = float(steady[:, :, 5].mean()), float(steady[:, :, 6].mean())
+        del trace
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            mod(x)
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / reps
+        _abi.set_timing(True)
+        mod(x)
+        kt = _abi.timings()
+        _abi.set_timing(False)
+    n_steps = T_long // mod.C - 2
+    chain_ms = sum(kt.get("bolt3_chain", []))
+    return dict(batch=1, seq_len=T_long, consolidation_steps=n_steps, ms_per_forward=round(ms, 3),
+                tokens_per_s=round(T_long / (ms * 1e-3), 1), chain_ms_per_forward=round(chain_ms, 3),
+                merged_share=round(merged, 3), m_res_share=round(to_m, 3),
+                data="synthetic clustered hidden states (512 centres, noise 0.15, Zipf 1.1)")
+
+
 def measured_traffic(entry: str):
     """HBM bytes of an entry point from the rocprofv3 PMC summary committed under profiles/
     (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel calibration): per forward for the
@@ -210,6 +243,7 @@ def main():
     ap.add_argument("--decode-steps", type=int, default=256)
     ap.add_argument("--decode-sets", type=int, default=4)
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-long", action="store_true", help="skip the consolidation-heavy B=1, T=65536 forward")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run a plain elementwise copy of 256 MiB (fp32 negate) three times, the known-size "
@@ -284,6 +318,8 @@ def main():
     }
     if not args.no_decode:
         out["decode"] = bench_decode(dev, args.decode_sets, args.decode_steps)
+    if not args.no_long:
+        out["long_prefill"] = bench_long(dev)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out))

@@ -414,3 +414,42 @@ def test_full_size_prefix_consistency(gpu):
     with torch.no_grad():
         y_ref = O.forward(O.Bolt3Params.from_module(mod), x[:1, :1024], ties="index")
     _check_out(y_pre.cpu(), y_ref, torch.bfloat16, "cfg2 prefix vs oracle")
+
+
+def test_consolidation_heavy_long_prefill(gpu):
+    """The consolidation-heavy configuration at full size (B=1, T=65536, Qwen3-4B layer, bf16
+    projections, fp32 Bolt-3 parameters; hidden states around 512 centres with noise 0.15 and
+    Zipf(1.1) cluster choice): 510 consolidation steps.  Checked: finite output; a steady share
+    of merges in the decision log (the configuration exists to exercise them); the first 2048
+    tokens do not depend on what follows; the first two chunks (before any consolidation)
+    equal the oracle.  Clustered keys put many tokens within rounding of the merge thresholds
+    and make fill scores tie exactly, so once slots are in play the GPU's bf16 projections
+    (summed in another order than the CPU's) may take the other side of a near-tie and the
+    trajectories part; the decisions themselves are checked step by step, from the oracle's
+    state, by the teacher-forced tests above."""
+    from bolt3_amd import Bolt3Attn
+    import recipes
+    cfg = dict(dim=2560, num_heads=32, num_kv_heads=8, head_dim=128, rope_theta=1e6, eps=1e-6, qk_norm=True)
+    mod = recipes.init_module(Bolt3Attn(cfg), 31, nondefault=False)
+    for n, prm in mod.named_parameters():
+        if "proj" in n and not n.startswith(("beta", "eta")) or "norm" in n and not n.startswith("res"):
+            prm.data = prm.data.to(torch.bfloat16)
+    print("[case] consolidation-heavy prefill B=1 T=65536 bf16", flush=True)
+    x = recipes.clustered_hidden(31, 1, 65536, 2560, n_centres=512, noise=0.15).to(torch.bfloat16)
+    mod_d = __import__("copy").deepcopy(mod).to(gpu)
+    trace = {}
+    with torch.no_grad():
+        y = mod_d(x.to(gpu), _trace=trace)
+        y_pre = mod_d(x[:, :2048].to(gpu))
+    assert torch.isfinite(y).all()
+    log = trace["log"]                       # [steps, bh, rows, cols]; rows 5 / 6: merged / to M_res
+    steady = log[4:, :, :, :128]             # the slots are full after the first steps
+    merged = float(steady[:, :, 5].mean())
+    to_m = float(steady[:, :, 6].mean())
+    print(f"[case] merged share {merged:.3f}, M_res share {to_m:.3f} over {steady.shape[0]} steady steps", flush=True)
+    assert 0.05 <= merged <= 0.95 and to_m > 0.0
+    ma, cs = max_abs(y[:, :2048].cpu(), y_pre.cpu()), cosine(y[:, :2048].cpu(), y_pre.cpu())
+    assert ma <= 2e-2 and cs >= 0.9995, (ma, cs)
+    with torch.no_grad():
+        y_ref = O.forward(O.Bolt3Params.from_module(mod), x[:, :256], ties="index")
+    _check_out(y_pre[:, :256].cpu(), y_ref, torch.bfloat16, "consolidation-heavy first chunks vs oracle")

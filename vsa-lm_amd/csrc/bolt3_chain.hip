@@ -105,7 +105,12 @@ struct DecSmem {
       float xbv[NP][2][BF ? 1 : 32];
       int xbs[NP][2][BF ? 1 : 32];
     } sc;
-    struct { int cnt[S], off[S], hits[S], mlist[LMAX]; float psum[S]; int nhit; } mg;
+    struct {
+      int cnt[S], off[S], hits[S], mlist[LMAX];
+      float psum[S], pos[LMAX];
+      unsigned bits[S][LMAX / 32];   // bit j of row s: token j merges into slot s
+      int nhit;
+    } mg;
     struct { float mx[2][S]; int nan[2][S]; } kp;
     struct { alignas(16) uint64_t a[LMAX]; alignas(16) uint64_t b[S]; } ok;
   } u;
@@ -1060,44 +1065,103 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
       const int any_merge = sm.any_merge;
       // ---------------- merge: per-slot mass-weighted means, tokens in ascending order
       if (any_merge) {
+        // which tokens merge into which slot, as a bitmap [slot][token]; the positions to LDS
+        constexpr int LW = LMAX / 32;
+        for (int i = tid; i < S * LW; i += DT) (&sm.u.mg.bits[0][0])[i] = 0u;
+        if (tid < l) sm.u.mg.pos[tid] = pos[tid];
+        sync_lds();
+        if (tid < l && (sm.flags[tid] & F_MERGE)) atomicOr(&sm.u.mg.bits[sm.slot[tid]][tid >> 5], 1u << (tid & 31));
+        sync_lds();
+        // per slot: count and position sum, its tokens in ascending order
         if (tid < S) {
           int c = 0;
           float ps = 0.f;
-          for (int j = 0; j < l; ++j)
-            if ((sm.flags[j] & F_MERGE) && sm.slot[j] == tid) { ++c; ps += pos[j]; }
+#pragma unroll
+          for (int w = 0; w < LW; ++w) {
+            unsigned m = sm.u.mg.bits[tid][w];
+            while (m) {
+              const int j = 32 * w + __builtin_ctz(m);
+              m &= m - 1;
+              ++c;
+              ps += sm.u.mg.pos[j];
+            }
+          }
           sm.u.mg.cnt[tid] = c;
           sm.u.mg.psum[tid] = ps;
         }
         sync_lds();
-        if (tid == 0) {
-          int o = 0, nh = 0;
-          for (int s = 0; s < S; ++s) {
-            sm.u.mg.off[s] = o;
-            o += sm.u.mg.cnt[s];
-            if (sm.u.mg.cnt[s] > 0) sm.u.mg.hits[nh++] = s;
+        // slot offsets (exclusive prefix of the counts) and the hit slots in ascending order, by
+        // wavefront 0 with two slots per lane
+        static_assert(S == 2 * WAVE, "two slots per lane");
+        if (wave == 0) {
+          const int c0 = sm.u.mg.cnt[2 * lane], c1 = sm.u.mg.cnt[2 * lane + 1];
+          const int hh = (c0 > 0 ? 1 : 0) + (c1 > 0 ? 1 : 0);
+          int ic = c0 + c1, ih = hh;   // inclusive prefix sums over the lanes
+#pragma unroll
+          for (int o = 1; o < WAVE; o <<= 1) {
+            const int tc = __shfl_up(ic, o, WAVE), th = __shfl_up(ih, o, WAVE);
+            if (lane >= o) {
+              ic += tc;
+              ih += th;
+            }
           }
-          sm.u.mg.nhit = nh;
+          const int ec = ic - c0 - c1;
+          int k = ih - hh;
+          sm.u.mg.off[2 * lane] = ec;
+          sm.u.mg.off[2 * lane + 1] = ec + c0;
+          if (c0 > 0) sm.u.mg.hits[k++] = 2 * lane;
+          if (c1 > 0) sm.u.mg.hits[k] = 2 * lane + 1;
+          if (lane == WAVE - 1) sm.u.mg.nhit = ih;
         }
         sync_lds();
         const int nhit = sm.u.mg.nhit;
-        if (tid < l && (sm.flags[tid] & F_MERGE)) {
-          const int s = sm.slot[tid];
-          int rank = 0;
-          for (int j = 0; j < tid; ++j) rank += ((sm.flags[j] & F_MERGE) && sm.slot[j] == s) ? 1 : 0;
-          sm.u.mg.mlist[sm.u.mg.off[s] + rank] = tid;
+        // the merged tokens of each slot at its offset, in ascending order
+        if (tid < S && sm.u.mg.cnt[tid] > 0) {
+          int k = sm.u.mg.off[tid];
+#pragma unroll
+          for (int w = 0; w < LW; ++w) {
+            unsigned m = sm.u.mg.bits[tid][w];
+            while (m) {
+              sm.u.mg.mlist[k++] = 32 * w + __builtin_ctz(m);
+              m &= m - 1;
+            }
+          }
         }
         sync_lds();
-        for (int it = tid; it < nhit * HD; it += DT) {
-          const int s = sm.u.mg.hits[it / HD], d = it % HD;
-          float ks = 0.f, vs = 0.f;
-          for (int q = 0; q < sm.u.mg.cnt[s]; ++q) {
-            const int j = sm.u.mg.mlist[sm.u.mg.off[s] + q];
-            ks += St<T>::ld(kr + (long long)j * HD + d);
-            vs += St<T>::ld(v + (long long)j * HD + d);
+        // one thread per (hit slot, 8 features): the merged rows in ascending token order, four
+        // tokens' loads in flight at a time
+        constexpr int NC8 = HD / 8;
+        for (int it = tid; it < nhit * NC8; it += DT) {
+          const int s = sm.u.mg.hits[it / NC8], d0 = 8 * (it % NC8);
+          const int cnt = sm.u.mg.cnt[s], o0 = sm.u.mg.off[s];
+          float ks[8], vs[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) ks[e] = vs[e] = 0.f;
+          for (int q0 = 0; q0 < cnt; q0 += 4) {
+            Vec8<T> kx[4], vx[4];   // rows kept in the storage dtype until they are added
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+              if (q0 + u < cnt) {
+                const int j = sm.u.mg.mlist[o0 + q0 + u];
+                kx[u].load(kr + (long long)j * HD + d0);
+                vx[u].load(v + (long long)j * HD + d0);
+              }
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+              if (q0 + u < cnt)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                  ks[e] += kx[u].get(e);
+                  vs[e] += vx[u].get(e);
+                }
           }
-          const float m0 = sm.mass[s], nm = add_rn(m0, (float)sm.u.mg.cnt[s]);
-          sm.ak[s * KS + d] = St<T>::from_f(div_rn(add_rn(mul_rn(m0, St<T>::to_f(sm.ak[s * KS + d])), ks), nm));
-          sm.av[s * KS + d] = St<T>::from_f(div_rn(add_rn(mul_rn(m0, St<T>::to_f(sm.av[s * KS + d])), vs), nm));
+          const float m0 = sm.mass[s], nm = add_rn(m0, (float)cnt);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const int d = d0 + e;
+            sm.ak[s * KS + d] = St<T>::from_f(div_rn(add_rn(mul_rn(m0, St<T>::to_f(sm.ak[s * KS + d])), ks[e]), nm));
+            sm.av[s * KS + d] = St<T>::from_f(div_rn(add_rn(mul_rn(m0, St<T>::to_f(sm.av[s * KS + d])), vs[e]), nm));
+          }
         }
         sync_lds();
         if (tid < S && sm.u.mg.cnt[tid] > 0) {

@@ -291,9 +291,32 @@ __device__ void rope_dirty(DecSmem<T, HD>& sm, T* kread_g, int tid) {
   constexpr int HALF = HD / 2, P8 = HALF / 8;
   T* dst = sm.KREAD_LDS ? sm.kread : kread_g;
   const int rs = sm.KREAD_LDS ? sm.KS : HD;
-  for (int it = tid; it < S * P8; it += DT) {
-    const int s = it / P8, i0 = (it % P8) * 8;
-    if (!sm.dirty[s]) continue;
+  // the changed slots, found by every wavefront from two ballots (no barrier): item it takes
+  // the (it / P8)-th changed slot in ascending order, so that the rows spread over every thread
+  static_assert(S == 2 * WAVE, "two ballots of slots");
+  const int lane = tid & (WAVE - 1);
+  const unsigned long long m0 = __ballot(sm.dirty[lane] != 0), m1 = __ballot(sm.dirty[WAVE + lane] != 0);
+  const int n0 = __popcll(m0);
+  const int nd = n0 + __popcll(m1);
+  for (int it = tid; it < nd * P8; it += DT) {
+    int k = it / P8;
+    unsigned long long m = k < n0 ? m0 : m1;
+    int base = k < n0 ? 0 : WAVE;
+    if (k >= n0) k -= n0;
+    // position of the k-th set bit of m (k < popcount(m)) by halving
+#pragma unroll
+    for (int w = 32; w >= 1; w >>= 1) {
+      const unsigned long long lo = m & ((1ull << w) - 1);
+      const int c = __popcll(lo);
+      if (k >= c) {
+        k -= c;
+        m >>= w;
+        base += w;
+      } else {
+        m = lo;
+      }
+    }
+    const int s = base, i0 = (it % P8) * 8;
     float x0[8], x1[8];
     ld8(&sm.ak[s * sm.KS + i0], x0);
     ld8(&sm.ak[s * sm.KS + i0 + HALF], x1);

@@ -11,7 +11,7 @@ import pytest
 import torch
 
 from bolt3_amd import Bolt3Attn
-from bolt3_amd.bolt3 import _step_groups
+from bolt3_amd.bolt3 import _n_groups, _step_groups
 
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 CFG = dict(dim=64, num_heads=4, num_kv_heads=2, head_dim=16, rope_theta=1e4, eps=1e-6, qk_norm=True)
@@ -34,7 +34,12 @@ def test_step_groups_cover_the_steps_in_order(n, k):
 
 def test_step_groups_of_the_benchmark_forward():
     # cfg2: T = 4096, C = 128 -> 30 consolidation steps, three groups
+    assert _n_groups(30) == 3
     assert _step_groups(30, 3) == [(0, 8), (8, 19), (19, 30)]
+    # the consolidation-heavy configuration: T = 65536 -> 510 steps in 16 groups of about 32
+    assert _n_groups(510) == 16
+    g = _step_groups(510, 16)
+    assert len(g) == 16 and max(s1 - s0 for s0, s1 in g) <= 33
 
 
 def test_packed_parameters_follow_in_place_updates():

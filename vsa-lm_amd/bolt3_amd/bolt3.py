@@ -49,6 +49,13 @@ def _side_stream(dev: torch.device, i: int = 0) -> torch.cuda.Stream:
 # The forward's consolidation steps are issued in this many groups, so that the slot field and
 # readout of early chunks run while the chain still decides later steps.
 CHAIN_GROUPS = 3
+# ... and at least one group per this many steps, so that the work left after the last group's
+# slot decisions (its M_res updates, attention and o_proj) stays short on long sequences
+GROUP_STEPS = 32
+
+
+def _n_groups(n_steps: int) -> int:
+    return max(CHAIN_GROUPS, round(n_steps / GROUP_STEPS))
 
 
 def _step_groups(n: int, k: int) -> list[tuple[int, int]]:
@@ -287,7 +294,7 @@ class Bolt3Attn(nn.Module):
         # bf16: the chain's steps go out in groups; the slot decisions of a group run on one side
         # stream, its Gershgorin scales and M_res updates on another, and the main stream adds the
         # slot field and readout of a group's chunks as soon as that group is done
-        groups = _step_groups(n_cons, CHAIN_GROUPS if split else 1) if n_cons > 0 else []
+        groups = _step_groups(n_cons, _n_groups(n_cons) if split else 1) if n_cons > 0 else []
         done = []   # per group: event after its M_res updates
         if n_cons > 0:
             s_dec = _side_stream(dev, 0)

@@ -127,6 +127,9 @@ typedef struct {
      decided.  Phase 2 may run concurrently with the phase-1 call of the next steps when that call
      uses another `work` buffer. */
   int32_t phase;
+  /* optional (NULL to skip): each slot-decision workgroup adds 1 to *started when it begins, so
+     that bolt3_wait_count can hold another stream until all B*HKV of them hold a compute unit */
+  uint32_t* started;
 } b3_chain_args;
 
 /*
@@ -144,6 +147,17 @@ int bolt3_chain(const b3_chain_args* a, void* stream);
    scales (3 x n_steps x B*HKV x 256 floats) plus, for fp32 storage with HD == 128, the roped
    slot keys (B*HKV x S x HD floats). */
 int64_t bolt3_chain_workspace_bytes(int32_t dtype, int32_t B, int32_t HKV, int32_t HD, int32_t S, int32_t n_steps);
+
+/*
+ * Holds `stream` until *counter has reached `target` (compared modulo 2^32) or after max_polls
+ * polls of about 0.2 us each, whichever comes first.  No counterpart in the reference (its chain
+ * is serial host code): the forward launches the slot decisions (one workgroup per bh, each with
+ * the whole LDS of a compute unit) on a side stream and calls this on its main stream, with
+ * `counter` = b3_chain_args.started, before a full-chip GEMM, so that the GEMM's workgroups cannot
+ * take every compute unit first and leave the slot decisions waiting for the GEMM's end.  One
+ * 64-thread workgroup; counter is device memory.
+ */
+int bolt3_wait_count(const uint32_t* counter, uint32_t target, int32_t max_polls, void* stream);
 
 typedef struct {
   int32_t dtype, B, H, HKV, HD, S, C, n_sinks;

@@ -65,6 +65,7 @@ def test_rejects_bad_arguments_without_gpu_work():
     assert lib.bolt3_decode_layer(ctypes.byref(la), None) == 1002   # fp32: the unfused step only
     la.dec.dtype = 1
     assert lib.bolt3_decode_layer(ctypes.byref(la), None) == 1001
+    assert lib.bolt3_wait_count(None, 1, 10, None) == 1001
 
 
 STRUCTS = {"b3_heads_args": A.HeadsArgs, "b3_chain_args": A.ChainArgs, "b3_attn_args": A.AttnArgs,

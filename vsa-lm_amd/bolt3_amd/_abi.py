@@ -54,7 +54,7 @@ class ChainArgs(C.Structure):
         ("ak", p), ("av", p), ("mass", p), ("util", p), ("pm", p), ("act", p), ("m_res", p),
         ("kappa", p), ("gamma", p), ("inv_freq", p),
         ("snap_k", p), ("snap_v", p), ("snap_bias", p), ("snap_m", p), ("log", p),
-        ("work", p), ("work_bytes", i64), ("phase", i32),
+        ("work", p), ("work_bytes", i64), ("phase", i32), ("started", p),
     ]
 
 
@@ -99,7 +99,7 @@ class DecodeLayerArgs(C.Structure):
 
 EXPORTS = ("bolt3_heads", "bolt3_chain", "bolt3_chain_workspace_bytes", "bolt3_chunk_attn", "bolt3_decode",
            "bolt3_decode_layer", "bolt3_decode_layer_workspace_bytes", "bolt3_decode_workspace_bytes",
-           "bolt3_version")
+           "bolt3_version", "bolt3_wait_count")
 
 _lib = None
 
@@ -124,6 +124,8 @@ def load():
     lib.bolt3_decode_layer_workspace_bytes.restype = i64
     lib.bolt3_decode_workspace_bytes.argtypes = [i32, i32, i32, i32]
     lib.bolt3_decode_workspace_bytes.restype = i64
+    lib.bolt3_wait_count.argtypes = [p, C.c_uint32, i32, p]
+    lib.bolt3_wait_count.restype = C.c_int
     lib.bolt3_version.argtypes = []
     lib.bolt3_version.restype = C.c_char_p
     _lib = lib

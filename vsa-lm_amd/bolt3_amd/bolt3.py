@@ -35,6 +35,14 @@ def _require_gpu(t: torch.Tensor, what: str):
 
 
 _SIDE_STREAMS: dict = {}
+_N_CUS: dict = {}
+
+
+def _n_cus(dev: torch.device) -> int:
+    key = dev.index if dev.index is not None else torch.cuda.current_device()
+    if key not in _N_CUS:
+        _N_CUS[key] = torch.cuda.get_device_properties(key).multi_processor_count
+    return _N_CUS[key]
 
 
 def _side_stream(dev: torch.device, i: int = 0) -> torch.cuda.Stream:
@@ -44,6 +52,27 @@ def _side_stream(dev: torch.device, i: int = 0) -> torch.cuda.Stream:
     if key not in _SIDE_STREAMS:
         _SIDE_STREAMS[key] = torch.cuda.Stream(device=dev)
     return _SIDE_STREAMS[key]
+
+
+# Per device: a counter that the slot-decision workgroups of the forward's first step group bump
+# when they start, and the number of bumps issued so far.  The main stream waits on it
+# (bolt3_wait_count) before the q projection, so that those workgroups, each needing a whole
+# compute unit's LDS, are resident first instead of waiting for the GEMM's end.
+_STARTED: dict = {}
+WAIT_POLLS = 20000
+
+
+def _started_counter(dev: torch.device) -> list:
+    key = dev.index if dev.index is not None else torch.cuda.current_device()
+    if key not in _STARTED:
+        _STARTED[key] = [torch.zeros(1, dtype=torch.int32, device=dev), 0]
+    return _STARTED[key]
+
+
+def _wait_started(dev: torch.device, counter: torch.Tensor, target: int) -> None:
+    rc = A.load().bolt3_wait_count(counter.data_ptr(), target & 0xFFFFFFFF, WAIT_POLLS, A.stream_of(dev))
+    if rc != 0:
+        raise RuntimeError(f"bolt3_wait_count failed with code {rc}")
 
 
 # The forward's consolidation steps are issued in this many groups, so that the slot field and
@@ -225,7 +254,7 @@ class Bolt3Attn(nn.Module):
 
     def _chain(self, dt, device, B, kr, kp, v, tok_bh_stride, pos, beta, beta_bh_stride, n_steps, off0, len0,
                step_stride, step_len, n_filled, st: dict, m_res, gam, side, snap_k=None, snap_v=None,
-               snap_bias=None, snap_m=None, log=None, kp_exact=False, phase=0, work=None):
+               snap_bias=None, snap_m=None, log=None, kp_exact=False, phase=0, work=None, started=None):
         if work is None:
             work = torch.empty(A.chain_workspace_bytes(dt, B, self.HKV, self.HD, self.S, n_steps),
                                dtype=torch.uint8, device=device)
@@ -242,7 +271,7 @@ class Bolt3Attn(nn.Module):
         a.snap_k, a.snap_v, a.snap_bias, a.snap_m = A.ptr(snap_k), A.ptr(snap_v), A.ptr(snap_bias), A.ptr(snap_m)
         a.log = A.ptr(log)
         a.work, a.work_bytes = work.data_ptr(), work.numel()
-        a.phase = phase
+        a.phase, a.started = phase, started
         A.call("bolt3_chain", a, device)
 
     def _empty_slots(self, bh, dt, device):
@@ -275,8 +304,8 @@ class Bolt3Attn(nn.Module):
         main = torch.cuda.current_stream(dev)
         # k | v and the gates first: the consolidation chain needs only k, v and beta, so it runs
         # on side streams while the q projection, the q head preparation and the attention
-        # proceed on this one.  The q projection slows the latency-bound slot decisions of the
-        # first step group beside it, which the overlap more than pays for.
+        # proceed on this one.  The q projection is issued once the first step group's slot
+        # decisions hold their compute units (bolt3_wait_count) and runs on the rest of the chip.
         lin_kv = F.linear(x, side["wkv"], side["bkv"])
         gates = F.linear(x, side["wg"], side["bg"])
         k_raw = torch.empty(b, HKV, T, HD, dtype=dt, device=dev)
@@ -296,6 +325,10 @@ class Bolt3Attn(nn.Module):
         # slot field and readout of a group's chunks as soon as that group is done
         groups = _step_groups(n_cons, _n_groups(n_cons) if split else 1) if n_cons > 0 else []
         done = []   # per group: event after its M_res updates
+        # the first group's slot decisions hold their compute units before the q projection, a
+        # GEMM whose grid covers the whole chip, is issued: otherwise most of them wait for its end
+        ctr = _started_counter(dev) if split and 2 * b * HKV <= _n_cus(dev) else None
+        first_started = None
         if n_cons > 0:
             s_dec = _side_stream(dev, 0)
             s_m = _side_stream(dev, 1) if split else s_dec
@@ -327,8 +360,12 @@ class Bolt3Attn(nn.Module):
                         *(t[s0:s1] for t in snaps))
                 kw = dict(log=None if log is None else log[s0:s1], kp_exact=True, work=work)
                 if split:
+                    count = ctr is not None and s0 == 0
                     with torch.cuda.stream(s_dec):
-                        self._chain(*args, phase=1, **kw)
+                        self._chain(*args, phase=1, started=ctr[0].data_ptr() if count else None, **kw)
+                    if count:
+                        ctr[1] += bh
+                        first_started = ctr[1]
                     s_m.wait_stream(s_dec)
                     with torch.cuda.stream(s_m):
                         self._chain(*args, phase=2, **kw)
@@ -343,6 +380,8 @@ class Bolt3Attn(nn.Module):
             if trace is not None:
                 trace.update(state=st, m_res=m_res, snap_k=snaps[0], snap_v=snaps[1], snap_bias=snaps[2],
                              snap_m=snaps[3], log=log)
+        if first_started is not None:
+            _wait_started(dev, ctr[0], first_started)
         lin_q = F.linear(x, side["wq"], side["bq"])
         q_raw = torch.empty(b, H, T, HD, dtype=dt, device=dev)
         q_rope = torch.empty_like(q_raw)

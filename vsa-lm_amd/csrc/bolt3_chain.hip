@@ -914,6 +914,7 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
   T* kread_w = sm.KREAD_LDS ? sm.kread : kread_g;   // writable view of the roped slot keys
   const int krs = sm.KREAD_LDS ? KS : HD;
   const bool kp_copy = a.kp_exact != 0;              // a slot taken from token j gets kp_j as its roped key
+  if (a.started && tid == 0) __hip_atomic_fetch_add(a.started, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
   // state in; with n_filled == 0 the empty state (zero slots, mass 1) is built here
   const bool fresh = a.n_filled == 0;
@@ -1789,6 +1790,15 @@ __global__ void __launch_bounds__(MT) mres_kernel(b3_chain_args a) {
   }
 }
 
+// Holds its stream until *counter reaches target (modulo 2^32) or after max_polls polls.
+__global__ void __launch_bounds__(64) wait_count_kernel(const uint32_t* counter, uint32_t target, int max_polls) {
+  for (int i = 0; i < max_polls; ++i) {
+    const uint32_t c = __hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if ((int32_t)(c - target) >= 0) break;
+    __builtin_amdgcn_s_sleep(8);
+  }
+}
+
 template <typename T, int HD>
 static int launch_chain(const b3_chain_args& a, hipStream_t st) {
   const int BH = a.B * a.HKV;
@@ -1812,6 +1822,13 @@ extern "C" int64_t bolt3_chain_workspace_bytes(int32_t dtype, int32_t B, int32_t
   if (dtype == B3_BF16)
     return HD == 64 ? b3::Work<uint16_t, 64>::bytes(bh, n_steps) : b3::Work<uint16_t, 128>::bytes(bh, n_steps);
   return HD == 64 ? b3::Work<float, 64>::bytes(bh, n_steps) : b3::Work<float, 128>::bytes(bh, n_steps);
+}
+
+extern "C" int bolt3_wait_count(const uint32_t* counter, uint32_t target, int32_t max_polls, void* stream) {
+  if (!counter || max_polls < 0) return B3_ERR_ARG;
+  hipLaunchKernelGGL(b3::wait_count_kernel, dim3(1), dim3(64), 0, reinterpret_cast<hipStream_t>(stream), counter,
+                     target, max_polls);
+  return (int)hipGetLastError();
 }
 
 extern "C" int bolt3_chain(const b3_chain_args* a, void* stream) {

@@ -781,6 +781,17 @@ __device__ __forceinline__ float4 lds_read_f4(const float* p) {
   asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(r) : "v"(addr) : "memory");
   return r;
 }
+typedef float fx4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ fx4 lds_read_f4_nowait(const float* p) {
+  fx4 r;
+  const uint32_t addr = (uint32_t)(size_t)((__attribute__((address_space(3))) const float*)p);
+  asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(addr) : "memory");
+  return r;
+}
+// lgkmcnt(0), tied to four 16-byte LDS read results
+__device__ __forceinline__ void lds_wait4(fx4& r0, fx4& r1, fx4& r2, fx4& r3) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(r0), "+v"(r1), "+v"(r2), "+v"(r3));
+}
 // lgkmcnt(0), tied to the transposed-read results so that their users follow it
 __device__ __forceinline__ void lds_wait8(u16x4* r) {
   asm volatile("s_waitcnt lgkmcnt(0)"
@@ -915,7 +926,7 @@ __global__ void __launch_bounds__(64 * NW) attn_fwd2_kernel(b3_attn_args a, int 
   for (int j = 0; j < pre; ++j) issue(j, j);
   bool m_issued = false;
   if (pre == nb && readout) { issue_m(); m_issued = true; }
-  if (tid < 128) lds_write_f32(&sm.sbias[tid], sb);
+  if (tid < 128) lds_write_f32(&sm.sbias[tid], sb * L2E);   // bias in log2 units
 
   f32x16 o[NDB];
 #pragma unroll
@@ -942,18 +953,29 @@ __global__ void __launch_bounds__(64 * NW) attn_fwd2_kernel(b3_attn_args a, int 
     }
     // scores in log2 units: round_bf(q.k) * scale*log2(e) (+ slot bias * log2(e)), one FMA
     if (f.bias) {
+      fx4 b4[4];
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) b4[r4] = lds_read_f4_nowait(f.bias + 8 * r4 + 4 * h);
+      lds_wait4(b4[0], b4[1], b4[2], b4[3]);
 #pragma unroll
       for (int r4 = 0; r4 < 4; ++r4) {
-        const float4 b4 = lds_read_f4(f.bias + 8 * r4 + 4 * h);
-        const float bb[4] = {b4.x * L2E, b4.y * L2E, b4.z * L2E, b4.w * L2E};
-#pragma unroll
-        for (int q = 0; q < 4; ++q) sc[4 * r4 + q] = fmaf(round_bf(sc[4 * r4 + q]), sL, bb[q]);
+        const uint32_t u0 = pack_bf2(sc[4 * r4], sc[4 * r4 + 1]), u1 = pack_bf2(sc[4 * r4 + 2], sc[4 * r4 + 3]);
+        sc[4 * r4] = fmaf(bf_lo(u0), sL, b4[r4].x);
+        sc[4 * r4 + 1] = fmaf(bf_hi(u0), sL, b4[r4].y);
+        sc[4 * r4 + 2] = fmaf(bf_lo(u1), sL, b4[r4].z);
+        sc[4 * r4 + 3] = fmaf(bf_hi(u1), sL, b4[r4].w);
       }
     } else {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) sc[r] = round_bf(sc[r]) * sL;
+      for (int r = 0; r < 16; r += 2) {
+        const uint32_t u = pack_bf2(sc[r], sc[r + 1]);
+        sc[r] = bf_lo(u) * sL;
+        sc[r + 1] = bf_hi(u) * sL;
+      }
     }
-    if (f.kpos >= 0 || f.nvalid < KB) {
+    // masks: rows past the valid keys, and the causal diagonal (a current-chunk block wholly
+    // before the wave's first query needs none)
+    if (f.nvalid < KB || (f.kpos >= 0 && f.kpos + KB - 1 > wave_q0)) {
       const int lim = min(f.nvalid - 1, f.kpos >= 0 ? qi - f.kpos : KB - 1);
 #pragma unroll
       for (int r = 0; r < 16; ++r) sc[r] = d_row(lane, r) <= lim ? sc[r] : -INFINITY;
@@ -1016,14 +1038,17 @@ __global__ void __launch_bounds__(64 * NW) attn_fwd2_kernel(b3_attn_args a, int 
     }
   }
 
-  // ---- normalise; y = round(O)
+  // ---- normalise; y = round(O), kept as bf16 pairs (features d_row(lane, 2j), +1)
   const float inv_l = l_run > 0.f ? 1.0f / l_run : 0.f;
+  uint32_t yp[NDB][8];
 #pragma unroll
   for (int db = 0; db < NDB; ++db)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) o[db][r] = round_bf(o[db][r] * inv_l);
+    for (int j = 0; j < 8; ++j) yp[db][j] = pack_bf2(o[db][2 * j] * inv_l, o[db][2 * j + 1] * inv_l);
 
-  // ---- readout: eta * RMSNorm(normalize(q_raw) . M * (1-gamma)/sqrt(HD))
+  // ---- readout: y += round(eta * RMSNorm(normalize(q_raw) . M * (1-gamma)/sqrt(HD))), rounded.
+  // The fp32 interior is reassociated: sum(ym^2) is taken over the raw products and scaled
+  // once, and 1/|q|, (1-gamma)/sqrt(HD), the RMS scale and eta make one factor per query.
   if (readout) {
     wait_vm<0>();
     sync_lds();
@@ -1050,21 +1075,23 @@ __global__ void __launch_bounds__(64 * NW) attn_fwd2_kernel(b3_attn_args a, int 
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float y = mul_rn(rr[db][r] * inv_q, coef);
-        rr[db][r] = y;
-        ss += y * y;
-      }
+      for (int r = 0; r < 16; ++r) ss = fmaf(rr[db][r], rr[db][r], ss);
     ss += xor32(ss);
-    const float rs = 1.0f / sqrtf(div_rn(ss, (float)HD) + a.eps);
+    const float k1 = inv_q * coef;
+    const float rs = 1.0f / sqrtf(ss * (k1 * k1) * (1.0f / HD) + a.eps);
     const float eta = qok ? a.eta[b * a.e_sb + hq * a.e_sh + t] : 0.f;
+    const float kq = k1 * rs * eta;
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int d = 32 * db + d_row(lane, r);
-        const float ymn = mul_rn(mul_rn(rr[db][r], rs), a.res_w[d]);
-        o[db][r] = round_bf(add_rn(o[db][r], round_bf(mul_rn(eta, ymn))));
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const float4 w4 = *reinterpret_cast<const float4*>(a.res_w + 32 * db + 8 * r4 + 4 * h);
+        const uint32_t e0 = pack_bf2(rr[db][4 * r4] * kq * w4.x, rr[db][4 * r4 + 1] * kq * w4.y);
+        const uint32_t e1 = pack_bf2(rr[db][4 * r4 + 2] * kq * w4.z, rr[db][4 * r4 + 3] * kq * w4.w);
+        uint32_t& y0 = yp[db][2 * r4];
+        uint32_t& y1 = yp[db][2 * r4 + 1];
+        y0 = pack_bf2(bf_lo(y0) + bf_lo(e0), bf_hi(y0) + bf_hi(e0));
+        y1 = pack_bf2(bf_lo(y1) + bf_lo(e1), bf_hi(y1) + bf_hi(e1));
       }
   }
 
@@ -1074,12 +1101,8 @@ __global__ void __launch_bounds__(64 * NW) attn_fwd2_kernel(b3_attn_args a, int 
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
 #pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4) {
-        u16x4 w;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) w[e] = f2bf(o[db][4 * r4 + e]);
-        *reinterpret_cast<u16x4*>(yrow + 32 * db + 8 * r4 + 4 * h) = w;
-      }
+      for (int r4 = 0; r4 < 4; ++r4)
+        *reinterpret_cast<uint2*>(yrow + 32 * db + 8 * r4 + 4 * h) = make_uint2(yp[db][2 * r4], yp[db][2 * r4 + 1]);
   }
 }
 

@@ -33,6 +33,16 @@ __device__ __forceinline__ uint16_t f2bf(float f) { return __builtin_bit_cast(ui
 
 __device__ __forceinline__ float round_bf(float f) { return bf2f(f2bf(f)); }
 
+// Two values rounded to bf16 by one v_cvt_pk_bf16_f32: a in the low half (the lower address
+// in memory), b in the high half; bf_lo / bf_hi give them back as floats.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf2(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, bf16x2_t));
+}
+__device__ __forceinline__ float bf_lo(uint32_t u) { return __uint_as_float(u << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
+
 // Storage-type traits: T is float (fp32 modules) or uint16_t holding bf16 bits.
 template <typename T> struct St;
 template <> struct St<float> {

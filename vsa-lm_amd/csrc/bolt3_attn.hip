@@ -748,7 +748,8 @@ struct Fwd2Smem {
   static constexpr int TILE = KB * HD;   // elements of one K or V tile
   alignas(16) uint16_t ring[NST][2][TILE];
   alignas(16) uint16_t mt[2][HD * HD];   // M^T hi, lo
-  alignas(16) float sbias[128];          // slot bias row of the step (raw)
+  alignas(16) float sbias[128];          // slot bias row of the step (log2 units)
+  alignas(16) float resw[128];           // res_norm weight
 };
 
 __device__ __forceinline__ void lds_dma16(const void* src, void* lds) {
@@ -919,6 +920,7 @@ __global__ void __launch_bounds__(64 * NW) attn_fwd2_kernel(b3_attn_args a, int 
   // makes every later wait cover the loads issued before it)
   const float sb = (has_slots && tid < 128)
                        ? a.slot_bias[(long long)step * (a.slot_step / HD) + (long long)bh * a.S + tid] : 0.f;
+  const float rw = tid < HD ? a.res_w[tid] : 0.f;
   const uint16_t* qrow = reinterpret_cast<const uint16_t*>(a.q_rope) + b * a.q_sb + hq * a.q_sh + (long long)t * HD;
   QFrag<uint16_t, HD> qf;
   qf.load(qrow, qok, h);
@@ -927,6 +929,7 @@ __global__ void __launch_bounds__(64 * NW) attn_fwd2_kernel(b3_attn_args a, int 
   bool m_issued = false;
   if (pre == nb && readout) { issue_m(); m_issued = true; }
   if (tid < 128) lds_write_f32(&sm.sbias[tid], sb * L2E);   // bias in log2 units
+  if (tid < HD) lds_write_f32(&sm.resw[tid], rw);
 
   f32x16 o[NDB];
 #pragma unroll
@@ -1038,6 +1041,16 @@ __global__ void __launch_bounds__(64 * NW) attn_fwd2_kernel(b3_attn_args a, int 
     }
   }
 
+  // ---- the readout's global loads first (the q_raw fragment, eta), so that their latency
+  // overlaps the normalisation and the barrier before the readout
+  QFrag<uint16_t, HD> rf;
+  float eta = 0.f;
+  if (readout) {
+    const uint16_t* rrow = reinterpret_cast<const uint16_t*>(a.q_raw) + b * a.q_sb + hq * a.q_sh + (long long)t * HD;
+    rf.load(rrow, qok, h);
+    eta = qok ? a.eta[b * a.e_sb + hq * a.e_sh + t] : 0.f;
+  }
+
   // ---- normalise; y = round(O), kept as bf16 pairs (features d_row(lane, 2j), +1)
   const float inv_l = l_run > 0.f ? 1.0f / l_run : 0.f;
   uint32_t yp[NDB][8];
@@ -1052,9 +1065,6 @@ __global__ void __launch_bounds__(64 * NW) attn_fwd2_kernel(b3_attn_args a, int 
   if (readout) {
     wait_vm<0>();
     sync_lds();
-    const uint16_t* rrow = reinterpret_cast<const uint16_t*>(a.q_raw) + b * a.q_sb + hq * a.q_sh + (long long)t * HD;
-    QFrag<uint16_t, HD> rf;
-    rf.load(rrow, qok, h);
     float qq = rf.sumsq();
     qq += xor32(qq);
     const float inv_q = 1.0f / fmaxf(sqrtf(qq), 1e-12f);
@@ -1079,13 +1089,12 @@ __global__ void __launch_bounds__(64 * NW) attn_fwd2_kernel(b3_attn_args a, int 
     ss += xor32(ss);
     const float k1 = inv_q * coef;
     const float rs = 1.0f / sqrtf(ss * (k1 * k1) * (1.0f / HD) + a.eps);
-    const float eta = qok ? a.eta[b * a.e_sb + hq * a.e_sh + t] : 0.f;
     const float kq = k1 * rs * eta;
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
 #pragma unroll
       for (int r4 = 0; r4 < 4; ++r4) {
-        const float4 w4 = *reinterpret_cast<const float4*>(a.res_w + 32 * db + 8 * r4 + 4 * h);
+        const float4 w4 = *reinterpret_cast<const float4*>(&sm.resw[32 * db + 8 * r4 + 4 * h]);
         const uint32_t e0 = pack_bf2(rr[db][4 * r4] * kq * w4.x, rr[db][4 * r4 + 1] * kq * w4.y);
         const uint32_t e1 = pack_bf2(rr[db][4 * r4 + 2] * kq * w4.z, rr[db][4 * r4 + 3] * kq * w4.w);
         uint32_t& y0 = yp[db][2 * r4];

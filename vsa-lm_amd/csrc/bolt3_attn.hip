@@ -983,10 +983,22 @@ __global__ void __launch_bounds__(64 * NW) attn_fwd2_kernel(b3_attn_args a, int 
 #pragma unroll
       for (int r = 0; r < 16; ++r) sc[r] = d_row(lane, r) <= lim ? sc[r] : -INFINITY;
     }
+    // the first half of this block's V^T operand, read while the softmax runs
+    const int jv = lane & 15, grp = lane >> 4;
+    u16x4 tv0[8];
+    {
+      const int r1 = 4 * h + (jv >> 2), r2 = r1 + 8;
+#pragma unroll
+      for (int db = 0; db < NDB && db < 4; ++db) {
+        const int f0 = 32 * db + 16 * (grp & 1) + 4 * (jv & 3);
+        tv0[2 * db] = lds_read_tr(sV + r1 * HD + 8 * ((f0 >> 3) ^ (r1 % NP)) + (f0 & 7));
+        tv0[2 * db + 1] = lds_read_tr(sV + r2 * HD + 8 * ((f0 >> 3) ^ (r2 % NP)) + (f0 & 7));
+      }
+    }
     float bm = -INFINITY;
 #pragma unroll
     for (int r = 0; r < 16; ++r) bm = fmaxf(bm, sc[r]);
-    bm = fmaxf(bm, xor32(bm));
+    bm = pair_max32(bm);
     // the running max moves only when it grows by more than 2^8 (probabilities up to 2^8
     // before the final normalisation are exact enough in fp32 and rescale-free)
     const bool grow = bm > m_run + 8.0f;
@@ -999,7 +1011,7 @@ __global__ void __launch_bounds__(64 * NW) attn_fwd2_kernel(b3_attn_args a, int 
       sc[r] = p;
       ps += p;
     }
-    ps += xor32(ps);
+    ps = pair_sum32(ps);
     if (__builtin_amdgcn_ballot_w64(grow) != 0) {
       const float alpha = __builtin_amdgcn_exp2f(m_run - mu);   // m_run = -inf: alpha = 0
 #pragma unroll
@@ -1015,28 +1027,31 @@ __global__ void __launch_bounds__(64 * NW) attn_fwd2_kernel(b3_attn_args a, int 
     for (int kc = 0; kc < 2; ++kc)
 #pragma unroll
       for (int e = 0; e < 8; ++e) pv[kc][e] = f2bf(sc[8 * kc + e]);
-    // ---- O^T[d][q] += V^T . P^T; lane (j = l % 16, grp = l / 16) of a transposed read
-    // addresses row 16kc + 4h + j/4 (+ 8) and features 32db + 16*(grp & 1) + 4*(j & 3)
+    // ---- O^T[d][q] += V^T . P^T
     {
-      const int j = lane & 15, grp = lane >> 4;
+      lds_wait8(tv0);
+      u16x4 tv1[8];
+      const int r1 = 16 + 4 * h + (jv >> 2), r2 = r1 + 8;
 #pragma unroll
-      for (int kc = 0; kc < 2; ++kc) {
-        const int r1 = 16 * kc + 4 * h + (j >> 2), r2 = r1 + 8;
-        u16x4 tv[8];
+      for (int db = 0; db < NDB && db < 4; ++db) {
+        const int f0 = 32 * db + 16 * (grp & 1) + 4 * (jv & 3);
+        tv1[2 * db] = lds_read_tr(sV + r1 * HD + 8 * ((f0 >> 3) ^ (r1 % NP)) + (f0 & 7));
+        tv1[2 * db + 1] = lds_read_tr(sV + r2 * HD + 8 * ((f0 >> 3) ^ (r2 % NP)) + (f0 & 7));
+      }
 #pragma unroll
-        for (int db = 0; db < NDB && db < 4; ++db) {
-          const int f0 = 32 * db + 16 * (grp & 1) + 4 * (j & 3);
-          tv[2 * db] = lds_read_tr(sV + r1 * HD + 8 * ((f0 >> 3) ^ (r1 % NP)) + (f0 & 7));
-          tv[2 * db + 1] = lds_read_tr(sV + r2 * HD + 8 * ((f0 >> 3) ^ (r2 % NP)) + (f0 & 7));
-        }
-        lds_wait8(tv);
+      for (int db = 0; db < NDB && db < 4; ++db) {
+        u16x8 av;
 #pragma unroll
-        for (int db = 0; db < NDB && db < 4; ++db) {
-          u16x8 av;
+        for (int e = 0; e < 4; ++e) { av[e] = tv0[2 * db][e]; av[4 + e] = tv0[2 * db + 1][e]; }
+        mma_bf16(o[db], av, pv[0]);
+      }
+      lds_wait8(tv1);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) { av[e] = tv[2 * db][e]; av[4 + e] = tv[2 * db + 1][e]; }
-          mma_bf16(o[db], av, pv[kc]);
-        }
+      for (int db = 0; db < NDB && db < 4; ++db) {
+        u16x8 av;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) { av[e] = tv1[2 * db][e]; av[4 + e] = tv1[2 * db + 1][e]; }
+        mma_bf16(o[db], av, pv[1]);
       }
     }
   }
@@ -1066,7 +1081,7 @@ __global__ void __launch_bounds__(64 * NW) attn_fwd2_kernel(b3_attn_args a, int 
     wait_vm<0>();
     sync_lds();
     float qq = rf.sumsq();
-    qq += xor32(qq);
+    qq = pair_sum32(qq);
     const float inv_q = 1.0f / fmaxf(sqrtf(qq), 1e-12f);
     const float coef = div_rn(1.0f - a.gamma[hkv], sqrtf((float)HD));
     f32x16 rr[NDB];
@@ -1086,7 +1101,7 @@ __global__ void __launch_bounds__(64 * NW) attn_fwd2_kernel(b3_attn_args a, int 
     for (int db = 0; db < NDB; ++db)
 #pragma unroll
       for (int r = 0; r < 16; ++r) ss = fmaf(rr[db][r], rr[db][r], ss);
-    ss += xor32(ss);
+    ss = pair_sum32(ss);
     const float k1 = inv_q * coef;
     const float rs = 1.0f / sqrtf(ss * (k1 * k1) * (1.0f / HD) + a.eps);
     const float kq = k1 * rs * eta;

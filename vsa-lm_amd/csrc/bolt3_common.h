@@ -147,6 +147,17 @@ __device__ __forceinline__ void sync_lds() { asm volatile("s_waitcnt lgkmcnt(0)\
 // ---------------------------------------------------------------- reductions
 
 __device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32, 64); }
+// max / sum of v over the lane pair (l, l ^ 32), in both lanes: one v_permlane32_swap gives
+// every lane the two values (in either order; both operations are commutative), with no
+// cross-lane LDS exchange and its wait
+__device__ __forceinline__ float pair_max32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 __device__ __forceinline__ int xor32i(int v) { return __shfl_xor(v, 32, 64); }
 
 template <typename F>

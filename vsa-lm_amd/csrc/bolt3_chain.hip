@@ -86,6 +86,7 @@ struct DecSmem {
   int any_merge;
   float invf[HD / 2];
   float rel[LMAX], score[LMAX];
+  float tpos[LMAX], tbeta[LMAX];   // this step's token positions and delta-rule gates
   int slot[LMAX], flags[LMAX];
   float sk_a[LMAX];
   int si_a[LMAX];
@@ -107,7 +108,7 @@ struct DecSmem {
     } sc;
     struct {
       int cnt[S], off[S], hits[S], mlist[LMAX];
-      float psum[S], pos[LMAX];
+      float psum[S];
       unsigned bits[S][LMAX / 32];   // bit j of row s: token j merges into slot s
       int nhit;
     } mg;
@@ -982,6 +983,10 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
     const bool steady = nf >= S;
     float* log = a.log ? a.log + ((long long)step * BH + bh) * (B3_LOG_ROWS * B3_LOG_COLS) : nullptr;
     float* w_out = w_all + ((long long)step * BH + bh) * LMAX;
+    // positions and gates of the step's tokens: loaded here, stored to LDS after the scoring,
+    // so that their latency overlaps it
+    const float pos_t = tid < l ? pos[tid] : 0.f;
+    const float beta_t = tid < l ? beta[tid] : 0.f;
 
     if (tid == 0) sm.any_merge = 0;
     if (tid < S) {
@@ -1040,6 +1045,10 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
     td_ready = false;
     prefetch(step, wave, lane, steady ? 1 : 7);
     if (has) sm.any_merge = 1;
+    if (tid < l) {
+      sm.tpos[tid] = pos_t;
+      sm.tbeta[tid] = beta_t;
+    }
     sync_lds();
 
     if (!steady) {
@@ -1069,7 +1078,7 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
       }
       if (tid < m) {
         const int j = sm.si_a[tid], s = nf + tid;
-        sm.pm[s] = pos[j];
+        sm.pm[s] = sm.tpos[j];
         sm.mass[s] = 1.0f;
         sm.util[s] = sm.rel[j];
         sm.act[s] = 1;
@@ -1089,10 +1098,9 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
       const int any_merge = sm.any_merge;
       // ---------------- merge: per-slot mass-weighted means, tokens in ascending order
       if (any_merge) {
-        // which tokens merge into which slot, as a bitmap [slot][token]; the positions to LDS
+        // which tokens merge into which slot, as a bitmap [slot][token]
         constexpr int LW = LMAX / 32;
         for (int i = tid; i < S * LW; i += DT) (&sm.u.mg.bits[0][0])[i] = 0u;
-        if (tid < l) sm.u.mg.pos[tid] = pos[tid];
         sync_lds();
         if (tid < l && (sm.flags[tid] & F_MERGE)) atomicOr(&sm.u.mg.bits[sm.slot[tid]][tid >> 5], 1u << (tid & 31));
         sync_lds();
@@ -1107,7 +1115,7 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
               const int j = 32 * w + __builtin_ctz(m);
               m &= m - 1;
               ++c;
-              ps += sm.u.mg.pos[j];
+              ps += sm.tpos[j];
             }
           }
           sm.u.mg.cnt[tid] = c;
@@ -1315,7 +1323,7 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
         if (tv > bv && tv > -1e8f) {
           const int j = sm.si_a[tid], s = sm.si_b[tid];
           sm.flags[j] |= F_INS;
-          sm.pm[s] = pos[j];
+          sm.pm[s] = sm.tpos[j];
           sm.mass[s] = 1.0f;
           sm.util[s] = sm.rel[j];
           sm.vdirty[s] = 1;
@@ -1337,7 +1345,7 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
         const int f = sm.flags[tid];
         const bool dl = !(f & F_MERGE) && !(f & F_INS);
         if (dl) sm.flags[tid] = f | F_DELTA;
-        w_out[tid] = dl ? beta[tid] : 0.f;
+        w_out[tid] = dl ? sm.tbeta[tid] : 0.f;
       }
       sync_lds();
       if (log) {

@@ -734,20 +734,24 @@ __global__ void __launch_bounds__(512) attn_fwd_kernel(b3_attn_args a, int QW) {
 // ---------------------------------------------------------------- bf16 forward, DMA staging
 //
 // The same attention for the forward (mode 0, all key fields, bf16), with the K and V tiles
-// brought into LDS by global->LDS loads (global_load_lds_dwordx4) through a ring of NST
-// stages, NST - 1 tiles ahead of the MFMAs, so that no staging goes through registers and the
-// tile loads overlap NST - 2 blocks of compute.  Tiles keep the source row-major layout with
-// the 16-byte pieces of row r permuted by p ^ (r % (HD/8)) (conflict-free operand reads);
-// the V operand of O^T = V^T P^T is read with ds_read_b64_tr_b16, which transposes 16-bit
-// elements across lanes, so V needs no transpose when staged.  The M_res snapshot (M^T bf16
-// hi / lo) comes by the same loads, after the last tile.
-constexpr int NST = 4;
+// brought into LDS by global->LDS loads (global_load_lds_dwordx4), so that no staging goes
+// through registers.  Blocks go in pairs: one barrier per pair, and the QK products of a
+// pair's second block are issued before the softmax of its first, so that the softmax runs
+// beside MFMA work.  The ring has three pair slots (six stages): while pair p is computed,
+// pair p + 1 is in flight and pair p + 2 is issued into the slot pair p - 1 has left.  Tiles
+// keep the source row-major layout with the 16-byte pieces of row r permuted by
+// p ^ (r % (HD/8)) (conflict-free operand reads); the V operand of O^T = V^T P^T is read with
+// ds_read_b64_tr_b16, which transposes 16-bit elements across lanes, so V needs no transpose
+// when staged.  The M_res snapshot (M^T bf16 hi / lo) comes by the same loads into the two
+// pair slots the last pair leaves free: hi at the barrier before the last pair, lo at the
+// last barrier.
+constexpr int NST = 6;
 
 template <int HD>
 struct Fwd2Smem {
   static constexpr int TILE = KB * HD;   // elements of one K or V tile
+  static_assert(4 * TILE >= HD * HD, "an M^T half fits in one pair slot");
   alignas(16) uint16_t ring[NST][2][TILE];
-  alignas(16) uint16_t mt[2][HD * HD];   // M^T hi, lo
   alignas(16) float sbias[128];          // slot bias row of the step (log2 units)
   alignas(16) float resw[128];           // res_norm weight
 };
@@ -809,8 +813,8 @@ __global__ void __launch_bounds__(64 * NW) attn_fwd2_kernel(b3_attn_args a, int 
   constexpr int LPB = 2 * IPT / NW;                 // per wave per block (K and V)
   static_assert(LPB * NW == 2 * IPT, "tile loads must divide over the waves");
   constexpr int MIPT = HD / RPI;                    // instructions per M^T half (hi or lo)
-  constexpr int LPM = 2 * MIPT / NW;
-  static_assert(LPM * NW == 2 * MIPT, "M^T loads must divide over the waves");
+  constexpr int LPMH = MIPT / NW;                   // per wave per M^T half
+  static_assert(LPMH * NW == MIPT, "M^T loads must divide over the waves");
   const int G = a.H / a.HKV;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n = lane & 31, h = lane >> 5;
@@ -889,45 +893,37 @@ __global__ void __launch_bounds__(64 * NW) attn_fwd2_kernel(b3_attn_args a, int 
     }
   };
   const bool readout = a.m_res && step >= 0;
-  auto issue_m = [&]() {
+  // M^T half (0: hi, 1: lo) into pair slot ps
+  auto issue_mhalf = [&](int half, int ps) {
     const uint16_t* src = reinterpret_cast<const uint16_t*>(a.m_res + (long long)step * a.m_step) +
-                          (long long)bh * 2 * HD * HD;   // bf16 M^T hi, then lo
+                          (long long)bh * 2 * HD * HD + (long long)half * HD * HD;   // bf16 M^T hi, then lo
+    uint16_t* dst = &sm.ring[2 * ps][0][0];
 #pragma unroll
-    for (int q = 0; q < LPM; ++q) {
-      const int ins = wave * LPM + q;
-      const int half = ins / MIPT, ch = ins % MIPT;
+    for (int q = 0; q < LPMH; ++q) {
+      const int ch = wave * LPMH + q;
       const int r = ch * RPI + lane / NP, p = (lane % NP) ^ (r % NP);
-      lds_dma16(src + half * HD * HD + (long long)r * HD + 8 * p, &sm.mt[half][ch * 512]);
+      lds_dma16(src + (long long)r * HD + 8 * p, dst + ch * 512);
     }
   };
-  // wait for the loads of a block while `ahead` later blocks (and the snapshot, if issued)
-  // may still be in flight
-  auto wait_block = [&](int ahead, bool m_issued) {
-    if (m_issued) {
-      if (ahead >= 2) wait_vm<2 * LPB + LPM>();
-      else if (ahead == 1) wait_vm<LPB + LPM>();
-      else wait_vm<LPM>();
-    } else {
-      if (ahead >= 2) wait_vm<2 * LPB>();
-      else if (ahead == 1) wait_vm<LPB>();
-      else wait_vm<0>();
-    }
+  const int npair = (nb + 1) / 2, P = npair - 1;
+  // this wave's loads of pair q, and the stages of its blocks (pair slot q % 3)
+  auto issue_pair = [&](int q) {
+    issue(2 * q, 2 * (q % 3));
+    if (2 * q + 1 < nb) issue(2 * q + 1, 2 * (q % 3) + 1);
   };
-  static_assert(NST == 4, "wait_block covers up to NST - 2 blocks ahead");
 
-  // ---- prologue: the slot bias row and the query fragment into registers, the first NST - 1
-  // tiles into LDS; the bias goes to LDS after the tile loads are issued (in-order completion
-  // makes every later wait cover the loads issued before it)
+  // ---- prologue: the slot bias row, the res_norm weight and the query fragment into
+  // registers, pairs 0 and 1 into LDS; the bias and weight go to LDS after the tile loads are
+  // issued (in-order completion makes every later wait cover the loads issued before it)
   const float sb = (has_slots && tid < 128)
                        ? a.slot_bias[(long long)step * (a.slot_step / HD) + (long long)bh * a.S + tid] : 0.f;
   const float rw = tid < HD ? a.res_w[tid] : 0.f;
   const uint16_t* qrow = reinterpret_cast<const uint16_t*>(a.q_rope) + b * a.q_sb + hq * a.q_sh + (long long)t * HD;
   QFrag<uint16_t, HD> qf;
   qf.load(qrow, qok, h);
-  const int pre = min(nb, NST - 1);
-  for (int j = 0; j < pre; ++j) issue(j, j);
-  bool m_issued = false;
-  if (pre == nb && readout) { issue_m(); m_issued = true; }
+  issue_pair(0);
+  if (P >= 1) issue_pair(1);
+  if (P == 0 && readout) issue_mhalf(0, 1);
   if (tid < 128) lds_write_f32(&sm.sbias[tid], sb * L2E);   // bias in log2 units
   if (tid < HD) lds_write_f32(&sm.resw[tid], rw);
 
@@ -936,24 +932,20 @@ __global__ void __launch_bounds__(64 * NW) attn_fwd2_kernel(b3_attn_args a, int 
   for (int db = 0; db < NDB; ++db) o[db] = zero16();
   float m_run = -INFINITY, l_run = 0.f;
 
-  for (int i = 0; i < nb; ++i) {
-    const int st = i % NST;
-    wait_block(min(nb - 1, i + NST - 2) - i, m_issued);
-    sync_lds();   // block i is in LDS; every wave is done with stage (i - 1) % NST
-    if (i + NST - 1 < nb) {
-      issue(i + NST - 1, (i + NST - 1) % NST);
-      if (i + NST - 1 == nb - 1 && readout) { issue_m(); m_issued = true; }
-    }
-    const FwdBlock f = block(i);
-    if (f.kpos >= 0 && f.kpos > wave_q0 + 31) continue;   // the wave's queries all precede the block
+  // S^T = K Q^T of the block in stage st
+  auto qk = [&](int st) -> f32x16 {
     const uint16_t* sK = sm.ring[st][0];
-    const uint16_t* sV = sm.ring[st][1];
     f32x16 sc = zero16();
 #pragma unroll
     for (int ks = 0; ks < HD / 16; ++ks) {
       const int piece = (2 * ks + h) ^ (n % NP);
       mma_bf16(sc, *reinterpret_cast<const u16x8*>(sK + n * HD + 8 * piece), qf.v[ks]);
     }
+    return sc;
+  };
+  // softmax step and O^T += V^T P^T for block f in stage st, scores sc
+  auto attend = [&](f32x16 sc, const FwdBlock& f, int st) {
+    const uint16_t* sV = sm.ring[st][1];
     // scores in log2 units: round_bf(q.k) * scale*log2(e) (+ slot bias * log2(e)), one FMA
     if (f.bias) {
       fx4 b4[4];
@@ -1054,6 +1046,37 @@ __global__ void __launch_bounds__(64 * NW) attn_fwd2_kernel(b3_attn_args a, int 
         mma_bf16(o[db], av, pv[1]);
       }
     }
+  };
+
+  for (int pr = 0; pr < npair; ++pr) {
+    // wait for pair pr while pair pr + 1 (or, at the last pair, the M^T hi half) may still be
+    // in flight
+    if (pr < P) {
+      if (2 * pr + 3 < nb) wait_vm<2 * LPB>();
+      else wait_vm<LPB>();
+    } else if (readout) {
+      wait_vm<LPMH>();
+    } else {
+      wait_vm<0>();
+    }
+    sync_lds();   // pair pr is in LDS; every wave is done with pair pr - 1
+    if (pr + 2 <= P) issue_pair(pr + 2);
+    if (readout) {
+      if (pr == P - 1) issue_mhalf(0, (P + 1) % 3);
+      if (pr == P) issue_mhalf(1, (P + 2) % 3);
+    }
+    const int i0 = 2 * pr, i1 = 2 * pr + 1;
+    const FwdBlock f0 = block(i0);
+    const bool do0 = !(f0.kpos >= 0 && f0.kpos > wave_q0 + 31);   // the wave's queries all precede the block
+    const bool has1 = i1 < nb;
+    const FwdBlock f1 = block(has1 ? i1 : i0);
+    const bool do1 = has1 && !(f1.kpos >= 0 && f1.kpos > wave_q0 + 31);
+    const int st0 = 2 * (pr % 3);
+    f32x16 sc0 = zero16(), sc1 = zero16();
+    if (do0) sc0 = qk(st0);
+    if (do1) sc1 = qk(st0 + 1);
+    if (do0) attend(sc0, f0, st0);
+    if (do1) attend(sc1, f1, st0 + 1);
   }
 
   // ---- the readout's global loads first (the q_raw fragment, eta), so that their latency
@@ -1084,6 +1107,8 @@ __global__ void __launch_bounds__(64 * NW) attn_fwd2_kernel(b3_attn_args a, int 
     qq = pair_sum32(qq);
     const float inv_q = 1.0f / fmaxf(sqrtf(qq), 1e-12f);
     const float coef = div_rn(1.0f - a.gamma[hkv], sqrtf((float)HD));
+    const uint16_t* mt_hi = &sm.ring[2 * ((P + 1) % 3)][0][0];
+    const uint16_t* mt_lo = &sm.ring[2 * ((P + 2) % 3)][0][0];
     f32x16 rr[NDB];
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {
@@ -1092,8 +1117,8 @@ __global__ void __launch_bounds__(64 * NW) attn_fwd2_kernel(b3_attn_args a, int 
 #pragma unroll
       for (int ks = 0; ks < HD / 16; ++ks) {
         const int piece = (2 * ks + h) ^ (dr % NP);
-        mma_bf16(rr[db], *reinterpret_cast<const u16x8*>(&sm.mt[0][dr * HD + 8 * piece]), rf.v[ks]);
-        mma_bf16(rr[db], *reinterpret_cast<const u16x8*>(&sm.mt[1][dr * HD + 8 * piece]), rf.v[ks]);
+        mma_bf16(rr[db], *reinterpret_cast<const u16x8*>(mt_hi + dr * HD + 8 * piece), rf.v[ks]);
+        mma_bf16(rr[db], *reinterpret_cast<const u16x8*>(mt_lo + dr * HD + 8 * piece), rf.v[ks]);
       }
     }
     float ss = 0.f;

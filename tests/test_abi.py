@@ -66,6 +66,9 @@ def test_rejects_bad_arguments_without_gpu_work():
     la.dec.dtype = 1
     assert lib.bolt3_decode_layer(ctypes.byref(la), None) == 1001
     assert lib.bolt3_wait_count(None, 1, 10, None) == 1001
+    d2 = A.DecodeArgs()
+    d2.dtype, d2.B, d2.H, d2.HKV, d2.HD, d2.S, d2.has_slots = 1, 1, 4, 1, 128, 256, 1
+    assert lib.bolt3_decode(ctypes.byref(d2), None) in (1001, 1002)   # rejected before any launch
 
 
 STRUCTS = {"b3_heads_args": A.HeadsArgs, "b3_chain_args": A.ChainArgs, "b3_attn_args": A.AttnArgs,

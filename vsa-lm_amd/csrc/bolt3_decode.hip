@@ -1034,6 +1034,7 @@ static int check_decode(const b3_decode_args* a, bool need_lin) {
     return B3_ERR_ARG;
   if (a->work_bytes < bolt3_decode_workspace_bytes(a->B, a->H, a->HKV, a->HD)) return B3_ERR_WORKSPACE;
   if (a->has_slots && (!a->slot_k || !a->slot_v || !a->slot_bias)) return B3_ERR_ARG;
+  if (a->has_slots && (a->S <= 0 || a->S > 128)) return B3_ERR_UNSUPPORTED;   // the slot field's size
   if (a->n_sink_keys > 0 && (!a->sink_k || !a->sink_v)) return B3_ERR_ARG;
   if (a->has_qk_norm && (!a->qn_w || !a->kn_w)) return B3_ERR_ARG;
   // 16-byte rows: the projection row and every key / value row

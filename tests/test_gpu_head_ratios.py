@@ -1,0 +1,36 @@
+"""The bf16 forward at head ratios and head sizes the golden fixtures leave out, against the oracle
+(lowest-index ties, the kernel's rule) at the bf16 bar (max-abs <= 2e-2, cosine >= 0.9995):
+
+* one query head per kv head (two-wavefront attention workgroups),
+* eight query heads per kv head (one 32-query sub-tile per wavefront),
+* two per kv head at head_dim 128 (four wavefronts; the fixtures have it at head_dim 64),
+* one per kv head at head_dim 64.
+
+T = 700: a partial last chunk, and both odd and even numbers of 32-key blocks per workgroup,
+so the attention kernel's pairs of blocks end on a single block in some workgroups.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+import recipes
+from helpers import cosine, max_abs
+from oracle import bolt3_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("H,HKV,HD", [(8, 8, 128), (8, 1, 128), (4, 2, 128), (8, 8, 64)])
+def test_bf16_forward_head_ratios(H, HKV, HD, gpu):
+    from bolt3_amd import Bolt3Attn
+    cfg = dict(dim=256, num_heads=H, num_kv_heads=HKV, head_dim=HD, rope_theta=1e6, eps=1e-6, qk_norm=True)
+    print(f"[case] bf16 forward H={H} HKV={HKV} HD={HD} T=700", flush=True)
+    bf = torch.bfloat16
+    mod = recipes.init_module(Bolt3Attn(cfg), 11, nondefault=True).to(bf)
+    x = recipes.hidden(11, 1, 700, cfg["dim"]).to(bf)
+    with torch.no_grad():
+        ref = O.forward(O.Bolt3Params.from_module(mod), x, ties="index")
+        y = mod.to(gpu)(x.to(gpu)).cpu()
+    ma, cs = max_abs(y, ref), cosine(y, ref)
+    assert ma <= 2e-2 and cs >= 0.9995, f"H={H} HKV={HKV} HD={HD}: max-abs {ma:.3e} cos {cs:.6f}"

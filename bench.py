@@ -278,6 +278,12 @@ def main():
         ms_k, calls = kern.get(k, (0.0, 0.0))
         kernels[k] = dict(ms_per_forward=round(ms_k, 4), launches_per_forward=calls, bound=bound,
                           **({"flops": w} if bound == "mfma" else {"bytes": w}))
+        if ms_k > 0:   # each entry point against its own roofline (work per forward / its launch time)
+            rate = w / (ms_k * 1e-3)
+            if bound == "mfma":
+                kernels[k].update(achieved_tflops=round(rate / 1e12, 2), frac=round(rate / PEAK_BF16, 4))
+            else:
+                kernels[k].update(achieved_gbps=round(rate / 1e9, 1), frac=round(rate / PEAK_HBM, 4))
     dom = max(kernels, key=lambda k: kernels[k]["ms_per_forward"])
     d = kernels[dom]
     bound, w = work[dom]

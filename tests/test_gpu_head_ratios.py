@@ -4,7 +4,8 @@
 * one query head per kv head (two-wavefront attention workgroups),
 * eight query heads per kv head (one 32-query sub-tile per wavefront),
 * two per kv head at head_dim 128 (four wavefronts; the fixtures have it at head_dim 64),
-* one per kv head at head_dim 64.
+* one per kv head at head_dim 64,
+* and fp32 storage at head_dim 128 (fp32 bar: relative error <= 1e-4).
 
 T = 700: a partial last chunk, and both odd and even numbers of 32-key blocks per workgroup,
 so the attention kernel's pairs of blocks end on a single block in some workgroups.
@@ -15,7 +16,7 @@ import pytest
 import torch
 
 import recipes
-from helpers import cosine, max_abs
+from helpers import cosine, max_abs, rel_err
 from oracle import bolt3_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -34,3 +35,16 @@ def test_bf16_forward_head_ratios(H, HKV, HD, gpu):
         y = mod.to(gpu)(x.to(gpu)).cpu()
     ma, cs = max_abs(y, ref), cosine(y, ref)
     assert ma <= 2e-2 and cs >= 0.9995, f"H={H} HKV={HKV} HD={HD}: max-abs {ma:.3e} cos {cs:.6f}"
+
+
+def test_fp32_forward_head_dim_128(gpu):
+    from bolt3_amd import Bolt3Attn
+    cfg = dict(dim=256, num_heads=8, num_kv_heads=2, head_dim=128, rope_theta=1e6, eps=1e-6, qk_norm=True)
+    print("[case] fp32 forward H=8 HKV=2 HD=128 T=700", flush=True)
+    mod = recipes.init_module(Bolt3Attn(cfg), 12, nondefault=True)
+    x = recipes.hidden(12, 2, 700, cfg["dim"])
+    with torch.no_grad():
+        ref = O.forward(O.Bolt3Params.from_module(mod), x, ties="index")
+        y = mod.to(gpu)(x.to(gpu)).cpu()
+    e = rel_err(y, ref)
+    assert e <= 1e-4, f"fp32 HD=128: rel err {e:.3e}"

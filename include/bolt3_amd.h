@@ -150,7 +150,7 @@ int64_t bolt3_chain_workspace_bytes(int32_t dtype, int32_t B, int32_t HKV, int32
 
 /*
  * Holds `stream` until *counter has reached `target` (compared modulo 2^32) or after max_polls
- * polls of about 0.2 us each, whichever comes first.  No counterpart in the reference (its chain
+ * polls (each a device-scope read and a short sleep), whichever comes first.  No counterpart in the reference (its chain
  * is serial host code): the forward launches the slot decisions (one workgroup per bh, each with
  * the whole LDS of a compute unit) on a side stream and calls this on its main stream, with
  * `counter` = b3_chain_args.started, before a full-chip GEMM, so that the GEMM's workgroups cannot

@@ -6,7 +6,8 @@
 * two per kv head at head_dim 128 (four wavefronts; the fixtures have it at head_dim 64),
 * one per kv head at head_dim 64,
 * and fp32 storage at head_dim 128 (fp32 bar: relative error <= 1e-4);
-* chunk lengths 64 and 256 (the fixtures use 128), bf16 and fp32.
+* chunk lengths 64 and 256 (the fixtures use 128), bf16 and fp32;
+* biased q/k/v projections (qkv_bias; the fixtures have none), bf16 and fp32.
 
 T = 700: a partial last chunk, and both odd and even numbers of 32-key blocks per workgroup,
 so the attention kernel's pairs of blocks end on a single block in some workgroups.
@@ -68,3 +69,23 @@ def test_forward_chunk_lengths(C, dtype, gpu):
     else:
         ma, cs = max_abs(y, ref), cosine(y, ref)
         assert ma <= 2e-2 and cs >= 0.9995, f"C={C} bf16: max-abs {ma:.3e} cos {cs:.6f}"
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_forward_qkv_bias(dtype, gpu):
+    from bolt3_amd import Bolt3Attn
+    cfg = dict(dim=128, num_heads=4, num_kv_heads=2, head_dim=64, rope_theta=1e4, eps=1e-5, qk_norm=True,
+               qkv_bias=True)
+    print(f"[case] forward qkv_bias {dtype} T=700", flush=True)
+    mod = recipes.init_module(Bolt3Attn(cfg), 14, nondefault=True).to(dtype)
+    assert mod.q_proj.bias is not None and float(mod.k_proj.bias.detach().float().abs().sum()) > 0
+    x = recipes.hidden(14, 2, 700, cfg["dim"]).to(dtype)
+    with torch.no_grad():
+        ref = O.forward(O.Bolt3Params.from_module(mod), x, ties="index")
+        y = mod.to(gpu)(x.to(gpu)).cpu()
+    if dtype == torch.float32:
+        e = rel_err(y, ref)
+        assert e <= 1e-4, f"qkv_bias fp32: rel err {e:.3e}"
+    else:
+        ma, cs = max_abs(y, ref), cosine(y, ref)
+        assert ma <= 2e-2 and cs >= 0.9995, f"qkv_bias bf16: max-abs {ma:.3e} cos {cs:.6f}"

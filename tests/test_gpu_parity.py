@@ -360,20 +360,24 @@ def test_decoder_matches_golden(gpu):
     assert rel_err(states[0].cpu(), g["final.m_res"]) <= 1e-4
 
 
-@pytest.mark.parametrize("dtype,head_dim,heads", [(torch.float32, 128, (8, 2)), (torch.bfloat16, 128, (8, 2)),
-                                                  (torch.float32, 64, (8, 2)), (torch.bfloat16, 64, (8, 2)),
-                                                  (torch.bfloat16, 128, (8, 8)), (torch.bfloat16, 128, (8, 1))])
-def test_decode_kernel_vs_oracle_layer_step(dtype, head_dim, heads, gpu):
+@pytest.mark.parametrize("dtype,head_dim,heads,qkv_bias", [
+    (torch.float32, 128, (8, 2), False), (torch.bfloat16, 128, (8, 2), False),
+    (torch.float32, 64, (8, 2), False), (torch.bfloat16, 64, (8, 2), False),
+    (torch.bfloat16, 128, (8, 8), False), (torch.bfloat16, 128, (8, 1), False),
+    (torch.bfloat16, 64, (8, 2), True), (torch.float32, 64, (8, 2), True)])
+def test_decode_kernel_vs_oracle_layer_step(dtype, head_dim, heads, qkv_bias, gpu):
     """Prefill by chunks then single-token steps of one Bolt-3 layer, compared every step (both head
     dims the kernels are built for; bf16 runs the fused decode layer, fp32 the split kernels; the
-    fused layer also at one and at eight query heads per kv head, the most it takes)."""
+    fused layer also at one and at eight query heads per kv head, the most it takes; and with
+    biased q/k/v projections)."""
     from bolt3_amd import HybridLM, Bolt3Decoder
     import recipes
     torch.manual_seed(0)
     H, HKV = heads
-    print(f"[case] decode layer step {dtype} head_dim={head_dim} heads={H}/{HKV}", flush=True)
+    print(f"[case] decode layer step {dtype} head_dim={head_dim} heads={H}/{HKV} qkv_bias={qkv_bias}", flush=True)
     model = HybridLM(vocab_size=64, dim=128, num_layers=1, num_heads=H, num_kv_heads=HKV, intermediate=64,
-                     layer_types=["vsa"], head_dim=head_dim, qk_norm=True, rope_theta=1e6, eps=1e-6)
+                     layer_types=["vsa"], head_dim=head_dim, qk_norm=True, rope_theta=1e6, eps=1e-6,
+                     qkv_bias=qkv_bias)
     recipes.init_module(model.blocks[0].vsa, 11, nondefault=True)
     model.load_state_dict(recipes.model_params([(k, tuple(v.shape)) for k, v in model.state_dict().items()], 11),
                           strict=False)

@@ -242,3 +242,26 @@ def test_keep_score_uses_redundancy():
     keep = log["keep"][0]
     assert set(log["bot_slots"][0, :2].tolist()) == {2, 5}
     assert float(keep[2]) == pytest.approx(0.5 * 0.995 * 0.02, rel=1e-3)
+
+
+def test_llama3_inv_freq_against_transformers():
+    """The llama3 band rescaling (vsa_lm/surgery.py:56-72), oracle and product, against the
+    independent implementation in transformers (Llama 3.2 settings), and its band structure:
+    the high-frequency band unchanged, the low-frequency band divided by `factor`."""
+    tr = pytest.importorskip("transformers")
+    from transformers.modeling_rope_utils import ROPE_INIT_FUNCTIONS
+    from bolt3_amd.layers import rope_inv_freq
+    rs = {"rope_type": "llama3", "factor": 32.0, "low_freq_factor": 1.0, "high_freq_factor": 4.0,
+          "original_max_position_embeddings": 8192}
+    for hd, theta in ((64, 500000.0), (128, 500000.0)):
+        cfg = tr.LlamaConfig(hidden_size=32 * hd, num_attention_heads=32, head_dim=hd, rope_theta=theta,
+                             rope_scaling=rs, max_position_embeddings=131072)
+        ref, _ = ROPE_INIT_FUNCTIONS["llama3"](cfg, "cpu")
+        assert torch.equal(O.rope_inv_freq(hd, theta, rs), ref.float())
+        assert torch.equal(rope_inv_freq(hd, theta, rs), ref.float())
+        plain = O.rope_inv_freq(hd, theta)
+        wl = 2 * math.pi / plain
+        hi_band, lo_band = wl < 8192 / 4.0, wl > 8192 / 1.0
+        assert hi_band.any() and lo_band.any()
+        assert torch.equal(ref.float()[hi_band], plain[hi_band])
+        assert torch.allclose(ref.float()[lo_band], plain[lo_band] / 32.0, rtol=1e-6)

@@ -7,7 +7,8 @@
 * one per kv head at head_dim 64,
 * and fp32 storage at head_dim 128 (fp32 bar: relative error <= 1e-4);
 * chunk lengths 64 and 256 (the fixtures use 128), bf16 and fp32;
-* biased q/k/v projections (qkv_bias; the fixtures have none), bf16 and fp32.
+* biased q/k/v projections (qkv_bias; the fixtures have none), bf16 and fp32;
+* llama3 RoPE frequency rescaling, bf16 and fp32.
 
 T = 700: a partial last chunk, and both odd and even numbers of 32-key blocks per workgroup,
 so the attention kernel's pairs of blocks end on a single block in some workgroups.
@@ -89,3 +90,25 @@ def test_forward_qkv_bias(dtype, gpu):
     else:
         ma, cs = max_abs(y, ref), cosine(y, ref)
         assert ma <= 2e-2 and cs >= 0.9995, f"qkv_bias bf16: max-abs {ma:.3e} cos {cs:.6f}"
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_forward_llama3_rope(dtype, gpu):
+    from bolt3_amd import Bolt3Attn
+    rs = {"rope_type": "llama3", "factor": 32.0, "low_freq_factor": 1.0, "high_freq_factor": 4.0,
+          "original_max_position_embeddings": 8192}
+    cfg = dict(dim=128, num_heads=4, num_kv_heads=2, head_dim=64, rope_theta=500000.0, eps=1e-5, qk_norm=True,
+               rope_scaling=rs)
+    print(f"[case] forward llama3 RoPE {dtype} T=700", flush=True)
+    mod = recipes.init_module(Bolt3Attn(cfg), 15, nondefault=True).to(dtype)
+    assert not torch.equal(mod.rope.inv_freq.cpu(), O.rope_inv_freq(64, 500000.0))   # the scaling is in effect
+    x = recipes.hidden(15, 2, 700, cfg["dim"]).to(dtype)
+    with torch.no_grad():
+        ref = O.forward(O.Bolt3Params.from_module(mod), x, ties="index")
+        y = mod.to(gpu)(x.to(gpu)).cpu()
+    if dtype == torch.float32:
+        e = rel_err(y, ref)
+        assert e <= 1e-4, f"llama3 fp32: rel err {e:.3e}"
+    else:
+        ma, cs = max_abs(y, ref), cosine(y, ref)
+        assert ma <= 2e-2 and cs >= 0.9995, f"llama3 bf16: max-abs {ma:.3e} cos {cs:.6f}"

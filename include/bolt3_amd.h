@@ -41,8 +41,18 @@ enum {
   B3_LOG_KEEP = 10,    /* keep value per slot                        */
   B3_LOG_TOPVAL = 11,
   B3_LOG_BOTVAL = 12,
-  B3_LOG_ROWS = 13,
+  B3_LOG_INFO = 13,    /* column 0: B3_TIE_* bits of the step         */
+  B3_LOG_ROWS = 14,
   B3_LOG_COLS = 256
+};
+
+/* Tie handling of a consolidation step (B3_LOG_INFO, column 0).  Orderings are ranks; where
+ * exactly equal values decide which token takes which slot, the order among them is the
+ * reference's torch.topk order on the CPU (nth_element + sort, or partial_sort), restated. */
+enum {
+  B3_TIE_TOP = 1,      /* equal candidate (or fill) scores in the deciding prefix: reference order used */
+  B3_TIE_BOT = 2,      /* equal keep values in the deciding prefix: reference order used */
+  B3_TIE_LIMIT = 4     /* the library's depth-limit heap fallback would run: order not restated */
 };
 
 /* [B][heads][t][HD] output view: element (b, h, t, d) at p + b*sb + h*sh + t*HD + d. */

@@ -543,10 +543,11 @@ class HybridRef:
     UniversalVSALM attribute names (embed_tokens, blocks[i].{norm1,norm2,mlp,vsa|attn},
     norm, lm_head)."""
 
-    def __init__(self, model, C: int = 128, ties: str = "torch"):
+    def __init__(self, model, C: int = 128, ties: str = "torch", logs: dict | None = None):
         self.model = model
         self.C = C
         self.ties = ties
+        self.logs = logs            # optional {layer: [decision log of each consolidation]}
         self.params = {}
         for li, blk in enumerate(model.blocks):
             if hasattr(blk, "vsa"):
@@ -571,7 +572,8 @@ class HybridRef:
             h = blk.norm1(x)
             if li in self.params:
                 ms, cache = state[li]
-                _, out, ms = layer_step(self.params[li], h, pos_start, ms, cache, ties=self.ties)
+                lg = None if self.logs is None else self.logs.setdefault(li, [])
+                _, out, ms = layer_step(self.params[li], h, pos_start, ms, cache, log=lg, ties=self.ties)
                 state[li][0] = ms
                 x = x + out
             else:

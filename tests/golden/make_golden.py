@@ -139,16 +139,29 @@ CASES = [
     ("fwd_bf16_clustered", (64, 4, 2, 64, 10000.0, 1e-5, True, False), 1, 2048, 5, "bfloat16", True,
      dict(n_centres=24, noise=0.12), 1),
     ("fwd_cfg1_smollm", (576, 9, 3, 64, 10000.0, 1e-5, False, False), 1, 1024, 0, "float32", False, None, 8),
+    # the consolidation-heavy configuration's kernel (bf16, head_dim 128, eight kv heads, theta 1e6): about
+    # half the tokens merge, a third replace slots, the rest go to M_res
+    ("fwd_bf16_clustered_hd128", (256, 16, 8, 128, 1000000.0, 1e-6, True, False), 1, 2048, 8, "bfloat16", True,
+     dict(n_centres=512, noise=0.15), 2),
+]
+DECODER_CASES = [
+    # name, seed, dtype, prompt tokens, decoded tokens
+    ("dec_fp32", 6, "float32", 300, 220),
+    ("dec_bf16", 9, "bfloat16", 300, 220),
 ]
 
 
-def main(ref_root: str):
+def main(ref_root: str, only=()):
     sys.path.insert(0, ref_root)
     torch.set_num_threads(min(8, os.cpu_count() or 1))
     for name, c, B, T, seed, dt, nd, cl, every in CASES:
-        fwd_case(name, layer_cfg(*c), B, T, seed, getattr(torch, dt), nd, cl, every)
-    decoder_case("dec_fp32", seed=6, dtype=torch.float32, n_prompt=300, n_decode=220)
+        if not only or name in only:
+            fwd_case(name, layer_cfg(*c), B, T, seed, getattr(torch, dt), nd, cl, every)
+    for name, seed, dt, n_prompt, n_decode in DECODER_CASES:
+        if not only or name in only:
+            decoder_case(name, seed=seed, dtype=getattr(torch, dt), n_prompt=n_prompt, n_decode=n_decode)
 
 
 if __name__ == "__main__":
-    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference")
+    # python make_golden.py [reference root] [case ...]: all cases, or only the named ones
+    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference", tuple(sys.argv[2:]))

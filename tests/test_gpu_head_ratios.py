@@ -34,7 +34,7 @@ def test_bf16_forward_head_ratios(H, HKV, HD, gpu):
     mod = recipes.init_module(Bolt3Attn(cfg), 11, nondefault=True).to(bf)
     x = recipes.hidden(11, 1, 700, cfg["dim"]).to(bf)
     with torch.no_grad():
-        ref = O.forward(O.Bolt3Params.from_module(mod), x, ties="index")
+        ref = O.forward(O.Bolt3Params.from_module(mod), x, ties="torch")
         y = mod.to(gpu)(x.to(gpu)).cpu()
     ma, cs = max_abs(y, ref), cosine(y, ref)
     assert ma <= 2e-2 and cs >= 0.9995, f"H={H} HKV={HKV} HD={HD}: max-abs {ma:.3e} cos {cs:.6f}"
@@ -47,7 +47,7 @@ def test_fp32_forward_head_dim_128(gpu):
     mod = recipes.init_module(Bolt3Attn(cfg), 12, nondefault=True)
     x = recipes.hidden(12, 2, 700, cfg["dim"])
     with torch.no_grad():
-        ref = O.forward(O.Bolt3Params.from_module(mod), x, ties="index")
+        ref = O.forward(O.Bolt3Params.from_module(mod), x, ties="torch")
         y = mod.to(gpu)(x.to(gpu)).cpu()
     e = rel_err(y, ref)
     assert e <= 1e-4, f"fp32 HD=128: rel err {e:.3e}"
@@ -62,7 +62,7 @@ def test_forward_chunk_lengths(C, dtype, gpu):
     mod = recipes.init_module(Bolt3Attn(cfg, C=C), 13, nondefault=True).to(dtype)
     x = recipes.hidden(13, 2, 900, cfg["dim"]).to(dtype)
     with torch.no_grad():
-        ref = O.forward(O.Bolt3Params.from_module(mod), x, ties="index")
+        ref = O.forward(O.Bolt3Params.from_module(mod), x, ties="torch")
         y = mod.to(gpu)(x.to(gpu)).cpu()
     if dtype == torch.float32:
         e = rel_err(y, ref)
@@ -82,7 +82,7 @@ def test_forward_qkv_bias(dtype, gpu):
     assert mod.q_proj.bias is not None and float(mod.k_proj.bias.detach().float().abs().sum()) > 0
     x = recipes.hidden(14, 2, 700, cfg["dim"]).to(dtype)
     with torch.no_grad():
-        ref = O.forward(O.Bolt3Params.from_module(mod), x, ties="index")
+        ref = O.forward(O.Bolt3Params.from_module(mod), x, ties="torch")
         y = mod.to(gpu)(x.to(gpu)).cpu()
     if dtype == torch.float32:
         e = rel_err(y, ref)
@@ -104,7 +104,7 @@ def test_forward_llama3_rope(dtype, gpu):
     assert not torch.equal(mod.rope.inv_freq.cpu(), O.rope_inv_freq(64, 500000.0))   # the scaling is in effect
     x = recipes.hidden(15, 2, 700, cfg["dim"]).to(dtype)
     with torch.no_grad():
-        ref = O.forward(O.Bolt3Params.from_module(mod), x, ties="index")
+        ref = O.forward(O.Bolt3Params.from_module(mod), x, ties="torch")
         y = mod.to(gpu)(x.to(gpu)).cpu()
     if dtype == torch.float32:
         e = rel_err(y, ref)

@@ -15,13 +15,16 @@ import math
 import pytest
 import torch
 
+from bolt3_amd import _abi as A
 from oracle import bolt3_oracle as O
 from helpers import build_layer, build_model, cosine, fixture, max_abs, rel_err
 
 pytestmark = pytest.mark.gpu
 
-FWD = ["fwd_fp32_default", "fwd_fp32_eta", "fwd_fp32_g3", "fwd_bf16_eta", "fwd_cfg1_smollm"]
+FWD = ["fwd_fp32_default", "fwd_fp32_eta", "fwd_fp32_g3", "fwd_bf16_eta", "fwd_cfg1_smollm",
+       "fwd_fp32_clustered", "fwd_bf16_clustered", "fwd_bf16_clustered_hd128"]
 TIE = 1e-4
+LOG = {name: i for i, name in enumerate(A.LOG_FIELDS)}
 
 
 def _check_out(y, ref, dtype, what, normed=False):
@@ -38,21 +41,151 @@ def _check_out(y, ref, dtype, what, normed=False):
         assert ma <= 2e-2 and cs >= 0.9995, f"{what}: max-abs {ma:.3e} cos {cs:.6f}"
 
 
+def _near(a, b):
+    """A near-tie: two different values within the tolerance of each other (rounding can order
+    them either way).  Exactly equal values are not near-ties: the kernel orders them as the
+    reference does."""
+    return a != b and abs(a - b) <= TIE * max(abs(a), abs(b), 1e-6)
+
+
+def _any_near(vals, n):
+    return any(_near(vals[k], vals[k + 1]) for k in range(min(n, len(vals) - 1)))
+
+
+def _compare_step(lg, log, bh, l, where):
+    """Decisions of one consolidation step: the oracle's log (torch.topk order, the reference's)
+    against the kernel's.  Returns (mismatches, near_ties, tie_rows): a differing decision is a
+    near-tie when its compared values are within 1e-4 of a threshold or of a competitor on
+    either side; tie_rows counts rows where the kernel ordered exactly equal values itself."""
+    mism = near = 0
+    tie_rows = int(sum(1 for r in range(bh) if int(log[r, LOG["info"], 0]) & (A.TIE_TOP | A.TIE_BOT)))
+    for r in range(bh):
+        if int(log[r, LOG["info"], 0]) & A.TIE_LIMIT:
+            mism += 1
+            print(f"  {where} row {r}: tie order left the restatement (depth limit)", flush=True)
+        if lg["kind"] == "fill":
+            picked = lg["picked"][r].tolist()
+            got = [int(t) for t in log[r, LOG["top_tok"], :len(picked)].tolist()]
+            if got != picked:
+                srt = sorted(lg["score"][r].tolist(), reverse=True)
+                gsc = sorted(log[r, LOG["score"], :l].tolist(), reverse=True)
+                if _any_near(srt, len(picked)) or _any_near(gsc, len(picked)):
+                    near += 1
+                else:
+                    mism += 1
+                    print(f"  {where} row {r}: fill order {picked[:8]} vs {got[:8]}", flush=True)
+            continue
+        best, simv, best2 = lg["best"][r].tolist(), lg["sim_v"][r].tolist(), lg["best2"][r].tolist()
+        for j in range(l):
+            mr, mg = bool(lg["merge"][r, j]), bool(log[r, LOG["merge"], j])
+            sr, sg = int(lg["slot"][r, j]), int(log[r, LOG["slot"], j])
+            if mr == mg and (not mr or sr == sg):
+                continue
+            if _near(best[j], O.SIM_K) or _near(simv[j], O.SIM_V) or _near(best[j], best2[j]):
+                near += 1
+            else:
+                mism += 1
+                print(f"  {where} row {r} tok {j}: merge {mr}/{mg} slot {sr}/{sg} best {best[j]:.6f} "
+                      f"simv {simv[j]:.6f}", flush=True)
+        kc = lg["top_vals"].shape[1]
+        win_ref = {(int(a), int(s)) for a, s, w in zip(lg["top_toks"][r], lg["bot_slots"][r], lg["win"][r]) if w}
+        win_got = {(int(a), int(s)) for a, s, w in zip(log[r, LOG["top_tok"], :kc], log[r, LOG["bot_slot"], :kc],
+                                                       log[r, LOG["win"], :kc]) if w}
+        delta_same = lg["delta"][r].tolist() == [bool(v) for v in log[r, LOG["delta"], :l].tolist()]
+        if win_ref != win_got or not delta_same:
+            tv, bv = lg["top_vals"][r].tolist(), lg["bot_vals"][r].tolist()
+            gtv, gbv = log[r, LOG["top_val"], :kc].tolist(), log[r, LOG["bot_val"], :kc].tolist()
+            if any(_near(a, b) for a, b in zip(tv, bv)) or any(_near(a, b) for a, b in zip(gtv, gbv)) or \
+                    _any_near(tv, kc) or _any_near(bv, kc) or _any_near(gtv, kc) or _any_near(gbv, kc):
+                near += 1
+            else:
+                mism += 1
+                print(f"  {where} row {r}: swaps differ {sorted(win_ref ^ win_got)[:6]}", flush=True)
+    return mism, near, tie_rows
+
+
+def _step_has_near_tie(lg) -> bool:
+    """Whether an oracle decision log holds a near-tie anywhere a decision depends on it."""
+    if lg["kind"] == "fill":
+        m = lg["picked"].shape[1]
+        return any(_any_near(sorted(r.tolist(), reverse=True), m + 1) for r in lg["score"])
+    for r in range(lg["best"].shape[0]):
+        best, simv, best2 = lg["best"][r].tolist(), lg["sim_v"][r].tolist(), lg["best2"][r].tolist()
+        if any(_near(b, O.SIM_K) or _near(v, O.SIM_V) or _near(b, c) for b, v, c in zip(best, simv, best2)):
+            return True
+        tv, bv = lg["top_vals"][r].tolist(), lg["bot_vals"][r].tolist()
+        if any(_near(a, b) for a, b in zip(tv, bv)) or _any_near(tv, len(tv)) or _any_near(bv, len(bv)):
+            return True
+    return False
+
+
+def _oracle_departure(tr, g) -> int | None:
+    """First consolidation where this host's CPU oracle leaves the reference's trajectory (the
+    fixture's per-step activity, masses and mean positions), or None.  The fixture was written
+    on another CPU, whose BLAS sums in another order; a departure must sit on a near-tie."""
+    for i, st in enumerate(tr.states):
+        same = torch.equal(st.act.to(torch.uint8), g[f"cons{i}.act"]) and torch.equal(st.mass, g[f"cons{i}.mass"]) \
+            and rel_err(st.pm, g[f"cons{i}.pm"]) <= 1e-6
+        if not same:
+            assert _step_has_near_tie(tr.logs[i]), f"oracle left the reference at step {i} without a near-tie"
+            return i
+    return None
+
+
 @pytest.mark.parametrize("name", FWD)
 def test_forward_matches_golden(name, gpu):
-    """Against the oracle with lowest-index tie resolution, the kernel's rule.  On these inputs
-    that oracle evicts the same slots and inserts the same tokens as the reference (asserted on
-    CPU by test_oracle_ties for the random-data fixtures)."""
+    """The HIP forward against the reference's own output vector and consolidation states, and
+    against the reference's decisions step by step (through the oracle, whose trajectory is the
+    reference's: bit-identical on the CPU that wrote the fixtures).  Exactly equal values are
+    ordered as torch.topk orders them; only near-ties may go either way.  When one does (on the
+    GPU, or in this host's CPU oracle) the trajectories part at that step, and the output is
+    compared with the reference's on every chunk before the first consolidation it touches."""
     g, meta = fixture(name)
     mod, x = build_layer(meta)
+    p = O.Bolt3Params.from_module(mod)
+    tr = O.ForwardTrace()
     with torch.no_grad():
-        ref = O.forward(O.Bolt3Params.from_module(mod), x, ties="index")[:, ::meta["rows_every"]]
-    print(f"[case] {name} B={meta['B']} T={meta['T']} dtype={meta['dtype']} "
-          f"index-tie oracle vs reference vector rel err {rel_err(ref, g['y']):.2e}", flush=True)
+        O.forward(p, x, trace=tr)
+    d_oracle = _oracle_departure(tr, g)
     mod = mod.to(gpu)
+    trace = {}
     with torch.no_grad():
-        y = mod(x.to(gpu)).cpu()
-    _check_out(y[:, ::meta["rows_every"]], ref, x.dtype, name)
+        y = mod(x.to(gpu), _trace=trace).cpu()
+    log = trace["log"].cpu()
+    bh = log.shape[1]
+    mism = near = tie_rows = 0
+    d_gpu = None
+    for i, (lg, chunk) in enumerate(zip(tr.logs, tr.chunks)):
+        if d_oracle is not None and i > d_oracle:
+            break
+        a, b, c = _compare_step(lg, log[i], bh, chunk[0].shape[1], f"{name} step {i}")
+        mism, near, tie_rows = mism + a, near + b, tie_rows + c
+        if b:
+            d_gpu = i
+            break        # a near-tie taken the other way: the trajectories part from here
+    print(f"[decisions] {name}: steps={len(tr.logs)} mismatches={mism} near-ties={near} "
+          f"rows ordered on exact ties={tie_rows} oracle departs at={d_oracle} gpu departs at={d_gpu}", flush=True)
+    assert mism == 0
+    every = meta["rows_every"]
+    if d_oracle is None and d_gpu is None:
+        st = trace["state"]
+        last = len(tr.logs) - 1
+        assert torch.equal(st["act"].cpu().view_as(g[f"cons{last}.act"]), g[f"cons{last}.act"])
+        assert torch.equal(st["mass"].cpu().view_as(g[f"cons{last}.mass"]), g[f"cons{last}.mass"])
+        assert rel_err(st["pm"].cpu(), g[f"cons{last}.pm"].view_as(st["pm"])) <= 1e-6
+        tol_s = 1e-4 if x.dtype == torch.float32 else 1e-2
+        assert rel_err(st["ak"].cpu().float(), g["final.ak"].float().view_as(st["ak"])) <= tol_s
+        assert rel_err(st["av"].cpu().float(), g["final.av"].float().view_as(st["av"])) <= tol_s
+        assert rel_err(trace["m_res"].cpu(), g["final.m_res"].view_as(trace["m_res"])) <= \
+            (1e-4 if x.dtype == torch.float32 else 1e-3)
+        _check_out(y[:, ::every], g["y"], x.dtype, name)
+    else:
+        d = min(v for v in (d_oracle, d_gpu) if v is not None)
+        n_rows = (d + 2) * p.C          # chunks before the first one that reads step d's slots
+        ys, ref = y[:, :n_rows:every], g["y"][:, :(n_rows + every - 1) // every]
+        _check_out(ys, ref, x.dtype, f"{name} first {n_rows} tokens")
+        print(f"[case] {name}: near-tie at step {d}; tokens before {n_rows} match the reference; "
+              f"whole output vs reference rel err {rel_err(y[:, ::every], g['y']):.3e}", flush=True)
 
 
 def _gpu_step(mod, st_in, chunk, gam, b, dev):
@@ -73,86 +206,37 @@ def _gpu_step(mod, st_in, chunk, gam, b, dev):
     kr_d, kp_d, v_d = kr.to(dev).contiguous(), kp.to(dev).contiguous(), v.to(dev).contiguous()
     pos_d, b_d = pos.float().to(dev).contiguous(), beta.float().to(dev).contiguous()
     W, bias, side = mod._packed(dt, dev)
-    log = torch.zeros(1, bh, 13, 256, device=dev)
+    log = torch.zeros(1, bh, A.LOG_ROWS, A.LOG_COLS, device=dev)
     mod._chain(dt, dev, b, kr_d.data_ptr(), kp_d.data_ptr(), v_d.data_ptr(), l * hd, pos_d.data_ptr(),
                b_d.data_ptr(), l, 1, 0, l, l, l, nf, st, m, gam.to(dev), side, log=log)
     torch.cuda.synchronize()
     return {k: t.cpu() for k, t in st.items()}, m.cpu(), log[0].cpu()
 
 
-def _near(a, b):
-    return abs(a - b) <= TIE * max(abs(a), abs(b), 1e-6)
-
-
-@pytest.mark.parametrize("name", ["fwd_fp32_eta", "fwd_fp32_clustered", "fwd_bf16_clustered", "fwd_bf16_eta",
-                                  "fwd_cfg1_smollm"])
+@pytest.mark.parametrize("name", FWD)
 def test_chain_decisions_teacher_forced(name, gpu):
-    """Every consolidation step run on the GPU from the oracle's state before it."""
+    """Every consolidation step run on the GPU from the reference's state before it (the oracle's
+    trajectory, equal to the reference's): decisions bit-exact, exact ties included, near-ties
+    counted; the state after the step equal to the reference's where no near-tie was involved."""
     g, meta = fixture(name)
     mod, x = build_layer(meta)
     p = O.Bolt3Params.from_module(mod)
     tr = O.ForwardTrace()
     with torch.no_grad():
-        O.forward(p, x, trace=tr, ties="index")
+        O.forward(p, x, trace=tr)
     mod = mod.to(gpu)
     gam = O.gamma_delta(p.log_gamma)
     b = meta["B"]
-    ties = mism = compared = 0
+    mism = near = tie_rows = 0
     for i, (chunk, lg) in enumerate(zip(tr.chunks, tr.logs)):
         print(f"[case] {name} step {i} kind={lg['kind']}", flush=True)
         st_prev = tr.states[i - 1] if i > 0 else None
         st, m, log = _gpu_step(mod, st_prev, chunk, gam, b, gpu)
         ref = tr.states[i]
         bh, l = chunk[0].shape[:2]
-        step_tie = False
-        for r in range(bh):
-            if lg["kind"] == "fill":
-                sc = lg["score"][r].tolist()
-                picked = lg["picked"][r].tolist()
-                got = [int(t) for t in log[r, 7, :len(picked)].tolist()]
-                srt = sorted(sc, reverse=True)
-                amb = any(_near(srt[k], srt[k + 1]) for k in range(min(len(picked), len(srt) - 1)))
-                if got != picked:
-                    if amb:
-                        ties += 1
-                        step_tie = True
-                    else:
-                        mism += 1
-                compared += 1
-                continue
-            best, simv = lg["best"][r].tolist(), lg["sim_v"][r].tolist()
-            best2 = lg["best2"][r].tolist()
-            merge_ref, merge_got = lg["merge"][r].tolist(), [bool(v) for v in log[r, 5, :l].tolist()]
-            slot_ref, slot_got = lg["slot"][r].tolist(), [int(v) for v in log[r, 4, :l].tolist()]
-            delta_ref, delta_got = lg["delta"][r].tolist(), [bool(v) for v in log[r, 6, :l].tolist()]
-            for j in range(l):
-                compared += 1
-                if merge_ref[j] != merge_got[j]:
-                    tie = _near(best[j], O.SIM_K) or _near(simv[j], O.SIM_V) or _near(best[j], best2[j])
-                elif merge_ref[j] and slot_ref[j] != slot_got[j]:
-                    tie = _near(best[j], best2[j])
-                else:
-                    continue
-                if tie:
-                    ties += 1
-                    step_tie = True
-                else:
-                    mism += 1
-                    print(f"  mismatch step {i} row {r} tok {j}: merge {merge_ref[j]}/{merge_got[j]} "
-                          f"slot {slot_ref[j]}/{slot_got[j]} best {best[j]:.6f} simv {simv[j]:.6f}", flush=True)
-            tv, bvv = lg["top_vals"][r].tolist(), lg["bot_vals"][r].tolist()
-            boundary = any(_near(tv[k], bvv[k]) for k in range(len(tv)))
-            win_ref = {(int(a), int(s)) for a, s, w in zip(lg["top_toks"][r], lg["bot_slots"][r], lg["win"][r]) if w}
-            kc = len(tv)
-            win_got = {(int(a), int(s)) for a, s, w in zip(log[r, 7, :kc], log[r, 8, :kc], log[r, 9, :kc]) if w}
-            if win_ref != win_got or delta_ref != delta_got:
-                if boundary or step_tie:
-                    ties += 1
-                    step_tie = True
-                else:
-                    mism += 1
-                    print(f"  mismatch step {i} row {r}: wins {sorted(win_ref ^ win_got)}", flush=True)
-        if not step_tie:
+        a, c, t = _compare_step(lg, log, bh, l, f"{name} step {i}")
+        mism, near, tie_rows = mism + a, near + c, tie_rows + t
+        if c == 0:
             assert torch.equal(st["act"].bool(), ref.act), (name, i)
             assert torch.equal(st["mass"], ref.mass), (name, i)
             assert rel_err(st["pm"], ref.pm) <= 1e-6, (name, i)
@@ -161,7 +245,8 @@ def test_chain_decisions_teacher_forced(name, gpu):
             tol_m = 1e-4 if ref.ak.dtype == torch.float32 else 1e-3
             if ref.m_res.abs().max() > 0:
                 assert rel_err(m, ref.m_res) <= tol_m, (name, i, rel_err(m, ref.m_res))
-    print(f"[decisions] {name}: compared={compared} mismatches={mism} near-ties={ties}", flush=True)
+    print(f"[decisions] {name}: steps={len(tr.logs)} mismatches={mism} near-ties={near} "
+          f"rows ordered on exact ties={tie_rows}", flush=True)
     assert mism == 0
 
 
@@ -170,7 +255,8 @@ def _to_oracle_state(st: dict, m: torch.Tensor, nf: int) -> O.SlotState:
                        pm=st["pm"].cpu(), act=st["act"].cpu().bool(), m_res=m.cpu(), n_filled=nf)
 
 
-@pytest.mark.parametrize("name", ["fwd_fp32_clustered", "fwd_bf16_clustered", "fwd_fp32_eta", "fwd_bf16_eta"])
+@pytest.mark.parametrize("name", ["fwd_fp32_clustered", "fwd_bf16_clustered", "fwd_fp32_eta", "fwd_bf16_eta",
+                                  "fwd_bf16_clustered_hd128"])
 def test_chain_kernel_trajectory_checked(name, gpu):
     """The kernel's own trajectory: every step the oracle, started from the kernel's state, must
     make the same decisions (near-ties excepted) and reach the same state; and the one-launch
@@ -180,44 +266,21 @@ def test_chain_kernel_trajectory_checked(name, gpu):
     p = O.Bolt3Params.from_module(mod)
     tr_o = O.ForwardTrace()
     with torch.no_grad():
-        O.forward(p, x, trace=tr_o, ties="index")
+        O.forward(p, x, trace=tr_o)
     mod = mod.to(gpu)
     gam = O.gamma_delta(p.log_gamma)
     b = meta["B"]
-    st_k, nf = None, 0
-    ties = mism = 0
+    st_k = None
+    mism = near = tie_rows = 0
     for i, chunk in enumerate(tr_o.chunks):
         print(f"[case] {name} kernel-trajectory step {i}", flush=True)
         st_g, m_g, log = _gpu_step(mod, st_k, chunk, gam, b, gpu)
         lg = {}
-        ref = O.consolidate(p, st_k, *chunk, gam, b, log=lg, ties="index")
+        ref = O.consolidate(p, st_k, *chunk, gam, b, log=lg)
         bh, l = chunk[0].shape[:2]
-        step_tie = False
-        if lg["kind"] == "steady":
-            for r in range(bh):
-                for j in range(l):
-                    if bool(lg["merge"][r, j]) != bool(log[r, 5, j]) or (
-                            bool(lg["merge"][r, j]) and int(lg["slot"][r, j]) != int(log[r, 4, j])):
-                        if _near(float(lg["best"][r, j]), O.SIM_K) or _near(float(lg["sim_v"][r, j]), O.SIM_V) or \
-                                _near(float(lg["best"][r, j]), float(lg["best2"][r, j])):
-                            ties += 1
-                            step_tie = True
-                        else:
-                            mism += 1
-                kc = lg["top_vals"].shape[1]
-                wr = {(int(a), int(s)) for a, s, w in zip(lg["top_toks"][r], lg["bot_slots"][r], lg["win"][r]) if w}
-                wg = {(int(a), int(s)) for a, s, w in zip(log[r, 7, :kc], log[r, 8, :kc], log[r, 9, :kc]) if w}
-                if wr != wg:
-                    tv, bv = lg["top_vals"][r].tolist(), lg["bot_vals"][r].tolist()
-                    near = any(_near(tv[k], bv[k]) for k in range(kc)) or \
-                        any(_near(bv[k], bv[k + 1]) and bv[k] != bv[k + 1] for k in range(kc - 1)) or \
-                        any(_near(tv[k], tv[k + 1]) and tv[k] != tv[k + 1] for k in range(kc - 1))
-                    if near or step_tie:
-                        ties += 1
-                        step_tie = True
-                    else:
-                        mism += 1
-        if not step_tie:
+        a, c, t = _compare_step(lg, log, bh, l, f"{name} step {i}")
+        mism, near, tie_rows = mism + a, near + c, tie_rows + t
+        if c == 0:
             assert torch.equal(st_g["act"].bool(), ref.act) and torch.equal(st_g["mass"], ref.mass), (name, i)
             assert rel_err(st_g["util"], ref.util) <= 1e-4, (name, i)
             bf = ref.ak.dtype == torch.bfloat16
@@ -225,7 +288,8 @@ def test_chain_kernel_trajectory_checked(name, gpu):
             if ref.m_res.abs().max() > 0:
                 assert rel_err(m_g, ref.m_res) <= (1e-3 if bf else 1e-4), (name, i)
         st_k = _to_oracle_state(st_g, m_g, ref.n_filled)
-    print(f"[decisions] {name} kernel trajectory: mismatches={mism} near-ties={ties}", flush=True)
+    print(f"[decisions] {name} kernel trajectory: mismatches={mism} near-ties={near} "
+          f"rows ordered on exact ties={tie_rows}", flush=True)
     assert mism == 0
     # one launch over all steps (as the forward runs it) == the step-by-step run above
     dt = x.dtype
@@ -261,7 +325,7 @@ def test_attention_from_oracle_states(name, gpu):
     p = O.Bolt3Params.from_module(mod)
     tr = O.ForwardTrace()
     with torch.no_grad():
-        O.forward(p, x, trace=tr, ties="index")
+        O.forward(p, x, trace=tr, ties="torch")
     q_raw, q_rope, k_raw, k_rope, v, beta, eta = tr.heads
     b, T = meta["B"], meta["T"]
     dt = x.dtype
@@ -299,7 +363,7 @@ def test_consolidate_functional_api(gpu):
     mod, x = build_layer(meta)
     p = O.Bolt3Params.from_module(mod)
     tr = O.ForwardTrace()
-    O.forward(p, x, trace=tr, ties="index")
+    O.forward(p, x, trace=tr, ties="torch")
     mod = mod.to(gpu)
     i = 3
     st0, (kr, kp, v, pos, beta) = tr.states[i - 1], tr.chunks[i]
@@ -317,47 +381,81 @@ def test_consolidate_functional_api(gpu):
     assert rel_err(out[6].cpu(), ref.m_res) <= 1e-4
 
 
-def test_decoder_matches_golden(gpu):
-    """Against the oracle decoder with lowest-index tie resolution (the fixture's 96-token vocabulary
-    repeats keys exactly, so saturated redundancy scores tie); the oracle with torch's own tie
-    order reproduces the reference vectors bit for bit (test_oracle_golden)."""
-    g, meta = fixture("dec_fp32")
+@pytest.mark.parametrize("name", ["dec_fp32", "dec_bf16"])
+def test_decoder_matches_golden(name, gpu):
+    """The decoder (chunked prefill, 220 single-token steps, in-decode consolidations) against the
+    reference's own vectors: every step's final hidden state, and the slot state and M_res at
+    the end.  The fixture's 96-token vocabulary repeats keys exactly, so equal redundancy and
+    utility values decide evictions: the kernel orders them as torch.topk does.  Every
+    consolidation's decisions are compared with the oracle's (the reference's trajectory on the
+    CPU that wrote the fixture); after a near-tie taken the other way (by the GPU, or by this
+    host's CPU oracle) only the steps before it are compared with the reference."""
+    g, meta = fixture(name)
     model, ids = build_model(meta)
     from bolt3_amd import Bolt3Decoder
-    refd = O.HybridRef(model, ties="index")
-    n_prompt = meta["n_prompt"]
+    n_prompt, n_dec = meta["n_prompt"], meta["n_decode"]
+    ref_logs = {}
+    refd = O.HybridRef(model, logs=ref_logs)
     with torch.no_grad():
         h, st_ref = refd.prefill(ids[:, :n_prompt])
         hr = [h[:, -1]]
-        for i in range(meta["n_decode"]):
+        ev_ref = [len(ref_logs.get(0, []))]          # consolidations done before each compared step
+        for i in range(n_dec):
             pos = n_prompt + i
             hr.append(refd.step(ids[:, pos:pos + 1], pos, st_ref)[:, -1])
-    ref_h = torch.stack(hr, dim=1)
-    print(f"[case] dec_fp32 index-tie oracle == reference vector: {torch.equal(ref_h, g['h_last'])}", flush=True)
-    g = dict(g)
-    g["h_last"], g["final.m_res"] = ref_h, st_ref[0][0]
-    g["final.act"] = st_ref[0][1].st.act.to(torch.uint8).view_as(g["final.act"])
-    g["final.mass"] = st_ref[0][1].st.mass.view_as(g["final.mass"])
+            ev_ref.append(len(ref_logs.get(0, [])))
+    h_oracle = torch.stack(hr, dim=1)
     model = model.to(gpu)
     dec = Bolt3Decoder(model)
     ids_d = ids.to(gpu)
-    n_prompt = meta["n_prompt"]
+    rec = {}
+    print(f"[case] {name} prefill {n_prompt} + {n_dec} steps", flush=True)
     with torch.no_grad():
-        h, states, kv = dec.prefill(ids_d[:, :n_prompt])
+        states, kv = dec.blank_state(model, ids.shape[0], gpu, max_kv_len=n_prompt + n_dec + 64)
+        for s0 in range(0, n_prompt, dec.C):
+            h, states, kv = dec.step(ids_d[:, s0:min(n_prompt, s0 + dec.C)], s0, states, kv, record=rec)
         hs = [h[:, -1]]
-        for i in range(meta["n_decode"]):
+        for i in range(n_dec):
             pos = n_prompt + i
-            h, states, kv = dec.step(ids_d[:, pos:pos + 1], pos, states, kv)
+            h, states, kv = dec.step(ids_d[:, pos:pos + 1], pos, states, kv, record=rec)
             hs.append(h[:, -1])
     hs = torch.stack(hs, dim=1).cpu()
-    ref = g["h_last"]
-    errs = [rel_err(hs[:, k], ref[:, k]) for k in range(ref.shape[1])]
-    assert max(errs) <= 1e-4, (max(errs), int(torch.tensor(errs).argmax()))
-    st = kv[0]
-    assert st.n_filled == meta["n_filled"]
-    assert torch.equal(st["act"].cpu().to(torch.uint8).view_as(g["final.act"]), g["final.act"])
-    assert torch.equal(st["mass"].cpu().view_as(g["final.mass"]), g["final.mass"])
-    assert rel_err(states[0].cpu(), g["final.m_res"]) <= 1e-4
+    gpu_logs, lgs = rec.get(0, []), ref_logs.get(0, [])
+    assert len(gpu_logs) == len(lgs)
+    mism = near = tie_rows = 0
+    d_gpu = None
+    for e, (gl, lg) in enumerate(zip(gpu_logs, lgs)):
+        a, b, c = _compare_step(lg, gl["log"].cpu(), gl["log"].shape[0], gl["tokens"], f"{name} event {e}")
+        mism, near, tie_rows = mism + a, near + b, tie_rows + c
+        if b:
+            d_gpu = e
+            break
+    fp32 = meta["dtype"] == "float32"
+    close = lambda a, b: rel_err(a, b) <= (1e-5 if fp32 else 1e-2)
+    d_oracle = next((k for k in range(h_oracle.shape[1]) if not close(h_oracle[:, k], g["h_last"][:, k])), None)
+    if d_oracle is not None:            # a consolidation done before that step sat on a near-tie
+        assert any(_step_has_near_tie(lg) for lg in lgs[:ev_ref[d_oracle]]), \
+            f"oracle left the reference at step {d_oracle} without a near-tie"
+    print(f"[decisions] {name}: events={len(lgs)} mismatches={mism} near-ties={near} "
+          f"rows ordered on exact ties={tie_rows} oracle departs at step={d_oracle} gpu departs at event={d_gpu}",
+          flush=True)
+    assert mism == 0
+    n_cmp = hs.shape[1]
+    if d_gpu is not None:
+        n_cmp = min(n_cmp, next(k for k in range(len(ev_ref)) if ev_ref[k] > d_gpu))
+    if d_oracle is not None:
+        n_cmp = min(n_cmp, d_oracle)
+    for k in range(n_cmp):
+        _check_out(hs[:, k], g["h_last"][:, k], hs.dtype, f"{name} step {k}", normed=True)
+    if d_oracle is None and d_gpu is None:
+        st = kv[0]
+        assert st.n_filled == meta["n_filled"]
+        assert torch.equal(st["act"].cpu().to(torch.uint8).view_as(g["final.act"]), g["final.act"])
+        assert torch.equal(st["mass"].cpu().view_as(g["final.mass"]), g["final.mass"])
+        assert rel_err(st["ak"].cpu().float(), g["final.ak"].float().view_as(st["ak"])) <= (1e-5 if fp32 else 1e-2)
+        assert rel_err(states[0].cpu(), g["final.m_res"]) <= (1e-4 if fp32 else 1e-3)
+    else:
+        print(f"[case] {name}: compared with the reference on steps 0..{n_cmp - 1}", flush=True)
 
 
 @pytest.mark.parametrize("dtype,head_dim,heads,qkv_bias", [
@@ -382,7 +480,7 @@ def test_decode_kernel_vs_oracle_layer_step(dtype, head_dim, heads, qkv_bias, gp
     model.load_state_dict(recipes.model_params([(k, tuple(v.shape)) for k, v in model.state_dict().items()], 11),
                           strict=False)
     model = model.to(dtype).eval()
-    ref = O.HybridRef(model, ties="index")
+    ref = O.HybridRef(model, ties="torch")
     import copy
     dev_model = copy.deepcopy(model).to(gpu)
     dec = Bolt3Decoder(dev_model)
@@ -419,7 +517,7 @@ def test_full_size_prefix_consistency(gpu):
     ma, cs = max_abs(y_full[:1, :1024].cpu(), y_pre.cpu()), cosine(y_full[:1, :1024].cpu(), y_pre.cpu())
     assert ma <= 2e-2 and cs >= 0.9995, (ma, cs)
     with torch.no_grad():
-        y_ref = O.forward(O.Bolt3Params.from_module(mod), x[:1, :1024], ties="index")
+        y_ref = O.forward(O.Bolt3Params.from_module(mod), x[:1, :1024], ties="torch")
     _check_out(y_pre.cpu(), y_ref, torch.bfloat16, "cfg2 prefix vs oracle")
 
 
@@ -458,5 +556,5 @@ def test_consolidation_heavy_long_prefill(gpu):
     ma, cs = max_abs(y[:, :2048].cpu(), y_pre.cpu()), cosine(y[:, :2048].cpu(), y_pre.cpu())
     assert ma <= 2e-2 and cs >= 0.9995, (ma, cs)
     with torch.no_grad():
-        y_ref = O.forward(O.Bolt3Params.from_module(mod), x[:, :256], ties="index")
+        y_ref = O.forward(O.Bolt3Params.from_module(mod), x[:, :256], ties="torch")
     _check_out(y_pre[:, :256].cpu(), y_ref, torch.bfloat16, "consolidation-heavy first chunks vs oracle")

@@ -11,11 +11,12 @@ masses, positions) to be identical.
 import pytest
 import torch
 
-from oracle.bolt3_oracle import Bolt3Params, ForwardTrace, HybridRef, consolidate, forward, gamma_delta
+from oracle.bolt3_oracle import Bolt3Params, ForwardTrace, HybridRef, forward
+from oracle.torch_topk_order import tie_in_prefix, topk_order_wave
 from helpers import build_layer, build_model, fixture, rel_err
 
 FWD = ["fwd_fp32_default", "fwd_fp32_eta", "fwd_fp32_g3", "fwd_bf16_eta", "fwd_fp32_clustered",
-       "fwd_bf16_clustered", "fwd_cfg1_smollm"]
+       "fwd_bf16_clustered", "fwd_cfg1_smollm", "fwd_bf16_clustered_hd128"]
 
 
 @pytest.mark.parametrize("name", FWD)
@@ -54,13 +55,15 @@ def test_forward_fp32_bit_exact_here():
         pytest.skip(f"different BLAS rounding on this host (rel {rel_err(y, g['y']):.2e}); tolerance test covers it")
 
 
-def test_clustered_fixture_exercises_merges():
-    g, meta = fixture("fwd_fp32_clustered")
+@pytest.mark.parametrize("name", ["fwd_fp32_clustered", "fwd_bf16_clustered_hd128"])
+def test_clustered_fixture_exercises_merges(name):
+    g, meta = fixture(name)
     assert int((g[f"cons{meta['n_consolidations'] - 1}.mass"] > 1).sum()) > 50
 
 
-def test_decoder_matches_reference():
-    g, meta = fixture("dec_fp32")
+@pytest.mark.parametrize("name", ["dec_fp32", "dec_bf16"])
+def test_decoder_matches_reference(name):
+    g, meta = fixture(name)
     model, ids = build_model(meta)
     ref = HybridRef(model)
     n_prompt = meta["n_prompt"]
@@ -72,58 +75,60 @@ def test_decoder_matches_reference():
             h = ref.step(ids[:, pos:pos + 1], pos, state)
             hs.append(h[:, -1])
     hs = torch.stack(hs, dim=1)
-    assert rel_err(hs, g["h_last"]) <= 1e-5
+    tol = 1e-5 if meta["dtype"] == "float32" else 1e-2
+    assert rel_err(hs, g["h_last"]) <= tol
     ms, cache = state[0]
     assert rel_err(ms, g["final.m_res"]) <= 1e-5
     assert cache.st.n_filled == meta["n_filled"]
     assert torch.equal(cache.st.act.to(torch.uint8), g["final.act"])
     assert torch.equal(cache.st.mass, g["final.mass"])
     assert rel_err(cache.st.ak.float(), g["final.ak"].reshape(cache.st.ak.shape).float()) <= 1e-6
-    assert rel_err(cache.sinks[0], g["final.sink_k"]) <= 1e-6
+    assert rel_err(cache.sinks[0].float(), g["final.sink_k"].float()) <= 1e-6
 
 
-@pytest.mark.parametrize("name", ["fwd_fp32_default", "fwd_fp32_eta", "fwd_fp32_g3", "fwd_bf16_eta",
-                                  "fwd_cfg1_smollm"])
-def test_oracle_ties(name):
-    """Exact ties occur even on random data: two slots that are each other's nearest neighbour
-    and share a utility (every first-fill slot starts at 0.15) have bit-equal keep values.  On
-    these inputs the tie never straddles the replacement boundary, so the two tie rules evict
-    the same slots and insert the same tokens; only which of the tied slots receives which
-    token differs, and the outputs agree to rounding."""
+@pytest.mark.parametrize("name", FWD)
+def test_kernel_tie_order_on_fixture_decisions(name):
+    """Every ordering the reference made on this fixture (torch.topk in the oracle, whose
+    trajectory equals the reference's above) is reproduced by the kernel's wave-parallel
+    restatement of torch's order, including the steps where exactly equal values decide which
+    token takes which slot."""
     g, meta = fixture(name)
     mod, x = build_layer(meta)
     p = Bolt3Params.from_module(mod)
     tr = ForwardTrace()
     with torch.no_grad():
         forward(p, x, trace=tr)
-        y = forward(p, x, ties="index")[:, ::meta["rows_every"]]
-    tol = 1e-6 if meta["dtype"] == "float32" else 1e-2
-    assert rel_err(y, g["y"]) <= tol
-    gam = gamma_delta(p.log_gamma)
-    for i, (chunk, a) in enumerate(zip(tr.chunks, tr.logs)):
-        if a["kind"] != "steady":
+    n_tied = 0
+    for lg in tr.logs:
+        if lg["kind"] == "fill":
+            m = lg["picked"].shape[1]
+            for r in range(lg["score"].shape[0]):
+                assert topk_order_wave(lg["score"][r].tolist(), m, True)[0] == lg["picked"][r].tolist()
             continue
-        b = {}
-        consolidate(p, tr.states[i - 1], *chunk, gam, meta["B"], log=b, ties="index")
-        assert torch.equal(a["merge"], b["merge"]) and torch.equal(a["delta"], b["delta"])
-        for r in range(a["win"].shape[0]):
-            sets = [({int(t) for t, w in zip(lg["top_toks"][r], lg["win"][r]) if w},
-                     {int(t) for t, w in zip(lg["bot_slots"][r], lg["win"][r]) if w}) for lg in (a, b)]
-            assert sets[0] == sets[1], (name, i, r)
+        cand = torch.where(lg["merge"], torch.full_like(lg["score"], -1e9), lg["score"])
+        kc = lg["top_toks"].shape[1]
+        for r in range(cand.shape[0]):
+            assert topk_order_wave(cand[r].tolist(), kc, True)[0] == lg["top_toks"][r].tolist()
+            assert topk_order_wave(lg["keep"][r].tolist(), kc, False)[0] == lg["bot_slots"][r].tolist()
+            n_win = int(lg["win"][r].sum())
+            n_tied += tie_in_prefix(lg["top_vals"][r].tolist(), n_win) or \
+                tie_in_prefix(lg["bot_vals"][r].tolist(), n_win)
+    print(f"{name}: steady rows where equal values decide a swap: {n_tied}")
 
 
 def test_clustered_data_has_exact_ties():
-    """Clustered keys saturate the redundancy clamp (keep = 0.02 * util for many slots at once) and
-    merge whole chunks (candidate score -1e9), so torch.topk's order among equal values decides
-    which slot is evicted; the two tie rules then follow different (equally valid) trajectories."""
-    g, meta = fixture("fwd_fp32_clustered")
+    """Clustered keys saturate the redundancy clamp (keep = 0.02 * util for many slots at once)
+    and slots of equal utility are mutual nearest neighbours, so exactly equal keep values fall
+    inside the replacement prefix: there torch.topk's order among equal values decides which
+    slot is evicted, and the kernel must follow it (previous test)."""
+    g, meta = fixture("fwd_bf16_clustered_hd128")
     mod, x = build_layer(meta)
     tr = ForwardTrace()
     with torch.no_grad():
-        forward(Bolt3Params.from_module(mod), x, trace=tr, ties="index")
+        forward(Bolt3Params.from_module(mod), x, trace=tr)
     n_tied = 0
     for lg in tr.logs:
         if lg["kind"] == "steady":
-            bv = lg["bot_vals"]
-            n_tied += int((bv[:, 1:] == bv[:, :-1]).sum())
+            for r in range(lg["bot_vals"].shape[0]):
+                n_tied += tie_in_prefix(lg["bot_vals"][r].tolist(), int(lg["win"][r].sum()))
     assert n_tied > 0

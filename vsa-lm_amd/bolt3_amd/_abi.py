@@ -16,9 +16,10 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libbolt3_am
 B3_F32, B3_BF16 = 0, 1
 ERRORS = {1001: "invalid argument", 1002: "unsupported shape or dtype", 1003: "workspace too small"}
 
-LOG_ROWS, LOG_COLS = 13, 256
+LOG_ROWS, LOG_COLS = 14, 256
 LOG_FIELDS = ("rel", "score", "best", "simv", "slot", "merge", "delta", "top_tok", "bot_slot", "win", "keep",
-              "top_val", "bot_val")
+              "top_val", "bot_val", "info")
+TIE_TOP, TIE_BOT, TIE_LIMIT = 1, 2, 4
 
 p = C.c_void_p
 i32 = C.c_int32

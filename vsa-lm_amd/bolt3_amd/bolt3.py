@@ -642,7 +642,8 @@ class Bolt3Decoder:
 
     # ------------------------------------------------------------ one Bolt-3 layer
 
-    def _bolt3_layer(self, ly: Bolt3Attn, h, pos_start: int, m_state: torch.Tensor, st: Bolt3LayerState):
+    def _bolt3_layer(self, ly: Bolt3Attn, h, pos_start: int, m_state: torch.Tensor, st: Bolt3LayerState,
+                     record=None):
         B, t, _ = h.shape
         dt, dev = h.dtype, h.device
         if dt != st.dtype:
@@ -703,7 +704,7 @@ class Bolt3Decoder:
                 A.call("bolt3_decode_layer", call_args, dev)
                 st.cur = (cs, cl + 1)
                 if st.cur[1] >= ly.C:
-                    self._consolidate(ly, st, m_state, gam, side)
+                    self._consolidate(ly, st, m_state, gam, side, record)
                 return out
             lin = F.linear(h, W, bias)
             a.lin = lin.data_ptr()
@@ -736,10 +737,10 @@ class Bolt3Decoder:
         st.cur = (cs, cl + t)
         out = F.linear(y, side["wo"])
         if st.cur[1] >= ly.C:
-            self._consolidate(ly, st, m_state, gam, side)
+            self._consolidate(ly, st, m_state, gam, side, record)
         return out
 
-    def _consolidate(self, ly: Bolt3Attn, st: Bolt3LayerState, m_state, gam, side):
+    def _consolidate(self, ly: Bolt3Attn, st: Bolt3LayerState, m_state, gam, side, record=None):
         ps, pl = st.prev
         if pl > 0:
             off, l = ps, pl
@@ -753,10 +754,14 @@ class Bolt3Decoder:
                 for k, v in ly._empty_slots(st.B * st.HKV, st.dtype, m_state.device).items():
                     st.slots[k].copy_(v)
                 m_state.zero_()
+            log = None
+            if record is not None:
+                log = torch.zeros(1, st.B * st.HKV, A.LOG_ROWS, A.LOG_COLS, device=m_state.device)
+                record.append(dict(log=log[0], n_filled=st.n_filled, tokens=l))
             ly._chain(st.dtype, m_state.device, st.B, st.win_kr.data_ptr(), st.win_kp.data_ptr(),
                       st.win_v.data_ptr(), st.cap * st.HD, st.win_pos.data_ptr(), st.win_b.data_ptr(), st.cap,
                       1, off, l, l, l, st.n_filled, st.slots, m_state, gam, side,
-                      snap_k=st.slot_k, snap_bias=st.slot_bias, kp_exact=True)
+                      snap_k=st.slot_k, snap_bias=st.slot_bias, kp_exact=True, log=log)
             if st.n_filled < ly.S:
                 st.n_filled += min(ly.S - st.n_filled, l)
             st.has_slots = True
@@ -774,7 +779,10 @@ class Bolt3Decoder:
         for li, blk in enumerate(m.blocks):
             h = blk.norm1(x)
             if hasattr(blk, "vsa"):
-                x = x + self._bolt3_layer(blk.vsa, h, pos_start, states[li], kv_caches[li])
+                rec = None
+                if record is not None:
+                    rec = record.setdefault(li, []) if isinstance(record, dict) else record
+                x = x + self._bolt3_layer(blk.vsa, h, pos_start, states[li], kv_caches[li], rec)
             else:
                 ly = blk.attn
                 q, k, v = ly.head_qkv(h)

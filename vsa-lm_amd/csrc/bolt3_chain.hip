@@ -40,6 +40,7 @@ namespace b3 {
 
 constexpr int S = 128;     // attractor slots
 constexpr int LMAX = 256;  // tokens per consolidation step
+constexpr int TIE_STACK = 32;  // pending ranges of the tie-order sort
 constexpr int DT = 512;    // decide_kernel threads
 constexpr int DWAVES = DT / WAVE;
 constexpr int MT = 256;    // gersh_kernel / mres_kernel threads
@@ -84,6 +85,7 @@ struct DecSmem {
   float tnn[S];   // bf16 scoring: 1/|ak|, 0 for slots masked in a fill step
   int act[S], dirty[S], vdirty[S];
   int any_merge;
+  int tie;   // this step's tie handling: B3_TIE_* bits
   float invf[HD / 2];
   float rel[LMAX], score[LMAX];
   float tpos[LMAX], tbeta[LMAX];   // this step's token positions and delta-rule gates
@@ -114,6 +116,11 @@ struct DecSmem {
     } mg;
     struct { float mx[2][S]; int nan[2][S]; } kp;
     struct { alignas(16) uint64_t a[LMAX]; alignas(16) uint64_t b[S]; } ok;
+    struct {   // tie order (one wavefront per ordering): packed elements, stop positions, ranges
+      alignas(16) uint64_t e[2][LMAX];
+      int pr[2][LMAX + 1];
+      int stk[2][3 * TIE_STACK];
+    } to;
   } u;
 };
 static_assert(sizeof(DecSmem<uint16_t, 128>) <= 160 * 1024, "decide_kernel LDS");
@@ -281,6 +288,255 @@ __device__ __forceinline__ int count_below(const uint64_t* keys, int i0, int i1,
   }
   for (; i < i1; ++i) r += keys[i] < x ? 1 : 0;
   return r;
+}
+
+// ----------------------------------------------------------------- the reference's tie order
+//
+// The reference orders with torch.topk on the CPU (vsa_lm/config/bolt3.py:137-138, :183).
+// Among exactly equal values its order is that of the C++ library's algorithms it runs
+// (aten TopKImpl.h): nth_element at k-1 followed by sort of the first k-1 elements
+// (introselect / introsort: median-of-three pivot moved to the front, unguarded Hoare
+// partition, ranges of at most 16 (sort) or 3 (select) elements finished by insertion sort),
+// or partial_sort (a heap of k elements) when 64*k <= n.  tie_order_wave restates that order
+// on one wavefront, so the kernel's slot decisions follow the reference on ties too:
+//  * one Hoare partition in one pass: the left scan stops, in ascending position, at the
+//    elements not ordered before the pivot (L), the right scan, descending, at those not
+//    ordered after it (R); the i-th L and the i-th R swap while the L lies below the R (m
+//    swaps), and the cut is the (m+1)-th L or the m-th R, whichever is lower.  Ballots and
+//    prefix counts rank every stop, so the swaps are done at once;
+//  * the ranges sort leaves to insertion sort keep equal elements in their order after the
+//    partitions, and insertion sort is stable, so a stable rank of the whole sorted range
+//    gives the final order;
+//  * partial_sort (k <= 4) runs its heap steps uniformly on the whole wavefront.
+// Elements are packed as (key << 32 | source index) with a 32-bit key that is lowest for the
+// element that comes first (NaN first when largest, last otherwise; -0 equals +0, as in a float
+// comparison).  A depth limit reached (heap fallback of the library, not restated) sets bit 0
+// of the returned flags.
+__device__ __forceinline__ void wave_lds_fence() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+__device__ __forceinline__ uint32_t tie_key(float v, bool largest) {
+  const uint32_t k = ord_key(v + 0.0f);
+  return largest ? ~k : k;
+}
+__device__ __forceinline__ uint32_t pk_key(uint64_t e) { return (uint32_t)(e >> 32); }
+
+// Median-of-three move and Hoare partition of e[f, l) (l - f > 3); returns the cut.
+__device__ int tie_partition(uint64_t* e, int* pr, int f, int l, int lane, int& flags) {
+  const int a = f + 1, b = f + (l - f) / 2, c = l - 1;
+  const uint32_t ka = pk_key(e[a]), kb = pk_key(e[b]), kc = pk_key(e[c]);
+  int t;
+  if (ka < kb) t = kb < kc ? b : (ka < kc ? c : a);
+  else t = ka < kc ? a : (kb < kc ? c : b);
+  const uint64_t ef = e[f], et = e[t];
+  wave_lds_fence();
+  if (lane == 0) {
+    e[f] = et;
+    e[t] = ef;
+  }
+  wave_lds_fence();
+  const uint32_t piv = pk_key(et);
+  const unsigned long long below = (1ull << lane) - 1ull;
+  uint64_t x[4];
+  bool lf[4], rf[4];
+  unsigned long long bl[4], br[4];
+  int tot_r = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int q = a + lane + WAVE * j;
+    x[j] = 0ull;
+    if (q < l) x[j] = e[q];
+    const uint32_t k = pk_key(x[j]);
+    lf[j] = q < l && k >= piv;
+    rf[j] = q < l && k <= piv;
+    bl[j] = __ballot(lf[j]);
+    br[j] = __ballot(rf[j]);
+    tot_r += __popcll(br[j]);
+  }
+  int cl = 0, cr = 0, m = 0;
+  int rank_l[4], above[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    rank_l[j] = cl + __popcll(bl[j] & below) + 1;
+    above[j] = tot_r - (cr + __popcll(br[j] & below) + (rf[j] ? 1 : 0));   // R stops above q
+    cl += __popcll(bl[j]);
+    cr += __popcll(br[j]);
+    m += __popcll(__ballot(lf[j] && above[j] >= rank_l[j]));
+  }
+  const int tot_l = cl;
+  // pr[i] = position of the i-th right stop (i <= m); pr[0] = the (m+1)-th left stop
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int q = a + lane + WAVE * j;
+    if (rf[j] && above[j] + 1 <= m) pr[above[j] + 1] = q;
+    if (lf[j] && rank_l[j] == m + 1) pr[0] = q;
+  }
+  wave_lds_fence();
+  uint64_t y[4];
+  int pp[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    pp[j] = 0;
+    y[j] = 0ull;
+    if (lf[j] && rank_l[j] <= m) {
+      pp[j] = pr[rank_l[j]];
+      y[j] = e[pp[j]];
+    }
+  }
+  const int l_next = tot_l > m ? pr[0] : INT_MAX;
+  const int r_m = m > 0 ? pr[m] : INT_MAX;
+  wave_lds_fence();
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if (lf[j] && rank_l[j] <= m) {
+      e[a + lane + WAVE * j] = y[j];
+      e[pp[j]] = x[j];
+    }
+  }
+  wave_lds_fence();
+  int cut = min(l_next, r_m);
+  if (cut == INT_MAX) {   // no left stop at all: cannot happen after a median-of-three move
+    flags |= 1;
+    cut = l;
+  }
+  return __builtin_amdgcn_readfirstlane(cut);
+}
+
+// Stable order of e[f, l) by key, in place (insertion sort's result).
+__device__ void tie_stable_range(uint64_t* e, int f, int l, int lane) {
+  uint64_t x[4];
+  int r[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int i = f + lane + WAVE * j;
+    x[j] = 0ull;
+    r[j] = 0;
+    if (i < l) x[j] = e[i];
+  }
+  for (int t = f; t < l; ++t) {
+    const uint64_t y = e[t];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int i = f + lane + WAVE * j;
+      r[j] += (pk_key(y) < pk_key(x[j]) || (pk_key(y) == pk_key(x[j]) && t < i)) ? 1 : 0;
+    }
+  }
+  wave_lds_fence();
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    if (f + lane + WAVE * j < l) e[f + r[j]] = x[j];
+  wave_lds_fence();
+}
+
+// Heap steps of the library's partial_sort, executed alike by every lane (k <= 4, so the heap
+// is a few LDS words; the same value is stored by every lane).
+__device__ __forceinline__ void heap_put(uint64_t* e, int i, uint64_t v) {
+  e[i] = v;
+  wave_lds_fence();
+}
+__device__ void heap_adjust(uint64_t* e, int hole, int len, uint64_t v) {
+  const int top = hole;
+  int child = hole;
+  while (child < (len - 1) / 2) {
+    child = 2 * (child + 1);
+    if (pk_key(e[child]) < pk_key(e[child - 1])) child--;
+    heap_put(e, hole, e[child]);
+    hole = child;
+  }
+  if ((len & 1) == 0 && child == (len - 2) / 2) {
+    child = 2 * (child + 1);
+    heap_put(e, hole, e[child - 1]);
+    hole = child - 1;
+  }
+  int parent = (hole - 1) / 2;
+  while (hole > top && pk_key(e[parent]) < pk_key(v)) {
+    heap_put(e, hole, e[parent]);
+    hole = parent;
+    parent = (hole - 1) / 2;
+  }
+  heap_put(e, hole, v);
+}
+__device__ void heap_pop(uint64_t* e, int len, int res) {
+  const uint64_t v = e[res];
+  heap_put(e, res, e[0]);
+  heap_adjust(e, 0, len, v);
+}
+
+// torch.topk's order of the k first elements of e[0, n) (packed with tie_key): source indices
+// into out[0, k).  One wavefront; pr holds LMAX + 1 ints, stk 3 * TIE_STACK ints.
+__device__ int tie_order_wave(uint64_t* e, int* pr, int* stk, int n, int k, int* out, int lane) {
+  int flags = 0;
+  if (k <= 0) return 0;
+  wave_lds_fence();
+  if (k * 64 <= n) {
+    if (k >= 2)
+      for (int parent = (k - 2) / 2;; --parent) {
+        heap_adjust(e, parent, k, e[parent]);
+        if (parent == 0) break;
+      }
+    for (int i = k; i < n; ++i)
+      if (pk_key(e[i]) < pk_key(e[0])) heap_pop(e, k, i);
+    for (int last = k; last > 1;) {
+      --last;
+      heap_pop(e, last, last);
+    }
+  } else {
+    // nth_element at k - 1
+    int f = 0, l = n, depth = 2 * (31 - __clz(n));
+    while (l - f > 3) {
+      if (depth == 0) {
+        flags |= 1;
+        break;
+      }
+      --depth;
+      const int cut = tie_partition(e, pr, f, l, lane, flags);
+      if (cut <= k - 1) f = cut;
+      else l = cut;
+    }
+    tie_stable_range(e, f, l, lane);
+    // sort of [0, k - 1): the ranges above 16 elements are partitioned, the rest is left in
+    // place for the final insertion sort
+    const int ks = k - 1;
+    if (ks > 16) {
+      if (lane == 0) {
+        stk[0] = 0;
+        stk[1] = ks;
+        stk[2] = 2 * (31 - __clz(ks));
+      }
+      wave_lds_fence();
+      int sp = 1;
+      while (sp > 0) {
+        --sp;
+        const int sf = stk[3 * sp], sl = stk[3 * sp + 1], d = stk[3 * sp + 2];
+        wave_lds_fence();
+        if (sl - sf <= 16) continue;
+        if (d == 0 || sp + 2 > TIE_STACK) {
+          flags |= 1;
+          continue;
+        }
+        const int cut = tie_partition(e, pr, sf, sl, lane, flags);
+        if (lane == 0) {
+          stk[3 * sp + 0] = cut;
+          stk[3 * sp + 1] = sl;
+          stk[3 * sp + 2] = d - 1;
+          stk[3 * sp + 3] = sf;
+          stk[3 * sp + 4] = cut;
+          stk[3 * sp + 5] = d - 1;
+        }
+        sp += 2;
+        wave_lds_fence();
+      }
+    }
+    tie_stable_range(e, 0, ks, lane);
+  }
+  for (int i = lane; i < k; i += WAVE) out[i] = (int)(uint32_t)e[i];
+  wave_lds_fence();
+  return flags;
+}
+
+// Whether sorted[i] equals a neighbour of the sorted array (length n), by order key.
+__device__ __forceinline__ bool tie_at(const float* sorted, int i, int n) {
+  const uint32_t k = ord_key(sorted[i] + 0.0f);
+  return (i > 0 && ord_key(sorted[i - 1] + 0.0f) == k) || (i + 1 < n && ord_key(sorted[i + 1] + 0.0f) == k);
 }
 
 // ----------------------------------------------------------------- decide: helpers
@@ -988,7 +1244,10 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
     const float pos_t = tid < l ? pos[tid] : 0.f;
     const float beta_t = tid < l ? beta[tid] : 0.f;
 
-    if (tid == 0) sm.any_merge = 0;
+    if (tid == 0) {
+      sm.any_merge = 0;
+      sm.tie = 0;
+    }
     if (tid < S) {
       sm.util[tid] = mul_rn(sm.util[tid], UTIL_DECAY);
       const float lm = logf(fmaxf(sm.mass[tid], 1.0f));
@@ -1068,6 +1327,18 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
         }
       }
       sync_lds();
+      // exactly equal scores among the picked tokens or at the cut: the reference's order
+      if (tid < m && tie_at(sm.sk_a, tid, l)) atomicOr(&sm.tie, B3_TIE_TOP);
+      sync_lds();
+      if (sm.tie) {
+        if (wave == 0) {
+          for (int j = lane; j < l; j += WAVE)
+            sm.u.to.e[0][j] = ((uint64_t)tie_key(sm.score[j], true) << 32) | (uint32_t)j;
+          const int fl = tie_order_wave(sm.u.to.e[0], sm.u.to.pr[0], sm.u.to.stk[0], l, m, sm.si_a, lane);
+          if (fl && lane == 0) atomicOr(&sm.tie, B3_TIE_LIMIT);
+        }
+        sync_lds();
+      }
       // slots nf + i <- token si_a[i]
       for (int it = tid; it < m * (HD / 8); it += DT) {
         const int i = it / (HD / 8), d8 = (it % (HD / 8)) * 8;
@@ -1090,6 +1361,7 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
           log[B3_LOG_REL * B3_LOG_COLS + j] = j < l ? sm.rel[j] : 0.f;
           log[B3_LOG_SCORE * B3_LOG_COLS + j] = j < l ? sm.score[j] : 0.f;
           log[B3_LOG_TOPTOK * B3_LOG_COLS + j] = j < m ? (float)sm.si_a[j] : -1.f;
+          log[B3_LOG_INFO * B3_LOG_COLS + j] = j == 0 ? (float)sm.tie : 0.f;
         }
       }
       nf += m;
@@ -1317,6 +1589,28 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
       sync_lds();
       prefetch(step, wave, lane, 4);
       const int kc = min(l, S);
+      // Exactly equal values where they decide a swap (win_i is a prefix of the ranks, and the
+      // values by rank do not depend on the order among equal ones): the reference's order.
+      if (tid < kc && sm.sk_a[tid] > sm.sk_b[tid] && sm.sk_a[tid] > -1e8f) {
+        if (tie_at(sm.sk_a, tid, l)) atomicOr(&sm.tie, B3_TIE_TOP);
+        if (tie_at(sm.sk_b, tid, S)) atomicOr(&sm.tie, B3_TIE_BOT);
+      }
+      sync_lds();
+      if (const int tie = sm.tie) {
+        int fl = 0;
+        if (wave == 0 && (tie & B3_TIE_TOP)) {
+          for (int j = lane; j < l; j += WAVE)
+            sm.u.to.e[0][j] = ((uint64_t)tie_key(cand_value(sm, j), true) << 32) | (uint32_t)j;
+          fl = tie_order_wave(sm.u.to.e[0], sm.u.to.pr[0], sm.u.to.stk[0], l, kc, sm.si_a, lane);
+        }
+        if (wave == 1 && (tie & B3_TIE_BOT)) {
+          for (int j = lane; j < S; j += WAVE)
+            sm.u.to.e[1][j] = ((uint64_t)tie_key(sm.keep[j], false) << 32) | (uint32_t)j;
+          fl = tie_order_wave(sm.u.to.e[1], sm.u.to.pr[1], sm.u.to.stk[1], S, kc, sm.si_b, lane);
+        }
+        if (fl && lane == 0) atomicOr(&sm.tie, B3_TIE_LIMIT);
+        sync_lds();
+      }
       // win_i = top_i > bot_i and top_i > -1e8 ; token top_i replaces slot bot_i
       if (tid < kc) {
         const float tv = sm.sk_a[tid], bv = sm.sk_b[tid];
@@ -1367,6 +1661,7 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
           log[B3_LOG_KEEP * B3_LOG_COLS + j] = j < S ? sm.keep[j] : 0.f;
           log[B3_LOG_TOPVAL * B3_LOG_COLS + j] = j < kc ? sm.sk_a[j] : 0.f;
           log[B3_LOG_BOTVAL * B3_LOG_COLS + j] = j < kc ? sm.sk_b[j] : 0.f;
+          log[B3_LOG_INFO * B3_LOG_COLS + j] = j == 0 ? (float)sm.tie : 0.f;
         }
       }
     }

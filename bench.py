@@ -172,9 +172,17 @@ def bench_long(dev, reps=3, T_long=65536):
     with torch.no_grad():
         trace = {}
         mod(x, _trace=trace)                                # warm-up, and the decision log
-        steady = trace["log"][4:, :, :, :128]
-        merged, to_m = float(steady[:, :, 5].mean()), float(steady[:, :, 6].mean())
-        del trace
+        log = trace["log"]
+        steady = log[4:, :, :, :128]
+        merged = float(steady[:, :, _abi.LOG_FIELDS.index("merge")].mean())
+        to_m = float(steady[:, :, _abi.LOG_FIELDS.index("delta")].mean())
+        # rows (step, kv head) where exactly equal values decided a swap or a fill, ordered as the
+        # reference's torch.topk orders them; and rows where that order would leave the restatement
+        info = log[:, :, _abi.LOG_FIELDS.index("info"), 0].to(torch.int32)
+        tie_rows = int(((info & (_abi.TIE_TOP | _abi.TIE_BOT)) != 0).sum())
+        limit_rows = int(((info & _abi.TIE_LIMIT) != 0).sum())
+        rows = int(info.numel())
+        del trace, log
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for _ in range(reps):
@@ -190,6 +198,7 @@ def bench_long(dev, reps=3, T_long=65536):
     return dict(batch=1, seq_len=T_long, consolidation_steps=n_steps, ms_per_forward=round(ms, 3),
                 tokens_per_s=round(T_long / (ms * 1e-3), 1), chain_ms_per_forward=round(chain_ms, 3),
                 merged_share=round(merged, 3), m_res_share=round(to_m, 3),
+                exact_tie_rows=tie_rows, tie_order_limit_rows=limit_rows, decision_rows=rows,
                 data="synthetic clustered hidden states (512 centres, noise 0.15, Zipf 1.1)")
 
 

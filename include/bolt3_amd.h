@@ -158,6 +158,27 @@ int bolt3_chain(const b3_chain_args* a, void* stream);
    slot keys (B*HKV x S x HD floats). */
 int64_t bolt3_chain_workspace_bytes(int32_t dtype, int32_t B, int32_t HKV, int32_t HD, int32_t S, int32_t n_steps);
 
+typedef struct {
+  int32_t dtype, B, HKV, HD, S;
+  const void* ak;             /* [bh][S][HD] un-roped slot keys (storage dtype) */
+  const float* pm;            /* [bh][S] mean positions */
+  const float* mass;          /* [bh][S] */
+  const uint8_t* act;         /* [bh][S] */
+  const float* kappa;         /* [HKV] */
+  const float* inv_freq;      /* [HD/2] */
+  void* slot_k;               /* out: [bh][S][HD] slot keys roped at their mean positions */
+  float* slot_bias;           /* out: [bh][S] kappa*log(max(mass,1)), -inf where inactive */
+} b3_slot_keys_args;
+
+/*
+ * The slot field's keys and bias as the attention reads them, from a slot state (with the
+ * chain's own RoPE rounding).  The decoder keeps them cached and the chain refreshes them; this
+ * rebuilds them for a state restored from the reference's kv_caches dict.
+ * Replaces the attractor RoPE and bias of vsa_lm/config/bolt3.py:383-388 (recomputed there at
+ * every step) and :236-241.  S == 128, HD in {64, 128}.
+ */
+int bolt3_slot_keys(const b3_slot_keys_args* a, void* stream);
+
 /*
  * Holds `stream` until *counter has reached `target` (compared modulo 2^32) or after max_polls
  * polls (each a device-scope read and a short sleep), whichever comes first.  No counterpart in the reference (its chain

@@ -604,3 +604,79 @@ class HybridRef:
         for s0 in range(0, ids.shape[1], self.C):
             h = self.step(ids[:, s0:s0 + self.C], s0, state)
         return h, state
+
+    # -------------------------------------------------------------- generation and memory (checkers)
+
+    @torch.no_grad()
+    def logits(self, h: torch.Tensor) -> torch.Tensor:
+        return self.model.lm_head(h[:, -1])
+
+    @torch.no_grad()
+    def generate_greedy(self, ids: torch.Tensor, n_new: int, eos_ids=None, close_think_ids=None):
+        """Bolt3Decoder.generate_batch at temperature 0 (vsa_lm/config/bolt3.py:459-500), one token at a
+        time with the reference's per-row rules: eos rows keep their first eos position as length;
+        from the budget point max(64, n_new - 64) every row still thinking (not closed, not done)
+        is forced through close_think_ids; a row counts as closed after the forced sequence or when
+        it emits close_think_ids[1]; every 16 tokens the loop stops if all rows are done.
+        Returns (tokens [B, n], lengths [B], the top-2 logit gap of each step [n])."""
+        B, T = ids.shape
+        h, state = self.prefill(ids)
+        lg = self.logits(h)
+        close = list(close_think_ids or ())
+        eos = set(eos_ids or ())
+        done, closed = [False] * B, [False] * B
+        lengths, cursor = [n_new] * B, [-1] * B
+        budget = max(64, n_new - 64)
+        toks, gaps = [], []
+        for i in range(n_new):
+            top2 = lg.float().topk(2, dim=-1).values
+            gaps.append(float((top2[:, 0] - top2[:, 1]).min()))
+            nxt = lg.argmax(dim=-1).tolist()
+            if close:
+                if i == budget:
+                    for r in range(B):
+                        if not closed[r] and not done[r] and cursor[r] < 0:
+                            cursor[r] = 0
+                for r in range(B):
+                    if cursor[r] >= 0:
+                        nxt[r] = close[cursor[r]]
+                        cursor[r] += 1
+                        if cursor[r] >= len(close):
+                            cursor[r], closed[r] = -1, True
+                if len(close) > 1:
+                    for r in range(B):
+                        closed[r] = closed[r] or nxt[r] == close[1]
+            toks.append(nxt)
+            if eos:
+                for r in range(B):
+                    if not done[r] and nxt[r] in eos:
+                        lengths[r], done[r] = i + 1, True
+                if i % 16 == 15 and all(done):
+                    break
+            h = self.step(torch.tensor(nxt).view(B, 1), T + i, state)
+            lg = self.logits(h)
+        return torch.tensor(toks).T.contiguous(), torch.tensor(lengths), gaps
+
+    @torch.no_grad()
+    def memorize(self, ids: torch.Tensor, state: dict, start_pos: int):
+        """Bolt3Decoder.memorize (vsa_lm/config/bolt3.py:528-546): feed ids in chunks of C, then per
+        Bolt-3 layer the trace (end position, M_after - gamma^(len // C) * M_before)."""
+        before = {li: st[0].clone() for li, st in state.items() if li in self.params}
+        pos = start_pos
+        for s0 in range(0, ids.shape[1], self.C):
+            part = ids[:, s0:s0 + self.C]
+            self.step(part, pos, state)
+            pos += part.shape[1]
+        traces = {}
+        for li, m0 in before.items():
+            g = gamma_delta(self.params[li].log_gamma).view(1, -1, 1, 1)
+            traces[li] = (pos, state[li][0] - g ** (ids.shape[1] // self.C) * m0)
+        return pos, traces
+
+    def forget(self, traces: dict, state: dict, next_pos: int):
+        """Bolt3Decoder.forget (vsa_lm/config/bolt3.py:548-557): subtract each trace decayed by gamma
+        once per C positions since its end."""
+        for li, (end, delta) in traces.items():
+            g = gamma_delta(self.params[li].log_gamma).view(1, -1, 1, 1)
+            state[li][0] = state[li][0] - g ** max(0, (next_pos - end) // self.C) * delta
+

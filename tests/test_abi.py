@@ -66,13 +66,19 @@ def test_rejects_bad_arguments_without_gpu_work():
     la.dec.dtype = 1
     assert lib.bolt3_decode_layer(ctypes.byref(la), None) == 1001
     assert lib.bolt3_wait_count(None, 1, 10, None) == 1001
+    sk = A.SlotKeysArgs()
+    sk.dtype, sk.B, sk.HKV, sk.HD, sk.S = 1, 1, 1, 128, 128
+    assert lib.bolt3_slot_keys(ctypes.byref(sk), None) == 1001        # null pointers
+    sk.S = 64
+    assert lib.bolt3_slot_keys(ctypes.byref(sk), None) == 1002        # S != 128
     d2 = A.DecodeArgs()
     d2.dtype, d2.B, d2.H, d2.HKV, d2.HD, d2.S, d2.has_slots = 1, 1, 4, 1, 128, 256, 1
     assert lib.bolt3_decode(ctypes.byref(d2), None) in (1001, 1002)   # rejected before any launch
 
 
 STRUCTS = {"b3_heads_args": A.HeadsArgs, "b3_chain_args": A.ChainArgs, "b3_attn_args": A.AttnArgs,
-           "b3_decode_args": A.DecodeArgs, "b3_decode_layer_args": A.DecodeLayerArgs}
+           "b3_decode_args": A.DecodeArgs, "b3_decode_layer_args": A.DecodeLayerArgs,
+           "b3_slot_keys_args": A.SlotKeysArgs}
 
 
 def _flat_fields(st, prefix=""):
@@ -101,3 +107,19 @@ def test_struct_layout_matches_header():
         assert got[(cname, "sizeof")] == ctypes.sizeof(st), cname
         for field, off, _ in _flat_fields(st):
             assert got[(cname, field)] == off, (cname, field)
+
+
+def test_no_packed_fp32_in_device_code():
+    """The build keeps packed fp32 VALU ops out of the code objects (-Xclang -target-feature
+    -Xclang -packed-fp32-ops acts on the device pass; only the host pass warns that it does not
+    know it): every kernel source compiled to gfx950 assembly has none."""
+    import re
+    from bolt3_amd import build as Bd
+    pat = re.compile(r"\bv_pk_(" + "|".join(("add", "mul", "fma")) + r")_f32\b")
+    with tempfile.TemporaryDirectory() as d:
+        for src in Bd.sources():
+            out = os.path.join(d, os.path.basename(src) + ".s")
+            r = subprocess.run([Bd.HIPCC, *Bd.FLAGS, "-S", "--cuda-device-only", src, "-o", out],
+                               capture_output=True, text=True)
+            assert r.returncode == 0, r.stderr[-2000:]
+            assert not pat.search(open(out).read()), src

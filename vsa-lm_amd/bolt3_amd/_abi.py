@@ -98,9 +98,17 @@ class DecodeLayerArgs(C.Structure):
     ]
 
 
+class SlotKeysArgs(C.Structure):
+    _fields_ = [
+        ("dtype", i32), ("B", i32), ("HKV", i32), ("HD", i32), ("S", i32),
+        ("ak", p), ("pm", p), ("mass", p), ("act", p), ("kappa", p), ("inv_freq", p),
+        ("slot_k", p), ("slot_bias", p),
+    ]
+
+
 EXPORTS = ("bolt3_heads", "bolt3_chain", "bolt3_chain_workspace_bytes", "bolt3_chunk_attn", "bolt3_decode",
            "bolt3_decode_layer", "bolt3_decode_layer_workspace_bytes", "bolt3_decode_workspace_bytes",
-           "bolt3_version", "bolt3_wait_count")
+           "bolt3_slot_keys", "bolt3_version", "bolt3_wait_count")
 
 _lib = None
 
@@ -115,7 +123,8 @@ def load():
                            f"(python -m bolt3_amd.build); there is no CPU implementation")
     lib = C.CDLL(LIB_PATH)
     for name, st in (("bolt3_heads", HeadsArgs), ("bolt3_chain", ChainArgs), ("bolt3_chunk_attn", AttnArgs),
-                     ("bolt3_decode", DecodeArgs), ("bolt3_decode_layer", DecodeLayerArgs)):
+                     ("bolt3_decode", DecodeArgs), ("bolt3_decode_layer", DecodeLayerArgs),
+                     ("bolt3_slot_keys", SlotKeysArgs)):
         fn = getattr(lib, name)
         fn.argtypes = [C.POINTER(st), p]
         fn.restype = C.c_int

@@ -100,6 +100,33 @@ def _step_groups(n: int, k: int) -> list[tuple[int, int]]:
     return [(bounds[i], bounds[i + 1]) for i in range(k) if bounds[i + 1] > bounds[i]]
 
 
+class _storage_dtype:
+    """The dtype the kernels store activations in: the input's, or under autocast the autocast
+    dtype (the projections then produce it, as the reference's linears do under autocast).
+    Autocast is switched off inside, so every projection output has exactly this dtype."""
+
+    def __init__(self, x: torch.Tensor):
+        dev = x.device.type
+        self.auto = torch.is_autocast_enabled(dev)
+        self.dt = torch.get_autocast_dtype(dev) if self.auto else x.dtype
+        self.ctx = torch.autocast(dev, enabled=False) if self.auto else None
+
+    def __enter__(self):
+        if self.ctx is not None:
+            self.ctx.__enter__()
+        return self.dt
+
+    def __exit__(self, *exc):
+        if self.ctx is not None:
+            return self.ctx.__exit__(*exc)
+        return False
+
+
+def _check_dtype(t: torch.Tensor, dt: torch.dtype, what: str):
+    if t.dtype != dt:
+        raise TypeError(f"{what} is {t.dtype}, the kernels were told {dt}")
+
+
 class _NoBackward(torch.autograd.Function):
     """Keeps autograd edges to the inputs but refuses to differentiate the HIP path."""
 
@@ -288,7 +315,8 @@ class Bolt3Attn(nn.Module):
 
     def forward(self, x: torch.Tensor, _trace: dict | None = None) -> torch.Tensor:
         _require_gpu(x, "Bolt3Attn.forward")
-        out = self._forward_hip(x, _trace)
+        with _storage_dtype(x) as dt:
+            out = self._forward_hip(x.to(dt), _trace)
         if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters())):
             out = _NoBackward.apply(out, x, *[p for p in self.parameters() if p.requires_grad])
         return out
@@ -308,6 +336,8 @@ class Bolt3Attn(nn.Module):
         # decisions hold their compute units (bolt3_wait_count) and runs on the rest of the chip.
         lin_kv = F.linear(x, side["wkv"], side["bkv"])
         gates = F.linear(x, side["wg"], side["bg"])
+        _check_dtype(lin_kv, dt, "k|v projection")
+        _check_dtype(gates, dt, "gate projection")
         k_raw = torch.empty(b, HKV, T, HD, dtype=dt, device=dev)
         k_rope, v = torch.empty_like(k_raw), torch.empty_like(k_raw)
         beta = torch.empty(b, HKV, T, device=dev)
@@ -383,6 +413,7 @@ class Bolt3Attn(nn.Module):
         if first_started is not None:
             _wait_started(dev, ctr[0], first_started)
         lin_q = F.linear(x, side["wq"], side["bq"])
+        _check_dtype(lin_q, dt, "q projection")
         q_raw = torch.empty(b, H, T, HD, dtype=dt, device=dev)
         q_rope = torch.empty_like(q_raw)
         eta = torch.empty(b, H, T, device=dev)
@@ -480,429 +511,9 @@ class Bolt3Attn(nn.Module):
         return st["ak"], st["av"], st["mass"], st["util"], st["pm"], st["act"].bool(), m, nf
 
 
-# ==================================================================== decoder
-
-class StaticKV:
-    """Growing key/value cache of a softmax-anchor layer (vsa_lm/decode.py:88-106)."""
-
-    def __init__(self, B: int, HKV: int, Tmax: int, HD: int, dev, dt=torch.bfloat16):
-        self.k = torch.empty(B, HKV, Tmax, HD, device=dev, dtype=dt)
-        self.v = torch.empty_like(self.k)
-        self.n = 0
-
-    def append(self, k_new, v_new):
-        L = k_new.shape[2]
-        if self.n + L > self.k.shape[2]:
-            cap = max(self.n + L + 1024, self.k.shape[2] * 2)
-            nk = torch.empty(*self.k.shape[:2], cap, self.k.shape[3], device=self.k.device, dtype=self.k.dtype)
-            nv = torch.empty_like(nk)
-            nk[:, :, :self.n] = self.k[:, :, :self.n]
-            nv[:, :, :self.n] = self.v[:, :, :self.n]
-            self.k, self.v = nk, nv
-        self.k[:, :, self.n:self.n + L] = k_new
-        self.v[:, :, self.n:self.n + L] = v_new
-        self.n += L
-        return self.k[:, :, :self.n], self.v[:, :, :self.n]
-
-
-class Bolt3LayerState:
-    """Decoder state of one Bolt-3 layer in preallocated device buffers.
-
-    The window is a ring of two halves of 2C tokens each: the previous chunk
-    ("prev") in one half, the chunk being filled ("cur") in the other.  Slot
-    state keeps the un-roped keys (ak) plus a cache of the keys roped at their
-    mean positions (slot_k) and the attention bias (slot_bias), refreshed by
-    every consolidation.  Reads with the reference's key names are served by
-    ``__getitem__`` (vsa_lm/config/bolt3.py:310-315).
-    """
-
-    def __init__(self, ly: Bolt3Attn, B: int, device, dtype):
-        C, S, HKV, HD = ly.C, ly.S, ly.HKV, ly.HD
-        self.B, self.C, self.S, self.HKV, self.HD, self.dtype = B, C, S, HKV, HD, dtype
-        self.cap = 4 * C
-        self.win_kr = torch.zeros(B, HKV, self.cap, HD, dtype=dtype, device=device)
-        self.win_kp = torch.zeros_like(self.win_kr)
-        self.win_v = torch.zeros_like(self.win_kr)
-        self.win_b = torch.zeros(B, HKV, self.cap, device=device)
-        self.win_pos = torch.zeros(self.cap, device=device)
-        self.sink_k = torch.zeros(B, HKV, N_SINKS, HD, dtype=dtype, device=device)
-        self.sink_v = torch.zeros_like(self.sink_k)
-        self.n_sink = 0
-        bh = B * HKV
-        self.slots = ly._empty_slots(bh, dtype, device)
-        self.slot_k = torch.zeros(bh, S, HD, dtype=dtype, device=device)
-        self.slot_bias = torch.zeros(bh, S, device=device)
-        self.has_slots = False
-        self.n_filled = 0
-        self.prev = (0, 0)          # (start, length) in the ring
-        self.cur = (2 * C, 0)
-        self._dec_work = None
-        self._dec = None   # the one-token step: key, argument blocks, output and projection workspace
-
-    def decode_workspace(self, H: int) -> torch.Tensor:
-        """Scratch of the one-token decode kernels (partial softmax state per key range)."""
-        n = A.decode_workspace_bytes(self.B, H, self.HKV, self.HD) // 4
-        if self._dec_work is None or self._dec_work.numel() < n:
-            self._dec_work = torch.empty(n, device=self.win_kr.device)
-        return self._dec_work
-
-    def _seg(self, name, seg):
-        s, n = seg
-        if n == 0:
-            return None
-        if name == "pos":
-            return self.win_pos[s:s + n].view(1, 1, n)
-        if name == "b":
-            return self.win_b[:, :, s:s + n]
-        return {"kr": self.win_kr, "kp": self.win_kp, "v": self.win_v}[name][:, :, s:s + n]
-
-    def __getitem__(self, key):
-        B, HKV = self.B, self.HKV
-        if key in ("ak", "av"):
-            return self.slots[key].view(B, HKV, self.S, self.HD) if self.has_slots else None
-        if key in ("mass", "util", "pm"):
-            return self.slots[key].view(B * HKV, self.S) if self.has_slots else None
-        if key == "act":
-            return self.slots["act"].bool() if self.has_slots else None
-        if key in ("sink_k", "sink_v"):
-            return getattr(self, key)[:, :, :self.n_sink] if self.n_sink else None
-        if key == "n_filled":
-            return self.n_filled
-        for pre, seg in (("prev_", self.prev), ("cur_", self.cur)):
-            if key.startswith(pre):
-                return self._seg(key[len(pre):], seg)
-        raise KeyError(key)
-
-    def get(self, key, default=None):
-        try:
-            v = self[key]
-        except KeyError:
-            return default
-        return default if v is None else v
-
-
-class Bolt3Decoder:
-    """Constant-memory decoder over a hybrid Bolt-3 / softmax stack (vsa_lm/config/bolt3.py:279-557)."""
-
-    def __init__(self, model, wrap_positions: bool = False, max_cache_pos: int = 65536, **kwargs):
-        self.model = model.eval()
-        self.max_T = model.config["max_T"]
-        self.max_cache_pos = max_cache_pos
-        self.C = int(model.config.get("bolt3_C", 128))
-        # bf16 one-token steps run as one bolt3_decode_layer call (projections included); False
-        # keeps the projections in torch around bolt3_decode (the tests compare the two)
-        self.fuse_projections = True
-
-    def _graph_runner(self, B: int, need_len: int, device):
-        return None
-
-    @staticmethod
-    def state_bytes(model):
-        flat, per_tok = 0, 0
-        for blk in model.blocks:
-            if hasattr(blk, "vsa"):
-                ly = blk.vsa
-                flat += ly.HKV * ly.HD * ly.HD * 4 + 2 * ly.S * ly.HKV * ly.HD * 2 + 4 * ly.C * ly.HKV * ly.HD * 2
-            else:
-                s = blk.attn
-                per_tok += 2 * s.HKV * s.HD * 2
-        return flat, per_tok
-
-    @staticmethod
-    def blank_state(model, batch_size: int, device, max_kv_len: int = 4096, state_dtype=torch.float32,
-                    dtype=None, **kwargs):
-        device = torch.device(device)
-        if device.type != "cuda":
-            raise RuntimeError("Bolt3Decoder.blank_state: the Bolt-3 HIP path needs a ROCm device")
-        dt = dtype or next(model.parameters()).dtype
-        states, kv = [None] * len(model.blocks), [None] * len(model.blocks)
-        for li, blk in enumerate(model.blocks):
-            if hasattr(blk, "vsa"):
-                ly = blk.vsa
-                states[li] = torch.zeros(batch_size, ly.HKV, ly.HD, ly.HD, device=device, dtype=state_dtype)
-                kv[li] = Bolt3LayerState(ly, batch_size, device, dt)
-            else:
-                s = blk.attn
-                kv[li] = StaticKV(batch_size, s.HKV, max_kv_len, s.HD, device, dt=dt)
-        return states, kv
-
-    @staticmethod
-    def _sample(logits, temperature: float, top_k: int = 40, top_p: float = 0.95):
-        if temperature <= 1e-5:
-            return logits.argmax(-1, keepdim=True)
-        probs = F.softmax(logits.float() / temperature, dim=-1)
-        if top_p < 1.0:
-            sp, si = torch.sort(probs, descending=True, dim=-1)
-            cp = torch.cumsum(sp, dim=-1)
-            sp[cp - sp > top_p] = 0.0
-            sp.div_(sp.sum(dim=-1, keepdim=True).clamp_min(1e-12))
-            return si.gather(-1, torch.multinomial(sp, 1))
-        tv, ti = torch.topk(logits.float() / temperature, min(top_k, logits.size(-1)), dim=-1)
-        return ti.gather(-1, torch.multinomial(F.softmax(tv, -1), 1))
-
-    # ------------------------------------------------------------ one Bolt-3 layer
-
-    def _bolt3_layer(self, ly: Bolt3Attn, h, pos_start: int, m_state: torch.Tensor, st: Bolt3LayerState,
-                     record=None):
-        B, t, _ = h.shape
-        dt, dev = h.dtype, h.device
-        if dt != st.dtype:
-            raise TypeError(f"activation dtype {dt} differs from the decoder state dtype {st.dtype}")
-        if t > ly.C:
-            raise NotImplementedError(f"step takes at most C={ly.C} tokens per call (got {t})")
-        H, HKV, HD, S = ly.H, ly.HKV, ly.HD, ly.S
-        W, bias, side = ly._packed(dt, dev)
-        gam = side["gamma"]
-        cs, cl = st.cur
-        ps, pl = st.prev
-        h = h if h.is_contiguous() else h.contiguous()
-        if t == 1:
-            # The argument block, the projection row and the attention output are kept in the
-            # layer state; a step only refreshes the position, the ring segments and the input
-            # and output rows.  bf16 runs the whole step (both projections included) in one
-            # bolt3_decode_layer call.
-            fused = self.fuse_projections and dt == torch.bfloat16 and h.shape[-1] % 32 == 0 and \
-                side["wo"].shape[0] % 16 == 0
-            key = (id(side), m_state.data_ptr(), W.data_ptr(), fused)
-            if st._dec is None or st._dec[0] != key:
-                y = torch.empty(B, H * HD, dtype=dt, device=dev)
-                n_out = side["wo"].shape[0]
-                pw = torch.empty(A.decode_layer_workspace_bytes(B, h.shape[-1], W.shape[0], H * HD, n_out) // 4,
-                                 device=dev) if fused else None
-                la = A.DecodeLayerArgs() if fused else None
-                a = la.dec if fused else A.DecodeArgs()   # la.dec shares la's memory
-                a.dtype, a.B, a.H, a.HKV, a.HD, a.S = A.dtype_code(dt), B, H, HKV, HD, S
-                a.lin_row_stride = W.shape[0]
-                a.qn_w, a.kn_w, a.has_qk_norm = A.ptr(side["qn"]), A.ptr(side["kn"]), int(side["qn"] is not None)
-                a.eps, a.inv_freq = float(ly.res_norm.eps), side["inv_freq"].data_ptr()
-                a.win_kr, a.win_kp, a.win_v = st.win_kr.data_ptr(), st.win_kp.data_ptr(), st.win_v.data_ptr()
-                a.w_sb, a.w_sh = st.win_kr.stride(0), st.win_kr.stride(1)
-                a.win_beta, a.wb_sb, a.wb_sh = st.win_b.data_ptr(), st.win_b.stride(0), st.win_b.stride(1)
-                a.win_pos = st.win_pos.data_ptr()
-                a.sink_k, a.sink_v = st.sink_k.data_ptr(), st.sink_v.data_ptr()
-                a.s_sb, a.s_sh = st.sink_k.stride(0), st.sink_k.stride(1)
-                a.slot_k, a.slot_v, a.slot_bias = st.slot_k.data_ptr(), st.slots["av"].data_ptr(), \
-                    st.slot_bias.data_ptr()
-                a.m_res, a.gamma, a.res_w, a.y = m_state.data_ptr(), gam.data_ptr(), side["res_w"].data_ptr(), \
-                    y.data_ptr()
-                work = st.decode_workspace(H)
-                a.work, a.work_bytes = work.data_ptr(), work.numel() * 4
-                if fused:
-                    la.proj_work, la.proj_work_bytes = pw.data_ptr(), pw.numel() * 4
-                    la.x_row_stride, la.d_model = h.shape[-1], h.shape[-1]
-                    la.w_in, la.b_in, la.n_in = W.data_ptr(), A.ptr(bias), W.shape[0]
-                    la.w_out, la.b_out, la.n_out = side["wo"].data_ptr(), None, side["wo"].shape[0]
-                    la.out_row_stride = side["wo"].shape[0]
-                st._dec = (key, la if fused else a, a, y, pw, side, W, bias)
-            _, call_args, a, y, _, _, _, _ = st._dec
-            a.pos = int(pos_start)
-            a.a_start, a.a_len, a.b_start, a.b_len = ps, pl, cs, cl
-            a.n_sink_keys, a.has_slots = st.n_sink, int(st.has_slots)
-            if fused:
-                out = torch.empty(B, 1, side["wo"].shape[0], dtype=dt, device=dev)
-                call_args.x, call_args.out = h.data_ptr(), out.data_ptr()
-                A.call("bolt3_decode_layer", call_args, dev)
-                st.cur = (cs, cl + 1)
-                if st.cur[1] >= ly.C:
-                    self._consolidate(ly, st, m_state, gam, side, record)
-                return out
-            lin = F.linear(h, W, bias)
-            a.lin = lin.data_ptr()
-            A.call("bolt3_decode", a, dev)
-            y = y.view(B, 1, H * HD)
-        else:
-            lin = F.linear(h, W, bias)
-            q_raw = torch.empty(B, H, t, HD, dtype=dt, device=dev)
-            q_rope = torch.empty_like(q_raw)
-            eta = torch.empty(B, H, t, device=dev)
-            ly._heads(lin, B, t, dt, side, pos_start, q_raw, q_rope, st.win_kr, st.win_kp, st.win_v, st.win_b, eta,
-                      pos_out=st.win_pos, kv_offset=cs + cl)
-            y = torch.empty(B, t, H * HD, dtype=dt, device=dev)
-            a = A.AttnArgs()
-            a.dtype, a.B, a.H, a.HKV, a.HD, a.S, a.C, a.n_sinks = A.dtype_code(dt), B, H, HKV, HD, S, ly.C, ly.n_sinks
-            a.mode, a.n_q, a.score_round = 1, t, 0
-            a.q_rope, a.q_raw, a.q_sb, a.q_sh = q_rope.data_ptr(), q_raw.data_ptr(), q_rope.stride(0), q_rope.stride(1)
-            a.eta, a.e_sb, a.e_sh = eta.data_ptr(), eta.stride(0), eta.stride(1)
-            a.win_k, a.win_v, a.w_sb, a.w_sh = st.win_kp.data_ptr(), st.win_v.data_ptr(), st.win_kp.stride(0), \
-                st.win_kp.stride(1)
-            a.a_start, a.a_len, a.b_start, a.b_len = ps, pl, cs, cl + t
-            a.sink_k, a.sink_v = st.sink_k.data_ptr(), st.sink_v.data_ptr()
-            a.s_sb, a.s_sh, a.n_sink_keys = st.sink_k.stride(0), st.sink_k.stride(1), st.n_sink
-            a.slot_k, a.slot_v, a.slot_bias = st.slot_k.data_ptr(), st.slots["av"].data_ptr(), st.slot_bias.data_ptr()
-            a.slot_step, a.has_slots = 0, int(st.has_slots)
-            a.m_res, a.m_step = m_state.data_ptr(), 0
-            a.gamma, a.res_w, a.eps = gam.data_ptr(), side["res_w"].data_ptr(), float(ly.res_norm.eps)
-            a.y, a.y_sb, a.y_st = y.data_ptr(), y.stride(0), y.stride(1)
-            A.call("bolt3_chunk_attn", a, dev)
-        st.cur = (cs, cl + t)
-        out = F.linear(y, side["wo"])
-        if st.cur[1] >= ly.C:
-            self._consolidate(ly, st, m_state, gam, side, record)
-        return out
-
-    def _consolidate(self, ly: Bolt3Attn, st: Bolt3LayerState, m_state, gam, side, record=None):
-        ps, pl = st.prev
-        if pl > 0:
-            off, l = ps, pl
-            if st.n_sink == 0:
-                ns = min(ly.n_sinks, l)
-                st.sink_k[:, :, :ns].copy_(st.win_kp[:, :, off:off + ns])
-                st.sink_v[:, :, :ns].copy_(st.win_v[:, :, off:off + ns])
-                st.n_sink = ns
-                off, l = off + ns, l - ns
-            if st.n_filled == 0:
-                for k, v in ly._empty_slots(st.B * st.HKV, st.dtype, m_state.device).items():
-                    st.slots[k].copy_(v)
-                m_state.zero_()
-            log = None
-            if record is not None:
-                log = torch.zeros(1, st.B * st.HKV, A.LOG_ROWS, A.LOG_COLS, device=m_state.device)
-                record.append(dict(log=log[0], n_filled=st.n_filled, tokens=l))
-            ly._chain(st.dtype, m_state.device, st.B, st.win_kr.data_ptr(), st.win_kp.data_ptr(),
-                      st.win_v.data_ptr(), st.cap * st.HD, st.win_pos.data_ptr(), st.win_b.data_ptr(), st.cap,
-                      1, off, l, l, l, st.n_filled, st.slots, m_state, gam, side,
-                      snap_k=st.slot_k, snap_bias=st.slot_bias, kp_exact=True, log=log)
-            if st.n_filled < ly.S:
-                st.n_filled += min(ly.S - st.n_filled, l)
-            st.has_slots = True
-        cs, cl = st.cur
-        st.prev = (cs, cl)
-        st.cur = (0 if cs == 2 * ly.C else 2 * ly.C, 0)
-
-    # ------------------------------------------------------------ model-level API
-
-    @torch.no_grad()
-    def step(self, tokens: torch.Tensor, pos_start: int, states, kv_caches, record=None):
-        m = self.model
-        b, t = tokens.shape
-        x = m.embed_tokens(tokens)
-        for li, blk in enumerate(m.blocks):
-            h = blk.norm1(x)
-            if hasattr(blk, "vsa"):
-                rec = None
-                if record is not None:
-                    rec = record.setdefault(li, []) if isinstance(record, dict) else record
-                x = x + self._bolt3_layer(blk.vsa, h, pos_start, states[li], kv_caches[li], rec)
-            else:
-                ly = blk.attn
-                q, k, v = ly.head_qkv(h)
-                q, k = ly.rope(q, pos_start=pos_start), ly.rope(k, pos_start=pos_start)
-                n_prev = kv_caches[li].n
-                pk, pv = kv_caches[li].append(k, v)
-                if t > 1:
-                    qi = torch.arange(t, device=tokens.device)[:, None]
-                    kj = torch.arange(n_prev + t, device=tokens.device)[None, :]
-                    cmask = (kj <= (n_prev + qi)).view(1, 1, t, n_prev + t)
-                    y = F.scaled_dot_product_attention(q, pk.to(q.dtype), pv.to(q.dtype), attn_mask=cmask,
-                                                       enable_gqa=ly.G > 1)
-                else:
-                    y = F.scaled_dot_product_attention(q, pk.to(q.dtype), pv.to(q.dtype), enable_gqa=ly.G > 1)
-                x = x + ly.o_proj(y.transpose(1, 2).reshape(b, t, ly.H * ly.HD))
-            x = x + blk.mlp(blk.norm2(x))
-        return m.norm(x), states, kv_caches
-
-    @torch.no_grad()
-    def prefill(self, ids: torch.Tensor, max_kv_len: int = 4096):
-        b, t = ids.shape
-        states, kv = self.blank_state(self.model, b, ids.device, max_kv_len=max(max_kv_len, t + 1024))
-        h = None
-        for s in range(0, t, self.C):
-            h, states, kv = self.step(ids[:, s:min(t, s + self.C)], s, states, kv)
-        return h, states, kv
-
-    @torch.no_grad()
-    def generate_batch(self, ids: torch.Tensor, max_new_tokens: int, temperature: float = 0.6, top_k: int = 40,
-                       top_p: float = 0.95, eos_ids: set[int] | None = None,
-                       close_think_ids: list[int] | None = None):
-        B, T = ids.shape
-        h, states, kv = self.prefill(ids, max_kv_len=T + max_new_tokens + 64)
-        logits = self.model.lm_head(h[:, -1, :])
-        eos = torch.tensor(sorted(eos_ids or ()), device=ids.device, dtype=torch.long)
-        done = torch.zeros(B, dtype=torch.bool, device=ids.device)
-        lengths = torch.full((B,), max_new_tokens, dtype=torch.long, device=ids.device)
-        end_think = close_think_ids[1] if (close_think_ids and len(close_think_ids) > 1) else None
-        closed = torch.zeros(B, dtype=torch.bool, device=ids.device)
-        q_pos = torch.full((B,), -1, dtype=torch.long, device=ids.device)
-        trigger = max(64, max_new_tokens - 64)
-        out, pos = [], T
-        for i in range(max_new_tokens):
-            nxt = self._sample(logits, temperature, top_k=top_k, top_p=top_p)
-            if close_think_ids:
-                if i == trigger:
-                    q_pos[(~closed) & (~done) & (q_pos < 0)] = 0
-                active = q_pos >= 0
-                if bool(active.any()):
-                    for r in torch.nonzero(active, as_tuple=False).view(-1).tolist():
-                        nxt[r, 0] = close_think_ids[int(q_pos[r])]
-                        q_pos[r] += 1
-                        if q_pos[r] >= len(close_think_ids):
-                            q_pos[r] = -1
-                            closed[r] = True
-                if end_think is not None:
-                    closed |= nxt[:, 0] == end_think
-            out.append(nxt)
-            if eos.numel():
-                hit = torch.isin(nxt[:, 0], eos) & ~done
-                lengths[hit] = i + 1
-                done |= hit
-                if i % 16 == 15 and bool(done.all()):
-                    break
-            h, states, kv = self.step(nxt, pos, states, kv)
-            logits = self.model.lm_head(h[:, -1, :])
-            pos += 1
-        return torch.cat(out, dim=1), lengths
-
-    @torch.no_grad()
-    def generate(self, prompt: torch.Tensor, max_new_tokens: int, temperature: float = 0.0, top_k: int = 40,
-                 top_p: float = 0.95, eos_ids: set[int] | None = None, close_think_ids: list[int] | None = None):
-        toks, n = self.generate_batch(prompt, max_new_tokens, temperature, top_k, top_p, eos_ids, close_think_ids)
-        return torch.cat([prompt, toks[:, : int(n[0].item())]], dim=1)
-
-    @torch.no_grad()
-    def continue_generate(self, ids: torch.Tensor, states, kv_caches, start_pos: int, max_new_tokens: int,
-                          temperature: float = 0.0, top_k: int = 40, top_p: float = 0.95,
-                          eos_ids: set[int] | None = None):
-        out, pos, h = [], start_pos, None
-        for s in range(0, ids.shape[1], self.C):
-            e = min(ids.shape[1], s + self.C)
-            h, states, kv_caches = self.step(ids[:, s:e], pos, states, kv_caches)
-            pos += e - s
-        logits = self.model.lm_head(h[:, -1, :])
-        for _ in range(max_new_tokens):
-            nxt = self._sample(logits, temperature, top_k=top_k, top_p=top_p)
-            out.append(nxt)
-            if eos_ids and int(nxt[0, 0].item()) in eos_ids:
-                break
-            h, states, kv_caches = self.step(nxt, pos, states, kv_caches)
-            logits = self.model.lm_head(h[:, -1, :])
-            pos += 1
-        toks = torch.cat(out, dim=1) if out else torch.empty(ids.shape[0], 0, dtype=torch.long, device=ids.device)
-        return toks, states, kv_caches, pos
-
-    @torch.no_grad()
-    def memorize(self, ids: torch.Tensor, states, kv_caches, start_pos: int):
-        pre = [s.clone() if s is not None else None for s in states]
-        pos = start_pos
-        for s in range(0, ids.shape[1], self.C):
-            e = min(ids.shape[1], s + self.C)
-            _, states, kv_caches = self.step(ids[:, s:e], pos, states, kv_caches)
-            pos += e - s
-        n_tok = ids.shape[1]
-        traces = []
-        for li, blk in enumerate(self.model.blocks):
-            if hasattr(blk, "vsa"):
-                gam = blk.vsa.gamma_delta().view(1, -1, 1, 1).to(states[li].device)
-                traces.append((pos, states[li] - (gam ** (n_tok // blk.vsa.C)) * pre[li]))
-            else:
-                traces.append(None)
-        return states, kv_caches, pos, traces
-
-    @torch.no_grad()
-    def forget(self, traces, states, next_pos: int, kv_caches=None, pre_kv_lens=None):
-        for li, tr in enumerate(traces):
-            if tr is not None and states[li] is not None:
-                end_p, delta = tr
-                blk = self.model.blocks[li]
-                gam = blk.vsa.gamma_delta().view(1, -1, 1, 1).to(states[li].device)
-                states[li] = states[li] - (gam ** max(0, (next_pos - end_p) // blk.vsa.C)) * delta
-        return states
+def __getattr__(name):
+    # the reference imports the decoder from the layer's module (vsa_lm.config.bolt3)
+    if name in ("Bolt3Decoder", "Bolt3LayerState", "StaticKV", "AnchorCache"):
+        from . import decoder
+        return getattr(decoder, name)
+    raise AttributeError(name)

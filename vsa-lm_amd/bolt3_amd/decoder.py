@@ -1,0 +1,689 @@
+"""Bolt-3 decoder on MI355X: constant-memory generation over a hybrid stack.
+
+Drop-in for ``Bolt3Decoder`` of vsa_lm/config/bolt3.py:279-557 (reference
+tree): same constructor, ``step`` / ``prefill`` / ``generate_batch`` /
+``generate`` / ``continue_generate`` / ``memorize`` / ``forget`` /
+``blank_state`` / ``state_bytes`` / ``_sample`` with the reference's argument
+meaning and results.
+
+Design (not the reference's):
+  * Bolt-3 layers keep their whole state in preallocated device buffers
+    (``Bolt3LayerState``: a window ring, sinks, slots with cached roped keys,
+    M_res) and step through the HIP entry points: one ``bolt3_decode_layer``
+    call per token in bf16 (both projections included), ``bolt3_chain`` when a
+    chunk leaves the window.
+  * Softmax-anchor layers keep keys and values in an ``AnchorCache`` that grows
+    by whole pages.
+  * ``generate_batch`` keeps its bookkeeping on the device (tokens, end of
+    sequence, lengths, the forced close-of-thinking sequence) and never waits
+    for the GPU inside the loop: the all-rows-done test the reference makes
+    every 16 tokens is read back one period later from a copy taken then, and
+    the output is cut where the reference would have stopped.
+"""
+from __future__ import annotations
+
+from collections.abc import MutableMapping
+
+import torch
+import torch.nn.functional as F
+
+from . import _abi as A
+from .bolt3 import N_SINKS, Bolt3Attn, _check_dtype, _gout, _tout
+
+DONE_CHECK_EVERY = 16      # tokens between the all-rows-done tests (the reference's period)
+
+
+def _check_m_state(m: torch.Tensor, B: int, ly: Bolt3Attn):
+    """The kernels read and write M_res as contiguous fp32 [B][HKV][HD][HD] on the device."""
+    want = (B, ly.HKV, ly.HD, ly.HD)
+    if m.dtype != torch.float32 or tuple(m.shape) != want or not m.is_contiguous() or not m.is_cuda:
+        raise TypeError(f"M_res state must be a contiguous fp32 device tensor of shape {want}; "
+                        f"got {m.dtype} {tuple(m.shape)} contiguous={m.is_contiguous()} on {m.device}")
+
+
+def _fused_step_ok(dt: torch.dtype, d_model: int, hd_total: int, n_out: int) -> bool:
+    """Whether bolt3_decode_layer takes this layer: bf16, input width a multiple of 32, output width
+    a multiple of 16, and at most 8 K chunks of 512 in either projection."""
+    return dt == torch.bfloat16 and d_model >= 32 and d_model % 32 == 0 and n_out % 16 == 0 and \
+        (d_model + 511) // 512 <= 8 and (hd_total + 511) // 512 <= 8
+
+
+class AnchorCache:
+    """Key/value cache of one softmax-anchor layer.
+
+    Same surface as the reference's StaticKV (vsa_lm/decode.py:88-106): tensors
+    ``k`` / ``v`` of shape [B, HKV, capacity, HD], the count ``n`` of cached
+    tokens, and ``append(k, v)`` returning the cached prefix.  Capacity is a
+    whole number of PAGE-token pages and at least doubles when it grows.
+    """
+
+    PAGE = 256
+
+    def __init__(self, B: int, HKV: int, Tmax: int, HD: int, dev, dt=torch.bfloat16):
+        cap = -(-max(int(Tmax), 1) // self.PAGE) * self.PAGE
+        self.k = torch.empty(B, HKV, cap, HD, device=dev, dtype=dt)
+        self.v = torch.empty_like(self.k)
+        self.n = 0
+
+    @property
+    def capacity(self) -> int:
+        return self.k.shape[2]
+
+    def reserve(self, tokens: int):
+        if tokens <= self.capacity:
+            return
+        pages = -(-max(tokens, 2 * self.capacity) // self.PAGE)
+        for name in ("k", "v"):
+            old = getattr(self, name)
+            new = old.new_empty(*old.shape[:2], pages * self.PAGE, old.shape[3])
+            new.narrow(2, 0, self.n).copy_(old.narrow(2, 0, self.n))
+            setattr(self, name, new)
+
+    def append(self, k_new: torch.Tensor, v_new: torch.Tensor):
+        t = k_new.shape[2]
+        self.reserve(self.n + t)
+        self.k.narrow(2, self.n, t).copy_(k_new)
+        self.v.narrow(2, self.n, t).copy_(v_new)
+        self.n += t
+        return self.k.narrow(2, 0, self.n), self.v.narrow(2, 0, self.n)
+
+
+# the reference's name for the softmax layers' cache
+StaticKV = AnchorCache
+
+
+class Bolt3LayerState(MutableMapping):
+    """Decoder state of one Bolt-3 layer in preallocated device buffers.
+
+    The window is a ring of two halves of 2C tokens each: the previous chunk
+    ("prev") in one half, the chunk being filled ("cur") in the other.  Slot
+    state keeps the un-roped keys (ak) plus a cache of the keys roped at their
+    mean positions (slot_k) and the attention bias (slot_bias), refreshed by
+    every consolidation.  No tensor grows while decoding (the reference
+    concatenates).
+
+    It is a mapping with the keys of the reference's per-layer kv_caches dict
+    (vsa_lm/config/bolt3.py:310-315): reading a key gives a view in the
+    reference's shape (None for an empty part), assigning one rewrites the
+    state, ``to_dict`` / ``from_dict`` convert both ways (the form the memory
+    bank saves, vsa_lm/memory_bank.py:57-68).
+    """
+
+    KEYS = ("ak", "av", "mass", "util", "pm", "act", "sink_k", "sink_v", "prev_kr", "prev_kp", "prev_v",
+            "prev_pos", "prev_b", "cur_kr", "cur_kp", "cur_v", "cur_pos", "cur_b", "n_filled")
+
+    def __init__(self, ly: Bolt3Attn, B: int, device, dtype):
+        C, S, HKV, HD = ly.C, ly.S, ly.HKV, ly.HD
+        self.B, self.C, self.S, self.HKV, self.HD, self.dtype = B, C, S, HKV, HD, dtype
+        self._ly = ly
+        self.cap = 4 * C
+        self.win_kr = torch.zeros(B, HKV, self.cap, HD, dtype=dtype, device=device)
+        self.win_kp = torch.zeros_like(self.win_kr)
+        self.win_v = torch.zeros_like(self.win_kr)
+        self.win_b = torch.zeros(B, HKV, self.cap, device=device)
+        self.win_pos = torch.zeros(self.cap, device=device)
+        self.sink_k = torch.zeros(B, HKV, N_SINKS, HD, dtype=dtype, device=device)
+        self.sink_v = torch.zeros_like(self.sink_k)
+        self.n_sink = 0
+        bh = B * HKV
+        self.slots = ly._empty_slots(bh, dtype, device)
+        self.slot_k = torch.zeros(bh, S, HD, dtype=dtype, device=device)
+        self.slot_bias = torch.zeros(bh, S, device=device)
+        self.has_slots = False
+        self.n_filled = 0
+        self.prev = (0, 0)          # (start, length) in the ring
+        self.cur = (2 * C, 0)
+        self._dec_work = None
+        self._dec = None   # the one-token step: key, argument blocks, output and projection workspace
+
+    def decode_workspace(self, H: int) -> torch.Tensor:
+        """Scratch of the one-token decode kernels (partial softmax state per key range)."""
+        n = A.decode_workspace_bytes(self.B, H, self.HKV, self.HD) // 4
+        if self._dec_work is None or self._dec_work.numel() < n:
+            self._dec_work = torch.empty(n, device=self.win_kr.device)
+        return self._dec_work
+
+    def _seg(self, name, seg):
+        s, n = seg
+        if n == 0:
+            return None
+        if name == "pos":
+            return self.win_pos[s:s + n].view(1, 1, n)
+        if name == "b":
+            return self.win_b[:, :, s:s + n]
+        return {"kr": self.win_kr, "kp": self.win_kp, "v": self.win_v}[name][:, :, s:s + n]
+
+    def __getitem__(self, key):
+        B, HKV = self.B, self.HKV
+        if key in ("ak", "av"):   # [bh, S, HD], as _consolidate_functional returns them
+            return self.slots[key] if self.has_slots else None
+        if key in ("mass", "util", "pm"):
+            return self.slots[key].view(B * HKV, self.S) if self.has_slots else None
+        if key == "act":
+            return self.slots["act"].bool() if self.has_slots else None
+        if key in ("sink_k", "sink_v"):
+            return getattr(self, key)[:, :, :self.n_sink] if self.n_sink else None
+        if key == "n_filled":
+            return self.n_filled
+        for pre, seg in (("prev_", self.prev), ("cur_", self.cur)):
+            if key.startswith(pre):
+                return self._seg(key[len(pre):], seg)
+        raise KeyError(key)
+
+    # ------------------------------------------------------------ mapping with the reference's keys
+
+    def __iter__(self):
+        return iter(self.KEYS)
+
+    def __len__(self):
+        return len(self.KEYS)
+
+    def __setitem__(self, key, value):
+        if key not in self.KEYS:
+            raise KeyError(key)
+        d = self.to_dict()
+        d[key] = value
+        self.load_dict(d)
+
+    def __delitem__(self, key):
+        raise TypeError("Bolt3LayerState has a fixed key set; assign None to clear a part")
+
+    def to_dict(self) -> dict:
+        """Snapshot in the reference's kv_caches form (tensors copied, n_filled an int)."""
+        out = {}
+        for k in self.KEYS:
+            v = self[k]
+            out[k] = v.clone() if torch.is_tensor(v) else v
+        return out
+
+    @classmethod
+    def from_dict(cls, ly: "Bolt3Attn", d: dict, device=None, dtype=None) -> "Bolt3LayerState":
+        """State of layer ``ly`` from a reference kv_caches dict (any device; tensors are copied)."""
+        ref = next((v for v in d.values() if torch.is_tensor(v) and v.dim() == 4), None)
+        if ref is None:
+            raise ValueError("the dict holds no window, sink or slot tensors to size the state from")
+        B = ref.shape[0] if d.get("ak") is None else d["ak"].numel() // (ly.HKV * ly.S * ly.HD)
+        device = torch.device(device) if device is not None else ref.device
+        dtype = dtype or (d["ak"].dtype if d.get("ak") is not None else ref.dtype)
+        st = cls(ly, B, device, dtype)
+        st.load_dict(d)
+        return st
+
+    def load_dict(self, d: dict):
+        """Rewrite the whole state from a reference kv_caches dict.  The previous chunk goes to the
+        ring's first half, the current one to its second; the roped slot keys and the slot bias are
+        rebuilt from ak, pm, mass and act by the chain's own rotation (bolt3_slot_keys)."""
+        B, HKV, HD, S, C, dt = self.B, self.HKV, self.HD, self.S, self.C, self.dtype
+        dev = self.win_kr.device
+        bh = B * HKV
+
+        def put(dst, src, shape):
+            dst.copy_(src.detach().reshape(shape).to(device=dev, dtype=dst.dtype))
+
+        if d.get("ak") is None:
+            for k, v in self._ly._empty_slots(bh, dt, dev).items():
+                self.slots[k].copy_(v)
+            self.has_slots = False
+        else:
+            for k in ("ak", "av"):
+                put(self.slots[k], d[k], (bh, S, HD))
+            for k in ("mass", "util", "pm"):
+                put(self.slots[k], d[k], (bh, S))
+            put(self.slots["act"], d["act"].to(torch.uint8), (bh, S))
+            self.has_slots = True
+            self._refresh_slot_keys()
+        self.n_filled = int(d.get("n_filled") or 0)
+        if d.get("sink_k") is None:
+            self.n_sink = 0
+        else:
+            ns = d["sink_k"].shape[2]
+            if ns > N_SINKS:
+                raise ValueError(f"{ns} sink tokens; the state holds at most {N_SINKS}")
+            put(self.sink_k[:, :, :ns], d["sink_k"], (B, HKV, ns, HD))
+            put(self.sink_v[:, :, :ns], d["sink_v"], (B, HKV, ns, HD))
+            self.n_sink = ns
+        for pre, start in (("prev_", 0), ("cur_", 2 * C)):
+            kp = d.get(pre + "kp")
+            n = 0 if kp is None else kp.shape[2]
+            if n > 2 * C:
+                raise ValueError(f"{pre}* holds {n} tokens; a ring half holds at most {2 * C}")
+            if n:
+                put(self.win_kr[:, :, start:start + n], d[pre + "kr"], (B, HKV, n, HD))
+                put(self.win_kp[:, :, start:start + n], kp, (B, HKV, n, HD))
+                put(self.win_v[:, :, start:start + n], d[pre + "v"], (B, HKV, n, HD))
+                put(self.win_b[:, :, start:start + n], d[pre + "b"], (B, HKV, n))
+                put(self.win_pos[start:start + n], d[pre + "pos"], (n,))
+            if pre == "prev_":
+                self.prev = (start, n)
+            else:
+                self.cur = (start, n)
+
+    def _refresh_slot_keys(self):
+        ly = self._ly
+        dev = self.win_kr.device
+        a = A.SlotKeysArgs()
+        a.dtype, a.B, a.HKV, a.HD, a.S = A.dtype_code(self.dtype), self.B, self.HKV, self.HD, self.S
+        a.ak, a.pm, a.mass, a.act = (self.slots[k].data_ptr() for k in ("ak", "pm", "mass", "act"))
+        a.kappa = ly.kappa.detach().to(device=dev, dtype=torch.float32).contiguous().data_ptr()
+        a.inv_freq = ly.rope.inv_freq.to(device=dev, dtype=torch.float32).contiguous().data_ptr()
+        a.slot_k, a.slot_bias = self.slot_k.data_ptr(), self.slot_bias.data_ptr()
+        A.call("bolt3_slot_keys", a, dev)
+
+
+
+
+
+def sample_tokens(logits: torch.Tensor, temperature: float, top_k: int = 40, top_p: float = 0.95) -> torch.Tensor:
+    """Next token per row, [B, 1] (vsa_lm/config/bolt3.py:321-333): greedy at temperature <= 1e-5;
+    otherwise nucleus sampling of softmax(logits / temperature) when top_p < 1 (the smallest set of
+    most likely tokens whose mass before the last one is at most top_p), else sampling among the
+    top_k logits.  One multinomial draw per call, on the logits' device."""
+    if temperature <= 1e-5:
+        return logits.argmax(dim=-1, keepdim=True)
+    z = logits.float() / temperature
+    if top_p < 1.0:
+        prob, order = torch.softmax(z, dim=-1).sort(dim=-1, descending=True)
+        ahead = prob.cumsum(dim=-1) - prob           # probability mass ranked above each token
+        prob = prob.masked_fill(ahead > top_p, 0.0)
+        prob = prob / prob.sum(dim=-1, keepdim=True).clamp_min(1e-12)
+        return torch.gather(order, -1, torch.multinomial(prob, 1))
+    vals, idx = torch.topk(z, min(top_k, z.shape[-1]), dim=-1)
+    return torch.gather(idx, -1, torch.multinomial(torch.softmax(vals, dim=-1), 1))
+
+
+class _Bookkeeping:
+    """Per-row generation state on the device (vsa_lm/config/bolt3.py:464-494): the tokens, which
+    rows ended (eos) and after how many tokens, and the close-of-thinking sequence forced on rows
+    still thinking once the budget point is reached."""
+
+    def __init__(self, B: int, n_max: int, eos_ids, close_ids, dev):
+        self.n_max = n_max
+        self.toks = torch.zeros(B, n_max, dtype=torch.long, device=dev)
+        self.lengths = torch.full((B,), n_max, dtype=torch.long, device=dev)
+        self.done = torch.zeros(B, dtype=torch.bool, device=dev)
+        self.eos = torch.tensor(sorted(eos_ids or ()), dtype=torch.long, device=dev)
+        self.close = torch.tensor(list(close_ids or ()), dtype=torch.long, device=dev)
+        self.end_think = int(close_ids[1]) if close_ids and len(close_ids) > 1 else None
+        self.closed = torch.zeros(B, dtype=torch.bool, device=dev)
+        self.cursor = torch.full((B,), -1, dtype=torch.long, device=dev)   # next forced index, -1: none
+        self.budget = max(64, n_max - 64)
+        self._flag = torch.zeros(1, dtype=torch.bool).pin_memory() if torch.cuda.is_available() else None
+        self._flag_at = None
+        self._flag_ev = None
+
+    def take(self, i: int, nxt: torch.Tensor) -> torch.Tensor:
+        """Record token i of every row ([B, 1]) after the forced sequence is applied."""
+        n_close = self.close.numel()
+        if n_close:
+            if i == self.budget:
+                start = ~self.closed & ~self.done & (self.cursor < 0)
+                self.cursor = torch.where(start, torch.zeros_like(self.cursor), self.cursor)
+            forcing = self.cursor >= 0
+            forced = self.close[self.cursor.clamp(0, n_close - 1)]
+            nxt = torch.where(forcing.unsqueeze(1), forced.unsqueeze(1), nxt)
+            self.cursor = torch.where(forcing, self.cursor + 1, self.cursor)
+            finished = forcing & (self.cursor >= n_close)
+            self.cursor = torch.where(finished, torch.full_like(self.cursor, -1), self.cursor)
+            self.closed = self.closed | finished
+            if self.end_think is not None:
+                self.closed = self.closed | (nxt[:, 0] == self.end_think)
+        self.toks[:, i] = nxt[:, 0]
+        if self.eos.numel():
+            hit = torch.isin(nxt[:, 0], self.eos) & ~self.done
+            self.lengths = torch.where(hit, torch.full_like(self.lengths, i + 1), self.lengths)
+            self.done = self.done | hit
+        return nxt
+
+    def stop_at(self, i: int) -> int | None:
+        """Token count at which the reference would have stopped, as far as known now.  At every
+        DONE_CHECK_EVERY-th token the all-done flag is copied to host memory without waiting; it is
+        read at the next check (or at the end), by which time the copy has long finished."""
+        if not self.eos.numel():
+            return None
+        last = i == self.n_max - 1
+        if i % DONE_CHECK_EVERY != DONE_CHECK_EVERY - 1 and not last:
+            return None
+        stop = None
+        if self._flag_at is not None:
+            self._flag_ev.synchronize()
+            if bool(self._flag[0]):
+                stop = self._flag_at + 1
+            self._flag_at = None
+        if stop is None and i % DONE_CHECK_EVERY == DONE_CHECK_EVERY - 1:
+            self._flag.copy_(self.done.all().view(1), non_blocking=True)
+            self._flag_ev = torch.cuda.Event()
+            self._flag_ev.record()
+            self._flag_at = i
+            if last:                         # nothing runs after the last token: read it now
+                self._flag_ev.synchronize()
+                stop = i + 1 if bool(self._flag[0]) else None
+        return stop
+
+
+class Bolt3Decoder:
+    """Constant-memory decoder over a hybrid Bolt-3 / softmax stack (vsa_lm/config/bolt3.py:279-557)."""
+
+    def __init__(self, model, wrap_positions: bool = False, max_cache_pos: int = 65536, **kwargs):
+        self.model = model.eval()
+        self.max_T = model.config["max_T"]
+        self.max_cache_pos = max_cache_pos
+        self.wrap_positions = wrap_positions
+        self.C = int(model.config.get("bolt3_C", 128))
+        # bf16 one-token steps run as one bolt3_decode_layer call (projections included); False
+        # keeps the projections in torch around bolt3_decode (the tests compare the two)
+        self.fuse_projections = True
+
+    def _graph_runner(self, B: int, need_len: int, device):
+        return None
+
+    # ------------------------------------------------------------ state
+
+    @staticmethod
+    def state_bytes(model):
+        """(bytes that do not grow with the context, bytes per cached token) of a decode state, counted
+        as the reference counts them (vsa_lm/config/bolt3.py:290-300): M_res in fp32, slot keys and
+        values, a window of two chunks of keys and values, anchor keys and values, all at 2 bytes."""
+        fixed = per_token = 0
+        for blk in model.blocks:
+            if hasattr(blk, "vsa"):
+                a = blk.vsa
+                row = a.HKV * a.HD                    # one token's (or slot's) keys across kv heads
+                fixed += row * a.HD * 4 + (2 * a.S + 4 * a.C) * row * 2
+            else:
+                per_token += 4 * blk.attn.HKV * blk.attn.HD
+        return fixed, per_token
+
+    @staticmethod
+    def blank_state(model, batch_size: int, device, max_kv_len: int = 4096, state_dtype=torch.float32,
+                    dtype=None, **kwargs):
+        """Empty decode state: M_res per Bolt-3 layer (fp32 [B, HKV, HD, HD], None for anchors) and a
+        cache per layer (Bolt3LayerState / AnchorCache) in the model's activation dtype."""
+        device = torch.device(device)
+        if device.type != "cuda":
+            raise RuntimeError("Bolt3Decoder.blank_state: the Bolt-3 HIP path needs a ROCm device")
+        if state_dtype != torch.float32:
+            raise TypeError(f"M_res is kept in fp32 by the kernels (state_dtype={state_dtype} requested)")
+        dt = dtype or next(model.parameters()).dtype
+        states, caches = [], []
+        for blk in model.blocks:
+            if hasattr(blk, "vsa"):
+                ly = blk.vsa
+                states.append(torch.zeros(batch_size, ly.HKV, ly.HD, ly.HD, device=device))
+                caches.append(Bolt3LayerState(ly, batch_size, device, dt))
+            else:
+                states.append(None)
+                caches.append(AnchorCache(batch_size, blk.attn.HKV, max_kv_len, blk.attn.HD, device, dt))
+        return states, caches
+
+    @staticmethod
+    def _sample(logits, temperature: float, top_k: int = 40, top_p: float = 0.95):
+        return sample_tokens(logits, temperature, top_k, top_p)
+
+    # ------------------------------------------------------------ one Bolt-3 layer
+
+    def _bolt3_layer(self, ly: Bolt3Attn, h, pos_start: int, m_state: torch.Tensor, st: Bolt3LayerState,
+                     record=None):
+        B, t, _ = h.shape
+        dt, dev = h.dtype, h.device
+        if dt != st.dtype:
+            raise TypeError(f"activation dtype {dt} differs from the decoder state dtype {st.dtype}")
+        _check_m_state(m_state, B, ly)
+        if t > ly.C:
+            raise NotImplementedError(f"step takes at most C={ly.C} tokens per call (got {t})")
+        H, HKV, HD, S = ly.H, ly.HKV, ly.HD, ly.S
+        W, bias, side = ly._packed(dt, dev)
+        gam = side["gamma"]
+        cs, cl = st.cur
+        ps, pl = st.prev
+        h = h if h.is_contiguous() else h.contiguous()
+        if t == 1:
+            # The argument block, the projection row and the attention output are kept in the
+            # layer state; a step only refreshes the position, the ring segments and the input
+            # and output rows.  bf16 runs the whole step (both projections included) in one
+            # bolt3_decode_layer call.
+            fused = self.fuse_projections and _fused_step_ok(dt, h.shape[-1], H * HD, side["wo"].shape[0])
+            key = (id(side), m_state.data_ptr(), W.data_ptr(), fused)
+            if st._dec is None or st._dec[0] != key:
+                y = torch.empty(B, H * HD, dtype=dt, device=dev)
+                n_out = side["wo"].shape[0]
+                pw = torch.empty(A.decode_layer_workspace_bytes(B, h.shape[-1], W.shape[0], H * HD, n_out) // 4,
+                                 device=dev) if fused else None
+                la = A.DecodeLayerArgs() if fused else None
+                a = la.dec if fused else A.DecodeArgs()   # la.dec shares la's memory
+                a.dtype, a.B, a.H, a.HKV, a.HD, a.S = A.dtype_code(dt), B, H, HKV, HD, S
+                a.lin_row_stride = W.shape[0]
+                a.qn_w, a.kn_w, a.has_qk_norm = A.ptr(side["qn"]), A.ptr(side["kn"]), int(side["qn"] is not None)
+                a.eps, a.inv_freq = float(ly.res_norm.eps), side["inv_freq"].data_ptr()
+                a.win_kr, a.win_kp, a.win_v = st.win_kr.data_ptr(), st.win_kp.data_ptr(), st.win_v.data_ptr()
+                a.w_sb, a.w_sh = st.win_kr.stride(0), st.win_kr.stride(1)
+                a.win_beta, a.wb_sb, a.wb_sh = st.win_b.data_ptr(), st.win_b.stride(0), st.win_b.stride(1)
+                a.win_pos = st.win_pos.data_ptr()
+                a.sink_k, a.sink_v = st.sink_k.data_ptr(), st.sink_v.data_ptr()
+                a.s_sb, a.s_sh = st.sink_k.stride(0), st.sink_k.stride(1)
+                a.slot_k, a.slot_v, a.slot_bias = st.slot_k.data_ptr(), st.slots["av"].data_ptr(), \
+                    st.slot_bias.data_ptr()
+                a.m_res, a.gamma, a.res_w, a.y = m_state.data_ptr(), gam.data_ptr(), side["res_w"].data_ptr(), \
+                    y.data_ptr()
+                work = st.decode_workspace(H)
+                a.work, a.work_bytes = work.data_ptr(), work.numel() * 4
+                if fused:
+                    la.proj_work, la.proj_work_bytes = pw.data_ptr(), pw.numel() * 4
+                    la.x_row_stride, la.d_model = h.shape[-1], h.shape[-1]
+                    la.w_in, la.b_in, la.n_in = W.data_ptr(), A.ptr(bias), W.shape[0]
+                    la.w_out, la.b_out, la.n_out = side["wo"].data_ptr(), None, side["wo"].shape[0]
+                    la.out_row_stride = side["wo"].shape[0]
+                st._dec = (key, la if fused else a, a, y, pw, side, W, bias)
+            _, call_args, a, y, _, _, _, _ = st._dec
+            a.pos = int(pos_start)
+            a.a_start, a.a_len, a.b_start, a.b_len = ps, pl, cs, cl
+            a.n_sink_keys, a.has_slots = st.n_sink, int(st.has_slots)
+            if fused:
+                out = torch.empty(B, 1, side["wo"].shape[0], dtype=dt, device=dev)
+                call_args.x, call_args.out = h.data_ptr(), out.data_ptr()
+                A.call("bolt3_decode_layer", call_args, dev)
+                st.cur = (cs, cl + 1)
+                if st.cur[1] >= ly.C:
+                    self._consolidate(ly, st, m_state, gam, side, record)
+                return out
+            lin = F.linear(h, W, bias)
+            _check_dtype(lin, dt, "packed projection")
+            a.lin = lin.data_ptr()
+            A.call("bolt3_decode", a, dev)
+            y = y.view(B, 1, H * HD)
+        else:
+            lin = F.linear(h, W, bias)
+            _check_dtype(lin, dt, "packed projection")
+            q_raw = torch.empty(B, H, t, HD, dtype=dt, device=dev)
+            q_rope = torch.empty_like(q_raw)
+            eta = torch.empty(B, H, t, device=dev)
+            ly._heads(lin, B, t, dt, side, pos_start, q_raw, q_rope, st.win_kr, st.win_kp, st.win_v, st.win_b, eta,
+                      pos_out=st.win_pos, kv_offset=cs + cl)
+            y = torch.empty(B, t, H * HD, dtype=dt, device=dev)
+            a = A.AttnArgs()
+            a.dtype, a.B, a.H, a.HKV, a.HD, a.S, a.C, a.n_sinks = A.dtype_code(dt), B, H, HKV, HD, S, ly.C, ly.n_sinks
+            a.mode, a.n_q, a.score_round = 1, t, 0
+            a.q_rope, a.q_raw, a.q_sb, a.q_sh = q_rope.data_ptr(), q_raw.data_ptr(), q_rope.stride(0), q_rope.stride(1)
+            a.eta, a.e_sb, a.e_sh = eta.data_ptr(), eta.stride(0), eta.stride(1)
+            a.win_k, a.win_v, a.w_sb, a.w_sh = st.win_kp.data_ptr(), st.win_v.data_ptr(), st.win_kp.stride(0), \
+                st.win_kp.stride(1)
+            a.a_start, a.a_len, a.b_start, a.b_len = ps, pl, cs, cl + t
+            a.sink_k, a.sink_v = st.sink_k.data_ptr(), st.sink_v.data_ptr()
+            a.s_sb, a.s_sh, a.n_sink_keys = st.sink_k.stride(0), st.sink_k.stride(1), st.n_sink
+            a.slot_k, a.slot_v, a.slot_bias = st.slot_k.data_ptr(), st.slots["av"].data_ptr(), st.slot_bias.data_ptr()
+            a.slot_step, a.has_slots = 0, int(st.has_slots)
+            a.m_res, a.m_step = m_state.data_ptr(), 0
+            a.gamma, a.res_w, a.eps = gam.data_ptr(), side["res_w"].data_ptr(), float(ly.res_norm.eps)
+            a.y, a.y_sb, a.y_st = y.data_ptr(), y.stride(0), y.stride(1)
+            A.call("bolt3_chunk_attn", a, dev)
+        st.cur = (cs, cl + t)
+        out = F.linear(y, side["wo"])
+        if st.cur[1] >= ly.C:
+            self._consolidate(ly, st, m_state, gam, side, record)
+        return out
+
+    def _consolidate(self, ly: Bolt3Attn, st: Bolt3LayerState, m_state, gam, side, record=None):
+        ps, pl = st.prev
+        if pl > 0:
+            off, l = ps, pl
+            if st.n_sink == 0:
+                ns = min(ly.n_sinks, l)
+                st.sink_k[:, :, :ns].copy_(st.win_kp[:, :, off:off + ns])
+                st.sink_v[:, :, :ns].copy_(st.win_v[:, :, off:off + ns])
+                st.n_sink = ns
+                off, l = off + ns, l - ns
+            if st.n_filled == 0:
+                for k, v in ly._empty_slots(st.B * st.HKV, st.dtype, m_state.device).items():
+                    st.slots[k].copy_(v)
+                m_state.zero_()
+            log = None
+            if record is not None:
+                log = torch.zeros(1, st.B * st.HKV, A.LOG_ROWS, A.LOG_COLS, device=m_state.device)
+                record.append(dict(log=log[0], n_filled=st.n_filled, tokens=l))
+            ly._chain(st.dtype, m_state.device, st.B, st.win_kr.data_ptr(), st.win_kp.data_ptr(),
+                      st.win_v.data_ptr(), st.cap * st.HD, st.win_pos.data_ptr(), st.win_b.data_ptr(), st.cap,
+                      1, off, l, l, l, st.n_filled, st.slots, m_state, gam, side,
+                      snap_k=st.slot_k, snap_bias=st.slot_bias, kp_exact=True, log=log)
+            if st.n_filled < ly.S:
+                st.n_filled += min(ly.S - st.n_filled, l)
+            st.has_slots = True
+        cs, cl = st.cur
+        st.prev = (cs, cl)
+        st.cur = (0 if cs == 2 * ly.C else 2 * ly.C, 0)
+
+    # ------------------------------------------------------------ one softmax-anchor layer
+
+    def _anchor_layer(self, ly, h: torch.Tensor, pos_start: int, cache: AnchorCache) -> torch.Tensor:
+        """Causal softmax attention of t new tokens over the cached ones and themselves
+        (vsa_lm/config/bolt3.py:426-445): query i sees cached keys and new keys up to i."""
+        b, t, _ = h.shape
+        q, k, v = ly.head_qkv(h)
+        q, k = ly.rope(q, pos_start=pos_start), ly.rope(k, pos_start=pos_start)
+        n_old = cache.n
+        keys, vals = cache.append(k, v)
+        visible = None
+        if t > 1:
+            visible = torch.ones(t, n_old + t, dtype=torch.bool, device=h.device).tril(diagonal=n_old)
+        y = F.scaled_dot_product_attention(q, keys.to(q.dtype), vals.to(q.dtype), attn_mask=visible,
+                                           enable_gqa=ly.G > 1)
+        return ly.o_proj(y.transpose(1, 2).reshape(b, t, ly.H * ly.HD))
+
+    # ------------------------------------------------------------ model-level API
+
+    @torch.no_grad()
+    def step(self, tokens: torch.Tensor, pos_start: int, states, kv_caches, record=None):
+        """Run the tokens [B, t] (t <= C) through every layer at positions pos_start.. and update the
+        states in place.  Returns (normed hidden states [B, t, D], states, kv_caches).  ``record``: a
+        list (or a dict per layer index) that receives the decision log of every consolidation."""
+        m = self.model
+        with torch.autocast(tokens.device.type, enabled=False):
+            x = m.embed_tokens(tokens)
+            for li, blk in enumerate(m.blocks):
+                h = blk.norm1(x)
+                if hasattr(blk, "vsa"):
+                    rec = record.setdefault(li, []) if isinstance(record, dict) else record
+                    x = x + self._bolt3_layer(blk.vsa, h, pos_start, states[li], kv_caches[li], rec)
+                else:
+                    x = x + self._anchor_layer(blk.attn, h, pos_start, kv_caches[li])
+                x = x + blk.mlp(blk.norm2(x))
+            return m.norm(x), states, kv_caches
+
+    def _feed(self, ids: torch.Tensor, pos: int, states, kv_caches):
+        """Step ids through the model in chunks of C tokens; returns (last hidden states, next position)."""
+        h = None
+        for s in range(0, ids.shape[1], self.C):
+            part = ids[:, s:s + self.C]
+            h, _, _ = self.step(part, pos, states, kv_caches)
+            pos += part.shape[1]
+        return h, pos
+
+    @torch.no_grad()
+    def prefill(self, ids: torch.Tensor, max_kv_len: int = 4096):
+        b, t = ids.shape
+        states, kv = self.blank_state(self.model, b, ids.device, max_kv_len=max(max_kv_len, t + 1024))
+        h, _ = self._feed(ids, 0, states, kv)
+        return h, states, kv
+
+    @torch.no_grad()
+    def generate_batch(self, ids: torch.Tensor, max_new_tokens: int, temperature: float = 0.6, top_k: int = 40,
+                       top_p: float = 0.95, eos_ids: set[int] | None = None,
+                       close_think_ids: list[int] | None = None):
+        """Prefill ids [B, T], then generate up to max_new_tokens per row.  Returns (tokens
+        [B, n], lengths [B]): n is max_new_tokens unless every row has ended by a check point (then
+        the tokens up to that point), lengths the tokens up to and including each row's eos."""
+        B, T = ids.shape
+        h, states, kv = self.prefill(ids, max_kv_len=T + max_new_tokens + 64)
+        book = _Bookkeeping(B, max_new_tokens, eos_ids, close_think_ids, ids.device)
+        logits = self.model.lm_head(h[:, -1])
+        n_out = max_new_tokens
+        for i in range(max_new_tokens):
+            nxt = book.take(i, sample_tokens(logits, temperature, top_k, top_p))
+            stop = book.stop_at(i)
+            if stop is not None:
+                n_out = stop
+                break
+            if i + 1 < max_new_tokens:
+                h, _, _ = self.step(nxt, T + i, states, kv)
+                logits = self.model.lm_head(h[:, -1])
+        return book.toks[:, :n_out], book.lengths
+
+    @torch.no_grad()
+    def generate(self, prompt: torch.Tensor, max_new_tokens: int, temperature: float = 0.0, top_k: int = 40,
+                 top_p: float = 0.95, eos_ids: set[int] | None = None, close_think_ids: list[int] | None = None):
+        """The prompt followed by the first row's generated tokens (up to its eos), [B, T + n]."""
+        toks, lengths = self.generate_batch(prompt, max_new_tokens, temperature, top_k, top_p, eos_ids,
+                                            close_think_ids)
+        return torch.cat([prompt, toks[:, :int(lengths[0])]], dim=1)
+
+    @torch.no_grad()
+    def continue_generate(self, ids: torch.Tensor, states, kv_caches, start_pos: int, max_new_tokens: int,
+                          temperature: float = 0.0, top_k: int = 40, top_p: float = 0.95,
+                          eos_ids: set[int] | None = None):
+        """Feed ids from start_pos on an existing state, then generate until the first row emits an
+        eos id (that token is returned but not fed).  Returns (tokens, states, kv_caches, next position).
+        The returned state must not include tokens after the stop, so each token's stop test is read
+        back before the token is fed."""
+        h, pos = self._feed(ids, start_pos, states, kv_caches)
+        stop = torch.tensor(sorted(eos_ids or ()), dtype=torch.long, device=ids.device)
+        toks = torch.empty(ids.shape[0], max_new_tokens, dtype=torch.long, device=ids.device)
+        n = 0
+        logits = self.model.lm_head(h[:, -1])
+        while n < max_new_tokens:
+            nxt = sample_tokens(logits, temperature, top_k, top_p)
+            toks[:, n] = nxt[:, 0]
+            n += 1
+            if stop.numel() and bool(torch.isin(nxt[0, 0], stop)):
+                break
+            h, _, _ = self.step(nxt, pos, states, kv_caches)
+            logits = self.model.lm_head(h[:, -1])
+            pos += 1
+        return toks[:, :n], states, kv_caches, pos
+
+    @torch.no_grad()
+    def memorize(self, ids: torch.Tensor, states, kv_caches, start_pos: int):
+        """Feed ids and return, per Bolt-3 layer, what they wrote into M_res: (next position,
+        M_after - gamma^(tokens // C) * M_before), None for anchor layers
+        (vsa_lm/config/bolt3.py:528-546).  Returns (states, kv_caches, next position, traces)."""
+        before = [None if s is None else s.clone() for s in states]
+        _, pos = self._feed(ids, start_pos, states, kv_caches)
+        traces = []
+        for li, blk in enumerate(self.model.blocks):
+            if not hasattr(blk, "vsa"):
+                traces.append(None)
+                continue
+            ly = blk.vsa
+            decay = ly.gamma_delta().view(1, -1, 1, 1).to(states[li].device) ** (ids.shape[1] // ly.C)
+            traces.append((pos, states[li] - decay * before[li]))
+        return states, kv_caches, pos, traces
+
+    @torch.no_grad()
+    def forget(self, traces, states, next_pos: int, kv_caches=None, pre_kv_lens=None):
+        """Take memorized writes back out of M_res, each decayed by gamma once per C positions between
+        the end of its tokens and next_pos (vsa_lm/config/bolt3.py:548-557)."""
+        for li, tr in enumerate(traces):
+            if tr is None or states[li] is None:
+                continue
+            end_pos, delta = tr
+            ly = self.model.blocks[li].vsa
+            k = max(0, (next_pos - end_pos) // ly.C)
+            states[li] = states[li] - ly.gamma_delta().view(1, -1, 1, 1).to(delta.device) ** k * delta
+        return states

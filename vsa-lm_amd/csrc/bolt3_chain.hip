@@ -2102,6 +2102,38 @@ __global__ void __launch_bounds__(64) wait_count_kernel(const uint32_t* counter,
   }
 }
 
+// Roped slot keys and attention bias of a slot state, with the chain's own rounding: one
+// workgroup per bh, 8 rotation pairs per item (the per-step snapshot the decode step reads).
+template <typename T, int HD>
+__global__ void __launch_bounds__(MT) slot_keys_kernel(b3_slot_keys_args a) {
+  constexpr int HALF = HD / 2, P8 = HALF / 8;
+  const int bh = blockIdx.x, hkv = bh % a.HKV;
+  const T* ak = reinterpret_cast<const T*>(a.ak) + (long long)bh * S * HD;
+  T* dst = reinterpret_cast<T*>(a.slot_k) + (long long)bh * S * HD;
+  for (int it = threadIdx.x; it < S * P8; it += MT) {
+    const int s = it / P8, i0 = (it % P8) * 8;
+    float x0[8], x1[8];
+    ld8(ak + s * HD + i0, x0);
+    ld8(ak + s * HD + i0 + HALF, x1);
+    const float p = a.pm[bh * S + s];
+    alignas(16) T r0[8];
+    alignas(16) T r1[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      float sn, cs;
+      sincos_rope(mul_rn(p, a.inv_freq[i0 + q]), &sn, &cs);
+      const float c = St<T>::rnd(cs), si = St<T>::rnd(sn);
+      r0[q] = St<T>::from_f(add_rn(St<T>::rnd(mul_rn(x0[q], c)), St<T>::rnd(mul_rn(-x1[q], si))));
+      r1[q] = St<T>::from_f(add_rn(St<T>::rnd(mul_rn(x1[q], c)), St<T>::rnd(mul_rn(x0[q], si))));
+    }
+    copy8(dst + s * HD + i0, r0);
+    copy8(dst + s * HD + i0 + HALF, r1);
+  }
+  for (int s = threadIdx.x; s < S; s += MT)
+    a.slot_bias[bh * S + s] = a.act[bh * S + s] ? mul_rn(a.kappa[hkv], logf(fmaxf(a.mass[bh * S + s], 1.0f)))
+                                                : -INFINITY;
+}
+
 template <typename T, int HD>
 static int launch_chain(const b3_chain_args& a, hipStream_t st) {
   const int BH = a.B * a.HKV;
@@ -2151,4 +2183,23 @@ extern "C" int bolt3_chain(const b3_chain_args* a, void* stream) {
   if (a->dtype == B3_BF16)
     return a->HD == 64 ? b3::launch_chain<uint16_t, 64>(*a, st) : b3::launch_chain<uint16_t, 128>(*a, st);
   return B3_ERR_UNSUPPORTED;
+}
+
+extern "C" int bolt3_slot_keys(const b3_slot_keys_args* a, void* stream) {
+  if (!a || a->B <= 0 || a->HKV <= 0) return B3_ERR_ARG;
+  if (a->S != b3::S || (a->HD != 64 && a->HD != 128)) return B3_ERR_UNSUPPORTED;
+  if (!a->ak || !a->pm || !a->mass || !a->act || !a->kappa || !a->inv_freq || !a->slot_k || !a->slot_bias)
+    return B3_ERR_ARG;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid(a->B * a->HKV), block(b3::MT);
+  if (a->dtype == B3_F32) {
+    if (a->HD == 64) hipLaunchKernelGGL((b3::slot_keys_kernel<float, 64>), grid, block, 0, st, *a);
+    else hipLaunchKernelGGL((b3::slot_keys_kernel<float, 128>), grid, block, 0, st, *a);
+  } else if (a->dtype == B3_BF16) {
+    if (a->HD == 64) hipLaunchKernelGGL((b3::slot_keys_kernel<uint16_t, 64>), grid, block, 0, st, *a);
+    else hipLaunchKernelGGL((b3::slot_keys_kernel<uint16_t, 128>), grid, block, 0, st, *a);
+  } else {
+    return B3_ERR_UNSUPPORTED;
+  }
+  return (int)hipGetLastError();
 }

@@ -92,10 +92,22 @@ template <> struct Vec8<float> {
 };
 
 // IEEE single ops that the compiler must not contract into FMAs (the
-// reference evaluates these as separate tensor ops).
-__device__ __forceinline__ float mul_rn(float a, float b) { return __fmul_rn(a, b); }
-__device__ __forceinline__ float add_rn(float a, float b) { return __fadd_rn(a, b); }
-__device__ __forceinline__ float sub_rn(float a, float b) { return __fsub_rn(a, b); }
+// reference evaluates these as separate tensor ops).  HIP's __fmul_rn / __fadd_rn
+// are plain operators, which hipcc (fp-contract=fast) fuses with a neighbouring
+// add wherever inlining puts one; the instructions emitted here carry no
+// contraction flag, so every call site rounds alike.
+__device__ __forceinline__ float mul_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a * b;
+}
+__device__ __forceinline__ float add_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a + b;
+}
+__device__ __forceinline__ float sub_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a - b;
+}
 __device__ __forceinline__ float div_rn(float a, float b) { return __fdiv_rn(a, b); }
 
 // ---------------------------------------------------------------- MFMA

@@ -5,13 +5,15 @@
 // Elementary Functions", 1980); the reduced argument |r| <= ~pi/4 feeds the
 // Taylor series of sin (to r^9) and cos (to r^10), whose truncation error on
 // that interval is below 2e-10.  Valid for |x| < 2^20 (RoPE angles here are
-// position * inverse frequency <= 65536 * 1); max error about 2 ulp.
+// position * inverse frequency <= 65536 * 1); max error about 2 ulp.  Host and device
+// evaluate the same IEEE operations (fmaf, rintf), so a host build reproduces the device
+// values bit for bit (tests/test_rope_math.py checks the whole range that way).
 #pragma once
 #include <hip/hip_runtime.h>
 
 namespace b3 {
 
-__device__ __forceinline__ void sincos_rope(float x, float* s_out, float* c_out) {
+__host__ __device__ __forceinline__ void sincos_rope(float x, float* s_out, float* c_out) {
   const float k = rintf(x * 0.636619772367581343f);
   // pi/2 = P1 + P2 + P3 (each the fp32 rounding of what remains)
   const float P1 = 1.57079637050628662109375f;

@@ -153,6 +153,20 @@ typedef struct {
  * S == 128, HD in {64, 128}.
  */
 int bolt3_chain(const b3_chain_args* a, void* stream);
+/*
+ * bolt3_chain without a caller workspace: the same kernels and results, with the workspace taken
+ * from a scratch array of B3_CHAIN_NOALLOC_SCRATCH_BYTES that the library keeps on each GPU (held
+ * until the process ends).  No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops).  a->work and
+ * a->work_bytes are ignored; a launch whose bolt3_chain_workspace_bytes(...) exceeds the
+ * scratch size is rejected with B3_ERR_WORKSPACE before anything runs.  Call it with the
+ * stream's device current.  Every call on one GPU shares that GPU's scratch, so calls that
+ * overlap on one GPU race (also a phase-2 call beside another phase-1 call); the scratch needs
+ * no clearing (every byte the kernels read was written by the same call).  Allocates nothing.
+ */
+#define B3_CHAIN_NOALLOC_SCRATCH_BYTES (4 << 20)
+int bolt3_chain_noalloc(const b3_chain_args* a, void* stream);
+
 /* Workspace bytes for a launch of n_steps steps: per-step delta-rule weights and Gershgorin
    scales (3 x n_steps x B*HKV x 256 floats) plus, for fp32 storage with HD == 128, the roped
    slot keys (B*HKV x S x HD floats). */

@@ -66,6 +66,10 @@ def test_rejects_bad_arguments_without_gpu_work():
     la.dec.dtype = 1
     assert lib.bolt3_decode_layer(ctypes.byref(la), None) == 1001
     assert lib.bolt3_wait_count(None, 1, 10, None) == 1001
+    assert lib.bolt3_chain_noalloc(None, None) == 1001
+    big = A.ChainArgs()
+    big.dtype, big.B, big.HKV, big.HD, big.S, big.n_steps = 1, 64, 8, 128, 128, 100
+    assert lib.bolt3_chain_noalloc(ctypes.byref(big), None) == 1003   # beyond the library's scratch
     sk = A.SlotKeysArgs()
     sk.dtype, sk.B, sk.HKV, sk.HD, sk.S = 1, 1, 1, 128, 128
     assert lib.bolt3_slot_keys(ctypes.byref(sk), None) == 1001        # null pointers
@@ -123,3 +127,10 @@ def test_no_packed_fp32_in_device_code():
                                capture_output=True, text=True)
             assert r.returncode == 0, r.stderr[-2000:]
             assert not pat.search(open(out).read()), src
+
+
+def test_noalloc_scratch_size_matches_header():
+    txt = open(HEADER).read()
+    m = re.search(r"#define B3_CHAIN_NOALLOC_SCRATCH_BYTES \((\d+) << (\d+)\)", txt)
+    assert m and int(m.group(1)) << int(m.group(2)) == A.CHAIN_NOALLOC_SCRATCH_BYTES
+

@@ -106,7 +106,10 @@ class SlotKeysArgs(C.Structure):
     ]
 
 
-EXPORTS = ("bolt3_heads", "bolt3_chain", "bolt3_chain_workspace_bytes", "bolt3_chunk_attn", "bolt3_decode",
+CHAIN_NOALLOC_SCRATCH_BYTES = 4 << 20   # B3_CHAIN_NOALLOC_SCRATCH_BYTES
+
+EXPORTS = ("bolt3_heads", "bolt3_chain", "bolt3_chain_noalloc", "bolt3_chain_workspace_bytes", "bolt3_chunk_attn",
+           "bolt3_decode",
            "bolt3_decode_layer", "bolt3_decode_layer_workspace_bytes", "bolt3_decode_workspace_bytes",
            "bolt3_slot_keys", "bolt3_version", "bolt3_wait_count")
 
@@ -122,7 +125,8 @@ def load():
         raise RuntimeError(f"{LIB_PATH} is missing: build it with __graft_entry__.build() "
                            f"(python -m bolt3_amd.build); there is no CPU implementation")
     lib = C.CDLL(LIB_PATH)
-    for name, st in (("bolt3_heads", HeadsArgs), ("bolt3_chain", ChainArgs), ("bolt3_chunk_attn", AttnArgs),
+    for name, st in (("bolt3_heads", HeadsArgs), ("bolt3_chain", ChainArgs), ("bolt3_chain_noalloc", ChainArgs),
+                     ("bolt3_chunk_attn", AttnArgs),
                      ("bolt3_decode", DecodeArgs), ("bolt3_decode_layer", DecodeLayerArgs),
                      ("bolt3_slot_keys", SlotKeysArgs)):
         fn = getattr(lib, name)

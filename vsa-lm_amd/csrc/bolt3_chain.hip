@@ -30,6 +30,7 @@
 // splits fp32 operands into hi + lo; fp32 storage uses the fp32 MFMA.
 // Orderings are ranks computed by counting on monotone integer keys (one pass,
 // stable): the larger value first (NaN first), equal values by lower index.
+#include <mutex>
 #include <type_traits>
 
 #include "bolt3_common.h"
@@ -2149,6 +2150,35 @@ static int launch_chain(const b3_chain_args& a, hipStream_t st) {
   return (int)hipGetLastError();
 }
 
+// ----------------------------------------------------------------- allocation-free entry
+//
+// bolt3_chain_noalloc takes its workspace from this file-scope array instead of the caller.
+// Host code never uses the array's name as an address: the device address of each GPU's copy
+// comes from hipGetSymbolAddress, taken once per device (with that device current) on the
+// first call there.
+static __device__ __align__(256) uint8_t scratch[B3_CHAIN_NOALLOC_SCRATCH_BYTES];
+
+constexpr int MAX_DEVICES = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[MAX_DEVICES];
+
+static int scratch_address(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= MAX_DEVICES) return B3_ERR_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (!p) return B3_ERR_UNSUPPORTED;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return B3_OK;
+}
+
 }  // namespace b3
 
 extern "C" int64_t bolt3_chain_workspace_bytes(int32_t dtype, int32_t B, int32_t HKV, int32_t HD, int32_t S,
@@ -2202,4 +2232,19 @@ extern "C" int bolt3_slot_keys(const b3_slot_keys_args* a, void* stream) {
     return B3_ERR_UNSUPPORTED;
   }
   return (int)hipGetLastError();
+}
+
+extern "C" int bolt3_chain_noalloc(const b3_chain_args* a, void* stream) {
+  if (!a || a->B <= 0 || a->HKV <= 0 || a->n_steps < 0) return B3_ERR_ARG;
+  if (a->S != b3::S || (a->HD != 64 && a->HD != 128)) return B3_ERR_UNSUPPORTED;
+  if (a->dtype != B3_F32 && a->dtype != B3_BF16) return B3_ERR_UNSUPPORTED;
+  if (bolt3_chain_workspace_bytes(a->dtype, a->B, a->HKV, a->HD, a->S, a->n_steps) > B3_CHAIN_NOALLOC_SCRATCH_BYTES)
+    return B3_ERR_WORKSPACE;
+  void* p = nullptr;
+  const int rc = b3::scratch_address(&p);
+  if (rc != B3_OK) return rc;
+  b3_chain_args c = *a;
+  c.work = p;
+  c.work_bytes = B3_CHAIN_NOALLOC_SCRATCH_BYTES;
+  return bolt3_chain(&c, stream);
 }

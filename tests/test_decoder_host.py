@@ -89,3 +89,18 @@ def test_state_bytes_counts():
     hkv, hd, S, C = 2, 32, 128, 128
     assert fixed == 3 * (hkv * hd * hd * 4 + 2 * S * hkv * hd * 2 + 4 * C * hkv * hd * 2)
     assert per_tok == 1 * (2 * hkv * hd * 2)
+
+
+def test_serve_dispatch():
+    """make_decoder gives a Bolt3Decoder for stacks with a Bolt-3 layer and None otherwise
+    (the reference server builds VSARecurrentDecoder for everything, vsa_lm/server.py:141,159)."""
+    from bolt3_amd.serve import is_bolt3_model, make_decoder
+    hyb = HybridLM(vocab_size=16, dim=64, num_layers=2, num_heads=4, num_kv_heads=2, intermediate=32, head_dim=32,
+                   layer_types=["vsa", "softmax"])
+    soft = HybridLM(vocab_size=16, dim=64, num_layers=1, num_heads=4, num_kv_heads=2, intermediate=32, head_dim=32,
+                    layer_types=["softmax"])
+    assert is_bolt3_model(hyb) and not is_bolt3_model(soft) and not is_bolt3_model(torch.nn.Linear(2, 2))
+    dec = make_decoder(hyb)
+    assert isinstance(dec, Bolt3Decoder) and dec.max_cache_pos == 8192 and dec.wrap_positions is False
+    assert make_decoder(hyb, "cuda:0").max_cache_pos == 65536
+    assert make_decoder(soft) is None

@@ -248,3 +248,43 @@ def test_generate_greedy_reduced_qwen3_stack(gpu):
     print(f"[case] compared {n_cmp} of 24 tokens; gaps {['%.3f' % g for g in gaps[:8]]}", flush=True)
     assert n_cmp >= 1
     assert torch.equal(toks[:, :n_cmp], t_r[:, :n_cmp])
+
+
+class _CharTokenizer:
+    """A toy tokenizer over the model's vocabulary: one id per character (code point mod vocab)."""
+
+    def __init__(self, vocab, eos):
+        self.vocab, self.eos_token_id = vocab, eos
+
+    def apply_chat_template(self, messages, tokenize=False, add_generation_prompt=True):
+        raise NotImplementedError     # exercise the role-prefixed fallback
+
+    def encode(self, text, add_special_tokens=False):
+        return [ord(ch) % self.vocab for ch in text]
+
+    def decode(self, ids, skip_special_tokens=True):
+        return "".join(chr(33 + (i % 90)) for i in ids if not (skip_special_tokens and i == self.eos_token_id))
+
+
+def test_serve_generate_completion(gpu):
+    """The serving completion on a Bolt-3 stack equals the oracle's greedy continuation of the same
+    prompt, cut at the first end-of-sequence id."""
+    from bolt3_amd.serve import generate_completion, make_decoder
+    model = _model(12, ["vsa", "softmax"], vocab=96)
+    tok = _CharTokenizer(96, eos=42)
+    msgs = [{"role": "user", "content": "x" * 150 + "tell me about slots"}]
+    prompt = "\n".join(f"{m['role']}: {m['content']}" for m in msgs) + "\nassistant: "
+    ids = torch.tensor([tok.encode(prompt)])
+    ref = O.HybridRef(model)
+    with torch.no_grad():
+        t_r, n_r, gaps = ref.generate_greedy(ids, 40, eos_ids={42})
+    dmodel = copy.deepcopy(model).to(gpu)
+    reply = generate_completion(dmodel, tok, gpu, msgs, max_tokens=40, decoder=make_decoder(dmodel, gpu))
+    n_cmp = next((i for i, g in enumerate(gaps) if g <= 1e-4), len(gaps))
+    want = t_r[0, :int(n_r[0])].tolist()
+    if want and want[-1] == 42:
+        want = want[:-1]
+    expect = tok.decode(want)               # one character per token, none of them blank
+    assert reply[:n_cmp] == expect[:n_cmp], (reply, expect)
+    if n_cmp == len(gaps):
+        assert reply == expect

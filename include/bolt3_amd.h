@@ -291,9 +291,23 @@ typedef struct {
   void* y;                    /* [B][H*HD] storage dtype */
   float* work;                /* scratch of >= bolt3_decode_workspace_bytes(B, H, HKV, HD) bytes */
   int64_t work_bytes;
+  /* Graph-stable steps (bf16 bolt3_decode_layer only): when step_desc is set the kernels read
+     pos, a_start, a_len, b_start, b_len, n_sink_keys, has_slots from step_desc[0..6] (device
+     memory, advanced by bolt3_step_advance) instead of the fields above, and clamp every window
+     index into [0, ring_cap), the tokens per (b, hkv) of win_*.  NULL: the fields above. */
+  const int32_t* step_desc;
+  int32_t ring_cap;
 } b3_decode_args;
 
 /*
+ * Softmax-anchor mode of the one-token step (bf16 bolt3_decode_layer only): win_kr == NULL and
+ * win_beta == NULL, no sinks, no slots, m_res == NULL.  The projection row then holds only
+ * q | k | v; the roped key and the value are appended at b_start + b_len of win_kp / win_v (the
+ * layer's key/value cache) and the output is plain causal softmax attention over
+ * [a_start, a_start + a_len) and the new token, with any number of keys.  Replaces the anchor
+ * branch of vsa_lm/config/bolt3.py:426-445 for t_s == 1 (StaticKV append + SDPA), projections
+ * and o_proj included.
+ *
  * One-token decode step of a Bolt-3 layer: head prep for the new token, append to
  * the window ring, attention over sinks + slots + window in fp32 scores, M_res
  * readout.  Three kernels on the stream: the new token's head preparation, the key
@@ -302,6 +316,14 @@ typedef struct {
  * Replaces vsa_lm/config/bolt3.py:346-402 for t_s == 1.
  */
 int bolt3_decode(const b3_decode_args* a, void* stream);
+/*
+ * Adds (d_pos, d_a_start, d_a_len, d_b_start, d_b_len) to step_desc[0..4]: the device-side
+ * advance of a graph-captured decode step (one workgroup of one wavefront).  No counterpart in
+ * the reference (its step has no graph, vsa_lm/config/bolt3.py:287-288).
+ */
+int bolt3_step_advance(int32_t* step_desc, int32_t d_pos, int32_t d_a_start, int32_t d_a_len, int32_t d_b_start,
+                       int32_t d_b_len, void* stream);
+
 /* Workspace of bolt3_decode: partial softmax state of the key ranges and the readout per (batch, kv head). */
 int64_t bolt3_decode_workspace_bytes(int32_t B, int32_t H, int32_t HKV, int32_t HD);
 

@@ -87,6 +87,7 @@ class DecodeArgs(C.Structure):
         ("sink_k", p), ("sink_v", p), ("s_sb", i64), ("s_sh", i64), ("n_sink_keys", i32),
         ("slot_k", p), ("slot_v", p), ("slot_bias", p), ("has_slots", i32),
         ("m_res", p), ("gamma", p), ("res_w", p), ("y", p), ("work", p), ("work_bytes", i64),
+        ("step_desc", p), ("ring_cap", i32),
     ]
 
 
@@ -111,7 +112,7 @@ CHAIN_NOALLOC_SCRATCH_BYTES = 4 << 20   # B3_CHAIN_NOALLOC_SCRATCH_BYTES
 EXPORTS = ("bolt3_heads", "bolt3_chain", "bolt3_chain_noalloc", "bolt3_chain_workspace_bytes", "bolt3_chunk_attn",
            "bolt3_decode",
            "bolt3_decode_layer", "bolt3_decode_layer_workspace_bytes", "bolt3_decode_workspace_bytes",
-           "bolt3_slot_keys", "bolt3_version", "bolt3_wait_count")
+           "bolt3_slot_keys", "bolt3_step_advance", "bolt3_version", "bolt3_wait_count")
 
 _lib = None
 
@@ -138,6 +139,8 @@ def load():
     lib.bolt3_decode_layer_workspace_bytes.restype = i64
     lib.bolt3_decode_workspace_bytes.argtypes = [i32, i32, i32, i32]
     lib.bolt3_decode_workspace_bytes.restype = i64
+    lib.bolt3_step_advance.argtypes = [p, i32, i32, i32, i32, i32, p]
+    lib.bolt3_step_advance.restype = C.c_int
     lib.bolt3_wait_count.argtypes = [p, C.c_uint32, i32, p]
     lib.bolt3_wait_count.restype = C.c_int
     lib.bolt3_version.argtypes = []

@@ -372,9 +372,20 @@ class Bolt3Decoder:
         # bf16 one-token steps run as one bolt3_decode_layer call (projections included); False
         # keeps the projections in torch around bolt3_decode (the tests compare the two)
         self.fuse_projections = True
+        # generate_batch replays a captured graph of the one-token step when the stack allows it
+        self.use_graphs = True
+        self._anchor_packs: dict = {}
+        self._scratch_bufs: dict = {}
 
-    def _graph_runner(self, B: int, need_len: int, device):
-        return None
+    def _graph_runner(self, B: int, need_len: int, device, states=None, kv_caches=None, pos: int = 0):
+        """A DecodeGraph of the one-token step for this state (anchor caches sized for need_len
+        tokens), or None when some layer cannot take it (not bf16, or outside the fused step's
+        limits).  The reference has no graph (vsa_lm/config/bolt3.py:287-288)."""
+        if states is None or not self.use_graphs or not self.fuse_projections:
+            return None
+        if not DecodeGraph.supported(self.model):
+            return None
+        return DecodeGraph(self, states, kv_caches, B, need_len, torch.device(device), pos)
 
     # ------------------------------------------------------------ state
 
@@ -422,7 +433,10 @@ class Bolt3Decoder:
     # ------------------------------------------------------------ one Bolt-3 layer
 
     def _bolt3_layer(self, ly: Bolt3Attn, h, pos_start: int, m_state: torch.Tensor, st: Bolt3LayerState,
-                     record=None):
+                     record=None, desc: int | None = None):
+        """One step of a Bolt-3 layer on t tokens.  ``desc``: device address of a step descriptor
+        (graph capture): the fused one-token kernels then take the position and ring segments from
+        it, and the ring bookkeeping and consolidation are left to the caller."""
         B, t, _ = h.shape
         dt, dev = h.dtype, h.device
         if dt != st.dtype:
@@ -480,11 +494,16 @@ class Bolt3Decoder:
             if fused:
                 out = torch.empty(B, 1, side["wo"].shape[0], dtype=dt, device=dev)
                 call_args.x, call_args.out = h.data_ptr(), out.data_ptr()
+                a.step_desc, a.ring_cap = desc, st.cap
                 A.call("bolt3_decode_layer", call_args, dev)
-                st.cur = (cs, cl + 1)
-                if st.cur[1] >= ly.C:
-                    self._consolidate(ly, st, m_state, gam, side, record)
+                a.step_desc = None
+                if desc is None:
+                    st.cur = (cs, cl + 1)
+                    if st.cur[1] >= ly.C:
+                        self._consolidate(ly, st, m_state, gam, side, record)
                 return out
+            if desc is not None:
+                raise NotImplementedError("graph-captured steps need the fused bf16 layer step")
             lin = F.linear(h, W, bias)
             _check_dtype(lin, dt, "packed projection")
             a.lin = lin.data_ptr()
@@ -552,10 +571,90 @@ class Bolt3Decoder:
 
     # ------------------------------------------------------------ one softmax-anchor layer
 
+    def _anchor_pack(self, ly, dt: torch.dtype, dev: torch.device):
+        """(W_in rows q | k | v padded to 16, their bias or None, side tensors) of a softmax layer's
+        fused one-token step, rebuilt when a parameter changes."""
+        params = list(ly.parameters())
+        key = (dt, dev, tuple((q.data_ptr(), q._version) for q in params))
+        ent = self._anchor_packs.get(id(ly))
+        if ent is not None and ent[0] == key:
+            return ent[1]
+        with torch.no_grad():
+            lins = (ly.q_proj, ly.k_proj, ly.v_proj)
+            D = ly.q_proj.in_features
+            pad = (-sum(m.out_features for m in lins)) % 16
+            W = torch.cat([m.weight.to(device=dev, dtype=dt) for m in lins] +
+                          [torch.zeros(pad, D, device=dev, dtype=dt)]).contiguous()
+            bias = None
+            if any(m.bias is not None for m in lins):
+                bias = torch.cat([(m.bias if m.bias is not None else torch.zeros(m.out_features)).to(dev, dt)
+                                  for m in lins] + [torch.zeros(pad, device=dev, dtype=dt)]).contiguous()
+            norm = ly.q_norm is not None
+            side = dict(wo=ly.o_proj.weight.to(device=dev, dtype=dt).contiguous(),
+                        inv_freq=ly.rope.inv_freq.to(dev).float().contiguous(),
+                        qn=ly.q_norm.weight.detach().to(dev).float().contiguous() if norm else None,
+                        kn=ly.k_norm.weight.detach().to(dev).float().contiguous() if norm else None,
+                        eps=float(ly.q_norm.eps) if norm else 1e-6,
+                        gamma=torch.zeros(ly.HKV, device=dev), res_w=torch.ones(ly.HD, device=dev))
+        self._anchor_packs[id(ly)] = (key, (W, bias, side))
+        return W, bias, side
+
+    def _scratch(self, dev, name: str, n_floats: int) -> torch.Tensor:
+        """Kernel workspaces kept per device and purpose (stable addresses for captured graphs)."""
+        t = self._scratch_bufs.get((dev, name))
+        if t is None or t.numel() < n_floats:
+            t = torch.empty(n_floats, device=dev)
+            self._scratch_bufs[(dev, name)] = t
+        return t
+
+    def _anchor_fused(self, ly, h: torch.Tensor, pos_start: int, cache: AnchorCache, desc: int | None = None):
+        """One token of a softmax-anchor layer as one bolt3_decode_layer call in its anchor mode:
+        q | k | v projection, q/k norm and RoPE, the new key and value appended to the cache,
+        causal softmax over the cache, o_proj.  ``desc`` as in _bolt3_layer (cache.n is then the
+        caller's to advance)."""
+        B, _, D = h.shape
+        dt, dev = h.dtype, h.device
+        W, bias, side = self._anchor_pack(ly, dt, dev)
+        if desc is None:
+            cache.reserve(cache.n + 1)
+        H, HKV, HD = ly.H, ly.HKV, ly.HD
+        n_out = side["wo"].shape[0]
+        la = A.DecodeLayerArgs()
+        a = la.dec
+        a.dtype, a.B, a.H, a.HKV, a.HD, a.S = A.dtype_code(dt), B, H, HKV, HD, 128
+        a.lin_row_stride = W.shape[0]
+        a.qn_w, a.kn_w, a.has_qk_norm = A.ptr(side["qn"]), A.ptr(side["kn"]), int(side["qn"] is not None)
+        a.eps, a.inv_freq, a.pos = side["eps"], side["inv_freq"].data_ptr(), int(pos_start)
+        a.win_kr, a.win_kp, a.win_v = None, cache.k.data_ptr(), cache.v.data_ptr()
+        a.w_sb, a.w_sh = cache.k.stride(0), cache.k.stride(1)
+        a.win_beta, a.win_pos = None, None
+        a.a_start, a.a_len, a.b_start, a.b_len = 0, cache.n, cache.n, 0
+        a.gamma, a.res_w = side["gamma"].data_ptr(), side["res_w"].data_ptr()
+        y = self._scratch(dev, f"anchor_y{B}x{H * HD}", B * H * HD // (2 if dt == torch.bfloat16 else 1))
+        a.y = y.data_ptr()
+        work = self._scratch(dev, "decode_work", A.decode_workspace_bytes(B, H, HKV, HD) // 4)
+        a.work, a.work_bytes = work.data_ptr(), work.numel() * 4
+        a.step_desc, a.ring_cap = desc, cache.capacity
+        pw = self._scratch(dev, "proj_work", A.decode_layer_workspace_bytes(B, D, W.shape[0], H * HD, n_out) // 4)
+        la.proj_work, la.proj_work_bytes = pw.data_ptr(), pw.numel() * 4
+        la.x, la.x_row_stride, la.d_model = h.data_ptr(), D, D
+        la.w_in, la.b_in, la.n_in = W.data_ptr(), A.ptr(bias), W.shape[0]
+        la.w_out, la.b_out, la.n_out, la.out_row_stride = side["wo"].data_ptr(), None, n_out, n_out
+        out = torch.empty(B, 1, n_out, dtype=dt, device=dev)
+        la.out = out.data_ptr()
+        A.call("bolt3_decode_layer", la, dev)
+        if desc is None:
+            cache.n += 1
+        return out
+
     def _anchor_layer(self, ly, h: torch.Tensor, pos_start: int, cache: AnchorCache) -> torch.Tensor:
         """Causal softmax attention of t new tokens over the cached ones and themselves
-        (vsa_lm/config/bolt3.py:426-445): query i sees cached keys and new keys up to i."""
+        (vsa_lm/config/bolt3.py:426-445): query i sees cached keys and new keys up to i.  One bf16
+        token: the fused HIP step; otherwise torch's attention on the cache."""
         b, t, _ = h.shape
+        if t == 1 and self.fuse_projections and _fused_step_ok(h.dtype, h.shape[-1], ly.H * ly.HD,
+                                                               ly.o_proj.out_features) and ly.G <= 8:
+            return self._anchor_fused(ly, h, pos_start, cache)
         q, k, v = ly.head_qkv(h)
         q, k = ly.rope(q, pos_start=pos_start), ly.rope(k, pos_start=pos_start)
         n_old = cache.n
@@ -614,6 +713,8 @@ class Bolt3Decoder:
         h, states, kv = self.prefill(ids, max_kv_len=T + max_new_tokens + 64)
         book = _Bookkeeping(B, max_new_tokens, eos_ids, close_think_ids, ids.device)
         logits = self.model.lm_head(h[:, -1])
+        graph = self._graph_runner(B, T + max_new_tokens + 1, ids.device, states, kv, T) if max_new_tokens > 1 \
+            else None
         n_out = max_new_tokens
         for i in range(max_new_tokens):
             nxt = book.take(i, sample_tokens(logits, temperature, top_k, top_p))
@@ -622,8 +723,11 @@ class Bolt3Decoder:
                 n_out = stop
                 break
             if i + 1 < max_new_tokens:
-                h, _, _ = self.step(nxt, T + i, states, kv)
-                logits = self.model.lm_head(h[:, -1])
+                if graph is not None:
+                    logits = graph.step(nxt)
+                else:
+                    h, _, _ = self.step(nxt, T + i, states, kv)
+                    logits = self.model.lm_head(h[:, -1])
         return book.toks[:, :n_out], book.lengths
 
     @torch.no_grad()
@@ -687,3 +791,107 @@ class Bolt3Decoder:
             k = max(0, (next_pos - end_pos) // ly.C)
             states[li] = states[li] - ly.gamma_delta().view(1, -1, 1, 1).to(delta.device) ** k * delta
         return states
+
+
+class DecodeGraph:
+    """The one-token step of a whole stack (embedding to last-position logits) captured once as a
+    HIP graph and replayed per token.
+
+    Every fused kernel of the step reads its position and window segments from a device step
+    descriptor (one shared by the Bolt-3 layers, whose rings move in lockstep, one by the anchor
+    layers), and the graph ends by advancing both descriptors on the device.  The host mirrors
+    the ring positions; when the current chunk fills, it runs the layers' consolidations eagerly
+    after the replay (a layer's consolidation only changes that layer's later steps, so this is
+    the eager order's result) and rewrites the descriptors.  Anchor caches are sized for every
+    token before capture, so no buffer moves while the graph lives.
+    """
+
+    @staticmethod
+    def supported(model) -> bool:
+        for blk in model.blocks:
+            ly = blk.vsa if hasattr(blk, "vsa") else blk.attn
+            dt = ly.q_proj.weight.dtype
+            if not _fused_step_ok(dt, ly.q_proj.in_features, ly.H * ly.HD, ly.o_proj.out_features) or ly.G > 8:
+                return False
+        return True
+
+    def __init__(self, dec: Bolt3Decoder, states, kv, B: int, need_len: int, dev: torch.device, pos: int):
+        self.dec, self.states, self.kv, self.dev = dec, states, kv, dev
+        m = dec.model
+        self.b3 = [(li, blk.vsa, kv[li]) for li, blk in enumerate(m.blocks) if hasattr(blk, "vsa")]
+        self.an = [(li, blk.attn, kv[li]) for li, blk in enumerate(m.blocks) if not hasattr(blk, "vsa")]
+        rings = {(c.prev, c.cur, c.n_sink, c.has_slots) for _, _, c in self.b3}
+        lens = {c.n for _, _, c in self.an}
+        if len(rings) > 1 or len(lens) > 1:
+            raise ValueError("the layers' states are not in lockstep")
+        for _, _, c in self.an:
+            c.reserve(need_len)
+        self.pos = pos
+        self.d_b3 = torch.zeros(8, dtype=torch.int32, device=dev)
+        self.d_an = torch.zeros(8, dtype=torch.int32, device=dev)
+        self._write_descriptors()
+        self.tok = torch.zeros(B, 1, dtype=torch.long, device=dev)
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        # warm-up on the capture stream with scratch descriptors of the same values: it writes the
+        # new token's key and value where the first replay writes them again, and initialises
+        # the libraries' per-stream state outside the capture
+        warm_b3, warm_an = self.d_b3.clone(), self.d_an.clone()
+        with torch.cuda.stream(side):
+            self._forward(warm_b3.data_ptr(), warm_an.data_ptr())
+        side.synchronize()
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph, stream=side):
+            self.logits = self._forward(self.d_b3.data_ptr(), self.d_an.data_ptr())
+            s = A.stream_of(dev)
+            lib = A.load()
+            rc = lib.bolt3_step_advance(self.d_b3.data_ptr(), 1, 0, 0, 0, 1, s)
+            rc = rc or lib.bolt3_step_advance(self.d_an.data_ptr(), 1, 0, 1, 1, 0, s)
+            if rc:
+                raise RuntimeError(f"bolt3_step_advance failed with code {rc}")
+
+    def _forward(self, d_b3: int, d_an: int) -> torch.Tensor:
+        m, dec = self.dec.model, self.dec
+        x = m.embed_tokens(self.tok)
+        for li, blk in enumerate(m.blocks):
+            h = blk.norm1(x)
+            if hasattr(blk, "vsa"):
+                y = dec._bolt3_layer(blk.vsa, h, self.pos, self.states[li], self.kv[li], desc=d_b3)
+            else:
+                y = dec._anchor_fused(blk.attn, h, self.pos, self.kv[li], desc=d_an)
+            x = x + y
+            x = x + blk.mlp(blk.norm2(x))
+        return m.lm_head(m.norm(x)[:, -1])
+
+    def _write_descriptors(self):
+        vals = [0] * 16
+        if self.b3:
+            c = self.b3[0][2]
+            vals[:7] = [self.pos, c.prev[0], c.prev[1], c.cur[0], c.cur[1], c.n_sink, int(c.has_slots)]
+        if self.an:
+            n = self.an[0][2].n
+            vals[8:13] = [self.pos, 0, n, n, 0]
+        host = torch.tensor(vals, dtype=torch.int32).pin_memory()
+        self.d_b3.copy_(host[:8], non_blocking=True)
+        self.d_an.copy_(host[8:], non_blocking=True)
+
+    def step(self, tokens: torch.Tensor) -> torch.Tensor:
+        """Feed one token per row ([B, 1]) at the next position; returns the logits [B, V] (a
+        buffer the next step overwrites)."""
+        self.tok.copy_(tokens)
+        self.graph.replay()
+        self.pos += 1
+        for _, _, c in self.an:
+            c.n += 1
+        full = False
+        for _, ly, c in self.b3:
+            cs, cl = c.cur
+            c.cur = (cs, cl + 1)
+            full = c.cur[1] >= ly.C
+        if full:
+            for li, ly, c in self.b3:
+                _, _, side = ly._packed(c.dtype, self.dev)
+                self.dec._consolidate(ly, c, self.states[li], side["gamma"], side)
+            self._write_descriptors()
+        return self.logits
+

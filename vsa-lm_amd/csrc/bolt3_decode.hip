@@ -122,11 +122,41 @@ struct PrepOut {
   T* new_v;
 };
 
+// The step's position and window segments: the argument fields, or (graph-captured steps) the
+// device descriptor, clamped so that every window index stays in [0, ring_cap).
+struct StepView {
+  int pos, a_start, a_len, b_start, b_len, n_sink, has_slots;
+};
+__device__ __forceinline__ StepView step_view(const b3_decode_args& a) {
+  StepView v;
+  if (a.step_desc) {
+    const int32_t* d = a.step_desc;
+    const int cap = a.ring_cap;
+    v.pos = d[0];
+    v.a_start = min(max(d[1], 0), cap);
+    v.a_len = min(max(d[2], 0), cap - v.a_start);
+    v.b_start = min(max(d[3], 0), cap - 1);
+    v.b_len = min(max(d[4], 0), cap - 1 - v.b_start);   // the new token goes to b_start + b_len
+    v.n_sink = min(max(d[5], 0), 4);
+    v.has_slots = d[6] != 0;
+  } else {
+    v.pos = a.pos;
+    v.a_start = a.a_start;
+    v.a_len = a.a_len;
+    v.b_start = a.b_start;
+    v.b_len = a.b_len;
+    v.n_sink = a.n_sink_keys;
+    v.has_slots = a.has_slots;
+  }
+  return v;
+}
+
 // The head preparation of (batch, kv head) bh by the 128 threads tid = 0..127 (two whole
-// wavefronts).
+// wavefronts).  Softmax-anchor mode (win_beta == NULL): no gate columns, eta = 0, and the
+// un-roped key is kept only when win_kr is set.
 template <typename T, int HD>
-__device__ __forceinline__ void prep_token(const b3_decode_args& a, const LinParts& lp, int bh, int tid,
-                                           const PrepOut<T>& out) {
+__device__ __forceinline__ void prep_token(const b3_decode_args& a, const StepView& sv, const LinParts& lp, int bh,
+                                           int tid, const PrepOut<T>& out) {
   constexpr int HALF = HD / 2, P8 = HALF / 8;
   const int b = bh / a.HKV, hkv = bh % a.HKV;
   const int G = a.H / a.HKV;
@@ -135,7 +165,7 @@ __device__ __forceinline__ void prep_token(const b3_decode_args& a, const LinPar
   T* q_rope = out.q_rope;
   float* q_raw = out.q_raw;
   const long long wbase = (long long)b * a.w_sb + (long long)hkv * a.w_sh;
-  const int ni = a.b_start + a.b_len;   // ring index of the new token
+  const int ni = sv.b_start + sv.b_len;   // ring index of the new token
   const int gcol = (a.H + 2 * a.HKV) * HD;
   const int p = tid % P8, u = tid / P8;
   const bool live = u < G + 2;
@@ -230,7 +260,7 @@ __device__ __forceinline__ void prep_token(const b3_decode_args& a, const LinPar
         v1.store(out.new_v + HALF + 8 * p);
       }
     } else {
-      const float pos = (float)a.pos;
+      const float pos = (float)sv.pos;
       Vec8<T> r0, r1, u0, u1;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -252,10 +282,12 @@ __device__ __forceinline__ void prep_token(const b3_decode_args& a, const LinPar
         }
         if (p == 0) ws_stat[2 * u] = 1.0f / fmaxf(sqrtf(qq), 1e-12f);
       } else {
-        T* kr = reinterpret_cast<T*>(a.win_kr) + wbase + (long long)ni * HD;
         T* kp = reinterpret_cast<T*>(a.win_kp) + wbase + (long long)ni * HD;
-        u0.store(kr + 8 * p);
-        u1.store(kr + HALF + 8 * p);
+        if (a.win_kr) {
+          T* kr = reinterpret_cast<T*>(a.win_kr) + wbase + (long long)ni * HD;
+          u0.store(kr + 8 * p);
+          u1.store(kr + HALF + 8 * p);
+        }
         r0.store(kp + 8 * p);
         r1.store(kp + HALF + 8 * p);
         if (out.new_k) {
@@ -265,11 +297,11 @@ __device__ __forceinline__ void prep_token(const b3_decode_args& a, const LinPar
       }
     }
   }
-  if (tid < G) ws_stat[2 * tid + 1] = St<T>::rnd(tanhf(lin1(gcol + a.HKV + hkv * G + tid)));
-  if (tid == G) {
+  if (tid < G) ws_stat[2 * tid + 1] = a.win_beta ? St<T>::rnd(tanhf(lin1(gcol + a.HKV + hkv * G + tid))) : 0.f;
+  if (tid == G && a.win_beta) {
     const float z = lin1(gcol + hkv);
     a.win_beta[b * a.wb_sb + hkv * a.wb_sh + ni] = St<T>::rnd(1.0f / (1.0f + expf(-z)));
-    if (bh == 0 && a.win_pos) a.win_pos[ni] = (float)a.pos;
+    if (bh == 0 && a.win_pos) a.win_pos[ni] = (float)sv.pos;
   }
 }
 
@@ -280,7 +312,7 @@ __global__ void __launch_bounds__(128) decode_prep_kernel(b3_decode_args a, LinP
   float* ws = a.work + (long long)bh * dec_ws_per_bh(G, HD);
   const PrepOut<T> out{reinterpret_cast<T*>(ws + dec_ws_q(G, HD)), ws + dec_ws_q(G, HD) + G * HD,
                        ws + dec_ws_q(G, HD) - 2 * G, nullptr, nullptr};
-  prep_token<T, HD>(a, lp, bh, threadIdx.x, out);
+  prep_token<T, HD>(a, step_view(a), lp, bh, threadIdx.x, out);
 }
 
 // Key-row fragment of a 32-key tile (fp32 storage): lane (key n = lane%32, h = lane/32) holds
@@ -611,7 +643,8 @@ __global__ void __launch_bounds__(ANT, 4) decode_attn_kernel(b3_decode_args a, L
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const long long wbase = (long long)b * a.w_sb + (long long)hkv * a.w_sh;
-  const int ns = a.n_sink_keys, nsl = a.has_slots ? a.S : 0, na = a.a_len, nbk = a.b_len + 1;
+  const StepView sv = step_view(a);
+  const int ns = sv.n_sink, nsl = sv.has_slots ? a.S : 0, na = sv.a_len, nbk = sv.b_len + 1;
   const int nk = ns + nsl + na + nbk;
   const int ntile = (nk + 31) / 32;
   constexpr int PER = (GMAX * HD + ANT - 1) / ANT;
@@ -643,12 +676,12 @@ __global__ void __launch_bounds__(ANT, 4) decode_attn_kernel(b3_decode_args a, L
       vp = reinterpret_cast<const uint16_t*>(a.slot_v) + ((long long)bh * a.S + k) * HD;
       slot = k;
     } else if ((k -= nsl) < na) {
-      kp = reinterpret_cast<const uint16_t*>(a.win_kp) + wbase + (long long)(a.a_start + k) * HD;
-      vp = reinterpret_cast<const uint16_t*>(a.win_v) + wbase + (long long)(a.a_start + k) * HD;
+      kp = reinterpret_cast<const uint16_t*>(a.win_kp) + wbase + (long long)(sv.a_start + k) * HD;
+      vp = reinterpret_cast<const uint16_t*>(a.win_v) + wbase + (long long)(sv.a_start + k) * HD;
     } else {
       k -= na;
-      kp = reinterpret_cast<const uint16_t*>(a.win_kp) + wbase + (long long)(a.b_start + k) * HD;
-      vp = reinterpret_cast<const uint16_t*>(a.win_v) + wbase + (long long)(a.b_start + k) * HD;
+      kp = reinterpret_cast<const uint16_t*>(a.win_kp) + wbase + (long long)(sv.b_start + k) * HD;
+      vp = reinterpret_cast<const uint16_t*>(a.win_v) + wbase + (long long)(sv.b_start + k) * HD;
     }
   };
   // one tile's loads: the value rows to LDS (instruction ch fills rows RPI*ch .. RPI*ch +
@@ -689,7 +722,7 @@ __global__ void __launch_bounds__(ANT, 4) decode_attn_kernel(b3_decode_args a, L
     if (wave < ntile) load_tile(wave);
   } else {
     const PrepOut<uint16_t> po{&sm.qrope[0][0], &sm.qhat[0][0], sm.stat, sm.newk, sm.newv};
-    prep_token<uint16_t, HD>(a, lp, bh, tid - 64 * ADW, po);
+    prep_token<uint16_t, HD>(a, sv, lp, bh, tid - 64 * ADW, po);
   }
   __syncthreads();   // the prepared token is in LDS
   if (wave < ADW) {
@@ -1024,18 +1057,30 @@ extern "C" int64_t bolt3_decode_workspace_bytes(int32_t B, int32_t H, int32_t HK
 
 // Argument checks shared by bolt3_decode and bolt3_decode_layer (need_lin: the row comes from
 // a->lin rather than from the layer's own projection).
-static int check_decode(const b3_decode_args* a, bool need_lin) {
+static int check_decode(const b3_decode_args* a, bool need_lin, bool fused) {
   if (!a || a->B <= 0 || a->HKV <= 0 || a->H % a->HKV != 0) return B3_ERR_ARG;
   if (a->H / a->HKV > b3::GMAX || (a->HD != 64 && a->HD != 128)) return B3_ERR_UNSUPPORTED;
-  const int nk = a->n_sink_keys + (a->has_slots ? a->S : 0) + a->a_len + a->b_len + 1;
-  if (nk > b3::NKMAX || a->n_sink_keys < 0 || a->a_len < 0 || a->b_len < 0) return B3_ERR_UNSUPPORTED;
-  if ((need_lin && !a->lin) || !a->win_kr || !a->win_kp || !a->win_v || !a->win_beta || !a->inv_freq ||
-      !a->gamma || !a->res_w || !a->y || !a->work)
+  const bool anchor = a->win_beta == nullptr;   // softmax-anchor mode (fused path only)
+  if (!fused && (anchor || !a->win_kr || a->step_desc)) return B3_ERR_ARG;
+  if (anchor && (a->has_slots || a->n_sink_keys || a->m_res)) return B3_ERR_ARG;
+  if (a->step_desc) {
+    // fields come from device memory at run time; the kernels clamp them to the ring
+    if (a->ring_cap <= 0) return B3_ERR_ARG;
+    if (!anchor && (!a->slot_k || !a->slot_v || !a->slot_bias || !a->sink_k || !a->sink_v)) return B3_ERR_ARG;
+  } else {
+    if (a->n_sink_keys < 0 || a->a_len < 0 || a->b_len < 0 || a->a_start < 0 || a->b_start < 0) return B3_ERR_ARG;
+    const int nk = a->n_sink_keys + (a->has_slots ? a->S : 0) + a->a_len + a->b_len + 1;
+    if (!fused && nk > b3::NKMAX) return B3_ERR_UNSUPPORTED;   // the split path's partial-state count
+    if (a->ring_cap > 0 && (a->a_start + a->a_len > a->ring_cap || a->b_start + a->b_len + 1 > a->ring_cap))
+      return B3_ERR_ARG;
+    if (a->has_slots && (!a->slot_k || !a->slot_v || !a->slot_bias)) return B3_ERR_ARG;
+    if (a->n_sink_keys > 0 && (!a->sink_k || !a->sink_v)) return B3_ERR_ARG;
+  }
+  if ((need_lin && !a->lin) || !a->win_kp || !a->win_v || !a->inv_freq || !a->gamma || !a->res_w || !a->y ||
+      !a->work)
     return B3_ERR_ARG;
   if (a->work_bytes < bolt3_decode_workspace_bytes(a->B, a->H, a->HKV, a->HD)) return B3_ERR_WORKSPACE;
-  if (a->has_slots && (!a->slot_k || !a->slot_v || !a->slot_bias)) return B3_ERR_ARG;
-  if (a->has_slots && (a->S <= 0 || a->S > 128)) return B3_ERR_UNSUPPORTED;   // the slot field's size
-  if (a->n_sink_keys > 0 && (!a->sink_k || !a->sink_v)) return B3_ERR_ARG;
+  if (!anchor && (a->S <= 0 || a->S > 128)) return B3_ERR_UNSUPPORTED;   // the slot field's size
   if (a->has_qk_norm && (!a->qn_w || !a->kn_w)) return B3_ERR_ARG;
   // 16-byte rows: the projection row and every key / value row
   const int64_t es = a->dtype == B3_BF16 ? 2 : 4;
@@ -1044,7 +1089,7 @@ static int check_decode(const b3_decode_args* a, bool need_lin) {
 }
 
 extern "C" int bolt3_decode(const b3_decode_args* a, void* stream) {
-  const int rc = check_decode(a, true);
+  const int rc = check_decode(a, true, false);
   if (rc) return rc;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const b3::LinParts lp{nullptr, 0, 0, nullptr};
@@ -1066,12 +1111,13 @@ extern "C" int bolt3_decode_layer(const b3_decode_layer_args* a, void* stream) {
   if (!a) return B3_ERR_ARG;
   const b3_decode_args& d = a->dec;
   if (d.dtype != B3_BF16) return B3_ERR_UNSUPPORTED;
-  int rc = check_decode(&d, false);
+  int rc = check_decode(&d, false, true);
   if (rc) return rc;
   const int hd_total = d.H * d.HD;
   if (!a->x || !a->w_in || !a->w_out || !a->out || !a->proj_work) return B3_ERR_ARG;
+  const int n_gates = d.win_beta ? d.HKV + d.H : 0;   // anchor mode: q | k | v only
   if (a->d_model < 32 || a->d_model % 32 || a->n_in != d.lin_row_stride || a->n_in % 16 ||
-      a->n_in < d.H * d.HD + 2 * d.HKV * d.HD + d.HKV + d.H || a->n_out <= 0 || a->n_out % 16 ||
+      a->n_in < d.H * d.HD + 2 * d.HKV * d.HD + n_gates || a->n_out <= 0 || a->n_out % 16 ||
       a->x_row_stride < a->d_model || a->x_row_stride % 8 || a->out_row_stride < a->n_out ||
       a->out_row_stride % 4 || reinterpret_cast<uintptr_t>(a->x) % 16 || reinterpret_cast<uintptr_t>(a->out) % 8 ||
       reinterpret_cast<uintptr_t>(a->proj_work) % 16)
@@ -1100,3 +1146,21 @@ extern "C" int bolt3_decode_layer(const b3_decode_layer_args* a, void* stream) {
 }
 
 extern "C" const char* bolt3_version(void) { return "bolt3_amd 0.1 gfx950 (MFMA 32x32, wave64)"; }
+
+namespace b3 {
+__global__ void __launch_bounds__(64) step_advance_kernel(int32_t* desc, int32_t d0, int32_t d1, int32_t d2, int32_t d3,
+                                                          int32_t d4) {
+  const int i = threadIdx.x;
+  const int32_t add = i == 0 ? d0 : i == 1 ? d1 : i == 2 ? d2 : i == 3 ? d3 : d4;
+  if (i < 5) desc[i] += add;
+}
+}  // namespace b3
+
+extern "C" int bolt3_step_advance(int32_t* step_desc, int32_t d_pos, int32_t d_a_start, int32_t d_a_len,
+                                  int32_t d_b_start, int32_t d_b_len, void* stream) {
+  if (!step_desc) return B3_ERR_ARG;
+  hipLaunchKernelGGL(b3::step_advance_kernel, dim3(1), dim3(64), 0, reinterpret_cast<hipStream_t>(stream), step_desc,
+                     d_pos, d_a_start, d_a_len, d_b_start, d_b_len);
+  return (int)hipGetLastError();
+}
+

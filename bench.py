@@ -202,6 +202,75 @@ def bench_long(dev, reps=3, T_long=65536):
                 data="synthetic clustered hidden states (512 centres, noise 0.15, Zipf 1.1)")
 
 
+def build_e2e(dev, layers=36, vocab=151936, dim=2560, inter=9728):
+    """The end-to-end configuration's model with random weights, made on the GPU: Qwen3-4B shape
+    (hidden 2560, 32 / 8 heads, head_dim 128, SwiGLU 9728, vocabulary 151936, tied embeddings,
+    q/k norm, theta 1e6), every 4th layer softmax (9) and 27 Bolt-3 layers at their default
+    init; projections ~N(0, 0.02), embedding ~N(0, 1); bf16."""
+    import torch
+    from bolt3_amd import Bolt3Attn, HybridLM, RMSNorm
+    from bolt3_amd.layers import rope_inv_freq
+    types = ["softmax" if (i + 1) % 4 == 0 else "vsa" for i in range(layers)]
+    with torch.device("meta"):
+        m = HybridLM(vocab_size=vocab, dim=dim, num_layers=layers, num_heads=32, num_kv_heads=8, intermediate=inter,
+                     layer_types=types, head_dim=128, qk_norm=True, rope_theta=1e6, eps=1e-6, max_T=65536)
+    m = m.to_empty(device=dev)
+    m.lm_head.weight = m.embed_tokens.weight
+    g = torch.Generator(device=dev).manual_seed(SEED + 3)
+    with torch.no_grad():
+        for mod in m.modules():
+            if isinstance(mod, torch.nn.Linear):
+                mod.weight.normal_(0.0, 0.02, generator=g)
+                if mod.bias is not None:
+                    mod.bias.zero_()
+            elif isinstance(mod, RMSNorm):
+                mod.weight.fill_(1.0)
+            if hasattr(mod, "rope"):
+                mod.rope.inv_freq.copy_(rope_inv_freq(128, 1e6).to(dev))
+        m.embed_tokens.weight.normal_(0.0, 1.0, generator=g)
+        for mod in m.modules():
+            if isinstance(mod, Bolt3Attn):      # the reference's constructor defaults
+                mod.kappa.fill_(1.0)
+                mod.log_gamma.fill_(3.5)
+                mod.beta_proj.weight.zero_()
+                mod.beta_proj.bias.fill_(-1.0)
+                mod.eta_proj.weight.zero_()
+                mod.eta_proj.bias.zero_()
+                mod.res_norm.weight.fill_(0.05)
+    return m.to(torch.bfloat16).eval()
+
+
+def bench_e2e(dev, batch=32, prompt=2048, new=256, layers=36):
+    """End-to-end generation: prefill of `prompt` uniform-random token ids for
+    `batch` sequences, then `new` greedy tokens through Bolt3Decoder.generate_batch (graph-replayed
+    one-token steps).  Prefill is timed alone; decode = generate_batch - prefill."""
+    import torch
+    import recipes
+    from bolt3_amd import Bolt3Decoder
+    m = build_e2e(dev, layers=layers)
+    ids = recipes.tokens(SEED + 4, batch, prompt, m.config["vocab_size"]).to(dev)
+    dec = Bolt3Decoder(m)
+    with torch.no_grad():
+        dec.generate_batch(ids[:, :256], 8, temperature=0.0)          # warm-up: kernels, handles, a capture
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        dec.prefill(ids)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        toks, _ = dec.generate_batch(ids, new, temperature=0.0)
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+    pre_s, gen_s = t1 - t0, t2 - t1
+    dec_s = max(gen_s - pre_s, 1e-9)
+    return dict(layers=layers, bolt3_layers=sum(hasattr(b, "vsa") for b in m.blocks),
+                softmax_layers=sum(not hasattr(b, "vsa") for b in m.blocks), batch=batch, prompt_tokens=prompt,
+                new_tokens=int(toks.shape[1]), prefill_ms=round(pre_s * 1e3, 1), decode_ms=round(dec_s * 1e3, 1),
+                prefill_tokens_per_s=round(batch * prompt / pre_s, 1),
+                decode_tokens_per_s=round(batch * int(toks.shape[1]) / dec_s, 1),
+                ms_per_decode_step=round(dec_s * 1e3 / max(1, int(toks.shape[1])), 3),
+                data="random-init bf16 weights, uniform-random prompt ids, greedy decoding")
+
+
 def measured_traffic(entry: str):
     """HBM bytes of an entry point from the rocprofv3 PMC summary committed under profiles/
     (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel calibration): per forward for the
@@ -254,6 +323,7 @@ def main():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-long", action="store_true", help="skip the consolidation-heavy B=1, T=65536 forward")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-e2e", action="store_true", help="skip the 36-layer end-to-end generation")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run a plain elementwise copy of 256 MiB (fp32 negate) three times, the known-size "
                          "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
@@ -335,6 +405,8 @@ def main():
         out["decode"] = bench_decode(dev, args.decode_sets, args.decode_steps)
     if not args.no_long:
         out["long_prefill"] = bench_long(dev)
+    if not args.no_e2e:
+        out["e2e"] = bench_e2e(dev)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out))

@@ -117,9 +117,10 @@ def bench_decode(dev, n_sets, n_steps, prefill_tokens=8192, batch=64):
                 dec._bolt3_layer(mod, hs[s], prefill_tokens + s, m, st)
         torch.cuda.synchronize()
         t1 = time.perf_counter()
-        # launch durations: a further block of steps with HIP events around every entry point
-        # (outside the timed loop above, whose per-step figure carries no event overhead)
-        n_time = min(64, n_steps)
+        # launch durations: a further full cycle of steps (every window length from 129 to 256
+        # once, two consolidations per set) with HIP events around every entry point, outside
+        # the timed loop above, whose per-step figure carries no event overhead
+        n_time = n_steps
         tw = []
         _abi.set_timing(True)
         for s in range(n_time):
@@ -149,6 +150,8 @@ def bench_decode(dev, n_sets, n_steps, prefill_tokens=8192, batch=64):
         layer_step_us=round(step_us, 2),
         decode_layer_us=round(dec_avg * 1e3, 2),
         consolidation_us=round(sum(cons_ms) / max(1, len(cons_ms)) * 1e3, 2) if cons_ms else None,
+        consolidations=len(cons_ms),
+        amortized_kernel_us=round((sum(dec_ms) + sum(cons_ms)) / max(1, len(dec_ms)) * 1e3, 2),
         avg_window=round(sum(win_lens) / len(win_lens), 1),
         tokens_per_s=round(batch * 1e6 / step_us, 1),
         roofline=dict(bound="hbm", achieved=round(bytes_launch / (dec_avg * 1e-3) / 1e9, 1),

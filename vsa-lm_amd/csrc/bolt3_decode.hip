@@ -727,12 +727,9 @@ __global__ void __launch_bounds__(ANT, 4) decode_attn_kernel(b3_decode_args a, L
   __syncthreads();   // the prepared token is in LDS
   if (wave < ADW) {
     // queries as the B operand: lane (head m, group g4) holds features 32ks + 8g4 .. of head m
-    u16x8 qb[NKS];
-#pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) {
-      if (m < G) qb[ks] = *reinterpret_cast<const u16x8*>(&sm.qrope[m][32 * ks + 8 * g4]);
-      else qb[ks] = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
-    }
+    // (read from LDS at every tile rather than held in registers for the whole loop)
+    const int qrow = m < G ? m : 0;
+    const bool qlive = m < G;
     const float scale = 1.0f / sqrtf((float)HD);
     for (int j = wave; j < ntile; j += ADW) {
       const int kt0 = 32 * j;
@@ -747,12 +744,13 @@ __global__ void __launch_bounds__(ANT, 4) decode_attn_kernel(b3_decode_args a, L
 #pragma unroll
             for (int ks = 0; ks < NKS; ++ks) ka[kb][ks] = *reinterpret_cast<const u16x8*>(&sm.newk[32 * ks + 8 * g4]);
       }
-      f32x4 sc[2];
+      f32x4 sc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        sc[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int ks = 0; ks < NKS; ++ks) {
+        u16x8 qb = *reinterpret_cast<const u16x8*>(&sm.qrope[qrow][32 * ks + 8 * g4]);
+        if (!qlive) qb = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) mma16_bf16(sc[kb], ka[kb][ks], qb[ks]);
+        for (int kb = 0; kb < 2; ++kb) mma16_bf16(sc[kb], ka[kb][ks], qb);
       }
       // fp32 scores (the decoder step does not round q.k), slot bias, keys past nk masked
       float tmx = -INFINITY;
@@ -810,7 +808,7 @@ __global__ void __launch_bounds__(ANT, 4) decode_attn_kernel(b3_decode_args a, L
     // r^T[d][g] = sum over the wavefront's rows c of M[c][d] q^[g][c]: 16x16x4 fp32 MFMAs,
     // lane (l % 16, l / 16) loads A = M[c0 + l/16][d0 + l%16] and B = q^[l%16][c0 + l/16]
     constexpr int RR = HD / ARW, NDT = HD / 16;
-    constexpr int NCS = RR / 4 < 8 ? RR / 4 : 8;   // K steps of 4 rows per pass (register budget)
+    constexpr int NCS = RR / 4 < 4 ? RR / 4 : 4;   // K steps of 4 rows per pass (register budget)
     constexpr int NPASS = RR / (4 * NCS);
     const int q = wave - ADW;
     const int r16 = lane & 15, k4 = lane >> 4;

@@ -258,6 +258,66 @@ typedef struct {
  */
 int bolt3_chunk_attn(const b3_attn_args* a, void* stream);
 
+/*
+ * Backward of a forward's chunk attention and M_res readout (bolt3_chunk_attn, mode 0): given
+ * dy, the gradient of the attention + readout output, the gradients with respect to the roped
+ * queries, the un-roped queries (readout), eta, every key field (window keys and values, sinks,
+ * the slot snapshots of every step), the slot bias, M_res of every step, res_norm's weight and
+ * gamma.  fp32 arithmetic for either storage dtype; outputs are fp32.  Every output element has
+ * one writer; d_q_raw, d_eta, d_res_w and d_gamma must be zero-filled by the caller (chunks
+ * without a readout leave them untouched).
+ * Replaces the autograd backward of vsa_lm/config/bolt3.py:219-256 (softmax over
+ * [sinks | slots | window], the value read, the readout eta * res_norm(normalize(q) M (1-g)/sqrt(HD))).
+ */
+typedef struct {
+  int32_t dtype, B, T, H, HKV, HD, S, C, n_sinks;
+  int32_t n_chunks;           /* ceil(T / C) */
+  int32_t n_qtiles;           /* ceil(C / 64): query tiles per chunk */
+  int32_t n_steps;            /* consolidation steps of the forward: chunk c >= 2 reads step c - 2 */
+  int32_t score_round;        /* as in b3_attn_args (1 for the forward) */
+  const void* q_rope;         /* (b, h, t, d) at + b*q_sb + h*q_sh + t*HD + d, storage dtype */
+  const void* q_raw;
+  int64_t q_sb, q_sh;
+  const void* win_k;          /* (b, hkv, t, d) at + b*w_sb + hkv*w_sh + t*HD + d: roped keys of every token */
+  const void* win_v;
+  int64_t w_sb, w_sh;
+  const void* slot_k;         /* [step][B*HKV][S][HD] roped slot keys, as the forward's snapshots */
+  const void* slot_v;
+  const float* slot_bias;     /* [step][B*HKV][S] */
+  int64_t slot_step;          /* elements between steps of slot_k / slot_v */
+  const float* m_res;         /* [step][B*HKV] blocks of HD*HD floats, layout as b3_attn_args.m_split */
+  int64_t m_step;
+  int32_t m_split;
+  const float* eta;           /* (b, h, t) at + b*e_sb + h*e_sh + t */
+  int64_t e_sb, e_sh;
+  const float* gamma;         /* [HKV] */
+  const float* res_w;         /* [HD] */
+  float eps;
+  const void* y;              /* forward output before o_proj, (b, t, h, d) at + b*y_sb + t*y_st + h*HD + d */
+  int64_t y_sb, y_st;
+  const float* dy;            /* its gradient, fp32, (b, t, h, d) at + b*dy_sb + t*dy_st + h*HD + d */
+  int64_t dy_sb, dy_st;
+  float* d_rows;              /* [B][H][T] written: sum over d of dy * attention output */
+  float* lse;                 /* [B][H][T] written: log-sum-exp of every query row */
+  float* d_q_rope;            /* [B][H][T][HD] */
+  float* d_q_raw;             /* [B][H][T][HD] (readout part; zero-filled by the caller) */
+  float* d_eta;               /* [B][H][T] (zero-filled) */
+  float* d_m;                 /* [step][B*HKV][HD][HD]: gradient of M_res of step c - 2 from chunk c */
+  float* d_res_w;             /* [B*HKV][n_chunks][HD] partial sums (zero-filled) */
+  float* d_gamma;             /* [B*HKV][n_chunks] partial sums (zero-filled) */
+  float* d_bias;              /* [step][B*H][n_qtiles][S] partial sums of the slot bias gradient */
+  float* d_k_own;             /* [B][HKV][T][HD]: keys of chunk c from chunk c's queries */
+  float* d_v_own;
+  float* d_k_next;            /* [B][HKV][T][HD]: keys of chunk c from chunk c+1's queries (rows of the
+                                 last chunk are not written) */
+  float* d_v_next;
+  float* d_slot_k;            /* [step][B*HKV][S][HD] */
+  float* d_slot_v;
+  float* d_sink_k;            /* [n_chunks][B*HKV][n_sinks][HD] (chunks 0 and 1 are not written) */
+  float* d_sink_v;
+} b3_attn_bwd_args;
+int bolt3_attn_bwd(const b3_attn_bwd_args* a, void* stream);
+
 typedef struct {
   int32_t dtype, B, H, HKV, HD, S;
   const void* lin;            /* [B][lin_row_stride] packed projection row of the new token */

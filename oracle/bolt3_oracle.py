@@ -344,7 +344,9 @@ def consolidate(p: Bolt3Params, st: SlotState | None, kr, kp, v, pos, beta, gam,
     st.mass[r_w, s_w] = 1.0
     st.util[r_w, s_w] = rel[r_w, t_w]
 
-    # Gershgorin-safe delta rule into M_res
+    # Gershgorin-safe delta rule into M_res; the normalised keys are taken again outside no_grad,
+    # as the reference does (vsa_lm/config/bolt3.py:157): gradients reach kr through this rule
+    kn = F.normalize(kr.float(), dim=-1)
     w = beta.float() * to_delta.float()
     gram = torch.bmm(kn, kn.transpose(-1, -2)).abs()
     rowsum = torch.bmm(gram, w.unsqueeze(-1)).squeeze(-1).clamp_min(1.0)
@@ -468,6 +470,34 @@ def forward(p: Bolt3Params, x: torch.Tensor, trace: ForwardTrace | None = None, 
         trace.y_pre = y
         trace.heads = (q_raw, q_rope, k_raw, k_rope, v_all, beta_all, eta_all)
     return F.linear(y.transpose(1, 2).reshape(b, T, p.H * p.HD), p.wo.to(y.dtype))
+
+
+# Reference parameter names of the Bolt3Params fields (vsa_lm/config/bolt3.py:24-54)
+PARAM_NAMES = dict(wq="q_proj.weight", bq="q_proj.bias", wk="k_proj.weight", bk="k_proj.bias",
+                   wv="v_proj.weight", bv="v_proj.bias", wo="o_proj.weight", wb="beta_proj.weight",
+                   bb="beta_proj.bias", we="eta_proj.weight", be="eta_proj.bias", kappa="kappa",
+                   log_gamma="log_gamma", res_w="res_norm.weight", qn_w="q_norm.weight", kn_w="k_norm.weight")
+
+
+def forward_grads(p: Bolt3Params, x: torch.Tensor, upstream: torch.Tensor, ties: str = "torch"):
+    """Gradients of sum(forward(x) * upstream) with respect to x and every parameter, by autograd
+    through this restatement of the forward (the reference's own backward: its slot selection
+    runs under no_grad, vsa_lm/config/bolt3.py:98-112, :121-135, :165-180, and the gradients
+    follow the forward's decisions).  Returns (y, {"x": dx, reference name: grad}); parameters
+    the forward does not reach get zeros, like the reference's zero-weighted term (:257-258)."""
+    leaves = {}
+    for f_name in PARAM_NAMES:
+        t = getattr(p, f_name)
+        if t is not None:
+            leaves[f_name] = t.detach().clone().requires_grad_(True)
+    q = Bolt3Params(**{**p.__dict__, **leaves})
+    xg = x.detach().clone().requires_grad_(True)
+    y = forward(q, xg, ties=ties)
+    (y * upstream.to(y.dtype)).sum().backward()
+    out = {"x": xg.grad}
+    for f_name, t in leaves.items():
+        out[PARAM_NAMES[f_name]] = t.grad if t.grad is not None else torch.zeros_like(t)
+    return y.detach(), out
 
 
 # ----------------------------------------------------------------- decoder

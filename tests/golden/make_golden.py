@@ -9,7 +9,8 @@ them the seeded synthetic inputs of tests/golden/recipes.py and stores what
 they compute as safetensors files next to this script.  These pin the parts of
 the oracle that no closed form covers: the composite Bolt3Attn.forward
 (vsa_lm/config/bolt3.py:194-276), the multi-step _consolidate_functional
-trajectories (:68-192) and the Bolt3Decoder.step state machine (:335-457).
+trajectories (:68-192), the Bolt3Decoder.step state machine (:335-457) and the
+gradients of the forward (CPU autograd, fp32).
 
 Every file carries a JSON header in its metadata (torch version, case
 parameters, seed).  Parameters and inputs are regenerated from the recipes by
@@ -91,6 +92,34 @@ def fwd_case(name, cfg, B, T, seed, dtype, nondefault, clustered=None, rows_ever
           f"slots with mass>1 at end={merged}")
 
 
+def grad_case(name, cfg, B, T, seed, nondefault, clustered=None, S=128, C=128):
+    """Gradients of loss = sum(y * upstream) with respect to x and every parameter, fp32 CPU
+    autograd through the reference forward (vsa_lm/config/bolt3.py:194-276): the slot
+    selection runs under no_grad there, so the gradients follow that forward's decisions."""
+    from vsa_lm.config.bolt3 import Bolt3Attn
+    mod = recipes.init_module(Bolt3Attn(cfg, S=S, C=C), seed, nondefault)
+    D = cfg["dim"]
+    x = recipes.clustered_hidden(seed, B, T, D, **clustered) if clustered else recipes.hidden(seed, B, T, D)
+    g = recipes.upstream(seed, B, T, D)
+    inputs = {f"param.{k}": v for k, v in mod.state_dict().items()}
+    inputs["x"] = x
+    inputs["upstream"] = g
+    calls = record_consolidations(mod)
+    xg = x.clone().requires_grad_(True)
+    y = mod(xg)
+    (y * g).sum().backward()
+    tensors = {"y": y.detach().contiguous(), "grad.x": xg.grad.contiguous()}
+    for k, prm in mod.named_parameters():
+        tensors[f"grad.{k}"] = (prm.grad if prm.grad is not None else torch.zeros_like(prm)).contiguous()
+    merged = sum(int((c[2] > 1).sum()) for c in calls[-1:])
+    meta = dict(case=name, torch=torch.__version__, cfg=cfg, B=B, T=T, S=S, C=C, seed=seed, dtype="float32",
+                nondefault=nondefault, clustered=clustered, n_consolidations=len(calls),
+                n_filled=[int(c[7]) for c in calls], inputs_sha256=digest(inputs))
+    save_file(tensors, os.path.join(HERE, f"{name}.safetensors"), metadata={"header": json.dumps(meta)})
+    print(f"{name}: consolidations={len(calls)} slots with mass>1 at end={merged} "
+          f"|grad x|={float(xg.grad.norm()):.4g}")
+
+
 def decoder_case(name, seed, dtype, n_prompt, n_decode, B=2):
     from vsa_lm.config.bolt3 import Bolt3Decoder
     from vsa_lm.config.standard import UniversalVSALM
@@ -144,6 +173,15 @@ CASES = [
     ("fwd_bf16_clustered_hd128", (256, 16, 8, 128, 1000000.0, 1e-6, True, False), 1, 2048, 8, "bfloat16", True,
      dict(n_centres=512, noise=0.15), 2),
 ]
+GRAD_CASES = [
+    # name, cfg args, B, T, seed, nondefault, clustered
+    ("grad_fp32_clustered", (64, 4, 2, 64, 10000.0, 1e-5, True, True), 1, 1280, 21, True,
+     dict(n_centres=24, noise=0.12)),
+    ("grad_fp32_eta", (64, 4, 2, 64, 10000.0, 1e-5, True, False), 2, 1000, 22, True, None),
+    ("grad_fp32_short", (64, 4, 2, 64, 10000.0, 1e-5, False, False), 2, 200, 23, False, None),
+    ("grad_fp32_hd128", (256, 8, 2, 128, 1000000.0, 1e-6, True, False), 1, 896, 24, True,
+     dict(n_centres=64, noise=0.12)),
+]
 DECODER_CASES = [
     # name, seed, dtype, prompt tokens, decoded tokens
     ("dec_fp32", 6, "float32", 300, 220),
@@ -157,6 +195,9 @@ def main(ref_root: str, only=()):
     for name, c, B, T, seed, dt, nd, cl, every in CASES:
         if not only or name in only:
             fwd_case(name, layer_cfg(*c), B, T, seed, getattr(torch, dt), nd, cl, every)
+    for name, c, B, T, seed, nd, cl in GRAD_CASES:
+        if not only or name in only:
+            grad_case(name, layer_cfg(*c), B, T, seed, nd, cl)
     for name, seed, dt, n_prompt, n_decode in DECODER_CASES:
         if not only or name in only:
             decoder_case(name, seed=seed, dtype=getattr(torch, dt), n_prompt=n_prompt, n_decode=n_decode)

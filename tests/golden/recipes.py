@@ -81,6 +81,13 @@ def clustered_hidden(seed: int, B: int, T: int, D: int, n_centres: int, noise: f
     return centres[torch.from_numpy(z)] + _n(rng, (B, T, D), noise)
 
 
+def upstream(seed: int, B: int, T: int, D: int) -> torch.Tensor:
+    """Gradient of the loss with respect to the layer output, ~N(0, 1) [B, T, D] (fp32): the
+    gradient fixtures back-propagate loss = sum(y * upstream)."""
+    rng = np.random.default_rng([seed, 5])
+    return _n(rng, (B, T, D), 1.0)
+
+
 def tokens(seed: int, B: int, T: int, vocab: int) -> torch.Tensor:
     rng = np.random.default_rng([seed, 3])
     return torch.from_numpy(rng.integers(0, vocab, size=(B, T))).long()

@@ -42,6 +42,23 @@ def build_layer(meta: dict, dtype=None):
     return mod.to(dt), x.to(dt)
 
 
+def build_grad_case(meta: dict):
+    """Product Bolt3Attn (CPU, fp32) of a gradient fixture, its input x and the upstream gradient;
+    checks the recipe digest (parameters, x, upstream) against the fixture."""
+    from bolt3_amd import Bolt3Attn
+    mod = recipes.init_module(Bolt3Attn(layer_cfg(meta), S=meta["S"], C=meta["C"]), meta["seed"], meta["nondefault"])
+    D = meta["cfg"]["dim"]
+    cl = meta.get("clustered")
+    x = recipes.clustered_hidden(meta["seed"], meta["B"], meta["T"], D, **cl) if cl else \
+        recipes.hidden(meta["seed"], meta["B"], meta["T"], D)
+    g = recipes.upstream(meta["seed"], meta["B"], meta["T"], D)
+    inputs = {f"param.{k}": v for k, v in mod.state_dict().items()}
+    inputs["x"] = x
+    inputs["upstream"] = g
+    assert digest(inputs) == meta["inputs_sha256"], "recipe drifted from the golden fixture"
+    return mod, x, g
+
+
 def build_model(meta: dict, dtype=None):
     """Product HybridLM on CPU matching the decoder fixture."""
     from bolt3_amd import HybridLM

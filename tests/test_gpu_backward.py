@@ -1,0 +1,102 @@
+"""Backward of Bolt3Attn on the HIP path (bolt3_attn_bwd + the chain replay).
+
+* Against the reference's own gradients (tests/golden/grad_*.safetensors, fp32 CPU autograd
+  through vsa_lm/config/bolt3.py): the gradient of x and of every parameter within 1e-4
+  relative (1e-5 absolute for gradients that are zero in the reference).
+* bf16 storage (the heal trainer's autocast) at head_dim 128 with merges: against the oracle's
+  autograd on the same bf16 forward, within bf16 tolerance, decisions equal.
+* The backward leaves the forward's output unchanged and runs twice in a row with the same
+  result (every buffer it reads is the forward's, every output has one writer).
+"""
+import pytest
+import torch
+
+import recipes
+from helpers import build_grad_case, cosine, fixture, rel_err
+from oracle import bolt3_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+GRAD = ["grad_fp32_short", "grad_fp32_eta", "grad_fp32_clustered", "grad_fp32_hd128"]
+
+
+def _grads(mod, x, up, dev):
+    """(y, {"x": dx, name: grad}) of sum(mod(x) * up) on dev."""
+    mod = mod.to(dev)
+    mod.zero_grad(set_to_none=True)
+    xg = x.to(dev).clone().requires_grad_(True)
+    y = mod(xg)
+    (y * up.to(dev).to(y.dtype)).sum().backward()
+    out = {"x": xg.grad.detach().cpu()}
+    for k, prm in mod.named_parameters():
+        out[k] = (prm.grad if prm.grad is not None else torch.zeros_like(prm)).detach().cpu()
+    return y.detach().cpu(), out
+
+
+@pytest.mark.parametrize("name", GRAD)
+def test_backward_matches_reference_gradients(name, gpu):
+    g, meta = fixture(name)
+    mod, x, up = build_grad_case(meta)
+    print(f"[case] backward vs reference gradients: {name}", flush=True)
+    y, gr = _grads(mod, x, up, gpu)
+    assert rel_err(y, g["y"]) <= 1e-5, rel_err(y, g["y"])
+    errs = {}
+    for k in sorted(gr):
+        ref = g["grad." + k]
+        errs[k] = rel_err(gr[k], ref) if float(ref.norm()) > 0 else float(gr[k].abs().max())
+    print("  " + " ".join(f"{k}={v:.2e}" for k, v in errs.items()), flush=True)
+    bad = {k: v for k, v in errs.items() if v > (1e-4 if float(g["grad." + k].norm()) > 0 else 1e-5)}
+    assert not bad, bad
+
+
+def test_backward_bf16_hd128_vs_oracle(gpu):
+    """bf16 storage, head_dim 128, G = 4, clustered input where tokens merge, replace slots and
+    go to M_res: the HIP gradients against autograd through the oracle's bf16 forward (the
+    reference's bf16 arithmetic), relative error <= 3e-2 and cosine >= 0.999 for x and every
+    parameter, the readout's parameters included."""
+    cfg = dict(dim=256, num_heads=8, num_kv_heads=2, head_dim=128, rope_theta=1e6, eps=1e-6, qk_norm=True)
+    from bolt3_amd import Bolt3Attn
+    mod = recipes.init_module(Bolt3Attn(cfg), 31, nondefault=True).to(torch.bfloat16)
+    x = recipes.clustered_hidden(31, 1, 1024, 256, n_centres=512, noise=0.15).to(torch.bfloat16)
+    up = recipes.upstream(31, 1, 1024, 256)
+    print("[case] backward bf16 hd128 vs oracle", flush=True)
+    y, gr = _grads(mod, x, up, gpu)
+    yr, ref = O.forward_grads(O.Bolt3Params.from_module(mod), x, up)
+    assert rel_err(y.float(), yr.float()) <= 2e-2
+    for k in ("eta_proj.weight", "res_norm.weight", "log_gamma", "beta_proj.weight"):
+        assert float(ref[k].norm()) > 0, k          # the M_res path is exercised
+    out = []
+    for k in sorted(ref):
+        a, b = gr[k].float(), ref[k].float()
+        out.append((k, rel_err(a, b), cosine(a, b)))
+    print("  " + " ".join(f"{k}={e:.2e}/{c:.5f}" for k, e, c in out), flush=True)
+    bad = [(k, e, c) for k, e, c in out if e > 3e-2 or c < 0.999]
+    assert not bad, bad
+
+
+def test_backward_under_autocast_and_repeatable(gpu):
+    """fp32 parameters under bf16 autocast (the heal trainer's setting): parameter gradients
+    come back in fp32, x's in fp32, two backward passes give identical gradients, and the
+    output equals the no-grad forward's."""
+    g, meta = fixture("grad_fp32_eta")
+    mod, x, up = build_grad_case(meta)
+    mod = mod.to(gpu)
+    xs = x.to(gpu)
+    res = []
+    for _ in range(2):
+        mod.zero_grad(set_to_none=True)
+        xg = xs.clone().requires_grad_(True)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            y = mod(xg)
+        assert y.dtype == torch.bfloat16
+        (y.float() * up.to(gpu)).sum().backward()
+        assert xg.grad.dtype == torch.float32
+        assert all(p.grad.dtype == torch.float32 for p in mod.parameters())
+        res.append((y.detach().clone(), xg.grad.clone(), [p.grad.clone() for p in mod.parameters()]))
+    assert torch.equal(res[0][0], res[1][0]) and torch.equal(res[0][1], res[1][1])
+    assert all(torch.equal(a, b) for a, b in zip(res[0][2], res[1][2]))
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        y0 = mod(xs)
+    assert torch.equal(y0, res[0][0])
+    # against the fixture's fp32 gradients: bf16 storage, so a loose bound
+    assert cosine(res[0][1].cpu(), g["grad.x"]) >= 0.99

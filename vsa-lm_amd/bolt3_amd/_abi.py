@@ -107,9 +107,27 @@ class SlotKeysArgs(C.Structure):
     ]
 
 
+class AttnBwdArgs(C.Structure):
+    _fields_ = [
+        ("dtype", i32), ("B", i32), ("T", i32), ("H", i32), ("HKV", i32), ("HD", i32), ("S", i32), ("C", i32),
+        ("n_sinks", i32), ("n_chunks", i32), ("n_qtiles", i32), ("n_steps", i32), ("score_round", i32),
+        ("q_rope", p), ("q_raw", p), ("q_sb", i64), ("q_sh", i64),
+        ("win_k", p), ("win_v", p), ("w_sb", i64), ("w_sh", i64),
+        ("slot_k", p), ("slot_v", p), ("slot_bias", p), ("slot_step", i64),
+        ("m_res", p), ("m_step", i64), ("m_split", i32),
+        ("eta", p), ("e_sb", i64), ("e_sh", i64),
+        ("gamma", p), ("res_w", p), ("eps", f32),
+        ("y", p), ("y_sb", i64), ("y_st", i64),
+        ("dy", p), ("dy_sb", i64), ("dy_st", i64),
+        ("d_rows", p), ("lse", p), ("d_q_rope", p), ("d_q_raw", p), ("d_eta", p), ("d_m", p), ("d_res_w", p),
+        ("d_gamma", p), ("d_bias", p), ("d_k_own", p), ("d_v_own", p), ("d_k_next", p), ("d_v_next", p),
+        ("d_slot_k", p), ("d_slot_v", p), ("d_sink_k", p), ("d_sink_v", p),
+    ]
+
+
 CHAIN_NOALLOC_SCRATCH_BYTES = 4 << 20   # B3_CHAIN_NOALLOC_SCRATCH_BYTES
 
-EXPORTS = ("bolt3_heads", "bolt3_chain", "bolt3_chain_noalloc", "bolt3_chain_workspace_bytes", "bolt3_chunk_attn",
+EXPORTS = ("bolt3_attn_bwd", "bolt3_heads", "bolt3_chain", "bolt3_chain_noalloc", "bolt3_chain_workspace_bytes", "bolt3_chunk_attn",
            "bolt3_decode",
            "bolt3_decode_layer", "bolt3_decode_layer_workspace_bytes", "bolt3_decode_workspace_bytes",
            "bolt3_slot_keys", "bolt3_step_advance", "bolt3_version", "bolt3_wait_count")
@@ -129,7 +147,7 @@ def load():
     for name, st in (("bolt3_heads", HeadsArgs), ("bolt3_chain", ChainArgs), ("bolt3_chain_noalloc", ChainArgs),
                      ("bolt3_chunk_attn", AttnArgs),
                      ("bolt3_decode", DecodeArgs), ("bolt3_decode_layer", DecodeLayerArgs),
-                     ("bolt3_slot_keys", SlotKeysArgs)):
+                     ("bolt3_slot_keys", SlotKeysArgs), ("bolt3_attn_bwd", AttnBwdArgs)):
         fn = getattr(lib, name)
         fn.argtypes = [C.POINTER(st), p]
         fn.restype = C.c_int

@@ -1,0 +1,342 @@
+"""Backward of Bolt3Attn.forward on the HIP path.
+
+The reference differentiates its forward with autograd (vsa_lm/config/bolt3.py:194-276); its
+slot decisions run under no_grad (:98-112, :121-135, :165-180), so the gradient is that of a
+forward whose decisions are constants.  This module computes the same gradients from what the
+HIP forward keeps:
+
+* the attention over [sinks | slots | window] and the M_res readout of every chunk are
+  differentiated by ``bolt3_attn_bwd`` (three HIP kernels, fp32), which returns the gradients
+  of the roped queries, the un-roped queries (readout), eta, every key field, every slot
+  snapshot, the slot bias, M_res of every step, res_norm's weight and gamma;
+* the consolidation chain is differentiated by replaying the forward's decision log (the chain
+  kernel's per-step record of fills, merges, evictions and delta-rule writes) backwards over
+  the steps: the slots' keys and values are copies and mass-weighted means of token keys and
+  values (:121-155, :182-191), M_res follows the Gershgorin-scaled delta rule (:157-166);
+* RoPE, the q/k RMSNorm, the gates' sigmoid / tanh, gamma's clamp and the projections close the
+  chain back to x and the parameters.
+
+The replay is a fixed sequence of batched products over all (batch, kv head) rows per step,
+run on the forward's device and stream.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _abi as A
+
+LOG = {name: i for i, name in enumerate(A.LOG_FIELDS)}
+
+
+def _rope_t(g: torch.Tensor, ang: torch.Tensor) -> torch.Tensor:
+    """Transpose of x -> x*cos + rotate_half(x)*sin (a rotation by the angle): the rotation by
+    minus the angle.  ang broadcasts against g's leading axes, last axis HD/2."""
+    a = torch.cat((ang, ang), dim=-1)
+    half = g.shape[-1] // 2
+    rot = torch.cat((-g[..., half:], g[..., :half]), dim=-1)
+    return g * a.cos() - rot * a.sin()
+
+
+def _rms_bwd(x: torch.Tensor, w: torch.Tensor, dy: torch.Tensor, eps: float):
+    """y = x * rsqrt(mean(x^2) + eps) * w (statistic in fp32): (dx, dw) for fp32 x, dy."""
+    r = torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps)
+    g = dy * w
+    dx = r * g - x * r.pow(3) * (g * x).mean(-1, keepdim=True)
+    dw = (dy * x * r).reshape(-1, x.shape[-1]).sum(0)
+    return dx, dw
+
+
+def _snap_m(snap_m: torch.Tensor, i: int, split: bool, bh: int, HD: int) -> torch.Tensor:
+    """M_res after step i as fp32 [bh, HD, HD] (bf16 snapshots hold M^T as bf16 hi then lo)."""
+    if not split:
+        return snap_m[i]
+    raw = snap_m[i].view(torch.bfloat16).view(bh, 2, HD, HD)
+    return (raw[:, 0].float() + raw[:, 1].float()).transpose(1, 2)
+
+
+def replay_slots(log: torch.Tensor, pos: torch.Tensor, S: int, C: int, ns: int):
+    """Mass and mean position of every slot after each step, rebuilt from the decision log
+    (fills set mass 1 and the token's position; merges add counts and position sums,
+    vsa_lm/config/bolt3.py:125-136; evictions set mass 1 and the winner's position, :145-150).
+    Counts and position sums are integers, so the replay reproduces the forward's fp32 values.
+    Returns (steps, masses, positions): per step a record of its decisions."""
+    n, bh = log.shape[0], log.shape[1]
+    dev = log.device
+    mass = torch.ones(bh, S, device=dev)
+    pm = torch.zeros(bh, S, device=dev)
+    rows = torch.arange(bh, device=dev)[:, None]
+    nf = 0
+    steps, masses, pms = [], [], []
+    for i in range(n):
+        t0, l = (ns, C - ns) if i == 0 else (i * C, C)
+        p = pos[t0:t0 + l]
+        lg = log[i]
+        if nf < S:
+            m = min(S - nf, l)
+            picked = lg[:, LOG["top_tok"], :m].long()
+            mass = mass.clone()
+            pm = pm.clone()
+            mass[:, nf:nf + m] = 1.0
+            pm[:, nf:nf + m] = p[picked]
+            steps.append(dict(kind="fill", t0=t0, l=l, nf=nf, m=m, picked=picked))
+            nf += m
+        else:
+            kc = min(l, S)
+            slot = lg[:, LOG["slot"], :l].long().clamp_min(0)
+            merge = lg[:, LOG["merge"], :l] > 0.5
+            mo = merge.float()
+            cnt = torch.zeros(bh, S, device=dev).scatter_add_(1, slot, mo)
+            p_acc = torch.zeros(bh, S, device=dev).scatter_add_(1, slot, mo * p)
+            hit = cnt > 0
+            new_m = mass + cnt
+            rec = dict(kind="steady", t0=t0, l=l, slot=slot, merge=merge, hit=hit, mass=mass, new_m=new_m,
+                       toks=lg[:, LOG["top_tok"], :kc].long(), bots=lg[:, LOG["bot_slot"], :kc].long(),
+                       win=lg[:, LOG["win"], :kc] > 0.5, delta=lg[:, LOG["delta"], :l] > 0.5)
+            pm = torch.where(hit, (mass * pm + p_acc) / new_m, pm)
+            mass = torch.where(hit, new_m, mass)
+            w = rec["win"]
+            r_w = rows.expand_as(w)[w]
+            mass = mass.clone()
+            mass[r_w, rec["bots"][w]] = 1.0
+            pm[r_w, rec["bots"][w]] = p[rec["toks"][w]]
+            steps.append(rec)
+        masses.append(mass)
+        pms.append(pm)
+    return steps, masses, pms
+
+
+def chain_backward(steps, d_slot_k, d_slot_v, d_m, pms, inv_freq, kr, v, beta, gam, snap_m, m_split, b, HKV):
+    """Gradients of the consolidated tokens' keys (un-roped), values and beta, and of gamma,
+    from the gradients of every step's slot snapshot (roped keys, values) and M_res, by the
+    steps in reverse (vsa_lm/config/bolt3.py:121-166 for steady steps, :182-191 for fills).
+    kr, v: [bh, T, HD]; beta: [bh, T].  Returns (d_kr, d_v, d_beta, d_gamma)."""
+    bh, T, HD = kr.shape
+    S = d_slot_k.shape[2]
+    dev = kr.device
+    d_kr = torch.zeros(bh, T, HD, device=dev)
+    d_v = torch.zeros(bh, T, HD, device=dev)
+    d_beta = torch.zeros(bh, T, device=dev)
+    d_gam = torch.zeros(HKV, device=dev)
+    dak = torch.zeros(bh, S, HD, device=dev)
+    dav = torch.zeros(bh, S, HD, device=dev)
+    dM = torch.zeros(bh, HD, HD, device=dev)
+    rows = torch.arange(bh, device=dev)[:, None]
+    gam_bh = gam.float().repeat(b).view(bh, 1, 1)
+    for i in range(len(steps) - 1, -1, -1):
+        st = steps[i]
+        # the snapshot of step i is read by the attention as rope(ak, pm) and av, and M_res by the readout
+        dak = dak + _rope_t(d_slot_k[i], pms[i][..., None] * inv_freq)
+        dav = dav + d_slot_v[i]
+        dM = dM + d_m[i]
+        t0, l = st["t0"], st["l"]
+        if st["kind"] == "fill":
+            nf, m, picked = st["nf"], st["m"], st["picked"]
+            r = rows.expand_as(picked)
+            d_kr[:, t0:t0 + l].index_put_((r, picked), dak[:, nf:nf + m], accumulate=True)
+            d_v[:, t0:t0 + l].index_put_((r, picked), dav[:, nf:nf + m], accumulate=True)
+            dak = dak.clone()
+            dav = dav.clone()
+            dak[:, nf:nf + m] = 0.0
+            dav[:, nf:nf + m] = 0.0
+            continue
+        # eviction: a winning pair's slot is the token's copy (vsa_lm/config/bolt3.py:145-150)
+        w = st["win"]
+        r_w, s_w, t_w = rows.expand_as(w)[w], st["bots"][w], st["toks"][w]
+        gk = d_kr[:, t0:t0 + l]
+        gv = d_v[:, t0:t0 + l]
+        gk.index_put_((r_w, t_w), dak[r_w, s_w], accumulate=True)
+        gv.index_put_((r_w, t_w), dav[r_w, s_w], accumulate=True)
+        dak = dak.clone()
+        dav = dav.clone()
+        dak[r_w, s_w] = 0.0
+        dav[r_w, s_w] = 0.0
+        # merge: ak <- (mass * ak + sum of merged keys) / (mass + count) (:125-136)
+        slot, new_m = st["slot"], st["new_m"]
+        coef = (st["merge"].float() / new_m.gather(1, slot))[..., None]
+        idx = slot[..., None].expand(-1, -1, HD)
+        gk += coef * dak.gather(1, idx)
+        gv += coef * dav.gather(1, idx)
+        keep = torch.where(st["hit"], st["mass"] / new_m, torch.ones_like(new_m))[..., None]
+        dak = dak * keep
+        dav = dav * keep
+        # delta rule: M <- gam M + kn^T (bsafe * (v - kn M)), bsafe = w / max(|kn kn^T| w, 1) (:157-166)
+        kri = kr[:, t0:t0 + l].float()
+        vi = v[:, t0:t0 + l].float()
+        dmask = st["delta"].float()
+        wv = beta[:, t0:t0 + l].float() * dmask
+        M0 = _snap_m(snap_m, i - 1, m_split, bh, HD) if i > 0 else torch.zeros(bh, HD, HD, device=dev)
+        nrm = kri.norm(dim=-1, keepdim=True).clamp_min(1e-12)
+        kn = kri / nrm
+        P = torch.bmm(kn, kn.transpose(1, 2))
+        G = P.abs()
+        rs_raw = torch.bmm(G, wv[..., None]).squeeze(-1)
+        rs = rs_raw.clamp_min(1.0)
+        bs = wv / rs
+        R = vi - torch.bmm(kn, M0)
+        E = bs[..., None] * R
+        dE = torch.bmm(kn, dM)
+        d_kn = torch.bmm(E, dM.transpose(1, 2))
+        dR = bs[..., None] * dE
+        gv += dR
+        d_kn -= torch.bmm(dR, M0.transpose(1, 2))
+        d_bs = (dE * R).sum(-1)
+        d_w = d_bs / rs
+        d_rs = torch.where(rs_raw >= 1.0, -d_bs * wv / (rs * rs), torch.zeros_like(rs))
+        d_w += torch.bmm(G.transpose(1, 2), d_rs[..., None]).squeeze(-1)
+        dP = (d_rs[..., None] * wv[:, None, :]) * torch.sign(P)
+        d_kn += torch.bmm(dP + dP.transpose(1, 2), kn)
+        d_beta[:, t0:t0 + l] += d_w * dmask
+        d_gam += (dM * M0).sum(dim=(1, 2)).view(b, HKV).sum(0)
+        dM = gam_bh * dM - torch.bmm(kn.transpose(1, 2), dR)
+        gk += (d_kn - kn * (kn * d_kn).sum(-1, keepdim=True)) / nrm
+    return d_kr, d_v, d_beta, d_gam
+
+
+def attn_backward(mod, tr: dict, dy: torch.Tensor, dt: torch.dtype, n_steps: int):
+    """bolt3_attn_bwd on the forward's tensors: returns its output buffers by name."""
+    q_rope, q_raw, k_rope, v, eta = tr["q_rope"], tr["q_raw"], tr["k_rope"], tr["v"], tr["eta"]
+    b, H, T, HD = q_rope.shape
+    HKV, S, C = mod.HKV, mod.S, mod.C
+    dev = q_rope.device
+    bh = b * HKV
+    n_chunks = (T + C - 1) // C
+    n_qt = (C + 63) // 64
+    ns = min(mod.n_sinks, C)
+    f32 = dict(device=dev, dtype=torch.float32)
+    o = dict(d_rows=torch.empty(b, H, T, **f32), lse=torch.empty(b, H, T, **f32),
+             d_q_rope=torch.empty(b, H, T, HD, **f32), d_q_raw=torch.zeros(b, H, T, HD, **f32),
+             d_eta=torch.zeros(b, H, T, **f32), d_res_w=torch.zeros(bh, n_chunks, HD, **f32),
+             d_gamma=torch.zeros(bh, n_chunks, **f32),
+             d_k_own=torch.empty(b, HKV, T, HD, **f32), d_v_own=torch.empty(b, HKV, T, HD, **f32),
+             d_k_next=torch.zeros(b, HKV, T, HD, **f32), d_v_next=torch.zeros(b, HKV, T, HD, **f32))
+    a = A.AttnBwdArgs()
+    a.dtype, a.B, a.T, a.H, a.HKV, a.HD, a.S, a.C = A.dtype_code(dt), b, T, H, HKV, HD, S, C
+    a.n_sinks, a.n_chunks, a.n_qtiles, a.n_steps, a.score_round = mod.n_sinks, n_chunks, n_qt, n_steps, 1
+    a.q_rope, a.q_raw, a.q_sb, a.q_sh = q_rope.data_ptr(), q_raw.data_ptr(), q_rope.stride(0), q_rope.stride(1)
+    a.win_k, a.win_v, a.w_sb, a.w_sh = k_rope.data_ptr(), v.data_ptr(), k_rope.stride(0), k_rope.stride(1)
+    if n_steps > 0:
+        o.update(d_m=torch.empty(n_steps, bh, HD, HD, **f32), d_bias=torch.zeros(n_steps, b * H, n_qt, S, **f32),
+                 d_slot_k=torch.empty(n_steps, bh, S, HD, **f32), d_slot_v=torch.empty(n_steps, bh, S, HD, **f32),
+                 d_sink_k=torch.zeros(n_chunks, bh, ns, HD, **f32), d_sink_v=torch.zeros(n_chunks, bh, ns, HD, **f32))
+        a.slot_k, a.slot_v, a.slot_bias = tr["snap_k"].data_ptr(), tr["snap_v"].data_ptr(), tr["snap_bias"].data_ptr()
+        a.slot_step = bh * S * HD
+        a.m_res, a.m_step, a.m_split = tr["snap_m"].data_ptr(), bh * HD * HD, int(dt == torch.bfloat16)
+    a.eta, a.e_sb, a.e_sh = eta.data_ptr(), eta.stride(0), eta.stride(1)
+    side = mod._packed(dt, dev)[2]
+    a.gamma, a.res_w, a.eps = side["gamma"].data_ptr(), side["res_w"].data_ptr(), float(mod.res_norm.eps)
+    y = tr["y"]
+    a.y, a.y_sb, a.y_st = y.data_ptr(), y.stride(0), y.stride(1)
+    a.dy, a.dy_sb, a.dy_st = dy.data_ptr(), dy.stride(0), dy.stride(1)
+    for name, t in o.items():
+        setattr(a, name, t.data_ptr())
+    A.call("bolt3_attn_bwd", a, dev)
+    return o
+
+
+def layer_backward(mod, x: torch.Tensor, tr: dict, d_out: torch.Tensor, dt: torch.dtype):
+    """Gradients of Bolt3Attn.forward: (dx in fp32, {parameter name: fp32 gradient})."""
+    b, T, D = x.shape
+    H, HKV, HD, S, C = mod.H, mod.HKV, mod.HD, mod.S, mod.C
+    G = H // HKV
+    bh = b * HKV
+    dev = x.device
+    n_chunks = (T + C - 1) // C
+    n_steps = max(0, n_chunks - 2)
+    ns = min(mod.n_sinks, C)
+    grads = {}
+    d_out = d_out.float()
+    xf = x.float()
+    # o_proj
+    y = tr["y"]
+    grads["o_proj.weight"] = d_out.reshape(-1, D).t() @ y.reshape(-1, H * HD).float()
+    dy = (d_out @ mod.o_proj.weight.float()).contiguous()          # [b, T, H*HD]
+    # attention and readout
+    o = attn_backward(mod, tr, dy, dt, n_steps)
+    pos = torch.arange(T, device=dev, dtype=torch.float32)
+    inv_freq = mod.rope.inv_freq.to(dev).float()
+    ang_t = pos[:, None] * inv_freq                                # [T, HD/2]
+    d_krope = o["d_k_own"] + o["d_k_next"]
+    d_v = o["d_v_own"] + o["d_v_next"]
+    gam = mod.gamma_delta().detach().to(dev)
+    d_gam = o["d_gamma"].view(b, HKV, n_chunks).sum(dim=(0, 2))
+    d_beta = torch.zeros(b, HKV, T, device=dev)
+    d_kraw = torch.zeros(b, HKV, T, HD, device=dev)
+    d_kappa = torch.zeros(HKV, device=dev)
+    if n_steps > 0:
+        d_krope[:, :, :ns] += o["d_sink_k"].sum(0).view(b, HKV, ns, HD)
+        d_v[:, :, :ns] += o["d_sink_v"].sum(0).view(b, HKV, ns, HD)
+        steps, masses, pms = replay_slots(tr["log"], pos, S, C, ns)
+        # kappa: the slot bias is kappa * log(max(mass, 1)) (vsa_lm/config/bolt3.py:238-241)
+        dbias = o["d_bias"].sum(2).view(n_steps, b, HKV, G, S).sum(3)             # [step, b, HKV, S]
+        logm = torch.stack(masses).clamp_min(1.0).log().view(n_steps, b, HKV, S)
+        d_kappa = (dbias * logm).sum(dim=(0, 1, 3))
+        dk_c, dv_c, db_c, dg_c = chain_backward(
+            steps, o["d_slot_k"], o["d_slot_v"], o["d_m"], pms, inv_freq, tr["k_raw"].reshape(bh, T, HD),
+            tr["v"].reshape(bh, T, HD), tr["beta"].reshape(bh, T), gam, tr["snap_m"], dt == torch.bfloat16, b, HKV)
+        d_kraw += dk_c.view(b, HKV, T, HD)
+        d_v += dv_c.view(b, HKV, T, HD)
+        d_beta += db_c.view(b, HKV, T)
+        d_gam += dg_c
+    d_kraw += _rope_t(d_krope, ang_t)
+    d_qraw = o["d_q_raw"] + _rope_t(o["d_q_rope"], ang_t)
+    # q / k RMSNorm (the statistic in fp32, vsa_lm/surgery.py:48-52) on the projections
+    lin_q = torch.nn.functional.linear(xf, mod.q_proj.weight.float(),
+                                       None if mod.q_proj.bias is None else mod.q_proj.bias.float())
+    lin_k = torch.nn.functional.linear(xf, mod.k_proj.weight.float(),
+                                       None if mod.k_proj.bias is None else mod.k_proj.bias.float())
+    dq = d_qraw.transpose(1, 2)                                      # [b, T, H, HD]
+    dk = d_kraw.transpose(1, 2)
+    if mod.q_norm is not None:
+        dq, grads["q_norm.weight"] = _rms_bwd(lin_q.view(b, T, H, HD), mod.q_norm.weight.float(), dq,
+                                              float(mod.q_norm.eps))
+        dk, grads["k_norm.weight"] = _rms_bwd(lin_k.view(b, T, HKV, HD), mod.k_norm.weight.float(), dk,
+                                              float(mod.k_norm.eps))
+    dq = dq.reshape(b * T, H * HD)
+    dk = dk.reshape(b * T, HKV * HD)
+    dvv = d_v.transpose(1, 2).reshape(b * T, HKV * HD)
+    # gates: beta = sigmoid(.), eta = tanh(.) (vsa_lm/config/bolt3.py:198-199)
+    bet = tr["beta"].float()
+    d_zb = (d_beta * bet * (1.0 - bet)).transpose(1, 2).reshape(b * T, HKV)
+    eta = tr["eta"].float()
+    d_ze = (o["d_eta"] * (1.0 - eta * eta)).transpose(1, 2).reshape(b * T, H)
+    x2 = xf.reshape(b * T, D)
+    dx = torch.zeros(b * T, D, device=dev)
+    for name, lin, dz in (("q_proj", mod.q_proj, dq), ("k_proj", mod.k_proj, dk), ("v_proj", mod.v_proj, dvv),
+                          ("beta_proj", mod.beta_proj, d_zb), ("eta_proj", mod.eta_proj, d_ze)):
+        dx += dz @ lin.weight.float()
+        grads[f"{name}.weight"] = dz.t() @ x2
+        if lin.bias is not None:
+            grads[f"{name}.bias"] = dz.sum(0)
+    grads["kappa"] = d_kappa
+    # gamma = clamp(0.999 * sigmoid(log_gamma), 1e-3, 0.999); clamp passes its bounds inclusive
+    sg = torch.sigmoid(mod.log_gamma.detach().float().to(dev))
+    g0 = 0.999 * sg
+    inside = ((g0 >= 1e-3) & (g0 <= 0.999)).float()
+    grads["log_gamma"] = d_gam * 0.999 * sg * (1.0 - sg) * inside
+    grads["res_norm.weight"] = o["d_res_w"].sum(dim=(0, 1))
+    return dx.view(b, T, D), grads
+
+
+class Bolt3Function(torch.autograd.Function):
+    """Bolt3Attn.forward as one autograd node: the HIP forward keeps its trace, the backward is
+    layer_backward.  Inputs: (module, x in the storage dtype, *parameters in named order)."""
+
+    @staticmethod
+    def forward(ctx, mod, x, *params):
+        tr = {}
+        out = mod._forward_hip(x, tr)
+        ctx.mod, ctx.tr, ctx.dt = mod, tr, x.dtype
+        ctx.names = [n for n, _ in mod.named_parameters()]
+        ctx.save_for_backward(x)
+        return out
+
+    @staticmethod
+    def backward(ctx, d_out):
+        (x,) = ctx.saved_tensors
+        dx, grads = layer_backward(ctx.mod, x, ctx.tr, d_out, ctx.dt)
+        ctx.tr = None
+        out = [None, dx.to(x.dtype)]
+        for name, prm in zip(ctx.names, ctx.mod.parameters()):
+            g = grads.get(name)
+            out.append(None if g is None else g.to(prm.dtype).view_as(prm))
+        return tuple(out)

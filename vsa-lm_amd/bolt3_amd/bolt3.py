@@ -7,7 +7,9 @@ constructor signatures, parameter / state-dict names, ``gamma_delta``,
 ``memorize`` / ``forget`` / ``blank_state`` / ``state_bytes`` / ``_sample``.
 
 Everything between the input projections and ``o_proj`` runs in the HIP
-kernels of libbolt3_amd.so (include/bolt3_amd.h).  The projections are one
+kernels of libbolt3_amd.so (include/bolt3_amd.h), and so does the backward of
+the attention and readout (backward.py replays the consolidation chain's
+decisions for the rest of the gradient).  The projections are one
 packed GEMM (q | k | v | beta | eta) through torch.  There is no CPU or eager
 fallback: a CPU tensor or a missing library raises.
 
@@ -23,6 +25,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import _abi as A
+from .backward import Bolt3Function
 from .layers import RMSNorm, RoPE
 
 N_SINKS = 4
@@ -125,18 +128,6 @@ class _storage_dtype:
 def _check_dtype(t: torch.Tensor, dt: torch.dtype, what: str):
     if t.dtype != dt:
         raise TypeError(f"{what} is {t.dtype}, the kernels were told {dt}")
-
-
-class _NoBackward(torch.autograd.Function):
-    """Keeps autograd edges to the inputs but refuses to differentiate the HIP path."""
-
-    @staticmethod
-    def forward(ctx, out, *inputs):
-        return out.view_as(out)
-
-    @staticmethod
-    def backward(ctx, *grads):
-        raise NotImplementedError("Bolt3Attn backward is not implemented in the HIP path yet")
 
 
 def _tout(t: torch.Tensor | None, offset: int = 0) -> A.TensorOut:
@@ -315,11 +306,13 @@ class Bolt3Attn(nn.Module):
 
     def forward(self, x: torch.Tensor, _trace: dict | None = None) -> torch.Tensor:
         _require_gpu(x, "Bolt3Attn.forward")
+        need_grad = torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters()))
         with _storage_dtype(x) as dt:
-            out = self._forward_hip(x.to(dt), _trace)
-        if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters())):
-            out = _NoBackward.apply(out, x, *[p for p in self.parameters() if p.requires_grad])
-        return out
+            if need_grad:
+                # one autograd node: the forward keeps its trace, the backward runs bolt3_attn_bwd
+                # and replays the consolidation chain (backward.py)
+                return Bolt3Function.apply(self, x.to(dt), *self.parameters())
+            return self._forward_hip(x.to(dt), _trace)
 
     @torch.no_grad()
     def _forward_hip(self, x: torch.Tensor, trace: dict | None) -> torch.Tensor:

@@ -1,0 +1,685 @@
+// Backward of the Bolt-3 chunk attention and M_res readout (gfx950).
+//
+// The forward of every chunk c is a joint softmax over four key fields of its (batch, kv head)
+// row -- [sinks | attractor slots | previous chunk | own chunk (causal)] -- with the slot field's
+// bias kappa*log(mass) (-inf for inactive slots), plus the readout
+//     y += eta * RMSNorm(normalize(q_raw) . M * (1 - gamma) / sqrt(HD))
+// for chunks c >= 2, which use the slot snapshot and M_res of consolidation step c - 2
+// (vsa_lm/config/bolt3.py:219-256).  bolt3_attn_bwd runs three kernels:
+//
+//   readout_bwd_kernel, grid (B*HKV, chunks): per row D = sum_d dy * (attention output),
+//     with the readout's own contribution taken out of y; the readout's gradients with respect
+//     to eta, q_raw, M (one dM per chunk), res_norm's weight and gamma.
+//   attn_bwd_dq_kernel, grid (query tiles, B*H, chunks): recomputes each row's log-sum-exp over
+//     all key fields, then dS = P * (dO . V^T - D) block by block, dQ = scale * dS . K and the
+//     slot columns' sums of dS (the gradient of the slot bias).
+//   attn_bwd_dkv_kernel, grid (key blocks, B*HKV, chunks): one 32-key block of one field per
+//     workgroup, over every query row of the chunk's G heads: dV = P^T . dO, dK = scale * dS^T . Q.
+//     Every key row has one writer: the previous chunk's keys go to d_k_next, the chunk's own
+//     keys to d_k_own, slots to d_slot_k of step c - 2, sinks to d_sink_k of chunk c.
+//
+// All arithmetic is fp32 (fp32 FMAs on the vector ALUs); operands of either storage dtype are
+// widened while they are staged in LDS.  Scores are rebuilt like the forward's (the q.k
+// product rounded to the storage dtype first when score_round is set, then scale, bias, mask).
+#include <math.h>
+
+#include "bolt3_common.h"
+#include "bolt3_amd.h"
+
+namespace b3 {
+namespace bwd {
+
+constexpr int NT = 256;     // threads of every backward workgroup
+constexpr int BQ = 64;      // query rows per tile
+constexpr int BK = 32;      // keys per block
+constexpr int RT = 16;      // query rows per readout tile
+
+// one key field of a chunk: rows of HD elements, `len` of them
+struct KField {
+  const void* k;
+  const void* v;
+  const float* bias;   // slots only
+  int len;
+  int kind;            // 0 sinks, 1 slots, 2 previous chunk, 3 own chunk
+};
+
+__device__ __forceinline__ int chunk_len(const b3_attn_bwd_args& a, int c) { return min(a.C, a.T - c * a.C); }
+
+// which fields chunk c has: bit k for kind k (sinks and slots once step c - 2 exists)
+__device__ __forceinline__ int field_mask(const b3_attn_bwd_args& a, int c) {
+  const bool state = c >= 2 && c - 2 < a.n_steps;
+  return (state && a.n_sinks > 0 ? 1 : 0) | (state ? 2 : 0) | (c >= 1 ? 4 : 0) | 8;
+}
+
+// the fi-th field of chunk c of row (b, hkv), in the order sinks, slots, previous chunk, own chunk
+template <typename T>
+__device__ __forceinline__ KField chunk_field(const b3_attn_bwd_args& a, int b, int hkv, int c, int fi) {
+  const int mask = field_mask(a, c);
+  int kind = 0;
+  for (int k = 0, seen = 0; k < 4; ++k)
+    if (mask & (1 << k)) {
+      if (seen == fi) kind = k;
+      ++seen;
+    }
+  const int HD = a.HD;
+  const T* wk = reinterpret_cast<const T*>(a.win_k) + (long long)b * a.w_sb + (long long)hkv * a.w_sh;
+  const T* wv = reinterpret_cast<const T*>(a.win_v) + (long long)b * a.w_sb + (long long)hkv * a.w_sh;
+  if (kind == 0) return KField{wk, wv, nullptr, min(a.n_sinks, a.C), 0};
+  if (kind == 1) {
+    const long long bh = (long long)b * a.HKV + hkv;
+    const long long so = (long long)(c - 2) * a.slot_step + bh * a.S * HD;
+    return KField{reinterpret_cast<const T*>(a.slot_k) + so, reinterpret_cast<const T*>(a.slot_v) + so,
+                  a.slot_bias + (long long)(c - 2) * (a.slot_step / HD) + bh * a.S, a.S, 1};
+  }
+  if (kind == 2)
+    return KField{wk + (long long)(c - 1) * a.C * HD, wv + (long long)(c - 1) * a.C * HD, nullptr, a.C, 2};
+  return KField{wk + (long long)c * a.C * HD, wv + (long long)c * a.C * HD, nullptr, chunk_len(a, c), 3};
+}
+
+// rows [0, n_rows) of a [rows][HD] source (row stride `rs` elements) into fp32 LDS rows of
+// stride `ls`; rows at or past n_valid are zeros
+template <typename T, int HD>
+__device__ __forceinline__ void stage_rows(float* lds, int ls, const T* src, long long rs, int n_rows, int n_valid,
+                                           int tid) {
+  for (int it = tid; it < n_rows * (HD / 4); it += NT) {
+    const int r = it / (HD / 4), c4 = (it % (HD / 4)) * 4;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (r < n_valid) {
+      const T* p = src + (long long)r * rs + c4;
+      if constexpr (St<T>::is_bf16) {
+        const u16x4 u = *reinterpret_cast<const u16x4*>(p);
+        v = make_float4(bf2f(u[0]), bf2f(u[1]), bf2f(u[2]), bf2f(u[3]));
+      } else {
+        v = *reinterpret_cast<const float4*>(p);
+      }
+    }
+    *reinterpret_cast<float4*>(lds + r * ls + c4) = v;
+  }
+}
+
+__device__ __forceinline__ float red16_sum(float x) {
+#pragma unroll
+  for (int o = 8; o >= 1; o >>= 1) x += __shfl_xor(x, o, 64);
+  return x;
+}
+__device__ __forceinline__ float red16_max(float x) {
+#pragma unroll
+  for (int o = 8; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o, 64));
+  return x;
+}
+
+// s[i][j] = sum_d A[4 rg + i][d] * B[2 cg + j][d] (A: BQ rows, B: BK rows, both fp32 in LDS)
+template <int HD>
+__device__ __forceinline__ void tile_dot(float (&s)[4][2], const float* A, const float* B, int ls, int rg, int cg) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) s[i][0] = s[i][1] = 0.f;
+#pragma unroll 4
+  for (int d = 0; d < HD; d += 4) {
+    float4 av[4], bv[2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) av[i] = *reinterpret_cast<const float4*>(A + (4 * rg + i) * ls + d);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) bv[j] = *reinterpret_cast<const float4*>(B + (2 * cg + j) * ls + d);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        s[i][j] += av[i].x * bv[j].x + av[i].y * bv[j].y + av[i].z * bv[j].z + av[i].w * bv[j].w;
+  }
+}
+
+// The forward's score of query row i (index in the chunk) and key `col` of a block starting at
+// key j0 of field f: rounding, scale, slot bias, validity (field length, causal own field).
+template <typename T>
+__device__ __forceinline__ float score_of(const b3_attn_bwd_args& a, float dot, const KField& f, int j0, int col,
+                                          int i, float scale) {
+  const int j = j0 + col;
+  if (j >= f.len) return -INFINITY;
+  if (f.kind == 3 && j > i) return -INFINITY;
+  float x = a.score_round ? St<T>::rnd(dot) : dot;
+  x = mul_rn(x, scale);
+  if (f.kind == 1) x = add_rn(x, f.bias[j]);
+  return x;
+}
+
+template <int HD>
+struct DqSmem {
+  float q[BQ][HD + 4];
+  float dout[BQ][HD + 4];
+  float k[BK][HD + 4];
+  float v[BK][HD + 4];
+  float ds[BQ][BK + 4];
+};
+
+template <typename T, int HD>
+__global__ void __launch_bounds__(NT) attn_bwd_dq_kernel(b3_attn_bwd_args a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
+  DqSmem<HD>& sm = *reinterpret_cast<DqSmem<HD>*>(smem_raw);
+  constexpr int LS = HD + 4, DPT = HD / 16;
+  const int tid = threadIdx.x, rg = tid >> 4, cg = tid & 15;
+  const int qb = blockIdx.x, b = blockIdx.y / a.H, h = blockIdx.y % a.H, c = blockIdx.z;
+  const int G = a.H / a.HKV, hkv = h / G;
+  const int tc = chunk_len(a, c), q0 = qb * BQ;
+  if (q0 >= tc) return;
+  const int nq = min(BQ, tc - q0);
+  const float scale = 1.0f / sqrtf((float)HD);
+  const long long row0 = ((long long)b * a.H + h) * a.T + (long long)c * a.C + q0;   // (b, h, t) row index
+  stage_rows<T, HD>(&sm.q[0][0], LS, reinterpret_cast<const T*>(a.q_rope) + (long long)b * a.q_sb +
+                                         (long long)h * a.q_sh + ((long long)c * a.C + q0) * HD,
+                    HD, BQ, nq, tid);
+  stage_rows<float, HD>(&sm.dout[0][0], LS, a.dy + (long long)b * a.dy_sb + ((long long)c * a.C + q0) * a.dy_st +
+                                                (long long)h * HD,
+                        a.dy_st, BQ, nq, tid);
+  float drow[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) drow[i] = 4 * rg + i < nq ? a.d_rows[row0 + 4 * rg + i] : 0.f;
+  const int n_fields = __popc(field_mask(a, c));
+
+  // pass 1: log-sum-exp of every row over all fields
+  float m[4], l[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) { m[i] = -INFINITY; l[i] = 0.f; }
+  for (int fi = 0; fi < n_fields; ++fi) {
+    const KField f = chunk_field<T>(a, b, hkv, c, fi);
+    for (int j0 = 0; j0 < f.len; j0 += BK) {
+      if (f.kind == 3 && j0 > q0 + nq - 1) break;
+      __syncthreads();
+      stage_rows<T, HD>(&sm.k[0][0], LS, reinterpret_cast<const T*>(f.k) + (long long)j0 * HD, HD, BK, f.len - j0,
+                        tid);
+      __syncthreads();
+      float s[4][2];
+      tile_dot<HD>(s, &sm.q[0][0], &sm.k[0][0], LS, rg, cg);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float x0 = score_of<T>(a, s[i][0], f, j0, 2 * cg, q0 + 4 * rg + i, scale);
+        const float x1 = score_of<T>(a, s[i][1], f, j0, 2 * cg + 1, q0 + 4 * rg + i, scale);
+        const float bm = red16_max(fmaxf(x0, x1));
+        const float mn = fmaxf(m[i], bm);
+        if (mn == -INFINITY) continue;
+        const float e = (x0 == -INFINITY ? 0.f : expf(x0 - mn)) + (x1 == -INFINITY ? 0.f : expf(x1 - mn));
+        l[i] = l[i] * (m[i] == -INFINITY ? 0.f : expf(m[i] - mn)) + red16_sum(e);
+        m[i] = mn;
+      }
+    }
+  }
+  float lse[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    lse[i] = m[i] + logf(l[i]);
+    if (cg == 0 && 4 * rg + i < nq) a.lse[row0 + 4 * rg + i] = lse[i];
+  }
+
+  // pass 2: dS block by block, dQ += dS . K, slot-bias gradient
+  float dq[4][DPT];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int e = 0; e < DPT; ++e) dq[i][e] = 0.f;
+  const long long bias_row = (((long long)(c - 2) * a.B * a.H + (long long)b * a.H + h) * a.n_qtiles + qb) * a.S;
+  for (int fi = 0; fi < n_fields; ++fi) {
+    const KField f = chunk_field<T>(a, b, hkv, c, fi);
+    for (int j0 = 0; j0 < f.len; j0 += BK) {
+      if (f.kind == 3 && j0 > q0 + nq - 1) break;
+      __syncthreads();
+      stage_rows<T, HD>(&sm.k[0][0], LS, reinterpret_cast<const T*>(f.k) + (long long)j0 * HD, HD, BK, f.len - j0,
+                        tid);
+      stage_rows<T, HD>(&sm.v[0][0], LS, reinterpret_cast<const T*>(f.v) + (long long)j0 * HD, HD, BK, f.len - j0,
+                        tid);
+      __syncthreads();
+      float s[4][2], dp[4][2];
+      tile_dot<HD>(s, &sm.q[0][0], &sm.k[0][0], LS, rg, cg);
+      tile_dot<HD>(dp, &sm.dout[0][0], &sm.v[0][0], LS, rg, cg);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const float x = score_of<T>(a, s[i][j], f, j0, 2 * cg + j, q0 + 4 * rg + i, scale);
+          const bool live = 4 * rg + i < nq && x != -INFINITY;
+          const float p = live ? expf(x - lse[i]) : 0.f;
+          sm.ds[4 * rg + i][2 * cg + j] = live ? p * (dp[i][j] - drow[i]) : 0.f;
+        }
+      __syncthreads();
+      if (f.kind == 1 && tid < BK && j0 + tid < f.len) {
+        float cs = 0.f;
+        for (int r = 0; r < nq; ++r) cs += sm.ds[r][tid];
+        a.d_bias[bias_row + j0 + tid] = cs;
+      }
+      // dq[i][e] += sum_j ds[4 rg + i][j] * k[j][DPT cg + e]
+#pragma unroll 2
+      for (int j = 0; j < BK; j += 4) {
+        float4 dsv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dsv[i] = *reinterpret_cast<const float4*>(&sm.ds[4 * rg + i][j]);
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          float kv[DPT];
+#pragma unroll
+          for (int e = 0; e < DPT; e += 4) {
+            const float4 t = *reinterpret_cast<const float4*>(&sm.k[j + jj][DPT * cg + e]);
+            kv[e] = t.x; kv[e + 1] = t.y; kv[e + 2] = t.z; kv[e + 3] = t.w;
+          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float w = jj == 0 ? dsv[i].x : jj == 1 ? dsv[i].y : jj == 2 ? dsv[i].z : dsv[i].w;
+#pragma unroll
+            for (int e = 0; e < DPT; ++e) dq[i][e] += w * kv[e];
+          }
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (4 * rg + i >= nq) continue;
+    float* o = a.d_q_rope + (row0 + 4 * rg + i) * HD + DPT * cg;
+#pragma unroll
+    for (int e = 0; e < DPT; e += 4)
+      *reinterpret_cast<float4*>(o + e) =
+          make_float4(dq[i][e] * scale, dq[i][e + 1] * scale, dq[i][e + 2] * scale, dq[i][e + 3] * scale);
+  }
+}
+
+template <int HD>
+struct DkvSmem {
+  float q[BQ][HD + 4];
+  float dout[BQ][HD + 4];
+  float k[BK][HD + 4];
+  float v[BK][HD + 4];
+  float pt[BK][BQ + 4];    // P transposed: [key][row]
+  float dst[BK][BQ + 4];   // dS transposed
+  float lse[BQ];
+  float drow[BQ];
+};
+
+template <typename T, int HD>
+__global__ void __launch_bounds__(NT) attn_bwd_dkv_kernel(b3_attn_bwd_args a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
+  DkvSmem<HD>& sm = *reinterpret_cast<DkvSmem<HD>*>(smem_raw);
+  constexpr int LS = HD + 4, DPT = HD / 16;
+  const int tid = threadIdx.x, rg = tid >> 4, cg = tid & 15;
+  const int bh = blockIdx.y, b = bh / a.HKV, hkv = bh % a.HKV, c = blockIdx.z;
+  const int G = a.H / a.HKV;
+  const int tc = chunk_len(a, c);
+  const float scale = 1.0f / sqrtf((float)HD);
+  // this workgroup's block: the blockIdx.x-th 32-key block of the chunk's fields in order
+  const int n_fields = __popc(field_mask(a, c));
+  int fi = 0, j0 = blockIdx.x * BK;
+  KField f = chunk_field<T>(a, b, hkv, c, 0);
+  while (j0 >= f.len) {
+    j0 -= (f.len + BK - 1) / BK * BK;
+    if (++fi >= n_fields) return;
+    f = chunk_field<T>(a, b, hkv, c, fi);
+  }
+  const int nk = min(BK, f.len - j0);
+  stage_rows<T, HD>(&sm.k[0][0], LS, reinterpret_cast<const T*>(f.k) + (long long)j0 * HD, HD, BK, nk, tid);
+  stage_rows<T, HD>(&sm.v[0][0], LS, reinterpret_cast<const T*>(f.v) + (long long)j0 * HD, HD, BK, nk, tid);
+  // accumulators: keys 2 jg + jj, columns DPT dg + e
+  const int jg = tid >> 4, dg = tid & 15;
+  float dk[2][DPT], dv[2][DPT];
+#pragma unroll
+  for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+    for (int e = 0; e < DPT; ++e) dk[jj][e] = dv[jj][e] = 0.f;
+  for (int g = 0; g < G; ++g) {
+    const int h = hkv * G + g;
+    for (int q0 = 0; q0 < tc; q0 += BQ) {
+      const int nq = min(BQ, tc - q0);
+      if (f.kind == 3 && j0 > q0 + nq - 1) continue;   // every row of the tile precedes the keys
+      const long long row0 = ((long long)b * a.H + h) * a.T + (long long)c * a.C + q0;
+      __syncthreads();
+      stage_rows<T, HD>(&sm.q[0][0], LS, reinterpret_cast<const T*>(a.q_rope) + (long long)b * a.q_sb +
+                                             (long long)h * a.q_sh + ((long long)c * a.C + q0) * HD,
+                        HD, BQ, nq, tid);
+      stage_rows<float, HD>(&sm.dout[0][0], LS,
+                            a.dy + (long long)b * a.dy_sb + ((long long)c * a.C + q0) * a.dy_st + (long long)h * HD,
+                            a.dy_st, BQ, nq, tid);
+      if (tid < BQ) {
+        sm.lse[tid] = tid < nq ? a.lse[row0 + tid] : INFINITY;
+        sm.drow[tid] = tid < nq ? a.d_rows[row0 + tid] : 0.f;
+      }
+      __syncthreads();
+      float s[4][2], dp[4][2];
+      tile_dot<HD>(s, &sm.q[0][0], &sm.k[0][0], LS, rg, cg);
+      tile_dot<HD>(dp, &sm.dout[0][0], &sm.v[0][0], LS, rg, cg);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int r = 4 * rg + i;
+          const float x = score_of<T>(a, s[i][j], f, j0, 2 * cg + j, q0 + r, scale);
+          const bool live = r < nq && x != -INFINITY;
+          const float p = live ? expf(x - sm.lse[r]) : 0.f;
+          sm.pt[2 * cg + j][r] = p;
+          sm.dst[2 * cg + j][r] = live ? p * (dp[i][j] - sm.drow[r]) : 0.f;
+        }
+      __syncthreads();
+      // dv[jj][e] += sum_r pt[2 jg + jj][r] * dout[r][DPT dg + e]; dk likewise with dst and q
+#pragma unroll 2
+      for (int r = 0; r < BQ; r += 4) {
+        float4 pv[2], dsv[2];
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+          pv[jj] = *reinterpret_cast<const float4*>(&sm.pt[2 * jg + jj][r]);
+          dsv[jj] = *reinterpret_cast<const float4*>(&sm.dst[2 * jg + jj][r]);
+        }
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          float ov[DPT], qv[DPT];
+#pragma unroll
+          for (int e = 0; e < DPT; e += 4) {
+            const float4 to = *reinterpret_cast<const float4*>(&sm.dout[r + rr][DPT * dg + e]);
+            const float4 tq = *reinterpret_cast<const float4*>(&sm.q[r + rr][DPT * dg + e]);
+            ov[e] = to.x; ov[e + 1] = to.y; ov[e + 2] = to.z; ov[e + 3] = to.w;
+            qv[e] = tq.x; qv[e + 1] = tq.y; qv[e + 2] = tq.z; qv[e + 3] = tq.w;
+          }
+#pragma unroll
+          for (int jj = 0; jj < 2; ++jj) {
+            const float wp = rr == 0 ? pv[jj].x : rr == 1 ? pv[jj].y : rr == 2 ? pv[jj].z : pv[jj].w;
+            const float ws = rr == 0 ? dsv[jj].x : rr == 1 ? dsv[jj].y : rr == 2 ? dsv[jj].z : dsv[jj].w;
+#pragma unroll
+            for (int e = 0; e < DPT; ++e) {
+              dv[jj][e] += wp * ov[e];
+              dk[jj][e] += ws * qv[e];
+            }
+          }
+        }
+      }
+    }
+  }
+  // destination rows of this block's keys
+  float *ok = nullptr, *ov = nullptr;
+  const long long HDl = HD;
+  if (f.kind == 0) {
+    const long long o = (((long long)c * a.B * a.HKV + bh) * a.n_sinks + j0) * HDl;
+    ok = a.d_sink_k + o;
+    ov = a.d_sink_v + o;
+  } else if (f.kind == 1) {
+    const long long o = (((long long)(c - 2) * a.B * a.HKV + bh) * a.S + j0) * HDl;
+    ok = a.d_slot_k + o;
+    ov = a.d_slot_v + o;
+  } else {
+    const long long o = ((long long)bh * a.T + (long long)(f.kind == 2 ? c - 1 : c) * a.C + j0) * HDl;
+    ok = (f.kind == 2 ? a.d_k_next : a.d_k_own) + o;
+    ov = (f.kind == 2 ? a.d_v_next : a.d_v_own) + o;
+  }
+#pragma unroll
+  for (int jj = 0; jj < 2; ++jj) {
+    const int j = 2 * jg + jj;
+    if (j >= nk) continue;
+#pragma unroll
+    for (int e = 0; e < DPT; e += 4) {
+      *reinterpret_cast<float4*>(ok + j * HDl + DPT * dg + e) =
+          make_float4(dk[jj][e] * scale, dk[jj][e + 1] * scale, dk[jj][e + 2] * scale, dk[jj][e + 3] * scale);
+      *reinterpret_cast<float4*>(ov + j * HDl + DPT * dg + e) =
+          make_float4(dv[jj][e], dv[jj][e + 1], dv[jj][e + 2], dv[jj][e + 3]);
+    }
+  }
+}
+
+template <int HD>
+struct RdSmem {
+  float m[HD][HD + 4];     // M[c][d]
+  float qn[RT][HD + 4];    // normalised q_raw rows of the tile
+  float du[RT][HD + 4];    // gradient of qn . M
+  float part[RT][HD + 4];  // per-row d res_w terms, then reduced
+  float inv[RT];           // 1 / max(|q_raw|, 1e-12)
+};
+
+// d_rows for every chunk; for chunks with a readout also its gradients.
+template <typename T, int HD>
+__global__ void __launch_bounds__(NT) readout_bwd_kernel(b3_attn_bwd_args a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
+  RdSmem<HD>& sm = *reinterpret_cast<RdSmem<HD>*>(smem_raw);
+  constexpr int DPT = HD / 16;
+  const int tid = threadIdx.x, r = tid >> 4, dg = tid & 15;   // row of the tile, column group
+  const int bh = blockIdx.x, b = bh / a.HKV, hkv = bh % a.HKV, c = blockIdx.y;
+  const int G = a.H / a.HKV;
+  const int tc = chunk_len(a, c);
+  const int n_rows = G * tc;
+  const bool has_m = c >= 2 && c - 2 < a.n_steps && a.m_res != nullptr;
+  const float* M = has_m ? a.m_res + (long long)(c - 2) * a.m_step + (long long)bh * HD * HD : nullptr;
+  if (has_m) {
+    if (a.m_split) {
+      // M^T[d][c] stored as bf16 hi then bf16 lo
+      const uint16_t* src = reinterpret_cast<const uint16_t*>(M);
+      for (int it = tid; it < HD * HD; it += NT) {
+        const int d = it / HD, cc = it % HD;
+        sm.m[cc][d] = bf2f(src[it]) + bf2f(src[HD * HD + it]);
+      }
+    } else {
+      for (int it = tid; it < HD * HD; it += NT) sm.m[it / HD][it % HD] = M[it];
+    }
+  }
+  const float gam = a.gamma[hkv];
+  const float sg = (1.0f - gam) / sqrtf((float)HD);
+  float dm[DPT][DPT];   // dM[DPT r' + i][DPT dg + j] with r' = tid >> 4 as the row group of M
+#pragma unroll
+  for (int i = 0; i < DPT; ++i)
+#pragma unroll
+    for (int j = 0; j < DPT; ++j) dm[i][j] = 0.f;
+  float dres[DPT], dsg = 0.f;
+#pragma unroll
+  for (int e = 0; e < DPT; ++e) dres[e] = 0.f;
+  float wv[DPT];
+#pragma unroll
+  for (int e = 0; e < DPT; ++e) wv[e] = a.res_w[DPT * dg + e];
+
+  for (int r0 = 0; r0 < n_rows; r0 += RT) {
+    const int q = r0 + r;                 // row of the chunk: head g = q / tc, token i = q % tc
+    const bool live = q < n_rows;
+    const int g = live ? q / tc : 0, i = live ? q % tc : 0;
+    const int h = hkv * G + g;
+    const long long t = (long long)c * a.C + i;
+    const long long row = ((long long)b * a.H + h) * a.T + t;
+    // this thread's DPT columns of dy and y
+    float dyv[DPT], yv[DPT];
+#pragma unroll
+    for (int e = 0; e < DPT; ++e) { dyv[e] = 0.f; yv[e] = 0.f; }
+    if (live) {
+      const float* dyp = a.dy + (long long)b * a.dy_sb + t * a.dy_st + (long long)h * HD + DPT * dg;
+      const T* yp = reinterpret_cast<const T*>(a.y) + (long long)b * a.y_sb + t * a.y_st + (long long)h * HD + DPT * dg;
+#pragma unroll
+      for (int e = 0; e < DPT; ++e) { dyv[e] = dyp[e]; yv[e] = St<T>::ld(yp + e); }
+    }
+    if (!has_m) {
+      float dd = 0.f;
+#pragma unroll
+      for (int e = 0; e < DPT; ++e) dd += dyv[e] * yv[e];
+      dd = red16_sum(dd);
+      if (live && dg == 0) a.d_rows[row] = dd;
+      continue;
+    }
+    // q_raw row -> normalised
+    float qv[DPT];
+#pragma unroll
+    for (int e = 0; e < DPT; ++e) qv[e] = 0.f;
+    if (live) {
+      const T* qp = reinterpret_cast<const T*>(a.q_raw) + (long long)b * a.q_sb + (long long)h * a.q_sh + t * HD +
+                    DPT * dg;
+#pragma unroll
+      for (int e = 0; e < DPT; ++e) qv[e] = St<T>::ld(qp + e);
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < DPT; ++e) ss += qv[e] * qv[e];
+    ss = red16_sum(ss);
+    const float inv = 1.0f / fmaxf(sqrtf(ss), 1e-12f);
+    __syncthreads();   // the previous tile's qn / du reads are done
+#pragma unroll
+    for (int e = 0; e < DPT; ++e) sm.qn[r][DPT * dg + e] = qv[e] * inv;
+    if (dg == 0) sm.inv[r] = inv;
+    __syncthreads();
+    // u = qn . M for this thread's columns
+    float u[DPT];
+#pragma unroll
+    for (int e = 0; e < DPT; ++e) u[e] = 0.f;
+    for (int cc = 0; cc < HD; ++cc) {
+      const float x = sm.qn[r][cc];
+#pragma unroll
+      for (int e = 0; e < DPT; e += 4) {
+        const float4 mv = *reinterpret_cast<const float4*>(&sm.m[cc][DPT * dg + e]);
+        u[e] += x * mv.x; u[e + 1] += x * mv.y; u[e + 2] += x * mv.z; u[e + 3] += x * mv.w;
+      }
+    }
+    float ym[DPT], sq = 0.f;
+#pragma unroll
+    for (int e = 0; e < DPT; ++e) { ym[e] = u[e] * sg; sq += ym[e] * ym[e]; }
+    sq = red16_sum(sq);
+    const float rr = 1.0f / sqrtf(sq / (float)HD + a.eps);
+    const float eta = live ? a.eta[(long long)b * a.e_sb + (long long)h * a.e_sh + t] : 0.f;
+    float dd = 0.f, deta = 0.f, gdot = 0.f, gv[DPT];
+#pragma unroll
+    for (int e = 0; e < DPT; ++e) {
+      const float yn = ym[e] * rr * wv[e];
+      dd += dyv[e] * (yv[e] - eta * yn);
+      deta += dyv[e] * yn;
+      gv[e] = eta * dyv[e] * wv[e];
+      gdot += gv[e] * ym[e];
+      dres[e] += eta * dyv[e] * ym[e] * rr;
+    }
+    dd = red16_sum(dd);
+    deta = red16_sum(deta);
+    gdot = red16_sum(gdot);
+    if (live && dg == 0) {
+      a.d_rows[row] = dd;
+      a.d_eta[row] = deta;
+    }
+    float dsg_r = 0.f;
+#pragma unroll
+    for (int e = 0; e < DPT; ++e) {
+      const float dym = rr * gv[e] - ym[e] * rr * rr * rr * gdot / (float)HD;
+      dsg_r += dym * u[e];
+      sm.du[r][DPT * dg + e] = live ? dym * sg : 0.f;
+    }
+    dsg += red16_sum(dsg_r) * (dg == 0 && live ? 1.f : 0.f);
+    __syncthreads();
+    // dqn[cc] = sum_d du[d] * M[cc][d] for this thread's columns cc
+    float dqn[DPT];
+#pragma unroll
+    for (int e = 0; e < DPT; ++e) dqn[e] = 0.f;
+    for (int d = 0; d < HD; d += 4) {
+      const float4 dv4 = *reinterpret_cast<const float4*>(&sm.du[r][d]);
+#pragma unroll
+      for (int e = 0; e < DPT; ++e) {
+        const float4 mv = *reinterpret_cast<const float4*>(&sm.m[DPT * dg + e][d]);
+        dqn[e] += dv4.x * mv.x + dv4.y * mv.y + dv4.z * mv.z + dv4.w * mv.w;
+      }
+    }
+    float qd = 0.f;
+#pragma unroll
+    for (int e = 0; e < DPT; ++e) qd += sm.qn[r][DPT * dg + e] * dqn[e];
+    qd = red16_sum(qd);
+    if (live) {
+      float* o = a.d_q_raw + row * HD + DPT * dg;
+#pragma unroll
+      for (int e = 0; e < DPT; ++e) o[e] = (dqn[e] - sm.qn[r][DPT * dg + e] * qd) * inv;
+    }
+    // dM[cc][d] += sum over the tile's rows of qn[row][cc] * du[row][d]; this thread: cc in
+    // DPT * (tid >> 4) .. and d in DPT * dg ..
+    for (int rr2 = 0; rr2 < RT; ++rr2) {
+      float qa[DPT], db[DPT];
+#pragma unroll
+      for (int e = 0; e < DPT; ++e) {
+        qa[e] = sm.qn[rr2][DPT * r + e];
+        db[e] = sm.du[rr2][DPT * dg + e];
+      }
+#pragma unroll
+      for (int i2 = 0; i2 < DPT; ++i2)
+#pragma unroll
+        for (int j2 = 0; j2 < DPT; ++j2) dm[i2][j2] += qa[i2] * db[j2];
+    }
+  }
+  if (!has_m) return;
+  // rows past n_rows left zeros in qn / du, so they added nothing
+  float* dmo = a.d_m + ((long long)(c - 2) * a.B * a.HKV + bh) * HD * HD;
+#pragma unroll
+  for (int i2 = 0; i2 < DPT; ++i2)
+#pragma unroll
+    for (int j2 = 0; j2 < DPT; ++j2) dmo[(DPT * r + i2) * HD + DPT * dg + j2] = dm[i2][j2];
+  // res_w and gamma partials of this (bh, chunk)
+  __syncthreads();
+#pragma unroll
+  for (int e = 0; e < DPT; ++e) sm.part[r][DPT * dg + e] = dres[e];
+  __syncthreads();
+  const long long pc = (long long)bh * a.n_chunks + c;
+  if (tid < HD) {
+    float s = 0.f;
+    for (int k = 0; k < RT; ++k) s += sm.part[k][tid];
+    a.d_res_w[pc * HD + tid] = s;
+  }
+  __syncthreads();
+  if (dg == 0) sm.inv[r] = dsg;
+  __syncthreads();
+  if (tid == 0) {
+    float s = 0.f;
+    for (int k = 0; k < RT; ++k) s += sm.inv[k];
+    a.d_gamma[pc] = -s / sqrtf((float)HD);   // d/dgamma of (1 - gamma) / sqrt(HD)
+  }
+}
+
+template <typename T, int HD>
+static int launch(const b3_attn_bwd_args& a, hipStream_t st) {
+  const int n_chunks = a.n_chunks;
+  const int BH = a.B * a.HKV;
+  hipLaunchKernelGGL((readout_bwd_kernel<T, HD>), dim3(BH, n_chunks), dim3(NT), sizeof(RdSmem<HD>), st, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  hipLaunchKernelGGL((attn_bwd_dq_kernel<T, HD>), dim3(a.n_qtiles, a.B * a.H, n_chunks), dim3(NT),
+                     sizeof(DqSmem<HD>), st, a);
+  e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  const int max_blocks = 1 + (a.S + BK - 1) / BK + 2 * ((a.C + BK - 1) / BK);
+  hipLaunchKernelGGL((attn_bwd_dkv_kernel<T, HD>), dim3(max_blocks, BH, n_chunks), dim3(NT), sizeof(DkvSmem<HD>),
+                     st, a);
+  return (int)hipGetLastError();
+}
+
+template <typename T, int HD>
+static int set_smem() {
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_bwd_dq_kernel<T, HD>),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(DqSmem<HD>));
+  if (e == hipSuccess)
+    e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_bwd_dkv_kernel<T, HD>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(DkvSmem<HD>));
+  if (e == hipSuccess)
+    e = hipFuncSetAttribute(reinterpret_cast<const void*>(&readout_bwd_kernel<T, HD>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(RdSmem<HD>));
+  return (int)e;
+}
+
+}  // namespace bwd
+}  // namespace b3
+
+extern "C" int bolt3_attn_bwd(const b3_attn_bwd_args* a, void* stream) {
+  if (!a || a->B <= 0 || a->T <= 0 || a->HKV <= 0 || a->H % a->HKV != 0 || a->C <= 0 || a->S <= 0) return B3_ERR_ARG;
+  if (a->HD != 64 && a->HD != 128) return B3_ERR_UNSUPPORTED;
+  if (a->dtype != B3_F32 && a->dtype != B3_BF16) return B3_ERR_UNSUPPORTED;
+  const int n_chunks = (a->T + a->C - 1) / a->C;
+  if (a->n_chunks != n_chunks || a->n_qtiles != (a->C + b3::bwd::BQ - 1) / b3::bwd::BQ) return B3_ERR_ARG;
+  if (a->n_steps < 0 || a->n_steps > (n_chunks > 2 ? n_chunks - 2 : 0) || a->n_sinks < 0 || a->n_sinks > a->C)
+    return B3_ERR_ARG;
+  if (!a->q_rope || !a->q_raw || !a->win_k || !a->win_v || !a->eta || !a->gamma || !a->res_w || !a->y || !a->dy ||
+      !a->d_rows || !a->lse || !a->d_q_rope || !a->d_q_raw || !a->d_eta || !a->d_res_w || !a->d_gamma ||
+      !a->d_k_own || !a->d_v_own || !a->d_k_next || !a->d_v_next)
+    return B3_ERR_ARG;
+  if (a->n_steps > 0 && (!a->slot_k || !a->slot_v || !a->slot_bias || !a->m_res || !a->d_m || !a->d_bias ||
+                         !a->d_slot_k || !a->d_slot_v || (a->n_sinks > 0 && (!a->d_sink_k || !a->d_sink_v)) ||
+                         a->slot_step < (int64_t)a->B * a->HKV * a->S * a->HD))
+    return B3_ERR_ARG;
+  if (a->m_split && a->dtype != B3_BF16) return B3_ERR_ARG;
+  // 16-byte rows: every (b, h, t) row of the staged operands
+  const int64_t es = a->dtype == B3_BF16 ? 2 : 4;
+  if ((a->q_sb * es) % 16 || (a->q_sh * es) % 16 || (a->w_sb * es) % 16 || (a->w_sh * es) % 16 ||
+      (a->dy_sb * 4) % 16 || (a->dy_st * 4) % 16)
+    return B3_ERR_ARG;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  int rc;
+  if (a->dtype == B3_F32) {
+    rc = a->HD == 64 ? b3::bwd::set_smem<float, 64>() : b3::bwd::set_smem<float, 128>();
+    if (rc) return rc;
+    return a->HD == 64 ? b3::bwd::launch<float, 64>(*a, st) : b3::bwd::launch<float, 128>(*a, st);
+  }
+  rc = a->HD == 64 ? b3::bwd::set_smem<uint16_t, 64>() : b3::bwd::set_smem<uint16_t, 128>();
+  if (rc) return rc;
+  return a->HD == 64 ? b3::bwd::launch<uint16_t, 64>(*a, st) : b3::bwd::launch<uint16_t, 128>(*a, st);
+}

@@ -64,7 +64,6 @@ def replay_slots(log: torch.Tensor, pos: torch.Tensor, S: int, C: int, ns: int):
     dev = log.device
     mass = torch.ones(bh, S, device=dev)
     pm = torch.zeros(bh, S, device=dev)
-    rows = torch.arange(bh, device=dev)[:, None]
     nf = 0
     steps, masses, pms = [], [], []
     for i in range(n):
@@ -94,11 +93,9 @@ def replay_slots(log: torch.Tensor, pos: torch.Tensor, S: int, C: int, ns: int):
                        win=lg[:, LOG["win"], :kc] > 0.5, delta=lg[:, LOG["delta"], :l] > 0.5)
             pm = torch.where(hit, (mass * pm + p_acc) / new_m, pm)
             mass = torch.where(hit, new_m, mass)
-            w = rec["win"]
-            r_w = rows.expand_as(w)[w]
-            mass = mass.clone()
-            mass[r_w, rec["bots"][w]] = 1.0
-            pm[r_w, rec["bots"][w]] = p[rec["toks"][w]]
+            w, bots = rec["win"], rec["bots"]
+            mass = mass.scatter(1, bots, torch.where(w, torch.ones_like(p[rec["toks"]]), mass.gather(1, bots)))
+            pm = pm.scatter(1, bots, torch.where(w, p[rec["toks"]], pm.gather(1, bots)))
             steps.append(rec)
         masses.append(mass)
         pms.append(pm)
@@ -109,62 +106,30 @@ def chain_backward(steps, d_slot_k, d_slot_v, d_m, pms, inv_freq, kr, v, beta, g
     """Gradients of the consolidated tokens' keys (un-roped), values and beta, and of gamma,
     from the gradients of every step's slot snapshot (roped keys, values) and M_res, by the
     steps in reverse (vsa_lm/config/bolt3.py:121-166 for steady steps, :182-191 for fills).
-    kr, v: [bh, T, HD]; beta: [bh, T].  Returns (d_kr, d_v, d_beta, d_gamma)."""
+    kr, v: [bh, T, HD]; beta: [bh, T].  Returns (d_kr, d_v, d_beta, d_gamma).
+
+    Only two recursions are sequential over the steps: the slots' gradient (copied, scaled by
+    mass / new mass at merges, cleared at evictions) and M_res's, G_i = dM_i + A_{i+1} G_{i+1}
+    with A = gam I - kn^T diag(bsafe) kn.  Everything else is batched over all steps."""
     bh, T, HD = kr.shape
     S = d_slot_k.shape[2]
+    n = len(steps)
     dev = kr.device
     d_kr = torch.zeros(bh, T, HD, device=dev)
     d_v = torch.zeros(bh, T, HD, device=dev)
     d_beta = torch.zeros(bh, T, device=dev)
-    d_gam = torch.zeros(HKV, device=dev)
-    dak = torch.zeros(bh, S, HD, device=dev)
-    dav = torch.zeros(bh, S, HD, device=dev)
-    dM = torch.zeros(bh, HD, HD, device=dev)
-    rows = torch.arange(bh, device=dev)[:, None]
     gam_bh = gam.float().repeat(b).view(bh, 1, 1)
-    for i in range(len(steps) - 1, -1, -1):
-        st = steps[i]
-        # the snapshot of step i is read by the attention as rope(ak, pm) and av, and M_res by the readout
-        dak = dak + _rope_t(d_slot_k[i], pms[i][..., None] * inv_freq)
-        dav = dav + d_slot_v[i]
-        dM = dM + d_m[i]
-        t0, l = st["t0"], st["l"]
-        if st["kind"] == "fill":
-            nf, m, picked = st["nf"], st["m"], st["picked"]
-            r = rows.expand_as(picked)
-            d_kr[:, t0:t0 + l].index_put_((r, picked), dak[:, nf:nf + m], accumulate=True)
-            d_v[:, t0:t0 + l].index_put_((r, picked), dav[:, nf:nf + m], accumulate=True)
-            dak = dak.clone()
-            dav = dav.clone()
-            dak[:, nf:nf + m] = 0.0
-            dav[:, nf:nf + m] = 0.0
-            continue
-        # eviction: a winning pair's slot is the token's copy (vsa_lm/config/bolt3.py:145-150)
-        w = st["win"]
-        r_w, s_w, t_w = rows.expand_as(w)[w], st["bots"][w], st["toks"][w]
-        gk = d_kr[:, t0:t0 + l]
-        gv = d_v[:, t0:t0 + l]
-        gk.index_put_((r_w, t_w), dak[r_w, s_w], accumulate=True)
-        gv.index_put_((r_w, t_w), dav[r_w, s_w], accumulate=True)
-        dak = dak.clone()
-        dav = dav.clone()
-        dak[r_w, s_w] = 0.0
-        dav[r_w, s_w] = 0.0
-        # merge: ak <- (mass * ak + sum of merged keys) / (mass + count) (:125-136)
-        slot, new_m = st["slot"], st["new_m"]
-        coef = (st["merge"].float() / new_m.gather(1, slot))[..., None]
-        idx = slot[..., None].expand(-1, -1, HD)
-        gk += coef * dak.gather(1, idx)
-        gv += coef * dav.gather(1, idx)
-        keep = torch.where(st["hit"], st["mass"] / new_m, torch.ones_like(new_m))[..., None]
-        dak = dak * keep
-        dav = dav * keep
-        # delta rule: M <- gam M + kn^T (bsafe * (v - kn M)), bsafe = w / max(|kn kn^T| w, 1) (:157-166)
-        kri = kr[:, t0:t0 + l].float()
-        vi = v[:, t0:t0 + l].float()
-        dmask = st["delta"].float()
-        wv = beta[:, t0:t0 + l].float() * dmask
-        M0 = _snap_m(snap_m, i - 1, m_split, bh, HD) if i > 0 else torch.zeros(bh, HD, HD, device=dev)
+    steady = [i for i in range(n) if steps[i]["kind"] == "steady"]
+    # ---- batched over the steady steps: normalised keys, Gershgorin scales, residuals
+    if steady:
+        t0s = [steps[i]["t0"] for i in steady]
+        l = steps[steady[0]]["l"]
+        idx = torch.tensor(t0s, device=dev)[:, None] + torch.arange(l, device=dev)           # [ns, l]
+        kri = kr[:, idx].float().transpose(0, 1).reshape(-1, l, HD)                          # [ns*bh, l, HD]
+        vi = v[:, idx].float().transpose(0, 1).reshape(-1, l, HD)
+        dmask = torch.stack([steps[i]["delta"] for i in steady]).float().reshape(-1, l)
+        wv = beta[:, idx].float().transpose(0, 1).reshape(-1, l) * dmask
+        M0 = torch.stack([_snap_m(snap_m, i - 1, m_split, bh, HD) for i in steady]).reshape(-1, HD, HD)
         nrm = kri.norm(dim=-1, keepdim=True).clamp_min(1e-12)
         kn = kri / nrm
         P = torch.bmm(kn, kn.transpose(1, 2))
@@ -174,10 +139,70 @@ def chain_backward(steps, d_slot_k, d_slot_v, d_m, pms, inv_freq, kr, v, beta, g
         bs = wv / rs
         R = vi - torch.bmm(kn, M0)
         E = bs[..., None] * R
-        dE = torch.bmm(kn, dM)
-        d_kn = torch.bmm(E, dM.transpose(1, 2))
+        kn_s = kn.view(len(steady), bh, l, HD)
+        bs_s = bs.view(len(steady), bh, l, 1)
+    pos_of = {i: k for k, i in enumerate(steady)}
+    # ---- the two sequential recursions
+    slot_grad = _rope_t(d_slot_k, torch.stack(pms)[..., None] * inv_freq)    # [n, bh, S, HD]
+    dak = torch.zeros(bh, S, HD, device=dev)
+    dav = torch.zeros(bh, S, HD, device=dev)
+    cur = torch.zeros(bh, HD, HD, device=dev)
+    g_m = [None] * n
+    at_evict, at_merge = [None] * n, [None] * n
+    for i in range(n - 1, -1, -1):
+        st = steps[i]
+        cur = cur + d_m[i]
+        g_m[i] = cur
+        dak = dak + slot_grad[i]
+        dav = dav + d_slot_v[i]
+        if st["kind"] == "fill":
+            nf, m, picked = st["nf"], st["m"], st["picked"]
+            t0 = st["t0"]
+            pi = picked[..., None].expand(-1, -1, HD)
+            d_kr[:, t0:t0 + st["l"]].scatter_add_(1, pi, dak[:, nf:nf + m])
+            d_v[:, t0:t0 + st["l"]].scatter_add_(1, pi, dav[:, nf:nf + m])
+            keep = torch.ones(1, S, 1, device=dev)
+            keep[:, nf:nf + m] = 0.0
+            dak = dak * keep
+            dav = dav * keep
+            continue
+        at_evict[i] = (dak, dav)
+        # a winning pair's slot was overwritten by the token (vsa_lm/config/bolt3.py:145-150)
+        wmask = torch.zeros(bh, S, device=dev).scatter_(1, st["bots"], st["win"].float())
+        clear = (1.0 - wmask)[..., None]
+        dak = dak * clear
+        dav = dav * clear
+        at_merge[i] = (dak, dav)
+        # ak <- (mass * ak + merged keys) / (mass + count) (:125-136)
+        keep = torch.where(st["hit"], st["mass"] / st["new_m"], torch.ones_like(st["new_m"]))[..., None]
+        dak = dak * keep
+        dav = dav * keep
+        # M_res: dM_before = gam dM - kn^T (bsafe * (kn dM)) (:157-166)
+        k = pos_of[i]
+        cur = gam_bh * cur - torch.bmm(kn_s[k].transpose(1, 2), bs_s[k] * torch.bmm(kn_s[k], cur))
+    # ---- token gradients of the steady steps, batched
+    d_gam = torch.zeros(HKV, device=dev)
+    if steady:
+        for i in steady:
+            st = steps[i]
+            t0, l = st["t0"], st["l"]
+            wf = st["win"].float()[..., None]
+            bi = st["bots"][..., None].expand(-1, -1, HD)
+            ti = st["toks"][..., None].expand(-1, -1, HD)
+            dak_e, dav_e = at_evict[i]
+            d_kr[:, t0:t0 + l].scatter_add_(1, ti, dak_e.gather(1, bi) * wf)
+            d_v[:, t0:t0 + l].scatter_add_(1, ti, dav_e.gather(1, bi) * wf)
+        coef = torch.stack([steps[i]["merge"].float() / steps[i]["new_m"].gather(1, steps[i]["slot"])
+                            for i in steady])[..., None]                                    # [ns, bh, l, 1]
+        sidx = torch.stack([steps[i]["slot"] for i in steady])[..., None].expand(-1, -1, -1, HD)
+        dak_m = torch.stack([at_merge[i][0] for i in steady])
+        dav_m = torch.stack([at_merge[i][1] for i in steady])
+        gk = coef * dak_m.gather(2, sidx)                                                  # [ns, bh, l, HD]
+        gv = coef * dav_m.gather(2, sidx)
+        Gm = torch.stack([g_m[i] for i in steady]).reshape(-1, HD, HD)
+        dE = torch.bmm(kn, Gm)
+        d_kn = torch.bmm(E, Gm.transpose(1, 2))
         dR = bs[..., None] * dE
-        gv += dR
         d_kn -= torch.bmm(dR, M0.transpose(1, 2))
         d_bs = (dE * R).sum(-1)
         d_w = d_bs / rs
@@ -185,10 +210,13 @@ def chain_backward(steps, d_slot_k, d_slot_v, d_m, pms, inv_freq, kr, v, beta, g
         d_w += torch.bmm(G.transpose(1, 2), d_rs[..., None]).squeeze(-1)
         dP = (d_rs[..., None] * wv[:, None, :]) * torch.sign(P)
         d_kn += torch.bmm(dP + dP.transpose(1, 2), kn)
-        d_beta[:, t0:t0 + l] += d_w * dmask
-        d_gam += (dM * M0).sum(dim=(1, 2)).view(b, HKV).sum(0)
-        dM = gam_bh * dM - torch.bmm(kn.transpose(1, 2), dR)
-        gk += (d_kn - kn * (kn * d_kn).sum(-1, keepdim=True)) / nrm
+        d_kn = (d_kn - kn * (kn * d_kn).sum(-1, keepdim=True)) / nrm
+        gk = gk + d_kn.view(len(steady), bh, l, HD)
+        gv = gv + dR.view(len(steady), bh, l, HD)
+        d_kr[:, idx] += gk.transpose(0, 1)
+        d_v[:, idx] += gv.transpose(0, 1)
+        d_beta[:, idx] += (d_w * dmask).view(len(steady), bh, l).transpose(0, 1)
+        d_gam = (Gm * M0).sum(dim=(1, 2)).view(len(steady), b, HKV).sum(dim=(0, 1))
     return d_kr, d_v, d_beta, d_gam
 
 
@@ -244,12 +272,14 @@ def layer_backward(mod, x: torch.Tensor, tr: dict, d_out: torch.Tensor, dt: torc
     n_steps = max(0, n_chunks - 2)
     ns = min(mod.n_sinks, C)
     grads = {}
-    d_out = d_out.float()
-    xf = x.float()
+    # the projections' products run in the storage dtype, as the reference's linears do under
+    # autocast (fp32 storage: fp32 products)
+    W, _, side = mod._packed(dt, dev)
+    d_out = d_out.to(dt)
     # o_proj
     y = tr["y"]
-    grads["o_proj.weight"] = d_out.reshape(-1, D).t() @ y.reshape(-1, H * HD).float()
-    dy = (d_out @ mod.o_proj.weight.float()).contiguous()          # [b, T, H*HD]
+    grads["o_proj.weight"] = (d_out.reshape(-1, D).t() @ y.reshape(-1, H * HD)).float()
+    dy = (d_out @ side["wo"]).float().contiguous()                  # [b, T, H*HD]
     # attention and readout
     o = attn_backward(mod, tr, dy, dt, n_steps)
     pos = torch.arange(T, device=dev, dtype=torch.float32)
@@ -279,34 +309,41 @@ def layer_backward(mod, x: torch.Tensor, tr: dict, d_out: torch.Tensor, dt: torc
         d_gam += dg_c
     d_kraw += _rope_t(d_krope, ang_t)
     d_qraw = o["d_q_raw"] + _rope_t(o["d_q_rope"], ang_t)
-    # q / k RMSNorm (the statistic in fp32, vsa_lm/surgery.py:48-52) on the projections
-    lin_q = torch.nn.functional.linear(xf, mod.q_proj.weight.float(),
-                                       None if mod.q_proj.bias is None else mod.q_proj.bias.float())
-    lin_k = torch.nn.functional.linear(xf, mod.k_proj.weight.float(),
-                                       None if mod.k_proj.bias is None else mod.k_proj.bias.float())
     dq = d_qraw.transpose(1, 2)                                      # [b, T, H, HD]
     dk = d_kraw.transpose(1, 2)
     if mod.q_norm is not None:
+        # q / k RMSNorm (the statistic in fp32, vsa_lm/surgery.py:48-52) on the projections,
+        # recomputed by the forward's own products
+        lin_q = torch.nn.functional.linear(x, side["wq"], side["bq"]).float()
+        lin_k = torch.nn.functional.linear(x, side["wkv"], side["bkv"])[..., :HKV * HD].float()
         dq, grads["q_norm.weight"] = _rms_bwd(lin_q.view(b, T, H, HD), mod.q_norm.weight.float(), dq,
                                               float(mod.q_norm.eps))
-        dk, grads["k_norm.weight"] = _rms_bwd(lin_k.view(b, T, HKV, HD), mod.k_norm.weight.float(), dk,
+        dk, grads["k_norm.weight"] = _rms_bwd(lin_k.reshape(b, T, HKV, HD), mod.k_norm.weight.float(), dk,
                                               float(mod.k_norm.eps))
-    dq = dq.reshape(b * T, H * HD)
-    dk = dk.reshape(b * T, HKV * HD)
-    dvv = d_v.transpose(1, 2).reshape(b * T, HKV * HD)
     # gates: beta = sigmoid(.), eta = tanh(.) (vsa_lm/config/bolt3.py:198-199)
     bet = tr["beta"].float()
-    d_zb = (d_beta * bet * (1.0 - bet)).transpose(1, 2).reshape(b * T, HKV)
+    d_zb = (d_beta * bet * (1.0 - bet)).transpose(1, 2)
     eta = tr["eta"].float()
-    d_ze = (o["d_eta"] * (1.0 - eta * eta)).transpose(1, 2).reshape(b * T, H)
-    x2 = xf.reshape(b * T, D)
-    dx = torch.zeros(b * T, D, device=dev)
-    for name, lin, dz in (("q_proj", mod.q_proj, dq), ("k_proj", mod.k_proj, dk), ("v_proj", mod.v_proj, dvv),
-                          ("beta_proj", mod.beta_proj, d_zb), ("eta_proj", mod.eta_proj, d_ze)):
-        dx += dz @ lin.weight.float()
-        grads[f"{name}.weight"] = dz.t() @ x2
+    d_ze = (o["d_eta"] * (1.0 - eta * eta)).transpose(1, 2)
+    # one product each for dx and for the packed weight's gradient: rows q | k | v | beta | eta
+    parts = [dq.reshape(b, T, H * HD), dk.reshape(b, T, HKV * HD), d_v.transpose(1, 2).reshape(b, T, HKV * HD),
+             d_zb, d_ze]
+    widths = [t.shape[-1] for t in parts]
+    pad = W.shape[0] - sum(widths)
+    if pad:
+        parts.append(torch.zeros(b, T, pad, device=dev))
+    dz = torch.cat(parts, dim=-1).reshape(b * T, -1)
+    dz_s = dz.to(dt)
+    dx = (dz_s @ W).float()
+    dW = (dz_s.t() @ x.reshape(b * T, D)).float()
+    db = dz.sum(0)
+    off = 0
+    for name, lin, width in zip(("q_proj", "k_proj", "v_proj", "beta_proj", "eta_proj"),
+                                (mod.q_proj, mod.k_proj, mod.v_proj, mod.beta_proj, mod.eta_proj), widths):
+        grads[f"{name}.weight"] = dW[off:off + width]
         if lin.bias is not None:
-            grads[f"{name}.bias"] = dz.sum(0)
+            grads[f"{name}.bias"] = db[off:off + width]
+        off += width
     grads["kappa"] = d_kappa
     # gamma = clamp(0.999 * sigmoid(log_gamma), 1e-3, 0.999); clamp passes its bounds inclusive
     sg = torch.sigmoid(mod.log_gamma.detach().float().to(dev))

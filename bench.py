@@ -327,6 +327,8 @@ def main():
     ap.add_argument("--no-long", action="store_true", help="skip the consolidation-heavy B=1, T=65536 forward")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-e2e", action="store_true", help="skip the 36-layer end-to-end generation")
+    ap.add_argument("--no-tunableop", action="store_true",
+                    help="keep hipBLASLt's default solutions for the projection GEMMs (no TunableOp search)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run a plain elementwise copy of 256 MiB (fp32 negate) three times, the known-size "
                          "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
@@ -348,7 +350,17 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     _, mod = build_layer(dev)
+    if not args.no_tunableop:
+        # PyTorch's TunableOp times the hipBLASLt / rocBLAS solutions of each projection GEMM shape
+        # on its first call (in the warm-up forwards) and keeps the fastest; tuning stops after the
+        # prefill leg, so no later timed region pays for a search
+        import tempfile
+        torch.cuda.tunable.enable(True)
+        torch.cuda.tunable.tuning_enable(True)
+        torch.cuda.tunable.set_filename(os.path.join(tempfile.gettempdir(), "bolt3_bench_tunableop.csv"))
     ms, kern = bench_prefill(mod, dev, args.steps, args.warmup)
+    if not args.no_tunableop:
+        torch.cuda.tunable.tuning_enable(False)
     fl = prefill_flops(B, T)
     total = sum(fl.values())
     # entry points: algorithmic work per forward (FLOPs, or bytes for the head preparation)
@@ -403,6 +415,8 @@ def main():
         "whole_forward": dict(flops=total, tflops=round(total / (ms * 1e-3) / 1e12, 2),
                               frac_bf16_peak=round(total / (ms * 1e-3) / PEAK_BF16, 4)),
         "kernels": kernels,
+        "gemm_selection": "hipBLASLt default" if args.no_tunableop else
+                          "PyTorch TunableOp (hipBLASLt/rocBLAS solutions timed in the warm-up forwards)",
     }
     if not args.no_decode:
         out["decode"] = bench_decode(dev, args.decode_sets, args.decode_steps)

@@ -13,6 +13,9 @@ with fresh hidden ~N(0,1).  Several independent state sets are stepped in
 turn so that one round touches more than the 256 MB Infinity Cache; each set
 sees consecutive steps (consolidation every 128 of them).
 
+Backward (the heal trainer's step on one layer): forward + backward of the
+cfg2 layer with bf16 storage, gradients of x and every parameter.
+
 One JSON line on stdout.  ``value`` is prefill tokens/s of the whole forward
 (projections + HIP kernels + o_proj) with inputs resident in HBM.
 """
@@ -49,6 +52,59 @@ def prefill_flops(b, t, D=2560, H=32, HKV=8, HD=128, C=128):
     steady = max(0, n_chunks - 4)
     cons = b * HKV * steady * 2 * (5 * C * 128 * HD + 2 * C * HD * HD)
     return dict(proj=proj, attn=attn, readout=readout, consolidation=cons)
+
+
+PEAK_F32 = 157.3e12       # dense fp32 (vector FMA), FLOP/s
+
+
+def backward_flops(b, t, H=32, HD=128, C=128):
+    """Algorithmic FLOPs of bolt3_attn_bwd per forward: the attention's four gradient products
+    (dP = dO.V^T, dV = P^T.dO, dQ = dS.K, dK = dS^T.Q) over the forward's key rectangle, and the
+    readout's three HD x HD products per query row (q.M, dqn = du.M^T, dM += qn^T du)."""
+    n_chunks = (t + C - 1) // C
+    keys = sum(128 if c == 0 else 256 if c == 1 else 4 + 128 + 256 for c in range(n_chunks))
+    attn = 8 * b * H * C * HD * keys
+    readout = 3 * 2 * b * H * C * HD * HD * max(0, n_chunks - 2)
+    return attn + readout
+
+
+def bench_backward(mod, dev, steps, warmup):
+    """cfg2 forward + backward (the heal trainer's step on one layer): bf16 storage, gradients of
+    x and every parameter for loss = sum(y * g) with a seeded upstream g."""
+    import torch
+    from bolt3_amd import _abi
+    g = torch.Generator(device=dev).manual_seed(SEED + 2)
+    x = torch.randn(B, T, CFG["dim"], generator=g, device=dev).to(torch.bfloat16)
+    up = torch.randn(B, T, CFG["dim"], generator=g, device=dev).to(torch.bfloat16)
+
+    def step():
+        mod.zero_grad(set_to_none=True)
+        xg = x.clone().requires_grad_(True)
+        (mod(xg) * up).sum().backward()
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    _abi.set_timing(True)
+    for _ in range(steps):
+        step()
+    kt = _abi.timings()
+    _abi.set_timing(False)
+    mod.zero_grad(set_to_none=True)
+    ms = (t1 - t0) * 1e3 / steps
+    bwd = kt.get("bolt3_attn_bwd", [])
+    bwd_ms = sum(bwd) / max(1, len(bwd))
+    fl = backward_flops(B, T)
+    return dict(ms_per_forward_backward=round(ms, 3), tokens_per_s=round(B * T / (ms * 1e-3), 1),
+                attn_bwd_ms=round(bwd_ms, 3),
+                roofline=dict(bound="fp32 VALU", kernel="bolt3_attn_bwd", flops=fl,
+                              achieved=round(fl / (bwd_ms * 1e-3) / 1e12, 2), peak=PEAK_F32 / 1e12, unit="TFLOP/s",
+                              frac=round(fl / (bwd_ms * 1e-3) / PEAK_F32, 4)))
 
 
 def build_layer(dev):
@@ -327,6 +383,7 @@ def main():
     ap.add_argument("--no-long", action="store_true", help="skip the consolidation-heavy B=1, T=65536 forward")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-e2e", action="store_true", help="skip the 36-layer end-to-end generation")
+    ap.add_argument("--no-backward", action="store_true", help="skip the forward + backward leg")
     ap.add_argument("--no-tunableop", action="store_true",
                     help="keep hipBLASLt's default solutions for the projection GEMMs (no TunableOp search)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -418,6 +475,8 @@ def main():
         "gemm_selection": "hipBLASLt default" if args.no_tunableop else
                           "PyTorch TunableOp (hipBLASLt/rocBLAS solutions timed in the warm-up forwards)",
     }
+    if not args.no_backward:
+        out["backward"] = bench_backward(mod, dev, max(2, args.steps // 2), 2)
     if not args.no_decode:
         out["decode"] = bench_decode(dev, args.decode_sets, args.decode_steps)
     if not args.no_long:

@@ -418,6 +418,26 @@ int bolt3_decode_layer(const b3_decode_layer_args* a, void* stream);
 /* Workspace of bolt3_decode_layer's projections (besides dec.work): the fp32 partial products. */
 int64_t bolt3_decode_layer_workspace_bytes(int32_t B, int32_t d_model, int32_t n_in, int32_t hd_total, int32_t n_out);
 
+/*
+ * RMSNorm of rows: y = (x * rsqrt(mean(x^2) + eps)) * w with an fp32 statistic, each product
+ * rounded in fp32 and the result cast to the storage dtype (x's) once.  For the layers around
+ * the Bolt-3 path in a hybrid stack (block norms, final norm, the softmax layers' q/k norms).
+ * Replaces vsa_lm/surgery.py:48-52 (LlamaRMSNorm.forward) on the device.
+ */
+typedef struct {
+  int32_t dtype;              /* of x and y */
+  int64_t rows;
+  int32_t dim;                /* multiple of 8 */
+  const void* x;              /* [rows][x_row_stride], 16-byte aligned rows */
+  int64_t x_row_stride;
+  const void* w;              /* [dim] */
+  int32_t w_dtype;
+  void* y;                    /* [rows][y_row_stride] */
+  int64_t y_row_stride;
+  float eps;
+} b3_rms_norm_args;
+int bolt3_rms_norm(const b3_rms_norm_args* a, void* stream);
+
 /* Library identification: returns a static string (build flags, gfx target). */
 const char* bolt3_version(void);
 

@@ -82,7 +82,8 @@ def test_rejects_bad_arguments_without_gpu_work():
 
 STRUCTS = {"b3_heads_args": A.HeadsArgs, "b3_chain_args": A.ChainArgs, "b3_attn_args": A.AttnArgs,
            "b3_decode_args": A.DecodeArgs, "b3_decode_layer_args": A.DecodeLayerArgs,
-           "b3_slot_keys_args": A.SlotKeysArgs, "b3_attn_bwd_args": A.AttnBwdArgs}
+           "b3_slot_keys_args": A.SlotKeysArgs, "b3_attn_bwd_args": A.AttnBwdArgs,
+           "b3_rms_norm_args": A.RmsNormArgs}
 
 
 def _flat_fields(st, prefix=""):

@@ -125,12 +125,17 @@ class AttnBwdArgs(C.Structure):
     ]
 
 
+class RmsNormArgs(C.Structure):
+    _fields_ = [("dtype", i32), ("rows", i64), ("dim", i32), ("x", p), ("x_row_stride", i64), ("w", p),
+                ("w_dtype", i32), ("y", p), ("y_row_stride", i64), ("eps", f32)]
+
+
 CHAIN_NOALLOC_SCRATCH_BYTES = 4 << 20   # B3_CHAIN_NOALLOC_SCRATCH_BYTES
 
 EXPORTS = ("bolt3_attn_bwd", "bolt3_heads", "bolt3_chain", "bolt3_chain_noalloc", "bolt3_chain_workspace_bytes", "bolt3_chunk_attn",
            "bolt3_decode",
            "bolt3_decode_layer", "bolt3_decode_layer_workspace_bytes", "bolt3_decode_workspace_bytes",
-           "bolt3_slot_keys", "bolt3_step_advance", "bolt3_version", "bolt3_wait_count")
+           "bolt3_rms_norm", "bolt3_slot_keys", "bolt3_step_advance", "bolt3_version", "bolt3_wait_count")
 
 _lib = None
 
@@ -147,7 +152,8 @@ def load():
     for name, st in (("bolt3_heads", HeadsArgs), ("bolt3_chain", ChainArgs), ("bolt3_chain_noalloc", ChainArgs),
                      ("bolt3_chunk_attn", AttnArgs),
                      ("bolt3_decode", DecodeArgs), ("bolt3_decode_layer", DecodeLayerArgs),
-                     ("bolt3_slot_keys", SlotKeysArgs), ("bolt3_attn_bwd", AttnBwdArgs)):
+                     ("bolt3_slot_keys", SlotKeysArgs), ("bolt3_attn_bwd", AttnBwdArgs),
+                     ("bolt3_rms_norm", RmsNormArgs)):
         fn = getattr(lib, name)
         fn.argtypes = [C.POINTER(st), p]
         fn.restype = C.c_int

@@ -315,7 +315,12 @@ class Bolt3Attn(nn.Module):
             return self._forward_hip(x.to(dt), _trace)
 
     @torch.no_grad()
-    def _forward_hip(self, x: torch.Tensor, trace: dict | None) -> torch.Tensor:
+    def _forward_hip(self, x: torch.Tensor, trace: dict | None, score_round: int = 1,
+                     keep_log: bool = True) -> torch.Tensor:
+        """The forward on the HIP path.  ``trace`` (a dict) receives the head tensors, the chain's
+        final state and snapshots, the attention output and (keep_log) the decision log.
+        score_round 1: q.k rounded to the storage dtype before scaling (the forward); 0: fp32
+        scores (the decoder's step, used by its prefill)."""
         b, T, _ = x.shape
         dt, dev = x.dtype, x.device
         H, HKV, HD, S, C = self.H, self.HKV, self.HD, self.S, self.C
@@ -366,7 +371,7 @@ class Bolt3Attn(nn.Module):
                      torch.empty(n_cons, bh, HD, HD, device=dev))
             ns = min(self.n_sinks, C)
             log = None
-            if trace is not None:
+            if trace is not None and keep_log:
                 log = torch.zeros(n_cons, bh, A.LOG_ROWS, A.LOG_COLS, device=dev)
             works = [torch.empty(A.chain_workspace_bytes(dt, b, HKV, HD, S, s1 - s0), dtype=torch.uint8, device=dev)
                      for s0, s1 in groups]
@@ -402,7 +407,7 @@ class Bolt3Attn(nn.Module):
                     nf = min(S, nf + (C - ns if i == 0 else C))
             if trace is not None:
                 trace.update(state=st, m_res=m_res, snap_k=snaps[0], snap_v=snaps[1], snap_bias=snaps[2],
-                             snap_m=snaps[3], log=log)
+                             snap_m=snaps[3], log=log, n_filled=nf)
         if first_started is not None:
             _wait_started(dev, ctr[0], first_started)
         lin_q = F.linear(x, side["wq"], side["bq"])
@@ -418,7 +423,7 @@ class Bolt3Attn(nn.Module):
         K = H * HD
         a = A.AttnArgs()
         a.dtype, a.B, a.H, a.HKV, a.HD, a.S, a.C, a.n_sinks = A.dtype_code(dt), b, H, HKV, HD, S, C, self.n_sinks
-        a.mode, a.n_q, a.score_round = 0, T, 1
+        a.mode, a.n_q, a.score_round = 0, T, int(score_round)
         a.q_rope, a.q_raw, a.q_sb, a.q_sh = q_rope.data_ptr(), q_raw.data_ptr(), q_rope.stride(0), q_rope.stride(1)
         a.eta, a.e_sb, a.e_sh = eta.data_ptr(), eta.stride(0), eta.stride(1)
         a.win_k, a.win_v, a.w_sb, a.w_sh = k_rope.data_ptr(), v.data_ptr(), k_rope.stride(0), k_rope.stride(1)

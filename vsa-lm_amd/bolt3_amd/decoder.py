@@ -540,6 +540,52 @@ class Bolt3Decoder:
             self._consolidate(ly, st, m_state, gam, side, record)
         return out
 
+    def _bolt3_prefill(self, ly: Bolt3Attn, h: torch.Tensor, m_state: torch.Tensor, st: Bolt3LayerState):
+        """A whole prompt through one Bolt-3 layer from an empty state, as the forward computes it
+        (every chunk's attention at once, the chain in step groups beside it) with the decoder
+        step's fp32 scores; then the state the reference's chunk-by-chunk prefill leaves
+        (vsa_lm/config/bolt3.py:452-457): with n = T // C full chunks, chunks 0 .. n-2 consolidated,
+        chunk n-1 as prev, the remaining tokens as cur.  The forward consolidates ceil(T/C) - 2
+        chunks, one fewer when C divides T; that step runs here.  Returns the layer output."""
+        B, T, _ = h.shape
+        C, S, HD, HKV = ly.C, ly.S, ly.HD, ly.HKV
+        dt, dev = h.dtype, h.device
+        tr = {}
+        out = ly._forward_hip(h, tr, score_round=0, keep_log=False)
+        side = ly._packed(dt, dev)[2]
+        gam = side["gamma"]
+        n_full = T // C
+        n_steps = max(0, (T + C - 1) // C - 2)
+        ns = min(ly.n_sinks, C)
+        k_raw, k_rope, v, beta, pos = tr["k_raw"], tr["k_rope"], tr["v"], tr["beta"], tr["pos"]
+        if n_steps > 0:
+            slots, m_res, nf = tr["state"], tr["m_res"], tr["n_filled"]
+        else:
+            slots, m_res, nf = ly._empty_slots(B * HKV, dt, dev), torch.zeros(B * HKV, HD, HD, device=dev), 0
+        if T % C == 0 and n_full >= 2:
+            i = n_full - 2                       # the step the forward leaves out
+            off, l = (ns, C - ns) if i == 0 else (0, C)
+            esz = k_raw.element_size()
+            tok = i * C
+            ly._chain(dt, dev, B, k_raw.data_ptr() + tok * HD * esz, k_rope.data_ptr() + tok * HD * esz,
+                      v.data_ptr() + tok * HD * esz, T * HD, pos.data_ptr() + tok * 4, beta.data_ptr() + tok * 4,
+                      T, 1, off, l, C, C, nf, slots, m_res, gam, side, kp_exact=True)
+            nf = min(S, nf + l)
+            n_steps += 1
+        m_state.copy_(m_res.view_as(m_state))
+        # the reference's kv_caches form, loaded like any saved state
+        d = dict.fromkeys(Bolt3LayerState.KEYS)
+        d["n_filled"] = nf if n_steps > 0 else 0
+        if n_steps > 0:
+            d.update(ak=slots["ak"], av=slots["av"], mass=slots["mass"], util=slots["util"], pm=slots["pm"],
+                     act=slots["act"].bool(), sink_k=k_rope[:, :, :ns], sink_v=v[:, :, :ns])
+        for pre, (t0, t1) in (("prev_", ((n_full - 1) * C, n_full * C)), ("cur_", (n_full * C, T))):
+            if t1 > t0 >= 0:
+                d.update({pre + "kr": k_raw[:, :, t0:t1], pre + "kp": k_rope[:, :, t0:t1], pre + "v": v[:, :, t0:t1],
+                          pre + "b": beta[:, :, t0:t1], pre + "pos": pos[t0:t1].view(1, 1, -1)})
+        st.load_dict(d)
+        return out
+
     def _consolidate(self, ly: Bolt3Attn, st: Bolt3LayerState, m_state, gam, side, record=None):
         ps, pl = st.prev
         if pl > 0:
@@ -659,11 +705,16 @@ class Bolt3Decoder:
         q, k = ly.rope(q, pos_start=pos_start), ly.rope(k, pos_start=pos_start)
         n_old = cache.n
         keys, vals = cache.append(k, v)
-        visible = None
-        if t > 1:
-            visible = torch.ones(t, n_old + t, dtype=torch.bool, device=h.device).tril(diagonal=n_old)
-        y = F.scaled_dot_product_attention(q, keys.to(q.dtype), vals.to(q.dtype), attn_mask=visible,
-                                           enable_gqa=ly.G > 1)
+        if t > 1 and n_old == 0:
+            # nothing cached: plain causal attention, which keeps torch on its fused kernel
+            y = F.scaled_dot_product_attention(q, keys.to(q.dtype), vals.to(q.dtype), is_causal=True,
+                                               enable_gqa=ly.G > 1)
+        else:
+            visible = None
+            if t > 1:
+                visible = torch.ones(t, n_old + t, dtype=torch.bool, device=h.device).tril(diagonal=n_old)
+            y = F.scaled_dot_product_attention(q, keys.to(q.dtype), vals.to(q.dtype), attn_mask=visible,
+                                               enable_gqa=ly.G > 1)
         return ly.o_proj(y.transpose(1, 2).reshape(b, t, ly.H * ly.HD))
 
     # ------------------------------------------------------------ model-level API
@@ -697,10 +748,26 @@ class Bolt3Decoder:
 
     @torch.no_grad()
     def prefill(self, ids: torch.Tensor, max_kv_len: int = 4096):
+        """The prompt through every layer (vsa_lm/config/bolt3.py:450-457).  The reference steps it
+        chunk by chunk through all layers; here each layer takes the whole prompt at once (a layer's
+        output for a chunk depends only on that layer's inputs up to the chunk, so the order of the
+        two loops does not change what is computed): the Bolt-3 layers through the forward's
+        kernels (_bolt3_prefill), the anchors through causal attention over the prompt.  Returns
+        (normed hidden states of the last chunk's tokens, states, kv_caches), as the reference."""
         b, t = ids.shape
         states, kv = self.blank_state(self.model, b, ids.device, max_kv_len=max(max_kv_len, t + 1024))
-        h, _ = self._feed(ids, 0, states, kv)
-        return h, states, kv
+        m = self.model
+        with torch.autocast(ids.device.type, enabled=False):
+            x = m.embed_tokens(ids)
+            for li, blk in enumerate(m.blocks):
+                h = blk.norm1(x)
+                if hasattr(blk, "vsa"):
+                    x = x + self._bolt3_prefill(blk.vsa, h, states[li], kv[li])
+                else:
+                    x = x + self._anchor_layer(blk.attn, h, 0, kv[li])
+                x = x + blk.mlp(blk.norm2(x))
+            s_last = ((t - 1) // self.C) * self.C
+            return m.norm(x[:, s_last:]), states, kv
 
     @torch.no_grad()
     def generate_batch(self, ids: torch.Tensor, max_new_tokens: int, temperature: float = 0.6, top_k: int = 40,

@@ -4,8 +4,9 @@
 (``weight``; non-persistent buffer ``inv_freq``) so checkpoints load
 unchanged.  ``SoftmaxAttn``, ``MLP`` and ``HybridLM`` are the caller side of the
 path (the softmax-anchor layers and the model container that
-``Bolt3Decoder`` walks); they run as plain PyTorch ops on the device and are
-not part of the HIP path.
+``Bolt3Decoder`` walks); they run as PyTorch ops on the device, except
+``RMSNorm``, whose device forward is the library's ``bolt3_rms_norm`` (one pass
+per row instead of the torch ops' six; CPU tensors keep the torch ops).
   RMSNorm      -- vsa_lm/surgery.py:43-53
   rope_inv_freq-- vsa_lm/surgery.py:56-72
   RoPE         -- vsa_lm/surgery.py:80-93
@@ -29,9 +30,35 @@ class RMSNorm(nn.Module):
         self.eps = eps
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if x.is_cuda and _hip_norm_ok(x, self.weight):
+            return _rms_norm_hip(x, self.weight, self.eps)
         xf = x.float()
         xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)
         return (xf * self.weight.float()).to(x.dtype)
+
+
+def _hip_norm_ok(x: torch.Tensor, w: torch.Tensor) -> bool:
+    """bolt3_rms_norm takes the device forward when nothing asks for a gradient (it has no
+    backward) and the shape and dtypes are its own; CPU tensors keep the torch ops."""
+    needs_grad = torch.is_grad_enabled() and (x.requires_grad or w.requires_grad)
+    return (not needs_grad and x.dtype in (torch.float32, torch.bfloat16) and
+            w.dtype in (torch.float32, torch.bfloat16) and x.shape[-1] % 8 == 0 and x.numel() > 0)
+
+
+def _rms_norm_hip(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+    from . import _abi as A
+    D = x.shape[-1]
+    x2 = x.reshape(-1, D)
+    if x2.stride(-1) != 1 or (x2.stride(0) * x2.element_size()) % 16 or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    y = torch.empty(x2.shape, dtype=x.dtype, device=x.device)
+    wc = w.detach().contiguous()
+    a = A.RmsNormArgs()
+    a.dtype, a.rows, a.dim = A.dtype_code(x.dtype), x2.shape[0], D
+    a.x, a.x_row_stride, a.w, a.w_dtype = x2.data_ptr(), x2.stride(0), wc.data_ptr(), A.dtype_code(wc.dtype)
+    a.y, a.y_row_stride, a.eps = y.data_ptr(), y.stride(0), float(eps)
+    A.call("bolt3_rms_norm", a, x.device)
+    return y.view(x.shape)
 
 
 def rope_inv_freq(head_dim: int, theta: float, rope_scaling: dict | None = None) -> torch.Tensor:

@@ -946,27 +946,41 @@ __global__ void __launch_bounds__(64 * NW) attn_fwd2_kernel(b3_attn_args a, int 
   // softmax step and O^T += V^T P^T for block f in stage st, scores sc
   auto attend = [&](f32x16 sc, const FwdBlock& f, int st) {
     const uint16_t* sV = sm.ring[st][1];
-    // scores in log2 units: round_bf(q.k) * scale*log2(e) (+ slot bias * log2(e)), one FMA
+    // scores in log2 units: round_bf(q.k) * scale*log2(e) (+ slot bias * log2(e)), one FMA; the
+    // rounding is skipped when score_round is 0 (fp32 scores, as the decoder step computes them)
     if (f.bias) {
       fx4 b4[4];
 #pragma unroll
       for (int r4 = 0; r4 < 4; ++r4) b4[r4] = lds_read_f4_nowait(f.bias + 8 * r4 + 4 * h);
       lds_wait4(b4[0], b4[1], b4[2], b4[3]);
+      if (a.score_round) {
 #pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4) {
-        const uint32_t u0 = pack_bf2(sc[4 * r4], sc[4 * r4 + 1]), u1 = pack_bf2(sc[4 * r4 + 2], sc[4 * r4 + 3]);
-        sc[4 * r4] = fmaf(bf_lo(u0), sL, b4[r4].x);
-        sc[4 * r4 + 1] = fmaf(bf_hi(u0), sL, b4[r4].y);
-        sc[4 * r4 + 2] = fmaf(bf_lo(u1), sL, b4[r4].z);
-        sc[4 * r4 + 3] = fmaf(bf_hi(u1), sL, b4[r4].w);
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const uint32_t u0 = pack_bf2(sc[4 * r4], sc[4 * r4 + 1]), u1 = pack_bf2(sc[4 * r4 + 2], sc[4 * r4 + 3]);
+          sc[4 * r4] = fmaf(bf_lo(u0), sL, b4[r4].x);
+          sc[4 * r4 + 1] = fmaf(bf_hi(u0), sL, b4[r4].y);
+          sc[4 * r4 + 2] = fmaf(bf_lo(u1), sL, b4[r4].z);
+          sc[4 * r4 + 3] = fmaf(bf_hi(u1), sL, b4[r4].w);
+        }
+      } else {
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          sc[4 * r4] = fmaf(sc[4 * r4], sL, b4[r4].x);
+          sc[4 * r4 + 1] = fmaf(sc[4 * r4 + 1], sL, b4[r4].y);
+          sc[4 * r4 + 2] = fmaf(sc[4 * r4 + 2], sL, b4[r4].z);
+          sc[4 * r4 + 3] = fmaf(sc[4 * r4 + 3], sL, b4[r4].w);
+        }
       }
-    } else {
+    } else if (a.score_round) {
 #pragma unroll
       for (int r = 0; r < 16; r += 2) {
         const uint32_t u = pack_bf2(sc[r], sc[r + 1]);
         sc[r] = bf_lo(u) * sL;
         sc[r + 1] = bf_hi(u) * sL;
       }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sc[r] *= sL;
     }
     // masks: rows past the valid keys, and the causal diagonal (a current-chunk block wholly
     // before the wave's first query needs none)

@@ -558,3 +558,29 @@ def test_consolidation_heavy_long_prefill(gpu):
     with torch.no_grad():
         y_ref = O.forward(O.Bolt3Params.from_module(mod), x[:, :256], ties="torch")
     _check_out(y_pre[:, :256].cpu(), y_ref, torch.bfloat16, "consolidation-heavy first chunks vs oracle")
+
+
+def test_forward_under_autocast_matches_bf16_oracle(gpu):
+    """An fp32 module called under bf16 autocast (the reference's eval, benchmark and heal paths
+    run it so) stores its activations in bf16, as the reference's autocast linears produce them.
+    With every parameter and input exactly representable in bf16, autocast's weight casts are
+    exact, so the bf16 oracle (the reference's CPU semantics on the bf16-cast module) is the
+    expected result: compared over the first chunks (before any consolidation, where no
+    near-tie can move a decision) and, with bf16 tolerance, over the whole sequence."""
+    import copy
+    import recipes
+    from bolt3_amd import Bolt3Attn
+    cfg = dict(dim=256, num_heads=8, num_kv_heads=2, head_dim=128, rope_theta=1e6, eps=1e-6, qk_norm=True)
+    mod = recipes.init_module(Bolt3Attn(cfg), 41, nondefault=True)
+    with torch.no_grad():
+        for prm in mod.parameters():
+            prm.copy_(prm.to(torch.bfloat16).float())
+    x = recipes.hidden(41, 2, 640, 256).to(torch.bfloat16).float()
+    mod_bf = copy.deepcopy(mod).to(torch.bfloat16)
+    with torch.no_grad():
+        ref = O.forward(O.Bolt3Params.from_module(mod_bf), x.to(torch.bfloat16))
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            y = copy.deepcopy(mod).to(gpu)(x.to(gpu))
+    assert y.dtype == torch.bfloat16
+    _check_out(y[:, :256].float().cpu(), ref[:, :256].float(), torch.bfloat16, "autocast, first chunks")
+    _check_out(y.float().cpu(), ref.float(), torch.bfloat16, "autocast, whole sequence")

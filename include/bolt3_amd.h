@@ -272,7 +272,7 @@ int bolt3_chunk_attn(const b3_attn_args* a, void* stream);
 typedef struct {
   int32_t dtype, B, T, H, HKV, HD, S, C, n_sinks;
   int32_t n_chunks;           /* ceil(T / C) */
-  int32_t n_qtiles;           /* ceil(C / 64): query tiles per chunk */
+  int32_t n_qtiles;           /* ceil(C / 32): query tiles per chunk */
   int32_t n_steps;            /* consolidation steps of the forward: chunk c >= 2 reads step c - 2 */
   int32_t score_round;        /* as in b3_attn_args (1 for the forward) */
   const void* q_rope;         /* (b, h, t, d) at + b*q_sb + h*q_sh + t*HD + d, storage dtype */

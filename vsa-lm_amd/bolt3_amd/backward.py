@@ -228,7 +228,7 @@ def attn_backward(mod, tr: dict, dy: torch.Tensor, dt: torch.dtype, n_steps: int
     dev = q_rope.device
     bh = b * HKV
     n_chunks = (T + C - 1) // C
-    n_qt = (C + 63) // 64
+    n_qt = (C + 31) // 32
     ns = min(mod.n_sinks, C)
     f32 = dict(device=dev, dtype=torch.float32)
     o = dict(d_rows=torch.empty(b, H, T, **f32), lse=torch.empty(b, H, T, **f32),

@@ -108,7 +108,9 @@ __device__ __forceinline__ float red16_max(float x) {
   return x;
 }
 
-// s[i][j] = sum_d A[4 rg + i][d] * B[2 cg + j][d] (A: BQ rows, B: BK rows, both fp32 in LDS)
+// s[i][j] = sum_d A[4 rg + i][d] * B[cg + 16 j][d] (A: BQ rows, B: BK rows, both fp32 in LDS).
+// The 16 lanes of a row group read B rows one row stride apart (132 floats = 4 banks): the
+// two-pass minimum for 16-byte reads
 template <int HD>
 __device__ __forceinline__ void tile_dot(float (&s)[4][2], const float* A, const float* B, int ls, int rg, int cg) {
 #pragma unroll
@@ -119,7 +121,7 @@ __device__ __forceinline__ void tile_dot(float (&s)[4][2], const float* A, const
 #pragma unroll
     for (int i = 0; i < 4; ++i) av[i] = *reinterpret_cast<const float4*>(A + (4 * rg + i) * ls + d);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) bv[j] = *reinterpret_cast<const float4*>(B + (2 * cg + j) * ls + d);
+    for (int j = 0; j < 2; ++j) bv[j] = *reinterpret_cast<const float4*>(B + (cg + 16 * j) * ls + d);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -191,8 +193,8 @@ __global__ void __launch_bounds__(NT) attn_bwd_dq_kernel(b3_attn_bwd_args a) {
       tile_dot<HD>(s, &sm.q[0][0], &sm.k[0][0], LS, rg, cg);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float x0 = score_of<T>(a, s[i][0], f, j0, 2 * cg, q0 + 4 * rg + i, scale);
-        const float x1 = score_of<T>(a, s[i][1], f, j0, 2 * cg + 1, q0 + 4 * rg + i, scale);
+        const float x0 = score_of<T>(a, s[i][0], f, j0, cg, q0 + 4 * rg + i, scale);
+        const float x1 = score_of<T>(a, s[i][1], f, j0, cg + 16, q0 + 4 * rg + i, scale);
         const float bm = red16_max(fmaxf(x0, x1));
         const float mn = fmaxf(m[i], bm);
         if (mn == -INFINITY) continue;
@@ -233,10 +235,10 @@ __global__ void __launch_bounds__(NT) attn_bwd_dq_kernel(b3_attn_bwd_args a) {
       for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-          const float x = score_of<T>(a, s[i][j], f, j0, 2 * cg + j, q0 + 4 * rg + i, scale);
+          const float x = score_of<T>(a, s[i][j], f, j0, cg + 16 * j, q0 + 4 * rg + i, scale);
           const bool live = 4 * rg + i < nq && x != -INFINITY;
           const float p = live ? expf(x - lse[i]) : 0.f;
-          sm.ds[4 * rg + i][2 * cg + j] = live ? p * (dp[i][j] - drow[i]) : 0.f;
+          sm.ds[4 * rg + i][cg + 16 * j] = live ? p * (dp[i][j] - drow[i]) : 0.f;
         }
       __syncthreads();
       if (f.kind == 1 && tid < BK && j0 + tid < f.len) {
@@ -313,7 +315,8 @@ __global__ void __launch_bounds__(NT) attn_bwd_dkv_kernel(b3_attn_bwd_args a) {
   const int nk = min(BK, f.len - j0);
   stage_rows<T, HD>(&sm.k[0][0], LS, reinterpret_cast<const T*>(f.k) + (long long)j0 * HD, HD, BK, nk, tid);
   stage_rows<T, HD>(&sm.v[0][0], LS, reinterpret_cast<const T*>(f.v) + (long long)j0 * HD, HD, BK, nk, tid);
-  // accumulators: keys 2 jg + jj, columns DPT dg + e
+  // accumulators: keys jg + 16 jj (rows of pt / dst one row stride apart across the lanes),
+  // columns DPT dg + e
   const int jg = tid >> 4, dg = tid & 15;
   float dk[2][DPT], dv[2][DPT];
 #pragma unroll
@@ -346,21 +349,21 @@ __global__ void __launch_bounds__(NT) attn_bwd_dkv_kernel(b3_attn_bwd_args a) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
           const int r = 4 * rg + i;
-          const float x = score_of<T>(a, s[i][j], f, j0, 2 * cg + j, q0 + r, scale);
+          const float x = score_of<T>(a, s[i][j], f, j0, cg + 16 * j, q0 + r, scale);
           const bool live = r < nq && x != -INFINITY;
           const float p = live ? expf(x - sm.lse[r]) : 0.f;
-          sm.pt[2 * cg + j][r] = p;
-          sm.dst[2 * cg + j][r] = live ? p * (dp[i][j] - sm.drow[r]) : 0.f;
+          sm.pt[cg + 16 * j][r] = p;
+          sm.dst[cg + 16 * j][r] = live ? p * (dp[i][j] - sm.drow[r]) : 0.f;
         }
       __syncthreads();
-      // dv[jj][e] += sum_r pt[2 jg + jj][r] * dout[r][DPT dg + e]; dk likewise with dst and q
+      // dv[jj][e] += sum_r pt[jg + 16 jj][r] * dout[r][DPT dg + e]; dk likewise with dst and q
 #pragma unroll 2
       for (int r = 0; r < BQ; r += 4) {
         float4 pv[2], dsv[2];
 #pragma unroll
         for (int jj = 0; jj < 2; ++jj) {
-          pv[jj] = *reinterpret_cast<const float4*>(&sm.pt[2 * jg + jj][r]);
-          dsv[jj] = *reinterpret_cast<const float4*>(&sm.dst[2 * jg + jj][r]);
+          pv[jj] = *reinterpret_cast<const float4*>(&sm.pt[jg + 16 * jj][r]);
+          dsv[jj] = *reinterpret_cast<const float4*>(&sm.dst[jg + 16 * jj][r]);
         }
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
@@ -404,7 +407,7 @@ __global__ void __launch_bounds__(NT) attn_bwd_dkv_kernel(b3_attn_bwd_args a) {
   }
 #pragma unroll
   for (int jj = 0; jj < 2; ++jj) {
-    const int j = 2 * jg + jj;
+    const int j = jg + 16 * jj;
     if (j >= nk) continue;
 #pragma unroll
     for (int e = 0; e < DPT; e += 4) {
@@ -414,6 +417,363 @@ __global__ void __launch_bounds__(NT) attn_bwd_dkv_kernel(b3_attn_bwd_args a) {
           make_float4(dv[jj][e], dv[jj][e + 1], dv[jj][e + 2], dv[jj][e + 3]);
     }
   }
+}
+
+// ---------------------------------------------------------------- bf16 storage: MFMA kernels
+//
+// The same gradients for bf16 storage on v_mfma_f32_32x32x16_bf16 with fp32 accumulation, one
+// wavefront per workgroup.  The bf16 operands are the stored q, k, v (exact) and dO, P, dS
+// rounded to bf16 where they enter a product, as the reference's autocast backward rounds them.
+// Layouts follow the forward: a 32x32 product tile holds, in lane l, column l % 32 and rows
+// d_row(l, r); the A operand row l % 32 and the B operand column l % 32 carry the K elements
+// 8 * (l / 32) .. + 7.  A product whose K dimension is the rows of an earlier accumulator (dQ^T =
+// K^T dS^T, dK^T = Q^T dS, dV^T = dO^T P) takes that accumulator as its B operand in the
+// accumulator's own row order and reads the A operand with ds_read_b64_tr_b16 from a row-major
+// tile in LDS whose 16-byte pieces p of row r sit at p ^ (r % (HD/8)).
+constexpr float L2E = 1.4426950408889634f;
+
+__device__ __forceinline__ u16x4 lds_read_tr(const uint16_t* p) {
+  u16x4 r;
+  const uint32_t addr = (uint32_t)(size_t)((__attribute__((address_space(3))) const uint16_t*)p);
+  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r) : "v"(addr) : "memory");
+  return r;
+}
+__device__ __forceinline__ void lds_wait_tr(u16x4* r) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7]));
+}
+
+// the transposed operand of tile `t` ([32 rows][HD], swizzled): rows are the K index (key or
+// query), the result's row m is feature 32 db + lane % 32; K chunk kc covers tile rows
+// 16 kc + {4h..4h+3, 8+4h..8+4h+3} in the order of an accumulator's rows
+template <int HD>
+__device__ __forceinline__ u16x8 tr_operand(const uint16_t* t, int db, int kc, int lane) {
+  constexpr int NP = HD / 8;
+  const int jv = lane & 15, grp = lane >> 4, h = lane >> 5;
+  const int f0 = 32 * db + 16 * (grp & 1) + 4 * (jv & 3);
+  const int r1 = 16 * kc + 4 * h + (jv >> 2), r2 = r1 + 8;
+  u16x4 v[8];
+  v[0] = lds_read_tr(t + r1 * HD + 8 * ((f0 >> 3) ^ (r1 % NP)) + (f0 & 7));
+  v[1] = lds_read_tr(t + r2 * HD + 8 * ((f0 >> 3) ^ (r2 % NP)) + (f0 & 7));
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v[0]), "+v"(v[1]));
+  u16x8 a;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    a[e] = v[0][e];
+    a[4 + e] = v[1][e];
+  }
+  return a;
+}
+
+// accumulator values as the B operand of K chunk kc (rows 8 kc .. 8 kc + 7 of the 16), bf16
+__device__ __forceinline__ u16x8 acc_operand(const f32x16& v, int kc) {
+  u16x8 b;
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) {
+    const uint32_t u = pack_bf2(v[8 * kc + e], v[8 * kc + e + 1]);
+    b[e] = (uint16_t)(u & 0xffffu);
+    b[e + 1] = (uint16_t)(u >> 16);
+  }
+  return b;
+}
+
+// 8 fp32 values as bf16 (the dO rows)
+__device__ __forceinline__ u16x8 f32x8_to_bf(const float* p) {
+  const float4 a = *reinterpret_cast<const float4*>(p), b = *reinterpret_cast<const float4*>(p + 4);
+  u16x8 r;
+  uint32_t u = pack_bf2(a.x, a.y);
+  r[0] = (uint16_t)u; r[1] = (uint16_t)(u >> 16);
+  u = pack_bf2(a.z, a.w);
+  r[2] = (uint16_t)u; r[3] = (uint16_t)(u >> 16);
+  u = pack_bf2(b.x, b.y);
+  r[4] = (uint16_t)u; r[5] = (uint16_t)(u >> 16);
+  u = pack_bf2(b.z, b.w);
+  r[6] = (uint16_t)u; r[7] = (uint16_t)(u >> 16);
+  return r;
+}
+
+// score in log2 units: round_bf(q.k) * scale * log2(e) (+ slot bias * log2(e)); -inf when masked
+__device__ __forceinline__ float score2(const b3_attn_bwd_args& a, float dot, const KField& f, int j, int i,
+                                        float sl) {
+  if (j >= f.len || (f.kind == 3 && j > i)) return -INFINITY;
+  const float x = a.score_round ? round_bf(dot) : dot;
+  return f.kind == 1 ? fmaf(x, sl, f.bias[j] * L2E) : x * sl;
+}
+
+template <int HD>
+struct DqMfmaSmem {
+  alignas(16) uint16_t k[32 * HD];   // the key block, row-major, swizzled pieces
+};
+
+// dQ for one 32-query tile of one query head: lane l owns query l % 32 of the tile.
+template <int HD>
+__global__ void __launch_bounds__(64) attn_bwd_dq_mfma_kernel(b3_attn_bwd_args a) {
+  __shared__ DqMfmaSmem<HD> sm;
+  constexpr int KS = HD / 16, NDB = HD / 32, NP = HD / 8;
+  const int lane = threadIdx.x, n = lane & 31, h = lane >> 5;
+  const int qt = blockIdx.x, b = blockIdx.y / a.H, hq = blockIdx.y % a.H, c = blockIdx.z;
+  const int G = a.H / a.HKV, hkv = hq / G;
+  const int tc = chunk_len(a, c), q0 = qt * 32;
+  if (q0 >= tc) return;
+  const int nq = min(32, tc - q0);
+  const int qi = q0 + n;                      // this lane's query, index in the chunk
+  const bool qok = qi < tc;
+  const long long t = (long long)c * a.C + qi;
+  const long long row = ((long long)b * a.H + hq) * a.T + t;
+  const float sl = L2E / sqrtf((float)HD);
+  // B operands: the lane's query row and dO row, K elements 16 ks + 8 h ..
+  u16x8 qf[KS], of[KS];
+  {
+    const uint16_t* qr = reinterpret_cast<const uint16_t*>(a.q_rope) + (long long)b * a.q_sb + (long long)hq * a.q_sh +
+                         min(t, (long long)c * a.C + tc - 1) * HD;
+    const float* dr = a.dy + (long long)b * a.dy_sb + min(t, (long long)c * a.C + tc - 1) * a.dy_st +
+                      (long long)hq * HD;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      qf[ks] = *reinterpret_cast<const u16x8*>(qr + 16 * ks + 8 * h);
+      of[ks] = f32x8_to_bf(dr + 16 * ks + 8 * h);
+      if (!qok) {
+        qf[ks] = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+        of[ks] = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+      }
+    }
+  }
+  const float drow = qok ? a.d_rows[row] : 0.f;
+  const int n_fields = __popc(field_mask(a, c));
+  // A operand of K rows: lane row = key l % 32 of the block (rows past the field repeat its last)
+  auto load_rows = [&](const KField& f, int j0, bool v_too, u16x8* ka, u16x8* va) {
+    const int kr = min(j0 + n, f.len - 1);
+    const uint16_t* kp = reinterpret_cast<const uint16_t*>(f.k) + (long long)kr * HD;
+    const uint16_t* vp = reinterpret_cast<const uint16_t*>(f.v) + (long long)kr * HD;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      ka[ks] = *reinterpret_cast<const u16x8*>(kp + 16 * ks + 8 * h);
+      if (v_too) va[ks] = *reinterpret_cast<const u16x8*>(vp + 16 * ks + 8 * h);
+    }
+  };
+  // pass 1: log-sum-exp (log2 units) of the lane's query over all fields
+  float m_run = -INFINITY, l_run = 0.f;
+  for (int fi = 0; fi < n_fields; ++fi) {
+    const KField f = chunk_field<uint16_t>(a, b, hkv, c, fi);
+    for (int j0 = 0; j0 < f.len; j0 += 32) {
+      if (f.kind == 3 && j0 > q0 + nq - 1) break;
+      u16x8 ka[KS], va[KS];
+      load_rows(f, j0, false, ka, va);
+      f32x16 st = zero16();
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) mma_bf16(st, ka[ks], qf[ks]);
+      float bm = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        st[r] = score2(a, st[r], f, j0 + d_row(lane, r), qi, sl);
+        bm = fmaxf(bm, st[r]);
+      }
+      bm = pair_max32(bm);
+      const float mn = fmaxf(m_run, bm);
+      if (mn == -INFINITY) continue;
+      float ps = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) ps += st[r] == -INFINITY ? 0.f : exp2f(st[r] - mn);
+      ps = pair_sum32(ps);
+      l_run = l_run * (m_run == -INFINITY ? 0.f : exp2f(m_run - mn)) + ps;
+      m_run = mn;
+    }
+  }
+  const float lse2 = m_run + log2f(l_run);
+  if (qok && h == 0) a.lse[row] = lse2 / L2E;
+  // pass 2: dS block by block; dQ^T += K^T dS^T; the slot bias gradient
+  f32x16 dq[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) dq[db] = zero16();
+  const long long bias_row = (((long long)(c - 2) * a.B * a.H + (long long)b * a.H + hq) * a.n_qtiles + qt) * a.S;
+  for (int fi = 0; fi < n_fields; ++fi) {
+    const KField f = chunk_field<uint16_t>(a, b, hkv, c, fi);
+    for (int j0 = 0; j0 < f.len; j0 += 32) {
+      if (f.kind == 3 && j0 > q0 + nq - 1) break;
+      u16x8 ka[KS], va[KS];
+      load_rows(f, j0, true, ka, va);
+      // the key block into LDS for the transposed reads (piece 2 ks + h of row n)
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+        *reinterpret_cast<u16x8*>(&sm.k[n * HD + 8 * ((2 * ks + h) ^ (n % NP))]) = ka[ks];
+      f32x16 st = zero16(), dpt = zero16();
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        mma_bf16(st, ka[ks], qf[ks]);
+        mma_bf16(dpt, va[ks], of[ks]);
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float x = score2(a, st[r], f, j0 + d_row(lane, r), qi, sl);
+        const float p = (x == -INFINITY || !qok) ? 0.f : exp2f(x - lse2);
+        st[r] = p * (dpt[r] - drow);          // dS^T
+      }
+      if (f.kind == 1) {
+        // column sums over the tile's queries: the lanes of each half
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          float v = st[r];
+#pragma unroll
+          for (int o = 16; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+          const int j = j0 + d_row(lane, r);
+          if (n == 0 && j < f.len) a.d_bias[bias_row + j] = v;
+        }
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the key block is in LDS
+#pragma unroll
+      for (int kc = 0; kc < 2; ++kc) {
+        const u16x8 bs = acc_operand(st, kc);
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) mma_bf16(dq[db], tr_operand<HD>(sm.k, db, kc, lane), bs);
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // reads done before the next block's writes
+    }
+  }
+  if (!qok) return;
+  const float scale = 1.0f / sqrtf((float)HD);
+  float* o = a.d_q_rope + row * HD;
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      *reinterpret_cast<float4*>(o + 32 * db + 8 * g + 4 * h) =
+          make_float4(dq[db][4 * g] * scale, dq[db][4 * g + 1] * scale, dq[db][4 * g + 2] * scale,
+                      dq[db][4 * g + 3] * scale);
+}
+
+template <int HD>
+struct DkvMfmaSmem {
+  alignas(16) uint16_t q[32 * HD];    // the query tile, row-major, swizzled pieces
+  alignas(16) uint16_t o[32 * HD];    // its dO rows in bf16
+  float lse2[32], drow[32];
+};
+
+// dK, dV for one 32-key block of one field: lane l owns key l % 32; all query rows of the
+// chunk's G heads in 32-row tiles.
+template <int HD>
+__global__ void __launch_bounds__(64) attn_bwd_dkv_mfma_kernel(b3_attn_bwd_args a) {
+  __shared__ DkvMfmaSmem<HD> sm;
+  constexpr int KS = HD / 16, NDB = HD / 32, NP = HD / 8;
+  const int lane = threadIdx.x, n = lane & 31, h = lane >> 5;
+  const int bh = blockIdx.y, b = bh / a.HKV, hkv = bh % a.HKV, c = blockIdx.z;
+  const int G = a.H / a.HKV;
+  const int tc = chunk_len(a, c);
+  const float sl = L2E / sqrtf((float)HD);
+  const int n_fields = __popc(field_mask(a, c));
+  int fi = 0, j0 = blockIdx.x * 32;
+  KField f = chunk_field<uint16_t>(a, b, hkv, c, 0);
+  while (j0 >= f.len) {
+    j0 -= (f.len + 31) / 32 * 32;
+    if (++fi >= n_fields) return;
+    f = chunk_field<uint16_t>(a, b, hkv, c, fi);
+  }
+  const int nk = min(32, f.len - j0);
+  const int j = j0 + n;                       // this lane's key
+  // B operands: the lane's key and value rows
+  u16x8 kf[KS], vf[KS];
+  {
+    const int kr = min(j, f.len - 1);
+    const uint16_t* kp = reinterpret_cast<const uint16_t*>(f.k) + (long long)kr * HD;
+    const uint16_t* vp = reinterpret_cast<const uint16_t*>(f.v) + (long long)kr * HD;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      kf[ks] = *reinterpret_cast<const u16x8*>(kp + 16 * ks + 8 * h);
+      vf[ks] = *reinterpret_cast<const u16x8*>(vp + 16 * ks + 8 * h);
+    }
+  }
+  f32x16 dk[NDB], dv[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) {
+    dk[db] = zero16();
+    dv[db] = zero16();
+  }
+  for (int g = 0; g < G; ++g) {
+    const int hq = hkv * G + g;
+    for (int q0 = 0; q0 < tc; q0 += 32) {
+      const int nq = min(32, tc - q0);
+      if (f.kind == 3 && j0 > q0 + nq - 1) continue;   // every query of the tile precedes the keys
+      const long long row0 = ((long long)b * a.H + hq) * a.T + (long long)c * a.C + q0;
+      // the query tile and its dO rows into LDS (row n, piece 2 ks + h); rows past the chunk zero
+      {
+        const int qr = min(q0 + n, tc - 1);
+        const long long t = (long long)c * a.C + qr;
+        const uint16_t* qp = reinterpret_cast<const uint16_t*>(a.q_rope) + (long long)b * a.q_sb +
+                             (long long)hq * a.q_sh + t * HD;
+        const float* dp = a.dy + (long long)b * a.dy_sb + t * a.dy_st + (long long)hq * HD;
+        const bool ok = q0 + n < tc;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          u16x8 qv = *reinterpret_cast<const u16x8*>(qp + 16 * ks + 8 * h);
+          u16x8 ov = f32x8_to_bf(dp + 16 * ks + 8 * h);
+          if (!ok) {
+            qv = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+            ov = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+          }
+          const int slot = 8 * ((2 * ks + h) ^ (n % NP));
+          *reinterpret_cast<u16x8*>(&sm.q[n * HD + slot]) = qv;
+          *reinterpret_cast<u16x8*>(&sm.o[n * HD + slot]) = ov;
+        }
+        if (h == 0) {
+          sm.lse2[n] = ok ? a.lse[row0 + n] * L2E : INFINITY;
+          sm.drow[n] = ok ? a.d_rows[row0 + n] : 0.f;
+        }
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      // S = Q K^T and dP = dO V^T: rows queries (A operand from the tile rows), columns keys
+      f32x16 s = zero16(), dp = zero16();
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const int slot = 8 * ((2 * ks + h) ^ (n % NP));
+        mma_bf16(s, *reinterpret_cast<const u16x8*>(&sm.q[n * HD + slot]), kf[ks]);
+        mma_bf16(dp, *reinterpret_cast<const u16x8*>(&sm.o[n * HD + slot]), vf[ks]);
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int qr = d_row(lane, r);
+        const float x = score2(a, s[r], f, j, q0 + qr, sl);
+        const float p = x == -INFINITY ? 0.f : exp2f(x - sm.lse2[qr]);
+        s[r] = p;
+        dp[r] = p * (dp[r] - sm.drow[qr]);     // dS
+      }
+#pragma unroll
+      for (int kc = 0; kc < 2; ++kc) {
+        const u16x8 bp = acc_operand(s, kc), bs = acc_operand(dp, kc);
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+          mma_bf16(dv[db], tr_operand<HD>(sm.o, db, kc, lane), bp);
+          mma_bf16(dk[db], tr_operand<HD>(sm.q, db, kc, lane), bs);
+        }
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // reads done before the next tile's writes
+    }
+  }
+  if (n >= nk) return;
+  const float scale = 1.0f / sqrtf((float)HD);
+  float *ok, *ov;
+  const long long HDl = HD;
+  if (f.kind == 0) {
+    const long long o = (((long long)c * a.B * a.HKV + bh) * a.n_sinks + j) * HDl;
+    ok = a.d_sink_k + o;
+    ov = a.d_sink_v + o;
+  } else if (f.kind == 1) {
+    const long long o = (((long long)(c - 2) * a.B * a.HKV + bh) * a.S + j) * HDl;
+    ok = a.d_slot_k + o;
+    ov = a.d_slot_v + o;
+  } else {
+    const long long o = ((long long)bh * a.T + (long long)(f.kind == 2 ? c - 1 : c) * a.C + j) * HDl;
+    ok = (f.kind == 2 ? a.d_k_next : a.d_k_own) + o;
+    ov = (f.kind == 2 ? a.d_v_next : a.d_v_own) + o;
+  }
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const int d0 = 32 * db + 8 * g4 + 4 * h;
+      *reinterpret_cast<float4*>(ok + d0) = make_float4(dk[db][4 * g4] * scale, dk[db][4 * g4 + 1] * scale,
+                                                        dk[db][4 * g4 + 2] * scale, dk[db][4 * g4 + 3] * scale);
+      *reinterpret_cast<float4*>(ov + d0) =
+          make_float4(dv[db][4 * g4], dv[db][4 * g4 + 1], dv[db][4 * g4 + 2], dv[db][4 * g4 + 3]);
+    }
 }
 
 template <int HD>
@@ -553,7 +913,8 @@ __global__ void __launch_bounds__(NT) readout_bwd_kernel(b3_attn_bwd_args a) {
     }
     dsg += red16_sum(dsg_r) * (dg == 0 && live ? 1.f : 0.f);
     __syncthreads();
-    // dqn[cc] = sum_d du[d] * M[cc][d] for this thread's columns cc
+    // dqn[cc] = sum_d du[d] * M[cc][d] for this thread's columns cc = 16 e + dg (the lanes of a
+    // row read M rows one row stride apart: distinct banks)
     float dqn[DPT];
 #pragma unroll
     for (int e = 0; e < DPT; ++e) dqn[e] = 0.f;
@@ -561,18 +922,18 @@ __global__ void __launch_bounds__(NT) readout_bwd_kernel(b3_attn_bwd_args a) {
       const float4 dv4 = *reinterpret_cast<const float4*>(&sm.du[r][d]);
 #pragma unroll
       for (int e = 0; e < DPT; ++e) {
-        const float4 mv = *reinterpret_cast<const float4*>(&sm.m[DPT * dg + e][d]);
+        const float4 mv = *reinterpret_cast<const float4*>(&sm.m[16 * e + dg][d]);
         dqn[e] += dv4.x * mv.x + dv4.y * mv.y + dv4.z * mv.z + dv4.w * mv.w;
       }
     }
     float qd = 0.f;
 #pragma unroll
-    for (int e = 0; e < DPT; ++e) qd += sm.qn[r][DPT * dg + e] * dqn[e];
+    for (int e = 0; e < DPT; ++e) qd += sm.qn[r][16 * e + dg] * dqn[e];
     qd = red16_sum(qd);
     if (live) {
-      float* o = a.d_q_raw + row * HD + DPT * dg;
+      float* o = a.d_q_raw + row * HD;
 #pragma unroll
-      for (int e = 0; e < DPT; ++e) o[e] = (dqn[e] - sm.qn[r][DPT * dg + e] * qd) * inv;
+      for (int e = 0; e < DPT; ++e) o[16 * e + dg] = (dqn[e] - sm.qn[r][16 * e + dg] * qd) * inv;
     }
     // dM[cc][d] += sum over the tile's rows of qn[row][cc] * du[row][d]; this thread: cc in
     // DPT * (tid >> 4) .. and d in DPT * dg ..
@@ -624,11 +985,18 @@ static int launch(const b3_attn_bwd_args& a, hipStream_t st) {
   hipLaunchKernelGGL((readout_bwd_kernel<T, HD>), dim3(BH, n_chunks), dim3(NT), sizeof(RdSmem<HD>), st, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return (int)e;
-  hipLaunchKernelGGL((attn_bwd_dq_kernel<T, HD>), dim3(a.n_qtiles, a.B * a.H, n_chunks), dim3(NT),
+  const int max_blocks = 1 + (a.S + 31) / 32 + 2 * ((a.C + 31) / 32);
+  if constexpr (St<T>::is_bf16) {
+    hipLaunchKernelGGL((attn_bwd_dq_mfma_kernel<HD>), dim3((a.C + 31) / 32, a.B * a.H, n_chunks), dim3(64), 0, st, a);
+    e = hipGetLastError();
+    if (e != hipSuccess) return (int)e;
+    hipLaunchKernelGGL((attn_bwd_dkv_mfma_kernel<HD>), dim3(max_blocks, BH, n_chunks), dim3(64), 0, st, a);
+    return (int)hipGetLastError();
+  }
+  hipLaunchKernelGGL((attn_bwd_dq_kernel<T, HD>), dim3((a.C + BQ - 1) / BQ, a.B * a.H, n_chunks), dim3(NT),
                      sizeof(DqSmem<HD>), st, a);
   e = hipGetLastError();
   if (e != hipSuccess) return (int)e;
-  const int max_blocks = 1 + (a.S + BK - 1) / BK + 2 * ((a.C + BK - 1) / BK);
   hipLaunchKernelGGL((attn_bwd_dkv_kernel<T, HD>), dim3(max_blocks, BH, n_chunks), dim3(NT), sizeof(DkvSmem<HD>),
                      st, a);
   return (int)hipGetLastError();
@@ -655,7 +1023,7 @@ extern "C" int bolt3_attn_bwd(const b3_attn_bwd_args* a, void* stream) {
   if (a->HD != 64 && a->HD != 128) return B3_ERR_UNSUPPORTED;
   if (a->dtype != B3_F32 && a->dtype != B3_BF16) return B3_ERR_UNSUPPORTED;
   const int n_chunks = (a->T + a->C - 1) / a->C;
-  if (a->n_chunks != n_chunks || a->n_qtiles != (a->C + b3::bwd::BQ - 1) / b3::bwd::BQ) return B3_ERR_ARG;
+  if (a->n_chunks != n_chunks || a->n_qtiles != (a->C + 31) / 32) return B3_ERR_ARG;
   if (a->n_steps < 0 || a->n_steps > (n_chunks > 2 ? n_chunks - 2 : 0) || a->n_sinks < 0 || a->n_sinks > a->C)
     return B3_ERR_ARG;
   if (!a->q_rope || !a->q_raw || !a->win_k || !a->win_v || !a->eta || !a->gamma || !a->res_w || !a->y || !a->dy ||

@@ -432,37 +432,53 @@ __global__ void __launch_bounds__(NT) attn_bwd_dkv_kernel(b3_attn_bwd_args a) {
 // tile in LDS whose 16-byte pieces p of row r sit at p ^ (r % (HD/8)).
 constexpr float L2E = 1.4426950408889634f;
 
-__device__ __forceinline__ u16x4 lds_read_tr(const uint16_t* p) {
-  u16x4 r;
-  const uint32_t addr = (uint32_t)(size_t)((__attribute__((address_space(3))) const uint16_t*)p);
-  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r) : "v"(addr) : "memory");
-  return r;
-}
-__device__ __forceinline__ void lds_wait_tr(u16x4* r) {
-  asm volatile("s_waitcnt lgkmcnt(0)"
-               : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7]));
-}
-
-// the transposed operand of tile `t` ([32 rows][HD], swizzled): rows are the K index (key or
-// query), the result's row m is feature 32 db + lane % 32; K chunk kc covers tile rows
-// 16 kc + {4h..4h+3, 8+4h..8+4h+3} in the order of an accumulator's rows
+// Lane offsets of the transposed reads in a [32 rows][HD] tile whose 16-byte pieces p of row r
+// sit at p ^ (r % (HD/8)): off[fb][s] for feature block fb (features 32 fb ..) and the read of
+// rows 4 h + (lane % 16) / 4 + 8 s.  A K chunk kc adds 16 kc rows, which leaves r % (HD/8) as it
+// is, so every read is one of these offsets plus a constant.
 template <int HD>
-__device__ __forceinline__ u16x8 tr_operand(const uint16_t* t, int db, int kc, int lane) {
+struct TrLanes {
+  int off[HD / 32][2];
+  __device__ __forceinline__ explicit TrLanes(int lane) {
+    constexpr int NP = HD / 8;
+    const int jv = lane & 15, grp = lane >> 4, h = lane >> 5;
+#pragma unroll
+    for (int fb = 0; fb < HD / 32; ++fb)
+#pragma unroll
+      for (int sc = 0; sc < 2; ++sc) {
+        const int r = 4 * h + (jv >> 2) + 8 * sc, f0 = 32 * fb + 16 * (grp & 1) + 4 * (jv & 3);
+        off[fb][sc] = r * HD + 8 * ((f0 >> 3) ^ (r % NP)) + (f0 & 7);
+      }
+  }
+};
+
+// TrLanes::off[fb][sc] for a feature block known only at run time
+template <int HD>
+__device__ __forceinline__ int tr_off(int lane, int fb, int sc) {
   constexpr int NP = HD / 8;
   const int jv = lane & 15, grp = lane >> 4, h = lane >> 5;
-  const int f0 = 32 * db + 16 * (grp & 1) + 4 * (jv & 3);
-  const int r1 = 16 * kc + 4 * h + (jv >> 2), r2 = r1 + 8;
-  u16x4 v[8];
-  v[0] = lds_read_tr(t + r1 * HD + 8 * ((f0 >> 3) ^ (r1 % NP)) + (f0 & 7));
-  v[1] = lds_read_tr(t + r2 * HD + 8 * ((f0 >> 3) ^ (r2 % NP)) + (f0 & 7));
-  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v[0]), "+v"(v[1]));
-  u16x8 a;
+  const int r = 4 * h + (jv >> 2) + 8 * sc, f0 = 32 * fb + 16 * (grp & 1) + 4 * (jv & 3);
+  return r * HD + 8 * ((f0 >> 3) ^ (r % NP)) + (f0 & 7);
+}
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ s16x4 lds_tr16(const uint16_t* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(p));
+}
+
+// the transposed operand of tile `t`: the result's row m is feature 32 fb + lane % 32; K chunk
+// kc covers tile rows 16 kc + {4h..4h+3, 8+4h..8+4h+3} in the order of an accumulator's rows
+template <int HD>
+__device__ __forceinline__ u16x8 tr_operand(const uint16_t* t, const TrLanes<HD>& L, int fb, int kc) {
+  const uint16_t* p = t + 16 * kc * HD;
+  const s16x4 a = lds_tr16(p + L.off[fb][0]), b = lds_tr16(p + L.off[fb][1]);
+  u16x8 r;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    a[e] = v[0][e];
-    a[4 + e] = v[1][e];
+    r[e] = (uint16_t)a[e];
+    r[4 + e] = (uint16_t)b[e];
   }
-  return a;
+  return r;
 }
 
 // accumulator values as the B operand of K chunk kc (rows 8 kc .. 8 kc + 7 of the 16), bf16
@@ -540,6 +556,7 @@ __global__ void __launch_bounds__(64) attn_bwd_dq_mfma_kernel(b3_attn_bwd_args a
   }
   const float drow = qok ? a.d_rows[row] : 0.f;
   const int n_fields = __popc(field_mask(a, c));
+  const TrLanes<HD> TL(lane);
   // A operand of K rows: lane row = key l % 32 of the block (rows past the field repeat its last)
   auto load_rows = [&](const KField& f, int j0, bool v_too, u16x8* ka, u16x8* va) {
     const int kr = min(j0 + n, f.len - 1);
@@ -619,14 +636,12 @@ __global__ void __launch_bounds__(64) attn_bwd_dq_mfma_kernel(b3_attn_bwd_args a
           if (n == 0 && j < f.len) a.d_bias[bias_row + j] = v;
         }
       }
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the key block is in LDS
 #pragma unroll
       for (int kc = 0; kc < 2; ++kc) {
         const u16x8 bs = acc_operand(st, kc);
 #pragma unroll
-        for (int db = 0; db < NDB; ++db) mma_bf16(dq[db], tr_operand<HD>(sm.k, db, kc, lane), bs);
+        for (int db = 0; db < NDB; ++db) mma_bf16(dq[db], tr_operand<HD>(sm.k, TL, db, kc), bs);
       }
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // reads done before the next block's writes
     }
   }
   if (!qok) return;
@@ -669,6 +684,7 @@ __global__ void __launch_bounds__(64) attn_bwd_dkv_mfma_kernel(b3_attn_bwd_args 
   }
   const int nk = min(32, f.len - j0);
   const int j = j0 + n;                       // this lane's key
+  const TrLanes<HD> TL(lane);
   // B operands: the lane's key and value rows
   u16x8 kf[KS], vf[KS];
   {
@@ -718,7 +734,6 @@ __global__ void __launch_bounds__(64) attn_bwd_dkv_mfma_kernel(b3_attn_bwd_args 
           sm.drow[n] = ok ? a.d_rows[row0 + n] : 0.f;
         }
       }
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       // S = Q K^T and dP = dO V^T: rows queries (A operand from the tile rows), columns keys
       f32x16 s = zero16(), dp = zero16();
 #pragma unroll
@@ -740,11 +755,10 @@ __global__ void __launch_bounds__(64) attn_bwd_dkv_mfma_kernel(b3_attn_bwd_args 
         const u16x8 bp = acc_operand(s, kc), bs = acc_operand(dp, kc);
 #pragma unroll
         for (int db = 0; db < NDB; ++db) {
-          mma_bf16(dv[db], tr_operand<HD>(sm.o, db, kc, lane), bp);
-          mma_bf16(dk[db], tr_operand<HD>(sm.q, db, kc, lane), bs);
+          mma_bf16(dv[db], tr_operand<HD>(sm.o, TL, db, kc), bp);
+          mma_bf16(dk[db], tr_operand<HD>(sm.q, TL, db, kc), bs);
         }
       }
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // reads done before the next tile's writes
     }
   }
   if (n >= nk) return;
@@ -978,11 +992,346 @@ __global__ void __launch_bounds__(NT) readout_bwd_kernel(b3_attn_bwd_args a) {
   }
 }
 
+// ---------------------------------------------------------------- readout, bf16 storage: MFMA
+//
+// The readout's gradients for bf16 storage on MFMA, one workgroup of four wavefronts per (b, kv
+// head, chunk), one query row per lane column, 32 rows per wavefront and round:
+//   U^T = M^T q_raw^T            (M^T as bf16 hi + lo, q_raw exact: two products, as the forward)
+//   u = U / |q_raw|, ym = u (1-gamma)/sqrt(HD), the RMSNorm backward as the fp32 kernel
+//   dqn^T = M du^T               (M^T read transposed; hi/lo on both sides: three products)
+//   dM += q_raw^T (du / |q_raw|) (bf16 operands from per-wavefront row tiles in LDS; wavefront w
+//                                 accumulates its share of the (HD/32)^2 output tiles)
+template <int HD>
+struct RdMfmaSmem {
+  alignas(16) uint16_t mt[2][HD * HD];   // M^T hi, lo: row d, 16-byte piece p at p ^ (d % (HD/8))
+  alignas(16) uint16_t qt[4][32 * HD];   // per wavefront: q_raw rows of its tile (same swizzle)
+  alignas(16) uint16_t ut[4][32 * HD];   // per wavefront: du / |q_raw| rows, bf16
+  float resw[HD];
+  float red[4][HD + 1];
+};
+
+// the accumulator's rows 8 kc .. 8 kc + 7 as a B operand split into bf16 hi and lo
+__device__ __forceinline__ void acc_operand_split(const f32x16& v, int kc, u16x8& hi, u16x8& lo) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const uint16_t hb = f2bf(v[8 * kc + e]);
+    hi[e] = hb;
+    lo[e] = f2bf(v[8 * kc + e] - bf2f(hb));
+  }
+}
+
+template <int HD>
+__global__ void __launch_bounds__(256) readout_bwd_mfma_kernel(b3_attn_bwd_args a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
+  RdMfmaSmem<HD>& sm = *reinterpret_cast<RdMfmaSmem<HD>*>(smem_raw);
+  constexpr int KS = HD / 16, NDB = HD / 32, NP = HD / 8, TPW = NDB * NDB / 4;
+  static_assert(NDB * NDB % 4 == 0, "dM tiles split over four wavefronts");
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, n = lane & 31, h = lane >> 5;
+  const int bh = blockIdx.x, b = bh / a.HKV, hkv = bh % a.HKV, c = blockIdx.y;
+  const int G = a.H / a.HKV;
+  const int tc = chunk_len(a, c);
+  const int n_rows = G * tc;
+  const bool has_m = c >= 2 && c - 2 < a.n_steps && a.m_res != nullptr;
+  if (!has_m) {
+    // D = rowsum(dy * y) only: 16 lanes per row, HD / 16 elements each
+    constexpr int DPT = HD / 16;
+    const int rq = lane >> 4, dg = lane & 15;
+    for (int r0 = 4 * w; r0 < n_rows; r0 += 16) {
+      const int q = r0 + rq;
+      const bool live = q < n_rows;
+      const int g = live ? q / tc : 0, i = live ? q % tc : 0;
+      const int hq = hkv * G + g;
+      const long long t = (long long)c * a.C + i;
+      float dd = 0.f;
+      if (live) {
+        const float* dyp = a.dy + (long long)b * a.dy_sb + t * a.dy_st + (long long)hq * HD + DPT * dg;
+        const uint16_t* yp = reinterpret_cast<const uint16_t*>(a.y) + (long long)b * a.y_sb + t * a.y_st +
+                             (long long)hq * HD + DPT * dg;
+#pragma unroll
+        for (int e = 0; e < DPT; ++e) dd += dyp[e] * bf2f(yp[e]);
+      }
+      dd = red16_sum(dd);
+      if (live && dg == 0) a.d_rows[((long long)b * a.H + hq) * a.T + t] = dd;
+    }
+    return;
+  }
+  // M^T hi / lo into LDS
+  {
+    const uint16_t* src = reinterpret_cast<const uint16_t*>(a.m_res + (long long)(c - 2) * a.m_step +
+                                                            (long long)bh * HD * HD);
+    for (int it = tid; it < 2 * HD * NP; it += 256) {
+      const int half = it / (HD * NP), rem = it % (HD * NP), d = rem / NP, pc = rem % NP;
+      *reinterpret_cast<u16x8*>(&sm.mt[half][d * HD + 8 * (pc ^ (d % NP))]) =
+          *reinterpret_cast<const u16x8*>(src + (long long)half * HD * HD + d * HD + 8 * pc);
+    }
+    for (int it = tid; it < HD; it += 256) sm.resw[it] = a.res_w[it];
+  }
+  __syncthreads();
+  const float sg = (1.0f - a.gamma[hkv]) / sqrtf((float)HD);
+  const TrLanes<HD> TL(lane);
+  int dm_off[TPW][4];   // transposed-read offsets of output tile tt: A (rows cf) then B (columns d)
+#pragma unroll
+  for (int tt = 0; tt < TPW; ++tt) {
+    const int id = w * TPW + tt, cb = id / NDB, db = id % NDB;
+    dm_off[tt][0] = tr_off<HD>(lane, cb, 0);
+    dm_off[tt][1] = tr_off<HD>(lane, cb, 1);
+    dm_off[tt][2] = tr_off<HD>(lane, db, 0);
+    dm_off[tt][3] = tr_off<HD>(lane, db, 1);
+  }
+  f32x16 dm[TPW];
+#pragma unroll
+  for (int tt = 0; tt < TPW; ++tt) dm[tt] = zero16();
+  // res_w partials: dres[db] is feature 32 db + d_row(lane, r) with r = 8 (n >> 4 & 1) +
+  // 4 (n >> 3 & 1) + 2 (n >> 2 & 1) + (n >> 1 & 1) (the reduce-scatter below leaves it there)
+  float dres[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) dres[db] = 0.f;
+  float dsg = 0.f;
+  uint16_t* qt = sm.qt[w];
+  uint16_t* ut = sm.ut[w];
+  const int n_tiles = (n_rows + 31) / 32;
+#pragma unroll 1
+  for (int r0 = 0; r0 < n_tiles; r0 += 4) {
+    const int q = 32 * (r0 + w) + n;
+    const bool live = q < n_rows;
+    const int g = live ? q / tc : 0, i = live ? q % tc : 0;
+    const int hq = hkv * G + g;
+    const long long t = (long long)c * a.C + i;
+    const long long row = ((long long)b * a.H + hq) * a.T + t;
+    // the lane's q_raw row: B operand (K elements 16 ks + 8 h ..) and row n of the tile
+    u16x8 qf[KS];
+    {
+      const uint16_t* qp = reinterpret_cast<const uint16_t*>(a.q_raw) + (long long)b * a.q_sb + (long long)hq * a.q_sh +
+                           t * HD;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        qf[ks] = live ? *reinterpret_cast<const u16x8*>(qp + 16 * ks + 8 * h) : u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+        *reinterpret_cast<u16x8*>(&qt[n * HD + 8 * ((2 * ks + h) ^ (n % NP))]) = qf[ks];
+      }
+    }
+    const float eta = live ? a.eta[(long long)b * a.e_sb + (long long)hq * a.e_sh + t] : 0.f;
+    float qq = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float x = bf2f(qf[ks][e]);
+        qq += x * x;
+      }
+    qq = pair_sum32(qq);
+    const float inv = 1.0f / fmaxf(sqrtf(qq), 1e-12f);
+    // U^T: rows d, column = the lane's query
+    f32x16 u[NDB];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) u[db] = zero16();
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      // one K step's operands at a time (the scheduler would otherwise hoist every read)
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+        const int dr = 32 * db + n, pc = (2 * ks + h) ^ (dr % NP);
+        mma_bf16(u[db], *reinterpret_cast<const u16x8*>(&sm.mt[0][dr * HD + 8 * pc]), qf[ks]);
+        mma_bf16(u[db], *reinterpret_cast<const u16x8*>(&sm.mt[1][dr * HD + 8 * pc]), qf[ks]);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // the RMSNorm backward of ym = u * sg at this lane's features d = 32 db + d_row(lane, r)
+    const float* dyp = a.dy + (long long)b * a.dy_sb + t * a.dy_st + (long long)hq * HD;
+    const uint16_t* yp = reinterpret_cast<const uint16_t*>(a.y) + (long long)b * a.y_sb + t * a.y_st + (long long)hq * HD;
+    // u becomes ym = U sg / |q_raw| (sg > 0: gamma <= 0.999)
+    const float ks_ = inv * sg;
+    float sq = 0.f;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        u[db][r] *= ks_;
+        sq += u[db][r] * u[db][r];
+      }
+    sq = pair_sum32(sq);
+    const float rr = 1.0f / sqrtf(sq / (float)HD + a.eps);
+    float dd = 0.f, deta = 0.f, gdot = 0.f;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      __builtin_amdgcn_sched_barrier(0);   // one block's loads live at a time
+      float xr[16];   // res_w terms of the block
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const int d0 = 32 * db + 8 * r4 + 4 * h;
+        float4 dy4 = make_float4(0.f, 0.f, 0.f, 0.f);
+        uint2 y2 = make_uint2(0u, 0u);
+        if (live) {
+          dy4 = *reinterpret_cast<const float4*>(dyp + d0);
+          y2 = *reinterpret_cast<const uint2*>(yp + d0);
+        }
+        const float4 w4 = *reinterpret_cast<const float4*>(&sm.resw[d0]);
+        const float dyv[4] = {dy4.x, dy4.y, dy4.z, dy4.w};
+        const float yv[4] = {bf_lo(y2.x), bf_hi(y2.x), bf_lo(y2.y), bf_hi(y2.y)};
+        const float wv[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int r = 4 * r4 + j;
+          const float ym = u[db][r];
+          const float yn = ym * rr * wv[j];
+          dd += dyv[j] * (yv[j] - eta * yn);
+          deta += dyv[j] * yn;
+          gdot += eta * dyv[j] * wv[j] * ym;
+          xr[r] = eta * dyv[j] * ym * rr;
+        }
+      }
+      // reduce-scatter over the 32 lanes of the half: the step with lane mask m keeps the half
+      // of the values selected by (n & m); the last step adds the partner's single value
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        const int m = 16 >> st, len = 8 >> st;
+        const bool up = (n & m) != 0;
+#pragma unroll
+        for (int j = 0; j < len; ++j) {
+          // the empty asm keeps the choice a select of two values (not an indexed array read)
+          float lo = xr[j], hi = xr[len + j];
+          asm("" : "+v"(lo), "+v"(hi));
+          const float keep = up ? hi : lo, send = up ? lo : hi;
+          xr[j] = keep + __shfl_xor(send, m, 64);
+        }
+      }
+      dres[db] += xr[0] + __shfl_xor(xr[0], 1, 64);
+    }
+    dd = pair_sum32(dd);
+    deta = pair_sum32(deta);
+    gdot = pair_sum32(gdot);
+    if (live && h == 0) {
+      a.d_rows[row] = dd;
+      a.d_eta[row] = deta;
+    }
+    // du = sg (rr g - ym rr^3 gdot / HD), g = eta dy w (dy read again), in place of u; the gamma
+    // partial; du / |q_raw| as bf16 into the wavefront's tile
+    float dsg_r = 0.f;
+    const float c3 = rr * rr * rr * gdot / (float)HD;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        if (r4 == 0) __builtin_amdgcn_sched_barrier(0);
+        const int d0 = 32 * db + 8 * r4 + 4 * h;
+        float4 dy4 = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (live) dy4 = *reinterpret_cast<const float4*>(dyp + d0);
+        const float4 w4 = *reinterpret_cast<const float4*>(&sm.resw[d0]);
+        const float dyv[4] = {dy4.x, dy4.y, dy4.z, dy4.w};
+        const float wv[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int r = 4 * r4 + j;
+          const float ym = u[db][r];
+          const float dym = rr * (eta * dyv[j] * wv[j]) - ym * c3;
+          dsg_r += dym * ym;
+          u[db][r] = live ? dym * sg : 0.f;
+        }
+        const uint2 v = make_uint2(pack_bf2(u[db][4 * r4] * inv, u[db][4 * r4 + 1] * inv),
+                                   pack_bf2(u[db][4 * r4 + 2] * inv, u[db][4 * r4 + 3] * inv));
+        *reinterpret_cast<uint2*>(&ut[n * HD + 8 * ((4 * db + r4) ^ (n % NP)) + 4 * h]) = v;
+      }
+    // sum_d dym ym: the gamma partial (times 1/sg) and qn . dqn (qn . M du = u . du)
+    const float sdy = pair_sum32(dsg_r);
+    if (live && h == 0) dsg += sdy / sg;
+    // dqn^T[cf][q] = sum_d M[cf][d] du[q][d]: A = M read transposed out of M^T, K = d in the
+    // accumulator's row order, du as bf16 hi + lo; d q_raw = (dqn - qn (qn . dqn)) / |q_raw|,
+    // qn = q_raw / |q_raw| (q_raw from the tile), one 32-feature block at a time
+    u16x8 bhi[NDB][2], blo[NDB][2];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int kc = 0; kc < 2; ++kc) acc_operand_split(u[db], kc, bhi[db][kc], blo[db][kc]);
+    const float qi2 = sdy * inv;
+    float* o = a.d_q_raw + row * HD;
+#pragma unroll
+    for (int cb = 0; cb < NDB; ++cb) {
+      __builtin_amdgcn_sched_barrier(0);
+      f32x16 dq = zero16();
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int kc = 0; kc < 2; ++kc) {
+          const u16x8 ah = tr_operand<HD>(&sm.mt[0][32 * db * HD], TL, cb, kc);
+          const u16x8 al = tr_operand<HD>(&sm.mt[1][32 * db * HD], TL, cb, kc);
+          mma_bf16(dq, ah, bhi[db][kc]);
+          mma_bf16(dq, al, bhi[db][kc]);
+          mma_bf16(dq, ah, blo[db][kc]);
+        }
+      if (live) {
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const uint2 q2 = *reinterpret_cast<const uint2*>(&qt[n * HD + 8 * ((4 * cb + r4) ^ (n % NP)) + 4 * h]);
+          float4 v;
+          v.x = (dq[4 * r4] - bf_lo(q2.x) * qi2) * inv;
+          v.y = (dq[4 * r4 + 1] - bf_hi(q2.x) * qi2) * inv;
+          v.z = (dq[4 * r4 + 2] - bf_lo(q2.y) * qi2) * inv;
+          v.w = (dq[4 * r4 + 3] - bf_hi(q2.y) * qi2) * inv;
+          *reinterpret_cast<float4*>(o + 32 * cb + 8 * r4 + 4 * h) = v;
+        }
+      }
+    }
+    __syncthreads();   // every wavefront's q_raw and du tiles are in LDS
+    // dM[cf][d] += sum_q q_raw[q][cf] du'[q][d] over the round's tiles; output tile tt of this
+    // wavefront is (cb, db) = ((w TPW + tt) / NDB, (w TPW + tt) % NDB)
+    for (int ws = 0; ws < 4; ++ws) {
+      if (32 * (r0 + ws) >= n_rows) break;
+#pragma unroll
+      for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+        for (int tt = 0; tt < TPW; ++tt) {
+          const uint16_t* pq = sm.qt[ws] + 16 * kc * HD;
+          const uint16_t* pu = sm.ut[ws] + 16 * kc * HD;
+          const s16x4 a0 = lds_tr16(pq + dm_off[tt][0]), a1 = lds_tr16(pq + dm_off[tt][1]);
+          const s16x4 b0 = lds_tr16(pu + dm_off[tt][2]), b1 = lds_tr16(pu + dm_off[tt][3]);
+          u16x8 av, bv;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            av[e] = (uint16_t)a0[e];
+            av[4 + e] = (uint16_t)a1[e];
+            bv[e] = (uint16_t)b0[e];
+            bv[4 + e] = (uint16_t)b1[e];
+          }
+          mma_bf16(dm[tt], av, bv);
+        }
+    }
+    __syncthreads();   // the tiles are read before the next round writes them
+  }
+  // dM out: tile (cb, db) holds rows cf = 32 cb + d_row(lane, r), column d = 32 db + n
+  float* dmo = a.d_m + ((long long)(c - 2) * a.B * a.HKV + bh) * HD * HD;
+#pragma unroll
+  for (int tt = 0; tt < TPW; ++tt) {
+    const int id = w * TPW + tt, cb = id / NDB, db = id % NDB;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dmo[(32 * cb + d_row(lane, r)) * HD + 32 * db + n] = dm[tt][r];
+  }
+  // res_w and gamma partials over the wavefronts (lanes n and n ^ 1 hold the same sums)
+  if ((n & 1) == 0) {
+    const int r = 8 * ((n >> 4) & 1) + 4 * ((n >> 3) & 1) + 2 * ((n >> 2) & 1) + ((n >> 1) & 1);
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) sm.red[w][32 * db + d_row(lane, r)] = dres[db];
+  }
+  {
+    float v = dsg;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    if (lane == 0) sm.red[w][HD] = v;
+  }
+  __syncthreads();
+  const long long pc = (long long)bh * a.n_chunks + c;
+  if (tid < HD) a.d_res_w[pc * HD + tid] = sm.red[0][tid] + sm.red[1][tid] + sm.red[2][tid] + sm.red[3][tid];
+  if (tid == 0)
+    a.d_gamma[pc] = -(sm.red[0][HD] + sm.red[1][HD] + sm.red[2][HD] + sm.red[3][HD]) / sqrtf((float)HD);
+}
+
 template <typename T, int HD>
 static int launch(const b3_attn_bwd_args& a, hipStream_t st) {
   const int n_chunks = a.n_chunks;
   const int BH = a.B * a.HKV;
-  hipLaunchKernelGGL((readout_bwd_kernel<T, HD>), dim3(BH, n_chunks), dim3(NT), sizeof(RdSmem<HD>), st, a);
+  if constexpr (St<T>::is_bf16)
+    hipLaunchKernelGGL((readout_bwd_mfma_kernel<HD>), dim3(BH, n_chunks), dim3(256), sizeof(RdMfmaSmem<HD>), st, a);
+  else
+    hipLaunchKernelGGL((readout_bwd_kernel<T, HD>), dim3(BH, n_chunks), dim3(NT), sizeof(RdSmem<HD>), st, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return (int)e;
   const int max_blocks = 1 + (a.S + 31) / 32 + 2 * ((a.C + 31) / 32);
@@ -1012,6 +1361,10 @@ static int set_smem() {
   if (e == hipSuccess)
     e = hipFuncSetAttribute(reinterpret_cast<const void*>(&readout_bwd_kernel<T, HD>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(RdSmem<HD>));
+  if constexpr (St<T>::is_bf16)
+    if (e == hipSuccess)
+      e = hipFuncSetAttribute(reinterpret_cast<const void*>(&readout_bwd_mfma_kernel<HD>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(RdMfmaSmem<HD>));
   return (int)e;
 }
 

@@ -140,6 +140,10 @@ typedef struct {
   /* optional (NULL to skip): each slot-decision workgroup adds 1 to *started when it begins, so
      that bolt3_wait_count can hold another stream until all B*HKV of them hold a compute unit */
   uint32_t* started;
+  /* optional (NULL to skip): the slots' mass and mean position after every step,
+     [n_steps][B*HKV][S] fp32 each (the backward's record of merges and evictions) */
+  float* snap_mass;
+  float* snap_pm;
 } b3_chain_args;
 
 /*
@@ -437,6 +441,44 @@ typedef struct {
   float eps;
 } b3_rms_norm_args;
 int bolt3_rms_norm(const b3_rms_norm_args* a, void* stream);
+
+/*
+ * Backward of the consolidation chain (bf16 storage, HD == 128, S == 128, at most 128 tokens
+ * per step), from the forward chain's decision log and per-step snapshots.  The decisions are
+ * constants (the reference takes them under no_grad, vsa_lm/config/bolt3.py:98-112, :121-135,
+ * :165-180); the gradient flows through the copies and mass-weighted means that fill, merge and
+ * evict the slots (:121-155, :182-191) and through the Gershgorin-safe delta rule
+ * M <- gamma M + Khat^T diag(bsafe) (V - Khat M) (:154-162).  Four kernels on the stream: per
+ * (step, bh) the tokens' 1/|k|, Gershgorin row sums and delta weights; per (bh, 16 features)
+ * the slot-gradient recursion with its token scatters; per (bh, 32 columns of M) the
+ * M_res-gradient recursion G_i = dM_i + (gamma I - Khat^T diag(bsafe) Khat) G_{i+1}; per
+ * (step, bh) the delta rule's token gradients.  Replaces the autograd of :121-166 and :182-191
+ * for Bolt3Attn.forward's chain (:262-273).
+ */
+typedef struct {
+  int32_t dtype, B, HKV, HD, S, T;
+  int32_t n_steps, off0, len0, step_stride, step_len;   /* the forward chain's step layout (empty start) */
+  const void* kr;             /* [B*HKV][T][HD] un-roped keys (storage dtype) */
+  const void* v;              /* [B*HKV][T][HD] values (storage dtype) */
+  const float* beta;          /* [B*HKV][T] delta-rule gates */
+  const float* log;           /* [n_steps][B*HKV][B3_LOG_ROWS][B3_LOG_COLS] the forward's decision log */
+  const float* snap_mass;     /* [n_steps][B*HKV][S] slot mass after every step */
+  const float* snap_pm;       /* [n_steps][B*HKV][S] slot mean position after every step */
+  const float* snap_m;        /* [n_steps][B*HKV] blocks of HD*HD floats: M^T as bf16 hi then bf16 lo */
+  const float* gamma;         /* [HKV] */
+  const float* inv_freq;      /* [HD/2] */
+  const float* d_slot_k;      /* [n_steps][B*HKV][S][HD] gradient of the roped slot keys the attention read */
+  const float* d_slot_v;      /* [n_steps][B*HKV][S][HD] */
+  const float* d_m;           /* [n_steps][B*HKV][HD][HD] gradient of M_res after every step, M[c][d] */
+  float* d_kr;                /* added to: [B*HKV][T][HD] gradient of the un-roped keys */
+  float* d_v;                 /* added to: [B*HKV][T][HD] */
+  float* d_beta;              /* added to: [B*HKV][T] */
+  float* d_gamma;             /* out: [n_steps][B*HKV][HD/32] partial sums of dL/dgamma */
+  void* work;                 /* >= bolt3_chain_bwd_workspace_bytes(...) bytes */
+  int64_t work_bytes;
+} b3_chain_bwd_args;
+int bolt3_chain_bwd(const b3_chain_bwd_args* a, void* stream);
+int64_t bolt3_chain_bwd_workspace_bytes(int32_t B, int32_t HKV, int32_t HD, int32_t n_steps);
 
 /* Library identification: returns a static string (build flags, gfx target). */
 const char* bolt3_version(void);

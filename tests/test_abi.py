@@ -75,6 +75,20 @@ def test_rejects_bad_arguments_without_gpu_work():
     assert lib.bolt3_slot_keys(ctypes.byref(sk), None) == 1001        # null pointers
     sk.S = 64
     assert lib.bolt3_slot_keys(ctypes.byref(sk), None) == 1002        # S != 128
+    cb = A.ChainBwdArgs()
+    cb.dtype, cb.B, cb.HKV, cb.HD, cb.S, cb.T = 0, 1, 1, 128, 128, 512
+    cb.n_steps, cb.off0, cb.len0, cb.step_stride, cb.step_len = 2, 4, 124, 128, 128
+    assert lib.bolt3_chain_bwd(ctypes.byref(cb), None) == 1002        # fp32 storage: not this entry point
+    cb.dtype, cb.HD = 1, 64
+    assert lib.bolt3_chain_bwd(ctypes.byref(cb), None) == 1002        # head dim 64
+    cb.HD, cb.step_len = 128, 200
+    assert lib.bolt3_chain_bwd(ctypes.byref(cb), None) == 1002        # steps longer than 128 tokens
+    cb.step_len, cb.T = 128, 200
+    assert lib.bolt3_chain_bwd(ctypes.byref(cb), None) == 1001        # steps past the sequence
+    cb.T = 512
+    assert lib.bolt3_chain_bwd(ctypes.byref(cb), None) == 1001        # null pointers
+    assert lib.bolt3_chain_bwd_workspace_bytes(4, 8, 128, 30) == 4 * 30 * 32 * 4 * 128 + 30 * 32 * 128 * 128 * 4
+    assert lib.bolt3_chain_bwd_workspace_bytes(4, 8, 64, 30) == 0
     d2 = A.DecodeArgs()
     d2.dtype, d2.B, d2.H, d2.HKV, d2.HD, d2.S, d2.has_slots = 1, 1, 4, 1, 128, 256, 1
     assert lib.bolt3_decode(ctypes.byref(d2), None) in (1001, 1002)   # rejected before any launch
@@ -83,7 +97,7 @@ def test_rejects_bad_arguments_without_gpu_work():
 STRUCTS = {"b3_heads_args": A.HeadsArgs, "b3_chain_args": A.ChainArgs, "b3_attn_args": A.AttnArgs,
            "b3_decode_args": A.DecodeArgs, "b3_decode_layer_args": A.DecodeLayerArgs,
            "b3_slot_keys_args": A.SlotKeysArgs, "b3_attn_bwd_args": A.AttnBwdArgs,
-           "b3_rms_norm_args": A.RmsNormArgs}
+           "b3_rms_norm_args": A.RmsNormArgs, "b3_chain_bwd_args": A.ChainBwdArgs}
 
 
 def _flat_fields(st, prefix=""):

@@ -55,7 +55,7 @@ class ChainArgs(C.Structure):
         ("ak", p), ("av", p), ("mass", p), ("util", p), ("pm", p), ("act", p), ("m_res", p),
         ("kappa", p), ("gamma", p), ("inv_freq", p),
         ("snap_k", p), ("snap_v", p), ("snap_bias", p), ("snap_m", p), ("log", p),
-        ("work", p), ("work_bytes", i64), ("phase", i32), ("started", p),
+        ("work", p), ("work_bytes", i64), ("phase", i32), ("started", p), ("snap_mass", p), ("snap_pm", p),
     ]
 
 
@@ -132,7 +132,18 @@ class RmsNormArgs(C.Structure):
 
 CHAIN_NOALLOC_SCRATCH_BYTES = 4 << 20   # B3_CHAIN_NOALLOC_SCRATCH_BYTES
 
-EXPORTS = ("bolt3_attn_bwd", "bolt3_heads", "bolt3_chain", "bolt3_chain_noalloc", "bolt3_chain_workspace_bytes", "bolt3_chunk_attn",
+class ChainBwdArgs(C.Structure):
+    _fields_ = [
+        ("dtype", i32), ("B", i32), ("HKV", i32), ("HD", i32), ("S", i32), ("T", i32),
+        ("n_steps", i32), ("off0", i32), ("len0", i32), ("step_stride", i32), ("step_len", i32),
+        ("kr", p), ("v", p), ("beta", p), ("log", p), ("snap_mass", p), ("snap_pm", p), ("snap_m", p),
+        ("gamma", p), ("inv_freq", p), ("d_slot_k", p), ("d_slot_v", p), ("d_m", p),
+        ("d_kr", p), ("d_v", p), ("d_beta", p), ("d_gamma", p), ("work", p), ("work_bytes", i64),
+    ]
+
+
+EXPORTS = ("bolt3_attn_bwd", "bolt3_heads", "bolt3_chain", "bolt3_chain_bwd", "bolt3_chain_bwd_workspace_bytes",
+           "bolt3_chain_noalloc", "bolt3_chain_workspace_bytes", "bolt3_chunk_attn",
            "bolt3_decode",
            "bolt3_decode_layer", "bolt3_decode_layer_workspace_bytes", "bolt3_decode_workspace_bytes",
            "bolt3_rms_norm", "bolt3_slot_keys", "bolt3_step_advance", "bolt3_version", "bolt3_wait_count")
@@ -153,12 +164,14 @@ def load():
                      ("bolt3_chunk_attn", AttnArgs),
                      ("bolt3_decode", DecodeArgs), ("bolt3_decode_layer", DecodeLayerArgs),
                      ("bolt3_slot_keys", SlotKeysArgs), ("bolt3_attn_bwd", AttnBwdArgs),
-                     ("bolt3_rms_norm", RmsNormArgs)):
+                     ("bolt3_rms_norm", RmsNormArgs), ("bolt3_chain_bwd", ChainBwdArgs)):
         fn = getattr(lib, name)
         fn.argtypes = [C.POINTER(st), p]
         fn.restype = C.c_int
     lib.bolt3_chain_workspace_bytes.argtypes = [i32, i32, i32, i32, i32, i32]
     lib.bolt3_chain_workspace_bytes.restype = i64
+    lib.bolt3_chain_bwd_workspace_bytes.argtypes = [i32, i32, i32, i32]
+    lib.bolt3_chain_bwd_workspace_bytes.restype = i64
     lib.bolt3_decode_layer_workspace_bytes.argtypes = [i32, i32, i32, i32, i32]
     lib.bolt3_decode_layer_workspace_bytes.restype = i64
     lib.bolt3_decode_workspace_bytes.argtypes = [i32, i32, i32, i32]
@@ -229,3 +242,7 @@ def decode_layer_workspace_bytes(B: int, d_model: int, n_in: int, hd_total: int,
 
 def chain_workspace_bytes(dt: torch.dtype, B: int, HKV: int, HD: int, S: int, n_steps: int) -> int:
     return int(load().bolt3_chain_workspace_bytes(dtype_code(dt), B, HKV, HD, S, n_steps))
+
+
+def chain_bwd_workspace_bytes(B: int, HKV: int, HD: int, n_steps: int) -> int:
+    return int(load().bolt3_chain_bwd_workspace_bytes(B, HKV, HD, n_steps))

@@ -220,6 +220,38 @@ def chain_backward(steps, d_slot_k, d_slot_v, d_m, pms, inv_freq, kr, v, beta, g
     return d_kr, d_v, d_beta, d_gam
 
 
+def chain_backward_hip(mod, tr: dict, o: dict, gam: torch.Tensor, b: int, n_steps: int):
+    """bolt3_chain_bwd on the forward's trace and the attention backward's outputs: returns
+    (d_kr, d_v, d_beta, d_gamma) like chain_backward."""
+    HKV, HD, S, C = mod.HKV, mod.HD, mod.S, mod.C
+    k_raw = tr["k_raw"]
+    T = k_raw.shape[2]
+    bh = b * HKV
+    dev = k_raw.device
+    ns = min(mod.n_sinks, C)
+    f32 = dict(device=dev, dtype=torch.float32)
+    d_kr, d_v = torch.zeros(bh, T, HD, **f32), torch.zeros(bh, T, HD, **f32)
+    d_beta = torch.zeros(bh, T, **f32)
+    d_gamma = torch.empty(n_steps, bh, HD // 32, **f32)
+    work = torch.empty(A.chain_bwd_workspace_bytes(b, HKV, HD, n_steps), dtype=torch.uint8, device=dev)
+    a = A.ChainBwdArgs()
+    a.dtype, a.B, a.HKV, a.HD, a.S, a.T = A.dtype_code(k_raw.dtype), b, HKV, HD, S, T
+    a.n_steps, a.off0, a.len0, a.step_stride, a.step_len = n_steps, ns, C - ns, C, C
+    a.kr, a.v, a.beta, a.log = k_raw.data_ptr(), tr["v"].data_ptr(), tr["beta"].data_ptr(), tr["log"].data_ptr()
+    a.snap_mass, a.snap_pm, a.snap_m = tr["snap_mass"].data_ptr(), tr["snap_pm"].data_ptr(), tr["snap_m"].data_ptr()
+    a.gamma, a.inv_freq = gam.data_ptr(), mod._packed(k_raw.dtype, dev)[2]["inv_freq"].data_ptr()
+    a.d_slot_k, a.d_slot_v, a.d_m = o["d_slot_k"].data_ptr(), o["d_slot_v"].data_ptr(), o["d_m"].data_ptr()
+    a.d_kr, a.d_v, a.d_beta, a.d_gamma = d_kr.data_ptr(), d_v.data_ptr(), d_beta.data_ptr(), d_gamma.data_ptr()
+    a.work, a.work_bytes = work.data_ptr(), work.numel()
+    A.call("bolt3_chain_bwd", a, dev)
+    return d_kr, d_v, d_beta, d_gamma.view(n_steps, b, HKV, -1).sum(dim=(0, 1, 3))
+
+
+def native_chain_ok(mod, dt: torch.dtype) -> bool:
+    """Whether bolt3_chain_bwd takes this layer's chain (bf16 storage, HD = S = 128, C <= 128)."""
+    return dt == torch.bfloat16 and mod.HD == 128 and mod.S == 128 and mod.C <= 128
+
+
 def attn_backward(mod, tr: dict, dy: torch.Tensor, dt: torch.dtype, n_steps: int):
     """bolt3_attn_bwd on the forward's tensors: returns its output buffers by name."""
     q_rope, q_raw, k_rope, v, eta = tr["q_rope"], tr["q_raw"], tr["k_rope"], tr["v"], tr["eta"]
@@ -295,14 +327,18 @@ def layer_backward(mod, x: torch.Tensor, tr: dict, d_out: torch.Tensor, dt: torc
     if n_steps > 0:
         d_krope[:, :, :ns] += o["d_sink_k"].sum(0).view(b, HKV, ns, HD)
         d_v[:, :, :ns] += o["d_sink_v"].sum(0).view(b, HKV, ns, HD)
-        steps, masses, pms = replay_slots(tr["log"], pos, S, C, ns)
         # kappa: the slot bias is kappa * log(max(mass, 1)) (vsa_lm/config/bolt3.py:238-241)
         dbias = o["d_bias"].sum(2).view(n_steps, b, HKV, G, S).sum(3)             # [step, b, HKV, S]
-        logm = torch.stack(masses).clamp_min(1.0).log().view(n_steps, b, HKV, S)
+        logm = tr["snap_mass"].clamp_min(1.0).log().view(n_steps, b, HKV, S)
         d_kappa = (dbias * logm).sum(dim=(0, 1, 3))
-        dk_c, dv_c, db_c, dg_c = chain_backward(
-            steps, o["d_slot_k"], o["d_slot_v"], o["d_m"], pms, inv_freq, tr["k_raw"].reshape(bh, T, HD),
-            tr["v"].reshape(bh, T, HD), tr["beta"].reshape(bh, T), gam, tr["snap_m"], dt == torch.bfloat16, b, HKV)
+        if native_chain_ok(mod, dt):
+            dk_c, dv_c, db_c, dg_c = chain_backward_hip(mod, tr, o, gam, b, n_steps)
+        else:
+            steps, _, pms = replay_slots(tr["log"], pos, S, C, ns)
+            dk_c, dv_c, db_c, dg_c = chain_backward(
+                steps, o["d_slot_k"], o["d_slot_v"], o["d_m"], pms, inv_freq, tr["k_raw"].reshape(bh, T, HD),
+                tr["v"].reshape(bh, T, HD), tr["beta"].reshape(bh, T), gam, tr["snap_m"], dt == torch.bfloat16, b,
+                HKV)
         d_kraw += dk_c.view(b, HKV, T, HD)
         d_v += dv_c.view(b, HKV, T, HD)
         d_beta += db_c.view(b, HKV, T)

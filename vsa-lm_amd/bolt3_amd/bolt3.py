@@ -272,7 +272,8 @@ class Bolt3Attn(nn.Module):
 
     def _chain(self, dt, device, B, kr, kp, v, tok_bh_stride, pos, beta, beta_bh_stride, n_steps, off0, len0,
                step_stride, step_len, n_filled, st: dict, m_res, gam, side, snap_k=None, snap_v=None,
-               snap_bias=None, snap_m=None, log=None, kp_exact=False, phase=0, work=None, started=None):
+               snap_bias=None, snap_m=None, log=None, kp_exact=False, phase=0, work=None, started=None,
+               snap_mass=None, snap_pm=None):
         if work is None:
             work = torch.empty(A.chain_workspace_bytes(dt, B, self.HKV, self.HD, self.S, n_steps),
                                dtype=torch.uint8, device=device)
@@ -288,6 +289,7 @@ class Bolt3Attn(nn.Module):
         a.kappa, a.gamma, a.inv_freq = side["kappa"].data_ptr(), gam.data_ptr(), side["inv_freq"].data_ptr()
         a.snap_k, a.snap_v, a.snap_bias, a.snap_m = A.ptr(snap_k), A.ptr(snap_v), A.ptr(snap_bias), A.ptr(snap_m)
         a.log = A.ptr(log)
+        a.snap_mass, a.snap_pm = A.ptr(snap_mass), A.ptr(snap_pm)
         a.work, a.work_bytes = work.data_ptr(), work.numel()
         a.phase, a.started = phase, started
         A.call("bolt3_chain", a, device)
@@ -373,6 +375,9 @@ class Bolt3Attn(nn.Module):
             log = None
             if trace is not None and keep_log:
                 log = torch.zeros(n_cons, bh, A.LOG_ROWS, A.LOG_COLS, device=dev)
+            # the slots' mass and mean position after every step, for the backward
+            snap_mp = (torch.empty(n_cons, bh, S, device=dev), torch.empty(n_cons, bh, S, device=dev)) \
+                if trace is not None else None
             works = [torch.empty(A.chain_workspace_bytes(dt, b, HKV, HD, S, s1 - s0), dtype=torch.uint8, device=dev)
                      for s0, s1 in groups]
             s_dec.wait_stream(main)   # after the head preparation and the allocations above
@@ -387,6 +392,8 @@ class Bolt3Attn(nn.Module):
                         T, s1 - s0, off0, len0, C, C, nf, st, m_res, gam, side,
                         *(t[s0:s1] for t in snaps))
                 kw = dict(log=None if log is None else log[s0:s1], kp_exact=True, work=work)
+                if snap_mp is not None:
+                    kw.update(snap_mass=snap_mp[0][s0:s1], snap_pm=snap_mp[1][s0:s1])
                 if split:
                     count = ctr is not None and s0 == 0
                     with torch.cuda.stream(s_dec):
@@ -407,7 +414,7 @@ class Bolt3Attn(nn.Module):
                     nf = min(S, nf + (C - ns if i == 0 else C))
             if trace is not None:
                 trace.update(state=st, m_res=m_res, snap_k=snaps[0], snap_v=snaps[1], snap_bias=snaps[2],
-                             snap_m=snaps[3], log=log, n_filled=nf)
+                             snap_m=snaps[3], log=log, n_filled=nf, snap_mass=snap_mp[0], snap_pm=snap_mp[1])
         if first_started is not None:
             _wait_started(dev, ctr[0], first_started)
         lin_q = F.linear(x, side["wq"], side["bq"])

@@ -432,55 +432,6 @@ __global__ void __launch_bounds__(NT) attn_bwd_dkv_kernel(b3_attn_bwd_args a) {
 // tile in LDS whose 16-byte pieces p of row r sit at p ^ (r % (HD/8)).
 constexpr float L2E = 1.4426950408889634f;
 
-// Lane offsets of the transposed reads in a [32 rows][HD] tile whose 16-byte pieces p of row r
-// sit at p ^ (r % (HD/8)): off[fb][s] for feature block fb (features 32 fb ..) and the read of
-// rows 4 h + (lane % 16) / 4 + 8 s.  A K chunk kc adds 16 kc rows, which leaves r % (HD/8) as it
-// is, so every read is one of these offsets plus a constant.
-template <int HD>
-struct TrLanes {
-  int off[HD / 32][2];
-  __device__ __forceinline__ explicit TrLanes(int lane) {
-    constexpr int NP = HD / 8;
-    const int jv = lane & 15, grp = lane >> 4, h = lane >> 5;
-#pragma unroll
-    for (int fb = 0; fb < HD / 32; ++fb)
-#pragma unroll
-      for (int sc = 0; sc < 2; ++sc) {
-        const int r = 4 * h + (jv >> 2) + 8 * sc, f0 = 32 * fb + 16 * (grp & 1) + 4 * (jv & 3);
-        off[fb][sc] = r * HD + 8 * ((f0 >> 3) ^ (r % NP)) + (f0 & 7);
-      }
-  }
-};
-
-// TrLanes::off[fb][sc] for a feature block known only at run time
-template <int HD>
-__device__ __forceinline__ int tr_off(int lane, int fb, int sc) {
-  constexpr int NP = HD / 8;
-  const int jv = lane & 15, grp = lane >> 4, h = lane >> 5;
-  const int r = 4 * h + (jv >> 2) + 8 * sc, f0 = 32 * fb + 16 * (grp & 1) + 4 * (jv & 3);
-  return r * HD + 8 * ((f0 >> 3) ^ (r % NP)) + (f0 & 7);
-}
-
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ s16x4 lds_tr16(const uint16_t* p) {
-  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(p));
-}
-
-// the transposed operand of tile `t`: the result's row m is feature 32 fb + lane % 32; K chunk
-// kc covers tile rows 16 kc + {4h..4h+3, 8+4h..8+4h+3} in the order of an accumulator's rows
-template <int HD>
-__device__ __forceinline__ u16x8 tr_operand(const uint16_t* t, const TrLanes<HD>& L, int fb, int kc) {
-  const uint16_t* p = t + 16 * kc * HD;
-  const s16x4 a = lds_tr16(p + L.off[fb][0]), b = lds_tr16(p + L.off[fb][1]);
-  u16x8 r;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    r[e] = (uint16_t)a[e];
-    r[4 + e] = (uint16_t)b[e];
-  }
-  return r;
-}
-
 // accumulator values as the B operand of K chunk kc (rows 8 kc .. 8 kc + 7 of the 16), bf16
 __device__ __forceinline__ u16x8 acc_operand(const f32x16& v, int kc) {
   u16x8 b;
@@ -1009,16 +960,6 @@ struct RdMfmaSmem {
   float resw[HD];
   float red[4][HD + 1];
 };
-
-// the accumulator's rows 8 kc .. 8 kc + 7 as a B operand split into bf16 hi and lo
-__device__ __forceinline__ void acc_operand_split(const f32x16& v, int kc, u16x8& hi, u16x8& lo) {
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const uint16_t hb = f2bf(v[8 * kc + e]);
-    hi[e] = hb;
-    lo[e] = f2bf(v[8 * kc + e] - bf2f(hb));
-  }
-}
 
 template <int HD>
 __global__ void __launch_bounds__(256) readout_bwd_mfma_kernel(b3_attn_bwd_args a) {

@@ -1694,6 +1694,8 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
       a.snap_bias[(step * BH + bh) * S + tid] =
           sm.act[tid] ? mul_rn(kap, logf(fmaxf(sm.mass[tid], 1.0f))) : -INFINITY;
     }
+    if (a.snap_mass && tid < S) a.snap_mass[(step * BH + bh) * S + tid] = sm.mass[tid];
+    if (a.snap_pm && tid < S) a.snap_pm[(step * BH + bh) * S + tid] = sm.pm[tid];
   }
 
   // store the slot state

@@ -1,0 +1,662 @@
+// Backward of the consolidation chain for bf16 storage (HD = 128, S = 128, at most 128 tokens
+// per step).
+//
+// The reference differentiates _consolidate_functional (vsa_lm/config/bolt3.py:68-192) with
+// autograd; every decision in it (fill picks, merge targets, evictions, delta-rule membership)
+// is taken under no_grad (:98-112, :121-135, :165-180), so the gradient is that of a fixed
+// sequence of copies, mass-weighted means and delta-rule updates.  The forward chain's decision
+// log and its per-step snapshots (slot mass and mean position, M_res) record that sequence; the
+// kernels below walk it backwards:
+//   tok_stats_kernel  per (step, bh): 1/|k_j|, the Gershgorin row sums r_j = sum_i |khat_i .
+//                     khat_j| w_i and bsafe_j = w_j / max(r_j, 1), w_j = beta_j [j goes to M_res]
+//                     (:154-158), the forward's own arithmetic;
+//   slot_rec_kernel   per (bh, 16 features): the slots' key / value gradients over the steps in
+//                     reverse -- the attention's slot gradients (keys through the transpose of
+//                     their RoPE), fills and evictions hand a slot's gradient to its token and
+//                     clear it (:145-150, :182-191), merges give token j 1/new_mass of its
+//                     slot's gradient and scale the slot's by mass/new_mass (:121-136);
+//   m_rec_kernel      per (bh, 32 columns of M): G_i = dM_i + (gamma I - Khat^T diag(bsafe)
+//                     Khat) G_{i+1} (the columns evolve independently) and each step's share of
+//                     dL/dgamma = sum(G_i * M_{i-1}) (:159-162);
+//   tok_grad_kernel   per (step, bh): the delta rule's token gradients with R = V - Khat M_{i-1},
+//                     E = bsafe R:  dV = bsafe (Khat G), dKhat = E G^T - dV M^T + (dP + dP^T)
+//                     Khat with dP through the row sums (|Khat Khat^T| and the clamp at 1), dw,
+//                     and the normalisation's backward to the un-roped keys.
+// Products run on MFMA with exact bf16 keys; fp32 operands (M, G, E, dV, the Gram weights) are
+// split into bf16 hi + lo, so every product is fp32-accurate to about 2^-16.
+#include <math.h>
+
+#include "bolt3_common.h"
+#include "bolt3_amd.h"
+
+namespace b3 {
+namespace cbwd {
+
+constexpr int S = 128;
+constexpr int HD = 128;
+constexpr int LT = 128;          // tokens per step, at most
+constexpr int NT = 256;          // threads of every kernel (4 wavefronts)
+constexpr int NP = HD / 8;       // 16-byte pieces of a row (LT / 8 as well)
+constexpr int NSL = HD / 16;     // feature slices of the slot recursion
+constexpr int NCB = HD / 32;     // 32-column blocks of M
+constexpr int KS = HD / 16;      // K steps of 16 over the features
+
+__device__ __forceinline__ int step_len(const b3_chain_bwd_args& a, int i) { return i == 0 ? a.len0 : a.step_len; }
+__device__ __forceinline__ int step_off(const b3_chain_bwd_args& a, int i) {
+  return i == 0 ? a.off0 : i * a.step_stride;
+}
+// slots filled before step i (the chain starts from the empty state)
+__device__ __forceinline__ int filled_before(const b3_chain_bwd_args& a, int i) {
+  int nf = 0;
+  for (int s = 0; s < i && nf < S; ++s) nf = min(S, nf + step_len(a, s));
+  return nf;
+}
+__device__ __forceinline__ const float* log_rec(const b3_chain_bwd_args& a, int i, int bh) {
+  return a.log + ((long long)i * a.B * a.HKV + bh) * B3_LOG_ROWS * B3_LOG_COLS;
+}
+
+// Workspace: per (step, bh) four rows of LT floats (1/|k|, row sum, bsafe, w), then per (step,
+// bh) G^T as bf16 hi and lo planes of HD x HD (G^T[d][c] = G[c][d], the layout of M_res
+// snapshots).
+__host__ __device__ __forceinline__ long long stats_floats(long long n, long long bh) { return n * bh * 4 * LT; }
+__host__ __device__ __forceinline__ long long ws_bytes(long long n, long long bh) {
+  return 4 * stats_floats(n, bh) + n * bh * HD * HD * 4;
+}
+__device__ __forceinline__ float* stats_of(const b3_chain_bwd_args& a, int i, int bh) {
+  return reinterpret_cast<float*>(a.work) + ((long long)i * a.B * a.HKV + bh) * 4 * LT;
+}
+__device__ __forceinline__ uint16_t* gt_of(const b3_chain_bwd_args& a, int i, int bh) {
+  const long long BH = (long long)a.B * a.HKV;
+  return reinterpret_cast<uint16_t*>(reinterpret_cast<float*>(a.work) + stats_floats(a.n_steps, BH)) +
+         ((long long)i * BH + bh) * 2 * HD * HD;
+}
+
+// the step's keys [LT][HD] into LDS (16-byte piece p of row r at p ^ (r % NP)), rows >= l zero
+__device__ __forceinline__ void stage_keys(uint16_t* kt, const uint16_t* kr, int l, int tid) {
+  for (int it = tid; it < LT * NP; it += NT) {
+    const int r = it / NP, p = it % NP;
+    u16x8 v = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    if (r < l) v = *reinterpret_cast<const u16x8*>(kr + (long long)r * HD + 8 * p);
+    *reinterpret_cast<u16x8*>(&kt[r * HD + 8 * (p ^ (r % NP))]) = v;
+  }
+}
+// an M^T hi / lo pair of planes (bf16, rows d) into LDS with the same swizzle
+__device__ __forceinline__ void stage_mt(uint16_t* mt, const uint16_t* src, int tid) {
+  for (int it = tid; it < 2 * HD * NP; it += NT) {
+    const int pl = it / (HD * NP), rem = it % (HD * NP), d = rem / NP, p = rem % NP;
+    *reinterpret_cast<u16x8*>(&mt[pl * HD * HD + d * HD + 8 * (p ^ (d % NP))]) =
+        *reinterpret_cast<const u16x8*>(src + (long long)pl * HD * HD + d * HD + 8 * p);
+  }
+}
+__device__ __forceinline__ u16x8 row_piece(const uint16_t* t, int r, int p) {
+  return *reinterpret_cast<const u16x8*>(&t[r * HD + 8 * (p ^ (r % NP))]);
+}
+// four consecutive bf16 of row r from column c0 (c0 % 4 == 0) of a swizzled tile
+__device__ __forceinline__ uint2 row_quad(const uint16_t* t, int r, int c0) {
+  return *reinterpret_cast<const uint2*>(&t[r * HD + 8 * ((c0 >> 3) ^ (r % NP)) + (c0 & 7)]);
+}
+__device__ __forceinline__ u16x8 neg_bf(u16x8 v) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] ^= 0x8000u;
+  return v;
+}
+
+// ---------------------------------------------------------------- per-token statistics
+
+__global__ void __launch_bounds__(NT) tok_stats_kernel(b3_chain_bwd_args a) {
+  __shared__ alignas(16) uint16_t kt[LT * HD];
+  __shared__ float s_inv[LT], s_w[LT];
+  const int i = blockIdx.x, bh = blockIdx.y;
+  if (filled_before(a, i) < S) return;   // fill step: no delta rule
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, n = lane & 31, h = lane >> 5;
+  const int l = step_len(a, i), t0 = step_off(a, i);
+  const uint16_t* kr = reinterpret_cast<const uint16_t*>(a.kr) + ((long long)bh * a.T + t0) * HD;
+  stage_keys(kt, kr, l, tid);
+  float* st = stats_of(a, i, bh);
+  if (tid < LT) {
+    float iv = 0.f, wv = 0.f;
+    if (tid < l) {
+      float ss = 0.f;
+      for (int d = 0; d < HD; d += 8) {
+        const u16x8 x = *reinterpret_cast<const u16x8*>(kr + (long long)tid * HD + d);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float f = bf2f(x[e]);
+          ss += f * f;
+        }
+      }
+      iv = 1.0f / fmaxf(sqrtf(ss), 1e-12f);
+      if (log_rec(a, i, bh)[B3_LOG_DELTA * B3_LOG_COLS + tid] > 0.5f) wv = a.beta[(long long)bh * a.T + t0 + tid];
+    }
+    s_inv[tid] = iv;
+    s_w[tid] = wv;
+    st[tid] = iv;
+    st[3 * LT + tid] = wv;
+  }
+  __syncthreads();
+  // column j = 32 w + n: sum over rows i of |khat_i . khat_j| w_i
+  const int j = 32 * w + n;
+  const float inj = s_inv[j];
+  float colsum = 0.f;
+  for (int ti = 0; ti < LT / 32; ++ti) {
+    if (32 * ti >= l) break;
+    f32x16 acc = zero16();
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) mma_bf16(acc, row_piece(kt, 32 * ti + n, 2 * ks + h), row_piece(kt, j, 2 * ks + h));
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int ii = 32 * ti + d_row(lane, r);
+      if (ii < l) colsum += fabsf(acc[r] * (s_inv[ii] * inj)) * s_w[ii];
+    }
+  }
+  colsum = pair_sum32(colsum);
+  if (h == 0 && j < LT) {
+    st[LT + j] = j < l ? colsum : 0.f;
+    st[2 * LT + j] = j < l ? s_w[j] / fmaxf(colsum, 1.0f) : 0.f;
+  }
+}
+
+// ---------------------------------------------------------------- slot recursion
+
+// Features of slice sl: 8 sl .. 8 sl + 7 and HD/2 + 8 sl .. (the RoPE pairs).
+__device__ __forceinline__ int slice_col(int sl, int e) { return e < 8 ? 8 * sl + e : HD / 2 + 8 * sl + (e - 8); }
+
+__device__ __forceinline__ void add_row16(float* out, int sl, const float* v) {
+  float4* p0 = reinterpret_cast<float4*>(out + 8 * sl);
+  float4* p1 = reinterpret_cast<float4*>(out + HD / 2 + 8 * sl);
+  float4 x;
+  x = p0[0]; x.x += v[0]; x.y += v[1]; x.z += v[2]; x.w += v[3]; p0[0] = x;
+  x = p0[1]; x.x += v[4]; x.y += v[5]; x.z += v[6]; x.w += v[7]; p0[1] = x;
+  x = p1[0]; x.x += v[8]; x.y += v[9]; x.z += v[10]; x.w += v[11]; p1[0] = x;
+  x = p1[1]; x.x += v[12]; x.y += v[13]; x.z += v[14]; x.w += v[15]; p1[1] = x;
+}
+
+__global__ void __launch_bounds__(NT) slot_rec_kernel(b3_chain_bwd_args a) {
+  // gradients of the slots' un-roped keys (g[0]) and values (g[1]) on this slice
+  __shared__ float g[2][S][17];
+  __shared__ int map_tok[S], cnt[S];
+  __shared__ float massb[S], newm[S];
+  const int bh = blockIdx.x, sl = blockIdx.y;
+  const int tid = threadIdx.x, s = tid >> 1, arr = tid & 1;
+  const long long BH = (long long)a.B * a.HKV;
+  float* grow = g[arr][s];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) grow[e] = 0.f;
+  float invf[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) invf[e] = a.inv_freq[8 * sl + e];
+  float* const out_all = arr ? a.d_v : a.d_kr;
+  for (int i = a.n_steps - 1; i >= 0; --i) {
+    const int l = step_len(a, i), t0 = step_off(a, i), nfb = filled_before(a, i);
+    const float* lg = log_rec(a, i, bh);
+    float* out = out_all + ((long long)bh * a.T + t0) * HD;
+    // the attention's gradients of the slots after step i: keys through the transpose of
+    // their RoPE at the slot's mean position
+    {
+      const long long base = (((long long)i * BH + bh) * S + s) * HD;
+      const float* src = (arr ? a.d_slot_v : a.d_slot_k) + base;
+      float lo[8], hi[8];
+      *reinterpret_cast<float4*>(lo) = *reinterpret_cast<const float4*>(src + 8 * sl);
+      *reinterpret_cast<float4*>(lo + 4) = *reinterpret_cast<const float4*>(src + 8 * sl + 4);
+      *reinterpret_cast<float4*>(hi) = *reinterpret_cast<const float4*>(src + HD / 2 + 8 * sl);
+      *reinterpret_cast<float4*>(hi + 4) = *reinterpret_cast<const float4*>(src + HD / 2 + 8 * sl + 4);
+      if (arr == 0) {
+        const float p = a.snap_pm[((long long)i * BH + bh) * S + s];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          float sn, cs;
+          sincosf(p * invf[e], &sn, &cs);
+          grow[e] += lo[e] * cs + hi[e] * sn;
+          grow[8 + e] += hi[e] * cs - lo[e] * sn;
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          grow[e] += lo[e];
+          grow[8 + e] += hi[e];
+        }
+      }
+    }
+    if (nfb < S) {
+      // fill: slots nfb .. nfb + m - 1 are copies of the picked tokens
+      const int m = min(S - nfb, l);
+      if (s >= nfb && s < nfb + m) {
+        const int tok = (int)lg[B3_LOG_TOPTOK * B3_LOG_COLS + (s - nfb)];
+        if ((unsigned)tok < (unsigned)l) add_row16(out + (long long)tok * HD, sl, grow);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) grow[e] = 0.f;
+      }
+      continue;   // every thread touches only its own row in this step
+    }
+    // steady step: winners (token -> slot) and merge counts
+    if (tid < S) {
+      map_tok[tid] = -1;
+      cnt[tid] = 0;
+    }
+    __syncthreads();
+    {
+      const int kc = min(l, S);
+      // (indices outside the step's tokens or the slots are ignored)
+      if (tid < kc && lg[B3_LOG_WIN * B3_LOG_COLS + tid] > 0.5f) {
+        const int bs = (int)lg[B3_LOG_BOTSLOT * B3_LOG_COLS + tid], tk = (int)lg[B3_LOG_TOPTOK * B3_LOG_COLS + tid];
+        if ((unsigned)bs < (unsigned)S && (unsigned)tk < (unsigned)l) map_tok[bs] = tk;
+      }
+      if (tid < l && lg[B3_LOG_MERGE * B3_LOG_COLS + tid] > 0.5f) {
+        const int ts = (int)lg[B3_LOG_SLOT * B3_LOG_COLS + tid];
+        if ((unsigned)ts < (unsigned)S) atomicAdd(&cnt[ts], 1);
+      }
+    }
+    __syncthreads();
+    // eviction: the winning token took the slot, so the slot's gradient is the token's
+    {
+      const int tok = map_tok[s];
+      if (tok >= 0) {
+        add_row16(out + (long long)tok * HD, sl, grow);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) grow[e] = 0.f;
+      }
+      if (arr == 0) {
+        const float mb = a.snap_mass[((long long)(i - 1) * BH + bh) * S + s];
+        massb[s] = mb;
+        newm[s] = mb + (float)cnt[s];
+      }
+    }
+    __syncthreads();
+    // merge: slot <- (mass * slot + sum of merged tokens) / new_mass
+    {
+      const int j = tid >> 1;
+      const int ts = j < l ? (int)lg[B3_LOG_SLOT * B3_LOG_COLS + j] : -1;
+      if (j < l && lg[B3_LOG_MERGE * B3_LOG_COLS + j] > 0.5f && (unsigned)ts < (unsigned)S) {
+        const float coef = 1.0f / newm[ts];
+        float v[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) v[e] = g[arr][ts][e] * coef;
+        add_row16(out + (long long)j * HD, sl, v);
+      }
+    }
+    __syncthreads();
+    if (cnt[s] > 0) {
+      const float kp = massb[s] / newm[s];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) grow[e] *= kp;
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------- M_res recursion
+
+struct MrecSmem {
+  alignas(16) uint16_t kt[LT * HD];      // the step's keys
+  alignas(16) uint16_t ct[2][32 * HD];   // G^T of the column block, hi / lo: row n, columns c
+  alignas(16) uint16_t tt[2][32 * LT];   // T^T hi / lo: row n, columns j (tokens)
+  float coef[LT];
+  float gp[4];
+};
+
+__global__ void __launch_bounds__(NT) m_rec_kernel(b3_chain_bwd_args a) {
+  __shared__ MrecSmem sm;
+  const int bh = blockIdx.x / NCB, db = blockIdx.x % NCB;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, n = lane & 31, h = lane >> 5;
+  const long long BH = (long long)a.B * a.HKV;
+  const float gam = a.gamma[bh % a.HKV];
+  const TrLanes<HD> TL(lane);
+  // G of the block: rows c = 32 w + d_row(lane, r), column d = 32 db + n
+  f32x16 cur = zero16();
+  for (int i = a.n_steps - 1; i >= 0; --i) {
+    const float* dm = a.d_m + ((long long)i * BH + bh) * HD * HD;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) cur[r] += dm[(32 * w + d_row(lane, r)) * HD + 32 * db + n];
+    if (filled_before(a, i) < S) {   // fill steps leave M_res as it is
+      if (tid == 0) a.d_gamma[((long long)i * BH + bh) * NCB + db] = 0.f;
+      continue;
+    }
+    const int l = step_len(a, i), t0 = step_off(a, i);
+    // G_i out (as G^T hi / lo) and this step's share of dL/dgamma: sum(G_i * M_{i-1})
+    {
+      uint16_t* gt = gt_of(a, i, bh);
+      const uint16_t* m0 =
+          reinterpret_cast<const uint16_t*>(a.snap_m + ((long long)(i - 1) * BH + bh) * HD * HD);
+      const int d = 32 * db + n;
+      float gs = 0.f;
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const int c0 = 32 * w + 8 * r4 + 4 * h;
+        uint16_t hb[4], lb[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float x = cur[4 * r4 + q];
+          hb[q] = f2bf(x);
+          lb[q] = f2bf(x - bf2f(hb[q]));
+        }
+        const uint2 ph = make_uint2(hb[0] | ((uint32_t)hb[1] << 16), hb[2] | ((uint32_t)hb[3] << 16));
+        const uint2 pl = make_uint2(lb[0] | ((uint32_t)lb[1] << 16), lb[2] | ((uint32_t)lb[3] << 16));
+        *reinterpret_cast<uint2*>(gt + d * HD + c0) = ph;
+        *reinterpret_cast<uint2*>(gt + HD * HD + d * HD + c0) = pl;
+        *reinterpret_cast<uint2*>(&sm.ct[0][n * HD + 8 * ((4 * w + r4) ^ (n % NP)) + 4 * h]) = ph;
+        *reinterpret_cast<uint2*>(&sm.ct[1][n * HD + 8 * ((4 * w + r4) ^ (n % NP)) + 4 * h]) = pl;
+        const uint2 mh = *reinterpret_cast<const uint2*>(m0 + d * HD + c0);
+        const uint2 ml = *reinterpret_cast<const uint2*>(m0 + HD * HD + d * HD + c0);
+        gs += cur[4 * r4] * (bf_lo(mh.x) + bf_lo(ml.x)) + cur[4 * r4 + 1] * (bf_hi(mh.x) + bf_hi(ml.x)) +
+              cur[4 * r4 + 2] * (bf_lo(mh.y) + bf_lo(ml.y)) + cur[4 * r4 + 3] * (bf_hi(mh.y) + bf_hi(ml.y));
+      }
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) gs += __shfl_xor(gs, o, 64);
+      if (lane == 0) sm.gp[w] = gs;
+    }
+    stage_keys(sm.kt, reinterpret_cast<const uint16_t*>(a.kr) + ((long long)bh * a.T + t0) * HD, l, tid);
+    if (tid < LT) {
+      const float* st = stats_of(a, i, bh);
+      sm.coef[tid] = tid < l ? st[tid] * st[tid] * st[2 * LT + tid] : 0.f;   // bsafe / |k|^2
+    }
+    __syncthreads();
+    if (tid == 0) a.d_gamma[((long long)i * BH + bh) * NCB + db] = sm.gp[0] + sm.gp[1] + sm.gp[2] + sm.gp[3];
+    // T = K G (wavefront w: tokens 32 w ..), then scaled by bsafe / |k|^2 into T^T
+    {
+      f32x16 t1 = zero16();
+      const int jr = 32 * w + n;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const u16x8 ka = row_piece(sm.kt, jr, 2 * ks + h);
+        const u16x8 bhv = *reinterpret_cast<const u16x8*>(&sm.ct[0][n * HD + 8 * ((2 * ks + h) ^ (n % NP))]);
+        const u16x8 blv = *reinterpret_cast<const u16x8*>(&sm.ct[1][n * HD + 8 * ((2 * ks + h) ^ (n % NP))]);
+        mma_bf16(t1, ka, bhv);
+        mma_bf16(t1, ka, blv);
+      }
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const int j0 = 32 * w + 8 * r4 + 4 * h;
+        uint16_t hb[4], lb[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float x = t1[4 * r4 + q] * sm.coef[j0 + q];
+          hb[q] = f2bf(x);
+          lb[q] = f2bf(x - bf2f(hb[q]));
+        }
+        const int off = n * LT + 8 * ((4 * w + r4) ^ (n % NP)) + 4 * h;
+        *reinterpret_cast<uint2*>(&sm.tt[0][off]) = make_uint2(hb[0] | ((uint32_t)hb[1] << 16), hb[2] | ((uint32_t)hb[3] << 16));
+        *reinterpret_cast<uint2*>(&sm.tt[1][off]) = make_uint2(lb[0] | ((uint32_t)lb[1] << 16), lb[2] | ((uint32_t)lb[3] << 16));
+      }
+    }
+    __syncthreads();
+    // G <- gamma G - K^T T (wavefront w: rows c = 32 w ..); K^T read transposed, T^T in the
+    // accumulator's row order
+    {
+      f32x16 u = zero16();
+#pragma unroll
+      for (int t4 = 0; t4 < LT / 32; ++t4)
+#pragma unroll
+        for (int kc = 0; kc < 2; ++kc) {
+          const u16x8 ka = tr_operand<HD>(sm.kt + 32 * t4 * HD, TL, w, kc);
+          const int p0 = 4 * t4 + 2 * kc;
+          const uint2 h0 = *reinterpret_cast<const uint2*>(&sm.tt[0][n * LT + 8 * (p0 ^ (n % NP)) + 4 * h]);
+          const uint2 h1 = *reinterpret_cast<const uint2*>(&sm.tt[0][n * LT + 8 * ((p0 + 1) ^ (n % NP)) + 4 * h]);
+          const uint2 l0 = *reinterpret_cast<const uint2*>(&sm.tt[1][n * LT + 8 * (p0 ^ (n % NP)) + 4 * h]);
+          const uint2 l1 = *reinterpret_cast<const uint2*>(&sm.tt[1][n * LT + 8 * ((p0 + 1) ^ (n % NP)) + 4 * h]);
+          u16x8 bhv, blv;
+          bhv[0] = h0.x & 0xffff; bhv[1] = h0.x >> 16; bhv[2] = h0.y & 0xffff; bhv[3] = h0.y >> 16;
+          bhv[4] = h1.x & 0xffff; bhv[5] = h1.x >> 16; bhv[6] = h1.y & 0xffff; bhv[7] = h1.y >> 16;
+          blv[0] = l0.x & 0xffff; blv[1] = l0.x >> 16; blv[2] = l0.y & 0xffff; blv[3] = l0.y >> 16;
+          blv[4] = l1.x & 0xffff; blv[5] = l1.x >> 16; blv[6] = l1.y & 0xffff; blv[7] = l1.y >> 16;
+          mma_bf16(u, ka, bhv);
+          mma_bf16(u, ka, blv);
+        }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) cur[r] = gam * cur[r] - u[r];
+    }
+    __syncthreads();   // the tiles are rewritten by the next step
+  }
+}
+
+// ---------------------------------------------------------------- token gradients
+
+struct TgSmem {
+  alignas(16) uint16_t mt[2 * HD * HD];   // M_{i-1}^T or G_i^T, hi then lo (rows d)
+  alignas(16) uint16_t kt[LT * HD];       // the step's keys
+  float inv[LT], raw[LT], bs[LT], wv[LT], drs[LT];
+};
+
+__global__ void __launch_bounds__(NT) tok_grad_kernel(b3_chain_bwd_args a) {
+  __shared__ TgSmem sm;
+  const int i = blockIdx.x, bh = blockIdx.y;
+  if (filled_before(a, i) < S) return;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, n = lane & 31, h = lane >> 5;
+  const long long BH = (long long)a.B * a.HKV;
+  const int l = step_len(a, i), t0 = step_off(a, i);
+  const TrLanes<HD> TL(lane);
+  const uint16_t* m0 = reinterpret_cast<const uint16_t*>(a.snap_m + ((long long)(i - 1) * BH + bh) * HD * HD);
+  stage_mt(sm.mt, m0, tid);
+  stage_keys(sm.kt, reinterpret_cast<const uint16_t*>(a.kr) + ((long long)bh * a.T + t0) * HD, l, tid);
+  if (tid < LT) {
+    const float* st = stats_of(a, i, bh);
+    const bool ok = tid < l;
+    sm.inv[tid] = ok ? st[tid] : 0.f;
+    sm.raw[tid] = ok ? st[LT + tid] : 0.f;
+    sm.bs[tid] = ok ? st[2 * LT + tid] : 0.f;
+    sm.wv[tid] = ok ? st[3 * LT + tid] : 0.f;
+    sm.drs[tid] = 0.f;
+  }
+  __syncthreads();
+  const int j = 32 * w + n;   // this lane's token
+  const bool live = j < l;
+  const float inj = sm.inv[j], bsj = sm.bs[j], wj = sm.wv[j], rawj = sm.raw[j];
+  const long long trow = (long long)bh * a.T + t0 + j;
+  // R^T[d][j] = v[j][d] - (M^T k_j)[d] / |k_j|
+  f32x16 R[NCB];
+#pragma unroll
+  for (int db = 0; db < NCB; ++db) R[db] = zero16();
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    const u16x8 kb = row_piece(sm.kt, j, 2 * ks + h);
+#pragma unroll
+    for (int db = 0; db < NCB; ++db) {
+      const int dr = 32 * db + n;
+      mma_bf16(R[db], row_piece(sm.mt, dr, 2 * ks + h), kb);
+      mma_bf16(R[db], row_piece(sm.mt + HD * HD, dr, 2 * ks + h), kb);
+    }
+  }
+  {
+    const uint16_t* vp = reinterpret_cast<const uint16_t*>(a.v) + trow * HD;
+#pragma unroll
+    for (int db = 0; db < NCB; ++db)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        uint2 v2 = make_uint2(0u, 0u);
+        if (live) v2 = *reinterpret_cast<const uint2*>(vp + 32 * db + 8 * r4 + 4 * h);
+        R[db][4 * r4] = bf_lo(v2.x) - R[db][4 * r4] * inj;
+        R[db][4 * r4 + 1] = bf_hi(v2.x) - R[db][4 * r4 + 1] * inj;
+        R[db][4 * r4 + 2] = bf_lo(v2.y) - R[db][4 * r4 + 2] * inj;
+        R[db][4 * r4 + 3] = bf_hi(v2.y) - R[db][4 * r4 + 3] * inj;
+      }
+  }
+  __syncthreads();   // M_{i-1}^T read
+  stage_mt(sm.mt, gt_of(a, i, bh), tid);
+  __syncthreads();
+  // dE^T = (G^T k_j) / |k_j|  (gradient of E's row j through V - Khat M is dE; of R: bsafe dE)
+  f32x16 dE[NCB];
+#pragma unroll
+  for (int db = 0; db < NCB; ++db) dE[db] = zero16();
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    const u16x8 kb = row_piece(sm.kt, j, 2 * ks + h);
+#pragma unroll
+    for (int db = 0; db < NCB; ++db) {
+      const int dr = 32 * db + n;
+      mma_bf16(dE[db], row_piece(sm.mt, dr, 2 * ks + h), kb);
+      mma_bf16(dE[db], row_piece(sm.mt + HD * HD, dr, 2 * ks + h), kb);
+    }
+  }
+  float dbs = 0.f;
+#pragma unroll
+  for (int db = 0; db < NCB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      dE[db][r] *= inj;
+      dbs += dE[db][r] * R[db][r];
+    }
+  dbs = pair_sum32(dbs);
+  // dKhat^T[c][j] = sum_d G[c][d] E[j][d]: G read transposed out of G^T, E = bsafe R
+  f32x16 dkn[NCB];
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb) dkn[cb] = zero16();
+#pragma unroll
+  for (int db = 0; db < NCB; ++db) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) R[db][r] *= bsj;
+#pragma unroll
+    for (int kc = 0; kc < 2; ++kc) {
+      u16x8 eh, el;
+      acc_operand_split(R[db], kc, eh, el);
+#pragma unroll
+      for (int cb = 0; cb < NCB; ++cb) {
+        const u16x8 ah = tr_operand<HD>(sm.mt + 32 * db * HD, TL, cb, kc);
+        const u16x8 al = tr_operand<HD>(sm.mt + HD * HD + 32 * db * HD, TL, cb, kc);
+        mma_bf16(dkn[cb], ah, eh);
+        mma_bf16(dkn[cb], al, eh);
+        mma_bf16(dkn[cb], ah, el);
+      }
+    }
+  }
+  // dV = bsafe dE (the gradient of R), added to the values' gradient
+#pragma unroll
+  for (int db = 0; db < NCB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dE[db][r] *= bsj;
+  if (live) {
+    float* dv = a.d_v + trow * HD;
+#pragma unroll
+    for (int db = 0; db < NCB; ++db)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        float4* p = reinterpret_cast<float4*>(dv + 32 * db + 8 * r4 + 4 * h);
+        float4 x = *p;
+        x.x += dE[db][4 * r4];
+        x.y += dE[db][4 * r4 + 1];
+        x.z += dE[db][4 * r4 + 2];
+        x.w += dE[db][4 * r4 + 3];
+        *p = x;
+      }
+  }
+  // the clamp of the row sum at 1 passes its gradient where r_j >= 1
+  const float rsj = fmaxf(rawj, 1.0f);
+  const float drsj = (live && rawj >= 1.0f) ? -dbs * wj / (rsj * rsj) : 0.f;
+  if (h == 0 && live) sm.drs[j] = drsj;
+  __syncthreads();   // G^T read; drs complete
+  stage_mt(sm.mt, m0, tid);
+  __syncthreads();
+  // dKhat^T -= sum_d M[c][d] dV[j][d]
+#pragma unroll
+  for (int db = 0; db < NCB; ++db)
+#pragma unroll
+    for (int kc = 0; kc < 2; ++kc) {
+      u16x8 vh, vl;
+      acc_operand_split(dE[db], kc, vh, vl);
+      vh = neg_bf(vh);
+      vl = neg_bf(vl);
+#pragma unroll
+      for (int cb = 0; cb < NCB; ++cb) {
+        const u16x8 ah = tr_operand<HD>(sm.mt + 32 * db * HD, TL, cb, kc);
+        const u16x8 al = tr_operand<HD>(sm.mt + HD * HD + 32 * db * HD, TL, cb, kc);
+        mma_bf16(dkn[cb], ah, vh);
+        mma_bf16(dkn[cb], al, vh);
+        mma_bf16(dkn[cb], ah, vl);
+      }
+    }
+  // through the row sums: P = Khat Khat^T, dw_j += sum_i |P_ij| drs_i, and
+  // dKhat_j += sum_i sign(P_ij) (drs_j w_i + drs_i w_j) khat_i
+  float dwg = 0.f;
+#pragma unroll
+  for (int ti = 0; ti < LT / 32; ++ti) {
+    f32x16 p = zero16();
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      mma_bf16(p, row_piece(sm.kt, 32 * ti + n, 2 * ks + h), row_piece(sm.kt, j, 2 * ks + h));
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int ii = 32 * ti + d_row(lane, r);
+      const float pv = p[r] * (sm.inv[ii] * inj);
+      const float sgn = pv > 0.f ? 1.f : (pv < 0.f ? -1.f : 0.f);
+      dwg += fabsf(pv) * sm.drs[ii];
+      p[r] = sm.inv[ii] * sgn * (drsj * sm.wv[ii] + sm.drs[ii] * wj);
+    }
+#pragma unroll
+    for (int kc = 0; kc < 2; ++kc) {
+      u16x8 qh, ql;
+      acc_operand_split(p, kc, qh, ql);
+#pragma unroll
+      for (int cb = 0; cb < NCB; ++cb) {
+        const u16x8 ka = tr_operand<HD>(sm.kt + 32 * ti * HD, TL, cb, kc);
+        mma_bf16(dkn[cb], ka, qh);
+        mma_bf16(dkn[cb], ka, ql);
+      }
+    }
+  }
+  dwg = pair_sum32(dwg);
+  // the normalisation: dk = (dKhat - khat (khat . dKhat)) / |k|
+  float sdot = 0.f;
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb)
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      const uint2 k2 = row_quad(sm.kt, j, 32 * cb + 8 * r4 + 4 * h);
+      sdot += bf_lo(k2.x) * dkn[cb][4 * r4] + bf_hi(k2.x) * dkn[cb][4 * r4 + 1] + bf_lo(k2.y) * dkn[cb][4 * r4 + 2] +
+              bf_hi(k2.y) * dkn[cb][4 * r4 + 3];
+    }
+  sdot = pair_sum32(sdot);
+  if (!live) return;
+  const float f2 = inj * inj * sdot;
+  float* dk = a.d_kr + trow * HD;
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb)
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      const uint2 k2 = row_quad(sm.kt, j, 32 * cb + 8 * r4 + 4 * h);
+      float4* p = reinterpret_cast<float4*>(dk + 32 * cb + 8 * r4 + 4 * h);
+      float4 x = *p;
+      x.x += (dkn[cb][4 * r4] - bf_lo(k2.x) * f2) * inj;
+      x.y += (dkn[cb][4 * r4 + 1] - bf_hi(k2.x) * f2) * inj;
+      x.z += (dkn[cb][4 * r4 + 2] - bf_lo(k2.y) * f2) * inj;
+      x.w += (dkn[cb][4 * r4 + 3] - bf_hi(k2.y) * f2) * inj;
+      *p = x;
+    }
+  if (h == 0 && log_rec(a, i, bh)[B3_LOG_DELTA * B3_LOG_COLS + j] > 0.5f)
+    a.d_beta[trow] += (rsj > 0.f ? dbs / rsj : 0.f) + dwg;
+}
+
+}  // namespace cbwd
+}  // namespace b3
+
+extern "C" int64_t bolt3_chain_bwd_workspace_bytes(int32_t B, int32_t HKV, int32_t HD, int32_t n_steps) {
+  if (B <= 0 || HKV <= 0 || HD != b3::cbwd::HD || n_steps <= 0) return 0;
+  return b3::cbwd::ws_bytes(n_steps, (long long)B * HKV);
+}
+
+extern "C" int bolt3_chain_bwd(const b3_chain_bwd_args* a, void* stream) {
+  using namespace b3::cbwd;
+  if (!a) return B3_ERR_ARG;
+  if (a->dtype != B3_BF16 || a->HD != HD || a->S != S) return B3_ERR_UNSUPPORTED;
+  if (a->B <= 0 || a->HKV <= 0 || a->T <= 0 || a->n_steps <= 0) return B3_ERR_ARG;
+  if (a->len0 <= 0 || a->len0 > LT || a->step_len <= 0 || a->step_len > LT || a->off0 < 0 || a->step_stride <= 0)
+    return B3_ERR_UNSUPPORTED;
+  if ((long long)a->off0 + a->len0 > a->T ||
+      (a->n_steps > 1 && (long long)(a->n_steps - 1) * a->step_stride + a->step_len > a->T))
+    return B3_ERR_ARG;
+  if (!a->kr || !a->v || !a->beta || !a->log || !a->snap_mass || !a->snap_pm || !a->snap_m || !a->gamma ||
+      !a->inv_freq || !a->d_slot_k || !a->d_slot_v || !a->d_m || !a->d_kr || !a->d_v || !a->d_beta || !a->d_gamma ||
+      !a->work)
+    return B3_ERR_ARG;
+  const long long BH = (long long)a->B * a->HKV;
+  if (a->work_bytes < ws_bytes(a->n_steps, BH)) return B3_ERR_WORKSPACE;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(tok_stats_kernel, dim3(a->n_steps, (unsigned)BH), dim3(NT), 0, st, *a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  hipLaunchKernelGGL(slot_rec_kernel, dim3((unsigned)BH, NSL), dim3(NT), 0, st, *a);
+  e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  hipLaunchKernelGGL(m_rec_kernel, dim3((unsigned)(BH * NCB)), dim3(NT), 0, st, *a);
+  e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  hipLaunchKernelGGL(tok_grad_kernel, dim3(a->n_steps, (unsigned)BH), dim3(NT), 0, st, *a);
+  return (int)hipGetLastError();
+}

@@ -480,6 +480,50 @@ typedef struct {
 int bolt3_chain_bwd(const b3_chain_bwd_args* a, void* stream);
 int64_t bolt3_chain_bwd_workspace_bytes(int32_t B, int32_t HKV, int32_t HD, int32_t n_steps);
 
+/*
+ * Backward of Bolt3Attn's head preparation, one pass per token row: the gradients of the roped
+ * queries and keys through the transpose of their RoPE (vsa_lm/config/bolt3.py:214-215,
+ * vsa_lm/surgery.py:86-93), plus the readout's gradient of the un-roped queries and the chain's
+ * of the un-roped keys and values; the sinks' and the next chunk's key / value gradients; the q / k
+ * RMSNorm backward (:203-206, vsa_lm/surgery.py:48-52) with per-block partial sums of the norm
+ * weights' gradients; the gates' derivatives beta = sigmoid(.), eta = tanh(.) (:198-199).  Writes
+ * dz, the gradient of the packed projection output [q | k | v | beta | eta | zero pad] per row
+ * (storage dtype), which the projection-gradient products read.  HD in {64, 128}.
+ */
+typedef struct {
+  int32_t dtype, B, T, H, HKV, HD, n_sinks, n_chunks;
+  const float* d_q_raw;       /* [B][H][T][HD] gradient of the un-roped queries (readout) */
+  const float* d_q_rope;      /* [B][H][T][HD] gradient of the roped queries (attention) */
+  const float* d_k_own;       /* [B][HKV][T][HD] gradient of the roped keys as their own chunk's keys */
+  const float* d_k_next;      /* [B][HKV][T][HD] ... as the next chunk's keys */
+  const float* d_v_own;
+  const float* d_v_next;
+  const float* d_sink_k;      /* [n_chunks][B*HKV][n_sinks][HD] or NULL: the sinks' roped-key gradients */
+  const float* d_sink_v;
+  const float* d_k_chain;     /* [B*HKV][T][HD] or NULL: the chain's gradient of the un-roped keys */
+  const float* d_v_chain;     /* [B*HKV][T][HD] or NULL */
+  const float* d_beta;        /* [B*HKV][T] or NULL */
+  const float* d_eta;         /* [B][H][T] */
+  const float* beta;          /* [B][HKV][T] gate values */
+  const float* eta;           /* [B][H][T] */
+  const void* lin_q;          /* [B*T][lin_q_row_stride] pre-norm q projection (storage dtype) */
+  int64_t lin_q_row_stride;
+  const void* lin_k;          /* [B*T][lin_k_row_stride] pre-norm k projection */
+  int64_t lin_k_row_stride;
+  const float* qn_w;          /* [HD] */
+  const float* kn_w;
+  int32_t has_qk_norm;
+  float q_eps, k_eps;
+  const float* inv_freq;      /* [HD/2] */
+  void* dz;                   /* out: [B*T][dz_row_stride] storage dtype */
+  int64_t dz_row_stride;
+  int32_t dz_cols;            /* >= (H + 2 HKV) HD + HKV + H; the columns past those are zeroed */
+  float* d_qn_w;              /* out: [bolt3_heads_bwd_blocks(B, T)][HD] partial sums (has_qk_norm) */
+  float* d_kn_w;
+} b3_heads_bwd_args;
+int bolt3_heads_bwd(const b3_heads_bwd_args* a, void* stream);
+int32_t bolt3_heads_bwd_blocks(int32_t B, int32_t T);
+
 /* Library identification: returns a static string (build flags, gfx target). */
 const char* bolt3_version(void);
 

@@ -17,7 +17,7 @@ HEADER = os.path.join(REPO, "include", "bolt3_amd.h")
 
 def _declared_functions():
     txt = open(HEADER).read()
-    return sorted(set(re.findall(r"^\s*(?:int|int64_t|const char\s*\*)\s*(bolt3_\w+)\s*\(", txt, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|int32_t|int64_t|const char\s*\*)\s*(bolt3_\w+)\s*\(", txt, re.M)))
 
 
 def test_header_declares_the_bound_functions():
@@ -97,7 +97,8 @@ def test_rejects_bad_arguments_without_gpu_work():
 STRUCTS = {"b3_heads_args": A.HeadsArgs, "b3_chain_args": A.ChainArgs, "b3_attn_args": A.AttnArgs,
            "b3_decode_args": A.DecodeArgs, "b3_decode_layer_args": A.DecodeLayerArgs,
            "b3_slot_keys_args": A.SlotKeysArgs, "b3_attn_bwd_args": A.AttnBwdArgs,
-           "b3_rms_norm_args": A.RmsNormArgs, "b3_chain_bwd_args": A.ChainBwdArgs}
+           "b3_rms_norm_args": A.RmsNormArgs, "b3_chain_bwd_args": A.ChainBwdArgs,
+           "b3_heads_bwd_args": A.HeadsBwdArgs}
 
 
 def _flat_fields(st, prefix=""):

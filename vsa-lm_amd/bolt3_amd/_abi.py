@@ -142,7 +142,20 @@ class ChainBwdArgs(C.Structure):
     ]
 
 
-EXPORTS = ("bolt3_attn_bwd", "bolt3_heads", "bolt3_chain", "bolt3_chain_bwd", "bolt3_chain_bwd_workspace_bytes",
+class HeadsBwdArgs(C.Structure):
+    _fields_ = [
+        ("dtype", i32), ("B", i32), ("T", i32), ("H", i32), ("HKV", i32), ("HD", i32), ("n_sinks", i32),
+        ("n_chunks", i32),
+        ("d_q_raw", p), ("d_q_rope", p), ("d_k_own", p), ("d_k_next", p), ("d_v_own", p), ("d_v_next", p),
+        ("d_sink_k", p), ("d_sink_v", p), ("d_k_chain", p), ("d_v_chain", p), ("d_beta", p), ("d_eta", p),
+        ("beta", p), ("eta", p), ("lin_q", p), ("lin_q_row_stride", i64), ("lin_k", p), ("lin_k_row_stride", i64),
+        ("qn_w", p), ("kn_w", p), ("has_qk_norm", i32), ("q_eps", f32), ("k_eps", f32), ("inv_freq", p),
+        ("dz", p), ("dz_row_stride", i64), ("dz_cols", i32), ("d_qn_w", p), ("d_kn_w", p),
+    ]
+
+
+EXPORTS = ("bolt3_attn_bwd", "bolt3_heads", "bolt3_heads_bwd", "bolt3_heads_bwd_blocks", "bolt3_chain",
+           "bolt3_chain_bwd", "bolt3_chain_bwd_workspace_bytes",
            "bolt3_chain_noalloc", "bolt3_chain_workspace_bytes", "bolt3_chunk_attn",
            "bolt3_decode",
            "bolt3_decode_layer", "bolt3_decode_layer_workspace_bytes", "bolt3_decode_workspace_bytes",
@@ -164,7 +177,8 @@ def load():
                      ("bolt3_chunk_attn", AttnArgs),
                      ("bolt3_decode", DecodeArgs), ("bolt3_decode_layer", DecodeLayerArgs),
                      ("bolt3_slot_keys", SlotKeysArgs), ("bolt3_attn_bwd", AttnBwdArgs),
-                     ("bolt3_rms_norm", RmsNormArgs), ("bolt3_chain_bwd", ChainBwdArgs)):
+                     ("bolt3_rms_norm", RmsNormArgs), ("bolt3_chain_bwd", ChainBwdArgs),
+                     ("bolt3_heads_bwd", HeadsBwdArgs)):
         fn = getattr(lib, name)
         fn.argtypes = [C.POINTER(st), p]
         fn.restype = C.c_int
@@ -172,6 +186,8 @@ def load():
     lib.bolt3_chain_workspace_bytes.restype = i64
     lib.bolt3_chain_bwd_workspace_bytes.argtypes = [i32, i32, i32, i32]
     lib.bolt3_chain_bwd_workspace_bytes.restype = i64
+    lib.bolt3_heads_bwd_blocks.argtypes = [i32, i32]
+    lib.bolt3_heads_bwd_blocks.restype = i32
     lib.bolt3_decode_layer_workspace_bytes.argtypes = [i32, i32, i32, i32, i32]
     lib.bolt3_decode_layer_workspace_bytes.restype = i64
     lib.bolt3_decode_workspace_bytes.argtypes = [i32, i32, i32, i32]
@@ -246,3 +262,7 @@ def chain_workspace_bytes(dt: torch.dtype, B: int, HKV: int, HD: int, S: int, n_
 
 def chain_bwd_workspace_bytes(B: int, HKV: int, HD: int, n_steps: int) -> int:
     return int(load().bolt3_chain_bwd_workspace_bytes(B, HKV, HD, n_steps))
+
+
+def heads_bwd_blocks(B: int, T: int) -> int:
+    return int(load().bolt3_heads_bwd_blocks(B, T))

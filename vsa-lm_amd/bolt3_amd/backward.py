@@ -37,15 +37,6 @@ def _rope_t(g: torch.Tensor, ang: torch.Tensor) -> torch.Tensor:
     return g * a.cos() - rot * a.sin()
 
 
-def _rms_bwd(x: torch.Tensor, w: torch.Tensor, dy: torch.Tensor, eps: float):
-    """y = x * rsqrt(mean(x^2) + eps) * w (statistic in fp32): (dx, dw) for fp32 x, dy."""
-    r = torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps)
-    g = dy * w
-    dx = r * g - x * r.pow(3) * (g * x).mean(-1, keepdim=True)
-    dw = (dy * x * r).reshape(-1, x.shape[-1]).sum(0)
-    return dx, dw
-
-
 def _snap_m(snap_m: torch.Tensor, i: int, split: bool, bh: int, HD: int) -> torch.Tensor:
     """M_res after step i as fp32 [bh, HD, HD] (bf16 snapshots hold M^T as bf16 hi then lo)."""
     if not split:
@@ -314,19 +305,11 @@ def layer_backward(mod, x: torch.Tensor, tr: dict, d_out: torch.Tensor, dt: torc
     dy = (d_out @ side["wo"]).float().contiguous()                  # [b, T, H*HD]
     # attention and readout
     o = attn_backward(mod, tr, dy, dt, n_steps)
-    pos = torch.arange(T, device=dev, dtype=torch.float32)
     inv_freq = mod.rope.inv_freq.to(dev).float()
-    ang_t = pos[:, None] * inv_freq                                # [T, HD/2]
-    d_krope = o["d_k_own"] + o["d_k_next"]
-    d_v = o["d_v_own"] + o["d_v_next"]
     gam = mod.gamma_delta().detach().to(dev)
     d_gam = o["d_gamma"].view(b, HKV, n_chunks).sum(dim=(0, 2))
-    d_beta = torch.zeros(b, HKV, T, device=dev)
-    d_kraw = torch.zeros(b, HKV, T, HD, device=dev)
     d_kappa = torch.zeros(HKV, device=dev)
     if n_steps > 0:
-        d_krope[:, :, :ns] += o["d_sink_k"].sum(0).view(b, HKV, ns, HD)
-        d_v[:, :, :ns] += o["d_sink_v"].sum(0).view(b, HKV, ns, HD)
         # kappa: the slot bias is kappa * log(max(mass, 1)) (vsa_lm/config/bolt3.py:238-241)
         dbias = o["d_bias"].sum(2).view(n_steps, b, HKV, G, S).sum(3)             # [step, b, HKV, S]
         logm = tr["snap_mass"].clamp_min(1.0).log().view(n_steps, b, HKV, S)
@@ -334,48 +317,52 @@ def layer_backward(mod, x: torch.Tensor, tr: dict, d_out: torch.Tensor, dt: torc
         if native_chain_ok(mod, dt):
             dk_c, dv_c, db_c, dg_c = chain_backward_hip(mod, tr, o, gam, b, n_steps)
         else:
+            pos = torch.arange(T, device=dev, dtype=torch.float32)
             steps, _, pms = replay_slots(tr["log"], pos, S, C, ns)
             dk_c, dv_c, db_c, dg_c = chain_backward(
                 steps, o["d_slot_k"], o["d_slot_v"], o["d_m"], pms, inv_freq, tr["k_raw"].reshape(bh, T, HD),
                 tr["v"].reshape(bh, T, HD), tr["beta"].reshape(bh, T), gam, tr["snap_m"], dt == torch.bfloat16, b,
                 HKV)
-        d_kraw += dk_c.view(b, HKV, T, HD)
-        d_v += dv_c.view(b, HKV, T, HD)
-        d_beta += db_c.view(b, HKV, T)
         d_gam += dg_c
-    d_kraw += _rope_t(d_krope, ang_t)
-    d_qraw = o["d_q_raw"] + _rope_t(o["d_q_rope"], ang_t)
-    dq = d_qraw.transpose(1, 2)                                      # [b, T, H, HD]
-    dk = d_kraw.transpose(1, 2)
-    if mod.q_norm is not None:
-        # q / k RMSNorm (the statistic in fp32, vsa_lm/surgery.py:48-52) on the projections,
-        # recomputed by the forward's own products
-        lin_q = torch.nn.functional.linear(x, side["wq"], side["bq"]).float()
-        lin_k = torch.nn.functional.linear(x, side["wkv"], side["bkv"])[..., :HKV * HD].float()
-        dq, grads["q_norm.weight"] = _rms_bwd(lin_q.view(b, T, H, HD), mod.q_norm.weight.float(), dq,
-                                              float(mod.q_norm.eps))
-        dk, grads["k_norm.weight"] = _rms_bwd(lin_k.reshape(b, T, HKV, HD), mod.k_norm.weight.float(), dk,
-                                              float(mod.k_norm.eps))
-    # gates: beta = sigmoid(.), eta = tanh(.) (vsa_lm/config/bolt3.py:198-199)
-    bet = tr["beta"].float()
-    d_zb = (d_beta * bet * (1.0 - bet)).transpose(1, 2)
-    eta = tr["eta"].float()
-    d_ze = (o["d_eta"] * (1.0 - eta * eta)).transpose(1, 2)
+    # RoPE transposes, the q / k norms' backward and the gates' derivatives, one pass over the
+    # token rows into dz, the gradient of the packed projection output [q | k | v | beta | eta | pad]
+    f32 = dict(device=dev, dtype=torch.float32)
+    dz = torch.empty(b * T, W.shape[0], dtype=dt, device=dev)
+    has_norm = mod.q_norm is not None
+    nb = A.heads_bwd_blocks(b, T)
+    ha = A.HeadsBwdArgs()
+    ha.dtype, ha.B, ha.T, ha.H, ha.HKV, ha.HD, ha.n_sinks, ha.n_chunks = A.dtype_code(dt), b, T, H, HKV, HD, ns, \
+        n_chunks
+    ha.d_q_raw, ha.d_q_rope = o["d_q_raw"].data_ptr(), o["d_q_rope"].data_ptr()
+    ha.d_k_own, ha.d_k_next = o["d_k_own"].data_ptr(), o["d_k_next"].data_ptr()
+    ha.d_v_own, ha.d_v_next = o["d_v_own"].data_ptr(), o["d_v_next"].data_ptr()
+    if n_steps > 0:
+        ha.d_sink_k, ha.d_sink_v = o["d_sink_k"].data_ptr(), o["d_sink_v"].data_ptr()
+        ha.d_k_chain, ha.d_v_chain, ha.d_beta = dk_c.data_ptr(), dv_c.data_ptr(), db_c.data_ptr()
+    ha.d_eta, ha.beta, ha.eta = o["d_eta"].data_ptr(), tr["beta"].data_ptr(), tr["eta"].data_ptr()
+    if has_norm:
+        lin_q, lin_kv = tr["lin_q"], tr["lin_kv"]
+        qn_w, kn_w = mod.q_norm.weight.detach().float().contiguous(), mod.k_norm.weight.detach().float().contiguous()
+        d_qn, d_kn = torch.empty(nb, HD, **f32), torch.empty(nb, HD, **f32)
+        ha.lin_q, ha.lin_q_row_stride = lin_q.data_ptr(), lin_q.shape[-1]
+        ha.lin_k, ha.lin_k_row_stride = lin_kv.data_ptr(), lin_kv.shape[-1]
+        ha.qn_w, ha.kn_w, ha.has_qk_norm = qn_w.data_ptr(), kn_w.data_ptr(), 1
+        ha.q_eps, ha.k_eps = float(mod.q_norm.eps), float(mod.k_norm.eps)
+        ha.d_qn_w, ha.d_kn_w = d_qn.data_ptr(), d_kn.data_ptr()
+    inv_f = inv_freq.contiguous()
+    ha.inv_freq = inv_f.data_ptr()
+    ha.dz, ha.dz_row_stride, ha.dz_cols = dz.data_ptr(), dz.shape[1], dz.shape[1]
+    A.call("bolt3_heads_bwd", ha, dev)
+    if has_norm:
+        grads["q_norm.weight"], grads["k_norm.weight"] = d_qn.sum(0), d_kn.sum(0)
+    widths = [H * HD, HKV * HD, HKV * HD, HKV, H]
     # one product each for dx and for the packed weight's gradient: rows q | k | v | beta | eta
-    parts = [dq.reshape(b, T, H * HD), dk.reshape(b, T, HKV * HD), d_v.transpose(1, 2).reshape(b, T, HKV * HD),
-             d_zb, d_ze]
-    widths = [t.shape[-1] for t in parts]
-    pad = W.shape[0] - sum(widths)
-    if pad:
-        parts.append(torch.zeros(b, T, pad, device=dev))
-    dz = torch.cat(parts, dim=-1).reshape(b * T, -1)
-    dz_s = dz.to(dt)
-    dx = (dz_s @ W).float()
-    dW = (dz_s.t() @ x.reshape(b * T, D)).float()
-    db = dz.sum(0)
+    dx = (dz @ W).float()
+    dW = (dz.t() @ x.reshape(b * T, D)).float()
+    lins = (mod.q_proj, mod.k_proj, mod.v_proj, mod.beta_proj, mod.eta_proj)
+    db = dz.float().sum(0) if any(lin.bias is not None for lin in lins) else None
     off = 0
-    for name, lin, width in zip(("q_proj", "k_proj", "v_proj", "beta_proj", "eta_proj"),
-                                (mod.q_proj, mod.k_proj, mod.v_proj, mod.beta_proj, mod.eta_proj), widths):
+    for name, lin, width in zip(("q_proj", "k_proj", "v_proj", "beta_proj", "eta_proj"), lins, widths):
         grads[f"{name}.weight"] = dW[off:off + width]
         if lin.bias is not None:
             grads[f"{name}.bias"] = db[off:off + width]

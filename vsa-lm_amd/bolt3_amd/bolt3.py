@@ -425,7 +425,8 @@ class Bolt3Attn(nn.Module):
         self._heads(lin_q, b, T, dt, side, 0, q_raw, q_rope, None, None, None, None, eta, lin_kv=lin_kv, parts=1,
                     gates=gates)
         if trace is not None:
-            trace.update(q_raw=q_raw, q_rope=q_rope, k_raw=k_raw, k_rope=k_rope, v=v, beta=beta, eta=eta, pos=pos)
+            trace.update(q_raw=q_raw, q_rope=q_rope, k_raw=k_raw, k_rope=k_rope, v=v, beta=beta, eta=eta, pos=pos,
+                         lin_q=lin_q, lin_kv=lin_kv)
 
         K = H * HD
         a = A.AttnArgs()

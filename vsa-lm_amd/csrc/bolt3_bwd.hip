@@ -434,37 +434,53 @@ constexpr float L2E = 1.4426950408889634f;
 
 // accumulator values as the B operand of K chunk kc (rows 8 kc .. 8 kc + 7 of the 16), bf16
 __device__ __forceinline__ u16x8 acc_operand(const f32x16& v, int kc) {
-  u16x8 b;
+  u32x4v b;
 #pragma unroll
-  for (int e = 0; e < 8; e += 2) {
-    const uint32_t u = pack_bf2(v[8 * kc + e], v[8 * kc + e + 1]);
-    b[e] = (uint16_t)(u & 0xffffu);
-    b[e + 1] = (uint16_t)(u >> 16);
-  }
-  return b;
+  for (int e = 0; e < 4; ++e) b[e] = pack_bf2(v[8 * kc + 2 * e], v[8 * kc + 2 * e + 1]);
+  return __builtin_bit_cast(u16x8, b);
 }
 
 // 8 fp32 values as bf16 (the dO rows)
 __device__ __forceinline__ u16x8 f32x8_to_bf(const float* p) {
   const float4 a = *reinterpret_cast<const float4*>(p), b = *reinterpret_cast<const float4*>(p + 4);
-  u16x8 r;
-  uint32_t u = pack_bf2(a.x, a.y);
-  r[0] = (uint16_t)u; r[1] = (uint16_t)(u >> 16);
-  u = pack_bf2(a.z, a.w);
-  r[2] = (uint16_t)u; r[3] = (uint16_t)(u >> 16);
-  u = pack_bf2(b.x, b.y);
-  r[4] = (uint16_t)u; r[5] = (uint16_t)(u >> 16);
-  u = pack_bf2(b.z, b.w);
-  r[6] = (uint16_t)u; r[7] = (uint16_t)(u >> 16);
-  return r;
+  const u32x4v r = {pack_bf2(a.x, a.y), pack_bf2(a.z, a.w), pack_bf2(b.x, b.y), pack_bf2(b.z, b.w)};
+  return __builtin_bit_cast(u16x8, r);
 }
 
-// score in log2 units: round_bf(q.k) * scale * log2(e) (+ slot bias * log2(e)); -inf when masked
-__device__ __forceinline__ float score2(const b3_attn_bwd_args& a, float dot, const KField& f, int j, int i,
-                                        float sl) {
-  if (j >= f.len || (f.kind == 3 && j > i)) return -INFINITY;
-  const float x = a.score_round ? round_bf(dot) : dot;
-  return f.kind == 1 ? fmaf(x, sl, f.bias[j] * L2E) : x * sl;
+
+// 16-byte piece p of row r of a [32][HD] tile whose pieces sit at p ^ (r % (HD/8))
+template <int HD>
+__device__ __forceinline__ u16x8 row_piece16(const uint16_t* t, int r, int p) {
+  return *reinterpret_cast<const u16x8*>(&t[r * HD + 8 * (p ^ (r % (HD / 8)))]);
+}
+
+// Scores of key block j0 of field f against the lane's query qi in log2 units (rows keys j0 +
+// d_row(lane, r), the forward's rounding, scale and slot bias), -inf where the key is past the
+// field or after the query in the own chunk.  q0: the first query of the tile.
+__device__ __forceinline__ void block_scores(const b3_attn_bwd_args& a, f32x16& st, const KField& f, int j0, int qi,
+                                             int q0, float sl, int lane) {
+  if (a.score_round) {
+#pragma unroll
+    for (int r = 0; r < 16; r += 2) {
+      const uint32_t u = pack_bf2(st[r], st[r + 1]);
+      st[r] = bf_lo(u);
+      st[r + 1] = bf_hi(u);
+    }
+  }
+  if (f.kind == 1) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) st[r] = fmaf(st[r], sl, f.bias[min(j0 + d_row(lane, r), f.len - 1)] * L2E);
+  } else {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) st[r] *= sl;
+  }
+  if (j0 + 32 > f.len || (f.kind == 3 && j0 + 31 > q0)) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int j = j0 + d_row(lane, r);
+      if (j >= f.len || (f.kind == 3 && j > qi)) st[r] = -INFINITY;
+    }
+  }
 }
 
 template <int HD>
@@ -530,20 +546,18 @@ __global__ void __launch_bounds__(64) attn_bwd_dq_mfma_kernel(b3_attn_bwd_args a
       f32x16 st = zero16();
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) mma_bf16(st, ka[ks], qf[ks]);
+      block_scores(a, st, f, j0, qi, q0, sl, lane);
       float bm = -INFINITY;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        st[r] = score2(a, st[r], f, j0 + d_row(lane, r), qi, sl);
-        bm = fmaxf(bm, st[r]);
-      }
+      for (int r = 0; r < 16; ++r) bm = fmaxf(bm, st[r]);
       bm = pair_max32(bm);
       const float mn = fmaxf(m_run, bm);
       if (mn == -INFINITY) continue;
       float ps = 0.f;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) ps += st[r] == -INFINITY ? 0.f : exp2f(st[r] - mn);
+      for (int r = 0; r < 16; ++r) ps += __builtin_amdgcn_exp2f(st[r] - mn);
       ps = pair_sum32(ps);
-      l_run = l_run * (m_run == -INFINITY ? 0.f : exp2f(m_run - mn)) + ps;
+      l_run = l_run * __builtin_amdgcn_exp2f(m_run - mn) + ps;
       m_run = mn;
     }
   }
@@ -570,10 +584,10 @@ __global__ void __launch_bounds__(64) attn_bwd_dq_mfma_kernel(b3_attn_bwd_args a
         mma_bf16(st, ka[ks], qf[ks]);
         mma_bf16(dpt, va[ks], of[ks]);
       }
+      block_scores(a, st, f, j0, qi, q0, sl, lane);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float x = score2(a, st[r], f, j0 + d_row(lane, r), qi, sl);
-        const float p = (x == -INFINITY || !qok) ? 0.f : exp2f(x - lse2);
+        const float p = qok ? __builtin_amdgcn_exp2f(st[r] - lse2) : 0.f;
         st[r] = p * (dpt[r] - drow);          // dS^T
       }
       if (f.kind == 1) {
@@ -608,35 +622,60 @@ __global__ void __launch_bounds__(64) attn_bwd_dq_mfma_kernel(b3_attn_bwd_args a
 }
 
 template <int HD>
-struct DkvMfmaSmem {
-  alignas(16) uint16_t q[32 * HD];    // the query tile, row-major, swizzled pieces
-  alignas(16) uint16_t o[32 * HD];    // its dO rows in bf16
-  float lse2[32], drow[32];
+struct Dkv4Smem {
+  alignas(16) uint16_t q[2][32 * HD];   // query tile, row-major, swizzled pieces (double buffer)
+  alignas(16) uint16_t o[2][32 * HD];   // its dO rows in bf16
+  float lse2[2][32], drow[2][32];
 };
 
-// dK, dV for one 32-key block of one field: lane l owns key l % 32; all query rows of the
-// chunk's G heads in 32-row tiles.
+// 8 fp32 values as bf16
+__device__ __forceinline__ u16x8 pack8_bf(const float* v) {
+  u32x4v r;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) r[e] = pack_bf2(v[2 * e], v[2 * e + 1]);
+  return __builtin_bit_cast(u16x8, r);
+}
+
+// dK, dV for 32-key blocks of one field, four blocks of one (bh, chunk) per workgroup (one per
+// wavefront; lane l owns key l % 32 of its block): the 32-row query tiles of the chunk's G heads
+// are staged once for all four by the whole workgroup, double-buffered so that the next tile's
+// loads are in flight during the current tile's products.  Per tile: S = Q K^T and dP = dO V^T
+// (tile rows as the A operand, the lane's key and value rows as B), P and dS, then
+// dV^T += dO^T P and dK^T += Q^T dS with dO^T, Q^T read transposed and P, dS in the
+// accumulator's row order.
 template <int HD>
-__global__ void __launch_bounds__(64) attn_bwd_dkv_mfma_kernel(b3_attn_bwd_args a) {
-  __shared__ DkvMfmaSmem<HD> sm;
+__global__ void __launch_bounds__(256) attn_bwd_dkv4_kernel(b3_attn_bwd_args a) {
+  __shared__ Dkv4Smem<HD> sm;
   constexpr int KS = HD / 16, NDB = HD / 32, NP = HD / 8;
-  const int lane = threadIdx.x, n = lane & 31, h = lane >> 5;
+  static_assert(NP == 16 || NP == 8, "head dim");
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, n = lane & 31, h = lane >> 5;
   const int bh = blockIdx.y, b = bh / a.HKV, hkv = bh % a.HKV, c = blockIdx.z;
   const int G = a.H / a.HKV;
   const int tc = chunk_len(a, c);
   const float sl = L2E / sqrtf((float)HD);
   const int n_fields = __popc(field_mask(a, c));
-  int fi = 0, j0 = blockIdx.x * 32;
+  // this wavefront's key block (none: the wavefront stages and waits, and writes nothing)
+  int fi = 0, j0 = (4 * (int)blockIdx.x + w) * 32;
   KField f = chunk_field<uint16_t>(a, b, hkv, c, 0);
+  bool have = true;
   while (j0 >= f.len) {
     j0 -= (f.len + 31) / 32 * 32;
-    if (++fi >= n_fields) return;
+    if (++fi >= n_fields) {
+      have = false;
+      break;
+    }
     f = chunk_field<uint16_t>(a, b, hkv, c, fi);
   }
+  if (!have) {
+    f = chunk_field<uint16_t>(a, b, hkv, c, 0);
+    j0 = 0;
+  }
   const int nk = min(32, f.len - j0);
-  const int j = j0 + n;                       // this lane's key
+  const int j = j0 + n;
   const TrLanes<HD> TL(lane);
-  // B operands: the lane's key and value rows
+  // this lane's key: valid, and its slot bias in log2 units
+  const bool kval = j < f.len;
+  const float kb2 = f.kind == 1 ? f.bias[min(j, f.len - 1)] * L2E : 0.f;
   u16x8 kf[KS], vf[KS];
   {
     const int kr = min(j, f.len - 1);
@@ -654,65 +693,100 @@ __global__ void __launch_bounds__(64) attn_bwd_dkv_mfma_kernel(b3_attn_bwd_args 
     dk[db] = zero16();
     dv[db] = zero16();
   }
-  for (int g = 0; g < G; ++g) {
-    const int hq = hkv * G + g;
-    for (int q0 = 0; q0 < tc; q0 += 32) {
-      const int nq = min(32, tc - q0);
-      if (f.kind == 3 && j0 > q0 + nq - 1) continue;   // every query of the tile precedes the keys
-      const long long row0 = ((long long)b * a.H + hq) * a.T + (long long)c * a.C + q0;
-      // the query tile and its dO rows into LDS (row n, piece 2 ks + h); rows past the chunk zero
-      {
-        const int qr = min(q0 + n, tc - 1);
-        const long long t = (long long)c * a.C + qr;
-        const uint16_t* qp = reinterpret_cast<const uint16_t*>(a.q_rope) + (long long)b * a.q_sb +
-                             (long long)hq * a.q_sh + t * HD;
-        const float* dp = a.dy + (long long)b * a.dy_sb + t * a.dy_st + (long long)hq * HD;
-        const bool ok = q0 + n < tc;
+  // staging: thread t takes row t / 8 of the tile, 16-byte pieces (t % 8) * NP / 8 .. (t % 8 + 1) * NP / 8 - 1
+  constexpr int PPT = NP / 8;   // pieces per thread (2 at HD = 128)
+  const int sr = tid >> 3, sp = (tid & 7) * PPT;
+  const int nqt = (tc + 31) / 32, n_it = G * nqt;
+  u16x8 pq[PPT];
+  float po[PPT][8];
+  float plse = INFINITY, pdrow = 0.f;
+  auto load = [&](int it) {
+    const int g = it / nqt, q0 = 32 * (it % nqt), hq = hkv * G + g;
+    const bool ok = q0 + sr < tc;
+    const long long t = (long long)c * a.C + min(q0 + sr, tc - 1);
+    const uint16_t* qp = reinterpret_cast<const uint16_t*>(a.q_rope) + (long long)b * a.q_sb + (long long)hq * a.q_sh +
+                         t * HD;
+    const float* dp = a.dy + (long long)b * a.dy_sb + t * a.dy_st + (long long)hq * HD;
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          u16x8 qv = *reinterpret_cast<const u16x8*>(qp + 16 * ks + 8 * h);
-          u16x8 ov = f32x8_to_bf(dp + 16 * ks + 8 * h);
-          if (!ok) {
-            qv = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
-            ov = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
-          }
-          const int slot = 8 * ((2 * ks + h) ^ (n % NP));
-          *reinterpret_cast<u16x8*>(&sm.q[n * HD + slot]) = qv;
-          *reinterpret_cast<u16x8*>(&sm.o[n * HD + slot]) = ov;
-        }
-        if (h == 0) {
-          sm.lse2[n] = ok ? a.lse[row0 + n] * L2E : INFINITY;
-          sm.drow[n] = ok ? a.d_rows[row0 + n] : 0.f;
-        }
+    for (int k = 0; k < PPT; ++k) {
+      const int p = sp + k;
+      pq[k] = ok ? *reinterpret_cast<const u16x8*>(qp + 8 * p) : u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+      float4 x0 = make_float4(0.f, 0.f, 0.f, 0.f), x1 = x0;
+      if (ok) {
+        x0 = *reinterpret_cast<const float4*>(dp + 8 * p);
+        x1 = *reinterpret_cast<const float4*>(dp + 8 * p + 4);
       }
-      // S = Q K^T and dP = dO V^T: rows queries (A operand from the tile rows), columns keys
+      po[k][0] = x0.x; po[k][1] = x0.y; po[k][2] = x0.z; po[k][3] = x0.w;
+      po[k][4] = x1.x; po[k][5] = x1.y; po[k][6] = x1.z; po[k][7] = x1.w;
+    }
+    if ((tid & 7) == 0) {
+      const long long row = ((long long)b * a.H + hq) * a.T + t;
+      plse = ok ? a.lse[row] * L2E : INFINITY;
+      pdrow = ok ? a.d_rows[row] : 0.f;
+    }
+  };
+  auto store = [&](int buf) {
+#pragma unroll
+    for (int k = 0; k < PPT; ++k) {
+      const int p = sp + k, off = sr * HD + 8 * (p ^ (sr % NP));
+      *reinterpret_cast<u16x8*>(&sm.q[buf][off]) = pq[k];
+      *reinterpret_cast<u16x8*>(&sm.o[buf][off]) = pack8_bf(po[k]);
+    }
+    if ((tid & 7) == 0) {
+      sm.lse2[buf][sr] = plse;
+      sm.drow[buf][sr] = pdrow;
+    }
+  };
+  load(0);
+  store(0);
+  __syncthreads();
+  for (int it = 0; it < n_it; ++it) {
+    const int buf = it & 1;
+    if (it + 1 < n_it) load(it + 1);
+    const int q0 = 32 * (it % nqt), nq = min(32, tc - q0);
+    if (have && !(f.kind == 3 && j0 > q0 + nq - 1)) {
+      const uint16_t* tq = sm.q[buf];
+      const uint16_t* to = sm.o[buf];
       f32x16 s = zero16(), dp = zero16();
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         const int slot = 8 * ((2 * ks + h) ^ (n % NP));
-        mma_bf16(s, *reinterpret_cast<const u16x8*>(&sm.q[n * HD + slot]), kf[ks]);
-        mma_bf16(dp, *reinterpret_cast<const u16x8*>(&sm.o[n * HD + slot]), vf[ks]);
+        mma_bf16(s, *reinterpret_cast<const u16x8*>(&tq[n * HD + slot]), kf[ks]);
+        mma_bf16(dp, *reinterpret_cast<const u16x8*>(&to[n * HD + slot]), vf[ks]);
       }
+      // scores as the forward's: round_bf(q.k) * scale * log2(e) + bias * log2(e); the causal
+      // mask of the own chunk only where the tile reaches past the block's first key
+      if (a.score_round) {
+#pragma unroll
+        for (int r = 0; r < 16; r += 2) {
+          const uint32_t u = pack_bf2(s[r], s[r + 1]);
+          s[r] = bf_lo(u);
+          s[r + 1] = bf_hi(u);
+        }
+      }
+      const bool causal = f.kind == 3 && j0 + 31 > q0;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int qr = d_row(lane, r);
-        const float x = score2(a, s[r], f, j, q0 + qr, sl);
-        const float p = x == -INFINITY ? 0.f : exp2f(x - sm.lse2[qr]);
+        const bool on = kval && !(causal && j > q0 + qr);
+        const float p = on ? __builtin_amdgcn_exp2f(fmaf(s[r], sl, kb2) - sm.lse2[buf][qr]) : 0.f;
         s[r] = p;
-        dp[r] = p * (dp[r] - sm.drow[qr]);     // dS
+        dp[r] = p * (dp[r] - sm.drow[buf][qr]);
       }
 #pragma unroll
       for (int kc = 0; kc < 2; ++kc) {
         const u16x8 bp = acc_operand(s, kc), bs = acc_operand(dp, kc);
 #pragma unroll
         for (int db = 0; db < NDB; ++db) {
-          mma_bf16(dv[db], tr_operand<HD>(sm.o, TL, db, kc), bp);
-          mma_bf16(dk[db], tr_operand<HD>(sm.q, TL, db, kc), bs);
+          mma_bf16(dv[db], tr_operand<HD>(to, TL, db, kc), bp);
+          mma_bf16(dk[db], tr_operand<HD>(tq, TL, db, kc), bs);
         }
       }
     }
+    if (it + 1 < n_it) store(buf ^ 1);
+    __syncthreads();
   }
-  if (n >= nk) return;
+  if (!have || n >= nk) return;
   const float scale = 1.0f / sqrtf((float)HD);
   float *ok, *ov;
   const long long HDl = HD;
@@ -1280,7 +1354,7 @@ static int launch(const b3_attn_bwd_args& a, hipStream_t st) {
     hipLaunchKernelGGL((attn_bwd_dq_mfma_kernel<HD>), dim3((a.C + 31) / 32, a.B * a.H, n_chunks), dim3(64), 0, st, a);
     e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
-    hipLaunchKernelGGL((attn_bwd_dkv_mfma_kernel<HD>), dim3(max_blocks, BH, n_chunks), dim3(64), 0, st, a);
+    hipLaunchKernelGGL((attn_bwd_dkv4_kernel<HD>), dim3((max_blocks + 3) / 4, BH, n_chunks), dim3(256), 0, st, a);
     return (int)hipGetLastError();
   }
   hipLaunchKernelGGL((attn_bwd_dq_kernel<T, HD>), dim3((a.C + BQ - 1) / BQ, a.B * a.H, n_chunks), dim3(NT),

@@ -240,23 +240,22 @@ template <int HD>
 __device__ __forceinline__ u16x8 tr_operand(const uint16_t* t, const TrLanes<HD>& L, int fb, int kc) {
   const uint16_t* p = t + 16 * kc * HD;
   const s16x4 a = lds_tr16(p + L.off[fb][0]), b = lds_tr16(p + L.off[fb][1]);
-  u16x8 r;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    r[e] = (uint16_t)a[e];
-    r[4 + e] = (uint16_t)b[e];
-  }
-  return r;
+  return __builtin_bit_cast(u16x8, __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
 // the accumulator's rows 8 kc .. 8 kc + 7 as a B operand split into bf16 hi and lo
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ void acc_operand_split(const f32x16& v, int kc, u16x8& hi, u16x8& lo) {
+  u32x4v h, l;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const uint16_t hb = f2bf(v[8 * kc + e]);
-    hi[e] = hb;
-    lo[e] = f2bf(v[8 * kc + e] - bf2f(hb));
+  for (int e = 0; e < 4; ++e) {
+    const float x0 = v[8 * kc + 2 * e], x1 = v[8 * kc + 2 * e + 1];
+    const uint32_t u = pack_bf2(x0, x1);
+    h[e] = u;
+    l[e] = pack_bf2(x0 - bf_lo(u), x1 - bf_hi(u));
   }
+  hi = __builtin_bit_cast(u16x8, h);
+  lo = __builtin_bit_cast(u16x8, l);
 }
 
 }  // namespace b3

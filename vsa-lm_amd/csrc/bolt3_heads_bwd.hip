@@ -4,9 +4,9 @@
 // dtype.  Replaces the autograd of vsa_lm/config/bolt3.py:196-215 (projections' outputs through
 // the norms, RoPE and gates) and vsa_lm/surgery.py:48-52, :86-93.
 //
-// One workgroup of four wavefronts takes RPB token rows; a wavefront takes one head of a row at a
-// time, lane j holding the RoPE pair (j, j + HD/2), so the rotation's transpose is lane-local and
-// the norm statistics are wavefront sums.
+// One workgroup of four wavefronts takes RPB token rows; a wavefront takes four heads of a row at
+// a time (all their loads issued before the first sum), lane j holding the RoPE pair (j, j + HD/2),
+// so the rotation's transpose is lane-local and the norm statistics are wavefront sums.
 #include <math.h>
 
 #include "bolt3_common.h"
@@ -52,7 +52,6 @@ __global__ void __launch_bounds__(NT) heads_bwd_kernel(b3_heads_bwd_args a) {
   float dqw0 = 0.f, dqw1 = 0.f, dkw0 = 0.f, dkw1 = 0.f;
   const long long BT = (long long)a.B * a.T;
   const long long BH = (long long)a.B * HKV;
-  const int U = H + 2 * HKV;
   for (int rr = 0; rr < RPB; ++rr) {
     const long long row = (long long)blockIdx.x * RPB + rr;
     if (row >= BT) break;
@@ -60,71 +59,83 @@ __global__ void __launch_bounds__(NT) heads_bwd_kernel(b3_heads_bwd_args a) {
     T* dz = reinterpret_cast<T*>(a.dz) + row * a.dz_row_stride;
     float sn, cs;
     sincosf((float)t * invf, &sn, &cs);
-    for (int u = w; u < U; u += 4) {
-      float g0, g1;
-      if (u < H) {
-        const long long base = (((long long)b * H + u) * a.T + t) * HD;
-        const float r0 = on ? a.d_q_rope[base + j] : 0.f, r1 = on ? a.d_q_rope[base + j + half] : 0.f;
-        g0 = (on ? a.d_q_raw[base + j] : 0.f) + (r0 * cs + r1 * sn);
-        g1 = (on ? a.d_q_raw[base + j + half] : 0.f) + (r1 * cs - r0 * sn);
-        if (a.has_qk_norm) {
+    // query heads u = w + 4 i, four at a time: every load of the four first, then the sums
+    for (int i0 = 0; i0 < H; i0 += 16) {
+      float q0[4], q1[4], r0[4], r1[4], x0[4], x1[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int u = i0 + w + 4 * k;
+        const bool ok = on && u < H;
+        const long long base = (((long long)b * H + min(u, H - 1)) * a.T + t) * HD;
+        q0[k] = ok ? a.d_q_raw[base + j] : 0.f;
+        q1[k] = ok ? a.d_q_raw[base + j + half] : 0.f;
+        r0[k] = ok ? a.d_q_rope[base + j] : 0.f;
+        r1[k] = ok ? a.d_q_rope[base + j + half] : 0.f;
+        x0[k] = x1[k] = 0.f;
+        if (a.has_qk_norm && ok) {
           const T* lq = reinterpret_cast<const T*>(a.lin_q) + row * a.lin_q_row_stride + (long long)u * HD;
-          const float x0 = on ? St<T>::ld(lq + j) : 0.f, x1 = on ? St<T>::ld(lq + j + half) : 0.f;
-          rms_bwd_pair(g0, g1, x0, x1, qw0, qw1, a.q_eps, HD, dqw0, dqw1);
+          x0[k] = St<T>::ld(lq + j);
+          x1[k] = St<T>::ld(lq + j + half);
         }
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int u = i0 + w + 4 * k;
+        if (u >= H) break;   // uniform over the wavefront
+        float g0 = q0[k] + (r0[k] * cs + r1[k] * sn), g1 = q1[k] + (r1[k] * cs - r0[k] * sn);
+        if (a.has_qk_norm) rms_bwd_pair(g0, g1, x0[k], x1[k], qw0, qw1, a.q_eps, HD, dqw0, dqw1);
         if (on) {
           dz[(long long)u * HD + j] = St<T>::from_f(g0);
           dz[(long long)u * HD + j + half] = St<T>::from_f(g1);
         }
-      } else if (u < H + HKV) {
-        const int hk = u - H;
-        const long long bh = (long long)b * HKV + hk;
+      }
+    }
+    // kv heads hk = w + 4 i, four at a time: keys, then values
+    for (int i0 = 0; i0 < HKV; i0 += 16) {
+      float k0[4], k1[4], c0[4], c1[4], x0[4], x1[4], v0[4], v1[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int hk = i0 + w + 4 * k;
+        const bool ok = on && hk < HKV;
+        const long long bh = (long long)b * HKV + min(hk, HKV - 1);
         const long long base = (bh * a.T + t) * HD;
-        float r0 = 0.f, r1 = 0.f;
-        if (on) {
-          r0 = a.d_k_own[base + j] + a.d_k_next[base + j];
-          r1 = a.d_k_own[base + j + half] + a.d_k_next[base + j + half];
-          if (a.d_sink_k && t < a.n_sinks)
-            for (int c = 0; c < a.n_chunks; ++c) {
-              const long long sb = (((long long)c * BH + bh) * a.n_sinks + t) * HD;
-              r0 += a.d_sink_k[sb + j];
-              r1 += a.d_sink_k[sb + j + half];
-            }
+        k0[k] = ok ? a.d_k_own[base + j] + a.d_k_next[base + j] : 0.f;
+        k1[k] = ok ? a.d_k_own[base + j + half] + a.d_k_next[base + j + half] : 0.f;
+        v0[k] = ok ? a.d_v_own[base + j] + a.d_v_next[base + j] : 0.f;
+        v1[k] = ok ? a.d_v_own[base + j + half] + a.d_v_next[base + j + half] : 0.f;
+        if (ok && a.d_sink_k && t < a.n_sinks)
+          for (int cc = 0; cc < a.n_chunks; ++cc) {
+            const long long sb = (((long long)cc * BH + bh) * a.n_sinks + t) * HD;
+            k0[k] += a.d_sink_k[sb + j];
+            k1[k] += a.d_sink_k[sb + j + half];
+            v0[k] += a.d_sink_v[sb + j];
+            v1[k] += a.d_sink_v[sb + j + half];
+          }
+        c0[k] = c1[k] = 0.f;
+        if (ok && a.d_k_chain) {
+          c0[k] = a.d_k_chain[base + j];
+          c1[k] = a.d_k_chain[base + j + half];
+          v0[k] += a.d_v_chain[base + j];
+          v1[k] += a.d_v_chain[base + j + half];
         }
-        g0 = r0 * cs + r1 * sn;
-        g1 = r1 * cs - r0 * sn;
-        if (a.d_k_chain && on) {
-          g0 += a.d_k_chain[base + j];
-          g1 += a.d_k_chain[base + j + half];
-        }
-        if (a.has_qk_norm) {
+        x0[k] = x1[k] = 0.f;
+        if (a.has_qk_norm && ok) {
           const T* lk = reinterpret_cast<const T*>(a.lin_k) + row * a.lin_k_row_stride + (long long)hk * HD;
-          const float x0 = on ? St<T>::ld(lk + j) : 0.f, x1 = on ? St<T>::ld(lk + j + half) : 0.f;
-          rms_bwd_pair(g0, g1, x0, x1, kw0, kw1, a.k_eps, HD, dkw0, dkw1);
+          x0[k] = St<T>::ld(lk + j);
+          x1[k] = St<T>::ld(lk + j + half);
         }
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int hk = i0 + w + 4 * k;
+        if (hk >= HKV) break;   // uniform over the wavefront
+        float g0 = c0[k] + (k0[k] * cs + k1[k] * sn), g1 = c1[k] + (k1[k] * cs - k0[k] * sn);
+        if (a.has_qk_norm) rms_bwd_pair(g0, g1, x0[k], x1[k], kw0, kw1, a.k_eps, HD, dkw0, dkw1);
         if (on) {
           dz[(long long)(H + hk) * HD + j] = St<T>::from_f(g0);
           dz[(long long)(H + hk) * HD + j + half] = St<T>::from_f(g1);
-        }
-      } else {
-        const int hk = u - H - HKV;
-        const long long bh = (long long)b * HKV + hk;
-        const long long base = (bh * a.T + t) * HD;
-        if (on) {
-          g0 = a.d_v_own[base + j] + a.d_v_next[base + j];
-          g1 = a.d_v_own[base + j + half] + a.d_v_next[base + j + half];
-          if (a.d_sink_v && t < a.n_sinks)
-            for (int c = 0; c < a.n_chunks; ++c) {
-              const long long sb = (((long long)c * BH + bh) * a.n_sinks + t) * HD;
-              g0 += a.d_sink_v[sb + j];
-              g1 += a.d_sink_v[sb + j + half];
-            }
-          if (a.d_v_chain) {
-            g0 += a.d_v_chain[base + j];
-            g1 += a.d_v_chain[base + j + half];
-          }
-          dz[(long long)(H + HKV + hk) * HD + j] = St<T>::from_f(g0);
-          dz[(long long)(H + HKV + hk) * HD + j + half] = St<T>::from_f(g1);
+          dz[(long long)(H + HKV + hk) * HD + j] = St<T>::from_f(v0[k]);
+          dz[(long long)(H + HKV + hk) * HD + j + half] = St<T>::from_f(v1[k]);
         }
       }
     }

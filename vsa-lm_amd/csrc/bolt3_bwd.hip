@@ -622,60 +622,37 @@ __global__ void __launch_bounds__(64) attn_bwd_dq_mfma_kernel(b3_attn_bwd_args a
 }
 
 template <int HD>
-struct Dkv4Smem {
-  alignas(16) uint16_t q[2][32 * HD];   // query tile, row-major, swizzled pieces (double buffer)
-  alignas(16) uint16_t o[2][32 * HD];   // its dO rows in bf16
-  float lse2[2][32], drow[2][32];
+struct DkvMfmaSmem {
+  alignas(16) uint16_t q[32 * HD];    // the query tile, row-major, swizzled pieces
+  alignas(16) uint16_t o[32 * HD];    // its dO rows in bf16
+  float lse2[32], drow[32];
 };
 
-// 8 fp32 values as bf16
-__device__ __forceinline__ u16x8 pack8_bf(const float* v) {
-  u32x4v r;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) r[e] = pack_bf2(v[2 * e], v[2 * e + 1]);
-  return __builtin_bit_cast(u16x8, r);
-}
-
-// dK, dV for 32-key blocks of one field, four blocks of one (bh, chunk) per workgroup (one per
-// wavefront; lane l owns key l % 32 of its block): the 32-row query tiles of the chunk's G heads
-// are staged once for all four by the whole workgroup, double-buffered so that the next tile's
-// loads are in flight during the current tile's products.  Per tile: S = Q K^T and dP = dO V^T
-// (tile rows as the A operand, the lane's key and value rows as B), P and dS, then
-// dV^T += dO^T P and dK^T += Q^T dS with dO^T, Q^T read transposed and P, dS in the
-// accumulator's row order.
+// dK, dV for one 32-key block of one field: lane l owns key l % 32; all query rows of the
+// chunk's G heads in 32-row tiles.
 template <int HD>
-__global__ void __launch_bounds__(256) attn_bwd_dkv4_kernel(b3_attn_bwd_args a) {
-  __shared__ Dkv4Smem<HD> sm;
+__global__ void __launch_bounds__(64) attn_bwd_dkv_mfma_kernel(b3_attn_bwd_args a) {
+  __shared__ DkvMfmaSmem<HD> sm;
   constexpr int KS = HD / 16, NDB = HD / 32, NP = HD / 8;
-  static_assert(NP == 16 || NP == 8, "head dim");
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, n = lane & 31, h = lane >> 5;
+  const int lane = threadIdx.x, n = lane & 31, h = lane >> 5;
   const int bh = blockIdx.y, b = bh / a.HKV, hkv = bh % a.HKV, c = blockIdx.z;
   const int G = a.H / a.HKV;
   const int tc = chunk_len(a, c);
   const float sl = L2E / sqrtf((float)HD);
   const int n_fields = __popc(field_mask(a, c));
-  // this wavefront's key block (none: the wavefront stages and waits, and writes nothing)
-  int fi = 0, j0 = (4 * (int)blockIdx.x + w) * 32;
+  int fi = 0, j0 = blockIdx.x * 32;
   KField f = chunk_field<uint16_t>(a, b, hkv, c, 0);
-  bool have = true;
   while (j0 >= f.len) {
     j0 -= (f.len + 31) / 32 * 32;
-    if (++fi >= n_fields) {
-      have = false;
-      break;
-    }
+    if (++fi >= n_fields) return;
     f = chunk_field<uint16_t>(a, b, hkv, c, fi);
   }
-  if (!have) {
-    f = chunk_field<uint16_t>(a, b, hkv, c, 0);
-    j0 = 0;
-  }
   const int nk = min(32, f.len - j0);
-  const int j = j0 + n;
+  const int j = j0 + n;                       // this lane's key
   const TrLanes<HD> TL(lane);
-  // this lane's key: valid, and its slot bias in log2 units
   const bool kval = j < f.len;
   const float kb2 = f.kind == 1 ? f.bias[min(j, f.len - 1)] * L2E : 0.f;
+  // B operands: the lane's key and value rows
   u16x8 kf[KS], vf[KS];
   {
     const int kr = min(j, f.len - 1);
@@ -693,69 +670,45 @@ __global__ void __launch_bounds__(256) attn_bwd_dkv4_kernel(b3_attn_bwd_args a) 
     dk[db] = zero16();
     dv[db] = zero16();
   }
-  // staging: thread t takes row t / 8 of the tile, 16-byte pieces (t % 8) * NP / 8 .. (t % 8 + 1) * NP / 8 - 1
-  constexpr int PPT = NP / 8;   // pieces per thread (2 at HD = 128)
-  const int sr = tid >> 3, sp = (tid & 7) * PPT;
-  const int nqt = (tc + 31) / 32, n_it = G * nqt;
-  u16x8 pq[PPT];
-  float po[PPT][8];
-  float plse = INFINITY, pdrow = 0.f;
-  auto load = [&](int it) {
-    const int g = it / nqt, q0 = 32 * (it % nqt), hq = hkv * G + g;
-    const bool ok = q0 + sr < tc;
-    const long long t = (long long)c * a.C + min(q0 + sr, tc - 1);
-    const uint16_t* qp = reinterpret_cast<const uint16_t*>(a.q_rope) + (long long)b * a.q_sb + (long long)hq * a.q_sh +
-                         t * HD;
-    const float* dp = a.dy + (long long)b * a.dy_sb + t * a.dy_st + (long long)hq * HD;
+  for (int g = 0; g < G; ++g) {
+    const int hq = hkv * G + g;
+    for (int q0 = 0; q0 < tc; q0 += 32) {
+      const int nq = min(32, tc - q0);
+      if (f.kind == 3 && j0 > q0 + nq - 1) continue;   // every query of the tile precedes the keys
+      const long long row0 = ((long long)b * a.H + hq) * a.T + (long long)c * a.C + q0;
+      // the query tile and its dO rows into LDS (row n, piece 2 ks + h); rows past the chunk zero
+      {
+        const int qr = min(q0 + n, tc - 1);
+        const long long t = (long long)c * a.C + qr;
+        const uint16_t* qp = reinterpret_cast<const uint16_t*>(a.q_rope) + (long long)b * a.q_sb +
+                             (long long)hq * a.q_sh + t * HD;
+        const float* dp = a.dy + (long long)b * a.dy_sb + t * a.dy_st + (long long)hq * HD;
+        const bool ok = q0 + n < tc;
 #pragma unroll
-    for (int k = 0; k < PPT; ++k) {
-      const int p = sp + k;
-      pq[k] = ok ? *reinterpret_cast<const u16x8*>(qp + 8 * p) : u16x8{0, 0, 0, 0, 0, 0, 0, 0};
-      float4 x0 = make_float4(0.f, 0.f, 0.f, 0.f), x1 = x0;
-      if (ok) {
-        x0 = *reinterpret_cast<const float4*>(dp + 8 * p);
-        x1 = *reinterpret_cast<const float4*>(dp + 8 * p + 4);
+        for (int ks = 0; ks < KS; ++ks) {
+          u16x8 qv = *reinterpret_cast<const u16x8*>(qp + 16 * ks + 8 * h);
+          u16x8 ov = f32x8_to_bf(dp + 16 * ks + 8 * h);
+          if (!ok) {
+            qv = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+            ov = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+          }
+          const int slot = 8 * ((2 * ks + h) ^ (n % NP));
+          *reinterpret_cast<u16x8*>(&sm.q[n * HD + slot]) = qv;
+          *reinterpret_cast<u16x8*>(&sm.o[n * HD + slot]) = ov;
+        }
+        if (h == 0) {
+          sm.lse2[n] = ok ? a.lse[row0 + n] * L2E : INFINITY;
+          sm.drow[n] = ok ? a.d_rows[row0 + n] : 0.f;
+        }
       }
-      po[k][0] = x0.x; po[k][1] = x0.y; po[k][2] = x0.z; po[k][3] = x0.w;
-      po[k][4] = x1.x; po[k][5] = x1.y; po[k][6] = x1.z; po[k][7] = x1.w;
-    }
-    if ((tid & 7) == 0) {
-      const long long row = ((long long)b * a.H + hq) * a.T + t;
-      plse = ok ? a.lse[row] * L2E : INFINITY;
-      pdrow = ok ? a.d_rows[row] : 0.f;
-    }
-  };
-  auto store = [&](int buf) {
-#pragma unroll
-    for (int k = 0; k < PPT; ++k) {
-      const int p = sp + k, off = sr * HD + 8 * (p ^ (sr % NP));
-      *reinterpret_cast<u16x8*>(&sm.q[buf][off]) = pq[k];
-      *reinterpret_cast<u16x8*>(&sm.o[buf][off]) = pack8_bf(po[k]);
-    }
-    if ((tid & 7) == 0) {
-      sm.lse2[buf][sr] = plse;
-      sm.drow[buf][sr] = pdrow;
-    }
-  };
-  load(0);
-  store(0);
-  __syncthreads();
-  for (int it = 0; it < n_it; ++it) {
-    const int buf = it & 1;
-    if (it + 1 < n_it) load(it + 1);
-    const int q0 = 32 * (it % nqt), nq = min(32, tc - q0);
-    if (have && !(f.kind == 3 && j0 > q0 + nq - 1)) {
-      const uint16_t* tq = sm.q[buf];
-      const uint16_t* to = sm.o[buf];
+      // S = Q K^T and dP = dO V^T: rows queries (A operand from the tile rows), columns keys
       f32x16 s = zero16(), dp = zero16();
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         const int slot = 8 * ((2 * ks + h) ^ (n % NP));
-        mma_bf16(s, *reinterpret_cast<const u16x8*>(&tq[n * HD + slot]), kf[ks]);
-        mma_bf16(dp, *reinterpret_cast<const u16x8*>(&to[n * HD + slot]), vf[ks]);
+        mma_bf16(s, *reinterpret_cast<const u16x8*>(&sm.q[n * HD + slot]), kf[ks]);
+        mma_bf16(dp, *reinterpret_cast<const u16x8*>(&sm.o[n * HD + slot]), vf[ks]);
       }
-      // scores as the forward's: round_bf(q.k) * scale * log2(e) + bias * log2(e); the causal
-      // mask of the own chunk only where the tile reaches past the block's first key
       if (a.score_round) {
 #pragma unroll
         for (int r = 0; r < 16; r += 2) {
@@ -769,24 +722,22 @@ __global__ void __launch_bounds__(256) attn_bwd_dkv4_kernel(b3_attn_bwd_args a) 
       for (int r = 0; r < 16; ++r) {
         const int qr = d_row(lane, r);
         const bool on = kval && !(causal && j > q0 + qr);
-        const float p = on ? __builtin_amdgcn_exp2f(fmaf(s[r], sl, kb2) - sm.lse2[buf][qr]) : 0.f;
+        const float p = on ? __builtin_amdgcn_exp2f(fmaf(s[r], sl, kb2) - sm.lse2[qr]) : 0.f;
         s[r] = p;
-        dp[r] = p * (dp[r] - sm.drow[buf][qr]);
+        dp[r] = p * (dp[r] - sm.drow[qr]);     // dS
       }
 #pragma unroll
       for (int kc = 0; kc < 2; ++kc) {
         const u16x8 bp = acc_operand(s, kc), bs = acc_operand(dp, kc);
 #pragma unroll
         for (int db = 0; db < NDB; ++db) {
-          mma_bf16(dv[db], tr_operand<HD>(to, TL, db, kc), bp);
-          mma_bf16(dk[db], tr_operand<HD>(tq, TL, db, kc), bs);
+          mma_bf16(dv[db], tr_operand<HD>(sm.o, TL, db, kc), bp);
+          mma_bf16(dk[db], tr_operand<HD>(sm.q, TL, db, kc), bs);
         }
       }
     }
-    if (it + 1 < n_it) store(buf ^ 1);
-    __syncthreads();
   }
-  if (!have || n >= nk) return;
+  if (n >= nk) return;
   const float scale = 1.0f / sqrtf((float)HD);
   float *ok, *ov;
   const long long HDl = HD;
@@ -1354,7 +1305,7 @@ static int launch(const b3_attn_bwd_args& a, hipStream_t st) {
     hipLaunchKernelGGL((attn_bwd_dq_mfma_kernel<HD>), dim3((a.C + 31) / 32, a.B * a.H, n_chunks), dim3(64), 0, st, a);
     e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
-    hipLaunchKernelGGL((attn_bwd_dkv4_kernel<HD>), dim3((max_blocks + 3) / 4, BH, n_chunks), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((attn_bwd_dkv_mfma_kernel<HD>), dim3(max_blocks, BH, n_chunks), dim3(64), 0, st, a);
     return (int)hipGetLastError();
   }
   hipLaunchKernelGGL((attn_bwd_dq_kernel<T, HD>), dim3((a.C + BQ - 1) / BQ, a.B * a.H, n_chunks), dim3(NT),

@@ -27,6 +27,7 @@
 #include <math.h>
 
 #include "bolt3_common.h"
+#include "bolt3_math.h"
 #include "bolt3_amd.h"
 
 namespace b3 {
@@ -205,7 +206,7 @@ __global__ void __launch_bounds__(NT) slot_rec_kernel(b3_chain_bwd_args a) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           float sn, cs;
-          sincosf(p * invf[e], &sn, &cs);
+          sincos_rope(p * invf[e], &sn, &cs);   // the forward RoPE's own values
           grow[e] += lo[e] * cs + hi[e] * sn;
           grow[8 + e] += hi[e] * cs - lo[e] * sn;
         }

@@ -10,6 +10,7 @@
 #include <math.h>
 
 #include "bolt3_common.h"
+#include "bolt3_math.h"
 #include "bolt3_amd.h"
 
 namespace b3 {
@@ -58,7 +59,7 @@ __global__ void __launch_bounds__(NT) heads_bwd_kernel(b3_heads_bwd_args a) {
     const int b = (int)(row / a.T), t = (int)(row % a.T);
     T* dz = reinterpret_cast<T*>(a.dz) + row * a.dz_row_stride;
     float sn, cs;
-    sincosf((float)t * invf, &sn, &cs);
+    sincos_rope((float)t * invf, &sn, &cs);   // the forward RoPE's own values
     // query heads u = w + 4 i, four at a time: every load of the four first, then the sums
     for (int i0 = 0; i0 < H; i0 += 16) {
       float q0[4], q1[4], r0[4], r1[4], x0[4], x1[4];

@@ -299,7 +299,7 @@ typedef struct {
   float eps;
   const void* y;              /* forward output before o_proj, (b, t, h, d) at + b*y_sb + t*y_st + h*HD + d */
   int64_t y_sb, y_st;
-  const float* dy;            /* its gradient, fp32, (b, t, h, d) at + b*dy_sb + t*dy_st + h*HD + d */
+  const void* dy;             /* its gradient in the storage dtype, (b, t, h, d) at + b*dy_sb + t*dy_st + h*HD + d */
   int64_t dy_sb, dy_st;
   float* d_rows;              /* [B][H][T] written: sum over d of dy * attention output */
   float* lse;                 /* [B][H][T] written: log-sum-exp of every query row */

@@ -302,7 +302,7 @@ def layer_backward(mod, x: torch.Tensor, tr: dict, d_out: torch.Tensor, dt: torc
     # o_proj
     y = tr["y"]
     grads["o_proj.weight"] = (d_out.reshape(-1, D).t() @ y.reshape(-1, H * HD)).float()
-    dy = (d_out @ side["wo"]).float().contiguous()                  # [b, T, H*HD]
+    dy = (d_out @ side["wo"]).contiguous()                          # [b, T, H*HD], storage dtype
     # attention and readout
     o = attn_backward(mod, tr, dy, dt, n_steps)
     inv_freq = mod.rope.inv_freq.to(dev).float()

@@ -169,7 +169,7 @@ __global__ void __launch_bounds__(NT) attn_bwd_dq_kernel(b3_attn_bwd_args a) {
   stage_rows<T, HD>(&sm.q[0][0], LS, reinterpret_cast<const T*>(a.q_rope) + (long long)b * a.q_sb +
                                          (long long)h * a.q_sh + ((long long)c * a.C + q0) * HD,
                     HD, BQ, nq, tid);
-  stage_rows<float, HD>(&sm.dout[0][0], LS, a.dy + (long long)b * a.dy_sb + ((long long)c * a.C + q0) * a.dy_st +
+  stage_rows<float, HD>(&sm.dout[0][0], LS, reinterpret_cast<const float*>(a.dy) + (long long)b * a.dy_sb + ((long long)c * a.C + q0) * a.dy_st +
                                                 (long long)h * HD,
                         a.dy_st, BQ, nq, tid);
   float drow[4];
@@ -334,7 +334,7 @@ __global__ void __launch_bounds__(NT) attn_bwd_dkv_kernel(b3_attn_bwd_args a) {
                                              (long long)h * a.q_sh + ((long long)c * a.C + q0) * HD,
                         HD, BQ, nq, tid);
       stage_rows<float, HD>(&sm.dout[0][0], LS,
-                            a.dy + (long long)b * a.dy_sb + ((long long)c * a.C + q0) * a.dy_st + (long long)h * HD,
+                            reinterpret_cast<const float*>(a.dy) + (long long)b * a.dy_sb + ((long long)c * a.C + q0) * a.dy_st + (long long)h * HD,
                             a.dy_st, BQ, nq, tid);
       if (tid < BQ) {
         sm.lse[tid] = tid < nq ? a.lse[row0 + tid] : INFINITY;
@@ -509,12 +509,12 @@ __global__ void __launch_bounds__(64) attn_bwd_dq_mfma_kernel(b3_attn_bwd_args a
   {
     const uint16_t* qr = reinterpret_cast<const uint16_t*>(a.q_rope) + (long long)b * a.q_sb + (long long)hq * a.q_sh +
                          min(t, (long long)c * a.C + tc - 1) * HD;
-    const float* dr = a.dy + (long long)b * a.dy_sb + min(t, (long long)c * a.C + tc - 1) * a.dy_st +
-                      (long long)hq * HD;
+    const uint16_t* dr = reinterpret_cast<const uint16_t*>(a.dy) + (long long)b * a.dy_sb +
+                         min(t, (long long)c * a.C + tc - 1) * a.dy_st + (long long)hq * HD;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       qf[ks] = *reinterpret_cast<const u16x8*>(qr + 16 * ks + 8 * h);
-      of[ks] = f32x8_to_bf(dr + 16 * ks + 8 * h);
+      of[ks] = *reinterpret_cast<const u16x8*>(dr + 16 * ks + 8 * h);
       if (!qok) {
         qf[ks] = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
         of[ks] = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
@@ -682,12 +682,13 @@ __global__ void __launch_bounds__(64) attn_bwd_dkv_mfma_kernel(b3_attn_bwd_args 
         const long long t = (long long)c * a.C + qr;
         const uint16_t* qp = reinterpret_cast<const uint16_t*>(a.q_rope) + (long long)b * a.q_sb +
                              (long long)hq * a.q_sh + t * HD;
-        const float* dp = a.dy + (long long)b * a.dy_sb + t * a.dy_st + (long long)hq * HD;
+        const uint16_t* dp = reinterpret_cast<const uint16_t*>(a.dy) + (long long)b * a.dy_sb + t * a.dy_st +
+                             (long long)hq * HD;
         const bool ok = q0 + n < tc;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
           u16x8 qv = *reinterpret_cast<const u16x8*>(qp + 16 * ks + 8 * h);
-          u16x8 ov = f32x8_to_bf(dp + 16 * ks + 8 * h);
+          u16x8 ov = *reinterpret_cast<const u16x8*>(dp + 16 * ks + 8 * h);
           if (!ok) {
             qv = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
             ov = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
@@ -826,7 +827,7 @@ __global__ void __launch_bounds__(NT) readout_bwd_kernel(b3_attn_bwd_args a) {
 #pragma unroll
     for (int e = 0; e < DPT; ++e) { dyv[e] = 0.f; yv[e] = 0.f; }
     if (live) {
-      const float* dyp = a.dy + (long long)b * a.dy_sb + t * a.dy_st + (long long)h * HD + DPT * dg;
+      const float* dyp = reinterpret_cast<const float*>(a.dy) + (long long)b * a.dy_sb + t * a.dy_st + (long long)h * HD + DPT * dg;
       const T* yp = reinterpret_cast<const T*>(a.y) + (long long)b * a.y_sb + t * a.y_st + (long long)h * HD + DPT * dg;
 #pragma unroll
       for (int e = 0; e < DPT; ++e) { dyv[e] = dyp[e]; yv[e] = St<T>::ld(yp + e); }
@@ -1010,11 +1011,12 @@ __global__ void __launch_bounds__(256) readout_bwd_mfma_kernel(b3_attn_bwd_args 
       const long long t = (long long)c * a.C + i;
       float dd = 0.f;
       if (live) {
-        const float* dyp = a.dy + (long long)b * a.dy_sb + t * a.dy_st + (long long)hq * HD + DPT * dg;
+        const uint16_t* dyp = reinterpret_cast<const uint16_t*>(a.dy) + (long long)b * a.dy_sb + t * a.dy_st +
+                              (long long)hq * HD + DPT * dg;
         const uint16_t* yp = reinterpret_cast<const uint16_t*>(a.y) + (long long)b * a.y_sb + t * a.y_st +
                              (long long)hq * HD + DPT * dg;
 #pragma unroll
-        for (int e = 0; e < DPT; ++e) dd += dyp[e] * bf2f(yp[e]);
+        for (int e = 0; e < DPT; ++e) dd += bf2f(dyp[e]) * bf2f(yp[e]);
       }
       dd = red16_sum(dd);
       if (live && dg == 0) a.d_rows[((long long)b * a.H + hq) * a.T + t] = dd;
@@ -1103,7 +1105,8 @@ __global__ void __launch_bounds__(256) readout_bwd_mfma_kernel(b3_attn_bwd_args 
     }
     __builtin_amdgcn_sched_barrier(0);
     // the RMSNorm backward of ym = u * sg at this lane's features d = 32 db + d_row(lane, r)
-    const float* dyp = a.dy + (long long)b * a.dy_sb + t * a.dy_st + (long long)hq * HD;
+    const uint16_t* dyp = reinterpret_cast<const uint16_t*>(a.dy) + (long long)b * a.dy_sb + t * a.dy_st +
+                          (long long)hq * HD;
     const uint16_t* yp = reinterpret_cast<const uint16_t*>(a.y) + (long long)b * a.y_sb + t * a.y_st + (long long)hq * HD;
     // u becomes ym = U sg / |q_raw| (sg > 0: gamma <= 0.999)
     const float ks_ = inv * sg;
@@ -1128,7 +1131,8 @@ __global__ void __launch_bounds__(256) readout_bwd_mfma_kernel(b3_attn_bwd_args 
         float4 dy4 = make_float4(0.f, 0.f, 0.f, 0.f);
         uint2 y2 = make_uint2(0u, 0u);
         if (live) {
-          dy4 = *reinterpret_cast<const float4*>(dyp + d0);
+          const uint2 g2 = *reinterpret_cast<const uint2*>(dyp + d0);
+          dy4 = make_float4(bf_lo(g2.x), bf_hi(g2.x), bf_lo(g2.y), bf_hi(g2.y));
           y2 = *reinterpret_cast<const uint2*>(yp + d0);
         }
         const float4 w4 = *reinterpret_cast<const float4*>(&sm.resw[d0]);
@@ -1181,7 +1185,10 @@ __global__ void __launch_bounds__(256) readout_bwd_mfma_kernel(b3_attn_bwd_args 
         if (r4 == 0) __builtin_amdgcn_sched_barrier(0);
         const int d0 = 32 * db + 8 * r4 + 4 * h;
         float4 dy4 = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (live) dy4 = *reinterpret_cast<const float4*>(dyp + d0);
+        if (live) {
+          const uint2 g2 = *reinterpret_cast<const uint2*>(dyp + d0);
+          dy4 = make_float4(bf_lo(g2.x), bf_hi(g2.x), bf_lo(g2.y), bf_hi(g2.y));
+        }
         const float4 w4 = *reinterpret_cast<const float4*>(&sm.resw[d0]);
         const float dyv[4] = {dy4.x, dy4.y, dy4.z, dy4.w};
         const float wv[4] = {w4.x, w4.y, w4.z, w4.w};
@@ -1357,7 +1364,7 @@ extern "C" int bolt3_attn_bwd(const b3_attn_bwd_args* a, void* stream) {
   // 16-byte rows: every (b, h, t) row of the staged operands
   const int64_t es = a->dtype == B3_BF16 ? 2 : 4;
   if ((a->q_sb * es) % 16 || (a->q_sh * es) % 16 || (a->w_sb * es) % 16 || (a->w_sh * es) % 16 ||
-      (a->dy_sb * 4) % 16 || (a->dy_st * 4) % 16)
+      (a->dy_sb * es) % 16 || (a->dy_st * es) % 16)
     return B3_ERR_ARG;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   int rc;

@@ -670,38 +670,52 @@ __global__ void __launch_bounds__(64) attn_bwd_dkv_mfma_kernel(b3_attn_bwd_args 
     dk[db] = zero16();
     dv[db] = zero16();
   }
-  for (int g = 0; g < G; ++g) {
-    const int hq = hkv * G + g;
-    for (int q0 = 0; q0 < tc; q0 += 32) {
-      const int nq = min(32, tc - q0);
-      if (f.kind == 3 && j0 > q0 + nq - 1) continue;   // every query of the tile precedes the keys
-      const long long row0 = ((long long)b * a.H + hq) * a.T + (long long)c * a.C + q0;
-      // the query tile and its dO rows into LDS (row n, piece 2 ks + h); rows past the chunk zero
-      {
-        const int qr = min(q0 + n, tc - 1);
-        const long long t = (long long)c * a.C + qr;
-        const uint16_t* qp = reinterpret_cast<const uint16_t*>(a.q_rope) + (long long)b * a.q_sb +
-                             (long long)hq * a.q_sh + t * HD;
-        const uint16_t* dp = reinterpret_cast<const uint16_t*>(a.dy) + (long long)b * a.dy_sb + t * a.dy_st +
-                             (long long)hq * HD;
-        const bool ok = q0 + n < tc;
+  // the tiles this block needs: all 32-row query tiles of the G heads, for the own chunk's keys
+  // only those from the block's first key on (earlier queries precede every key of the block);
+  // tile it + 1's rows are loaded into registers while tile it's products run
+  const int q_start = f.kind == 3 ? j0 : 0;
+  const int nqt = (tc - q_start + 31) / 32, n_it = G * nqt;
+  u16x8 nqv[KS], nov[KS];
+  float nls = INFINITY, ndr = 0.f;
+  auto fetch = [&](int it) {
+    const int hq = hkv * G + it / nqt, q0 = q_start + 32 * (it % nqt);
+    const bool ok = q0 + n < tc;
+    const long long t = (long long)c * a.C + min(q0 + n, tc - 1);
+    const uint16_t* qp = reinterpret_cast<const uint16_t*>(a.q_rope) + (long long)b * a.q_sb + (long long)hq * a.q_sh +
+                         t * HD;
+    const uint16_t* dp = reinterpret_cast<const uint16_t*>(a.dy) + (long long)b * a.dy_sb + t * a.dy_st +
+                         (long long)hq * HD;
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          u16x8 qv = *reinterpret_cast<const u16x8*>(qp + 16 * ks + 8 * h);
-          u16x8 ov = *reinterpret_cast<const u16x8*>(dp + 16 * ks + 8 * h);
-          if (!ok) {
-            qv = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
-            ov = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
-          }
-          const int slot = 8 * ((2 * ks + h) ^ (n % NP));
-          *reinterpret_cast<u16x8*>(&sm.q[n * HD + slot]) = qv;
-          *reinterpret_cast<u16x8*>(&sm.o[n * HD + slot]) = ov;
-        }
-        if (h == 0) {
-          sm.lse2[n] = ok ? a.lse[row0 + n] * L2E : INFINITY;
-          sm.drow[n] = ok ? a.d_rows[row0 + n] : 0.f;
-        }
-      }
+    for (int ks = 0; ks < KS; ++ks) {
+      nqv[ks] = ok ? *reinterpret_cast<const u16x8*>(qp + 16 * ks + 8 * h) : u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+      nov[ks] = ok ? *reinterpret_cast<const u16x8*>(dp + 16 * ks + 8 * h) : u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    }
+    if (h == 0) {
+      const long long row = ((long long)b * a.H + hq) * a.T + t;
+      nls = ok ? a.lse[row] * L2E : INFINITY;
+      ndr = ok ? a.d_rows[row] : 0.f;
+    }
+  };
+  auto put = [&]() {   // the fetched tile into LDS (row n, piece 2 ks + h)
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int slot = 8 * ((2 * ks + h) ^ (n % NP));
+      *reinterpret_cast<u16x8*>(&sm.q[n * HD + slot]) = nqv[ks];
+      *reinterpret_cast<u16x8*>(&sm.o[n * HD + slot]) = nov[ks];
+    }
+    if (h == 0) {
+      sm.lse2[n] = nls;
+      sm.drow[n] = ndr;
+    }
+  };
+  if (n_it > 0) {
+    fetch(0);
+    put();
+  }
+  for (int it = 0; it < n_it; ++it) {
+    {
+      if (it + 1 < n_it) fetch(it + 1);
+      const int q0 = q_start + 32 * (it % nqt);
       // S = Q K^T and dP = dO V^T: rows queries (A operand from the tile rows), columns keys
       f32x16 s = zero16(), dp = zero16();
 #pragma unroll
@@ -737,6 +751,7 @@ __global__ void __launch_bounds__(64) attn_bwd_dkv_mfma_kernel(b3_attn_bwd_args 
         }
       }
     }
+    if (it + 1 < n_it) put();   // after this tile's LDS reads (one wavefront: LDS in order)
   }
   if (n >= nk) return;
   const float scale = 1.0f / sqrtf((float)HD);

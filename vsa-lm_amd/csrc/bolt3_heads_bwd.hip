@@ -17,7 +17,7 @@ namespace b3 {
 namespace hbwd {
 
 constexpr int NT = 256;
-constexpr int RPB = 8;     // token rows per workgroup
+constexpr int RPB = 2;     // token rows per workgroup (more workgroups in flight beat longer ones)
 
 __device__ __forceinline__ float wsum(float v) {
 #pragma unroll

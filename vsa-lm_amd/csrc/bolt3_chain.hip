@@ -594,6 +594,39 @@ __device__ void rope_dirty(DecSmem<T, HD>& sm, T* kread_g, int tid) {
   }
 }
 
+// Step token rows into slots: for each i < n where pick(i, j, s) holds, slot s takes token j's
+// un-roped key and value (and, with kp_copy, its roped key).  n <= S and every picked slot is
+// distinct, so a thread's items (at most S*HD/8/DT) are independent: all their global loads go
+// out before the first store, one memory round trip instead of one per item.
+template <typename T, int HD, typename Pick>
+__device__ __forceinline__ void take_rows(DecSmem<T, HD>& sm, T* kread_w, int krs, bool kp_copy, const T* kr,
+                                          const T* v, const T* kp, int n, Pick pick, int tid) {
+  constexpr int NC8 = HD / 8, PER = (S * NC8 + DT - 1) / DT;
+  Vec8<T> kx[PER], vx[PER], px[PER];
+  int dst[PER];
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const int it = tid + u * DT, i = it / NC8, d8 = 8 * (it % NC8);
+    int j = 0, s = -1;
+    if (i < n && pick(i, j, s)) {
+      kx[u].load(kr + (long long)j * HD + d8);
+      vx[u].load(v + (long long)j * HD + d8);
+      if (kp_copy) px[u].load(kp + (long long)j * HD + d8);
+    } else {
+      s = -1;
+    }
+    dst[u] = s;
+  }
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    if (dst[u] < 0) continue;
+    const int d8 = 8 * ((tid + u * DT) % NC8);
+    kx[u].store(&sm.ak[dst[u] * sm.KS + d8]);
+    vx[u].store(&sm.av[dst[u] * sm.KS + d8]);
+    if (kp_copy) px[u].store(kread_w + dst[u] * krs + d8);
+  }
+}
+
 // 1 / max(||ak_s||, 1e-12) for every slot (four threads per slot).
 template <typename T, int HD>
 __device__ void slot_norms(DecSmem<T, HD>& sm, int tid) {
@@ -1341,13 +1374,13 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
         sync_lds();
       }
       // slots nf + i <- token si_a[i]
-      for (int it = tid; it < m * (HD / 8); it += DT) {
-        const int i = it / (HD / 8), d8 = (it % (HD / 8)) * 8;
-        const int j = sm.si_a[i], s = nf + i;
-        copy8(&sm.ak[s * KS + d8], kr + (long long)j * HD + d8);
-        copy8(&sm.av[s * KS + d8], v + (long long)j * HD + d8);
-        if (kp_copy) copy8(kread_w + s * krs + d8, kp + (long long)j * HD + d8);
-      }
+      take_rows<T, HD>(sm, kread_w, krs, kp_copy, kr, v, kp, m,
+                       [&](int i, int& j, int& s) {
+                         j = sm.si_a[i];
+                         s = nf + i;
+                         return true;
+                       },
+                       tid);
       if (tid < m) {
         const int j = sm.si_a[tid], s = nf + tid;
         sm.pm[s] = sm.tpos[j];
@@ -1625,16 +1658,14 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
           if (!kp_copy) sm.dirty[s] = 1;
         }
       }
-      for (int it = tid; it < kc * (HD / 8); it += DT) {
-        const int i = it / (HD / 8), d8 = (it % (HD / 8)) * 8;
-        const float tv = sm.sk_a[i], bv = sm.sk_b[i];
-        if (tv > bv && tv > -1e8f) {
-          const int j = sm.si_a[i], s = sm.si_b[i];
-          copy8(&sm.ak[s * KS + d8], kr + (long long)j * HD + d8);
-          copy8(&sm.av[s * KS + d8], v + (long long)j * HD + d8);
-          if (kp_copy) copy8(kread_w + s * krs + d8, kp + (long long)j * HD + d8);
-        }
-      }
+      take_rows<T, HD>(sm, kread_w, krs, kp_copy, kr, v, kp, kc,
+                       [&](int i, int& j, int& s) {
+                         const float tv = sm.sk_a[i], bv = sm.sk_b[i];
+                         j = sm.si_a[i];
+                         s = sm.si_b[i];
+                         return tv > bv && tv > -1e8f;
+                       },
+                       tid);
       sync_lds();
       if (tid < l) {
         const int f = sm.flags[tid];
@@ -1717,11 +1748,73 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
 // For steady step blockIdx.x and row blockIdx.y:
 //   inv_j   = 1 / max(|k_j|, 1e-12)
 //   bsafe_j = w_j / max(sum_i |khat_i . khat_j| w_i, 1)
+// bf16: the step's keys come into LDS once (thread t stages row t and takes its 1/|k| from the
+// same registers), 16-byte piece p of row r at p ^ (r % (HD/8)), and the products read their
+// operands there: one global round trip per workgroup.  The products and the summation order
+// are those of the fp32-storage path below.
+template <int HD>
+__device__ __forceinline__ void gersh_bf16(const b3_chain_args& a, const uint16_t* kr, const float* w, float* bsafe,
+                                           float* inv, int l) {
+  constexpr int NP = HD / 8;
+  extern __shared__ __attribute__((aligned(16))) unsigned char gsm_raw[];
+  uint16_t* kt = reinterpret_cast<uint16_t*>(gsm_raw);   // [32 * ceil(l / 32)][HD]
+  __shared__ float s_inv[LMAX], s_w[LMAX];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, n = lane & 31, h = lane >> 5;
+  const int nT = (l + 31) / 32;
+  if (tid < 32 * nT) {
+    u16x8 x[NP];
+    if (tid < l) {
+#pragma unroll
+      for (int p = 0; p < NP; ++p) x[p] = *reinterpret_cast<const u16x8*>(kr + (long long)tid * HD + 8 * p);
+    } else {
+#pragma unroll
+      for (int p = 0; p < NP; ++p) x[p] = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    }
+    const float wv = tid < l ? w[tid] : 0.f;
+    float ss = 0.f;
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float f = bf2f(x[p][i]);
+        ss += f * f;
+      }
+#pragma unroll
+    for (int p = 0; p < NP; ++p) *reinterpret_cast<u16x8*>(&kt[tid * HD + 8 * (p ^ (tid % NP))]) = x[p];
+    if (tid < l) {
+      const float iv = 1.0f / fmaxf(sqrtf(ss), 1e-12f);
+      s_inv[tid] = iv;
+      s_w[tid] = wv;
+      inv[tid] = iv;
+    }
+  }
+  __syncthreads();
+  auto piece = [&](int r, int p) { return *reinterpret_cast<const u16x8*>(&kt[r * HD + 8 * (p ^ (r % NP))]); };
+  for (int tj = wave; tj < nT; tj += MWAVES) {
+    const int j = 32 * tj + n;
+    u16x8 fj[HD / 16];
+#pragma unroll
+    for (int ks = 0; ks < HD / 16; ++ks) fj[ks] = piece(j, 2 * ks + h);
+    const float inj = j < l ? s_inv[j] : 0.f;
+    float colsum = 0.f;
+    for (int ti = 0; ti < nT; ++ti) {
+      f32x16 acc = zero16();
+#pragma unroll
+      for (int ks = 0; ks < HD / 16; ++ks) mma_bf16(acc, piece(32 * ti + n, 2 * ks + h), fj[ks]);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int i = 32 * ti + d_row(lane, r);
+        if (i < l) colsum += fabsf(acc[r] * (s_inv[i] * inj)) * s_w[i];
+      }
+    }
+    colsum += xor32(colsum);
+    if (h == 0 && j < l) bsafe[j] = s_w[j] / fmaxf(colsum, 1.0f);
+  }
+}
+
 template <typename T, int HD>
 __global__ void __launch_bounds__(MT) gersh_kernel(b3_chain_args a) {
-  __shared__ float s_inv[LMAX], s_w[LMAX];
   const int step = blockIdx.x, bh = blockIdx.y;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, n = lane & 31;
   int nf = a.n_filled;
   for (int s = 0; s < step && nf < S; ++s) nf += min(S - nf, step_len(a, s));
   if (nf < S) return;  // fill step: M_res untouched
@@ -1735,48 +1828,48 @@ __global__ void __launch_bounds__(MT) gersh_kernel(b3_chain_args a) {
   const float* w = reinterpret_cast<const float*>(ws) + row;
   float* bsafe = reinterpret_cast<float*>(ws) + plane + row;
   float* inv = reinterpret_cast<float*>(ws) + 2 * plane + row;
-
-  if (tid < l) {
-    float ss = 0.f;
-    for (int d = 0; d < HD; d += 8) {
-      float x[8];
-      ld8(kr + (long long)tid * HD + d, x);
+  if constexpr (St<T>::is_bf16) {
+    gersh_bf16<HD>(a, kr, w, bsafe, inv, l);
+  } else {
+    __shared__ float s_inv[LMAX], s_w[LMAX];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, n = lane & 31;
+    if (tid < l) {
+      float ss = 0.f;
+      for (int d = 0; d < HD; d += 8) {
+        float x[8];
+        ld8(kr + (long long)tid * HD + d, x);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) ss += x[i] * x[i];
+        for (int i = 0; i < 8; ++i) ss += x[i] * x[i];
+      }
+      const float iv = 1.0f / fmaxf(sqrtf(ss), 1e-12f);
+      s_inv[tid] = iv;
+      s_w[tid] = w[tid];
+      inv[tid] = iv;
     }
-    const float iv = 1.0f / fmaxf(sqrtf(ss), 1e-12f);
-    s_inv[tid] = iv;
-    s_w[tid] = w[tid];
-    inv[tid] = iv;
-  }
-  __syncthreads();
-  const int nT = (l + 31) / 32;
-  for (int tj = wave; tj < nT; tj += MWAVES) {
-    const int j = 32 * tj + n;
-    Frag<T, HD> fj;
-    fj.load(kr, j, l, lane);
-    const float inj = j < l ? s_inv[j] : 0.f;
-    float colsum = 0.f;
-    for (int ti = 0; ti < nT; ++ti) {
-      f32x16 acc = zero16();
-      Frag<T, HD> fi;
-      fi.load(kr, 32 * ti + n, l, lane);
-      // rows i of tile ti as the A operand: same fragment layout as a B fragment
-      if constexpr (St<T>::is_bf16) {
-#pragma unroll
-        for (int ks = 0; ks < HD / 16; ++ks) mma_bf16(acc, fi.v[ks], fj.v[ks]);
-      } else {
+    __syncthreads();
+    const int nT = (l + 31) / 32;
+    for (int tj = wave; tj < nT; tj += MWAVES) {
+      const int j = 32 * tj + n;
+      Frag<T, HD> fj;
+      fj.load(kr, j, l, lane);
+      const float inj = j < l ? s_inv[j] : 0.f;
+      float colsum = 0.f;
+      for (int ti = 0; ti < nT; ++ti) {
+        f32x16 acc = zero16();
+        Frag<T, HD> fi;
+        fi.load(kr, 32 * ti + n, l, lane);
+        // rows i of tile ti as the A operand: same fragment layout as a B fragment
 #pragma unroll 8
         for (int ks = 0; ks < HD / 2; ++ks) mma_f32(acc, fi.v[ks], fj.v[ks]);
-      }
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int i = 32 * ti + d_row(lane, r);
-        if (i < l) colsum += fabsf(acc[r] * (s_inv[i] * inj)) * s_w[i];
+        for (int r = 0; r < 16; ++r) {
+          const int i = 32 * ti + d_row(lane, r);
+          if (i < l) colsum += fabsf(acc[r] * (s_inv[i] * inj)) * s_w[i];
+        }
       }
+      colsum += xor32(colsum);
+      if ((lane >> 5) == 0 && j < l) bsafe[j] = s_w[j] / fmaxf(colsum, 1.0f);
     }
-    colsum += xor32(colsum);
-    if ((lane >> 5) == 0 && j < l) bsafe[j] = s_w[j] / fmaxf(colsum, 1.0f);
   }
 }
 
@@ -2145,7 +2238,10 @@ static int launch_chain(const b3_chain_args& a, hipStream_t st) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.phase == 1) return (int)e;
   }
-  hipLaunchKernelGGL((gersh_kernel<T, HD>), dim3(a.n_steps, BH), dim3(MT), 0, st, a);
+  // bf16: LDS for the longest step's keys, rows padded to a multiple of 32
+  const int lmax = a.n_steps > 1 ? std::max(a.len0, a.step_len) : a.len0;
+  const size_t gsm = St<T>::is_bf16 ? (size_t)32 * ((lmax + 31) / 32) * HD * sizeof(T) : 0;
+  hipLaunchKernelGGL((gersh_kernel<T, HD>), dim3(a.n_steps, BH), dim3(MT), gsm, st, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return (int)e;
   hipLaunchKernelGGL((mres_kernel<T, HD>), dim3(BH * (HD / 32)), dim3(MT), 0, st, a);

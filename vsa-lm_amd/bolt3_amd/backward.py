@@ -255,11 +255,19 @@ def attn_backward(mod, tr: dict, dy: torch.Tensor, dt: torch.dtype, n_steps: int
     ns = min(mod.n_sinks, C)
     f32 = dict(device=dev, dtype=torch.float32)
     o = dict(d_rows=torch.empty(b, H, T, **f32), lse=torch.empty(b, H, T, **f32),
-             d_q_rope=torch.empty(b, H, T, HD, **f32), d_q_raw=torch.zeros(b, H, T, HD, **f32),
-             d_eta=torch.zeros(b, H, T, **f32), d_res_w=torch.zeros(bh, n_chunks, HD, **f32),
+             d_q_rope=torch.empty(b, H, T, HD, **f32), d_q_raw=torch.empty(b, H, T, HD, **f32),
+             d_eta=torch.empty(b, H, T, **f32), d_res_w=torch.zeros(bh, n_chunks, HD, **f32),
              d_gamma=torch.zeros(bh, n_chunks, **f32),
              d_k_own=torch.empty(b, HKV, T, HD, **f32), d_v_own=torch.empty(b, HKV, T, HD, **f32),
-             d_k_next=torch.zeros(b, HKV, T, HD, **f32), d_v_next=torch.zeros(b, HKV, T, HD, **f32))
+             d_k_next=torch.empty(b, HKV, T, HD, **f32), d_v_next=torch.empty(b, HKV, T, HD, **f32))
+    # rows no kernel writes are zero: the q_raw and eta gradients of chunks without a readout
+    # (0 and 1, or all when nothing was consolidated), the next-chunk key / value gradients of
+    # the last chunk's keys
+    t_m = min(T, 2 * C) if n_steps > 0 else T
+    o["d_q_raw"][:, :, :t_m].zero_()
+    o["d_eta"][:, :, :t_m].zero_()
+    o["d_k_next"][:, :, (n_chunks - 1) * C:].zero_()
+    o["d_v_next"][:, :, (n_chunks - 1) * C:].zero_()
     a = A.AttnBwdArgs()
     a.dtype, a.B, a.T, a.H, a.HKV, a.HD, a.S, a.C = A.dtype_code(dt), b, T, H, HKV, HD, S, C
     a.n_sinks, a.n_chunks, a.n_qtiles, a.n_steps, a.score_round = mod.n_sinks, n_chunks, n_qt, n_steps, 1
@@ -285,7 +293,8 @@ def attn_backward(mod, tr: dict, dy: torch.Tensor, dt: torch.dtype, n_steps: int
 
 
 def layer_backward(mod, x: torch.Tensor, tr: dict, d_out: torch.Tensor, dt: torch.dtype):
-    """Gradients of Bolt3Attn.forward: (dx in fp32, {parameter name: fp32 gradient})."""
+    """Gradients of Bolt3Attn.forward: (dx, {parameter name: gradient}); the projections'
+    gradients (dx among them) in the storage dtype their products run in, the rest fp32."""
     b, T, D = x.shape
     H, HKV, HD, S, C = mod.H, mod.HKV, mod.HD, mod.S, mod.C
     G = H // HKV
@@ -301,7 +310,7 @@ def layer_backward(mod, x: torch.Tensor, tr: dict, d_out: torch.Tensor, dt: torc
     d_out = d_out.to(dt)
     # o_proj
     y = tr["y"]
-    grads["o_proj.weight"] = (d_out.reshape(-1, D).t() @ y.reshape(-1, H * HD)).float()
+    grads["o_proj.weight"] = d_out.reshape(-1, D).t() @ y.reshape(-1, H * HD)
     dy = (d_out @ side["wo"]).contiguous()                          # [b, T, H*HD], storage dtype
     # attention and readout
     o = attn_backward(mod, tr, dy, dt, n_steps)
@@ -357,15 +366,14 @@ def layer_backward(mod, x: torch.Tensor, tr: dict, d_out: torch.Tensor, dt: torc
         grads["q_norm.weight"], grads["k_norm.weight"] = d_qn.sum(0), d_kn.sum(0)
     widths = [H * HD, HKV * HD, HKV * HD, HKV, H]
     # one product each for dx and for the packed weight's gradient: rows q | k | v | beta | eta
-    dx = (dz @ W).float()
-    dW = (dz.t() @ x.reshape(b * T, D)).float()
+    dx = dz @ W
+    dW = dz.t() @ x.reshape(b * T, D)
     lins = (mod.q_proj, mod.k_proj, mod.v_proj, mod.beta_proj, mod.eta_proj)
-    db = dz.float().sum(0) if any(lin.bias is not None for lin in lins) else None
     off = 0
     for name, lin, width in zip(("q_proj", "k_proj", "v_proj", "beta_proj", "eta_proj"), lins, widths):
         grads[f"{name}.weight"] = dW[off:off + width]
-        if lin.bias is not None:
-            grads[f"{name}.bias"] = db[off:off + width]
+        if lin.bias is not None:   # column sums of dz, accumulated in fp32 (no fp32 copy of dz)
+            grads[f"{name}.bias"] = dz[:, off:off + width].sum(0, dtype=torch.float32)
         off += width
     grads["kappa"] = d_kappa
     # gamma = clamp(0.999 * sigmoid(log_gamma), 1e-3, 0.999); clamp passes its bounds inclusive

@@ -303,18 +303,21 @@ typedef struct {
   int64_t dy_sb, dy_st;
   float* d_rows;              /* [B][H][T] written: sum over d of dy * attention output */
   float* lse;                 /* [B][H][T] written: log-sum-exp of every query row */
-  float* d_q_rope;            /* [B][H][T][HD] */
-  float* d_q_raw;             /* [B][H][T][HD] (readout part; zero-filled by the caller) */
-  float* d_eta;               /* [B][H][T] (zero-filled) */
+  /* d_q_rope, d_q_raw and the d_k_* / d_v_* row gradients are in the storage dtype (the
+     gradients of storage-dtype tensors); the rest is fp32 */
+  void* d_q_rope;             /* [B][H][T][HD] */
+  void* d_q_raw;              /* [B][H][T][HD] (readout part; rows of chunks without a readout are
+                                 not written) */
+  float* d_eta;               /* [B][H][T] (rows of chunks without a readout are not written) */
   float* d_m;                 /* [step][B*HKV][HD][HD]: gradient of M_res of step c - 2 from chunk c */
   float* d_res_w;             /* [B*HKV][n_chunks][HD] partial sums (zero-filled) */
   float* d_gamma;             /* [B*HKV][n_chunks] partial sums (zero-filled) */
   float* d_bias;              /* [step][B*H][n_qtiles][S] partial sums of the slot bias gradient */
-  float* d_k_own;             /* [B][HKV][T][HD]: keys of chunk c from chunk c's queries */
-  float* d_v_own;
-  float* d_k_next;            /* [B][HKV][T][HD]: keys of chunk c from chunk c+1's queries (rows of the
+  void* d_k_own;              /* [B][HKV][T][HD]: keys of chunk c from chunk c's queries */
+  void* d_v_own;
+  void* d_k_next;             /* [B][HKV][T][HD]: keys of chunk c from chunk c+1's queries (rows of the
                                  last chunk are not written) */
-  float* d_v_next;
+  void* d_v_next;
   float* d_slot_k;            /* [step][B*HKV][S][HD] */
   float* d_slot_v;
   float* d_sink_k;            /* [n_chunks][B*HKV][n_sinks][HD] (chunks 0 and 1 are not written) */
@@ -492,12 +495,13 @@ int64_t bolt3_chain_bwd_workspace_bytes(int32_t B, int32_t HKV, int32_t HD, int3
  */
 typedef struct {
   int32_t dtype, B, T, H, HKV, HD, n_sinks, n_chunks;
-  const float* d_q_raw;       /* [B][H][T][HD] gradient of the un-roped queries (readout) */
-  const float* d_q_rope;      /* [B][H][T][HD] gradient of the roped queries (attention) */
-  const float* d_k_own;       /* [B][HKV][T][HD] gradient of the roped keys as their own chunk's keys */
-  const float* d_k_next;      /* [B][HKV][T][HD] ... as the next chunk's keys */
-  const float* d_v_own;
-  const float* d_v_next;
+  /* the six row gradients of bolt3_attn_bwd, in the storage dtype */
+  const void* d_q_raw;        /* [B][H][T][HD] gradient of the un-roped queries (readout) */
+  const void* d_q_rope;       /* [B][H][T][HD] gradient of the roped queries (attention) */
+  const void* d_k_own;        /* [B][HKV][T][HD] gradient of the roped keys as their own chunk's keys */
+  const void* d_k_next;       /* [B][HKV][T][HD] ... as the next chunk's keys */
+  const void* d_v_own;
+  const void* d_v_next;
   const float* d_sink_k;      /* [n_chunks][B*HKV][n_sinks][HD] or NULL: the sinks' roped-key gradients */
   const float* d_sink_v;
   const float* d_k_chain;     /* [B*HKV][T][HD] or NULL: the chain's gradient of the un-roped keys */
@@ -515,7 +519,8 @@ typedef struct {
   int32_t has_qk_norm;
   float q_eps, k_eps;
   const float* inv_freq;      /* [HD/2] */
-  void* dz;                   /* out: [B*T][dz_row_stride] storage dtype */
+  void* dz;                   /* out: [B*T][dz_row_stride] storage dtype; dz_row_stride and the lin row
+                                 strides are multiples of 4 elements (rows move as 4-element vectors) */
   int64_t dz_row_stride;
   int32_t dz_cols;            /* >= (H + 2 HKV) HD + HKV + H; the columns past those are zeroed */
   float* d_qn_w;              /* out: [bolt3_heads_bwd_blocks(B, T)][HD] partial sums (has_qk_norm) */

@@ -254,12 +254,13 @@ def attn_backward(mod, tr: dict, dy: torch.Tensor, dt: torch.dtype, n_steps: int
     n_qt = (C + 31) // 32
     ns = min(mod.n_sinks, C)
     f32 = dict(device=dev, dtype=torch.float32)
+    sdt = dict(device=dev, dtype=dt)   # the row gradients of storage-dtype tensors
     o = dict(d_rows=torch.empty(b, H, T, **f32), lse=torch.empty(b, H, T, **f32),
-             d_q_rope=torch.empty(b, H, T, HD, **f32), d_q_raw=torch.empty(b, H, T, HD, **f32),
+             d_q_rope=torch.empty(b, H, T, HD, **sdt), d_q_raw=torch.empty(b, H, T, HD, **sdt),
              d_eta=torch.empty(b, H, T, **f32), d_res_w=torch.zeros(bh, n_chunks, HD, **f32),
              d_gamma=torch.zeros(bh, n_chunks, **f32),
-             d_k_own=torch.empty(b, HKV, T, HD, **f32), d_v_own=torch.empty(b, HKV, T, HD, **f32),
-             d_k_next=torch.empty(b, HKV, T, HD, **f32), d_v_next=torch.empty(b, HKV, T, HD, **f32))
+             d_k_own=torch.empty(b, HKV, T, HD, **sdt), d_v_own=torch.empty(b, HKV, T, HD, **sdt),
+             d_k_next=torch.empty(b, HKV, T, HD, **sdt), d_v_next=torch.empty(b, HKV, T, HD, **sdt))
     # rows no kernel writes are zero: the q_raw and eta gradients of chunks without a readout
     # (0 and 1, or all when nothing was consolidated), the next-chunk key / value gradients of
     # the last chunk's keys

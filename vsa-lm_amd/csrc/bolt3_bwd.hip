@@ -273,7 +273,7 @@ __global__ void __launch_bounds__(NT) attn_bwd_dq_kernel(b3_attn_bwd_args a) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     if (4 * rg + i >= nq) continue;
-    float* o = a.d_q_rope + (row0 + 4 * rg + i) * HD + DPT * cg;
+    float* o = static_cast<float*>(a.d_q_rope) + (row0 + 4 * rg + i) * HD + DPT * cg;
 #pragma unroll
     for (int e = 0; e < DPT; e += 4)
       *reinterpret_cast<float4*>(o + e) =
@@ -402,8 +402,8 @@ __global__ void __launch_bounds__(NT) attn_bwd_dkv_kernel(b3_attn_bwd_args a) {
     ov = a.d_slot_v + o;
   } else {
     const long long o = ((long long)bh * a.T + (long long)(f.kind == 2 ? c - 1 : c) * a.C + j0) * HDl;
-    ok = (f.kind == 2 ? a.d_k_next : a.d_k_own) + o;
-    ov = (f.kind == 2 ? a.d_v_next : a.d_v_own) + o;
+    ok = static_cast<float*>(f.kind == 2 ? a.d_k_next : a.d_k_own) + o;
+    ov = static_cast<float*>(f.kind == 2 ? a.d_v_next : a.d_v_own) + o;
   }
 #pragma unroll
   for (int jj = 0; jj < 2; ++jj) {
@@ -611,14 +611,14 @@ __global__ void __launch_bounds__(64) attn_bwd_dq_mfma_kernel(b3_attn_bwd_args a
   }
   if (!qok) return;
   const float scale = 1.0f / sqrtf((float)HD);
-  float* o = a.d_q_rope + row * HD;
+  uint16_t* o = static_cast<uint16_t*>(a.d_q_rope) + row * HD;   // bf16, the storage dtype
 #pragma unroll
   for (int db = 0; db < NDB; ++db)
 #pragma unroll
     for (int g = 0; g < 4; ++g)
-      *reinterpret_cast<float4*>(o + 32 * db + 8 * g + 4 * h) =
-          make_float4(dq[db][4 * g] * scale, dq[db][4 * g + 1] * scale, dq[db][4 * g + 2] * scale,
-                      dq[db][4 * g + 3] * scale);
+      *reinterpret_cast<uint2*>(o + 32 * db + 8 * g + 4 * h) =
+          make_uint2(pack_bf2(dq[db][4 * g] * scale, dq[db][4 * g + 1] * scale),
+                     pack_bf2(dq[db][4 * g + 2] * scale, dq[db][4 * g + 3] * scale));
 }
 
 template <int HD>
@@ -755,20 +755,34 @@ __global__ void __launch_bounds__(64) attn_bwd_dkv_mfma_kernel(b3_attn_bwd_args 
   }
   if (n >= nk) return;
   const float scale = 1.0f / sqrtf((float)HD);
-  float *ok, *ov;
   const long long HDl = HD;
+  if (f.kind >= 2) {
+    // token rows: bf16, the storage dtype
+    const long long o = ((long long)bh * a.T + (long long)(f.kind == 2 ? c - 1 : c) * a.C + j) * HDl;
+    uint16_t* ok = static_cast<uint16_t*>(f.kind == 2 ? a.d_k_next : a.d_k_own) + o;
+    uint16_t* ov = static_cast<uint16_t*>(f.kind == 2 ? a.d_v_next : a.d_v_own) + o;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const int d0 = 32 * db + 8 * g4 + 4 * h;
+        *reinterpret_cast<uint2*>(ok + d0) = make_uint2(pack_bf2(dk[db][4 * g4] * scale, dk[db][4 * g4 + 1] * scale),
+                                                        pack_bf2(dk[db][4 * g4 + 2] * scale, dk[db][4 * g4 + 3] * scale));
+        *reinterpret_cast<uint2*>(ov + d0) =
+            make_uint2(pack_bf2(dv[db][4 * g4], dv[db][4 * g4 + 1]), pack_bf2(dv[db][4 * g4 + 2], dv[db][4 * g4 + 3]));
+      }
+    return;
+  }
+  // sinks and slots: fp32 (the chain's backward sums them further)
+  float *ok, *ov;
   if (f.kind == 0) {
     const long long o = (((long long)c * a.B * a.HKV + bh) * a.n_sinks + j) * HDl;
     ok = a.d_sink_k + o;
     ov = a.d_sink_v + o;
-  } else if (f.kind == 1) {
+  } else {
     const long long o = (((long long)(c - 2) * a.B * a.HKV + bh) * a.S + j) * HDl;
     ok = a.d_slot_k + o;
     ov = a.d_slot_v + o;
-  } else {
-    const long long o = ((long long)bh * a.T + (long long)(f.kind == 2 ? c - 1 : c) * a.C + j) * HDl;
-    ok = (f.kind == 2 ? a.d_k_next : a.d_k_own) + o;
-    ov = (f.kind == 2 ? a.d_v_next : a.d_v_own) + o;
   }
 #pragma unroll
   for (int db = 0; db < NDB; ++db)
@@ -937,7 +951,7 @@ __global__ void __launch_bounds__(NT) readout_bwd_kernel(b3_attn_bwd_args a) {
     for (int e = 0; e < DPT; ++e) qd += sm.qn[r][16 * e + dg] * dqn[e];
     qd = red16_sum(qd);
     if (live) {
-      float* o = a.d_q_raw + row * HD;
+      float* o = static_cast<float*>(a.d_q_raw) + row * HD;
 #pragma unroll
       for (int e = 0; e < DPT; ++e) o[16 * e + dg] = (dqn[e] - sm.qn[r][16 * e + dg] * qd) * inv;
     }
@@ -1231,7 +1245,7 @@ __global__ void __launch_bounds__(256) readout_bwd_mfma_kernel(b3_attn_bwd_args 
 #pragma unroll
       for (int kc = 0; kc < 2; ++kc) acc_operand_split(u[db], kc, bhi[db][kc], blo[db][kc]);
     const float qi2 = sdy * inv;
-    float* o = a.d_q_raw + row * HD;
+    uint16_t* o = static_cast<uint16_t*>(a.d_q_raw) + row * HD;   // bf16, the storage dtype
 #pragma unroll
     for (int cb = 0; cb < NDB; ++cb) {
       __builtin_amdgcn_sched_barrier(0);
@@ -1255,7 +1269,7 @@ __global__ void __launch_bounds__(256) readout_bwd_mfma_kernel(b3_attn_bwd_args 
           v.y = (dq[4 * r4 + 1] - bf_hi(q2.x) * qi2) * inv;
           v.z = (dq[4 * r4 + 2] - bf_lo(q2.y) * qi2) * inv;
           v.w = (dq[4 * r4 + 3] - bf_hi(q2.y) * qi2) * inv;
-          *reinterpret_cast<float4*>(o + 32 * cb + 8 * r4 + 4 * h) = v;
+          *reinterpret_cast<uint2*>(o + 32 * cb + 8 * r4 + 4 * h) = make_uint2(pack_bf2(v.x, v.y), pack_bf2(v.z, v.w));
         }
       }
     }
@@ -1329,14 +1343,15 @@ static int launch(const b3_attn_bwd_args& a, hipStream_t st) {
     if (e != hipSuccess) return (int)e;
     hipLaunchKernelGGL((attn_bwd_dkv_mfma_kernel<HD>), dim3(max_blocks, BH, n_chunks), dim3(64), 0, st, a);
     return (int)hipGetLastError();
+  } else {
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<T, HD>), dim3((a.C + BQ - 1) / BQ, a.B * a.H, n_chunks), dim3(NT),
+                       sizeof(DqSmem<HD>), st, a);
+    e = hipGetLastError();
+    if (e != hipSuccess) return (int)e;
+    hipLaunchKernelGGL((attn_bwd_dkv_kernel<T, HD>), dim3(max_blocks, BH, n_chunks), dim3(NT), sizeof(DkvSmem<HD>),
+                       st, a);
+    return (int)hipGetLastError();
   }
-  hipLaunchKernelGGL((attn_bwd_dq_kernel<T, HD>), dim3((a.C + BQ - 1) / BQ, a.B * a.H, n_chunks), dim3(NT),
-                     sizeof(DqSmem<HD>), st, a);
-  e = hipGetLastError();
-  if (e != hipSuccess) return (int)e;
-  hipLaunchKernelGGL((attn_bwd_dkv_kernel<T, HD>), dim3(max_blocks, BH, n_chunks), dim3(NT), sizeof(DkvSmem<HD>),
-                     st, a);
-  return (int)hipGetLastError();
 }
 
 template <typename T, int HD>

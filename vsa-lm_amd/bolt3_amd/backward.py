@@ -22,6 +22,7 @@ run on the forward's device and stream.
 from __future__ import annotations
 
 import torch
+import torch.nn.functional as F
 
 from . import _abi as A
 
@@ -308,11 +309,13 @@ def layer_backward(mod, x: torch.Tensor, tr: dict, d_out: torch.Tensor, dt: torc
     # the projections' products run in the storage dtype, as the reference's linears do under
     # autocast (fp32 storage: fp32 products)
     W, _, side = mod._packed(dt, dev)
+    if "wT" not in side:   # the weights' transposes, for products in F.linear's layout (cached with the pack)
+        side["wT"], side["woT"] = W.t().contiguous(), side["wo"].t().contiguous()
     d_out = d_out.to(dt)
     # o_proj
     y = tr["y"]
     grads["o_proj.weight"] = d_out.reshape(-1, D).t() @ y.reshape(-1, H * HD)
-    dy = (d_out @ side["wo"]).contiguous()                          # [b, T, H*HD], storage dtype
+    dy = F.linear(d_out, side["woT"])                               # [b, T, H*HD], storage dtype
     # attention and readout
     o = attn_backward(mod, tr, dy, dt, n_steps)
     inv_freq = mod.rope.inv_freq.to(dev).float()
@@ -367,7 +370,7 @@ def layer_backward(mod, x: torch.Tensor, tr: dict, d_out: torch.Tensor, dt: torc
         grads["q_norm.weight"], grads["k_norm.weight"] = d_qn.sum(0), d_kn.sum(0)
     widths = [H * HD, HKV * HD, HKV * HD, HKV, H]
     # one product each for dx and for the packed weight's gradient: rows q | k | v | beta | eta
-    dx = dz @ W
+    dx = F.linear(dz, side["wT"])
     dW = dz.t() @ x.reshape(b * T, D)
     lins = (mod.q_proj, mod.k_proj, mod.v_proj, mod.beta_proj, mod.eta_proj)
     off = 0

@@ -738,20 +738,32 @@ __global__ void __launch_bounds__(512) attn_fwd_kernel(b3_attn_args a, int QW) {
 // through registers.  Blocks go in pairs: one barrier per pair, and the QK products of a
 // pair's second block are issued before the softmax of its first, so that the softmax runs
 // beside MFMA work.  The ring has three pair slots (six stages): while pair p is computed,
-// pair p + 1 is in flight and pair p + 2 is issued into the slot pair p - 1 has left.  Tiles
-// keep the source row-major layout with the 16-byte pieces of row r permuted by
-// p ^ (r % (HD/8)) (conflict-free operand reads); the V operand of O^T = V^T P^T is read with
-// ds_read_b64_tr_b16, which transposes 16-bit elements across lanes, so V needs no transpose
-// when staged.  The M_res snapshot (M^T bf16 hi / lo) comes by the same loads into the two
+// pair p + 1 is in flight and pair p + 2 is issued into the slot pair p - 1 has left.  A
+// tile is stored as blocks of 8 rows x 8 sixteen-byte pieces (one global->LDS instruction each:
+// 8 whole 128-byte row segments), piece-major inside a block and 128 bytes of padding between
+// blocks (f2_off below).  Every operand read of the loop is then a per-lane base plus a
+// compile-time offset (no address arithmetic per read), the K reads (ds_read_b128) are
+// conflict-free and the transposed V reads take the minimum two LDS cycles.  The V operand of
+// O^T = V^T P^T is read with ds_read_b64_tr_b16, which transposes 16-bit elements across lanes,
+// so V needs no transpose when staged.  The M_res snapshot (M^T bf16 hi / lo) comes by the same loads into the two
 // pair slots the last pair leaves free: hi at the barrier before the last pair, lo at the
 // last barrier.
 constexpr int NST = 6;
 
+constexpr int F2_BLK = 1024 + 128;      // bytes of one 8-row x 8-piece block and its padding
+
+// Byte offset of 16-byte piece p (elements 8p .. 8p+7) of row r in a staged K or V tile:
+// block (p / 8, r / 8) at F2_BLK * ((p / 8) * (KB / 8) + r / 8), and inside it the piece at
+// 16 * ((r % 8) + 8 * (p % 8)).
+__host__ __device__ constexpr int f2_off(int r, int p) {
+  return F2_BLK * ((p >> 3) * (KB / 8) + (r >> 3)) + 16 * ((r & 7) + 8 * (p & 7));
+}
+
 template <int HD>
 struct Fwd2Smem {
-  static constexpr int TILE = KB * HD;   // elements of one K or V tile
-  static_assert(4 * TILE >= HD * HD, "an M^T half fits in one pair slot");
-  alignas(16) uint16_t ring[NST][2][TILE];
+  static constexpr int TILEB = (HD / 64) * (KB / 8) * F2_BLK;   // bytes of one K or V tile
+  static_assert(4 * TILEB >= 2 * HD * HD, "an M^T half fits in one pair slot");
+  alignas(16) unsigned char ring[NST][2][TILEB];
   alignas(16) float sbias[128];          // slot bias row of the step (log2 units)
   alignas(16) float resw[128];           // res_norm weight
 };
@@ -765,14 +777,35 @@ __device__ __forceinline__ void wait_vm() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
   __builtin_amdgcn_s_waitcnt((N & 15) | (((N >> 4) & 3) << 14) | (7 << 4) | (15 << 8));
 }
-// ds_read_b64_tr_b16 as inline assembly: the compiler cannot tell these reads from the
-// LDS-DMA destinations and would otherwise wait for every outstanding tile load before them.
-// The caller waits for LDS (lds_wait8) before using the results.
-__device__ __forceinline__ u16x4 lds_read_tr(const uint16_t* p) {
+// ds_read_b64_tr_b16 as inline assembly, at a compile-time byte offset from the address (the
+// instruction's offset field): the compiler cannot tell these reads from the LDS-DMA
+// destinations and would otherwise wait for every outstanding tile load before them.  The
+// caller waits for LDS (lds_wait8) before using the results.
+template <int OFF>
+__device__ __forceinline__ u16x4 lds_read_tr_at(uint32_t addr) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset range");
   u16x4 r;
-  const uint32_t addr = (uint32_t)(size_t)((__attribute__((address_space(3))) const uint16_t*)p);
-  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r) : "v"(addr) : "memory");
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF) : "memory");
   return r;
+}
+// The V^T operand reads of rows 16 H2 .. 16 H2 + 15 of a staged V tile (f2_off layout) for the
+// NDB feature blocks: tv[2 db] holds rows 16 H2 + r1, tv[2 db + 1] rows 16 H2 + 8 + r1, where the
+// lane's row r1 and piece are in its base address.
+template <int NDB, int H2>
+__device__ __forceinline__ void f2_vreads(u16x4 (&tv)[8], uint32_t base) {
+  tv[0] = lds_read_tr_at<f2_off(16 * H2, 0)>(base);
+  tv[1] = lds_read_tr_at<f2_off(16 * H2 + 8, 0)>(base);
+  tv[2] = lds_read_tr_at<f2_off(16 * H2, 4)>(base);
+  tv[3] = lds_read_tr_at<f2_off(16 * H2 + 8, 4)>(base);
+  if constexpr (NDB > 2) {
+    tv[4] = lds_read_tr_at<f2_off(16 * H2, 8)>(base);
+    tv[5] = lds_read_tr_at<f2_off(16 * H2 + 8, 8)>(base);
+    tv[6] = lds_read_tr_at<f2_off(16 * H2, 12)>(base);
+    tv[7] = lds_read_tr_at<f2_off(16 * H2 + 8, 12)>(base);
+  }
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(size_t)((__attribute__((address_space(3))) const unsigned char*)p);
 }
 // The slot bias row goes through LDS by inline assembly as well (the compiler cannot separate
 // it from the LDS-DMA destinations either).
@@ -887,9 +920,9 @@ __global__ void __launch_bounds__(64 * NW) attn_fwd2_kernel(b3_attn_args a, int 
 #pragma unroll
     for (int q = 0; q < LPB; ++q) {
       const int ins = wave * LPB + q;
-      const int tile = ins / IPT, ch = ins % IPT;
-      const int r = ch * RPI + lane / NP, p = (lane % NP) ^ (r % NP);
-      lds_dma16((tile ? f.v : f.k) + (long long)min(r, last) * HD + 8 * p, &sm.ring[st][tile][ch * 512]);
+      const int tile = ins / IPT, ch = ins % IPT;     // block ch = (piece group, row group)
+      const int r = 8 * (ch % (KB / 8)) + (lane & 7), p = 8 * (ch / (KB / 8)) + (lane >> 3);
+      lds_dma16((tile ? f.v : f.k) + (long long)min(r, last) * HD + 8 * p, sm.ring[st][tile] + ch * F2_BLK);
     }
   };
   const bool readout = a.m_res && step >= 0;
@@ -897,7 +930,7 @@ __global__ void __launch_bounds__(64 * NW) attn_fwd2_kernel(b3_attn_args a, int 
   auto issue_mhalf = [&](int half, int ps) {
     const uint16_t* src = reinterpret_cast<const uint16_t*>(a.m_res + (long long)step * a.m_step) +
                           (long long)bh * 2 * HD * HD + (long long)half * HD * HD;   // bf16 M^T hi, then lo
-    uint16_t* dst = &sm.ring[2 * ps][0][0];
+    uint16_t* dst = reinterpret_cast<uint16_t*>(sm.ring[2 * ps][0]);   // 2 HD^2 bytes, row-major
 #pragma unroll
     for (int q = 0; q < LPMH; ++q) {
       const int ch = wave * LPMH + q;
@@ -933,21 +966,28 @@ __global__ void __launch_bounds__(64 * NW) attn_fwd2_kernel(b3_attn_args a, int 
   float m_run = -INFINITY, l_run = 0.f;
 
   // S^T = K Q^T of the block in stage st
+  // (row n, piece 2 ks + h) of a staged tile is at f2_off(n, h) + f2_off(0, 2 ks)
+  const int lane_k = f2_off(n, h);
   auto qk = [&](int st) -> f32x16 {
-    const uint16_t* sK = sm.ring[st][0];
+    const unsigned char* sK = sm.ring[st][0] + lane_k;
     f32x16 sc = zero16();
 #pragma unroll
-    for (int ks = 0; ks < HD / 16; ++ks) {
-      const int piece = (2 * ks + h) ^ (n % NP);
-      mma_bf16(sc, *reinterpret_cast<const u16x8*>(sK + n * HD + 8 * piece), qf.v[ks]);
-    }
+    for (int ks = 0; ks < HD / 16; ++ks)
+      mma_bf16(sc, *reinterpret_cast<const u16x8*>(sK + f2_off(0, 2 * ks)), qf.v[ks]);
     return sc;
   };
+  // the lane's V^T operand base: row r1 = 4h + jv/4 (+8, +16, +24 at compile-time offsets),
+  // elements 32 db + 16 (grp & 1) + 4 (jv & 3) .. +3 of the row (piece 4 db + c, half jv & 1)
+  const int jv = lane & 15, grp = lane >> 4;
+  const uint32_t lane_v = f2_off(4 * h + (jv >> 2), 2 * (grp & 1) + ((jv >> 1) & 1)) + 8 * (jv & 1);
   // softmax step and O^T += V^T P^T for block f in stage st, scores sc
   auto attend = [&](f32x16 sc, const FwdBlock& f, int st) {
-    const uint16_t* sV = sm.ring[st][1];
-    // scores in log2 units: round_bf(q.k) * scale*log2(e) (+ slot bias * log2(e)), one FMA; the
-    // rounding is skipped when score_round is 0 (fp32 scores, as the decoder step computes them)
+    const uint32_t vb = lds_addr(sm.ring[st][1]) + lane_v;
+    // scores in log2 units: round_bf(q.k) * scale*log2(e) + slot bias * log2(e), one FMA, for the
+    // slot blocks; the other blocks keep round_bf(q.k) and take the factor ksc inside the
+    // exponent's FMA (and on their maximum).  The rounding is skipped when score_round is 0
+    // (fp32 scores, as the decoder step computes them).
+    const float ksc = f.bias ? 1.0f : sL;
     if (f.bias) {
       fx4 b4[4];
 #pragma unroll
@@ -975,12 +1015,9 @@ __global__ void __launch_bounds__(64 * NW) attn_fwd2_kernel(b3_attn_args a, int 
 #pragma unroll
       for (int r = 0; r < 16; r += 2) {
         const uint32_t u = pack_bf2(sc[r], sc[r + 1]);
-        sc[r] = bf_lo(u) * sL;
-        sc[r + 1] = bf_hi(u) * sL;
+        sc[r] = bf_lo(u);
+        sc[r + 1] = bf_hi(u);
       }
-    } else {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) sc[r] *= sL;
     }
     // masks: rows past the valid keys, and the causal diagonal (a current-chunk block wholly
     // before the wave's first query needs none)
@@ -990,21 +1027,12 @@ __global__ void __launch_bounds__(64 * NW) attn_fwd2_kernel(b3_attn_args a, int 
       for (int r = 0; r < 16; ++r) sc[r] = d_row(lane, r) <= lim ? sc[r] : -INFINITY;
     }
     // the first half of this block's V^T operand, read while the softmax runs
-    const int jv = lane & 15, grp = lane >> 4;
     u16x4 tv0[8];
-    {
-      const int r1 = 4 * h + (jv >> 2), r2 = r1 + 8;
-#pragma unroll
-      for (int db = 0; db < NDB && db < 4; ++db) {
-        const int f0 = 32 * db + 16 * (grp & 1) + 4 * (jv & 3);
-        tv0[2 * db] = lds_read_tr(sV + r1 * HD + 8 * ((f0 >> 3) ^ (r1 % NP)) + (f0 & 7));
-        tv0[2 * db + 1] = lds_read_tr(sV + r2 * HD + 8 * ((f0 >> 3) ^ (r2 % NP)) + (f0 & 7));
-      }
-    }
+    f2_vreads<NDB, 0>(tv0, vb);
     float bm = -INFINITY;
 #pragma unroll
     for (int r = 0; r < 16; ++r) bm = fmaxf(bm, sc[r]);
-    bm = pair_max32(bm);
+    bm = pair_max32(bm) * ksc;
     // the running max moves only when it grows by more than 2^8 (probabilities up to 2^8
     // before the final normalisation are exact enough in fp32 and rescale-free)
     const bool grow = bm > m_run + 8.0f;
@@ -1013,7 +1041,7 @@ __global__ void __launch_bounds__(64 * NW) attn_fwd2_kernel(b3_attn_args a, int 
     float ps = 0.f;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const float p = __builtin_amdgcn_exp2f(sc[r] - mu);
+      const float p = __builtin_amdgcn_exp2f(fmaf(sc[r], ksc, -mu));
       sc[r] = p;
       ps += p;
     }
@@ -1037,13 +1065,7 @@ __global__ void __launch_bounds__(64 * NW) attn_fwd2_kernel(b3_attn_args a, int 
     {
       lds_wait8(tv0);
       u16x4 tv1[8];
-      const int r1 = 16 + 4 * h + (jv >> 2), r2 = r1 + 8;
-#pragma unroll
-      for (int db = 0; db < NDB && db < 4; ++db) {
-        const int f0 = 32 * db + 16 * (grp & 1) + 4 * (jv & 3);
-        tv1[2 * db] = lds_read_tr(sV + r1 * HD + 8 * ((f0 >> 3) ^ (r1 % NP)) + (f0 & 7));
-        tv1[2 * db + 1] = lds_read_tr(sV + r2 * HD + 8 * ((f0 >> 3) ^ (r2 % NP)) + (f0 & 7));
-      }
+      f2_vreads<NDB, 1>(tv1, vb);
 #pragma unroll
       for (int db = 0; db < NDB && db < 4; ++db) {
         u16x8 av;
@@ -1086,7 +1108,7 @@ __global__ void __launch_bounds__(64 * NW) attn_fwd2_kernel(b3_attn_args a, int 
     const FwdBlock f1 = block(has1 ? i1 : i0);
     const bool do1 = has1 && !(f1.kpos >= 0 && f1.kpos > wave_q0 + 31);
     const int st0 = 2 * (pr % 3);
-    f32x16 sc0 = zero16(), sc1 = zero16();
+    f32x16 sc0, sc1;   // set and read under the same conditions
     if (do0) sc0 = qk(st0);
     if (do1) sc1 = qk(st0 + 1);
     if (do0) attend(sc0, f0, st0);
@@ -1121,8 +1143,8 @@ __global__ void __launch_bounds__(64 * NW) attn_fwd2_kernel(b3_attn_args a, int 
     qq = pair_sum32(qq);
     const float inv_q = 1.0f / fmaxf(sqrtf(qq), 1e-12f);
     const float coef = div_rn(1.0f - a.gamma[hkv], sqrtf((float)HD));
-    const uint16_t* mt_hi = &sm.ring[2 * ((P + 1) % 3)][0][0];
-    const uint16_t* mt_lo = &sm.ring[2 * ((P + 2) % 3)][0][0];
+    const uint16_t* mt_hi = reinterpret_cast<const uint16_t*>(sm.ring[2 * ((P + 1) % 3)][0]);
+    const uint16_t* mt_lo = reinterpret_cast<const uint16_t*>(sm.ring[2 * ((P + 2) % 3)][0]);
     f32x16 rr[NDB];
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {

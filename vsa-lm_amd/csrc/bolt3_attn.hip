@@ -1108,7 +1108,7 @@ __global__ void __launch_bounds__(64 * NW) attn_fwd2_kernel(b3_attn_args a, int 
     const FwdBlock f1 = block(has1 ? i1 : i0);
     const bool do1 = has1 && !(f1.kpos >= 0 && f1.kpos > wave_q0 + 31);
     const int st0 = 2 * (pr % 3);
-    f32x16 sc0, sc1;   // set and read under the same conditions
+    f32x16 sc0 = zero16(), sc1 = zero16();
     if (do0) sc0 = qk(st0);
     if (do1) sc1 = qk(st0 + 1);
     if (do0) attend(sc0, f0, st0);

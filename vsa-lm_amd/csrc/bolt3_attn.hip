@@ -852,12 +852,20 @@ __global__ void __launch_bounds__(64 * NW) attn_fwd2_kernel(b3_attn_args a, int 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n = lane & 31, h = lane >> 5;
   const int g = wave / QW, qsub = wave % QW;
-  const int bh = blockIdx.z, b = bh / a.HKV, hkv = bh % a.HKV;
+  // XCD-aware order: consecutive workgroups go to the 8 XCDs in turn, so linear id L runs
+  // task (L % 8) * (N / 8) + L / 8 of the (query tile, chunk, bh) order; the query tiles and
+  // neighbouring chunks of one bh, which read the same key/value tiles and snapshots, then
+  // share one XCD's L2
+  int wg = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+  const int n_wg = gridDim.x * gridDim.y * gridDim.z;
+  if (n_wg % 8 == 0) wg = (wg % 8) * (n_wg / 8) + wg / 8;
+  const int bx = wg % gridDim.x, by = (wg / gridDim.x) % gridDim.y, bz = wg / (gridDim.x * gridDim.y);
+  const int bh = bz, b = bh / a.HKV, hkv = bh % a.HKV;
   const int hq = hkv * G + g;
-  const int chunk = blockIdx.y + a.chunk_begin, C = a.C;
+  const int chunk = by + a.chunk_begin, C = a.C;
   const int qbase = chunk * C;
   const int nq_chunk = min(C, a.n_q - qbase);
-  const int qt0 = blockIdx.x * 32 * QW;
+  const int qt0 = bx * 32 * QW;
   if (qt0 >= nq_chunk) return;                  // uniform across the workgroup
   const int qi = qt0 + 32 * qsub + n;
   const bool qok = qi < nq_chunk;

@@ -852,15 +852,10 @@ __global__ void __launch_bounds__(64 * NW) attn_fwd2_kernel(b3_attn_args a, int 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n = lane & 31, h = lane >> 5;
   const int g = wave / QW, qsub = wave % QW;
-  // XCD-aware order: consecutive workgroups go to the 8 XCDs in turn, so linear id L runs
-  // task (L % 8) * (N / 8) + L / 8 of the (query tile, chunk, bh) order; the query tiles and
-  // neighbouring chunks of one bh, which read the same key/value tiles and snapshots, then
-  // share one XCD's L2
-  int wg = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
-  const int n_wg = gridDim.x * gridDim.y * gridDim.z;
-  if (n_wg % 8 == 0) wg = (wg % 8) * (n_wg / 8) + wg / 8;
-  const int bx = wg % gridDim.x, by = (wg / gridDim.x) % gridDim.y, bz = wg / (gridDim.x * gridDim.y);
-  const int bh = bz, b = bh / a.HKV, hkv = bh % a.HKV;
+  // XCD-aware order: the query tiles and neighbouring chunks of one bh, which read the same
+  // key/value tiles and snapshots, share one XCD's L2
+  const GridPos gp = xcd_grid_pos();
+  const int bx = gp.x, by = gp.y, bh = gp.z, b = bh / a.HKV, hkv = bh % a.HKV;
   const int hq = hkv * G + g;
   const int chunk = by + a.chunk_begin, C = a.C;
   const int qbase = chunk * C;

@@ -494,7 +494,10 @@ __global__ void __launch_bounds__(64) attn_bwd_dq_mfma_kernel(b3_attn_bwd_args a
   __shared__ DqMfmaSmem<HD> sm;
   constexpr int KS = HD / 16, NDB = HD / 32, NP = HD / 8;
   const int lane = threadIdx.x, n = lane & 31, h = lane >> 5;
-  const int qt = blockIdx.x, b = blockIdx.y / a.H, hq = blockIdx.y % a.H, c = blockIdx.z;
+  // XCD-aware order: the query tiles and heads of one (kv head, chunk) read the same key and
+  // value blocks
+  const GridPos gp = xcd_grid_pos();
+  const int qt = gp.x, b = gp.y / a.H, hq = gp.y % a.H, c = gp.z;
   const int G = a.H / a.HKV, hkv = hq / G;
   const int tc = chunk_len(a, c), q0 = qt * 32;
   if (q0 >= tc) return;
@@ -635,12 +638,14 @@ __global__ void __launch_bounds__(64) attn_bwd_dkv_mfma_kernel(b3_attn_bwd_args 
   __shared__ DkvMfmaSmem<HD> sm;
   constexpr int KS = HD / 16, NDB = HD / 32, NP = HD / 8;
   const int lane = threadIdx.x, n = lane & 31, h = lane >> 5;
-  const int bh = blockIdx.y, b = bh / a.HKV, hkv = bh % a.HKV, c = blockIdx.z;
+  // XCD-aware order: the key blocks of one (bh, chunk) read the same query and dO rows
+  const GridPos gp = xcd_grid_pos();
+  const int bh = gp.y, b = bh / a.HKV, hkv = bh % a.HKV, c = gp.z;
   const int G = a.H / a.HKV;
   const int tc = chunk_len(a, c);
   const float sl = L2E / sqrtf((float)HD);
   const int n_fields = __popc(field_mask(a, c));
-  int fi = 0, j0 = blockIdx.x * 32;
+  int fi = 0, j0 = gp.x * 32;
   KField f = chunk_field<uint16_t>(a, b, hkv, c, 0);
   while (j0 >= f.len) {
     j0 -= (f.len + 31) / 32 * 32;

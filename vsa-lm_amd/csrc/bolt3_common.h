@@ -15,6 +15,19 @@
 
 namespace b3 {
 
+// Grid position in XCD-aware order.  Consecutive workgroups go to the 8 XCDs in turn, so
+// linear id L runs task (L % 8) * (N / 8) + L / 8 of the x-fastest grid order: neighbouring
+// tasks (which read the same tiles) share one XCD's L2.  Identity when the grid size N is not
+// a multiple of 8.
+struct GridPos { int x, y, z; };
+__device__ __forceinline__ GridPos xcd_grid_pos() {
+  const int gx = gridDim.x, gy = gridDim.y, gz = gridDim.z;
+  int wg = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
+  const int n = gx * gy * gz;
+  if (n % 8 == 0) wg = (wg % 8) * (n / 8) + wg / 8;
+  return GridPos{wg % gx, (wg / gx) % gy, wg / (gx * gy)};
+}
+
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));

@@ -1923,7 +1923,7 @@ struct MStepIn {
   }
 };
 
-// Columns [32*db, 32*db + 32) of M for row bh = blockIdx.x / (HD/32):
+// Columns [32*db, 32*db + 32) of M for row bh (workgroup bh * (HD/32) + db in XCD-aware order):
 //   E^T[d][j] = (v[j][d] - (K M)[j][d] / |k_j|) * bsafe_j / |k_j|
 //   M^T[d][c] <- gamma * M^T[d][c] + sum_j E^T[d][j] k[j][c]
 // Steps of at most 128 tokens (every forward and decoder step) keep the next step's inputs
@@ -1933,7 +1933,9 @@ __global__ void __launch_bounds__(MT) mres_kernel(b3_chain_args a) {
   __shared__ MSmem<T, HD> sm;
   using Sm = MSmem<T, HD>;
   constexpr int NDB = HD / 32, NCB = HD / 32;
-  const int bh = blockIdx.x / NDB, db = blockIdx.x % NDB;
+  // XCD-aware order: the NDB column blocks of one bh read the same keys and values
+  const int wg = xcd_grid_pos().x;
+  const int bh = wg / NDB, db = wg % NDB;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, n = lane & 31, h = lane >> 5;
   const int hkv = bh % a.HKV;
   const float gam = a.gamma[hkv];

@@ -297,7 +297,9 @@ struct MrecSmem {
 
 __global__ void __launch_bounds__(NT) m_rec_kernel(b3_chain_bwd_args a) {
   __shared__ MrecSmem sm;
-  const int bh = blockIdx.x / NCB, db = blockIdx.x % NCB;
+  // XCD-aware order: the NCB column blocks of one bh read the same per-step rows
+  const int wg = xcd_grid_pos().x;
+  const int bh = wg / NCB, db = wg % NCB;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, n = lane & 31, h = lane >> 5;
   const long long BH = (long long)a.B * a.HKV;
   const float gam = a.gamma[bh % a.HKV];

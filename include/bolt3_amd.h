@@ -446,8 +446,8 @@ typedef struct {
 int bolt3_rms_norm(const b3_rms_norm_args* a, void* stream);
 
 /*
- * Backward of the consolidation chain (bf16 storage, HD == 128, S == 128, at most 128 tokens
- * per step), from the forward chain's decision log and per-step snapshots.  The decisions are
+ * Backward of the consolidation chain (bf16 or fp32 storage, HD in {64, 128}, S == 128, at most
+ * 128 tokens per step), from the forward chain's decision log and per-step snapshots.  The decisions are
  * constants (the reference takes them under no_grad, vsa_lm/config/bolt3.py:98-112, :121-135,
  * :165-180); the gradient flows through the copies and mass-weighted means that fill, merge and
  * evict the slots (:121-155, :182-191) and through the Gershgorin-safe delta rule
@@ -467,7 +467,8 @@ typedef struct {
   const float* log;           /* [n_steps][B*HKV][B3_LOG_ROWS][B3_LOG_COLS] the forward's decision log */
   const float* snap_mass;     /* [n_steps][B*HKV][S] slot mass after every step */
   const float* snap_pm;       /* [n_steps][B*HKV][S] slot mean position after every step */
-  const float* snap_m;        /* [n_steps][B*HKV] blocks of HD*HD floats: M^T as bf16 hi then bf16 lo */
+  const float* snap_m;        /* [n_steps][B*HKV] blocks of HD*HD floats: bf16 storage M^T as bf16 hi then
+                                 bf16 lo, fp32 storage M[c][d] (the forward chain's snapshots) */
   const float* gamma;         /* [HKV] */
   const float* inv_freq;      /* [HD/2] */
   const float* d_slot_k;      /* [n_steps][B*HKV][S][HD] gradient of the roped slot keys the attention read */

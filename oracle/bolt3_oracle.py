@@ -245,13 +245,22 @@ def _retrieval(p, st, b, kp, v32, dt, bias, mask_inactive):
 
 
 def consolidate(p: Bolt3Params, st: SlotState | None, kr, kp, v, pos, beta, gam, b: int,
-                log: dict | None = None, ties: str = "torch") -> SlotState:
+                log: dict | None = None, ties: str = "torch", force: dict | None = None) -> SlotState:
     """One consolidation of a chunk that left the window (vsa_lm/config/bolt3.py:68-192).
 
     kr/kp/v: [bh, l, HD] storage dtype (un-roped, roped keys, values); pos: [l] or
     [bh, l] fp32 positions; beta: [bh, l]; gam: [HKV] fp32.  Returns the new state.
     ``log`` (optional dict) receives the per-token / per-slot decisions; ``ties`` selects
     the order among exactly equal scores (see ``_select``).
+
+    ``force`` imposes another implementation's decisions (see ``decisions_from_log``): fill
+    ``picked`` [bh, m] (slot n_filled + i takes token picked[:, i]); steady ``slot``, ``merge``
+    [bh, l] and the replacements ``top_toks``, ``bot_slots``, ``win`` [bh, min(l, S)] (token
+    top_toks[:, i] replaces slot bot_slots[:, i] where win[:, i]).  Every value is still computed
+    here; only which tokens go where is taken from ``force``.  ``log`` then holds this oracle's
+    own decisions from the same state, each stage given the forced stages before it: the merge
+    decisions from the state before the step, the replacements from the state after the forced
+    merges.
     """
     bh, l, hd = kr.shape
     dt = kr.dtype
@@ -281,6 +290,9 @@ def consolidate(p: Bolt3Params, st: SlotState | None, kr, kp, v, pos, beta, gam,
                 score = F.normalize(v32, dim=-1).var(dim=-1)
                 init_u = torch.full((bh, l), 0.15)
             picked = _select(score, m, True, ties)[1]                          # [bh, m]
+        own_picked = picked
+        if force is not None:
+            picked = force["picked"][:, :m].long()
         slots = torch.arange(st.n_filled, st.n_filled + m).expand(bh, m)
         st.ak[rows, slots] = kr[rows, picked]
         st.av[rows, slots] = v[rows, picked]
@@ -289,7 +301,7 @@ def consolidate(p: Bolt3Params, st: SlotState | None, kr, kp, v, pos, beta, gam,
         st.util[rows, slots] = init_u[rows, picked]
         st.act[rows, slots] = True
         if log is not None:
-            log.update(kind="fill", picked=picked.clone(), score=score.clone())
+            log.update(kind="fill", picked=own_picked.clone(), score=score.clone())
         st.n_filled += m
         return st
 
@@ -305,6 +317,9 @@ def consolidate(p: Bolt3Params, st: SlotState | None, kr, kp, v, pos, beta, gam,
         sim_v = F.cosine_similarity(v32, partner, dim=-1)
         score = rel * (1.0 - best.clamp(0.0, 1.0))
         merge = (best >= SIM_K) & (sim_v >= SIM_V)
+        own = dict(slot=slot, merge=merge)
+        if force is not None:
+            slot, merge = force["slot"][:, :l].long(), force["merge"][:, :l].bool()
 
     # merge: mass-weighted means of the slot and the tokens assigned to it
     onehot = F.one_hot(slot, num_classes=S).float() * merge.float().unsqueeze(-1)   # [bh, l, S]
@@ -332,6 +347,9 @@ def consolidate(p: Bolt3Params, st: SlotState | None, kr, kp, v, pos, beta, gam,
         tv, tj = _select(cand, kc, True, ties)
         bv, bs = _select(keep, kc, False, ties)
         win = (tv > bv) & (tv > -1e8)
+        own.update(top_toks=tj, bot_slots=bs, win=win)
+        if force is not None:
+            tj, bs, win = force["top_toks"][:, :kc].long(), force["bot_slots"][:, :kc].long(), force["win"][:, :kc].bool()
         inserted = torch.zeros(bh, l, dtype=torch.bool)
         inserted[rows, tj] = win
         to_delta = (~merge) & (~inserted)
@@ -355,11 +373,14 @@ def consolidate(p: Bolt3Params, st: SlotState | None, kr, kp, v, pos, beta, gam,
     st.m_res = gam.repeat(b).view(bh, 1, 1) * st.m_res + torch.bmm(kn.transpose(1, 2), err)
 
     if log is not None:
-        log.update(kind="steady", best=best.clone(), slot=slot.clone(), sim_v=sim_v.clone(),
+        own_ins = torch.zeros(bh, l, dtype=torch.bool)
+        own_ins[rows, own["top_toks"]] = own["win"]
+        log.update(kind="steady", best=best.clone(), slot=own["slot"].clone(), sim_v=sim_v.clone(),
                    best2=cos.topk(2, dim=-1).values[..., 1].clone(),
-                   rel=rel.clone(), score=score.clone(), merge=merge.clone(), keep=keep.clone(),
-                   top_vals=tv.clone(), top_toks=tj.clone(), bot_vals=bv.clone(), bot_slots=bs.clone(),
-                   win=win.clone(), delta=to_delta.clone())
+                   rel=rel.clone(), score=score.clone(), merge=own["merge"].clone(), keep=keep.clone(),
+                   top_vals=tv.clone(), top_toks=own["top_toks"].clone(), bot_vals=bv.clone(),
+                   bot_slots=own["bot_slots"].clone(), win=own["win"].clone(),
+                   delta=((~merge) & (~own_ins)).clone(), delta_applied=to_delta.clone())
     return st
 
 
@@ -420,8 +441,13 @@ class ForwardTrace:
     heads: tuple | None = None                   # (q_raw, q_rope, k_raw, k_rope, v, beta, eta)
 
 
-def forward(p: Bolt3Params, x: torch.Tensor, trace: ForwardTrace | None = None, ties: str = "torch") -> torch.Tensor:
-    """Bolt3Attn.forward (vsa_lm/config/bolt3.py:194-276).  Returns [b, T, D]."""
+def forward(p: Bolt3Params, x: torch.Tensor, trace: ForwardTrace | None = None, ties: str = "torch",
+            decisions=None) -> torch.Tensor:
+    """Bolt3Attn.forward (vsa_lm/config/bolt3.py:194-276).  Returns [b, T, D].
+
+    ``decisions``: optional sequence, one entry per consolidation step (``force`` of
+    ``consolidate``, or None to decide freely), imposing another implementation's slot decisions
+    so that its whole output can be compared with this arithmetic along its own trajectory."""
     b, T, _ = x.shape
     q_raw, k_raw, v_all, beta_all, eta_all = project(p, x)
     q_rope = rope_at(q_raw, torch.arange(T, dtype=torch.float32), p.inv_freq)
@@ -434,6 +460,7 @@ def forward(p: Bolt3Params, x: torch.Tensor, trace: ForwardTrace | None = None, 
     sinks = st = None
     prev = None            # (start, end) of the chunk held as "prev"
     ys = []
+    n_done = 0
     for s0 in range(0, T, p.C):
         e0 = min(T, s0 + p.C)
         tc = e0 - s0
@@ -458,7 +485,9 @@ def forward(p: Bolt3Params, x: torch.Tensor, trace: ForwardTrace | None = None, 
                 chunk = (flat(k_raw[:, :, a:z]), flat(k_rope[:, :, a:z]), flat(v_all[:, :, a:z]),
                          torch.arange(a, z, dtype=torch.float32), flat(beta_all[:, :, a:z]))
                 log = {} if trace is not None else None
-                st = consolidate(p, st, *chunk, gam, b, log=log, ties=ties)
+                force = decisions[n_done] if decisions is not None else None
+                st = consolidate(p, st, *chunk, gam, b, log=log, ties=ties, force=force)
+                n_done += 1
                 if trace is not None:
                     trace.states.append(st.clone())
                     trace.logs.append(log)
@@ -512,12 +541,13 @@ class LayerCache:
 
 
 def layer_step(p: Bolt3Params, h: torch.Tensor, pos_start: int, m_state: torch.Tensor, cache: LayerCache,
-               log: list | None = None, ties: str = "torch"):
+               log: list | None = None, ties: str = "torch", force=None):
     """Bolt-3 branch of Bolt3Decoder.step for one layer (vsa_lm/config/bolt3.py:343-425).
 
     h: normed input [b, t, D].  m_state: M_res [b, HKV, HD, HD] fp32.  Returns
     (attention output before o_proj [b, H, t, HD], o_proj output [b, t, D], new m_state).
-    ``cache`` is updated in place.
+    ``cache`` is updated in place.  ``force``: a callable returning the decisions to impose on
+    the consolidation this step runs (``force`` of ``consolidate``), called only when one runs.
     """
     b, t, _ = h.shape
     q_r, k_r, v_n, beta_n, eta_n = project(p, h)
@@ -559,7 +589,7 @@ def layer_step(p: Bolt3Params, h: torch.Tensor, pos_start: int, m_state: torch.T
             lg = {} if log is not None else None
             cache.st = consolidate(p, st_in, kr_.reshape(bh, n, p.HD), kp_.reshape(bh, n, p.HD),
                                    v_.reshape(bh, n, p.HD), pos_.reshape(n), b_.reshape(bh, n), gam, b, log=lg,
-                                   ties=ties)
+                                   ties=ties, force=None if force is None else force())
             if log is not None:
                 log.append(lg)
             m_state = cache.st.m_res.view(b, p.HKV, p.HD, p.HD)
@@ -573,15 +603,28 @@ class HybridRef:
     UniversalVSALM attribute names (embed_tokens, blocks[i].{norm1,norm2,mlp,vsa|attn},
     norm, lm_head)."""
 
-    def __init__(self, model, C: int = 128, ties: str = "torch", logs: dict | None = None):
+    def __init__(self, model, C: int = 128, ties: str = "torch", logs: dict | None = None,
+                 decisions: dict | None = None):
         self.model = model
         self.C = C
         self.ties = ties
         self.logs = logs            # optional {layer: [decision log of each consolidation]}
+        # optional {layer: [decisions to impose on each consolidation, in order]} (consolidate's
+        # ``force``): the oracle then follows another implementation's trajectory
+        self.decisions = decisions
+        self._n_forced: dict = {}
         self.params = {}
         for li, blk in enumerate(model.blocks):
             if hasattr(blk, "vsa"):
                 self.params[li] = Bolt3Params.from_module(blk.vsa)
+
+    def _next_forced(self, li: int):
+        i = self._n_forced.get(li, 0)
+        self._n_forced[li] = i + 1
+        seq = self.decisions[li]
+        if i >= len(seq):
+            raise IndexError(f"layer {li}: consolidation {i} has no decisions to impose ({len(seq)} given)")
+        return seq[i]
 
     def blank(self, b: int):
         st = {}
@@ -603,7 +646,10 @@ class HybridRef:
             if li in self.params:
                 ms, cache = state[li]
                 lg = None if self.logs is None else self.logs.setdefault(li, [])
-                _, out, ms = layer_step(self.params[li], h, pos_start, ms, cache, log=lg, ties=self.ties)
+                fc = None
+                if self.decisions is not None and li in self.decisions:
+                    fc = (lambda li=li: self._next_forced(li))
+                _, out, ms = layer_step(self.params[li], h, pos_start, ms, cache, log=lg, ties=self.ties, force=fc)
                 state[li][0] = ms
                 x = x + out
             else:

@@ -9,7 +9,8 @@ them the seeded synthetic inputs of tests/golden/recipes.py and stores what
 they compute as safetensors files next to this script.  These pin the parts of
 the oracle that no closed form covers: the composite Bolt3Attn.forward
 (vsa_lm/config/bolt3.py:194-276), the multi-step _consolidate_functional
-trajectories (:68-192), the Bolt3Decoder.step state machine (:335-457) and the
+trajectories (:68-192), the Bolt3Decoder.step state machine (:335-457), the
+generation rules of generate_batch (:459-500), memorize / forget (:528-557) and the
 gradients of the forward (CPU autograd, fp32).
 
 Every file carries a JSON header in its metadata (torch version, case
@@ -157,6 +158,92 @@ def decoder_case(name, seed, dtype, n_prompt, n_decode, B=2):
     print(f"{name}: steps={n_decode} n_filled={meta['n_filled']}")
 
 
+def _ref_model(seed, tied=True, vocab=96):
+    """The reference's UniversalVSALM of the decoder fixtures: two layers (Bolt-3, softmax anchor),
+    hidden 64; with ``tied=False`` an output head of its own (drawn by the recipe), so that greedy
+    tokens depend on the context instead of repeating the last token.  With a vocabulary of 96
+    every token's key repeats within a chunk, so tokens merge into slots and nothing reaches
+    M_res; the memory case takes 1024."""
+    from vsa_lm.config.standard import UniversalVSALM
+    mcfg = dict(vocab_size=vocab, dim=64, num_layers=2, num_heads=4, num_kv_heads=2, intermediate=128,
+                max_T=4096, chunk_size=32, hybrid_every=0, rope_theta=10000.0, eps=1e-5, head_dim=64,
+                tie_word_embeddings=tied, layer_types=["vsa", "softmax"], is_bolt3=True,
+                bolt3_S=128, bolt3_C=128, qk_norm=True)
+    model = UniversalVSALM(**mcfg)
+    shapes = [(k, tuple(v.shape)) for k, v in model.state_dict().items()]
+    model.load_state_dict(recipes.model_params(shapes, seed, head=not tied), strict=False)
+    recipes.init_module(model.blocks[0].vsa, seed, nondefault=True)
+    inputs = {f"param.{k}": v for k, v in model.state_dict().items()}
+    return model.eval(), mcfg, inputs
+
+
+def generate_case(name, seed, n_prompt, n_new, eos, close, B=3):
+    """Bolt3Decoder.generate_batch at temperature 0 (vsa_lm/config/bolt3.py:459-500): per-row end of
+    sequence, the forced close-of-thinking sequence at the budget point, the all-rows-done test
+    every 16 tokens.  Stores the tokens, the lengths and, per step, the smallest top-2 logit gap
+    over the rows (where a greedy pick could go either way)."""
+    from vsa_lm.config.bolt3 import Bolt3Decoder
+    model, mcfg, inputs = _ref_model(seed, tied=False)
+    ids = recipes.tokens(seed, B, n_prompt, mcfg["vocab_size"])
+    inputs["ids"] = ids.float()
+    gaps = []
+
+    def gap_hook(mod, inp, out):
+        top2 = out.float().topk(2, dim=-1).values
+        gaps.append(float((top2[..., 0] - top2[..., 1]).min()))
+
+    hook = model.lm_head.register_forward_hook(gap_hook)
+    with torch.no_grad():
+        toks, lengths = Bolt3Decoder(model).generate_batch(ids, n_new, temperature=0.0, eos_ids=set(eos),
+                                                           close_think_ids=list(close))
+    hook.remove()
+    tensors = {"toks": toks.contiguous(), "lengths": lengths.contiguous(),
+               "gaps": torch.tensor(gaps[:toks.shape[1]], dtype=torch.float32)}
+    meta = dict(case=name, torch=torch.__version__, model_cfg=mcfg, seed=seed, B=B, n_prompt=n_prompt, n_new=n_new,
+                eos_ids=sorted(eos), close_think_ids=list(close), dtype="float32", inputs_sha256=digest(inputs))
+    save_file(tensors, os.path.join(HERE, f"{name}.safetensors"), metadata={"header": json.dumps(meta)})
+    print(f"{name}: tokens {tuple(toks.shape)} lengths {lengths.tolist()} smallest gap {min(gaps):.4g}")
+
+
+def memory_case(name, seed, n_prompt, n_doc, n_after, n_probe, B=2):
+    """Bolt3Decoder.memorize then forget (vsa_lm/config/bolt3.py:528-557): prefill a prompt,
+    memorize a document (its trace: M_after - gamma^(len // C) M_before per Bolt-3 layer), feed
+    more tokens, forget the trace (decayed by gamma per C positions since its end), then step a
+    few tokens on the result.  Stores the trace, M_res after memorize, before and after forget,
+    and the probe steps' hidden states."""
+    from vsa_lm.config.bolt3 import Bolt3Decoder
+    model, mcfg, inputs = _ref_model(seed, tied=True, vocab=1024)
+    n = n_prompt + n_doc + n_after + n_probe
+    ids = recipes.tokens(seed, B, n, mcfg["vocab_size"])
+    inputs["ids"] = ids.float()
+    dec = Bolt3Decoder(model)
+    C = dec.C
+    with torch.no_grad():
+        _, states, kv = dec.prefill(ids[:, :n_prompt])
+        states, kv, pos, traces = dec.memorize(ids[:, n_prompt:n_prompt + n_doc], states, kv, n_prompt)
+        m_mem = states[0].clone()
+        for s0 in range(n_prompt + n_doc, n_prompt + n_doc + n_after, C):
+            e0 = min(n_prompt + n_doc + n_after, s0 + C)
+            _, states, kv = dec.step(ids[:, s0:e0], s0, states, kv)
+        m_before = states[0].clone()
+        nxt = n_prompt + n_doc + n_after
+        states = dec.forget(traces, states, nxt)
+        m_after = states[0].clone()
+        hs = []
+        for i in range(n_probe):
+            h, states, kv = dec.step(ids[:, nxt + i:nxt + i + 1], nxt + i, states, kv)
+            hs.append(h[:, -1].clone())
+    tensors = {"trace": traces[0][1].contiguous(), "m_memorized": m_mem.contiguous(),
+               "m_before_forget": m_before.contiguous(), "m_after_forget": m_after.contiguous(),
+               "h_probe": torch.stack(hs, dim=1).contiguous()}
+    meta = dict(case=name, torch=torch.__version__, model_cfg=mcfg, seed=seed, B=B, n_prompt=n_prompt, n_doc=n_doc,
+                n_after=n_after, n_probe=n_probe, trace_end=int(traces[0][0]), dtype="float32",
+                inputs_sha256=digest(inputs))
+    save_file(tensors, os.path.join(HERE, f"{name}.safetensors"), metadata={"header": json.dumps(meta)})
+    print(f"{name}: trace end {traces[0][0]} |trace| {float(traces[0][1].norm()):.4g} "
+          f"|M before forget| {float(m_before.norm()):.4g} |M after| {float(m_after.norm()):.4g}")
+
+
 CASES = [
     # name, cfg args, B, T, seed, dtype, nondefault, clustered, rows_every
     ("fwd_fp32_default", (64, 4, 2, 64, 10000.0, 1e-5, False, False), 2, 896, 1, "float32", False, None, 1),
@@ -187,6 +274,20 @@ DECODER_CASES = [
     ("dec_fp32", 6, "float32", 300, 220),
     ("dec_bf16", 9, "bfloat16", 300, 220),
 ]
+GENERATE_CASES = [
+    # name, seed, prompt tokens, new tokens, eos ids, close-of-thinking ids
+    # rows 1 and 2 end early (eos 77); row 0 runs on and is forced through 5, 6, 7 at the budget point
+    ("gen_eos_close", 42, 260, 150, (77,), (5, 6, 7)),
+    # row 0 closes on its own (it emits 21, the sequence's second id); every row has ended by token 8,
+    # so the loop stops at the check after token 16
+    ("gen_all_done", 42, 260, 150, (77, 87), (5, 21, 7)),
+    # row 0 closes on its own and never ends: the full 150 tokens
+    ("gen_full_length", 42, 260, 150, (77,), (5, 21, 7)),
+]
+MEMORY_CASES = [
+    # name, seed, prompt, document, tokens between memorize and forget, probe steps
+    ("mem_forget", 12, 260, 384, 256, 8),
+]
 
 
 def main(ref_root: str, only=()):
@@ -201,6 +302,12 @@ def main(ref_root: str, only=()):
     for name, seed, dt, n_prompt, n_decode in DECODER_CASES:
         if not only or name in only:
             decoder_case(name, seed=seed, dtype=getattr(torch, dt), n_prompt=n_prompt, n_decode=n_decode)
+    for name, seed, n_prompt, n_new, eos, close in GENERATE_CASES:
+        if not only or name in only:
+            generate_case(name, seed, n_prompt, n_new, eos, close)
+    for name, seed, n_prompt, n_doc, n_after, n_probe in MEMORY_CASES:
+        if not only or name in only:
+            memory_case(name, seed, n_prompt, n_doc, n_after, n_probe)
 
 
 if __name__ == "__main__":

@@ -93,9 +93,11 @@ def tokens(seed: int, B: int, T: int, vocab: int) -> torch.Tensor:
     return torch.from_numpy(rng.integers(0, vocab, size=(B, T))).long()
 
 
-def model_params(named_shapes, seed: int) -> dict:
+def model_params(named_shapes, seed: int, head: bool = False) -> dict:
     """Non-Bolt-3 weights of a small hybrid model: 2-D weights ~N(0, 0.02), the
-    embedding ~N(0, 1); norms keep their ones."""
+    embedding ~N(0, 1); norms keep their ones.  ``head``: an untied output head,
+    drawn ~N(0, 1) after everything else (with tied embeddings the head is the
+    embedding and is not drawn)."""
     rng = np.random.default_rng([seed, 4])
     out = {}
     for name, shape in sorted(named_shapes):
@@ -103,4 +105,7 @@ def model_params(named_shapes, seed: int) -> dict:
             out[name] = _n(rng, tuple(shape), 1.0)
         elif len(shape) == 2 and "beta_proj" not in name and "eta_proj" not in name and name != "lm_head.weight":
             out[name] = _n(rng, tuple(shape), 0.02)
+    if head:
+        shape = dict(named_shapes)["lm_head.weight"]
+        out["lm_head.weight"] = _n(np.random.default_rng([seed, 6]), tuple(shape), 1.0)
     return out

@@ -76,19 +76,26 @@ def test_rejects_bad_arguments_without_gpu_work():
     sk.S = 64
     assert lib.bolt3_slot_keys(ctypes.byref(sk), None) == 1002        # S != 128
     cb = A.ChainBwdArgs()
-    cb.dtype, cb.B, cb.HKV, cb.HD, cb.S, cb.T = 0, 1, 1, 128, 128, 512
+    cb.dtype, cb.B, cb.HKV, cb.HD, cb.S, cb.T = 2, 1, 1, 128, 128, 512
     cb.n_steps, cb.off0, cb.len0, cb.step_stride, cb.step_len = 2, 4, 124, 128, 128
-    assert lib.bolt3_chain_bwd(ctypes.byref(cb), None) == 1002        # fp32 storage: not this entry point
-    cb.dtype, cb.HD = 1, 64
-    assert lib.bolt3_chain_bwd(ctypes.byref(cb), None) == 1002        # head dim 64
-    cb.HD, cb.step_len = 128, 200
+    assert lib.bolt3_chain_bwd(ctypes.byref(cb), None) == 1002        # unknown dtype code
+    cb.dtype, cb.HD = 1, 96
+    assert lib.bolt3_chain_bwd(ctypes.byref(cb), None) == 1002        # head dim not 64 or 128
+    cb.HD, cb.S = 64, 64
+    assert lib.bolt3_chain_bwd(ctypes.byref(cb), None) == 1002        # S != 128
+    cb.S = 128
+    for dt, hd in ((0, 64), (0, 128), (1, 64)):                       # fp32 and head dim 64 are taken
+        cb.dtype, cb.HD = dt, hd
+        assert lib.bolt3_chain_bwd(ctypes.byref(cb), None) == 1001    # (null pointers)
+    cb.dtype, cb.HD, cb.step_len = 1, 128, 200
     assert lib.bolt3_chain_bwd(ctypes.byref(cb), None) == 1002        # steps longer than 128 tokens
     cb.step_len, cb.T = 128, 200
     assert lib.bolt3_chain_bwd(ctypes.byref(cb), None) == 1001        # steps past the sequence
     cb.T = 512
     assert lib.bolt3_chain_bwd(ctypes.byref(cb), None) == 1001        # null pointers
     assert lib.bolt3_chain_bwd_workspace_bytes(4, 8, 128, 30) == 4 * 30 * 32 * 4 * 128 + 30 * 32 * 128 * 128 * 4
-    assert lib.bolt3_chain_bwd_workspace_bytes(4, 8, 64, 30) == 0
+    assert lib.bolt3_chain_bwd_workspace_bytes(4, 8, 64, 30) == 4 * 30 * 32 * 4 * 128 + 30 * 32 * 64 * 64 * 4
+    assert lib.bolt3_chain_bwd_workspace_bytes(4, 8, 96, 30) == 0
     d2 = A.DecodeArgs()
     d2.dtype, d2.B, d2.H, d2.HKV, d2.HD, d2.S, d2.has_slots = 1, 1, 4, 1, 128, 256, 1
     assert lib.bolt3_decode(ctypes.byref(d2), None) in (1001, 1002)   # rejected before any launch

@@ -1,6 +1,6 @@
-"""The host half of the backward on the CPU: the slot replay and the consolidation chain's
-reverse pass (bolt3_amd/backward.py) against autograd through the oracle's consolidate, which
-the reference's gradient fixtures pin (test_oracle_golden.py).
+"""The torch restatement of the chain's backward on the CPU (tests/chain_bwd_ref.py, the checker
+of the HIP chain backward): the slot replay and the reverse pass against autograd through the
+oracle's consolidate, which the reference's gradient fixtures pin (test_oracle_golden.py).
 
 The decision log is the chain kernel's format (include/bolt3_amd.h, B3_LOG_*), filled here from
 the oracle's per-step decisions, so no kernel runs."""
@@ -8,7 +8,7 @@ import pytest
 import torch
 
 from bolt3_amd import _abi as A
-from bolt3_amd.backward import chain_backward, replay_slots
+from chain_bwd_ref import chain_backward, replay_slots
 from helpers import build_grad_case, fixture, rel_err
 from oracle import bolt3_oracle as O
 

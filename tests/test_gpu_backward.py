@@ -1,4 +1,4 @@
-"""Backward of Bolt3Attn on the HIP path (bolt3_attn_bwd + the chain replay).
+"""Backward of Bolt3Attn on the HIP path (bolt3_attn_bwd, bolt3_chain_bwd, bolt3_heads_bwd).
 
 * Against the reference's own gradients (tests/golden/grad_*.safetensors, fp32 CPU autograd
   through vsa_lm/config/bolt3.py): the gradient of x and of every parameter within 1e-4
@@ -76,7 +76,7 @@ def test_backward_bf16_hd128_vs_oracle(gpu):
 
 def test_backward_under_autocast_and_repeatable(gpu):
     """fp32 parameters under bf16 autocast (the heal trainer's setting): parameter gradients
-    come back in fp32, x's in fp32, two backward passes give identical gradients, and the
+    come back in fp32, x's in fp32, two forward + backward passes give identical gradients, and the
     output equals the no-grad forward's."""
     g, meta = fixture("grad_fp32_eta")
     mod, x, up = build_grad_case(meta)
@@ -100,3 +100,48 @@ def test_backward_under_autocast_and_repeatable(gpu):
     assert torch.equal(y0, res[0][0])
     # against the fixture's fp32 gradients: bf16 storage, so a loose bound
     assert cosine(res[0][1].cpu(), g["grad.x"]) >= 0.99
+
+
+def test_backward_under_activation_checkpointing(gpu):
+    """The heal trainer wraps every block in torch.utils.checkpoint(use_reentrant=False)
+    (vsa_lm/converter.py:698-700): the layer's trace goes through save_for_backward, so between
+    the forward and the backward the checkpointed layer holds none of it (the device memory it
+    adds over its output is under a quarter of the plain run's), the backward recomputes it, and
+    the gradients equal the plain run's bit for bit (the forward is deterministic).  A second
+    backward with retain_graph=True gives the same gradients again."""
+    from torch.utils.checkpoint import checkpoint
+    from bolt3_amd import Bolt3Attn
+    cfg = dict(dim=1024, num_heads=8, num_kv_heads=2, head_dim=128, rope_theta=1e6, eps=1e-6, qk_norm=True)
+    mod = recipes.init_module(Bolt3Attn(cfg), 43, nondefault=True).to(torch.bfloat16).to(gpu)
+    x = recipes.clustered_hidden(43, 2, 2048, 1024, n_centres=512, noise=0.15).to(torch.bfloat16).to(gpu)
+    up = recipes.upstream(43, 2, 2048, 1024).to(torch.bfloat16).to(gpu)
+    print("[case] backward under activation checkpointing", flush=True)
+
+    def run(ckpt: bool, twice: bool = False):
+        mod.zero_grad(set_to_none=True)
+        xg = x.clone().requires_grad_(True)
+        torch.cuda.synchronize()
+        base = torch.cuda.memory_allocated(gpu)
+        y = checkpoint(mod, xg, use_reentrant=False) if ckpt else mod(xg)
+        torch.cuda.synchronize()
+        held = torch.cuda.memory_allocated(gpu) - base - y.numel() * y.element_size()
+        torch.cuda.reset_peak_memory_stats(gpu)
+        loss = (y * up).sum()
+        loss.backward(retain_graph=twice)
+        peak = torch.cuda.max_memory_allocated(gpu) - base
+        grads = [xg.grad.clone()] + [p.grad.clone() for p in mod.parameters()]
+        if twice:
+            xg.grad = None
+            mod.zero_grad(set_to_none=True)
+            loss.backward()
+            again = [xg.grad.clone()] + [p.grad.clone() for p in mod.parameters()]
+            assert all(torch.equal(a, b) for a, b in zip(grads, again))
+        return grads, held, peak
+
+    g_plain, held_plain, peak_plain = run(False, twice=True)
+    g_ckpt, held_ckpt, peak_ckpt = run(True)
+    print(f"[case] held between forward and backward: plain {held_plain / 2**20:.1f} MiB, checkpointed "
+          f"{held_ckpt / 2**20:.1f} MiB; backward peak: plain {peak_plain / 2**20:.1f} MiB, checkpointed "
+          f"{peak_ckpt / 2**20:.1f} MiB", flush=True)
+    assert held_plain > 0 and held_ckpt < held_plain / 4
+    assert all(torch.equal(a, b) for a, b in zip(g_plain, g_ckpt))

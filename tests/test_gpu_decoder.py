@@ -97,22 +97,38 @@ def test_state_round_trip_through_reference_dict(dtype, gpu):
     assert torch.equal(states[0], states2[0])
 
 
-def test_state_setitem_rewrites_state(gpu):
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_state_setitem_rewrites_state(dtype, gpu):
     """Assigning a reference key rewrites that part (here: the slot masses) and the cached slot
-    bias follows."""
+    bias follows: kappa * log(max(mass, 1)) on active slots, after the prefill and after the
+    assignment.  kappa is not 1 and differs per kv head; in bf16 the module's kappa and inv_freq
+    are converted to fp32 for the rotation kernel, so a conversion freed before that kernel runs
+    would show here as a wrong bias."""
     from bolt3_amd import Bolt3Decoder
-    model = _model(6, ["vsa"]).to(gpu)
+    model = _model(6, ["vsa"], dtype=dtype)
+    ly = model.blocks[0].vsa
+    with torch.no_grad():
+        ly.kappa.copy_(torch.tensor([0.75, 1.625]).to(ly.kappa.dtype))
+    model = model.to(gpu)
     dec = Bolt3Decoder(model)
     ids = recipes.tokens(6, 1, 400, 1024).to(gpu)
+    kap = ly.kappa.float().to(gpu).view(-1, 1)
+
+    def expect_bias(st):
+        b = kap * torch.log(st["mass"].clamp_min(1.0))
+        return b.masked_fill(~st["act"], float("-inf"))
+
     with torch.no_grad():
         _, states, kv = dec.prefill(ids)
         st = kv[0]
+        assert torch.allclose(st.slot_bias, expect_bias(st), rtol=1e-6, atol=0.0)
         m = st["mass"].clone()
         m[:, 5] = 7.0
+        m[:, 17:40] = torch.linspace(1.5, 30.0, 23, device=gpu)
         st["mass"] = m
         assert torch.equal(st["mass"], m)
-        kap = model.blocks[0].vsa.kappa.float().to(gpu)
-        assert torch.allclose(st.slot_bias[:, 5], kap * torch.log(torch.tensor(7.0, device=gpu)), rtol=1e-6)
+        assert torch.allclose(st.slot_bias[:, 5], kap[:, 0] * torch.log(torch.tensor(7.0, device=gpu)), rtol=1e-6)
+        assert torch.allclose(st.slot_bias, expect_bias(st), rtol=1e-6, atol=0.0)
         assert set(st.keys()) == set(st.KEYS) and st.get("n_filled") == 128
 
 
@@ -288,3 +304,87 @@ def test_serve_generate_completion(gpu):
     assert reply[:n_cmp] == expect[:n_cmp], (reply, expect)
     if n_cmp == len(gaps):
         assert reply == expect
+
+
+@pytest.mark.parametrize("name", ["gen_eos_close", "gen_all_done", "gen_full_length"])
+def test_generate_matches_reference_fixture(name, gpu):
+    """generate_batch (greedy, B = 3) against the reference's own tokens and lengths
+    (tests/golden/gen_*: per-row end of sequence, the forced close-of-thinking sequence at the
+    budget point, a row closing on its own, the all-rows-done stop at a 16-token check, a row
+    running to the 150-token limit).  Every greedy pick of the fixtures has a top-2 logit gap
+    above 0.06, so the tokens must match exactly; the graph-replayed step is not used (fp32)."""
+    from bolt3_amd import Bolt3Decoder
+    from helpers import build_fixture_model, fixture
+    g, meta = fixture(name)
+    model, ids = build_fixture_model(meta, meta["n_prompt"])
+    print(f"[case] generate vs reference fixture {name}", flush=True)
+    dec = Bolt3Decoder(model.to(gpu))
+    with torch.no_grad():
+        toks, lengths = dec.generate_batch(ids.to(gpu), meta["n_new"], temperature=0.0,
+                                           eos_ids=set(meta["eos_ids"]), close_think_ids=meta["close_think_ids"])
+    assert toks.shape == g["toks"].shape and torch.equal(toks.cpu(), g["toks"])
+    assert torch.equal(lengths.cpu(), g["lengths"])
+
+
+def test_memorize_forget_matches_reference_fixture(gpu):
+    """memorize -> more tokens -> forget -> decode (tests/golden/mem_forget, the reference's own
+    vectors): the trace, M_res after memorize, before and after forget, and the hidden states of
+    the steps decoded afterwards, fp32 tolerance."""
+    from bolt3_amd import Bolt3Decoder
+    from helpers import build_fixture_model, fixture
+    g, meta = fixture("mem_forget")
+    n0, nd, na, npb = meta["n_prompt"], meta["n_doc"], meta["n_after"], meta["n_probe"]
+    model, ids = build_fixture_model(meta, n0 + nd + na + npb)
+    print("[case] memorize / forget vs reference fixture", flush=True)
+    dec = Bolt3Decoder(model.to(gpu))
+    ids = ids.to(gpu)
+    with torch.no_grad():
+        _, states, kv = dec.prefill(ids[:, :n0])
+        states, kv, pos, traces = dec.memorize(ids[:, n0:n0 + nd], states, kv, n0)
+        assert pos == meta["trace_end"] and traces[1] is None
+        _close(traces[0][1].cpu(), g["trace"], torch.float32, "trace")
+        _close(states[0].cpu(), g["m_memorized"], torch.float32, "M_res after memorize")
+        _, pos = dec._feed(ids[:, n0 + nd:n0 + nd + na], pos, states, kv)
+        _close(states[0].cpu(), g["m_before_forget"], torch.float32, "M_res before forget")
+        states = dec.forget(traces, states, pos)
+        _close(states[0].cpu(), g["m_after_forget"], torch.float32, "M_res after forget")
+        hs = []
+        for i in range(npb):
+            h, states, kv = dec.step(ids[:, pos + i:pos + i + 1], pos + i, states, kv)
+            hs.append(h[:, -1])
+    _close(torch.stack(hs, dim=1).cpu(), g["h_probe"], torch.float32, "steps after forget")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_step_longer_than_a_chunk(dtype, gpu):
+    """A step of more than C tokens (the reference's step takes any t, vsa_lm/config/bolt3.py:335-425):
+    200 tokens at once on a current chunk of 44 (one attention over the window and all 244
+    tokens, then one consolidation, after which the previous chunk holds 244 tokens), then
+    single tokens across the next consolidation (of those 244 tokens), every step against the
+    oracle's layer_step; a step that would make a chunk of more than 2C tokens is refused before
+    any state changes."""
+    from bolt3_amd import Bolt3Decoder
+    print(f"[case] step of 200 tokens mid-chunk {dtype}", flush=True)
+    model = _model(13, ["vsa", "softmax"], dtype=dtype)
+    ref = O.HybridRef(model)
+    dec = Bolt3Decoder(copy.deepcopy(model).to(gpu))
+    ids = recipes.tokens(13, 2, 300 + 200 + 140, 1024)
+    with torch.no_grad():
+        h_r, st_r = ref.prefill(ids[:, :300])
+        h, states, kv = dec.prefill(ids[:, :300].to(gpu))
+        assert kv[0].cur[1] == 44
+        h_r = ref.step(ids[:, 300:500], 300, st_r)
+        h, states, kv = dec.step(ids[:, 300:500].to(gpu), 300, states, kv)
+        _close(h.float().cpu(), h_r.float(), dtype, "200-token step")
+        assert kv[0].prev[1] == 244 and kv[0].cur[1] == 0
+        for i in range(140):
+            pos = 500 + i
+            h_r = ref.step(ids[:, pos:pos + 1], pos, st_r)
+            h, states, kv = dec.step(ids[:, pos:pos + 1].to(gpu), pos, states, kv)
+            _close(h.float().cpu(), h_r.float(), dtype, f"step {i}")
+        assert kv[0].n_filled == st_r[0][1].st.n_filled
+        _close(states[0].cpu(), st_r[0][0], torch.float32 if dtype == torch.float32 else torch.bfloat16, "M_res")
+        before = (states[0].clone(), kv[0].cur, kv[1].n)
+        with pytest.raises(NotImplementedError):
+            dec.step(ids[:, :250].to(gpu), 640, states, kv)
+        assert torch.equal(states[0], before[0]) and kv[0].cur == before[1] and kv[1].n == before[2]

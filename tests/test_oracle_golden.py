@@ -2,7 +2,8 @@
 
 The fixtures were written by tests/golden/make_golden.py from
 vsa_lm/config/bolt3.py (Bolt3Attn.forward, the _consolidate_functional
-trajectory, Bolt3Decoder.prefill/step).  In fp32 the oracle issues the same
+trajectory, Bolt3Decoder.prefill/step, generate_batch's generation rules,
+memorize / forget).  In fp32 the oracle issues the same
 torch ops in the same order, so outputs and slot states match to the last bit
 on the machine that wrote them; the check allows 1e-6 relative to absorb a
 different CPU's BLAS blocking, and requires the slot decisions (activity,
@@ -13,7 +14,7 @@ import torch
 
 from oracle.bolt3_oracle import Bolt3Params, ForwardTrace, HybridRef, forward
 from oracle.torch_topk_order import tie_in_prefix, topk_order_wave
-from helpers import build_grad_case, build_layer, build_model, fixture, rel_err
+from helpers import build_fixture_model, build_grad_case, build_layer, build_model, fixture, rel_err
 from oracle import bolt3_oracle as O
 
 FWD = ["fwd_fp32_default", "fwd_fp32_eta", "fwd_fp32_g3", "fwd_bf16_eta", "fwd_fp32_clustered",
@@ -172,3 +173,63 @@ def test_gradient_fixtures_cover_every_path():
                 assert float(g["grad." + k].norm()) == 0.0
     assert {"grad.kappa", "grad.log_gamma", "grad.res_norm.weight", "grad.beta_proj.weight",
             "grad.eta_proj.weight", "grad.q_norm.weight", "grad.k_norm.weight", "grad.q_proj.bias"} <= seen
+
+
+GEN = ["gen_eos_close", "gen_all_done", "gen_full_length"]
+
+
+@pytest.mark.parametrize("name", GEN)
+def test_generate_rules_match_reference(name):
+    """The oracle's greedy generation (generate_batch's rules restated: per-row end of sequence,
+    the forced close-of-thinking sequence at the budget point, the all-rows-done test every 16
+    tokens) against the reference's tokens and lengths, B = 3."""
+    g, meta = fixture(name)
+    model, ids = build_fixture_model(meta, meta["n_prompt"])
+    ref = HybridRef(model)
+    with torch.no_grad():
+        toks, lengths, gaps = ref.generate_greedy(ids, meta["n_new"], eos_ids=set(meta["eos_ids"]),
+                                                  close_think_ids=meta["close_think_ids"])
+    assert float(g["gaps"].min()) > 1e-3          # no greedy pick of the fixture is a near-tie
+    assert toks.shape == g["toks"].shape and torch.equal(toks, g["toks"]), name
+    assert torch.equal(lengths, g["lengths"]), (lengths, g["lengths"])
+
+
+def test_generate_fixtures_exercise_the_rules():
+    """Between them the fixtures end rows early (eos), force the close-of-thinking sequence on a row
+    still thinking at the budget point, close a row on its own, stop every row before the token
+    limit at a 16-token check, and run a row to the full 150 tokens."""
+    a, ma = fixture("gen_eos_close")
+    b, mb = fixture("gen_all_done")
+    c, mc = fixture("gen_full_length")
+    budget = max(64, ma["n_new"] - 64)
+    assert (a["lengths"] < a["toks"].shape[1]).any()
+    row0 = a["toks"][0].tolist()
+    assert row0[budget:budget + 3] == list(ma["close_think_ids"])        # forced at the budget point
+    assert b["toks"].shape[1] == 16 and (b["lengths"] < 16).all()       # all done: stop at the check
+    assert mb["close_think_ids"][1] in b["toks"][0].tolist()[:16]        # row 0 closed on its own
+    assert c["toks"].shape[1] == mc["n_new"] == 150 and int(c["lengths"][0]) == 150
+
+
+def test_memorize_forget_match_reference():
+    """Bolt3Decoder.memorize then forget (vsa_lm/config/bolt3.py:528-557) through the oracle: the
+    trace, M_res after memorize, before and after forget, and the steps decoded afterwards."""
+    g, meta = fixture("mem_forget")
+    n0, nd, na, npb = meta["n_prompt"], meta["n_doc"], meta["n_after"], meta["n_probe"]
+    model, ids = build_fixture_model(meta, n0 + nd + na + npb)
+    ref = HybridRef(model)
+    C = ref.C
+    with torch.no_grad():
+        _, st = ref.prefill(ids[:, :n0])
+        pos, traces = ref.memorize(ids[:, n0:n0 + nd], st, n0)
+        assert pos == meta["trace_end"] == n0 + nd
+        assert rel_err(traces[0][1], g["trace"]) <= 1e-5
+        assert rel_err(st[0][0], g["m_memorized"]) <= 1e-5
+        for s0 in range(n0 + nd, n0 + nd + na, C):
+            ref.step(ids[:, s0:min(n0 + nd + na, s0 + C)], s0, st)
+        assert rel_err(st[0][0], g["m_before_forget"]) <= 1e-5
+        nxt = n0 + nd + na
+        ref.forget(traces, st, nxt)
+        assert rel_err(st[0][0], g["m_after_forget"]) <= 1e-5
+        hs = [ref.step(ids[:, nxt + i:nxt + i + 1], nxt + i, st)[:, -1] for i in range(npb)]
+    assert rel_err(torch.stack(hs, dim=1), g["h_probe"]) <= 1e-5
+    assert float(g["trace"].norm()) > 0 and not torch.allclose(g["m_after_forget"], g["m_before_forget"])

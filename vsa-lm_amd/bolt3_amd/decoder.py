@@ -41,6 +41,17 @@ def _check_m_state(m: torch.Tensor, B: int, ly: Bolt3Attn):
                         f"got {m.dtype} {tuple(m.shape)} contiguous={m.is_contiguous()} on {m.device}")
 
 
+def _check_step_len(ly: Bolt3Attn, st: "Bolt3LayerState", t: int):
+    """A step's tokens join the current chunk, which the reference consolidates whole once it holds
+    C or more (vsa_lm/config/bolt3.py:404-425): with the tokens already in it, at most 2C per
+    chunk (a ring half; the chain takes at most 256 tokens per consolidation)."""
+    if st.cur[1] + t > 2 * ly.C:
+        raise NotImplementedError(
+            f"a step of {t} tokens on a current chunk of {st.cur[1]} would make a chunk of more than 2C = "
+            f"{2 * ly.C} tokens, which the reference consolidates as one (the chain takes at most {2 * ly.C}); "
+            f"feed longer inputs through prefill or in pieces of at most C tokens")
+
+
 def _fused_step_ok(dt: torch.dtype, d_model: int, hd_total: int, n_out: int) -> bool:
     """Whether bolt3_decode_layer takes this layer: bf16, input width a multiple of 32, output width
     a multiple of 16, and at most 8 K chunks of 512 in either projection."""
@@ -264,10 +275,15 @@ class Bolt3LayerState(MutableMapping):
         a = A.SlotKeysArgs()
         a.dtype, a.B, a.HKV, a.HD, a.S = A.dtype_code(self.dtype), self.B, self.HKV, self.HD, self.S
         a.ak, a.pm, a.mass, a.act = (self.slots[k].data_ptr() for k in ("ak", "pm", "mass", "act"))
-        a.kappa = ly.kappa.detach().to(device=dev, dtype=torch.float32).contiguous().data_ptr()
-        a.inv_freq = ly.rope.inv_freq.to(device=dev, dtype=torch.float32).contiguous().data_ptr()
+        # fp32 copies bound to names until the launch is queued: a bf16 module's kappa and
+        # inv_freq are converted here, and a temporary freed before the launch could hand its
+        # block to the next conversion
+        kappa = ly.kappa.detach().to(device=dev, dtype=torch.float32).contiguous()
+        inv_freq = ly.rope.inv_freq.to(device=dev, dtype=torch.float32).contiguous()
+        a.kappa, a.inv_freq = kappa.data_ptr(), inv_freq.data_ptr()
         a.slot_k, a.slot_bias = self.slot_k.data_ptr(), self.slot_bias.data_ptr()
         A.call("bolt3_slot_keys", a, dev)
+        del kappa, inv_freq
 
 
 
@@ -442,8 +458,7 @@ class Bolt3Decoder:
         if dt != st.dtype:
             raise TypeError(f"activation dtype {dt} differs from the decoder state dtype {st.dtype}")
         _check_m_state(m_state, B, ly)
-        if t > ly.C:
-            raise NotImplementedError(f"step takes at most C={ly.C} tokens per call (got {t})")
+        _check_step_len(ly, st, t)
         H, HKV, HD, S = ly.H, ly.HKV, ly.HD, ly.S
         W, bias, side = ly._packed(dt, dev)
         gam = side["gamma"]
@@ -540,18 +555,20 @@ class Bolt3Decoder:
             self._consolidate(ly, st, m_state, gam, side, record)
         return out
 
-    def _bolt3_prefill(self, ly: Bolt3Attn, h: torch.Tensor, m_state: torch.Tensor, st: Bolt3LayerState):
+    def _bolt3_prefill(self, ly: Bolt3Attn, h: torch.Tensor, m_state: torch.Tensor, st: Bolt3LayerState,
+                       record=None):
         """A whole prompt through one Bolt-3 layer from an empty state, as the forward computes it
         (every chunk's attention at once, the chain in step groups beside it) with the decoder
         step's fp32 scores; then the state the reference's chunk-by-chunk prefill leaves
         (vsa_lm/config/bolt3.py:452-457): with n = T // C full chunks, chunks 0 .. n-2 consolidated,
         chunk n-1 as prev, the remaining tokens as cur.  The forward consolidates ceil(T/C) - 2
-        chunks, one fewer when C divides T; that step runs here.  Returns the layer output."""
+        chunks, one fewer when C divides T; that step runs here.  Returns the layer output.
+        ``record`` (a list) receives the decision log of every consolidation, as ``step`` records."""
         B, T, _ = h.shape
         C, S, HD, HKV = ly.C, ly.S, ly.HD, ly.HKV
         dt, dev = h.dtype, h.device
         tr = {}
-        out = ly._forward_hip(h, tr, score_round=0, keep_log=False)
+        out = ly._forward_hip(h, tr, score_round=0, keep_log=record is not None)
         side = ly._packed(dt, dev)[2]
         gam = side["gamma"]
         n_full = T // C
@@ -560,6 +577,12 @@ class Bolt3Decoder:
         k_raw, k_rope, v, beta, pos = tr["k_raw"], tr["k_rope"], tr["v"], tr["beta"], tr["pos"]
         if n_steps > 0:
             slots, m_res, nf = tr["state"], tr["m_res"], tr["n_filled"]
+            if record is not None:
+                nf_i = 0
+                for i in range(n_steps):
+                    l_i = C - ns if i == 0 else C
+                    record.append(dict(log=tr["log"][i], n_filled=nf_i, tokens=l_i))
+                    nf_i = min(S, nf_i + l_i)
         else:
             slots, m_res, nf = ly._empty_slots(B * HKV, dt, dev), torch.zeros(B * HKV, HD, HD, device=dev), 0
         if T % C == 0 and n_full >= 2:
@@ -567,9 +590,13 @@ class Bolt3Decoder:
             off, l = (ns, C - ns) if i == 0 else (0, C)
             esz = k_raw.element_size()
             tok = i * C
+            log = None
+            if record is not None:
+                log = torch.zeros(1, B * HKV, A.LOG_ROWS, A.LOG_COLS, device=dev)
+                record.append(dict(log=log[0], n_filled=nf, tokens=l))
             ly._chain(dt, dev, B, k_raw.data_ptr() + tok * HD * esz, k_rope.data_ptr() + tok * HD * esz,
                       v.data_ptr() + tok * HD * esz, T * HD, pos.data_ptr() + tok * 4, beta.data_ptr() + tok * 4,
-                      T, 1, off, l, C, C, nf, slots, m_res, gam, side, kp_exact=True)
+                      T, 1, off, l, C, C, nf, slots, m_res, gam, side, kp_exact=True, log=log)
             nf = min(S, nf + l)
             n_steps += 1
         m_state.copy_(m_res.view_as(m_state))
@@ -721,10 +748,17 @@ class Bolt3Decoder:
 
     @torch.no_grad()
     def step(self, tokens: torch.Tensor, pos_start: int, states, kv_caches, record=None):
-        """Run the tokens [B, t] (t <= C) through every layer at positions pos_start.. and update the
-        states in place.  Returns (normed hidden states [B, t, D], states, kv_caches).  ``record``: a
-        list (or a dict per layer index) that receives the decision log of every consolidation."""
+        """Run the tokens [B, t] through every layer at positions pos_start.. and update the states in
+        place, as the reference's step does for any t (vsa_lm/config/bolt3.py:335-425): one
+        attention over the window and the new tokens, then, once the current chunk holds C or more
+        tokens, one consolidation of the previous chunk.  t is at most 2C minus the tokens already
+        in the current chunk (checked for every layer before any state changes).  Returns (normed
+        hidden states [B, t, D], states, kv_caches).  ``record``: a list (or a dict per layer index)
+        that receives the decision log of every consolidation."""
         m = self.model
+        for li, blk in enumerate(m.blocks):
+            if hasattr(blk, "vsa"):
+                _check_step_len(blk.vsa, kv_caches[li], tokens.shape[1])
         with torch.autocast(tokens.device.type, enabled=False):
             x = m.embed_tokens(tokens)
             for li, blk in enumerate(m.blocks):
@@ -747,13 +781,14 @@ class Bolt3Decoder:
         return h, pos
 
     @torch.no_grad()
-    def prefill(self, ids: torch.Tensor, max_kv_len: int = 4096):
+    def prefill(self, ids: torch.Tensor, max_kv_len: int = 4096, record=None):
         """The prompt through every layer (vsa_lm/config/bolt3.py:450-457).  The reference steps it
         chunk by chunk through all layers; here each layer takes the whole prompt at once (a layer's
         output for a chunk depends only on that layer's inputs up to the chunk, so the order of the
         two loops does not change what is computed): the Bolt-3 layers through the forward's
         kernels (_bolt3_prefill), the anchors through causal attention over the prompt.  Returns
-        (normed hidden states of the last chunk's tokens, states, kv_caches), as the reference."""
+        (normed hidden states of the last chunk's tokens, states, kv_caches), as the reference.
+        ``record``: as for ``step``."""
         b, t = ids.shape
         states, kv = self.blank_state(self.model, b, ids.device, max_kv_len=max(max_kv_len, t + 1024))
         m = self.model
@@ -762,7 +797,8 @@ class Bolt3Decoder:
             for li, blk in enumerate(m.blocks):
                 h = blk.norm1(x)
                 if hasattr(blk, "vsa"):
-                    x = x + self._bolt3_prefill(blk.vsa, h, states[li], kv[li])
+                    rec = record.setdefault(li, []) if isinstance(record, dict) else record
+                    x = x + self._bolt3_prefill(blk.vsa, h, states[li], kv[li], rec)
                 else:
                     x = x + self._anchor_layer(blk.attn, h, 0, kv[li])
                 x = x + blk.mlp(blk.norm2(x))

@@ -1,5 +1,5 @@
-// Backward of the consolidation chain for bf16 storage (HD = 128, S = 128, at most 128 tokens
-// per step).
+// Backward of the consolidation chain (S = 128, HD in {64, 128}, bf16 or fp32 storage, at most
+// 128 tokens per step).
 //
 // The reference differentiates _consolidate_functional (vsa_lm/config/bolt3.py:68-192) with
 // autograd; every decision in it (fill picks, merge targets, evictions, delta-rule membership)
@@ -22,8 +22,10 @@
 //                     E = bsafe R:  dV = bsafe (Khat G), dKhat = E G^T - dV M^T + (dP + dP^T)
 //                     Khat with dP through the row sums (|Khat Khat^T| and the clamp at 1), dw,
 //                     and the normalisation's backward to the un-roped keys.
-// Products run on MFMA with exact bf16 keys; fp32 operands (M, G, E, dV, the Gram weights) are
-// split into bf16 hi + lo, so every product is fp32-accurate to about 2^-16.
+// Products run on bf16 MFMA.  fp32 operands (M, G, E, dV, the Gram weights, and the keys when the
+// storage is fp32) are split into bf16 hi + lo; a product of two split operands takes hi*hi +
+// hi*lo + lo*hi, so every product is fp32-accurate to about 2^-16 (bf16 keys are exact: one
+// product fewer).
 #include <math.h>
 
 #include "bolt3_common.h"
@@ -34,13 +36,17 @@ namespace b3 {
 namespace cbwd {
 
 constexpr int S = 128;
-constexpr int HD = 128;
 constexpr int LT = 128;          // tokens per step, at most
-constexpr int NT = 256;          // threads of every kernel (4 wavefronts)
-constexpr int NP = HD / 8;       // 16-byte pieces of a row (LT / 8 as well)
-constexpr int NSL = HD / 16;     // feature slices of the slot recursion
-constexpr int NCB = HD / 32;     // 32-column blocks of M
-constexpr int KS = HD / 16;      // K steps of 16 over the features
+constexpr int NPT = LT / 8;      // 16-byte pieces of a row of LT bf16
+constexpr int NT = 256;          // threads of the per-step kernels and of slot_rec (4 wavefronts)
+
+template <int HD>
+struct Dims {
+  static constexpr int NP = HD / 8;     // 16-byte pieces of a row of HD bf16
+  static constexpr int NSL = HD / 16;   // feature slices of the slot recursion
+  static constexpr int NCB = HD / 32;   // 32-column blocks of M (and wavefronts of m_rec)
+  static constexpr int KS = HD / 16;    // K steps of 16 over the features
+};
 
 __device__ __forceinline__ int step_len(const b3_chain_bwd_args& a, int i) { return i == 0 ? a.len0 : a.step_len; }
 __device__ __forceinline__ int step_off(const b3_chain_bwd_args& a, int i) {
@@ -57,74 +63,129 @@ __device__ __forceinline__ const float* log_rec(const b3_chain_bwd_args& a, int 
 }
 
 // Workspace: per (step, bh) four rows of LT floats (1/|k|, row sum, bsafe, w), then per (step,
-// bh) G^T as bf16 hi and lo planes of HD x HD (G^T[d][c] = G[c][d], the layout of M_res
-// snapshots).
+// bh) G^T as bf16 hi and lo planes of HD x HD (G^T[d][c] = G[c][d], the layout of the bf16
+// forward's M_res snapshots).
 __host__ __device__ __forceinline__ long long stats_floats(long long n, long long bh) { return n * bh * 4 * LT; }
-__host__ __device__ __forceinline__ long long ws_bytes(long long n, long long bh) {
-  return 4 * stats_floats(n, bh) + n * bh * HD * HD * 4;
+__host__ __device__ __forceinline__ long long ws_bytes(long long n, long long bh, int hd) {
+  return 4 * stats_floats(n, bh) + n * bh * (long long)hd * hd * 4;
 }
 __device__ __forceinline__ float* stats_of(const b3_chain_bwd_args& a, int i, int bh) {
   return reinterpret_cast<float*>(a.work) + ((long long)i * a.B * a.HKV + bh) * 4 * LT;
 }
+template <int HD>
 __device__ __forceinline__ uint16_t* gt_of(const b3_chain_bwd_args& a, int i, int bh) {
   const long long BH = (long long)a.B * a.HKV;
   return reinterpret_cast<uint16_t*>(reinterpret_cast<float*>(a.work) + stats_floats(a.n_steps, BH)) +
          ((long long)i * BH + bh) * 2 * HD * HD;
 }
 
-// the step's keys [LT][HD] into LDS (16-byte piece p of row r at p ^ (r % NP)), rows >= l zero
-__device__ __forceinline__ void stage_keys(uint16_t* kt, const uint16_t* kr, int l, int tid) {
-  for (int it = tid; it < LT * NP; it += NT) {
+// Keys of one step in LDS: [LT][HD] bf16 with 16-byte piece p of row r at p ^ (r % NP), rows >= l
+// zero; fp32 storage keeps the bf16 remainder of every key in a second plane.
+template <int HD, bool F32>
+struct KeyTile {
+  alignas(16) uint16_t hi[LT * HD];
+  alignas(16) uint16_t lo[F32 ? LT * HD : 8];
+};
+
+template <int HD, bool F32, int NTH>
+__device__ __forceinline__ void stage_keys(KeyTile<HD, F32>& kt, const void* kr_rows, int l, int tid) {
+  constexpr int NP = Dims<HD>::NP;
+  for (int it = tid; it < LT * NP; it += NTH) {
     const int r = it / NP, p = it % NP;
-    u16x8 v = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
-    if (r < l) v = *reinterpret_cast<const u16x8*>(kr + (long long)r * HD + 8 * p);
-    *reinterpret_cast<u16x8*>(&kt[r * HD + 8 * (p ^ (r % NP))]) = v;
+    const int o = r * HD + 8 * (p ^ (r % NP));
+    if constexpr (F32) {
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = 0.f;
+      if (r < l) {
+        const float* src = reinterpret_cast<const float*>(kr_rows) + (long long)r * HD + 8 * p;
+        *reinterpret_cast<float4*>(v) = *reinterpret_cast<const float4*>(src);
+        *reinterpret_cast<float4*>(v + 4) = *reinterpret_cast<const float4*>(src + 4);
+      }
+      u16x8 h, lw;
+      split8(v, h, lw);
+      *reinterpret_cast<u16x8*>(&kt.hi[o]) = h;
+      *reinterpret_cast<u16x8*>(&kt.lo[o]) = lw;
+    } else {
+      u16x8 v = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+      if (r < l) v = *reinterpret_cast<const u16x8*>(reinterpret_cast<const uint16_t*>(kr_rows) + (long long)r * HD + 8 * p);
+      *reinterpret_cast<u16x8*>(&kt.hi[o]) = v;
+    }
   }
 }
-// an M^T hi / lo pair of planes (bf16, rows d) into LDS with the same swizzle
+
+// an M^T hi / lo pair of planes into LDS (rows d, swizzled as the keys): from the bf16 forward's
+// snapshot (already M^T hi / lo) or, split here, from an fp32 M[c][d] (the fp32 forward's)
+template <int HD, int NTH>
 __device__ __forceinline__ void stage_mt(uint16_t* mt, const uint16_t* src, int tid) {
-  for (int it = tid; it < 2 * HD * NP; it += NT) {
+  constexpr int NP = Dims<HD>::NP;
+  for (int it = tid; it < 2 * HD * NP; it += NTH) {
     const int pl = it / (HD * NP), rem = it % (HD * NP), d = rem / NP, p = rem % NP;
     *reinterpret_cast<u16x8*>(&mt[pl * HD * HD + d * HD + 8 * (p ^ (d % NP))]) =
         *reinterpret_cast<const u16x8*>(src + (long long)pl * HD * HD + d * HD + 8 * p);
   }
 }
-__device__ __forceinline__ u16x8 row_piece(const uint16_t* t, int r, int p) {
-  return *reinterpret_cast<const u16x8*>(&t[r * HD + 8 * (p ^ (r % NP))]);
+template <int HD, int NTH>
+__device__ __forceinline__ void stage_mt_f32(uint16_t* mt, const float* m, int tid) {
+  constexpr int NP = Dims<HD>::NP;
+  for (int it = tid; it < HD * NP; it += NTH) {
+    const int d = it % HD, p = it / HD;   // consecutive threads: consecutive columns d of one row block
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = m[(long long)(8 * p + e) * HD + d];
+    u16x8 h, lw;
+    split8(v, h, lw);
+    const int o = d * HD + 8 * (p ^ (d % NP));
+    *reinterpret_cast<u16x8*>(&mt[o]) = h;
+    *reinterpret_cast<u16x8*>(&mt[HD * HD + o]) = lw;
+  }
 }
-// four consecutive bf16 of row r from column c0 (c0 % 4 == 0) of a swizzled tile
-__device__ __forceinline__ uint2 row_quad(const uint16_t* t, int r, int c0) {
-  return *reinterpret_cast<const uint2*>(&t[r * HD + 8 * ((c0 >> 3) ^ (r % NP)) + (c0 & 7)]);
+template <int HD>
+__device__ __forceinline__ u16x8 row_piece(const uint16_t* t, int r, int p) {
+  return *reinterpret_cast<const u16x8*>(&t[r * HD + 8 * (p ^ (r % Dims<HD>::NP))]);
 }
 __device__ __forceinline__ u16x8 neg_bf(u16x8 v) {
 #pragma unroll
   for (int e = 0; e < 8; ++e) v[e] ^= 0x8000u;
   return v;
 }
+// four consecutive features c0.. of key row r of the step (global memory, storage dtype)
+template <int HD, bool F32>
+__device__ __forceinline__ float4 key_quad(const void* kr_rows, int r, int c0) {
+  if constexpr (F32) {
+    return *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(kr_rows) + (long long)r * HD + c0);
+  } else {
+    const uint2 k2 = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(kr_rows) + (long long)r * HD + c0);
+    return make_float4(bf_lo(k2.x), bf_hi(k2.x), bf_lo(k2.y), bf_hi(k2.y));
+  }
+}
+template <bool F32>
+__device__ __forceinline__ const void* rows_at(const void* base, long long row, int hd) {
+  return F32 ? (const void*)(reinterpret_cast<const float*>(base) + row * hd)
+             : (const void*)(reinterpret_cast<const uint16_t*>(base) + row * hd);
+}
 
 // ---------------------------------------------------------------- per-token statistics
 
+template <int HD, bool F32>
 __global__ void __launch_bounds__(NT) tok_stats_kernel(b3_chain_bwd_args a) {
-  __shared__ alignas(16) uint16_t kt[LT * HD];
+  using Dm = Dims<HD>;
+  __shared__ KeyTile<HD, F32> kt;
   __shared__ float s_inv[LT], s_w[LT];
   const int i = blockIdx.x, bh = blockIdx.y;
   if (filled_before(a, i) < S) return;   // fill step: no delta rule
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, n = lane & 31, h = lane >> 5;
   const int l = step_len(a, i), t0 = step_off(a, i);
-  const uint16_t* kr = reinterpret_cast<const uint16_t*>(a.kr) + ((long long)bh * a.T + t0) * HD;
-  stage_keys(kt, kr, l, tid);
+  const void* kr = rows_at<F32>(a.kr, (long long)bh * a.T + t0, HD);
+  stage_keys<HD, F32, NT>(kt, kr, l, tid);
   float* st = stats_of(a, i, bh);
   if (tid < LT) {
     float iv = 0.f, wv = 0.f;
     if (tid < l) {
       float ss = 0.f;
-      for (int d = 0; d < HD; d += 8) {
-        const u16x8 x = *reinterpret_cast<const u16x8*>(kr + (long long)tid * HD + d);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float f = bf2f(x[e]);
-          ss += f * f;
-        }
+      for (int d = 0; d < HD; d += 4) {
+        const float4 x = key_quad<HD, F32>(kr, tid, d);
+        ss += x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w;
       }
       iv = 1.0f / fmaxf(sqrtf(ss), 1e-12f);
       if (log_rec(a, i, bh)[B3_LOG_DELTA * B3_LOG_COLS + tid] > 0.5f) wv = a.beta[(long long)bh * a.T + t0 + tid];
@@ -143,7 +204,14 @@ __global__ void __launch_bounds__(NT) tok_stats_kernel(b3_chain_bwd_args a) {
     if (32 * ti >= l) break;
     f32x16 acc = zero16();
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) mma_bf16(acc, row_piece(kt, 32 * ti + n, 2 * ks + h), row_piece(kt, j, 2 * ks + h));
+    for (int ks = 0; ks < Dm::KS; ++ks) {
+      const u16x8 ai = row_piece<HD>(kt.hi, 32 * ti + n, 2 * ks + h), bj = row_piece<HD>(kt.hi, j, 2 * ks + h);
+      mma_bf16(acc, ai, bj);
+      if constexpr (F32) {
+        mma_bf16(acc, ai, row_piece<HD>(kt.lo, j, 2 * ks + h));
+        mma_bf16(acc, row_piece<HD>(kt.lo, 32 * ti + n, 2 * ks + h), bj);
+      }
+    }
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int ii = 32 * ti + d_row(lane, r);
@@ -160,8 +228,7 @@ __global__ void __launch_bounds__(NT) tok_stats_kernel(b3_chain_bwd_args a) {
 // ---------------------------------------------------------------- slot recursion
 
 // Features of slice sl: 8 sl .. 8 sl + 7 and HD/2 + 8 sl .. (the RoPE pairs).
-__device__ __forceinline__ int slice_col(int sl, int e) { return e < 8 ? 8 * sl + e : HD / 2 + 8 * sl + (e - 8); }
-
+template <int HD>
 __device__ __forceinline__ void add_row16(float* out, int sl, const float* v) {
   float4* p0 = reinterpret_cast<float4*>(out + 8 * sl);
   float4* p1 = reinterpret_cast<float4*>(out + HD / 2 + 8 * sl);
@@ -172,6 +239,7 @@ __device__ __forceinline__ void add_row16(float* out, int sl, const float* v) {
   x = p1[1]; x.x += v[12]; x.y += v[13]; x.z += v[14]; x.w += v[15]; p1[1] = x;
 }
 
+template <int HD>
 __global__ void __launch_bounds__(NT) slot_rec_kernel(b3_chain_bwd_args a) {
   // gradients of the slots' un-roped keys (g[0]) and values (g[1]) on this slice
   __shared__ float g[2][S][17];
@@ -223,7 +291,7 @@ __global__ void __launch_bounds__(NT) slot_rec_kernel(b3_chain_bwd_args a) {
       const int m = min(S - nfb, l);
       if (s >= nfb && s < nfb + m) {
         const int tok = (int)lg[B3_LOG_TOPTOK * B3_LOG_COLS + (s - nfb)];
-        if ((unsigned)tok < (unsigned)l) add_row16(out + (long long)tok * HD, sl, grow);
+        if ((unsigned)tok < (unsigned)l) add_row16<HD>(out + (long long)tok * HD, sl, grow);
 #pragma unroll
         for (int e = 0; e < 16; ++e) grow[e] = 0.f;
       }
@@ -252,7 +320,7 @@ __global__ void __launch_bounds__(NT) slot_rec_kernel(b3_chain_bwd_args a) {
     {
       const int tok = map_tok[s];
       if (tok >= 0) {
-        add_row16(out + (long long)tok * HD, sl, grow);
+        add_row16<HD>(out + (long long)tok * HD, sl, grow);
 #pragma unroll
         for (int e = 0; e < 16; ++e) grow[e] = 0.f;
       }
@@ -272,7 +340,7 @@ __global__ void __launch_bounds__(NT) slot_rec_kernel(b3_chain_bwd_args a) {
         float v[16];
 #pragma unroll
         for (int e = 0; e < 16; ++e) v[e] = g[arr][ts][e] * coef;
-        add_row16(out + (long long)j * HD, sl, v);
+        add_row16<HD>(out + (long long)j * HD, sl, v);
       }
     }
     __syncthreads();
@@ -287,16 +355,21 @@ __global__ void __launch_bounds__(NT) slot_rec_kernel(b3_chain_bwd_args a) {
 
 // ---------------------------------------------------------------- M_res recursion
 
+template <int HD, bool F32>
 struct MrecSmem {
-  alignas(16) uint16_t kt[LT * HD];      // the step's keys
+  KeyTile<HD, F32> kt;                   // the step's keys
   alignas(16) uint16_t ct[2][32 * HD];   // G^T of the column block, hi / lo: row n, columns c
   alignas(16) uint16_t tt[2][32 * LT];   // T^T hi / lo: row n, columns j (tokens)
   float coef[LT];
-  float gp[4];
+  float gp[Dims<HD>::NCB];
 };
 
-__global__ void __launch_bounds__(NT) m_rec_kernel(b3_chain_bwd_args a) {
-  __shared__ MrecSmem sm;
+// one wavefront per 32 rows of M: HD / 32 wavefronts
+template <int HD, bool F32>
+__global__ void __launch_bounds__(HD * 2) m_rec_kernel(b3_chain_bwd_args a) {
+  using Dm = Dims<HD>;
+  constexpr int NCB = Dm::NCB, NP = Dm::NP, NTH = 64 * NCB;
+  __shared__ MrecSmem<HD, F32> sm;
   // XCD-aware order: the NCB column blocks of one bh read the same per-step rows
   const int wg = xcd_grid_pos().x;
   const int bh = wg / NCB, db = wg % NCB;
@@ -317,9 +390,8 @@ __global__ void __launch_bounds__(NT) m_rec_kernel(b3_chain_bwd_args a) {
     const int l = step_len(a, i), t0 = step_off(a, i);
     // G_i out (as G^T hi / lo) and this step's share of dL/dgamma: sum(G_i * M_{i-1})
     {
-      uint16_t* gt = gt_of(a, i, bh);
-      const uint16_t* m0 =
-          reinterpret_cast<const uint16_t*>(a.snap_m + ((long long)(i - 1) * BH + bh) * HD * HD);
+      uint16_t* gt = gt_of<HD>(a, i, bh);
+      const float* m0 = a.snap_m + ((long long)(i - 1) * BH + bh) * HD * HD;
       const int d = 32 * db + n;
       float gs = 0.f;
 #pragma unroll
@@ -338,37 +410,51 @@ __global__ void __launch_bounds__(NT) m_rec_kernel(b3_chain_bwd_args a) {
         *reinterpret_cast<uint2*>(gt + HD * HD + d * HD + c0) = pl;
         *reinterpret_cast<uint2*>(&sm.ct[0][n * HD + 8 * ((4 * w + r4) ^ (n % NP)) + 4 * h]) = ph;
         *reinterpret_cast<uint2*>(&sm.ct[1][n * HD + 8 * ((4 * w + r4) ^ (n % NP)) + 4 * h]) = pl;
-        const uint2 mh = *reinterpret_cast<const uint2*>(m0 + d * HD + c0);
-        const uint2 ml = *reinterpret_cast<const uint2*>(m0 + HD * HD + d * HD + c0);
-        gs += cur[4 * r4] * (bf_lo(mh.x) + bf_lo(ml.x)) + cur[4 * r4 + 1] * (bf_hi(mh.x) + bf_hi(ml.x)) +
-              cur[4 * r4 + 2] * (bf_lo(mh.y) + bf_lo(ml.y)) + cur[4 * r4 + 3] * (bf_hi(mh.y) + bf_hi(ml.y));
+        if constexpr (F32) {
+          // the fp32 forward's snapshot: M[c][d]
+#pragma unroll
+          for (int q = 0; q < 4; ++q) gs += cur[4 * r4 + q] * m0[(long long)(c0 + q) * HD + d];
+        } else {
+          // the bf16 forward's snapshot: M^T as bf16 hi, then lo
+          const uint16_t* mt = reinterpret_cast<const uint16_t*>(m0);
+          const uint2 mh = *reinterpret_cast<const uint2*>(mt + d * HD + c0);
+          const uint2 ml = *reinterpret_cast<const uint2*>(mt + HD * HD + d * HD + c0);
+          gs += cur[4 * r4] * (bf_lo(mh.x) + bf_lo(ml.x)) + cur[4 * r4 + 1] * (bf_hi(mh.x) + bf_hi(ml.x)) +
+                cur[4 * r4 + 2] * (bf_lo(mh.y) + bf_lo(ml.y)) + cur[4 * r4 + 3] * (bf_hi(mh.y) + bf_hi(ml.y));
+        }
       }
 #pragma unroll
       for (int o = 32; o >= 1; o >>= 1) gs += __shfl_xor(gs, o, 64);
       if (lane == 0) sm.gp[w] = gs;
     }
-    stage_keys(sm.kt, reinterpret_cast<const uint16_t*>(a.kr) + ((long long)bh * a.T + t0) * HD, l, tid);
-    if (tid < LT) {
+    stage_keys<HD, F32, NTH>(sm.kt, rows_at<F32>(a.kr, (long long)bh * a.T + t0, HD), l, tid);
+    for (int j = tid; j < LT; j += NTH) {
       const float* st = stats_of(a, i, bh);
-      sm.coef[tid] = tid < l ? st[tid] * st[tid] * st[2 * LT + tid] : 0.f;   // bsafe / |k|^2
+      sm.coef[j] = j < l ? st[j] * st[j] * st[2 * LT + j] : 0.f;   // bsafe / |k|^2
     }
     __syncthreads();
-    if (tid == 0) a.d_gamma[((long long)i * BH + bh) * NCB + db] = sm.gp[0] + sm.gp[1] + sm.gp[2] + sm.gp[3];
-    // T = K G (wavefront w: tokens 32 w ..), then scaled by bsafe / |k|^2 into T^T
-    {
-      f32x16 t1 = zero16();
-      const int jr = 32 * w + n;
+    if (tid == 0) {
+      float gsum = 0.f;
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const u16x8 ka = row_piece(sm.kt, jr, 2 * ks + h);
+      for (int q = 0; q < NCB; ++q) gsum += sm.gp[q];
+      a.d_gamma[((long long)i * BH + bh) * NCB + db] = gsum;
+    }
+    // T = K G (token blocks tb = w, w + NCB, ..), then scaled by bsafe / |k|^2 into T^T
+    for (int tb = w; tb < LT / 32; tb += NCB) {
+      f32x16 t1 = zero16();
+      const int jr = 32 * tb + n;
+#pragma unroll
+      for (int ks = 0; ks < Dm::KS; ++ks) {
+        const u16x8 ka = row_piece<HD>(sm.kt.hi, jr, 2 * ks + h);
         const u16x8 bhv = *reinterpret_cast<const u16x8*>(&sm.ct[0][n * HD + 8 * ((2 * ks + h) ^ (n % NP))]);
         const u16x8 blv = *reinterpret_cast<const u16x8*>(&sm.ct[1][n * HD + 8 * ((2 * ks + h) ^ (n % NP))]);
         mma_bf16(t1, ka, bhv);
         mma_bf16(t1, ka, blv);
+        if constexpr (F32) mma_bf16(t1, row_piece<HD>(sm.kt.lo, jr, 2 * ks + h), bhv);
       }
 #pragma unroll
       for (int r4 = 0; r4 < 4; ++r4) {
-        const int j0 = 32 * w + 8 * r4 + 4 * h;
+        const int j0 = 32 * tb + 8 * r4 + 4 * h;
         uint16_t hb[4], lb[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -376,7 +462,7 @@ __global__ void __launch_bounds__(NT) m_rec_kernel(b3_chain_bwd_args a) {
           hb[q] = f2bf(x);
           lb[q] = f2bf(x - bf2f(hb[q]));
         }
-        const int off = n * LT + 8 * ((4 * w + r4) ^ (n % NP)) + 4 * h;
+        const int off = n * LT + 8 * ((4 * tb + r4) ^ (n % NPT)) + 4 * h;
         *reinterpret_cast<uint2*>(&sm.tt[0][off]) = make_uint2(hb[0] | ((uint32_t)hb[1] << 16), hb[2] | ((uint32_t)hb[3] << 16));
         *reinterpret_cast<uint2*>(&sm.tt[1][off]) = make_uint2(lb[0] | ((uint32_t)lb[1] << 16), lb[2] | ((uint32_t)lb[3] << 16));
       }
@@ -390,12 +476,12 @@ __global__ void __launch_bounds__(NT) m_rec_kernel(b3_chain_bwd_args a) {
       for (int t4 = 0; t4 < LT / 32; ++t4)
 #pragma unroll
         for (int kc = 0; kc < 2; ++kc) {
-          const u16x8 ka = tr_operand<HD>(sm.kt + 32 * t4 * HD, TL, w, kc);
+          const u16x8 ka = tr_operand<HD>(sm.kt.hi + 32 * t4 * HD, TL, w, kc);
           const int p0 = 4 * t4 + 2 * kc;
-          const uint2 h0 = *reinterpret_cast<const uint2*>(&sm.tt[0][n * LT + 8 * (p0 ^ (n % NP)) + 4 * h]);
-          const uint2 h1 = *reinterpret_cast<const uint2*>(&sm.tt[0][n * LT + 8 * ((p0 + 1) ^ (n % NP)) + 4 * h]);
-          const uint2 l0 = *reinterpret_cast<const uint2*>(&sm.tt[1][n * LT + 8 * (p0 ^ (n % NP)) + 4 * h]);
-          const uint2 l1 = *reinterpret_cast<const uint2*>(&sm.tt[1][n * LT + 8 * ((p0 + 1) ^ (n % NP)) + 4 * h]);
+          const uint2 h0 = *reinterpret_cast<const uint2*>(&sm.tt[0][n * LT + 8 * (p0 ^ (n % NPT)) + 4 * h]);
+          const uint2 h1 = *reinterpret_cast<const uint2*>(&sm.tt[0][n * LT + 8 * ((p0 + 1) ^ (n % NPT)) + 4 * h]);
+          const uint2 l0 = *reinterpret_cast<const uint2*>(&sm.tt[1][n * LT + 8 * (p0 ^ (n % NPT)) + 4 * h]);
+          const uint2 l1 = *reinterpret_cast<const uint2*>(&sm.tt[1][n * LT + 8 * ((p0 + 1) ^ (n % NPT)) + 4 * h]);
           u16x8 bhv, blv;
           bhv[0] = h0.x & 0xffff; bhv[1] = h0.x >> 16; bhv[2] = h0.y & 0xffff; bhv[3] = h0.y >> 16;
           bhv[4] = h1.x & 0xffff; bhv[5] = h1.x >> 16; bhv[6] = h1.y & 0xffff; bhv[7] = h1.y >> 16;
@@ -403,6 +489,7 @@ __global__ void __launch_bounds__(NT) m_rec_kernel(b3_chain_bwd_args a) {
           blv[4] = l1.x & 0xffff; blv[5] = l1.x >> 16; blv[6] = l1.y & 0xffff; blv[7] = l1.y >> 16;
           mma_bf16(u, ka, bhv);
           mma_bf16(u, ka, blv);
+          if constexpr (F32) mma_bf16(u, tr_operand<HD>(sm.kt.lo + 32 * t4 * HD, TL, w, kc), bhv);
         }
 #pragma unroll
       for (int r = 0; r < 16; ++r) cur[r] = gam * cur[r] - u[r];
@@ -413,23 +500,34 @@ __global__ void __launch_bounds__(NT) m_rec_kernel(b3_chain_bwd_args a) {
 
 // ---------------------------------------------------------------- token gradients
 
+template <int HD, bool F32>
 struct TgSmem {
   alignas(16) uint16_t mt[2 * HD * HD];   // M_{i-1}^T or G_i^T, hi then lo (rows d)
-  alignas(16) uint16_t kt[LT * HD];       // the step's keys
+  KeyTile<HD, F32> kt;                    // the step's keys
   float inv[LT], raw[LT], bs[LT], wv[LT], drs[LT];
 };
 
+template <int HD, bool F32>
+__device__ __forceinline__ void stage_m_prev(uint16_t* mt, const b3_chain_bwd_args& a, const float* m0, int tid) {
+  if constexpr (F32) stage_mt_f32<HD, NT>(mt, m0, tid);
+  else stage_mt<HD, NT>(mt, reinterpret_cast<const uint16_t*>(m0), tid);
+}
+
+template <int HD, bool F32>
 __global__ void __launch_bounds__(NT) tok_grad_kernel(b3_chain_bwd_args a) {
-  __shared__ TgSmem sm;
+  using Dm = Dims<HD>;
+  constexpr int NCB = Dm::NCB, KS = Dm::KS;
+  __shared__ TgSmem<HD, F32> sm;
   const int i = blockIdx.x, bh = blockIdx.y;
   if (filled_before(a, i) < S) return;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, n = lane & 31, h = lane >> 5;
   const long long BH = (long long)a.B * a.HKV;
   const int l = step_len(a, i), t0 = step_off(a, i);
   const TrLanes<HD> TL(lane);
-  const uint16_t* m0 = reinterpret_cast<const uint16_t*>(a.snap_m + ((long long)(i - 1) * BH + bh) * HD * HD);
-  stage_mt(sm.mt, m0, tid);
-  stage_keys(sm.kt, reinterpret_cast<const uint16_t*>(a.kr) + ((long long)bh * a.T + t0) * HD, l, tid);
+  const float* m0 = a.snap_m + ((long long)(i - 1) * BH + bh) * HD * HD;
+  const void* krows = rows_at<F32>(a.kr, (long long)bh * a.T + t0, HD);
+  stage_m_prev<HD, F32>(sm.mt, a, m0, tid);
+  stage_keys<HD, F32, NT>(sm.kt, krows, l, tid);
   if (tid < LT) {
     const float* st = stats_of(a, i, bh);
     const bool ok = tid < l;
@@ -450,30 +548,31 @@ __global__ void __launch_bounds__(NT) tok_grad_kernel(b3_chain_bwd_args a) {
   for (int db = 0; db < NCB; ++db) R[db] = zero16();
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
-    const u16x8 kb = row_piece(sm.kt, j, 2 * ks + h);
+    const u16x8 kb = row_piece<HD>(sm.kt.hi, j, 2 * ks + h);
 #pragma unroll
     for (int db = 0; db < NCB; ++db) {
       const int dr = 32 * db + n;
-      mma_bf16(R[db], row_piece(sm.mt, dr, 2 * ks + h), kb);
-      mma_bf16(R[db], row_piece(sm.mt + HD * HD, dr, 2 * ks + h), kb);
+      const u16x8 mh = row_piece<HD>(sm.mt, dr, 2 * ks + h);
+      mma_bf16(R[db], mh, kb);
+      mma_bf16(R[db], row_piece<HD>(sm.mt + HD * HD, dr, 2 * ks + h), kb);
+      if constexpr (F32) mma_bf16(R[db], mh, row_piece<HD>(sm.kt.lo, j, 2 * ks + h));
     }
   }
   {
-    const uint16_t* vp = reinterpret_cast<const uint16_t*>(a.v) + trow * HD;
 #pragma unroll
     for (int db = 0; db < NCB; ++db)
 #pragma unroll
       for (int r4 = 0; r4 < 4; ++r4) {
-        uint2 v2 = make_uint2(0u, 0u);
-        if (live) v2 = *reinterpret_cast<const uint2*>(vp + 32 * db + 8 * r4 + 4 * h);
-        R[db][4 * r4] = bf_lo(v2.x) - R[db][4 * r4] * inj;
-        R[db][4 * r4 + 1] = bf_hi(v2.x) - R[db][4 * r4 + 1] * inj;
-        R[db][4 * r4 + 2] = bf_lo(v2.y) - R[db][4 * r4 + 2] * inj;
-        R[db][4 * r4 + 3] = bf_hi(v2.y) - R[db][4 * r4 + 3] * inj;
+        float4 v4 = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (live) v4 = key_quad<HD, F32>(rows_at<F32>(a.v, trow, HD), 0, 32 * db + 8 * r4 + 4 * h);
+        R[db][4 * r4] = v4.x - R[db][4 * r4] * inj;
+        R[db][4 * r4 + 1] = v4.y - R[db][4 * r4 + 1] * inj;
+        R[db][4 * r4 + 2] = v4.z - R[db][4 * r4 + 2] * inj;
+        R[db][4 * r4 + 3] = v4.w - R[db][4 * r4 + 3] * inj;
       }
   }
   __syncthreads();   // M_{i-1}^T read
-  stage_mt(sm.mt, gt_of(a, i, bh), tid);
+  stage_mt<HD, NT>(sm.mt, gt_of<HD>(a, i, bh), tid);
   __syncthreads();
   // dE^T = (G^T k_j) / |k_j|  (gradient of E's row j through V - Khat M is dE; of R: bsafe dE)
   f32x16 dE[NCB];
@@ -481,12 +580,14 @@ __global__ void __launch_bounds__(NT) tok_grad_kernel(b3_chain_bwd_args a) {
   for (int db = 0; db < NCB; ++db) dE[db] = zero16();
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
-    const u16x8 kb = row_piece(sm.kt, j, 2 * ks + h);
+    const u16x8 kb = row_piece<HD>(sm.kt.hi, j, 2 * ks + h);
 #pragma unroll
     for (int db = 0; db < NCB; ++db) {
       const int dr = 32 * db + n;
-      mma_bf16(dE[db], row_piece(sm.mt, dr, 2 * ks + h), kb);
-      mma_bf16(dE[db], row_piece(sm.mt + HD * HD, dr, 2 * ks + h), kb);
+      const u16x8 gh = row_piece<HD>(sm.mt, dr, 2 * ks + h);
+      mma_bf16(dE[db], gh, kb);
+      mma_bf16(dE[db], row_piece<HD>(sm.mt + HD * HD, dr, 2 * ks + h), kb);
+      if constexpr (F32) mma_bf16(dE[db], gh, row_piece<HD>(sm.kt.lo, j, 2 * ks + h));
     }
   }
   float dbs = 0.f;
@@ -545,7 +646,7 @@ __global__ void __launch_bounds__(NT) tok_grad_kernel(b3_chain_bwd_args a) {
   const float drsj = (live && rawj >= 1.0f) ? -dbs * wj / (rsj * rsj) : 0.f;
   if (h == 0 && live) sm.drs[j] = drsj;
   __syncthreads();   // G^T read; drs complete
-  stage_mt(sm.mt, m0, tid);
+  stage_m_prev<HD, F32>(sm.mt, a, m0, tid);
   __syncthreads();
   // dKhat^T -= sum_d M[c][d] dV[j][d]
 #pragma unroll
@@ -572,8 +673,14 @@ __global__ void __launch_bounds__(NT) tok_grad_kernel(b3_chain_bwd_args a) {
   for (int ti = 0; ti < LT / 32; ++ti) {
     f32x16 p = zero16();
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-      mma_bf16(p, row_piece(sm.kt, 32 * ti + n, 2 * ks + h), row_piece(sm.kt, j, 2 * ks + h));
+    for (int ks = 0; ks < KS; ++ks) {
+      const u16x8 ai = row_piece<HD>(sm.kt.hi, 32 * ti + n, 2 * ks + h), bj = row_piece<HD>(sm.kt.hi, j, 2 * ks + h);
+      mma_bf16(p, ai, bj);
+      if constexpr (F32) {
+        mma_bf16(p, ai, row_piece<HD>(sm.kt.lo, j, 2 * ks + h));
+        mma_bf16(p, row_piece<HD>(sm.kt.lo, 32 * ti + n, 2 * ks + h), bj);
+      }
+    }
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int ii = 32 * ti + d_row(lane, r);
@@ -588,22 +695,26 @@ __global__ void __launch_bounds__(NT) tok_grad_kernel(b3_chain_bwd_args a) {
       acc_operand_split(p, kc, qh, ql);
 #pragma unroll
       for (int cb = 0; cb < NCB; ++cb) {
-        const u16x8 ka = tr_operand<HD>(sm.kt + 32 * ti * HD, TL, cb, kc);
+        const u16x8 ka = tr_operand<HD>(sm.kt.hi + 32 * ti * HD, TL, cb, kc);
         mma_bf16(dkn[cb], ka, qh);
         mma_bf16(dkn[cb], ka, ql);
+        if constexpr (F32) mma_bf16(dkn[cb], tr_operand<HD>(sm.kt.lo + 32 * ti * HD, TL, cb, kc), qh);
       }
     }
   }
   dwg = pair_sum32(dwg);
   // the normalisation: dk = (dKhat - khat (khat . dKhat)) / |k|
+  float kq[NCB][4][4];
   float sdot = 0.f;
 #pragma unroll
   for (int cb = 0; cb < NCB; ++cb)
 #pragma unroll
     for (int r4 = 0; r4 < 4; ++r4) {
-      const uint2 k2 = row_quad(sm.kt, j, 32 * cb + 8 * r4 + 4 * h);
-      sdot += bf_lo(k2.x) * dkn[cb][4 * r4] + bf_hi(k2.x) * dkn[cb][4 * r4 + 1] + bf_lo(k2.y) * dkn[cb][4 * r4 + 2] +
-              bf_hi(k2.y) * dkn[cb][4 * r4 + 3];
+      float4 k4 = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (live) k4 = key_quad<HD, F32>(krows, j, 32 * cb + 8 * r4 + 4 * h);
+      kq[cb][r4][0] = k4.x; kq[cb][r4][1] = k4.y; kq[cb][r4][2] = k4.z; kq[cb][r4][3] = k4.w;
+      sdot += k4.x * dkn[cb][4 * r4] + k4.y * dkn[cb][4 * r4 + 1] + k4.z * dkn[cb][4 * r4 + 2] +
+              k4.w * dkn[cb][4 * r4 + 3];
     }
   sdot = pair_sum32(sdot);
   if (!live) return;
@@ -613,31 +724,48 @@ __global__ void __launch_bounds__(NT) tok_grad_kernel(b3_chain_bwd_args a) {
   for (int cb = 0; cb < NCB; ++cb)
 #pragma unroll
     for (int r4 = 0; r4 < 4; ++r4) {
-      const uint2 k2 = row_quad(sm.kt, j, 32 * cb + 8 * r4 + 4 * h);
       float4* p = reinterpret_cast<float4*>(dk + 32 * cb + 8 * r4 + 4 * h);
       float4 x = *p;
-      x.x += (dkn[cb][4 * r4] - bf_lo(k2.x) * f2) * inj;
-      x.y += (dkn[cb][4 * r4 + 1] - bf_hi(k2.x) * f2) * inj;
-      x.z += (dkn[cb][4 * r4 + 2] - bf_lo(k2.y) * f2) * inj;
-      x.w += (dkn[cb][4 * r4 + 3] - bf_hi(k2.y) * f2) * inj;
+      x.x += (dkn[cb][4 * r4] - kq[cb][r4][0] * f2) * inj;
+      x.y += (dkn[cb][4 * r4 + 1] - kq[cb][r4][1] * f2) * inj;
+      x.z += (dkn[cb][4 * r4 + 2] - kq[cb][r4][2] * f2) * inj;
+      x.w += (dkn[cb][4 * r4 + 3] - kq[cb][r4][3] * f2) * inj;
       *p = x;
     }
   if (h == 0 && log_rec(a, i, bh)[B3_LOG_DELTA * B3_LOG_COLS + j] > 0.5f)
     a.d_beta[trow] += (rsj > 0.f ? dbs / rsj : 0.f) + dwg;
 }
 
+template <int HD, bool F32>
+static int launch(const b3_chain_bwd_args& a, hipStream_t st) {
+  const long long BH = (long long)a.B * a.HKV;
+  hipLaunchKernelGGL((tok_stats_kernel<HD, F32>), dim3(a.n_steps, (unsigned)BH), dim3(NT), 0, st, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  hipLaunchKernelGGL((slot_rec_kernel<HD>), dim3((unsigned)BH, Dims<HD>::NSL), dim3(NT), 0, st, a);
+  e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  hipLaunchKernelGGL((m_rec_kernel<HD, F32>), dim3((unsigned)(BH * Dims<HD>::NCB)), dim3(64 * Dims<HD>::NCB), 0, st,
+                     a);
+  e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  hipLaunchKernelGGL((tok_grad_kernel<HD, F32>), dim3(a.n_steps, (unsigned)BH), dim3(NT), 0, st, a);
+  return (int)hipGetLastError();
+}
+
 }  // namespace cbwd
 }  // namespace b3
 
 extern "C" int64_t bolt3_chain_bwd_workspace_bytes(int32_t B, int32_t HKV, int32_t HD, int32_t n_steps) {
-  if (B <= 0 || HKV <= 0 || HD != b3::cbwd::HD || n_steps <= 0) return 0;
-  return b3::cbwd::ws_bytes(n_steps, (long long)B * HKV);
+  if (B <= 0 || HKV <= 0 || (HD != 64 && HD != 128) || n_steps <= 0) return 0;
+  return b3::cbwd::ws_bytes(n_steps, (long long)B * HKV, HD);
 }
 
 extern "C" int bolt3_chain_bwd(const b3_chain_bwd_args* a, void* stream) {
   using namespace b3::cbwd;
   if (!a) return B3_ERR_ARG;
-  if (a->dtype != B3_BF16 || a->HD != HD || a->S != S) return B3_ERR_UNSUPPORTED;
+  if ((a->dtype != B3_BF16 && a->dtype != B3_F32) || (a->HD != 64 && a->HD != 128) || a->S != S)
+    return B3_ERR_UNSUPPORTED;
   if (a->B <= 0 || a->HKV <= 0 || a->T <= 0 || a->n_steps <= 0) return B3_ERR_ARG;
   if (a->len0 <= 0 || a->len0 > LT || a->step_len <= 0 || a->step_len > LT || a->off0 < 0 || a->step_stride <= 0)
     return B3_ERR_UNSUPPORTED;
@@ -649,17 +777,9 @@ extern "C" int bolt3_chain_bwd(const b3_chain_bwd_args* a, void* stream) {
       !a->work)
     return B3_ERR_ARG;
   const long long BH = (long long)a->B * a->HKV;
-  if (a->work_bytes < ws_bytes(a->n_steps, BH)) return B3_ERR_WORKSPACE;
+  if (a->work_bytes < ws_bytes(a->n_steps, BH, a->HD)) return B3_ERR_WORKSPACE;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(tok_stats_kernel, dim3(a->n_steps, (unsigned)BH), dim3(NT), 0, st, *a);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return (int)e;
-  hipLaunchKernelGGL(slot_rec_kernel, dim3((unsigned)BH, NSL), dim3(NT), 0, st, *a);
-  e = hipGetLastError();
-  if (e != hipSuccess) return (int)e;
-  hipLaunchKernelGGL(m_rec_kernel, dim3((unsigned)(BH * NCB)), dim3(NT), 0, st, *a);
-  e = hipGetLastError();
-  if (e != hipSuccess) return (int)e;
-  hipLaunchKernelGGL(tok_grad_kernel, dim3(a->n_steps, (unsigned)BH), dim3(NT), 0, st, *a);
-  return (int)hipGetLastError();
+  if (a->dtype == B3_BF16)
+    return a->HD == 128 ? launch<128, false>(*a, st) : launch<64, false>(*a, st);
+  return a->HD == 128 ? launch<128, true>(*a, st) : launch<64, true>(*a, st);
 }

@@ -80,5 +80,8 @@ def test_cfg3_prefill_8192_and_decode_steps(gpu):
     print(f"[decisions] cfg3: events={len(rec)} x {B * 8} rows mismatches={mism} near-ties={near} "
           f"rounding divergences={rnd} rows ordered on exact ties={ties}", flush=True)
     assert mism == 0 and rnd <= len(rec) * B * 8 // 1000 and len(logs) == len(rec)
-    _check_state(st, m.view(B * 8, 128, 128), cache.st, torch.bfloat16, "cfg3 end state vs forced oracle")
+    # M_res after 61 steady delta-rule steps (products of fp32 operands split into bf16 hi + lo keep
+    # about 16 bits each step, and gamma ~ 0.9 carries each step's rounding into the next ones)
+    _check_state(st, m.view(B * 8, 128, 128), cache.st, torch.bfloat16, "cfg3 end state vs forced oracle",
+                 m_tol=2e-3)
     assert st.n_filled == cache.st.n_filled == 128

@@ -58,18 +58,21 @@ def _any_near(vals, n):
 ROUND = 2.0 ** -7   # bf16: two roundings of a score apart (8 significant bits)
 
 
-def _pair(a_o, b_o, a_k, b_k, bf16=False):
+def _pair(a_o, b_o, a_k, b_k, bf16=False, same_inputs=True):
     """Class of two items an ordering placed differently: "near" -- their values within 4e-4
     relative of each other in the oracle's arithmetic (a_o, b_o) or in the kernel's (a_k, b_k),
-    and not exactly equal in both (exactly equal values must be ordered as torch.topk orders
-    them; 4e-4 because items of one near-tied group can trade places with any member of it);
+    and not exactly equal in both (4e-4 because items of one near-tied group can trade places
+    with any member of it).  Values exactly equal in both arithmetics must be ordered as
+    torch.topk orders them when the two orderings sort bit-identical arrays (same_inputs); when
+    any value of the array differs between the arithmetics, torch.topk's partition steps differ
+    and so may its order among equal values, and such a pair is a tie like any other ("near");
     "round" (bf16 storage only) -- within 2^-7 instead, where the two arithmetics already differ
     by more than 1e-4 on one of the items: the reference rounds the slot scores to bf16 before
     their softmax, and a score that rounds the other way moves the read-out by about one bf16
     ulp; "bad" -- anything else."""
     close = lambda a, b, tol: abs(a - b) <= tol * max(abs(a), abs(b), 1e-6)
     if a_o == b_o and a_k == b_k:
-        return "bad"
+        return "bad" if same_inputs else "near"
     if close(a_o, b_o, 4 * TIE) or close(a_k, b_k, 4 * TIE):
         return "near"
     if bf16 and (close(a_o, b_o, ROUND) or close(a_k, b_k, ROUND)) and \
@@ -137,7 +140,8 @@ def _compare_step(lg, log, bh, l, where, bf16=False):
             picked, got = lg["picked"][r].tolist(), got_all[r].tolist()
             so, sk = lg["score"][r].tolist(), log[r, LOG["score"], :l].tolist()
             # every pair of tokens the two fills order differently must be a near-tie
-            cls = {(x, y): _pair(so[x], so[y], sk[x], sk[y], bf16) for x, y in _inversions(picked, got, l, m)}
+            same = so == sk
+            cls = {(x, y): _pair(so[x], so[y], sk[x], sk[y], bf16, same) for x, y in _inversions(picked, got, l, m)}
             bad = [xy for xy, c in cls.items() if c == "bad"]
             row = _row_class(cls.values())
             if row != "bad" and all(0 <= t < l for t in got):
@@ -179,9 +183,10 @@ def _compare_step(lg, log, bh, l, where, bf16=False):
         # the other does not, the token's score against the slot's keep value must be one
         nw_o, nw_k = int(lg["win"][r].sum()), int(w_g[r].sum())
         W = max(nw_o, nw_k)
-        ct = {(x, y): _pair(so[x], so[y], sk[x], sk[y], bf16)
+        same_t, same_s = so == sk, ko == kk
+        ct = {(x, y): _pair(so[x], so[y], sk[x], sk[y], bf16, same_t)
               for x, y in _inversions(lg["top_toks"][r].tolist(), tt_g[r].tolist(), l, W)}
-        cs = {(x, y): _pair(ko[x], ko[y], kk[x], kk[y], bf16)
+        cs = {(x, y): _pair(ko[x], ko[y], kk[x], kk[y], bf16, same_s)
               for x, y in _inversions(lg["bot_slots"][r].tolist(), bs_g[r].tolist(), len(ko), W)}
         cw = {k: _pair(tv[k], bv[k], gtv[k], gbv[k], bf16) for k in range(min(nw_o, nw_k), W)}
         bad_t = [xy for xy, c in ct.items() if c == "bad"]
@@ -251,8 +256,9 @@ def _max_rounding(log) -> int:
     return (log.shape[0] * log.shape[1]) // 1000
 
 
-def _check_state(st, m_res, ref: O.SlotState, dtype, what):
-    """The kernel's slot state and M_res against the oracle's at the same point of one trajectory."""
+def _check_state(st, m_res, ref: O.SlotState, dtype, what, m_tol=None):
+    """The kernel's slot state and M_res against the oracle's at the same point of one trajectory
+    (M_res: 1e-4 relative in fp32, 1e-3 in bf16 unless ``m_tol`` says otherwise)."""
     bf = dtype == torch.bfloat16
     assert torch.equal(st["act"].cpu().bool().view_as(ref.act), ref.act), what
     assert torch.equal(st["mass"].cpu().view_as(ref.mass), ref.mass), what
@@ -262,7 +268,8 @@ def _check_state(st, m_res, ref: O.SlotState, dtype, what):
     assert rel_err(st["av"].cpu().float().view_as(ref.av), ref.av.float()) <= (1e-2 if bf else 1e-5), what
     if ref.m_res.abs().max() > 0:
         e = rel_err(m_res.cpu().view_as(ref.m_res), ref.m_res)
-        assert e <= (1e-3 if bf else 1e-4), (what, e)
+        print(f"  {what}: M_res rel err {e:.2e}", flush=True)
+        assert e <= (m_tol or (1e-3 if bf else 1e-4)), (what, e)
 
 
 @pytest.mark.parametrize("name", FWD)

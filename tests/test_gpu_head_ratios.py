@@ -1,5 +1,5 @@
 """The bf16 forward at head ratios and head sizes the golden fixtures leave out, against the oracle
-(lowest-index ties, the kernel's rule) at the bf16 bar (max-abs <= 2e-2, cosine >= 0.9995):
+(torch.topk's order among equal values, the reference's) at the bf16 bar (max-abs <= 2e-2, cosine >= 0.9995):
 
 * one query head per kv head (two-wavefront attention workgroups),
 * eight query heads per kv head (one 32-query sub-tile per wavefront),

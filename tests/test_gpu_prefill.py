@@ -77,3 +77,72 @@ def test_prefill_matches_chunked_feed(T, dt, gpu):
             hb, _, _ = dec.step(tok, T + i, st_b, kv_b)
             hc, _, _ = dec.step(tok, T + i, st_c, kv_c)
             assert _close(hb, hc, dt), i
+
+
+@pytest.mark.parametrize("T", [100, 128, 300, 512, 700])
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
+def test_prefill_matches_forced_oracle(T, dt, gpu):
+    """The layer-major prefill against the reference's chunk-by-chunk decoder step (the oracle's
+    layer_step, vsa_lm/config/bolt3.py:343-425, 450-457) forced onto the prefill's own decisions,
+    layer by layer on the inputs the prefill gave each Bolt-3 layer: every chunk's output, every
+    consolidation's decisions against the oracle's own from the same state (near-ties counted),
+    and the layer's end state; and the stack's last hidden states against the oracle's whole
+    chunk-by-chunk prefill, forced likewise."""
+    import copy
+    from bolt3_amd import Bolt3Decoder
+    from helpers import bf16_check, decisions_from_kernel_log, rel_err
+    from oracle import bolt3_oracle as O
+    from test_gpu_parity import _check_out, _check_state, _compare_step
+    print(f"[case] prefill vs forced oracle T={T} {dt}", flush=True)
+    model = _model(31, ["vsa", "softmax", "vsa"], head_dim=64).to(dt)
+    model_cpu = copy.deepcopy(model)
+    dec = Bolt3Decoder(model.to(gpu))
+    ids = recipes.tokens(31, 2, T, 512)
+    taps = {}
+    layer_prefill = dec._bolt3_prefill
+    index = {id(blk.vsa): li for li, blk in enumerate(model.blocks) if hasattr(blk, "vsa")}
+
+    def tapped(ly, h, m_state, st, record=None):
+        out = layer_prefill(ly, h, m_state, st, record)
+        taps[index[id(ly)]] = (h.cpu(), out.cpu())
+        return out
+
+    dec._bolt3_prefill = tapped
+    rec = {}
+    with torch.no_grad():
+        h, states, kv = dec.prefill(ids.to(gpu), record=rec)
+    forced = {li: [decisions_from_kernel_log(e["log"]) for e in evs] for li, evs in rec.items()}
+    n_ev = max(0, -(-T // 128) - 2 + (T % 128 == 0 and T >= 256))
+    bf16 = dt == torch.bfloat16
+    for li in (0, 2):
+        evs = rec.get(li, [])
+        assert len(evs) == n_ev
+        p = O.Bolt3Params.from_module(model_cpu.blocks[li].vsa)
+        h_in, out_k = taps[li]
+        it = iter(forced.get(li, []))
+        cache, m_r, logs = O.LayerCache(), torch.zeros(2, p.HKV, p.HD, p.HD), []
+        with torch.no_grad():
+            for c0 in range(0, T, 128):
+                c1 = min(T, c0 + 128)
+                _, out, m_r = O.layer_step(p, h_in[:, c0:c1], c0, m_r, cache, log=logs, force=lambda: next(it))
+                got = out_k[:, c0:c1]
+                if bf16:
+                    ok, ma, ratio, cs = bf16_check(got, out)
+                    assert ok, (li, c0, ma, ratio, cs)
+                else:
+                    assert rel_err(got, out) <= 1e-4, (li, c0, rel_err(got, out))
+        assert len(logs) == n_ev
+        mism = near = rnd = 0
+        for e, (gl, lg) in enumerate(zip(evs, logs)):
+            a, b_, _, d = _compare_step(lg, gl["log"].cpu(), gl["log"].shape[0], gl["tokens"], f"layer {li} event {e}",
+                                        bf16)
+            mism, near, rnd = mism + a, near + b_, rnd + d
+        print(f"  layer {li}: events={len(evs)} mismatches={mism} near-ties={near} rounding={rnd}", flush=True)
+        assert mism == 0 and rnd == 0
+        assert kv[li].n_filled == (cache.st.n_filled if cache.st is not None else 0)
+        if cache.st is not None:
+            _check_state(kv[li], states[li].reshape(-1, p.HD, p.HD), cache.st, dt, f"layer {li} state")
+    ref = O.HybridRef(model_cpu, decisions=forced)
+    with torch.no_grad():
+        h_r, _ = ref.prefill(ids)
+    _check_out(h.cpu(), h_r, dt, f"prefill T={T}", normed=True)

@@ -251,6 +251,9 @@ typedef struct {
   /* mode 0, bf16: only chunks [chunk_begin, chunk_end) (chunk_end == 0: to the last chunk), so that
      the slot field of early chunks can run while the chain still works on later steps */
   int32_t chunk_begin, chunk_end;
+  /* mode 0, optional (NULL: not written): [B][H][n_q] fp32, every query's log-sum-exp (natural log)
+     of its scaled, biased scores over all its keys -- the softmax normaliser the backward reuses */
+  float* lse;
 } b3_attn_args;
 
 /*
@@ -322,6 +325,11 @@ typedef struct {
   float* d_slot_v;
   float* d_sink_k;            /* [n_chunks][B*HKV][n_sinks][HD] (chunks 0 and 1 are not written) */
   float* d_sink_v;
+  int32_t part;               /* 0: everything; 1: the readout kernel only (d_m, d_q_raw, d_eta, d_res_w,
+                                 d_gamma, d_rows); 2: the attention kernels only, after a part-1 call
+                                 with the same arguments (they read d_rows) */
+  int32_t lse_ready;          /* 1: lse already holds every query row's log-sum-exp (natural log), as
+                                 bolt3_chunk_attn writes it when given an lse buffer; 0: computed here */
 } b3_attn_bwd_args;
 int bolt3_attn_bwd(const b3_attn_bwd_args* a, void* stream);
 
@@ -480,7 +488,22 @@ typedef struct {
   float* d_gamma;             /* out: [n_steps][B*HKV][HD/32] partial sums of dL/dgamma */
   void* work;                 /* >= bolt3_chain_bwd_workspace_bytes(...) bytes */
   int64_t work_bytes;
+  int32_t kernels;            /* which of the four kernels this call launches, in their order: a mask of
+                                 B3_CBWD_* bits, 0 = all.  Calls that split them keep the order (token
+                                 statistics before the M_res recursion and the token gradients, both
+                                 recursions before the token gradients) and the same arguments and
+                                 workspace; the two recursions touch disjoint data and may run on
+                                 different streams.  The statistics and the M_res recursion read d_m
+                                 only, the slot recursion d_slot_k / d_slot_v only */
+  uint32_t* started;          /* optional (NULL to skip): each workgroup of the M_res and slot recursions
+                                 that this call launches adds 1 when it begins (B*HKV*HD/32 and
+                                 B*HKV*HD/16 of them), for bolt3_wait_count */
 } b3_chain_bwd_args;
+#define B3_CBWD_STATS 1
+#define B3_CBWD_M_REC 2
+#define B3_CBWD_SLOT_REC 4
+#define B3_CBWD_TOK_GRAD 8
+#define B3_CBWD_ALL 15
 int bolt3_chain_bwd(const b3_chain_bwd_args* a, void* stream);
 int64_t bolt3_chain_bwd_workspace_bytes(int32_t B, int32_t HKV, int32_t HD, int32_t n_steps);
 

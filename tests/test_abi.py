@@ -157,3 +157,17 @@ def test_noalloc_scratch_size_matches_header():
     m = re.search(r"#define B3_CHAIN_NOALLOC_SCRATCH_BYTES \((\d+) << (\d+)\)", txt)
     assert m and int(m.group(1)) << int(m.group(2)) == A.CHAIN_NOALLOC_SCRATCH_BYTES
 
+
+
+def test_chain_bwd_kernel_bits_match_header():
+    txt = open(HEADER).read()
+    bits = {k: int(v) for k, v in re.findall(r"#define B3_CBWD_(\w+) (\d+)", txt)}
+    assert bits == {"STATS": A.CBWD_STATS, "M_REC": A.CBWD_M_REC, "SLOT_REC": A.CBWD_SLOT_REC,
+                    "TOK_GRAD": A.CBWD_TOK_GRAD, "ALL": 15}
+    # a mask outside the four bits is rejected before any launch
+    lib = A.load()
+    cb = A.ChainBwdArgs()
+    cb.dtype, cb.B, cb.HKV, cb.HD, cb.S, cb.T = 1, 1, 1, 128, 128, 512
+    cb.n_steps, cb.off0, cb.len0, cb.step_stride, cb.step_len = 2, 4, 124, 128, 128
+    cb.kernels = 16
+    assert lib.bolt3_chain_bwd(ctypes.byref(cb), None) == 1001

@@ -72,7 +72,7 @@ class AttnArgs(C.Structure):
         ("m_res", p), ("m_step", i64), ("m_split", i32),
         ("gamma", p), ("res_w", p), ("eps", f32),
         ("y", p), ("y_sb", i64), ("y_st", i64),
-        ("part", i32), ("partial", p), ("chunk_begin", i32), ("chunk_end", i32),
+        ("part", i32), ("partial", p), ("chunk_begin", i32), ("chunk_end", i32), ("lse", p),
     ]
 
 
@@ -121,7 +121,7 @@ class AttnBwdArgs(C.Structure):
         ("dy", p), ("dy_sb", i64), ("dy_st", i64),
         ("d_rows", p), ("lse", p), ("d_q_rope", p), ("d_q_raw", p), ("d_eta", p), ("d_m", p), ("d_res_w", p),
         ("d_gamma", p), ("d_bias", p), ("d_k_own", p), ("d_v_own", p), ("d_k_next", p), ("d_v_next", p),
-        ("d_slot_k", p), ("d_slot_v", p), ("d_sink_k", p), ("d_sink_v", p),
+        ("d_slot_k", p), ("d_slot_v", p), ("d_sink_k", p), ("d_sink_v", p), ("part", i32), ("lse_ready", i32),
     ]
 
 
@@ -131,6 +131,8 @@ class RmsNormArgs(C.Structure):
 
 
 CHAIN_NOALLOC_SCRATCH_BYTES = 4 << 20   # B3_CHAIN_NOALLOC_SCRATCH_BYTES
+# b3_chain_bwd_args.kernels bits (B3_CBWD_*)
+CBWD_STATS, CBWD_M_REC, CBWD_SLOT_REC, CBWD_TOK_GRAD = 1, 2, 4, 8
 
 class ChainBwdArgs(C.Structure):
     _fields_ = [
@@ -138,7 +140,8 @@ class ChainBwdArgs(C.Structure):
         ("n_steps", i32), ("off0", i32), ("len0", i32), ("step_stride", i32), ("step_len", i32),
         ("kr", p), ("v", p), ("beta", p), ("log", p), ("snap_mass", p), ("snap_pm", p), ("snap_m", p),
         ("gamma", p), ("inv_freq", p), ("d_slot_k", p), ("d_slot_v", p), ("d_m", p),
-        ("d_kr", p), ("d_v", p), ("d_beta", p), ("d_gamma", p), ("work", p), ("work_bytes", i64),
+        ("d_kr", p), ("d_v", p), ("d_beta", p), ("d_gamma", p), ("work", p), ("work_bytes", i64), ("kernels", i32),
+        ("started", p),
     ]
 
 
@@ -226,6 +229,19 @@ def set_timing(enabled: bool):
     enabled; ``timings()`` then returns {entry point: [milliseconds per launch]}."""
     global _timers
     _timers = {} if enabled else None
+
+
+_SIDE_STREAMS: dict = {}
+
+
+def side_stream(dev: torch.device, i: int = 0) -> torch.cuda.Stream:
+    """Extra streams per device, at the default priority.  The forward runs the chain's slot
+    decisions on 0 and its M_res updates on 1; the backward runs the M_res recursion, the o_proj
+    weight gradient and the parameter reductions on 0."""
+    key = (dev.index if dev.index is not None else torch.cuda.current_device(), i)
+    if key not in _SIDE_STREAMS:
+        _SIDE_STREAMS[key] = torch.cuda.Stream(device=dev)
+    return _SIDE_STREAMS[key]
 
 
 def timings() -> dict:

@@ -37,7 +37,6 @@ def _require_gpu(t: torch.Tensor, what: str):
                            f"there is no CPU implementation")
 
 
-_SIDE_STREAMS: dict = {}
 _N_CUS: dict = {}
 
 
@@ -46,15 +45,6 @@ def _n_cus(dev: torch.device) -> int:
     if key not in _N_CUS:
         _N_CUS[key] = torch.cuda.get_device_properties(key).multi_processor_count
     return _N_CUS[key]
-
-
-def _side_stream(dev: torch.device, i: int = 0) -> torch.cuda.Stream:
-    """Extra streams per device (default priority): 0 for the chain's slot decisions, 1 for its
-    M_res updates."""
-    key = (dev.index if dev.index is not None else torch.cuda.current_device(), i)
-    if key not in _SIDE_STREAMS:
-        _SIDE_STREAMS[key] = torch.cuda.Stream(device=dev)
-    return _SIDE_STREAMS[key]
 
 
 # Per device: a counter that the slot-decision workgroups of the forward's first step group bump
@@ -360,8 +350,8 @@ class Bolt3Attn(nn.Module):
         ctr = _started_counter(dev) if split and 2 * b * HKV <= _n_cus(dev) else None
         first_started = None
         if n_cons > 0:
-            s_dec = _side_stream(dev, 0)
-            s_m = _side_stream(dev, 1) if split else s_dec
+            s_dec = A.side_stream(dev, 0)
+            s_m = A.side_stream(dev, 1) if split else s_dec
             # n_filled = 0: the chain builds the empty state itself, these are outputs only
             st = dict(ak=torch.empty(bh, S, HD, dtype=dt, device=dev), av=torch.empty(bh, S, HD, dtype=dt, device=dev),
                       mass=torch.empty(bh, S, device=dev), util=torch.empty(bh, S, device=dev),
@@ -441,42 +431,29 @@ class Bolt3Attn(nn.Module):
             a.m_res, a.m_step = snaps[3].data_ptr(), bh * HD * HD
             a.m_split = int(dt == torch.bfloat16)
         a.gamma, a.res_w, a.eps = gam.data_ptr(), side["res_w"].data_ptr(), float(self.res_norm.eps)
+        # The attention output goes into one [B, T, H * HD] buffer.  bf16: group by group, as soon
+        # as the chain has produced a group's snapshots, one launch over the group's chunks (the
+        # first group also takes chunks 0 and 1); then o_proj as one GEMM.  (o_proj per group,
+        # on [B * rows] blocks copied into place, measured the same, 1.379 vs 1.380 ms at cfg2,
+        # and needed a copy of the whole output for the backward's trace.)
+        y = torch.empty(b, T, K, dtype=dt, device=dev)
+        a.y, a.y_sb, a.y_st = y.data_ptr(), y.stride(0), y.stride(1)
+        if trace is not None:   # every query row's softmax normaliser, which the backward reuses
+            trace["lse"] = torch.empty(b, H, T, device=dev)
+            a.lse = trace["lse"].data_ptr()
         if not split:
-            y = torch.empty(b, T, K, dtype=dt, device=dev)
-            a.y, a.y_sb, a.y_st = y.data_ptr(), y.stride(0), y.stride(1)
             for ev in done:
                 main.wait_event(ev)
             A.call("bolt3_chunk_attn", a, dev)
-            if trace is not None:
-                trace["y"] = y
-            return F.linear(y, side["wo"])
-
-        # Group by group, as soon as the chain has produced a group's snapshots: the attention
-        # over all key fields of the group's chunks (the first group also takes chunks 0 and 1),
-        # the readout and o_proj.  The attention output of a group of chunks is one
-        # [B * rows, H * HD] block (token ranges of all batch rows together), so o_proj of a
-        # group is one GEMM.
-        spans = [(0, min(T, (groups[0][1] + 2) * C))] + \
-                [(min(T, (s0 + 2) * C), min(T, (s1 + 2) * C)) for s0, s1 in groups[1:]]
-        y_all = torch.empty(b * T * K, dtype=dt, device=dev)
-        blocks, off = [], 0
-        for t0, t1 in spans:
-            blocks.append(y_all[off:off + b * (t1 - t0) * K].view(b * (t1 - t0), K))
-            off += b * (t1 - t0) * K
-        out = torch.empty(b, T, self.o_proj.out_features, dtype=dt, device=dev)
-        esz = y_all.element_size()
-        a.part = 0
-        for gi, ((s0, s1), ev) in enumerate(zip(groups, done)):
-            t0, t1 = spans[gi]
-            main.wait_event(ev)
-            a.chunk_begin, a.chunk_end = (0 if gi == 0 else s0 + 2), s1 + 2
-            # element (b, t) of block gi at block + (b * rows + t - t0) * K
-            a.y, a.y_sb, a.y_st = blocks[gi].data_ptr() - t0 * K * esz, (t1 - t0) * K, K
-            A.call("bolt3_chunk_attn", a, dev)
-            out[:, t0:t1].copy_(F.linear(blocks[gi], side["wo"]).view(b, t1 - t0, -1))
+        else:
+            a.part = 0
+            for gi, ((s0, s1), ev) in enumerate(zip(groups, done)):
+                main.wait_event(ev)
+                a.chunk_begin, a.chunk_end = (0 if gi == 0 else s0 + 2), s1 + 2
+                A.call("bolt3_chunk_attn", a, dev)
         if trace is not None:
-            trace["y"] = torch.cat([blk.view(b, t1 - t0, K) for blk, (t0, t1) in zip(blocks, spans)], dim=1)
-        return out
+            trace["y"] = y
+        return F.linear(y, side["wo"])
 
     # ------------------------------------------------------------ consolidation (reference internal API)
 

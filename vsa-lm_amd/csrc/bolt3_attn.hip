@@ -267,6 +267,7 @@ __global__ void __launch_bounds__(512) attn_kernel(b3_attn_args a, int QW) {
 
   // ---- normalise; y = round(O)
   const float inv_l = l_run > 0.f ? 1.0f / l_run : 0.f;
+  if (a.mode == 0 && a.lse && qok && h == 0) a.lse[((long long)b * a.H + hq) * a.n_q + t] = m_run + logf(l_run);
 #pragma unroll
   for (int db = 0; db < NDB; ++db)
 #pragma unroll
@@ -651,6 +652,7 @@ __global__ void __launch_bounds__(512) attn_fwd_kernel(b3_attn_args a, int QW) {
 
   // ---- normalise; y = round(O)
   const float inv_l = l_run > 0.f ? 1.0f / l_run : 0.f;
+  if (a.lse && qok && h == 0) a.lse[((long long)b * a.H + hq) * a.n_q + t] = (m_run + log2f(l_run)) / L2E;
 #pragma unroll
   for (int db = 0; db < NDB; ++db)
 #pragma unroll
@@ -1130,6 +1132,7 @@ __global__ void __launch_bounds__(64 * NW) attn_fwd2_kernel(b3_attn_args a, int 
 
   // ---- normalise; y = round(O), kept as bf16 pairs (features d_row(lane, 2j), +1)
   const float inv_l = l_run > 0.f ? 1.0f / l_run : 0.f;
+  if (a.lse && qok && h == 0) a.lse[((long long)b * a.H + hq) * a.n_q + t] = (m_run + log2f(l_run)) / L2E;
   uint32_t yp[NDB][8];
 #pragma unroll
   for (int db = 0; db < NDB; ++db)

@@ -177,11 +177,11 @@ __global__ void __launch_bounds__(NT) attn_bwd_dq_kernel(b3_attn_bwd_args a) {
   for (int i = 0; i < 4; ++i) drow[i] = 4 * rg + i < nq ? a.d_rows[row0 + 4 * rg + i] : 0.f;
   const int n_fields = __popc(field_mask(a, c));
 
-  // pass 1: log-sum-exp of every row over all fields
+  // pass 1: log-sum-exp of every row over all fields (unless the forward kept it)
   float m[4], l[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) { m[i] = -INFINITY; l[i] = 0.f; }
-  for (int fi = 0; fi < n_fields; ++fi) {
+  for (int fi = 0; fi < (a.lse_ready ? 0 : n_fields); ++fi) {
     const KField f = chunk_field<T>(a, b, hkv, c, fi);
     for (int j0 = 0; j0 < f.len; j0 += BK) {
       if (f.kind == 3 && j0 > q0 + nq - 1) break;
@@ -207,8 +207,12 @@ __global__ void __launch_bounds__(NT) attn_bwd_dq_kernel(b3_attn_bwd_args a) {
   float lse[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    lse[i] = m[i] + logf(l[i]);
-    if (cg == 0 && 4 * rg + i < nq) a.lse[row0 + 4 * rg + i] = lse[i];
+    if (a.lse_ready) {
+      lse[i] = 4 * rg + i < nq ? a.lse[row0 + 4 * rg + i] : 0.f;
+    } else {
+      lse[i] = m[i] + logf(l[i]);
+      if (cg == 0 && 4 * rg + i < nq) a.lse[row0 + 4 * rg + i] = lse[i];
+    }
   }
 
   // pass 2: dS block by block, dQ += dS . K, slot-bias gradient
@@ -538,9 +542,10 @@ __global__ void __launch_bounds__(64) attn_bwd_dq_mfma_kernel(b3_attn_bwd_args a
       if (v_too) va[ks] = *reinterpret_cast<const u16x8*>(vp + 16 * ks + 8 * h);
     }
   };
-  // pass 1: log-sum-exp (log2 units) of the lane's query over all fields
+  // pass 1: log-sum-exp (log2 units) of the lane's query over all fields (unless the forward
+  // kept it)
   float m_run = -INFINITY, l_run = 0.f;
-  for (int fi = 0; fi < n_fields; ++fi) {
+  for (int fi = 0; fi < (a.lse_ready ? 0 : n_fields); ++fi) {
     const KField f = chunk_field<uint16_t>(a, b, hkv, c, fi);
     for (int j0 = 0; j0 < f.len; j0 += 32) {
       if (f.kind == 3 && j0 > q0 + nq - 1) break;
@@ -564,8 +569,13 @@ __global__ void __launch_bounds__(64) attn_bwd_dq_mfma_kernel(b3_attn_bwd_args a
       m_run = mn;
     }
   }
-  const float lse2 = m_run + log2f(l_run);
-  if (qok && h == 0) a.lse[row] = lse2 / L2E;
+  float lse2;
+  if (a.lse_ready) {
+    lse2 = qok ? a.lse[row] * L2E : 0.f;
+  } else {
+    lse2 = m_run + log2f(l_run);
+    if (qok && h == 0) a.lse[row] = lse2 / L2E;
+  }
   // pass 2: dS block by block; dQ^T += K^T dS^T; the slot bias gradient
   f32x16 dq[NDB];
 #pragma unroll
@@ -1335,12 +1345,15 @@ template <typename T, int HD>
 static int launch(const b3_attn_bwd_args& a, hipStream_t st) {
   const int n_chunks = a.n_chunks;
   const int BH = a.B * a.HKV;
-  if constexpr (St<T>::is_bf16)
-    hipLaunchKernelGGL((readout_bwd_mfma_kernel<HD>), dim3(BH, n_chunks), dim3(256), sizeof(RdMfmaSmem<HD>), st, a);
-  else
-    hipLaunchKernelGGL((readout_bwd_kernel<T, HD>), dim3(BH, n_chunks), dim3(NT), sizeof(RdSmem<HD>), st, a);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return (int)e;
+  hipError_t e = hipSuccess;
+  if (a.part != 2) {
+    if constexpr (St<T>::is_bf16)
+      hipLaunchKernelGGL((readout_bwd_mfma_kernel<HD>), dim3(BH, n_chunks), dim3(256), sizeof(RdMfmaSmem<HD>), st, a);
+    else
+      hipLaunchKernelGGL((readout_bwd_kernel<T, HD>), dim3(BH, n_chunks), dim3(NT), sizeof(RdSmem<HD>), st, a);
+    e = hipGetLastError();
+    if (e != hipSuccess || a.part == 1) return (int)e;
+  }
   const int max_blocks = 1 + (a.S + 31) / 32 + 2 * ((a.C + 31) / 32);
   if constexpr (St<T>::is_bf16) {
     hipLaunchKernelGGL((attn_bwd_dq_mfma_kernel<HD>), dim3((a.C + 31) / 32, a.B * a.H, n_chunks), dim3(64), 0, st, a);
@@ -1396,6 +1409,7 @@ extern "C" int bolt3_attn_bwd(const b3_attn_bwd_args* a, void* stream) {
                          a->slot_step < (int64_t)a->B * a->HKV * a->S * a->HD))
     return B3_ERR_ARG;
   if (a->m_split && a->dtype != B3_BF16) return B3_ERR_ARG;
+  if (a->part < 0 || a->part > 2 || (a->lse_ready != 0 && a->lse_ready != 1)) return B3_ERR_ARG;
   // 16-byte rows: every (b, h, t) row of the staged operands
   const int64_t es = a->dtype == B3_BF16 ? 2 : 4;
   if ((a->q_sb * es) % 16 || (a->q_sh * es) % 16 || (a->w_sb * es) % 16 || (a->w_sh * es) % 16 ||

@@ -247,6 +247,7 @@ __global__ void __launch_bounds__(NT) slot_rec_kernel(b3_chain_bwd_args a) {
   __shared__ float massb[S], newm[S];
   const int bh = blockIdx.x, sl = blockIdx.y;
   const int tid = threadIdx.x, s = tid >> 1, arr = tid & 1;
+  if (a.started && tid == 0) __hip_atomic_fetch_add(a.started, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const long long BH = (long long)a.B * a.HKV;
   float* grow = g[arr][s];
 #pragma unroll
@@ -374,6 +375,7 @@ __global__ void __launch_bounds__(HD * 2) m_rec_kernel(b3_chain_bwd_args a) {
   const int wg = xcd_grid_pos().x;
   const int bh = wg / NCB, db = wg % NCB;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, n = lane & 31, h = lane >> 5;
+  if (a.started && tid == 0) __hip_atomic_fetch_add(a.started, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const long long BH = (long long)a.B * a.HKV;
   const float gam = a.gamma[bh % a.HKV];
   const TrLanes<HD> TL(lane);
@@ -739,17 +741,26 @@ __global__ void __launch_bounds__(NT) tok_grad_kernel(b3_chain_bwd_args a) {
 template <int HD, bool F32>
 static int launch(const b3_chain_bwd_args& a, hipStream_t st) {
   const long long BH = (long long)a.B * a.HKV;
-  hipLaunchKernelGGL((tok_stats_kernel<HD, F32>), dim3(a.n_steps, (unsigned)BH), dim3(NT), 0, st, a);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return (int)e;
-  hipLaunchKernelGGL((slot_rec_kernel<HD>), dim3((unsigned)BH, Dims<HD>::NSL), dim3(NT), 0, st, a);
-  e = hipGetLastError();
-  if (e != hipSuccess) return (int)e;
-  hipLaunchKernelGGL((m_rec_kernel<HD, F32>), dim3((unsigned)(BH * Dims<HD>::NCB)), dim3(64 * Dims<HD>::NCB), 0, st,
-                     a);
-  e = hipGetLastError();
-  if (e != hipSuccess) return (int)e;
-  hipLaunchKernelGGL((tok_grad_kernel<HD, F32>), dim3(a.n_steps, (unsigned)BH), dim3(NT), 0, st, a);
+  const int k = a.kernels == 0 ? B3_CBWD_ALL : a.kernels;
+  hipError_t e = hipSuccess;
+  if (k & B3_CBWD_STATS) {
+    hipLaunchKernelGGL((tok_stats_kernel<HD, F32>), dim3(a.n_steps, (unsigned)BH), dim3(NT), 0, st, a);
+    e = hipGetLastError();
+    if (e != hipSuccess) return (int)e;
+  }
+  if (k & B3_CBWD_M_REC) {
+    hipLaunchKernelGGL((m_rec_kernel<HD, F32>), dim3((unsigned)(BH * Dims<HD>::NCB)), dim3(64 * Dims<HD>::NCB), 0,
+                       st, a);
+    e = hipGetLastError();
+    if (e != hipSuccess) return (int)e;
+  }
+  if (k & B3_CBWD_SLOT_REC) {
+    hipLaunchKernelGGL((slot_rec_kernel<HD>), dim3((unsigned)BH, Dims<HD>::NSL), dim3(NT), 0, st, a);
+    e = hipGetLastError();
+    if (e != hipSuccess) return (int)e;
+  }
+  if (k & B3_CBWD_TOK_GRAD)
+    hipLaunchKernelGGL((tok_grad_kernel<HD, F32>), dim3(a.n_steps, (unsigned)BH), dim3(NT), 0, st, a);
   return (int)hipGetLastError();
 }
 
@@ -769,6 +780,7 @@ extern "C" int bolt3_chain_bwd(const b3_chain_bwd_args* a, void* stream) {
   if (a->B <= 0 || a->HKV <= 0 || a->T <= 0 || a->n_steps <= 0) return B3_ERR_ARG;
   if (a->len0 <= 0 || a->len0 > LT || a->step_len <= 0 || a->step_len > LT || a->off0 < 0 || a->step_stride <= 0)
     return B3_ERR_UNSUPPORTED;
+  if (a->kernels < 0 || a->kernels > B3_CBWD_ALL) return B3_ERR_ARG;
   if ((long long)a->off0 + a->len0 > a->T ||
       (a->n_steps > 1 && (long long)(a->n_steps - 1) * a->step_stride + a->step_len > a->T))
     return B3_ERR_ARG;

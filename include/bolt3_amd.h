@@ -305,7 +305,8 @@ typedef struct {
   const void* dy;             /* its gradient in the storage dtype, (b, t, h, d) at + b*dy_sb + t*dy_st + h*HD + d */
   int64_t dy_sb, dy_st;
   float* d_rows;              /* [B][H][T] written: sum over d of dy * attention output */
-  float* lse;                 /* [B][H][T] written: log-sum-exp of every query row */
+  const float* lse;           /* [B][H][T] every query row's log-sum-exp (natural log) as the forward wrote it
+                                 (b3_attn_args.lse of the bolt3_chunk_attn call that made y) */
   /* d_q_rope, d_q_raw and the d_k_* / d_v_* row gradients are in the storage dtype (the
      gradients of storage-dtype tensors); the rest is fp32 */
   void* d_q_rope;             /* [B][H][T][HD] */
@@ -328,8 +329,6 @@ typedef struct {
   int32_t part;               /* 0: everything; 1: the readout kernel only (d_m, d_q_raw, d_eta, d_res_w,
                                  d_gamma, d_rows); 2: the attention kernels only, after a part-1 call
                                  with the same arguments (they read d_rows) */
-  int32_t lse_ready;          /* 1: lse already holds every query row's log-sum-exp (natural log), as
-                                 bolt3_chunk_attn writes it when given an lse buffer; 0: computed here */
 } b3_attn_bwd_args;
 int bolt3_attn_bwd(const b3_attn_bwd_args* a, void* stream);
 

@@ -49,28 +49,48 @@ def test_backward_matches_reference_gradients(name, gpu):
     assert not bad, bad
 
 
-def test_backward_bf16_hd128_vs_oracle(gpu):
-    """bf16 storage, head_dim 128, G = 4, clustered input where tokens merge, replace slots and
-    go to M_res: the HIP gradients against autograd through the oracle's bf16 forward (the
-    reference's bf16 arithmetic), relative error <= 3e-2 and cosine >= 0.999 for x and every
-    parameter, the readout's parameters included."""
-    cfg = dict(dim=256, num_heads=8, num_kv_heads=2, head_dim=128, rope_theta=1e6, eps=1e-6, qk_norm=True)
+@pytest.mark.parametrize("hd,heads,kv,T", [(128, 8, 2, 1024), (64, 4, 2, 1000), (128, 8, 8, 700), (64, 16, 2, 520)])
+def test_backward_bf16_vs_oracle(hd, heads, kv, T, gpu):
+    """bf16 storage, clustered input where tokens merge, replace slots and go to M_res: the HIP
+    gradients against autograd through the oracle's bf16 forward (the reference's bf16
+    arithmetic), relative error <= 3e-2 and cosine >= 0.999 for x and every parameter, the
+    readout's parameters included.  Head dims 64 and 128, G = 4, 2, 1 and 8, sequence lengths
+    with a partial last chunk and a partial last query tile.
+
+    Where the reference's own bf16 arithmetic is more than 5e-2 from the exact gradient (the
+    oracle's fp32 autograd on the same bf16-valued weights and input) -- a sum like kappa's, over
+    a few slot columns of the softmax gradient, whose rows sum to zero -- two bf16 computations
+    cannot agree to 3e-2; there the HIP gradient has to be as close to the exact one as the
+    reference's (within 25 % and 5e-3).  Parameters whose gradient is exactly zero in both
+    (no token reached M_res) compare equal."""
+    import copy
+    cfg = dict(dim=256, num_heads=heads, num_kv_heads=kv, head_dim=hd, rope_theta=1e6, eps=1e-6, qk_norm=True)
     from bolt3_amd import Bolt3Attn
     mod = recipes.init_module(Bolt3Attn(cfg), 31, nondefault=True).to(torch.bfloat16)
-    x = recipes.clustered_hidden(31, 1, 1024, 256, n_centres=512, noise=0.15).to(torch.bfloat16)
-    up = recipes.upstream(31, 1, 1024, 256)
-    print("[case] backward bf16 hd128 vs oracle", flush=True)
+    x = recipes.clustered_hidden(31, 1, T, 256, n_centres=512, noise=0.15).to(torch.bfloat16)
+    up = recipes.upstream(31, 1, T, 256)
+    print(f"[case] backward bf16 vs oracle hd={hd} H={heads} HKV={kv} T={T}", flush=True)
+    exact = O.forward_grads(O.Bolt3Params.from_module(copy.deepcopy(mod).float()), x.float(), up)[1]
     y, gr = _grads(mod, x, up, gpu)
     yr, ref = O.forward_grads(O.Bolt3Params.from_module(mod), x, up)
     assert rel_err(y.float(), yr.float()) <= 2e-2
-    for k in ("eta_proj.weight", "res_norm.weight", "log_gamma", "beta_proj.weight"):
-        assert float(ref[k].norm()) > 0, k          # the M_res path is exercised
-    out = []
+    if T >= 1000:
+        for k in ("eta_proj.weight", "res_norm.weight", "log_gamma", "beta_proj.weight"):
+            assert float(ref[k].norm()) > 0, k      # the M_res path is exercised
+    out, bad = [], []
     for k in sorted(ref):
-        a, b = gr[k].float(), ref[k].float()
-        out.append((k, rel_err(a, b), cosine(a, b)))
-    print("  " + " ".join(f"{k}={e:.2e}/{c:.5f}" for k, e, c in out), flush=True)
-    bad = [(k, e, c) for k, e, c in out if e > 3e-2 or c < 0.999]
+        a, b, e = gr[k].float(), ref[k].float(), exact[k].float()
+        if float(a.norm()) == 0 and float(b.norm()) == 0:
+            continue
+        err, cos = rel_err(a, b), cosine(a, b)
+        e_ref, e_hip = rel_err(b, e), rel_err(a, e)
+        out.append(f"{k}={err:.2e}/{cos:.5f} (exact: hip {e_hip:.2e}, ref {e_ref:.2e})")
+        if e_ref > 5e-2:
+            if e_hip > 1.25 * e_ref + 5e-3:
+                bad.append((k, e_hip, e_ref))
+        elif err > 3e-2 or cos < 0.999:
+            bad.append((k, err, cos))
+    print("  " + "\n  ".join(out), flush=True)
     assert not bad, bad
 
 

@@ -103,8 +103,7 @@ def attn_backward_args(mod, tr: dict, dy: torch.Tensor, dt: torch.dtype, n_steps
                        d_sink_v=(n_chunks, bh, ns, HD))
     zshapes.update(extra_zeros or {})
     o = _zero_arena(dev, zshapes)
-    lse_ready = "lse" in tr
-    o.update(d_rows=torch.empty(b, H, T, **f32), lse=tr["lse"] if lse_ready else torch.empty(b, H, T, **f32),
+    o.update(d_rows=torch.empty(b, H, T, **f32), lse=tr["lse"],
              d_q_rope=torch.empty(b, H, T, HD, **sdt), d_q_raw=torch.empty(b, H, T, HD, **sdt),
              d_eta=torch.empty(b, H, T, **f32),
              d_k_own=torch.empty(b, HKV, T, HD, **sdt), d_v_own=torch.empty(b, HKV, T, HD, **sdt),
@@ -120,7 +119,6 @@ def attn_backward_args(mod, tr: dict, dy: torch.Tensor, dt: torch.dtype, n_steps
     a = A.AttnBwdArgs()
     a.dtype, a.B, a.T, a.H, a.HKV, a.HD, a.S, a.C = A.dtype_code(dt), b, T, H, HKV, HD, S, C
     a.n_sinks, a.n_chunks, a.n_qtiles, a.n_steps, a.score_round = mod.n_sinks, n_chunks, n_qt, n_steps, 1
-    a.lse_ready = int(lse_ready)
     a.q_rope, a.q_raw, a.q_sb, a.q_sh = q_rope.data_ptr(), q_raw.data_ptr(), q_rope.stride(0), q_rope.stride(1)
     a.win_k, a.win_v, a.w_sb, a.w_sh = k_rope.data_ptr(), v.data_ptr(), k_rope.stride(0), k_rope.stride(1)
     if n_steps > 0:

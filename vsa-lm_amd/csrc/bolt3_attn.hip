@@ -17,11 +17,13 @@
 // the online-softmax state is per lane and only one cross-half exchange is
 // needed per reduction.
 #include "bolt3_common.h"
+#include "bolt3_lds.h"
 #include "bolt3_amd.h"
 
 namespace b3 {
 
 constexpr int KB = 32;  // keys per LDS stage
+static_assert(KB == F2_ROWS, "the staged tiles hold one key block");
 
 template <typename T, int HD>
 struct AttnSmem {
@@ -752,15 +754,6 @@ __global__ void __launch_bounds__(512) attn_fwd_kernel(b3_attn_args a, int QW) {
 // last barrier.
 constexpr int NST = 6;
 
-constexpr int F2_BLK = 1024 + 128;      // bytes of one 8-row x 8-piece block and its padding
-
-// Byte offset of 16-byte piece p (elements 8p .. 8p+7) of row r in a staged K or V tile:
-// block (p / 8, r / 8) at F2_BLK * ((p / 8) * (KB / 8) + r / 8), and inside it the piece at
-// 16 * ((r % 8) + 8 * (p % 8)).
-__host__ __device__ constexpr int f2_off(int r, int p) {
-  return F2_BLK * ((p >> 3) * (KB / 8) + (r >> 3)) + 16 * ((r & 7) + 8 * (p & 7));
-}
-
 template <int HD>
 struct Fwd2Smem {
   static constexpr int TILEB = (HD / 64) * (KB / 8) * F2_BLK;   // bytes of one K or V tile
@@ -770,73 +763,6 @@ struct Fwd2Smem {
   alignas(16) float resw[128];           // res_norm weight
 };
 
-__device__ __forceinline__ void lds_dma16(const void* src, void* lds) {
-  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
-}
-// wait until at most N vector-memory operations of this wave are outstanding
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | (((N >> 4) & 3) << 14) | (7 << 4) | (15 << 8));
-}
-// ds_read_b64_tr_b16 as inline assembly, at a compile-time byte offset from the address (the
-// instruction's offset field): the compiler cannot tell these reads from the LDS-DMA
-// destinations and would otherwise wait for every outstanding tile load before them.  The
-// caller waits for LDS (lds_wait8) before using the results.
-template <int OFF>
-__device__ __forceinline__ u16x4 lds_read_tr_at(uint32_t addr) {
-  static_assert(OFF >= 0 && OFF < 65536, "ds offset range");
-  u16x4 r;
-  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF) : "memory");
-  return r;
-}
-// The V^T operand reads of rows 16 H2 .. 16 H2 + 15 of a staged V tile (f2_off layout) for the
-// NDB feature blocks: tv[2 db] holds rows 16 H2 + r1, tv[2 db + 1] rows 16 H2 + 8 + r1, where the
-// lane's row r1 and piece are in its base address.
-template <int NDB, int H2>
-__device__ __forceinline__ void f2_vreads(u16x4 (&tv)[8], uint32_t base) {
-  tv[0] = lds_read_tr_at<f2_off(16 * H2, 0)>(base);
-  tv[1] = lds_read_tr_at<f2_off(16 * H2 + 8, 0)>(base);
-  tv[2] = lds_read_tr_at<f2_off(16 * H2, 4)>(base);
-  tv[3] = lds_read_tr_at<f2_off(16 * H2 + 8, 4)>(base);
-  if constexpr (NDB > 2) {
-    tv[4] = lds_read_tr_at<f2_off(16 * H2, 8)>(base);
-    tv[5] = lds_read_tr_at<f2_off(16 * H2 + 8, 8)>(base);
-    tv[6] = lds_read_tr_at<f2_off(16 * H2, 12)>(base);
-    tv[7] = lds_read_tr_at<f2_off(16 * H2 + 8, 12)>(base);
-  }
-}
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return (uint32_t)(size_t)((__attribute__((address_space(3))) const unsigned char*)p);
-}
-// The slot bias row goes through LDS by inline assembly as well (the compiler cannot separate
-// it from the LDS-DMA destinations either).
-__device__ __forceinline__ void lds_write_f32(float* p, float v) {
-  const uint32_t addr = (uint32_t)(size_t)((__attribute__((address_space(3))) const float*)p);
-  asm volatile("ds_write_b32 %0, %1" : : "v"(addr), "v"(v) : "memory");
-}
-__device__ __forceinline__ float4 lds_read_f4(const float* p) {
-  float4 r;
-  const uint32_t addr = (uint32_t)(size_t)((__attribute__((address_space(3))) const float*)p);
-  asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(r) : "v"(addr) : "memory");
-  return r;
-}
-typedef float fx4 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ fx4 lds_read_f4_nowait(const float* p) {
-  fx4 r;
-  const uint32_t addr = (uint32_t)(size_t)((__attribute__((address_space(3))) const float*)p);
-  asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(addr) : "memory");
-  return r;
-}
-// lgkmcnt(0), tied to four 16-byte LDS read results
-__device__ __forceinline__ void lds_wait4(fx4& r0, fx4& r1, fx4& r2, fx4& r3) {
-  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(r0), "+v"(r1), "+v"(r2), "+v"(r3));
-}
-// lgkmcnt(0), tied to the transposed-read results so that their users follow it
-__device__ __forceinline__ void lds_wait8(u16x4* r) {
-  asm volatile("s_waitcnt lgkmcnt(0)"
-               : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7]));
-}
 
 template <int HD, int NW>
 __global__ void __launch_bounds__(64 * NW) attn_fwd2_kernel(b3_attn_args a, int QW) {

@@ -7,23 +7,26 @@
 // for chunks c >= 2, which use the slot snapshot and M_res of consolidation step c - 2
 // (vsa_lm/config/bolt3.py:219-256).  bolt3_attn_bwd runs three kernels:
 //
-//   readout_bwd_kernel, grid (B*HKV, chunks): per row D = sum_d dy * (attention output),
-//     with the readout's own contribution taken out of y; the readout's gradients with respect
-//     to eta, q_raw, M (one dM per chunk), res_norm's weight and gamma.
-//   attn_bwd_dq_kernel, grid (query tiles, B*H, chunks): recomputes each row's log-sum-exp over
-//     all key fields, then dS = P * (dO . V^T - D) block by block, dQ = scale * dS . K and the
-//     slot columns' sums of dS (the gradient of the slot bias).
-//   attn_bwd_dkv_kernel, grid (key blocks, B*HKV, chunks): one 32-key block of one field per
-//     workgroup, over every query row of the chunk's G heads: dV = P^T . dO, dK = scale * dS^T . Q.
-//     Every key row has one writer: the previous chunk's keys go to d_k_next, the chunk's own
-//     keys to d_k_own, slots to d_slot_k of step c - 2, sinks to d_sink_k of chunk c.
+//   readout: per row D = sum_d dy * (attention output), with the readout's own contribution
+//     taken out of y; the readout's gradients with respect to eta, q_raw, M (one dM per
+//     chunk), res_norm's weight and gamma.
+//   dq: with each row's log-sum-exp as the forward kept it, dS = P * (dO . V^T - D) block by
+//     block, dQ = scale * dS . K and the slot columns' sums of dS (the gradient of the slot bias).
+//   dkv: every 32-key block of every field over every query row of the chunk's G heads:
+//     dV = P^T . dO, dK = scale * dS^T . Q.  Every key row has one writer: the previous chunk's
+//     keys go to d_k_next, the chunk's own keys to d_k_own, slots to d_slot_k of step c - 2,
+//     sinks to d_sink_k of chunk c.
 //
-// All arithmetic is fp32 (fp32 FMAs on the vector ALUs); operands of either storage dtype are
-// widened while they are staged in LDS.  Scores are rebuilt like the forward's (the q.k
-// product rounded to the storage dtype first when score_round is set, then scale, bias, mask).
+// fp32 storage runs kernels with fp32 arithmetic on the vector ALUs (operands widened while they
+// are staged in LDS); bf16 storage runs MFMA kernels (described with them below).  Scores are
+// rebuilt like the forward's (the q.k product rounded to the storage dtype first when
+// score_round is set, then scale, bias, mask).
 #include <math.h>
 
+#include <type_traits>
+
 #include "bolt3_common.h"
+#include "bolt3_lds.h"
 #include "bolt3_amd.h"
 
 namespace b3 {
@@ -177,45 +180,12 @@ __global__ void __launch_bounds__(NT) attn_bwd_dq_kernel(b3_attn_bwd_args a) {
   for (int i = 0; i < 4; ++i) drow[i] = 4 * rg + i < nq ? a.d_rows[row0 + 4 * rg + i] : 0.f;
   const int n_fields = __popc(field_mask(a, c));
 
-  // pass 1: log-sum-exp of every row over all fields (unless the forward kept it)
-  float m[4], l[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) { m[i] = -INFINITY; l[i] = 0.f; }
-  for (int fi = 0; fi < (a.lse_ready ? 0 : n_fields); ++fi) {
-    const KField f = chunk_field<T>(a, b, hkv, c, fi);
-    for (int j0 = 0; j0 < f.len; j0 += BK) {
-      if (f.kind == 3 && j0 > q0 + nq - 1) break;
-      __syncthreads();
-      stage_rows<T, HD>(&sm.k[0][0], LS, reinterpret_cast<const T*>(f.k) + (long long)j0 * HD, HD, BK, f.len - j0,
-                        tid);
-      __syncthreads();
-      float s[4][2];
-      tile_dot<HD>(s, &sm.q[0][0], &sm.k[0][0], LS, rg, cg);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float x0 = score_of<T>(a, s[i][0], f, j0, cg, q0 + 4 * rg + i, scale);
-        const float x1 = score_of<T>(a, s[i][1], f, j0, cg + 16, q0 + 4 * rg + i, scale);
-        const float bm = red16_max(fmaxf(x0, x1));
-        const float mn = fmaxf(m[i], bm);
-        if (mn == -INFINITY) continue;
-        const float e = (x0 == -INFINITY ? 0.f : expf(x0 - mn)) + (x1 == -INFINITY ? 0.f : expf(x1 - mn));
-        l[i] = l[i] * (m[i] == -INFINITY ? 0.f : expf(m[i] - mn)) + red16_sum(e);
-        m[i] = mn;
-      }
-    }
-  }
+  // every row's log-sum-exp, as the forward kept it
   float lse[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    if (a.lse_ready) {
-      lse[i] = 4 * rg + i < nq ? a.lse[row0 + 4 * rg + i] : 0.f;
-    } else {
-      lse[i] = m[i] + logf(l[i]);
-      if (cg == 0 && 4 * rg + i < nq) a.lse[row0 + 4 * rg + i] = lse[i];
-    }
-  }
+  for (int i = 0; i < 4; ++i) lse[i] = 4 * rg + i < nq ? a.lse[row0 + 4 * rg + i] : 0.f;
 
-  // pass 2: dS block by block, dQ += dS . K, slot-bias gradient
+  // dS block by block, dQ += dS . K, slot-bias gradient
   float dq[4][DPT];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
@@ -425,16 +395,45 @@ __global__ void __launch_bounds__(NT) attn_bwd_dkv_kernel(b3_attn_bwd_args a) {
 
 // ---------------------------------------------------------------- bf16 storage: MFMA kernels
 //
-// The same gradients for bf16 storage on v_mfma_f32_32x32x16_bf16 with fp32 accumulation, one
-// wavefront per workgroup.  The bf16 operands are the stored q, k, v (exact) and dO, P, dS
-// rounded to bf16 where they enter a product, as the reference's autocast backward rounds them.
-// Layouts follow the forward: a 32x32 product tile holds, in lane l, column l % 32 and rows
-// d_row(l, r); the A operand row l % 32 and the B operand column l % 32 carry the K elements
-// 8 * (l / 32) .. + 7.  A product whose K dimension is the rows of an earlier accumulator (dQ^T =
-// K^T dS^T, dK^T = Q^T dS, dV^T = dO^T P) takes that accumulator as its B operand in the
-// accumulator's own row order and reads the A operand with ds_read_b64_tr_b16 from a row-major
-// tile in LDS whose 16-byte pieces p of row r sit at p ^ (r % (HD/8)).
+// The same gradients for bf16 storage on v_mfma_f32_32x32x16_bf16 with fp32 accumulation.  The
+// bf16 operands are the stored q, k, v (exact) and dO, P, dS rounded to bf16 where they enter a
+// product, as the reference's autocast backward rounds them.  Layouts follow the forward: a
+// 32x32 product tile holds, in lane l, column l % 32 and rows d_row(l, r); the A operand row
+// l % 32 and the B operand column l % 32 carry the K elements 8 * (l / 32) .. + 7.  A product
+// whose K dimension is the rows of an earlier accumulator (dQ^T = K^T dS^T, dK^T = Q^T dS,
+// dV^T = dO^T P) takes that accumulator as its B operand in the accumulator's own row order and
+// reads the A operand transposed (ds_read_b64_tr_b16) out of a staged tile.
+//
+// Both kernels run four wavefronts per workgroup over a ring of NSB LDS stages that
+// global->LDS loads fill NSB - 1 tiles ahead of the one in use (f2 layout, bolt3_lds.h; every
+// wavefront issues a quarter of each tile), with one barrier per tile:
+//   attn_bwd_dkv_mfma_kernel, grid (key-block quads, B*HKV, chunks): wavefront w owns key block
+//     4 x + w of the chunk's block list [sinks | slots | previous chunk | own chunk] (32 keys,
+//     its K and V rows in registers, its dK and dV in accumulators); the four share the 32-row
+//     query tiles of the chunk's G heads (q_rope and dO rows, lse and D per row).
+//   attn_bwd_dq_mfma_kernel, grid (query-tile quads, B*HKV, chunks): wavefront w owns the
+//     (query tile, head) pair 4 x + w of the chunk's pairs, tile-major (for G = 4 the four heads
+//     of one tile, whose causal extents agree); the four share the key blocks (K and V rows, the
+//     slot bias).
 constexpr float L2E = 1.4426950408889634f;
+constexpr int NSB = 4;   // LDS stages of the ring
+
+// key block kb of chunk c in the list [sinks | slots | previous chunk | own chunk] (32 keys per
+// block, a field's last block partial): its field and first key; false past the list
+__device__ __forceinline__ bool key_block(const b3_attn_bwd_args& a, int b, int hkv, int c, int kb, KField& f,
+                                          int& j0) {
+  const int n_fields = __popc(field_mask(a, c));
+  for (int fi = 0; fi < n_fields; ++fi) {
+    f = chunk_field<uint16_t>(a, b, hkv, c, fi);
+    const int nb = (f.len + 31) / 32;
+    if (kb < nb) {
+      j0 = 32 * kb;
+      return true;
+    }
+    kb -= nb;
+  }
+  return false;
+}
 
 // accumulator values as the B operand of K chunk kc (rows 8 kc .. 8 kc + 7 of the 16), bf16
 __device__ __forceinline__ u16x8 acc_operand(const f32x16& v, int kc) {
@@ -444,301 +443,183 @@ __device__ __forceinline__ u16x8 acc_operand(const f32x16& v, int kc) {
   return __builtin_bit_cast(u16x8, b);
 }
 
-// 8 fp32 values as bf16 (the dO rows)
-__device__ __forceinline__ u16x8 f32x8_to_bf(const float* p) {
-  const float4 a = *reinterpret_cast<const float4*>(p), b = *reinterpret_cast<const float4*>(p + 4);
-  const u32x4v r = {pack_bf2(a.x, a.y), pack_bf2(a.z, a.w), pack_bf2(b.x, b.y), pack_bf2(b.z, b.w)};
-  return __builtin_bit_cast(u16x8, r);
-}
-
-
-// 16-byte piece p of row r of a [32][HD] tile whose pieces sit at p ^ (r % (HD/8))
-template <int HD>
-__device__ __forceinline__ u16x8 row_piece16(const uint16_t* t, int r, int p) {
-  return *reinterpret_cast<const u16x8*>(&t[r * HD + 8 * (p ^ (r % (HD / 8)))]);
-}
-
-// Scores of key block j0 of field f against the lane's query qi in log2 units (rows keys j0 +
-// d_row(lane, r), the forward's rounding, scale and slot bias), -inf where the key is past the
-// field or after the query in the own chunk.  q0: the first query of the tile.
-__device__ __forceinline__ void block_scores(const b3_attn_bwd_args& a, f32x16& st, const KField& f, int j0, int qi,
-                                             int q0, float sl, int lane) {
-  if (a.score_round) {
-#pragma unroll
-    for (int r = 0; r < 16; r += 2) {
-      const uint32_t u = pack_bf2(st[r], st[r + 1]);
-      st[r] = bf_lo(u);
-      st[r + 1] = bf_hi(u);
-    }
-  }
-  if (f.kind == 1) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) st[r] = fmaf(st[r], sl, f.bias[min(j0 + d_row(lane, r), f.len - 1)] * L2E);
-  } else {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) st[r] *= sl;
-  }
-  if (j0 + 32 > f.len || (f.kind == 3 && j0 + 31 > q0)) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int j = j0 + d_row(lane, r);
-      if (j >= f.len || (f.kind == 3 && j > qi)) st[r] = -INFINITY;
-    }
+template <int N, int I = 0, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<N, I + 1>(f);
   }
 }
 
-template <int HD>
-struct DqMfmaSmem {
-  alignas(16) uint16_t k[32 * HD];   // the key block, row-major, swizzled pieces
-};
-
-// dQ for one 32-query tile of one query head: lane l owns query l % 32 of the tile.
-template <int HD>
-__global__ void __launch_bounds__(64) attn_bwd_dq_mfma_kernel(b3_attn_bwd_args a) {
-  __shared__ DqMfmaSmem<HD> sm;
-  constexpr int KS = HD / 16, NDB = HD / 32, NP = HD / 8;
-  const int lane = threadIdx.x, n = lane & 31, h = lane >> 5;
-  // XCD-aware order: the query tiles and heads of one (kv head, chunk) read the same key and
-  // value blocks
-  const GridPos gp = xcd_grid_pos();
-  const int qt = gp.x, b = gp.y / a.H, hq = gp.y % a.H, c = gp.z;
-  const int G = a.H / a.HKV, hkv = hq / G;
-  const int tc = chunk_len(a, c), q0 = qt * 32;
-  if (q0 >= tc) return;
-  const int nq = min(32, tc - q0);
-  const int qi = q0 + n;                      // this lane's query, index in the chunk
-  const bool qok = qi < tc;
-  const long long t = (long long)c * a.C + qi;
-  const long long row = ((long long)b * a.H + hq) * a.T + t;
-  const float sl = L2E / sqrtf((float)HD);
-  // B operands: the lane's query row and dO row, K elements 16 ks + 8 h ..
-  u16x8 qf[KS], of[KS];
-  {
-    const uint16_t* qr = reinterpret_cast<const uint16_t*>(a.q_rope) + (long long)b * a.q_sb + (long long)hq * a.q_sh +
-                         min(t, (long long)c * a.C + tc - 1) * HD;
-    const uint16_t* dr = reinterpret_cast<const uint16_t*>(a.dy) + (long long)b * a.dy_sb +
-                         min(t, (long long)c * a.C + tc - 1) * a.dy_st + (long long)hq * HD;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      qf[ks] = *reinterpret_cast<const u16x8*>(qr + 16 * ks + 8 * h);
-      of[ks] = *reinterpret_cast<const u16x8*>(dr + 16 * ks + 8 * h);
-      if (!qok) {
-        qf[ks] = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
-        of[ks] = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
-      }
-    }
+// One 32-row tile of [rows][HD] bf16 in the f2 layout: the global->LDS loads of its 8-row x
+// 8-piece blocks blk0 .. blk0 + nblk - 1, row r of the tile from src_row(r) (lane L: row
+// 8 (blk % 4) + L % 8, piece 8 (blk / 4) + L / 8)
+template <int HD, typename RowPtr>
+__device__ __forceinline__ void issue_tile(unsigned char* dst, int blk0, int nblk, int lane, RowPtr src_row) {
+  for (int k = 0; k < nblk; ++k) {
+    const int blk = blk0 + k;
+    const int r = 8 * (blk % (F2_ROWS / 8)) + (lane & 7), pc = 8 * (blk / (F2_ROWS / 8)) + (lane >> 3);
+    lds_dma16(src_row(r) + 8 * pc, dst + F2_BLK * blk);
   }
-  const float drow = qok ? a.d_rows[row] : 0.f;
-  const int n_fields = __popc(field_mask(a, c));
-  const TrLanes<HD> TL(lane);
-  // A operand of K rows: lane row = key l % 32 of the block (rows past the field repeat its last)
-  auto load_rows = [&](const KField& f, int j0, bool v_too, u16x8* ka, u16x8* va) {
-    const int kr = min(j0 + n, f.len - 1);
-    const uint16_t* kp = reinterpret_cast<const uint16_t*>(f.k) + (long long)kr * HD;
-    const uint16_t* vp = reinterpret_cast<const uint16_t*>(f.v) + (long long)kr * HD;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      ka[ks] = *reinterpret_cast<const u16x8*>(kp + 16 * ks + 8 * h);
-      if (v_too) va[ks] = *reinterpret_cast<const u16x8*>(vp + 16 * ks + 8 * h);
-    }
-  };
-  // pass 1: log-sum-exp (log2 units) of the lane's query over all fields (unless the forward
-  // kept it)
-  float m_run = -INFINITY, l_run = 0.f;
-  for (int fi = 0; fi < (a.lse_ready ? 0 : n_fields); ++fi) {
-    const KField f = chunk_field<uint16_t>(a, b, hkv, c, fi);
-    for (int j0 = 0; j0 < f.len; j0 += 32) {
-      if (f.kind == 3 && j0 > q0 + nq - 1) break;
-      u16x8 ka[KS], va[KS];
-      load_rows(f, j0, false, ka, va);
-      f32x16 st = zero16();
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) mma_bf16(st, ka[ks], qf[ks]);
-      block_scores(a, st, f, j0, qi, q0, sl, lane);
-      float bm = -INFINITY;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) bm = fmaxf(bm, st[r]);
-      bm = pair_max32(bm);
-      const float mn = fmaxf(m_run, bm);
-      if (mn == -INFINITY) continue;
-      float ps = 0.f;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) ps += __builtin_amdgcn_exp2f(st[r] - mn);
-      ps = pair_sum32(ps);
-      l_run = l_run * __builtin_amdgcn_exp2f(m_run - mn) + ps;
-      m_run = mn;
-    }
-  }
-  float lse2;
-  if (a.lse_ready) {
-    lse2 = qok ? a.lse[row] * L2E : 0.f;
-  } else {
-    lse2 = m_run + log2f(l_run);
-    if (qok && h == 0) a.lse[row] = lse2 / L2E;
-  }
-  // pass 2: dS block by block; dQ^T += K^T dS^T; the slot bias gradient
-  f32x16 dq[NDB];
-#pragma unroll
-  for (int db = 0; db < NDB; ++db) dq[db] = zero16();
-  const long long bias_row = (((long long)(c - 2) * a.B * a.H + (long long)b * a.H + hq) * a.n_qtiles + qt) * a.S;
-  for (int fi = 0; fi < n_fields; ++fi) {
-    const KField f = chunk_field<uint16_t>(a, b, hkv, c, fi);
-    for (int j0 = 0; j0 < f.len; j0 += 32) {
-      if (f.kind == 3 && j0 > q0 + nq - 1) break;
-      u16x8 ka[KS], va[KS];
-      load_rows(f, j0, true, ka, va);
-      // the key block into LDS for the transposed reads (piece 2 ks + h of row n)
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-        *reinterpret_cast<u16x8*>(&sm.k[n * HD + 8 * ((2 * ks + h) ^ (n % NP))]) = ka[ks];
-      f32x16 st = zero16(), dpt = zero16();
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        mma_bf16(st, ka[ks], qf[ks]);
-        mma_bf16(dpt, va[ks], of[ks]);
-      }
-      block_scores(a, st, f, j0, qi, q0, sl, lane);
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = qok ? __builtin_amdgcn_exp2f(st[r] - lse2) : 0.f;
-        st[r] = p * (dpt[r] - drow);          // dS^T
-      }
-      if (f.kind == 1) {
-        // column sums over the tile's queries: the lanes of each half
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          float v = st[r];
-#pragma unroll
-          for (int o = 16; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-          const int j = j0 + d_row(lane, r);
-          if (n == 0 && j < f.len) a.d_bias[bias_row + j] = v;
-        }
-      }
-#pragma unroll
-      for (int kc = 0; kc < 2; ++kc) {
-        const u16x8 bs = acc_operand(st, kc);
-#pragma unroll
-        for (int db = 0; db < NDB; ++db) mma_bf16(dq[db], tr_operand<HD>(sm.k, TL, db, kc), bs);
-      }
-    }
-  }
-  if (!qok) return;
-  const float scale = 1.0f / sqrtf((float)HD);
-  uint16_t* o = static_cast<uint16_t*>(a.d_q_rope) + row * HD;   // bf16, the storage dtype
-#pragma unroll
-  for (int db = 0; db < NDB; ++db)
-#pragma unroll
-    for (int g = 0; g < 4; ++g)
-      *reinterpret_cast<uint2*>(o + 32 * db + 8 * g + 4 * h) =
-          make_uint2(pack_bf2(dq[db][4 * g] * scale, dq[db][4 * g + 1] * scale),
-                     pack_bf2(dq[db][4 * g + 2] * scale, dq[db][4 * g + 3] * scale));
 }
+
+// The transposed operand (K chunk kc, feature block db) of a staged f2 tile from the eight
+// reads f2_vreads made for that K chunk
+__device__ __forceinline__ u16x8 tr_pair(const u16x4 (&tv)[8], int db) {
+  u16x8 av;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    av[e] = tv[2 * db][e];
+    av[4 + e] = tv[2 * db + 1][e];
+  }
+  return av;
+}
+
+// dkv: eight wavefronts, two per key block of the workgroup's four.  The first of a pair ("P
+// wavefront", w < 4) forms S = Q K^T and P for a query tile, adds dO^T P to dV and leaves P in
+// LDS; the second ("dS wavefront") takes that P one tile later, forms dP = dO V^T and
+// dS = P (dP - D) and adds Q^T dS to dK.  Each holds one of K / V and one of dK / dV, which
+// keeps both within the registers of two wavefronts per SIMD.
+constexpr int NSK = 4;   // LDS stages of the dkv ring (the dS wavefronts use the stage before)
 
 template <int HD>
 struct DkvMfmaSmem {
-  alignas(16) uint16_t q[32 * HD];    // the query tile, row-major, swizzled pieces
-  alignas(16) uint16_t o[32 * HD];    // its dO rows in bf16
-  float lse2[32], drow[32];
+  static constexpr int TB = (HD / 64) * (F2_ROWS / 8) * F2_BLK;   // bytes of one staged tile
+  alignas(16) unsigned char q[NSK][TB];   // the query tile's q_rope rows
+  alignas(16) unsigned char o[NSK][TB];   // its dO rows
+  alignas(16) float ld[NSK][64];          // its rows' lse (natural log), then D
+  alignas(16) float pt[2][4][16 * 64];    // P of each key block, in the accumulator's lane order
 };
 
-// dK, dV for one 32-key block of one field: lane l owns key l % 32; all query rows of the
-// chunk's G heads in 32-row tiles.
 template <int HD>
-__global__ void __launch_bounds__(64) attn_bwd_dkv_mfma_kernel(b3_attn_bwd_args a) {
-  __shared__ DkvMfmaSmem<HD> sm;
-  constexpr int KS = HD / 16, NDB = HD / 32, NP = HD / 8;
-  const int lane = threadIdx.x, n = lane & 31, h = lane >> 5;
-  // XCD-aware order: the key blocks of one (bh, chunk) read the same query and dO rows
+__global__ void __launch_bounds__(512, 1) attn_bwd_dkv_mfma_kernel(b3_attn_bwd_args a) {
+  using Sm = DkvMfmaSmem<HD>;
+  __shared__ Sm sm;
+  constexpr int KS = HD / 16, NDB = HD / 32;
+  constexpr int IPT = Sm::TB / F2_BLK;    // loads per tile
+  constexpr int LPW = 2 * IPT / 8;        // per wavefront per query tile (q_rope and dO)
+  static_assert(LPW * 8 == 2 * IPT && IPT % LPW == 0, "tile loads divide over the wavefronts");
+  const int tid = threadIdx.x, lane = tid & 63, n = lane & 31, h = lane >> 5;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // (wavefront-uniform: scalar branches)
+  const int kbw = w & 3;                                     // the wavefront's key block
+  const bool ds_wave = w >= 4;
+  // XCD-aware order: the key-block quads of one (bh, chunk) read the same query tiles
   const GridPos gp = xcd_grid_pos();
   const int bh = gp.y, b = bh / a.HKV, hkv = bh % a.HKV, c = gp.z;
   const int G = a.H / a.HKV;
   const int tc = chunk_len(a, c);
   const float sl = L2E / sqrtf((float)HD);
-  const int n_fields = __popc(field_mask(a, c));
-  int fi = 0, j0 = gp.x * 32;
-  KField f = chunk_field<uint16_t>(a, b, hkv, c, 0);
-  while (j0 >= f.len) {
-    j0 -= (f.len + 31) / 32 * 32;
-    if (++fi >= n_fields) return;
-    f = chunk_field<uint16_t>(a, b, hkv, c, fi);
+  // the workgroup's four blocks (every wavefront derives all four: uniform decisions), the first
+  // query row any of them needs, and this wavefront's own
+  KField f{};
+  int j0 = 0, q_lo = 1 << 30;
+  bool mine = false, any = false;
+  for (int i = 0; i < 4; ++i) {
+    KField fi;
+    int ji;
+    if (!key_block(a, b, hkv, c, 4 * gp.x + i, fi, ji)) break;
+    any = true;
+    q_lo = min(q_lo, fi.kind == 3 ? ji : 0);
+    if (i == kbw) {
+      f = fi;
+      j0 = ji;
+      mine = true;
+    }
   }
-  const int nk = min(32, f.len - j0);
-  const int j = j0 + n;                       // this lane's key
-  const TrLanes<HD> TL(lane);
-  const bool kval = j < f.len;
-  const float kb2 = f.kind == 1 ? f.bias[min(j, f.len - 1)] * L2E : 0.f;
-  // B operands: the lane's key and value rows
-  u16x8 kf[KS], vf[KS];
-  {
+  if (!any) return;   // the whole workgroup
+  const int qt0 = q_lo / 32, nqt = (tc + 31) / 32 - qt0, n_it = G * nqt;
+  const int j = j0 + n;   // this lane's key
+  const bool kval = mine && j < f.len;
+  const float kb2 = (mine && f.kind == 1) ? f.bias[min(j, f.len - 1)] * L2E : 0.f;
+  // B operands: the lane's key row (P wavefronts) or value row (dS wavefronts), 16 ks + 8 h ..
+  u16x8 kv[KS];
+  if (mine) {
     const int kr = min(j, f.len - 1);
-    const uint16_t* kp = reinterpret_cast<const uint16_t*>(f.k) + (long long)kr * HD;
-    const uint16_t* vp = reinterpret_cast<const uint16_t*>(f.v) + (long long)kr * HD;
+    const uint16_t* p = reinterpret_cast<const uint16_t*>(ds_wave ? f.v : f.k) + (long long)kr * HD;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      kf[ks] = *reinterpret_cast<const u16x8*>(kp + 16 * ks + 8 * h);
-      vf[ks] = *reinterpret_cast<const u16x8*>(vp + 16 * ks + 8 * h);
-    }
+    for (int ks = 0; ks < KS; ++ks) kv[ks] = *reinterpret_cast<const u16x8*>(p + 16 * ks + 8 * h);
   }
-  f32x16 dk[NDB], dv[NDB];
-#pragma unroll
-  for (int db = 0; db < NDB; ++db) {
-    dk[db] = zero16();
-    dv[db] = zero16();
-  }
-  // the tiles this block needs: all 32-row query tiles of the G heads, for the own chunk's keys
-  // only those from the block's first key on (earlier queries precede every key of the block);
-  // tile it + 1's rows are loaded into registers while tile it's products run
-  const int q_start = f.kind == 3 ? j0 : 0;
-  const int nqt = (tc - q_start + 31) / 32, n_it = G * nqt;
-  u16x8 nqv[KS], nov[KS];
-  float nls = INFINITY, ndr = 0.f;
-  auto fetch = [&](int it) {
-    const int hq = hkv * G + it / nqt, q0 = q_start + 32 * (it % nqt);
-    const bool ok = q0 + n < tc;
-    const long long t = (long long)c * a.C + min(q0 + n, tc - 1);
-    const uint16_t* qp = reinterpret_cast<const uint16_t*>(a.q_rope) + (long long)b * a.q_sb + (long long)hq * a.q_sh +
-                         t * HD;
-    const uint16_t* dp = reinterpret_cast<const uint16_t*>(a.dy) + (long long)b * a.dy_sb + t * a.dy_st +
-                         (long long)hq * HD;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      nqv[ks] = ok ? *reinterpret_cast<const u16x8*>(qp + 16 * ks + 8 * h) : u16x8{0, 0, 0, 0, 0, 0, 0, 0};
-      nov[ks] = ok ? *reinterpret_cast<const u16x8*>(dp + 16 * ks + 8 * h) : u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+  const uint16_t* qr_base = reinterpret_cast<const uint16_t*>(a.q_rope) + (long long)b * a.q_sb;
+  const uint16_t* dy_base = reinterpret_cast<const uint16_t*>(a.dy) + (long long)b * a.dy_sb;
+  // the loads of query tile it into stage it % NSK: wavefront w issues loads w LPW .. of the
+  // tile's 2 IPT (q_rope blocks, then dO blocks); wavefront 0 also the 32 rows' lse and D
+  auto issue = [&](int it) {
+    const int st = it % NSK, hq = hkv * G + it / nqt, q0 = 32 * (qt0 + it % nqt);
+    const long long t0 = (long long)c * a.C;
+    if (w * LPW < IPT) {
+      const uint16_t* qb = qr_base + (long long)hq * a.q_sh;
+      issue_tile<HD>(sm.q[st], w * LPW, LPW, lane,
+                     [&](int r) { return qb + (t0 + min(q0 + r, tc - 1)) * HD; });
+    } else {
+      const uint16_t* ob = dy_base + (long long)hq * HD;
+      issue_tile<HD>(sm.o[st], w * LPW - IPT, LPW, lane,
+                     [&](int r) { return ob + (t0 + min(q0 + r, tc - 1)) * a.dy_st; });
     }
-    if (h == 0) {
-      const long long row = ((long long)b * a.H + hq) * a.T + t;
-      nls = ok ? a.lse[row] * L2E : INFINITY;
-      ndr = ok ? a.d_rows[row] : 0.f;
+    if (w == 0) {
+      const long long row = ((long long)b * a.H + hq) * a.T + t0 + min(q0 + n, tc - 1);
+      lds_dma4((h == 0 ? a.lse : a.d_rows) + row, sm.ld[st]);
     }
   };
-  auto put = [&]() {   // the fetched tile into LDS (row n, piece 2 ks + h)
+  const int my_lpt = LPW + (w == 0 ? 1 : 0);
+  for (int i = 0; i < min(NSK - 2, n_it); ++i) issue(i);
+
+  // dV (P wavefronts) or dK (dS wavefronts) of the block: rows features, columns keys
+  f32x16 acc[NDB];
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const int slot = 8 * ((2 * ks + h) ^ (n % NP));
-      *reinterpret_cast<u16x8*>(&sm.q[n * HD + slot]) = nqv[ks];
-      *reinterpret_cast<u16x8*>(&sm.o[n * HD + slot]) = nov[ks];
+  for (int db = 0; db < NDB; ++db) acc[db] = zero16();
+  // per-lane LDS bases: row reads (row n, piece 2 ks + h), transposed reads, the P exchange
+  const int jv = lane & 15, grp = lane >> 4;
+  const uint32_t lane_row = f2_off(n, h);
+  const uint32_t lane_tr = f2_off(4 * h + (jv >> 2), 2 * (grp & 1) + ((jv >> 1) & 1)) + 8 * (jv & 1);
+  // the P wavefront takes tile it, the dS wavefront tile it - 1 (whose P the barrier at the top
+  // of this iteration has published)
+  for (int it = 0; it <= n_it; ++it) {
+    if (it < n_it) wait_vm_rt(min(NSK - 3, n_it - 1 - it) * my_lpt);
+    sync_lds();   // tile it is in LDS; tile it - 2's stage is free
+    if (it + NSK - 2 < n_it) issue(it + NSK - 2);
+    const int ti = ds_wave ? it - 1 : it;
+    if (ti < 0 || ti >= n_it || !mine) continue;
+    const int st = ti % NSK, q0 = 32 * (qt0 + ti % nqt);
+    if (f.kind == 3 && q0 + 31 < j0) continue;   // every query precedes every key
+    const uint32_t qa = lds_addr(sm.q[st]), oa = lds_addr(sm.o[st]);
+    const uint32_t pa = lds_addr(sm.pt[ti & 1][kbw]) + 16 * lane;
+    const uint32_t la = lds_addr(sm.ld[st]) + 16 * h;
+    // S = Q K^T (P wavefront) or dP = dO V^T (dS wavefront): rows queries, columns the keys
+    const uint32_t ra = (ds_wave ? oa : qa) + lane_row;
+    f32x16 s = zero16();
+    static_for<KS / 2>([&](auto ic) {
+      constexpr int k2 = decltype(ic)::value;
+      u16x8 v0 = lds_read_b128_at<f2_off(0, 4 * k2)>(ra);
+      u16x8 v1 = lds_read_b128_at<f2_off(0, 4 * k2 + 2)>(ra);
+      lds_wait2(v0, v1);
+      mma_bf16(s, v0, kv[2 * k2]);
+      mma_bf16(s, v1, kv[2 * k2 + 1]);
+    });
+    // the first K chunk's transposed operand (dO^T for dV, Q^T for dK) and the rows' lse / D
+    // (and P), read while the products finish
+    const uint32_t ta = (ds_wave ? qa : oa) + lane_tr;
+    u16x4 tv[8];
+    f2_vreads<NDB, 0>(tv, ta);
+    fx4 rs[4], pv[4];
+    if (!ds_wave) {
+      rs[0] = lds_read_f4_at<0>(la);
+      rs[1] = lds_read_f4_at<32>(la);
+      rs[2] = lds_read_f4_at<64>(la);
+      rs[3] = lds_read_f4_at<96>(la);
+    } else {
+      rs[0] = lds_read_f4_at<128>(la);
+      rs[1] = lds_read_f4_at<160>(la);
+      rs[2] = lds_read_f4_at<192>(la);
+      rs[3] = lds_read_f4_at<224>(la);
+      pv[0] = lds_read_f4_at<0>(pa);
+      pv[1] = lds_read_f4_at<1024>(pa);
+      pv[2] = lds_read_f4_at<2048>(pa);
+      pv[3] = lds_read_f4_at<3072>(pa);
+      lds_wait4(pv[0], pv[1], pv[2], pv[3]);
     }
-    if (h == 0) {
-      sm.lse2[n] = nls;
-      sm.drow[n] = ndr;
-    }
-  };
-  if (n_it > 0) {
-    fetch(0);
-    put();
-  }
-  for (int it = 0; it < n_it; ++it) {
-    {
-      if (it + 1 < n_it) fetch(it + 1);
-      const int q0 = q_start + 32 * (it % nqt);
-      // S = Q K^T and dP = dO V^T: rows queries (A operand from the tile rows), columns keys
-      f32x16 s = zero16(), dp = zero16();
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const int slot = 8 * ((2 * ks + h) ^ (n % NP));
-        mma_bf16(s, *reinterpret_cast<const u16x8*>(&sm.q[n * HD + slot]), kf[ks]);
-        mma_bf16(dp, *reinterpret_cast<const u16x8*>(&sm.o[n * HD + slot]), vf[ks]);
-      }
+    lds_wait4(rs[0], rs[1], rs[2], rs[3]);
+    lds_wait8(tv);
+    if (!ds_wave) {
       if (a.score_round) {
 #pragma unroll
         for (int r = 0; r < 16; r += 2) {
@@ -751,64 +632,250 @@ __global__ void __launch_bounds__(64) attn_bwd_dkv_mfma_kernel(b3_attn_bwd_args 
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int qr = d_row(lane, r);
-        const bool on = kval && !(causal && j > q0 + qr);
-        const float p = on ? __builtin_amdgcn_exp2f(fmaf(s[r], sl, kb2) - sm.lse2[qr]) : 0.f;
-        s[r] = p;
-        dp[r] = p * (dp[r] - sm.drow[qr]);     // dS
+        const bool on = kval && q0 + qr < tc && !(causal && j > q0 + qr);
+        s[r] = on ? __builtin_amdgcn_exp2f(fmaf(s[r], sl, kb2) - rs[r >> 2][r & 3] * L2E) : 0.f;
       }
+      // P for the dS wavefront
 #pragma unroll
-      for (int kc = 0; kc < 2; ++kc) {
-        const u16x8 bp = acc_operand(s, kc), bs = acc_operand(dp, kc);
+      for (int r4 = 0; r4 < 4; ++r4) {
+        fx4 v;
 #pragma unroll
-        for (int db = 0; db < NDB; ++db) {
-          mma_bf16(dv[db], tr_operand<HD>(sm.o, TL, db, kc), bp);
-          mma_bf16(dk[db], tr_operand<HD>(sm.q, TL, db, kc), bs);
-        }
+        for (int e = 0; e < 4; ++e) v[e] = s[4 * r4 + e];
+        lds_write_f4(pa + 1024 * r4, v);
       }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[r] = pv[r >> 2][r & 3] * (s[r] - rs[r >> 2][r & 3]);   // dS
     }
-    if (it + 1 < n_it) put();   // after this tile's LDS reads (one wavefront: LDS in order)
+    // dV^T += dO^T P or dK^T += Q^T dS (K = the tile's rows)
+    {
+      const u16x8 bp = acc_operand(s, 0);
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) mma_bf16(acc[db], tr_pair(tv, db), bp);
+    }
+    f2_vreads<NDB, 1>(tv, ta);
+    lds_wait8(tv);
+    {
+      const u16x8 bp = acc_operand(s, 1);
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) mma_bf16(acc[db], tr_pair(tv, db), bp);
+    }
   }
-  if (n >= nk) return;
-  const float scale = 1.0f / sqrtf((float)HD);
+  if (!mine || n >= min(32, f.len - j0)) return;
+  const float scale = ds_wave ? 1.0f / sqrtf((float)HD) : 1.0f;
   const long long HDl = HD;
   if (f.kind >= 2) {
     // token rows: bf16, the storage dtype
     const long long o = ((long long)bh * a.T + (long long)(f.kind == 2 ? c - 1 : c) * a.C + j) * HDl;
-    uint16_t* ok = static_cast<uint16_t*>(f.kind == 2 ? a.d_k_next : a.d_k_own) + o;
-    uint16_t* ov = static_cast<uint16_t*>(f.kind == 2 ? a.d_v_next : a.d_v_own) + o;
+    uint16_t* out = static_cast<uint16_t*>(ds_wave ? (f.kind == 2 ? a.d_k_next : a.d_k_own)
+                                                   : (f.kind == 2 ? a.d_v_next : a.d_v_own)) + o;
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
 #pragma unroll
       for (int g4 = 0; g4 < 4; ++g4) {
         const int d0 = 32 * db + 8 * g4 + 4 * h;
-        *reinterpret_cast<uint2*>(ok + d0) = make_uint2(pack_bf2(dk[db][4 * g4] * scale, dk[db][4 * g4 + 1] * scale),
-                                                        pack_bf2(dk[db][4 * g4 + 2] * scale, dk[db][4 * g4 + 3] * scale));
-        *reinterpret_cast<uint2*>(ov + d0) =
-            make_uint2(pack_bf2(dv[db][4 * g4], dv[db][4 * g4 + 1]), pack_bf2(dv[db][4 * g4 + 2], dv[db][4 * g4 + 3]));
+        *reinterpret_cast<uint2*>(out + d0) =
+            make_uint2(pack_bf2(acc[db][4 * g4] * scale, acc[db][4 * g4 + 1] * scale),
+                       pack_bf2(acc[db][4 * g4 + 2] * scale, acc[db][4 * g4 + 3] * scale));
       }
     return;
   }
   // sinks and slots: fp32 (the chain's backward sums them further)
-  float *ok, *ov;
+  float* out;
   if (f.kind == 0) {
     const long long o = (((long long)c * a.B * a.HKV + bh) * a.n_sinks + j) * HDl;
-    ok = a.d_sink_k + o;
-    ov = a.d_sink_v + o;
+    out = (ds_wave ? a.d_sink_k : a.d_sink_v) + o;
   } else {
     const long long o = (((long long)(c - 2) * a.B * a.HKV + bh) * a.S + j) * HDl;
-    ok = a.d_slot_k + o;
-    ov = a.d_slot_v + o;
+    out = (ds_wave ? a.d_slot_k : a.d_slot_v) + o;
   }
 #pragma unroll
   for (int db = 0; db < NDB; ++db)
 #pragma unroll
     for (int g4 = 0; g4 < 4; ++g4) {
       const int d0 = 32 * db + 8 * g4 + 4 * h;
-      *reinterpret_cast<float4*>(ok + d0) = make_float4(dk[db][4 * g4] * scale, dk[db][4 * g4 + 1] * scale,
-                                                        dk[db][4 * g4 + 2] * scale, dk[db][4 * g4 + 3] * scale);
-      *reinterpret_cast<float4*>(ov + d0) =
-          make_float4(dv[db][4 * g4], dv[db][4 * g4 + 1], dv[db][4 * g4 + 2], dv[db][4 * g4 + 3]);
+      *reinterpret_cast<float4*>(out + d0) = make_float4(acc[db][4 * g4] * scale, acc[db][4 * g4 + 1] * scale,
+                                                         acc[db][4 * g4 + 2] * scale, acc[db][4 * g4 + 3] * scale);
     }
+}
+
+template <int HD>
+struct DqMfmaSmem {
+  static constexpr int TB = (HD / 64) * (F2_ROWS / 8) * F2_BLK;   // bytes of one staged tile
+  alignas(16) unsigned char k[NSB][TB];   // the key block's K rows
+  alignas(16) unsigned char v[NSB][TB];   // its V rows
+  alignas(16) float bias[NSB][64];        // slot blocks: the 32 keys' bias (twice)
+};
+
+template <int HD>
+__global__ void __launch_bounds__(256, 2) attn_bwd_dq_mfma_kernel(b3_attn_bwd_args a) {
+  using Sm = DqMfmaSmem<HD>;
+  __shared__ Sm sm;
+  constexpr int KS = HD / 16, NDB = HD / 32;
+  constexpr int IPT = Sm::TB / F2_BLK;
+  constexpr int LPW = 2 * IPT / 4;
+  static_assert(LPW * 4 == 2 * IPT && IPT % LPW == 0, "tile loads divide over the wavefronts");
+  const int tid = threadIdx.x, lane = tid & 63, n = lane & 31, h = lane >> 5;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // (wavefront-uniform: scalar branches)
+  // XCD-aware order: the query-tile quads of one (bh, chunk) read the same key blocks
+  const GridPos gp = xcd_grid_pos();
+  const int bh = gp.y, b = bh / a.HKV, hkv = bh % a.HKV, c = gp.z;
+  const int G = a.H / a.HKV;
+  const int tc = chunk_len(a, c), nqt = (tc + 31) / 32;
+  const int n_pairs = G * nqt;
+  if (4 * gp.x >= n_pairs) return;   // the whole workgroup
+  // this wavefront's (query tile, head) pair and the workgroup's last query row
+  const int pair = 4 * gp.x + w;
+  const bool mine = pair < n_pairs;
+  const int qt = mine ? pair / G : 0, g = mine ? pair % G : 0;
+  const int q_hi = min(tc - 1, 32 * ((min(n_pairs, 4 * gp.x + 4) - 1) / G) + 31);
+  const int hq = hkv * G + g, q0 = 32 * qt;
+  const int qi = q0 + n;   // this lane's query
+  const bool qok = mine && qi < tc;
+  const long long t = (long long)c * a.C + min(qi, tc - 1);
+  const long long row = ((long long)b * a.H + hq) * a.T + t;
+  const float sl = L2E / sqrtf((float)HD);
+  // B operands: the lane's query row and dO row; its lse (log2 units) and D
+  u16x8 qf[KS], of[KS];
+  {
+    const uint16_t* qr = reinterpret_cast<const uint16_t*>(a.q_rope) + (long long)b * a.q_sb + (long long)hq * a.q_sh +
+                         t * HD;
+    const uint16_t* dr = reinterpret_cast<const uint16_t*>(a.dy) + (long long)b * a.dy_sb + t * a.dy_st + (long long)hq * HD;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      qf[ks] = *reinterpret_cast<const u16x8*>(qr + 16 * ks + 8 * h);
+      of[ks] = *reinterpret_cast<const u16x8*>(dr + 16 * ks + 8 * h);
+    }
+  }
+  const float lse2 = a.lse[row] * L2E, drow = a.d_rows[row];
+  // key blocks: every block of the fields before the own chunk, the own chunk's up to q_hi
+  int n_blk = 0;
+  {
+    const int n_fields = __popc(field_mask(a, c));
+    for (int fi = 0; fi < n_fields; ++fi) {
+      const KField f = chunk_field<uint16_t>(a, b, hkv, c, fi);
+      n_blk += f.kind == 3 ? q_hi / 32 + 1 : (f.len + 31) / 32;
+    }
+  }
+  // the loads of key block kb into stage kb % NSB: wavefront w issues loads w LPW .. of the
+  // block's 2 IPT (K blocks, then V blocks); wavefront 0 also the slot bias (any valid address
+  // for the other fields)
+  auto issue = [&](int kb) {
+    const int st = kb % NSB;
+    KField f;
+    int j0;
+    key_block(a, b, hkv, c, kb, f, j0);
+    const int last = f.len - 1;
+    if (w * LPW < IPT) {
+      const uint16_t* kp = reinterpret_cast<const uint16_t*>(f.k);
+      issue_tile<HD>(sm.k[st], w * LPW, LPW, lane, [&](int r) { return kp + (long long)min(j0 + r, last) * HD; });
+    } else {
+      const uint16_t* vp = reinterpret_cast<const uint16_t*>(f.v);
+      issue_tile<HD>(sm.v[st], w * LPW - IPT, LPW, lane,
+                     [&](int r) { return vp + (long long)min(j0 + r, last) * HD; });
+    }
+    if (w == 0) lds_dma4(f.kind == 1 ? f.bias + min(j0 + n, last) : a.lse, sm.bias[st]);
+  };
+  const int my_lpt = LPW + (w == 0 ? 1 : 0);
+  for (int i = 0; i < min(NSB - 1, n_blk); ++i) issue(i);
+
+  f32x16 dq[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) dq[db] = zero16();
+  const int jv = lane & 15, grp = lane >> 4;
+  const uint32_t lane_row = f2_off(n, h);
+  const uint32_t lane_tr = f2_off(4 * h + (jv >> 2), 2 * (grp & 1) + ((jv >> 1) & 1)) + 8 * (jv & 1);
+  const long long bias_row = (((long long)(c - 2) * a.B * a.H + (long long)b * a.H + hq) * a.n_qtiles + qt) * a.S;
+  for (int kb = 0; kb < n_blk; ++kb) {
+    wait_vm_rt(min(NSB - 2, n_blk - 1 - kb) * my_lpt);
+    sync_lds();   // block kb is in LDS; every wavefront is done with block kb - 1, whose stage is refilled
+    if (kb + NSB - 1 < n_blk) issue(kb + NSB - 1);
+    KField f;
+    int j0;
+    key_block(a, b, hkv, c, kb, f, j0);
+    if (!mine || (f.kind == 3 && j0 > q0 + 31)) continue;   // every key follows every query
+    const int st = kb % NSB;
+    const uint32_t ka = lds_addr(sm.k[st]), va = lds_addr(sm.v[st]);
+    // S^T = K Q^T and dP^T = V dO^T: rows the block's keys, columns the wavefront's queries
+    f32x16 s = zero16(), dp = zero16();
+    static_for<KS / 2>([&](auto ic) {
+      constexpr int k2 = decltype(ic)::value;
+      u16x8 k0v = lds_read_b128_at<f2_off(0, 4 * k2)>(ka + lane_row);
+      u16x8 v0v = lds_read_b128_at<f2_off(0, 4 * k2)>(va + lane_row);
+      u16x8 k1v = lds_read_b128_at<f2_off(0, 4 * k2 + 2)>(ka + lane_row);
+      u16x8 v1v = lds_read_b128_at<f2_off(0, 4 * k2 + 2)>(va + lane_row);
+      lds_wait2(k0v, v0v);
+      lds_wait2(k1v, v1v);
+      mma_bf16(s, k0v, qf[2 * k2]);
+      mma_bf16(dp, v0v, of[2 * k2]);
+      mma_bf16(s, k1v, qf[2 * k2 + 1]);
+      mma_bf16(dp, v1v, of[2 * k2 + 1]);
+    });
+    // K^T for the first K chunk and the bias, read while the scores are formed
+    u16x4 tk[8];
+    f2_vreads<NDB, 0>(tk, ka + lane_tr);
+    fx4 bv[4];
+    if (f.kind == 1) {
+      const uint32_t ba = lds_addr(sm.bias[st]) + 16 * h;
+      bv[0] = lds_read_f4_at<0>(ba);
+      bv[1] = lds_read_f4_at<32>(ba);
+      bv[2] = lds_read_f4_at<64>(ba);
+      bv[3] = lds_read_f4_at<96>(ba);
+      lds_wait4(bv[0], bv[1], bv[2], bv[3]);
+    }
+    lds_wait8(tk);
+    if (a.score_round) {
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) {
+        const uint32_t u = pack_bf2(s[r], s[r + 1]);
+        s[r] = bf_lo(u);
+        s[r + 1] = bf_hi(u);
+      }
+    }
+    const bool edge = j0 + 32 > f.len || (f.kind == 3 && j0 + 31 > q0);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int jj = j0 + d_row(lane, r);
+      float x = f.kind == 1 ? fmaf(s[r], sl, bv[r >> 2][r & 3] * L2E) : s[r] * sl;
+      if (edge && (jj >= f.len || (f.kind == 3 && jj > qi))) x = -INFINITY;
+      const float p = qok ? __builtin_amdgcn_exp2f(x - lse2) : 0.f;
+      s[r] = p * (dp[r] - drow);   // dS^T
+    }
+    if (f.kind == 1) {
+      // the slot bias gradient: column sums over the wavefront's queries (the lanes of each half)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float v = s[r];
+#pragma unroll
+        for (int o = 16; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+        const int jj = j0 + d_row(lane, r);
+        if (n == 0 && jj < f.len) a.d_bias[bias_row + jj] = v;
+      }
+    }
+    // dQ^T += K^T dS^T (K = the block's keys)
+    {
+      const u16x8 bs = acc_operand(s, 0);
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) mma_bf16(dq[db], tr_pair(tk, db), bs);
+    }
+    f2_vreads<NDB, 1>(tk, ka + lane_tr);
+    lds_wait8(tk);
+    {
+      const u16x8 bs = acc_operand(s, 1);
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) mma_bf16(dq[db], tr_pair(tk, db), bs);
+    }
+  }
+  if (!qok) return;
+  const float scale = 1.0f / sqrtf((float)HD);
+  uint16_t* o = static_cast<uint16_t*>(a.d_q_rope) + row * HD;   // bf16, the storage dtype
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4)
+      *reinterpret_cast<uint2*>(o + 32 * db + 8 * g4 + 4 * h) =
+          make_uint2(pack_bf2(dq[db][4 * g4] * scale, dq[db][4 * g4 + 1] * scale),
+                     pack_bf2(dq[db][4 * g4 + 2] * scale, dq[db][4 * g4 + 3] * scale));
 }
 
 template <int HD>
@@ -1354,12 +1421,14 @@ static int launch(const b3_attn_bwd_args& a, hipStream_t st) {
     e = hipGetLastError();
     if (e != hipSuccess || a.part == 1) return (int)e;
   }
-  const int max_blocks = 1 + (a.S + 31) / 32 + 2 * ((a.C + 31) / 32);
+  // key blocks per chunk at most: sinks, slots, previous and own chunk
+  const int max_blocks = (min(a.n_sinks, a.C) + 31) / 32 + (a.S + 31) / 32 + 2 * ((a.C + 31) / 32);
   if constexpr (St<T>::is_bf16) {
-    hipLaunchKernelGGL((attn_bwd_dq_mfma_kernel<HD>), dim3((a.C + 31) / 32, a.B * a.H, n_chunks), dim3(64), 0, st, a);
+    const int n_pairs = (a.H / a.HKV) * ((a.C + 31) / 32);
+    hipLaunchKernelGGL((attn_bwd_dq_mfma_kernel<HD>), dim3((n_pairs + 3) / 4, BH, n_chunks), dim3(256), 0, st, a);
     e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
-    hipLaunchKernelGGL((attn_bwd_dkv_mfma_kernel<HD>), dim3(max_blocks, BH, n_chunks), dim3(64), 0, st, a);
+    hipLaunchKernelGGL((attn_bwd_dkv_mfma_kernel<HD>), dim3((max_blocks + 3) / 4, BH, n_chunks), dim3(512), 0, st, a);
     return (int)hipGetLastError();
   } else {
     hipLaunchKernelGGL((attn_bwd_dq_kernel<T, HD>), dim3((a.C + BQ - 1) / BQ, a.B * a.H, n_chunks), dim3(NT),
@@ -1409,7 +1478,7 @@ extern "C" int bolt3_attn_bwd(const b3_attn_bwd_args* a, void* stream) {
                          a->slot_step < (int64_t)a->B * a->HKV * a->S * a->HD))
     return B3_ERR_ARG;
   if (a->m_split && a->dtype != B3_BF16) return B3_ERR_ARG;
-  if (a->part < 0 || a->part > 2 || (a->lse_ready != 0 && a->lse_ready != 1)) return B3_ERR_ARG;
+  if (a->part < 0 || a->part > 2) return B3_ERR_ARG;
   // 16-byte rows: every (b, h, t) row of the staged operands
   const int64_t es = a->dtype == B3_BF16 ? 2 : 4;
   if ((a->q_sb * es) % 16 || (a->q_sh * es) % 16 || (a->w_sb * es) % 16 || (a->w_sh * es) % 16 ||

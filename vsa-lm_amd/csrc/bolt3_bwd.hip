@@ -435,6 +435,22 @@ __device__ __forceinline__ bool key_block(const b3_attn_bwd_args& a, int b, int 
   return false;
 }
 
+// A walk over a chunk's key blocks in list order (the block's field and first key), one block
+// per step
+struct BlockCursor {
+  KField f;
+  int fi, j0;
+  __device__ __forceinline__ BlockCursor(const b3_attn_bwd_args& a, int b, int hkv, int c)
+      : f(chunk_field<uint16_t>(a, b, hkv, c, 0)), fi(0), j0(0) {}
+  __device__ __forceinline__ void next(const b3_attn_bwd_args& a, int b, int hkv, int c) {
+    j0 += 32;
+    if (j0 >= f.len && fi + 1 < __popc(field_mask(a, c))) {
+      j0 = 0;
+      f = chunk_field<uint16_t>(a, b, hkv, c, ++fi);
+    }
+  }
+};
+
 // accumulator values as the B operand of K chunk kc (rows 8 kc .. 8 kc + 7 of the 16), bf16
 __device__ __forceinline__ u16x8 acc_operand(const f32x16& v, int kc) {
   u32x4v b;
@@ -760,12 +776,11 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_dq_mfma_kernel(b3_attn_bwd_ar
   // the loads of key block kb into stage kb % NSB: wavefront w issues loads w LPW .. of the
   // block's 2 IPT (K blocks, then V blocks); wavefront 0 also the slot bias (any valid address
   // for the other fields)
+  BlockCursor icur(a, b, hkv, c);   // the next block to issue
   auto issue = [&](int kb) {
     const int st = kb % NSB;
-    KField f;
-    int j0;
-    key_block(a, b, hkv, c, kb, f, j0);
-    const int last = f.len - 1;
+    const KField& f = icur.f;
+    const int j0 = icur.j0, last = f.len - 1;
     if (w * LPW < IPT) {
       const uint16_t* kp = reinterpret_cast<const uint16_t*>(f.k);
       issue_tile<HD>(sm.k[st], w * LPW, LPW, lane, [&](int r) { return kp + (long long)min(j0 + r, last) * HD; });
@@ -775,6 +790,7 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_dq_mfma_kernel(b3_attn_bwd_ar
                      [&](int r) { return vp + (long long)min(j0 + r, last) * HD; });
     }
     if (w == 0) lds_dma4(f.kind == 1 ? f.bias + min(j0 + n, last) : a.lse, sm.bias[st]);
+    icur.next(a, b, hkv, c);
   };
   const int my_lpt = LPW + (w == 0 ? 1 : 0);
   for (int i = 0; i < min(NSB - 1, n_blk); ++i) issue(i);
@@ -786,13 +802,14 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_dq_mfma_kernel(b3_attn_bwd_ar
   const uint32_t lane_row = f2_off(n, h);
   const uint32_t lane_tr = f2_off(4 * h + (jv >> 2), 2 * (grp & 1) + ((jv >> 1) & 1)) + 8 * (jv & 1);
   const long long bias_row = (((long long)(c - 2) * a.B * a.H + (long long)b * a.H + hq) * a.n_qtiles + qt) * a.S;
+  BlockCursor ccur(a, b, hkv, c);   // the block computed
   for (int kb = 0; kb < n_blk; ++kb) {
     wait_vm_rt(min(NSB - 2, n_blk - 1 - kb) * my_lpt);
     sync_lds();   // block kb is in LDS; every wavefront is done with block kb - 1, whose stage is refilled
     if (kb + NSB - 1 < n_blk) issue(kb + NSB - 1);
-    KField f;
-    int j0;
-    key_block(a, b, hkv, c, kb, f, j0);
+    if (kb > 0) ccur.next(a, b, hkv, c);
+    const KField& f = ccur.f;
+    const int j0 = ccur.j0;
     if (!mine || (f.kind == 3 && j0 > q0 + 31)) continue;   // every key follows every query
     const int st = kb % NSB;
     const uint32_t ka = lds_addr(sm.k[st]), va = lds_addr(sm.v[st]);

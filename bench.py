@@ -94,13 +94,17 @@ def bench_backward(mod, dev, steps, warmup):
     _abi.set_timing(False)
     mod.zero_grad(set_to_none=True)
     ms = (t1 - t0) * 1e3 / steps
+    # per backward: the sum over the entry point's calls (the attention backward runs as two
+    # calls, the readout's and the attention's; the chain backward as four, one per kernel, the
+    # M_res recursion on a side stream)
     bwd = kt.get("bolt3_attn_bwd", [])
-    bwd_ms = sum(bwd) / max(1, len(bwd))
+    bwd_ms = sum(bwd) / steps
     cb = kt.get("bolt3_chain_bwd", [])
     fl = backward_flops(B, T)
     # bf16 storage: the attention and readout gradients run on bf16 MFMA
     return dict(ms_per_forward_backward=round(ms, 3), tokens_per_s=round(B * T / (ms * 1e-3), 1),
-                attn_bwd_ms=round(bwd_ms, 3), chain_bwd_ms=round(sum(cb) / max(1, len(cb)), 3),
+                attn_bwd_ms=round(bwd_ms, 3), attn_bwd_calls=len(bwd) // steps,
+                chain_bwd_ms=round(sum(cb) / steps, 3), chain_bwd_calls=len(cb) // steps,
                 roofline=dict(bound="mfma", kernel="bolt3_attn_bwd", flops=fl,
                               achieved=round(fl / (bwd_ms * 1e-3) / 1e12, 2), peak=PEAK_BF16 / 1e12, unit="TFLOP/s",
                               frac=round(fl / (bwd_ms * 1e-3) / PEAK_BF16, 4)))

@@ -961,16 +961,6 @@ __global__ void __launch_bounds__(64 * PNW, 2) rowproj_kernel(ProjArgs p) {
   const int nst = min(PKS, (p.K - kc0) >> 5);      // K steps in this chunk
   const int r = lane & 15, kg = lane >> 4;
   const bool live = nt * 16 < p.N;
-  // W rows first: all steps of the chunk; steps past the chunk multiply a zero operand
-  u16x8 wa[PKS];
-  if (live) {
-    const uint16_t* wrow = p.w + (long long)(nt * 16 + r) * p.K + kc0 + 8 * kg;
-#pragma unroll
-    for (int i = 0; i < PKS; ++i) wa[i] = *reinterpret_cast<const u16x8*>(wrow + 32 * min(i, nst - 1));
-#pragma unroll
-    for (int i = 0; i < PKS; ++i)
-      if (i >= nst) wa[i] = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
-  }
   // x rows m0 .. m0+63 of the chunk, one 1 KB row per global->LDS load (lane: 8 columns);
   // rows past M repeat row M - 1 and columns past K repeat the last 8 (both multiply zeros
   // or are never stored)
@@ -980,9 +970,20 @@ __global__ void __launch_bounds__(64 * PNW, 2) rowproj_kernel(ProjArgs p) {
     const uint16_t* src = p.x + (long long)min(m0 + m, p.M - 1) * p.x_rs + min(kc0 + 8 * lane, p.K - 8);
     __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(xs + m * PXS), 16, 0, 0);
   }
+  // the W rows: all steps of the chunk, in flight together with the x loads (steps past the
+  // chunk re-read its last step and multiply a zero operand, set once everything has arrived)
+  u16x8 wa[PKS];
+  if (live) {
+    const uint16_t* wrow = p.w + (long long)(nt * 16 + r) * p.K + kc0 + 8 * kg;
+#pragma unroll
+    for (int i = 0; i < PKS; ++i) wa[i] = *reinterpret_cast<const u16x8*>(wrow + 32 * min(i, nst - 1));
+  }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (!live) return;
+#pragma unroll
+  for (int i = 0; i < PKS; ++i)
+    if (i >= nst) wa[i] = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
   f32x4 acc[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};

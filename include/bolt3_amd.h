@@ -548,6 +548,10 @@ typedef struct {
   int32_t dz_cols;            /* >= (H + 2 HKV) HD + HKV + H; the columns past those are zeroed */
   float* d_qn_w;              /* out: [bolt3_heads_bwd_blocks(B, T)][HD] partial sums (has_qk_norm) */
   float* d_kn_w;
+  int32_t parts;              /* 0: everything; 1: the query heads, the eta columns and d_qn_w (reads
+                                 neither the chain's nor the keys' gradients); 2: the key / value heads,
+                                 the beta columns, the pad and d_kn_w.  Parts 1 and 2 write disjoint
+                                 columns and may run on different streams */
 } b3_heads_bwd_args;
 int bolt3_heads_bwd(const b3_heads_bwd_args* a, void* stream);
 int32_t bolt3_heads_bwd_blocks(int32_t B, int32_t T);

@@ -153,7 +153,7 @@ class HeadsBwdArgs(C.Structure):
         ("d_sink_k", p), ("d_sink_v", p), ("d_k_chain", p), ("d_v_chain", p), ("d_beta", p), ("d_eta", p),
         ("beta", p), ("eta", p), ("lin_q", p), ("lin_q_row_stride", i64), ("lin_k", p), ("lin_k_row_stride", i64),
         ("qn_w", p), ("kn_w", p), ("has_qk_norm", i32), ("q_eps", f32), ("k_eps", f32), ("inv_freq", p),
-        ("dz", p), ("dz_row_stride", i64), ("dz_cols", i32), ("d_qn_w", p), ("d_kn_w", p),
+        ("dz", p), ("dz_row_stride", i64), ("dz_cols", i32), ("d_qn_w", p), ("d_kn_w", p), ("parts", i32),
     ]
 
 

@@ -145,10 +145,11 @@ def layer_backward(mod, x: torch.Tensor, tr: dict, d_out: torch.Tensor, dt: torc
 
     Two streams.  This one: the o_proj products, the readout's backward, the chain's token
     statistics, the attention's backward, the chain's slot recursion and token gradients, the
-    head backward and the projections' products.  The side stream: the chain's M_res recursion,
-    a few long-lived workgroups that run beside the attention's backward (this stream holds the
-    attention until they are resident, bolt3_wait_count), then the reductions to the small
-    parameters.  Every buffer the side stream touches is allocated on this stream and held here
+    key / value part of the head backward and the projections' products.  The side stream: the
+    chain's M_res recursion, a few long-lived workgroups that run beside the attention's backward
+    (this stream holds the attention until they are resident, bolt3_wait_count), then the query
+    part of the head backward beside the chain's slot recursion and token gradients, and the
+    reductions to the small parameters.  Every buffer the side stream touches is allocated on this stream and held here
     until this stream has waited for the side stream's last kernel; the side stream's own results
     are marked as used on this stream."""
     from .bolt3 import WAIT_POLLS, _n_cus, _started_counter   # (bolt3 imports this module)
@@ -204,32 +205,10 @@ def layer_backward(mod, x: torch.Tensor, tr: dict, d_out: torch.Tensor, dt: torc
                 raise RuntimeError(f"bolt3_wait_count failed with code {rc}")
     aa.part = 2
     A.call("bolt3_attn_bwd", aa, dev)
-    aux.wait_stream(main)
-    with torch.cuda.stream(aux):
-        small = {}
-        d_gam = o["d_gamma"].view(b, HKV, n_chunks).sum(dim=(0, 2))
-        if n_steps > 0:
-            d_gam = d_gam + cbuf["d_gamma"].view(n_steps, b, HKV, -1).sum(dim=(0, 1, 3))
-            # kappa: the slot bias is kappa * log(max(mass, 1)) (vsa_lm/config/bolt3.py:238-241)
-            dbias = o["d_bias"].sum(2).view(n_steps, b, HKV, G, S).sum(3)             # [step, b, HKV, S]
-            logm = tr["snap_mass"].clamp_min(1.0).log().view(n_steps, b, HKV, S)
-            small["kappa"] = (dbias * logm).sum(dim=(0, 1, 3))
-        else:
-            small["kappa"] = torch.zeros(HKV, device=dev)
-        # gamma = clamp(0.999 * sigmoid(log_gamma), 1e-3, 0.999); clamp passes its bounds inclusive
-        sg = torch.sigmoid(mod.log_gamma.detach().float().to(dev))
-        g0 = 0.999 * sg
-        inside = ((g0 >= 1e-3) & (g0 <= 0.999)).float()
-        small["log_gamma"] = d_gam * 0.999 * sg * (1.0 - sg) * inside
-        small["res_norm.weight"] = o["d_res_w"].sum(dim=(0, 1))
-    if n_steps > 0:
-        ca.kernels = A.CBWD_SLOT_REC
-        A.call("bolt3_chain_bwd", ca, dev)
-        main.wait_event(ev_m)
-        ca.kernels = A.CBWD_TOK_GRAD
-        A.call("bolt3_chain_bwd", ca, dev)
     # RoPE transposes, the q / k norms' backward and the gates' derivatives, one pass over the
-    # token rows into dz, the gradient of the packed projection output [q | k | v | beta | eta | pad]
+    # token rows into dz, the gradient of the packed projection output [q | k | v | beta | eta | pad]:
+    # the query heads (part 1) on the side stream beside the chain's slot recursion and token
+    # gradients, the key / value heads (part 2) here once the chain is done
     f32 = dict(device=dev, dtype=torch.float32)
     dz = torch.empty(b * T, side["wT"].shape[1], dtype=dt, device=dev)
     has_norm = mod.q_norm is not None
@@ -255,16 +234,46 @@ def layer_backward(mod, x: torch.Tensor, tr: dict, d_out: torch.Tensor, dt: torc
         ha.d_qn_w, ha.d_kn_w = d_qn.data_ptr(), d_kn.data_ptr()
     ha.inv_freq = side["inv_freq"].data_ptr()
     ha.dz, ha.dz_row_stride, ha.dz_cols = dz.data_ptr(), dz.shape[1], dz.shape[1]
+    aux.wait_stream(main)
+    with torch.cuda.stream(aux):
+        ha.parts = 1
+        A.call("bolt3_heads_bwd", ha, dev)
+        small = {}
+        d_gam = o["d_gamma"].view(b, HKV, n_chunks).sum(dim=(0, 2))
+        if n_steps > 0:
+            d_gam = d_gam + cbuf["d_gamma"].view(n_steps, b, HKV, -1).sum(dim=(0, 1, 3))
+            # kappa: the slot bias is kappa * log(max(mass, 1)) (vsa_lm/config/bolt3.py:238-241)
+            dbias = o["d_bias"].sum(2).view(n_steps, b, HKV, G, S).sum(3)             # [step, b, HKV, S]
+            logm = tr["snap_mass"].clamp_min(1.0).log().view(n_steps, b, HKV, S)
+            small["kappa"] = (dbias * logm).sum(dim=(0, 1, 3))
+        else:
+            small["kappa"] = torch.zeros(HKV, device=dev)
+        # gamma = clamp(0.999 * sigmoid(log_gamma), 1e-3, 0.999); clamp passes its bounds inclusive
+        sg = torch.sigmoid(mod.log_gamma.detach().float().to(dev))
+        g0 = 0.999 * sg
+        inside = ((g0 >= 1e-3) & (g0 <= 0.999)).float()
+        small["log_gamma"] = d_gam * 0.999 * sg * (1.0 - sg) * inside
+        small["res_norm.weight"] = o["d_res_w"].sum(dim=(0, 1))
+        if has_norm:
+            small["q_norm.weight"] = d_qn.sum(0)
+    if n_steps > 0:
+        ca.kernels = A.CBWD_SLOT_REC
+        A.call("bolt3_chain_bwd", ca, dev)
+        main.wait_event(ev_m)
+        ca.kernels = A.CBWD_TOK_GRAD
+        A.call("bolt3_chain_bwd", ca, dev)
+    ha.parts = 2
     A.call("bolt3_heads_bwd", ha, dev)
+    main.wait_stream(aux)   # dz's query columns
     widths = [H * HD, HKV * HD, HKV * HD, HKV, H]
     lins = (mod.q_proj, mod.k_proj, mod.v_proj, mod.beta_proj, mod.eta_proj)
     names = ("q_proj", "k_proj", "v_proj", "beta_proj", "eta_proj")
-    # the norms' weight gradients and the biases' column sums of dz (accumulated in fp32, no fp32
+    # the k norm's weight gradient and the biases' column sums of dz (accumulated in fp32, no fp32
     # copy of dz) on the side stream, beside the projections' products
     aux.wait_stream(main)
     with torch.cuda.stream(aux):
         if has_norm:
-            small["q_norm.weight"], small["k_norm.weight"] = d_qn.sum(0), d_kn.sum(0)
+            small["k_norm.weight"] = d_kn.sum(0)
         off = 0
         for name, lin, width in zip(names, lins, widths):
             if lin.bias is not None:

@@ -372,25 +372,33 @@ class Bolt3Attn(nn.Module):
                      for s0, s1 in groups]
             s_dec.wait_stream(main)   # after the head preparation and the allocations above
             esz = k_raw.element_size()
-            nf = 0
-            for (s0, s1), work in zip(groups, works):
+            # filled slots before each group (they depend only on the token counts)
+            nf_at, nf = [], 0
+            for s0, s1 in groups:
+                nf_at.append(nf)
+                for i in range(s0, s1):
+                    nf = min(S, nf + (C - ns if i == 0 else C))
+
+            def issue_group(gi):
+                s0, s1 = groups[gi]
                 # step 0 takes the first chunk after its sinks; step i > 0 takes chunk i
                 tok = s0 * C
                 off0, len0 = (ns, C - ns) if s0 == 0 else (0, C)
                 args = (dt, dev, b, k_raw.data_ptr() + tok * HD * esz, k_rope.data_ptr() + tok * HD * esz,
                         v.data_ptr() + tok * HD * esz, T * HD, pos.data_ptr() + tok * 4, beta.data_ptr() + tok * 4,
-                        T, s1 - s0, off0, len0, C, C, nf, st, m_res, gam, side,
+                        T, s1 - s0, off0, len0, C, C, nf_at[gi], st, m_res, gam, side,
                         *(t[s0:s1] for t in snaps))
-                kw = dict(log=None if log is None else log[s0:s1], kp_exact=True, work=work)
+                kw = dict(log=None if log is None else log[s0:s1], kp_exact=True, work=works[gi])
                 if snap_mp is not None:
                     kw.update(snap_mass=snap_mp[0][s0:s1], snap_pm=snap_mp[1][s0:s1])
+                started = None
                 if split:
                     count = ctr is not None and s0 == 0
                     with torch.cuda.stream(s_dec):
                         self._chain(*args, phase=1, started=ctr[0].data_ptr() if count else None, **kw)
                     if count:
                         ctr[1] += bh
-                        first_started = ctr[1]
+                        started = ctr[1]
                     s_m.wait_stream(s_dec)
                     with torch.cuda.stream(s_m):
                         self._chain(*args, phase=2, **kw)
@@ -400,8 +408,11 @@ class Bolt3Attn(nn.Module):
                 ev = torch.cuda.Event()
                 ev.record(s_m)
                 done.append(ev)
-                for i in range(s0, s1):   # filled slots after each step depend only on the token counts
-                    nf = min(S, nf + (C - ns if i == 0 else C))
+                return started
+
+            # the first group goes out before the q projection and its head preparation, the
+            # others after them (the main stream has work while the host issues them)
+            first_started = issue_group(0)
             if trace is not None:
                 trace.update(state=st, m_res=m_res, snap_k=snaps[0], snap_v=snaps[1], snap_bias=snaps[2],
                              snap_m=snaps[3], log=log, n_filled=nf, snap_mass=snap_mp[0], snap_pm=snap_mp[1])
@@ -414,6 +425,8 @@ class Bolt3Attn(nn.Module):
         eta = torch.empty(b, H, T, device=dev)
         self._heads(lin_q, b, T, dt, side, 0, q_raw, q_rope, None, None, None, None, eta, lin_kv=lin_kv, parts=1,
                     gates=gates)
+        for gi in range(1, len(groups)):
+            issue_group(gi)
         if trace is not None:
             trace.update(q_raw=q_raw, q_rope=q_rope, k_raw=k_raw, k_rope=k_rope, v=v, beta=beta, eta=eta, pos=pos,
                          lin_q=lin_q, lin_kv=lin_kv)

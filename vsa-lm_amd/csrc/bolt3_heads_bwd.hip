@@ -101,6 +101,7 @@ __global__ void __launch_bounds__(NT) heads_bwd_kernel(b3_heads_bwd_args a) {
   const T* g_k_next = static_cast<const T*>(a.d_k_next);
   const T* g_v_own = static_cast<const T*>(a.d_v_own);
   const T* g_v_next = static_cast<const T*>(a.d_v_next);
+  const bool do_q = a.parts != 2, do_kv = a.parts != 1;
   for (int rr = 0; rr < RPB; ++rr) {
     const long long row = (long long)blockIdx.x * RPB + rr;
     if (row >= BT) break;
@@ -110,7 +111,7 @@ __global__ void __launch_bounds__(NT) heads_bwd_kernel(b3_heads_bwd_args a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) sincos_rope((float)t * invf[i], &sn[i], &cs[i]);   // the forward RoPE's own values
     // query heads u = i0 + HPW w + hl: every load first, then the sums
-    for (int i0 = 0; i0 < H; i0 += HPB) {
+    for (int i0 = 0; i0 < (do_q ? H : 0); i0 += HPB) {
       const int u = i0 + HPW * w + hl;
       const bool ok = u < H;
       const long long base = (((long long)b * H + min(u, H - 1)) * a.T + t) * HD;
@@ -141,7 +142,7 @@ __global__ void __launch_bounds__(NT) heads_bwd_kernel(b3_heads_bwd_args a) {
     }
     // kv heads hk = i0 + HPW w + hl: keys (own + next chunk + sinks, the chain's gradient of the
     // un-roped keys, the norm) and values
-    for (int i0 = 0; i0 < HKV; i0 += HPB) {
+    for (int i0 = 0; i0 < (do_kv ? HKV : 0); i0 += HPB) {
       const int hk = i0 + HPW * w + hl;
       const bool ok = hk < HKV;
       const long long bh = (long long)b * HKV + min(hk, HKV - 1);
@@ -213,9 +214,10 @@ __global__ void __launch_bounds__(NT) heads_bwd_kernel(b3_heads_bwd_args a) {
         st4v(dz + (long long)(H + HKV + hk) * HD + HALF + j, v1);
       }
     }
-    // gates and the zero pad
+    // gates and the zero pad (part 1: the eta columns; part 2: beta and the pad)
     const int g_off = (H + 2 * HKV) * HD;
     for (int c = tid; c < a.dz_cols - g_off; c += NT) {
+      if ((c >= HKV && c < HKV + H) ? !do_q : !do_kv) continue;
       float v = 0.f;
       if (c < HKV) {
         const long long bh = (long long)b * HKV + c;
@@ -251,8 +253,10 @@ __global__ void __launch_bounds__(NT) heads_bwd_kernel(b3_heads_bwd_args a) {
   }
   __syncthreads();
   if (tid < HD) {
-    a.d_qn_w[(long long)blockIdx.x * HD + tid] = red[0][0][tid] + red[0][1][tid] + red[0][2][tid] + red[0][3][tid];
-    a.d_kn_w[(long long)blockIdx.x * HD + tid] = red[1][0][tid] + red[1][1][tid] + red[1][2][tid] + red[1][3][tid];
+    if (do_q)
+      a.d_qn_w[(long long)blockIdx.x * HD + tid] = red[0][0][tid] + red[0][1][tid] + red[0][2][tid] + red[0][3][tid];
+    if (do_kv)
+      a.d_kn_w[(long long)blockIdx.x * HD + tid] = red[1][0][tid] + red[1][1][tid] + red[1][2][tid] + red[1][3][tid];
   }
 }
 
@@ -271,6 +275,7 @@ extern "C" int bolt3_heads_bwd(const b3_heads_bwd_args* a, void* stream) {
   if (a->HD != 64 && a->HD != 128) return B3_ERR_UNSUPPORTED;
   if (a->B <= 0 || a->T <= 0 || a->H <= 0 || a->HKV <= 0 || a->H % a->HKV || a->n_sinks < 0 || a->n_chunks < 0)
     return B3_ERR_ARG;
+  if (a->parts < 0 || a->parts > 2) return B3_ERR_ARG;
   const long long need = (long long)(a->H + 2 * a->HKV) * a->HD + a->HKV + a->H;
   if (a->dz_cols < need || a->dz_row_stride < a->dz_cols || a->dz_row_stride % 4) return B3_ERR_ARG;
   if (!a->d_q_raw || !a->d_q_rope || !a->d_k_own || !a->d_k_next || !a->d_v_own || !a->d_v_next || !a->d_eta ||

@@ -444,11 +444,33 @@ class Bolt3Attn(nn.Module):
             a.m_res, a.m_step = snaps[3].data_ptr(), bh * HD * HD
             a.m_split = int(dt == torch.bfloat16)
         a.gamma, a.res_w, a.eps = gam.data_ptr(), side["res_w"].data_ptr(), float(self.res_norm.eps)
-        # The attention output goes into one [B, T, H * HD] buffer.  bf16: group by group, as soon
-        # as the chain has produced a group's snapshots, one launch over the group's chunks (the
-        # first group also takes chunks 0 and 1); then o_proj as one GEMM.  (o_proj per group,
-        # on [B * rows] blocks copied into place, measured the same, 1.379 vs 1.380 ms at cfg2,
-        # and needed a copy of the whole output for the backward's trace.)
+        if split and trace is None:
+            # Group by group, as soon as the chain has produced a group's snapshots: the attention
+            # over all key fields of the group's chunks (the first group also takes chunks 0 and
+            # 1) into one [B * rows, H * HD] block (the group's token range of every batch row),
+            # then o_proj of that block as one GEMM, copied into place.  Only the last group's
+            # attention and o_proj follow the chain's end.
+            spans = [(0, min(T, (groups[0][1] + 2) * C))] + \
+                    [(min(T, (s0 + 2) * C), min(T, (s1 + 2) * C)) for s0, s1 in groups[1:]]
+            y_all = torch.empty(b * T * K, dtype=dt, device=dev)
+            out = torch.empty(b, T, side["wo"].shape[0], dtype=dt, device=dev)
+            esz, off = y_all.element_size(), 0
+            a.part = 0
+            for gi, ((s0, s1), ev) in enumerate(zip(groups, done)):
+                t0, t1 = spans[gi]
+                blk = y_all[off:off + b * (t1 - t0) * K].view(b * (t1 - t0), K)
+                off += b * (t1 - t0) * K
+                main.wait_event(ev)
+                a.chunk_begin, a.chunk_end = (0 if gi == 0 else s0 + 2), s1 + 2
+                # element (b, t) of the block at its base + (b * rows + t - t0) * K (the kernel
+                # writes rows t >= t0 only)
+                a.y, a.y_sb, a.y_st = blk.data_ptr() - t0 * K * esz, (t1 - t0) * K, K
+                A.call("bolt3_chunk_attn", a, dev)
+                out[:, t0:t1].copy_(F.linear(blk, side["wo"]).view(b, t1 - t0, -1))
+            return out
+        # One [B, T, H * HD] attention output (the backward reads it), o_proj as one GEMM.  bf16:
+        # group by group, as soon as the chain has produced a group's snapshots, one launch over
+        # the group's chunks (the first group also takes chunks 0 and 1).
         y = torch.empty(b, T, K, dtype=dt, device=dev)
         a.y, a.y_sb, a.y_st = y.data_ptr(), y.stride(0), y.stride(1)
         if trace is not None:   # every query row's softmax normaliser, which the backward reuses

@@ -270,9 +270,12 @@ int bolt3_chunk_attn(const b3_attn_args* a, void* stream);
  * dy, the gradient of the attention + readout output, the gradients with respect to the roped
  * queries, the un-roped queries (readout), eta, every key field (window keys and values, sinks,
  * the slot snapshots of every step), the slot bias, M_res of every step, res_norm's weight and
- * gamma.  fp32 arithmetic for either storage dtype; outputs are fp32.  Every output element has
- * one writer; d_q_raw, d_eta, d_res_w and d_gamma must be zero-filled by the caller (chunks
- * without a readout leave them untouched).
+ * gamma, from the forward's own row log-sum-exps (b3_attn_args.lse).  fp32 storage: fp32
+ * arithmetic; bf16 storage: MFMA products of bf16 operands with fp32 accumulation.  The row
+ * gradients of storage-dtype tensors come in the storage dtype, the rest in fp32.  Every output
+ * element has one writer; d_q_raw, d_eta, d_res_w, d_gamma, d_bias and the sink gradients must be
+ * zero-filled by the caller (chunks without a readout or without those fields leave them
+ * untouched).
  * Replaces the autograd backward of vsa_lm/config/bolt3.py:219-256 (softmax over
  * [sinks | slots | window], the value read, the readout eta * res_norm(normalize(q) M (1-g)/sqrt(HD))).
  */

@@ -741,32 +741,35 @@ __global__ void __launch_bounds__(512) attn_fwd_kernel(b3_attn_args a, int QW) {
 // brought into LDS by global->LDS loads (global_load_lds_dwordx4), so that no staging goes
 // through registers.  Blocks go in pairs: one barrier per pair, and the QK products of a
 // pair's second block are issued before the softmax of its first, so that the softmax runs
-// beside MFMA work.  The ring has three pair slots (six stages): while pair p is computed,
-// pair p + 1 is in flight and pair p + 2 is issued into the slot pair p - 1 has left.  A
+// beside MFMA work.  The ring has NPS pair slots.  Three (one eight-wavefront workgroup per
+// CU): while pair p is computed, pair p + 1 is in flight and pair p + 2 is issued into the
+// slot pair p - 1 has left.  Two (74 KB of LDS, two four-wavefront workgroups per CU, each
+// covering the other's load waits, start and readout): pair p + 1 is issued at pair p's
+// barrier into the slot pair p - 1 has left.  A
 // tile is stored as blocks of 8 rows x 8 sixteen-byte pieces (one global->LDS instruction each:
 // 8 whole 128-byte row segments), piece-major inside a block and 128 bytes of padding between
 // blocks (f2_off below).  Every operand read of the loop is then a per-lane base plus a
 // compile-time offset (no address arithmetic per read), the K reads (ds_read_b128) are
 // conflict-free and the transposed V reads take the minimum two LDS cycles.  The V operand of
 // O^T = V^T P^T is read with ds_read_b64_tr_b16, which transposes 16-bit elements across lanes,
-// so V needs no transpose when staged.  The M_res snapshot (M^T bf16 hi / lo) comes by the same loads into the two
-// pair slots the last pair leaves free: hi at the barrier before the last pair, lo at the
-// last barrier.
-constexpr int NST = 6;
-
-template <int HD>
+// so V needs no transpose when staged.  The M_res snapshot (M^T bf16 hi / lo) comes by the same
+// loads into pair slots the last pair leaves free.  Three slots: hi at the barrier before the
+// last pair, lo at the last barrier.  Two: hi at the last barrier, lo once every wavefront is
+// done with the last pair.
+template <int HD, int NPS>
 struct Fwd2Smem {
   static constexpr int TILEB = (HD / 64) * (KB / 8) * F2_BLK;   // bytes of one K or V tile
   static_assert(4 * TILEB >= 2 * HD * HD, "an M^T half fits in one pair slot");
-  alignas(16) unsigned char ring[NST][2][TILEB];
+  alignas(16) unsigned char ring[2 * NPS][2][TILEB];
   alignas(16) float sbias[128];          // slot bias row of the step (log2 units)
   alignas(16) float resw[128];           // res_norm weight
 };
 
 
-template <int HD, int NW>
-__global__ void __launch_bounds__(64 * NW) attn_fwd2_kernel(b3_attn_args a, int QW) {
-  using Sm = Fwd2Smem<HD>;
+template <int HD, int NW, int NPS>
+__global__ void __launch_bounds__(64 * NW, NPS == 2 ? 2 : 1) attn_fwd2_kernel(b3_attn_args a, int QW) {
+  static_assert(NPS == 2 || NPS == 3, "two or three pair slots");
+  using Sm = Fwd2Smem<HD, NPS>;
   __shared__ Sm sm;
   constexpr int NDB = HD / 32, NP = HD / 8;
   constexpr int RPI = 1024 / (2 * HD);              // tile rows per 1 KB load instruction
@@ -870,10 +873,10 @@ __global__ void __launch_bounds__(64 * NW) attn_fwd2_kernel(b3_attn_args a, int 
     }
   };
   const int npair = (nb + 1) / 2, P = npair - 1;
-  // this wave's loads of pair q, and the stages of its blocks (pair slot q % 3)
+  // this wave's loads of pair q, and the stages of its blocks (pair slot q % NPS)
   auto issue_pair = [&](int q) {
-    issue(2 * q, 2 * (q % 3));
-    if (2 * q + 1 < nb) issue(2 * q + 1, 2 * (q % 3) + 1);
+    issue(2 * q, 2 * (q % NPS));
+    if (2 * q + 1 < nb) issue(2 * q + 1, 2 * (q % NPS) + 1);
   };
 
   // ---- prologue: the slot bias row, the res_norm weight and the query fragment into
@@ -886,8 +889,10 @@ __global__ void __launch_bounds__(64 * NW) attn_fwd2_kernel(b3_attn_args a, int 
   QFrag<uint16_t, HD> qf;
   qf.load(qrow, qok, h);
   issue_pair(0);
-  if (P >= 1) issue_pair(1);
-  if (P == 0 && readout) issue_mhalf(0, 1);
+  if constexpr (NPS == 3) {
+    if (P >= 1) issue_pair(1);
+    if (P == 0 && readout) issue_mhalf(0, 1);
+  }
   if (tid < 128) lds_write_f32(&sm.sbias[tid], sb * L2E);   // bias in log2 units
   if (tid < HD) lds_write_f32(&sm.resw[tid], rw);
 
@@ -1017,20 +1022,29 @@ __global__ void __launch_bounds__(64 * NW) attn_fwd2_kernel(b3_attn_args a, int 
 
   for (int pr = 0; pr < npair; ++pr) {
     // wait for pair pr while pair pr + 1 (or, at the last pair, the M^T hi half) may still be
-    // in flight
-    if (pr < P) {
-      if (2 * pr + 3 < nb) wait_vm<2 * LPB>();
-      else wait_vm<LPB>();
-    } else if (readout) {
-      wait_vm<LPMH>();
+    // in flight (three slots; with two, nothing is issued after pair pr before its barrier)
+    if constexpr (NPS == 3) {
+      if (pr < P) {
+        if (2 * pr + 3 < nb) wait_vm<2 * LPB>();
+        else wait_vm<LPB>();
+      } else if (readout) {
+        wait_vm<LPMH>();
+      } else {
+        wait_vm<0>();
+      }
     } else {
       wait_vm<0>();
     }
     sync_lds();   // pair pr is in LDS; every wave is done with pair pr - 1
-    if (pr + 2 <= P) issue_pair(pr + 2);
-    if (readout) {
-      if (pr == P - 1) issue_mhalf(0, (P + 1) % 3);
-      if (pr == P) issue_mhalf(1, (P + 2) % 3);
+    if constexpr (NPS == 3) {
+      if (pr + 2 <= P) issue_pair(pr + 2);
+      if (readout) {
+        if (pr == P - 1) issue_mhalf(0, (P + 1) % 3);
+        if (pr == P) issue_mhalf(1, (P + 2) % 3);
+      }
+    } else {
+      if (pr + 1 <= P) issue_pair(pr + 1);
+      if (readout && pr == P) issue_mhalf(0, (P + 1) % 2);
     }
     const int i0 = 2 * pr, i1 = 2 * pr + 1;
     const FwdBlock f0 = block(i0);
@@ -1038,7 +1052,7 @@ __global__ void __launch_bounds__(64 * NW) attn_fwd2_kernel(b3_attn_args a, int 
     const bool has1 = i1 < nb;
     const FwdBlock f1 = block(has1 ? i1 : i0);
     const bool do1 = has1 && !(f1.kpos >= 0 && f1.kpos > wave_q0 + 31);
-    const int st0 = 2 * (pr % 3);
+    const int st0 = 2 * (pr % NPS);
     f32x16 sc0 = zero16(), sc1 = zero16();
     if (do0) sc0 = qk(st0);
     if (do1) sc1 = qk(st0 + 1);
@@ -1050,6 +1064,12 @@ __global__ void __launch_bounds__(64 * NW) attn_fwd2_kernel(b3_attn_args a, int 
   // overlaps the normalisation and the barrier before the readout
   QFrag<uint16_t, HD> rf;
   float eta = 0.f;
+  if constexpr (NPS == 2) {
+    if (readout) {
+      sync_lds();   // every wave is done with the last pair: its slot takes the M^T lo half
+      issue_mhalf(1, P % 2);
+    }
+  }
   if (readout) {
     const uint16_t* rrow = reinterpret_cast<const uint16_t*>(a.q_raw) + b * a.q_sb + hq * a.q_sh + (long long)t * HD;
     rf.load(rrow, qok, h);
@@ -1075,8 +1095,8 @@ __global__ void __launch_bounds__(64 * NW) attn_fwd2_kernel(b3_attn_args a, int 
     qq = pair_sum32(qq);
     const float inv_q = 1.0f / fmaxf(sqrtf(qq), 1e-12f);
     const float coef = div_rn(1.0f - a.gamma[hkv], sqrtf((float)HD));
-    const uint16_t* mt_hi = reinterpret_cast<const uint16_t*>(sm.ring[2 * ((P + 1) % 3)][0]);
-    const uint16_t* mt_lo = reinterpret_cast<const uint16_t*>(sm.ring[2 * ((P + 2) % 3)][0]);
+    const uint16_t* mt_hi = reinterpret_cast<const uint16_t*>(sm.ring[2 * ((P + 1) % NPS)][0]);
+    const uint16_t* mt_lo = reinterpret_cast<const uint16_t*>(sm.ring[2 * (NPS == 3 ? (P + 2) % 3 : P % 2)][0]);
     f32x16 rr[NDB];
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {
@@ -1142,9 +1162,17 @@ static int launch_attn(const b3_attn_args& a, hipStream_t st) {
       ab.chunk_begin = c0;
       const int nw = nthreads / 64;
       if (a.part == 0 && (a.S == 128 || a.n_q <= 2 * a.C) && (nw == 2 || nw == 4 || nw == 8)) {
-        if (nw == 8) hipLaunchKernelGGL((attn_fwd2_kernel<HD, 8>), grid, dim3(nthreads), 0, st, ab, QW);
-        else if (nw == 4) hipLaunchKernelGGL((attn_fwd2_kernel<HD, 4>), grid, dim3(nthreads), 0, st, ab, QW);
-        else hipLaunchKernelGGL((attn_fwd2_kernel<HD, 2>), grid, dim3(nthreads), 0, st, ab, QW);
+        if (G == 4) {
+          // one query tile of the four heads per workgroup (four wavefronts), two workgroups per CU
+          const dim3 grid1((qlen + 31) / 32, n_chunks, a.B * a.HKV);
+          hipLaunchKernelGGL((attn_fwd2_kernel<HD, 4, 2>), grid1, dim3(256), 0, st, ab, 1);
+        } else if (nw == 8) {
+          hipLaunchKernelGGL((attn_fwd2_kernel<HD, 8, 3>), grid, dim3(nthreads), 0, st, ab, QW);
+        } else if (nw == 4) {
+          hipLaunchKernelGGL((attn_fwd2_kernel<HD, 4, 3>), grid, dim3(nthreads), 0, st, ab, QW);
+        } else {
+          hipLaunchKernelGGL((attn_fwd2_kernel<HD, 2, 3>), grid, dim3(nthreads), 0, st, ab, QW);
+        }
         return (int)hipGetLastError();
       }
       const int ipt = (KB * (HD / 8) + nthreads - 1) / nthreads;

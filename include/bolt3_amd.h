@@ -329,9 +329,14 @@ typedef struct {
   float* d_slot_v;
   float* d_sink_k;            /* [n_chunks][B*HKV][n_sinks][HD] (chunks 0 and 1 are not written) */
   float* d_sink_v;
-  int32_t part;               /* 0: everything; 1: the readout kernel only (d_m, d_q_raw, d_eta, d_res_w,
+  int32_t part;               /* 0: everything; 1: the readout kernels only (d_m, d_q_raw, d_eta, d_res_w,
                                  d_gamma, d_rows); 2: the attention kernels only, after a part-1 call
                                  with the same arguments (they read d_rows) */
+  void* rd_rows;              /* bf16 storage, parts 0 and 1 with a readout: [B][H][T][HD] bf16 scratch
+                                 rows (du / |q_raw| of the readout's rows, written by its row kernel and
+                                 read by its dM kernel).  May be d_q_rope: with part 0, or part 2 after
+                                 part 1, the attention kernels overwrite every row of it afterwards.
+                                 Unused (may be NULL) for fp32 storage or part 2. */
 } b3_attn_bwd_args;
 int bolt3_attn_bwd(const b3_attn_bwd_args* a, void* stream);
 

@@ -122,6 +122,7 @@ class AttnBwdArgs(C.Structure):
         ("d_rows", p), ("lse", p), ("d_q_rope", p), ("d_q_raw", p), ("d_eta", p), ("d_m", p), ("d_res_w", p),
         ("d_gamma", p), ("d_bias", p), ("d_k_own", p), ("d_v_own", p), ("d_k_next", p), ("d_v_next", p),
         ("d_slot_k", p), ("d_slot_v", p), ("d_sink_k", p), ("d_sink_v", p), ("part", i32),
+        ("rd_rows", p),
     ]
 
 

@@ -136,6 +136,9 @@ def attn_backward_args(mod, tr: dict, dy: torch.Tensor, dt: torch.dtype, n_steps
     for name, t in o.items():
         if hasattr(a, name):
             setattr(a, name, t.data_ptr())
+    # the readout's du / |q_raw| rows between its two kernels: d_q_rope's memory, which the
+    # attention kernels (part 2) overwrite afterwards
+    a.rd_rows = o["d_q_rope"].data_ptr()
     return a, o
 
 

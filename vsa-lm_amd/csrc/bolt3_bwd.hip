@@ -1099,28 +1099,33 @@ __global__ void __launch_bounds__(NT) readout_bwd_kernel(b3_attn_bwd_args a) {
 
 // ---------------------------------------------------------------- readout, bf16 storage: MFMA
 //
-// The readout's gradients for bf16 storage on MFMA, one workgroup of four wavefronts per (b, kv
-// head, chunk), one query row per lane column, 32 rows per wavefront and round:
+// The readout's gradients for bf16 storage on MFMA in two kernels.  The row kernel: one
+// workgroup of RD_W wavefronts per (b, kv head, chunk), one query row per lane column, 32 rows
+// per wavefront and round:
 //   U^T = M^T q_raw^T            (M^T as bf16 hi + lo, q_raw exact: two products, as the forward)
 //   u = U / |q_raw|, ym = u (1-gamma)/sqrt(HD), the RMSNorm backward as the fp32 kernel
 //   dqn^T = M du^T               (M^T read transposed; hi/lo on both sides: three products)
-//   dM += q_raw^T (du / |q_raw|) (bf16 operands from per-wavefront row tiles in LDS; wavefront w
-//                                 accumulates its share of the (HD/32)^2 output tiles)
+//   du / |q_raw| as bf16 rows into rd_rows
+// with each round's dy and y rows loaded once, at its start.  The dM kernel, one workgroup of
+// four wavefronts per (b, kv head, chunk):
+//   dM = q_raw^T (du / |q_raw|)  (32-row tiles of both staged in LDS, read transposed; wavefront
+//                                 w accumulates its share of the (HD/32)^2 output tiles, the
+//                                 tiles and their two K halves in row order)
+constexpr int RD_W = 8;   // wavefronts of the row kernel
+
 template <int HD>
 struct RdMfmaSmem {
-  alignas(16) uint16_t mt[2][HD * HD];   // M^T hi, lo: row d, 16-byte piece p at p ^ (d % (HD/8))
-  alignas(16) uint16_t qt[4][32 * HD];   // per wavefront: q_raw rows of its tile (same swizzle)
-  alignas(16) uint16_t ut[4][32 * HD];   // per wavefront: du / |q_raw| rows, bf16
+  alignas(16) uint16_t mt[2][HD * HD];     // M^T hi, lo: row d, 16-byte piece p at p ^ (d % (HD/8))
+  alignas(16) uint16_t qt[RD_W][32 * HD];  // per wavefront: q_raw rows of its tile (same swizzle)
   float resw[HD];
-  float red[4][HD + 1];
+  float red[RD_W][HD + 1];
 };
 
 template <int HD>
-__global__ void __launch_bounds__(256) readout_bwd_mfma_kernel(b3_attn_bwd_args a) {
+__global__ void __launch_bounds__(64 * RD_W) readout_bwd_mfma_kernel(b3_attn_bwd_args a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
   RdMfmaSmem<HD>& sm = *reinterpret_cast<RdMfmaSmem<HD>*>(smem_raw);
-  constexpr int KS = HD / 16, NDB = HD / 32, NP = HD / 8, TPW = NDB * NDB / 4;
-  static_assert(NDB * NDB % 4 == 0, "dM tiles split over four wavefronts");
+  constexpr int KS = HD / 16, NDB = HD / 32, NP = HD / 8, NT_RD = 64 * RD_W;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, n = lane & 31, h = lane >> 5;
   const int bh = blockIdx.x, b = bh / a.HKV, hkv = bh % a.HKV, c = blockIdx.y;
   const int G = a.H / a.HKV;
@@ -1131,7 +1136,7 @@ __global__ void __launch_bounds__(256) readout_bwd_mfma_kernel(b3_attn_bwd_args 
     // D = rowsum(dy * y) only: 16 lanes per row, HD / 16 elements each
     constexpr int DPT = HD / 16;
     const int rq = lane >> 4, dg = lane & 15;
-    for (int r0 = 4 * w; r0 < n_rows; r0 += 16) {
+    for (int r0 = 4 * w; r0 < n_rows; r0 += 4 * RD_W) {
       const int q = r0 + rq;
       const bool live = q < n_rows;
       const int g = live ? q / tc : 0, i = live ? q % tc : 0;
@@ -1155,28 +1160,16 @@ __global__ void __launch_bounds__(256) readout_bwd_mfma_kernel(b3_attn_bwd_args 
   {
     const uint16_t* src = reinterpret_cast<const uint16_t*>(a.m_res + (long long)(c - 2) * a.m_step +
                                                             (long long)bh * HD * HD);
-    for (int it = tid; it < 2 * HD * NP; it += 256) {
+    for (int it = tid; it < 2 * HD * NP; it += NT_RD) {
       const int half = it / (HD * NP), rem = it % (HD * NP), d = rem / NP, pc = rem % NP;
       *reinterpret_cast<u16x8*>(&sm.mt[half][d * HD + 8 * (pc ^ (d % NP))]) =
           *reinterpret_cast<const u16x8*>(src + (long long)half * HD * HD + d * HD + 8 * pc);
     }
-    for (int it = tid; it < HD; it += 256) sm.resw[it] = a.res_w[it];
+    for (int it = tid; it < HD; it += NT_RD) sm.resw[it] = a.res_w[it];
   }
   __syncthreads();
   const float sg = (1.0f - a.gamma[hkv]) / sqrtf((float)HD);
   const TrLanes<HD> TL(lane);
-  int dm_off[TPW][4];   // transposed-read offsets of output tile tt: A (rows cf) then B (columns d)
-#pragma unroll
-  for (int tt = 0; tt < TPW; ++tt) {
-    const int id = w * TPW + tt, cb = id / NDB, db = id % NDB;
-    dm_off[tt][0] = tr_off<HD>(lane, cb, 0);
-    dm_off[tt][1] = tr_off<HD>(lane, cb, 1);
-    dm_off[tt][2] = tr_off<HD>(lane, db, 0);
-    dm_off[tt][3] = tr_off<HD>(lane, db, 1);
-  }
-  f32x16 dm[TPW];
-#pragma unroll
-  for (int tt = 0; tt < TPW; ++tt) dm[tt] = zero16();
   // res_w partials: dres[db] is feature 32 db + d_row(lane, r) with r = 8 (n >> 4 & 1) +
   // 4 (n >> 3 & 1) + 2 (n >> 2 & 1) + (n >> 1 & 1) (the reduce-scatter below leaves it there)
   float dres[NDB];
@@ -1184,10 +1177,9 @@ __global__ void __launch_bounds__(256) readout_bwd_mfma_kernel(b3_attn_bwd_args 
   for (int db = 0; db < NDB; ++db) dres[db] = 0.f;
   float dsg = 0.f;
   uint16_t* qt = sm.qt[w];
-  uint16_t* ut = sm.ut[w];
   const int n_tiles = (n_rows + 31) / 32;
 #pragma unroll 1
-  for (int r0 = 0; r0 < n_tiles; r0 += 4) {
+  for (int r0 = 0; r0 < n_tiles; r0 += RD_W) {
     const int q = 32 * (r0 + w) + n;
     const bool live = q < n_rows;
     const int g = live ? q / tc : 0, i = live ? q % tc : 0;
@@ -1196,16 +1188,25 @@ __global__ void __launch_bounds__(256) readout_bwd_mfma_kernel(b3_attn_bwd_args 
     const long long row = ((long long)b * a.H + hq) * a.T + t;
     // the lane's q_raw row: B operand (K elements 16 ks + 8 h ..) and row n of the tile
     u16x8 qf[KS];
-    {
-      const uint16_t* qp = reinterpret_cast<const uint16_t*>(a.q_raw) + (long long)b * a.q_sb + (long long)hq * a.q_sh +
-                           t * HD;
+    const uint16_t* qp = reinterpret_cast<const uint16_t*>(a.q_raw) + (long long)b * a.q_sb + (long long)hq * a.q_sh +
+                         t * HD;
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        qf[ks] = live ? *reinterpret_cast<const u16x8*>(qp + 16 * ks + 8 * h) : u16x8{0, 0, 0, 0, 0, 0, 0, 0};
-        *reinterpret_cast<u16x8*>(&qt[n * HD + 8 * ((2 * ks + h) ^ (n % NP))]) = qf[ks];
-      }
-    }
+    for (int ks = 0; ks < KS; ++ks)
+      qf[ks] = live ? *reinterpret_cast<const u16x8*>(qp + 16 * ks + 8 * h) : u16x8{0, 0, 0, 0, 0, 0, 0, 0};
     const float eta = live ? a.eta[(long long)b * a.e_sb + (long long)hq * a.e_sh + t] : 0.f;
+    // the round's dy at this lane's accumulator features 32 db + 8 r4 + 4 h .. + 3, loaded once,
+    // while the U^T products run (y follows once they are issued)
+    const uint16_t* dyp = reinterpret_cast<const uint16_t*>(a.dy) + (long long)b * a.dy_sb + t * a.dy_st +
+                          (long long)hq * HD;
+    const uint16_t* yp = reinterpret_cast<const uint16_t*>(a.y) + (long long)b * a.y_sb + t * a.y_st + (long long)hq * HD;
+    uint2 dyr[NDB][4], yr[NDB][4];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4)
+        dyr[db][r4] = live ? *reinterpret_cast<const uint2*>(dyp + 32 * db + 8 * r4 + 4 * h) : make_uint2(0u, 0u);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) *reinterpret_cast<u16x8*>(&qt[n * HD + 8 * ((2 * ks + h) ^ (n % NP))]) = qf[ks];
     float qq = 0.f;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
@@ -1232,10 +1233,12 @@ __global__ void __launch_bounds__(256) readout_bwd_mfma_kernel(b3_attn_bwd_args 
       }
     }
     __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4)
+        yr[db][r4] = live ? *reinterpret_cast<const uint2*>(yp + 32 * db + 8 * r4 + 4 * h) : make_uint2(0u, 0u);
     // the RMSNorm backward of ym = u * sg at this lane's features d = 32 db + d_row(lane, r)
-    const uint16_t* dyp = reinterpret_cast<const uint16_t*>(a.dy) + (long long)b * a.dy_sb + t * a.dy_st +
-                          (long long)hq * HD;
-    const uint16_t* yp = reinterpret_cast<const uint16_t*>(a.y) + (long long)b * a.y_sb + t * a.y_st + (long long)hq * HD;
     // u becomes ym = U sg / |q_raw| (sg > 0: gamma <= 0.999)
     const float ks_ = inv * sg;
     float sq = 0.f;
@@ -1251,20 +1254,13 @@ __global__ void __launch_bounds__(256) readout_bwd_mfma_kernel(b3_attn_bwd_args 
     float dd = 0.f, deta = 0.f, gdot = 0.f;
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {
-      __builtin_amdgcn_sched_barrier(0);   // one block's loads live at a time
       float xr[16];   // res_w terms of the block
 #pragma unroll
       for (int r4 = 0; r4 < 4; ++r4) {
         const int d0 = 32 * db + 8 * r4 + 4 * h;
-        float4 dy4 = make_float4(0.f, 0.f, 0.f, 0.f);
-        uint2 y2 = make_uint2(0u, 0u);
-        if (live) {
-          const uint2 g2 = *reinterpret_cast<const uint2*>(dyp + d0);
-          dy4 = make_float4(bf_lo(g2.x), bf_hi(g2.x), bf_lo(g2.y), bf_hi(g2.y));
-          y2 = *reinterpret_cast<const uint2*>(yp + d0);
-        }
+        const uint2 g2 = dyr[db][r4], y2 = yr[db][r4];
         const float4 w4 = *reinterpret_cast<const float4*>(&sm.resw[d0]);
-        const float dyv[4] = {dy4.x, dy4.y, dy4.z, dy4.w};
+        const float dyv[4] = {bf_lo(g2.x), bf_hi(g2.x), bf_lo(g2.y), bf_hi(g2.y)};
         const float yv[4] = {bf_lo(y2.x), bf_hi(y2.x), bf_lo(y2.y), bf_hi(y2.y)};
         const float wv[4] = {w4.x, w4.y, w4.z, w4.w};
 #pragma unroll
@@ -1302,23 +1298,19 @@ __global__ void __launch_bounds__(256) readout_bwd_mfma_kernel(b3_attn_bwd_args 
       a.d_rows[row] = dd;
       a.d_eta[row] = deta;
     }
-    // du = sg (rr g - ym rr^3 gdot / HD), g = eta dy w (dy read again), in place of u; the gamma
-    // partial; du / |q_raw| as bf16 into the wavefront's tile
+    // du = sg (rr g - ym rr^3 gdot / HD), g = eta dy w, in place of u; the gamma partial; du /
+    // |q_raw| as bf16 into the row scratch (the dM kernel's operand)
     float dsg_r = 0.f;
     const float c3 = rr * rr * rr * gdot / (float)HD;
+    uint16_t* ru = static_cast<uint16_t*>(a.rd_rows) + row * HD;
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
 #pragma unroll
       for (int r4 = 0; r4 < 4; ++r4) {
-        if (r4 == 0) __builtin_amdgcn_sched_barrier(0);
         const int d0 = 32 * db + 8 * r4 + 4 * h;
-        float4 dy4 = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (live) {
-          const uint2 g2 = *reinterpret_cast<const uint2*>(dyp + d0);
-          dy4 = make_float4(bf_lo(g2.x), bf_hi(g2.x), bf_lo(g2.y), bf_hi(g2.y));
-        }
+        const uint2 g2 = dyr[db][r4];
         const float4 w4 = *reinterpret_cast<const float4*>(&sm.resw[d0]);
-        const float dyv[4] = {dy4.x, dy4.y, dy4.z, dy4.w};
+        const float dyv[4] = {bf_lo(g2.x), bf_hi(g2.x), bf_lo(g2.y), bf_hi(g2.y)};
         const float wv[4] = {w4.x, w4.y, w4.z, w4.w};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -1328,9 +1320,9 @@ __global__ void __launch_bounds__(256) readout_bwd_mfma_kernel(b3_attn_bwd_args 
           dsg_r += dym * ym;
           u[db][r] = live ? dym * sg : 0.f;
         }
-        const uint2 v = make_uint2(pack_bf2(u[db][4 * r4] * inv, u[db][4 * r4 + 1] * inv),
-                                   pack_bf2(u[db][4 * r4 + 2] * inv, u[db][4 * r4 + 3] * inv));
-        *reinterpret_cast<uint2*>(&ut[n * HD + 8 * ((4 * db + r4) ^ (n % NP)) + 4 * h]) = v;
+        if (live)
+          *reinterpret_cast<uint2*>(ru + d0) = make_uint2(pack_bf2(u[db][4 * r4] * inv, u[db][4 * r4 + 1] * inv),
+                                                          pack_bf2(u[db][4 * r4 + 2] * inv, u[db][4 * r4 + 3] * inv));
       }
     // sum_d dym ym: the gamma partial (times 1/sg) and qn . dqn (qn . M du = u . du)
     const float sdy = pair_sum32(dsg_r);
@@ -1372,39 +1364,6 @@ __global__ void __launch_bounds__(256) readout_bwd_mfma_kernel(b3_attn_bwd_args 
         }
       }
     }
-    __syncthreads();   // every wavefront's q_raw and du tiles are in LDS
-    // dM[cf][d] += sum_q q_raw[q][cf] du'[q][d] over the round's tiles; output tile tt of this
-    // wavefront is (cb, db) = ((w TPW + tt) / NDB, (w TPW + tt) % NDB)
-    for (int ws = 0; ws < 4; ++ws) {
-      if (32 * (r0 + ws) >= n_rows) break;
-#pragma unroll
-      for (int kc = 0; kc < 2; ++kc)
-#pragma unroll
-        for (int tt = 0; tt < TPW; ++tt) {
-          const uint16_t* pq = sm.qt[ws] + 16 * kc * HD;
-          const uint16_t* pu = sm.ut[ws] + 16 * kc * HD;
-          const s16x4 a0 = lds_tr16(pq + dm_off[tt][0]), a1 = lds_tr16(pq + dm_off[tt][1]);
-          const s16x4 b0 = lds_tr16(pu + dm_off[tt][2]), b1 = lds_tr16(pu + dm_off[tt][3]);
-          u16x8 av, bv;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            av[e] = (uint16_t)a0[e];
-            av[4 + e] = (uint16_t)a1[e];
-            bv[e] = (uint16_t)b0[e];
-            bv[4 + e] = (uint16_t)b1[e];
-          }
-          mma_bf16(dm[tt], av, bv);
-        }
-    }
-    __syncthreads();   // the tiles are read before the next round writes them
-  }
-  // dM out: tile (cb, db) holds rows cf = 32 cb + d_row(lane, r), column d = 32 db + n
-  float* dmo = a.d_m + ((long long)(c - 2) * a.B * a.HKV + bh) * HD * HD;
-#pragma unroll
-  for (int tt = 0; tt < TPW; ++tt) {
-    const int id = w * TPW + tt, cb = id / NDB, db = id % NDB;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) dmo[(32 * cb + d_row(lane, r)) * HD + 32 * db + n] = dm[tt][r];
   }
   // res_w and gamma partials over the wavefronts (lanes n and n ^ 1 hold the same sums)
   if ((n & 1) == 0) {
@@ -1420,9 +1379,114 @@ __global__ void __launch_bounds__(256) readout_bwd_mfma_kernel(b3_attn_bwd_args 
   }
   __syncthreads();
   const long long pc = (long long)bh * a.n_chunks + c;
-  if (tid < HD) a.d_res_w[pc * HD + tid] = sm.red[0][tid] + sm.red[1][tid] + sm.red[2][tid] + sm.red[3][tid];
-  if (tid == 0)
-    a.d_gamma[pc] = -(sm.red[0][HD] + sm.red[1][HD] + sm.red[2][HD] + sm.red[3][HD]) / sqrtf((float)HD);
+  if (tid <= HD) {
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < RD_W; ++k) s += sm.red[k][tid];
+    if (tid < HD) a.d_res_w[pc * HD + tid] = s;
+    else a.d_gamma[pc] = -s / sqrtf((float)HD);
+  }
+}
+
+// dM[cf][d] = sum over the chunk's readout rows q of q_raw[q][cf] (du / |q_raw|)[q][d], chunk c
+// >= 2 (blockIdx.y = c - 2).  32-row tiles of both operands go through registers into two LDS
+// buffers (the next tile's loads in flight while the current one multiplies), rows past the
+// chunk's as zeros; one barrier per tile.
+template <int HD>
+struct RdDmSmem {
+  alignas(16) uint16_t qt[2][32 * HD];   // row n, 16-byte piece p at p ^ (n % (HD/8))
+  alignas(16) uint16_t ut[2][32 * HD];
+};
+
+template <int HD>
+__global__ void __launch_bounds__(256) readout_dm_kernel(b3_attn_bwd_args a) {
+  __shared__ RdDmSmem<HD> sm;
+  constexpr int NDB = HD / 32, NP = HD / 8, TPW = NDB * NDB / 4, PPT = 32 * NP / 256;
+  static_assert(NDB * NDB % 4 == 0 && PPT >= 1 && 32 * NP % 256 == 0, "dM tiles and staging split over 256 threads");
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, n = lane & 31;
+  const int bh = blockIdx.x, b = bh / a.HKV, hkv = bh % a.HKV, c = blockIdx.y + 2;
+  const int G = a.H / a.HKV;
+  const int tc = chunk_len(a, c);
+  const int n_rows = G * tc;
+  const int n_tiles = (n_rows + 31) / 32;
+  int dm_off[TPW][4];   // transposed-read offsets of output tile tt: A (rows cf) then B (columns d)
+#pragma unroll
+  for (int tt = 0; tt < TPW; ++tt) {
+    const int id = w * TPW + tt, cb = id / NDB, db = id % NDB;
+    dm_off[tt][0] = tr_off<HD>(lane, cb, 0);
+    dm_off[tt][1] = tr_off<HD>(lane, cb, 1);
+    dm_off[tt][2] = tr_off<HD>(lane, db, 0);
+    dm_off[tt][3] = tr_off<HD>(lane, db, 1);
+  }
+  // this thread's 16-byte pieces of a tile: piece tid + 256 j is row / NP, piece % NP
+  u16x8 rq[PPT], ru[PPT];
+  auto load = [&](int k) {
+#pragma unroll
+    for (int j = 0; j < PPT; ++j) {
+      const int pi = tid + 256 * j, rl = pi / NP, p = pi % NP;
+      const int q = 32 * k + rl;
+      rq[j] = ru[j] = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+      if (q < n_rows) {
+        const int g = q / tc, i = q % tc, hq = hkv * G + g;
+        const long long t = (long long)c * a.C + i;
+        rq[j] = *reinterpret_cast<const u16x8*>(reinterpret_cast<const uint16_t*>(a.q_raw) + (long long)b * a.q_sb +
+                                                (long long)hq * a.q_sh + t * HD + 8 * p);
+        ru[j] = *reinterpret_cast<const u16x8*>(static_cast<const uint16_t*>(a.rd_rows) +
+                                                (((long long)b * a.H + hq) * a.T + t) * HD + 8 * p);
+      }
+    }
+  };
+  auto store = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < PPT; ++j) {
+      const int pi = tid + 256 * j, rl = pi / NP, p = pi % NP;
+      const int o = rl * HD + 8 * (p ^ (rl % NP));
+      *reinterpret_cast<u16x8*>(&sm.qt[buf][o]) = rq[j];
+      *reinterpret_cast<u16x8*>(&sm.ut[buf][o]) = ru[j];
+    }
+  };
+  f32x16 dm[TPW];
+#pragma unroll
+  for (int tt = 0; tt < TPW; ++tt) dm[tt] = zero16();
+  if (n_tiles > 0) {
+    load(0);
+    store(0);
+  }
+  __syncthreads();
+#pragma unroll 1
+  for (int k = 0; k < n_tiles; ++k) {
+    if (k + 1 < n_tiles) load(k + 1);
+    const int buf = k & 1;
+#pragma unroll
+    for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+      for (int tt = 0; tt < TPW; ++tt) {
+        const uint16_t* pq = sm.qt[buf] + 16 * kc * HD;
+        const uint16_t* pu = sm.ut[buf] + 16 * kc * HD;
+        const s16x4 a0 = lds_tr16(pq + dm_off[tt][0]), a1 = lds_tr16(pq + dm_off[tt][1]);
+        const s16x4 b0 = lds_tr16(pu + dm_off[tt][2]), b1 = lds_tr16(pu + dm_off[tt][3]);
+        u16x8 av, bv;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          av[e] = (uint16_t)a0[e];
+          av[4 + e] = (uint16_t)a1[e];
+          bv[e] = (uint16_t)b0[e];
+          bv[4 + e] = (uint16_t)b1[e];
+        }
+        mma_bf16(dm[tt], av, bv);
+      }
+    // the other buffer was last read in the previous tile, before the barrier that ended it
+    if (k + 1 < n_tiles) store(buf ^ 1);
+    __syncthreads();
+  }
+  // dM out: tile (cb, db) holds rows cf = 32 cb + d_row(lane, r), column d = 32 db + n
+  float* dmo = a.d_m + ((long long)(c - 2) * a.B * a.HKV + bh) * HD * HD;
+#pragma unroll
+  for (int tt = 0; tt < TPW; ++tt) {
+    const int id = w * TPW + tt, cb = id / NDB, db = id % NDB;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dmo[(32 * cb + d_row(lane, r)) * HD + 32 * db + n] = dm[tt][r];
+  }
 }
 
 template <typename T, int HD>
@@ -1431,11 +1495,20 @@ static int launch(const b3_attn_bwd_args& a, hipStream_t st) {
   const int BH = a.B * a.HKV;
   hipError_t e = hipSuccess;
   if (a.part != 2) {
-    if constexpr (St<T>::is_bf16)
-      hipLaunchKernelGGL((readout_bwd_mfma_kernel<HD>), dim3(BH, n_chunks), dim3(256), sizeof(RdMfmaSmem<HD>), st, a);
-    else
+    if constexpr (St<T>::is_bf16) {
+      hipLaunchKernelGGL((readout_bwd_mfma_kernel<HD>), dim3(BH, n_chunks), dim3(64 * RD_W), sizeof(RdMfmaSmem<HD>),
+                         st, a);
+      // dM of the chunks with a readout: c = 2 .. min(n_chunks, n_steps + 2) - 1
+      const int n_m = a.m_res ? min(n_chunks, a.n_steps + 2) - 2 : 0;
+      e = hipGetLastError();
+      if (e == hipSuccess && n_m > 0) {
+        hipLaunchKernelGGL((readout_dm_kernel<HD>), dim3(BH, n_m), dim3(256), 0, st, a);
+        e = hipGetLastError();
+      }
+    } else {
       hipLaunchKernelGGL((readout_bwd_kernel<T, HD>), dim3(BH, n_chunks), dim3(NT), sizeof(RdSmem<HD>), st, a);
-    e = hipGetLastError();
+      e = hipGetLastError();
+    }
     if (e != hipSuccess || a.part == 1) return (int)e;
   }
   // key blocks per chunk at most: sinks, slots, previous and own chunk
@@ -1496,6 +1569,10 @@ extern "C" int bolt3_attn_bwd(const b3_attn_bwd_args* a, void* stream) {
     return B3_ERR_ARG;
   if (a->m_split && a->dtype != B3_BF16) return B3_ERR_ARG;
   if (a->part < 0 || a->part > 2) return B3_ERR_ARG;
+  // the bf16 readout's row scratch, 16-byte aligned rows
+  if (a->dtype == B3_BF16 && a->part != 2 && a->n_steps > 0 && a->m_res &&
+      (!a->rd_rows || reinterpret_cast<uintptr_t>(a->rd_rows) % 16))
+    return B3_ERR_ARG;
   // 16-byte rows: every (b, h, t) row of the staged operands
   const int64_t es = a->dtype == B3_BF16 ? 2 : 4;
   if ((a->q_sb * es) % 16 || (a->q_sh * es) % 16 || (a->w_sb * es) % 16 || (a->w_sh * es) % 16 ||

@@ -784,9 +784,15 @@ __global__ void __launch_bounds__(ANT, 4) decode_attn_kernel(b3_decode_args a, L
       mx = nmx;
       // every load of the tile (the value rows in LDS included) has landed
       wait_vm<0>();
-      if (r_new < 32 && lane < NP)
-        *reinterpret_cast<u16x8*>(vbuf + r_new * HD + 8 * (lane ^ (r_new % NP))) =
-            *reinterpret_cast<const u16x8*>(&sm.newv[8 * lane]);
+      // the new token's value row from LDS, in its own row and in every row after it: keys past
+      // nk - 1 were clamped to its ring position, read before the token was written there, and
+      // their zero probabilities must not meet whatever that memory held (0 * NaN is NaN)
+      if (r_new < 32)
+        for (int it = lane; it < (32 - r_new) * NP; it += 64) {
+          const int rr = r_new + it / NP, pc = it % NP;
+          *reinterpret_cast<u16x8*>(vbuf + rr * HD + 8 * (pc ^ (rr % NP))) =
+              *reinterpret_cast<const u16x8*>(&sm.newv[8 * pc]);
+        }
       const int s = lane & 15;
 #pragma unroll
       for (int db = 0; db < NDB; ++db) {

@@ -766,7 +766,7 @@ struct Fwd2Smem {
 };
 
 
-template <int HD, int NW, int NPS>
+template <int HD, int NW, int NPS, bool SR>
 __global__ void __launch_bounds__(64 * NW, NPS == 2 ? 2 : 1) attn_fwd2_kernel(b3_attn_args a, int QW) {
   static_assert(NPS == 2 || NPS == 3, "two or three pair slots");
   using Sm = Fwd2Smem<HD, NPS>;
@@ -919,41 +919,32 @@ __global__ void __launch_bounds__(64 * NW, NPS == 2 ? 2 : 1) attn_fwd2_kernel(b3
   // softmax step and O^T += V^T P^T for block f in stage st, scores sc
   auto attend = [&](f32x16 sc, const FwdBlock& f, int st) {
     const uint32_t vb = lds_addr(sm.ring[st][1]) + lane_v;
-    // scores in log2 units: round_bf(q.k) * scale*log2(e) + slot bias * log2(e), one FMA, for the
-    // slot blocks; the other blocks keep round_bf(q.k) and take the factor ksc inside the
-    // exponent's FMA (and on their maximum).  The rounding is skipped when score_round is 0
-    // (fp32 scores, as the decoder step computes them).
-    const float ksc = f.bias ? 1.0f : sL;
+    // scores in log2 units: round_bf(q.k) * scale*log2(e) + slot bias * log2(e), one FMA for
+    // every block (bias 0 outside the slot field), so that every block takes the same
+    // instructions.  SR = false skips the rounding (fp32 scores, as the decoder step computes them).
+    fx4 b4[4];
     if (f.bias) {
-      fx4 b4[4];
 #pragma unroll
       for (int r4 = 0; r4 < 4; ++r4) b4[r4] = lds_read_f4_nowait(f.bias + 8 * r4 + 4 * h);
       lds_wait4(b4[0], b4[1], b4[2], b4[3]);
-      if (a.score_round) {
+    } else {
 #pragma unroll
-        for (int r4 = 0; r4 < 4; ++r4) {
-          const uint32_t u0 = pack_bf2(sc[4 * r4], sc[4 * r4 + 1]), u1 = pack_bf2(sc[4 * r4 + 2], sc[4 * r4 + 3]);
-          sc[4 * r4] = fmaf(bf_lo(u0), sL, b4[r4].x);
-          sc[4 * r4 + 1] = fmaf(bf_hi(u0), sL, b4[r4].y);
-          sc[4 * r4 + 2] = fmaf(bf_lo(u1), sL, b4[r4].z);
-          sc[4 * r4 + 3] = fmaf(bf_hi(u1), sL, b4[r4].w);
-        }
-      } else {
+      for (int r4 = 0; r4 < 4; ++r4) b4[r4] = fx4{0.f, 0.f, 0.f, 0.f};
+    }
 #pragma unroll
-        for (int r4 = 0; r4 < 4; ++r4) {
-          sc[4 * r4] = fmaf(sc[4 * r4], sL, b4[r4].x);
-          sc[4 * r4 + 1] = fmaf(sc[4 * r4 + 1], sL, b4[r4].y);
-          sc[4 * r4 + 2] = fmaf(sc[4 * r4 + 2], sL, b4[r4].z);
-          sc[4 * r4 + 3] = fmaf(sc[4 * r4 + 3], sL, b4[r4].w);
-        }
+    for (int r4 = 0; r4 < 4; ++r4) {
+      float x[4] = {sc[4 * r4], sc[4 * r4 + 1], sc[4 * r4 + 2], sc[4 * r4 + 3]};
+      if constexpr (SR) {
+        const uint32_t u0 = pack_bf2(x[0], x[1]), u1 = pack_bf2(x[2], x[3]);
+        x[0] = bf_lo(u0);
+        x[1] = bf_hi(u0);
+        x[2] = bf_lo(u1);
+        x[3] = bf_hi(u1);
       }
-    } else if (a.score_round) {
-#pragma unroll
-      for (int r = 0; r < 16; r += 2) {
-        const uint32_t u = pack_bf2(sc[r], sc[r + 1]);
-        sc[r] = bf_lo(u);
-        sc[r + 1] = bf_hi(u);
-      }
+      sc[4 * r4] = fmaf(x[0], sL, b4[r4].x);
+      sc[4 * r4 + 1] = fmaf(x[1], sL, b4[r4].y);
+      sc[4 * r4 + 2] = fmaf(x[2], sL, b4[r4].z);
+      sc[4 * r4 + 3] = fmaf(x[3], sL, b4[r4].w);
     }
     // masks: rows past the valid keys, and the causal diagonal (a current-chunk block wholly
     // before the wave's first query needs none)
@@ -968,7 +959,7 @@ __global__ void __launch_bounds__(64 * NW, NPS == 2 ? 2 : 1) attn_fwd2_kernel(b3
     float bm = -INFINITY;
 #pragma unroll
     for (int r = 0; r < 16; ++r) bm = fmaxf(bm, sc[r]);
-    bm = pair_max32(bm) * ksc;
+    bm = pair_max32(bm);
     // the running max moves only when it grows by more than 2^8 (probabilities up to 2^8
     // before the final normalisation are exact enough in fp32 and rescale-free)
     const bool grow = bm > m_run + 8.0f;
@@ -977,7 +968,7 @@ __global__ void __launch_bounds__(64 * NW, NPS == 2 ? 2 : 1) attn_fwd2_kernel(b3
     float ps = 0.f;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const float p = __builtin_amdgcn_exp2f(fmaf(sc[r], ksc, -mu));
+      const float p = __builtin_amdgcn_exp2f(sc[r] - mu);
       sc[r] = p;
       ps += p;
     }
@@ -1053,9 +1044,10 @@ __global__ void __launch_bounds__(64 * NW, NPS == 2 ? 2 : 1) attn_fwd2_kernel(b3
     const FwdBlock f1 = block(has1 ? i1 : i0);
     const bool do1 = has1 && !(f1.kpos >= 0 && f1.kpos > wave_q0 + 31);
     const int st0 = 2 * (pr % NPS);
-    f32x16 sc0 = zero16(), sc1 = zero16();
-    if (do0) sc0 = qk(st0);
-    if (do1) sc1 = qk(st0 + 1);
+    // both blocks' products unconditionally (a block the wave skips, or the stage of a missing
+    // second block, gives a tile that is never used), so that no register tile is merged
+    // across branches (each merge would be a 16-register copy)
+    f32x16 sc0 = qk(st0), sc1 = qk(st0 + 1);
     if (do0) attend(sc0, f0, st0);
     if (do1) attend(sc1, f1, st0 + 1);
   }
@@ -1143,6 +1135,22 @@ __global__ void __launch_bounds__(64 * NW, NPS == 2 ? 2 : 1) attn_fwd2_kernel(b3
   }
 }
 
+template <int HD, bool SR>
+static void launch_fwd2(const b3_attn_args& ab, int G, int nw, int qlen, int n_chunks, dim3 grid, int nthreads, int QW,
+                        hipStream_t st) {
+  if (G == 4) {
+    // one query tile of the four heads per workgroup (four wavefronts), two workgroups per CU
+    const dim3 grid1((qlen + 31) / 32, n_chunks, ab.B * ab.HKV);
+    hipLaunchKernelGGL((attn_fwd2_kernel<HD, 4, 2, SR>), grid1, dim3(256), 0, st, ab, 1);
+  } else if (nw == 8) {
+    hipLaunchKernelGGL((attn_fwd2_kernel<HD, 8, 3, SR>), grid, dim3(nthreads), 0, st, ab, QW);
+  } else if (nw == 4) {
+    hipLaunchKernelGGL((attn_fwd2_kernel<HD, 4, 3, SR>), grid, dim3(nthreads), 0, st, ab, QW);
+  } else {
+    hipLaunchKernelGGL((attn_fwd2_kernel<HD, 2, 3, SR>), grid, dim3(nthreads), 0, st, ab, QW);
+  }
+}
+
 template <typename T, int HD>
 static int launch_attn(const b3_attn_args& a, hipStream_t st) {
   const int G = a.H / a.HKV;
@@ -1162,17 +1170,8 @@ static int launch_attn(const b3_attn_args& a, hipStream_t st) {
       ab.chunk_begin = c0;
       const int nw = nthreads / 64;
       if (a.part == 0 && (a.S == 128 || a.n_q <= 2 * a.C) && (nw == 2 || nw == 4 || nw == 8)) {
-        if (G == 4) {
-          // one query tile of the four heads per workgroup (four wavefronts), two workgroups per CU
-          const dim3 grid1((qlen + 31) / 32, n_chunks, a.B * a.HKV);
-          hipLaunchKernelGGL((attn_fwd2_kernel<HD, 4, 2>), grid1, dim3(256), 0, st, ab, 1);
-        } else if (nw == 8) {
-          hipLaunchKernelGGL((attn_fwd2_kernel<HD, 8, 3>), grid, dim3(nthreads), 0, st, ab, QW);
-        } else if (nw == 4) {
-          hipLaunchKernelGGL((attn_fwd2_kernel<HD, 4, 3>), grid, dim3(nthreads), 0, st, ab, QW);
-        } else {
-          hipLaunchKernelGGL((attn_fwd2_kernel<HD, 2, 3>), grid, dim3(nthreads), 0, st, ab, QW);
-        }
+        if (a.score_round) launch_fwd2<HD, true>(ab, G, nw, qlen, n_chunks, grid, nthreads, QW, st);
+        else launch_fwd2<HD, false>(ab, G, nw, qlen, n_chunks, grid, nthreads, QW, st);
         return (int)hipGetLastError();
       }
       const int ipt = (KB * (HD / 8) + nthreads - 1) / nthreads;

@@ -984,22 +984,31 @@ __global__ void __launch_bounds__(64 * PNW, 2) rowproj_kernel(ProjArgs p) {
 #pragma unroll
     for (int i = 0; i < PKS; ++i) wa[i] = *reinterpret_cast<const u16x8*>(wrow + 32 * min(i, nst - 1));
   }
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
+  // the x rows and the first half of the W steps (in-order completion: at most the second
+  // half's PKS / 2 loads still outstanding); the first half multiplies while the rest arrives.
+  // A wavefront past the last W row issued only its x rows: it waits for all of them.
+  static_assert(PKS == 16, "vmcnt below");
+  if (live) __builtin_amdgcn_s_waitcnt(8 | (7 << 4) | (15 << 8));   // vmcnt(8)
+  else __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));        // vmcnt(0)
+  sync_lds();   // every wavefront's x rows are in LDS (a barrier without a drain of the W loads)
   if (!live) return;
-#pragma unroll
-  for (int i = 0; i < PKS; ++i)
-    if (i >= nst) wa[i] = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
   f32x4 acc[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int i = 0; i < PKS; ++i)
+  for (int half = 0; half < 2; ++half) {
+    if (half == 1) __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));   // vmcnt(0)
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const u16x8 xb = *reinterpret_cast<const u16x8*>(xs + (16 * t + r) * PXS + (32 * i + 8 * kg) * 2);
-      mma16_bf16(acc[t], wa[i], xb);
-    }
+    for (int i = half * PKS / 2; i < (half + 1) * PKS / 2; ++i)
+      if (i >= nst) wa[i] = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int i = half * PKS / 2; i < (half + 1) * PKS / 2; ++i)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const u16x8 xb = *reinterpret_cast<const u16x8*>(xs + (16 * t + r) * PXS + (32 * i + 8 * kg) * 2);
+        mma16_bf16(acc[t], wa[i], xb);
+      }
+  }
   // D of tile t: column m = 16t + r, rows n = 4 kg + i: four consecutive n per lane
   float* out = p.parts + (long long)ch * p.M * p.N + nt * 16 + 4 * kg;
 #pragma unroll

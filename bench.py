@@ -423,10 +423,13 @@ def main():
         torch.cuda.tunable.tuning_enable(False)
     fl = prefill_flops(B, T)
     total = sum(fl.values())
-    # entry points: algorithmic work per forward (FLOPs, or bytes for the head preparation)
+    # entry points: algorithmic work per forward (FLOPs, or bytes for the head preparation).  The
+    # query heads are prepared inside the attention kernel, so bolt3_heads is the key/value launch:
+    # per token the k | v columns and the beta gate read (2048 + 8 bf16), k_raw, k_rope and v written
+    # (3 x 8 x 128 bf16) and beta (8 fp32); per position pos (fp32) and the (cos, sin) table row (64 x 4 B)
     work = {"bolt3_chunk_attn": ("mfma", fl["attn"] + fl["readout"]),
             "bolt3_chain": ("mfma", fl["consolidation"]),
-            "bolt3_heads": ("hbm", B * T * (6184 * 2 + (32 * 2 + 8 * 3) * 128 * 2 + 40 * 4))}
+            "bolt3_heads": ("hbm", B * T * ((2048 + 8) * 2 + 3 * 8 * 128 * 2 + 8 * 4) + T * (4 + 64 * 4))}
     kernels = {}
     for k, (bound, w) in work.items():
         ms_k, calls = kern.get(k, (0.0, 0.0))

@@ -80,6 +80,8 @@ typedef struct {
   const void* gates;          /* optional [B][T][gates_row_stride]: beta (HKV) | eta (H) projection columns;
                                  when set, the gates are read here instead of from lin / lin_kv */
   int64_t gates_row_stride;
+  uint32_t* rope_cs;          /* optional, bf16 only: [T][HD/2] the rounded (cos, sin) of position pos0 + t and
+                                 frequency i, cos in the low 16 bits -- the table b3_attn_args.rope_cs reads */
 } b3_heads_args;
 
 /*
@@ -254,6 +256,21 @@ typedef struct {
   /* mode 0, optional (NULL: not written): [B][H][n_q] fp32, every query's log-sum-exp (natural log)
      of its scaled, biased scores over all its keys -- the softmax normaliser the backward reuses */
   float* lse;
+  /* mode 0, part 0, bf16, optional: the query heads straight from the q projection output, so that
+     the q head preparation is done inside this kernel and q_rope, q_raw and eta are neither read
+     nor needed (they may be NULL).  The values are those bolt3_heads computes (q RMSNorm, RoPE,
+     tanh gate), bit for bit.  q_lin: element (b, t, c) at + (b*n_q + t)*q_lin_stride + c, query head
+     h at columns h*HD..; qn_w: [HD] fp32 q RMSNorm weight, or NULL for none; rope_cs: the (cos, sin)
+     table of positions 0..n_q-1 (b3_heads_args.rope_cs); gates: eta's pre-activation of head h at
+     + (b*n_q + t)*gates_stride + gates_col + h.  Rows 16-byte aligned. */
+  const void* q_lin;
+  int64_t q_lin_stride;
+  const float* qn_w;
+  float qn_eps;
+  const uint32_t* rope_cs;
+  const void* gates;
+  int64_t gates_stride;
+  int32_t gates_col;
 } b3_attn_args;
 
 /*

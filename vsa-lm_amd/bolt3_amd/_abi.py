@@ -43,6 +43,7 @@ class HeadsArgs(C.Structure):
         ("inv_freq", p), ("pos0", i32),
         ("q_raw", TensorOut), ("q_rope", TensorOut), ("k_raw", TensorOut), ("k_rope", TensorOut), ("v", TensorOut),
         ("beta", GateOut), ("eta", GateOut), ("pos_out", p), ("gates", p), ("gates_row_stride", i64),
+        ("rope_cs", p),
     ]
 
 
@@ -73,6 +74,8 @@ class AttnArgs(C.Structure):
         ("gamma", p), ("res_w", p), ("eps", f32),
         ("y", p), ("y_sb", i64), ("y_st", i64),
         ("part", i32), ("partial", p), ("chunk_begin", i32), ("chunk_end", i32), ("lse", p),
+        ("q_lin", p), ("q_lin_stride", i64), ("qn_w", p), ("qn_eps", f32), ("rope_cs", p),
+        ("gates", p), ("gates_stride", i64), ("gates_col", i32),
     ]
 
 

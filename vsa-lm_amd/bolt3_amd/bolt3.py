@@ -76,6 +76,12 @@ CHAIN_GROUPS = 3
 GROUP_STEPS = 32
 
 
+# The bf16 forward without a trace prepares the query heads (q RMSNorm, RoPE, the eta gate)
+# inside the attention kernel from the q projection output (b3_attn_args.q_lin) instead of in a
+# head-preparation pass of its own; both give the same bits.
+FUSED_Q_PREP = True
+
+
 def _n_groups(n_steps: int) -> int:
     return max(CHAIN_GROUPS, round(n_steps / GROUP_STEPS))
 
@@ -240,7 +246,7 @@ class Bolt3Attn(nn.Module):
         return self._pack
 
     def _heads(self, lin, B, T, dt, side, pos0, q_raw, q_rope, k_raw, k_rope, v, beta, eta, pos_out=None,
-               kv_offset=0, lin_kv=None, parts=0, gates=None):
+               kv_offset=0, lin_kv=None, parts=0, gates=None, rope_cs=None):
         a = A.HeadsArgs()
         a.dtype, a.B, a.T, a.H, a.HKV, a.HD = A.dtype_code(dt), B, T, self.H, self.HKV, self.HD
         if lin is not None:
@@ -258,6 +264,7 @@ class Bolt3Attn(nn.Module):
         a.k_raw, a.k_rope, a.v = _tout(k_raw, kv_offset), _tout(k_rope, kv_offset), _tout(v, kv_offset)
         a.beta, a.eta = _gout(beta, kv_offset), _gout(eta)
         a.pos_out = None if pos_out is None else pos_out.data_ptr() + kv_offset * 4
+        a.rope_cs = None if rope_cs is None else rope_cs.data_ptr()
         A.call("bolt3_heads", a, (lin if lin is not None else lin_kv).device)
 
     def _chain(self, dt, device, B, kr, kp, v, tok_bh_stride, pos, beta, beta_bh_stride, n_steps, off0, len0,
@@ -332,14 +339,18 @@ class Bolt3Attn(nn.Module):
         k_rope, v = torch.empty_like(k_raw), torch.empty_like(k_raw)
         beta = torch.empty(b, HKV, T, device=dev)
         pos = torch.empty(T, device=dev)
-        self._heads(None, b, T, dt, side, 0, None, None, k_raw, k_rope, v, beta, None, pos_out=pos,
-                    lin_kv=lin_kv, parts=2, gates=gates)
-
         n_chunks = (T + C - 1) // C
         n_cons = max(0, n_chunks - 2)
         bh = b * HKV
         snaps = (None, None, None, None)
         split = n_cons > 0 and dt == torch.bfloat16
+        # bf16 without a trace: the attention prepares the query heads itself, from the q
+        # projection output and the (cos, sin) table that the k head preparation writes
+        fuse_q = split and trace is None and FUSED_Q_PREP and S == 128 and H // HKV in (1, 2, 4, 8)
+        rope_cs = torch.empty(T, HD // 2, dtype=torch.int32, device=dev) if fuse_q else None
+        self._heads(None, b, T, dt, side, 0, None, None, k_raw, k_rope, v, beta, None, pos_out=pos,
+                    lin_kv=lin_kv, parts=2, gates=gates, rope_cs=rope_cs)
+
         # bf16: the chain's steps go out in groups; the slot decisions of a group run on one side
         # stream, its Gershgorin scales and M_res updates on another, and the main stream adds the
         # slot field and readout of a group's chunks as soon as that group is done
@@ -420,11 +431,12 @@ class Bolt3Attn(nn.Module):
             _wait_started(dev, ctr[0], first_started)
         lin_q = F.linear(x, side["wq"], side["bq"])
         _check_dtype(lin_q, dt, "q projection")
-        q_raw = torch.empty(b, H, T, HD, dtype=dt, device=dev)
-        q_rope = torch.empty_like(q_raw)
-        eta = torch.empty(b, H, T, device=dev)
-        self._heads(lin_q, b, T, dt, side, 0, q_raw, q_rope, None, None, None, None, eta, lin_kv=lin_kv, parts=1,
-                    gates=gates)
+        if not fuse_q:
+            q_raw = torch.empty(b, H, T, HD, dtype=dt, device=dev)
+            q_rope = torch.empty_like(q_raw)
+            eta = torch.empty(b, H, T, device=dev)
+            self._heads(lin_q, b, T, dt, side, 0, q_raw, q_rope, None, None, None, None, eta, lin_kv=lin_kv,
+                        parts=1, gates=gates)
         for gi in range(1, len(groups)):
             issue_group(gi)
         if trace is not None:
@@ -435,8 +447,14 @@ class Bolt3Attn(nn.Module):
         a = A.AttnArgs()
         a.dtype, a.B, a.H, a.HKV, a.HD, a.S, a.C, a.n_sinks = A.dtype_code(dt), b, H, HKV, HD, S, C, self.n_sinks
         a.mode, a.n_q, a.score_round = 0, T, int(score_round)
-        a.q_rope, a.q_raw, a.q_sb, a.q_sh = q_rope.data_ptr(), q_raw.data_ptr(), q_rope.stride(0), q_rope.stride(1)
-        a.eta, a.e_sb, a.e_sh = eta.data_ptr(), eta.stride(0), eta.stride(1)
+        if fuse_q:
+            a.q_lin, a.q_lin_stride = lin_q.data_ptr(), lin_q.shape[-1]
+            a.qn_w, a.qn_eps = A.ptr(side["qn"]), float(self.res_norm.eps)
+            a.rope_cs = rope_cs.data_ptr()
+            a.gates, a.gates_stride, a.gates_col = gates.data_ptr(), gates.shape[-1], HKV
+        else:
+            a.q_rope, a.q_raw, a.q_sb, a.q_sh = q_rope.data_ptr(), q_raw.data_ptr(), q_rope.stride(0), q_rope.stride(1)
+            a.eta, a.e_sb, a.e_sh = eta.data_ptr(), eta.stride(0), eta.stride(1)
         a.win_k, a.win_v, a.w_sb, a.w_sh = k_rope.data_ptr(), v.data_ptr(), k_rope.stride(0), k_rope.stride(1)
         if n_cons > 0:
             a.slot_k, a.slot_v, a.slot_bias = snaps[0].data_ptr(), snaps[1].data_ptr(), snaps[2].data_ptr()

@@ -66,6 +66,109 @@ template <int HD> struct QFrag<uint16_t, HD> {
     return s;
   }
 };
+// The query preparation inside the forward attention (b3_attn_args.q_lin): the lane's fragment
+// of row t of query head hq (pieces 2 ks + h, as QFrag) from the q projection output, then the
+// optional RMSNorm and RoPE with the arithmetic of bolt3_heads -- the q half of head_qkv
+// (vsa_lm/config/bolt3.py:197, the norm of vsa_lm/surgery.py:49-53) and LlamaRoPE
+// (vsa_lm/surgery.py:86-93): the fp32 statistic as the same tree of sumsq_pair8 partials
+// (within the lane over its pieces, then across the row's two lanes), the weight and one
+// rounding; each product and the sum of the rotation rounded.  Fetches are separate from the
+// arithmetic so that their latency can overlap other work.
+template <int HD> struct QPrep {
+  static constexpr int NKH = HD / 32;   // the lane's pieces in the first half of the head
+  float4 w[HD / 8];                     // q RMSNorm weight of the lane's elements
+  uint32_t cs[NKH][8];                  // (cos, sin) of the lane's first-half elements
+  // t: a valid row (rows past the chunk's queries take its last one: each query's scores,
+  // softmax and output depend on its own row only, and such rows are never written)
+  __device__ static void fetch_row(QFrag<uint16_t, HD>& f, const b3_attn_args& a, int b, int hq, int t, int h) {
+    const uint16_t* row = static_cast<const uint16_t*>(a.q_lin) + ((long long)b * a.n_q + t) * a.q_lin_stride + hq * HD;
+#pragma unroll
+    for (int ks = 0; ks < HD / 16; ++ks) f.v[ks] = *reinterpret_cast<const u16x8*>(row + 16 * ks + 8 * h);
+  }
+  __device__ void fetch_w(const b3_attn_args& a, int h) {
+    if (!a.qn_w) return;
+#pragma unroll
+    for (int ks = 0; ks < HD / 16; ++ks) {
+      w[2 * ks] = *reinterpret_cast<const float4*>(a.qn_w + 16 * ks + 8 * h);
+      w[2 * ks + 1] = *reinterpret_cast<const float4*>(a.qn_w + 16 * ks + 8 * h + 4);
+    }
+  }
+  __device__ void fetch_cs(const b3_attn_args& a, int t, int h) {   // t: a valid row, as fetch_row
+    const uint32_t* c = a.rope_cs + (long long)t * (HD / 2);
+#pragma unroll
+    for (int k = 0; k < NKH; ++k) {
+      const uint4 lo = *reinterpret_cast<const uint4*>(c + 16 * k + 8 * h);
+      const uint4 hi = *reinterpret_cast<const uint4*>(c + 16 * k + 8 * h + 4);
+      cs[k][0] = lo.x; cs[k][1] = lo.y; cs[k][2] = lo.z; cs[k][3] = lo.w;
+      cs[k][4] = hi.x; cs[k][5] = hi.y; cs[k][6] = hi.z; cs[k][7] = hi.w;
+    }
+  }
+  // the fragment as fp32 values, x[ks][e] = element 16 ks + 8 h + e
+  __device__ static void unpack(const QFrag<uint16_t, HD>& f, float (*x)[8]) {
+#pragma unroll
+    for (int ks = 0; ks < HD / 16; ++ks)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[ks][e] = bf2f(f.v[ks][e]);
+  }
+  // the row's RMS factor 1 / sqrt(mean(x^2) + eps); every lane of the wave takes part (shuffle)
+  __device__ static float rms_factor(const float (*x)[8], float eps) {
+    float s[NKH];
+#pragma unroll
+    for (int k = 0; k < NKH; ++k) s[k] = sumsq_pair8(x[k], x[k + NKH]);
+    // pieces p = 2k + h: the pairs (p, p ^ HD/32) ... (p, p ^ 2) are in the lane, (p, p ^ 1) across
+#pragma unroll
+    for (int off = NKH / 2; off >= 1; off >>= 1)
+#pragma unroll
+      for (int k = 0; k < off; ++k) s[k] = add_rn(s[k], s[k + off]);
+    const float ss = add_rn(s[0], __shfl_xor(s[0], 32, 64));
+    return 1.0f / sqrtf(div_rn(ss, (float)HD) + eps);
+  }
+  // x <- round(x * r * qn_w) in place (q_raw), two elements per rounding instruction
+  __device__ void scale(float (*x)[8], float r) const {
+#pragma unroll
+    for (int ks = 0; ks < HD / 16; ++ks) {
+      const float wv[8] = {w[2 * ks].x, w[2 * ks].y, w[2 * ks].z, w[2 * ks].w,
+                           w[2 * ks + 1].x, w[2 * ks + 1].y, w[2 * ks + 1].z, w[2 * ks + 1].w};
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        const uint32_t pk = pack_bf2(mul_rn(mul_rn(x[ks][e], r), wv[e]), mul_rn(mul_rn(x[ks][e + 1], r), wv[e + 1]));
+        x[ks][e] = bf_lo(pk);
+        x[ks][e + 1] = bf_hi(pk);
+      }
+    }
+  }
+  // the fragment from rounded fp32 values (exact: they are bf16 values)
+  __device__ static void pack(QFrag<uint16_t, HD>& f, const float (*x)[8]) {
+#pragma unroll
+    for (int ks = 0; ks < HD / 16; ++ks)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) f.v[ks][e] = f2bf(x[ks][e]);
+  }
+  // f <- RoPE(x): out = x*cos + rotate_half(x)*sin, each product and the sum rounded
+  __device__ void rope(QFrag<uint16_t, HD>& f, const float (*x)[8]) const {
+#pragma unroll
+    for (int k = 0; k < NKH; ++k) {
+      uint32_t lo[4], hi[4];
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        const float c0 = bf_lo(cs[k][e]), s0 = bf_hi(cs[k][e]), c1 = bf_lo(cs[k][e + 1]), s1 = bf_hi(cs[k][e + 1]);
+        const float u0 = x[k][e], u1 = x[k][e + 1], v0 = x[k + NKH][e], v1 = x[k + NKH][e + 1];
+        const uint32_t uc = pack_bf2(mul_rn(u0, c0), mul_rn(u1, c1)), vs = pack_bf2(mul_rn(-v0, s0), mul_rn(-v1, s1));
+        const uint32_t vc = pack_bf2(mul_rn(v0, c0), mul_rn(v1, c1)), us = pack_bf2(mul_rn(u0, s0), mul_rn(u1, s1));
+        lo[e / 2] = pack_bf2(add_rn(bf_lo(uc), bf_lo(vs)), add_rn(bf_hi(uc), bf_hi(vs)));
+        hi[e / 2] = pack_bf2(add_rn(bf_lo(vc), bf_lo(us)), add_rn(bf_hi(vc), bf_hi(us)));
+      }
+      f.v[k] = __builtin_bit_cast(u16x8, u32x4v{lo[0], lo[1], lo[2], lo[3]});
+      f.v[k + NKH] = __builtin_bit_cast(u16x8, u32x4v{hi[0], hi[1], hi[2], hi[3]});
+    }
+  }
+};
+// eta = tanh(eta_proj x) of query head hq at row t, rounded to bf16 (vsa_lm/config/bolt3.py:199)
+__device__ __forceinline__ float eta_from_gates(const b3_attn_args& a, int b, int hq, int t) {
+  const uint16_t* g = static_cast<const uint16_t*>(a.gates) + ((long long)b * a.n_q + t) * a.gates_stride + a.gates_col + hq;
+  return round_bf(tanhf(bf2f(*g)));
+}
+
 template <int HD> struct QFrag<float, HD> {
   float v[HD / 2];
   __device__ void load(const float* row, bool ok, int h) {
@@ -885,9 +988,18 @@ __global__ void __launch_bounds__(64 * NW, NPS == 2 ? 2 : 1) attn_fwd2_kernel(b3
   const float sb = (has_slots && tid < 128)
                        ? a.slot_bias[(long long)step * (a.slot_step / HD) + (long long)bh * a.S + tid] : 0.f;
   const float rw = tid < HD ? a.res_w[tid] : 0.f;
-  const uint16_t* qrow = reinterpret_cast<const uint16_t*>(a.q_rope) + b * a.q_sb + hq * a.q_sh + (long long)t * HD;
+  const bool fuse_q = a.q_lin != nullptr;   // the q head preparation done here
   QFrag<uint16_t, HD> qf;
-  qf.load(qrow, qok, h);
+  QPrep<HD> qp;
+  const int t_valid = qok ? t : qbase + nq_chunk - 1;
+  if (fuse_q) {
+    QPrep<HD>::fetch_row(qf, a, b, hq, t_valid, h);
+    qp.fetch_w(a, h);
+    qp.fetch_cs(a, t_valid, h);
+  } else {
+    const uint16_t* qrow = reinterpret_cast<const uint16_t*>(a.q_rope) + b * a.q_sb + hq * a.q_sh + (long long)t * HD;
+    qf.load(qrow, qok, h);
+  }
   issue_pair(0);
   if constexpr (NPS == 3) {
     if (P >= 1) issue_pair(1);
@@ -895,6 +1007,16 @@ __global__ void __launch_bounds__(64 * NW, NPS == 2 ? 2 : 1) attn_fwd2_kernel(b3
   }
   if (tid < 128) lds_write_f32(&sm.sbias[tid], sb * L2E);   // bias in log2 units
   if (tid < HD) lds_write_f32(&sm.resw[tid], rw);
+  float q_r = 1.f;   // the rows' RMS factor, kept for the readout's q_raw
+  if (fuse_q) {
+    float x[HD / 16][8];
+    QPrep<HD>::unpack(qf, x);
+    if (a.qn_w) {
+      q_r = QPrep<HD>::rms_factor(x, a.qn_eps);
+      qp.scale(x, q_r);
+    }
+    qp.rope(qf, x);
+  }
 
   f32x16 o[NDB];
 #pragma unroll
@@ -1063,9 +1185,14 @@ __global__ void __launch_bounds__(64 * NW, NPS == 2 ? 2 : 1) attn_fwd2_kernel(b3
     }
   }
   if (readout) {
-    const uint16_t* rrow = reinterpret_cast<const uint16_t*>(a.q_raw) + b * a.q_sb + hq * a.q_sh + (long long)t * HD;
-    rf.load(rrow, qok, h);
-    eta = qok ? a.eta[b * a.e_sb + hq * a.e_sh + t] : 0.f;
+    if (fuse_q) {
+      QPrep<HD>::fetch_row(rf, a, b, hq, t_valid, h);
+      eta = qok ? eta_from_gates(a, b, hq, t) : 0.f;
+    } else {
+      const uint16_t* rrow = reinterpret_cast<const uint16_t*>(a.q_raw) + b * a.q_sb + hq * a.q_sh + (long long)t * HD;
+      rf.load(rrow, qok, h);
+      eta = qok ? a.eta[b * a.e_sb + hq * a.e_sh + t] : 0.f;
+    }
   }
 
   // ---- normalise; y = round(O), kept as bf16 pairs (features d_row(lane, 2j), +1)
@@ -1083,6 +1210,13 @@ __global__ void __launch_bounds__(64 * NW, NPS == 2 ? 2 : 1) attn_fwd2_kernel(b3
   if (readout) {
     wait_vm<0>();
     sync_lds();
+    if (fuse_q && a.qn_w) {   // q_raw: the normalised row (the weight loads hit the cache)
+      qp.fetch_w(a, h);
+      float x[HD / 16][8];
+      QPrep<HD>::unpack(rf, x);
+      qp.scale(x, q_r);
+      QPrep<HD>::pack(rf, x);
+    }
     float qq = rf.sumsq();
     qq = pair_sum32(qq);
     const float inv_q = 1.0f / fmaxf(sqrtf(qq), 1e-12f);
@@ -1174,6 +1308,7 @@ static int launch_attn(const b3_attn_args& a, hipStream_t st) {
         else launch_fwd2<HD, false>(ab, G, nw, qlen, n_chunks, grid, nthreads, QW, st);
         return (int)hipGetLastError();
       }
+      if (a.q_lin) return B3_ERR_UNSUPPORTED;   // the in-kernel query preparation is fwd2's
       const int ipt = (KB * (HD / 8) + nthreads - 1) / nthreads;
       if (ipt <= 1) hipLaunchKernelGGL((attn_fwd_kernel<HD, 1>), grid, dim3(nthreads), 0, st, ab, QW);
       else if (ipt <= 2) hipLaunchKernelGGL((attn_fwd_kernel<HD, 2>), grid, dim3(nthreads), 0, st, ab, QW);
@@ -1181,7 +1316,7 @@ static int launch_attn(const b3_attn_args& a, hipStream_t st) {
       return (int)hipGetLastError();
     }
   }
-  if (a.part != 0 || c0 != 0 || c1 != all_chunks) return B3_ERR_UNSUPPORTED;
+  if (a.part != 0 || c0 != 0 || c1 != all_chunks || a.q_lin) return B3_ERR_UNSUPPORTED;
   hipLaunchKernelGGL((attn_kernel<T, HD>), grid, dim3(nthreads), 0, st, a, QW);
   return (int)hipGetLastError();
 }
@@ -1191,7 +1326,17 @@ static int launch_attn(const b3_attn_args& a, hipStream_t st) {
 extern "C" int bolt3_chunk_attn(const b3_attn_args* a, void* stream) {
   if (!a || a->B <= 0 || a->HKV <= 0 || a->n_q <= 0 || a->H % a->HKV != 0) return B3_ERR_ARG;
   if (a->H / a->HKV > 8 || (a->HD != 64 && a->HD != 128)) return B3_ERR_UNSUPPORTED;
-  if (!a->q_rope || !a->win_k || !a->win_v || !a->y || !a->gamma || !a->res_w || !a->eta) return B3_ERR_ARG;
+  const bool fuse_q = a->q_lin != nullptr;
+  if (!a->win_k || !a->win_v || !a->y || !a->gamma || !a->res_w) return B3_ERR_ARG;
+  if (!fuse_q && (!a->q_rope || !a->eta)) return B3_ERR_ARG;
+  if (fuse_q) {
+    const auto mis16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 != 0; };
+    if (a->dtype != B3_BF16 || a->mode != 0 || a->part != 0) return B3_ERR_UNSUPPORTED;
+    if (!a->rope_cs || !a->gates || a->gates_col < 0 || a->gates_stride < a->gates_col + a->H ||
+        a->q_lin_stride < (int64_t)a->H * a->HD || (a->q_lin_stride * 2) % 16 || mis16(a->q_lin) ||
+        mis16(a->rope_cs) || (a->qn_w && mis16(a->qn_w)))
+      return B3_ERR_ARG;
+  }
   if (a->mode == 0) {
     if (a->C <= 0 || a->n_sinks < 0) return B3_ERR_ARG;
     if (a->part == 0 && a->n_q > 2 * a->C && (!a->slot_k || !a->slot_v || !a->slot_bias)) return B3_ERR_ARG;
@@ -1202,7 +1347,7 @@ extern "C" int bolt3_chunk_attn(const b3_attn_args* a, void* stream) {
   } else {
     return B3_ERR_ARG;
   }
-  if (a->m_res && !a->q_raw) return B3_ERR_ARG;
+  if (a->m_res && !fuse_q && !a->q_raw) return B3_ERR_ARG;
   if (a->m_split && a->dtype != B3_BF16) return B3_ERR_ARG;
   if (a->part < 0 || a->part > 2 || (a->part != 0 && (a->mode != 0 || !a->partial))) return B3_ERR_ARG;
   if (a->chunk_begin < 0 || a->chunk_end < 0 || (a->chunk_end != 0 && a->chunk_end < a->chunk_begin) ||

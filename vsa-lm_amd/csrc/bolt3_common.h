@@ -123,6 +123,21 @@ __device__ __forceinline__ float sub_rn(float a, float b) {
 }
 __device__ __forceinline__ float div_rn(float a, float b) { return __fdiv_rn(a, b); }
 
+// A head's RMS statistic, partial over one piece pair: the 8 elements of a piece of the head's
+// first half (u) and the 8 of its RoPE partner piece in the second half (w), in element order.
+// The head preparation and the attention's in-kernel query preparation reduce these partials
+// over the head's HD/16 piece pairs in one tree (pairs p and p ^ HD/32 first, ..., p and p ^ 1
+// last), so both reach the same value.
+__device__ __forceinline__ float sumsq_pair8(const float* u, const float* w) {
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    s = fmaf(u[e], u[e], s);
+    s = fmaf(w[e], w[e], s);
+  }
+  return s;
+}
+
 // ---------------------------------------------------------------- MFMA
 
 __device__ __forceinline__ int d_row(int lane, int r) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }

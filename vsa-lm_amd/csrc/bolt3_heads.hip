@@ -36,6 +36,8 @@ __global__ void __launch_bounds__(HEADS_NT) heads_kernel(b3_heads_args a) {
     sincos_rope(mul_rn((float)(a.pos0 + t0 + tt), a.inv_freq[i]), &sn, &cs);
     cs_tab[tt][i] = St<T>::rnd(cs);
     sn_tab[tt][i] = St<T>::rnd(sn);
+    if constexpr (St<T>::is_bf16)
+      if (a.rope_cs && b == 0 && t0 + tt < a.T) a.rope_cs[(long long)(t0 + tt) * HALF + i] = pack_bf2(cs, sn);
   }
   __syncthreads();
 
@@ -67,12 +69,13 @@ __global__ void __launch_bounds__(HEADS_NT) heads_kernel(b3_heads_args a) {
     }
     // RMSNorm over the head (fp32 statistic), then weight, one rounding
     if (a.has_qk_norm) {
-      float ss = 0.f;
+      float u8[8], w8[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float u = x0.get(e), w = x1.get(e);
-        ss += u * u + w * w;
+        u8[e] = x0.get(e);
+        w8[e] = x1.get(e);
       }
+      float ss = sumsq_pair8(u8, w8);
 #pragma unroll
       for (int o = P8 / 2; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
       const float* wt = kind == 0 ? a.qn_w : a.kn_w;
@@ -146,6 +149,7 @@ extern "C" int bolt3_heads(const b3_heads_args* a, void* stream) {
   if (a->gates && a->gates_row_stride < a->HKV + a->H) return B3_ERR_ARG;
   if ((parts & 2) && (!a->k_rope.p || !a->v.p || !a->beta.p || (!a->lin && !a->lin_kv))) return B3_ERR_ARG;
   if (a->has_qk_norm && (!a->qn_w || !a->kn_w)) return B3_ERR_ARG;
+  if (a->rope_cs && (a->dtype != B3_BF16 || reinterpret_cast<uintptr_t>(a->rope_cs) % 4)) return B3_ERR_ARG;
   // 16-byte vector moves: projection rows and head rows must start 16-byte aligned
   const int64_t es = a->dtype == B3_BF16 ? 2 : 4;
   if (a->lin && ((a->lin_row_stride * es) % 16 || reinterpret_cast<uintptr_t>(a->lin) % 16)) return B3_ERR_ARG;

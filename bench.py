@@ -65,9 +65,10 @@ def backward_flops(b, t, H=32, HD=128, C=128):
     return attn + readout
 
 
-def bench_backward(mod, dev, steps, warmup):
+def bench_backward(mod, dev, steps, warmup, tune=False):
     """cfg2 forward + backward (the heal trainer's step on one layer): bf16 storage, gradients of
-    x and every parameter for loss = sum(y * g) with a seeded upstream g."""
+    x and every parameter for loss = sum(y * g) with a seeded upstream g.  tune: TunableOp times
+    the solutions of the backward's GEMM shapes in the warm-up steps (and only there)."""
     import torch
     from bolt3_amd import _abi
     g = torch.Generator(device=dev).manual_seed(SEED + 2)
@@ -79,8 +80,12 @@ def bench_backward(mod, dev, steps, warmup):
         xg = x.clone().requires_grad_(True)
         (mod(xg) * up).sum().backward()
 
+    if tune:
+        torch.cuda.tunable.tuning_enable(True)
     for _ in range(warmup):
         step()
+    if tune:
+        torch.cuda.tunable.tuning_enable(False)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
@@ -413,7 +418,8 @@ def main():
     if not args.no_tunableop:
         # PyTorch's TunableOp times the hipBLASLt / rocBLAS solutions of each projection GEMM shape
         # on its first call (in the warm-up forwards) and keeps the fastest; tuning stops after the
-        # prefill leg, so no later timed region pays for a search
+        # prefill leg and runs again only in the backward leg's warm-up steps (its GEMM shapes), so
+        # no timed region pays for a search
         import tempfile
         torch.cuda.tunable.enable(True)
         torch.cuda.tunable.tuning_enable(True)
@@ -479,10 +485,11 @@ def main():
                               frac_bf16_peak=round(total / (ms * 1e-3) / PEAK_BF16, 4)),
         "kernels": kernels,
         "gemm_selection": "hipBLASLt default" if args.no_tunableop else
-                          "PyTorch TunableOp (hipBLASLt/rocBLAS solutions timed in the warm-up forwards)",
+                          "PyTorch TunableOp (hipBLASLt/rocBLAS solutions timed in the warm-up forwards and, "
+                          "for the backward's products, the warm-up forward + backward steps)",
     }
     if not args.no_backward:
-        out["backward"] = bench_backward(mod, dev, max(2, args.steps // 2), 2)
+        out["backward"] = bench_backward(mod, dev, max(2, args.steps // 2), 2, tune=not args.no_tunableop)
     if not args.no_decode:
         out["decode"] = bench_decode(dev, args.decode_sets, args.decode_steps)
     if not args.no_long:

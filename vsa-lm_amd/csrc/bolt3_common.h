@@ -286,4 +286,22 @@ __device__ __forceinline__ void acc_operand_split(const f32x16& v, int kc, u16x8
   lo = __builtin_bit_cast(u16x8, l);
 }
 
+// ---------------------------------------------------------------- host
+
+// Compute units of the current device (cached per device; callers that race store the same
+// value), or minus the HIP error code.
+static inline int cu_count() {
+  static int cache[64];
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return -(int)e;
+  int n = dev >= 0 && dev < 64 ? cache[dev] : 0;
+  if (n <= 0) {
+    e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return -(int)e;
+    if (dev >= 0 && dev < 64) cache[dev] = n;
+  }
+  return n;
+}
+
 }  // namespace b3

@@ -939,8 +939,11 @@ __global__ void __launch_bounds__(ANT, 4) decode_attn_kernel(b3_decode_args a, L
 // before the first MFMA) by the staged x (v_mfma_f32_16x16x32_bf16: W rows as the A operand,
 // x rows as the B columns).  Each workgroup writes the fp32 partial product of its chunk to
 // parts[chunk][m][n]; the consumer adds the chunks in order, adds the bias and rounds once
-// (the decode prep kernel for the input projection, proj_reduce_kernel for o_proj).
-constexpr int PNW = 8;                 // wavefronts (weight-row tiles) per projection workgroup
+// (the decode prep kernel for the input projection, proj_reduce_kernel for o_proj).  The
+// number of tiles per workgroup (NW, 4 to 8) is the smallest that keeps the grid within one
+// workgroup per compute unit, so that every compute unit streams its share of W: at B = 64 the
+// Qwen3-4B input projection takes 245 workgroups of 8 and o_proj 256 of 5 (160 of 8 would leave
+// 96 compute units idle).
 constexpr int PKC = 512;               // K columns per chunk
 constexpr int PKS = PKC / 32;          // MFMA K steps per chunk
 constexpr int PXS = PKC * 2 + 16;      // LDS bytes per staged x row (16-byte pad: conflict-free reads)
@@ -958,10 +961,12 @@ struct ProjArgs {
   int M, N, K;
 };
 
-__global__ void __launch_bounds__(64 * PNW, 2) rowproj_kernel(ProjArgs p) {
+template <int NW>
+__global__ void __launch_bounds__(64 * NW, 2) rowproj_kernel(ProjArgs p) {
+  constexpr int XR = (64 + NW - 1) / NW;           // staged x rows per wavefront
   __shared__ __attribute__((aligned(16))) unsigned char xs[64 * PXS];
   const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int nt = blockIdx.x * PNW + wv;            // this wavefront's 16-row tile of W
+  const int nt = blockIdx.x * NW + wv;             // this wavefront's 16-row tile of W
   const int ch = blockIdx.y, m0 = blockIdx.z * 64;
   const int kc0 = ch * PKC;
   const int nst = min(PKS, (p.K - kc0) >> 5);      // K steps in this chunk
@@ -971,8 +976,9 @@ __global__ void __launch_bounds__(64 * PNW, 2) rowproj_kernel(ProjArgs p) {
   // rows past M repeat row M - 1 and columns past K repeat the last 8 (both multiply zeros
   // or are never stored)
 #pragma unroll
-  for (int j = 0; j < 64 / PNW; ++j) {
-    const int m = wv * (64 / PNW) + j;
+  for (int j = 0; j < XR; ++j) {
+    const int m = wv * XR + j;
+    if (m >= 64) break;   // uniform across the wavefront
     const uint16_t* src = p.x + (long long)min(m0 + m, p.M - 1) * p.x_rs + min(kc0 + 8 * lane, p.K - 8);
     __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(xs + m * PXS), 16, 0, 0);
   }
@@ -1039,8 +1045,20 @@ __global__ void __launch_bounds__(256) proj_reduce_kernel(const float* parts, in
 }
 
 static int launch_rowproj(const ProjArgs& p, hipStream_t st) {
-  const dim3 grid((p.N / 16 + PNW - 1) / PNW, proj_chunks(p.K), (p.M + 63) / 64);
-  hipLaunchKernelGGL(rowproj_kernel, grid, dim3(64 * PNW), 0, st, p);
+  const int n_cu = cu_count();
+  if (n_cu < 0) return -n_cu;
+  const int tiles = p.N / 16, other = proj_chunks(p.K) * ((p.M + 63) / 64);
+  int nw = 8;
+  for (int w = 4; w <= 8; ++w)
+    if ((long long)(tiles + w - 1) / w * other <= n_cu) { nw = w; break; }
+  const dim3 grid((tiles + nw - 1) / nw, proj_chunks(p.K), (p.M + 63) / 64);
+  switch (nw) {
+    case 4: hipLaunchKernelGGL(rowproj_kernel<4>, grid, dim3(256), 0, st, p); break;
+    case 5: hipLaunchKernelGGL(rowproj_kernel<5>, grid, dim3(320), 0, st, p); break;
+    case 6: hipLaunchKernelGGL(rowproj_kernel<6>, grid, dim3(384), 0, st, p); break;
+    case 7: hipLaunchKernelGGL(rowproj_kernel<7>, grid, dim3(448), 0, st, p); break;
+    default: hipLaunchKernelGGL(rowproj_kernel<8>, grid, dim3(512), 0, st, p); break;
+  }
   return (int)hipGetLastError();
 }
 

@@ -1352,9 +1352,13 @@ __global__ void __launch_bounds__(64 * RD_W) readout_bwd_mfma_kernel(b3_attn_bwd
           mma_bf16(dq, ah, blo[db][kc]);
         }
       if (live) {
+        // the row's swizzle, opaque here so that the sixteen read addresses are formed at their
+        // use (hoisted out of the row loop they were spilled, and every reload waited on vmcnt)
+        int sw = n % NP;
+        asm volatile("" : "+v"(sw));
 #pragma unroll
         for (int r4 = 0; r4 < 4; ++r4) {
-          const uint2 q2 = *reinterpret_cast<const uint2*>(&qt[n * HD + 8 * ((4 * cb + r4) ^ (n % NP)) + 4 * h]);
+          const uint2 q2 = *reinterpret_cast<const uint2*>(&qt[n * HD + 8 * ((4 * cb + r4) ^ sw) + 4 * h]);
           float4 v;
           v.x = (dq[4 * r4] - bf_lo(q2.x) * qi2) * inv;
           v.y = (dq[4 * r4 + 1] - bf_hi(q2.x) * qi2) * inv;

@@ -484,7 +484,10 @@ class Bolt3Attn(nn.Module):
                 # writes rows t >= t0 only)
                 a.y, a.y_sb, a.y_st = blk.data_ptr() - t0 * K * esz, (t1 - t0) * K, K
                 A.call("bolt3_chunk_attn", a, dev)
-                out[:, t0:t1].copy_(F.linear(blk, side["wo"]).view(b, t1 - t0, -1))
+                if b == 1:   # the group's output rows are one contiguous slab of the result
+                    torch.mm(blk, side["wo"].t(), out=out[0, t0:t1])
+                else:
+                    out[:, t0:t1].copy_(F.linear(blk, side["wo"]).view(b, t1 - t0, -1))
             return out
         # One [B, T, H * HD] attention output (the backward reads it), o_proj as one GEMM.  bf16:
         # group by group, as soon as the chain has produced a group's snapshots, one launch over

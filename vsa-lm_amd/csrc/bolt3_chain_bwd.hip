@@ -239,6 +239,65 @@ __device__ __forceinline__ void add_row16(float* out, int sl, const float* v) {
   x = p1[1]; x.x += v[12]; x.y += v[13]; x.z += v[14]; x.w += v[15]; p1[1] = x;
 }
 
+// What a thread of slot_rec reads for step i that does not depend on the recursion: its slot's
+// attention gradient slice, the slot's mean position and previous mass, and the decision-log
+// entries its indices select.  Fetched one step ahead, so that a step waits for one round trip
+// (its token rows) instead of three.
+template <int HD>
+struct SlotRecIn {
+  float lo[8], hi[8];     // d_slot_{k|v} of (step, slot): features 8 sl .., HD/2 + 8 sl ..
+  float p, mb;            // snap_pm of the step, snap_mass of the step before (arr 0)
+  int fill;               // fill step: slot s takes a picked token (log TOPTOK at s - nfb)
+  float fill_tok;
+  float win, bs, tk;      // steady step, tid < min(l, S): log WIN / BOTSLOT / TOPTOK at tid
+  float mg, ts;           // tid < l: log MERGE / SLOT at tid
+  float mgj, tsj;         // j = tid / 2 < l: log MERGE / SLOT at j
+};
+
+template <int HD>
+__device__ __forceinline__ SlotRecIn<HD> slot_rec_fetch(const b3_chain_bwd_args& a, int i, int bh, int sl, int s,
+                                                        int arr, int tid) {
+  SlotRecIn<HD> f;
+  const long long BH = (long long)a.B * a.HKV;
+  const int l = step_len(a, i), nfb = filled_before(a, i);
+  const float* lg = log_rec(a, i, bh);
+  const long long base = (((long long)i * BH + bh) * S + s) * HD;
+  const float* src = (arr ? a.d_slot_v : a.d_slot_k) + base;
+  *reinterpret_cast<float4*>(f.lo) = *reinterpret_cast<const float4*>(src + 8 * sl);
+  *reinterpret_cast<float4*>(f.lo + 4) = *reinterpret_cast<const float4*>(src + 8 * sl + 4);
+  *reinterpret_cast<float4*>(f.hi) = *reinterpret_cast<const float4*>(src + HD / 2 + 8 * sl);
+  *reinterpret_cast<float4*>(f.hi + 4) = *reinterpret_cast<const float4*>(src + HD / 2 + 8 * sl + 4);
+  f.p = arr == 0 ? a.snap_pm[((long long)i * BH + bh) * S + s] : 0.f;
+  f.mb = 0.f;
+  f.fill = 0;
+  f.fill_tok = -1.f;
+  f.win = f.bs = f.tk = f.mg = f.ts = f.mgj = f.tsj = -1.f;
+  if (nfb < S) {
+    const int m = min(S - nfb, l);
+    if (s >= nfb && s < nfb + m) {
+      f.fill = 1;
+      f.fill_tok = lg[B3_LOG_TOPTOK * B3_LOG_COLS + (s - nfb)];
+    }
+  } else {
+    if (arr == 0) f.mb = a.snap_mass[((long long)(i - 1) * BH + bh) * S + s];   // steady: i >= 1
+    if (tid < min(l, S)) {
+      f.win = lg[B3_LOG_WIN * B3_LOG_COLS + tid];
+      f.bs = lg[B3_LOG_BOTSLOT * B3_LOG_COLS + tid];
+      f.tk = lg[B3_LOG_TOPTOK * B3_LOG_COLS + tid];
+    }
+    if (tid < l) {
+      f.mg = lg[B3_LOG_MERGE * B3_LOG_COLS + tid];
+      f.ts = lg[B3_LOG_SLOT * B3_LOG_COLS + tid];
+    }
+    const int jj = tid >> 1;
+    if (jj < l) {
+      f.mgj = lg[B3_LOG_MERGE * B3_LOG_COLS + jj];
+      f.tsj = lg[B3_LOG_SLOT * B3_LOG_COLS + jj];
+    }
+  }
+  return f;
+}
+
 template <int HD>
 __global__ void __launch_bounds__(NT) slot_rec_kernel(b3_chain_bwd_args a) {
   // gradients of the slots' un-roped keys (g[0]) and values (g[1]) on this slice
@@ -248,7 +307,6 @@ __global__ void __launch_bounds__(NT) slot_rec_kernel(b3_chain_bwd_args a) {
   const int bh = blockIdx.x, sl = blockIdx.y;
   const int tid = threadIdx.x, s = tid >> 1, arr = tid & 1;
   if (a.started && tid == 0) __hip_atomic_fetch_add(a.started, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const long long BH = (long long)a.B * a.HKV;
   float* grow = g[arr][s];
 #pragma unroll
   for (int e = 0; e < 16; ++e) grow[e] = 0.f;
@@ -256,46 +314,39 @@ __global__ void __launch_bounds__(NT) slot_rec_kernel(b3_chain_bwd_args a) {
 #pragma unroll
   for (int e = 0; e < 8; ++e) invf[e] = a.inv_freq[8 * sl + e];
   float* const out_all = arr ? a.d_v : a.d_kr;
+  if (a.n_steps <= 0) return;
+  SlotRecIn<HD> cur = slot_rec_fetch<HD>(a, a.n_steps - 1, bh, sl, s, arr, tid);
   for (int i = a.n_steps - 1; i >= 0; --i) {
     const int l = step_len(a, i), t0 = step_off(a, i), nfb = filled_before(a, i);
-    const float* lg = log_rec(a, i, bh);
+    SlotRecIn<HD> nxt;
+    if (i > 0) nxt = slot_rec_fetch<HD>(a, i - 1, bh, sl, s, arr, tid);
     float* out = out_all + ((long long)bh * a.T + t0) * HD;
     // the attention's gradients of the slots after step i: keys through the transpose of
     // their RoPE at the slot's mean position
-    {
-      const long long base = (((long long)i * BH + bh) * S + s) * HD;
-      const float* src = (arr ? a.d_slot_v : a.d_slot_k) + base;
-      float lo[8], hi[8];
-      *reinterpret_cast<float4*>(lo) = *reinterpret_cast<const float4*>(src + 8 * sl);
-      *reinterpret_cast<float4*>(lo + 4) = *reinterpret_cast<const float4*>(src + 8 * sl + 4);
-      *reinterpret_cast<float4*>(hi) = *reinterpret_cast<const float4*>(src + HD / 2 + 8 * sl);
-      *reinterpret_cast<float4*>(hi + 4) = *reinterpret_cast<const float4*>(src + HD / 2 + 8 * sl + 4);
-      if (arr == 0) {
-        const float p = a.snap_pm[((long long)i * BH + bh) * S + s];
+    if (arr == 0) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          float sn, cs;
-          sincos_rope(p * invf[e], &sn, &cs);   // the forward RoPE's own values
-          grow[e] += lo[e] * cs + hi[e] * sn;
-          grow[8 + e] += hi[e] * cs - lo[e] * sn;
-        }
-      } else {
+      for (int e = 0; e < 8; ++e) {
+        float sn, cs;
+        sincos_rope(cur.p * invf[e], &sn, &cs);   // the forward RoPE's own values
+        grow[e] += cur.lo[e] * cs + cur.hi[e] * sn;
+        grow[8 + e] += cur.hi[e] * cs - cur.lo[e] * sn;
+      }
+    } else {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          grow[e] += lo[e];
-          grow[8 + e] += hi[e];
-        }
+      for (int e = 0; e < 8; ++e) {
+        grow[e] += cur.lo[e];
+        grow[8 + e] += cur.hi[e];
       }
     }
     if (nfb < S) {
       // fill: slots nfb .. nfb + m - 1 are copies of the picked tokens
-      const int m = min(S - nfb, l);
-      if (s >= nfb && s < nfb + m) {
-        const int tok = (int)lg[B3_LOG_TOPTOK * B3_LOG_COLS + (s - nfb)];
+      if (cur.fill) {
+        const int tok = (int)cur.fill_tok;
         if ((unsigned)tok < (unsigned)l) add_row16<HD>(out + (long long)tok * HD, sl, grow);
 #pragma unroll
         for (int e = 0; e < 16; ++e) grow[e] = 0.f;
       }
+      cur = nxt;
       continue;   // every thread touches only its own row in this step
     }
     // steady step: winners (token -> slot) and merge counts
@@ -304,17 +355,14 @@ __global__ void __launch_bounds__(NT) slot_rec_kernel(b3_chain_bwd_args a) {
       cnt[tid] = 0;
     }
     __syncthreads();
-    {
-      const int kc = min(l, S);
-      // (indices outside the step's tokens or the slots are ignored)
-      if (tid < kc && lg[B3_LOG_WIN * B3_LOG_COLS + tid] > 0.5f) {
-        const int bs = (int)lg[B3_LOG_BOTSLOT * B3_LOG_COLS + tid], tk = (int)lg[B3_LOG_TOPTOK * B3_LOG_COLS + tid];
-        if ((unsigned)bs < (unsigned)S && (unsigned)tk < (unsigned)l) map_tok[bs] = tk;
-      }
-      if (tid < l && lg[B3_LOG_MERGE * B3_LOG_COLS + tid] > 0.5f) {
-        const int ts = (int)lg[B3_LOG_SLOT * B3_LOG_COLS + tid];
-        if ((unsigned)ts < (unsigned)S) atomicAdd(&cnt[ts], 1);
-      }
+    // (indices outside the step's tokens or the slots are ignored)
+    if (cur.win > 0.5f) {
+      const int bs = (int)cur.bs, tk = (int)cur.tk;
+      if ((unsigned)bs < (unsigned)S && (unsigned)tk < (unsigned)l) map_tok[bs] = tk;
+    }
+    if (cur.mg > 0.5f) {
+      const int ts = (int)cur.ts;
+      if ((unsigned)ts < (unsigned)S) atomicAdd(&cnt[ts], 1);
     }
     __syncthreads();
     // eviction: the winning token took the slot, so the slot's gradient is the token's
@@ -326,17 +374,16 @@ __global__ void __launch_bounds__(NT) slot_rec_kernel(b3_chain_bwd_args a) {
         for (int e = 0; e < 16; ++e) grow[e] = 0.f;
       }
       if (arr == 0) {
-        const float mb = a.snap_mass[((long long)(i - 1) * BH + bh) * S + s];
-        massb[s] = mb;
-        newm[s] = mb + (float)cnt[s];
+        massb[s] = cur.mb;
+        newm[s] = cur.mb + (float)cnt[s];
       }
     }
     __syncthreads();
     // merge: slot <- (mass * slot + sum of merged tokens) / new_mass
     {
       const int j = tid >> 1;
-      const int ts = j < l ? (int)lg[B3_LOG_SLOT * B3_LOG_COLS + j] : -1;
-      if (j < l && lg[B3_LOG_MERGE * B3_LOG_COLS + j] > 0.5f && (unsigned)ts < (unsigned)S) {
+      const int ts = (int)cur.tsj;
+      if (cur.mgj > 0.5f && (unsigned)ts < (unsigned)S) {
         const float coef = 1.0f / newm[ts];
         float v[16];
 #pragma unroll
@@ -351,6 +398,7 @@ __global__ void __launch_bounds__(NT) slot_rec_kernel(b3_chain_bwd_args a) {
       for (int e = 0; e < 16; ++e) grow[e] *= kp;
     }
     __syncthreads();
+    cur = nxt;
   }
 }
 

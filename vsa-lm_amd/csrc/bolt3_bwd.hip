@@ -1160,10 +1160,20 @@ __global__ void __launch_bounds__(64 * RD_W) readout_bwd_mfma_kernel(b3_attn_bwd
   {
     const uint16_t* src = reinterpret_cast<const uint16_t*>(a.m_res + (long long)(c - 2) * a.m_step +
                                                             (long long)bh * HD * HD);
-    for (int it = tid; it < 2 * HD * NP; it += NT_RD) {
+    // every load of the thread's items before their stores: one memory round trip
+    constexpr int NI = (2 * HD * NP + NT_RD - 1) / NT_RD;
+    u16x8 mv[NI];
+#pragma unroll
+    for (int q = 0; q < NI; ++q) {
+      const int it = tid + NT_RD * q;
       const int half = it / (HD * NP), rem = it % (HD * NP), d = rem / NP, pc = rem % NP;
-      *reinterpret_cast<u16x8*>(&sm.mt[half][d * HD + 8 * (pc ^ (d % NP))]) =
-          *reinterpret_cast<const u16x8*>(src + (long long)half * HD * HD + d * HD + 8 * pc);
+      if (it < 2 * HD * NP) mv[q] = *reinterpret_cast<const u16x8*>(src + (long long)half * HD * HD + d * HD + 8 * pc);
+    }
+#pragma unroll
+    for (int q = 0; q < NI; ++q) {
+      const int it = tid + NT_RD * q;
+      const int half = it / (HD * NP), rem = it % (HD * NP), d = rem / NP, pc = rem % NP;
+      if (it < 2 * HD * NP) *reinterpret_cast<u16x8*>(&sm.mt[half][d * HD + 8 * (pc ^ (d % NP))]) = mv[q];
     }
     for (int it = tid; it < HD; it += NT_RD) sm.resw[it] = a.res_w[it];
   }

@@ -87,8 +87,15 @@ struct KeyTile {
   alignas(16) uint16_t lo[F32 ? LT * HD : 8];
 };
 
+template <int HD, int NTH>
+__device__ __forceinline__ void stage_keys_bf16(KeyTile<HD, false>& kt, const uint16_t* kr_rows, int l, int tid);
+
 template <int HD, bool F32, int NTH>
 __device__ __forceinline__ void stage_keys(KeyTile<HD, F32>& kt, const void* kr_rows, int l, int tid) {
+  if constexpr (!F32) {
+    stage_keys_bf16<HD, NTH>(kt, reinterpret_cast<const uint16_t*>(kr_rows), l, tid);
+    return;
+  }
   constexpr int NP = Dims<HD>::NP;
   for (int it = tid; it < LT * NP; it += NTH) {
     const int r = it / NP, p = it % NP;
@@ -113,16 +120,51 @@ __device__ __forceinline__ void stage_keys(KeyTile<HD, F32>& kt, const void* kr_
     }
   }
 }
+// bf16: the thread's items in batches of 8, every load of a batch before its stores (one
+// memory round trip per batch; a load and its store per iteration would wait for each load)
+template <int HD, int NTH>
+__device__ __forceinline__ void stage_keys_bf16(KeyTile<HD, false>& kt, const uint16_t* kr_rows, int l, int tid) {
+  constexpr int NP = Dims<HD>::NP, N = (LT * NP + NTH - 1) / NTH, NB = N < 8 ? N : 8;
+  static_assert(N % NB == 0, "batches of the thread's items");
+#pragma unroll
+  for (int q0 = 0; q0 < N; q0 += NB) {
+    u16x8 v[NB];
+#pragma unroll
+    for (int q = 0; q < NB; ++q) {
+      const int it = tid + NTH * (q0 + q), r = it / NP, p = it % NP;
+      v[q] = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+      if (it < LT * NP && r < l) v[q] = *reinterpret_cast<const u16x8*>(kr_rows + (long long)r * HD + 8 * p);
+    }
+#pragma unroll
+    for (int q = 0; q < NB; ++q) {
+      const int it = tid + NTH * (q0 + q), r = it / NP, p = it % NP;
+      if (it < LT * NP) *reinterpret_cast<u16x8*>(&kt.hi[r * HD + 8 * (p ^ (r % NP))]) = v[q];
+    }
+  }
+}
 
 // an M^T hi / lo pair of planes into LDS (rows d, swizzled as the keys): from the bf16 forward's
 // snapshot (already M^T hi / lo) or, split here, from an fp32 M[c][d] (the fp32 forward's)
 template <int HD, int NTH>
 __device__ __forceinline__ void stage_mt(uint16_t* mt, const uint16_t* src, int tid) {
-  constexpr int NP = Dims<HD>::NP;
-  for (int it = tid; it < 2 * HD * NP; it += NTH) {
-    const int pl = it / (HD * NP), rem = it % (HD * NP), d = rem / NP, p = rem % NP;
-    *reinterpret_cast<u16x8*>(&mt[pl * HD * HD + d * HD + 8 * (p ^ (d % NP))]) =
-        *reinterpret_cast<const u16x8*>(src + (long long)pl * HD * HD + d * HD + 8 * p);
+  // the thread's items in batches of 8, every load of a batch before its stores
+  constexpr int NP = Dims<HD>::NP, N = (2 * HD * NP + NTH - 1) / NTH, NB = N < 8 ? N : 8;
+  static_assert(N % NB == 0, "batches of the thread's items");
+#pragma unroll
+  for (int q0 = 0; q0 < N; q0 += NB) {
+    u16x8 v[NB];
+#pragma unroll
+    for (int q = 0; q < NB; ++q) {
+      const int it = tid + NTH * (q0 + q);
+      const int pl = it / (HD * NP), rem = it % (HD * NP), d = rem / NP, p = rem % NP;
+      if (it < 2 * HD * NP) v[q] = *reinterpret_cast<const u16x8*>(src + (long long)pl * HD * HD + d * HD + 8 * p);
+    }
+#pragma unroll
+    for (int q = 0; q < NB; ++q) {
+      const int it = tid + NTH * (q0 + q);
+      const int pl = it / (HD * NP), rem = it % (HD * NP), d = rem / NP, p = rem % NP;
+      if (it < 2 * HD * NP) *reinterpret_cast<u16x8*>(&mt[pl * HD * HD + d * HD + 8 * (p ^ (d % NP))]) = v[q];
+    }
   }
 }
 template <int HD, int NTH>

@@ -1209,17 +1209,36 @@ __global__ void __launch_bounds__(DT) decide_kernel(b3_chain_args a) {
 
   // state in; with n_filled == 0 the empty state (zero slots, mass 1) is built here
   const bool fresh = a.n_filled == 0;
-  for (int it = tid; it < S * (HD / 8); it += DT) {
-    const int s = it / (HD / 8), d8 = (it % (HD / 8)) * 8;
-    if (fresh) {
-      alignas(16) T z[8];
+  if (!fresh && St<T>::is_bf16) {
+    // every load of the thread's rows before their stores: one memory round trip
+    constexpr int NI = S * (HD / 8) / DT;
+    static_assert(NI * DT == S * (HD / 8), "state rows over the threads");
+    u16x8 kx[NI], vx[NI];
 #pragma unroll
-      for (int q = 0; q < 8; ++q) z[q] = St<T>::from_f(0.f);
-      copy8(&sm.ak[s * KS + d8], z);
-      copy8(&sm.av[s * KS + d8], z);
-    } else {
-      copy8(&sm.ak[s * KS + d8], g_ak + s * HD + d8);
-      copy8(&sm.av[s * KS + d8], g_av + s * HD + d8);
+    for (int q = 0; q < NI; ++q) {
+      const int it = tid + DT * q, s = it / (HD / 8), d8 = (it % (HD / 8)) * 8;
+      kx[q] = *reinterpret_cast<const u16x8*>(g_ak + s * HD + d8);
+      vx[q] = *reinterpret_cast<const u16x8*>(g_av + s * HD + d8);
+    }
+#pragma unroll
+    for (int q = 0; q < NI; ++q) {
+      const int it = tid + DT * q, s = it / (HD / 8), d8 = (it % (HD / 8)) * 8;
+      *reinterpret_cast<u16x8*>(&sm.ak[s * KS + d8]) = kx[q];
+      *reinterpret_cast<u16x8*>(&sm.av[s * KS + d8]) = vx[q];
+    }
+  } else {
+    for (int it = tid; it < S * (HD / 8); it += DT) {
+      const int s = it / (HD / 8), d8 = (it % (HD / 8)) * 8;
+      if (fresh) {
+        alignas(16) T z[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) z[q] = St<T>::from_f(0.f);
+        copy8(&sm.ak[s * KS + d8], z);
+        copy8(&sm.av[s * KS + d8], z);
+      } else {
+        copy8(&sm.ak[s * KS + d8], g_ak + s * HD + d8);
+        copy8(&sm.av[s * KS + d8], g_av + s * HD + d8);
+      }
     }
   }
   if (tid < S) {
@@ -1948,10 +1967,20 @@ __global__ void __launch_bounds__(MT) mres_kernel(b3_chain_args a) {
   auto tok_base = [&](int step) { return (long long)bh * a.tok_bh_stride + (long long)step_off(a, step) * HD; };
   auto row_base = [&](int step) { return ((long long)step * BH + bh) * LMAX; };
 
-  // M^T block: mt[dd][c] = M[c][32*db + dd]
-  for (int it = tid; it < HD * 32; it += MT) {
-    const int c = it / 32, dd = it % 32;
-    const float x = a.n_filled == 0 ? 0.0f : M[c * HD + 32 * db + dd];   // empty state: M_res = 0
+  // M^T block: mt[dd][c] = M[c][32*db + dd]; every load of the thread before its stores (one
+  // memory round trip)
+  constexpr int NMI = HD * 32 / MT;
+  static_assert(NMI * MT == HD * 32, "M^T block over the threads");
+  float mx[NMI];
+#pragma unroll
+  for (int q = 0; q < NMI; ++q) {
+    const int it = tid + MT * q, c = it / 32, dd = it % 32;
+    mx[q] = a.n_filled == 0 ? 0.0f : M[c * HD + 32 * db + dd];   // empty state: M_res = 0
+  }
+#pragma unroll
+  for (int q = 0; q < NMI; ++q) {
+    const int it = tid + MT * q, c = it / 32, dd = it % 32;
+    const float x = mx[q];
     sm.mt[dd * Sm::MS + c] = x;
     if constexpr (St<T>::is_bf16) {
       const uint16_t hb = f2bf(x);

@@ -16,6 +16,8 @@
 // bolt3_decode_layer (bf16) adds the two projections around these: rowproj_kernel streams
 // a weight once per step and leaves fp32 partial products per K chunk; the prep kernel sums
 // those of the input projection and proj_reduce_kernel those of o_proj.
+#include <utility>
+
 #include "bolt3_common.h"
 #include "bolt3_math.h"
 #include "bolt3_amd.h"
@@ -954,12 +956,60 @@ __host__ __device__ inline long long proj_parts_floats(int M, int N, int K) {
   return (long long)proj_chunks(K) * M * N;
 }
 
+// ds_read_b128 of a staged x row at a compile-time byte offset (inline assembly, as dec_read_tr:
+// an ordinary LDS read would make the compiler wait for every outstanding W load first)
+template <int OFF>
+__device__ __forceinline__ u16x8 rp_read_at(uint32_t addr) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset range");
+  u16x8 r;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF) : "memory");
+  return r;
+}
+// lgkmcnt(N), tied to the four x operands of one K step
+template <int N>
+__device__ __forceinline__ void rp_lds_wait(u16x8 (&x)[4]) {
+  asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]) : "i"(N));
+}
+
 struct ProjArgs {
   const uint16_t* x; int64_t x_rs;
   const uint16_t* w;
   float* parts;                        // [chunk][M][N]
   int M, N, K;
 };
+
+template <int I>
+__device__ __forceinline__ void rp_read_step(u16x8 (&x)[4], uint32_t base) {
+  static_assert(48 * PXS + 64 * I < 65536, "ds offset range");
+  x[0] = rp_read_at<64 * I>(base);
+  x[1] = rp_read_at<16 * PXS + 64 * I>(base);
+  x[2] = rp_read_at<32 * PXS + 64 * I>(base);
+  x[3] = rp_read_at<48 * PXS + 64 * I>(base);
+}
+// K step I of the chunk: the x reads of step I + 1 go out before the MFMAs of step I.  The W
+// loads were issued in step order and complete in order: quarter q of the steps waits until at
+// most the later quarters' loads are outstanding.  Steps past the chunk multiply zeros.
+template <int I>
+__device__ __forceinline__ void rp_step(f32x4 (&acc)[4], u16x8 (&wa)[PKS], u16x8 (&xb)[2][4], uint32_t base,
+                                        int nst) {
+  constexpr int C = I & 1;
+  __builtin_amdgcn_sched_barrier(0);   // nothing of this step moves above the wait of its quarter
+  if constexpr (I + 1 < PKS) rp_read_step<I + 1>(xb[C ^ 1], base);
+  if constexpr (I > 0 && I % (PKS / 4) == 0) {
+    wait_vm<PKS - PKS / 4 - I>();
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (I >= nst) wa[I] = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+  if constexpr (I + 1 < PKS) rp_lds_wait<4>(xb[C]);
+  else rp_lds_wait<0>(xb[C]);
+#pragma unroll
+  for (int t = 0; t < 4; ++t) mma16_bf16(acc[t], wa[I], xb[C][t]);
+}
+template <int... I>
+__device__ __forceinline__ void rp_steps(f32x4 (&acc)[4], u16x8 (&wa)[PKS], u16x8 (&xb)[2][4], uint32_t base,
+                                         int nst, std::integer_sequence<int, I...>) {
+  (rp_step<I>(acc, wa, xb, base, nst), ...);
+}
 
 template <int NW>
 __global__ void __launch_bounds__(64 * NW, 2) rowproj_kernel(ProjArgs p) {
@@ -983,38 +1033,32 @@ __global__ void __launch_bounds__(64 * NW, 2) rowproj_kernel(ProjArgs p) {
     __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(xs + m * PXS), 16, 0, 0);
   }
   // the W rows: all steps of the chunk, in flight together with the x loads (steps past the
-  // chunk re-read its last step and multiply a zero operand, set once everything has arrived)
+  // chunk re-read its last step and multiply a zero operand, set once their quarter has arrived)
   u16x8 wa[PKS];
   if (live) {
     const uint16_t* wrow = p.w + (long long)(nt * 16 + r) * p.K + kc0 + 8 * kg;
 #pragma unroll
-    for (int i = 0; i < PKS; ++i) wa[i] = *reinterpret_cast<const u16x8*>(wrow + 32 * min(i, nst - 1));
+    for (int i = 0; i < PKS; ++i) {
+      wa[i] = *reinterpret_cast<const u16x8*>(wrow + 32 * min(i, nst - 1));
+      __builtin_amdgcn_sched_barrier(0);   // issued in step order: the waits below count on it
+    }
   }
-  // the x rows and the first half of the W steps (in-order completion: at most the second
-  // half's PKS / 2 loads still outstanding); the first half multiplies while the rest arrives.
-  // A wavefront past the last W row issued only its x rows: it waits for all of them.
+  // the x rows and the first quarter of the W steps (in-order completion: at most the other
+  // quarters' 3 PKS / 4 loads still outstanding); each quarter multiplies while the later ones
+  // arrive.  A wavefront past the last W row issued only its x rows: it waits for all of them.
   static_assert(PKS == 16, "vmcnt below");
-  if (live) __builtin_amdgcn_s_waitcnt(8 | (7 << 4) | (15 << 8));   // vmcnt(8)
-  else __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));        // vmcnt(0)
+  if (live) __builtin_amdgcn_s_waitcnt(12 | (7 << 4) | (15 << 8));   // vmcnt(12)
+  else __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));         // vmcnt(0)
   sync_lds();   // every wavefront's x rows are in LDS (a barrier without a drain of the W loads)
   if (!live) return;
   f32x4 acc[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int half = 0; half < 2; ++half) {
-    if (half == 1) __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));   // vmcnt(0)
-#pragma unroll
-    for (int i = half * PKS / 2; i < (half + 1) * PKS / 2; ++i)
-      if (i >= nst) wa[i] = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
-#pragma unroll
-    for (int i = half * PKS / 2; i < (half + 1) * PKS / 2; ++i)
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const u16x8 xb = *reinterpret_cast<const u16x8*>(xs + (16 * t + r) * PXS + (32 * i + 8 * kg) * 2);
-        mma16_bf16(acc[t], wa[i], xb);
-      }
-  }
+  // x operand of tile t, step i: row 16 t + r, bytes 64 i + 16 kg of it
+  const uint32_t xbase = (uint32_t)(size_t)((__attribute__((address_space(3))) unsigned char*)xs) + r * PXS + 16 * kg;
+  u16x8 xb[2][4];
+  rp_read_step<0>(xb[0], xbase);
+  rp_steps(acc, wa, xb, xbase, nst, std::make_integer_sequence<int, PKS>{});
   // D of tile t: column m = 16t + r, rows n = 4 kg + i: four consecutive n per lane
   float* out = p.parts + (long long)ch * p.M * p.N + nt * 16 + 4 * kg;
 #pragma unroll

@@ -229,6 +229,10 @@ __device__ __forceinline__ void prep_token(const b3_decode_args& a, const StepVi
       load8<float>(w + HALF + 8 * p, w1);
     }
   }
+  // the gate logits (eta of the G query heads, beta of the kv head) are loaded with the rows,
+  // not after the stores below: the preparation then waits for one memory round trip, not two
+  const bool gate = a.win_beta && tid <= G;
+  const float gz = gate ? lin1(tid < G ? gcol + a.HKV + hkv * G + tid : gcol + hkv) : 0.f;
   // the RMS statistic needs all P8 lanes of a unit: the shuffles run on every lane
   float ss = 0.f;
 #pragma unroll
@@ -299,10 +303,9 @@ __device__ __forceinline__ void prep_token(const b3_decode_args& a, const StepVi
       }
     }
   }
-  if (tid < G) ws_stat[2 * tid + 1] = a.win_beta ? St<T>::rnd(tanhf(lin1(gcol + a.HKV + hkv * G + tid))) : 0.f;
+  if (tid < G) ws_stat[2 * tid + 1] = a.win_beta ? St<T>::rnd(tanhf(gz)) : 0.f;
   if (tid == G && a.win_beta) {
-    const float z = lin1(gcol + hkv);
-    a.win_beta[b * a.wb_sb + hkv * a.wb_sh + ni] = St<T>::rnd(1.0f / (1.0f + expf(-z)));
+    a.win_beta[b * a.wb_sb + hkv * a.wb_sh + ni] = St<T>::rnd(1.0f / (1.0f + expf(-gz)));
     if (bh == 0 && a.win_pos) a.win_pos[ni] = (float)sv.pos;
   }
 }
